@@ -1,0 +1,221 @@
+/*
+ * pcl_hip.h -- C ABI of libpcl_hip, the MI355X (gfx950) matrix-multiply engine
+ * for pure-c-llm.
+ *
+ * Three families of entry points:
+ *
+ *  1. Host-pointer drop-ins with the reference's exact C signatures. A C
+ *     program that declares these functions (tensor.h, model.h, or the
+ *     `static` ones of train.c / transformer.c / generate.c / gemm_bench.c
+ *     turned into `extern` declarations) links against libpcl_hip instead of
+ *     the CPU code. Each call copies its operands to the GPU, runs the HIP
+ *     kernels and copies the result back before returning, exactly as
+ *     synchronous as the CPU original. They return void like the reference;
+ *     a failure is recorded in pcl_last_status()/pcl_last_error() (and aborts
+ *     the process when pcl_set_abort_on_error(1) was called, like the
+ *     reference's CUDA_CHECK / xmalloc).
+ *
+ *  2. Device-pointer drop-ins of the reference GPU API (gpu_kernels.h:38-51):
+ *     gpu_init, gemm_nn, gemm_nt, gemm_tn, bias_bwd. Asynchronous on the
+ *     calling thread's stream (pcl_set_stream; default: the null stream).
+ *
+ *  3. Native pcl_* entry points: device pointers, explicit leading
+ *     dimensions and stream, an int status return (PCL_OK == 0). These are the
+ *     timed path: inputs resident in HBM, no host traffic.
+ *
+ * Conventions (all families): row-major storage, the caller owns every buffer
+ * (the library never frees caller memory; tensor.h:17-20), outputs never
+ * alias inputs (tensor.h:37). M, N, K count elements; leading dimensions
+ * count elements of the operand's type. Dimensions of 0 are valid and do
+ * nothing except the defined output writes (e.g. C = bias when K == 0).
+ */
+#ifndef PCL_HIP_H
+#define PCL_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------ status ---- */
+enum {
+    PCL_OK = 0,
+    PCL_ERR_INVALID_ARG = 1, /* negative dims, NULL operand, bad leading dim  */
+    PCL_ERR_HIP = 2,         /* a HIP runtime call or kernel launch failed    */
+    PCL_ERR_NO_DEVICE = 3,   /* no usable gfx950 device                       */
+    PCL_ERR_OOM = 4,         /* device or host allocation failed              */
+    PCL_ERR_UNSET_DIMS = 5,  /* a drop-in that needs pcl_set_model_dims       */
+    PCL_ERR_RANGE = 6        /* an INT8 shape whose int32 sum could overflow  */
+};
+
+/* Library set-up. Every entry point initialises lazily; calling this first
+ * only moves the cost (device query, workspace) out of the first GEMM. */
+int pcl_init(void);
+/* Status and message of the most recent failing call on this thread. */
+int pcl_last_status(void);
+const char *pcl_last_error(void);
+void pcl_clear_error(void);
+/* 1: a failing void drop-in prints its message and calls exit(1), matching
+ * the reference's CUDA_CHECK (gpu_kernels.h:34-36). Default 0. */
+void pcl_set_abort_on_error(int on);
+/* Stream used by this thread's calls (a hipStream_t; NULL = null stream). */
+int pcl_set_stream(void *hip_stream);
+void *pcl_get_stream(void);
+int pcl_stream_synchronize(void);
+/* Device name and compute-unit count of the current device, for reports. */
+int pcl_device_info(char *name, int name_len, int *num_cus, int *clock_khz);
+
+/* Device memory plumbing for C hosts and bindings (hipMalloc & co.). */
+void *pcl_malloc(size_t bytes);
+int pcl_free(void *p);
+int pcl_memcpy_h2d(void *dst, const void *src, size_t bytes);
+int pcl_memcpy_d2h(void *dst, const void *src, size_t bytes);
+int pcl_memcpy_d2d(void *dst, const void *src, size_t bytes);
+int pcl_memset(void *dst, int value, size_t bytes);
+
+/* Event timing on this thread's stream (hipEvent_t behind an opaque handle). */
+void *pcl_event_create(void);
+int pcl_event_record(void *ev);
+int pcl_event_elapsed_ms(void *start, void *stop, float *ms); /* synchronises on stop */
+int pcl_event_destroy(void *ev);
+
+/* The reference's tied-head functions read compile-time D_MODEL/VOCAB_SIZE
+ * (train.c:34-51, transformer.h:35-39, model.h:24). The drop-ins below read
+ * them from here instead; they fail with PCL_ERR_UNSET_DIMS until set. */
+int pcl_set_model_dims(int d_model, int vocab_size);
+
+/* ============================== 1. host-pointer drop-ins ================= */
+
+/* tensor.h:40 / tensor.c:34-53: C(M,N) = A(M,K)·B(K,N), C fully overwritten.
+ * Also the signature of gemm_bench's gemm_fn rungs (gemm_bench.c:328). */
+void matmul(const float *A, const float *B, float *C, int M, int K, int N);
+
+/* train.c:181-211: out(M,N) = in(M,K)·W(K,N) + bias(N) (bias may be NULL). */
+void matmul_forward(float *out, const float *in, const float *Wt, const float *bias,
+                    int M, int K, int N);
+
+/* train.c:219-252: dX += dY·W^T, dW += X^T·dY, db += colsum(dY) (db may be NULL). */
+void matmul_backward(const float *dY, const float *X, const float *Wt, float *dX, float *dW,
+                     float *db, int M, int K, int N);
+
+/* train.c:412-423: logits(M,V) = lnf(M,D)·wte(V,D)^T. D,V from pcl_set_model_dims. */
+void tied_head_forward(float *logits, const float *lnf, const float *wte, int M);
+
+/* train.c:424-447: d_lnf = d_logits·wte (SET), dwte += d_logits^T·lnf. */
+void tied_head_backward(float *d_lnf, float *dwte, const float *d_logits, const float *lnf,
+                        const float *wte, int M);
+
+/* model.h:56 / model.c:64-77: logits[t,v] = x[t]·wte[v], t < num_tokens. */
+void lm_head(float *logits, const float *x, const float *wte, int num_tokens);
+
+/* transformer.c:174-195: out(N) = in(K)·W(K,N) + bias (bias may be NULL). */
+void proj_token(float *out, const float *in, const float *W, const float *bias, int K, int N);
+
+/* generate.c:95-107: same contract as proj_token. */
+void matvec(float *out, const float *x, const float *W, const float *b, int K, int N);
+
+/* gemm_bench.c:225-236: per-tensor symmetric quantisation to u8 (+128 offset),
+ * K padded to Kpad with 128. Returns the scale amax*fl(1/127). */
+float quantize_A(const float *A, uint8_t *Au, int M, int K, int Kpad);
+
+/* gemm_bench.c:238-259: per-column s8 quantisation into the VNNI panel layout
+ * Bp[p*(Kpad/4)*64 + kg*64 + i*4 + j] = Bq[kg*4+j][p*16+i]; colsum[n] = sum_k Bq.
+ * N must be a multiple of 16 (gemm_bench.c:245). */
+void quantize_B_pack(const float *B, int8_t *Bp, float *bscale, int32_t *colsum, int K, int N,
+                     int Kpad);
+
+/* gemm_bench.c:278-285: C(M,N) = float(sum_k Au·Bq - corr[n]) * dq[n] over the
+ * VNNI layout above; int32 result bit-exact, dequant in the reference op order. */
+void gemm_int8_kernel(const uint8_t *Au, int Kpad, const int8_t *Bp, const int32_t *corr,
+                      const float *dq, float *C, int M, int N);
+
+/* ============================== 2. device-pointer drop-ins =============== */
+
+/* gpu_kernels.h:39 -- one-time set-up; here an alias of pcl_init. */
+void gpu_init(void);
+/* gpu_kernels.h:48: C(M,N) = A(M,K)·B(K,N) + bias (bias may be NULL). */
+void gemm_nn(const float *A, const float *B, const float *bias, float *C, int M, int K, int N);
+/* gpu_kernels.h:49: C(M,N) ?= A(M,K)·B(N,K)^T; accum != 0 adds into C. */
+void gemm_nt(const float *A, const float *B, float *C, int M, int K, int N, int accum);
+/* gpu_kernels.h:50: C(K,N) += A(M,K)^T·B(M,N). */
+void gemm_tn(const float *A, const float *B, float *C, int M, int K, int N);
+/* gpu_kernels.h:51: db(N) += colsum(dY(M,N)). */
+void bias_bwd(float *db, const float *dY, int M, int N);
+
+/* ============================== 3. native entry points =================== */
+
+#define PCL_OP_N 0 /* operand stored as written: A is M x K, B is K x N */
+#define PCL_OP_T 1 /* operand stored transposed: A is K x M, B is N x K */
+
+/* FP32 GEMM on the f32 MFMA: C(M,N) = (accumulate ? C : 0) + op(A)·op(B) + bias.
+ * Decode shapes (M <= 8, opA == N) run the HBM-bound GEMV kernels instead.
+ * Replaces tensor.c:34-53, train.c:181-252/412-447, gpu_kernels.cu:112-138. */
+int pcl_sgemm(int opA, int opB, int M, int N, int K, const float *A, int lda, const float *B,
+              int ldb, const float *bias, int accumulate, float *C, int ldc, void *stream);
+
+/* FP32 GEMV (M <= 8 rows): Y(M,N) = (accumulate ? Y : 0) + X(M,K)·op(W) + bias.
+ * opW == PCL_OP_N: W is K x N (generate.c:95-107, transformer.c:174-195);
+ * opW == PCL_OP_T: W is N x K (the tied head, model.c:64-77, generate.c:176-182). */
+int pcl_sgemv(int opW, int M, int N, int K, const float *X, int ldx, const float *W, int ldw,
+              const float *bias, int accumulate, float *Y, int ldy, void *stream);
+
+/* db(N) += colsum(dY) (gpu_kernels.cu:102-108), fixed m order per column. */
+int pcl_bias_bwd(float *db, const float *dY, int M, int N, int ld, void *stream);
+
+/* ---- INT8: u8 activations x s8 weights -> int32 (gemm_bench.c:212-285) ----
+ * Weights live in the GPU-native packed layout: N rows of Kp = pcl_s8_kpad(K)
+ * bytes (K-contiguous per output column, zero-padded), i.e. B^T. */
+int pcl_s8_kpad(int K);
+size_t pcl_s8_packed_bytes(int K, int N);
+/* Pack row-major s8 B(K,N) (ldb) into the native layout; colsum (may be NULL)
+ * receives sum_k B[k,n]. */
+int pcl_pack_b_s8(const int8_t *B, int ldb, int K, int N, int8_t *Bpk, int32_t *colsum,
+                  void *stream);
+/* Repack the reference VNNI layout (gemm_bench.c:245-257; N % 16 == 0) into
+ * the native layout; colsum (may be NULL) as above. */
+int pcl_pack_b_vnni(const int8_t *Bp, int K, int Kpad, int N, int8_t *Bpk, int32_t *colsum,
+                    void *stream);
+
+/* C32(M,N) = sum_k (A[m,k]-128)·B[k,n] exactly (the reference's fixed-up `v`,
+ * gemm_bench.c:216-217, 274). A is M x K u8 with leading dim lda. */
+int pcl_gemm_u8s8_i32(const uint8_t *A, int lda, const int8_t *Bpk, int32_t *C, int ldc, int M,
+                      int N, int K, void *stream);
+
+/* C(M,N) = float(v + col_off[n]) * dq with v as above and
+ *   dq = sa[m]*sb[n]  (per-token x per-channel) when sa != NULL,
+ *   dq = sb[n]        (gemm_bench.c:272-275, sb = a_scale*bscale) otherwise.
+ * col_off may be NULL; the reference's `corr` maps to col_off = 128*colsum-corr. */
+int pcl_gemm_u8s8_dq(const uint8_t *A, int lda, const int8_t *Bpk, const int32_t *col_off,
+                     const float *sa, const float *sb, float *C, int ldc, int M, int N, int K,
+                     void *stream);
+
+/* Decode GEMV forms of the two calls above for M <= 8 (HBM-bound kernel). */
+int pcl_gemv_u8s8_i32(const uint8_t *X, int ldx, const int8_t *Bpk, int32_t *Y, int ldy, int M,
+                      int N, int K, void *stream);
+int pcl_gemv_u8s8_dq(const uint8_t *X, int ldx, const int8_t *Bpk, const int32_t *col_off,
+                     const float *sa, const float *sb, float *Y, int ldy, int M, int N, int K,
+                     void *stream);
+
+/* ---- quantisers (gemm_bench.c:225-259 rules: scale = amax * fl(1/127), the
+ * reference's -ffast-math build of amax/127.0f (README.md:104), with amax
+ * starting at 1e-8; q = clamp(lroundf(x * (1/scale)), -127, 127)) ---- */
+/* Per-tensor: Au = q + 128, Kpad columns (padding 128); *scale_dev = scale. */
+int pcl_quantize_a_tensor(const float *A, int M, int K, uint8_t *Au, int Kpad, float *scale_dev,
+                          void *stream);
+/* Per-row (per-token): sa[m] = amax(row m) * fl(1/127). */
+int pcl_quantize_a_rows(const float *A, int M, int K, uint8_t *Au, int Kpad, float *sa,
+                        void *stream);
+/* Per-column weights from row-major fp32 B(K,N): writes the native packed
+ * layout, bscale[n], and colsum[n] (may be NULL). */
+int pcl_quantize_b_cols(const float *B, int K, int N, int8_t *Bpk, float *bscale, int32_t *colsum,
+                        void *stream);
+/* Same quantisation written in the reference VNNI layout (N % 16 == 0). */
+int pcl_quantize_b_vnni(const float *B, int K, int N, int Kpad, int8_t *Bp, float *bscale,
+                        int32_t *colsum, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* PCL_HIP_H */

@@ -1,0 +1,216 @@
+"""ctypes binding of the CPU checker libraries. TEST INFRASTRUCTURE ONLY.
+
+Loaded only by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
+leg:
+  oracle/liboracle.so          this repository's C restatement (pcl_oracle.h)
+  oracle/_ref/libref_*.so      the reference's own sources built in place by
+                               oracle/Makefile (optional: absent when the
+                               reference tree was not available at build time)
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ORACLE_PATH = os.path.join(HERE, "liboracle.so")
+REF_DIR = os.path.join(HERE, "_ref")
+
+_vp, _i, _f, _d, _l, _u32 = C.c_void_p, C.c_int, C.c_float, C.c_double, C.c_long, C.c_uint32
+_sz = C.c_size_t
+
+_ORACLE_PROTOS = {
+    "orc_xorshift32": (_u32, [C.POINTER(_u32)]),
+    "orc_fill_frand": (None, [_vp, _sz, _u32, _f]),
+    "orc_fill_uniform": (None, [_vp, _sz, _u32, _f, _f]),
+    "orc_fill_normal": (None, [_vp, _sz, _u32, _f, _f]),
+    "orc_fill_u8": (None, [_vp, _sz, _u32]),
+    "orc_fill_s8": (None, [_vp, _sz, _u32]),
+    "orc_fill_kat_tensor": (None, [_vp, _sz, _vp, _sz]),
+    "orc_matmul_ikj": (None, [_vp, _vp, _vp, _i, _i, _i]),
+    "orc_matmul_naive": (None, [_vp, _vp, _vp, _i, _i, _i]),
+    "orc_gemm_f64": (None, [_vp, _l, _l, _vp, _l, _l, _vp, _vp, _l, _i, _i, _i, _i]),
+    "orc_gemm_nn": (None, [_vp, _vp, _vp, _vp, _i, _i, _i]),
+    "orc_gemm_nt": (None, [_vp, _vp, _vp, _i, _i, _i, _i]),
+    "orc_gemm_tn": (None, [_vp, _vp, _vp, _i, _i, _i]),
+    "orc_bias_bwd": (None, [_vp, _vp, _i, _i]),
+    "orc_matmul_forward": (None, [_vp, _vp, _vp, _vp, _i, _i, _i]),
+    "orc_matmul_backward": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i]),
+    "orc_tied_head_forward": (None, [_vp, _vp, _vp, _i, _i, _i]),
+    "orc_tied_head_backward": (None, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i]),
+    "orc_lm_head": (None, [_vp, _vp, _vp, _i, _i, _i]),
+    "orc_matvec": (None, [_vp, _vp, _vp, _vp, _i, _i, _i]),
+    "orc_quantize_A": (_f, [_vp, _vp, _i, _i, _i]),
+    "orc_quantize_A_rows": (None, [_vp, _vp, _vp, _i, _i, _i]),
+    "orc_quantize_B_pack": (None, [_vp, _vp, _vp, _vp, _i, _i, _i]),
+    "orc_quantize_B_cols": (None, [_vp, _vp, _vp, _i, _i]),
+    "orc_unpack_vnni": (None, [_vp, _vp, _i, _i, _i]),
+    "orc_gemm_u8s8_i32": (_l, [_vp, _i, _vp, _i, _vp, _i, _i, _i, _i]),
+    "orc_gemm_u8s8_raw_i32": (_l, [_vp, _i, _vp, _i, _vp, _i, _i, _i, _i]),
+    "orc_gemm_int8_kernel": (None, [_vp, _i, _vp, _vp, _vp, _vp, _i, _i]),
+    "orc_dequant": (None, [_vp, _i, _vp, _vp, _vp, _i, _i, _i]),
+    "orc_rms_rel": (_d, [_vp, _vp, _l]),
+    "orc_max_abs_diff": (_d, [_vp, _vp, _l]),
+}
+
+_REF_PROTOS = {
+    "libref_gemm_bench.so": {
+        "pcl_ref_cpu_ok": (_i, []),
+        "pcl_ref_set_threads": (None, [_i]),
+        "pcl_ref_max_threads": (_i, []),
+        "pcl_ref_gemm_naive": (None, [_vp, _vp, _vp, _i, _i, _i]),
+        "pcl_ref_gemm_ikj": (None, [_vp, _vp, _vp, _i, _i, _i]),
+        "pcl_ref_gemm_micro": (None, [_vp, _vp, _vp, _i, _i, _i]),
+        "pcl_ref_gemm_packed": (None, [_vp, _vp, _vp, _i, _i, _i]),
+        "pcl_ref_gemm_packed_mt": (None, [_vp, _vp, _vp, _i, _i, _i]),
+        "pcl_ref_quantize_A": (_f, [_vp, _vp, _i, _i, _i]),
+        "pcl_ref_quantize_B_pack": (None, [_vp, _vp, _vp, _vp, _i, _i, _i]),
+        "pcl_ref_gemm_int8_kernel": (None, [_vp, _i, _vp, _vp, _vp, _vp, _i, _i]),
+        "pcl_ref_rms_rel": (_d, [_vp, _vp, _l]),
+        "pcl_ref_max_abs_diff": (_d, [_vp, _vp, _l]),
+        "pcl_ref_srand": (None, [C.c_uint]),
+        "pcl_ref_fill_rand": (None, [_vp, _l]),
+    },
+    "libref_train.so": {
+        "pcl_ref_train_d_model": (_i, []),
+        "pcl_ref_train_vocab": (_i, []),
+        "pcl_ref_matmul_forward": (None, [_vp, _vp, _vp, _vp, _i, _i, _i]),
+        "pcl_ref_matmul_backward": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i]),
+        "pcl_ref_tied_head_forward": (None, [_vp, _vp, _vp, _i]),
+        "pcl_ref_tied_head_backward": (None, [_vp, _vp, _vp, _vp, _vp, _i]),
+    },
+    "libref_model.so": {
+        "pcl_ref_model_d_model": (_i, []),
+        "pcl_ref_proj_token": (None, [_vp, _vp, _vp, _vp, _i, _i]),
+        "lm_head": (None, [_vp, _vp, _vp, _i]),
+        "matmul": (None, [_vp, _vp, _vp, _i, _i, _i]),
+    },
+}
+
+
+def _declare(lib, protos):
+    for name, (res, args) in protos.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+_oracle = None
+
+
+def oracle():
+    """liboracle.so; raises if it has not been built."""
+    global _oracle
+    if _oracle is None:
+        if not os.path.exists(ORACLE_PATH):
+            raise ImportError(f"{ORACLE_PATH} not built (make -C oracle)")
+        _oracle = _declare(C.CDLL(ORACLE_PATH), _ORACLE_PROTOS)
+    return _oracle
+
+
+_refs: dict = {}
+
+
+def ref(name: str):
+    """oracle/_ref/<name> (the reference built from source), or None."""
+    if name not in _refs:
+        path = os.path.join(REF_DIR, name)
+        _refs[name] = _declare(C.CDLL(path), _REF_PROTOS[name]) if os.path.exists(path) else None
+    return _refs[name]
+
+
+def p(a):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+# ------------------------------------------------------------- inputs ----
+def frand(shape, seed, scale=1.0):
+    a = np.empty(shape, np.float32)
+    oracle().orc_fill_frand(p(a), a.size, seed, scale)
+    return a
+
+
+def uniform(shape, seed, lo, hi):
+    a = np.empty(shape, np.float32)
+    oracle().orc_fill_uniform(p(a), a.size, seed, lo, hi)
+    return a
+
+
+def normal(shape, seed, mean=0.0, std=1.0):
+    a = np.empty(shape, np.float32)
+    oracle().orc_fill_normal(p(a), a.size, seed, mean, std)
+    return a
+
+
+def u8(shape, seed):
+    a = np.empty(shape, np.uint8)
+    oracle().orc_fill_u8(p(a), a.size, seed)
+    return a
+
+
+def s8(shape, seed):
+    a = np.empty(shape, np.int8)
+    oracle().orc_fill_s8(p(a), a.size, seed)
+    return a
+
+
+# ------------------------------------------------------------ wrappers ----
+def matmul_ikj(A, B):
+    M, K = A.shape
+    N = B.shape[1]
+    Cm = np.empty((M, N), np.float32)
+    oracle().orc_matmul_ikj(p(A), p(B), p(Cm), M, K, N)
+    return Cm
+
+
+def gemm_f64(A, B, transA=False, transB=False, bias=None, C0=None):
+    """(C0 or 0) + op(A).op(B) + bias, double accumulation, one rounding."""
+    A = np.ascontiguousarray(A, np.float32)
+    B = np.ascontiguousarray(B, np.float32)
+    if transA:
+        K, M = A.shape
+        sam, sak = 1, M
+    else:
+        M, K = A.shape
+        sam, sak = K, 1
+    if transB:
+        N = B.shape[0]
+        sbk, sbn = 1, K
+    else:
+        N = B.shape[1]
+        sbk, sbn = N, 1
+    Cm = np.zeros((M, N), np.float32) if C0 is None else np.array(C0, np.float32, copy=True)
+    oracle().orc_gemm_f64(p(A), sam, sak, p(B), sbk, sbn, p(bias), p(Cm), N, M, N, K,
+                          0 if C0 is None else 1)
+    return Cm
+
+
+def gemm_u8s8_i32(Au, Bq):
+    """exact sum_k (Au-128)*Bq; Bq is K x N row-major."""
+    Au = np.ascontiguousarray(Au)
+    Bq = np.ascontiguousarray(Bq)
+    M, K = Au.shape
+    N = Bq.shape[1]
+    Cm = np.empty((M, N), np.int32)
+    bad = oracle().orc_gemm_u8s8_i32(p(Au), K, p(Bq), N, p(Cm), N, M, N, K)
+    assert bad == 0, "int32 overflow in the oracle"
+    return Cm
+
+
+def dequant(V, sa, sb):
+    M, N = V.shape
+    out = np.empty((M, N), np.float32)
+    oracle().orc_dequant(p(np.ascontiguousarray(V)), N, p(sa), p(sb), p(out), N, M, N)
+    return out
+
+
+def normwise_rel_err(X, R):
+    """max|X-R| / max|R| -- the FP32 parity metric (tolerance 1e-4)."""
+    X = np.asarray(X, np.float64)
+    R = np.asarray(R, np.float64)
+    den = np.max(np.abs(R)) if R.size else 0.0
+    num = np.max(np.abs(X - R)) if R.size else 0.0
+    return 0.0 if num == 0 else num / max(den, 1e-30)

@@ -1,0 +1,472 @@
+/*
+ * pcl_oracle.c -- CPU restatement of pure-c-llm's matrix-multiply hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY (the checker, never the product): see pcl_oracle.h.
+ * Reference citations are file:line into the pure-c-llm repository.
+ *
+ * Pinning (how each function is checked independently of this file):
+ *   orc_matmul_ikj / naive ...... tensor.c:204-241 closed-form KAT (C[0,0]=0.07
+ *                                 and the full closed-form matrix), identity and
+ *                                 ones-matrix invariants, the reference's own
+ *                                 tensor.c matmul built from source (oracle/_ref)
+ *   orc_gemm_f64 / nn / nt / tn . brute-force identities ((AB)^T = B^T A^T links
+ *                                 the three layouts), A=I, K=0, accumulate=twice
+ *   orc_matmul_backward, tied_* . train.c built from source (oracle/_ref) at small
+ *                                 dims, plus f64 transposition identities
+ *   orc_quantize_*, VNNI pack ... gemm_bench.c built from source (oracle/_ref):
+ *                                 byte-exact comparison of Au, Bp, scales, colsum
+ *   orc_gemm_u8s8_i32 ........... exact int64 brute force; the VNNI identity
+ *                                 sum Au*Bq - 128*colsum = sum (Au-128)*Bq checked
+ *                                 against the reference gemm_int8_kernel output
+ *   orc_dequant ................. bit-exact against gemm_bench.c's float output
+ */
+#include "pcl_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#ifndef M_PI
+#define M_PI 3.14159265358979323846
+#endif
+
+/* ---------------------------------------------------------------- PRNG ---- */
+static uint32_t seed_or_default(uint32_t seed) { return seed ? seed : 0x9E3779B9u; }
+
+uint32_t orc_xorshift32(uint32_t *s) {
+    /* train.c:75 / model.c:120-122 */
+    uint32_t x = *s;
+    x ^= x << 13;
+    x ^= x >> 17;
+    x ^= x << 5;
+    *s = x;
+    return x;
+}
+
+static float unit24(uint32_t x) { return (float)(x & 0x00FFFFFFu) / (float)0x01000000; }
+
+void orc_fill_frand(float *p, size_t n, uint32_t seed, float scale) {
+    uint32_t s = seed_or_default(seed);
+    for (size_t i = 0; i < n; i++) {
+        float u = unit24(orc_xorshift32(&s));
+        p[i] = (u * 2.0f - 1.0f) * scale; /* train.c:76-77 */
+    }
+}
+
+void orc_fill_uniform(float *p, size_t n, uint32_t seed, float lo, float hi) {
+    uint32_t s = seed_or_default(seed);
+    for (size_t i = 0; i < n; i++) p[i] = lo + (hi - lo) * unit24(orc_xorshift32(&s));
+}
+
+void orc_fill_normal(float *p, size_t n, uint32_t seed, float mean, float std) {
+    uint32_t s = seed_or_default(seed);
+    for (size_t i = 0; i < n; i++) {
+        double u1 = ((double)(orc_xorshift32(&s) & 0x00FFFFFFu) + 0.5) / 16777216.0;
+        double u2 = (double)(orc_xorshift32(&s) & 0x00FFFFFFu) / 16777216.0;
+        double z = sqrt(-2.0 * log(u1)) * cos(2.0 * M_PI * u2);
+        p[i] = (float)(mean + std * z);
+    }
+}
+
+void orc_fill_u8(uint8_t *p, size_t n, uint32_t seed) {
+    uint32_t s = seed_or_default(seed);
+    for (size_t i = 0; i < n; i++) p[i] = (uint8_t)((orc_xorshift32(&s) >> 16) & 0xFFu);
+}
+
+void orc_fill_s8(int8_t *p, size_t n, uint32_t seed) {
+    uint32_t s = seed_or_default(seed);
+    for (size_t i = 0; i < n; i++) p[i] = (int8_t)(uint8_t)((orc_xorshift32(&s) >> 16) & 0xFFu);
+}
+
+void orc_fill_kat_tensor(float *A, size_t na, float *B, size_t nb) {
+    /* tensor.c:204-205 (int index i, so the pattern restarts per element index) */
+    for (size_t i = 0; i < na; i++) A[i] = (float)((int)(i % 13) - 6) * 0.1f;
+    for (size_t i = 0; i < nb; i++) B[i] = (float)((int)(i % 7) - 3) * 0.1f;
+}
+
+/* ---------------------------------------------------- FP32 GEMM family ---- */
+void orc_matmul_ikj(const float *A, const float *B, float *C, int M, int K, int N) {
+    /* tensor.c:34-53 */
+#pragma omp parallel for schedule(static)
+    for (int i = 0; i < M; i++) {
+        float *crow = C + (size_t)i * N;
+        for (int j = 0; j < N; j++) crow[j] = 0.0f;
+        for (int k = 0; k < K; k++) {
+            const float a = A[(size_t)i * K + k];
+            const float *brow = B + (size_t)k * N;
+            for (int j = 0; j < N; j++) crow[j] += a * brow[j];
+        }
+    }
+}
+
+void orc_matmul_naive(const float *A, const float *B, float *C, int M, int K, int N) {
+    /* gemm_bench.c:60-67 */
+#pragma omp parallel for schedule(static)
+    for (int i = 0; i < M; i++)
+        for (int j = 0; j < N; j++) {
+            float acc = 0.0f;
+            for (int k = 0; k < K; k++) acc += A[(size_t)i * K + k] * B[(size_t)k * N + j];
+            C[(size_t)i * N + j] = acc;
+        }
+}
+
+void orc_gemm_f64(const float *A, long sam, long sak, const float *B, long sbk, long sbn,
+                  const float *bias, float *C, long ldc, int M, int N, int K, int accum) {
+    double *row = NULL;
+#pragma omp parallel private(row)
+    {
+        row = (double *)malloc(sizeof(double) * (size_t)(N > 0 ? N : 1));
+#pragma omp for schedule(static)
+        for (int m = 0; m < M; m++) {
+            for (int n = 0; n < N; n++) row[n] = 0.0;
+            for (int k = 0; k < K; k++) {
+                double a = (double)A[(long)m * sam + (long)k * sak];
+                const float *bk = B + (long)k * sbk;
+                if (sbn == 1) {
+                    for (int n = 0; n < N; n++) row[n] += a * (double)bk[n];
+                } else {
+                    for (int n = 0; n < N; n++) row[n] += a * (double)bk[(long)n * sbn];
+                }
+            }
+            float *c = C + (long)m * ldc;
+            for (int n = 0; n < N; n++) {
+                double v = row[n];
+                if (bias) v += (double)bias[n];
+                if (accum) v += (double)c[n];
+                c[n] = (float)v;
+            }
+        }
+        free(row);
+    }
+}
+
+void orc_gemm_nn(const float *A, const float *B, const float *bias, float *C, int M, int K, int N) {
+    /* gpu_kernels.h:44, gpu_kernels.cu:112-120 */
+    orc_gemm_f64(A, K, 1, B, N, 1, bias, C, N, M, N, K, 0);
+}
+
+void orc_gemm_nt(const float *A, const float *B, float *C, int M, int K, int N, int accum) {
+    /* gpu_kernels.h:45, gpu_kernels.cu:122-129: B is (N,K) row-major */
+    orc_gemm_f64(A, K, 1, B, 1, K, NULL, C, N, M, N, K, accum);
+}
+
+void orc_gemm_tn(const float *A, const float *B, float *C, int M, int K, int N) {
+    /* gpu_kernels.h:46, gpu_kernels.cu:131-138: C(K,N) += A(M,K)^T B(M,N) */
+    orc_gemm_f64(A, 1, K, B, N, 1, NULL, C, N, K, N, M, 1);
+}
+
+void orc_bias_bwd(float *db, const float *dY, int M, int N) {
+    /* gpu_kernels.cu:102-108 */
+    for (int n = 0; n < N; n++) {
+        float s = 0.0f;
+        for (int m = 0; m < M; m++) s += dY[(size_t)m * N + n];
+        db[n] += s;
+    }
+}
+
+void orc_matmul_forward(float *out, const float *in, const float *W, const float *bias,
+                        int M, int K, int N) {
+    /* train.c:181-211, the i-k-j branch (:192-203) and the bias pass (:204-210) */
+    orc_matmul_ikj(in, W, out, M, K, N);
+    if (bias)
+        for (int m = 0; m < M; m++) {
+            float *o = out + (size_t)m * N;
+            for (int n = 0; n < N; n++) o[n] += bias[n];
+        }
+}
+
+void orc_matmul_backward(const float *dY, const float *X, const float *W, float *dX,
+                         float *dW, float *db, int M, int K, int N) {
+    /* train.c:219-252 */
+    if (dX) {
+#pragma omp parallel for schedule(static)
+        for (int m = 0; m < M; m++) {
+            const float *dy = dY + (size_t)m * N;
+            float *dx = dX + (size_t)m * K;
+            for (int k = 0; k < K; k++) {
+                const float *wr = W + (size_t)k * N;
+                float s = 0.0f;
+                for (int n = 0; n < N; n++) s += dy[n] * wr[n];
+                dx[k] += s;
+            }
+        }
+    }
+    if (dW) {
+#pragma omp parallel for schedule(static)
+        for (int k = 0; k < K; k++) {
+            float *dwr = dW + (size_t)k * N;
+            for (int m = 0; m < M; m++) {
+                float a = X[(size_t)m * K + k];
+                const float *dy = dY + (size_t)m * N;
+                for (int n = 0; n < N; n++) dwr[n] += a * dy[n];
+            }
+        }
+    }
+    if (db) {
+        for (int n = 0; n < N; n++) {
+            float s = 0.0f;
+            for (int m = 0; m < M; m++) s += dY[(size_t)m * N + n];
+            db[n] += s;
+        }
+    }
+}
+
+void orc_tied_head_forward(float *logits, const float *lnf, const float *wte, int M, int D, int V) {
+    /* train.c:412-423 */
+#pragma omp parallel for schedule(static)
+    for (int m = 0; m < M; m++) {
+        const float *x = lnf + (size_t)m * D;
+        float *lo = logits + (size_t)m * V;
+        for (int vv = 0; vv < V; vv++) {
+            const float *wr = wte + (size_t)vv * D;
+            float s = 0.0f;
+            for (int d = 0; d < D; d++) s += x[d] * wr[d];
+            lo[vv] = s;
+        }
+    }
+}
+
+void orc_tied_head_backward(float *d_lnf, float *dwte, const float *dlogits, const float *lnf,
+                            const float *wte, int M, int D, int V) {
+    /* train.c:424-447 */
+    if (d_lnf) {
+#pragma omp parallel for schedule(static)
+        for (int m = 0; m < M; m++) {
+            const float *dl = dlogits + (size_t)m * V;
+            float *dx = d_lnf + (size_t)m * D;
+            for (int d = 0; d < D; d++) dx[d] = 0.0f;
+            for (int vv = 0; vv < V; vv++) {
+                float g = dl[vv];
+                const float *wr = wte + (size_t)vv * D;
+                for (int d = 0; d < D; d++) dx[d] += g * wr[d];
+            }
+        }
+    }
+    if (dwte) {
+#pragma omp parallel for schedule(static)
+        for (int vv = 0; vv < V; vv++) {
+            float *dw = dwte + (size_t)vv * D;
+            for (int m = 0; m < M; m++) {
+                float g = dlogits[(size_t)m * V + vv];
+                const float *lr = lnf + (size_t)m * D;
+                for (int d = 0; d < D; d++) dw[d] += g * lr[d];
+            }
+        }
+    }
+}
+
+void orc_lm_head(float *logits, const float *x, const float *wte, int T, int D, int V) {
+    /* model.c:64-77 */
+#pragma omp parallel for schedule(static)
+    for (int v = 0; v < V; v++) {
+        const float *wv = wte + (size_t)v * D;
+        for (int t = 0; t < T; t++) {
+            const float *xt = x + (size_t)t * D;
+            float dot = 0.0f;
+            for (int d = 0; d < D; d++) dot += xt[d] * wv[d];
+            logits[(size_t)t * V + v] = dot;
+        }
+    }
+}
+
+void orc_matvec(float *out, const float *x, const float *W, const float *b, int M, int K, int N) {
+    /* transformer.c:174-195, generate.c:95-107: bias initialises out, then
+     * k-sequential accumulation; one independent row per m. */
+    for (int m = 0; m < M; m++) {
+        float *o = out + (size_t)m * N;
+        const float *xm = x + (size_t)m * K;
+        for (int n = 0; n < N; n++) o[n] = b ? b[n] : 0.0f;
+        for (int k = 0; k < K; k++) {
+            const float a = xm[k];
+            const float *wr = W + (size_t)k * N;
+            for (int n = 0; n < N; n++) o[n] += a * wr[n];
+        }
+    }
+}
+
+/* ------------------------------------------------------------- INT8 ------ */
+/* gemm_bench.c:228 and :243 write `amax/127.0f`. The reference is built with
+ * -ffast-math (README.md:104, gemm_bench.c:8), under which gcc emits
+ * amax * fl(1/127): the scales (and hence the bytes) of the reference as it
+ * actually runs come from that multiplication, which differs from a correctly
+ * rounded division by one ulp for ~4% of inputs. The restatement follows the
+ * built reference; tests/test_oracle.py pins this against oracle/_ref. */
+#define RCP127 (1.0f / 127.0f)
+
+static int clamp127(int q) { return q > 127 ? 127 : (q < -127 ? -127 : q); }
+
+float orc_quantize_A(const float *A, uint8_t *Au, int M, int K, int Kpad) {
+    /* gemm_bench.c:225-236 */
+    float amax = 1e-8f;
+    for (size_t i = 0; i < (size_t)M * K; i++) {
+        float v = fabsf(A[i]);
+        if (v > amax) amax = v;
+    }
+    float scale = amax * RCP127, inv = 1.0f / scale;
+    for (int m = 0; m < M; m++)
+        for (int k = 0; k < Kpad; k++) {
+            int q = 0;
+            if (k < K) q = clamp127((int)lroundf(A[(size_t)m * K + k] * inv));
+            Au[(size_t)m * Kpad + k] = (uint8_t)(q + 128);
+        }
+    return scale;
+}
+
+void orc_quantize_A_rows(const float *A, uint8_t *Au, float *sa, int M, int K, int Kpad) {
+    /* gemm_bench.c:225-236 rule applied per row (per-token activation scale) */
+    for (int m = 0; m < M; m++) {
+        const float *a = A + (size_t)m * K;
+        float amax = 1e-8f;
+        for (int k = 0; k < K; k++) {
+            float v = fabsf(a[k]);
+            if (v > amax) amax = v;
+        }
+        float scale = amax * RCP127, inv = 1.0f / scale;
+        sa[m] = scale;
+        for (int k = 0; k < Kpad; k++) {
+            int q = 0;
+            if (k < K) q = clamp127((int)lroundf(a[k] * inv));
+            Au[(size_t)m * Kpad + k] = (uint8_t)(q + 128);
+        }
+    }
+}
+
+void orc_quantize_B_cols(const float *B, int8_t *Bq, float *bscale, int K, int N) {
+    /* gemm_bench.c:240-244 scale rule and :249-253 rounding, unpacked output */
+    for (int n = 0; n < N; n++) {
+        float bmax = 1e-8f;
+        for (int k = 0; k < K; k++) {
+            float v = fabsf(B[(size_t)k * N + n]);
+            if (v > bmax) bmax = v;
+        }
+        bscale[n] = bmax * RCP127;
+        float inv = 1.0f / bscale[n];
+        for (int k = 0; k < K; k++)
+            Bq[(size_t)k * N + n] = (int8_t)clamp127((int)lroundf(B[(size_t)k * N + n] * inv));
+    }
+}
+
+void orc_quantize_B_pack(const float *B, int8_t *Bp, float *bscale, int32_t *colsum,
+                         int K, int N, int Kpad) {
+    /* gemm_bench.c:238-259 */
+    for (int n = 0; n < N; n++) {
+        float bmax = 1e-8f;
+        for (int k = 0; k < K; k++) {
+            float v = fabsf(B[(size_t)k * N + n]);
+            if (v > bmax) bmax = v;
+        }
+        bscale[n] = bmax * RCP127;
+    }
+    int kgc = Kpad / 4, panels = N / 16;
+    for (int p = 0; p < panels; p++) {
+        int n0 = p * 16;
+        int8_t *base = Bp + (size_t)p * kgc * 64;
+        for (int i = 0; i < 16; i++) {
+            float inv = 1.0f / bscale[n0 + i];
+            int s = 0;
+            for (int kg = 0; kg < kgc; kg++)
+                for (int j = 0; j < 4; j++) {
+                    int kk = kg * 4 + j, q = 0;
+                    if (kk < K) q = clamp127((int)lroundf(B[(size_t)kk * N + n0 + i] * inv));
+                    base[(size_t)kg * 64 + i * 4 + j] = (int8_t)q;
+                    s += q;
+                }
+            colsum[n0 + i] = s;
+        }
+    }
+}
+
+void orc_unpack_vnni(const int8_t *Bp, int8_t *Bq, int K, int N, int Kpad) {
+    /* inverse of the layout written at gemm_bench.c:254 */
+    int kgc = Kpad / 4;
+    for (int k = 0; k < K; k++)
+        for (int n = 0; n < N; n++) {
+            int p = n / 16, i = n % 16, kg = k / 4, j = k % 4;
+            Bq[(size_t)k * N + n] = Bp[(size_t)p * kgc * 64 + (size_t)kg * 64 + i * 4 + j];
+        }
+}
+
+long orc_gemm_u8s8_i32(const uint8_t *Au, int lda, const int8_t *Bq, int ldb, int32_t *C, int ldc,
+                       int M, int N, int K) {
+    long bad = 0;
+#pragma omp parallel for schedule(static) reduction(+ : bad)
+    for (int m = 0; m < M; m++) {
+        const uint8_t *a = Au + (size_t)m * lda;
+        for (int n = 0; n < N; n++) {
+            int64_t acc = 0;
+            for (int k = 0; k < K; k++)
+                acc += (int64_t)((int)a[k] - 128) * (int64_t)Bq[(size_t)k * ldb + n];
+            if (acc > INT32_MAX || acc < INT32_MIN) bad++;
+            C[(size_t)m * ldc + n] = (int32_t)acc;
+        }
+    }
+    return bad;
+}
+
+long orc_gemm_u8s8_raw_i32(const uint8_t *Au, int lda, const int8_t *Bq, int ldb, int32_t *C,
+                           int ldc, int M, int N, int K) {
+    long bad = 0;
+#pragma omp parallel for schedule(static) reduction(+ : bad)
+    for (int m = 0; m < M; m++) {
+        const uint8_t *a = Au + (size_t)m * lda;
+        for (int n = 0; n < N; n++) {
+            int64_t acc = 0;
+            for (int k = 0; k < K; k++) acc += (int64_t)a[k] * (int64_t)Bq[(size_t)k * ldb + n];
+            if (acc > INT32_MAX || acc < INT32_MIN) bad++;
+            C[(size_t)m * ldc + n] = (int32_t)acc;
+        }
+    }
+    return bad;
+}
+
+void orc_gemm_int8_kernel(const uint8_t *Au, int Kpad, const int8_t *Bp, const int32_t *corr,
+                          const float *dq, float *C, int M, int N) {
+    /* gemm_bench.c:260-285: vpdpbusd accumulates in int32 with wrap-around;
+     * v = acc - corr (:274) and C = cvt(v) * dq (:275). */
+    int kgc = Kpad / 4, panels = N / 16;
+#pragma omp parallel for schedule(static)
+    for (int m = 0; m < M; m++)
+        for (int p = 0; p < panels; p++) {
+            const int8_t *bp = Bp + (size_t)p * kgc * 64;
+            for (int i = 0; i < 16; i++) {
+                uint32_t acc = 0;
+                for (int kg = 0; kg < kgc; kg++)
+                    for (int j = 0; j < 4; j++)
+                        acc += (uint32_t)((int32_t)Au[(size_t)m * Kpad + kg * 4 + j] *
+                                          (int32_t)bp[(size_t)kg * 64 + i * 4 + j]);
+                int n = p * 16 + i;
+                int32_t v = (int32_t)(acc - (uint32_t)corr[n]);
+                C[(size_t)m * N + n] = (float)v * dq[n];
+            }
+        }
+}
+
+void orc_dequant(const int32_t *V, int ldv, const float *sa, const float *sb, float *C, int ldc,
+                 int M, int N) {
+    for (int m = 0; m < M; m++)
+        for (int n = 0; n < N; n++) {
+            float dq = sa ? sa[m] * sb[n] : sb[n];
+            C[(size_t)m * ldc + n] = (float)V[(size_t)m * ldv + n] * dq;
+        }
+}
+
+double orc_rms_rel(const float *X, const float *R, long n) {
+    /* gemm_bench.c:302-306 */
+    double se = 0.0, sr = 0.0;
+    for (long i = 0; i < n; i++) {
+        double d = (double)X[i] - R[i];
+        se += d * d;
+        sr += (double)R[i] * R[i];
+    }
+    return sqrt(se / (sr + 1e-30));
+}
+
+double orc_max_abs_diff(const float *X, const float *Y, long n) {
+    /* gemm_bench.c:53-57 */
+    double d = 0.0;
+    for (long i = 0; i < n; i++) {
+        double e = fabs((double)X[i] - Y[i]);
+        if (e > d) d = e;
+    }
+    return d;
+}

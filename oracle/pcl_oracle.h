@@ -1,0 +1,126 @@
+/*
+ * pcl_oracle.h -- CPU restatement of pure-c-llm's matrix-multiply hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY. This library is the checker for the HIP kernels in
+ * libpcl_hip: only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
+ * leg may load it. The product path never links or calls it.
+ *
+ * Every function states the reference file:line whose semantics it follows
+ * (paths are relative to the reference repository root). Arithmetic choices:
+ *   - float functions that restate a reference loop keep the reference's
+ *     accumulation order (k-sequential per output element) in fp32;
+ *   - *_f64 functions accumulate in double and round once: the "truth" used to
+ *     judge both the reference-order restatements and the GPU kernels;
+ *   - integer functions accumulate in int64 and report overflow of int32.
+ * The library is compiled with -ffp-contract=off so that a*b+c is never fused:
+ * the restatements are reproducible bit-for-bit on any x86-64 host.
+ */
+#ifndef PCL_ORACLE_H
+#define PCL_ORACLE_H
+
+#include <stdint.h>
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------- PRNG ---- */
+/* xorshift32 step, the recurrence of train.c:73-78 and model.c:117-125. */
+uint32_t orc_xorshift32(uint32_t *state);
+/* p[i] = (u*2-1)*scale with u = (s & 0xFFFFFF)/2^24  (train.c:73-78 frand). */
+void orc_fill_frand(float *p, size_t n, uint32_t seed, float scale);
+/* p[i] = lo + (hi-lo)*u, same u as above (scales in U[1e-3,1e-2]). */
+void orc_fill_uniform(float *p, size_t n, uint32_t seed, float lo, float hi);
+/* Box-Muller N(mean, std) from two xorshift uniforms (u1 shifted off 0). */
+void orc_fill_normal(float *p, size_t n, uint32_t seed, float mean, float std);
+/* u8 uniform {0..255} and s8 uniform {-128..127}: bits 16..23 of each step. */
+void orc_fill_u8(uint8_t *p, size_t n, uint32_t seed);
+void orc_fill_s8(int8_t *p, size_t n, uint32_t seed);
+/* tensor.c:204-205 self-test pattern: A[i]=((i%13)-6)*0.1, B[i]=((i%7)-3)*0.1 */
+void orc_fill_kat_tensor(float *A, size_t na, float *B, size_t nb);
+
+/* ---------------------------------------------------- FP32 GEMM family ---- */
+/* tensor.c:34-53 matmul: C zeroed, then i-k-j accumulation in fp32. */
+void orc_matmul_ikj(const float *A, const float *B, float *C, int M, int K, int N);
+/* gemm_bench.c:60-67 v0 naive i-j-k, fp32 dot per element. */
+void orc_matmul_naive(const float *A, const float *B, float *C, int M, int K, int N);
+
+/*
+ * Generic double-accumulated GEMM over strided operands -- the truth.
+ *   C[m*ldc+n] = (accum ? C : 0) + sum_k A(m,k)*B(k,n) + (bias ? bias[n] : 0)
+ *   A(m,k) = A[m*sam + k*sak], B(k,n) = B[k*sbk + n*sbn]
+ * rounded once to fp32.
+ */
+void orc_gemm_f64(const float *A, long sam, long sak, const float *B, long sbk, long sbn,
+                  const float *bias, float *C, long ldc, int M, int N, int K, int accum);
+
+/* gpu_kernels.h:44-51 semantics (gpu_kernels.cu:112-142), computed in double:
+ *   nn: C(M,N)  = A(M,K)·B(K,N) + bias
+ *   nt: C(M,N) ?= A(M,K)·B(N,K)^T      (accum selects C += ...)
+ *   tn: C(K,N) += A(M,K)^T·B(M,N)
+ *   bias_bwd: db[n] += sum_m dY[m,n] (fp32, m-sequential; gpu_kernels.cu:102-108) */
+void orc_gemm_nn(const float *A, const float *B, const float *bias, float *C, int M, int K, int N);
+void orc_gemm_nt(const float *A, const float *B, float *C, int M, int K, int N, int accum);
+void orc_gemm_tn(const float *A, const float *B, float *C, int M, int K, int N);
+void orc_bias_bwd(float *db, const float *dY, int M, int N);
+
+/* train.c:181-211 matmul_forward: out = in·W (+ bias added in a second pass),
+ * fp32 i-k-j order of the non-AVX path. */
+void orc_matmul_forward(float *out, const float *in, const float *W, const float *bias,
+                        int M, int K, int N);
+/* train.c:219-252 matmul_backward: dX += dY·W^T, dW += X^T·dY, db += colsum(dY),
+ * each in the reference's fp32 loop order. dX/dW/db may be NULL to skip. */
+void orc_matmul_backward(const float *dY, const float *X, const float *W, float *dX,
+                         float *dW, float *db, int M, int K, int N);
+/* train.c:412-423 tied_head_forward with D,V explicit: logits = lnf·wte^T. */
+void orc_tied_head_forward(float *logits, const float *lnf, const float *wte, int M, int D, int V);
+/* train.c:424-447 tied_head_backward: d_lnf = dlogits·wte (SET), dwte += dlogits^T·lnf. */
+void orc_tied_head_backward(float *d_lnf, float *dwte, const float *dlogits, const float *lnf,
+                            const float *wte, int M, int D, int V);
+/* model.c:64-77 lm_head: logits[t,v] = x[t]·wte[v]. */
+void orc_lm_head(float *logits, const float *x, const float *wte, int T, int D, int V);
+/* transformer.c:174-195 proj_token / generate.c:95-107 matvec:
+ * out(N) = bias (or 0), then += x[k]*W[k,n] k-sequential. Batched over M rows. */
+void orc_matvec(float *out, const float *x, const float *W, const float *b, int M, int K, int N);
+
+/* ------------------------------------------------------------- INT8 ------ */
+/* gemm_bench.c:225-236 quantize_A: per-tensor scale amax*fl(1/127) (the -ffast-math
+ * build of amax/127.0f), q=clamp(lroundf(x*(1/s))),
+ * Au=q+128, K padded to Kpad with Au=128. Returns the scale. */
+float orc_quantize_A(const float *A, uint8_t *Au, int M, int K, int Kpad);
+/* Per-row (per-token) variant of the same rule: sa[m] = amax_row*fl(1/127). */
+void orc_quantize_A_rows(const float *A, uint8_t *Au, float *sa, int M, int K, int Kpad);
+/* gemm_bench.c:238-259 quantize_B_pack: per-column scale bmax*fl(1/127), VNNI panel
+ * layout Bp[p*(Kpad/4)*64 + kg*64 + i*4 + j] = Bq[kg*4+j][p*16+i], colsum[n]=sum q. */
+void orc_quantize_B_pack(const float *B, int8_t *Bp, float *bscale, int32_t *colsum,
+                         int K, int N, int Kpad);
+/* Same per-column rule, unpacked: Bq is K x N row-major s8. */
+void orc_quantize_B_cols(const float *B, int8_t *Bq, float *bscale, int K, int N);
+/* Unpack the VNNI panel layout back to Bq (K x N row-major; rows >= K unused). */
+void orc_unpack_vnni(const int8_t *Bp, int8_t *Bq, int K, int N, int Kpad);
+
+/* Exact u8 x s8 GEMM, the identity of gemm_bench.c:216-217:
+ *   C[m,n] = sum_k (Au[m,k]-128) * Bq[k,n]   (Bq K x N row-major, ldb)
+ * int64 accumulation; returns the number of outputs outside int32 (0 = ok). */
+long orc_gemm_u8s8_i32(const uint8_t *Au, int lda, const int8_t *Bq, int ldb, int32_t *C, int ldc,
+                       int M, int N, int K);
+/* Raw VNNI sum without the offset fixup: sum_k Au*Bq (gemm_bench.c:264-270). */
+long orc_gemm_u8s8_raw_i32(const uint8_t *Au, int lda, const int8_t *Bq, int ldb, int32_t *C,
+                           int ldc, int M, int N, int K);
+/* gemm_bench.c:260-285 gemm_int8_kernel restated in scalar C over the VNNI
+ * layout: v = sum Au*Bq - corr[n]; C = (float)v * dq[n]. M%8==0, N%16==0. */
+void orc_gemm_int8_kernel(const uint8_t *Au, int Kpad, const int8_t *Bp, const int32_t *corr,
+                          const float *dq, float *C, int M, int N);
+/* Dequant with the reference op order (gemm_bench.c:272-275, dq precomputed at :378):
+ *   rowcol: C = (float)v * (sa[m]*sb[n]);   col (sa==NULL): C = (float)v * sb[n] */
+void orc_dequant(const int32_t *V, int ldv, const float *sa, const float *sb, float *C, int ldc,
+                 int M, int N);
+/* gemm_bench.c:302-306 rms_rel and :53-57 max_abs_diff. */
+double orc_rms_rel(const float *X, const float *R, long n);
+double orc_max_abs_diff(const float *X, const float *Y, long n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* PCL_ORACLE_H */

@@ -1,0 +1,24 @@
+/*
+ * ref_shim_train.c -- build-time harness around the reference's own train.c
+ * (pure-c-llm), compiled where it lies with small -D dims from the Makefile.
+ * TEST INFRASTRUCTURE ONLY: exports its static GEMM functions
+ * (train.c:181-252, 412-447) under pcl_ref_* names to pin the oracle.
+ */
+#include REF_TRAIN_C
+
+int pcl_ref_train_d_model(void) { return D_MODEL; }
+int pcl_ref_train_vocab(void) { return VOCAB_SIZE; }
+void pcl_ref_matmul_forward(float *out, const float *in, const float *Wt, const float *bias, int M, int K, int N) {
+    matmul_forward(out, in, Wt, bias, M, K, N);
+}
+void pcl_ref_matmul_backward(const float *dY, const float *X, const float *Wt, float *dX, float *dW, float *db,
+                             int M, int K, int N) {
+    matmul_backward(dY, X, Wt, dX, dW, db, M, K, N);
+}
+void pcl_ref_tied_head_forward(float *logits, const float *lnf, const float *wte, int M) {
+    tied_head_forward(logits, lnf, wte, M);
+}
+void pcl_ref_tied_head_backward(float *d_lnf, float *dwte, const float *d_logits, const float *lnf,
+                                const float *wte, int M) {
+    tied_head_backward(d_lnf, dwte, d_logits, lnf, wte, M);
+}

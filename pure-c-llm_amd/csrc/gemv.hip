@@ -1,0 +1,489 @@
+// gemv.hip -- decode-shaped products (M <= 8 token rows), bound by HBM.
+//
+//   sgemv_n: Y = X.W + bias, W K x N row-major (N-contiguous):
+//            generate.c:95-107 matvec, transformer.c:174-195 proj_token.
+//   sgemv_t: Y = X.W^T + bias, W N x K (K-contiguous): the tied head,
+//            model.c:64-77 lm_head, generate.c:176-182.
+//   igemv:   u8 x s8 -> int32 over the packed N x Kp weights, with the same
+//            dequant epilogue as the INT8 GEMM (gemm_bench.c:260-285).
+//   bias_bwd (gpu_kernels.cu:102-108) is sgemv_n with X = ones.
+//
+// Every weight byte is read exactly once, with 16-byte loads along the
+// contiguous dimension; the few activation rows are staged in LDS per block.
+// To fill 256 CUs when N alone gives too few blocks, K is split across
+// blocks. Partial sums go to a workspace and the last block of each column
+// strip to arrive (an arrival counter, reset by that block) adds them in
+// split order, so results are deterministic run to run.
+#include "internal.h"
+
+namespace pcl {
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+constexpr int GV_THREADS = 256;
+constexpr int GV_TARGET_BLOCKS = 1024;   // ~4 per CU
+constexpr int SGN_KCH_MAX = 512;         // sgemv_n: staged X rows per block
+constexpr int SGT_KCH_MAX = 512;         // sgemv_t: staged X columns per block
+constexpr int IGV_KCH_MAX = 2048;        // igemv: staged X bytes per row per block
+constexpr int SGT_RPL = 2;               // sgemv_t / igemv rows per 16-lane group
+constexpr int SGT_ROWS = 16 * SGT_RPL;   // rows of W per block
+
+static int cdiv(long a, long b) { return (int)((a + b - 1) / b); }
+
+// Signals that this block is the last of `splits` to finish its strip.
+// Must be called by all threads after the block's partial stores.
+__device__ __forceinline__ bool last_block_arrived(unsigned *counters, int strip, int splits) {
+    __shared__ int is_last;
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned prev = atomicAdd(&counters[strip], 1u);
+        is_last = (prev == (unsigned)(splits - 1));
+    }
+    __syncthreads();
+    if (is_last) __threadfence();
+    return is_last != 0;
+}
+
+__device__ __forceinline__ void reset_counter(unsigned *counters, int strip) {
+    if (threadIdx.x == 0) atomicExch(&counters[strip], 0u);
+}
+
+// ------------------------------------------------------------- sgemv_n ----
+// Block = 64 columns x kchunk rows of W. Thread (c4 = tid%16, rg = tid/16)
+// owns columns 4*c4..4*c4+3 and a contiguous run of kchunk/16 rows.
+template <int MR, bool VEC, bool XONES>
+__global__ __launch_bounds__(GV_THREADS) void sgemv_n_kernel(
+    const float *__restrict__ X, long ldx, const float *__restrict__ W, long ldw,
+    const float *__restrict__ bias, float *__restrict__ Y, long ldy, int M, int N, int K,
+    int kchunk, int splits, float *__restrict__ part, unsigned *__restrict__ counters,
+    int accumulate) {
+    __shared__ float red[16][MR][64];
+    __shared__ float xs[XONES ? 1 : MR][XONES ? 1 : SGN_KCH_MAX];
+
+    const int tid = threadIdx.x;
+    const int c4 = tid & 15, rg = tid >> 4;
+    const int strip = blockIdx.x, sp = blockIdx.y;
+    const int n0 = strip * 64, col = n0 + 4 * c4;
+    const int kb = sp * kchunk;
+    const int run = kchunk / 16;  // multiple of 4
+
+    if (!XONES) {
+        for (int i = tid; i < MR * kchunk; i += GV_THREADS) {
+            int m = i / kchunk, kk = i % kchunk;
+            xs[m][kk] = (m < M && kb + kk < K) ? X[(long)m * ldx + kb + kk] : 0.f;
+        }
+        __syncthreads();
+    }
+
+    float acc[MR][4];
+#pragma unroll
+    for (int m = 0; m < MR; m++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[m][j] = 0.f;
+
+    const int r0 = rg * run;
+    for (int i = 0; i < run; i += 4) {
+        v4f w[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int k = kb + r0 + i + u;
+            w[u] = v4f{0.f, 0.f, 0.f, 0.f};
+            if (k < K) {
+                const float *src = W + (long)k * ldw + col;
+                if (VEC) {
+                    if (col < N) w[u] = *reinterpret_cast<const v4f *>(src);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 4; j++)
+                        if (col + j < N) w[u][j] = src[j];
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+#pragma unroll
+            for (int m = 0; m < MR; m++) {
+                const float xv = XONES ? 1.f : xs[m][r0 + i + u];
+#pragma unroll
+                for (int j = 0; j < 4; j++) acc[m][j] += xv * w[u][j];
+            }
+        }
+    }
+
+#pragma unroll
+    for (int m = 0; m < MR; m++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) red[rg][m][4 * c4 + j] = acc[m][j];
+    __syncthreads();
+
+    const int nround = gridDim.x * 64;
+    for (int o = tid; o < M * 64; o += GV_THREADS) {
+        const int m = o / 64, c = o % 64, n = n0 + c;
+        float s = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; r++) s += red[r][m][c];
+        if (splits == 1) {
+            if (n < N) {
+                float y = s + (bias ? bias[n] : 0.f);
+                float *dst = Y + (long)m * ldy + n;
+                *dst = accumulate ? *dst + y : y;
+            }
+        } else {
+            part[((long)sp * M + m) * nround + n] = s;
+        }
+    }
+    if (splits == 1) return;
+    if (!last_block_arrived(counters, strip, splits)) return;
+    for (int o = tid; o < M * 64; o += GV_THREADS) {
+        const int m = o / 64, c = o % 64, n = n0 + c;
+        if (n >= N) continue;
+        float s = 0.f;
+        for (int q = 0; q < splits; q++) s += part[((long)q * M + m) * nround + n];
+        float y = s + (bias ? bias[n] : 0.f);
+        float *dst = Y + (long)m * ldy + n;
+        *dst = accumulate ? *dst + y : y;
+    }
+    reset_counter(counters, strip);
+}
+
+// ------------------------------------------------------------- sgemv_t ----
+// Block = SGT_ROWS rows of W (N x K) x kchunk columns. Thread (j = tid%16,
+// rs = tid/16) reads 16-byte vectors k = 4j + 64i of rows rs + 16r.
+template <int MR, bool VEC>
+__global__ __launch_bounds__(GV_THREADS) void sgemv_t_kernel(
+    const float *__restrict__ X, long ldx, const float *__restrict__ W, long ldw,
+    const float *__restrict__ bias, float *__restrict__ Y, long ldy, int M, int N, int K,
+    int kchunk, int splits, float *__restrict__ part, unsigned *__restrict__ counters,
+    int accumulate) {
+    __shared__ __attribute__((aligned(16))) float xs[MR][SGT_KCH_MAX];
+    __shared__ float res[MR][SGT_ROWS];
+
+    const int tid = threadIdx.x;
+    const int j = tid & 15, rs = tid >> 4;
+    const int strip = blockIdx.x, sp = blockIdx.y;
+    const int n0 = strip * SGT_ROWS;
+    const int kb = sp * kchunk;
+    const int klen = min(kchunk, K - kb);
+
+    for (int i = tid; i < MR * kchunk; i += GV_THREADS) {
+        int m = i / kchunk, kk = i % kchunk;
+        xs[m][kk] = (m < M && kk < klen) ? X[(long)m * ldx + kb + kk] : 0.f;
+    }
+    __syncthreads();
+
+    float acc[SGT_RPL][MR];
+#pragma unroll
+    for (int r = 0; r < SGT_RPL; r++)
+#pragma unroll
+        for (int m = 0; m < MR; m++) acc[r][m] = 0.f;
+
+    for (int k = 4 * j; k < klen; k += 64) {
+        v4f xv[MR];
+#pragma unroll
+        for (int m = 0; m < MR; m++) xv[m] = *reinterpret_cast<const v4f *>(&xs[m][k]);
+#pragma unroll
+        for (int r = 0; r < SGT_RPL; r++) {
+            const int n = n0 + rs + 16 * r;
+            v4f w = {0.f, 0.f, 0.f, 0.f};
+            if (n < N) {
+                const float *src = W + (long)n * ldw + kb + k;
+                if (VEC) {
+                    w = *reinterpret_cast<const v4f *>(src);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+                        if (k + e < klen) w[e] = src[e];
+                }
+            }
+#pragma unroll
+            for (int m = 0; m < MR; m++)
+                acc[r][m] += xv[m][0] * w[0] + xv[m][1] * w[1] + xv[m][2] * w[2] + xv[m][3] * w[3];
+        }
+    }
+
+    // reduce over the 16 lanes of each row group (xor butterfly stays inside)
+#pragma unroll
+    for (int r = 0; r < SGT_RPL; r++)
+#pragma unroll
+        for (int m = 0; m < MR; m++) {
+            float v = acc[r][m];
+            v += __shfl_xor(v, 8, 16);
+            v += __shfl_xor(v, 4, 16);
+            v += __shfl_xor(v, 2, 16);
+            v += __shfl_xor(v, 1, 16);
+            acc[r][m] = v;
+        }
+    if (j == 0) {
+#pragma unroll
+        for (int r = 0; r < SGT_RPL; r++)
+#pragma unroll
+            for (int m = 0; m < MR; m++) res[m][rs + 16 * r] = acc[r][m];
+    }
+    __syncthreads();
+
+    const int nround = gridDim.x * SGT_ROWS;
+    for (int o = tid; o < M * SGT_ROWS; o += GV_THREADS) {
+        const int m = o / SGT_ROWS, c = o % SGT_ROWS, n = n0 + c;
+        const float s = res[m][c];
+        if (splits == 1) {
+            if (n < N) {
+                float y = s + (bias ? bias[n] : 0.f);
+                float *dst = Y + (long)m * ldy + n;
+                *dst = accumulate ? *dst + y : y;
+            }
+        } else {
+            part[((long)sp * M + m) * nround + n] = s;
+        }
+    }
+    if (splits == 1) return;
+    if (!last_block_arrived(counters, strip, splits)) return;
+    for (int o = tid; o < M * SGT_ROWS; o += GV_THREADS) {
+        const int m = o / SGT_ROWS, c = o % SGT_ROWS, n = n0 + c;
+        if (n >= N) continue;
+        float s = 0.f;
+        for (int q = 0; q < splits; q++) s += part[((long)q * M + m) * nround + n];
+        float y = s + (bias ? bias[n] : 0.f);
+        float *dst = Y + (long)m * ldy + n;
+        *dst = accumulate ? *dst + y : y;
+    }
+    reset_counter(counters, strip);
+}
+
+// --------------------------------------------------------------- igemv ----
+// Same geometry as sgemv_t over bytes: thread reads 16 weight bytes
+// (k = 16j + 256i) of rows rs + 16r; activations are staged re-centred
+// (x ^ 0x80 = x - 128) so v_dot4_i32_i8 accumulates sum (x-128)*w exactly.
+__device__ __forceinline__ int32_t epi_int(int32_t v, const int32_t *col_off, int n) {
+    return col_off ? (int32_t)((unsigned)v + (unsigned)col_off[n]) : v;
+}
+
+template <int MR, int OUT>
+__global__ __launch_bounds__(GV_THREADS) void igemv_kernel(
+    const uint8_t *__restrict__ X, long ldx, const int8_t *__restrict__ B, long ldb,
+    const int32_t *__restrict__ col_off, const float *__restrict__ sa,
+    const float *__restrict__ sb, void *__restrict__ Yv, long ldy, int M, int N, int K,
+    int kchunk, int splits, int32_t *__restrict__ part, unsigned *__restrict__ counters) {
+    __shared__ __attribute__((aligned(16))) int8_t xs[MR][IGV_KCH_MAX];
+    __shared__ int32_t res[MR][SGT_ROWS];
+
+    const int tid = threadIdx.x;
+    const int j = tid & 15, rs = tid >> 4;
+    const int strip = blockIdx.x, sp = blockIdx.y;
+    const int n0 = strip * SGT_ROWS;
+    const int kb = sp * kchunk;
+    // bytes of this split inside the packed rows (ldb >= roundup(K,16), zero pad)
+    const int kend = min(kb + kchunk, (K + 15) & ~15);
+    const int klen = kend - kb;
+
+    for (int i = tid; i < MR * kchunk; i += GV_THREADS) {
+        int m = i / kchunk, kk = i % kchunk;
+        int8_t v = 0;
+        if (m < M && kb + kk < K) v = (int8_t)(X[(long)m * ldx + kb + kk] ^ 0x80);
+        xs[m][kk] = v;
+    }
+    __syncthreads();
+
+    int32_t acc[SGT_RPL][MR];
+#pragma unroll
+    for (int r = 0; r < SGT_RPL; r++)
+#pragma unroll
+        for (int m = 0; m < MR; m++) acc[r][m] = 0;
+
+    for (int k = 16 * j; k < klen; k += 256) {
+        v4i xv[MR];
+#pragma unroll
+        for (int m = 0; m < MR; m++) xv[m] = *reinterpret_cast<const v4i *>(&xs[m][k]);
+#pragma unroll
+        for (int r = 0; r < SGT_RPL; r++) {
+            const int n = n0 + rs + 16 * r;
+            v4i w = {0, 0, 0, 0};
+            if (n < N) w = *reinterpret_cast<const v4i *>(B + (long)n * ldb + kb + k);
+#pragma unroll
+            for (int m = 0; m < MR; m++) {
+                int a = acc[r][m];
+                a = __builtin_amdgcn_sdot4(xv[m][0], w[0], a, false);
+                a = __builtin_amdgcn_sdot4(xv[m][1], w[1], a, false);
+                a = __builtin_amdgcn_sdot4(xv[m][2], w[2], a, false);
+                a = __builtin_amdgcn_sdot4(xv[m][3], w[3], a, false);
+                acc[r][m] = a;
+            }
+        }
+    }
+
+#pragma unroll
+    for (int r = 0; r < SGT_RPL; r++)
+#pragma unroll
+        for (int m = 0; m < MR; m++) {
+            int v = acc[r][m];
+            v += __shfl_xor(v, 8, 16);
+            v += __shfl_xor(v, 4, 16);
+            v += __shfl_xor(v, 2, 16);
+            v += __shfl_xor(v, 1, 16);
+            acc[r][m] = v;
+        }
+    if (j == 0) {
+#pragma unroll
+        for (int r = 0; r < SGT_RPL; r++)
+#pragma unroll
+            for (int m = 0; m < MR; m++) res[m][rs + 16 * r] = acc[r][m];
+    }
+    __syncthreads();
+
+    auto write_out = [&](int m, int n, int32_t v) {
+        v = epi_int(v, col_off, n);
+        if (OUT == 0) {
+            reinterpret_cast<int32_t *>(Yv)[(long)m * ldy + n] = v;
+        } else {
+            const float dq = (OUT == 2) ? sa[m] * sb[n] : sb[n];
+            reinterpret_cast<float *>(Yv)[(long)m * ldy + n] = (float)v * dq;
+        }
+    };
+
+    const int nround = gridDim.x * SGT_ROWS;
+    for (int o = tid; o < M * SGT_ROWS; o += GV_THREADS) {
+        const int m = o / SGT_ROWS, c = o % SGT_ROWS, n = n0 + c;
+        if (splits == 1) {
+            if (n < N) write_out(m, n, res[m][c]);
+        } else {
+            part[((long)sp * M + m) * nround + n] = res[m][c];
+        }
+    }
+    if (splits == 1) return;
+    if (!last_block_arrived(counters, strip, splits)) return;
+    for (int o = tid; o < M * SGT_ROWS; o += GV_THREADS) {
+        const int m = o / SGT_ROWS, c = o % SGT_ROWS, n = n0 + c;
+        if (n >= N) continue;
+        unsigned s = 0;
+        for (int q = 0; q < splits; q++) s += (unsigned)part[((long)q * M + m) * nround + n];
+        write_out(m, n, (int32_t)s);
+    }
+    reset_counter(counters, strip);
+}
+
+// ------------------------------------------------------------- planning ----
+static GemvPlan make_plan(int strips, int M, int K, int kstep, int kmax, int rows_per_strip) {
+    GemvPlan p;
+    p.strips = strips;
+    int want = GV_TARGET_BLOCKS / (strips > 0 ? strips : 1);
+    int max_splits = cdiv(K, kstep);
+    int splits = want < 1 ? 1 : want;
+    if (splits > max_splits) splits = max_splits;
+    if (splits < 1) splits = 1;
+    int kchunk = cdiv(cdiv(K, splits), kstep) * kstep;
+    if (kchunk > kmax) kchunk = kmax;
+    if (kchunk < kstep) kchunk = kstep;
+    splits = K > 0 ? cdiv(K, kchunk) : 1;
+    p.splits = splits;
+    p.kchunk = kchunk;
+    p.part_bytes = splits > 1 ? (size_t)splits * M * strips * rows_per_strip * 4 : 0;
+    return p;
+}
+
+GemvPlan plan_sgemv(int w_trans, int M, int N, int K) {
+    if (w_trans) return make_plan(cdiv(N, SGT_ROWS), M, K, 64, SGT_KCH_MAX, SGT_ROWS);
+    return make_plan(cdiv(N, 64), M, K, 64, SGN_KCH_MAX, 64);
+}
+
+GemvPlan plan_igemv(int M, int N, int K) {
+    return make_plan(cdiv(N, SGT_ROWS), M, K, 256, IGV_KCH_MAX, SGT_ROWS);
+}
+
+static bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+template <int MR>
+static void launch_sgemv_mr(const GemvPlan &p, int w_trans, bool vec, bool x_ones, int M, int N,
+                            int K, const float *X, long ldx, const float *W, long ldw,
+                            const float *bias, int accumulate, float *Y, long ldy,
+                            const Workspace &ws, hipStream_t s) {
+    dim3 grid(p.strips, p.splits), block(GV_THREADS);
+    float *part = (float *)ws.buf;
+    if (w_trans) {
+        if (vec)
+            hipLaunchKernelGGL((sgemv_t_kernel<MR, true>), grid, block, 0, s, X, ldx, W, ldw, bias,
+                               Y, ldy, M, N, K, p.kchunk, p.splits, part, ws.counters, accumulate);
+        else
+            hipLaunchKernelGGL((sgemv_t_kernel<MR, false>), grid, block, 0, s, X, ldx, W, ldw, bias,
+                               Y, ldy, M, N, K, p.kchunk, p.splits, part, ws.counters, accumulate);
+    } else if (x_ones) {
+        if (vec)
+            hipLaunchKernelGGL((sgemv_n_kernel<1, true, true>), grid, block, 0, s, X, ldx, W, ldw,
+                               bias, Y, ldy, M, N, K, p.kchunk, p.splits, part, ws.counters,
+                               accumulate);
+        else
+            hipLaunchKernelGGL((sgemv_n_kernel<1, false, true>), grid, block, 0, s, X, ldx, W, ldw,
+                               bias, Y, ldy, M, N, K, p.kchunk, p.splits, part, ws.counters,
+                               accumulate);
+    } else {
+        if (vec)
+            hipLaunchKernelGGL((sgemv_n_kernel<MR, true, false>), grid, block, 0, s, X, ldx, W, ldw,
+                               bias, Y, ldy, M, N, K, p.kchunk, p.splits, part, ws.counters,
+                               accumulate);
+        else
+            hipLaunchKernelGGL((sgemv_n_kernel<MR, false, false>), grid, block, 0, s, X, ldx, W,
+                               ldw, bias, Y, ldy, M, N, K, p.kchunk, p.splits, part, ws.counters,
+                               accumulate);
+    }
+}
+
+hipError_t launch_sgemv(const GemvPlan &p, int w_trans, int M, int N, int K, const float *X,
+                        long ldx, bool x_ones, const float *W, long ldw, const float *bias,
+                        int accumulate, float *Y, long ldy, const Workspace &ws,
+                        hipStream_t stream) {
+    if (M <= 0 || N <= 0) return hipSuccess;
+    bool vec = aligned16(W) && ldw % 4 == 0 && (w_trans ? K % 4 == 0 : N % 4 == 0);
+    if (x_ones) {
+        launch_sgemv_mr<1>(p, w_trans, vec, true, M, N, K, X, ldx, W, ldw, bias, accumulate, Y,
+                           ldy, ws, stream);
+    } else if (M == 1) {
+        launch_sgemv_mr<1>(p, w_trans, vec, false, M, N, K, X, ldx, W, ldw, bias, accumulate, Y,
+                           ldy, ws, stream);
+    } else if (M <= 2) {
+        launch_sgemv_mr<2>(p, w_trans, vec, false, M, N, K, X, ldx, W, ldw, bias, accumulate, Y,
+                           ldy, ws, stream);
+    } else if (M <= 4) {
+        launch_sgemv_mr<4>(p, w_trans, vec, false, M, N, K, X, ldx, W, ldw, bias, accumulate, Y,
+                           ldy, ws, stream);
+    } else {
+        launch_sgemv_mr<8>(p, w_trans, vec, false, M, N, K, X, ldx, W, ldw, bias, accumulate, Y,
+                           ldy, ws, stream);
+    }
+    return hipGetLastError();
+}
+
+template <int MR>
+static void launch_igemv_mr(const GemvPlan &p, int out_mode, int M, int N, int K,
+                            const uint8_t *X, long ldx, const int8_t *B, long ldb,
+                            const int32_t *col_off, const float *sa, const float *sb, void *Y,
+                            long ldy, const Workspace &ws, hipStream_t s) {
+    dim3 grid(p.strips, p.splits), block(GV_THREADS);
+    int32_t *part = (int32_t *)ws.buf;
+    if (out_mode == 0)
+        hipLaunchKernelGGL((igemv_kernel<MR, 0>), grid, block, 0, s, X, ldx, B, ldb, col_off, sa,
+                           sb, Y, ldy, M, N, K, p.kchunk, p.splits, part, ws.counters);
+    else if (out_mode == 1)
+        hipLaunchKernelGGL((igemv_kernel<MR, 1>), grid, block, 0, s, X, ldx, B, ldb, col_off, sa,
+                           sb, Y, ldy, M, N, K, p.kchunk, p.splits, part, ws.counters);
+    else
+        hipLaunchKernelGGL((igemv_kernel<MR, 2>), grid, block, 0, s, X, ldx, B, ldb, col_off, sa,
+                           sb, Y, ldy, M, N, K, p.kchunk, p.splits, part, ws.counters);
+}
+
+hipError_t launch_igemv(const GemvPlan &p, int out_mode, int M, int N, int K, const uint8_t *X,
+                        long ldx, const int8_t *Bpk, long ldb, const int32_t *col_off,
+                        const float *sa, const float *sb, void *Y, long ldy, const Workspace &ws,
+                        hipStream_t stream) {
+    if (M <= 0 || N <= 0) return hipSuccess;
+    if (M == 1)
+        launch_igemv_mr<1>(p, out_mode, M, N, K, X, ldx, Bpk, ldb, col_off, sa, sb, Y, ldy, ws, stream);
+    else if (M <= 2)
+        launch_igemv_mr<2>(p, out_mode, M, N, K, X, ldx, Bpk, ldb, col_off, sa, sb, Y, ldy, ws, stream);
+    else if (M <= 4)
+        launch_igemv_mr<4>(p, out_mode, M, N, K, X, ldx, Bpk, ldb, col_off, sa, sb, Y, ldy, ws, stream);
+    else
+        launch_igemv_mr<8>(p, out_mode, M, N, K, X, ldx, Bpk, ldb, col_off, sa, sb, Y, ldy, ws, stream);
+    return hipGetLastError();
+}
+
+}  // namespace pcl

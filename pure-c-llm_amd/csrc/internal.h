@@ -1,0 +1,107 @@
+// internal.h -- shared declarations between the HIP kernel files and the C-ABI
+// shim of libpcl_hip. Not part of the public ABI (that is include/pcl_hip.h).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace pcl {
+
+// Scratch memory that a launcher may use: partial sums of split-K GEMVs and
+// the per-strip arrival counters of their last-block reductions. The counters
+// are zero when a call starts and every kernel leaves them zero again.
+struct Workspace {
+    void *buf = nullptr;       // partial sums (bytes_cap bytes)
+    size_t bytes_cap = 0;
+    unsigned *counters = nullptr;  // counters_cap entries, kept all-zero
+    int counters_cap = 0;
+};
+
+// Split-K GEMV geometry chosen by the launchers; the shim sizes the workspace.
+struct GemvPlan {
+    int strips;      // blocks along N
+    int splits;      // blocks along K
+    int kchunk;      // K rows per split (multiple of the kernel's K step)
+    size_t part_bytes;  // workspace bytes for partials (0 when splits == 1)
+};
+
+// ---- FP32 GEMM (sgemm.hip) ----
+// C(M,N) = (accumulate ? C : 0) + op(A)(M,K) . op(B)(K,N) + bias
+// a_kcontig: element (m,k) of A at A[m*lda + k] (else A[k*lda + m]);
+// b_kcontig: element (k,n) of B at B[n*ldb + k] (else B[k*ldb + n]).
+hipError_t launch_sgemm(bool a_kcontig, bool b_kcontig, int M, int N, int K, const float *A,
+                        long lda, const float *B, long ldb, const float *bias, int accumulate,
+                        float *C, long ldc, hipStream_t stream);
+
+// ---- INT8 GEMM (igemm.hip) ----
+// out_mode 0: C is int32 v; 1: C = float(v+off)*sb[n]; 2: C = float(v+off)*(sa[m]*sb[n])
+// Requires K % 16 == 0, lda % 16 == 0, A and Bpk 16-byte aligned, ldb % 16 == 0.
+hipError_t launch_igemm(int out_mode, int M, int N, int K, const uint8_t *A, long lda,
+                        const int8_t *Bpk, long ldb, const int32_t *col_off, const float *sa,
+                        const float *sb, void *C, long ldc, hipStream_t stream);
+// Copy A (M x K, lda) into dst (M x K16, K16 = roundup(K,16)), padding with 0x80.
+hipError_t launch_pad_a_u8(const uint8_t *A, long lda, int M, int K, uint8_t *dst, int K16,
+                           hipStream_t stream);
+
+// ---- GEMV (gemv.hip) ----
+GemvPlan plan_sgemv(int w_trans, int M, int N, int K);
+GemvPlan plan_igemv(int M, int N, int K);
+// Y(M,N) = (accumulate ? Y : 0) + X(M,K) . op(W) + bias; M <= 8.
+// x_ones: X is the all-ones row (bias_bwd), X/ldx unused and M must be 1.
+hipError_t launch_sgemv(const GemvPlan &p, int w_trans, int M, int N, int K, const float *X,
+                        long ldx, bool x_ones, const float *W, long ldw, const float *bias,
+                        int accumulate, float *Y, long ldy, const Workspace &ws,
+                        hipStream_t stream);
+// INT8 GEMV over the packed layout (ldb = Kp); out_mode as in launch_igemm.
+hipError_t launch_igemv(const GemvPlan &p, int out_mode, int M, int N, int K, const uint8_t *X,
+                        long ldx, const int8_t *Bpk, long ldb, const int32_t *col_off,
+                        const float *sa, const float *sb, void *Y, long ldy, const Workspace &ws,
+                        hipStream_t stream);
+
+// ---- quantisers and packers (quant.hip) ----
+hipError_t launch_quantize_a_tensor(const float *A, int M, int K, uint8_t *Au, int Kpad,
+                                    float *scale_dev, unsigned *amax_bits, hipStream_t stream);
+hipError_t launch_quantize_a_rows(const float *A, int M, int K, uint8_t *Au, int Kpad, float *sa,
+                                  hipStream_t stream);
+// layout 0: native packed (N rows of ldb bytes); 1: reference VNNI (Kpad)
+hipError_t launch_quantize_b_cols(const float *B, int K, int N, int layout, int8_t *dst, long ldb,
+                                  int Kpad, float *bscale, int32_t *colsum, hipStream_t stream);
+hipError_t launch_pack_b_s8(const int8_t *B, long ldb_in, int K, int N, int8_t *Bpk, long ldb,
+                            int32_t *colsum, hipStream_t stream);
+hipError_t launch_pack_b_vnni(const int8_t *Bp, int K, int Kpad, int N, int8_t *Bpk, long ldb,
+                              int32_t *colsum, hipStream_t stream);
+// off[n] = 128*colsum[n] - corr[n]  (wrap-around int32)
+hipError_t launch_corr_to_offset(const int32_t *colsum, const int32_t *corr, int32_t *off, int N,
+                                 hipStream_t stream);
+
+}  // namespace pcl
+
+// ---- helpers shared by the kernels ----
+namespace pcl {
+
+// Workgroups are dispatched round-robin over the 8 XCDs of an MI355X
+// (workgroup i runs on XCD i % 8). Renumber them so that each XCD receives a
+// contiguous range of logical tiles; with the grouped tile order below those
+// tiles share A rows and B columns in that XCD's private L2.
+__device__ __forceinline__ int xcd_remap(int bid, int nblk) {
+    const int NX = 8;
+    int xcd = bid % NX, idx = bid / NX;
+    int q = nblk / NX, rem = nblk % NX;
+    return xcd * q + (xcd < rem ? xcd : rem) + idx;
+}
+
+// Grouped ("super-tile") order: walk GM tile-rows down a column strip before
+// moving right, so a wave of concurrent workgroups reuses a band of A and B.
+__device__ __forceinline__ void tile_coords(int logical, int nbm, int nbn, int GM, int &bm,
+                                            int &bn) {
+    int per_group = GM * nbn;
+    int group = logical / per_group;
+    int first_m = group * GM;
+    int gsz = nbm - first_m < GM ? nbm - first_m : GM;
+    int r = logical % per_group;
+    bm = first_m + r % gsz;
+    bn = r / gsz;
+}
+
+}  // namespace pcl

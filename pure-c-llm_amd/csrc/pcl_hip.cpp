@@ -1,0 +1,745 @@
+// pcl_hip.cpp -- the C ABI of libpcl_hip (include/pcl_hip.h): argument
+// checks, error reporting, streams, scratch workspaces, kernel dispatch and
+// the reference-signature drop-ins.
+//
+// Error convention: native pcl_* calls return a status (PCL_OK == 0) and
+// record a message; void drop-ins record the same and, when
+// pcl_set_abort_on_error(1) is in force, print it and exit(1) as the
+// reference's CUDA_CHECK does (gpu_kernels.h:34-36). Nothing ever falls back
+// to a CPU path: without a usable gfx950 device every call fails loudly.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/pcl_hip.h"
+#include "internal.h"
+
+namespace {
+
+// ----------------------------------------------------------- error state ----
+thread_local int t_status = PCL_OK;
+thread_local char t_msg[512] = "";
+thread_local hipStream_t t_stream = nullptr;
+int g_abort_on_error = 0;
+int g_d_model = 0, g_vocab = 0;
+
+int set_error(int status, const char *fmt, ...) {
+    t_status = status;
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(t_msg, sizeof t_msg, fmt, ap);
+    va_end(ap);
+    return status;
+}
+
+void finish_void(int status) {
+    if (status != PCL_OK && g_abort_on_error) {
+        fprintf(stderr, "libpcl_hip error %d: %s\n", status, t_msg);
+        exit(1);
+    }
+}
+
+#define HIP_OK(call)                                                                       \
+    do {                                                                                   \
+        hipError_t e_ = (call);                                                            \
+        if (e_ != hipSuccess)                                                              \
+            return set_error(PCL_ERR_HIP, "%s failed: %s", #call, hipGetErrorString(e_));  \
+    } while (0)
+
+#define CHECK_ARG(cond, ...)                                       \
+    do {                                                           \
+        if (!(cond)) return set_error(PCL_ERR_INVALID_ARG, __VA_ARGS__); \
+    } while (0)
+
+#define PCL_OK_OR_RETURN(expr)      \
+    do {                            \
+        int s_ = (expr);            \
+        if (s_ != PCL_OK) return s_; \
+    } while (0)
+
+// -------------------------------------------------------------- device ----
+std::mutex g_mu;
+bool g_inited = false;
+int g_init_status = PCL_OK;
+char g_init_msg[256] = "";
+
+int do_init() {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (g_inited) {
+        if (g_init_status != PCL_OK) return set_error(g_init_status, "%s", g_init_msg);
+        return PCL_OK;
+    }
+    g_inited = true;
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n == 0) {
+        g_init_status = PCL_ERR_NO_DEVICE;
+        snprintf(g_init_msg, sizeof g_init_msg, "no HIP device (%s)",
+                 e != hipSuccess ? hipGetErrorString(e) : "count 0");
+        return set_error(g_init_status, "%s", g_init_msg);
+    }
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    hipDeviceProp_t prop;
+    e = hipGetDeviceProperties(&prop, dev);
+    if (e != hipSuccess) {
+        g_init_status = PCL_ERR_HIP;
+        snprintf(g_init_msg, sizeof g_init_msg, "hipGetDeviceProperties: %s", hipGetErrorString(e));
+        return set_error(g_init_status, "%s", g_init_msg);
+    }
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        g_init_status = PCL_ERR_NO_DEVICE;
+        snprintf(g_init_msg, sizeof g_init_msg,
+                 "libpcl_hip is built for gfx950 only; device 0 is %s", prop.gcnArchName);
+        return set_error(g_init_status, "%s", g_init_msg);
+    }
+    return PCL_OK;
+}
+
+// ----------------------------------------------------------- workspaces ----
+// One scratch set per stream: work on one stream is ordered on the GPU, so
+// calls that share a stream may share its scratch.
+struct StreamScratch {
+    pcl::Workspace ws;
+    void *aux = nullptr;  // padded INT8 activations
+    size_t aux_cap = 0;
+    unsigned *amax = nullptr;  // per-tensor amax bits
+};
+std::unordered_map<hipStream_t, StreamScratch> g_scratch;
+
+int grow(void **p, size_t *cap, size_t need, hipStream_t s) {
+    if (need <= *cap) return PCL_OK;
+    size_t sz = need + need / 4 + 4096;
+    if (*p) {
+        HIP_OK(hipStreamSynchronize(s));
+        HIP_OK(hipFree(*p));
+        *p = nullptr;
+        *cap = 0;
+    }
+    if (hipMalloc(p, sz) != hipSuccess) {
+        *p = nullptr;
+        return set_error(PCL_ERR_OOM, "workspace allocation of %zu bytes failed", sz);
+    }
+    *cap = sz;
+    return PCL_OK;
+}
+
+int get_scratch(hipStream_t s, size_t part_bytes, int counters, size_t aux_bytes,
+                StreamScratch **out) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    StreamScratch &sc = g_scratch[s];
+    PCL_OK_OR_RETURN(grow(&sc.ws.buf, &sc.ws.bytes_cap, part_bytes, s));
+    PCL_OK_OR_RETURN(grow(&sc.aux, &sc.aux_cap, aux_bytes, s));
+    if (counters > sc.ws.counters_cap) {
+        if (sc.ws.counters) {
+            HIP_OK(hipStreamSynchronize(s));
+            HIP_OK(hipFree(sc.ws.counters));
+            sc.ws.counters = nullptr;
+            sc.ws.counters_cap = 0;
+        }
+        int cap = counters < 4096 ? 4096 : counters * 2;
+        if (hipMalloc((void **)&sc.ws.counters, sizeof(unsigned) * cap) != hipSuccess)
+            return set_error(PCL_ERR_OOM, "counter allocation failed");
+        HIP_OK(hipMemset(sc.ws.counters, 0, sizeof(unsigned) * cap));
+        sc.ws.counters_cap = cap;
+    }
+    if (!sc.amax) {
+        if (hipMalloc((void **)&sc.amax, 256) != hipSuccess)
+            return set_error(PCL_ERR_OOM, "amax scratch allocation failed");
+    }
+    *out = &sc;
+    return PCL_OK;
+}
+
+hipStream_t pick(void *stream) { return stream ? (hipStream_t)stream : t_stream; }
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+int kpad64(int K) { return ((K + 63) / 64) * 64; }
+
+// ------------------------------------------------------- host staging ----
+// Device copies of host operands for the host-pointer drop-ins; one growing
+// buffer per slot per thread, kept for the life of the process.
+struct HostStage {
+    void *p[8] = {nullptr};
+    size_t cap[8] = {0};
+};
+thread_local HostStage t_stage;
+
+int stage_buf(int slot, size_t bytes, void **out) {
+    if (bytes == 0) bytes = 16;
+    if (bytes > t_stage.cap[slot]) {
+        if (t_stage.p[slot]) {
+            HIP_OK(hipStreamSynchronize(t_stream));
+            HIP_OK(hipFree(t_stage.p[slot]));
+            t_stage.p[slot] = nullptr;
+            t_stage.cap[slot] = 0;
+        }
+        if (hipMalloc(&t_stage.p[slot], bytes) != hipSuccess) {
+            t_stage.p[slot] = nullptr;
+            return set_error(PCL_ERR_OOM, "staging allocation of %zu bytes failed", bytes);
+        }
+        t_stage.cap[slot] = bytes;
+    }
+    *out = t_stage.p[slot];
+    return PCL_OK;
+}
+
+// Upload `bytes` from host `src` into staging slot `slot` (src may be NULL:
+// then *dev is NULL too, for optional operands such as bias).
+int upload(int slot, const void *src, size_t bytes, void **dev) {
+    if (!src) {
+        *dev = nullptr;
+        return PCL_OK;
+    }
+    PCL_OK_OR_RETURN(stage_buf(slot, bytes, dev));
+    if (bytes) HIP_OK(hipMemcpyAsync(*dev, src, bytes, hipMemcpyHostToDevice, t_stream));
+    return PCL_OK;
+}
+
+int download(void *dst, const void *dev, size_t bytes) {
+    if (bytes) HIP_OK(hipMemcpyAsync(dst, dev, bytes, hipMemcpyDeviceToHost, t_stream));
+    return PCL_OK;
+}
+
+int sync_current() {
+    HIP_OK(hipStreamSynchronize(t_stream));
+    return PCL_OK;
+}
+
+}  // namespace
+
+// =========================================================================
+extern "C" {
+
+int pcl_init(void) { return do_init(); }
+int pcl_last_status(void) { return t_status; }
+const char *pcl_last_error(void) { return t_msg; }
+void pcl_clear_error(void) {
+    t_status = PCL_OK;
+    t_msg[0] = 0;
+}
+void pcl_set_abort_on_error(int on) { g_abort_on_error = on; }
+int pcl_set_stream(void *s) {
+    t_stream = (hipStream_t)s;
+    return PCL_OK;
+}
+void *pcl_get_stream(void) { return (void *)t_stream; }
+int pcl_stream_synchronize(void) {
+    PCL_OK_OR_RETURN(do_init());
+    return sync_current();
+}
+
+int pcl_device_info(char *name, int name_len, int *num_cus, int *clock_khz) {
+    PCL_OK_OR_RETURN(do_init());
+    int dev = 0;
+    HIP_OK(hipGetDevice(&dev));
+    hipDeviceProp_t prop;
+    HIP_OK(hipGetDeviceProperties(&prop, dev));
+    if (name && name_len > 0) snprintf(name, name_len, "%s (%s)", prop.name, prop.gcnArchName);
+    if (num_cus) *num_cus = prop.multiProcessorCount;
+    if (clock_khz) *clock_khz = prop.clockRate;
+    return PCL_OK;
+}
+
+void *pcl_malloc(size_t bytes) {
+    if (do_init() != PCL_OK) return nullptr;
+    void *p = nullptr;
+    if (hipMalloc(&p, bytes ? bytes : 16) != hipSuccess) {
+        set_error(PCL_ERR_OOM, "hipMalloc(%zu) failed", bytes);
+        return nullptr;
+    }
+    return p;
+}
+int pcl_free(void *p) {
+    if (!p) return PCL_OK;
+    HIP_OK(hipFree(p));
+    return PCL_OK;
+}
+int pcl_memcpy_h2d(void *dst, const void *src, size_t bytes) {
+    PCL_OK_OR_RETURN(do_init());
+    HIP_OK(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+    return PCL_OK;
+}
+int pcl_memcpy_d2h(void *dst, const void *src, size_t bytes) {
+    PCL_OK_OR_RETURN(do_init());
+    HIP_OK(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+    return PCL_OK;
+}
+int pcl_memcpy_d2d(void *dst, const void *src, size_t bytes) {
+    PCL_OK_OR_RETURN(do_init());
+    HIP_OK(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToDevice));
+    return PCL_OK;
+}
+int pcl_memset(void *dst, int value, size_t bytes) {
+    PCL_OK_OR_RETURN(do_init());
+    HIP_OK(hipMemset(dst, value, bytes));
+    return PCL_OK;
+}
+
+void *pcl_event_create(void) {
+    if (do_init() != PCL_OK) return nullptr;
+    hipEvent_t e;
+    if (hipEventCreate(&e) != hipSuccess) {
+        set_error(PCL_ERR_HIP, "hipEventCreate failed");
+        return nullptr;
+    }
+    return (void *)e;
+}
+int pcl_event_record(void *ev) {
+    HIP_OK(hipEventRecord((hipEvent_t)ev, t_stream));
+    return PCL_OK;
+}
+int pcl_event_elapsed_ms(void *start, void *stop, float *ms) {
+    HIP_OK(hipEventSynchronize((hipEvent_t)stop));
+    HIP_OK(hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)stop));
+    return PCL_OK;
+}
+int pcl_event_destroy(void *ev) {
+    HIP_OK(hipEventDestroy((hipEvent_t)ev));
+    return PCL_OK;
+}
+
+int pcl_set_model_dims(int d_model, int vocab_size) {
+    CHECK_ARG(d_model > 0 && vocab_size > 0, "pcl_set_model_dims: dims must be positive (%d, %d)",
+              d_model, vocab_size);
+    g_d_model = d_model;
+    g_vocab = vocab_size;
+    return PCL_OK;
+}
+
+// ----------------------------------------------------------- FP32 native ----
+int pcl_sgemv(int opW, int M, int N, int K, const float *X, int ldx, const float *W, int ldw,
+              const float *bias, int accumulate, float *Y, int ldy, void *stream) {
+    CHECK_ARG(M >= 0 && N >= 0 && K >= 0, "pcl_sgemv: negative dimension (M=%d N=%d K=%d)", M, N, K);
+    CHECK_ARG(M <= 8, "pcl_sgemv: M=%d exceeds the decode limit of 8 rows", M);
+    CHECK_ARG(opW == PCL_OP_N || opW == PCL_OP_T, "pcl_sgemv: bad opW %d", opW);
+    if (M == 0 || N == 0) return PCL_OK;
+    CHECK_ARG(Y != nullptr, "pcl_sgemv: Y is NULL");
+    CHECK_ARG(ldy >= N, "pcl_sgemv: ldy=%d < N=%d", ldy, N);
+    if (K > 0) {
+        CHECK_ARG(X && W, "pcl_sgemv: NULL operand");
+        CHECK_ARG(ldx >= K, "pcl_sgemv: ldx=%d < K=%d", ldx, K);
+        CHECK_ARG(ldw >= (opW == PCL_OP_N ? N : K), "pcl_sgemv: ldw=%d too small", ldw);
+    }
+    PCL_OK_OR_RETURN(do_init());
+    hipStream_t s = pick(stream);
+    pcl::GemvPlan p = pcl::plan_sgemv(opW == PCL_OP_T, M, N, K);
+    StreamScratch *sc;
+    PCL_OK_OR_RETURN(get_scratch(s, p.part_bytes, p.strips, 0, &sc));
+    HIP_OK(pcl::launch_sgemv(p, opW == PCL_OP_T, M, N, K, X, ldx, false, W, ldw, bias, accumulate,
+                             Y, ldy, sc->ws, s));
+    return PCL_OK;
+}
+
+int pcl_sgemm(int opA, int opB, int M, int N, int K, const float *A, int lda, const float *B,
+              int ldb, const float *bias, int accumulate, float *C, int ldc, void *stream) {
+    CHECK_ARG(M >= 0 && N >= 0 && K >= 0, "pcl_sgemm: negative dimension (M=%d N=%d K=%d)", M, N, K);
+    CHECK_ARG((opA == PCL_OP_N || opA == PCL_OP_T) && (opB == PCL_OP_N || opB == PCL_OP_T),
+              "pcl_sgemm: bad op (%d, %d)", opA, opB);
+    if (M == 0 || N == 0) return PCL_OK;
+    CHECK_ARG(C != nullptr, "pcl_sgemm: C is NULL");
+    CHECK_ARG(ldc >= N, "pcl_sgemm: ldc=%d < N=%d", ldc, N);
+    if (K > 0) {
+        CHECK_ARG(A && B, "pcl_sgemm: NULL operand");
+        CHECK_ARG(lda >= (opA == PCL_OP_N ? K : M), "pcl_sgemm: lda=%d too small", lda);
+        CHECK_ARG(ldb >= (opB == PCL_OP_N ? N : K), "pcl_sgemm: ldb=%d too small", ldb);
+    }
+    PCL_OK_OR_RETURN(do_init());
+    if (M <= 8 && opA == PCL_OP_N)
+        return pcl_sgemv(opB, M, N, K, A, lda, B, ldb, bias, accumulate, C, ldc, stream);
+    HIP_OK(pcl::launch_sgemm(opA == PCL_OP_N, opB == PCL_OP_T, M, N, K, A, lda, B, ldb, bias,
+                             accumulate, C, ldc, pick(stream)));
+    return PCL_OK;
+}
+
+int pcl_bias_bwd(float *db, const float *dY, int M, int N, int ld, void *stream) {
+    CHECK_ARG(M >= 0 && N >= 0, "pcl_bias_bwd: negative dimension");
+    if (N == 0) return PCL_OK;
+    CHECK_ARG(db != nullptr, "pcl_bias_bwd: db is NULL");
+    if (M > 0) {
+        CHECK_ARG(dY != nullptr, "pcl_bias_bwd: dY is NULL");
+        CHECK_ARG(ld >= N, "pcl_bias_bwd: ld=%d < N=%d", ld, N);
+    }
+    PCL_OK_OR_RETURN(do_init());
+    hipStream_t s = pick(stream);
+    pcl::GemvPlan p = pcl::plan_sgemv(0, 1, N, M);
+    StreamScratch *sc;
+    PCL_OK_OR_RETURN(get_scratch(s, p.part_bytes, p.strips, 0, &sc));
+    HIP_OK(pcl::launch_sgemv(p, 0, 1, N, M, nullptr, 0, true, dY, ld, nullptr, 1, db, N, sc->ws, s));
+    return PCL_OK;
+}
+
+// ----------------------------------------------------------- INT8 native ----
+int pcl_s8_kpad(int K) { return kpad64(K < 0 ? 0 : K); }
+size_t pcl_s8_packed_bytes(int K, int N) {
+    return (size_t)(N < 0 ? 0 : N) * (size_t)pcl_s8_kpad(K);
+}
+
+int pcl_pack_b_s8(const int8_t *B, int ldb, int K, int N, int8_t *Bpk, int32_t *colsum,
+                  void *stream) {
+    CHECK_ARG(K >= 0 && N >= 0, "pcl_pack_b_s8: negative dimension");
+    if (N == 0) return PCL_OK;
+    CHECK_ARG(Bpk != nullptr && (K == 0 || B != nullptr), "pcl_pack_b_s8: NULL operand");
+    CHECK_ARG(K == 0 || ldb >= N, "pcl_pack_b_s8: ldb=%d < N=%d", ldb, N);
+    PCL_OK_OR_RETURN(do_init());
+    HIP_OK(pcl::launch_pack_b_s8(B, ldb, K, N, Bpk, kpad64(K), colsum, pick(stream)));
+    return PCL_OK;
+}
+
+int pcl_pack_b_vnni(const int8_t *Bp, int K, int Kpad, int N, int8_t *Bpk, int32_t *colsum,
+                    void *stream) {
+    CHECK_ARG(K >= 0 && N >= 0 && Kpad >= K && Kpad % 4 == 0,
+              "pcl_pack_b_vnni: need 0 <= K <= Kpad, Kpad %% 4 == 0 (K=%d Kpad=%d)", K, Kpad);
+    CHECK_ARG(N % 16 == 0, "pcl_pack_b_vnni: N=%d is not a multiple of 16", N);
+    if (N == 0) return PCL_OK;
+    CHECK_ARG(Bpk != nullptr && (K == 0 || Bp != nullptr), "pcl_pack_b_vnni: NULL operand");
+    CHECK_ARG((reinterpret_cast<uintptr_t>(Bp) & 3) == 0, "pcl_pack_b_vnni: Bp not 4-byte aligned");
+    PCL_OK_OR_RETURN(do_init());
+    HIP_OK(pcl::launch_pack_b_vnni(Bp, K, Kpad, N, Bpk, kpad64(K), colsum, pick(stream)));
+    return PCL_OK;
+}
+
+static int check_i8_range(int K) {
+    // |sum (a-128)*b| <= K * 128 * 128 must fit int32 (K <= 131071).
+    if ((long long)K * 128 * 128 > 2147483647LL)
+        return set_error(PCL_ERR_RANGE, "K=%d may overflow the int32 accumulator", K);
+    return PCL_OK;
+}
+
+static int igemm_common(int out_mode, const uint8_t *A, int lda, const int8_t *Bpk,
+                        const int32_t *col_off, const float *sa, const float *sb, void *C, int ldc,
+                        int M, int N, int K, void *stream, const char *who) {
+    CHECK_ARG(M >= 0 && N >= 0 && K >= 0, "%s: negative dimension (M=%d N=%d K=%d)", who, M, N, K);
+    PCL_OK_OR_RETURN(check_i8_range(K));
+    if (M == 0 || N == 0) return PCL_OK;
+    CHECK_ARG(C && Bpk && (K == 0 || A), "%s: NULL operand", who);
+    CHECK_ARG(ldc >= N, "%s: ldc=%d < N=%d", who, ldc, N);
+    CHECK_ARG(K == 0 || lda >= K, "%s: lda=%d < K=%d", who, lda, K);
+    CHECK_ARG(out_mode == 0 || sb, "%s: sb is NULL", who);
+    CHECK_ARG(out_mode != 2 || sa, "%s: sa is NULL", who);
+    CHECK_ARG(aligned16(Bpk), "%s: packed weights must be 16-byte aligned", who);
+    PCL_OK_OR_RETURN(do_init());
+    const long ldb = kpad64(K);
+    hipStream_t s = pick(stream);
+    if (M <= 8) {
+        pcl::GemvPlan p = pcl::plan_igemv(M, N, K);
+        StreamScratch *sc;
+        PCL_OK_OR_RETURN(get_scratch(s, p.part_bytes, p.strips, 0, &sc));
+        HIP_OK(pcl::launch_igemv(p, out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa, sb, C, ldc,
+                                 sc->ws, s));
+        return PCL_OK;
+    }
+    if (K % 16 == 0 && lda % 16 == 0 && aligned16(A)) {
+        HIP_OK(pcl::launch_igemm(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa, sb, C, ldc, s));
+        return PCL_OK;
+    }
+    // Unaligned activations: copy into a K16-wide padded buffer first.
+    const int K16 = (K + 15) & ~15;
+    StreamScratch *sc;
+    PCL_OK_OR_RETURN(get_scratch(s, 0, 0, (size_t)M * K16, &sc));
+    uint8_t *Ap = (uint8_t *)sc->aux;
+    HIP_OK(pcl::launch_pad_a_u8(A, lda, M, K, Ap, K16, s));
+    HIP_OK(pcl::launch_igemm(out_mode, M, N, K16, Ap, K16, Bpk, ldb, col_off, sa, sb, C, ldc, s));
+    return PCL_OK;
+}
+
+int pcl_gemm_u8s8_i32(const uint8_t *A, int lda, const int8_t *Bpk, int32_t *C, int ldc, int M,
+                      int N, int K, void *stream) {
+    return igemm_common(0, A, lda, Bpk, nullptr, nullptr, nullptr, C, ldc, M, N, K, stream,
+                        "pcl_gemm_u8s8_i32");
+}
+
+int pcl_gemm_u8s8_dq(const uint8_t *A, int lda, const int8_t *Bpk, const int32_t *col_off,
+                     const float *sa, const float *sb, float *C, int ldc, int M, int N, int K,
+                     void *stream) {
+    return igemm_common(sa ? 2 : 1, A, lda, Bpk, col_off, sa, sb, C, ldc, M, N, K, stream,
+                        "pcl_gemm_u8s8_dq");
+}
+
+int pcl_gemv_u8s8_i32(const uint8_t *X, int ldx, const int8_t *Bpk, int32_t *Y, int ldy, int M,
+                      int N, int K, void *stream) {
+    if (M > 8) return set_error(PCL_ERR_INVALID_ARG, "pcl_gemv_u8s8_i32: M=%d > 8", M);
+    return igemm_common(0, X, ldx, Bpk, nullptr, nullptr, nullptr, Y, ldy, M, N, K, stream,
+                        "pcl_gemv_u8s8_i32");
+}
+
+int pcl_gemv_u8s8_dq(const uint8_t *X, int ldx, const int8_t *Bpk, const int32_t *col_off,
+                     const float *sa, const float *sb, float *Y, int ldy, int M, int N, int K,
+                     void *stream) {
+    if (M > 8) return set_error(PCL_ERR_INVALID_ARG, "pcl_gemv_u8s8_dq: M=%d > 8", M);
+    return igemm_common(sa ? 2 : 1, X, ldx, Bpk, col_off, sa, sb, Y, ldy, M, N, K, stream,
+                        "pcl_gemv_u8s8_dq");
+}
+
+int pcl_quantize_a_tensor(const float *A, int M, int K, uint8_t *Au, int Kpad, float *scale_dev,
+                          void *stream) {
+    CHECK_ARG(M >= 0 && K >= 0 && Kpad >= K, "pcl_quantize_a_tensor: bad dims (M=%d K=%d Kpad=%d)",
+              M, K, Kpad);
+    CHECK_ARG(Au && scale_dev && (M * (long)K == 0 || A), "pcl_quantize_a_tensor: NULL operand");
+    PCL_OK_OR_RETURN(do_init());
+    hipStream_t s = pick(stream);
+    StreamScratch *sc;
+    PCL_OK_OR_RETURN(get_scratch(s, 0, 0, 0, &sc));
+    HIP_OK(pcl::launch_quantize_a_tensor(A, M, K, Au, Kpad, scale_dev, sc->amax, s));
+    return PCL_OK;
+}
+
+int pcl_quantize_a_rows(const float *A, int M, int K, uint8_t *Au, int Kpad, float *sa,
+                        void *stream) {
+    CHECK_ARG(M >= 0 && K >= 0 && Kpad >= K, "pcl_quantize_a_rows: bad dims (M=%d K=%d Kpad=%d)",
+              M, K, Kpad);
+    if (M == 0) return PCL_OK;
+    CHECK_ARG(Au && sa && (K == 0 || A), "pcl_quantize_a_rows: NULL operand");
+    PCL_OK_OR_RETURN(do_init());
+    HIP_OK(pcl::launch_quantize_a_rows(A, M, K, Au, Kpad, sa, pick(stream)));
+    return PCL_OK;
+}
+
+int pcl_quantize_b_cols(const float *B, int K, int N, int8_t *Bpk, float *bscale, int32_t *colsum,
+                        void *stream) {
+    CHECK_ARG(K >= 0 && N >= 0, "pcl_quantize_b_cols: negative dimension");
+    if (N == 0) return PCL_OK;
+    CHECK_ARG(Bpk && bscale && (K == 0 || B), "pcl_quantize_b_cols: NULL operand");
+    PCL_OK_OR_RETURN(do_init());
+    HIP_OK(pcl::launch_quantize_b_cols(B, K, N, 0, Bpk, kpad64(K), 0, bscale, colsum, pick(stream)));
+    return PCL_OK;
+}
+
+int pcl_quantize_b_vnni(const float *B, int K, int N, int Kpad, int8_t *Bp, float *bscale,
+                        int32_t *colsum, void *stream) {
+    CHECK_ARG(K >= 0 && N >= 0 && Kpad >= K && Kpad % 4 == 0,
+              "pcl_quantize_b_vnni: need 0 <= K <= Kpad, Kpad %% 4 == 0");
+    CHECK_ARG(N % 16 == 0, "pcl_quantize_b_vnni: N=%d is not a multiple of 16", N);
+    if (N == 0) return PCL_OK;
+    CHECK_ARG(Bp && bscale && (K == 0 || B), "pcl_quantize_b_vnni: NULL operand");
+    PCL_OK_OR_RETURN(do_init());
+    HIP_OK(pcl::launch_quantize_b_cols(B, K, N, 1, Bp, 0, Kpad, bscale, colsum, pick(stream)));
+    return PCL_OK;
+}
+
+// ------------------------------------------------- device-pointer drop-ins ----
+void gpu_init(void) { finish_void(pcl_init()); }
+
+void gemm_nn(const float *A, const float *B, const float *bias, float *C, int M, int K, int N) {
+    finish_void(pcl_sgemm(PCL_OP_N, PCL_OP_N, M, N, K, A, K, B, N, bias, 0, C, N, nullptr));
+}
+void gemm_nt(const float *A, const float *B, float *C, int M, int K, int N, int accum) {
+    finish_void(pcl_sgemm(PCL_OP_N, PCL_OP_T, M, N, K, A, K, B, K, nullptr, accum ? 1 : 0, C, N,
+                          nullptr));
+}
+void gemm_tn(const float *A, const float *B, float *C, int M, int K, int N) {
+    finish_void(pcl_sgemm(PCL_OP_T, PCL_OP_N, K, N, M, A, K, B, N, nullptr, 1, C, N, nullptr));
+}
+void bias_bwd(float *db, const float *dY, int M, int N) {
+    finish_void(pcl_bias_bwd(db, dY, M, N, N, nullptr));
+}
+
+// --------------------------------------------------- host-pointer drop-ins ----
+// Slot numbers name the staging buffer each operand uses.
+enum { S_A = 0, S_B, S_C, S_BIAS, S_D, S_E, S_F, S_G };
+
+static int host_sgemm(int opA, int opB, int M, int N, int K, const float *A, const float *B,
+                      const float *bias, int accumulate, float *C) {
+    CHECK_ARG(M >= 0 && N >= 0 && K >= 0, "negative dimension (M=%d N=%d K=%d)", M, N, K);
+    if (M == 0 || N == 0) return PCL_OK;
+    CHECK_ARG(C && (K == 0 || (A && B)), "NULL operand");
+    PCL_OK_OR_RETURN(do_init());
+    void *dA, *dB, *dC, *dbias;
+    PCL_OK_OR_RETURN(upload(S_A, K ? A : nullptr, sizeof(float) * (size_t)M * K, &dA));
+    PCL_OK_OR_RETURN(upload(S_B, K ? B : nullptr, sizeof(float) * (size_t)K * N, &dB));
+    PCL_OK_OR_RETURN(upload(S_BIAS, bias, sizeof(float) * (size_t)N, &dbias));
+    if (accumulate) PCL_OK_OR_RETURN(upload(S_C, C, sizeof(float) * (size_t)M * N, &dC));
+    else PCL_OK_OR_RETURN(stage_buf(S_C, sizeof(float) * (size_t)M * N, &dC));
+    const int lda = opA == PCL_OP_N ? K : M, ldb = opB == PCL_OP_N ? N : K;
+    PCL_OK_OR_RETURN(pcl_sgemm(opA, opB, M, N, K, (const float *)dA, lda, (const float *)dB, ldb,
+                               (const float *)dbias, accumulate, (float *)dC, N, t_stream));
+    PCL_OK_OR_RETURN(download(C, dC, sizeof(float) * (size_t)M * N));
+    return sync_current();
+}
+
+void matmul(const float *A, const float *B, float *C, int M, int K, int N) {
+    finish_void(host_sgemm(PCL_OP_N, PCL_OP_N, M, N, K, A, B, nullptr, 0, C));
+}
+
+void matmul_forward(float *out, const float *in, const float *Wt, const float *bias, int M, int K,
+                    int N) {
+    finish_void(host_sgemm(PCL_OP_N, PCL_OP_N, M, N, K, in, Wt, bias, 0, out));
+}
+
+static int host_matmul_backward(const float *dY, const float *X, const float *Wt, float *dX,
+                                float *dW, float *db, int M, int K, int N) {
+    CHECK_ARG(M >= 0 && N >= 0 && K >= 0, "matmul_backward: negative dimension");
+    CHECK_ARG(dY && X && Wt && dX && dW, "matmul_backward: NULL operand");
+    PCL_OK_OR_RETURN(do_init());
+    void *ddY, *dXin, *dWt, *ddX, *ddW, *ddb;
+    PCL_OK_OR_RETURN(upload(S_A, dY, sizeof(float) * (size_t)M * N, &ddY));
+    PCL_OK_OR_RETURN(upload(S_B, X, sizeof(float) * (size_t)M * K, &dXin));
+    PCL_OK_OR_RETURN(upload(S_D, Wt, sizeof(float) * (size_t)K * N, &dWt));
+    PCL_OK_OR_RETURN(upload(S_C, dX, sizeof(float) * (size_t)M * K, &ddX));
+    PCL_OK_OR_RETURN(upload(S_E, dW, sizeof(float) * (size_t)K * N, &ddW));
+    PCL_OK_OR_RETURN(upload(S_BIAS, db, sizeof(float) * (size_t)N, &ddb));
+    // dX(M,K) += dY(M,N) . W(K,N)^T      (train.c:221-232)
+    PCL_OK_OR_RETURN(pcl_sgemm(PCL_OP_N, PCL_OP_T, M, K, N, (const float *)ddY, N,
+                               (const float *)dWt, N, nullptr, 1, (float *)ddX, K, t_stream));
+    // dW(K,N) += X(M,K)^T . dY(M,N)      (train.c:233-242)
+    PCL_OK_OR_RETURN(pcl_sgemm(PCL_OP_T, PCL_OP_N, K, N, M, (const float *)dXin, K,
+                               (const float *)ddY, N, nullptr, 1, (float *)ddW, N, t_stream));
+    // db(N) += colsum(dY)                (train.c:243-251)
+    if (db) PCL_OK_OR_RETURN(pcl_bias_bwd((float *)ddb, (const float *)ddY, M, N, N, t_stream));
+    PCL_OK_OR_RETURN(download(dX, ddX, sizeof(float) * (size_t)M * K));
+    PCL_OK_OR_RETURN(download(dW, ddW, sizeof(float) * (size_t)K * N));
+    if (db) PCL_OK_OR_RETURN(download(db, ddb, sizeof(float) * (size_t)N));
+    return sync_current();
+}
+
+void matmul_backward(const float *dY, const float *X, const float *Wt, float *dX, float *dW,
+                     float *db, int M, int K, int N) {
+    finish_void(host_matmul_backward(dY, X, Wt, dX, dW, db, M, K, N));
+}
+
+static int need_dims(const char *who) {
+    if (g_d_model <= 0 || g_vocab <= 0)
+        return set_error(PCL_ERR_UNSET_DIMS, "%s: call pcl_set_model_dims(d_model, vocab) first", who);
+    return PCL_OK;
+}
+
+void tied_head_forward(float *logits, const float *lnf, const float *wte, int M) {
+    int st = need_dims("tied_head_forward");
+    if (st == PCL_OK) st = host_sgemm(PCL_OP_N, PCL_OP_T, M, g_vocab, g_d_model, lnf, wte, nullptr, 0, logits);
+    finish_void(st);
+}
+
+static int host_tied_head_backward(float *d_lnf, float *dwte, const float *d_logits,
+                                   const float *lnf, const float *wte, int M) {
+    PCL_OK_OR_RETURN(need_dims("tied_head_backward"));
+    PCL_OK_OR_RETURN(do_init());
+    const int D = g_d_model, V = g_vocab;
+    CHECK_ARG(M >= 0, "tied_head_backward: negative M");
+    CHECK_ARG(d_lnf && dwte && d_logits && lnf && wte, "tied_head_backward: NULL operand");
+    void *ddl, *dlnf, *dwt, *ddlnf, *ddwte;
+    PCL_OK_OR_RETURN(upload(S_A, d_logits, sizeof(float) * (size_t)M * V, &ddl));
+    PCL_OK_OR_RETURN(upload(S_B, lnf, sizeof(float) * (size_t)M * D, &dlnf));
+    PCL_OK_OR_RETURN(upload(S_D, wte, sizeof(float) * (size_t)V * D, &dwt));
+    PCL_OK_OR_RETURN(stage_buf(S_C, sizeof(float) * (size_t)M * D, &ddlnf));
+    PCL_OK_OR_RETURN(upload(S_E, dwte, sizeof(float) * (size_t)V * D, &ddwte));
+    // d_lnf(M,D) = d_logits(M,V) . wte(V,D)        (train.c:426-435, SET)
+    PCL_OK_OR_RETURN(pcl_sgemm(PCL_OP_N, PCL_OP_N, M, D, V, (const float *)ddl, V,
+                               (const float *)dwt, D, nullptr, 0, (float *)ddlnf, D, t_stream));
+    // dwte(V,D) += d_logits(M,V)^T . lnf(M,D)      (train.c:436-446)
+    PCL_OK_OR_RETURN(pcl_sgemm(PCL_OP_T, PCL_OP_N, V, D, M, (const float *)ddl, V,
+                               (const float *)dlnf, D, nullptr, 1, (float *)ddwte, D, t_stream));
+    PCL_OK_OR_RETURN(download(d_lnf, ddlnf, sizeof(float) * (size_t)M * D));
+    PCL_OK_OR_RETURN(download(dwte, ddwte, sizeof(float) * (size_t)V * D));
+    return sync_current();
+}
+
+void tied_head_backward(float *d_lnf, float *dwte, const float *d_logits, const float *lnf,
+                        const float *wte, int M) {
+    finish_void(host_tied_head_backward(d_lnf, dwte, d_logits, lnf, wte, M));
+}
+
+void lm_head(float *logits, const float *x, const float *wte, int num_tokens) {
+    int st = need_dims("lm_head");
+    if (st == PCL_OK)
+        st = host_sgemm(PCL_OP_N, PCL_OP_T, num_tokens, g_vocab, g_d_model, x, wte, nullptr, 0, logits);
+    finish_void(st);
+}
+
+void proj_token(float *out, const float *in, const float *W, const float *bias, int K, int N) {
+    finish_void(host_sgemm(PCL_OP_N, PCL_OP_N, 1, N, K, in, W, bias, 0, out));
+}
+
+void matvec(float *out, const float *x, const float *W, const float *b, int K, int N) {
+    finish_void(host_sgemm(PCL_OP_N, PCL_OP_N, 1, N, K, x, W, b, 0, out));
+}
+
+static int host_quantize_A(const float *A, uint8_t *Au, int M, int K, int Kpad, float *scale) {
+    CHECK_ARG(M >= 0 && K >= 0 && Kpad >= K, "quantize_A: bad dims (M=%d K=%d Kpad=%d)", M, K, Kpad);
+    CHECK_ARG(Au && (M * (long)K == 0 || A), "quantize_A: NULL operand");
+    PCL_OK_OR_RETURN(do_init());
+    void *dA, *dAu, *dS;
+    PCL_OK_OR_RETURN(upload(S_A, A, sizeof(float) * (size_t)M * K, &dA));
+    PCL_OK_OR_RETURN(stage_buf(S_B, (size_t)M * Kpad, &dAu));
+    PCL_OK_OR_RETURN(stage_buf(S_D, sizeof(float), &dS));
+    PCL_OK_OR_RETURN(pcl_quantize_a_tensor((const float *)dA, M, K, (uint8_t *)dAu, Kpad,
+                                           (float *)dS, t_stream));
+    PCL_OK_OR_RETURN(download(Au, dAu, (size_t)M * Kpad));
+    PCL_OK_OR_RETURN(download(scale, dS, sizeof(float)));
+    return sync_current();
+}
+
+float quantize_A(const float *A, uint8_t *Au, int M, int K, int Kpad) {
+    float scale = NAN;
+    finish_void(host_quantize_A(A, Au, M, K, Kpad, &scale));
+    return scale;
+}
+
+static int host_quantize_B_pack(const float *B, int8_t *Bp, float *bscale, int32_t *colsum, int K,
+                                int N, int Kpad) {
+    CHECK_ARG(B && Bp && bscale && colsum, "quantize_B_pack: NULL operand");
+    CHECK_ARG(N >= 0 && N % 16 == 0, "quantize_B_pack: N=%d is not a multiple of 16", N);
+    CHECK_ARG(K >= 0 && Kpad >= K && Kpad % 4 == 0, "quantize_B_pack: bad K=%d Kpad=%d", K, Kpad);
+    PCL_OK_OR_RETURN(do_init());
+    const size_t bp_bytes = (size_t)(N / 16) * (Kpad / 4) * 64;
+    void *dB, *dBp, *dsc, *dcs;
+    PCL_OK_OR_RETURN(upload(S_A, B, sizeof(float) * (size_t)K * N, &dB));
+    PCL_OK_OR_RETURN(stage_buf(S_B, bp_bytes, &dBp));
+    PCL_OK_OR_RETURN(stage_buf(S_D, sizeof(float) * (size_t)N, &dsc));
+    PCL_OK_OR_RETURN(stage_buf(S_E, sizeof(int32_t) * (size_t)N, &dcs));
+    PCL_OK_OR_RETURN(pcl_quantize_b_vnni((const float *)dB, K, N, Kpad, (int8_t *)dBp,
+                                         (float *)dsc, (int32_t *)dcs, t_stream));
+    PCL_OK_OR_RETURN(download(Bp, dBp, bp_bytes));
+    PCL_OK_OR_RETURN(download(bscale, dsc, sizeof(float) * (size_t)N));
+    PCL_OK_OR_RETURN(download(colsum, dcs, sizeof(int32_t) * (size_t)N));
+    return sync_current();
+}
+
+void quantize_B_pack(const float *B, int8_t *Bp, float *bscale, int32_t *colsum, int K, int N,
+                     int Kpad) {
+    finish_void(host_quantize_B_pack(B, Bp, bscale, colsum, K, N, Kpad));
+}
+
+static int host_gemm_int8_kernel(const uint8_t *Au, int Kpad, const int8_t *Bp,
+                                 const int32_t *corr, const float *dq, float *C, int M, int N) {
+    CHECK_ARG(M >= 0 && N >= 0 && Kpad >= 0 && Kpad % 4 == 0,
+              "gemm_int8_kernel: bad dims (M=%d N=%d Kpad=%d)", M, N, Kpad);
+    CHECK_ARG(N % 16 == 0, "gemm_int8_kernel: N=%d is not a multiple of 16", N);
+    if (M == 0 || N == 0) return PCL_OK;
+    CHECK_ARG(Au && Bp && corr && dq && C, "gemm_int8_kernel: NULL operand");
+    PCL_OK_OR_RETURN(do_init());
+    const int K = Kpad;  // the reference kernel runs over all Kpad bytes
+    const size_t bp_bytes = (size_t)(N / 16) * (Kpad / 4) * 64;
+    void *dAu, *dBp, *dcorr, *ddq, *dC, *dBpk, *dcs, *doff;
+    PCL_OK_OR_RETURN(upload(S_A, Au, (size_t)M * Kpad, &dAu));
+    PCL_OK_OR_RETURN(upload(S_B, Bp, bp_bytes, &dBp));
+    PCL_OK_OR_RETURN(upload(S_D, corr, sizeof(int32_t) * (size_t)N, &dcorr));
+    PCL_OK_OR_RETURN(upload(S_BIAS, dq, sizeof(float) * (size_t)N, &ddq));
+    PCL_OK_OR_RETURN(stage_buf(S_C, sizeof(float) * (size_t)M * N, &dC));
+    PCL_OK_OR_RETURN(stage_buf(S_E, pcl_s8_packed_bytes(K, N), &dBpk));
+    PCL_OK_OR_RETURN(stage_buf(S_F, sizeof(int32_t) * (size_t)N, &dcs));
+    PCL_OK_OR_RETURN(stage_buf(S_G, sizeof(int32_t) * (size_t)N, &doff));
+    PCL_OK_OR_RETURN(pcl_pack_b_vnni((const int8_t *)dBp, K, Kpad, N, (int8_t *)dBpk,
+                                     (int32_t *)dcs, t_stream));
+    HIP_OK(pcl::launch_corr_to_offset((const int32_t *)dcs, (const int32_t *)dcorr,
+                                      (int32_t *)doff, N, t_stream));
+    PCL_OK_OR_RETURN(pcl_gemm_u8s8_dq((const uint8_t *)dAu, Kpad, (const int8_t *)dBpk,
+                                      (const int32_t *)doff, nullptr, (const float *)ddq,
+                                      (float *)dC, N, M, N, K, t_stream));
+    PCL_OK_OR_RETURN(download(C, dC, sizeof(float) * (size_t)M * N));
+    return sync_current();
+}
+
+void gemm_int8_kernel(const uint8_t *Au, int Kpad, const int8_t *Bp, const int32_t *corr,
+                      const float *dq, float *C, int M, int N) {
+    finish_void(host_gemm_int8_kernel(Au, Kpad, Bp, corr, dq, C, M, N));
+}
+
+}  // extern "C"

@@ -1,0 +1,262 @@
+"""INT8 parity on the GPU: u8 x s8 -> int32 must be bit-exact.
+
+Checked against the exact int64 oracle, against golden outputs written by the
+reference's own gemm_bench.c (tests/golden/gemm_bench_int8.npz), and at full
+config sizes by exact integer checksums (column sums of C equal
+colsum(A-128).B; row sums equal (A-128).rowsum(B)) plus exact sampled rows.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import binding as ob
+import pcl
+from gpu_util import announce, require_device
+
+pytestmark = pytest.mark.gpu
+GOLD = os.path.join(os.path.dirname(__file__), "golden")
+p = ob.p
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _device():
+    require_device()
+
+
+def pack(Bq):
+    """Bq (K x N row-major s8) -> device packed buffer + colsum."""
+    K, N = Bq.shape
+    dB = pcl.dev(Bq)
+    dBp = pcl.DeviceBuffer(pcl.lib.pcl_s8_packed_bytes(K, N))
+    dcs = pcl.empty((N,), np.int32)
+    pcl.check(pcl.lib.pcl_pack_b_s8(dB.ptr, N, K, N, dBp.ptr, dcs.ptr, None))
+    pcl.sync()
+    return dBp, dcs.download((N,), np.int32)
+
+
+def igemm_i32(Au, Bq, gemv=False):
+    M, K = Au.shape
+    N = Bq.shape[1]
+    dBp, _ = pack(Bq)
+    dA = pcl.dev(Au)
+    dC = pcl.empty((M, N), np.int32)
+    fn = pcl.lib.pcl_gemv_u8s8_i32 if gemv else pcl.lib.pcl_gemm_u8s8_i32
+    pcl.check(fn(dA.ptr, K, dBp.ptr, dC.ptr, N, M, N, K, None))
+    pcl.sync()
+    return dC.download((M, N), np.int32)
+
+
+def exact(Au, Bq):
+    return (Au.astype(np.int64) - 128) @ Bq.astype(np.int64)
+
+
+def test_pack_layout_and_colsum():
+    K, N = 200, 96
+    Bq = ob.s8((K, N), 11)
+    announce("pack_b_s8", K, N)
+    dBp, cs = pack(Bq)
+    Kp = pcl.lib.pcl_s8_kpad(K)
+    got = dBp.download((N, Kp), np.int8)
+    np.testing.assert_array_equal(got[:, :K], Bq.T)
+    assert not got[:, K:].any()  # zero padding beyond K
+    np.testing.assert_array_equal(cs, Bq.astype(np.int64).sum(0))
+
+
+@pytest.mark.parametrize("M,N,K", [(17, 33, 80), (64, 64, 64), (256, 512, 256), (129, 257, 1000),
+                                   (300, 200, 48), (9, 16, 4096), (1024, 1024, 1024)])
+def test_igemm_i32_exact(M, N, K):
+    Au = ob.u8((M, K), 20 + M)
+    Bq = ob.s8((K, N), 21 + N)
+    announce("igemm i32", M, N, K)
+    np.testing.assert_array_equal(igemm_i32(Au, Bq), ob.gemm_u8s8_i32(Au, Bq))
+
+
+def test_igemm_extremes():
+    # all -128 x all -128 and 255 x 127: the largest magnitudes of the range
+    M, N, K = 64, 64, 4096
+    announce("igemm extremes")
+    C = igemm_i32(np.zeros((M, K), np.uint8), np.full((K, N), -128, np.int8))
+    assert (C == K * 128 * 128).all()
+    C = igemm_i32(np.full((M, K), 255, np.uint8), np.full((K, N), 127, np.int8))
+    assert (C == K * 127 * 127).all()
+    C = igemm_i32(np.full((M, K), 128, np.uint8), ob.s8((K, N), 5))
+    assert not C.any()
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8])
+def test_igemv_i32_exact(M):
+    for N, K in ((1536, 512), (512, 2048), (2048, 512), (100, 77), (64, 8192)):
+        Au = ob.u8((M, K), 30 + M)
+        Bq = ob.s8((K, N), 31 + N)
+        announce("igemv i32", M, N, K)
+        np.testing.assert_array_equal(igemm_i32(Au, Bq, gemv=True), ob.gemm_u8s8_i32(Au, Bq))
+
+
+def _dq_run(Au, Bq, sa, sb, col_off=None):
+    M, K = Au.shape
+    N = Bq.shape[1]
+    dBp, _ = pack(Bq)
+    dA = pcl.dev(Au)
+    dsa = pcl.dev(sa) if sa is not None else None
+    dsb = pcl.dev(sb)
+    doff = pcl.dev(col_off) if col_off is not None else None
+    dC = pcl.empty((M, N), np.float32)
+    pcl.check(pcl.lib.pcl_gemm_u8s8_dq(dA.ptr, K, dBp.ptr, doff.ptr if doff else None,
+                                       dsa.ptr if dsa else None, dsb.ptr, dC.ptr, N, M, N, K, None))
+    pcl.sync()
+    return dC.download((M, N), np.float32)
+
+
+@pytest.mark.parametrize("M,N,K", [(2048, 2048, 2048), (4, 1536, 512), (200, 300, 96)])
+def test_igemm_dequant_bit_exact(M, N, K):
+    # gemm_bench INT8 config: per-row x per-column scales ~ U[1e-3, 1e-2]
+    Au = ob.u8((M, K), 40)
+    Bq = ob.s8((K, N), 41)
+    sa = ob.uniform((M,), 42, 1e-3, 1e-2)
+    sb = ob.uniform((N,), 43, 1e-3, 1e-2)
+    rows = np.unique(np.r_[0, M - 1, np.random.default_rng(1).choice(M, min(M, 64), replace=False)])
+    V = exact(Au[rows], Bq).astype(np.int32)
+    announce("igemm dq rowcol", M, N, K)
+    C = _dq_run(Au, Bq, sa, sb)
+    np.testing.assert_array_equal(C[rows], ob.dequant(V, sa[rows], sb))
+    announce("igemm dq col", M, N, K)
+    C = _dq_run(Au, Bq, None, sb)
+    np.testing.assert_array_equal(C[rows], ob.dequant(V, None, sb))
+    off = ob.s8((N,), 44).astype(np.int32) * 1000
+    announce("igemm dq col_off", M, N, K)
+    C = _dq_run(Au, Bq, None, sb, off)
+    np.testing.assert_array_equal(C[rows], ob.dequant((V + off).astype(np.int32), None, sb))
+
+
+@pytest.mark.parametrize("M,N,K", [(2048, 2048, 2048), (4096, 3072, 1024), (4096, 1024, 4096),
+                                   (4096, 50257, 1024)])
+def test_igemm_full_size_checksums(M, N, K):
+    # size-independent exact properties at the configs' full sizes
+    Au = ob.u8((M, K), 60 + K)
+    Bq = ob.s8((K, N), 61 + N)
+    announce("igemm full", M, N, K)
+    C = igemm_i32(Au, Bq).astype(np.int64)
+    A8 = Au.astype(np.int64) - 128
+    B8 = Bq.astype(np.int64)
+    np.testing.assert_array_equal(C.sum(0), A8.sum(0) @ B8)  # column checksums
+    np.testing.assert_array_equal(C.sum(1), A8 @ B8.sum(1))  # row checksums
+    rows = np.random.default_rng(2).choice(M, 8, replace=False)
+    np.testing.assert_array_equal(C[rows], A8[rows] @ B8)
+
+
+def test_quantizers_byte_exact():
+    M, K, N = 96, 250, 80
+    A = ob.normal((M, K), 70)
+    B = ob.normal((K, N), 71, 0, 0.02)
+    Kpad = 256
+    dA, dB = pcl.dev(A), pcl.dev(B)
+    # per-tensor (quantize_A rule)
+    dAu, ds = pcl.empty((M, Kpad), np.uint8), pcl.empty((1,), np.float32)
+    announce("quantize_a_tensor")
+    pcl.check(pcl.lib.pcl_quantize_a_tensor(dA.ptr, M, K, dAu.ptr, Kpad, ds.ptr, None))
+    pcl.sync()
+    Au_ref = np.empty((M, Kpad), np.uint8)
+    s_ref = ob.oracle().orc_quantize_A(p(A), p(Au_ref), M, K, Kpad)
+    assert ds.download((1,), np.float32)[0] == np.float32(s_ref)
+    np.testing.assert_array_equal(dAu.download((M, Kpad), np.uint8), Au_ref)
+    # per-row
+    dsa = pcl.empty((M,), np.float32)
+    announce("quantize_a_rows")
+    pcl.check(pcl.lib.pcl_quantize_a_rows(dA.ptr, M, K, dAu.ptr, Kpad, dsa.ptr, None))
+    pcl.sync()
+    sa_ref = np.empty(M, np.float32)
+    ob.oracle().orc_quantize_A_rows(p(A), p(Au_ref), p(sa_ref), M, K, Kpad)
+    np.testing.assert_array_equal(dsa.download((M,), np.float32), sa_ref)
+    np.testing.assert_array_equal(dAu.download((M, Kpad), np.uint8), Au_ref)
+    # per-column weights, native layout
+    Kp = pcl.lib.pcl_s8_kpad(K)
+    dBp = pcl.DeviceBuffer(pcl.lib.pcl_s8_packed_bytes(K, N))
+    dbs, dcs = pcl.empty((N,), np.float32), pcl.empty((N,), np.int32)
+    announce("quantize_b_cols")
+    pcl.check(pcl.lib.pcl_quantize_b_cols(dB.ptr, K, N, dBp.ptr, dbs.ptr, dcs.ptr, None))
+    pcl.sync()
+    Bq_ref = np.empty((K, N), np.int8)
+    bs_ref = np.empty(N, np.float32)
+    ob.oracle().orc_quantize_B_cols(p(B), p(Bq_ref), p(bs_ref), K, N)
+    got = dBp.download((N, Kp), np.int8)
+    np.testing.assert_array_equal(got[:, :K], Bq_ref.T)
+    assert not got[:, K:].any()
+    np.testing.assert_array_equal(dbs.download((N,), np.float32), bs_ref)
+    np.testing.assert_array_equal(dcs.download((N,), np.int32), Bq_ref.astype(np.int64).sum(0))
+    # reference VNNI layout
+    Kv = (K + 3) & ~3
+    nbp = (N // 16) * (Kv // 4) * 64
+    dBv = pcl.empty((nbp,), np.int8)
+    announce("quantize_b_vnni")
+    pcl.check(pcl.lib.pcl_quantize_b_vnni(dB.ptr, K, N, Kv, dBv.ptr, dbs.ptr, dcs.ptr, None))
+    pcl.sync()
+    Bp_ref, bs2, cs2 = np.empty(nbp, np.int8), np.empty(N, np.float32), np.empty(N, np.int32)
+    ob.oracle().orc_quantize_B_pack(p(B), p(Bp_ref), p(bs2), p(cs2), K, N, Kv)
+    np.testing.assert_array_equal(dBv.download((nbp,), np.int8), Bp_ref)
+    np.testing.assert_array_equal(dcs.download((N,), np.int32), cs2)
+
+
+def test_vnni_repack_matches_native_pack():
+    K, N, Kpad = 300, 64, 300
+    Bq = ob.s8((K, N), 80)
+    Bp = np.zeros((N // 16) * (Kpad // 4) * 64, np.int8)
+    for n in range(N):  # write the VNNI layout of gemm_bench.c:254 directly
+        pp, i = divmod(n, 16)
+        for k in range(K):
+            Bp[pp * (Kpad // 4) * 64 + (k // 4) * 64 + i * 4 + k % 4] = Bq[k, n]
+    dBp = pcl.dev(Bp)
+    dout = pcl.DeviceBuffer(pcl.lib.pcl_s8_packed_bytes(K, N))
+    dcs = pcl.empty((N,), np.int32)
+    announce("pack_b_vnni")
+    pcl.check(pcl.lib.pcl_pack_b_vnni(dBp.ptr, K, Kpad, N, dout.ptr, dcs.ptr, None))
+    pcl.sync()
+    ref_pk, ref_cs = pack(Bq)
+    Kp = pcl.lib.pcl_s8_kpad(K)
+    np.testing.assert_array_equal(dout.download((N, Kp), np.int8), ref_pk.download((N, Kp), np.int8))
+    np.testing.assert_array_equal(dcs.download((N,), np.int32), ref_cs)
+
+
+def test_dropins_vs_reference_golden():
+    """quantize_A / quantize_B_pack / gemm_int8_kernel host drop-ins against
+    the bytes and floats the reference's gemm_bench.c produced."""
+    g = np.load(os.path.join(GOLD, "gemm_bench_int8.npz"))
+    M, K, N, Kpad = (int(v) for v in g["dims"])
+    L = pcl.lib
+    Au = np.empty((M, Kpad), np.uint8)
+    announce("drop-in quantize_A")
+    scale = L.quantize_A(p(g["A"]), p(Au), M, K, Kpad)
+    pcl.check_void()
+    assert np.float32(scale) == g["scale"]
+    np.testing.assert_array_equal(Au, g["Au"])
+    Bp = np.empty_like(g["Bp"])
+    bs, cs = np.empty(N, np.float32), np.empty(N, np.int32)
+    announce("drop-in quantize_B_pack")
+    L.quantize_B_pack(p(g["B"]), p(Bp), p(bs), p(cs), K, N, Kpad)
+    pcl.check_void()
+    np.testing.assert_array_equal(Bp, g["Bp"])
+    np.testing.assert_array_equal(bs, g["bscale"])
+    np.testing.assert_array_equal(cs, g["colsum"])
+    C = np.empty((M, N), np.float32)
+    announce("drop-in gemm_int8_kernel")
+    L.gemm_int8_kernel(p(g["Au"]), Kpad, p(g["Bp"]), p(g["corr"]), p(g["dq"]), p(C), M, N)
+    pcl.check_void()
+    np.testing.assert_array_equal(C, g["C_int8"])
+    # a caller-supplied corr that is not 128*colsum is honoured too
+    corr2 = (g["corr"] + 7).astype(np.int32)
+    announce("drop-in gemm_int8_kernel corr+7")
+    L.gemm_int8_kernel(p(g["Au"]), Kpad, p(g["Bp"]), p(corr2), p(g["dq"]), p(C), M, N)
+    pcl.check_void()
+    C_ref = np.empty((M, N), np.float32)
+    ob.oracle().orc_gemm_int8_kernel(p(g["Au"]), Kpad, p(g["Bp"]), p(corr2), p(g["dq"]), p(C_ref), M, N)
+    np.testing.assert_array_equal(C, C_ref)
+
+
+def test_int8_arg_errors():
+    L = pcl.lib
+    assert L.pcl_gemm_u8s8_i32(None, 16, None, None, 16, 4, 16, 16, None) == pcl.PCL_ERR_INVALID_ARG
+    assert L.pcl_gemm_u8s8_i32(None, 200000, None, None, 16, 4, 16, 200000, None) == pcl.PCL_ERR_RANGE
+    buf = pcl.empty((64,), np.int8)
+    # packed weights must be 16-byte aligned
+    st = L.pcl_gemm_u8s8_i32(buf.ptr, 16, buf.ptr + 1, buf.ptr, 16, 1, 1, 16, None)
+    assert st == pcl.PCL_ERR_INVALID_ARG

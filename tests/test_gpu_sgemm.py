@@ -1,0 +1,125 @@
+"""FP32 GEMM parity on the GPU: libpcl_hip (f32 MFMA) vs the CPU oracle.
+
+Tolerance: max|C-R|/max|R| <= 1e-4 against both
+the reference-order fp32 restatement (tensor.c:34-53) and the f64 truth.
+Full 350M-class shapes are checked on sampled rows against f64 numpy.
+"""
+import numpy as np
+import pytest
+
+import binding as ob
+import pcl
+from gpu_util import FP32_TOL, announce, rel, require_device, sampled_rows_f64, sgemm
+
+pytestmark = pytest.mark.gpu
+
+N_, T_ = pcl.OP_N, pcl.OP_T
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _device():
+    require_device()
+
+
+def _operands(opA, opB, M, N, K, seed):
+    A = ob.frand((M, K) if opA == N_ else (K, M), seed)
+    B = ob.frand((K, N) if opB == N_ else (N, K), seed + 1)
+    return A, B
+
+
+SHAPES = [(17, 33, 65), (64, 64, 64), (128, 128, 128), (1000, 1001, 999), (256, 1536, 512),
+          (9, 5, 1), (33, 260, 300), (130, 70, 4)]
+
+
+@pytest.mark.parametrize("opA,opB", [(N_, N_), (N_, T_), (T_, N_), (T_, T_)])
+@pytest.mark.parametrize("M,N,K", SHAPES)
+def test_sgemm_layouts(opA, opB, M, N, K):
+    announce("sgemm", opA, opB, M, N, K)
+    A, B = _operands(opA, opB, M, N, K, 1000 + M + N + K)
+    C = sgemm(opA, opB, A, B, M, N, K)
+    R = ob.gemm_f64(A, B, transA=opA == T_, transB=opB == T_)
+    assert rel(C, R) <= FP32_TOL
+
+
+def test_sgemm_nn_matches_reference_order_restatement():
+    M, K, N = 1024, 1024, 1024  # gemm_bench FP32 config, A,B ~ U[-1,1]
+    announce("sgemm nn 1024^3 vs ikj")
+    A, B = ob.frand((M, K), 1234), ob.frand((K, N), 1235)
+    C = sgemm(N_, N_, A, B, M, N, K)
+    assert rel(C, ob.matmul_ikj(A, B)) <= FP32_TOL
+
+
+def test_sgemm_tensor_kat():
+    # tensor.c:204-205 / 237-241: C[0,0] = 0.07 on the 1024^3 mod pattern
+    M = K = N = 1024
+    A = np.empty(M * K, np.float32)
+    B = np.empty(K * N, np.float32)
+    ob.oracle().orc_fill_kat_tensor(ob.p(A), A.size, ob.p(B), B.size)
+    announce("sgemm tensor KAT")
+    C = sgemm(N_, N_, A.reshape(M, K), B.reshape(K, N), M, N, K)
+    assert abs(float(C[0, 0]) - 0.07) < 1e-5
+
+
+def test_sgemm_bias_accumulate_and_k0():
+    M, N, K = 70, 90, 50
+    A, B = _operands(N_, N_, M, N, K, 77)
+    bias = ob.normal((N,), 78)
+    C0 = ob.normal((M, N), 79)
+    announce("sgemm bias+accumulate")
+    C = sgemm(N_, N_, A, B, M, N, K, bias=bias, C0=C0)
+    assert rel(C, ob.gemm_f64(A, B, bias=bias, C0=C0)) <= FP32_TOL
+    # K == 0: C = bias (or C0 + bias)
+    A0, B0 = np.zeros((M, 0), np.float32), np.zeros((0, N), np.float32)
+    dA, dB, dbias = pcl.empty((1,), np.float32), pcl.empty((1,), np.float32), pcl.dev(bias)
+    dC = pcl.dev(C0)
+    pcl.check(pcl.lib.pcl_sgemm(N_, N_, M, N, 0, dA.ptr, 1, dB.ptr, N, dbias.ptr, 1, dC.ptr, N, None))
+    pcl.sync()
+    np.testing.assert_array_equal(dC.download((M, N), np.float32), C0 + bias)
+    del A0, B0
+
+
+def test_sgemm_strided_leading_dims():
+    # sub-matrix views: lda/ldb/ldc larger than the logical width
+    M, N, K = 96, 80, 72
+    Abig, Bbig = ob.frand((M, K + 8), 90), ob.frand((K, N + 12), 91)
+    dA, dB = pcl.dev(Abig), pcl.dev(Bbig)
+    dC = pcl.dev(np.full((M, N + 4), 5.0, np.float32))
+    announce("sgemm strided")
+    pcl.check(pcl.lib.pcl_sgemm(N_, N_, M, N, K, dA.ptr, K + 8, dB.ptr, N + 12, None, 0, dC.ptr, N + 4, None))
+    pcl.sync()
+    C = dC.download((M, N + 4), np.float32)
+    assert rel(C[:, :N], ob.gemm_f64(Abig[:, :K], Bbig[:, :N])) <= FP32_TOL
+    assert np.all(C[:, N:] == 5.0)  # untouched padding columns
+
+
+def test_sgemm_deterministic():
+    M, N, K = 512, 512, 777
+    A, B = _operands(N_, T_, M, N, K, 95)
+    announce("sgemm determinism")
+    C1 = sgemm(N_, T_, A, B, M, N, K)
+    C2 = sgemm(N_, T_, A, B, M, N, K)
+    np.testing.assert_array_equal(C1, C2)
+
+
+# 350M-class shapes (M = 4 x 1024 tokens): forward NN, tied-head NT, and the
+# trainer's backward layouts dX = dY.W^T (NT) and dW = X^T.dY (TN).
+FULL = [
+    ("qkv", N_, N_, 4096, 3072, 1024),
+    ("ff2", N_, N_, 4096, 1024, 4096),
+    ("head", N_, T_, 4096, 50257, 1024),
+    ("dX_ff1", N_, T_, 4096, 1024, 4096),
+    ("dW_ff1", T_, N_, 1024, 4096, 4096),
+]
+
+
+@pytest.mark.parametrize("name,opA,opB,M,N,K", FULL)
+def test_sgemm_350m_sampled(name, opA, opB, M, N, K):
+    A = ob.normal((M, K) if opA == N_ else (K, M), 500, 0.0, 1.0)
+    B = ob.normal((K, N) if opB == N_ else (N, K), 501, 0.0, 0.02)
+    announce("sgemm 350M", name, M, N, K)
+    C = sgemm(opA, opB, A, B, M, N, K)
+    rows = np.random.default_rng(0).choice(M, 48, replace=False)
+    Arows = A if opA == N_ else np.ascontiguousarray(A.T)
+    R = sampled_rows_f64(Arows, B, rows, transB=opB == T_)
+    assert rel(C[rows], R) <= FP32_TOL
+    assert np.isfinite(C).all()

@@ -1,0 +1,359 @@
+"""Pin the CPU oracle (oracle/pcl_oracle.c) before trusting it.
+
+Each restated function is checked by something other than its own formula:
+the reference's known-answer test, closed forms and invariants, numpy's f64
+matmul as a library routine, the golden fixtures written by the reference's
+own code (tests/golden/), and -- where this container built it -- the
+reference compiled from source (oracle/_ref). A planted mistake (dropped
+term, transposed operand, wrong offset) fails at least one of these.
+"""
+import hashlib
+import os
+
+import numpy as np
+import pytest
+
+import binding as ob
+
+p = ob.p
+O = ob.oracle
+# The reference is built with -ffast-math (reassociated, vectorised fp32 sums),
+# so reference-vs-restatement fp32 agreement is ~1e-6; 1e-5 is the bar here,
+# ten times tighter than the GPU's 1e-4 and far below any dropped-term error.
+REF_TOL = 1e-5
+GOLD = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def gold(name):
+    return np.load(os.path.join(GOLD, name))
+
+
+# ------------------------------------------------------------------ PRNG ----
+def _xorshift_py(s, n):
+    out = []
+    for _ in range(n):
+        s ^= (s << 13) & 0xFFFFFFFF
+        s ^= s >> 17
+        s ^= (s << 5) & 0xFFFFFFFF
+        out.append(s)
+    return out
+
+
+def test_xorshift_matches_recurrence():
+    # train.c:73-78 recurrence, restated independently in Python
+    import ctypes
+
+    st = ctypes.c_uint32(12345)
+    got = [O().orc_xorshift32(ctypes.byref(st)) for _ in range(10)]
+    assert got == _xorshift_py(12345, 10)
+
+
+def test_frand_formula():
+    a = ob.frand((8,), 1234, 0.02)
+    want = [((x & 0xFFFFFF) / 16777216.0 * 2.0 - 1.0) * 0.02 for x in _xorshift_py(1234, 8)]
+    np.testing.assert_allclose(a, np.float32(want), rtol=0, atol=1e-9)
+
+
+def test_int_fills_cover_range():
+    u = ob.u8((1 << 16,), 7)
+    s = ob.s8((1 << 16,), 8)
+    assert u.min() == 0 and u.max() == 255
+    assert s.min() == -128 and s.max() == 127
+    assert abs(u.astype(float).mean() - 127.5) < 2 and abs(s.astype(float).mean() + 0.5) < 2
+
+
+def test_normal_moments():
+    z = ob.normal((200000,), 99, 0.0, 1.0)
+    assert abs(z.mean()) < 0.01 and abs(z.std() - 1.0) < 0.01
+
+
+# ------------------------------------------------------------ FP32 KATs ----
+def _kat_closed_form(M, K, N):
+    i = np.arange(M)[:, None]
+    k = np.arange(K)[None, :]
+    a = ((i * K + k) % 13 - 6).astype(np.int64)  # A[i,k] = 0.1*a
+    kk = np.arange(K)[:, None]
+    j = np.arange(N)[None, :]
+    b = ((kk * N + j) % 7 - 3).astype(np.int64)
+    return (a @ b).astype(np.float64) * 0.01
+
+
+def test_tensor_selftest_kat_c00():
+    # tensor.c:204-205 inputs, tensor.c:237-241 check: C[0,0] = 0.07000
+    M = K = N = 1024
+    A = np.empty(M * K, np.float32)
+    B = np.empty(K * N, np.float32)
+    O().orc_fill_kat_tensor(p(A), A.size, p(B), B.size)
+    Cm = ob.matmul_ikj(A.reshape(M, K), B.reshape(K, N))
+    assert abs(float(Cm[0, 0]) - 0.07) < 5e-5
+    ref = _kat_closed_form(M, K, N)
+    assert abs(ref[0, 0] - 0.07) < 1e-12
+    assert ob.normwise_rel_err(Cm, ref) < 1e-5
+
+
+def test_closed_form_full_matrix_small():
+    M, K, N = 37, 90, 53  # K coprime to 7 and 13: non-degenerate sums
+    A = np.empty(M * K, np.float32)
+    B = np.empty(K * N, np.float32)
+    O().orc_fill_kat_tensor(p(A), A.size, p(B), B.size)
+    A, B = A.reshape(M, K), B.reshape(K, N)
+    want = _kat_closed_form(M, K, N)
+    for got in (ob.matmul_ikj(A, B), ob.gemm_f64(A, B)):
+        assert ob.normwise_rel_err(got, want) < 1e-6
+
+
+def test_identity_ones_and_empty_k():
+    B = ob.frand((64, 48), 3)
+    I = np.eye(64, dtype=np.float32)
+    np.testing.assert_array_equal(ob.matmul_ikj(I, B), B)
+    np.testing.assert_array_equal(ob.gemm_f64(I, B), B)
+    ones = np.ones((5, 64), np.float32)
+    np.testing.assert_allclose(ob.gemm_f64(ones, B), np.repeat(B.astype(np.float64).sum(0, keepdims=True), 5, 0),
+                               rtol=1e-6)
+    z = ob.gemm_f64(np.zeros((4, 0), np.float32), np.zeros((0, 6), np.float32),
+                    bias=np.arange(6, dtype=np.float32))
+    np.testing.assert_array_equal(z, np.tile(np.arange(6, dtype=np.float32), (4, 1)))
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 1, 1), (7, 13, 5), (64, 100, 33)])
+def test_gemm_layouts_against_numpy(M, K, N):
+    A = ob.frand((M, K), 11)
+    B = ob.frand((K, N), 12)
+    want = A.astype(np.float64) @ B.astype(np.float64)
+    Cnn = np.empty((M, N), np.float32)
+    O().orc_gemm_nn(p(A), p(B), None, p(Cnn), M, K, N)
+    assert ob.normwise_rel_err(Cnn, want) < 1e-7
+    Bt = np.ascontiguousarray(B.T)  # (N,K)
+    Cnt = np.full((M, N), 0.5, np.float32)
+    O().orc_gemm_nt(p(A), p(Bt), p(Cnt), M, K, N, 1)  # accumulate onto 0.5
+    assert ob.normwise_rel_err(Cnt - 0.5, want) < 1e-6
+    # TN: C(K,N) += A(M,K)^T B(M,N) -- use A as the (M,K) operand, A2 as (M,N)
+    A2 = ob.frand((M, N), 13)
+    Ctn = np.zeros((K, N), np.float32)
+    O().orc_gemm_tn(p(A), p(A2), p(Ctn), M, K, N)
+    assert ob.normwise_rel_err(Ctn, A.T.astype(np.float64) @ A2.astype(np.float64)) < 1e-7
+
+
+def test_transpose_identity_links_layouts():
+    # (A.B)^T = B^T A^T: nn(A,B) equals nt(A, B^T) and tn(A^T stored, B)
+    A = ob.frand((19, 23), 21)
+    B = ob.frand((23, 29), 22)
+    nn = ob.gemm_f64(A, B)
+    nt = ob.gemm_f64(A, np.ascontiguousarray(B.T), transB=True)
+    tn = ob.gemm_f64(np.ascontiguousarray(A.T), B, transA=True)
+    np.testing.assert_array_equal(nn, nt)
+    np.testing.assert_array_equal(nn, tn)
+
+
+def test_matvec_bias_init_and_order():
+    M, K, N = 3, 50, 70
+    x = ob.normal((M, K), 31)
+    W = ob.normal((K, N), 32, 0, 0.02)
+    b = ob.normal((N,), 33)
+    y = np.empty((M, N), np.float32)
+    O().orc_matvec(p(y), p(x), p(W), p(b), M, K, N)
+    assert ob.normwise_rel_err(y, x.astype(np.float64) @ W + b) < 1e-6
+    O().orc_matvec(p(y), p(x), p(W), None, M, K, N)
+    assert ob.normwise_rel_err(y, x.astype(np.float64) @ W) < 1e-6
+
+
+# ---------------------------------------------- golden (reference output) ----
+def test_golden_tensor_matmul():
+    g = gold("tensor_matmul_f32.npz")
+    for key in [k for k in g.files if k.startswith("C_")]:
+        tag = key[2:]
+        A, B, Cr = g["A_" + tag], g["B_" + tag], g[key]
+        assert ob.normwise_rel_err(ob.matmul_ikj(A, B), Cr) < REF_TOL, tag
+
+
+def test_golden_train_gemms():
+    g = gold("train_gemms.npz")
+    M, K, N, Mh, D, V = (int(v) for v in g["dims"])
+    Y = np.empty((M, N), np.float32)
+    O().orc_matmul_forward(p(Y), p(g["X"]), p(g["W"]), p(g["bias"]), M, K, N)
+    assert ob.normwise_rel_err(Y, g["Y"]) < REF_TOL
+    dX, dW, db = g["dX0"].copy(), g["dW0"].copy(), g["db0"].copy()
+    O().orc_matmul_backward(p(g["dY"]), p(g["X"]), p(g["W"]), p(dX), p(dW), p(db), M, K, N)
+    for got, want in ((dX, g["dX"]), (dW, g["dW"]), (db, g["db"])):
+        assert ob.normwise_rel_err(got, want) < REF_TOL
+    lo = np.empty((Mh, V), np.float32)
+    O().orc_tied_head_forward(p(lo), p(g["lnf"]), p(g["wte"]), Mh, D, V)
+    assert ob.normwise_rel_err(lo, g["logits"]) < REF_TOL
+    dlnf = np.full((Mh, D), 3.0, np.float32)
+    dwte = g["dwte0"].copy()
+    O().orc_tied_head_backward(p(dlnf), p(dwte), p(g["dlog"]), p(g["lnf"]), p(g["wte"]), Mh, D, V)
+    assert ob.normwise_rel_err(dlnf, g["dlnf"]) < REF_TOL
+    assert ob.normwise_rel_err(dwte, g["dwte"]) < REF_TOL
+
+
+def test_golden_decode():
+    g = gold("decode_gemv.npz")
+    K, N, T, D, V = (int(v) for v in g["dims"])
+    y = np.empty((1, N), np.float32)
+    O().orc_matvec(p(y), p(g["x"]), p(g["W"]), p(g["b"]), 1, K, N)
+    assert ob.normwise_rel_err(y[0], g["y"]) < REF_TOL
+    s1, s2 = (int(v) for v in g["head_seeds"])
+    xs = ob.normal((T, D), s1)
+    wte = ob.normal((V, D), s2, 0.0, 0.02)
+    assert hashlib.sha256(xs.tobytes() + wte.tobytes()).digest() == g["head_input_sha256"].tobytes()
+    lo = np.empty((T, V), np.float32)
+    O().orc_lm_head(p(lo), p(xs), p(wte), T, D, V)
+    assert ob.normwise_rel_err(lo, g["logits"]) < REF_TOL
+
+
+def test_golden_gemm_bench_int8():
+    g = gold("gemm_bench_int8.npz")
+    M, K, N, Kpad = (int(v) for v in g["dims"])
+    Au = np.empty((M, Kpad), np.uint8)
+    scale = O().orc_quantize_A(p(g["A"]), p(Au), M, K, Kpad)
+    assert np.float32(scale) == g["scale"]
+    np.testing.assert_array_equal(Au, g["Au"])
+    Bp = np.empty_like(g["Bp"])
+    bscale = np.empty(N, np.float32)
+    colsum = np.empty(N, np.int32)
+    O().orc_quantize_B_pack(p(g["B"]), p(Bp), p(bscale), p(colsum), K, N, Kpad)
+    np.testing.assert_array_equal(Bp, g["Bp"])
+    np.testing.assert_array_equal(bscale, g["bscale"])
+    np.testing.assert_array_equal(colsum, g["colsum"])
+    Cq = np.empty((M, N), np.float32)
+    O().orc_gemm_int8_kernel(p(g["Au"]), Kpad, p(g["Bp"]), p(g["corr"]), p(g["dq"]), p(Cq), M, N)
+    np.testing.assert_array_equal(Cq, g["C_int8"])  # bit-exact, reference op order
+    # the offset identity: v = sum Au*Bq - 128*colsum = sum (Au-128)*Bq
+    Bq = np.empty((Kpad, N), np.int8)
+    O().orc_unpack_vnni(p(g["Bp"]), p(Bq), Kpad, N, Kpad)
+    V = ob.gemm_u8s8_i32(g["Au"], Bq)
+    np.testing.assert_array_equal(ob.dequant(V, None, g["dq"]), g["C_int8"])
+    # INT8 vs FP32 of the same inputs: README.md:31 reports 0.56% RMS relative
+    assert O().orc_rms_rel(p(Cq), p(g["C_f32"]), Cq.size) < 0.02
+
+
+# -------------------------------------------------------- INT8 identities ----
+def test_vnni_offset_identity_and_special_cases():
+    M, K, N = 16, 96, 32
+    Au = ob.u8((M, K), 41)
+    Bq = ob.s8((K, N), 42)
+    raw = np.empty((M, N), np.int32)
+    O().orc_gemm_u8s8_raw_i32(p(Au), K, p(Bq), N, p(raw), N, M, N, K)
+    v = ob.gemm_u8s8_i32(Au, Bq)
+    colsum = Bq.astype(np.int64).sum(0)
+    np.testing.assert_array_equal(raw.astype(np.int64) - 128 * colsum, v)
+    np.testing.assert_array_equal(v, (Au.astype(np.int64) - 128) @ Bq.astype(np.int64))
+    # Au == 128 everywhere -> exactly zero; Bq == 1 -> row sums of (Au - 128)
+    assert not ob.gemm_u8s8_i32(np.full((M, K), 128, np.uint8), Bq).any()
+    rs = (Au.astype(np.int64) - 128).sum(1)
+    np.testing.assert_array_equal(ob.gemm_u8s8_i32(Au, np.ones((K, N), np.int8)), np.repeat(rs[:, None], N, 1))
+
+
+def test_int8_extreme_values_fit_int32():
+    # |sum| <= K*128*128: all -128 activations against all -128 weights
+    K = 4096
+    v = ob.gemm_u8s8_i32(np.zeros((1, K), np.uint8), np.full((K, 2), -128, np.int8))
+    assert int(v[0, 0]) == K * 128 * 128
+
+
+def test_quantizer_rules():
+    # round half away from zero, clamp to +-127, 128 padding
+    A = np.array([[0.5, -0.5, 1.5, -2.5, 127.0, -127.0, 0.0]], np.float32)
+    Au = np.empty((1, 8), np.uint8)
+    s = O().orc_quantize_A(p(A), p(Au), 1, 7, 8)
+    assert s == np.float32(127.0) * np.float32(np.float32(1) / np.float32(127))
+    np.testing.assert_array_equal(Au[0].astype(int) - 128, [1, -1, 2, -3, 127, -127, 0, 0])
+    sa = np.empty(2, np.float32)
+    A2 = np.array([[1.0, -2.0], [0.0, 0.0]], np.float32)
+    Au2 = np.empty((2, 2), np.uint8)
+    O().orc_quantize_A_rows(p(A2), p(Au2), p(sa), 2, 2, 2)
+    R = np.float32(np.float32(1) / np.float32(127))
+    assert sa[0] == np.float32(2.0) * R and sa[1] == np.float32(1e-8) * R
+    np.testing.assert_array_equal(Au2[1], [128, 128])
+
+
+def test_rms_rel_kat():
+    # README.md:31: per-tensor A / per-column B INT8 vs FP32 = 0.56% RMS rel.
+    M = K = N = 1024
+    A = ob.frand((M, K), 51)
+    B = ob.frand((K, N), 52)
+    Au = np.empty((M, K), np.uint8)
+    sa = O().orc_quantize_A(p(A), p(Au), M, K, K)
+    Bq = np.empty((K, N), np.int8)
+    bs = np.empty(N, np.float32)
+    O().orc_quantize_B_cols(p(B), p(Bq), p(bs), K, N)
+    V = ob.gemm_u8s8_i32(Au, Bq)
+    Cq = ob.dequant(V, None, (np.float32(sa) * bs).astype(np.float32))
+    Cf = ob.gemm_f64(A, B)
+    rel = O().orc_rms_rel(p(Cq), p(Cf), Cq.size)
+    assert 4.5e-3 < rel < 7e-3
+
+
+# -------------------------------------- the reference built from source ----
+def _ref_or_skip(name):
+    lib = ob.ref(name)
+    if lib is None:
+        pytest.skip(f"oracle/_ref/{name} not built (reference tree absent at build time)")
+    return lib
+
+
+def test_oracle_vs_ref_gemm_bench_rungs():
+    gb = _ref_or_skip("libref_gemm_bench.so")
+    if not gb.pcl_ref_cpu_ok():
+        pytest.skip("host CPU lacks AVX-512 VNNI")
+    M, K, N = 128, 256, 512  # gemm_bench's v3 block divisibility (gemm_bench.c:341)
+    A = ob.frand((M, K), 61)
+    B = ob.frand((K, N), 62)
+    mine = ob.matmul_ikj(A, B)
+    for name in ("pcl_ref_gemm_ikj", "pcl_ref_gemm_naive", "pcl_ref_gemm_micro", "pcl_ref_gemm_packed",
+                 "pcl_ref_gemm_packed_mt"):
+        Cr = np.empty((M, N), np.float32)
+        getattr(gb, name)(p(A), p(B), p(Cr), M, K, N)
+        assert ob.normwise_rel_err(mine, Cr) < REF_TOL, name
+
+
+def test_oracle_vs_ref_int8_random():
+    gb = _ref_or_skip("libref_gemm_bench.so")
+    if not gb.pcl_ref_cpu_ok():
+        pytest.skip("host CPU lacks AVX-512 VNNI")
+    M, K, N = 40, 333, 48
+    Kpad = (K + 3) & ~3
+    A = ob.normal((M, K), 71)
+    B = ob.normal((K, N), 72, 0, 0.02)
+    Au_r, Au_o = np.empty((M, Kpad), np.uint8), np.empty((M, Kpad), np.uint8)
+    s_r = gb.pcl_ref_quantize_A(p(A), p(Au_r), M, K, Kpad)
+    s_o = O().orc_quantize_A(p(A), p(Au_o), M, K, Kpad)
+    assert np.float32(s_r) == np.float32(s_o)
+    np.testing.assert_array_equal(Au_r, Au_o)
+    nbp = (N // 16) * (Kpad // 4) * 64
+    outs = []
+    for fn in (gb.pcl_ref_quantize_B_pack, O().orc_quantize_B_pack):
+        Bp, bs, cs = np.empty(nbp, np.int8), np.empty(N, np.float32), np.empty(N, np.int32)
+        fn(p(B), p(Bp), p(bs), p(cs), K, N, Kpad)
+        outs.append((Bp, bs, cs))
+    for a, b in zip(*outs):
+        np.testing.assert_array_equal(a, b)
+    Bp, bs, cs = outs[0]
+    corr = (128 * cs).astype(np.int32)
+    dq = (np.float32(s_r) * bs).astype(np.float32)
+    Cr, Co = np.empty((M, N), np.float32), np.empty((M, N), np.float32)
+    gb.pcl_ref_gemm_int8_kernel(p(Au_r), Kpad, p(Bp), p(corr), p(dq), p(Cr), M - M % 8, N)
+    O().orc_gemm_int8_kernel(p(Au_r), Kpad, p(Bp), p(corr), p(dq), p(Co), M, N)
+    np.testing.assert_array_equal(Cr[: M - M % 8], Co[: M - M % 8])
+
+
+def test_oracle_vs_ref_train_and_model():
+    tr = _ref_or_skip("libref_train.so")
+    md = _ref_or_skip("libref_model.so")
+    M, K, N = 33, 17, 48
+    dY = ob.normal((M, N), 81)
+    X = ob.normal((M, K), 82)
+    W = ob.normal((K, N), 83)
+    res = []
+    for fn in (tr.pcl_ref_matmul_backward, O().orc_matmul_backward):
+        dX, dW, db = np.ones((M, K), np.float32), np.ones((K, N), np.float32), np.ones(N, np.float32)
+        fn(p(dY), p(X), p(W), p(dX), p(dW), p(db), M, K, N)
+        res.append((dX, dW, db))
+    for a, b in zip(*res):
+        assert ob.normwise_rel_err(a, b) < REF_TOL
+    x = ob.normal((130,), 84)
+    Wp = ob.normal((130, 77), 85)
+    y_r, y_o = np.empty(77, np.float32), np.empty(77, np.float32)
+    md.pcl_ref_proj_token(p(y_r), p(x), p(Wp), None, 130, 77)
+    O().orc_matvec(p(y_o), p(x), p(Wp), None, 1, 130, 77)
+    assert ob.normwise_rel_err(y_o, y_r) < REF_TOL
