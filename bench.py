@@ -1,0 +1,235 @@
+#!/usr/bin/env python3
+"""bench.py -- BASELINE.json's headline metric on one MI355X.
+
+Metric: "INT8 GEMM TOPS & FP32 TFLOP/s at 1 MI355X; % of MFMA peak; GEMV HBM
+GB/s". `value` is the INT8 GEMM throughput on the configuration the metric is
+quoted on (gemm_bench INT8, M=N=K=2048, u8 x s8 ->
+int32, per-row x per-column dequant to fp32). One step = one pass of the hot
+path over the batch = one pcl_gemm_u8s8_dq call with inputs resident in HBM.
+The other configurations (FP32 1024^3, 350M-class GEMMs in both dtypes and
+backward layouts, grown-model prefill, decode GEMV sweeps) are reported under
+"extra". Timing loops run in C (libpcl_bench.so) between HIP events recorded
+on the stream the kernels are launched on.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--primary-only]
+"""
+import argparse
+import ctypes as C
+import json
+import os
+import re
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "pure-c-llm_amd")
+sys.path.insert(0, PKG)
+
+METRIC = "INT8 GEMM TOPS & FP32 TFLOP/s at 1 MI355X; % of MFMA peak; GEMV HBM GB/s"
+PEAK_I8_TOPS = 5033.0     # 256 CU x 2.4 GHz x 8192 OP/clk (dense)
+PEAK_F32_TFLOPS = 157.3   # 256 CU x 2.4 GHz x 256 FLOP/clk (dense)
+PEAK_HBM_GBS = 8000.0
+PROFILE_TRAFFIC = os.path.join(ROOT, "profiles", "igemm_2048_hbm_traffic.txt")
+
+
+def load_bench():
+    import pcl  # noqa: F401  (loads libpcl_hip.so first; raises if missing)
+
+    path = os.path.join(PKG, "libpcl_bench.so")
+    if not os.path.exists(path):
+        raise SystemExit(f"{path} is not built: run `make -C pure-c-llm_amd`")
+    lib = C.CDLL(path)
+    d, i = C.c_double, C.c_int
+    lib.pcl_bench_igemm.argtypes = [i, i, i, i, i, i, i, C.POINTER(d)]
+    lib.pcl_bench_sgemm.argtypes = [i, i, i, i, i, i, i, i, C.POINTER(d)]
+    lib.pcl_bench_gemv.argtypes = [i, i, i, C.POINTER(i), C.POINTER(i), i, i, i, C.POINTER(d), C.POINTER(d)]
+    for f in (lib.pcl_bench_igemm, lib.pcl_bench_sgemm, lib.pcl_bench_gemv):
+        f.restype = i
+    return pcl, lib
+
+
+def _check(pcl, st, what):
+    if st != 0:
+        raise RuntimeError(f"{what}: status {st}: {pcl.last_error()}")
+
+
+def igemm(pcl, lib, M, N, K, out_mode, warmup, steps):
+    ms = C.c_double(0)
+    _check(pcl, lib.pcl_bench_igemm(M, N, K, out_mode, 1, warmup, steps, C.byref(ms)), f"igemm {M}x{N}x{K}")
+    per = ms.value / steps
+    return {"M": M, "N": N, "K": K, "ms": round(per, 5),
+            "TOPS": round(2.0 * M * N * K / (per * 1e-3) / 1e12, 1),
+            "frac_peak": round(2.0 * M * N * K / (per * 1e-3) / 1e12 / PEAK_I8_TOPS, 4)}
+
+
+def sgemm(pcl, lib, opA, opB, M, N, K, accumulate, warmup, steps):
+    ms = C.c_double(0)
+    _check(pcl, lib.pcl_bench_sgemm(opA, opB, M, N, K, accumulate, warmup, steps, C.byref(ms)),
+           f"sgemm {M}x{N}x{K}")
+    per = ms.value / steps
+    tf = 2.0 * M * N * K / (per * 1e-3) / 1e12
+    return {"M": M, "N": N, "K": K, "layout": "NT"[opA] + "NT"[opB], "ms": round(per, 5),
+            "TFLOPS": round(tf, 2), "frac_peak": round(tf / PEAK_F32_TFLOPS, 4)}
+
+
+def gemv(pcl, lib, kind, M, shapes, copies, warmup, steps):
+    Ks = (C.c_int * len(shapes))(*[k for k, _ in shapes])
+    Ns = (C.c_int * len(shapes))(*[n for _, n in shapes])
+    ms, by = C.c_double(0), C.c_double(0)
+    _check(pcl, lib.pcl_bench_gemv(kind, M, len(shapes), Ks, Ns, copies, warmup, steps, C.byref(ms), C.byref(by)),
+           f"gemv kind {kind}")
+    per = ms.value / steps
+    gbs = by.value / (per * 1e-3) / 1e9
+    return {"M": M, "ms_per_sweep": round(per, 5), "bytes_per_sweep": int(by.value), "GBps": round(gbs, 1),
+            "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "weight_copies": copies}
+
+
+def read_traffic():
+    """HBM bytes per launch of the primary kernel, measured by rocprofv3 --pmc
+    (FETCH_SIZE + WRITE_SIZE, calibrated on a copy of known size) and recorded
+    in profiles/; None when no such measurement has been committed."""
+    if not os.path.exists(PROFILE_TRAFFIC):
+        return None
+    m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.eE+]+)", open(PROFILE_TRAFFIC).read(), re.M)
+    return float(m.group(1)) if m else None
+
+
+def cpu_baseline(M=2048, N=2048, K=2048):
+    """The reference's own INT8 rung (gemm_bench.c:278 gemm_int8_kernel,
+    AVX-512 VNNI, single-threaded as in the reference) built from source into
+    oracle/_ref, on the full primary problem; falls back to the oracle's exact
+    integer GEMM on a bounded row sample when that build is unusable here."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import numpy as np
+
+    import binding as ob
+
+    Au = ob.u8((M, K), 11)
+    gb = ob.ref("libref_gemm_bench.so")
+    if gb is not None and gb.pcl_ref_cpu_ok():
+        Bq = ob.s8((K, N), 12)
+        Bp = np.empty((N // 16) * (K // 4) * 64, np.int8)
+        for j in range(4):  # VNNI panel layout of gemm_bench.c:254
+            Bp.reshape(N // 16, K // 4, 16, 4)[:, :, :, j] = Bq[j::4, :].reshape(K // 4, N // 16, 16).transpose(1, 0, 2)
+        corr = (128 * Bq.astype(np.int64).sum(0)).astype(np.int32)
+        dq = ob.uniform((N,), 14, 1e-3, 1e-2)
+        Cm = np.empty((M, N), np.float32)
+        best = 1e30
+        for _ in range(3):
+            t0 = time.perf_counter()
+            gb.pcl_ref_gemm_int8_kernel(ob.p(Au), K, ob.p(Bp), ob.p(corr), ob.p(dq), ob.p(Cm), M, N)
+            best = min(best, time.perf_counter() - t0)
+        return {"value": round(2.0 * M * N * K / best / 1e12, 4), "unit": "TOP/s", "cores": 1,
+                "kind": "reference",
+                "sample": f"full {M}x{N}x{K} u8 x s8 problem through the reference gemm_int8_kernel "
+                          "(AVX-512 VNNI, gemm_bench.c:278-285, single-threaded as in gemm_bench), best of 3"}
+    rows = 128
+    Bq = ob.s8((K, N), 12)
+    threads = os.cpu_count() or 1
+    t0 = time.perf_counter()
+    ob.gemm_u8s8_i32(Au[:rows], Bq)
+    dt = time.perf_counter() - t0
+    return {"value": round(2.0 * rows * N * K / dt / 1e12, 6), "unit": "TOP/s", "cores": threads, "kind": "port",
+            "sample": f"{rows} of {M} rows of the {M}x{N}x{K} problem through the oracle's exact int64 GEMM "
+                      "(the reference VNNI build is unavailable on this host)"}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--primary-only", action="store_true", help="time only the headline kernel (profiling runs)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="also run device-to-device copies of this size (HBM counter calibration)")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one MI355X: this build has no multi-GPU path (each GPU box here has one GPU; "
+              "see DESIGN.md for how the GEMMs would shard). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    pcl, lib = load_bench()
+    pcl.check(pcl.lib.pcl_init())
+    info = pcl.device_info()
+    M = N = K = 2048
+    pcl.sync()
+    t0 = time.perf_counter()
+    prim = igemm(pcl, lib, M, N, K, 2, args.warmup, args.steps)
+    wall = time.perf_counter() - t0
+    tops = prim["TOPS"]
+    out = {
+        "metric": METRIC,
+        "value": tops,
+        "unit": "TOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": prim["ms"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (xorshift32 u8 activations, s8 weights, scales U[1e-3,1e-2])",
+        "config": {"workload": "gemm_bench INT8 GEMM M=N=K=2048, u8 x s8 -> int32, per-row x per-column dequant "
+                               "to fp32 (BASELINE.json configs[1])",
+                   "M": M, "N": N, "K": K, "kernel": "igemm_mfma_kernel (v_mfma_i32_32x32x32_i8)",
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": tops, "peak": PEAK_I8_TOPS, "unit": "TOP/s",
+                     "frac": round(tops / PEAK_I8_TOPS, 4), "traffic": read_traffic(),
+                     "algorithmic_ops_per_launch": 2 * M * N * K,
+                     "algorithmic_bytes_per_launch": M * K + K * N + 4 * M * N + 4 * (M + N)},
+        "device": info,
+        "timed_wall_s": round(wall, 3),
+    }
+    if args.calib_copy_mib:
+        nb = args.calib_copy_mib << 20
+        src, dst = pcl.DeviceBuffer(nb), pcl.DeviceBuffer(nb)
+        for _ in range(3):
+            pcl.check(pcl.lib.pcl_memcpy_d2d(dst.ptr, src.ptr, nb))
+        out["calib_copy_bytes"] = nb
+    if not args.primary_only:
+        w, s = 5, 20
+        ex = {}
+        ex["fp32_gemm_1024"] = sgemm(pcl, lib, 0, 0, 1024, 1024, 1024, 0, w, 50)
+        ex["int8_350m"] = {name: igemm(pcl, lib, m, n, k, 2, w, s) for name, (m, n, k) in {
+            "qkv": (4096, 3072, 1024), "attn_out": (4096, 1024, 1024), "ffn_up": (4096, 4096, 1024),
+            "ffn_down": (4096, 1024, 4096), "head": (4096, 50257, 1024)}.items()}
+        ex["fp32_350m"] = {name: sgemm(pcl, lib, a, b, m, n, k, acc, w, s) for name, (a, b, m, n, k, acc) in {
+            "qkv": (0, 0, 4096, 3072, 1024, 0), "attn_out": (0, 0, 4096, 1024, 1024, 0),
+            "ffn_up": (0, 0, 4096, 4096, 1024, 0), "ffn_down": (0, 0, 4096, 1024, 4096, 0),
+            "head_nt": (0, 1, 4096, 50257, 1024, 0),
+            "bwd_dX_ffn_up_nt": (0, 1, 4096, 1024, 4096, 1), "bwd_dW_ffn_up_tn": (1, 0, 1024, 4096, 4096, 1)}.items()}
+        ex["grown_prefill_t256"] = {
+            "fp32": {name: sgemm(pcl, lib, a, b, m, n, k, 0, w, 50) for name, (a, b, m, n, k) in {
+                "qkv": (0, 0, 256, 1536, 512), "attn_out": (0, 0, 256, 512, 512), "ffn_up": (0, 0, 256, 2048, 512),
+                "ffn_down": (0, 0, 256, 512, 2048), "head_nt": (0, 1, 256, 2048, 512)}.items()},
+            "int8": {name: igemm(pcl, lib, m, n, k, 2, w, 50) for name, (m, n, k) in {
+                "qkv": (256, 1536, 512), "attn_out": (256, 512, 512), "ffn_up": (256, 2048, 512),
+                "ffn_down": (256, 512, 2048), "head": (256, 2048, 512)}.items()},
+        }
+        layer = [(512, 1536), (512, 512), (512, 2048), (2048, 512)]
+        grown_i8 = layer * 16 + [(512, 2048)]
+        dec = {}
+        for Mt in (1, 4, 8):
+            # FP32: 16 layers (K x N weights) + tied head (N x K), 3 rotating copies
+            # (3 x 205 MB > the 256 MB Infinity Cache); INT8: 11 copies of 51 MB
+            lay = gemv(pcl, lib, 0, Mt, layer * 16, 3, 2, 10)
+            head = gemv(pcl, lib, 1, Mt, [(512, 2048)], 130, 2, 130)
+            t = lay["ms_per_sweep"] + head["ms_per_sweep"]
+            b = lay["bytes_per_sweep"] + head["bytes_per_sweep"]
+            dec[f"fp32_M{Mt}"] = {"ms_per_token_step": round(t, 4), "GBps": round(b / (t * 1e-3) / 1e9, 1),
+                                  "frac_hbm": round(b / (t * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+            dec[f"int8_M{Mt}"] = gemv(pcl, lib, 2, Mt, grown_i8, 11, 2, 10)
+        ex["grown_decode_gemv"] = dec
+        ex["head_350m_gemv_fp32"] = {f"M{Mt}": gemv(pcl, lib, 1, Mt, [(1024, 50257)], 3, 2, 20) for Mt in (1, 8)}
+        ex["head_350m_gemv_int8"] = {f"M{Mt}": gemv(pcl, lib, 2, Mt, [(1024, 50257)], 6, 2, 20) for Mt in (1, 8)}
+        out["extra"] = ex
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(M, N, K)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -53,7 +53,9 @@ enum {
 /* Library set-up. Every entry point initialises lazily; calling this first
  * only moves the cost (device query, workspace) out of the first GEMM. */
 int pcl_init(void);
-/* Status and message of the most recent failing call on this thread. */
+/* Status and message on this thread: the outcome of the most recent void
+ * drop-in call (PCL_OK after a success), or of a later native call that
+ * failed (native calls report success only through their return value). */
 int pcl_last_status(void);
 const char *pcl_last_error(void);
 void pcl_clear_error(void);

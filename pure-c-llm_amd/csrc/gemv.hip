@@ -11,9 +11,11 @@
 // Every weight byte is read exactly once, with 16-byte loads along the
 // contiguous dimension; the few activation rows are staged in LDS per block.
 // To fill 256 CUs when N alone gives too few blocks, K is split across
-// blocks. Partial sums go to a workspace and the last block of each column
-// strip to arrive (an arrival counter, reset by that block) adds them in
-// split order, so results are deterministic run to run.
+// blocks: each block writes its partial sums to a workspace and a second,
+// small kernel adds the splits in split order (plus bias / accumulate /
+// dequant), so results are deterministic run to run. The kernel boundary
+// orders the two; no block ever waits on another, and no cross-XCD cache
+// maintenance is issued inside a kernel.
 #include "internal.h"
 
 namespace pcl {
@@ -23,31 +25,31 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int GV_THREADS = 256;
 constexpr int GV_TARGET_BLOCKS = 1024;   // ~4 per CU
-constexpr int SGN_KCH_MAX = 512;         // sgemv_n: staged X rows per block
-constexpr int SGT_KCH_MAX = 512;         // sgemv_t: staged X columns per block
-constexpr int IGV_KCH_MAX = 2048;        // igemv: staged X bytes per row per block
+// Activation rows staged in LDS per block: MR rows x KCH elements, sized so
+// the staging takes 16 KB (sgemv_n), 32 KB (sgemv_t) or 16 KB (igemv).
+template <int MR> struct Kch {
+    static constexpr int SGN = 4096 / MR;   // floats
+    static constexpr int SGT = 8192 / MR;   // floats
+    static constexpr int IGV = 16384 / MR;  // bytes
+};
 constexpr int SGT_RPL = 2;               // sgemv_t / igemv rows per 16-lane group
 constexpr int SGT_ROWS = 16 * SGT_RPL;   // rows of W per block
 
 static int cdiv(long a, long b) { return (int)((a + b - 1) / b); }
 
-// Signals that this block is the last of `splits` to finish its strip.
-// Must be called by all threads after the block's partial stores.
-__device__ __forceinline__ bool last_block_arrived(unsigned *counters, int strip, int splits) {
-    __shared__ int is_last;
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        unsigned prev = atomicAdd(&counters[strip], 1u);
-        is_last = (prev == (unsigned)(splits - 1));
-    }
-    __syncthreads();
-    if (is_last) __threadfence();
-    return is_last != 0;
-}
-
-__device__ __forceinline__ void reset_counter(unsigned *counters, int strip) {
-    if (threadIdx.x == 0) atomicExch(&counters[strip], 0u);
+// Second pass of a split-K GEMV: Y[m,n] = sum over splits in order (+ bias,
+// + Y when accumulating). part is [splits][M][nround].
+__global__ void sgemv_reduce_kernel(const float *__restrict__ part, int splits, int M, int N,
+                                    int nround, const float *__restrict__ bias,
+                                    float *__restrict__ Y, long ldy, int accumulate) {
+    const long i = blockIdx.x * (long)blockDim.x + threadIdx.x;
+    if (i >= (long)M * N) return;
+    const int m = (int)(i / N), n = (int)(i % N);
+    float s = 0.f;
+    for (int q = 0; q < splits; q++) s += part[((long)q * M + m) * nround + n];
+    float y = s + (bias ? bias[n] : 0.f);
+    float *dst = Y + (long)m * ldy + n;
+    *dst = accumulate ? *dst + y : y;
 }
 
 // ------------------------------------------------------------- sgemv_n ----
@@ -57,10 +59,9 @@ template <int MR, bool VEC, bool XONES>
 __global__ __launch_bounds__(GV_THREADS) void sgemv_n_kernel(
     const float *__restrict__ X, long ldx, const float *__restrict__ W, long ldw,
     const float *__restrict__ bias, float *__restrict__ Y, long ldy, int M, int N, int K,
-    int kchunk, int splits, float *__restrict__ part, unsigned *__restrict__ counters,
-    int accumulate) {
+    int kchunk, int splits, float *__restrict__ part, int accumulate) {
     __shared__ float red[16][MR][64];
-    __shared__ float xs[XONES ? 1 : MR][XONES ? 1 : SGN_KCH_MAX];
+    __shared__ float xs[XONES ? 1 : MR][XONES ? 1 : Kch<MR>::SGN];
 
     const int tid = threadIdx.x;
     const int c4 = tid & 15, rg = tid >> 4;
@@ -134,18 +135,6 @@ __global__ __launch_bounds__(GV_THREADS) void sgemv_n_kernel(
             part[((long)sp * M + m) * nround + n] = s;
         }
     }
-    if (splits == 1) return;
-    if (!last_block_arrived(counters, strip, splits)) return;
-    for (int o = tid; o < M * 64; o += GV_THREADS) {
-        const int m = o / 64, c = o % 64, n = n0 + c;
-        if (n >= N) continue;
-        float s = 0.f;
-        for (int q = 0; q < splits; q++) s += part[((long)q * M + m) * nround + n];
-        float y = s + (bias ? bias[n] : 0.f);
-        float *dst = Y + (long)m * ldy + n;
-        *dst = accumulate ? *dst + y : y;
-    }
-    reset_counter(counters, strip);
 }
 
 // ------------------------------------------------------------- sgemv_t ----
@@ -155,9 +144,8 @@ template <int MR, bool VEC>
 __global__ __launch_bounds__(GV_THREADS) void sgemv_t_kernel(
     const float *__restrict__ X, long ldx, const float *__restrict__ W, long ldw,
     const float *__restrict__ bias, float *__restrict__ Y, long ldy, int M, int N, int K,
-    int kchunk, int splits, float *__restrict__ part, unsigned *__restrict__ counters,
-    int accumulate) {
-    __shared__ __attribute__((aligned(16))) float xs[MR][SGT_KCH_MAX];
+    int kchunk, int splits, float *__restrict__ part, int accumulate) {
+    __shared__ __attribute__((aligned(16))) float xs[MR][Kch<MR>::SGT];
     __shared__ float res[MR][SGT_ROWS];
 
     const int tid = threadIdx.x;
@@ -237,18 +225,6 @@ __global__ __launch_bounds__(GV_THREADS) void sgemv_t_kernel(
             part[((long)sp * M + m) * nround + n] = s;
         }
     }
-    if (splits == 1) return;
-    if (!last_block_arrived(counters, strip, splits)) return;
-    for (int o = tid; o < M * SGT_ROWS; o += GV_THREADS) {
-        const int m = o / SGT_ROWS, c = o % SGT_ROWS, n = n0 + c;
-        if (n >= N) continue;
-        float s = 0.f;
-        for (int q = 0; q < splits; q++) s += part[((long)q * M + m) * nround + n];
-        float y = s + (bias ? bias[n] : 0.f);
-        float *dst = Y + (long)m * ldy + n;
-        *dst = accumulate ? *dst + y : y;
-    }
-    reset_counter(counters, strip);
 }
 
 // --------------------------------------------------------------- igemv ----
@@ -259,13 +235,41 @@ __device__ __forceinline__ int32_t epi_int(int32_t v, const int32_t *col_off, in
     return col_off ? (int32_t)((unsigned)v + (unsigned)col_off[n]) : v;
 }
 
+template <int OUT>
+__device__ __forceinline__ void igemv_write(void *Yv, long ldy, int m, int n, int32_t v,
+                                            const int32_t *col_off, const float *sa,
+                                            const float *sb) {
+    v = epi_int(v, col_off, n);
+    if (OUT == 0) {
+        reinterpret_cast<int32_t *>(Yv)[(long)m * ldy + n] = v;
+    } else {
+        const float dq = (OUT == 2) ? sa[m] * sb[n] : sb[n];
+        reinterpret_cast<float *>(Yv)[(long)m * ldy + n] = (float)v * dq;
+    }
+}
+
+// Second pass of a split-K INT8 GEMV: exact int32 sum of the splits, then the
+// epilogue of the single-pass kernel.
+template <int OUT>
+__global__ void igemv_reduce_kernel(const int32_t *__restrict__ part, int splits, int M, int N,
+                                    int nround, const int32_t *__restrict__ col_off,
+                                    const float *__restrict__ sa, const float *__restrict__ sb,
+                                    void *__restrict__ Yv, long ldy) {
+    const long i = blockIdx.x * (long)blockDim.x + threadIdx.x;
+    if (i >= (long)M * N) return;
+    const int m = (int)(i / N), n = (int)(i % N);
+    unsigned s = 0;
+    for (int q = 0; q < splits; q++) s += (unsigned)part[((long)q * M + m) * nround + n];
+    igemv_write<OUT>(Yv, ldy, m, n, (int32_t)s, col_off, sa, sb);
+}
+
 template <int MR, int OUT>
 __global__ __launch_bounds__(GV_THREADS) void igemv_kernel(
     const uint8_t *__restrict__ X, long ldx, const int8_t *__restrict__ B, long ldb,
     const int32_t *__restrict__ col_off, const float *__restrict__ sa,
     const float *__restrict__ sb, void *__restrict__ Yv, long ldy, int M, int N, int K,
-    int kchunk, int splits, int32_t *__restrict__ part, unsigned *__restrict__ counters) {
-    __shared__ __attribute__((aligned(16))) int8_t xs[MR][IGV_KCH_MAX];
+    int kchunk, int splits, int32_t *__restrict__ part) {
+    __shared__ __attribute__((aligned(16))) int8_t xs[MR][Kch<MR>::IGV];
     __shared__ int32_t res[MR][SGT_ROWS];
 
     const int tid = threadIdx.x;
@@ -331,45 +335,30 @@ __global__ __launch_bounds__(GV_THREADS) void igemv_kernel(
     }
     __syncthreads();
 
-    auto write_out = [&](int m, int n, int32_t v) {
-        v = epi_int(v, col_off, n);
-        if (OUT == 0) {
-            reinterpret_cast<int32_t *>(Yv)[(long)m * ldy + n] = v;
-        } else {
-            const float dq = (OUT == 2) ? sa[m] * sb[n] : sb[n];
-            reinterpret_cast<float *>(Yv)[(long)m * ldy + n] = (float)v * dq;
-        }
-    };
-
     const int nround = gridDim.x * SGT_ROWS;
     for (int o = tid; o < M * SGT_ROWS; o += GV_THREADS) {
         const int m = o / SGT_ROWS, c = o % SGT_ROWS, n = n0 + c;
         if (splits == 1) {
-            if (n < N) write_out(m, n, res[m][c]);
+            if (n < N) igemv_write<OUT>(Yv, ldy, m, n, res[m][c], col_off, sa, sb);
         } else {
             part[((long)sp * M + m) * nround + n] = res[m][c];
         }
     }
-    if (splits == 1) return;
-    if (!last_block_arrived(counters, strip, splits)) return;
-    for (int o = tid; o < M * SGT_ROWS; o += GV_THREADS) {
-        const int m = o / SGT_ROWS, c = o % SGT_ROWS, n = n0 + c;
-        if (n >= N) continue;
-        unsigned s = 0;
-        for (int q = 0; q < splits; q++) s += (unsigned)part[((long)q * M + m) * nround + n];
-        write_out(m, n, (int32_t)s);
-    }
-    reset_counter(counters, strip);
 }
 
 // ------------------------------------------------------------- planning ----
-static GemvPlan make_plan(int strips, int M, int K, int kstep, int kmax, int rows_per_strip) {
+static int mr_of(int M) { return M <= 1 ? 1 : (M <= 2 ? 2 : (M <= 4 ? 4 : 8)); }
+
+// strips: blocks along N; kstep: K granularity of a split; kmin: least K per
+// block worth a block; kmax: most K a block can stage.
+static GemvPlan make_plan(int strips, int M, int K, int kstep, int kmin, int kmax,
+                          int rows_per_strip) {
     GemvPlan p;
     p.strips = strips;
     int want = GV_TARGET_BLOCKS / (strips > 0 ? strips : 1);
-    int max_splits = cdiv(K, kstep);
     int splits = want < 1 ? 1 : want;
-    if (splits > max_splits) splits = max_splits;
+    int most = cdiv(K, kmin);
+    if (splits > most) splits = most;
     if (splits < 1) splits = 1;
     int kchunk = cdiv(cdiv(K, splits), kstep) * kstep;
     if (kchunk > kmax) kchunk = kmax;
@@ -382,15 +371,18 @@ static GemvPlan make_plan(int strips, int M, int K, int kstep, int kmax, int row
 }
 
 GemvPlan plan_sgemv(int w_trans, int M, int N, int K) {
-    if (w_trans) return make_plan(cdiv(N, SGT_ROWS), M, K, 64, SGT_KCH_MAX, SGT_ROWS);
-    return make_plan(cdiv(N, 64), M, K, 64, SGN_KCH_MAX, 64);
+    const int mr = mr_of(M);
+    if (w_trans) return make_plan(cdiv(N, SGT_ROWS), M, K, 64, 256, 8192 / mr, SGT_ROWS);
+    return make_plan(cdiv(N, 64), M, K, 64, 128, 4096 / mr, 64);
 }
 
 GemvPlan plan_igemv(int M, int N, int K) {
-    return make_plan(cdiv(N, SGT_ROWS), M, K, 256, IGV_KCH_MAX, SGT_ROWS);
+    return make_plan(cdiv(N, SGT_ROWS), M, K, 256, 1024, 16384 / mr_of(M), SGT_ROWS);
 }
 
 static bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+static int reduce_grid(int M, int N) { return cdiv((long)M * N, 256); }
 
 template <int MR>
 static void launch_sgemv_mr(const GemvPlan &p, int w_trans, bool vec, bool x_ones, int M, int N,
@@ -402,28 +394,29 @@ static void launch_sgemv_mr(const GemvPlan &p, int w_trans, bool vec, bool x_one
     if (w_trans) {
         if (vec)
             hipLaunchKernelGGL((sgemv_t_kernel<MR, true>), grid, block, 0, s, X, ldx, W, ldw, bias,
-                               Y, ldy, M, N, K, p.kchunk, p.splits, part, ws.counters, accumulate);
+                               Y, ldy, M, N, K, p.kchunk, p.splits, part, accumulate);
         else
             hipLaunchKernelGGL((sgemv_t_kernel<MR, false>), grid, block, 0, s, X, ldx, W, ldw, bias,
-                               Y, ldy, M, N, K, p.kchunk, p.splits, part, ws.counters, accumulate);
+                               Y, ldy, M, N, K, p.kchunk, p.splits, part, accumulate);
     } else if (x_ones) {
         if (vec)
             hipLaunchKernelGGL((sgemv_n_kernel<1, true, true>), grid, block, 0, s, X, ldx, W, ldw,
-                               bias, Y, ldy, M, N, K, p.kchunk, p.splits, part, ws.counters,
-                               accumulate);
+                               bias, Y, ldy, M, N, K, p.kchunk, p.splits, part, accumulate);
         else
             hipLaunchKernelGGL((sgemv_n_kernel<1, false, true>), grid, block, 0, s, X, ldx, W, ldw,
-                               bias, Y, ldy, M, N, K, p.kchunk, p.splits, part, ws.counters,
-                               accumulate);
+                               bias, Y, ldy, M, N, K, p.kchunk, p.splits, part, accumulate);
     } else {
         if (vec)
             hipLaunchKernelGGL((sgemv_n_kernel<MR, true, false>), grid, block, 0, s, X, ldx, W, ldw,
-                               bias, Y, ldy, M, N, K, p.kchunk, p.splits, part, ws.counters,
-                               accumulate);
+                               bias, Y, ldy, M, N, K, p.kchunk, p.splits, part, accumulate);
         else
             hipLaunchKernelGGL((sgemv_n_kernel<MR, false, false>), grid, block, 0, s, X, ldx, W,
-                               ldw, bias, Y, ldy, M, N, K, p.kchunk, p.splits, part, ws.counters,
-                               accumulate);
+                               ldw, bias, Y, ldy, M, N, K, p.kchunk, p.splits, part, accumulate);
+    }
+    if (p.splits > 1) {
+        const int nround = p.strips * (w_trans ? SGT_ROWS : 64);
+        hipLaunchKernelGGL(sgemv_reduce_kernel, dim3(reduce_grid(M, N)), dim3(256), 0, s, part,
+                           p.splits, M, N, nround, bias, Y, ldy, accumulate);
     }
 }
 
@@ -459,15 +452,27 @@ static void launch_igemv_mr(const GemvPlan &p, int out_mode, int M, int N, int K
                             long ldy, const Workspace &ws, hipStream_t s) {
     dim3 grid(p.strips, p.splits), block(GV_THREADS);
     int32_t *part = (int32_t *)ws.buf;
-    if (out_mode == 0)
+    const int nround = p.strips * SGT_ROWS;
+    const dim3 rg(reduce_grid(M, N)), rb(256);
+    if (out_mode == 0) {
         hipLaunchKernelGGL((igemv_kernel<MR, 0>), grid, block, 0, s, X, ldx, B, ldb, col_off, sa,
-                           sb, Y, ldy, M, N, K, p.kchunk, p.splits, part, ws.counters);
-    else if (out_mode == 1)
+                           sb, Y, ldy, M, N, K, p.kchunk, p.splits, part);
+        if (p.splits > 1)
+            hipLaunchKernelGGL((igemv_reduce_kernel<0>), rg, rb, 0, s, part, p.splits, M, N,
+                               nround, col_off, sa, sb, Y, ldy);
+    } else if (out_mode == 1) {
         hipLaunchKernelGGL((igemv_kernel<MR, 1>), grid, block, 0, s, X, ldx, B, ldb, col_off, sa,
-                           sb, Y, ldy, M, N, K, p.kchunk, p.splits, part, ws.counters);
-    else
+                           sb, Y, ldy, M, N, K, p.kchunk, p.splits, part);
+        if (p.splits > 1)
+            hipLaunchKernelGGL((igemv_reduce_kernel<1>), rg, rb, 0, s, part, p.splits, M, N,
+                               nround, col_off, sa, sb, Y, ldy);
+    } else {
         hipLaunchKernelGGL((igemv_kernel<MR, 2>), grid, block, 0, s, X, ldx, B, ldb, col_off, sa,
-                           sb, Y, ldy, M, N, K, p.kchunk, p.splits, part, ws.counters);
+                           sb, Y, ldy, M, N, K, p.kchunk, p.splits, part);
+        if (p.splits > 1)
+            hipLaunchKernelGGL((igemv_reduce_kernel<2>), rg, rb, 0, s, part, p.splits, M, N,
+                               nround, col_off, sa, sb, Y, ldy);
+    }
 }
 
 hipError_t launch_igemv(const GemvPlan &p, int out_mode, int M, int N, int K, const uint8_t *X,

@@ -8,14 +8,12 @@
 
 namespace pcl {
 
-// Scratch memory that a launcher may use: partial sums of split-K GEMVs and
-// the per-strip arrival counters of their last-block reductions. The counters
-// are zero when a call starts and every kernel leaves them zero again.
+// Scratch memory that a launcher may use: the partial sums of a split-K GEMV
+// ([splits][M][strips * rows per strip]), written by the GEMV kernel and
+// summed by its reduce kernel on the same stream.
 struct Workspace {
-    void *buf = nullptr;       // partial sums (bytes_cap bytes)
+    void *buf = nullptr;  // bytes_cap bytes
     size_t bytes_cap = 0;
-    unsigned *counters = nullptr;  // counters_cap entries, kept all-zero
-    int counters_cap = 0;
 };
 
 // Split-K GEMV geometry chosen by the launchers; the shim sizes the workspace.
@@ -36,7 +34,8 @@ hipError_t launch_sgemm(bool a_kcontig, bool b_kcontig, int M, int N, int K, con
 
 // ---- INT8 GEMM (igemm.hip) ----
 // out_mode 0: C is int32 v; 1: C = float(v+off)*sb[n]; 2: C = float(v+off)*(sa[m]*sb[n])
-// Requires K % 16 == 0, lda % 16 == 0, A and Bpk 16-byte aligned, ldb % 16 == 0.
+// Requires K % 16 == 0, lda % 16 == 0, A and Bpk 16-byte aligned, and packed
+// weight rows of ldb = roundup(K, 256) bytes, zero past K.
 hipError_t launch_igemm(int out_mode, int M, int N, int K, const uint8_t *A, long lda,
                         const int8_t *Bpk, long ldb, const int32_t *col_off, const float *sa,
                         const float *sb, void *C, long ldc, hipStream_t stream);

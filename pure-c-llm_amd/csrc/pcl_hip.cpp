@@ -39,8 +39,13 @@ int set_error(int status, const char *fmt, ...) {
     return status;
 }
 
+// Every void drop-in ends here: its own outcome becomes pcl_last_status(),
+// so a success clears an earlier failure (the caller's only way to check).
 void finish_void(int status) {
-    if (status != PCL_OK && g_abort_on_error) {
+    if (status == PCL_OK) {
+        t_status = PCL_OK;
+        t_msg[0] = 0;
+    } else if (g_abort_on_error) {
         fprintf(stderr, "libpcl_hip error %d: %s\n", status, t_msg);
         exit(1);
     }
@@ -131,25 +136,11 @@ int grow(void **p, size_t *cap, size_t need, hipStream_t s) {
     return PCL_OK;
 }
 
-int get_scratch(hipStream_t s, size_t part_bytes, int counters, size_t aux_bytes,
-                StreamScratch **out) {
+int get_scratch(hipStream_t s, size_t part_bytes, size_t aux_bytes, StreamScratch **out) {
     std::lock_guard<std::mutex> lk(g_mu);
     StreamScratch &sc = g_scratch[s];
     PCL_OK_OR_RETURN(grow(&sc.ws.buf, &sc.ws.bytes_cap, part_bytes, s));
     PCL_OK_OR_RETURN(grow(&sc.aux, &sc.aux_cap, aux_bytes, s));
-    if (counters > sc.ws.counters_cap) {
-        if (sc.ws.counters) {
-            HIP_OK(hipStreamSynchronize(s));
-            HIP_OK(hipFree(sc.ws.counters));
-            sc.ws.counters = nullptr;
-            sc.ws.counters_cap = 0;
-        }
-        int cap = counters < 4096 ? 4096 : counters * 2;
-        if (hipMalloc((void **)&sc.ws.counters, sizeof(unsigned) * cap) != hipSuccess)
-            return set_error(PCL_ERR_OOM, "counter allocation failed");
-        HIP_OK(hipMemset(sc.ws.counters, 0, sizeof(unsigned) * cap));
-        sc.ws.counters_cap = cap;
-    }
     if (!sc.amax) {
         if (hipMalloc((void **)&sc.amax, 256) != hipSuccess)
             return set_error(PCL_ERR_OOM, "amax scratch allocation failed");
@@ -162,7 +153,10 @@ hipStream_t pick(void *stream) { return stream ? (hipStream_t)stream : t_stream;
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-int kpad64(int K) { return ((K + 63) / 64) * 64; }
+// Packed INT8 weight rows: K rounded up to 256 bytes (a multiple of every K
+// tile the INT8 GEMM uses), zero padded, so every K-tile read of a weight row
+// stays inside that row.
+int kpad256(int K) { return ((K + 255) / 256) * 256; }
 
 // ------------------------------------------------------- host staging ----
 // Device copies of host operands for the host-pointer drop-ins; one growing
@@ -333,7 +327,7 @@ int pcl_sgemv(int opW, int M, int N, int K, const float *X, int ldx, const float
     hipStream_t s = pick(stream);
     pcl::GemvPlan p = pcl::plan_sgemv(opW == PCL_OP_T, M, N, K);
     StreamScratch *sc;
-    PCL_OK_OR_RETURN(get_scratch(s, p.part_bytes, p.strips, 0, &sc));
+    PCL_OK_OR_RETURN(get_scratch(s, p.part_bytes, 0, &sc));
     HIP_OK(pcl::launch_sgemv(p, opW == PCL_OP_T, M, N, K, X, ldx, false, W, ldw, bias, accumulate,
                              Y, ldy, sc->ws, s));
     return PCL_OK;
@@ -372,13 +366,13 @@ int pcl_bias_bwd(float *db, const float *dY, int M, int N, int ld, void *stream)
     hipStream_t s = pick(stream);
     pcl::GemvPlan p = pcl::plan_sgemv(0, 1, N, M);
     StreamScratch *sc;
-    PCL_OK_OR_RETURN(get_scratch(s, p.part_bytes, p.strips, 0, &sc));
+    PCL_OK_OR_RETURN(get_scratch(s, p.part_bytes, 0, &sc));
     HIP_OK(pcl::launch_sgemv(p, 0, 1, N, M, nullptr, 0, true, dY, ld, nullptr, 1, db, N, sc->ws, s));
     return PCL_OK;
 }
 
 // ----------------------------------------------------------- INT8 native ----
-int pcl_s8_kpad(int K) { return kpad64(K < 0 ? 0 : K); }
+int pcl_s8_kpad(int K) { return kpad256(K < 0 ? 0 : K); }
 size_t pcl_s8_packed_bytes(int K, int N) {
     return (size_t)(N < 0 ? 0 : N) * (size_t)pcl_s8_kpad(K);
 }
@@ -390,7 +384,7 @@ int pcl_pack_b_s8(const int8_t *B, int ldb, int K, int N, int8_t *Bpk, int32_t *
     CHECK_ARG(Bpk != nullptr && (K == 0 || B != nullptr), "pcl_pack_b_s8: NULL operand");
     CHECK_ARG(K == 0 || ldb >= N, "pcl_pack_b_s8: ldb=%d < N=%d", ldb, N);
     PCL_OK_OR_RETURN(do_init());
-    HIP_OK(pcl::launch_pack_b_s8(B, ldb, K, N, Bpk, kpad64(K), colsum, pick(stream)));
+    HIP_OK(pcl::launch_pack_b_s8(B, ldb, K, N, Bpk, kpad256(K), colsum, pick(stream)));
     return PCL_OK;
 }
 
@@ -403,7 +397,7 @@ int pcl_pack_b_vnni(const int8_t *Bp, int K, int Kpad, int N, int8_t *Bpk, int32
     CHECK_ARG(Bpk != nullptr && (K == 0 || Bp != nullptr), "pcl_pack_b_vnni: NULL operand");
     CHECK_ARG((reinterpret_cast<uintptr_t>(Bp) & 3) == 0, "pcl_pack_b_vnni: Bp not 4-byte aligned");
     PCL_OK_OR_RETURN(do_init());
-    HIP_OK(pcl::launch_pack_b_vnni(Bp, K, Kpad, N, Bpk, kpad64(K), colsum, pick(stream)));
+    HIP_OK(pcl::launch_pack_b_vnni(Bp, K, Kpad, N, Bpk, kpad256(K), colsum, pick(stream)));
     return PCL_OK;
 }
 
@@ -427,12 +421,12 @@ static int igemm_common(int out_mode, const uint8_t *A, int lda, const int8_t *B
     CHECK_ARG(out_mode != 2 || sa, "%s: sa is NULL", who);
     CHECK_ARG(aligned16(Bpk), "%s: packed weights must be 16-byte aligned", who);
     PCL_OK_OR_RETURN(do_init());
-    const long ldb = kpad64(K);
+    const long ldb = kpad256(K);
     hipStream_t s = pick(stream);
     if (M <= 8) {
         pcl::GemvPlan p = pcl::plan_igemv(M, N, K);
         StreamScratch *sc;
-        PCL_OK_OR_RETURN(get_scratch(s, p.part_bytes, p.strips, 0, &sc));
+        PCL_OK_OR_RETURN(get_scratch(s, p.part_bytes, 0, &sc));
         HIP_OK(pcl::launch_igemv(p, out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa, sb, C, ldc,
                                  sc->ws, s));
         return PCL_OK;
@@ -444,7 +438,7 @@ static int igemm_common(int out_mode, const uint8_t *A, int lda, const int8_t *B
     // Unaligned activations: copy into a K16-wide padded buffer first.
     const int K16 = (K + 15) & ~15;
     StreamScratch *sc;
-    PCL_OK_OR_RETURN(get_scratch(s, 0, 0, (size_t)M * K16, &sc));
+    PCL_OK_OR_RETURN(get_scratch(s, 0, (size_t)M * K16, &sc));
     uint8_t *Ap = (uint8_t *)sc->aux;
     HIP_OK(pcl::launch_pad_a_u8(A, lda, M, K, Ap, K16, s));
     HIP_OK(pcl::launch_igemm(out_mode, M, N, K16, Ap, K16, Bpk, ldb, col_off, sa, sb, C, ldc, s));
@@ -487,7 +481,7 @@ int pcl_quantize_a_tensor(const float *A, int M, int K, uint8_t *Au, int Kpad, f
     PCL_OK_OR_RETURN(do_init());
     hipStream_t s = pick(stream);
     StreamScratch *sc;
-    PCL_OK_OR_RETURN(get_scratch(s, 0, 0, 0, &sc));
+    PCL_OK_OR_RETURN(get_scratch(s, 0, 0, &sc));
     HIP_OK(pcl::launch_quantize_a_tensor(A, M, K, Au, Kpad, scale_dev, sc->amax, s));
     return PCL_OK;
 }
@@ -509,7 +503,7 @@ int pcl_quantize_b_cols(const float *B, int K, int N, int8_t *Bpk, float *bscale
     if (N == 0) return PCL_OK;
     CHECK_ARG(Bpk && bscale && (K == 0 || B), "pcl_quantize_b_cols: NULL operand");
     PCL_OK_OR_RETURN(do_init());
-    HIP_OK(pcl::launch_quantize_b_cols(B, K, N, 0, Bpk, kpad64(K), 0, bscale, colsum, pick(stream)));
+    HIP_OK(pcl::launch_quantize_b_cols(B, K, N, 0, Bpk, kpad256(K), 0, bscale, colsum, pick(stream)));
     return PCL_OK;
 }
 

@@ -1,0 +1,273 @@
+/*
+ * bench_harness.c -- timing loops for bench.py, in C so that the launch rate
+ * of back-to-back kernels is set by the GPU, not by Python.
+ *
+ * Each pcl_bench_* call allocates its operands in HBM, fills them with
+ * synthetic data (xorshift32, the generator of train.c:73-78), runs `warmup`
+ * untimed steps, then times `steps` steps between two HIP events recorded on
+ * the library's stream, with the device synchronised before and after. One
+ * step is one call of the hot path (one kernel launch for GEMM/GEMV).
+ * Weight copies can be rotated (`copies` > 1) so a memory-bound kernel reads
+ * HBM rather than the 256 MB Infinity Cache.
+ *
+ * Built into libpcl_bench.so (see ../Makefile); only bench.py loads it.
+ */
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "pcl_hip.h"
+
+#define TRY(x)                          \
+    do {                                \
+        int s_ = (x);                   \
+        if (s_ != PCL_OK) {             \
+            rc = s_;                    \
+            goto done;                  \
+        }                               \
+    } while (0)
+
+static uint32_t xs32(uint32_t *s) {
+    uint32_t x = *s;
+    x ^= x << 13;
+    x ^= x >> 17;
+    x ^= x << 5;
+    return *s = x;
+}
+
+static void fill_f32(float *p, size_t n, uint32_t seed, float lo, float hi) {
+    uint32_t s = seed ? seed : 1u;
+    for (size_t i = 0; i < n; i++)
+        p[i] = lo + (hi - lo) * ((float)(xs32(&s) & 0xFFFFFFu) / 16777216.0f);
+}
+
+static void fill_bytes(uint8_t *p, size_t n, uint32_t seed) {
+    uint32_t s = seed ? seed : 1u;
+    size_t i = 0;
+    for (; i + 4 <= n; i += 4) {
+        uint32_t v = xs32(&s);
+        memcpy(p + i, &v, 4);
+    }
+    for (; i < n; i++) p[i] = (uint8_t)xs32(&s);
+}
+
+/* device buffer filled from a host staging copy */
+static void *dev_f32(size_t n, uint32_t seed, float lo, float hi) {
+    float *h = malloc(n * sizeof(float) + 16);
+    if (!h) return NULL;
+    fill_f32(h, n, seed, lo, hi);
+    void *d = pcl_malloc(n * sizeof(float));
+    if (d && pcl_memcpy_h2d(d, h, n * sizeof(float)) != PCL_OK) {
+        pcl_free(d);
+        d = NULL;
+    }
+    free(h);
+    return d;
+}
+
+static void *dev_bytes(size_t n, uint32_t seed) {
+    uint8_t *h = malloc(n + 16);
+    if (!h) return NULL;
+    fill_bytes(h, n, seed);
+    void *d = pcl_malloc(n);
+    if (d && pcl_memcpy_h2d(d, h, n) != PCL_OK) {
+        pcl_free(d);
+        d = NULL;
+    }
+    free(h);
+    return d;
+}
+
+typedef int (*step_fn)(void *ctx, int i);
+
+/* warmup + timed loop shared by every benchmark */
+static int time_steps(step_fn fn, void *ctx, int warmup, int steps, double *ms_total) {
+    int rc = PCL_OK;
+    void *e0 = NULL, *e1 = NULL;
+    float ms = 0.f;
+    for (int i = 0; i < warmup; i++) TRY(fn(ctx, i));
+    TRY(pcl_stream_synchronize());
+    e0 = pcl_event_create();
+    e1 = pcl_event_create();
+    if (!e0 || !e1) {
+        rc = PCL_ERR_HIP;
+        goto done;
+    }
+    TRY(pcl_event_record(e0));
+    for (int i = 0; i < steps; i++) TRY(fn(ctx, warmup + i));
+    TRY(pcl_event_record(e1));
+    TRY(pcl_event_elapsed_ms(e0, e1, &ms));
+    TRY(pcl_stream_synchronize());
+    *ms_total = ms;
+done:
+    if (e0) pcl_event_destroy(e0);
+    if (e1) pcl_event_destroy(e1);
+    return rc;
+}
+
+/* ------------------------------------------------------------ INT8 GEMM ---- */
+typedef struct {
+    int M, N, K, out_mode, copies;
+    void *A, *Bq, *Bpk[8], *sa, *sb, *C;
+} igemm_ctx;
+
+static int igemm_step(void *c_, int i) {
+    igemm_ctx *c = c_;
+    void *B = c->Bpk[i % c->copies];
+    if (c->out_mode == 0)
+        return pcl_gemm_u8s8_i32(c->A, c->K, B, c->C, c->N, c->M, c->N, c->K, NULL);
+    return pcl_gemm_u8s8_dq(c->A, c->K, B, NULL, c->out_mode == 2 ? c->sa : NULL, c->sb, c->C,
+                            c->N, c->M, c->N, c->K, NULL);
+}
+
+/* out_mode: 0 int32 out, 1 per-column dequant, 2 per-row x per-column dequant */
+int pcl_bench_igemm(int M, int N, int K, int out_mode, int copies, int warmup, int steps,
+                    double *ms_total) {
+    int rc = PCL_OK;
+    igemm_ctx c;
+    memset(&c, 0, sizeof c);
+    c.M = M, c.N = N, c.K = K, c.out_mode = out_mode;
+    c.copies = copies < 1 ? 1 : (copies > 8 ? 8 : copies);
+    c.A = dev_bytes((size_t)M * K, 11);
+    c.Bq = dev_bytes((size_t)K * N, 12);
+    c.sa = dev_f32(M, 13, 1e-3f, 1e-2f);
+    c.sb = dev_f32(N, 14, 1e-3f, 1e-2f);
+    c.C = pcl_malloc((size_t)M * N * 4);
+    if (!c.A || !c.Bq || !c.sa || !c.sb || !c.C) {
+        rc = PCL_ERR_OOM;
+        goto done;
+    }
+    for (int j = 0; j < c.copies; j++) {
+        c.Bpk[j] = pcl_malloc(pcl_s8_packed_bytes(K, N));
+        if (!c.Bpk[j]) {
+            rc = PCL_ERR_OOM;
+            goto done;
+        }
+        TRY(pcl_pack_b_s8(c.Bq, N, K, N, c.Bpk[j], NULL, NULL));
+    }
+    TRY(time_steps(igemm_step, &c, warmup, steps, ms_total));
+done:
+    pcl_free(c.A), pcl_free(c.Bq), pcl_free(c.sa), pcl_free(c.sb), pcl_free(c.C);
+    for (int j = 0; j < 8; j++) pcl_free(c.Bpk[j]);
+    return rc;
+}
+
+/* ------------------------------------------------------------ FP32 GEMM ---- */
+typedef struct {
+    int opA, opB, M, N, K, accumulate;
+    void *A, *B, *C;
+} sgemm_ctx;
+
+static int sgemm_step(void *c_, int i) {
+    sgemm_ctx *c = c_;
+    (void)i;
+    int lda = c->opA == PCL_OP_N ? c->K : c->M, ldb = c->opB == PCL_OP_N ? c->N : c->K;
+    return pcl_sgemm(c->opA, c->opB, c->M, c->N, c->K, c->A, lda, c->B, ldb, NULL, c->accumulate,
+                     c->C, c->N, NULL);
+}
+
+int pcl_bench_sgemm(int opA, int opB, int M, int N, int K, int accumulate, int warmup, int steps,
+                    double *ms_total) {
+    int rc = PCL_OK;
+    sgemm_ctx c = {opA, opB, M, N, K, accumulate, NULL, NULL, NULL};
+    c.A = dev_f32((size_t)M * K, 21, -1.f, 1.f);
+    c.B = dev_f32((size_t)K * N, 22, -1.f, 1.f);
+    c.C = dev_f32((size_t)M * N, 23, -1e-3f, 1e-3f);
+    if (!c.A || !c.B || !c.C) {
+        rc = PCL_ERR_OOM;
+        goto done;
+    }
+    TRY(time_steps(sgemm_step, &c, warmup, steps, ms_total));
+done:
+    pcl_free(c.A), pcl_free(c.B), pcl_free(c.C);
+    return rc;
+}
+
+/* ----------------------------------------------------------------- GEMV ---- */
+/* A decode sweep: per step, one GEMV per weight in `shapes` (K_i x N_i), as
+ * the layers of a model are visited, with `copies` rotating copies of the
+ * whole weight set. kind 0: FP32 K x N weights (matvec); 1: FP32 N x K
+ * (head-style); 2: INT8 packed weights with per-token x per-channel dequant. */
+typedef struct {
+    int kind, M, nshapes, copies;
+    const int *Ks, *Ns;
+    void **W;  /* [copies * nshapes] */
+    void *X, *Xu8, *Y, *sa, *sb;
+} gemv_ctx;
+
+static int gemv_step(void *c_, int i) {
+    gemv_ctx *c = c_;
+    int copy = i % c->copies;
+    for (int s = 0; s < c->nshapes; s++) {
+        int K = c->Ks[s], N = c->Ns[s], rc;
+        void *W = c->W[copy * c->nshapes + s];
+        if (c->kind == 0)
+            rc = pcl_sgemv(PCL_OP_N, c->M, N, K, c->X, K, W, N, NULL, 0, c->Y, N, NULL);
+        else if (c->kind == 1)
+            rc = pcl_sgemv(PCL_OP_T, c->M, N, K, c->X, K, W, K, NULL, 0, c->Y, N, NULL);
+        else
+            rc = pcl_gemv_u8s8_dq(c->Xu8, K, W, NULL, c->sa, c->sb, c->Y, N, c->M, N, K, NULL);
+        if (rc != PCL_OK) return rc;
+    }
+    return PCL_OK;
+}
+
+int pcl_bench_gemv(int kind, int M, int nshapes, const int *Ks, const int *Ns, int copies,
+                   int warmup, int steps, double *ms_total, double *bytes_per_step) {
+    int rc = PCL_OK;
+    gemv_ctx c;
+    memset(&c, 0, sizeof c);
+    c.kind = kind, c.M = M, c.nshapes = nshapes, c.Ks = Ks, c.Ns = Ns;
+    c.copies = copies < 1 ? 1 : copies;
+    int kmax = 0, nmax = 0;
+    double bytes = 0;
+    for (int s = 0; s < nshapes; s++) {
+        if (Ks[s] > kmax) kmax = Ks[s];
+        if (Ns[s] > nmax) nmax = Ns[s];
+        double wb = kind == 2 ? (double)Ns[s] * pcl_s8_kpad(Ks[s]) : 4.0 * Ks[s] * Ns[s];
+        double xb = kind == 2 ? (double)M * Ks[s] : 4.0 * M * Ks[s];
+        bytes += wb + xb + 4.0 * M * Ns[s] + (kind == 2 ? 4.0 * (Ns[s] + M) : 0.0);
+    }
+    *bytes_per_step = bytes;
+    c.W = calloc((size_t)c.copies * nshapes, sizeof(void *));
+    c.X = dev_f32((size_t)M * kmax, 31, -1.f, 1.f);
+    c.Xu8 = dev_bytes((size_t)M * kmax, 32);
+    c.Y = pcl_malloc((size_t)M * nmax * 4);
+    c.sa = dev_f32(M, 33, 1e-3f, 1e-2f);
+    c.sb = dev_f32(nmax, 34, 1e-3f, 1e-2f);
+    if (!c.W || !c.X || !c.Xu8 || !c.Y || !c.sa || !c.sb) {
+        rc = PCL_ERR_OOM;
+        goto done;
+    }
+    for (int cp = 0; cp < c.copies; cp++)
+        for (int s = 0; s < nshapes; s++) {
+            void **slot = &c.W[cp * nshapes + s];
+            if (kind == 2) {
+                void *Bq = dev_bytes((size_t)Ks[s] * Ns[s], 40 + s);
+                *slot = pcl_malloc(pcl_s8_packed_bytes(Ks[s], Ns[s]));
+                if (!Bq || !*slot) {
+                    pcl_free(Bq);
+                    rc = PCL_ERR_OOM;
+                    goto done;
+                }
+                rc = pcl_pack_b_s8(Bq, Ns[s], Ks[s], Ns[s], *slot, NULL, NULL);
+                pcl_stream_synchronize();
+                pcl_free(Bq);
+                if (rc != PCL_OK) goto done;
+            } else {
+                *slot = dev_f32((size_t)Ks[s] * Ns[s], 40 + s, -0.02f, 0.02f);
+                if (!*slot) {
+                    rc = PCL_ERR_OOM;
+                    goto done;
+                }
+            }
+        }
+    TRY(time_steps(gemv_step, &c, warmup, steps, ms_total));
+done:
+    if (c.W)
+        for (int j = 0; j < c.copies * nshapes; j++) pcl_free(c.W[j]);
+    free(c.W);
+    pcl_free(c.X), pcl_free(c.Xu8), pcl_free(c.Y), pcl_free(c.sa), pcl_free(c.sb);
+    return rc;
+}

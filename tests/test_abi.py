@@ -78,8 +78,8 @@ def test_argument_errors_before_device_work():
     assert L.pcl_set_model_dims(0, 1) == pcl.PCL_ERR_INVALID_ARG
     # empty problems are valid no-ops
     assert L.pcl_sgemm(0, 0, 0, 4, 4, None, 4, None, 4, None, 0, None, 4, None) == pcl.PCL_OK
-    assert L.pcl_s8_kpad(1) == 64 and L.pcl_s8_kpad(64) == 64 and L.pcl_s8_kpad(65) == 128
-    assert L.pcl_s8_packed_bytes(100, 3) == 3 * 128
+    assert L.pcl_s8_kpad(1) == 256 and L.pcl_s8_kpad(256) == 256 and L.pcl_s8_kpad(257) == 512
+    assert L.pcl_s8_packed_bytes(100, 3) == 3 * 256
 
 
 def test_no_device_fails_loudly():
@@ -102,9 +102,12 @@ def test_c_drivers_compile_and_link(tmp_path):
     srcs = [f for f in os.listdir(drivers) if f.endswith(".c")]
     assert srcs
     for src in srcs:
-        out = tmp_path / src.replace(".c", "")
-        cmd = ["gcc", "-O2", "-std=c11", "-Wall", "-Werror", "-I" + os.path.join(ROOT, "include"),
-               os.path.join(drivers, src), "-o", str(out), "-L" + os.path.join(ROOT, "pure-c-llm_amd"),
-               "-lpcl_hip", "-lm", "-fopenmp"]
+        path = os.path.join(drivers, src)
+        program = "int main(" in open(path).read()
+        out = tmp_path / src.replace(".c", "" if program else ".so")
+        cmd = ["gcc", "-O2", "-std=c11", "-Wall", "-Werror", "-I" + os.path.join(ROOT, "include"), path,
+               "-o", str(out), "-L" + os.path.join(ROOT, "pure-c-llm_amd"), "-lpcl_hip", "-lm", "-fopenmp"]
+        if not program:
+            cmd[1:1] = ["-shared", "-fPIC"]
         r = subprocess.run(cmd, capture_output=True, text=True)
         assert r.returncode == 0, r.stderr
