@@ -18,9 +18,10 @@
 // Data movement. Tiles of BM (BN) rows x 128 bytes of K go from HBM straight
 // into LDS with global_load_lds_dwordx4: each wave instruction moves 64 x 16
 // bytes into 1 KB of consecutive LDS, no VGPRs involved, so STAGES tiles can
-// be in flight at once. A K tile is consumed from LDS by 16-byte fragment
-// reads (ds_read_b128) feeding the MFMA; the A fragment is re-centred by XOR
-// in registers.
+// be in flight at once. Per-lane source offsets are computed once; per tile
+// only a scalar base moves. A K tile is consumed from LDS by 16-byte fragment
+// reads (ds_read_b128) feeding the MFMA; A fragments are re-centred by XOR in
+// registers one step ahead of their use.
 //
 // LDS layout: row r of a tile is 128 bytes = 8 chunks of 16 bytes; logical
 // chunk c lives at physical chunk c ^ ((r >> 1) & 7). The LDS serves a
@@ -31,16 +32,26 @@
 // instruction fills 8 whole rows, lanes choosing their global chunk so the
 // physical layout comes out swizzled.
 //
-// Tails are handled without branches or masks: rows past M (N) are clamped to
-// the last row and only feed outputs that are never stored; an A chunk past K
-// is clamped to the last in-bounds chunk, whose bytes meet the zero padding of
-// the packed weights (every B chunk read lies below nk*128 <= Kp).
+// Schedule. A tile is 4 steps of one 32-byte k-chunk; a step is TM x TN
+// MFMAs. The fragments of step s+2 are read while step s multiplies (a ring
+// of 4 register slots), and the work of a step -- its LDS reads, the DMA
+// issue, the wait and XOR for step s+1 -- is spread over the gaps between its
+// MFMAs, so the wave keeps issuing while each MFMA runs (a wave issues in
+// order: work bunched between two MFMAs would idle the matrix core).
 //
-// Synchronisation: one s_barrier per K tile. Before it, each wave waits with
-// s_waitcnt vmcnt for its own DMA loads of the tile about to be read (leaving
-// the STAGES-2 younger tiles in flight); after it, the stage freed by the
-// previous tile is refilled. No fence is used: a release fence would wait for
-// every outstanding load and drain the pipeline.
+// Synchronisation: one s_barrier per K tile, in step 2. Before it, each wave
+// waits (lgkmcnt) for its own fragment reads of the tile, which by then are
+// all issued, and (vmcnt) for its own DMA of the next tile, leaving STAGES-2
+// younger tiles in flight; after it, the current tile's stage is refilled and
+// the next tile's first fragments are read while the current tile's last
+// MFMAs run. No fence is used: a release fence would wait for every
+// outstanding load and drain the pipeline.
+//
+// Tails are handled without per-element branches: rows past M (N) are clamped
+// to the last row and only feed outputs that are never stored; in the last
+// K tile, an A chunk past K is clamped to the last in-bounds chunk, whose
+// bytes meet the zero padding of the packed weights (every B chunk read lies
+// below nk*128 <= Kp).
 //
 // K order: the 32x32x32 MFMA takes 16 bytes per lane; lane group g = lane/32
 // supplies logical chunk 2kc+g of the tile for A and for B alike, so the
@@ -52,59 +63,93 @@ namespace pcl {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) int32_t gint32_t;
+typedef __attribute__((address_space(1))) float gfloat_t;
 
 constexpr int IG_BK = 128;  // bytes of K per tile
+constexpr int IG_KC = 4;    // 32-byte MFMA k-chunks (steps) per tile
 
 // s_waitcnt immediate for "vmcnt <= n", leaving expcnt and lgkmcnt unchecked.
 constexpr int waitcnt_vm(int n) { return (n & 15) | (((n >> 4) & 3) << 14) | (7 << 4) | (15 << 8); }
-constexpr int WAITCNT_LGKM0 = (15) | (3 << 14) | (7 << 4);  // lgkmcnt(0) only
 
-__device__ __forceinline__ int swz_off(int r, int c) { return r * IG_BK + ((c ^ ((r >> 1) & 7)) << 4); }
-
-// DMA of one operand tile (ROWS x 128 bytes) by NW waves: instruction j of
-// wave w fills LDS rows 8*(j*NW + w) .. +7.
-template <int ROWS, int NW>
-struct DmaTile {
-    static constexpr int SIZE = ROWS * IG_BK;
-    static constexpr int INSTS = ROWS / (8 * NW);  // per wave
-    static_assert(ROWS % (8 * NW) == 0, "tile rows must split over the waves");
-
-    __device__ __forceinline__ static void issue(int8_t *lds, const int8_t *__restrict__ P, long ld,
-                                                 int rows0, int nrows, int k0, int kmax, int wave,
-                                                 int lane) {
-#pragma unroll
-        for (int j = 0; j < INSTS; j++) {
-            const int rb = (j * NW + wave) * 8;   // first row of this instruction
-            const int r = rb + (lane >> 3);
-            const int c = (lane & 7) ^ ((r >> 1) & 7);
-            const int grow = min(rows0 + r, nrows - 1);
-            const int gk = min(k0 + c * 16, kmax);
-            __builtin_amdgcn_global_load_lds((const void *)(P + (long)grow * ld + gk),
-                                             (lds_void_t *)(lds + rb * IG_BK), 16, 0, 0);
-        }
+// Compile-time loop: f(IC<I>{}) for I = LO .. HI-1.
+template <int V>
+struct IC {
+    static constexpr int value = V;
+};
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+    if constexpr (I < N) {
+        f(IC<I>{});
+        static_for<I + 1, N>(f);
     }
+}
+
+// Fragment reads from LDS are issued by inline assembly and waited for
+// explicitly. The compiler's own wait insertion turns every LDS wait into
+// lgkmcnt(0) once LDS DMA instructions are in flight, which would serialise
+// each read with the MFMAs it is meant to overlap. Contract: a register
+// written by lds_read16 is not touched until lds_wait<n>() has retired the
+// read and reg_fence() has been applied to it (the fence orders every later
+// use after the wait).
+template <int OFF>
+__device__ __forceinline__ void lds_read16(v4i &r, unsigned addr) {
+    static_assert(OFF >= 0 && OFF < 65536, "ds_read offset field");
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
+}
+template <int N>
+__device__ __forceinline__ void lds_wait() {
+    asm volatile("s_waitcnt lgkmcnt(%0)" ::"i"(N < 15 ? N : 15));
+}
+__device__ __forceinline__ void reg_fence(v4i &r) { asm volatile("" : "+v"(r)); }
+
+__device__ __forceinline__ unsigned lds_addr(const void *p) {
+    return (unsigned)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+
+// Work items of one step, spread over the gaps after its MFMAs (see the
+// schedule note above). Step kinds: 0/1 plain, 2 hand-over, 3 after it.
+template <int NR, int D1, int D2>
+struct StepPlan {
+    // items other than the final wait+XOR
+    static constexpr int body(int kc) { return kc < 2 ? NR : (kc == 2 ? 1 + D1 + NR : NR + D2); }
+    static constexpr bool has_x(int kc) { return kc != 2; }  // step 2 XORs inside its hand-over
 };
 
-template <int BM, int BN, int WM, int WN, int STAGES, int OUT>
-__global__ __launch_bounds__(64 * WM * WN) void igemm_mfma_kernel(
-    const uint8_t *__restrict__ A, long lda, const int8_t *__restrict__ B, long ldb,
-    const int32_t *__restrict__ col_off, const float *__restrict__ sa,
-    const float *__restrict__ sb, void *__restrict__ Cv, long ldc, int M, int N, int K) {
+// BM x BN output tile per workgroup of WM x WN waves; STAGES-deep LDS ring of
+// 128-byte K tiles; OCC workgroups are meant to share a CU (the LDS ring is
+// sized for it and the register budget is capped accordingly).
+// Requires M*lda and N*ldb below 2^32 (32-bit per-lane DMA offsets).
+template <int BM, int BN, int WM, int WN, int STAGES, int OCC, int OUT>
+__global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(
+    (OCC * WM * WN + 3) / 4))) void igemm_mfma_kernel(const uint8_t *__restrict__ A, long lda,
+                                                     const int8_t *__restrict__ B, long ldb,
+                                                     const int32_t *__restrict__ col_off,
+                                                     const float *__restrict__ sa,
+                                                     const float *__restrict__ sb,
+                                                     void *__restrict__ Cv, long ldc, int M, int N,
+                                                     int K) {
     constexpr int NW = WM * WN;
-    using TA = DmaTile<BM, NW>;
-    using TB = DmaTile<BN, NW>;
     constexpr int WTM = BM / WM, WTN = BN / WN;
     constexpr int TM = WTM / 32, TN = WTN / 32;
-    constexpr int KC = IG_BK / 32;                      // MFMA k-chunks per tile
-    constexpr int STAGE = TA::SIZE + TB::SIZE;
-    constexpr int LOADS = TA::INSTS + TB::INSTS;        // DMA instructions per tile per wave
+    constexpr int NM = TM * TN;                       // MFMAs per step
+    constexpr int NR = TM + TN;                       // fragment reads per step
+    constexpr int SIZE_A = BM * IG_BK, SIZE_B = BN * IG_BK;
+    constexpr int STAGE = SIZE_A + SIZE_B;
+    constexpr int INST_A = BM / (8 * NW), INST_B = BN / (8 * NW);  // DMA per wave per tile
+    constexpr int LOADS = INST_A + INST_B;
+    constexpr int D1 = (LOADS + 1) / 2, D2 = LOADS - D1;
+    using Plan = StepPlan<NR, D1, D2>;
     static_assert(TM >= 1 && TN >= 1 && STAGES >= 2, "bad tile configuration");
-    static_assert((STAGES - 2) * LOADS <= 63, "vmcnt range");
+    static_assert(BM % (8 * NW) == 0 && BN % (8 * NW) == 0, "tile rows must split over the waves");
+    static_assert((STAGES - 1) * LOADS <= 63, "vmcnt range");
+    static_assert(STAGES * STAGE * OCC <= 160 * 1024, "LDS budget of a CU");
 
     __shared__ __attribute__((aligned(1024))) int8_t lds[STAGES * STAGE];
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / WN, wn = wave % WN;
     const int r32 = lane & 31, g = lane >> 5;
 
@@ -112,16 +157,63 @@ __global__ __launch_bounds__(64 * WM * WN) void igemm_mfma_kernel(
     int bm, bn;
     tile_coords(xcd_remap(blockIdx.x, nbm * nbn), nbm, nbn, 8, bm, bn);
     const int m0 = bm * BM, n0 = bn * BN;
+    const int wrow0 = m0 + wm * WTM, wcol0 = n0 + wn * WTN;
 
+    // Epilogue operands are loaded before the first K tile (clamped indexes,
+    // no branches), so their latency hides behind the main loop. Lane l keeps
+    // the values of column wcol0 + 32j + l%32 and of row wrow0 + 32i + l%32.
+    float sbv[TN], sav[TM];
+    unsigned offv[TN];
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+        const int colc = min(wcol0 + j * 32 + r32, N - 1);
+        sbv[j] = (OUT != 0) ? sb[colc] : 0.f;
+        offv[j] = (OUT != 0 && col_off) ? (unsigned)col_off[colc] : 0u;
+    }
+#pragma unroll
+    for (int i = 0; i < TM; i++) sav[i] = (OUT == 2) ? sa[min(wrow0 + i * 32 + r32, M - 1)] : 0.f;
+
+    // Materialise the epilogue's scalar arguments now: a scalar load still
+    // in flight when the K loop starts would make every LDS wait in the loop
+    // a full lgkmcnt(0) (scalar loads complete out of order).
+    void *C_out = Cv;
+    long ld_out = ldc;
+    asm volatile("" : "+s"(C_out), "+s"(ld_out));
+
+    // DMA instruction d (A for d < INST_A, else B) of this wave fills tile
+    // rows rb .. rb+7, rb = 8*(j*NW + wave); lane l loads row rb + l/8 at the
+    // logical chunk whose swizzled slot is l%8. voff is the lane's byte offset
+    // in its operand at k = 0; ldso the instruction's uniform LDS offset.
     const int8_t *A8 = reinterpret_cast<const int8_t *>(A);
+    unsigned voff[LOADS];
+    int ldso[LOADS];
+#pragma unroll
+    for (int d = 0; d < LOADS; d++) {
+        const bool isA = d < INST_A;
+        const int rb = ((isA ? d : d - INST_A) * NW + wave) * 8;
+        const int r = rb + (lane >> 3);
+        const int c = (lane & 7) ^ ((r >> 1) & 7);
+        const int grow = min((isA ? m0 : n0) + r, (isA ? M : N) - 1);
+        voff[d] = (unsigned)grow * (unsigned)(isA ? lda : ldb) + (unsigned)(c * 16);
+        ldso[d] = (isA ? 0 : SIZE_A) + rb * IG_BK;
+    }
     const int nk = (K + IG_BK - 1) / IG_BK;
-    const int ka_max = K - 16;           // K % 16 == 0 and K > 0 whenever nk > 0
-    const int kb_max = nk * IG_BK - 16;  // inside the zero-padded weight row
+    const unsigned lds0 = lds_addr(lds);
 
-    auto issue = [&](int t) {
-        int8_t *st = lds + (t % STAGES) * STAGE;
-        TA::issue(st, A8, lda, m0, M, t * IG_BK, ka_max, wave, lane);
-        TB::issue(st + TA::SIZE, B, ldb, n0, N, t * IG_BK, kb_max, wave, lane);
+    // One DMA instruction of tile t; in a last partial K tile an A chunk past
+    // K is clamped to the chunk at K-16 (B rows are padded to Kp >= nk*128).
+    auto dma = [&](int t, int d) {
+        const bool isA = d < INST_A;
+        const int8_t *base = (isA ? A8 : B) + (long)t * IG_BK;
+        unsigned off = voff[d];
+        if (isA && (t + 1) * IG_BK > K) {
+            const int r = ((d * NW + wave) * 8) + (lane >> 3);
+            const int c16 = ((lane & 7) ^ ((r >> 1) & 7)) * 16;
+            off = off - c16 + min(c16, K - 16 - t * IG_BK);
+        }
+        __builtin_amdgcn_global_load_lds((const void *)(base + off),
+                                         (lds_void_t *)(lds + (t % STAGES) * STAGE + ldso[d]), 16, 0,
+                                         0);
     };
 
     v16i acc[TM][TN];
@@ -132,87 +224,134 @@ __global__ __launch_bounds__(64 * WM * WN) void igemm_mfma_kernel(
 #pragma unroll
             for (int v = 0; v < 16; v++) acc[i][j][v] = 0;
 
-    // tile row read by this lane for each A / B fragment
-    int rowa[TM], rowb[TN];
+    // Fragment ring: slot c holds k-chunk c of the current or the next tile.
+    // Lane l reads row l%32 of each 32-row block at logical chunk 2c + l/32;
+    // the row swizzle depends on l%32 only.
+    v4i fa[IG_KC][TM], fb[IG_KC][TN];
+    const int swz = (r32 >> 1) & 7;
+    unsigned offa[IG_KC], offb[IG_KC];
 #pragma unroll
-    for (int i = 0; i < TM; i++) rowa[i] = wm * WTM + i * 32 + r32;
-#pragma unroll
-    for (int j = 0; j < TN; j++) rowb[j] = wn * WTN + j * 32 + r32;
+    for (int c = 0; c < IG_KC; c++) {
+        const int chunk = ((2 * c + g) ^ swz) << 4;
+        offa[c] = (wm * WTM + r32) * IG_BK + chunk;
+        offb[c] = SIZE_A + (wn * WTN + r32) * IG_BK + chunk;
+    }
+    // read item r (A fragments first) of slot C from the stage at `base`
+    auto read_item = [&](unsigned base, auto C, auto R) {
+        constexpr int c = decltype(C)::value, r = decltype(R)::value;
+        if constexpr (r < TM) lds_read16<r * 32 * IG_BK>(fa[c][r], base + offa[c]);
+        else lds_read16<(r - TM) * 32 * IG_BK>(fb[c][r - TM], base + offb[c]);
+    };
+    // slot C has landed (after the caller's wait): fence it and re-centre A
+    auto xor_slot = [&](auto C) {
+        constexpr int c = decltype(C)::value;
+        static_for<0, TM>([&](auto I) { reg_fence(fa[c][I.value]); });
+        static_for<0, TN>([&](auto J) { reg_fence(fb[c][J.value]); });
+        static_for<0, TM>([&](auto I) { fa[c][I.value] ^= (int)0x80808080u; });
+    };
 
+    // Prologue: every stage is filled; tile 0 is waited for; slots 0 and 1
+    // are read and slot 0 is re-centred.
 #pragma unroll
-    for (int t = 0; t < STAGES - 1; t++)
-        if (t < nk) issue(t);
+    for (int t = 0; t < STAGES; t++)
+        if (t < nk) static_for<0, LOADS>([&](auto D) { dma(t, D.value); });
+    if (nk >= STAGES) __builtin_amdgcn_s_waitcnt(waitcnt_vm((STAGES - 1) * LOADS));
+    else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    __builtin_amdgcn_s_barrier();
+    static_for<0, NR>([&](auto R) { read_item(lds0, IC<0>{}, R); });
+    static_for<0, NR>([&](auto R) { read_item(lds0, IC<1>{}, R); });
+    lds_wait<NR>();
+    xor_slot(IC<0>{});
 
     for (int kt = 0; kt < nk; kt++) {
-        if (kt + STAGES - 2 < nk) __builtin_amdgcn_s_waitcnt(waitcnt_vm((STAGES - 2) * LOADS));
-        else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
-        __builtin_amdgcn_s_barrier();
-        if (kt + STAGES - 1 < nk) issue(kt + STAGES - 1);
-
-        const int8_t *la = lds + (kt % STAGES) * STAGE;
-        const int8_t *lb = la + TA::SIZE;
-        // Fragments are double-buffered by k-chunk, and the re-centred A
-        // fragments get registers of their own: no register that an issued
-        // MFMA still reads is rewritten by the next chunk's reads or XORs.
-        v4i fa[2][TM], fb[2][TN], ax[2][TM];
-#pragma unroll
-        for (int i = 0; i < TM; i++) fa[0][i] = *reinterpret_cast<const v4i *>(la + swz_off(rowa[i], g));
-#pragma unroll
-        for (int j = 0; j < TN; j++) fb[0][j] = *reinterpret_cast<const v4i *>(lb + swz_off(rowb[j], g));
-#pragma unroll
-        for (int kc = 0; kc < KC; kc++) {
-            const int cu = kc & 1;
-#pragma unroll
-            for (int i = 0; i < TM; i++) ax[cu][i] = fa[cu][i] ^ (int)0x80808080u;
-            if (kc + 1 < KC) {
-#pragma unroll
-                for (int i = 0; i < TM; i++)
-                    fa[cu ^ 1][i] = *reinterpret_cast<const v4i *>(la + swz_off(rowa[i], 2 * kc + 2 + g));
-#pragma unroll
-                for (int j = 0; j < TN; j++)
-                    fb[cu ^ 1][j] = *reinterpret_cast<const v4i *>(lb + swz_off(rowb[j], 2 * kc + 2 + g));
-            }
-            // keep the next chunk's reads ahead of this chunk's MFMAs (the
-            // scheduler would otherwise sink them and serialise read -> MFMA)
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int j = 0; j < TN; j++)
-#pragma unroll
-                for (int i = 0; i < TM; i++)
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ax[cu][i], fb[cu][j], acc[i][j], 0, 0, 0);
-        }
-        // every fragment read of this stage completes before the next
-        // barrier, after which the stage may be refilled
-        __builtin_amdgcn_s_waitcnt(WAITCNT_LGKM0);
+        const unsigned cur = lds0 + (kt % STAGES) * STAGE;
+        const unsigned nxt = lds0 + ((kt + 1) % STAGES) * STAGE;
+        const bool refill = kt + STAGES < nk;
+        static_for<0, IG_KC>([&](auto KC) {
+            constexpr int kc = KC.value;
+            constexpr int pc = (kc + 2) % IG_KC;  // slot being prefetched
+            const unsigned pbase = (kc + 2 < IG_KC) ? cur : nxt;
+            constexpr int NB = Plan::body(kc);
+            constexpr int G = NM > 1 ? NM - 1 : 1;  // gaps that take body items
+            // body item b of this step
+            auto item = [&](auto Bi) {
+                constexpr int b = decltype(Bi)::value;
+                if constexpr (kc < 2) {
+                    read_item(pbase, IC<pc>{}, IC<b>{});
+                } else if constexpr (kc == 2) {
+                    if constexpr (b == 0) {
+                        // Hand-over to tile kt+1: this wave's reads of tile
+                        // kt are complete and its DMA of tile kt+1 has
+                        // landed; after the barrier the same holds for every
+                        // wave, so tile kt's stage may be refilled.
+                        lds_wait<0>();
+                        xor_slot(IC<3>{});
+                        if (kt + STAGES - 1 < nk)
+                            __builtin_amdgcn_s_waitcnt(waitcnt_vm((STAGES - 2) * LOADS));
+                        else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+                        __builtin_amdgcn_s_barrier();
+                    } else if constexpr (b <= D1) {
+                        if (refill) dma(kt + STAGES, b - 1);
+                    } else {
+                        read_item(pbase, IC<pc>{}, IC<b - 1 - D1>{});
+                    }
+                } else {
+                    if constexpr (b < NR) read_item(pbase, IC<pc>{}, IC<b>{});
+                    else if (refill) dma(kt + STAGES, D1 + b - NR);
+                }
+            };
+            static_for<0, NM>([&](auto Q) {
+                constexpr int q = Q.value, i = q % TM, j = q / TM;
+                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[kc][i], fb[kc][j], acc[i][j], 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+                if constexpr (q < G) {
+                    static_for<q * NB / G, (q + 1) * NB / G>(item);
+                }
+                if constexpr (q == G - 1 && Plan::has_x(kc)) {
+                    // slot kc+1 is older than this step's NR reads
+                    lds_wait<NR>();
+                    xor_slot(IC<(kc + 1) % IG_KC>{});
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            });
+        });
     }
+    lds_wait<0>();  // the last prefetch reads retire before their registers are reused
 
-    // Epilogue: register v of lane l holds row (v/4)*8 + (l/32)*4 + v%4,
-    // column l%32 of each 32x32 block.
+    // Epilogue: register v of lane l holds row rl = (v/4)*8 + (l/32)*4 + v%4,
+    // column l%32 of each 32x32 block. The row scale of rl is fetched from
+    // lane rl by a cross-lane permute (no memory access); stores carry no
+    // waits, so they stream out back to back.
 #pragma unroll
-    for (int j = 0; j < TN; j++) {
-        const int col = n0 + wn * WTN + j * 32 + r32;
-        if (col >= N) continue;
-        const unsigned off = col_off ? (unsigned)col_off[col] : 0u;
-        const float sbv = (OUT != 0) ? sb[col] : 0.f;
+    for (int i = 0; i < TM; i++) {
+        float rs[16];
 #pragma unroll
-        for (int i = 0; i < TM; i++) {
+        for (int v = 0; v < 16; v++) rs[v] = (OUT == 2) ? __shfl(sav[i], (v >> 2) * 8 + g * 4 + (v & 3)) : 0.f;
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const int col = wcol0 + j * 32 + r32;
 #pragma unroll
             for (int v = 0; v < 16; v++) {
-                const int row = m0 + wm * WTM + i * 32 + (v >> 2) * 8 + g * 4 + (v & 3);
-                if (row >= M) continue;
-                if (OUT == 0) {
-                    reinterpret_cast<int32_t *>(Cv)[(long)row * ldc + col] = acc[i][j][v];
-                } else {
-                    const int32_t vv = (int32_t)((unsigned)acc[i][j][v] + off);
-                    const float dq = (OUT == 2) ? sa[row] * sbv : sbv;
-                    reinterpret_cast<float *>(Cv)[(long)row * ldc + col] = (float)vv * dq;
+                const int row = wrow0 + i * 32 + (v >> 2) * 8 + g * 4 + (v & 3);
+                if (row < M && col < N) {
+                    const long o = (long)row * ld_out + col;
+                    // streaming (non-temporal) stores: C is not re-read here,
+                    // and write-back through L2 would leave the whole output
+                    // dirty in L2 for the end-of-kernel release to flush
+                    if (OUT == 0) {
+                        __builtin_nontemporal_store(acc[i][j][v], (gint32_t *)C_out + o);
+                    } else {
+                        const int32_t vv = (int32_t)((unsigned)acc[i][j][v] + offv[j]);
+                        const float dq = (OUT == 2) ? rs[v] * sbv[j] : sbv[j];
+                        __builtin_nontemporal_store((float)vv * dq, (gfloat_t *)C_out + o);
+                    }
                 }
             }
         }
     }
 }
 
-template <int BM, int BN, int WM, int WN, int STAGES>
+template <int BM, int BN, int WM, int WN, int STAGES, int OCC>
 static hipError_t launch_icfg(int out_mode, int M, int N, int K, const uint8_t *A, long lda,
                               const int8_t *B, long ldb, const int32_t *col_off, const float *sa,
                               const float *sb, void *C, long ldc, hipStream_t stream) {
@@ -221,30 +360,64 @@ static hipError_t launch_icfg(int out_mode, int M, int N, int K, const uint8_t *
     dim3 grid(nblk), block(64 * WM * WN);
     switch (out_mode) {
         case 0:
-            hipLaunchKernelGGL((igemm_mfma_kernel<BM, BN, WM, WN, STAGES, 0>), grid, block, 0,
+            hipLaunchKernelGGL((igemm_mfma_kernel<BM, BN, WM, WN, STAGES, OCC, 0>), grid, block, 0,
                                stream, A, lda, B, ldb, col_off, sa, sb, C, ldc, M, N, K);
             break;
         case 1:
-            hipLaunchKernelGGL((igemm_mfma_kernel<BM, BN, WM, WN, STAGES, 1>), grid, block, 0,
+            hipLaunchKernelGGL((igemm_mfma_kernel<BM, BN, WM, WN, STAGES, OCC, 1>), grid, block, 0,
                                stream, A, lda, B, ldb, col_off, sa, sb, C, ldc, M, N, K);
             break;
         default:
-            hipLaunchKernelGGL((igemm_mfma_kernel<BM, BN, WM, WN, STAGES, 2>), grid, block, 0,
+            hipLaunchKernelGGL((igemm_mfma_kernel<BM, BN, WM, WN, STAGES, OCC, 2>), grid, block, 0,
                                stream, A, lda, B, ldb, col_off, sa, sb, C, ldc, M, N, K);
             break;
     }
     return hipGetLastError();
 }
 
+// The kernel addresses each operand with 32-bit per-lane offsets: split the
+// problem into row bands of A and column bands of B whose byte spans stay
+// below 2^31.
+template <int BM, int BN, int WM, int WN, int STAGES, int OCC>
+static hipError_t launch_split(int out_mode, int M, int N, int K, const uint8_t *A, long lda,
+                               const int8_t *B, long ldb, const int32_t *col_off, const float *sa,
+                               const float *sb, void *C, long ldc, hipStream_t stream) {
+    const long LIM = 1L << 31;
+    long mband = lda > 0 ? LIM / lda : M, nband = ldb > 0 ? LIM / ldb : N;
+    mband = mband >= M ? M : (mband / BM) * BM;
+    nband = nband >= N ? N : (nband / BN) * BN;
+    if (mband <= 0 || nband <= 0) return hipErrorInvalidValue;
+    const size_t esz = 4;  // int32 or float output
+    for (long m = 0; m < M; m += mband) {
+        for (long n = 0; n < N; n += nband) {
+            const int mm = (int)(M - m < mband ? M - m : mband);
+            const int nn = (int)(N - n < nband ? N - n : nband);
+            hipError_t e = launch_icfg<BM, BN, WM, WN, STAGES, OCC>(
+                out_mode, mm, nn, K, A + m * lda, lda, B + n * ldb, ldb, col_off ? col_off + n : nullptr,
+                sa ? sa + m : nullptr, sb ? sb + n : nullptr,
+                (char *)C + (m * ldc + n) * esz, ldc, stream);
+            if (e != hipSuccess) return e;
+        }
+    }
+    return hipSuccess;
+}
+
 hipError_t launch_igemm(int out_mode, int M, int N, int K, const uint8_t *A, long lda,
                         const int8_t *Bpk, long ldb, const int32_t *col_off, const float *sa,
                         const float *sb, void *C, long ldc, hipStream_t stream) {
-    long big = (long)((M + 127) / 128) * ((N + 127) / 128);
-    if (big >= 256)
-        return launch_icfg<128, 128, 2, 2, 4>(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa, sb,
-                                              C, ldc, stream);
-    return launch_icfg<64, 64, 2, 2, 4>(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa, sb, C,
-                                        ldc, stream);
+    // Tile choice (measured on the 350M-class and gemm_bench shapes): 256x256
+    // tiles with 8 waves when they still cover most of the 256 CUs; 128x128
+    // tiles, two workgroups per CU, when those fill the chip; 64x64 otherwise.
+    const long t256 = (long)((M + 255) / 256) * ((N + 255) / 256);
+    const long t128 = (long)((M + 127) / 128) * ((N + 127) / 128);
+    if (t256 >= 192)
+        return launch_split<256, 256, 4, 2, 2, 1>(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa,
+                                                  sb, C, ldc, stream);
+    if (t128 >= 256)
+        return launch_split<128, 128, 2, 2, 2, 2>(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa,
+                                                  sb, C, ldc, stream);
+    return launch_split<64, 64, 2, 2, 4, 1>(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa, sb, C,
+                                            ldc, stream);
 }
 
 // Copy A into a K16-wide buffer padded with 0x80 (zero after re-centring; the
