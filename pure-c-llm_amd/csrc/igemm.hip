@@ -116,20 +116,23 @@ struct StepPlan {
     static constexpr bool has_x(int kc) { return kc != 2; }  // step 2 XORs inside its hand-over
 };
 
-// BM x BN output tile per workgroup of WM x WN waves; STAGES-deep LDS ring of
-// 128-byte K tiles; OCC workgroups are meant to share a CU (the LDS ring is
-// sized for it and the register budget is capped accordingly).
+// BM x BN output tile per workgroup of WM x WN x KG waves; STAGES-deep LDS
+// ring of 128-byte K tiles; OCC workgroups are meant to share a CU (the LDS
+// ring is sized for it and the register budget is capped accordingly).
+// KG = 2 splits every K tile between two groups of WM x WN waves (k-chunks
+// 0-1 and 2-3), which doubles the waves issuing LDS reads and DMA for one
+// output tile; the two partial sums are added through LDS at the end.
 // Requires M*lda and N*ldb below 2^32 (32-bit per-lane DMA offsets).
-template <int BM, int BN, int WM, int WN, int STAGES, int OCC, int OUT>
-__global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(
-    (OCC * WM * WN + 3) / 4))) void igemm_mfma_kernel(const uint8_t *__restrict__ A, long lda,
+template <int BM, int BN, int WM, int WN, int KG, int STAGES, int OCC, int OUT>
+__global__ __launch_bounds__(64 * WM * WN * KG) __attribute__((amdgpu_waves_per_eu(
+    (OCC * WM * WN * KG + 3) / 4))) void igemm_mfma_kernel(const uint8_t *__restrict__ A, long lda,
                                                      const int8_t *__restrict__ B, long ldb,
                                                      const int32_t *__restrict__ col_off,
                                                      const float *__restrict__ sa,
                                                      const float *__restrict__ sb,
                                                      void *__restrict__ Cv, long ldc, int M, int N,
                                                      int K) {
-    constexpr int NW = WM * WN;
+    constexpr int NW = WM * WN * KG;
     constexpr int WTM = BM / WM, WTN = BN / WN;
     constexpr int TM = WTM / 32, TN = WTN / 32;
     constexpr int NM = TM * TN;                       // MFMAs per step
@@ -141,6 +144,9 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(
     constexpr int D1 = (LOADS + 1) / 2, D2 = LOADS - D1;
     using Plan = StepPlan<NR, D1, D2>;
     static_assert(TM >= 1 && TN >= 1 && STAGES >= 2, "bad tile configuration");
+    static_assert(KG == 1 || (KG == 2 && TM % 2 == 0), "K groups: 1, or 2 with an even TM");
+    static_assert(KG == 1 || WM * WN * TM * TN * 64 * 64 <= STAGES * STAGE,
+                  "the partial-sum exchange must fit in the LDS ring");
     static_assert(BM % (8 * NW) == 0 && BN % (8 * NW) == 0, "tile rows must split over the waves");
     static_assert((STAGES - 1) * LOADS <= 63, "vmcnt range");
     static_assert(STAGES * STAGE * OCC <= 160 * 1024, "LDS budget of a CU");
@@ -150,7 +156,8 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave / WN, wn = wave % WN;
+    const int kg = wave / (WM * WN), wq = wave % (WM * WN);
+    const int wm = wq / WN, wn = wq % WN;
     const int r32 = lane & 31, g = lane >> 5;
 
     const int nbm = (M + BM - 1) / BM, nbn = (N + BN - 1) / BN;
@@ -232,7 +239,8 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(
     unsigned offa[IG_KC], offb[IG_KC];
 #pragma unroll
     for (int c = 0; c < IG_KC; c++) {
-        const int chunk = ((2 * c + g) ^ swz) << 4;
+        const int kchunk = (KG == 1) ? c : 2 * kg + (c & 1);  // 32-byte k-chunk of slot c
+        const int chunk = ((2 * kchunk + g) ^ swz) << 4;
         offa[c] = (wm * WTM + r32) * IG_BK + chunk;
         offb[c] = SIZE_A + (wn * WTN + r32) * IG_BK + chunk;
     }
@@ -258,65 +266,154 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(
     if (nk >= STAGES) __builtin_amdgcn_s_waitcnt(waitcnt_vm((STAGES - 1) * LOADS));
     else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
     __builtin_amdgcn_s_barrier();
-    static_for<0, NR>([&](auto R) { read_item(lds0, IC<0>{}, R); });
-    static_for<0, NR>([&](auto R) { read_item(lds0, IC<1>{}, R); });
-    lds_wait<NR>();
-    xor_slot(IC<0>{});
+    if constexpr (KG == 1) {
+        static_for<0, NR>([&](auto R) { read_item(lds0, IC<0>{}, R); });
+        static_for<0, NR>([&](auto R) { read_item(lds0, IC<1>{}, R); });
+        lds_wait<NR>();
+        xor_slot(IC<0>{});
 
-    for (int kt = 0; kt < nk; kt++) {
-        const unsigned cur = lds0 + (kt % STAGES) * STAGE;
-        const unsigned nxt = lds0 + ((kt + 1) % STAGES) * STAGE;
-        const bool refill = kt + STAGES < nk;
-        static_for<0, IG_KC>([&](auto KC) {
-            constexpr int kc = KC.value;
-            constexpr int pc = (kc + 2) % IG_KC;  // slot being prefetched
-            const unsigned pbase = (kc + 2 < IG_KC) ? cur : nxt;
-            constexpr int NB = Plan::body(kc);
-            constexpr int G = NM > 1 ? NM - 1 : 1;  // gaps that take body items
-            // body item b of this step
-            auto item = [&](auto Bi) {
-                constexpr int b = decltype(Bi)::value;
-                if constexpr (kc < 2) {
-                    read_item(pbase, IC<pc>{}, IC<b>{});
-                } else if constexpr (kc == 2) {
-                    if constexpr (b == 0) {
-                        // Hand-over to tile kt+1: this wave's reads of tile
-                        // kt are complete and its DMA of tile kt+1 has
-                        // landed; after the barrier the same holds for every
-                        // wave, so tile kt's stage may be refilled.
-                        lds_wait<0>();
-                        xor_slot(IC<3>{});
-                        if (kt + STAGES - 1 < nk)
-                            __builtin_amdgcn_s_waitcnt(waitcnt_vm((STAGES - 2) * LOADS));
-                        else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
-                        __builtin_amdgcn_s_barrier();
-                    } else if constexpr (b <= D1) {
-                        if (refill) dma(kt + STAGES, b - 1);
+        for (int kt = 0; kt < nk; kt++) {
+            const unsigned cur = lds0 + (kt % STAGES) * STAGE;
+            const unsigned nxt = lds0 + ((kt + 1) % STAGES) * STAGE;
+            const bool refill = kt + STAGES < nk;
+            static_for<0, IG_KC>([&](auto KC) {
+                constexpr int kc = KC.value;
+                constexpr int pc = (kc + 2) % IG_KC;  // slot being prefetched
+                const unsigned pbase = (kc + 2 < IG_KC) ? cur : nxt;
+                constexpr int NB = Plan::body(kc);
+                constexpr int G = NM > 1 ? NM - 1 : 1;  // gaps that take body items
+                // body item b of this step
+                auto item = [&](auto Bi) {
+                    constexpr int b = decltype(Bi)::value;
+                    if constexpr (kc < 2) {
+                        read_item(pbase, IC<pc>{}, IC<b>{});
+                    } else if constexpr (kc == 2) {
+                        if constexpr (b == 0) {
+                            // Hand-over to tile kt+1: this wave's reads of tile
+                            // kt are complete and its DMA of tile kt+1 has
+                            // landed; after the barrier the same holds for every
+                            // wave, so tile kt's stage may be refilled.
+                            lds_wait<0>();
+                            xor_slot(IC<3>{});
+                            if (kt + STAGES - 1 < nk)
+                                __builtin_amdgcn_s_waitcnt(waitcnt_vm((STAGES - 2) * LOADS));
+                            else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+                            __builtin_amdgcn_s_barrier();
+                        } else if constexpr (b <= D1) {
+                            if (refill) dma(kt + STAGES, b - 1);
+                        } else {
+                            read_item(pbase, IC<pc>{}, IC<b - 1 - D1>{});
+                        }
                     } else {
-                        read_item(pbase, IC<pc>{}, IC<b - 1 - D1>{});
+                        if constexpr (b < NR) read_item(pbase, IC<pc>{}, IC<b>{});
+                        else if (refill) dma(kt + STAGES, D1 + b - NR);
                     }
-                } else {
-                    if constexpr (b < NR) read_item(pbase, IC<pc>{}, IC<b>{});
-                    else if (refill) dma(kt + STAGES, D1 + b - NR);
-                }
-            };
+                };
+                static_for<0, NM>([&](auto Q) {
+                    constexpr int q = Q.value, i = q % TM, j = q / TM;
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[kc][i], fb[kc][j], acc[i][j], 0, 0, 0);
+                    __builtin_amdgcn_sched_barrier(0);
+                    if constexpr (q < G) {
+                        static_for<q * NB / G, (q + 1) * NB / G>(item);
+                    }
+                    if constexpr (q == G - 1 && Plan::has_x(kc)) {
+                        // slot kc+1 is older than this step's NR reads
+                        lds_wait<NR>();
+                        xor_slot(IC<(kc + 1) % IG_KC>{});
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                });
+            });
+        }
+        lds_wait<0>();  // the last prefetch reads retire before their registers are reused
+    } else {
+        // Two K groups: group kg multiplies k-chunks 2kg and 2kg+1 of every
+        // tile (slots 0 and 1). Step 0 reads slot 1 of the same tile; step 1
+        // hands over to the next tile and reads its slot 0. Waits are full
+        // lgkmcnt(0): the other group's wave on the same SIMD covers them.
+        static_for<0, NR>([&](auto R) { read_item(lds0, IC<0>{}, R); });
+        for (int kt = 0; kt < nk; kt++) {
+            const unsigned cur = lds0 + (kt % STAGES) * STAGE;
+            const unsigned nxt = lds0 + ((kt + 1) % STAGES) * STAGE;
+            const bool refill = kt + STAGES < nk;
+            constexpr int G = NM;
+            // step 0: slot 0, prefetch slot 1 of this tile
+            lds_wait<0>();
+            xor_slot(IC<0>{});
             static_for<0, NM>([&](auto Q) {
                 constexpr int q = Q.value, i = q % TM, j = q / TM;
-                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[kc][i], fb[kc][j], acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[0][i], fb[0][j], acc[i][j], 0, 0, 0);
                 __builtin_amdgcn_sched_barrier(0);
-                if constexpr (q < G) {
-                    static_for<q * NB / G, (q + 1) * NB / G>(item);
-                }
-                if constexpr (q == G - 1 && Plan::has_x(kc)) {
-                    // slot kc+1 is older than this step's NR reads
-                    lds_wait<NR>();
-                    xor_slot(IC<(kc + 1) % IG_KC>{});
-                }
+                static_for<q * NR / G, (q + 1) * NR / G>([&](auto R) { read_item(cur, IC<1>{}, R); });
                 __builtin_amdgcn_sched_barrier(0);
             });
-        });
+            // step 1: hand-over to tile kt+1 (as in the single-group schedule),
+            // then slot 1 while the DMA refill and the next tile's slot 0 go out
+            lds_wait<0>();
+            if (kt + STAGES - 1 < nk) __builtin_amdgcn_s_waitcnt(waitcnt_vm((STAGES - 2) * LOADS));
+            else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+            __builtin_amdgcn_s_barrier();
+            xor_slot(IC<1>{});
+            constexpr int NI = LOADS + NR;
+            static_for<0, NM>([&](auto Q) {
+                constexpr int q = Q.value, i = q % TM, j = q / TM;
+                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[1][i], fb[1][j], acc[i][j], 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+                static_for<q * NI / G, (q + 1) * NI / G>([&](auto Bi) {
+                    constexpr int b = decltype(Bi)::value;
+                    if constexpr (b < LOADS) {
+                        if (refill) dma(kt + STAGES, b);
+                    } else {
+                        read_item(nxt, IC<0>{}, IC<b - LOADS>{});
+                    }
+                });
+                __builtin_amdgcn_sched_barrier(0);
+            });
+        }
+        lds_wait<0>();
+        // Add the groups' partial sums: group 0 keeps the upper half of the
+        // wave tile's 32-row blocks (i < TM/2), group 1 the lower half; each
+        // hands the other half to its partner through LDS (lane-major, so the
+        // partner's lanes read their own elements). The stages are free once
+        // every wave has passed the barrier.
+        __builtin_amdgcn_s_barrier();
+        constexpr int HALF = TM / 2;
+        v4i *xch = reinterpret_cast<v4i *>(lds);
+        auto slot_of = [&](int pair, int half, int ii, int j, int q4) {
+            return (((pair * 2 + half) * HALF + ii) * TN + j) * 4 + q4;  // in units of 64 x v4i
+        };
+        // (the two branches keep every accumulator index a compile-time
+        // constant: a run-time index would move the accumulators to scratch)
+        auto give = [&](auto I0) {  // store blocks I0 .. I0+HALF-1 for the partner
+            static_for<0, HALF>([&](auto II) {
+                static_for<0, TN>([&](auto J) {
+                    const v16i &a = acc[decltype(I0)::value + II.value][J.value];
+#pragma unroll
+                    for (int q4 = 0; q4 < 4; q4++)
+                        xch[slot_of(wq, kg, II.value, J.value, q4) * 64 + lane] =
+                            v4i{a[q4 * 4], a[q4 * 4 + 1], a[q4 * 4 + 2], a[q4 * 4 + 3]};
+                });
+            });
+        };
+        auto take = [&](auto I0) {  // add the partner's blocks into I0 .. I0+HALF-1
+            static_for<0, HALF>([&](auto II) {
+                static_for<0, TN>([&](auto J) {
+                    v16i &a = acc[decltype(I0)::value + II.value][J.value];
+#pragma unroll
+                    for (int q4 = 0; q4 < 4; q4++) {
+                        const v4i p = xch[slot_of(wq, kg ^ 1, II.value, J.value, q4) * 64 + lane];
+#pragma unroll
+                        for (int e = 0; e < 4; e++) a[q4 * 4 + e] += p[e];
+                    }
+                });
+            });
+        };
+        if (kg == 0) give(IC<HALF>{});
+        else give(IC<0>{});
+        __syncthreads();
+        if (kg == 0) take(IC<0>{});
+        else take(IC<HALF>{});
     }
-    lds_wait<0>();  // the last prefetch reads retire before their registers are reused
 
     // Epilogue: register v of lane l holds row rl = (v/4)*8 + (l/32)*4 + v%4,
     // column l%32 of each 32x32 block. The row scale of rl is fetched from
@@ -324,6 +421,7 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(
     // waits, so they stream out back to back.
 #pragma unroll
     for (int i = 0; i < TM; i++) {
+        if (KG == 2 && (i < TM / 2) != (kg == 0)) continue;  // the partner stores this half
         float rs[16];
 #pragma unroll
         for (int v = 0; v < 16; v++) rs[v] = (OUT == 2) ? __shfl(sav[i], (v >> 2) * 8 + g * 4 + (v & 3)) : 0.f;
@@ -351,24 +449,24 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(
     }
 }
 
-template <int BM, int BN, int WM, int WN, int STAGES, int OCC>
+template <int BM, int BN, int WM, int WN, int KG, int STAGES, int OCC>
 static hipError_t launch_icfg(int out_mode, int M, int N, int K, const uint8_t *A, long lda,
                               const int8_t *B, long ldb, const int32_t *col_off, const float *sa,
                               const float *sb, void *C, long ldc, hipStream_t stream) {
     const int nblk = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
     if (nblk == 0) return hipSuccess;
-    dim3 grid(nblk), block(64 * WM * WN);
+    dim3 grid(nblk), block(64 * WM * WN * KG);
     switch (out_mode) {
         case 0:
-            hipLaunchKernelGGL((igemm_mfma_kernel<BM, BN, WM, WN, STAGES, OCC, 0>), grid, block, 0,
+            hipLaunchKernelGGL((igemm_mfma_kernel<BM, BN, WM, WN, KG, STAGES, OCC, 0>), grid, block, 0,
                                stream, A, lda, B, ldb, col_off, sa, sb, C, ldc, M, N, K);
             break;
         case 1:
-            hipLaunchKernelGGL((igemm_mfma_kernel<BM, BN, WM, WN, STAGES, OCC, 1>), grid, block, 0,
+            hipLaunchKernelGGL((igemm_mfma_kernel<BM, BN, WM, WN, KG, STAGES, OCC, 1>), grid, block, 0,
                                stream, A, lda, B, ldb, col_off, sa, sb, C, ldc, M, N, K);
             break;
         default:
-            hipLaunchKernelGGL((igemm_mfma_kernel<BM, BN, WM, WN, STAGES, OCC, 2>), grid, block, 0,
+            hipLaunchKernelGGL((igemm_mfma_kernel<BM, BN, WM, WN, KG, STAGES, OCC, 2>), grid, block, 0,
                                stream, A, lda, B, ldb, col_off, sa, sb, C, ldc, M, N, K);
             break;
     }
@@ -378,7 +476,7 @@ static hipError_t launch_icfg(int out_mode, int M, int N, int K, const uint8_t *
 // The kernel addresses each operand with 32-bit per-lane offsets: split the
 // problem into row bands of A and column bands of B whose byte spans stay
 // below 2^31.
-template <int BM, int BN, int WM, int WN, int STAGES, int OCC>
+template <int BM, int BN, int WM, int WN, int KG, int STAGES, int OCC>
 static hipError_t launch_split(int out_mode, int M, int N, int K, const uint8_t *A, long lda,
                                const int8_t *B, long ldb, const int32_t *col_off, const float *sa,
                                const float *sb, void *C, long ldc, hipStream_t stream) {
@@ -392,7 +490,7 @@ static hipError_t launch_split(int out_mode, int M, int N, int K, const uint8_t 
         for (long n = 0; n < N; n += nband) {
             const int mm = (int)(M - m < mband ? M - m : mband);
             const int nn = (int)(N - n < nband ? N - n : nband);
-            hipError_t e = launch_icfg<BM, BN, WM, WN, STAGES, OCC>(
+            hipError_t e = launch_icfg<BM, BN, WM, WN, KG, STAGES, OCC>(
                 out_mode, mm, nn, K, A + m * lda, lda, B + n * ldb, ldb, col_off ? col_off + n : nullptr,
                 sa ? sa + m : nullptr, sb ? sb + n : nullptr,
                 (char *)C + (m * ldc + n) * esz, ldc, stream);
@@ -407,16 +505,17 @@ hipError_t launch_igemm(int out_mode, int M, int N, int K, const uint8_t *A, lon
                         const float *sb, void *C, long ldc, hipStream_t stream) {
     // Tile choice (measured on the 350M-class and gemm_bench shapes): 256x256
     // tiles with 8 waves when they still cover most of the 256 CUs; 128x128
-    // tiles, two workgroups per CU, when those fill the chip; 64x64 otherwise.
+    // tiles with two K groups (8 waves) when those fill the chip; 64x64
+    // otherwise.
     const long t256 = (long)((M + 255) / 256) * ((N + 255) / 256);
     const long t128 = (long)((M + 127) / 128) * ((N + 127) / 128);
     if (t256 >= 192)
-        return launch_split<256, 256, 4, 2, 2, 1>(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa,
+        return launch_split<256, 256, 4, 2, 1, 2, 1>(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa,
                                                   sb, C, ldc, stream);
     if (t128 >= 256)
-        return launch_split<128, 128, 2, 2, 2, 2>(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa,
+        return launch_split<128, 128, 2, 2, 2, 4, 1>(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa,
                                                   sb, C, ldc, stream);
-    return launch_split<64, 64, 2, 2, 4, 1>(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa, sb, C,
+    return launch_split<64, 64, 2, 2, 1, 4, 1>(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa, sb, C,
                                             ldc, stream);
 }
 

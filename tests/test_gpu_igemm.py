@@ -145,6 +145,19 @@ def test_igemm_full_size_checksums(M, N, K):
     np.testing.assert_array_equal(C[rows], A8[rows] @ B8)
 
 
+@pytest.mark.parametrize("M,N,K", [(2100, 2070, 1040), (4100, 3100, 528), (2056, 2048, 2064)])
+def test_igemm_ragged_large_tiles(M, N, K):
+    # ragged M, N and K (K % 128 != 0) on the 128x128 (two K groups) and
+    # 256x256 tile paths; float64 products of these integers are exact
+    # (every partial sum stays far below 2**53)
+    Au = ob.u8((M, K), 80 + M)
+    Bq = ob.s8((K, N), 81 + N)
+    announce("igemm ragged large", M, N, K)
+    C = igemm_i32(Au, Bq)
+    ref = (Au.astype(np.float64) - 128) @ Bq.astype(np.float64)
+    np.testing.assert_array_equal(C, ref.astype(np.int64))
+
+
 def test_quantizers_byte_exact():
     M, K, N = 96, 250, 80
     A = ob.normal((M, K), 70)
