@@ -131,7 +131,7 @@ __global__ __launch_bounds__(64 * WM * WN * KG) __attribute__((amdgpu_waves_per_
                                                      const float *__restrict__ sa,
                                                      const float *__restrict__ sb,
                                                      void *__restrict__ Cv, long ldc, int M, int N,
-                                                     int K) {
+                                                     int K, int nt_store) {
     constexpr int NW = WM * WN * KG;
     constexpr int WTM = BM / WM, WTN = BN / WN;
     constexpr int TM = WTM / 32, TN = WTN / 32;
@@ -433,15 +433,18 @@ __global__ __launch_bounds__(64 * WM * WN * KG) __attribute__((amdgpu_waves_per_
                 const int row = wrow0 + i * 32 + (v >> 2) * 8 + g * 4 + (v & 3);
                 if (row < M && col < N) {
                     const long o = (long)row * ld_out + col;
-                    // streaming (non-temporal) stores: C is not re-read here,
-                    // and write-back through L2 would leave the whole output
-                    // dirty in L2 for the end-of-kernel release to flush
+                    // Outputs up to 256 MiB are written with streaming (non-temporal)
+                    // stores: write-back through L2 would leave the whole
+                    // output dirty in L2 for the end-of-kernel release to
+                    // flush. Large outputs stream better through L2.
                     if (OUT == 0) {
-                        __builtin_nontemporal_store(acc[i][j][v], (gint32_t *)C_out + o);
+                        if (nt_store) __builtin_nontemporal_store(acc[i][j][v], (gint32_t *)C_out + o);
+                        else reinterpret_cast<int32_t *>(C_out)[o] = acc[i][j][v];
                     } else {
                         const int32_t vv = (int32_t)((unsigned)acc[i][j][v] + offv[j]);
                         const float dq = (OUT == 2) ? rs[v] * sbv[j] : sbv[j];
-                        __builtin_nontemporal_store((float)vv * dq, (gfloat_t *)C_out + o);
+                        if (nt_store) __builtin_nontemporal_store((float)vv * dq, (gfloat_t *)C_out + o);
+                        else reinterpret_cast<float *>(C_out)[o] = (float)vv * dq;
                     }
                 }
             }
@@ -456,18 +459,19 @@ static hipError_t launch_icfg(int out_mode, int M, int N, int K, const uint8_t *
     const int nblk = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
     if (nblk == 0) return hipSuccess;
     dim3 grid(nblk), block(64 * WM * WN * KG);
+    const int nt = (long)M * N * 4 <= (256L << 20);  // outputs up to 256 MiB: streaming stores
     switch (out_mode) {
         case 0:
             hipLaunchKernelGGL((igemm_mfma_kernel<BM, BN, WM, WN, KG, STAGES, OCC, 0>), grid, block, 0,
-                               stream, A, lda, B, ldb, col_off, sa, sb, C, ldc, M, N, K);
+                               stream, A, lda, B, ldb, col_off, sa, sb, C, ldc, M, N, K, nt);
             break;
         case 1:
             hipLaunchKernelGGL((igemm_mfma_kernel<BM, BN, WM, WN, KG, STAGES, OCC, 1>), grid, block, 0,
-                               stream, A, lda, B, ldb, col_off, sa, sb, C, ldc, M, N, K);
+                               stream, A, lda, B, ldb, col_off, sa, sb, C, ldc, M, N, K, nt);
             break;
         default:
             hipLaunchKernelGGL((igemm_mfma_kernel<BM, BN, WM, WN, KG, STAGES, OCC, 2>), grid, block, 0,
-                               stream, A, lda, B, ldb, col_off, sa, sb, C, ldc, M, N, K);
+                               stream, A, lda, B, ldb, col_off, sa, sb, C, ldc, M, N, K, nt);
             break;
     }
     return hipGetLastError();
