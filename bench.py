@@ -42,7 +42,8 @@ def load_bench():
     d, i = C.c_double, C.c_int
     lib.pcl_bench_igemm.argtypes = [i, i, i, i, i, i, i, C.POINTER(d)]
     lib.pcl_bench_sgemm.argtypes = [i, i, i, i, i, i, i, i, C.POINTER(d)]
-    lib.pcl_bench_gemv.argtypes = [i, i, i, C.POINTER(i), C.POINTER(i), i, i, i, C.POINTER(d), C.POINTER(d)]
+    lib.pcl_bench_gemv.argtypes = [C.POINTER(i), i, i, C.POINTER(i), C.POINTER(i), i, i, i, i, C.POINTER(d),
+                                   C.POINTER(d)]
     for f in (lib.pcl_bench_igemm, lib.pcl_bench_sgemm, lib.pcl_bench_gemv):
         f.restype = i
     return pcl, lib
@@ -72,16 +73,21 @@ def sgemm(pcl, lib, opA, opB, M, N, K, accumulate, warmup, steps):
             "TFLOPS": round(tf, 2), "frac_peak": round(tf / PEAK_F32_TFLOPS, 4)}
 
 
-def gemv(pcl, lib, kind, M, shapes, copies, warmup, steps):
+def gemv(pcl, lib, kind, M, shapes, copies, warmup, steps, graph=False):
+    """One sweep = one call per (K, N) shape; kind 0/1/2 = FP32 W (K x N),
+    FP32 W (N x K), INT8 packed (a list gives one kind per shape). graph=True
+    captures each weight copy's sweep once and replays it (one launch)."""
+    kinds = kind if isinstance(kind, (list, tuple)) else [kind] * len(shapes)
+    Kd = (C.c_int * len(shapes))(*kinds)
     Ks = (C.c_int * len(shapes))(*[k for k, _ in shapes])
     Ns = (C.c_int * len(shapes))(*[n for _, n in shapes])
     ms, by = C.c_double(0), C.c_double(0)
-    _check(pcl, lib.pcl_bench_gemv(kind, M, len(shapes), Ks, Ns, copies, warmup, steps, C.byref(ms), C.byref(by)),
-           f"gemv kind {kind}")
+    _check(pcl, lib.pcl_bench_gemv(Kd, M, len(shapes), Ks, Ns, copies, warmup, steps, int(graph), C.byref(ms),
+                                   C.byref(by)), f"gemv kinds {sorted(set(kinds))}")
     per = ms.value / steps
     gbs = by.value / (per * 1e-3) / 1e9
     return {"M": M, "ms_per_sweep": round(per, 5), "bytes_per_sweep": int(by.value), "GBps": round(gbs, 1),
-            "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "weight_copies": copies}
+            "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "weight_copies": copies, "graph": bool(graph)}
 
 
 def read_traffic():
@@ -212,16 +218,17 @@ def main():
         layer = [(512, 1536), (512, 512), (512, 2048), (2048, 512)]
         grown_i8 = layer * 16 + [(512, 2048)]
         dec = {}
+        # One token step: 16 layers (K x N weights) + the tied head (N x K).
+        # FP32 205 MB per step, 3 rotating weight copies (> the 256 MB
+        # Infinity Cache); INT8 51 MB per step, 11 copies. Each step is run as
+        # one call per product and as a captured graph (one launch per step).
+        fp32_step = layer * 16 + [(512, 2048)]
+        fp32_kinds = [0] * (len(layer) * 16) + [1]
         for Mt in (1, 4, 8):
-            # FP32: 16 layers (K x N weights) + tied head (N x K), 3 rotating copies
-            # (3 x 205 MB > the 256 MB Infinity Cache); INT8: 11 copies of 51 MB
-            lay = gemv(pcl, lib, 0, Mt, layer * 16, 3, 2, 10)
-            head = gemv(pcl, lib, 1, Mt, [(512, 2048)], 130, 2, 130)
-            t = lay["ms_per_sweep"] + head["ms_per_sweep"]
-            b = lay["bytes_per_sweep"] + head["bytes_per_sweep"]
-            dec[f"fp32_M{Mt}"] = {"ms_per_token_step": round(t, 4), "GBps": round(b / (t * 1e-3) / 1e9, 1),
-                                  "frac_hbm": round(b / (t * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
-            dec[f"int8_M{Mt}"] = gemv(pcl, lib, 2, Mt, grown_i8, 11, 2, 10)
+            for g in (False, True):
+                tag = "_graph" if g else ""
+                dec[f"fp32_M{Mt}{tag}"] = gemv(pcl, lib, fp32_kinds, Mt, fp32_step, 3, 2, 10, graph=g)
+                dec[f"int8_M{Mt}{tag}"] = gemv(pcl, lib, 2, Mt, grown_i8, 11, 2, 10, graph=g)
         ex["grown_decode_gemv"] = dec
         ex["head_350m_gemv_fp32"] = {f"M{Mt}": gemv(pcl, lib, 1, Mt, [(1024, 50257)], 3, 2, 20) for Mt in (1, 8)}
         ex["head_350m_gemv_int8"] = {f"M{Mt}": gemv(pcl, lib, 2, Mt, [(1024, 50257)], 6, 2, 20) for Mt in (1, 8)}

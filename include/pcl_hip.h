@@ -66,6 +66,25 @@ void pcl_set_abort_on_error(int on);
 int pcl_set_stream(void *hip_stream);
 void *pcl_get_stream(void);
 int pcl_stream_synchronize(void);
+/* Streams and graphs (no counterpart in the reference, which runs on the
+ * CPU). A decode loop issues a short sequence of small products per token;
+ * capturing the sequence once into a HIP graph and replaying it costs one
+ * launch per token instead of one or two per product.
+ *   pcl_stream_create: a new non-blocking stream (default priority).
+ *   pcl_stream_destroy: waits for the stream, frees its scratch; destroy the
+ *     graphs captured on it first.
+ *   pcl_graph_begin/end: capture this thread's native device-pointer calls on
+ *     its stream (which must come from pcl_stream_create) into *graph; the
+ *     calls are recorded, not run. Host-pointer drop-ins cannot be captured.
+ *   pcl_graph_launch: replay on this thread's stream. Every replay uses the
+ *     pointers and sizes recorded at capture time; scratch used by a graph
+ *     stays allocated until its stream is destroyed. */
+void *pcl_stream_create(void);
+int pcl_stream_destroy(void *stream);
+int pcl_graph_begin(void);
+int pcl_graph_end(void **graph);
+int pcl_graph_launch(void *graph);
+int pcl_graph_destroy(void *graph);
 /* Device name and compute-unit count of the current device, for reports. */
 int pcl_device_info(char *name, int name_len, int *num_cus, int *clock_khz);
 

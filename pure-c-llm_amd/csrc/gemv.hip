@@ -10,6 +10,9 @@
 //
 // Every weight byte is read exactly once, with 16-byte loads along the
 // contiguous dimension; the few activation rows are staged in LDS per block.
+// Each thread issues a batch of independent weight loads (clamped to valid
+// addresses, no branches) before it consumes any of them, so a block keeps
+// 16-32 KB of HBM reads in flight; the arithmetic on the batch is guarded.
 // To fill 256 CUs when N alone gives too few blocks, K is split across
 // blocks: each block writes its partial sums to a workspace and a second,
 // small kernel adds the splits in split order (plus bias / accumulate /
@@ -85,30 +88,34 @@ __global__ __launch_bounds__(GV_THREADS) void sgemv_n_kernel(
         for (int j = 0; j < 4; j++) acc[m][j] = 0.f;
 
     const int r0 = rg * run;
-    for (int i = 0; i < run; i += 4) {
-        v4f w[4];
+    // column clamp keeps the vector loads in bounds; clamped lanes only feed
+    // columns >= N, which are never stored
+    const int colc = VEC ? min(col, N - 4) : col;
+    constexpr int UR = 8;  // rows per load batch (run is a multiple of 8)
+    for (int i = 0; i < run; i += UR) {
+        v4f w[UR];
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const int k = kb + r0 + i + u;
-            w[u] = v4f{0.f, 0.f, 0.f, 0.f};
-            if (k < K) {
-                const float *src = W + (long)k * ldw + col;
-                if (VEC) {
-                    if (col < N) w[u] = *reinterpret_cast<const v4f *>(src);
-                } else {
+        for (int u = 0; u < UR; u++) {
+            const int k = min(kb + r0 + i + u, K - 1);
+            const float *src = W + (long)k * ldw + colc;
+            if (VEC) {
+                w[u] = *reinterpret_cast<const v4f *>(src);
+            } else {
+                w[u] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                    for (int j = 0; j < 4; j++)
-                        if (col + j < N) w[u][j] = src[j];
-                }
+                for (int j = 0; j < 4; j++)
+                    if (col + j < N) w[u][j] = src[j];
             }
         }
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
+        for (int u = 0; u < UR; u++) {
+            if (kb + r0 + i + u < K) {
 #pragma unroll
-            for (int m = 0; m < MR; m++) {
-                const float xv = XONES ? 1.f : xs[m][r0 + i + u];
+                for (int m = 0; m < MR; m++) {
+                    const float xv = XONES ? 1.f : xs[m][r0 + i + u];
 #pragma unroll
-                for (int j = 0; j < 4; j++) acc[m][j] += xv * w[u][j];
+                    for (int j = 0; j < 4; j++) acc[m][j] += xv * w[u][j];
+                }
             }
         }
     }
@@ -167,27 +174,42 @@ __global__ __launch_bounds__(GV_THREADS) void sgemv_t_kernel(
 #pragma unroll
         for (int m = 0; m < MR; m++) acc[r][m] = 0.f;
 
-    for (int k = 4 * j; k < klen; k += 64) {
-        v4f xv[MR];
+    // rows past N are clamped (their sums are never stored); k past klen is
+    // clamped for the load and skipped in the arithmetic
+    const float *wrow[SGT_RPL];
 #pragma unroll
-        for (int m = 0; m < MR; m++) xv[m] = *reinterpret_cast<const v4f *>(&xs[m][k]);
+    for (int r = 0; r < SGT_RPL; r++) wrow[r] = W + (long)min(n0 + rs + 16 * r, N - 1) * ldw + kb;
+    constexpr int UK = 4;  // 64-element k steps per load batch
+    for (int k0 = 4 * j; k0 < klen; k0 += 64 * UK) {
+        v4f w[UK][SGT_RPL];
 #pragma unroll
-        for (int r = 0; r < SGT_RPL; r++) {
-            const int n = n0 + rs + 16 * r;
-            v4f w = {0.f, 0.f, 0.f, 0.f};
-            if (n < N) {
-                const float *src = W + (long)n * ldw + kb + k;
+        for (int u = 0; u < UK; u++)
+#pragma unroll
+            for (int r = 0; r < SGT_RPL; r++) {
+                const int k = k0 + 64 * u;
                 if (VEC) {
-                    w = *reinterpret_cast<const v4f *>(src);
+                    w[u][r] = *reinterpret_cast<const v4f *>(wrow[r] + min(k, klen - 4));
                 } else {
+                    w[u][r] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                     for (int e = 0; e < 4; e++)
-                        if (k + e < klen) w[e] = src[e];
+                        if (k + e < klen) w[u][r][e] = wrow[r][k + e];
                 }
             }
 #pragma unroll
-            for (int m = 0; m < MR; m++)
-                acc[r][m] += xv[m][0] * w[0] + xv[m][1] * w[1] + xv[m][2] * w[2] + xv[m][3] * w[3];
+        for (int u = 0; u < UK; u++) {
+            const int k = k0 + 64 * u;
+            if (k < klen) {
+                v4f xv[MR];
+#pragma unroll
+                for (int m = 0; m < MR; m++) xv[m] = *reinterpret_cast<const v4f *>(&xs[m][k]);
+#pragma unroll
+                for (int r = 0; r < SGT_RPL; r++)
+#pragma unroll
+                    for (int m = 0; m < MR; m++)
+                        acc[r][m] += xv[m][0] * w[u][r][0] + xv[m][1] * w[u][r][1] +
+                                     xv[m][2] * w[u][r][2] + xv[m][3] * w[u][r][3];
+            }
         }
     }
 
@@ -295,23 +317,35 @@ __global__ __launch_bounds__(GV_THREADS) void igemv_kernel(
 #pragma unroll
         for (int m = 0; m < MR; m++) acc[r][m] = 0;
 
-    for (int k = 16 * j; k < klen; k += 256) {
-        v4i xv[MR];
+    const int8_t *brow[SGT_RPL];
 #pragma unroll
-        for (int m = 0; m < MR; m++) xv[m] = *reinterpret_cast<const v4i *>(&xs[m][k]);
+    for (int r = 0; r < SGT_RPL; r++) brow[r] = B + (long)min(n0 + rs + 16 * r, N - 1) * ldb + kb;
+    constexpr int UK = 4;  // 256-byte k steps per load batch
+    for (int k0 = 16 * j; k0 < klen; k0 += 256 * UK) {
+        v4i w[UK][SGT_RPL];
 #pragma unroll
-        for (int r = 0; r < SGT_RPL; r++) {
-            const int n = n0 + rs + 16 * r;
-            v4i w = {0, 0, 0, 0};
-            if (n < N) w = *reinterpret_cast<const v4i *>(B + (long)n * ldb + kb + k);
+        for (int u = 0; u < UK; u++)
 #pragma unroll
-            for (int m = 0; m < MR; m++) {
-                int a = acc[r][m];
-                a = __builtin_amdgcn_sdot4(xv[m][0], w[0], a, false);
-                a = __builtin_amdgcn_sdot4(xv[m][1], w[1], a, false);
-                a = __builtin_amdgcn_sdot4(xv[m][2], w[2], a, false);
-                a = __builtin_amdgcn_sdot4(xv[m][3], w[3], a, false);
-                acc[r][m] = a;
+            for (int r = 0; r < SGT_RPL; r++)
+                w[u][r] = *reinterpret_cast<const v4i *>(brow[r] + min(k0 + 256 * u, klen - 16));
+#pragma unroll
+        for (int u = 0; u < UK; u++) {
+            const int k = k0 + 256 * u;
+            if (k < klen) {
+                v4i xv[MR];
+#pragma unroll
+                for (int m = 0; m < MR; m++) xv[m] = *reinterpret_cast<const v4i *>(&xs[m][k]);
+#pragma unroll
+                for (int r = 0; r < SGT_RPL; r++)
+#pragma unroll
+                    for (int m = 0; m < MR; m++) {
+                        int a = acc[r][m];
+                        a = __builtin_amdgcn_sdot4(xv[m][0], w[u][r][0], a, false);
+                        a = __builtin_amdgcn_sdot4(xv[m][1], w[u][r][1], a, false);
+                        a = __builtin_amdgcn_sdot4(xv[m][2], w[u][r][2], a, false);
+                        a = __builtin_amdgcn_sdot4(xv[m][3], w[u][r][3], a, false);
+                        acc[r][m] = a;
+                    }
             }
         }
     }
@@ -373,7 +407,7 @@ static GemvPlan make_plan(int strips, int M, int K, int kstep, int kmin, int kma
 GemvPlan plan_sgemv(int w_trans, int M, int N, int K) {
     const int mr = mr_of(M);
     if (w_trans) return make_plan(cdiv(N, SGT_ROWS), M, K, 64, 256, 8192 / mr, SGT_ROWS);
-    return make_plan(cdiv(N, 64), M, K, 64, 128, 4096 / mr, 64);
+    return make_plan(cdiv(N, 64), M, K, 128, 128, 4096 / mr, 64);
 }
 
 GemvPlan plan_igemv(int M, int N, int K) {

@@ -116,15 +116,23 @@ struct StreamScratch {
     void *aux = nullptr;  // padded INT8 activations
     size_t aux_cap = 0;
     unsigned *amax = nullptr;  // per-tensor amax bits
+    // Set once a graph has been captured on the stream: buffers a graph may
+    // reference are never freed before the stream is destroyed.
+    bool pinned = false;
+    std::vector<void *> retired;
 };
 std::unordered_map<hipStream_t, StreamScratch> g_scratch;
 
-int grow(void **p, size_t *cap, size_t need, hipStream_t s) {
+int grow(void **p, size_t *cap, size_t need, hipStream_t s, StreamScratch &sc) {
     if (need <= *cap) return PCL_OK;
     size_t sz = need + need / 4 + 4096;
     if (*p) {
-        HIP_OK(hipStreamSynchronize(s));
-        HIP_OK(hipFree(*p));
+        if (sc.pinned) {
+            sc.retired.push_back(*p);  // a captured graph may still use it
+        } else {
+            HIP_OK(hipStreamSynchronize(s));
+            HIP_OK(hipFree(*p));
+        }
         *p = nullptr;
         *cap = 0;
     }
@@ -139,8 +147,8 @@ int grow(void **p, size_t *cap, size_t need, hipStream_t s) {
 int get_scratch(hipStream_t s, size_t part_bytes, size_t aux_bytes, StreamScratch **out) {
     std::lock_guard<std::mutex> lk(g_mu);
     StreamScratch &sc = g_scratch[s];
-    PCL_OK_OR_RETURN(grow(&sc.ws.buf, &sc.ws.bytes_cap, part_bytes, s));
-    PCL_OK_OR_RETURN(grow(&sc.aux, &sc.aux_cap, aux_bytes, s));
+    PCL_OK_OR_RETURN(grow(&sc.ws.buf, &sc.ws.bytes_cap, part_bytes, s, sc));
+    PCL_OK_OR_RETURN(grow(&sc.aux, &sc.aux_cap, aux_bytes, s, sc));
     if (!sc.amax) {
         if (hipMalloc((void **)&sc.amax, 256) != hipSuccess)
             return set_error(PCL_ERR_OOM, "amax scratch allocation failed");
@@ -229,6 +237,78 @@ void *pcl_get_stream(void) { return (void *)t_stream; }
 int pcl_stream_synchronize(void) {
     PCL_OK_OR_RETURN(do_init());
     return sync_current();
+}
+
+void *pcl_stream_create(void) {
+    if (do_init() != PCL_OK) return nullptr;
+    hipStream_t st = nullptr;
+    if (hipStreamCreateWithFlags(&st, hipStreamNonBlocking) != hipSuccess) {
+        set_error(PCL_ERR_HIP, "hipStreamCreateWithFlags failed");
+        return nullptr;
+    }
+    return (void *)st;
+}
+
+int pcl_stream_destroy(void *stream) {
+    CHECK_ARG(stream != nullptr, "pcl_stream_destroy: the null stream is not destroyed");
+    PCL_OK_OR_RETURN(do_init());
+    hipStream_t st = (hipStream_t)stream;
+    HIP_OK(hipStreamSynchronize(st));
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        auto it = g_scratch.find(st);
+        if (it != g_scratch.end()) {
+            StreamScratch &sc = it->second;
+            for (void *q : sc.retired) HIP_OK(hipFree(q));
+            if (sc.ws.buf) HIP_OK(hipFree(sc.ws.buf));
+            if (sc.aux) HIP_OK(hipFree(sc.aux));
+            if (sc.amax) HIP_OK(hipFree(sc.amax));
+            g_scratch.erase(it);
+        }
+    }
+    if (t_stream == st) t_stream = nullptr;
+    HIP_OK(hipStreamDestroy(st));
+    return PCL_OK;
+}
+
+int pcl_graph_begin(void) {
+    PCL_OK_OR_RETURN(do_init());
+    CHECK_ARG(t_stream != nullptr,
+              "pcl_graph_begin: capture needs a stream from pcl_stream_create (pcl_set_stream)");
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        g_scratch[t_stream].pinned = true;
+    }
+    HIP_OK(hipStreamBeginCapture(t_stream, hipStreamCaptureModeRelaxed));
+    return PCL_OK;
+}
+
+int pcl_graph_end(void **graph) {
+    CHECK_ARG(graph != nullptr, "pcl_graph_end: graph is NULL");
+    PCL_OK_OR_RETURN(do_init());
+    CHECK_ARG(t_stream != nullptr, "pcl_graph_end: this thread's stream is the null stream");
+    hipGraph_t g = nullptr;
+    HIP_OK(hipStreamEndCapture(t_stream, &g));
+    hipGraphExec_t ge = nullptr;
+    hipError_t e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) return set_error(PCL_ERR_HIP, "hipGraphInstantiate: %s", hipGetErrorString(e));
+    *graph = (void *)ge;
+    return PCL_OK;
+}
+
+int pcl_graph_launch(void *graph) {
+    CHECK_ARG(graph != nullptr, "pcl_graph_launch: graph is NULL");
+    PCL_OK_OR_RETURN(do_init());
+    HIP_OK(hipGraphLaunch((hipGraphExec_t)graph, t_stream));
+    return PCL_OK;
+}
+
+int pcl_graph_destroy(void *graph) {
+    CHECK_ARG(graph != nullptr, "pcl_graph_destroy: graph is NULL");
+    PCL_OK_OR_RETURN(do_init());
+    HIP_OK(hipGraphExecDestroy((hipGraphExec_t)graph));
+    return PCL_OK;
 }
 
 int pcl_device_info(char *name, int name_len, int *num_cus, int *clock_khz) {

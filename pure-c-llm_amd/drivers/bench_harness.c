@@ -189,9 +189,11 @@ done:
  * the layers of a model are visited, with `copies` rotating copies of the
  * whole weight set. kind 0: FP32 K x N weights (matvec); 1: FP32 N x K
  * (head-style); 2: INT8 packed weights with per-token x per-channel dequant. */
+/* kinds[s]: 0 = FP32 W (K x N), 1 = FP32 W (N x K, the tied head),
+ * 2 = INT8 packed weights with dequant */
 typedef struct {
-    int kind, M, nshapes, copies;
-    const int *Ks, *Ns;
+    int M, nshapes, copies;
+    const int *kinds, *Ks, *Ns;
     void **W;  /* [copies * nshapes] */
     void *X, *Xu8, *Y, *sa, *sb;
 } gemv_ctx;
@@ -202,9 +204,9 @@ static int gemv_step(void *c_, int i) {
     for (int s = 0; s < c->nshapes; s++) {
         int K = c->Ks[s], N = c->Ns[s], rc;
         void *W = c->W[copy * c->nshapes + s];
-        if (c->kind == 0)
+        if (c->kinds[s] == 0)
             rc = pcl_sgemv(PCL_OP_N, c->M, N, K, c->X, K, W, N, NULL, 0, c->Y, N, NULL);
-        else if (c->kind == 1)
+        else if (c->kinds[s] == 1)
             rc = pcl_sgemv(PCL_OP_T, c->M, N, K, c->X, K, W, K, NULL, 0, c->Y, N, NULL);
         else
             rc = pcl_gemv_u8s8_dq(c->Xu8, K, W, NULL, c->sa, c->sb, c->Y, N, c->M, N, K, NULL);
@@ -213,21 +215,36 @@ static int gemv_step(void *c_, int i) {
     return PCL_OK;
 }
 
-int pcl_bench_gemv(int kind, int M, int nshapes, const int *Ks, const int *Ns, int copies,
-                   int warmup, int steps, double *ms_total, double *bytes_per_step) {
+/* One token step of a decode sweep as a captured graph: a graph per weight
+ * copy, replayed in rotation (one launch per step). */
+typedef struct {
+    void **graphs;
+    int n;
+} graph_ctx;
+
+static int graph_step(void *c_, int i) {
+    graph_ctx *c = c_;
+    return pcl_graph_launch(c->graphs[i % c->n]);
+}
+
+/* use_graph: 0 = one call per product, 1 = the step captured once per weight
+ * copy and replayed (needs a stream of its own, created here). */
+int pcl_bench_gemv(const int *kinds, int M, int nshapes, const int *Ks, const int *Ns, int copies,
+                   int warmup, int steps, int use_graph, double *ms_total, double *bytes_per_step) {
     int rc = PCL_OK;
     gemv_ctx c;
     memset(&c, 0, sizeof c);
-    c.kind = kind, c.M = M, c.nshapes = nshapes, c.Ks = Ks, c.Ns = Ns;
+    c.kinds = kinds, c.M = M, c.nshapes = nshapes, c.Ks = Ks, c.Ns = Ns;
     c.copies = copies < 1 ? 1 : copies;
     int kmax = 0, nmax = 0;
     double bytes = 0;
     for (int s = 0; s < nshapes; s++) {
         if (Ks[s] > kmax) kmax = Ks[s];
         if (Ns[s] > nmax) nmax = Ns[s];
-        double wb = kind == 2 ? (double)Ns[s] * pcl_s8_kpad(Ks[s]) : 4.0 * Ks[s] * Ns[s];
-        double xb = kind == 2 ? (double)M * Ks[s] : 4.0 * M * Ks[s];
-        bytes += wb + xb + 4.0 * M * Ns[s] + (kind == 2 ? 4.0 * (Ns[s] + M) : 0.0);
+        const int i8 = kinds[s] == 2;
+        double wb = i8 ? (double)Ns[s] * pcl_s8_kpad(Ks[s]) : 4.0 * Ks[s] * Ns[s];
+        double xb = i8 ? (double)M * Ks[s] : 4.0 * M * Ks[s];
+        bytes += wb + xb + 4.0 * M * Ns[s] + (i8 ? 4.0 * (Ns[s] + M) : 0.0);
     }
     *bytes_per_step = bytes;
     c.W = calloc((size_t)c.copies * nshapes, sizeof(void *));
@@ -243,7 +260,7 @@ int pcl_bench_gemv(int kind, int M, int nshapes, const int *Ks, const int *Ns, i
     for (int cp = 0; cp < c.copies; cp++)
         for (int s = 0; s < nshapes; s++) {
             void **slot = &c.W[cp * nshapes + s];
-            if (kind == 2) {
+            if (kinds[s] == 2) {
                 void *Bq = dev_bytes((size_t)Ks[s] * Ns[s], 40 + s);
                 *slot = pcl_malloc(pcl_s8_packed_bytes(Ks[s], Ns[s]));
                 if (!Bq || !*slot) {
@@ -263,7 +280,35 @@ int pcl_bench_gemv(int kind, int M, int nshapes, const int *Ks, const int *Ns, i
                 }
             }
         }
-    TRY(time_steps(gemv_step, &c, warmup, steps, ms_total));
+    if (!use_graph) {
+        TRY(time_steps(gemv_step, &c, warmup, steps, ms_total));
+    } else {
+        void *prev = pcl_get_stream();
+        void *st = pcl_stream_create();
+        graph_ctx g = {calloc((size_t)c.copies, sizeof(void *)), c.copies};
+        if (!st || !g.graphs) {
+            rc = st ? PCL_ERR_OOM : pcl_last_status();
+        } else {
+            pcl_set_stream(st);
+            gemv_step(&c, 0); /* eager pass: sizes the stream's scratch */
+            rc = pcl_stream_synchronize();
+            for (int cp = 0; rc == PCL_OK && cp < c.copies; cp++) {
+                rc = pcl_graph_begin();
+                if (rc == PCL_OK) {
+                    int r1 = gemv_step(&c, cp);
+                    int r2 = pcl_graph_end(&g.graphs[cp]);
+                    rc = r1 != PCL_OK ? r1 : r2;
+                }
+            }
+            if (rc == PCL_OK) rc = time_steps(graph_step, &g, warmup, steps, ms_total);
+            for (int cp = 0; cp < c.copies; cp++)
+                if (g.graphs[cp]) pcl_graph_destroy(g.graphs[cp]);
+            pcl_set_stream(prev);
+            pcl_stream_destroy(st);
+        }
+        free(g.graphs);
+        if (rc != PCL_OK) goto done;
+    }
 done:
     if (c.W)
         for (int j = 0; j < c.copies * nshapes; j++) pcl_free(c.W[j]);

@@ -49,6 +49,12 @@ _PROTOS = {
     "pcl_set_stream": (_i, [_vp]),
     "pcl_get_stream": (_vp, []),
     "pcl_stream_synchronize": (_i, []),
+    "pcl_stream_create": (_vp, []),
+    "pcl_stream_destroy": (_i, [_vp]),
+    "pcl_graph_begin": (_i, []),
+    "pcl_graph_end": (_i, [C.POINTER(_vp)]),
+    "pcl_graph_launch": (_i, [_vp]),
+    "pcl_graph_destroy": (_i, [_vp]),
     "pcl_device_info": (_i, [_cp, _i, C.POINTER(_i), C.POINTER(_i)]),
     "pcl_malloc": (_vp, [_sz]),
     "pcl_free": (_i, [_vp]),
