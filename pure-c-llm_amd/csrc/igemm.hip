@@ -48,10 +48,9 @@
 // outstanding load and drain the pipeline.
 //
 // Tails are handled without per-element branches: rows past M (N) are clamped
-// to the last row and only feed outputs that are never stored; in the last
-// K tile, an A chunk past K is clamped to the last in-bounds chunk, whose
-// bytes meet the zero padding of the packed weights (every B chunk read lies
-// below nk*128 <= Kp).
+// to the last row and only feed outputs that are never stored. K is a
+// multiple of 128: the launcher pads A (with 0x80, i.e. zero) otherwise, and
+// packed weight rows are Kp = roundup(K, 256) >= K bytes, zero past K.
 //
 // K order: the 32x32x32 MFMA takes 16 bytes per lane; lane group g = lane/32
 // supplies logical chunk 2kc+g of the tile for A and for B alike, so the
@@ -207,18 +206,13 @@ __global__ __launch_bounds__(64 * WM * WN * KG) __attribute__((amdgpu_waves_per_
     const int nk = (K + IG_BK - 1) / IG_BK;
     const unsigned lds0 = lds_addr(lds);
 
-    // One DMA instruction of tile t; in a last partial K tile an A chunk past
-    // K is clamped to the chunk at K-16 (B rows are padded to Kp >= nk*128).
+    // One DMA instruction of tile t: a scalar base (operand + 128 t) plus the
+    // lane's fixed offset; no per-tile vector arithmetic. K is a multiple of
+    // 128 (the launcher pads A otherwise), so every chunk is in its row.
     auto dma = [&](int t, int d) {
         const bool isA = d < INST_A;
         const int8_t *base = (isA ? A8 : B) + (long)t * IG_BK;
-        unsigned off = voff[d];
-        if (isA && (t + 1) * IG_BK > K) {
-            const int r = ((d * NW + wave) * 8) + (lane >> 3);
-            const int c16 = ((lane & 7) ^ ((r >> 1) & 7)) * 16;
-            off = off - c16 + min(c16, K - 16 - t * IG_BK);
-        }
-        __builtin_amdgcn_global_load_lds((const void *)(base + off),
+        __builtin_amdgcn_global_load_lds((const void *)(base + voff[d]),
                                          (lds_void_t *)(lds + (t % STAGES) * STAGE + ldso[d]), 16, 0,
                                          0);
     };
@@ -507,6 +501,7 @@ static hipError_t launch_split(int out_mode, int M, int N, int K, const uint8_t 
 hipError_t launch_igemm(int out_mode, int M, int N, int K, const uint8_t *A, long lda,
                         const int8_t *Bpk, long ldb, const int32_t *col_off, const float *sa,
                         const float *sb, void *C, long ldc, hipStream_t stream) {
+    if (K % IG_BK != 0 || lda % 16 != 0 || ldb < K) return hipErrorInvalidValue;
     // Tile choice (measured on the 350M-class and gemm_bench shapes): 256x256
     // tiles with 8 waves when they still cover most of the 256 CUs; 128x128
     // tiles with two K groups (8 waves) when those fill the chip; 64x64
@@ -523,7 +518,7 @@ hipError_t launch_igemm(int out_mode, int M, int N, int K, const uint8_t *A, lon
                                             ldc, stream);
 }
 
-// Copy A into a K16-wide buffer padded with 0x80 (zero after re-centring; the
+// Copy A into a Kd-wide buffer (Kd >= K) padded with 0x80 (zero after re-centring; the
 // packed weights are zero there as well).
 __global__ void pad_a_u8_kernel(const uint8_t *__restrict__ A, long lda, int M, int K,
                                 uint8_t *__restrict__ dst, int K16) {

@@ -34,13 +34,14 @@ hipError_t launch_sgemm(bool a_kcontig, bool b_kcontig, int M, int N, int K, con
 
 // ---- INT8 GEMM (igemm.hip) ----
 // out_mode 0: C is int32 v; 1: C = float(v+off)*sb[n]; 2: C = float(v+off)*(sa[m]*sb[n])
-// Requires K % 16 == 0, lda % 16 == 0, A and Bpk 16-byte aligned, and packed
-// weight rows of ldb = roundup(K, 256) bytes, zero past K.
+// Requires K % 128 == 0, lda % 16 == 0, A and Bpk 16-byte aligned, and packed
+// weight rows of ldb >= K bytes (the packers use roundup(K_true, 256), zero
+// past the true K; A columns past the true K must be 0x80).
 hipError_t launch_igemm(int out_mode, int M, int N, int K, const uint8_t *A, long lda,
                         const int8_t *Bpk, long ldb, const int32_t *col_off, const float *sa,
                         const float *sb, void *C, long ldc, hipStream_t stream);
-// Copy A (M x K, lda) into dst (M x K16, K16 = roundup(K,16)), padding with 0x80.
-hipError_t launch_pad_a_u8(const uint8_t *A, long lda, int M, int K, uint8_t *dst, int K16,
+// Copy A (M x K, lda) into dst (M x Kd, Kd >= K), padding with 0x80.
+hipError_t launch_pad_a_u8(const uint8_t *A, long lda, int M, int K, uint8_t *dst, int Kd,
                            hipStream_t stream);
 
 // ---- GEMV (gemv.hip) ----

@@ -511,17 +511,19 @@ static int igemm_common(int out_mode, const uint8_t *A, int lda, const int8_t *B
                                  sc->ws, s));
         return PCL_OK;
     }
-    if (K % 16 == 0 && lda % 16 == 0 && aligned16(A)) {
+    if (K % 128 == 0 && lda % 16 == 0 && aligned16(A)) {
         HIP_OK(pcl::launch_igemm(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa, sb, C, ldc, s));
         return PCL_OK;
     }
-    // Unaligned activations: copy into a K16-wide padded buffer first.
-    const int K16 = (K + 15) & ~15;
+    // K not a multiple of the 128-byte K tile, or unaligned activations:
+    // copy A into a K128-wide buffer padded with 0x80 (zero after re-centring,
+    // and the packed weights are zero past K as well).
+    const int K128 = (K + 127) & ~127;
     StreamScratch *sc;
-    PCL_OK_OR_RETURN(get_scratch(s, 0, (size_t)M * K16, &sc));
+    PCL_OK_OR_RETURN(get_scratch(s, 0, (size_t)M * K128, &sc));
     uint8_t *Ap = (uint8_t *)sc->aux;
-    HIP_OK(pcl::launch_pad_a_u8(A, lda, M, K, Ap, K16, s));
-    HIP_OK(pcl::launch_igemm(out_mode, M, N, K16, Ap, K16, Bpk, ldb, col_off, sa, sb, C, ldc, s));
+    HIP_OK(pcl::launch_pad_a_u8(A, lda, M, K, Ap, K128, s));
+    HIP_OK(pcl::launch_igemm(out_mode, M, N, K128, Ap, K128, Bpk, ldb, col_off, sa, sb, C, ldc, s));
     return PCL_OK;
 }
 
