@@ -49,7 +49,7 @@
 //
 // Tails are handled without per-element branches: rows past M (N) are clamped
 // to the last row and only feed outputs that are never stored. K is a
-// multiple of 128: the launcher pads A (with 0x80, i.e. zero) otherwise, and
+// multiple of 256: the launcher pads A (with 0x80, i.e. zero) otherwise, and
 // packed weight rows are Kp = roundup(K, 256) >= K bytes, zero past K.
 //
 // K order: the 32x32x32 MFMA takes 16 bytes per lane; lane group g = lane/32
@@ -118,9 +118,11 @@ struct StepPlan {
 // BM x BN output tile per workgroup of WM x WN x KG waves; STAGES-deep LDS
 // ring of 128-byte K tiles; OCC workgroups are meant to share a CU (the LDS
 // ring is sized for it and the register budget is capped accordingly).
-// KG = 2 splits every K tile between two groups of WM x WN waves (k-chunks
-// 0-1 and 2-3), which doubles the waves issuing LDS reads and DMA for one
-// output tile; the two partial sums are added through LDS at the end.
+// KG = 2 uses 256-byte K tiles and two groups of WM x WN waves, group g
+// multiplying k-chunks 4g .. 4g+3 of every tile with the same four-step
+// schedule: twice the waves issue LDS reads and DMA for one output tile, and
+// each barrier covers twice the MFMAs. The groups' partial sums are added
+// through LDS at the end.
 // Requires M*lda and N*ldb below 2^32 (32-bit per-lane DMA offsets).
 template <int BM, int BN, int WM, int WN, int KG, int STAGES, int OCC, int OUT>
 __global__ __launch_bounds__(64 * WM * WN * KG) __attribute__((amdgpu_waves_per_eu(
@@ -136,9 +138,15 @@ __global__ __launch_bounds__(64 * WM * WN * KG) __attribute__((amdgpu_waves_per_
     constexpr int TM = WTM / 32, TN = WTN / 32;
     constexpr int NM = TM * TN;                       // MFMAs per step
     constexpr int NR = TM + TN;                       // fragment reads per step
-    constexpr int SIZE_A = BM * IG_BK, SIZE_B = BN * IG_BK;
+    // K tile: 128 bytes per K group (KG = 2: 256-byte tiles, group g takes
+    // k-chunks 4g .. 4g+3); a row of a tile is CH 16-byte chunks.
+    constexpr int BK = IG_BK * KG;
+    constexpr int CH = BK / 16;
+    constexpr int RSH = (CH == 8) ? 1 : 0;  // log2(16 / CH)
+    constexpr int RPI = 1024 / BK;          // tile rows per DMA instruction
+    constexpr int SIZE_A = BM * BK, SIZE_B = BN * BK;
     constexpr int STAGE = SIZE_A + SIZE_B;
-    constexpr int INST_A = BM / (8 * NW), INST_B = BN / (8 * NW);  // DMA per wave per tile
+    constexpr int INST_A = BM / (RPI * NW), INST_B = BN / (RPI * NW);  // DMA per wave per tile
     constexpr int LOADS = INST_A + INST_B;
     constexpr int D1 = (LOADS + 1) / 2, D2 = LOADS - D1;
     using Plan = StepPlan<NR, D1, D2>;
@@ -146,7 +154,7 @@ __global__ __launch_bounds__(64 * WM * WN * KG) __attribute__((amdgpu_waves_per_
     static_assert(KG == 1 || (KG == 2 && TM % 2 == 0), "K groups: 1, or 2 with an even TM");
     static_assert(KG == 1 || WM * WN * TM * TN * 64 * 64 <= STAGES * STAGE,
                   "the partial-sum exchange must fit in the LDS ring");
-    static_assert(BM % (8 * NW) == 0 && BN % (8 * NW) == 0, "tile rows must split over the waves");
+    static_assert(BM % (RPI * NW) == 0 && BN % (RPI * NW) == 0, "tile rows must split over the waves");
     static_assert((STAGES - 1) * LOADS <= 63, "vmcnt range");
     static_assert(STAGES * STAGE * OCC <= 160 * 1024, "LDS budget of a CU");
 
@@ -186,32 +194,32 @@ __global__ __launch_bounds__(64 * WM * WN * KG) __attribute__((amdgpu_waves_per_
     long ld_out = ldc;
     asm volatile("" : "+s"(C_out), "+s"(ld_out));
 
-    // DMA instruction d (A for d < INST_A, else B) of this wave fills tile
-    // rows rb .. rb+7, rb = 8*(j*NW + wave); lane l loads row rb + l/8 at the
-    // logical chunk whose swizzled slot is l%8. voff is the lane's byte offset
-    // in its operand at k = 0; ldso the instruction's uniform LDS offset.
+    // DMA instruction d (A for d < INST_A, else B) of this wave fills the RPI
+    // tile rows from rb = RPI*(j*NW + wave); lane l loads row rb + l/CH at the
+    // logical chunk whose swizzled slot is l%CH. voff is the lane's byte
+    // offset in its operand at k = 0; ldso the instruction's uniform LDS offset.
     const int8_t *A8 = reinterpret_cast<const int8_t *>(A);
     unsigned voff[LOADS];
     int ldso[LOADS];
 #pragma unroll
     for (int d = 0; d < LOADS; d++) {
         const bool isA = d < INST_A;
-        const int rb = ((isA ? d : d - INST_A) * NW + wave) * 8;
-        const int r = rb + (lane >> 3);
-        const int c = (lane & 7) ^ ((r >> 1) & 7);
+        const int rb = ((isA ? d : d - INST_A) * NW + wave) * RPI;
+        const int r = rb + lane / CH;
+        const int c = (lane % CH) ^ ((r >> RSH) & (CH - 1));
         const int grow = min((isA ? m0 : n0) + r, (isA ? M : N) - 1);
         voff[d] = (unsigned)grow * (unsigned)(isA ? lda : ldb) + (unsigned)(c * 16);
-        ldso[d] = (isA ? 0 : SIZE_A) + rb * IG_BK;
+        ldso[d] = (isA ? 0 : SIZE_A) + rb * BK;
     }
-    const int nk = (K + IG_BK - 1) / IG_BK;
+    const int nk = K / BK;
     const unsigned lds0 = lds_addr(lds);
 
-    // One DMA instruction of tile t: a scalar base (operand + 128 t) plus the
+    // One DMA instruction of tile t: a scalar base (operand + BK t) plus the
     // lane's fixed offset; no per-tile vector arithmetic. K is a multiple of
-    // 128 (the launcher pads A otherwise), so every chunk is in its row.
+    // BK (the launcher pads A otherwise), so every chunk is in its row.
     auto dma = [&](int t, int d) {
         const bool isA = d < INST_A;
-        const int8_t *base = (isA ? A8 : B) + (long)t * IG_BK;
+        const int8_t *base = (isA ? A8 : B) + (long)t * BK;
         __builtin_amdgcn_global_load_lds((const void *)(base + voff[d]),
                                          (lds_void_t *)(lds + (t % STAGES) * STAGE + ldso[d]), 16, 0,
                                          0);
@@ -225,24 +233,24 @@ __global__ __launch_bounds__(64 * WM * WN * KG) __attribute__((amdgpu_waves_per_
 #pragma unroll
             for (int v = 0; v < 16; v++) acc[i][j][v] = 0;
 
-    // Fragment ring: slot c holds k-chunk c of the current or the next tile.
-    // Lane l reads row l%32 of each 32-row block at logical chunk 2c + l/32;
-    // the row swizzle depends on l%32 only.
+    // Fragment ring: slot c holds this group's k-chunk c (32-byte chunk
+    // 4 kg + c of the tile) of the current or the next tile. Lane l reads row
+    // l%32 of each 32-row block at 16-byte chunk 2(4 kg + c) + l/32; the row
+    // swizzle depends on l%32 only.
     v4i fa[IG_KC][TM], fb[IG_KC][TN];
-    const int swz = (r32 >> 1) & 7;
+    const int swz = (r32 >> RSH) & (CH - 1);
     unsigned offa[IG_KC], offb[IG_KC];
 #pragma unroll
     for (int c = 0; c < IG_KC; c++) {
-        const int kchunk = (KG == 1) ? c : 2 * kg + (c & 1);  // 32-byte k-chunk of slot c
-        const int chunk = ((2 * kchunk + g) ^ swz) << 4;
-        offa[c] = (wm * WTM + r32) * IG_BK + chunk;
-        offb[c] = SIZE_A + (wn * WTN + r32) * IG_BK + chunk;
+        const int chunk = ((2 * (IG_KC * kg + c) + g) ^ swz) << 4;
+        offa[c] = (wm * WTM + r32) * BK + chunk;
+        offb[c] = SIZE_A + (wn * WTN + r32) * BK + chunk;
     }
     // read item r (A fragments first) of slot C from the stage at `base`
     auto read_item = [&](unsigned base, auto C, auto R) {
         constexpr int c = decltype(C)::value, r = decltype(R)::value;
-        if constexpr (r < TM) lds_read16<r * 32 * IG_BK>(fa[c][r], base + offa[c]);
-        else lds_read16<(r - TM) * 32 * IG_BK>(fb[c][r - TM], base + offb[c]);
+        if constexpr (r < TM) lds_read16<r * 32 * BK>(fa[c][r], base + offa[c]);
+        else lds_read16<(r - TM) * 32 * BK>(fb[c][r - TM], base + offb[c]);
     };
     // slot C has landed (after the caller's wait): fence it and re-centre A
     auto xor_slot = [&](auto C) {
@@ -260,111 +268,66 @@ __global__ __launch_bounds__(64 * WM * WN * KG) __attribute__((amdgpu_waves_per_
     if (nk >= STAGES) __builtin_amdgcn_s_waitcnt(waitcnt_vm((STAGES - 1) * LOADS));
     else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
     __builtin_amdgcn_s_barrier();
-    if constexpr (KG == 1) {
-        static_for<0, NR>([&](auto R) { read_item(lds0, IC<0>{}, R); });
-        static_for<0, NR>([&](auto R) { read_item(lds0, IC<1>{}, R); });
-        lds_wait<NR>();
-        xor_slot(IC<0>{});
+    static_for<0, NR>([&](auto R) { read_item(lds0, IC<0>{}, R); });
+    static_for<0, NR>([&](auto R) { read_item(lds0, IC<1>{}, R); });
+    lds_wait<NR>();
+    xor_slot(IC<0>{});
 
-        for (int kt = 0; kt < nk; kt++) {
-            const unsigned cur = lds0 + (kt % STAGES) * STAGE;
-            const unsigned nxt = lds0 + ((kt + 1) % STAGES) * STAGE;
-            const bool refill = kt + STAGES < nk;
-            static_for<0, IG_KC>([&](auto KC) {
-                constexpr int kc = KC.value;
-                constexpr int pc = (kc + 2) % IG_KC;  // slot being prefetched
-                const unsigned pbase = (kc + 2 < IG_KC) ? cur : nxt;
-                constexpr int NB = Plan::body(kc);
-                constexpr int G = NM > 1 ? NM - 1 : 1;  // gaps that take body items
-                // body item b of this step
-                auto item = [&](auto Bi) {
-                    constexpr int b = decltype(Bi)::value;
-                    if constexpr (kc < 2) {
-                        read_item(pbase, IC<pc>{}, IC<b>{});
-                    } else if constexpr (kc == 2) {
-                        if constexpr (b == 0) {
-                            // Hand-over to tile kt+1: this wave's reads of tile
-                            // kt are complete and its DMA of tile kt+1 has
-                            // landed; after the barrier the same holds for every
-                            // wave, so tile kt's stage may be refilled.
-                            lds_wait<0>();
-                            xor_slot(IC<3>{});
-                            if (kt + STAGES - 1 < nk)
-                                __builtin_amdgcn_s_waitcnt(waitcnt_vm((STAGES - 2) * LOADS));
-                            else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
-                            __builtin_amdgcn_s_barrier();
-                        } else if constexpr (b <= D1) {
-                            if (refill) dma(kt + STAGES, b - 1);
-                        } else {
-                            read_item(pbase, IC<pc>{}, IC<b - 1 - D1>{});
-                        }
+    for (int kt = 0; kt < nk; kt++) {
+        const unsigned cur = lds0 + (kt % STAGES) * STAGE;
+        const unsigned nxt = lds0 + ((kt + 1) % STAGES) * STAGE;
+        const bool refill = kt + STAGES < nk;
+        static_for<0, IG_KC>([&](auto KC) {
+            constexpr int kc = KC.value;
+            constexpr int pc = (kc + 2) % IG_KC;  // slot being prefetched
+            const unsigned pbase = (kc + 2 < IG_KC) ? cur : nxt;
+            constexpr int NB = Plan::body(kc);
+            constexpr int G = NM > 1 ? NM - 1 : 1;  // gaps that take body items
+            // body item b of this step
+            auto item = [&](auto Bi) {
+                constexpr int b = decltype(Bi)::value;
+                if constexpr (kc < 2) {
+                    read_item(pbase, IC<pc>{}, IC<b>{});
+                } else if constexpr (kc == 2) {
+                    if constexpr (b == 0) {
+                        // Hand-over to tile kt+1: this wave's reads of tile
+                        // kt are complete and its DMA of tile kt+1 has
+                        // landed; after the barrier the same holds for every
+                        // wave, so tile kt's stage may be refilled.
+                        lds_wait<0>();
+                        xor_slot(IC<3>{});
+                        if (kt + STAGES - 1 < nk)
+                            __builtin_amdgcn_s_waitcnt(waitcnt_vm((STAGES - 2) * LOADS));
+                        else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+                        __builtin_amdgcn_s_barrier();
+                    } else if constexpr (b <= D1) {
+                        if (refill) dma(kt + STAGES, b - 1);
                     } else {
-                        if constexpr (b < NR) read_item(pbase, IC<pc>{}, IC<b>{});
-                        else if (refill) dma(kt + STAGES, D1 + b - NR);
+                        read_item(pbase, IC<pc>{}, IC<b - 1 - D1>{});
                     }
-                };
-                static_for<0, NM>([&](auto Q) {
-                    constexpr int q = Q.value, i = q % TM, j = q / TM;
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[kc][i], fb[kc][j], acc[i][j], 0, 0, 0);
-                    __builtin_amdgcn_sched_barrier(0);
-                    if constexpr (q < G) {
-                        static_for<q * NB / G, (q + 1) * NB / G>(item);
-                    }
-                    if constexpr (q == G - 1 && Plan::has_x(kc)) {
-                        // slot kc+1 is older than this step's NR reads
-                        lds_wait<NR>();
-                        xor_slot(IC<(kc + 1) % IG_KC>{});
-                    }
-                    __builtin_amdgcn_sched_barrier(0);
-                });
-            });
-        }
-        lds_wait<0>();  // the last prefetch reads retire before their registers are reused
-    } else {
-        // Two K groups: group kg multiplies k-chunks 2kg and 2kg+1 of every
-        // tile (slots 0 and 1). Step 0 reads slot 1 of the same tile; step 1
-        // hands over to the next tile and reads its slot 0. Waits are full
-        // lgkmcnt(0): the other group's wave on the same SIMD covers them.
-        static_for<0, NR>([&](auto R) { read_item(lds0, IC<0>{}, R); });
-        for (int kt = 0; kt < nk; kt++) {
-            const unsigned cur = lds0 + (kt % STAGES) * STAGE;
-            const unsigned nxt = lds0 + ((kt + 1) % STAGES) * STAGE;
-            const bool refill = kt + STAGES < nk;
-            constexpr int G = NM;
-            // step 0: slot 0, prefetch slot 1 of this tile
-            lds_wait<0>();
-            xor_slot(IC<0>{});
+                } else {
+                    if constexpr (b < NR) read_item(pbase, IC<pc>{}, IC<b>{});
+                    else if (refill) dma(kt + STAGES, D1 + b - NR);
+                }
+            };
             static_for<0, NM>([&](auto Q) {
                 constexpr int q = Q.value, i = q % TM, j = q / TM;
-                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[0][i], fb[0][j], acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[kc][i], fb[kc][j], acc[i][j], 0, 0, 0);
                 __builtin_amdgcn_sched_barrier(0);
-                static_for<q * NR / G, (q + 1) * NR / G>([&](auto R) { read_item(cur, IC<1>{}, R); });
-                __builtin_amdgcn_sched_barrier(0);
-            });
-            // step 1: hand-over to tile kt+1 (as in the single-group schedule),
-            // then slot 1 while the DMA refill and the next tile's slot 0 go out
-            lds_wait<0>();
-            if (kt + STAGES - 1 < nk) __builtin_amdgcn_s_waitcnt(waitcnt_vm((STAGES - 2) * LOADS));
-            else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
-            __builtin_amdgcn_s_barrier();
-            xor_slot(IC<1>{});
-            constexpr int NI = LOADS + NR;
-            static_for<0, NM>([&](auto Q) {
-                constexpr int q = Q.value, i = q % TM, j = q / TM;
-                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[1][i], fb[1][j], acc[i][j], 0, 0, 0);
-                __builtin_amdgcn_sched_barrier(0);
-                static_for<q * NI / G, (q + 1) * NI / G>([&](auto Bi) {
-                    constexpr int b = decltype(Bi)::value;
-                    if constexpr (b < LOADS) {
-                        if (refill) dma(kt + STAGES, b);
-                    } else {
-                        read_item(nxt, IC<0>{}, IC<b - LOADS>{});
-                    }
-                });
+                if constexpr (q < G) {
+                    static_for<q * NB / G, (q + 1) * NB / G>(item);
+                }
+                if constexpr (q == G - 1 && Plan::has_x(kc)) {
+                    // slot kc+1 is older than this step's NR reads
+                    lds_wait<NR>();
+                    xor_slot(IC<(kc + 1) % IG_KC>{});
+                }
                 __builtin_amdgcn_sched_barrier(0);
             });
-        }
-        lds_wait<0>();
+        });
+    }
+    lds_wait<0>();  // the last prefetch reads retire before their registers are reused
+    if constexpr (KG == 2) {
         // Add the groups' partial sums: group 0 keeps the upper half of the
         // wave tile's 32-row blocks (i < TM/2), group 1 the lower half; each
         // hands the other half to its partner through LDS (lane-major, so the
@@ -501,7 +464,7 @@ static hipError_t launch_split(int out_mode, int M, int N, int K, const uint8_t 
 hipError_t launch_igemm(int out_mode, int M, int N, int K, const uint8_t *A, long lda,
                         const int8_t *Bpk, long ldb, const int32_t *col_off, const float *sa,
                         const float *sb, void *C, long ldc, hipStream_t stream) {
-    if (K % IG_BK != 0 || lda % 16 != 0 || ldb < K) return hipErrorInvalidValue;
+    if (K % 256 != 0 || lda % 16 != 0 || ldb < K) return hipErrorInvalidValue;
     // Tile choice (measured on the 350M-class and gemm_bench shapes): 256x256
     // tiles with 8 waves when they still cover most of the 256 CUs; 128x128
     // tiles with two K groups (8 waves) when those fill the chip; 64x64
@@ -512,7 +475,7 @@ hipError_t launch_igemm(int out_mode, int M, int N, int K, const uint8_t *A, lon
         return launch_split<256, 256, 4, 2, 1, 2, 1>(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa,
                                                   sb, C, ldc, stream);
     if (t128 >= 256)
-        return launch_split<128, 128, 2, 2, 2, 4, 1>(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa,
+        return launch_split<128, 128, 2, 2, 2, 2, 1>(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa,
                                                   sb, C, ldc, stream);
     return launch_split<64, 64, 2, 2, 1, 4, 1>(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa, sb, C,
                                             ldc, stream);

@@ -34,7 +34,7 @@ hipError_t launch_sgemm(bool a_kcontig, bool b_kcontig, int M, int N, int K, con
 
 // ---- INT8 GEMM (igemm.hip) ----
 // out_mode 0: C is int32 v; 1: C = float(v+off)*sb[n]; 2: C = float(v+off)*(sa[m]*sb[n])
-// Requires K % 128 == 0, lda % 16 == 0, A and Bpk 16-byte aligned, and packed
+// Requires K % 256 == 0, lda % 16 == 0, A and Bpk 16-byte aligned, and packed
 // weight rows of ldb >= K bytes (the packers use roundup(K_true, 256), zero
 // past the true K; A columns past the true K must be 0x80).
 hipError_t launch_igemm(int out_mode, int M, int N, int K, const uint8_t *A, long lda,

@@ -511,19 +511,19 @@ static int igemm_common(int out_mode, const uint8_t *A, int lda, const int8_t *B
                                  sc->ws, s));
         return PCL_OK;
     }
-    if (K % 128 == 0 && lda % 16 == 0 && aligned16(A)) {
+    if (K % 256 == 0 && lda % 16 == 0 && aligned16(A)) {
         HIP_OK(pcl::launch_igemm(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa, sb, C, ldc, s));
         return PCL_OK;
     }
-    // K not a multiple of the 128-byte K tile, or unaligned activations:
-    // copy A into a K128-wide buffer padded with 0x80 (zero after re-centring,
-    // and the packed weights are zero past K as well).
-    const int K128 = (K + 127) & ~127;
+    // K not a multiple of 256 (the K tile granularity), or unaligned
+    // activations: copy A into a Kp-wide buffer padded with 0x80 (zero after
+    // re-centring; the packed weights are zero past K as well).
+    const int Kp = (int)ldb;
     StreamScratch *sc;
-    PCL_OK_OR_RETURN(get_scratch(s, 0, (size_t)M * K128, &sc));
+    PCL_OK_OR_RETURN(get_scratch(s, 0, (size_t)M * Kp, &sc));
     uint8_t *Ap = (uint8_t *)sc->aux;
-    HIP_OK(pcl::launch_pad_a_u8(A, lda, M, K, Ap, K128, s));
-    HIP_OK(pcl::launch_igemm(out_mode, M, N, K128, Ap, K128, Bpk, ldb, col_off, sa, sb, C, ldc, s));
+    HIP_OK(pcl::launch_pad_a_u8(A, lda, M, K, Ap, Kp, s));
+    HIP_OK(pcl::launch_igemm(out_mode, M, N, Kp, Ap, Kp, Bpk, ldb, col_off, sa, sb, C, ldc, s));
     return PCL_OK;
 }
 
