@@ -71,19 +71,6 @@ constexpr int IG_KC = 4;    // 32-byte MFMA k-chunks (steps) per tile
 // s_waitcnt immediate for "vmcnt <= n", leaving expcnt and lgkmcnt unchecked.
 constexpr int waitcnt_vm(int n) { return (n & 15) | (((n >> 4) & 3) << 14) | (7 << 4) | (15 << 8); }
 
-// Compile-time loop: f(IC<I>{}) for I = LO .. HI-1.
-template <int V>
-struct IC {
-    static constexpr int value = V;
-};
-template <int I, int N, typename F>
-__device__ __forceinline__ void static_for(F &&f) {
-    if constexpr (I < N) {
-        f(IC<I>{});
-        static_for<I + 1, N>(f);
-    }
-}
-
 // Fragment reads from LDS are issued by inline assembly and waited for
 // explicitly. The compiler's own wait insertion turns every LDS wait into
 // lgkmcnt(0) once LDS DMA instructions are in flight, which would serialise

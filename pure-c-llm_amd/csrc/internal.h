@@ -25,12 +25,23 @@ struct GemvPlan {
 };
 
 // ---- FP32 GEMM (sgemm.hip) ----
+// Tile configuration and K split chosen for a shape; with splits > 1 the
+// partial products ([splits][M][N] fp32, part_bytes) go to the workspace and a
+// second kernel adds them in split order.
+struct SgemmPlan {
+    int cfg;
+    int splits;
+    int kchunk;         // K per split (a multiple of 64 when split)
+    size_t part_bytes;  // workspace bytes (0 when splits == 1)
+};
+SgemmPlan plan_sgemm(int M, int N, int K);
 // C(M,N) = (accumulate ? C : 0) + op(A)(M,K) . op(B)(K,N) + bias
 // a_kcontig: element (m,k) of A at A[m*lda + k] (else A[k*lda + m]);
 // b_kcontig: element (k,n) of B at B[n*ldb + k] (else B[k*ldb + n]).
-hipError_t launch_sgemm(bool a_kcontig, bool b_kcontig, int M, int N, int K, const float *A,
-                        long lda, const float *B, long ldb, const float *bias, int accumulate,
-                        float *C, long ldc, hipStream_t stream);
+hipError_t launch_sgemm(const SgemmPlan &p, bool a_kcontig, bool b_kcontig, int M, int N, int K,
+                        const float *A, long lda, const float *B, long ldb, const float *bias,
+                        int accumulate, float *C, long ldc, const Workspace &ws,
+                        hipStream_t stream);
 
 // ---- INT8 GEMM (igemm.hip) ----
 // out_mode 0: C is int32 v; 1: C = float(v+off)*sb[n]; 2: C = float(v+off)*(sa[m]*sb[n])
@@ -79,6 +90,19 @@ hipError_t launch_corr_to_offset(const int32_t *colsum, const int32_t *corr, int
 
 // ---- helpers shared by the kernels ----
 namespace pcl {
+
+// Compile-time loop: f(IC<I>{}) for I = LO .. HI-1.
+template <int V>
+struct IC {
+    static constexpr int value = V;
+};
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+    if constexpr (I < N) {
+        f(IC<I>{});
+        static_for<I + 1, N>(f);
+    }
+}
 
 // Workgroups are dispatched round-robin over the 8 XCDs of an MI355X
 // (workgroup i runs on XCD i % 8). Renumber them so that each XCD receives a

@@ -429,8 +429,12 @@ int pcl_sgemm(int opA, int opB, int M, int N, int K, const float *A, int lda, co
     PCL_OK_OR_RETURN(do_init());
     if (M <= 8 && opA == PCL_OP_N)
         return pcl_sgemv(opB, M, N, K, A, lda, B, ldb, bias, accumulate, C, ldc, stream);
-    HIP_OK(pcl::launch_sgemm(opA == PCL_OP_N, opB == PCL_OP_T, M, N, K, A, lda, B, ldb, bias,
-                             accumulate, C, ldc, pick(stream)));
+    hipStream_t s = pick(stream);
+    pcl::SgemmPlan p = pcl::plan_sgemm(M, N, K);
+    StreamScratch *sc;
+    PCL_OK_OR_RETURN(get_scratch(s, p.part_bytes, 0, &sc));
+    HIP_OK(pcl::launch_sgemm(p, opA == PCL_OP_N, opB == PCL_OP_T, M, N, K, A, lda, B, ldb, bias,
+                             accumulate, C, ldc, sc->ws, s));
     return PCL_OK;
 }
 

@@ -27,19 +27,18 @@ namespace pcl {
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
-constexpr int SG_THREADS = 256;
 constexpr int SG_PAD_K = 4;   // floats of padding per K-contiguous LDS row
 constexpr int SG_PAD_MN = 4;  // floats of padding per MN-contiguous LDS row
 
-template <int ROWS, int BK, bool KC>
+template <int NTHR, int ROWS, int BK, bool KC>
 struct OperandTile {
     // LDS footprint of one buffer, in floats
     static constexpr int LD = KC ? (BK + SG_PAD_K) : (ROWS + SG_PAD_MN);
     static constexpr int SIZE = KC ? ROWS * LD : BK * LD;
     // 4-float vectors per tile and per thread
     static constexpr int VECS = ROWS * BK / 4;
-    static constexpr int PER_THREAD = VECS / SG_THREADS;
-    static_assert(VECS % SG_THREADS == 0, "tile must split evenly over 256 threads");
+    static constexpr int PER_THREAD = VECS / NTHR;
+    static_assert(VECS % NTHR == 0, "tile must split evenly over the workgroup");
 
     // global -> registers. rows0: first row (m or n) of the tile; k0: first k.
     template <bool VEC>
@@ -48,7 +47,7 @@ struct OperandTile {
                                                 int tid) {
 #pragma unroll
         for (int i = 0; i < PER_THREAD; i++) {
-            int e = tid + i * SG_THREADS;
+            int e = tid + i * NTHR;
             int row, k;
             if (KC) {
                 row = e / (BK / 4);
@@ -81,7 +80,7 @@ struct OperandTile {
     __device__ __forceinline__ static void store(const v4f (&r)[PER_THREAD], float *lds, int tid) {
 #pragma unroll
         for (int i = 0; i < PER_THREAD; i++) {
-            int e = tid + i * SG_THREADS;
+            int e = tid + i * NTHR;
             int off;
             if (KC) off = (e / (BK / 4)) * LD + (e % (BK / 4)) * 4;
             else off = (e / (ROWS / 4)) * LD + (e % (ROWS / 4)) * 4;
@@ -103,30 +102,55 @@ struct OperandTile {
     }
 };
 
-template <int BM, int BN, int BK, bool A_KC, bool B_KC, bool VEC>
-__global__ __launch_bounds__(SG_THREADS) void sgemm_mfma_kernel(
+// BM x BN output tile per workgroup of 256*KG threads: 2x2 waves share the
+// tile spatially, and KG groups of those 4 waves split every BK-deep K tile
+// (group g multiplies chunks [g*BK/(8*KG), (g+1)*BK/(8*KG))), so a small grid
+// still puts KG waves on every SIMD. The groups' partial sums are added
+// through LDS at the end (group g finishes the accumulator registers
+// v in [16g/KG, 16(g+1)/KG) of every 32x32 block).
+// PF: global tiles in flight in registers ahead of the LDS tile being
+// multiplied (a ring of PF register slots, refilled PF tiles ahead).
+// Split K: workgroup row blockIdx.y multiplies k in [y*kchunk, (y+1)*kchunk)
+// and writes its partial product to C + y*M*ldc (kchunk = K: no split).
+template <int BM, int BN, int BK, int KG, int PF, bool A_KC, bool B_KC, bool VEC>
+__global__ __launch_bounds__(256 * KG) void sgemm_mfma_kernel(
     const float *__restrict__ A, long lda, const float *__restrict__ B, long ldb,
     const float *__restrict__ bias, float *__restrict__ C, long ldc, int M, int N, int K,
-    int accumulate) {
-    using TA = OperandTile<BM, BK, A_KC>;
-    using TB = OperandTile<BN, BK, B_KC>;
+    int accumulate, int kchunk) {
+    constexpr int NTHR = 256 * KG;
+    using TA = OperandTile<NTHR, BM, BK, A_KC>;
+    using TB = OperandTile<NTHR, BN, BK, B_KC>;
     constexpr int WTM = BM / 2, WTN = BN / 2;   // wave tile
     constexpr int TM = WTM / 32, TN = WTN / 32;  // 32x32 MFMA blocks per wave
-    static_assert(BK % 8 == 0, "BK must be a multiple of 8");
+    constexpr int KCH = BK / 8;                  // 8-deep k chunks per tile
+    constexpr int KCG = KCH / KG;                // chunks per K group
+    static_assert(BK % 8 == 0 && KCH % KG == 0, "K tile must split over the K groups");
+    static_assert(KG == 1 || KG == 2, "one or two K groups");
+    static_assert(PF >= 1, "at least one tile in flight");
 
-    // two buffers, each [A tile | B tile]
+    // two buffers, each [A tile | B tile]; the K groups' exchange reuses them
     constexpr int BUF = TA::SIZE + TB::SIZE;
-    __shared__ __attribute__((aligned(16))) float lds[2 * BUF];
+    constexpr int XCH = KG > 1 ? 2 * 256 * TM * TN * 8 : 0;
+    constexpr int LDS_FLOATS = 2 * BUF > XCH ? 2 * BUF : XCH;
+    __shared__ __attribute__((aligned(16))) float lds[LDS_FLOATS];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int kg = wave >> 2, wq = wave & 3;
+    const int wm = wq >> 1, wn = wq & 1;
     const int r32 = lane & 31, g = lane >> 5;
 
     const int nbm = (M + BM - 1) / BM, nbn = (N + BN - 1) / BN;
     int bm, bn;
     tile_coords(xcd_remap(blockIdx.x, nbm * nbn), nbm, nbn, 8, bm, bn);
     const int m0 = bm * BM, n0 = bn * BN;
+    {
+        const int kbeg = blockIdx.y * kchunk;
+        K = K - kbeg < kchunk ? K - kbeg : kchunk;
+        A += A_KC ? kbeg : (long)kbeg * lda;
+        B += B_KC ? kbeg : (long)kbeg * ldb;
+        C += (long)blockIdx.y * M * ldc;
+    }
 
     v16f acc[TM][TN];
 #pragma unroll
@@ -136,47 +160,79 @@ __global__ __launch_bounds__(SG_THREADS) void sgemm_mfma_kernel(
 #pragma unroll
             for (int v = 0; v < 16; v++) acc[i][j][v] = 0.f;
 
-    v4f ra[TA::PER_THREAD], rb[TB::PER_THREAD];
+    v4f ra[PF][TA::PER_THREAD], rb[PF][TB::PER_THREAD];
     const int nk = (K + BK - 1) / BK;
+    // tile t's registers live in slot t % PF; tiles past the end re-read the
+    // last tile (never stored), so every iteration issues the same loads
+    auto fetch = [&](auto S, int t) {
+        const int k0 = (t < nk ? t : nk - 1) * BK;
+        TA::template load<VEC>(ra[S.value], A, lda, m0, M, k0, K, tid);
+        TB::template load<VEC>(rb[S.value], B, ldb, n0, N, k0, K, tid);
+    };
+    auto put = [&](auto S, int buf) {
+        TA::store(ra[S.value], lds + buf * BUF, tid);
+        TB::store(rb[S.value], lds + buf * BUF + TA::SIZE, tid);
+    };
 
     if (nk > 0) {
-        TA::template load<VEC>(ra, A, lda, m0, M, 0, K, tid);
-        TB::template load<VEC>(rb, B, ldb, n0, N, 0, K, tid);
-        TA::store(ra, lds, tid);
-        TB::store(rb, lds + TA::SIZE, tid);
+        static_for<0, PF>([&](auto S) { fetch(S, S.value); });
+        put(IC<0>{}, 0);
     }
     __syncthreads();
 
-    for (int kt = 0; kt < nk; kt++) {
-        const int cur = kt & 1;
-        const bool more = kt + 1 < nk;
-        if (more) {
-            TA::template load<VEC>(ra, A, lda, m0, M, (kt + 1) * BK, K, tid);
-            TB::template load<VEC>(rb, B, ldb, n0, N, (kt + 1) * BK, K, tid);
-        }
-        const float *la = lds + cur * BUF;
-        const float *lb = la + TA::SIZE;
+    for (int kt0 = 0; kt0 < nk; kt0 += PF) {
+        static_for<0, PF>([&](auto S) {
+            const int kt = kt0 + S.value;
+            if (kt < nk) {
+                // slot S held tile kt, already in LDS: refill it PF tiles ahead
+                fetch(S, kt + PF);
+                const float *la = lds + (kt & 1) * BUF;
+                const float *lb = la + TA::SIZE;
 #pragma unroll
-        for (int kc = 0; kc < BK / 8; kc++) {
-            v4f fa[TM], fb[TN];
+                for (int c = 0; c < KCG; c++) {
+                    const int kc = kg * KCG + c;
+                    v4f fa[TM], fb[TN];
 #pragma unroll
-            for (int i = 0; i < TM; i++) fa[i] = TA::frag(la, wm * WTM + i * 32 + r32, kc, g);
+                    for (int i = 0; i < TM; i++) fa[i] = TA::frag(la, wm * WTM + i * 32 + r32, kc, g);
 #pragma unroll
-            for (int j = 0; j < TN; j++) fb[j] = TB::frag(lb, wn * WTN + j * 32 + r32, kc, g);
+                    for (int j = 0; j < TN; j++) fb[j] = TB::frag(lb, wn * WTN + j * 32 + r32, kc, g);
 #pragma unroll
-            for (int s = 0; s < 4; s++)
+                    for (int s = 0; s < 4; s++)
 #pragma unroll
-                for (int i = 0; i < TM; i++)
+                        for (int i = 0; i < TM; i++)
 #pragma unroll
-                    for (int j = 0; j < TN; j++)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][s], fb[j][s],
-                                                                         acc[i][j], 0, 0, 0);
-        }
-        if (more) {
-            TA::store(ra, lds + (cur ^ 1) * BUF, tid);
-            TB::store(rb, lds + (cur ^ 1) * BUF + TA::SIZE, tid);
-        }
+                            for (int j = 0; j < TN; j++)
+                                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+                                    fa[i][s], fb[j][s], acc[i][j], 0, 0, 0);
+                }
+                if (kt + 1 < nk) put(IC<(S.value + 1) % PF>{}, (kt + 1) & 1);
+                __syncthreads();
+            }
+        });
+    }
+
+    // K groups: group g hands the registers it does not finish to its partner
+    // (lane-contiguous, conflict-free), then adds the partner's share of its
+    // own registers. The last loop barrier has retired every tile read.
+    constexpr int VH = 16 / KG;  // accumulator registers finished per group
+    if constexpr (KG > 1) {
+        float *xg = lds + (1 - kg) * (XCH / 2);  // the partner's inbox
+        float *xm = lds + kg * (XCH / 2);
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+#pragma unroll
+                for (int v = 0; v < VH; v++)
+                    xg[(((wq * TM + i) * TN + j) * VH + v) * 64 + lane] = acc[i][j][(1 - kg) * VH + v];
         __syncthreads();
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+#pragma unroll
+                for (int v = 0; v < VH; v++)
+                    acc[i][j][kg * VH + v] += xm[(((wq * TM + i) * TN + j) * VH + v) * 64 + lane];
     }
 
     // Epilogue. 32x32 accumulator layout: register v of lane l holds
@@ -189,7 +245,8 @@ __global__ __launch_bounds__(SG_THREADS) void sgemm_mfma_kernel(
 #pragma unroll
         for (int i = 0; i < TM; i++) {
 #pragma unroll
-            for (int v = 0; v < 16; v++) {
+            for (int u = 0; u < VH; u++) {
+                const int v = (KG > 1 ? kg * VH : 0) + u;
                 const int row = m0 + wm * WTM + i * 32 + (v >> 2) * 8 + g * 4 + (v & 3);
                 if (row < M) {
                     float *c = C + (long)row * ldc + col;
@@ -202,52 +259,133 @@ __global__ __launch_bounds__(SG_THREADS) void sgemm_mfma_kernel(
     }
 }
 
-template <int BM, int BN, int BK, bool A_KC, bool B_KC>
-static hipError_t launch_cfg(bool vec, int M, int N, int K, const float *A, long lda,
-                             const float *B, long ldb, const float *bias, int accumulate, float *C,
-                             long ldc, hipStream_t stream) {
+// Split-K epilogue: C = (accumulate ? C : 0) + (P_0 + P_1 + ... + bias), the
+// partial products added in split order (deterministic).
+__global__ void sgemm_splitk_reduce_kernel(const float *__restrict__ P, int splits, int M, int N,
+                                           const float *__restrict__ bias, float *__restrict__ C,
+                                           long ldc, int accumulate) {
+    const long i = blockIdx.x * (long)blockDim.x + threadIdx.x;
+    const long MN = (long)M * N;
+    if (i >= MN) return;
+    const int m = (int)(i / N), n = (int)(i % N);
+    float s = P[i];
+    for (int z = 1; z < splits; z++) s += P[z * MN + i];
+    float out = s + (bias ? bias[n] : 0.f);
+    float *c = C + (long)m * ldc + n;
+    if (accumulate) out = *c + out;
+    *c = out;
+}
+
+template <int BM, int BN, int BK, int KG, int PF, bool A_KC, bool B_KC>
+static hipError_t launch_cfg(bool vec, int M, int N, int K, int splits, int kchunk,
+                             const float *A, long lda, const float *B, long ldb, const float *bias,
+                             int accumulate, float *C, long ldc, hipStream_t stream) {
     const int nblk = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
     if (nblk == 0) return hipSuccess;
-    dim3 grid(nblk), block(SG_THREADS);
+    dim3 grid(nblk, splits), block(256 * KG);
     if (vec)
-        hipLaunchKernelGGL((sgemm_mfma_kernel<BM, BN, BK, A_KC, B_KC, true>), grid, block, 0,
-                           stream, A, lda, B, ldb, bias, C, ldc, M, N, K, accumulate);
+        hipLaunchKernelGGL((sgemm_mfma_kernel<BM, BN, BK, KG, PF, A_KC, B_KC, true>), grid, block, 0,
+                           stream, A, lda, B, ldb, bias, C, ldc, M, N, K, accumulate, kchunk);
     else
-        hipLaunchKernelGGL((sgemm_mfma_kernel<BM, BN, BK, A_KC, B_KC, false>), grid, block, 0,
-                           stream, A, lda, B, ldb, bias, C, ldc, M, N, K, accumulate);
+        hipLaunchKernelGGL((sgemm_mfma_kernel<BM, BN, BK, KG, PF, A_KC, B_KC, false>), grid, block,
+                           0, stream, A, lda, B, ldb, bias, C, ldc, M, N, K, accumulate, kchunk);
     return hipGetLastError();
 }
 
 static bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-template <bool A_KC, bool B_KC>
-static hipError_t dispatch_layout(int M, int N, int K, const float *A, long lda, const float *B,
-                                  long ldb, const float *bias, int accumulate, float *C, long ldc,
-                                  hipStream_t stream) {
-    // 16-byte vector loads need the contiguous extent and leading dimension to
-    // be multiples of 4 floats and 16-byte aligned bases.
-    bool vec = aligned16(A) && aligned16(B) && lda % 4 == 0 && ldb % 4 == 0 &&
-               (A_KC ? K % 4 == 0 : M % 4 == 0) && (B_KC ? K % 4 == 0 : N % 4 == 0);
-    // 128x128 tiles when they still give >= 2 workgroups per CU (512 on the
-    // 256-CU MI355X); 64x64 otherwise so small GEMMs fill the chip.
-    long big = (long)((M + 127) / 128) * ((N + 127) / 128);
-    if (big >= 512)
-        return launch_cfg<128, 128, 16, A_KC, B_KC>(vec, M, N, K, A, lda, B, ldb, bias, accumulate,
-                                                    C, ldc, stream);
-    return launch_cfg<64, 64, 16, A_KC, B_KC>(vec, M, N, K, A, lda, B, ldb, bias, accumulate, C,
-                                              ldc, stream);
+// Tile configurations (launch_cfg parameters), chosen by plan_sgemm.
+enum SgemmCfg {
+    SG_128_BK16 = 0,     // 128x128, BK 16, 4 waves: up to 4 workgroups per CU
+    SG_128_BK32 = 1,     // 128x128, BK 32, 4 waves: 2 workgroups per CU
+    SG_128_KG2 = 2,      // 128x128, BK 32, 8 waves in two K groups, 2 tiles in flight
+    SG_64_KG2 = 3,       // 64x64, BK 64, 8 waves in two K groups, 2 tiles in flight
+};
+
+SgemmPlan plan_sgemm(int M, int N, int K) {
+    SgemmPlan p{SG_64_KG2, 1, K > 0 ? K : 1, 0};
+    const long t128 = (long)((M + 127) / 128) * ((N + 127) / 128);
+    const long t64 = (long)((M + 63) / 64) * ((N + 63) / 64);
+    if (t128 >= 512) {
+        // whole rounds of 2 per CU take the deeper tile, otherwise 4 per CU
+        // keep more of the grid resident at once
+        p.cfg = t128 % 512 == 0 ? SG_128_BK32 : SG_128_BK16;
+    } else if (t128 >= 256) {
+        p.cfg = SG_128_KG2;
+    } else if (t64 < 256 && K >= 128) {
+        // too few tiles for 256 CUs: split K (chunks of whole 64-deep tiles)
+        int splits = (int)(256 / (t64 > 0 ? t64 : 1));
+        if (splits > K / 64) splits = K / 64;
+        if (splits > 16) splits = 16;
+        if (splits > 1) {
+            const int kchunk = ((K + splits - 1) / splits + 63) / 64 * 64;
+            p.splits = (K + kchunk - 1) / kchunk;
+            p.kchunk = kchunk;
+            if (p.splits > 1) p.part_bytes = (size_t)p.splits * M * N * sizeof(float);
+            else p.kchunk = K;
+        }
+    }
+    return p;
 }
 
-hipError_t launch_sgemm(bool a_kcontig, bool b_kcontig, int M, int N, int K, const float *A,
-                        long lda, const float *B, long ldb, const float *bias, int accumulate,
-                        float *C, long ldc, hipStream_t stream) {
+template <bool A_KC, bool B_KC>
+static hipError_t dispatch_layout(const SgemmPlan &p, int M, int N, int K, const float *A,
+                                  long lda, const float *B, long ldb, const float *bias,
+                                  int accumulate, float *C, long ldc, const Workspace &ws,
+                                  hipStream_t stream) {
+    // 16-byte vector loads need the contiguous extent and leading dimension to
+    // be multiples of 4 floats and 16-byte aligned bases (split-K chunks are
+    // multiples of 64, so every chunk keeps that alignment).
+    bool vec = aligned16(A) && aligned16(B) && lda % 4 == 0 && ldb % 4 == 0 &&
+               (A_KC ? K % 4 == 0 : M % 4 == 0) && (B_KC ? K % 4 == 0 : N % 4 == 0);
+    const bool split = p.splits > 1;
+    if (split && (ws.buf == nullptr || ws.bytes_cap < p.part_bytes)) return hipErrorInvalidValue;
+    float *out = split ? static_cast<float *>(ws.buf) : C;
+    const long ldo = split ? N : ldc;
+    const float *b = split ? nullptr : bias;
+    const int acc = split ? 0 : accumulate;
+    hipError_t e;
+    switch (p.cfg) {
+    case SG_128_BK16:
+        e = launch_cfg<128, 128, 16, 1, 1, A_KC, B_KC>(vec, M, N, K, p.splits, p.kchunk, A, lda, B,
+                                                       ldb, b, acc, out, ldo, stream);
+        break;
+    case SG_128_BK32:
+        e = launch_cfg<128, 128, 32, 1, 1, A_KC, B_KC>(vec, M, N, K, p.splits, p.kchunk, A, lda, B,
+                                                       ldb, b, acc, out, ldo, stream);
+        break;
+    case SG_128_KG2:
+        e = launch_cfg<128, 128, 32, 2, 2, A_KC, B_KC>(vec, M, N, K, p.splits, p.kchunk, A, lda, B,
+                                                       ldb, b, acc, out, ldo, stream);
+        break;
+    default:
+        e = launch_cfg<64, 64, 64, 2, 2, A_KC, B_KC>(vec, M, N, K, p.splits, p.kchunk, A, lda, B,
+                                                     ldb, b, acc, out, ldo, stream);
+        break;
+    }
+    if (e != hipSuccess || !split) return e;
+    const long MN = (long)M * N;
+    hipLaunchKernelGGL(sgemm_splitk_reduce_kernel, dim3((unsigned)((MN + 255) / 256)), dim3(256), 0,
+                       stream, static_cast<const float *>(ws.buf), p.splits, M, N, bias, C, ldc,
+                       accumulate);
+    return hipGetLastError();
+}
+
+hipError_t launch_sgemm(const SgemmPlan &p, bool a_kcontig, bool b_kcontig, int M, int N, int K,
+                        const float *A, long lda, const float *B, long ldb, const float *bias,
+                        int accumulate, float *C, long ldc, const Workspace &ws,
+                        hipStream_t stream) {
     if (a_kcontig && !b_kcontig)
-        return dispatch_layout<true, false>(M, N, K, A, lda, B, ldb, bias, accumulate, C, ldc, stream);
+        return dispatch_layout<true, false>(p, M, N, K, A, lda, B, ldb, bias, accumulate, C, ldc, ws,
+                                            stream);
     if (a_kcontig && b_kcontig)
-        return dispatch_layout<true, true>(M, N, K, A, lda, B, ldb, bias, accumulate, C, ldc, stream);
+        return dispatch_layout<true, true>(p, M, N, K, A, lda, B, ldb, bias, accumulate, C, ldc, ws,
+                                           stream);
     if (!a_kcontig && !b_kcontig)
-        return dispatch_layout<false, false>(M, N, K, A, lda, B, ldb, bias, accumulate, C, ldc, stream);
-    return dispatch_layout<false, true>(M, N, K, A, lda, B, ldb, bias, accumulate, C, ldc, stream);
+        return dispatch_layout<false, false>(p, M, N, K, A, lda, B, ldb, bias, accumulate, C, ldc,
+                                             ws, stream);
+    return dispatch_layout<false, true>(p, M, N, K, A, lda, B, ldb, bias, accumulate, C, ldc, ws,
+                                        stream);
 }
 
 }  // namespace pcl

@@ -78,6 +78,20 @@ def test_sgemm_bias_accumulate_and_k0():
     del A0, B0
 
 
+@pytest.mark.parametrize("opA,opB", [(N_, N_), (N_, T_), (T_, N_)])
+@pytest.mark.parametrize("M,N,K", [(256, 512, 2048), (256, 512, 512), (100, 200, 1000), (64, 96, 4100)])
+def test_sgemm_split_k_bias_accumulate(opA, opB, M, N, K):
+    # grids of fewer than 256 64x64 tiles split K over workgroups; the partial
+    # products are added in split order, then bias, then the old C
+    A, B = _operands(opA, opB, M, N, K, 3000 + M + K)
+    bias = ob.normal((N,), 3001)
+    C0 = ob.normal((M, N), 3002)
+    announce("sgemm split-K", opA, opB, M, N, K)
+    C = sgemm(opA, opB, A, B, M, N, K, bias=bias, C0=C0)
+    R = ob.gemm_f64(A, B, transA=opA == T_, transB=opB == T_, bias=bias, C0=C0)
+    assert rel(C, R) <= FP32_TOL
+
+
 def test_sgemm_strided_leading_dims():
     # sub-matrix views: lda/ldb/ldc larger than the logical width
     M, N, K = 96, 80, 72
