@@ -56,22 +56,51 @@ __global__ void sgemv_reduce_kernel(const float *__restrict__ part, int splits, 
 }
 
 // ------------------------------------------------------------- sgemv_n ----
-// Block = 64 columns x kchunk rows of W. Thread (c4 = tid%16, rg = tid/16)
-// owns columns 4*c4..4*c4+3 and a contiguous run of kchunk/16 rows.
-template <int MR, bool VEC, bool XONES>
+// Block = CW columns x kchunk rows of W. Thread (c4 = tid%(CW/4),
+// rg = tid/(CW/4)) owns columns 4*c4..4*c4+3 and a contiguous run of
+// kchunk/RG rows (RG = row groups per block). Narrow strips (CW = 16) give
+// enough blocks without splitting K when N is small.
+template <int MR, bool VEC, bool XONES, int CW>
 __global__ __launch_bounds__(GV_THREADS) void sgemv_n_kernel(
     const float *__restrict__ X, long ldx, const float *__restrict__ W, long ldw,
     const float *__restrict__ bias, float *__restrict__ Y, long ldy, int M, int N, int K,
     int kchunk, int splits, float *__restrict__ part, int accumulate) {
-    __shared__ float red[16][MR][64];
+    constexpr int CQ = CW / 4;             // threads across a strip row
+    constexpr int RG = GV_THREADS / CQ;    // row groups
+    __shared__ float red[RG][MR][CW];
     __shared__ float xs[XONES ? 1 : MR][XONES ? 1 : Kch<MR>::SGN];
 
     const int tid = threadIdx.x;
-    const int c4 = tid & 15, rg = tid >> 4;
+    const int c4 = tid % CQ, rg = tid / CQ;
     const int strip = blockIdx.x, sp = blockIdx.y;
-    const int n0 = strip * 64, col = n0 + 4 * c4;
+    const int n0 = strip * CW, col = n0 + 4 * c4;
     const int kb = sp * kchunk;
-    const int run = kchunk / 16;  // multiple of 4
+    const int run = kchunk / RG;  // multiple of 8
+
+    const int r0 = rg * run;
+    // column clamp keeps the vector loads in bounds; clamped lanes only feed
+    // columns >= N, which are never stored. Rows past K are clamped for the
+    // load and skipped in the arithmetic (the host never launches K == 0).
+    const int colc = VEC ? min(col, N - 4) : col;
+    constexpr int UR = 8;  // rows per load batch (run is a multiple of 8)
+    auto load_batch = [&](v4f (&w)[UR], int i) {
+#pragma unroll
+        for (int u = 0; u < UR; u++) {
+            const int k = min(kb + r0 + i + u, K - 1);
+            const float *src = W + (long)k * ldw + colc;
+            if (VEC) {
+                w[u] = *reinterpret_cast<const v4f *>(src);
+            } else {
+                w[u] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    if (col + j < N) w[u][j] = src[j];
+            }
+        }
+    };
+    // the first weight batch is in flight while the activations are staged
+    v4f wn[UR];
+    load_batch(wn, 0);
 
     if (!XONES) {
         for (int i = tid; i < MR * kchunk; i += GV_THREADS) {
@@ -87,26 +116,11 @@ __global__ __launch_bounds__(GV_THREADS) void sgemv_n_kernel(
 #pragma unroll
         for (int j = 0; j < 4; j++) acc[m][j] = 0.f;
 
-    const int r0 = rg * run;
-    // column clamp keeps the vector loads in bounds; clamped lanes only feed
-    // columns >= N, which are never stored
-    const int colc = VEC ? min(col, N - 4) : col;
-    constexpr int UR = 8;  // rows per load batch (run is a multiple of 8)
     for (int i = 0; i < run; i += UR) {
         v4f w[UR];
 #pragma unroll
-        for (int u = 0; u < UR; u++) {
-            const int k = min(kb + r0 + i + u, K - 1);
-            const float *src = W + (long)k * ldw + colc;
-            if (VEC) {
-                w[u] = *reinterpret_cast<const v4f *>(src);
-            } else {
-                w[u] = v4f{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int j = 0; j < 4; j++)
-                    if (col + j < N) w[u][j] = src[j];
-            }
-        }
+        for (int u = 0; u < UR; u++) w[u] = wn[u];
+        if (i + UR < run) load_batch(wn, i + UR);
 #pragma unroll
         for (int u = 0; u < UR; u++) {
             if (kb + r0 + i + u < K) {
@@ -126,12 +140,12 @@ __global__ __launch_bounds__(GV_THREADS) void sgemv_n_kernel(
         for (int j = 0; j < 4; j++) red[rg][m][4 * c4 + j] = acc[m][j];
     __syncthreads();
 
-    const int nround = gridDim.x * 64;
-    for (int o = tid; o < M * 64; o += GV_THREADS) {
-        const int m = o / 64, c = o % 64, n = n0 + c;
+    const int nround = gridDim.x * CW;
+    for (int o = tid; o < M * CW; o += GV_THREADS) {
+        const int m = o / CW, c = o % CW, n = n0 + c;
         float s = 0.f;
-#pragma unroll
-        for (int r = 0; r < 16; r++) s += red[r][m][c];
+#pragma unroll 16
+        for (int r = 0; r < RG; r++) s += red[r][m][c];
         if (splits == 1) {
             if (n < N) {
                 float y = s + (bias ? bias[n] : 0.f);
@@ -162,26 +176,14 @@ __global__ __launch_bounds__(GV_THREADS) void sgemv_t_kernel(
     const int kb = sp * kchunk;
     const int klen = min(kchunk, K - kb);
 
-    for (int i = tid; i < MR * kchunk; i += GV_THREADS) {
-        int m = i / kchunk, kk = i % kchunk;
-        xs[m][kk] = (m < M && kk < klen) ? X[(long)m * ldx + kb + kk] : 0.f;
-    }
-    __syncthreads();
-
-    float acc[SGT_RPL][MR];
-#pragma unroll
-    for (int r = 0; r < SGT_RPL; r++)
-#pragma unroll
-        for (int m = 0; m < MR; m++) acc[r][m] = 0.f;
-
     // rows past N are clamped (their sums are never stored); k past klen is
-    // clamped for the load and skipped in the arithmetic
+    // clamped for the load and skipped in the arithmetic (klen >= 1: the
+    // host never launches K == 0)
     const float *wrow[SGT_RPL];
 #pragma unroll
     for (int r = 0; r < SGT_RPL; r++) wrow[r] = W + (long)min(n0 + rs + 16 * r, N - 1) * ldw + kb;
     constexpr int UK = 4;  // 64-element k steps per load batch
-    for (int k0 = 4 * j; k0 < klen; k0 += 64 * UK) {
-        v4f w[UK][SGT_RPL];
+    auto load_batch = [&](v4f (&w)[UK][SGT_RPL], int k0) {
 #pragma unroll
         for (int u = 0; u < UK; u++)
 #pragma unroll
@@ -196,6 +198,30 @@ __global__ __launch_bounds__(GV_THREADS) void sgemv_t_kernel(
                         if (k + e < klen) w[u][r][e] = wrow[r][k + e];
                 }
             }
+    };
+    // the first weight batch is in flight while the activations are staged
+    v4f wn[UK][SGT_RPL];
+    load_batch(wn, 4 * j);
+
+    for (int i = tid; i < MR * kchunk; i += GV_THREADS) {
+        int m = i / kchunk, kk = i % kchunk;
+        xs[m][kk] = (m < M && kk < klen) ? X[(long)m * ldx + kb + kk] : 0.f;
+    }
+    __syncthreads();
+
+    float acc[SGT_RPL][MR];
+#pragma unroll
+    for (int r = 0; r < SGT_RPL; r++)
+#pragma unroll
+        for (int m = 0; m < MR; m++) acc[r][m] = 0.f;
+
+    for (int k0 = 4 * j; k0 < klen; k0 += 64 * UK) {
+        v4f w[UK][SGT_RPL];
+#pragma unroll
+        for (int u = 0; u < UK; u++)
+#pragma unroll
+            for (int r = 0; r < SGT_RPL; r++) w[u][r] = wn[u][r];
+        if (k0 + 64 * UK < klen) load_batch(wn, k0 + 64 * UK);
 #pragma unroll
         for (int u = 0; u < UK; u++) {
             const int k = k0 + 64 * u;
@@ -303,6 +329,24 @@ __global__ __launch_bounds__(GV_THREADS) void igemv_kernel(
     const int kend = min(kb + kchunk, (K + 15) & ~15);
     const int klen = kend - kb;
 
+    // rows past N are clamped (never stored); k past klen is clamped for the
+    // load and skipped in the arithmetic (klen >= 16: the host never launches
+    // K == 0)
+    const int8_t *brow[SGT_RPL];
+#pragma unroll
+    for (int r = 0; r < SGT_RPL; r++) brow[r] = B + (long)min(n0 + rs + 16 * r, N - 1) * ldb + kb;
+    constexpr int UK = 4;  // 256-byte k steps per load batch
+    auto load_batch = [&](v4i (&w)[UK][SGT_RPL], int k0) {
+#pragma unroll
+        for (int u = 0; u < UK; u++)
+#pragma unroll
+            for (int r = 0; r < SGT_RPL; r++)
+                w[u][r] = *reinterpret_cast<const v4i *>(brow[r] + min(k0 + 256 * u, klen - 16));
+    };
+    // the first weight batch is in flight while the activations are staged
+    v4i wn[UK][SGT_RPL];
+    load_batch(wn, 16 * j);
+
     for (int i = tid; i < MR * kchunk; i += GV_THREADS) {
         int m = i / kchunk, kk = i % kchunk;
         int8_t v = 0;
@@ -317,17 +361,13 @@ __global__ __launch_bounds__(GV_THREADS) void igemv_kernel(
 #pragma unroll
         for (int m = 0; m < MR; m++) acc[r][m] = 0;
 
-    const int8_t *brow[SGT_RPL];
-#pragma unroll
-    for (int r = 0; r < SGT_RPL; r++) brow[r] = B + (long)min(n0 + rs + 16 * r, N - 1) * ldb + kb;
-    constexpr int UK = 4;  // 256-byte k steps per load batch
     for (int k0 = 16 * j; k0 < klen; k0 += 256 * UK) {
         v4i w[UK][SGT_RPL];
 #pragma unroll
         for (int u = 0; u < UK; u++)
 #pragma unroll
-            for (int r = 0; r < SGT_RPL; r++)
-                w[u][r] = *reinterpret_cast<const v4i *>(brow[r] + min(k0 + 256 * u, klen - 16));
+            for (int r = 0; r < SGT_RPL; r++) w[u][r] = wn[u][r];
+        if (k0 + 256 * UK < klen) load_batch(wn, k0 + 256 * UK);
 #pragma unroll
         for (int u = 0; u < UK; u++) {
             const int k = k0 + 256 * u;
@@ -383,16 +423,17 @@ __global__ __launch_bounds__(GV_THREADS) void igemv_kernel(
 // ------------------------------------------------------------- planning ----
 static int mr_of(int M) { return M <= 1 ? 1 : (M <= 2 ? 2 : (M <= 4 ? 4 : 8)); }
 
-// strips: blocks along N; kstep: K granularity of a split; kmin: least K per
-// block worth a block; kmax: most K a block can stage.
-static GemvPlan make_plan(int strips, int M, int K, int kstep, int kmin, int kmax,
+// strips: blocks along N; want: blocks wanted in all; kstep: K granularity
+// of a split; kmin: least K per split worth a second kernel; kmax: most K a
+// block can stage.
+static GemvPlan make_plan(int strips, int want, int M, int K, int kstep, int kmin, int kmax,
                           int rows_per_strip) {
     GemvPlan p;
     p.strips = strips;
-    int want = GV_TARGET_BLOCKS / (strips > 0 ? strips : 1);
-    int splits = want < 1 ? 1 : want;
+    int splits = cdiv(want, strips > 0 ? strips : 1);
     int most = cdiv(K, kmin);
     if (splits > most) splits = most;
+    if (splits < cdiv(K, kmax)) splits = cdiv(K, kmax);  // staging limit
     if (splits < 1) splits = 1;
     int kchunk = cdiv(cdiv(K, splits), kstep) * kstep;
     if (kchunk > kmax) kchunk = kmax;
@@ -401,17 +442,32 @@ static GemvPlan make_plan(int strips, int M, int K, int kstep, int kmin, int kma
     p.splits = splits;
     p.kchunk = kchunk;
     p.part_bytes = splits > 1 ? (size_t)splits * M * strips * rows_per_strip * 4 : 0;
+    p.cw = rows_per_strip;
     return p;
 }
 
+// A GEMV launch costs ~3 us before any weight arrives, so a second (reduce)
+// kernel only pays when a single pass would leave each thread several
+// dependent load batches on a small grid. Weights of K x N (N-contiguous)
+// take 16-column strips and stay unsplit up to K = 1024 (two 8-row batches
+// per thread); deeper K splits into 512-row chunks (one batch each) until the
+// grid has ~1024 blocks. Weights of N x K (K-contiguous rows: the tied head,
+// INT8 packed rows) split only when the grid has under 256 blocks and a split
+// still covers 1024 floats or 2048 bytes. bias_bwd (a K-deep column sum)
+// keeps 64-column strips.
 GemvPlan plan_sgemv(int w_trans, int M, int N, int K) {
     const int mr = mr_of(M);
-    if (w_trans) return make_plan(cdiv(N, SGT_ROWS), M, K, 64, 256, 8192 / mr, SGT_ROWS);
-    return make_plan(cdiv(N, 64), M, K, 128, 128, 4096 / mr, 64);
+    if (w_trans) return make_plan(cdiv(N, SGT_ROWS), 256, M, K, 64, 1024, 8192 / mr, SGT_ROWS);
+    if (K <= 1024 && K <= 4096 / mr) return make_plan(cdiv(N, 16), 1, M, K, 512, 1 << 30, 4096 / mr, 16);
+    return make_plan(cdiv(N, 16), GV_TARGET_BLOCKS, M, K, 512, 512, 4096 / mr, 16);
+}
+
+GemvPlan plan_bias_bwd(int N, int M) {
+    return make_plan(cdiv(N, 64), GV_TARGET_BLOCKS, 1, M, 128, 128, 4096, 64);
 }
 
 GemvPlan plan_igemv(int M, int N, int K) {
-    return make_plan(cdiv(N, SGT_ROWS), M, K, 256, 1024, 16384 / mr_of(M), SGT_ROWS);
+    return make_plan(cdiv(N, SGT_ROWS), 256, M, K, 256, 2048, 16384 / mr_of(M), SGT_ROWS);
 }
 
 static bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -434,21 +490,28 @@ static void launch_sgemv_mr(const GemvPlan &p, int w_trans, bool vec, bool x_one
                                Y, ldy, M, N, K, p.kchunk, p.splits, part, accumulate);
     } else if (x_ones) {
         if (vec)
-            hipLaunchKernelGGL((sgemv_n_kernel<1, true, true>), grid, block, 0, s, X, ldx, W, ldw,
-                               bias, Y, ldy, M, N, K, p.kchunk, p.splits, part, accumulate);
+            hipLaunchKernelGGL((sgemv_n_kernel<1, true, true, 64>), grid, block, 0, s, X, ldx, W,
+                               ldw, bias, Y, ldy, M, N, K, p.kchunk, p.splits, part, accumulate);
         else
-            hipLaunchKernelGGL((sgemv_n_kernel<1, false, true>), grid, block, 0, s, X, ldx, W, ldw,
-                               bias, Y, ldy, M, N, K, p.kchunk, p.splits, part, accumulate);
+            hipLaunchKernelGGL((sgemv_n_kernel<1, false, true, 64>), grid, block, 0, s, X, ldx, W,
+                               ldw, bias, Y, ldy, M, N, K, p.kchunk, p.splits, part, accumulate);
+    } else if (p.cw == 16) {
+        if (vec)
+            hipLaunchKernelGGL((sgemv_n_kernel<MR, true, false, 16>), grid, block, 0, s, X, ldx, W,
+                               ldw, bias, Y, ldy, M, N, K, p.kchunk, p.splits, part, accumulate);
+        else
+            hipLaunchKernelGGL((sgemv_n_kernel<MR, false, false, 16>), grid, block, 0, s, X, ldx,
+                               W, ldw, bias, Y, ldy, M, N, K, p.kchunk, p.splits, part, accumulate);
     } else {
         if (vec)
-            hipLaunchKernelGGL((sgemv_n_kernel<MR, true, false>), grid, block, 0, s, X, ldx, W, ldw,
-                               bias, Y, ldy, M, N, K, p.kchunk, p.splits, part, accumulate);
-        else
-            hipLaunchKernelGGL((sgemv_n_kernel<MR, false, false>), grid, block, 0, s, X, ldx, W,
+            hipLaunchKernelGGL((sgemv_n_kernel<MR, true, false, 64>), grid, block, 0, s, X, ldx, W,
                                ldw, bias, Y, ldy, M, N, K, p.kchunk, p.splits, part, accumulate);
+        else
+            hipLaunchKernelGGL((sgemv_n_kernel<MR, false, false, 64>), grid, block, 0, s, X, ldx,
+                               W, ldw, bias, Y, ldy, M, N, K, p.kchunk, p.splits, part, accumulate);
     }
     if (p.splits > 1) {
-        const int nround = p.strips * (w_trans ? SGT_ROWS : 64);
+        const int nround = p.strips * (w_trans ? SGT_ROWS : p.cw);
         hipLaunchKernelGGL(sgemv_reduce_kernel, dim3(reduce_grid(M, N)), dim3(256), 0, s, part,
                            p.splits, M, N, nround, bias, Y, ldy, accumulate);
     }
@@ -459,6 +522,12 @@ hipError_t launch_sgemv(const GemvPlan &p, int w_trans, int M, int N, int K, con
                         int accumulate, float *Y, long ldy, const Workspace &ws,
                         hipStream_t stream) {
     if (M <= 0 || N <= 0) return hipSuccess;
+    if (K <= 0) {  // Y = (accumulate ? Y : 0) + bias: the reduce pass over zero splits
+        hipLaunchKernelGGL(sgemv_reduce_kernel, dim3(reduce_grid(M, N)), dim3(256), 0, stream,
+                           nullptr, 0, M, N, N, bias, Y, ldy, accumulate);
+        return hipGetLastError();
+    }
+    if (p.splits > 1 && (ws.buf == nullptr || ws.bytes_cap < p.part_bytes)) return hipErrorInvalidValue;
     bool vec = aligned16(W) && ldw % 4 == 0 && (w_trans ? K % 4 == 0 : N % 4 == 0);
     if (x_ones) {
         launch_sgemv_mr<1>(p, w_trans, vec, true, M, N, K, X, ldx, W, ldw, bias, accumulate, Y,
@@ -514,6 +583,20 @@ hipError_t launch_igemv(const GemvPlan &p, int out_mode, int M, int N, int K, co
                         const float *sa, const float *sb, void *Y, long ldy, const Workspace &ws,
                         hipStream_t stream) {
     if (M <= 0 || N <= 0) return hipSuccess;
+    if (K <= 0) {  // v = 0: the reduce pass over zero splits applies the epilogue
+        const dim3 rg(reduce_grid(M, N)), rb(256);
+        if (out_mode == 0)
+            hipLaunchKernelGGL((igemv_reduce_kernel<0>), rg, rb, 0, stream, nullptr, 0, M, N, N,
+                               col_off, sa, sb, Y, ldy);
+        else if (out_mode == 1)
+            hipLaunchKernelGGL((igemv_reduce_kernel<1>), rg, rb, 0, stream, nullptr, 0, M, N, N,
+                               col_off, sa, sb, Y, ldy);
+        else
+            hipLaunchKernelGGL((igemv_reduce_kernel<2>), rg, rb, 0, stream, nullptr, 0, M, N, N,
+                               col_off, sa, sb, Y, ldy);
+        return hipGetLastError();
+    }
+    if (p.splits > 1 && (ws.buf == nullptr || ws.bytes_cap < p.part_bytes)) return hipErrorInvalidValue;
     if (M == 1)
         launch_igemv_mr<1>(p, out_mode, M, N, K, X, ldx, Bpk, ldb, col_off, sa, sb, Y, ldy, ws, stream);
     else if (M <= 2)

@@ -22,6 +22,7 @@ struct GemvPlan {
     int splits;      // blocks along K
     int kchunk;      // K rows per split (multiple of the kernel's K step)
     size_t part_bytes;  // workspace bytes for partials (0 when splits == 1)
+    int cw = 64;     // columns per strip (sgemv over K x N weights: 64 or 16)
 };
 
 // ---- FP32 GEMM (sgemm.hip) ----
@@ -57,6 +58,8 @@ hipError_t launch_pad_a_u8(const uint8_t *A, long lda, int M, int K, uint8_t *ds
 
 // ---- GEMV (gemv.hip) ----
 GemvPlan plan_sgemv(int w_trans, int M, int N, int K);
+// Column sums of a K x N matrix (bias_bwd): plan for launch_sgemv with x_ones.
+GemvPlan plan_bias_bwd(int N, int K);
 GemvPlan plan_igemv(int M, int N, int K);
 // Y(M,N) = (accumulate ? Y : 0) + X(M,K) . op(W) + bias; M <= 8.
 // x_ones: X is the all-ones row (bias_bwd), X/ldx unused and M must be 1.

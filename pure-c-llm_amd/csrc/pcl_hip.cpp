@@ -448,7 +448,7 @@ int pcl_bias_bwd(float *db, const float *dY, int M, int N, int ld, void *stream)
     }
     PCL_OK_OR_RETURN(do_init());
     hipStream_t s = pick(stream);
-    pcl::GemvPlan p = pcl::plan_sgemv(0, 1, N, M);
+    pcl::GemvPlan p = pcl::plan_bias_bwd(N, M);
     StreamScratch *sc;
     PCL_OK_OR_RETURN(get_scratch(s, p.part_bytes, 0, &sc));
     HIP_OK(pcl::launch_sgemv(p, 0, 1, N, M, nullptr, 0, true, dY, ld, nullptr, 1, db, N, sc->ws, s));

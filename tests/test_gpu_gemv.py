@@ -2,8 +2,8 @@
 
 FP32 against the reference-order restatement of matvec/proj_token
 (generate.c:95-107, transformer.c:174-195) and the f64 truth, <= 1e-4; the
-split-K last-block reduction is exercised by long-K shapes and must give
-identical bits on repeated calls (arrival counters reset correctly).
+split-K path (partial sums, then an ordered reduction kernel) is exercised by
+long-K shapes and must give identical bits on repeated calls.
 """
 import numpy as np
 import pytest
@@ -77,6 +77,27 @@ def test_sgemv_accumulate_and_determinism():
     assert rel(outs[0], ob.gemm_f64(X, W, bias=b, C0=Y0)) <= FP32_TOL
     for o in outs[1:]:
         np.testing.assert_array_equal(o, outs[0])
+
+
+@pytest.mark.parametrize("opW", [pcl.OP_N, pcl.OP_T])
+def test_sgemv_k0(opW):
+    # K == 0 reads no operand (NULL X and W): Y = Y0 + bias
+    M, N = 3, 50
+    b = ob.normal((N,), 60)
+    Y0 = ob.normal((M, N), 61)
+    db, dY = pcl.dev(b), pcl.dev(Y0)
+    announce("sgemv K=0", opW)
+    pcl.check(pcl.lib.pcl_sgemv(opW, M, N, 0, None, 1, None, N, db.ptr, 1, dY.ptr, N, None))
+    pcl.sync()
+    np.testing.assert_array_equal(dY.download((M, N), np.float32), Y0 + b)
+    dY2 = pcl.dev(Y0)
+    pcl.check(pcl.lib.pcl_sgemv(opW, M, N, 0, None, 1, None, N, None, 0, dY2.ptr, N, None))
+    pcl.sync()
+    np.testing.assert_array_equal(dY2.download((M, N), np.float32), np.zeros((M, N), np.float32))
+    ddb = pcl.dev(b)
+    pcl.check(pcl.lib.pcl_bias_bwd(ddb.ptr, None, 0, N, N, None))  # sum over no rows
+    pcl.sync()
+    np.testing.assert_array_equal(ddb.download((N,), np.float32), b)
 
 
 def test_sgemm_routes_small_m_to_gemv():

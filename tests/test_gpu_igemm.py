@@ -129,6 +129,29 @@ def test_igemm_dequant_bit_exact(M, N, K):
     np.testing.assert_array_equal(C[rows], ob.dequant((V + off).astype(np.int32), None, sb))
 
 
+@pytest.mark.parametrize("M", [3, 40])
+def test_int8_k0(M):
+    # K == 0 reads no activation (NULL A): v = 0, so C = float(col_off) * dq
+    N = 70
+    sa = ob.uniform((M,), 45, 1e-3, 1e-2)
+    sb = ob.uniform((N,), 46, 1e-3, 1e-2)
+    off = ob.s8((N,), 47).astype(np.int32) * 1000
+    dBp = pcl.DeviceBuffer(256)  # no packed bytes at K = 0
+    dsa, dsb, doff = pcl.dev(sa), pcl.dev(sb), pcl.dev(off)
+    dC = pcl.empty((M, N), np.float32)
+    announce("int8 K=0", M)
+    fn = pcl.lib.pcl_gemv_u8s8_dq if M <= 8 else pcl.lib.pcl_gemm_u8s8_dq
+    pcl.check(fn(None, 0, dBp.ptr, doff.ptr, dsa.ptr, dsb.ptr, dC.ptr, N, M, N, 0, None))
+    pcl.sync()
+    want = ob.dequant(np.broadcast_to(off, (M, N)).astype(np.int32), sa, sb)
+    np.testing.assert_array_equal(dC.download((M, N), np.float32), want)
+    dI = pcl.empty((M, N), np.int32)
+    fn = pcl.lib.pcl_gemv_u8s8_i32 if M <= 8 else pcl.lib.pcl_gemm_u8s8_i32
+    pcl.check(fn(None, 0, dBp.ptr, dI.ptr, N, M, N, 0, None))
+    pcl.sync()
+    np.testing.assert_array_equal(dI.download((M, N), np.int32), np.zeros((M, N), np.int32))
+
+
 @pytest.mark.parametrize("M,N,K", [(2048, 2048, 2048), (4096, 3072, 1024), (4096, 1024, 4096),
                                    (4096, 50257, 1024)])
 def test_igemm_full_size_checksums(M, N, K):
