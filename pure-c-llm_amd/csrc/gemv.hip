@@ -40,6 +40,33 @@ constexpr int SGT_ROWS = 16 * SGT_RPL;   // rows of W per block
 
 static int cdiv(long a, long b) { return (int)((a + b - 1) / b); }
 
+// Stage MR activation rows of kchunk elements into LDS (row stride ld):
+// each thread issues up to 16 independent loads (columns tid + 256 j of every
+// row) before it writes any of them, so the staging costs one memory latency
+// rather than one per element. get(m, kk) returns the bounds-checked element.
+template <int MR, typename T, typename Get>
+__device__ __forceinline__ void stage_rows(T *xs, int ld, int kchunk, Get get) {
+    constexpr int JU = MR >= 16 ? 1 : 16 / MR;  // columns per row per round
+    const int tid = (int)threadIdx.x;
+    for (int j0 = 0; j0 * GV_THREADS < kchunk; j0 += JU) {
+        T v[MR][JU];
+#pragma unroll
+        for (int m = 0; m < MR; m++)
+#pragma unroll
+            for (int ju = 0; ju < JU; ju++) {
+                const int kk = tid + (j0 + ju) * GV_THREADS;
+                v[m][ju] = kk < kchunk ? get(m, kk) : T(0);
+            }
+#pragma unroll
+        for (int m = 0; m < MR; m++)
+#pragma unroll
+            for (int ju = 0; ju < JU; ju++) {
+                const int kk = tid + (j0 + ju) * GV_THREADS;
+                if (kk < kchunk) xs[m * ld + kk] = v[m][ju];
+            }
+    }
+}
+
 // Second pass of a split-K GEMV: Y[m,n] = sum over splits in order (+ bias,
 // + Y when accumulating). part is [splits][M][nround].
 __global__ void sgemv_reduce_kernel(const float *__restrict__ part, int splits, int M, int N,
@@ -103,10 +130,9 @@ __global__ __launch_bounds__(GV_THREADS) void sgemv_n_kernel(
     load_batch(wn, 0);
 
     if (!XONES) {
-        for (int i = tid; i < MR * kchunk; i += GV_THREADS) {
-            int m = i / kchunk, kk = i % kchunk;
-            xs[m][kk] = (m < M && kb + kk < K) ? X[(long)m * ldx + kb + kk] : 0.f;
-        }
+        stage_rows<MR>(&xs[0][0], Kch<MR>::SGN, kchunk, [&](int m, int kk) {
+            return (m < M && kb + kk < K) ? X[(long)m * ldx + kb + kk] : 0.f;
+        });
         __syncthreads();
     }
 
@@ -203,10 +229,9 @@ __global__ __launch_bounds__(GV_THREADS) void sgemv_t_kernel(
     v4f wn[UK][SGT_RPL];
     load_batch(wn, 4 * j);
 
-    for (int i = tid; i < MR * kchunk; i += GV_THREADS) {
-        int m = i / kchunk, kk = i % kchunk;
-        xs[m][kk] = (m < M && kk < klen) ? X[(long)m * ldx + kb + kk] : 0.f;
-    }
+    stage_rows<MR>(&xs[0][0], Kch<MR>::SGT, kchunk, [&](int m, int kk) {
+        return (m < M && kk < klen) ? X[(long)m * ldx + kb + kk] : 0.f;
+    });
     __syncthreads();
 
     float acc[SGT_RPL][MR];
@@ -347,12 +372,9 @@ __global__ __launch_bounds__(GV_THREADS) void igemv_kernel(
     v4i wn[UK][SGT_RPL];
     load_batch(wn, 16 * j);
 
-    for (int i = tid; i < MR * kchunk; i += GV_THREADS) {
-        int m = i / kchunk, kk = i % kchunk;
-        int8_t v = 0;
-        if (m < M && kb + kk < K) v = (int8_t)(X[(long)m * ldx + kb + kk] ^ 0x80);
-        xs[m][kk] = v;
-    }
+    stage_rows<MR>(&xs[0][0], Kch<MR>::IGV, kchunk, [&](int m, int kk) {
+        return (m < M && kb + kk < K) ? (int8_t)(X[(long)m * ldx + kb + kk] ^ 0x80) : (int8_t)0;
+    });
     __syncthreads();
 
     int32_t acc[SGT_RPL][MR];
