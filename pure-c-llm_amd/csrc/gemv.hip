@@ -40,30 +40,76 @@ constexpr int SGT_ROWS = 16 * SGT_RPL;   // rows of W per block
 
 static int cdiv(long a, long b) { return (int)((a + b - 1) / b); }
 
-// Stage MR activation rows of kchunk elements into LDS (row stride ld):
-// each thread issues up to 16 independent loads (columns tid + 256 j of every
-// row) before it writes any of them, so the staging costs one memory latency
-// rather than one per element. get(m, kk) returns the bounds-checked element.
-template <int MR, typename T, typename Get>
-__device__ __forceinline__ void stage_rows(T *xs, int ld, int kchunk, Get get) {
-    constexpr int JU = MR >= 16 ? 1 : 16 / MR;  // columns per row per round
+// Stage MR activation rows of one split (elements [0, kchunk) of row m start
+// at X0 + m*ldx; elements at or past kvalid, and rows m >= M, stage as zero)
+// into LDS rows of stride ld. Each thread issues up to 16 independent loads
+// before it writes any of them, so the staging costs one memory latency
+// rather than one per element. With 16-byte aligned rows the loads are
+// 16-byte vectors (the chunk that straddles kvalid is assembled element by
+// element); otherwise single elements. RECENTRE: u8 activations are stored
+// as x ^ 0x80 (= x - 128 as s8), padding stays 0.
+template <int MR, bool RECENTRE, typename T>
+__device__ __forceinline__ void stage_rows(T *xs, int ld, int kchunk, int kvalid, int M,
+                                           const T *X0, long ldx) {
+    typedef T vec_t __attribute__((ext_vector_type(16 / sizeof(T))));
+    constexpr int V = 16 / sizeof(T);
     const int tid = (int)threadIdx.x;
-    for (int j0 = 0; j0 * GV_THREADS < kchunk; j0 += JU) {
-        T v[MR][JU];
+    auto fix = [](T x) -> T {
+        if constexpr (RECENTRE) return (T)(x ^ (T)0x80);
+        else return x;
+    };
+    const bool vec = ((reinterpret_cast<uintptr_t>(X0) | (uintptr_t)(ldx * sizeof(T))) & 15) == 0;
+    if (vec) {
+        constexpr int JU = MR >= 16 ? 1 : 16 / MR;  // vector loads per row per round
+        const int nch = kchunk / V;                  // kchunk is a multiple of 64 elements
+        for (int c0 = 0; c0 * GV_THREADS < nch; c0 += JU) {
+            vec_t v[MR][JU];
 #pragma unroll
-        for (int m = 0; m < MR; m++)
+            for (int m = 0; m < MR; m++)
 #pragma unroll
-            for (int ju = 0; ju < JU; ju++) {
-                const int kk = tid + (j0 + ju) * GV_THREADS;
-                v[m][ju] = kk < kchunk ? get(m, kk) : T(0);
-            }
+                for (int ju = 0; ju < JU; ju++) {
+                    const int kk = (tid + (c0 + ju) * GV_THREADS) * V;
+                    vec_t x = (T)0;
+                    if (m < M && kk < kchunk) {
+                        const T *src = X0 + (long)m * ldx + kk;
+                        if (kk + V <= kvalid) {
+                            x = *reinterpret_cast<const vec_t *>(src);
+                            if constexpr (RECENTRE) x ^= (T)0x80;
+                        } else {
 #pragma unroll
-        for (int m = 0; m < MR; m++)
+                            for (int e = 0; e < V; e++)
+                                if (kk + e < kvalid) x[e] = fix(src[e]);
+                        }
+                    }
+                    v[m][ju] = x;
+                }
 #pragma unroll
-            for (int ju = 0; ju < JU; ju++) {
-                const int kk = tid + (j0 + ju) * GV_THREADS;
-                if (kk < kchunk) xs[m * ld + kk] = v[m][ju];
-            }
+            for (int m = 0; m < MR; m++)
+#pragma unroll
+                for (int ju = 0; ju < JU; ju++) {
+                    const int kk = (tid + (c0 + ju) * GV_THREADS) * V;
+                    if (kk < kchunk) *reinterpret_cast<vec_t *>(xs + m * ld + kk) = v[m][ju];
+                }
+        }
+    } else {
+        constexpr int JU = MR >= 16 ? 1 : 16 / MR;  // element loads per row per round
+        for (int j0 = 0; j0 * GV_THREADS < kchunk; j0 += JU) {
+            T v[MR][JU];
+#pragma unroll
+            for (int m = 0; m < MR; m++)
+#pragma unroll
+                for (int ju = 0; ju < JU; ju++) {
+                    const int kk = tid + (j0 + ju) * GV_THREADS;
+                    v[m][ju] = (m < M && kk < kvalid) ? fix(X0[(long)m * ldx + kk]) : (T)0;
+                }
+#pragma unroll
+            for (int m = 0; m < MR; m++)
+#pragma unroll
+                for (int ju = 0; ju < JU; ju++) {
+                    const int kk = tid + (j0 + ju) * GV_THREADS;
+                    if (kk < kchunk) xs[m * ld + kk] = v[m][ju];
+                }
+        }
     }
 }
 
@@ -95,7 +141,7 @@ __global__ __launch_bounds__(GV_THREADS) void sgemv_n_kernel(
     constexpr int CQ = CW / 4;             // threads across a strip row
     constexpr int RG = GV_THREADS / CQ;    // row groups
     __shared__ float red[RG][MR][CW];
-    __shared__ float xs[XONES ? 1 : MR][XONES ? 1 : Kch<MR>::SGN];
+    __shared__ __attribute__((aligned(16))) float xs[XONES ? 1 : MR][XONES ? 1 : Kch<MR>::SGN];
 
     const int tid = threadIdx.x;
     const int c4 = tid % CQ, rg = tid / CQ;
@@ -130,9 +176,8 @@ __global__ __launch_bounds__(GV_THREADS) void sgemv_n_kernel(
     load_batch(wn, 0);
 
     if (!XONES) {
-        stage_rows<MR>(&xs[0][0], Kch<MR>::SGN, kchunk, [&](int m, int kk) {
-            return (m < M && kb + kk < K) ? X[(long)m * ldx + kb + kk] : 0.f;
-        });
+        stage_rows<MR, false>(&xs[0][0], Kch<MR>::SGN, kchunk, min(kchunk, K - kb), M, X + kb,
+                              ldx);
         __syncthreads();
     }
 
@@ -229,9 +274,7 @@ __global__ __launch_bounds__(GV_THREADS) void sgemv_t_kernel(
     v4f wn[UK][SGT_RPL];
     load_batch(wn, 4 * j);
 
-    stage_rows<MR>(&xs[0][0], Kch<MR>::SGT, kchunk, [&](int m, int kk) {
-        return (m < M && kk < klen) ? X[(long)m * ldx + kb + kk] : 0.f;
-    });
+    stage_rows<MR, false>(&xs[0][0], Kch<MR>::SGT, kchunk, klen, M, X + kb, ldx);
     __syncthreads();
 
     float acc[SGT_RPL][MR];
@@ -372,9 +415,8 @@ __global__ __launch_bounds__(GV_THREADS) void igemv_kernel(
     v4i wn[UK][SGT_RPL];
     load_batch(wn, 16 * j);
 
-    stage_rows<MR>(&xs[0][0], Kch<MR>::IGV, kchunk, [&](int m, int kk) {
-        return (m < M && kb + kk < K) ? (int8_t)(X[(long)m * ldx + kb + kk] ^ 0x80) : (int8_t)0;
-    });
+    stage_rows<MR, true>(reinterpret_cast<uint8_t *>(&xs[0][0]), Kch<MR>::IGV, kchunk,
+                         min(kchunk, K - kb), M, X + kb, ldx);
     __syncthreads();
 
     int32_t acc[SGT_RPL][MR];

@@ -80,6 +80,23 @@ def test_sgemv_accumulate_and_determinism():
 
 
 @pytest.mark.parametrize("opW", [pcl.OP_N, pcl.OP_T])
+@pytest.mark.parametrize("M,K,ldx", [(3, 130, 136), (8, 2050, 2052), (5, 61, 64)])
+def test_sgemv_padded_rows(opW, M, K, ldx):
+    # 16-byte aligned activation rows whose K is not a multiple of 4: the
+    # staging's vector loads stop at K and assemble the last chunk by element
+    N = 70
+    Xp = ob.normal((M, ldx), 70 + K)
+    X = np.ascontiguousarray(Xp[:, :K])
+    W = ob.normal((K, N) if opW == pcl.OP_N else (N, K), 71, 0.0, 0.02)
+    dX, dW, dY = pcl.dev(Xp), pcl.dev(W), pcl.empty((M, N), np.float32)
+    announce("sgemv padded rows", opW, M, K, ldx)
+    pcl.check(pcl.lib.pcl_sgemv(opW, M, N, K, dX.ptr, ldx, dW.ptr, W.shape[1], None, 0, dY.ptr, N, None))
+    pcl.sync()
+    R = ob.gemm_f64(X, W, transB=opW == pcl.OP_T)
+    assert rel(dY.download((M, N), np.float32), R) <= FP32_TOL
+
+
+@pytest.mark.parametrize("opW", [pcl.OP_N, pcl.OP_T])
 def test_sgemv_k0(opW):
     # K == 0 reads no operand (NULL X and W): Y = Y0 + bias
     M, N = 3, 50

@@ -93,6 +93,21 @@ def test_igemv_i32_exact(M):
         np.testing.assert_array_equal(igemm_i32(Au, Bq, gemv=True), ob.gemm_u8s8_i32(Au, Bq))
 
 
+@pytest.mark.parametrize("M,K,ldx", [(3, 130, 144), (8, 2050, 2064), (5, 61, 64)])
+def test_igemv_padded_rows(M, K, ldx):
+    # 16-byte aligned activation rows whose K is not a multiple of 16: the
+    # staging's vector loads stop at K (re-centred bytes past K stay zero)
+    N = 100
+    Ap = ob.u8((M, ldx), 35 + K)
+    Bq = ob.s8((K, N), 36)
+    dBp, _ = pack(Bq)
+    dA, dC = pcl.dev(Ap), pcl.empty((M, N), np.int32)
+    announce("igemv padded rows", M, K, ldx)
+    pcl.check(pcl.lib.pcl_gemv_u8s8_i32(dA.ptr, ldx, dBp.ptr, dC.ptr, N, M, N, K, None))
+    pcl.sync()
+    np.testing.assert_array_equal(dC.download((M, N), np.int32), exact(Ap[:, :K], Bq).astype(np.int32))
+
+
 def _dq_run(Au, Bq, sa, sb, col_off=None):
     M, K = Au.shape
     N = Bq.shape[1]
