@@ -125,12 +125,14 @@ __global__ __launch_bounds__(256 * KG) void sgemm_mfma_kernel(
     constexpr int KCH = BK / 8;                  // 8-deep k chunks per tile
     constexpr int KCG = KCH / KG;                // chunks per K group
     static_assert(BK % 8 == 0 && KCH % KG == 0, "K tile must split over the K groups");
-    static_assert(KG == 1 || KG == 2, "one or two K groups");
+    static_assert(KG == 1 || KG == 2 || KG == 4, "one, two or four K groups");
     static_assert(PF >= 1, "at least one tile in flight");
 
     // two buffers, each [A tile | B tile]; the K groups' exchange reuses them
     constexpr int BUF = TA::SIZE + TB::SIZE;
-    constexpr int XCH = KG > 1 ? 2 * 256 * TM * TN * 8 : 0;
+    constexpr int VH = 16 / KG;  // accumulator registers finished per group
+    // exchange inboxes: [owner group][KG - 1 senders][4 waves][TM][TN][VH][64 lanes]
+    constexpr int XCH = KG > 1 ? KG * (KG - 1) * 256 * TM * TN * VH : 0;
     constexpr int LDS_FLOATS = 2 * BUF > XCH ? 2 * BUF : XCH;
     __shared__ __attribute__((aligned(16))) float lds[LDS_FLOATS];
 
@@ -211,28 +213,38 @@ __global__ __launch_bounds__(256 * KG) void sgemm_mfma_kernel(
         });
     }
 
-    // K groups: group g hands the registers it does not finish to its partner
-    // (lane-contiguous, conflict-free), then adds the partner's share of its
-    // own registers. The last loop barrier has retired every tile read.
-    constexpr int VH = 16 / KG;  // accumulator registers finished per group
+    // K groups: group g finishes accumulator registers v in [g*VH, (g+1)*VH).
+    // Every group posts the registers it does not finish to their owner's
+    // inbox (lane-contiguous, conflict-free), then adds its senders' shares to
+    // its own registers in sender order. Register indices stay compile-time
+    // (a runtime index would move the accumulators out of registers). The last
+    // loop barrier has retired every tile read.
     if constexpr (KG > 1) {
-        float *xg = lds + (1 - kg) * (XCH / 2);  // the partner's inbox
-        float *xm = lds + kg * (XCH / 2);
+        auto slot = [&](int owner, int sender, int i, int j, int u) {
+            const int s = sender < owner ? sender : sender - 1;
+            return (((((owner * (KG - 1) + s) * 4 + wq) * TM + i) * TN + j) * VH + u) * 64 + lane;
+        };
 #pragma unroll
         for (int i = 0; i < TM; i++)
 #pragma unroll
             for (int j = 0; j < TN; j++)
-#pragma unroll
-                for (int v = 0; v < VH; v++)
-                    xg[(((wq * TM + i) * TN + j) * VH + v) * 64 + lane] = acc[i][j][(1 - kg) * VH + v];
+                static_for<0, 16>([&](auto V) {
+                    constexpr int v = V.value, owner = v / VH;
+                    if (owner != kg) lds[slot(owner, kg, i, j, v % VH)] = acc[i][j][v];
+                });
         __syncthreads();
 #pragma unroll
         for (int i = 0; i < TM; i++)
 #pragma unroll
             for (int j = 0; j < TN; j++)
+                static_for<0, 16>([&](auto V) {
+                    constexpr int v = V.value, owner = v / VH;
+                    if (owner == kg) {
 #pragma unroll
-                for (int v = 0; v < VH; v++)
-                    acc[i][j][kg * VH + v] += xm[(((wq * TM + i) * TN + j) * VH + v) * 64 + lane];
+                        for (int sdr = 0; sdr < KG; sdr++)
+                            if (sdr != kg) acc[i][j][v] += lds[slot(owner, sdr, i, j, v % VH)];
+                    }
+                });
     }
 
     // Epilogue. 32x32 accumulator layout: register v of lane l holds
@@ -244,17 +256,18 @@ __global__ __launch_bounds__(256 * KG) void sgemm_mfma_kernel(
         const float bv = bias ? bias[col] : 0.f;
 #pragma unroll
         for (int i = 0; i < TM; i++) {
-#pragma unroll
-            for (int u = 0; u < VH; u++) {
-                const int v = (KG > 1 ? kg * VH : 0) + u;
-                const int row = m0 + wm * WTM + i * 32 + (v >> 2) * 8 + g * 4 + (v & 3);
-                if (row < M) {
-                    float *c = C + (long)row * ldc + col;
-                    float out = acc[i][j][v] + bv;
-                    if (accumulate) out = *c + out;
-                    *c = out;
+            static_for<0, 16>([&](auto V) {
+                constexpr int v = V.value;
+                if (KG == 1 || v / VH == kg) {
+                    const int row = m0 + wm * WTM + i * 32 + (v >> 2) * 8 + g * 4 + (v & 3);
+                    if (row < M) {
+                        float *c = C + (long)row * ldc + col;
+                        float out = acc[i][j][v] + bv;
+                        if (accumulate) out = *c + out;
+                        *c = out;
+                    }
                 }
-            }
+            });
         }
     }
 }
