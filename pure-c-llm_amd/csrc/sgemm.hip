@@ -59,12 +59,18 @@ struct OperandTile {
             int grow = rows0 + row, gk = k0 + k;
             v4f v = {0.f, 0.f, 0.f, 0.f};
             if (VEC) {
-                // VEC guarantees the 4-vector lies entirely inside or outside
-                bool ok = KC ? (grow < nrows && gk < K) : (gk < K && grow < nrows);
-                if (ok) {
-                    const float *src = KC ? P + (long)grow * ld + gk : P + (long)gk * ld + grow;
-                    v = *reinterpret_cast<const v4f *>(src);
-                }
+                // VEC guarantees the 4-vector lies entirely inside or outside.
+                // The load is unconditional from a clamped (valid) address and
+                // the value is zeroed afterwards: with no branch around it the
+                // compiler can count loads in flight across the prefetch ring.
+                // KC: the row is scalar and k a 4-vector (K % 4 == 0, K >= 4);
+                // MN: k is scalar and the row a 4-vector (nrows % 4 == 0).
+                const bool ok = grow < nrows && gk < K;
+                const int gr = KC ? min(grow, nrows - 1) : min(grow, nrows - 4);
+                const int gc = KC ? min(gk, K - 4) : min(gk, K - 1);
+                const float *src = KC ? P + (long)gr * ld + gc : P + (long)gc * ld + gr;
+                v = *reinterpret_cast<const v4f *>(src);
+                if (!ok) v = v4f{0.f, 0.f, 0.f, 0.f};
             } else {
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
@@ -190,14 +196,19 @@ __global__ __launch_bounds__(256 * KG) void sgemm_mfma_kernel(
                 fetch(S, kt + PF);
                 const float *la = lds + (kt & 1) * BUF;
                 const float *lb = la + TA::SIZE;
+                // all of this group's fragments of the tile are requested
+                // before the first MFMA, so LDS latency overlaps the chain
+                v4f fa[KCG][TM], fb[KCG][TN];
 #pragma unroll
                 for (int c = 0; c < KCG; c++) {
                     const int kc = kg * KCG + c;
-                    v4f fa[TM], fb[TN];
 #pragma unroll
-                    for (int i = 0; i < TM; i++) fa[i] = TA::frag(la, wm * WTM + i * 32 + r32, kc, g);
+                    for (int i = 0; i < TM; i++) fa[c][i] = TA::frag(la, wm * WTM + i * 32 + r32, kc, g);
 #pragma unroll
-                    for (int j = 0; j < TN; j++) fb[j] = TB::frag(lb, wn * WTN + j * 32 + r32, kc, g);
+                    for (int j = 0; j < TN; j++) fb[c][j] = TB::frag(lb, wn * WTN + j * 32 + r32, kc, g);
+                }
+#pragma unroll
+                for (int c = 0; c < KCG; c++)
 #pragma unroll
                     for (int s = 0; s < 4; s++)
 #pragma unroll
@@ -205,8 +216,7 @@ __global__ __launch_bounds__(256 * KG) void sgemm_mfma_kernel(
 #pragma unroll
                             for (int j = 0; j < TN; j++)
                                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(
-                                    fa[i][s], fb[j][s], acc[i][j], 0, 0, 0);
-                }
+                                    fa[c][i][s], fb[c][j][s], acc[i][j], 0, 0, 0);
                 if (kt + 1 < nk) put(IC<(S.value + 1) % PF>{}, (kt + 1) & 1);
                 __syncthreads();
             }
@@ -256,15 +266,25 @@ __global__ __launch_bounds__(256 * KG) void sgemm_mfma_kernel(
         const float bv = bias ? bias[col] : 0.f;
 #pragma unroll
         for (int i = 0; i < TM; i++) {
+            const int rb = m0 + wm * WTM + i * 32 + g * 4;
+            // old C values (accumulate) are all requested before any is used,
+            // from clamped rows; rows past M are never stored
+            float old[16];
+            if (accumulate) {
+                static_for<0, 16>([&](auto V) {
+                    constexpr int v = V.value;
+                    if (KG == 1 || v / VH == kg)
+                        old[v] = C[(long)min(rb + (v >> 2) * 8 + (v & 3), M - 1) * ldc + col];
+                });
+            }
             static_for<0, 16>([&](auto V) {
                 constexpr int v = V.value;
                 if (KG == 1 || v / VH == kg) {
-                    const int row = m0 + wm * WTM + i * 32 + (v >> 2) * 8 + g * 4 + (v & 3);
+                    const int row = rb + (v >> 2) * 8 + (v & 3);
                     if (row < M) {
-                        float *c = C + (long)row * ldc + col;
                         float out = acc[i][j][v] + bv;
-                        if (accumulate) out = *c + out;
-                        *c = out;
+                        if (accumulate) out = old[v] + out;
+                        C[(long)row * ldc + col] = out;
                     }
                 }
             });
