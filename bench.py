@@ -11,7 +11,7 @@ backward layouts, grown-model prefill, decode GEMV sweeps) are reported under
 "extra". Timing loops run in C (libpcl_bench.so) between HIP events recorded
 on the stream the kernels are launched on.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--primary-only]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--primary-only] [--case NAME]
 """
 import argparse
 import ctypes as C
@@ -140,6 +140,68 @@ def cpu_baseline(M=2048, N=2048, K=2048):
                       "(the reference VNNI build is unavailable on this host)"}
 
 
+# Single configurations for profiling runs (bench.py --case NAME): the same
+# timing loops as the full run, one configuration per process.
+DECODE_LAYER = [(512, 1536), (512, 512), (512, 2048), (2048, 512)]
+CASES = {
+    "int8_2048": lambda pcl, lib, w, s: igemm(pcl, lib, 2048, 2048, 2048, 2, w, s),
+    "int8_ffn_up": lambda pcl, lib, w, s: igemm(pcl, lib, 4096, 4096, 1024, 2, w, s),
+    "fp32_1024": lambda pcl, lib, w, s: sgemm(pcl, lib, 0, 0, 1024, 1024, 1024, 0, w, s),
+    "fp32_ffn_up": lambda pcl, lib, w, s: sgemm(pcl, lib, 0, 0, 4096, 4096, 1024, 0, w, s),
+    "gemv_head_fp32_m1": lambda pcl, lib, w, s: gemv(pcl, lib, 1, 1, [(1024, 50257)], 3, w, s),
+    "gemv_head_int8_m1": lambda pcl, lib, w, s: gemv(pcl, lib, 2, 1, [(1024, 50257)], 6, w, s),
+    "decode_fp32_m1": lambda pcl, lib, w, s: gemv(pcl, lib, [0] * 64 + [1], 1, DECODE_LAYER * 16 + [(512, 2048)],
+                                                   3, w, s),
+}
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_ladder():
+    """The reference's FP32 gemm_bench rung v3-MT (gemm_packed_mt,
+    gemm_bench.c:167-192, OpenMP over M tiles) built from source into
+    oracle/_ref, on the gemm_bench FP32 config (1024^3, A and B uniform in
+    [-1, 1]) at the reference's own thread counts and at every core this
+    process may use; best of 6 as in gemm_bench.c:329-337. None when the
+    reference build is unusable on this host."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import binding as ob
+
+    gb = ob.ref("libref_gemm_bench.so")
+    if gb is None or not gb.pcl_ref_cpu_ok():
+        return None
+    M = N = K = 1024
+    A, B = ob.frand((M, K), 1234), ob.frand((K, N), 1235)
+    import numpy as np
+
+    Cm = np.empty((M, N), np.float32)
+    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    # the share of the host this process is given (OMP_NUM_THREADS on the GPU boxes)
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    if share > 0:
+        cores = min(cores, share)
+    out = {"cpu": cpu_model(), "cores_used_max": cores, "fp32_v3mt_1024": {}}
+    for t in sorted({1, 4, 8, cores}):
+        gb.pcl_ref_set_threads(t)
+        best = 1e30
+        for _ in range(6):
+            t0 = time.perf_counter()
+            gb.pcl_ref_gemm_packed_mt(ob.p(A), ob.p(B), ob.p(Cm), M, K, N)
+            best = min(best, time.perf_counter() - t0)
+        out["fp32_v3mt_1024"][f"{t}t"] = round(2.0 * M * N * K / best / 1e9, 1)
+    gb.pcl_ref_set_threads(1)
+    out["unit"] = "GFLOP/s"
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -149,6 +211,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="also run device-to-device copies of this size (HBM counter calibration)")
+    ap.add_argument("--case", choices=sorted(CASES),
+                    help="time only this configuration and print its numbers (profiling runs)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -159,6 +223,16 @@ def main():
     pcl, lib = load_bench()
     pcl.check(pcl.lib.pcl_init())
     info = pcl.device_info()
+    if args.case:
+        res = CASES[args.case](pcl, lib, args.warmup, args.steps)
+        if args.calib_copy_mib:
+            nb = args.calib_copy_mib << 20
+            src, dst = pcl.DeviceBuffer(nb), pcl.DeviceBuffer(nb)
+            for _ in range(3):
+                pcl.check(pcl.lib.pcl_memcpy_d2d(dst.ptr, src.ptr, nb))
+            res["calib_copy_bytes"] = nb
+        print(json.dumps({"case": args.case, "steps": args.steps, "warmup": args.warmup, **res}), flush=True)
+        return
     M = N = K = 2048
     pcl.sync()
     t0 = time.perf_counter()
@@ -235,6 +309,8 @@ def main():
         out["extra"] = ex
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(M, N, K)
+        if not args.primary_only:
+            out.setdefault("extra", {})["cpu_reference_fp32"] = cpu_ladder()
     print(json.dumps(out), flush=True)
 
 
