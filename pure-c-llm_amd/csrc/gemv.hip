@@ -141,7 +141,9 @@ __global__ __launch_bounds__(GV_THREADS) void sgemv_n_kernel(
     constexpr int CQ = CW / 4;             // threads across a strip row
     constexpr int RG = GV_THREADS / CQ;    // row groups
     __shared__ float red[RG][MR][CW];
-    __shared__ __attribute__((aligned(16))) float xs[XONES ? 1 : MR][XONES ? 1 : Kch<MR>::SGN];
+    // activation rows of this split, MR x kchunk (dynamic: sized at launch)
+    extern __shared__ __attribute__((aligned(16))) unsigned char gv_dyn[];
+    float *xs = reinterpret_cast<float *>(gv_dyn);
 
     const int tid = threadIdx.x;
     const int c4 = tid % CQ, rg = tid / CQ;
@@ -176,8 +178,7 @@ __global__ __launch_bounds__(GV_THREADS) void sgemv_n_kernel(
     load_batch(wn, 0);
 
     if (!XONES) {
-        stage_rows<MR, false>(&xs[0][0], Kch<MR>::SGN, kchunk, min(kchunk, K - kb), M, X + kb,
-                              ldx);
+        stage_rows<MR, false>(xs, kchunk, kchunk, min(kchunk, K - kb), M, X + kb, ldx);
         __syncthreads();
     }
 
@@ -197,7 +198,7 @@ __global__ __launch_bounds__(GV_THREADS) void sgemv_n_kernel(
             if (kb + r0 + i + u < K) {
 #pragma unroll
                 for (int m = 0; m < MR; m++) {
-                    const float xv = XONES ? 1.f : xs[m][r0 + i + u];
+                    const float xv = XONES ? 1.f : xs[m * kchunk + r0 + i + u];
 #pragma unroll
                     for (int j = 0; j < 4; j++) acc[m][j] += xv * w[u][j];
                 }
@@ -237,8 +238,9 @@ __global__ __launch_bounds__(GV_THREADS) void sgemv_t_kernel(
     const float *__restrict__ X, long ldx, const float *__restrict__ W, long ldw,
     const float *__restrict__ bias, float *__restrict__ Y, long ldy, int M, int N, int K,
     int kchunk, int splits, float *__restrict__ part, int accumulate) {
-    __shared__ __attribute__((aligned(16))) float xs[MR][Kch<MR>::SGT];
     __shared__ float res[MR][SGT_ROWS];
+    extern __shared__ __attribute__((aligned(16))) unsigned char gv_dyn[];
+    float *xs = reinterpret_cast<float *>(gv_dyn);  // MR x kchunk, sized at launch
 
     const int tid = threadIdx.x;
     const int j = tid & 15, rs = tid >> 4;
@@ -274,7 +276,7 @@ __global__ __launch_bounds__(GV_THREADS) void sgemv_t_kernel(
     v4f wn[UK][SGT_RPL];
     load_batch(wn, 4 * j);
 
-    stage_rows<MR, false>(&xs[0][0], Kch<MR>::SGT, kchunk, klen, M, X + kb, ldx);
+    stage_rows<MR, false>(xs, kchunk, kchunk, klen, M, X + kb, ldx);
     __syncthreads();
 
     float acc[SGT_RPL][MR];
@@ -296,7 +298,7 @@ __global__ __launch_bounds__(GV_THREADS) void sgemv_t_kernel(
             if (k < klen) {
                 v4f xv[MR];
 #pragma unroll
-                for (int m = 0; m < MR; m++) xv[m] = *reinterpret_cast<const v4f *>(&xs[m][k]);
+                for (int m = 0; m < MR; m++) xv[m] = *reinterpret_cast<const v4f *>(&xs[m * kchunk + k]);
 #pragma unroll
                 for (int r = 0; r < SGT_RPL; r++)
 #pragma unroll
@@ -385,8 +387,9 @@ __global__ __launch_bounds__(GV_THREADS) void igemv_kernel(
     const int32_t *__restrict__ col_off, const float *__restrict__ sa,
     const float *__restrict__ sb, void *__restrict__ Yv, long ldy, int M, int N, int K,
     int kchunk, int splits, int32_t *__restrict__ part) {
-    __shared__ __attribute__((aligned(16))) int8_t xs[MR][Kch<MR>::IGV];
     __shared__ int32_t res[MR][SGT_ROWS];
+    extern __shared__ __attribute__((aligned(16))) unsigned char gv_dyn[];
+    int8_t *xs = reinterpret_cast<int8_t *>(gv_dyn);  // MR x kchunk, sized at launch
 
     const int tid = threadIdx.x;
     const int j = tid & 15, rs = tid >> 4;
@@ -415,8 +418,8 @@ __global__ __launch_bounds__(GV_THREADS) void igemv_kernel(
     v4i wn[UK][SGT_RPL];
     load_batch(wn, 16 * j);
 
-    stage_rows<MR, true>(reinterpret_cast<uint8_t *>(&xs[0][0]), Kch<MR>::IGV, kchunk,
-                         min(kchunk, K - kb), M, X + kb, ldx);
+    stage_rows<MR, true>(reinterpret_cast<uint8_t *>(xs), kchunk, kchunk, min(kchunk, K - kb), M,
+                         X + kb, ldx);
     __syncthreads();
 
     int32_t acc[SGT_RPL][MR];
@@ -438,7 +441,7 @@ __global__ __launch_bounds__(GV_THREADS) void igemv_kernel(
             if (k < klen) {
                 v4i xv[MR];
 #pragma unroll
-                for (int m = 0; m < MR; m++) xv[m] = *reinterpret_cast<const v4i *>(&xs[m][k]);
+                for (int m = 0; m < MR; m++) xv[m] = *reinterpret_cast<const v4i *>(&xs[m * kchunk + k]);
 #pragma unroll
                 for (int r = 0; r < SGT_RPL; r++)
 #pragma unroll
@@ -545,12 +548,13 @@ static void launch_sgemv_mr(const GemvPlan &p, int w_trans, bool vec, bool x_one
                             const Workspace &ws, hipStream_t s) {
     dim3 grid(p.strips, p.splits), block(GV_THREADS);
     float *part = (float *)ws.buf;
+    const size_t xsb = (size_t)MR * p.kchunk * sizeof(float);  // staged activation rows
     if (w_trans) {
         if (vec)
-            hipLaunchKernelGGL((sgemv_t_kernel<MR, true>), grid, block, 0, s, X, ldx, W, ldw, bias,
+            hipLaunchKernelGGL((sgemv_t_kernel<MR, true>), grid, block, xsb, s, X, ldx, W, ldw, bias,
                                Y, ldy, M, N, K, p.kchunk, p.splits, part, accumulate);
         else
-            hipLaunchKernelGGL((sgemv_t_kernel<MR, false>), grid, block, 0, s, X, ldx, W, ldw, bias,
+            hipLaunchKernelGGL((sgemv_t_kernel<MR, false>), grid, block, xsb, s, X, ldx, W, ldw, bias,
                                Y, ldy, M, N, K, p.kchunk, p.splits, part, accumulate);
     } else if (x_ones) {
         if (vec)
@@ -561,17 +565,17 @@ static void launch_sgemv_mr(const GemvPlan &p, int w_trans, bool vec, bool x_one
                                ldw, bias, Y, ldy, M, N, K, p.kchunk, p.splits, part, accumulate);
     } else if (p.cw == 16) {
         if (vec)
-            hipLaunchKernelGGL((sgemv_n_kernel<MR, true, false, 16>), grid, block, 0, s, X, ldx, W,
+            hipLaunchKernelGGL((sgemv_n_kernel<MR, true, false, 16>), grid, block, xsb, s, X, ldx, W,
                                ldw, bias, Y, ldy, M, N, K, p.kchunk, p.splits, part, accumulate);
         else
-            hipLaunchKernelGGL((sgemv_n_kernel<MR, false, false, 16>), grid, block, 0, s, X, ldx,
+            hipLaunchKernelGGL((sgemv_n_kernel<MR, false, false, 16>), grid, block, xsb, s, X, ldx,
                                W, ldw, bias, Y, ldy, M, N, K, p.kchunk, p.splits, part, accumulate);
     } else {
         if (vec)
-            hipLaunchKernelGGL((sgemv_n_kernel<MR, true, false, 64>), grid, block, 0, s, X, ldx, W,
+            hipLaunchKernelGGL((sgemv_n_kernel<MR, true, false, 64>), grid, block, xsb, s, X, ldx, W,
                                ldw, bias, Y, ldy, M, N, K, p.kchunk, p.splits, part, accumulate);
         else
-            hipLaunchKernelGGL((sgemv_n_kernel<MR, false, false, 64>), grid, block, 0, s, X, ldx,
+            hipLaunchKernelGGL((sgemv_n_kernel<MR, false, false, 64>), grid, block, xsb, s, X, ldx,
                                W, ldw, bias, Y, ldy, M, N, K, p.kchunk, p.splits, part, accumulate);
     }
     if (p.splits > 1) {
@@ -619,22 +623,23 @@ static void launch_igemv_mr(const GemvPlan &p, int out_mode, int M, int N, int K
                             long ldy, const Workspace &ws, hipStream_t s) {
     dim3 grid(p.strips, p.splits), block(GV_THREADS);
     int32_t *part = (int32_t *)ws.buf;
+    const size_t xsb = (size_t)MR * p.kchunk;  // staged activation rows
     const int nround = p.strips * SGT_ROWS;
     const dim3 rg(reduce_grid(M, N)), rb(256);
     if (out_mode == 0) {
-        hipLaunchKernelGGL((igemv_kernel<MR, 0>), grid, block, 0, s, X, ldx, B, ldb, col_off, sa,
+        hipLaunchKernelGGL((igemv_kernel<MR, 0>), grid, block, xsb, s, X, ldx, B, ldb, col_off, sa,
                            sb, Y, ldy, M, N, K, p.kchunk, p.splits, part);
         if (p.splits > 1)
             hipLaunchKernelGGL((igemv_reduce_kernel<0>), rg, rb, 0, s, part, p.splits, M, N,
                                nround, col_off, sa, sb, Y, ldy);
     } else if (out_mode == 1) {
-        hipLaunchKernelGGL((igemv_kernel<MR, 1>), grid, block, 0, s, X, ldx, B, ldb, col_off, sa,
+        hipLaunchKernelGGL((igemv_kernel<MR, 1>), grid, block, xsb, s, X, ldx, B, ldb, col_off, sa,
                            sb, Y, ldy, M, N, K, p.kchunk, p.splits, part);
         if (p.splits > 1)
             hipLaunchKernelGGL((igemv_reduce_kernel<1>), rg, rb, 0, s, part, p.splits, M, N,
                                nround, col_off, sa, sb, Y, ldy);
     } else {
-        hipLaunchKernelGGL((igemv_kernel<MR, 2>), grid, block, 0, s, X, ldx, B, ldb, col_off, sa,
+        hipLaunchKernelGGL((igemv_kernel<MR, 2>), grid, block, xsb, s, X, ldx, B, ldb, col_off, sa,
                            sb, Y, ldy, M, N, K, p.kchunk, p.splits, part);
         if (p.splits > 1)
             hipLaunchKernelGGL((igemv_reduce_kernel<2>), rg, rb, 0, s, part, p.splits, M, N,
