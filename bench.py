@@ -150,6 +150,8 @@ CASES = {
     "fp32_ffn_up": lambda pcl, lib, w, s: sgemm(pcl, lib, 0, 0, 4096, 4096, 1024, 0, w, s),
     "gemv_head_fp32_m1": lambda pcl, lib, w, s: gemv(pcl, lib, 1, 1, [(1024, 50257)], 3, w, s),
     "gemv_head_int8_m1": lambda pcl, lib, w, s: gemv(pcl, lib, 2, 1, [(1024, 50257)], 6, w, s),
+    "gemv_head_fp32_m8": lambda pcl, lib, w, s: gemv(pcl, lib, 1, 8, [(1024, 50257)], 3, w, s),
+    "gemv_head_int8_m8": lambda pcl, lib, w, s: gemv(pcl, lib, 2, 8, [(1024, 50257)], 6, w, s),
     "decode_fp32_m1": lambda pcl, lib, w, s: gemv(pcl, lib, [0] * 64 + [1], 1, DECODE_LAYER * 16 + [(512, 2048)],
                                                    3, w, s),
 }

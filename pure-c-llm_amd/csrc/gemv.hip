@@ -406,7 +406,9 @@ __global__ __launch_bounds__(GV_THREADS) void igemv_kernel(
     const int8_t *brow[SGT_RPL];
 #pragma unroll
     for (int r = 0; r < SGT_RPL; r++) brow[r] = B + (long)min(n0 + rs + 16 * r, N - 1) * ldb + kb;
-    constexpr int UK = 4;  // 256-byte k steps per load batch
+    // 256-byte k steps per load batch; with 4-8 rows of X a batch's dot
+    // products take long enough that half-size batches overlap better
+    constexpr int UK = MR >= 4 ? 2 : 4;
     auto load_batch = [&](v4i (&w)[UK][SGT_RPL], int k0) {
 #pragma unroll
         for (int u = 0; u < UK; u++)
