@@ -396,6 +396,353 @@ __global__ __launch_bounds__(64 * WM * WN * KG) __attribute__((amdgpu_waves_per_
     }
 }
 
+// ---------------------------------------------------------------------------
+// Warp-specialised persistent variant for output-bound shapes (K small next
+// to the fp32 output, e.g. K = 1024): WM x WN consumer waves (one K group,
+// 128-byte K tiles, the four-step schedule of igemm_mfma_kernel) plus four
+// producer waves. The producers issue every LDS DMA and do every vmcnt wait,
+// so a consumer never waits on vmcnt: the output stores of one tile drain
+// while the consumers multiply the next (on gfx9 one counter tracks loads
+// and stores, so a wave that also loaded would wait for its own stores).
+// Each workgroup loops over output tiles slot, slot + gridDim, ...; the
+// K-tile stream runs across tile boundaries through a STAGES-deep ring. The
+// epilogue operands of a tile (sb, col_off, sa) are copied into LDS by the
+// producers (4-byte DMA), three tiles deep.
+//
+// Barrier protocol (all waves run the same number of s_barrier): P0 after
+// the prologue, then one barrier B(g) per K tile g in the consumers' step 2.
+// Before B(g) the producers have waited for K tile g+1 (leaving g+2 .. in
+// flight) and every consumer has issued and retired its reads of K tile g;
+// after it the producers refill tile g's stage with tile g + STAGES.
+constexpr int WP_NWP = 4;  // producer waves
+
+template <int BM, int BN, int WM, int WN, int STAGES, int OUT>
+__global__ __launch_bounds__(64 * (WM * WN + WP_NWP)) __attribute__((amdgpu_waves_per_eu(
+    (WM * WN + WP_NWP + 3) / 4))) void igemm_wp_kernel(const uint8_t *__restrict__ A, long lda,
+                                                      const int8_t *__restrict__ B, long ldb,
+                                                      const int32_t *__restrict__ col_off,
+                                                      const float *__restrict__ sa,
+                                                      const float *__restrict__ sb,
+                                                      void *__restrict__ Cv, long ldc, int M, int N,
+                                                      int K, int nt_store) {
+    constexpr int NWC = WM * WN, BK = IG_BK;
+    constexpr int WTM = BM / WM, WTN = BN / WN, TM = WTM / 32, TN = WTN / 32;
+    constexpr int NM = TM * TN, NR = TM + TN;
+    constexpr int CH = BK / 16, RPI = 1024 / BK;  // 8 chunks per row, 8 rows per DMA instruction
+    constexpr int SIZE_A = BM * BK, STAGE = (BM + BN) * BK;
+    constexpr int PIA = BM / (RPI * WP_NWP), PIB = BN / (RPI * WP_NWP), PL = PIA + PIB;
+    constexpr int SCL = 2 * BN + BM + 128;  // floats per tile: sb, col_off, sa, spare
+    constexpr int NS = OUT != 0 ? 2 : 0;  // epilogue-operand DMA instructions per producer wave
+    constexpr int LDS_BYTES = STAGES * STAGE + 3 * SCL * 4;
+    static_assert(BM % (RPI * WP_NWP) == 0 && BN % (RPI * WP_NWP) == 0, "rows per producer");
+    static_assert(TM >= 1 && TN >= 1 && STAGES >= 2, "tile configuration");
+    static_assert(LDS_BYTES <= 160 * 1024, "LDS budget of a CU");
+    static_assert(BN == 128 && BM <= 256, "epilogue operands: two 64-lane DMA per producer wave");
+    static_assert((STAGES - 1) * PL + NS <= 63, "vmcnt range");
+    __shared__ __attribute__((aligned(1024))) int8_t lds[LDS_BYTES];
+    float *scl = reinterpret_cast<float *>(lds + STAGES * STAGE);  // [3 tiles][sb | col_off | sa]
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nbm = (M + BM - 1) / BM, nbn = (N + BN - 1) / BN, ntiles = nbm * nbn;
+    const int nb = gridDim.x;
+    const int slot = xcd_remap(blockIdx.x, nb);
+    const int my_tiles = slot < ntiles ? (ntiles - 1 - slot) / nb + 1 : 0;
+    const int nk = K / BK;
+    const int G = my_tiles * nk;  // K tiles this workgroup streams
+    if (G == 0) return;           // uniform: no barrier is left unmatched
+    auto tile_origin = [&](int i, int &m0, int &n0) {
+        int bm, bn;
+        tile_coords(i * nb + slot, nbm, nbn, 8, bm, bn);
+        m0 = bm * BM;
+        n0 = bn * BN;
+    };
+
+    if (wave >= NWC) {
+        // ------------------------------------------------------ producers
+        const int pw = wave - NWC;
+        const int8_t *A8 = reinterpret_cast<const int8_t *>(A);
+        unsigned voff[PL];
+        int ldso[PL];
+        // Output tile i starts: per-lane source offsets of its A rows and B
+        // columns (swizzled chunk order, as in igemm_mfma_kernel), and two
+        // 4-byte DMA instructions of its epilogue operands into LDS buffer
+        // i % 3 (pw 0: sb, 1: col_off, 2-3: sa rows 0-127 / 128-255; where an
+        // operand is absent, sb again into the spare slot, so every producer
+        // issues the same count).
+        auto begin_tile = [&](int i) {
+            int m0, n0;
+            tile_origin(i, m0, n0);
+#pragma unroll
+            for (int d = 0; d < PL; d++) {
+                const bool isA = d < PIA;
+                const int rb = ((isA ? d : d - PIA) * WP_NWP + pw) * RPI;
+                const int r = rb + lane / CH;
+                const int c = (lane % CH) ^ ((r >> 1) & (CH - 1));
+                const int grow = min((isA ? m0 : n0) + r, (isA ? M : N) - 1);
+                voff[d] = (unsigned)grow * (unsigned)(isA ? lda : ldb) + (unsigned)(c * 16);
+                ldso[d] = (isA ? 0 : SIZE_A) + rb * BK;
+            }
+            if (OUT != 0) {
+                float *dst = scl + (i % 3) * SCL;
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    const float *src;
+                    float *to;
+                    if (pw == 0 || (pw == 1 && !col_off) ||
+                        (pw >= 2 && (OUT != 2 || (pw - 2) * 128 >= BM))) {
+                        src = sb + min(n0 + h * 64 + lane, N - 1);
+                        to = pw == 0 ? dst + h * 64 : dst + 2 * BN + BM + h * 64;
+                    } else if (pw == 1) {
+                        src = reinterpret_cast<const float *>(col_off) + min(n0 + h * 64 + lane, N - 1);
+                        to = dst + BN + h * 64;
+                    } else {
+                        const int rr = (pw - 2) * 128 + h * 64;
+                        src = sa + min(m0 + rr + lane, M - 1);
+                        to = dst + 2 * BN + rr;
+                    }
+                    __builtin_amdgcn_global_load_lds((const void *)src, (lds_void_t *)to, 4, 0, 0);
+                }
+            }
+        };
+        int di = 0, dk = 0;  // output tile and K tile of the next DMA
+        // issue K tile di*nk + dk; returns whether it carried epilogue operands
+        auto dma_next = [&]() -> bool {
+            const bool first = dk == 0;
+            if (first) begin_tile(di);
+            const long koff = (long)dk * BK;
+            int8_t *stage = lds + ((di * nk + dk) % STAGES) * STAGE;
+#pragma unroll
+            for (int d = 0; d < PL; d++)
+                __builtin_amdgcn_global_load_lds((const void *)((d < PIA ? A8 : B) + koff + voff[d]),
+                                                 (lds_void_t *)(stage + ldso[d]), 16, 0, 0);
+            if (++dk == nk) {
+                dk = 0;
+                di++;
+            }
+            return first && NS > 0;
+        };
+        // hist bit j: the j-th most recently issued K-tile DMA also carried
+        // epilogue operands (NS more vmcnt entries than PL); a wait that would
+        // have to count those waits for everything instead.
+        unsigned hist = 0;
+        // prologue: K tiles 0 .. STAGES-1; P0 once K tile 0 has landed
+#pragma unroll
+        for (int t = 0; t < STAGES; t++)
+            if (t < G) hist = (hist << 1) | (dma_next() ? 1u : 0u);
+        if (G >= STAGES && (hist & ((1u << (STAGES - 1)) - 1)) == 0)
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm((STAGES - 1) * PL));
+        else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+        __builtin_amdgcn_s_barrier();
+        // before B(g) K tiles g+1 .. g+STAGES-1 have been issued, oldest first
+        for (int g = 0; g < G; g++) {
+            // K tile g+1 has landed; the STAGES-2 younger ones may still fly
+            if (g + STAGES - 1 < G && (hist & ((1u << (STAGES - 2)) - 1)) == 0)
+                __builtin_amdgcn_s_waitcnt(waitcnt_vm((STAGES - 2) * PL));
+            else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+            __builtin_amdgcn_s_barrier();  // B(g)
+            if (g + STAGES < G) hist = (hist << 1) | (dma_next() ? 1u : 0u);  // into stage g % STAGES
+        }
+        return;
+    }
+
+    // ---------------------------------------------------------- consumers
+    const int wm = wave / WN, wn = wave % WN;
+    const int r32 = lane & 31, lg = lane >> 5;
+    void *C_out = Cv;
+    long ld_out = ldc;
+    int Mv = M, Nv = N;
+    asm volatile("" : "+s"(C_out), "+s"(ld_out), "+s"(Mv), "+s"(Nv));
+    const unsigned lds0 = lds_addr(lds);
+
+    v16i acc[TM][TN];
+    v4i fa[IG_KC][TM], fb[IG_KC][TN];
+    const int swz = (r32 >> 1) & (CH - 1);
+    unsigned offa[IG_KC], offb[IG_KC];
+#pragma unroll
+    for (int c = 0; c < IG_KC; c++) {
+        const int chunk = ((2 * c + lg) ^ swz) << 4;
+        offa[c] = (wm * WTM + r32) * BK + chunk;
+        offb[c] = SIZE_A + (wn * WTN + r32) * BK + chunk;
+    }
+    auto read_item = [&](unsigned base, auto C, auto R) {
+        constexpr int c = decltype(C)::value, r = decltype(R)::value;
+        if constexpr (r < TM) lds_read16<r * 32 * BK>(fa[c][r], base + offa[c]);
+        else lds_read16<(r - TM) * 32 * BK>(fb[c][r - TM], base + offb[c]);
+    };
+    auto xor_slot = [&](auto C) {
+        constexpr int c = decltype(C)::value;
+        static_for<0, TM>([&](auto I) { reg_fence(fa[c][I.value]); });
+        static_for<0, TN>([&](auto J) { reg_fence(fb[c][J.value]); });
+        static_for<0, TM>([&](auto I) { fa[c][I.value] ^= (int)0x80808080u; });
+    };
+
+    __builtin_amdgcn_s_barrier();  // P0
+    static_for<0, NR>([&](auto R) { read_item(lds0, IC<0>{}, R); });
+    static_for<0, NR>([&](auto R) { read_item(lds0, IC<1>{}, R); });
+    lds_wait<NR>();
+    xor_slot(IC<0>{});
+
+    int gk = 0;  // K tile index in this workgroup's stream
+    for (int i = 0; i < my_tiles; i++) {
+#pragma unroll
+        for (int a = 0; a < TM; a++)
+#pragma unroll
+            for (int b = 0; b < TN; b++)
+#pragma unroll
+                for (int v = 0; v < 16; v++) acc[a][b][v] = 0;
+
+        for (int kt = 0; kt < nk; kt++, gk++) {
+            const unsigned cur = lds0 + (gk % STAGES) * STAGE;
+            const unsigned nxt = lds0 + ((gk + 1) % STAGES) * STAGE;
+            static_for<0, IG_KC>([&](auto KC) {
+                constexpr int kc = KC.value;
+                constexpr int pc = (kc + 2) % IG_KC;
+                const unsigned pbase = (kc + 2 < IG_KC) ? cur : nxt;
+                constexpr int NB = kc == 2 ? 1 + NR : NR;
+                constexpr int GP = NM > 1 ? NM - 1 : 1;
+                auto item = [&](auto Bi) {
+                    constexpr int b = decltype(Bi)::value;
+                    if constexpr (kc == 2) {
+                        if constexpr (b == 0) {
+                            // B(gk): this wave's reads of K tile gk are retired
+                            lds_wait<0>();
+                            xor_slot(IC<3>{});
+                            __builtin_amdgcn_s_barrier();
+                        } else {
+                            read_item(pbase, IC<pc>{}, IC<b - 1>{});
+                        }
+                    } else {
+                        read_item(pbase, IC<pc>{}, IC<b>{});
+                    }
+                };
+                static_for<0, NM>([&](auto Q) {
+                    constexpr int q = Q.value, a = q % TM, b = q / TM;
+                    acc[a][b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[kc][a], fb[kc][b], acc[a][b], 0, 0, 0);
+                    __builtin_amdgcn_sched_barrier(0);
+                    if constexpr (q < GP) {
+                        static_for<q * NB / GP, (q + 1) * NB / GP>(item);
+                    }
+                    if constexpr (q == GP - 1 && kc != 2) {
+                        lds_wait<NR>();
+                        xor_slot(IC<(kc + 1) % IG_KC>{});
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                });
+            });
+        }
+
+        // Epilogue (layout as in igemm_mfma_kernel); operands from LDS. The
+        // stores carry no wait: they drain while the next tile is multiplied.
+        int m0, n0;
+        tile_origin(i, m0, n0);
+        const int wrow0 = m0 + wm * WTM, wcol0 = n0 + wn * WTN;
+        const float *sc = scl + (i % 3) * SCL;
+        float sbv[TN];
+        unsigned offv[TN];
+#pragma unroll
+        for (int b = 0; b < TN; b++) {
+            const int cl = wn * WTN + b * 32 + r32;
+            sbv[b] = (OUT != 0) ? sc[cl] : 0.f;
+            offv[b] = (OUT != 0 && col_off) ? reinterpret_cast<const unsigned *>(sc)[BN + cl] : 0u;
+        }
+#pragma unroll
+        for (int a = 0; a < TM; a++) {
+#pragma unroll
+            for (int vq = 0; vq < 4; vq++) {
+                typedef float v4f_t __attribute__((ext_vector_type(4)));
+                const v4f_t rs4 = (OUT == 2) ? *reinterpret_cast<const v4f_t *>(
+                                                   sc + 2 * BN + wm * WTM + a * 32 + vq * 8 + lg * 4)
+                                             : v4f_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int b = 0; b < TN; b++) {
+                    const int col = wcol0 + b * 32 + r32;
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const int v = vq * 4 + e;
+                        const int row = wrow0 + a * 32 + vq * 8 + lg * 4 + e;
+                        if (row < Mv && col < Nv) {
+                            const long o = (long)row * ld_out + col;
+                            if (OUT == 0) {
+                                if (nt_store) __builtin_nontemporal_store(acc[a][b][v], (gint32_t *)C_out + o);
+                                else reinterpret_cast<int32_t *>(C_out)[o] = acc[a][b][v];
+                            } else {
+                                const int32_t vv = (int32_t)((unsigned)acc[a][b][v] + offv[b]);
+                                const float dq = (OUT == 2) ? rs4[e] * sbv[b] : sbv[b];
+                                if (nt_store) __builtin_nontemporal_store((float)vv * dq, (gfloat_t *)C_out + o);
+                                else reinterpret_cast<float *>(C_out)[o] = (float)vv * dq;
+                            }
+                        }
+                    }
+                }
+            }
+        }
+    }
+}
+
+static int device_cus() {
+    static const int cus = [] {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+            n = 256;
+        return n;
+    }();
+    return cus;
+}
+
+template <int BM, int BN, int WM, int WN, int STAGES>
+static hipError_t launch_wp_band(int out_mode, int M, int N, int K, const uint8_t *A, long lda,
+                                 const int8_t *B, long ldb, const int32_t *col_off,
+                                 const float *sa, const float *sb, void *C, long ldc,
+                                 hipStream_t stream) {
+    const long ntiles = (long)((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+    if (ntiles == 0 || K / IG_BK == 0) return hipSuccess;
+    const int grid = (int)(ntiles < device_cus() ? ntiles : device_cus());
+    const dim3 block(64 * (WM * WN + WP_NWP));
+    const int nt = (long)M * N * 4 <= (256L << 20);
+    switch (out_mode) {
+        case 0:
+            hipLaunchKernelGGL((igemm_wp_kernel<BM, BN, WM, WN, STAGES, 0>), dim3(grid), block, 0,
+                               stream, A, lda, B, ldb, col_off, sa, sb, C, ldc, M, N, K, nt);
+            break;
+        case 1:
+            hipLaunchKernelGGL((igemm_wp_kernel<BM, BN, WM, WN, STAGES, 1>), dim3(grid), block, 0,
+                               stream, A, lda, B, ldb, col_off, sa, sb, C, ldc, M, N, K, nt);
+            break;
+        default:
+            hipLaunchKernelGGL((igemm_wp_kernel<BM, BN, WM, WN, STAGES, 2>), dim3(grid), block, 0,
+                               stream, A, lda, B, ldb, col_off, sa, sb, C, ldc, M, N, K, nt);
+            break;
+    }
+    return hipGetLastError();
+}
+
+// 32-bit per-lane DMA offsets: row bands of A and column bands of B whose
+// byte spans stay below 2^31 (as launch_split does for igemm_mfma_kernel).
+template <int BM, int BN, int WM, int WN, int STAGES>
+static hipError_t launch_wp(int out_mode, int M, int N, int K, const uint8_t *A, long lda,
+                            const int8_t *B, long ldb, const int32_t *col_off, const float *sa,
+                            const float *sb, void *C, long ldc, hipStream_t stream) {
+    const long LIM = 1L << 31;
+    long mband = lda > 0 ? LIM / lda : M, nband = ldb > 0 ? LIM / ldb : N;
+    mband = mband >= M ? M : (mband / BM) * BM;
+    nband = nband >= N ? N : (nband / BN) * BN;
+    if (mband <= 0 || nband <= 0) return hipErrorInvalidValue;
+    for (long m = 0; m < M; m += mband) {
+        for (long n = 0; n < N; n += nband) {
+            const int mm = (int)(M - m < mband ? M - m : mband);
+            const int nn = (int)(N - n < nband ? N - n : nband);
+            hipError_t e = launch_wp_band<BM, BN, WM, WN, STAGES>(
+                out_mode, mm, nn, K, A + m * lda, lda, B + n * ldb, ldb,
+                col_off ? col_off + n : nullptr, sa ? sa + m : nullptr, sb ? sb + n : nullptr,
+                (char *)C + (m * ldc + n) * 4, ldc, stream);
+            if (e != hipSuccess) return e;
+        }
+    }
+    return hipSuccess;
+}
+
 template <int BM, int BN, int WM, int WN, int KG, int STAGES, int OCC>
 static hipError_t launch_icfg(int out_mode, int M, int N, int K, const uint8_t *A, long lda,
                               const int8_t *B, long ldb, const int32_t *col_off, const float *sa,
@@ -452,18 +799,25 @@ hipError_t launch_igemm(int out_mode, int M, int N, int K, const uint8_t *A, lon
                         const int8_t *Bpk, long ldb, const int32_t *col_off, const float *sa,
                         const float *sb, void *C, long ldc, hipStream_t stream) {
     if (K % 256 != 0 || lda % 16 != 0 || ldb < K) return hipErrorInvalidValue;
-    // Tile choice (measured on the 350M-class and gemm_bench shapes): 256x256
-    // tiles with 8 waves when they still cover most of the 256 CUs; 128x128
-    // tiles with two K groups (8 waves) when those fill the chip; 64x64
-    // otherwise.
+    // Tile choice (measured on the 350M-class and gemm_bench shapes):
+    //  * outputs beyond 256 MiB (the 50257-vocab head): producer/consumer
+    //    256x128 tiles, the stores of one tile draining under the next;
+    //  * 256x256 tiles with 8 waves when they still cover most of the 256 CUs
+    //    (K = 1024 projections: fewer operand bytes per output);
+    //  * producer/consumer 128x128 tiles when those fill the chip;
+    //  * 64x64 otherwise, and for K = 0 (the epilogue alone).
     const long t256 = (long)((M + 255) / 256) * ((N + 255) / 256);
     const long t128 = (long)((M + 127) / 128) * ((N + 127) / 128);
-    if (t256 >= 192)
+    const bool huge = (long)M * N * 4 > (256L << 20);
+    if (K > 0 && t256 >= 192 && huge)
+        return launch_wp<256, 128, 4, 2, 3>(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa, sb, C,
+                                            ldc, stream);
+    if (K > 0 && t256 >= 192)
         return launch_split<256, 256, 4, 2, 1, 2, 1>(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa,
                                                   sb, C, ldc, stream);
-    if (t128 >= 256)
-        return launch_split<128, 128, 2, 2, 2, 2, 1>(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa,
-                                                  sb, C, ldc, stream);
+    if (K > 0 && t128 >= 256)
+        return launch_wp<128, 128, 4, 2, 4>(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa, sb, C,
+                                            ldc, stream);
     return launch_split<64, 64, 2, 2, 1, 4, 1>(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa, sb, C,
                                             ldc, stream);
 }

@@ -183,6 +183,26 @@ def test_igemm_full_size_checksums(M, N, K):
     np.testing.assert_array_equal(C[rows], A8[rows] @ B8)
 
 
+def test_igemm_dequant_output_beyond_256mib():
+    # outputs past 256 MiB take the producer/consumer 256x128 kernel; every
+    # dequant operand (per-row, per-column scales and column offsets) is
+    # staged through LDS there
+    M, N, K = 4096, 16400, 256
+    Au = ob.u8((M, K), 70)
+    Bq = ob.s8((K, N), 71)
+    sa = ob.uniform((M,), 72, 1e-3, 1e-2)
+    sb = ob.uniform((N,), 73, 1e-3, 1e-2)
+    off = ob.s8((N,), 74).astype(np.int32) * 1000
+    rows = np.unique(np.r_[0, 255, 256, M - 1, np.random.default_rng(3).choice(M, 24, replace=False)])
+    V = exact(Au[rows], Bq).astype(np.int32)
+    announce("igemm dq > 256 MiB", M, N, K)
+    C = _dq_run(Au, Bq, sa, sb, off)
+    np.testing.assert_array_equal(C[rows], ob.dequant((V + off).astype(np.int32), sa[rows], sb))
+    del C
+    C = _dq_run(Au, Bq, None, sb)
+    np.testing.assert_array_equal(C[rows], ob.dequant(V, None, sb))
+
+
 @pytest.mark.parametrize("M,N,K", [(2100, 2070, 1040), (4100, 3100, 528), (2056, 2048, 2064)])
 def test_igemm_ragged_large_tiles(M, N, K):
     # ragged M, N and K (K % 128 != 0) on the 128x128 (two K groups) and
