@@ -414,11 +414,9 @@ __global__ __launch_bounds__(64 * WM * WN * KG) __attribute__((amdgpu_waves_per_
 // Before B(g) the producers have waited for K tile g+1 (leaving g+2 .. in
 // flight) and every consumer has issued and retired its reads of K tile g;
 // after it the producers refill tile g's stage with tile g + STAGES.
-constexpr int WP_NWP = 4;  // producer waves
-
-template <int BM, int BN, int WM, int WN, int STAGES, int OUT>
-__global__ __launch_bounds__(64 * (WM * WN + WP_NWP)) __attribute__((amdgpu_waves_per_eu(
-    (WM * WN + WP_NWP + 3) / 4))) void igemm_wp_kernel(const uint8_t *__restrict__ A, long lda,
+template <int BM, int BN, int WM, int WN, int STAGES, int NWP, int OUT>
+__global__ __launch_bounds__(64 * (WM * WN + NWP)) __attribute__((amdgpu_waves_per_eu(
+    (WM * WN + NWP + 3) / 4))) void igemm_wp_kernel(const uint8_t *__restrict__ A, long lda,
                                                       const int8_t *__restrict__ B, long ldb,
                                                       const int32_t *__restrict__ col_off,
                                                       const float *__restrict__ sa,
@@ -430,11 +428,12 @@ __global__ __launch_bounds__(64 * (WM * WN + WP_NWP)) __attribute__((amdgpu_wave
     constexpr int NM = TM * TN, NR = TM + TN;
     constexpr int CH = BK / 16, RPI = 1024 / BK;  // 8 chunks per row, 8 rows per DMA instruction
     constexpr int SIZE_A = BM * BK, STAGE = (BM + BN) * BK;
-    constexpr int PIA = BM / (RPI * WP_NWP), PIB = BN / (RPI * WP_NWP), PL = PIA + PIB;
+    constexpr int PIA = BM / (RPI * NWP), PIB = BN / (RPI * NWP), PL = PIA + PIB;
     constexpr int SCL = 2 * BN + BM + 128;  // floats per tile: sb, col_off, sa, spare
-    constexpr int NS = OUT != 0 ? 2 : 0;  // epilogue-operand DMA instructions per producer wave
+    constexpr int NS = OUT != 0 ? 8 / NWP : 0;  // epilogue-operand DMA instructions per producer
     constexpr int LDS_BYTES = STAGES * STAGE + 3 * SCL * 4;
-    static_assert(BM % (RPI * WP_NWP) == 0 && BN % (RPI * WP_NWP) == 0, "rows per producer");
+    static_assert(BM % (RPI * NWP) == 0 && BN % (RPI * NWP) == 0, "rows per producer");
+    static_assert(NWP == 2 || NWP == 4 || NWP == 8, "producer waves");
     static_assert(TM >= 1 && TN >= 1 && STAGES >= 2, "tile configuration");
     static_assert(LDS_BYTES <= 160 * 1024, "LDS budget of a CU");
     static_assert(BN == 128 && BM <= 256, "epilogue operands: two 64-lane DMA per producer wave");
@@ -465,18 +464,19 @@ __global__ __launch_bounds__(64 * (WM * WN + WP_NWP)) __attribute__((amdgpu_wave
         unsigned voff[PL];
         int ldso[PL];
         // Output tile i starts: per-lane source offsets of its A rows and B
-        // columns (swizzled chunk order, as in igemm_mfma_kernel), and two
-        // 4-byte DMA instructions of its epilogue operands into LDS buffer
-        // i % 3 (pw 0: sb, 1: col_off, 2-3: sa rows 0-127 / 128-255; where an
-        // operand is absent, sb again into the spare slot, so every producer
-        // issues the same count).
+        // columns (swizzled chunk order, as in igemm_mfma_kernel), and the
+        // 4-byte DMA of its epilogue operands into LDS buffer i % 3: eight
+        // 64-lane pieces (sb 0-1, col_off 2-3, sa 4-7), producer pw issuing
+        // pieces [pw*NS, pw*NS + NS); an absent piece (no col_off, no sa, sa
+        // rows past BM) loads sb again into the spare slot, so every producer
+        // issues the same count.
         auto begin_tile = [&](int i) {
             int m0, n0;
             tile_origin(i, m0, n0);
 #pragma unroll
             for (int d = 0; d < PL; d++) {
                 const bool isA = d < PIA;
-                const int rb = ((isA ? d : d - PIA) * WP_NWP + pw) * RPI;
+                const int rb = ((isA ? d : d - PIA) * NWP + pw) * RPI;
                 const int r = rb + lane / CH;
                 const int c = (lane % CH) ^ ((r >> 1) & (CH - 1));
                 const int grow = min((isA ? m0 : n0) + r, (isA ? M : N) - 1);
@@ -486,20 +486,21 @@ __global__ __launch_bounds__(64 * (WM * WN + WP_NWP)) __attribute__((amdgpu_wave
             if (OUT != 0) {
                 float *dst = scl + (i % 3) * SCL;
 #pragma unroll
-                for (int h = 0; h < 2; h++) {
-                    const float *src;
-                    float *to;
-                    if (pw == 0 || (pw == 1 && !col_off) ||
-                        (pw >= 2 && (OUT != 2 || (pw - 2) * 128 >= BM))) {
-                        src = sb + min(n0 + h * 64 + lane, N - 1);
-                        to = pw == 0 ? dst + h * 64 : dst + 2 * BN + BM + h * 64;
-                    } else if (pw == 1) {
-                        src = reinterpret_cast<const float *>(col_off) + min(n0 + h * 64 + lane, N - 1);
-                        to = dst + BN + h * 64;
-                    } else {
-                        const int rr = (pw - 2) * 128 + h * 64;
-                        src = sa + min(m0 + rr + lane, M - 1);
-                        to = dst + 2 * BN + rr;
+                for (int h = 0; h < NS; h++) {
+                    const int piece = pw * NS + h;
+                    const float *src = sb + min(n0 + (piece & 1) * 64 + lane, N - 1);
+                    float *to = dst + 2 * BN + BM + (piece & 1) * 64;  // spare slot
+                    if (piece < 2) {
+                        to = dst + piece * 64;
+                    } else if (piece < 4) {
+                        if (col_off) {
+                            src = reinterpret_cast<const float *>(col_off) +
+                                  min(n0 + (piece - 2) * 64 + lane, N - 1);
+                            to = dst + BN + (piece - 2) * 64;
+                        }
+                    } else if (OUT == 2 && (piece - 4) * 64 < BM) {
+                        src = sa + min(m0 + (piece - 4) * 64 + lane, M - 1);
+                        to = dst + 2 * BN + (piece - 4) * 64;
                     }
                     __builtin_amdgcn_global_load_lds((const void *)src, (lds_void_t *)to, 4, 0, 0);
                 }
@@ -691,7 +692,7 @@ static int device_cus() {
     return cus;
 }
 
-template <int BM, int BN, int WM, int WN, int STAGES>
+template <int BM, int BN, int WM, int WN, int STAGES, int NWP>
 static hipError_t launch_wp_band(int out_mode, int M, int N, int K, const uint8_t *A, long lda,
                                  const int8_t *B, long ldb, const int32_t *col_off,
                                  const float *sa, const float *sb, void *C, long ldc,
@@ -699,19 +700,19 @@ static hipError_t launch_wp_band(int out_mode, int M, int N, int K, const uint8_
     const long ntiles = (long)((M + BM - 1) / BM) * ((N + BN - 1) / BN);
     if (ntiles == 0 || K / IG_BK == 0) return hipSuccess;
     const int grid = (int)(ntiles < device_cus() ? ntiles : device_cus());
-    const dim3 block(64 * (WM * WN + WP_NWP));
+    const dim3 block(64 * (WM * WN + NWP));
     const int nt = (long)M * N * 4 <= (256L << 20);
     switch (out_mode) {
         case 0:
-            hipLaunchKernelGGL((igemm_wp_kernel<BM, BN, WM, WN, STAGES, 0>), dim3(grid), block, 0,
+            hipLaunchKernelGGL((igemm_wp_kernel<BM, BN, WM, WN, STAGES, NWP, 0>), dim3(grid), block, 0,
                                stream, A, lda, B, ldb, col_off, sa, sb, C, ldc, M, N, K, nt);
             break;
         case 1:
-            hipLaunchKernelGGL((igemm_wp_kernel<BM, BN, WM, WN, STAGES, 1>), dim3(grid), block, 0,
+            hipLaunchKernelGGL((igemm_wp_kernel<BM, BN, WM, WN, STAGES, NWP, 1>), dim3(grid), block, 0,
                                stream, A, lda, B, ldb, col_off, sa, sb, C, ldc, M, N, K, nt);
             break;
         default:
-            hipLaunchKernelGGL((igemm_wp_kernel<BM, BN, WM, WN, STAGES, 2>), dim3(grid), block, 0,
+            hipLaunchKernelGGL((igemm_wp_kernel<BM, BN, WM, WN, STAGES, NWP, 2>), dim3(grid), block, 0,
                                stream, A, lda, B, ldb, col_off, sa, sb, C, ldc, M, N, K, nt);
             break;
     }
@@ -720,7 +721,7 @@ static hipError_t launch_wp_band(int out_mode, int M, int N, int K, const uint8_
 
 // 32-bit per-lane DMA offsets: row bands of A and column bands of B whose
 // byte spans stay below 2^31 (as launch_split does for igemm_mfma_kernel).
-template <int BM, int BN, int WM, int WN, int STAGES>
+template <int BM, int BN, int WM, int WN, int STAGES, int NWP = 4>
 static hipError_t launch_wp(int out_mode, int M, int N, int K, const uint8_t *A, long lda,
                             const int8_t *B, long ldb, const int32_t *col_off, const float *sa,
                             const float *sb, void *C, long ldc, hipStream_t stream) {
@@ -733,7 +734,7 @@ static hipError_t launch_wp(int out_mode, int M, int N, int K, const uint8_t *A,
         for (long n = 0; n < N; n += nband) {
             const int mm = (int)(M - m < mband ? M - m : mband);
             const int nn = (int)(N - n < nband ? N - n : nband);
-            hipError_t e = launch_wp_band<BM, BN, WM, WN, STAGES>(
+            hipError_t e = launch_wp_band<BM, BN, WM, WN, STAGES, NWP>(
                 out_mode, mm, nn, K, A + m * lda, lda, B + n * ldb, ldb,
                 col_off ? col_off + n : nullptr, sa ? sa + m : nullptr, sb ? sb + n : nullptr,
                 (char *)C + (m * ldc + n) * 4, ldc, stream);
@@ -816,7 +817,7 @@ hipError_t launch_igemm(int out_mode, int M, int N, int K, const uint8_t *A, lon
         return launch_split<256, 256, 4, 2, 1, 2, 1>(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa,
                                                   sb, C, ldc, stream);
     if (K > 0 && t128 >= 256)
-        return launch_wp<128, 128, 4, 2, 4>(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa, sb, C,
+        return launch_wp<128, 128, 4, 2, 3>(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa, sb, C,
                                             ldc, stream);
     return launch_split<64, 64, 2, 2, 1, 4, 1>(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa, sb, C,
                                             ldc, stream);
