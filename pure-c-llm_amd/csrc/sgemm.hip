@@ -292,6 +292,351 @@ __global__ __launch_bounds__(256 * KG) void sgemm_mfma_kernel(
     }
 }
 
+// ---------------------------------------------------------------------------
+// LDS-DMA pipeline. Operand tiles of SD_BK = 32 floats of K go from global
+// memory straight into a STAGES-deep LDS ring with global_load_lds_dwordx4
+// (no VGPR staging, no ds_write), issued by every wave; the wave's waits are
+// explicit (s_waitcnt), as are its fragment reads (inline ds_read), so the
+// compiler's loop-carried wait insertion cannot serialise the ring. Layouts
+// in LDS, unpadded and swizzled so fragment reads are conflict-free:
+//  * K-contiguous operand: ROWS rows of 128 bytes; logical 16-byte chunk c of
+//    row r sits at chunk c ^ ((r >> 1) & 7);
+//  * MN-contiguous operand: 32 k-rows of ROWS floats; logical chunk c of
+//    k-row k sits at chunk c ^ (((k >> 2) & 1) << 3).
+// A DMA instruction writes 1 KB of consecutive LDS; each lane picks the
+// global chunk that lands in its swizzled slot. Per K tile: wait for this
+// wave's fragment reads (issued during the previous tile's MFMAs) and for its
+// DMA of the next tile, one barrier, refill the stage just read, read the
+// next tile's fragments, then this tile's MFMAs. Requires K % 32 == 0 and the
+// 16-byte vector conditions of the register-staged kernel.
+constexpr int SD_BK = 32;
+
+template <int OFF>
+__device__ __forceinline__ void sd_read128(v4f &r, unsigned addr) {
+    static_assert(OFF >= 0 && OFF < 65536, "ds_read offset field");
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
+}
+template <int OFF>
+__device__ __forceinline__ void sd_read32(float &r, unsigned addr) {
+    static_assert(OFF >= 0 && OFF < 65536, "ds_read offset field");
+    asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
+}
+__device__ __forceinline__ void sd_fence(v4f &r) { asm volatile("" : "+v"(r)); }
+__device__ __forceinline__ void sd_fence(float &r) { asm volatile("" : "+v"(r)); }
+constexpr int sd_waitcnt_vm(int n) { return (n & 15) | (((n >> 4) & 3) << 14) | (7 << 4) | (15 << 8); }
+
+// One operand's tile in the LDS ring: ROWS (M or N) x SD_BK (K) floats.
+template <int ROWS, bool KC, int NW>
+struct DmaTile {
+    static constexpr int BYTES = ROWS * SD_BK * 4;  // ROWS * 128
+    static constexpr int INST = BYTES / 1024;        // DMA instructions per tile
+    static constexpr int PER_WAVE = INST / NW;
+    static_assert(INST % NW == 0, "DMA instructions must split over the waves");
+    static constexpr int CHR = KC ? 8 : ROWS / 4;    // 16-byte chunks per LDS row
+    static_assert(KC || CHR >= 16, "MN swizzle needs 16 chunks per k-row");
+
+    // per-lane source offset (floats, at k = 0) and LDS byte offset of this
+    // wave's instruction q; rows0: the tile's first row (m or n)
+    __device__ __forceinline__ static void setup(long (&voff)[PER_WAVE], int (&ldso)[PER_WAVE],
+                                                 int wave, int lane, int rows0, int nrows,
+                                                 long ld) {
+#pragma unroll
+        for (int q = 0; q < PER_WAVE; q++) {
+            const int inst = q * NW + wave;
+            if (KC) {
+                const int r = inst * 8 + lane / 8;
+                const int gc = (lane % 8) ^ ((r >> 1) & 7);
+                voff[q] = (long)min(rows0 + r, nrows - 1) * ld + gc * 4;
+            } else {
+                const int rpi = 64 / CHR;  // k-rows per instruction
+                const int k = inst * rpi + lane / CHR;
+                const int gc = (lane % CHR) ^ (((k >> 2) & 1) << 3);
+                voff[q] = (long)k * ld + min(rows0 + gc * 4, nrows - 4);
+            }
+            ldso[q] = inst * 1024;
+        }
+    }
+    // issue this wave's DMA of the tile at k0 into the stage at lds_stage
+    __device__ __forceinline__ static void dma(const float *P, long ld, int k0, const long (&voff)[PER_WAVE],
+                                               const int (&ldso)[PER_WAVE], int8_t *lds_stage) {
+        const float *base = KC ? P + k0 : P + (long)k0 * ld;
+#pragma unroll
+        for (int q = 0; q < PER_WAVE; q++)
+            __builtin_amdgcn_global_load_lds((const void *)(base + voff[q]),
+                                             (__attribute__((address_space(3))) void *)(lds_stage + ldso[q]),
+                                             16, 0, 0);
+    }
+};
+
+template <int BM, int BN, int KG, int STAGES, bool A_KC, bool B_KC>
+__global__ __launch_bounds__(256 * KG) void sgemm_dma_kernel(
+    const float *__restrict__ A, long lda, const float *__restrict__ B, long ldb,
+    const float *__restrict__ bias, float *__restrict__ C, long ldc, int M, int N, int K,
+    int accumulate, int kchunk) {
+    constexpr int NW = 4 * KG;
+    using TA = DmaTile<BM, A_KC, NW>;
+    using TB = DmaTile<BN, B_KC, NW>;
+    constexpr int WTM = BM / 2, WTN = BN / 2, TM = WTM / 32, TN = WTN / 32;
+    constexpr int KCH = SD_BK / 8;   // 8-deep k chunks per tile
+    constexpr int KCG = KCH / KG;    // chunks per K group
+    constexpr int STAGE = TA::BYTES + TB::BYTES;
+    constexpr int VH = 16 / KG;
+    constexpr int XCH = KG > 1 ? KG * (KG - 1) * 256 * TM * TN * VH * 4 : 0;
+    constexpr int LDS_BYTES = STAGES * STAGE > XCH ? STAGES * STAGE : XCH;
+    constexpr int LOADS = TA::PER_WAVE + TB::PER_WAVE;
+    static_assert(KCH % KG == 0 && STAGES >= 2, "tile configuration");
+    static_assert((STAGES - 1) * LOADS <= 63, "vmcnt range");
+    static_assert(LDS_BYTES <= 160 * 1024, "LDS budget of a CU");
+    __shared__ __attribute__((aligned(1024))) int8_t lds[LDS_BYTES];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int kg = wave >> 2, wq = wave & 3, wm = wq >> 1, wn = wq & 1;
+    const int r32 = lane & 31, g = lane >> 5;
+
+    const int nbm = (M + BM - 1) / BM, nbn = (N + BN - 1) / BN;
+    int bm, bn;
+    tile_coords(xcd_remap(blockIdx.x, nbm * nbn), nbm, nbn, 8, bm, bn);
+    const int m0 = bm * BM, n0 = bn * BN;
+    {
+        const int kbeg = blockIdx.y * kchunk;
+        K = K - kbeg < kchunk ? K - kbeg : kchunk;
+        A += A_KC ? kbeg : (long)kbeg * lda;
+        B += B_KC ? kbeg : (long)kbeg * ldb;
+        C += (long)blockIdx.y * M * ldc;
+    }
+    const int nk = K / SD_BK;
+
+    long voa[TA::PER_WAVE], vob[TB::PER_WAVE];
+    int lda_o[TA::PER_WAVE], ldb_o[TB::PER_WAVE];
+    TA::setup(voa, lda_o, wave, lane, m0, M, lda);
+    TB::setup(vob, ldb_o, wave, lane, n0, N, ldb);
+    auto dma = [&](int t) {
+        int8_t *st = lds + (t % STAGES) * STAGE;
+        TA::dma(A, lda, t * SD_BK, voa, lda_o, st);
+        TB::dma(B, ldb, t * SD_BK, vob, ldb_o, st + TA::BYTES);
+    };
+
+    // Fragment addresses (bytes within a stage). K-contiguous operand: row
+    // rb + 32i + r32 at logical chunk 2kc + g (a 16-byte read gives the four
+    // k of this lane's MFMA steps). MN-contiguous: element (k, n) with
+    // k = 8kc + 4g + s, n = cb + 32j + r32 (four 4-byte reads).
+    const unsigned lds0 = (unsigned)(uintptr_t)(const __attribute__((address_space(3))) void *)lds;
+    unsigned a_addr[A_KC ? KCG : TM], b_addr[B_KC ? KCG : TN];
+    if constexpr (A_KC) {
+#pragma unroll
+        for (int c = 0; c < KCG; c++)
+            a_addr[c] = (wm * WTM + r32) * 128 + (((2 * (kg * KCG + c) + g) ^ ((r32 >> 1) & 7)) << 4);
+    } else {
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+            const int m = wm * WTM + i * 32 + r32;
+            a_addr[i] = (kg * KCG * 8 + 4 * g) * BM * 4 + (((m >> 2) ^ (g << 3)) << 4) + (m & 3) * 4;
+        }
+    }
+    if constexpr (B_KC) {
+#pragma unroll
+        for (int c = 0; c < KCG; c++)
+            b_addr[c] = TA::BYTES + (wn * WTN + r32) * 128 +
+                        (((2 * (kg * KCG + c) + g) ^ ((r32 >> 1) & 7)) << 4);
+    } else {
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const int n = wn * WTN + j * 32 + r32;
+            b_addr[j] = TA::BYTES + (kg * KCG * 8 + 4 * g) * BN * 4 + (((n >> 2) ^ (g << 3)) << 4) + (n & 3) * 4;
+        }
+    }
+    // Fragments of one tile, two slots (current and next tile). A K-contiguous
+    // operand fills one 16-byte register quad per block; an MN-contiguous one
+    // four separate floats (each its own read, so no register copy can run
+    // ahead of the wait).
+    v4f fak[2][KCG][A_KC ? TM : 1], fbk[2][KCG][B_KC ? TN : 1];
+    float fam[2][KCG][A_KC ? 1 : TM][4], fbm[2][KCG][B_KC ? 1 : TN][4];
+    auto read_tile = [&](auto SL, int t) {
+        constexpr int sl = decltype(SL)::value;
+        const unsigned st = lds0 + (t % STAGES) * STAGE;
+        static_for<0, KCG>([&](auto Cc) {
+            constexpr int c = decltype(Cc)::value;
+            static_for<0, TM>([&](auto I) {
+                constexpr int i = decltype(I)::value;
+                if constexpr (A_KC) {
+                    sd_read128<i * 32 * 128>(fak[sl][c][i], st + a_addr[c]);
+                } else {
+                    sd_read32<(c * 8 + 0) * BM * 4>(fam[sl][c][i][0], st + a_addr[i]);
+                    sd_read32<(c * 8 + 1) * BM * 4>(fam[sl][c][i][1], st + a_addr[i]);
+                    sd_read32<(c * 8 + 2) * BM * 4>(fam[sl][c][i][2], st + a_addr[i]);
+                    sd_read32<(c * 8 + 3) * BM * 4>(fam[sl][c][i][3], st + a_addr[i]);
+                }
+            });
+            static_for<0, TN>([&](auto J) {
+                constexpr int j = decltype(J)::value;
+                if constexpr (B_KC) {
+                    sd_read128<j * 32 * 128>(fbk[sl][c][j], st + b_addr[c]);
+                } else {
+                    sd_read32<(c * 8 + 0) * BN * 4>(fbm[sl][c][j][0], st + b_addr[j]);
+                    sd_read32<(c * 8 + 1) * BN * 4>(fbm[sl][c][j][1], st + b_addr[j]);
+                    sd_read32<(c * 8 + 2) * BN * 4>(fbm[sl][c][j][2], st + b_addr[j]);
+                    sd_read32<(c * 8 + 3) * BN * 4>(fbm[sl][c][j][3], st + b_addr[j]);
+                }
+            });
+        });
+    };
+    // after the wait: order every later use of slot sl after it
+    auto fence_slot = [&](auto SL) {
+        constexpr int sl = decltype(SL)::value;
+        static_for<0, KCG>([&](auto Cc) {
+            constexpr int c = decltype(Cc)::value;
+#pragma unroll
+            for (int i = 0; i < TM; i++) {
+                if constexpr (A_KC) {
+                    sd_fence(fak[sl][c][i]);
+                } else {
+#pragma unroll
+                    for (int q = 0; q < 4; q++) sd_fence(fam[sl][c][i][q]);
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                if constexpr (B_KC) {
+                    sd_fence(fbk[sl][c][j]);
+                } else {
+#pragma unroll
+                    for (int q = 0; q < 4; q++) sd_fence(fbm[sl][c][j][q]);
+                }
+            }
+        });
+    };
+
+    v16f acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) acc[i][j][v] = 0.f;
+
+    // scalar arguments of the epilogue are materialised before the loop (a
+    // scalar load in flight would also count in lgkmcnt)
+    float *Cm = C;
+    long ldcm = ldc;
+    asm volatile("" : "+s"(Cm), "+s"(ldcm));
+
+    if (nk > 0) {
+#pragma unroll
+        for (int t = 0; t < STAGES; t++)
+            if (t < nk) dma(t);
+        if (nk >= STAGES) __builtin_amdgcn_s_waitcnt(sd_waitcnt_vm((STAGES - 1) * LOADS));
+        else __builtin_amdgcn_s_waitcnt(sd_waitcnt_vm(0));
+        __builtin_amdgcn_s_barrier();
+        read_tile(IC<0>{}, 0);
+    }
+    auto step = [&](auto SL, int kt) {
+        constexpr int sl = decltype(SL)::value;
+        // this wave's reads of tile kt have landed; its DMA of tile kt+1 too
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        fence_slot(SL);
+        if (kt + STAGES - 1 < nk) __builtin_amdgcn_s_waitcnt(sd_waitcnt_vm((STAGES - 2) * LOADS));
+        else __builtin_amdgcn_s_waitcnt(sd_waitcnt_vm(0));
+        __builtin_amdgcn_s_barrier();
+        if (kt + STAGES < nk) dma(kt + STAGES);  // into the stage of tile kt, read by every wave
+        if (kt + 1 < nk) read_tile(IC<sl ^ 1>{}, kt + 1);
+        static_for<0, KCG>([&](auto Cc) {
+            constexpr int c = decltype(Cc)::value;
+            static_for<0, 4>([&](auto S) {
+                constexpr int s4 = decltype(S)::value;
+                static_for<0, TM>([&](auto I) {
+                    constexpr int i = decltype(I)::value;
+                    static_for<0, TN>([&](auto J) {
+                        constexpr int j = decltype(J)::value;
+                        float av, bv;
+                        if constexpr (A_KC) av = fak[sl][c][i][s4];
+                        else av = fam[sl][c][i][s4];
+                        if constexpr (B_KC) bv = fbk[sl][c][j][s4];
+                        else bv = fbm[sl][c][j][s4];
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, acc[i][j], 0, 0, 0);
+                    });
+                });
+            });
+        });
+    };
+    for (int kt = 0; kt < nk; kt += 2) {
+        step(IC<0>{}, kt);
+        if (kt + 1 < nk) step(IC<1>{}, kt + 1);
+    }
+    __builtin_amdgcn_s_barrier();  // every wave is done with the ring (exchange reuses it)
+
+    if constexpr (KG > 1) {
+        float *xl = reinterpret_cast<float *>(lds);
+        auto slot = [&](int owner, int sender, int i, int j, int u) {
+            const int s = sender < owner ? sender : sender - 1;
+            return (((((owner * (KG - 1) + s) * 4 + wq) * TM + i) * TN + j) * VH + u) * 64 + lane;
+        };
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+                static_for<0, 16>([&](auto V) {
+                    constexpr int v = V.value, owner = v / VH;
+                    if (owner != kg) xl[slot(owner, kg, i, j, v % VH)] = acc[i][j][v];
+                });
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+                static_for<0, 16>([&](auto V) {
+                    constexpr int v = V.value, owner = v / VH;
+                    if (owner == kg) {
+#pragma unroll
+                        for (int sdr = 0; sdr < KG; sdr++)
+                            if (sdr != kg) acc[i][j][v] += xl[slot(owner, sdr, i, j, v % VH)];
+                    }
+                });
+    }
+
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+        const int col = n0 + wn * WTN + j * 32 + r32;
+        if (col >= N) continue;
+        const float bv = bias ? bias[col] : 0.f;
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+            const int rb = m0 + wm * WTM + i * 32 + g * 4;
+            float old[16];
+            if (accumulate) {
+                static_for<0, 16>([&](auto V) {
+                    constexpr int v = V.value;
+                    if (KG == 1 || v / VH == kg)
+                        old[v] = Cm[(long)min(rb + (v >> 2) * 8 + (v & 3), M - 1) * ldcm + col];
+                });
+            }
+            static_for<0, 16>([&](auto V) {
+                constexpr int v = V.value;
+                if (KG == 1 || v / VH == kg) {
+                    const int row = rb + (v >> 2) * 8 + (v & 3);
+                    if (row < M) {
+                        float out = acc[i][j][v] + bv;
+                        if (accumulate) out = old[v] + out;
+                        Cm[(long)row * ldcm + col] = out;
+                    }
+                }
+            });
+        }
+    }
+}
+
+template <int BM, int BN, int KG, int STAGES, bool A_KC, bool B_KC>
+static hipError_t launch_dma(int M, int N, int K, int splits, int kchunk, const float *A, long lda,
+                             const float *B, long ldb, const float *bias, int accumulate, float *C,
+                             long ldc, hipStream_t stream) {
+    const int nblk = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+    if (nblk == 0) return hipSuccess;
+    hipLaunchKernelGGL((sgemm_dma_kernel<BM, BN, KG, STAGES, A_KC, B_KC>), dim3(nblk, splits),
+                       dim3(256 * KG), 0, stream, A, lda, B, ldb, bias, C, ldc, M, N, K, accumulate,
+                       kchunk);
+    return hipGetLastError();
+}
+
 // Split-K epilogue: C = (accumulate ? C : 0) + (P_0 + P_1 + ... + bias), the
 // partial products added in split order (deterministic).
 __global__ void sgemm_splitk_reduce_kernel(const float *__restrict__ P, int splits, int M, int N,
@@ -378,7 +723,17 @@ static hipError_t dispatch_layout(const SgemmPlan &p, int M, int N, int K, const
     const float *b = split ? nullptr : bias;
     const int acc = split ? 0 : accumulate;
     hipError_t e;
-    switch (p.cfg) {
+    // Aligned operands with K a multiple of 32 (per split as well: split
+    // chunks are multiples of 64) take the LDS-DMA pipeline.
+    const bool dma_ok = vec && K % SD_BK == 0;
+    if (dma_ok) {
+        if (p.cfg == SG_64_KG2)
+            e = launch_dma<64, 64, 2, 4, A_KC, B_KC>(M, N, K, p.splits, p.kchunk, A, lda, B, ldb, b,
+                                                     acc, out, ldo, stream);
+        else
+            e = launch_dma<128, 128, 2, 4, A_KC, B_KC>(M, N, K, p.splits, p.kchunk, A, lda, B, ldb, b,
+                                                       acc, out, ldo, stream);
+    } else switch (p.cfg) {
     case SG_128_BK16:
         e = launch_cfg<128, 128, 16, 1, 1, A_KC, B_KC>(vec, M, N, K, p.splits, p.kchunk, A, lda, B,
                                                        ldb, b, acc, out, ldo, stream);

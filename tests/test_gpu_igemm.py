@@ -183,6 +183,29 @@ def test_igemm_full_size_checksums(M, N, K):
     np.testing.assert_array_equal(C[rows], A8[rows] @ B8)
 
 
+@pytest.mark.parametrize("M,N,K", [(2100, 4100, 256), (2100, 4100, 768), (4096, 2200, 1024)])
+def test_igemm_persistent_multi_tile(M, N, K):
+    # 128x128 grids of more tiles than CUs: each workgroup of the
+    # producer/consumer kernel loops over several output tiles (the K-tile
+    # stream crosses tile boundaries; K = 256 gives fewer K tiles per
+    # workgroup than ring stages on the last round); ragged edges, per-row and
+    # per-column scales and column offsets, int32 and dequantised outputs
+    Au = ob.u8((M, K), 80 + K)
+    Bq = ob.s8((K, N), 81)
+    sa = ob.uniform((M,), 82, 1e-3, 1e-2)
+    sb = ob.uniform((N,), 83, 1e-3, 1e-2)
+    off = ob.s8((N,), 84).astype(np.int32) * 1000
+    rows = np.unique(np.r_[0, 127, 128, M - 1, np.random.default_rng(4).choice(M, 24, replace=False)])
+    V = exact(Au[rows], Bq).astype(np.int32)
+    announce("igemm persistent", M, N, K)
+    C = igemm_i32(Au, Bq)
+    np.testing.assert_array_equal(C[rows], V)
+    A8 = Au.astype(np.int64) - 128
+    np.testing.assert_array_equal(C.astype(np.int64).sum(0), A8.sum(0) @ Bq.astype(np.int64))
+    C = _dq_run(Au, Bq, sa, sb, off)
+    np.testing.assert_array_equal(C[rows], ob.dequant((V + off).astype(np.int32), sa[rows], sb))
+
+
 def test_igemm_dequant_output_beyond_256mib():
     # outputs past 256 MiB take the producer/consumer 256x128 kernel; every
     # dequant operand (per-row, per-column scales and column offsets) is

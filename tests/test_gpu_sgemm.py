@@ -92,6 +92,30 @@ def test_sgemm_split_k_bias_accumulate(opA, opB, M, N, K):
     assert rel(C, R) <= FP32_TOL
 
 
+@pytest.mark.parametrize("opA,opB", [(N_, N_), (N_, T_), (T_, N_), (T_, T_)])
+@pytest.mark.parametrize("M,N,K", [(200, 260, 320), (132, 68, 96), (1000, 1004, 992)])
+def test_sgemm_lds_dma_edges(opA, opB, M, N, K):
+    # aligned operands with K % 32 == 0 take the LDS-DMA pipeline: ragged M
+    # and N (clamped rows / column chunks), all four layouts, padded leading
+    # dimensions, bias and accumulate
+    A = ob.frand((M, K + 8) if opA == N_ else (K, M + 12), 4000 + M)
+    B = ob.frand((K, N + 4) if opB == N_ else (N, K + 8), 4001 + N)
+    bias = ob.normal((N,), 4002)
+    C0 = ob.normal((M, N + 4), 4003)
+    dA, dB, db, dC = pcl.dev(A), pcl.dev(B), pcl.dev(bias), pcl.dev(C0)
+    announce("sgemm lds-dma", opA, opB, M, N, K)
+    pcl.check(pcl.lib.pcl_sgemm(opA, opB, M, N, K, dA.ptr, A.shape[1], dB.ptr, B.shape[1], db.ptr, 1, dC.ptr,
+                                N + 4, None))
+    pcl.sync()
+    C = dC.download((M, N + 4), np.float32)
+    Av = A[:, :K] if opA == N_ else A[:, :M]
+    Bv = B[:, :N] if opB == N_ else B[:, :K]
+    R = ob.gemm_f64(np.ascontiguousarray(Av), np.ascontiguousarray(Bv), transA=opA == T_, transB=opB == T_,
+                    bias=bias, C0=np.ascontiguousarray(C0[:, :N]))
+    assert rel(C[:, :N], R) <= FP32_TOL
+    np.testing.assert_array_equal(C[:, N:], C0[:, N:])  # padding columns untouched
+
+
 def test_sgemm_strided_leading_dims():
     # sub-matrix views: lda/ldb/ldc larger than the logical width
     M, N, K = 96, 80, 72
