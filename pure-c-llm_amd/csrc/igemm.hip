@@ -102,35 +102,28 @@ struct StepPlan {
     static constexpr bool has_x(int kc) { return kc != 2; }  // step 2 XORs inside its hand-over
 };
 
-// BM x BN output tile per workgroup of WM x WN x KG waves; STAGES-deep LDS
-// ring of 128-byte K tiles; OCC workgroups are meant to share a CU (the LDS
-// ring is sized for it and the register budget is capped accordingly).
-// KG = 2 uses 256-byte K tiles and two groups of WM x WN waves, group g
-// multiplying k-chunks 4g .. 4g+3 of every tile with the same four-step
-// schedule: twice the waves issue LDS reads and DMA for one output tile, and
-// each barrier covers twice the MFMAs. The groups' partial sums are added
-// through LDS at the end.
+// BM x BN output tile per workgroup of WM x WN waves; STAGES-deep LDS ring
+// of 128-byte K tiles; OCC workgroups are meant to share a CU (the LDS ring
+// is sized for it and the register budget is capped accordingly).
 // Requires M*lda and N*ldb below 2^32 (32-bit per-lane DMA offsets).
-template <int BM, int BN, int WM, int WN, int KG, int STAGES, int OCC, int OUT>
-__global__ __launch_bounds__(64 * WM * WN * KG) __attribute__((amdgpu_waves_per_eu(
-    (OCC * WM * WN * KG + 3) / 4))) void igemm_mfma_kernel(const uint8_t *__restrict__ A, long lda,
+template <int BM, int BN, int WM, int WN, int STAGES, int OCC, int OUT>
+__global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(
+    (OCC * WM * WN + 3) / 4))) void igemm_mfma_kernel(const uint8_t *__restrict__ A, long lda,
                                                      const int8_t *__restrict__ B, long ldb,
                                                      const int32_t *__restrict__ col_off,
                                                      const float *__restrict__ sa,
                                                      const float *__restrict__ sb,
                                                      void *__restrict__ Cv, long ldc, int M, int N,
                                                      int K, int nt_store) {
-    constexpr int NW = WM * WN * KG;
+    constexpr int NW = WM * WN;
     constexpr int WTM = BM / WM, WTN = BN / WN;
     constexpr int TM = WTM / 32, TN = WTN / 32;
     constexpr int NM = TM * TN;                       // MFMAs per step
     constexpr int NR = TM + TN;                       // fragment reads per step
-    // K tile: 128 bytes per K group (KG = 2: 256-byte tiles, group g takes
-    // k-chunks 4g .. 4g+3); a row of a tile is CH 16-byte chunks.
-    constexpr int BK = IG_BK * KG;
+    // K tile: 128 bytes; a row of a tile is CH = 8 16-byte chunks
+    constexpr int BK = IG_BK;
     constexpr int CH = BK / 16;
-    constexpr int RSH = (CH == 8) ? 1 : 0;  // log2(16 / CH)
-    constexpr int RPI = 1024 / BK;          // tile rows per DMA instruction
+    constexpr int RPI = 1024 / BK;  // tile rows per DMA instruction
     constexpr int SIZE_A = BM * BK, SIZE_B = BN * BK;
     constexpr int STAGE = SIZE_A + SIZE_B;
     constexpr int INST_A = BM / (RPI * NW), INST_B = BN / (RPI * NW);  // DMA per wave per tile
@@ -138,9 +131,6 @@ __global__ __launch_bounds__(64 * WM * WN * KG) __attribute__((amdgpu_waves_per_
     constexpr int D1 = (LOADS + 1) / 2, D2 = LOADS - D1;
     using Plan = StepPlan<NR, D1, D2>;
     static_assert(TM >= 1 && TN >= 1 && STAGES >= 2, "bad tile configuration");
-    static_assert(KG == 1 || (KG == 2 && TM % 2 == 0), "K groups: 1, or 2 with an even TM");
-    static_assert(KG == 1 || WM * WN * TM * TN * 64 * 64 <= STAGES * STAGE,
-                  "the partial-sum exchange must fit in the LDS ring");
     static_assert(BM % (RPI * NW) == 0 && BN % (RPI * NW) == 0, "tile rows must split over the waves");
     static_assert((STAGES - 1) * LOADS <= 63, "vmcnt range");
     static_assert(STAGES * STAGE * OCC <= 160 * 1024, "LDS budget of a CU");
@@ -150,8 +140,7 @@ __global__ __launch_bounds__(64 * WM * WN * KG) __attribute__((amdgpu_waves_per_
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int kg = wave / (WM * WN), wq = wave % (WM * WN);
-    const int wm = wq / WN, wn = wq % WN;
+    const int wm = wave / WN, wn = wave % WN;
     const int r32 = lane & 31, g = lane >> 5;
 
     const int nbm = (M + BM - 1) / BM, nbn = (N + BN - 1) / BN;
@@ -193,7 +182,7 @@ __global__ __launch_bounds__(64 * WM * WN * KG) __attribute__((amdgpu_waves_per_
         const bool isA = d < INST_A;
         const int rb = ((isA ? d : d - INST_A) * NW + wave) * RPI;
         const int r = rb + lane / CH;
-        const int c = (lane % CH) ^ ((r >> RSH) & (CH - 1));
+        const int c = (lane % CH) ^ ((r >> 1) & (CH - 1));
         const int grow = min((isA ? m0 : n0) + r, (isA ? M : N) - 1);
         voff[d] = (unsigned)grow * (unsigned)(isA ? lda : ldb) + (unsigned)(c * 16);
         ldso[d] = (isA ? 0 : SIZE_A) + rb * BK;
@@ -220,16 +209,15 @@ __global__ __launch_bounds__(64 * WM * WN * KG) __attribute__((amdgpu_waves_per_
 #pragma unroll
             for (int v = 0; v < 16; v++) acc[i][j][v] = 0;
 
-    // Fragment ring: slot c holds this group's k-chunk c (32-byte chunk
-    // 4 kg + c of the tile) of the current or the next tile. Lane l reads row
-    // l%32 of each 32-row block at 16-byte chunk 2(4 kg + c) + l/32; the row
-    // swizzle depends on l%32 only.
+    // Fragment ring: slot c holds k-chunk c (32-byte chunk c of the tile) of
+    // the current or the next tile. Lane l reads row l%32 of each 32-row
+    // block at 16-byte chunk 2c + l/32; the row swizzle depends on l%32 only.
     v4i fa[IG_KC][TM], fb[IG_KC][TN];
-    const int swz = (r32 >> RSH) & (CH - 1);
+    const int swz = (r32 >> 1) & (CH - 1);
     unsigned offa[IG_KC], offb[IG_KC];
 #pragma unroll
     for (int c = 0; c < IG_KC; c++) {
-        const int chunk = ((2 * (IG_KC * kg + c) + g) ^ swz) << 4;
+        const int chunk = ((2 * c + g) ^ swz) << 4;
         offa[c] = (wm * WTM + r32) * BK + chunk;
         offb[c] = SIZE_A + (wn * WTN + r32) * BK + chunk;
     }
@@ -314,58 +302,12 @@ __global__ __launch_bounds__(64 * WM * WN * KG) __attribute__((amdgpu_waves_per_
         });
     }
     lds_wait<0>();  // the last prefetch reads retire before their registers are reused
-    if constexpr (KG == 2) {
-        // Add the groups' partial sums: group 0 keeps the upper half of the
-        // wave tile's 32-row blocks (i < TM/2), group 1 the lower half; each
-        // hands the other half to its partner through LDS (lane-major, so the
-        // partner's lanes read their own elements). The stages are free once
-        // every wave has passed the barrier.
-        __builtin_amdgcn_s_barrier();
-        constexpr int HALF = TM / 2;
-        v4i *xch = reinterpret_cast<v4i *>(lds);
-        auto slot_of = [&](int pair, int half, int ii, int j, int q4) {
-            return (((pair * 2 + half) * HALF + ii) * TN + j) * 4 + q4;  // in units of 64 x v4i
-        };
-        // (the two branches keep every accumulator index a compile-time
-        // constant: a run-time index would move the accumulators to scratch)
-        auto give = [&](auto I0) {  // store blocks I0 .. I0+HALF-1 for the partner
-            static_for<0, HALF>([&](auto II) {
-                static_for<0, TN>([&](auto J) {
-                    const v16i &a = acc[decltype(I0)::value + II.value][J.value];
-#pragma unroll
-                    for (int q4 = 0; q4 < 4; q4++)
-                        xch[slot_of(wq, kg, II.value, J.value, q4) * 64 + lane] =
-                            v4i{a[q4 * 4], a[q4 * 4 + 1], a[q4 * 4 + 2], a[q4 * 4 + 3]};
-                });
-            });
-        };
-        auto take = [&](auto I0) {  // add the partner's blocks into I0 .. I0+HALF-1
-            static_for<0, HALF>([&](auto II) {
-                static_for<0, TN>([&](auto J) {
-                    v16i &a = acc[decltype(I0)::value + II.value][J.value];
-#pragma unroll
-                    for (int q4 = 0; q4 < 4; q4++) {
-                        const v4i p = xch[slot_of(wq, kg ^ 1, II.value, J.value, q4) * 64 + lane];
-#pragma unroll
-                        for (int e = 0; e < 4; e++) a[q4 * 4 + e] += p[e];
-                    }
-                });
-            });
-        };
-        if (kg == 0) give(IC<HALF>{});
-        else give(IC<0>{});
-        __syncthreads();
-        if (kg == 0) take(IC<0>{});
-        else take(IC<HALF>{});
-    }
-
     // Epilogue: register v of lane l holds row rl = (v/4)*8 + (l/32)*4 + v%4,
     // column l%32 of each 32x32 block. The row scale of rl is fetched from
     // lane rl by a cross-lane permute (no memory access); stores carry no
     // waits, so they stream out back to back.
 #pragma unroll
     for (int i = 0; i < TM; i++) {
-        if (KG == 2 && (i < TM / 2) != (kg == 0)) continue;  // the partner stores this half
         float rs[16];
 #pragma unroll
         for (int v = 0; v < 16; v++) rs[v] = (OUT == 2) ? __shfl(sav[i], (v >> 2) * 8 + g * 4 + (v & 3)) : 0.f;
@@ -744,25 +686,25 @@ static hipError_t launch_wp(int out_mode, int M, int N, int K, const uint8_t *A,
     return hipSuccess;
 }
 
-template <int BM, int BN, int WM, int WN, int KG, int STAGES, int OCC>
+template <int BM, int BN, int WM, int WN, int STAGES, int OCC>
 static hipError_t launch_icfg(int out_mode, int M, int N, int K, const uint8_t *A, long lda,
                               const int8_t *B, long ldb, const int32_t *col_off, const float *sa,
                               const float *sb, void *C, long ldc, hipStream_t stream) {
     const int nblk = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
     if (nblk == 0) return hipSuccess;
-    dim3 grid(nblk), block(64 * WM * WN * KG);
+    dim3 grid(nblk), block(64 * WM * WN);
     const int nt = (long)M * N * 4 <= (256L << 20);  // outputs up to 256 MiB: streaming stores
     switch (out_mode) {
         case 0:
-            hipLaunchKernelGGL((igemm_mfma_kernel<BM, BN, WM, WN, KG, STAGES, OCC, 0>), grid, block, 0,
+            hipLaunchKernelGGL((igemm_mfma_kernel<BM, BN, WM, WN, STAGES, OCC, 0>), grid, block, 0,
                                stream, A, lda, B, ldb, col_off, sa, sb, C, ldc, M, N, K, nt);
             break;
         case 1:
-            hipLaunchKernelGGL((igemm_mfma_kernel<BM, BN, WM, WN, KG, STAGES, OCC, 1>), grid, block, 0,
+            hipLaunchKernelGGL((igemm_mfma_kernel<BM, BN, WM, WN, STAGES, OCC, 1>), grid, block, 0,
                                stream, A, lda, B, ldb, col_off, sa, sb, C, ldc, M, N, K, nt);
             break;
         default:
-            hipLaunchKernelGGL((igemm_mfma_kernel<BM, BN, WM, WN, KG, STAGES, OCC, 2>), grid, block, 0,
+            hipLaunchKernelGGL((igemm_mfma_kernel<BM, BN, WM, WN, STAGES, OCC, 2>), grid, block, 0,
                                stream, A, lda, B, ldb, col_off, sa, sb, C, ldc, M, N, K, nt);
             break;
     }
@@ -772,7 +714,7 @@ static hipError_t launch_icfg(int out_mode, int M, int N, int K, const uint8_t *
 // The kernel addresses each operand with 32-bit per-lane offsets: split the
 // problem into row bands of A and column bands of B whose byte spans stay
 // below 2^31.
-template <int BM, int BN, int WM, int WN, int KG, int STAGES, int OCC>
+template <int BM, int BN, int WM, int WN, int STAGES, int OCC>
 static hipError_t launch_split(int out_mode, int M, int N, int K, const uint8_t *A, long lda,
                                const int8_t *B, long ldb, const int32_t *col_off, const float *sa,
                                const float *sb, void *C, long ldc, hipStream_t stream) {
@@ -786,7 +728,7 @@ static hipError_t launch_split(int out_mode, int M, int N, int K, const uint8_t 
         for (long n = 0; n < N; n += nband) {
             const int mm = (int)(M - m < mband ? M - m : mband);
             const int nn = (int)(N - n < nband ? N - n : nband);
-            hipError_t e = launch_icfg<BM, BN, WM, WN, KG, STAGES, OCC>(
+            hipError_t e = launch_icfg<BM, BN, WM, WN, STAGES, OCC>(
                 out_mode, mm, nn, K, A + m * lda, lda, B + n * ldb, ldb, col_off ? col_off + n : nullptr,
                 sa ? sa + m : nullptr, sb ? sb + n : nullptr,
                 (char *)C + (m * ldc + n) * esz, ldc, stream);
@@ -814,12 +756,12 @@ hipError_t launch_igemm(int out_mode, int M, int N, int K, const uint8_t *A, lon
         return launch_wp<256, 128, 4, 2, 3>(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa, sb, C,
                                             ldc, stream);
     if (K > 0 && t256 >= 192)
-        return launch_split<256, 256, 4, 2, 1, 2, 1>(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa,
+        return launch_split<256, 256, 4, 2, 2, 1>(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa,
                                                   sb, C, ldc, stream);
     if (K > 0 && t128 >= 256)
         return launch_wp<128, 128, 4, 2, 3>(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa, sb, C,
                                             ldc, stream);
-    return launch_split<64, 64, 2, 2, 1, 4, 1>(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa, sb, C,
+    return launch_split<64, 64, 2, 2, 4, 1>(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa, sb, C,
                                             ldc, stream);
 }
 
