@@ -106,6 +106,11 @@ int pcl_event_destroy(void *ev);
  * (train.c:34-51, transformer.h:35-39, model.h:24). The drop-ins below read
  * them from here instead; they fail with PCL_ERR_UNSET_DIMS until set. */
 int pcl_set_model_dims(int d_model, int vocab_size);
+/* The attention drop-ins read compile-time N_HEADS (train.c:41) and, for the
+ * GPU API, B_SIZE/T_SIZE/DIM (gpu_kernels.h:17-31); here they come from
+ * pcl_set_attn_dims and pcl_set_model_dims (d_model = DIM), PCL_ERR_UNSET_DIMS
+ * until set. Head size d_model / n_heads must be 32, 64 or 128. */
+int pcl_set_attn_dims(int batch, int seq_len, int n_heads);
 
 /* ============================== 1. host-pointer drop-ins ================= */
 
@@ -137,6 +142,14 @@ void proj_token(float *out, const float *in, const float *W, const float *bias, 
 /* generate.c:95-107: same contract as proj_token. */
 void matvec(float *out, const float *x, const float *W, const float *b, int K, int N);
 
+/* train.c:339-370: causal multi-head attention over B sequences of T tokens;
+ * q/k/v/att are (B*T) x D_MODEL (head h at columns [h*D/H, (h+1)*D/H)),
+ * probs [B*H][T][T] normalised for j <= i. Entries j > i are written 0 (the
+ * CPU original leaves them untouched; gpu_kernels.cu:279 zeroes them).
+ * D_MODEL from pcl_set_model_dims, N_HEADS from pcl_set_attn_dims. */
+void attention_forward(const float *q, const float *k, const float *v, float *att, float *probs,
+                       int B, int T);
+
 /* gemm_bench.c:225-236: per-tensor symmetric quantisation to u8 (+128 offset),
  * K padded to Kpad with 128. Returns the scale amax*fl(1/127). */
 float quantize_A(const float *A, uint8_t *Au, int M, int K, int Kpad);
@@ -164,6 +177,10 @@ void gemm_nt(const float *A, const float *B, float *C, int M, int K, int N, int 
 void gemm_tn(const float *A, const float *B, float *C, int M, int K, int N);
 /* gpu_kernels.h:51: db(N) += colsum(dY(M,N)). */
 void bias_bwd(float *db, const float *dY, int M, int N);
+/* gpu_kernels.h:63-64: causal attention of B_SIZE x T_SIZE tokens, DIM wide,
+ * N_HEADS heads (pcl_set_attn_dims / pcl_set_model_dims); probs [B*H][T][T]
+ * normalised, zero above the diagonal (gpu_kernels.cu:264-281, 403-432). */
+void attn_fwd(const float *Q, const float *K, const float *V, float *att, float *probs);
 
 /* ============================== 3. native entry points =================== */
 
@@ -184,6 +201,16 @@ int pcl_sgemv(int opW, int M, int N, int K, const float *X, int ldx, const float
 
 /* db(N) += colsum(dY) (gpu_kernels.cu:102-108), fixed m order per column. */
 int pcl_bias_bwd(float *db, const float *dY, int M, int N, int ld, void *stream);
+
+/* Causal multi-head attention forward on the f32 MFMA (train.c:339-370,
+ * gpu_kernels.cu:264-281/403-432), one fused launch: Q, K, V are (B*T) x ld
+ * row-major with head h at columns [h*dh, (h+1)*dh); att (B*T) x ld_att gets
+ * att_i = sum_{j<=i} p_ij v_j, p_ij = softmax_j(q_i.k_j / sqrtf(dh)). probs is
+ * NULL or [B*H][T][T] (row (b*H+h)*T + i; p for j <= i, 0 above). dh must be
+ * 32, 64 or 128; ld and ld_att multiples of 4; Q, K, V, att 16-byte aligned.
+ * Q/K/V may be column slices of one fused (B*T) x 3D QKV buffer (ld = 3D). */
+int pcl_attn_fwd(const float *Q, const float *K, const float *V, int ld, float *att, int ld_att,
+                 float *probs, int B, int T, int H, int dh, void *stream);
 
 /* ---- INT8: u8 activations x s8 weights -> int32 (gemm_bench.c:212-285) ----
  * Weights live in the GPU-native packed layout: N rows of Kp = pcl_s8_kpad(K)

@@ -51,6 +51,9 @@ _ORACLE_PROTOS = {
     "orc_gemm_u8s8_raw_i32": (_l, [_vp, _i, _vp, _i, _vp, _i, _i, _i, _i]),
     "orc_gemm_int8_kernel": (None, [_vp, _i, _vp, _vp, _vp, _vp, _i, _i]),
     "orc_dequant": (None, [_vp, _i, _vp, _vp, _vp, _i, _i, _i]),
+    "orc_attention_forward": (None, [_vp, _vp, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i]),
+    "orc_attention_backward": (None, [_vp, _vp, _vp, _vp, _i, _vp, _vp, _vp, _i, _vp, _i, _i, _i, _i]),
+    "orc_attention_forward_f64": (None, [_vp, _vp, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i]),
     "orc_rms_rel": (_d, [_vp, _vp, _l]),
     "orc_max_abs_diff": (_d, [_vp, _vp, _l]),
 }
@@ -80,6 +83,17 @@ _REF_PROTOS = {
         "pcl_ref_matmul_backward": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i]),
         "pcl_ref_tied_head_forward": (None, [_vp, _vp, _vp, _i]),
         "pcl_ref_tied_head_backward": (None, [_vp, _vp, _vp, _vp, _vp, _i]),
+        "pcl_ref_train_n_heads": (_i, []),
+        "pcl_ref_train_t_size": (_i, []),
+        "pcl_ref_attention_forward": (None, [_vp, _vp, _vp, _vp, _vp, _i, _i]),
+        "pcl_ref_attention_backward": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i]),
+    },
+    "libref_train_h64.so": {
+        "pcl_ref_train_d_model": (_i, []),
+        "pcl_ref_train_n_heads": (_i, []),
+        "pcl_ref_train_t_size": (_i, []),
+        "pcl_ref_attention_forward": (None, [_vp, _vp, _vp, _vp, _vp, _i, _i]),
+        "pcl_ref_attention_backward": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i]),
     },
     "libref_model.so": {
         "pcl_ref_model_d_model": (_i, []),
@@ -205,6 +219,29 @@ def dequant(V, sa, sb):
     out = np.empty((M, N), np.float32)
     oracle().orc_dequant(p(np.ascontiguousarray(V)), N, p(sa), p(sb), p(out), N, M, N)
     return out
+
+
+def attention_forward(q, k, v, B, T, H, dh, f64=False):
+    """(att, probs) of the causal attention restatement; q/k/v (B*T) x ld."""
+    q, k, v = (np.ascontiguousarray(x, np.float32) for x in (q, k, v))
+    ld = q.shape[1]
+    att = np.zeros((B * T, ld), np.float32)
+    probs = np.empty((B * H, T, T), np.float32)
+    fn = oracle().orc_attention_forward_f64 if f64 else oracle().orc_attention_forward
+    fn(p(q), p(k), p(v), ld, p(att), ld, p(probs), B, T, H, dh)
+    return att, probs
+
+
+def attention_backward(d_att, q, k, v, probs, B, T, H, dh, dq=None, dk=None, dv=None):
+    """(dq, dk, dv) accumulated onto the given arrays (zeros if None)."""
+    q, k, v, d_att = (np.ascontiguousarray(x, np.float32) for x in (q, k, v, d_att))
+    ld = q.shape[1]
+    dq, dk, dv = (np.zeros_like(q) if a is None else np.array(a, np.float32, copy=True)
+                  for a in (dq, dk, dv))
+    oracle().orc_attention_backward(p(dq), p(dk), p(dv), p(d_att), d_att.shape[1], p(q), p(k),
+                                    p(v), ld, p(np.ascontiguousarray(probs, np.float32)), B, T,
+                                    H, dh)
+    return dq, dk, dv
 
 
 def normwise_rel_err(X, R):

@@ -19,6 +19,13 @@
  *                                 sum Au*Bq - 128*colsum = sum (Au-128)*Bq checked
  *                                 against the reference gemm_int8_kernel output
  *   orc_dequant ................. bit-exact against gemm_bench.c's float output
+ *   orc_attention_forward / _backward
+ *                                 train.c built from source (oracle/_ref) at two
+ *                                 head sizes (16 and 64); closed forms (T = 1 gives
+ *                                 att = v; equal keys give uniform p and running
+ *                                 means of v); probability rows sum to one; the
+ *                                 backward against central differences of the
+ *                                 f64 forward
  */
 #include "pcl_oracle.h"
 
@@ -282,6 +289,126 @@ void orc_matvec(float *out, const float *x, const float *W, const float *b, int 
             for (int n = 0; n < N; n++) o[n] += a * wr[n];
         }
     }
+}
+
+/* -------------------------------------------------------- attention ------ */
+void orc_attention_forward(const float *q, const float *k, const float *v, int ld, float *att,
+                           int ld_att, float *probs, int B, int T, int H, int dh) {
+    /* train.c:339-370, per (b, h) and query i: scores over j <= i with the
+     * running max, expf and the sum in j order, p *= 1/sum, then the
+     * j-sequential weighted sum of v rows. */
+    const float scale = 1.0f / sqrtf((float)dh);
+    float *row = (float *)malloc(sizeof(float) * (size_t)(T > 0 ? T : 1));
+    for (int bh = 0; bh < B * H; bh++) {
+        const int b = bh / H, off = (bh % H) * dh;
+        for (int i = 0; i < T; i++) {
+            const float *qi = q + (size_t)(b * T + i) * ld + off;
+            float *p = probs ? probs + ((size_t)bh * T + i) * T : row;
+            float maxv = -1e30f;
+            for (int j = 0; j <= i; j++) {
+                const float *kj = k + (size_t)(b * T + j) * ld + off;
+                float dot = 0.0f;
+                for (int d = 0; d < dh; d++) dot += qi[d] * kj[d];
+                dot *= scale;
+                p[j] = dot;
+                if (dot > maxv) maxv = dot;
+            }
+            float sum = 0.0f;
+            for (int j = 0; j <= i; j++) {
+                const float e = expf(p[j] - maxv);
+                p[j] = e;
+                sum += e;
+            }
+            const float inv = 1.0f / sum;
+            for (int j = 0; j <= i; j++) p[j] *= inv;
+            for (int j = i + 1; j < T; j++) p[j] = 0.0f;
+            float *oi = att + (size_t)(b * T + i) * ld_att + off;
+            for (int d = 0; d < dh; d++) oi[d] = 0.0f;
+            for (int j = 0; j <= i; j++) {
+                const float pj = p[j];
+                const float *vj = v + (size_t)(b * T + j) * ld + off;
+                for (int d = 0; d < dh; d++) oi[d] += pj * vj[d];
+            }
+        }
+    }
+    free(row);
+}
+
+void orc_attention_backward(float *dq, float *dk, float *dv, const float *d_att, int ld_att,
+                            const float *q, const float *k, const float *v, int ld,
+                            const float *probs, int B, int T, int H, int dh) {
+    /* train.c:374-407: d_probs_j = dao . v_j and dv_j += p_j dao; then
+     * dot = sum_j p_j d_probs_j, ds_j = p_j (d_probs_j - dot) scale,
+     * dq_i += ds_j k_j, dk_j += ds_j q_i -- all in j order per query i. */
+    const float scale = 1.0f / sqrtf((float)dh);
+    float *dprobs = (float *)malloc(sizeof(float) * (size_t)(T > 0 ? T : 1));
+    for (int bh = 0; bh < B * H; bh++) {
+        const int b = bh / H, off = (bh % H) * dh;
+        for (int i = 0; i < T; i++) {
+            const float *dao = d_att + (size_t)(b * T + i) * ld_att + off;
+            const float *p = probs + ((size_t)bh * T + i) * T;
+            for (int j = 0; j <= i; j++) {
+                const float *vj = v + (size_t)(b * T + j) * ld + off;
+                float *dvj = dv + (size_t)(b * T + j) * ld + off;
+                float dp = 0.0f;
+                for (int d = 0; d < dh; d++) {
+                    dp += dao[d] * vj[d];
+                    dvj[d] += p[j] * dao[d];
+                }
+                dprobs[j] = dp;
+            }
+            float dot = 0.0f;
+            for (int j = 0; j <= i; j++) dot += p[j] * dprobs[j];
+            float *dqi = dq + (size_t)(b * T + i) * ld + off;
+            const float *qi = q + (size_t)(b * T + i) * ld + off;
+            for (int j = 0; j <= i; j++) {
+                const float ds = p[j] * (dprobs[j] - dot) * scale;
+                const float *kj = k + (size_t)(b * T + j) * ld + off;
+                float *dkj = dk + (size_t)(b * T + j) * ld + off;
+                for (int d = 0; d < dh; d++) {
+                    dqi[d] += ds * kj[d];
+                    dkj[d] += ds * qi[d];
+                }
+            }
+        }
+    }
+    free(dprobs);
+}
+
+void orc_attention_forward_f64(const float *q, const float *k, const float *v, int ld, float *att,
+                               int ld_att, float *probs, int B, int T, int H, int dh) {
+    const double scale = 1.0 / sqrt((double)dh);
+    double *row = (double *)malloc(sizeof(double) * (size_t)(T > 0 ? T : 1));
+    for (int bh = 0; bh < B * H; bh++) {
+        const int b = bh / H, off = (bh % H) * dh;
+        for (int i = 0; i < T; i++) {
+            const float *qi = q + (size_t)(b * T + i) * ld + off;
+            double maxv = -1e300, sum = 0.0;
+            for (int j = 0; j <= i; j++) {
+                const float *kj = k + (size_t)(b * T + j) * ld + off;
+                double dot = 0.0;
+                for (int d = 0; d < dh; d++) dot += (double)qi[d] * kj[d];
+                row[j] = dot * scale;
+                if (row[j] > maxv) maxv = row[j];
+            }
+            for (int j = 0; j <= i; j++) {
+                row[j] = exp(row[j] - maxv);
+                sum += row[j];
+            }
+            for (int j = 0; j <= i; j++) row[j] /= sum;
+            if (probs) {
+                float *p = probs + ((size_t)bh * T + i) * T;
+                for (int j = 0; j < T; j++) p[j] = j <= i ? (float)row[j] : 0.0f;
+            }
+            float *oi = att + (size_t)(b * T + i) * ld_att + off;
+            for (int d = 0; d < dh; d++) {
+                double o = 0.0;
+                for (int j = 0; j <= i; j++) o += row[j] * v[(size_t)(b * T + j) * ld + off + d];
+                oi[d] = (float)o;
+            }
+        }
+    }
+    free(row);
 }
 
 /* ------------------------------------------------------------- INT8 ------ */

@@ -100,6 +100,24 @@ void orc_quantize_B_cols(const float *B, int8_t *Bq, float *bscale, int K, int N
 /* Unpack the VNNI panel layout back to Bq (K x N row-major; rows >= K unused). */
 void orc_unpack_vnni(const int8_t *Bp, int8_t *Bq, int K, int N, int Kpad);
 
+/* Causal multi-head attention, train.c:339-370 attention_forward generalised
+ * to B sequences of T tokens, H heads of dh: q/k/v rows of ld floats (row
+ * b*T + t, head h at columns [h*dh, (h+1)*dh)), att rows of ld_att.
+ *   p_ij = exp(s_ij - max_j s) / sum_j exp(...),  s_ij = (q_i . k_j) * (1/sqrtf(dh)), j <= i
+ *   att_i = sum_{j<=i} p_ij v_j
+ * probs: NULL or [B*H][T][T]; entries j > i are set to 0 (gpu_kernels.cu:279). */
+void orc_attention_forward(const float *q, const float *k, const float *v, int ld, float *att,
+                           int ld_att, float *probs, int B, int T, int H, int dh);
+/* train.c:374-407 attention_backward: dq, dk, dv (rows of ld) ACCUMULATE the
+ * gradients given d_att (rows of ld_att) and the forward's probs. */
+void orc_attention_backward(float *dq, float *dk, float *dv, const float *d_att, int ld_att,
+                            const float *q, const float *k, const float *v, int ld,
+                            const float *probs, int B, int T, int H, int dh);
+/* Same mathematics in double precision (score, softmax and sums), rounded once
+ * to float: the tolerance anchor for dh the reference is not built at. */
+void orc_attention_forward_f64(const float *q, const float *k, const float *v, int ld, float *att,
+                               int ld_att, float *probs, int B, int T, int H, int dh);
+
 /* Exact u8 x s8 GEMM, the identity of gemm_bench.c:216-217:
  *   C[m,n] = sum_k (Au[m,k]-128) * Bq[k,n]   (Bq K x N row-major, ldb)
  * int64 accumulation; returns the number of outputs outside int32 (0 = ok). */

@@ -1,8 +1,8 @@
 /*
  * ref_shim_train.c -- build-time harness around the reference's own train.c
  * (pure-c-llm), compiled where it lies with small -D dims from the Makefile.
- * TEST INFRASTRUCTURE ONLY: exports its static GEMM functions
- * (train.c:181-252, 412-447) under pcl_ref_* names to pin the oracle.
+ * TEST INFRASTRUCTURE ONLY: exports its static GEMM and attention functions
+ * (train.c:181-252, 339-407, 412-447) under pcl_ref_* names to pin the oracle.
  */
 #include REF_TRAIN_C
 
@@ -21,4 +21,14 @@ void pcl_ref_tied_head_forward(float *logits, const float *lnf, const float *wte
 void pcl_ref_tied_head_backward(float *d_lnf, float *dwte, const float *d_logits, const float *lnf,
                                 const float *wte, int M) {
     tied_head_backward(d_lnf, dwte, d_logits, lnf, wte, M);
+}
+int pcl_ref_train_n_heads(void) { return N_HEADS; }
+int pcl_ref_train_t_size(void) { return T_SIZE; }
+void pcl_ref_attention_forward(const float *q, const float *k, const float *v, float *att, float *probs,
+                               int B, int T) {
+    attention_forward(q, k, v, att, probs, B, T);
+}
+void pcl_ref_attention_backward(float *dq, float *dk, float *dv, const float *d_att, const float *q,
+                                const float *k, const float *v, const float *probs, int B, int T) {
+    attention_backward(dq, dk, dv, d_att, q, k, v, probs, B, T);
 }

@@ -56,6 +56,14 @@ hipError_t launch_igemm(int out_mode, int M, int N, int K, const uint8_t *A, lon
 hipError_t launch_pad_a_u8(const uint8_t *A, long lda, int M, int K, uint8_t *dst, int Kd,
                            hipStream_t stream);
 
+// ---- causal attention (attn.hip) ----
+// Q, K, V: (B*T) x ld row-major, head h at columns [h*dh, (h+1)*dh); O: (B*T) x
+// ldo; P: NULL or [B*H][T][T] probabilities (zero above the diagonal).
+// dh in {32, 64, 128}; ld, ldo multiples of 4 and 16-byte aligned bases.
+hipError_t launch_attn_fwd(const float *Q, const float *K, const float *V, long ld, float *O,
+                           long ldo, float *P, int B, int T, int H, int dh, float scale,
+                           hipStream_t stream);
+
 // ---- GEMV (gemv.hip) ----
 GemvPlan plan_sgemv(int w_trans, int M, int N, int K);
 // Column sums of a K x N matrix (bias_bwd): plan for launch_sgemv with x_ones.

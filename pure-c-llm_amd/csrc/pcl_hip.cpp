@@ -29,6 +29,7 @@ thread_local char t_msg[512] = "";
 thread_local hipStream_t t_stream = nullptr;
 int g_abort_on_error = 0;
 int g_d_model = 0, g_vocab = 0;
+int g_attn_batch = 0, g_attn_seq = 0, g_attn_heads = 0;
 
 int set_error(int status, const char *fmt, ...) {
     t_status = status;
@@ -389,6 +390,15 @@ int pcl_set_model_dims(int d_model, int vocab_size) {
     return PCL_OK;
 }
 
+int pcl_set_attn_dims(int batch, int seq_len, int n_heads) {
+    CHECK_ARG(batch > 0 && seq_len > 0 && n_heads > 0,
+              "pcl_set_attn_dims: dims must be positive (%d, %d, %d)", batch, seq_len, n_heads);
+    g_attn_batch = batch;
+    g_attn_seq = seq_len;
+    g_attn_heads = n_heads;
+    return PCL_OK;
+}
+
 // ----------------------------------------------------------- FP32 native ----
 int pcl_sgemv(int opW, int M, int N, int K, const float *X, int ldx, const float *W, int ldw,
               const float *bias, int accumulate, float *Y, int ldy, void *stream) {
@@ -452,6 +462,28 @@ int pcl_bias_bwd(float *db, const float *dY, int M, int N, int ld, void *stream)
     StreamScratch *sc;
     PCL_OK_OR_RETURN(get_scratch(s, p.part_bytes, 0, &sc));
     HIP_OK(pcl::launch_sgemv(p, 0, 1, N, M, nullptr, 0, true, dY, ld, nullptr, 1, db, N, sc->ws, s));
+    return PCL_OK;
+}
+
+int pcl_attn_fwd(const float *Q, const float *K, const float *V, int ld, float *att, int ld_att,
+                 float *probs, int B, int T, int H, int dh, void *stream) {
+    CHECK_ARG(B >= 0 && T >= 0 && H >= 0, "pcl_attn_fwd: negative dimension (B=%d T=%d H=%d)", B,
+              T, H);
+    CHECK_ARG(dh == 32 || dh == 64 || dh == 128, "pcl_attn_fwd: head size %d is not 32, 64 or 128",
+              dh);
+    if (B == 0 || T == 0 || H == 0) return PCL_OK;
+    CHECK_ARG(Q && K && V && att, "pcl_attn_fwd: NULL operand");
+    CHECK_ARG(ld >= H * dh && ld_att >= H * dh, "pcl_attn_fwd: ld=%d / ld_att=%d < H*dh=%d", ld,
+              ld_att, H * dh);
+    CHECK_ARG(ld % 4 == 0 && ld_att % 4 == 0, "pcl_attn_fwd: ld=%d, ld_att=%d not multiples of 4",
+              ld, ld_att);
+    CHECK_ARG(aligned16(Q) && aligned16(K) && aligned16(V) && aligned16(att),
+              "pcl_attn_fwd: Q, K, V and att must be 16-byte aligned");
+    CHECK_ARG((long)B * T <= INT32_MAX && (long)B * H * T <= INT32_MAX,
+              "pcl_attn_fwd: B*T or B*H*T beyond 2^31");
+    PCL_OK_OR_RETURN(do_init());
+    HIP_OK(pcl::launch_attn_fwd(Q, K, V, ld, att, ld_att, probs, B, T, H, dh,
+                                1.0f / sqrtf((float)dh), pick(stream)));
     return PCL_OK;
 }
 
@@ -622,6 +654,21 @@ void bias_bwd(float *db, const float *dY, int M, int N) {
     finish_void(pcl_bias_bwd(db, dY, M, N, N, nullptr));
 }
 
+static int need_attn_dims(const char *who) {
+    if (g_d_model <= 0 || g_attn_heads <= 0 || g_attn_batch <= 0)
+        return set_error(PCL_ERR_UNSET_DIMS,
+                         "%s: call pcl_set_model_dims and pcl_set_attn_dims first", who);
+    return PCL_OK;
+}
+
+void attn_fwd(const float *Q, const float *K, const float *V, float *att, float *probs) {
+    int st = need_attn_dims("attn_fwd");
+    if (st == PCL_OK)
+        st = pcl_attn_fwd(Q, K, V, g_d_model, att, g_d_model, probs, g_attn_batch, g_attn_seq,
+                          g_attn_heads, g_d_model / g_attn_heads, nullptr);
+    finish_void(st);
+}
+
 // --------------------------------------------------- host-pointer drop-ins ----
 // Slot numbers name the staging buffer each operand uses.
 enum { S_A = 0, S_B, S_C, S_BIAS, S_D, S_E, S_F, S_G };
@@ -683,6 +730,34 @@ static int host_matmul_backward(const float *dY, const float *X, const float *Wt
 void matmul_backward(const float *dY, const float *X, const float *Wt, float *dX, float *dW,
                      float *db, int M, int K, int N) {
     finish_void(host_matmul_backward(dY, X, Wt, dX, dW, db, M, K, N));
+}
+
+static int host_attention_forward(const float *q, const float *k, const float *v, float *att,
+                                  float *probs, int B, int T) {
+    PCL_OK_OR_RETURN(need_attn_dims("attention_forward"));
+    CHECK_ARG(B >= 0 && T >= 0, "attention_forward: negative dimension (B=%d T=%d)", B, T);
+    if (B == 0 || T == 0) return PCL_OK;
+    CHECK_ARG(q && k && v && att && probs, "attention_forward: NULL operand");
+    const int D = g_d_model, H = g_attn_heads;
+    CHECK_ARG(D % H == 0, "attention_forward: d_model %d not divisible by %d heads", D, H);
+    PCL_OK_OR_RETURN(do_init());
+    const size_t act = sizeof(float) * (size_t)B * T * D, pb = sizeof(float) * (size_t)B * H * T * T;
+    void *dq, *dk, *dv, *datt, *dp;
+    PCL_OK_OR_RETURN(upload(S_A, q, act, &dq));
+    PCL_OK_OR_RETURN(upload(S_B, k, act, &dk));
+    PCL_OK_OR_RETURN(upload(S_D, v, act, &dv));
+    PCL_OK_OR_RETURN(stage_buf(S_C, act, &datt));
+    PCL_OK_OR_RETURN(stage_buf(S_E, pb, &dp));
+    PCL_OK_OR_RETURN(pcl_attn_fwd((const float *)dq, (const float *)dk, (const float *)dv, D,
+                                  (float *)datt, D, (float *)dp, B, T, H, D / H, t_stream));
+    PCL_OK_OR_RETURN(download(att, datt, act));
+    PCL_OK_OR_RETURN(download(probs, dp, pb));
+    return sync_current();
+}
+
+void attention_forward(const float *q, const float *k, const float *v, float *att, float *probs,
+                       int B, int T) {
+    finish_void(host_attention_forward(q, k, v, att, probs, B, T));
 }
 
 static int need_dims(const char *who) {

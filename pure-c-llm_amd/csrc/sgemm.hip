@@ -325,13 +325,14 @@ __device__ __forceinline__ void sd_fence(v4f &r) { asm volatile("" : "+v"(r)); }
 __device__ __forceinline__ void sd_fence(float &r) { asm volatile("" : "+v"(r)); }
 constexpr int sd_waitcnt_vm(int n) { return (n & 15) | (((n >> 4) & 3) << 14) | (7 << 4) | (15 << 8); }
 
-// One operand's tile in the LDS ring: ROWS (M or N) x SD_BK (K) floats.
-template <int ROWS, bool KC, int NW>
+// One operand's part of a ring stage: SUB consecutive K tiles of ROWS (M or
+// N) x SD_BK (K) floats, tile s at byte SUBB * s of the stage.
+template <int ROWS, bool KC, int NW, int SUB, int SUBB>
 struct DmaTile {
-    static constexpr int BYTES = ROWS * SD_BK * 4;  // ROWS * 128
-    static constexpr int INST = BYTES / 1024;        // DMA instructions per tile
-    static constexpr int PER_WAVE = INST / NW;
-    static_assert(INST % NW == 0, "DMA instructions must split over the waves");
+    static constexpr int BYTES = ROWS * SD_BK * 4;  // ROWS * 128, one K tile
+    static constexpr int INST = BYTES / 1024;        // DMA instructions per K tile
+    static constexpr int PER_WAVE = SUB * INST / NW;
+    static_assert((SUB * INST) % NW == 0, "DMA instructions must split over the waves");
     static constexpr int CHR = KC ? 8 : ROWS / 4;    // 16-byte chunks per LDS row
     static_assert(KC || CHR >= 16, "MN swizzle needs 16 chunks per k-row");
 
@@ -342,21 +343,21 @@ struct DmaTile {
                                                  long ld) {
 #pragma unroll
         for (int q = 0; q < PER_WAVE; q++) {
-            const int inst = q * NW + wave;
+            const int sub = (q * NW + wave) / INST, inst = (q * NW + wave) % INST;
             if (KC) {
                 const int r = inst * 8 + lane / 8;
                 const int gc = (lane % 8) ^ ((r >> 1) & 7);
-                voff[q] = (long)min(rows0 + r, nrows - 1) * ld + gc * 4;
+                voff[q] = (long)min(rows0 + r, nrows - 1) * ld + sub * SD_BK + gc * 4;
             } else {
                 const int rpi = 64 / CHR;  // k-rows per instruction
                 const int k = inst * rpi + lane / CHR;
                 const int gc = (lane % CHR) ^ (((k >> 2) & 1) << 3);
-                voff[q] = (long)k * ld + min(rows0 + gc * 4, nrows - 4);
+                voff[q] = (long)(sub * SD_BK + k) * ld + min(rows0 + gc * 4, nrows - 4);
             }
-            ldso[q] = inst * 1024;
+            ldso[q] = sub * SUBB + inst * 1024;
         }
     }
-    // issue this wave's DMA of the tile at k0 into the stage at lds_stage
+    // issue this wave's DMA of the SUB tiles from k0 into the stage at lds_stage
     __device__ __forceinline__ static void dma(const float *P, long ld, int k0, const long (&voff)[PER_WAVE],
                                                const int (&ldso)[PER_WAVE], int8_t *lds_stage) {
         const float *base = KC ? P + k0 : P + (long)k0 * ld;
@@ -368,24 +369,26 @@ struct DmaTile {
     }
 };
 
-template <int BM, int BN, int KG, int STAGES, bool A_KC, bool B_KC>
+template <int BM, int BN, int KG, int STAGES, int SUB, bool A_KC, bool B_KC>
 __global__ __launch_bounds__(256 * KG) void sgemm_dma_kernel(
     const float *__restrict__ A, long lda, const float *__restrict__ B, long ldb,
     const float *__restrict__ bias, float *__restrict__ C, long ldc, int M, int N, int K,
     int accumulate, int kchunk) {
     constexpr int NW = 4 * KG;
-    using TA = DmaTile<BM, A_KC, NW>;
-    using TB = DmaTile<BN, B_KC, NW>;
+    constexpr int SUBB = (BM + BN) * SD_BK * 4;  // one K tile of both operands
+    using TA = DmaTile<BM, A_KC, NW, SUB, SUBB>;
+    using TB = DmaTile<BN, B_KC, NW, SUB, SUBB>;
     constexpr int WTM = BM / 2, WTN = BN / 2, TM = WTM / 32, TN = WTN / 32;
     constexpr int KCH = SD_BK / 8;   // 8-deep k chunks per tile
     constexpr int KCG = KCH / KG;    // chunks per K group
-    constexpr int STAGE = TA::BYTES + TB::BYTES;
+    constexpr int STAGE = SUB * SUBB;
     constexpr int VH = 16 / KG;
     constexpr int XCH = KG > 1 ? KG * (KG - 1) * 256 * TM * TN * VH * 4 : 0;
     constexpr int LDS_BYTES = STAGES * STAGE > XCH ? STAGES * STAGE : XCH;
     constexpr int LOADS = TA::PER_WAVE + TB::PER_WAVE;
     static_assert(KCH % KG == 0 && STAGES >= 2, "tile configuration");
     static_assert((STAGES - 1) * LOADS <= 63, "vmcnt range");
+    static_assert(STAGE <= 65536, "ds_read offset field");
     static_assert(LDS_BYTES <= 160 * 1024, "LDS budget of a CU");
     __shared__ __attribute__((aligned(1024))) int8_t lds[LDS_BYTES];
 
@@ -405,7 +408,7 @@ __global__ __launch_bounds__(256 * KG) void sgemm_dma_kernel(
         B += B_KC ? kbeg : (long)kbeg * ldb;
         C += (long)blockIdx.y * M * ldc;
     }
-    const int nk = K / SD_BK;
+    const int nk = K / (SD_BK * SUB);  // ring stages (SUB K tiles each)
 
     long voa[TA::PER_WAVE], vob[TB::PER_WAVE];
     int lda_o[TA::PER_WAVE], ldb_o[TB::PER_WAVE];
@@ -413,8 +416,8 @@ __global__ __launch_bounds__(256 * KG) void sgemm_dma_kernel(
     TB::setup(vob, ldb_o, wave, lane, n0, N, ldb);
     auto dma = [&](int t) {
         int8_t *st = lds + (t % STAGES) * STAGE;
-        TA::dma(A, lda, t * SD_BK, voa, lda_o, st);
-        TB::dma(B, ldb, t * SD_BK, vob, ldb_o, st + TA::BYTES);
+        TA::dma(A, lda, t * SUB * SD_BK, voa, lda_o, st);
+        TB::dma(B, ldb, t * SUB * SD_BK, vob, ldb_o, st + TA::BYTES);
     };
 
     // Fragment addresses (bytes within a stage). K-contiguous operand: row
@@ -446,65 +449,70 @@ __global__ __launch_bounds__(256 * KG) void sgemm_dma_kernel(
             b_addr[j] = TA::BYTES + (kg * KCG * 8 + 4 * g) * BN * 4 + (((n >> 2) ^ (g << 3)) << 4) + (n & 3) * 4;
         }
     }
-    // Fragments of one tile, two slots (current and next tile). A K-contiguous
-    // operand fills one 16-byte register quad per block; an MN-contiguous one
-    // four separate floats (each its own read, so no register copy can run
-    // ahead of the wait).
-    v4f fak[2][KCG][A_KC ? TM : 1], fbk[2][KCG][B_KC ? TN : 1];
-    float fam[2][KCG][A_KC ? 1 : TM][4], fbm[2][KCG][B_KC ? 1 : TN][4];
+    // Fragments of one stage, two slots (current and next stage). A
+    // K-contiguous operand fills one 16-byte register quad per block; an
+    // MN-contiguous one four separate floats (each its own read, so no
+    // register copy can run ahead of the wait).
+    v4f fak[2][SUB][KCG][A_KC ? TM : 1], fbk[2][SUB][KCG][B_KC ? TN : 1];
+    float fam[2][SUB][KCG][A_KC ? 1 : TM][4], fbm[2][SUB][KCG][B_KC ? 1 : TN][4];
     auto read_tile = [&](auto SL, int t) {
         constexpr int sl = decltype(SL)::value;
         const unsigned st = lds0 + (t % STAGES) * STAGE;
+        static_for<0, SUB>([&](auto U) {
+        constexpr int u = decltype(U)::value, uo = u * SUBB;
         static_for<0, KCG>([&](auto Cc) {
             constexpr int c = decltype(Cc)::value;
             static_for<0, TM>([&](auto I) {
                 constexpr int i = decltype(I)::value;
                 if constexpr (A_KC) {
-                    sd_read128<i * 32 * 128>(fak[sl][c][i], st + a_addr[c]);
+                    sd_read128<uo + i * 32 * 128>(fak[sl][u][c][i], st + a_addr[c]);
                 } else {
-                    sd_read32<(c * 8 + 0) * BM * 4>(fam[sl][c][i][0], st + a_addr[i]);
-                    sd_read32<(c * 8 + 1) * BM * 4>(fam[sl][c][i][1], st + a_addr[i]);
-                    sd_read32<(c * 8 + 2) * BM * 4>(fam[sl][c][i][2], st + a_addr[i]);
-                    sd_read32<(c * 8 + 3) * BM * 4>(fam[sl][c][i][3], st + a_addr[i]);
+                    sd_read32<uo + (c * 8 + 0) * BM * 4>(fam[sl][u][c][i][0], st + a_addr[i]);
+                    sd_read32<uo + (c * 8 + 1) * BM * 4>(fam[sl][u][c][i][1], st + a_addr[i]);
+                    sd_read32<uo + (c * 8 + 2) * BM * 4>(fam[sl][u][c][i][2], st + a_addr[i]);
+                    sd_read32<uo + (c * 8 + 3) * BM * 4>(fam[sl][u][c][i][3], st + a_addr[i]);
                 }
             });
             static_for<0, TN>([&](auto J) {
                 constexpr int j = decltype(J)::value;
                 if constexpr (B_KC) {
-                    sd_read128<j * 32 * 128>(fbk[sl][c][j], st + b_addr[c]);
+                    sd_read128<uo + j * 32 * 128>(fbk[sl][u][c][j], st + b_addr[c]);
                 } else {
-                    sd_read32<(c * 8 + 0) * BN * 4>(fbm[sl][c][j][0], st + b_addr[j]);
-                    sd_read32<(c * 8 + 1) * BN * 4>(fbm[sl][c][j][1], st + b_addr[j]);
-                    sd_read32<(c * 8 + 2) * BN * 4>(fbm[sl][c][j][2], st + b_addr[j]);
-                    sd_read32<(c * 8 + 3) * BN * 4>(fbm[sl][c][j][3], st + b_addr[j]);
+                    sd_read32<uo + (c * 8 + 0) * BN * 4>(fbm[sl][u][c][j][0], st + b_addr[j]);
+                    sd_read32<uo + (c * 8 + 1) * BN * 4>(fbm[sl][u][c][j][1], st + b_addr[j]);
+                    sd_read32<uo + (c * 8 + 2) * BN * 4>(fbm[sl][u][c][j][2], st + b_addr[j]);
+                    sd_read32<uo + (c * 8 + 3) * BN * 4>(fbm[sl][u][c][j][3], st + b_addr[j]);
                 }
             });
+        });
         });
     };
     // after the wait: order every later use of slot sl after it
     auto fence_slot = [&](auto SL) {
         constexpr int sl = decltype(SL)::value;
-        static_for<0, KCG>([&](auto Cc) {
-            constexpr int c = decltype(Cc)::value;
+#pragma unroll
+        for (int u = 0; u < SUB; u++)
+#pragma unroll
+        for (int c = 0; c < KCG; c++) {
 #pragma unroll
             for (int i = 0; i < TM; i++) {
                 if constexpr (A_KC) {
-                    sd_fence(fak[sl][c][i]);
+                    sd_fence(fak[sl][u][c][i]);
                 } else {
 #pragma unroll
-                    for (int q = 0; q < 4; q++) sd_fence(fam[sl][c][i][q]);
+                    for (int q = 0; q < 4; q++) sd_fence(fam[sl][u][c][i][q]);
                 }
             }
 #pragma unroll
             for (int j = 0; j < TN; j++) {
                 if constexpr (B_KC) {
-                    sd_fence(fbk[sl][c][j]);
+                    sd_fence(fbk[sl][u][c][j]);
                 } else {
 #pragma unroll
-                    for (int q = 0; q < 4; q++) sd_fence(fbm[sl][c][j][q]);
+                    for (int q = 0; q < 4; q++) sd_fence(fbm[sl][u][c][j][q]);
                 }
             }
-        });
+        }
     };
 
     v16f acc[TM][TN];
@@ -540,8 +548,8 @@ __global__ __launch_bounds__(256 * KG) void sgemm_dma_kernel(
         __builtin_amdgcn_s_barrier();
         if (kt + STAGES < nk) dma(kt + STAGES);  // into the stage of tile kt, read by every wave
         if (kt + 1 < nk) read_tile(IC<sl ^ 1>{}, kt + 1);
-        static_for<0, KCG>([&](auto Cc) {
-            constexpr int c = decltype(Cc)::value;
+        static_for<0, SUB * KCG>([&](auto UC) {
+            constexpr int u = decltype(UC)::value / KCG, c = decltype(UC)::value % KCG;
             static_for<0, 4>([&](auto S) {
                 constexpr int s4 = decltype(S)::value;
                 static_for<0, TM>([&](auto I) {
@@ -549,10 +557,10 @@ __global__ __launch_bounds__(256 * KG) void sgemm_dma_kernel(
                     static_for<0, TN>([&](auto J) {
                         constexpr int j = decltype(J)::value;
                         float av, bv;
-                        if constexpr (A_KC) av = fak[sl][c][i][s4];
-                        else av = fam[sl][c][i][s4];
-                        if constexpr (B_KC) bv = fbk[sl][c][j][s4];
-                        else bv = fbm[sl][c][j][s4];
+                        if constexpr (A_KC) av = fak[sl][u][c][i][s4];
+                        else av = fam[sl][u][c][i][s4];
+                        if constexpr (B_KC) bv = fbk[sl][u][c][j][s4];
+                        else bv = fbm[sl][u][c][j][s4];
                         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, acc[i][j], 0, 0, 0);
                     });
                 });
@@ -625,13 +633,13 @@ __global__ __launch_bounds__(256 * KG) void sgemm_dma_kernel(
     }
 }
 
-template <int BM, int BN, int KG, int STAGES, bool A_KC, bool B_KC>
+template <int BM, int BN, int KG, int STAGES, int SUB, bool A_KC, bool B_KC>
 static hipError_t launch_dma(int M, int N, int K, int splits, int kchunk, const float *A, long lda,
                              const float *B, long ldb, const float *bias, int accumulate, float *C,
                              long ldc, hipStream_t stream) {
     const int nblk = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
     if (nblk == 0) return hipSuccess;
-    hipLaunchKernelGGL((sgemm_dma_kernel<BM, BN, KG, STAGES, A_KC, B_KC>), dim3(nblk, splits),
+    hipLaunchKernelGGL((sgemm_dma_kernel<BM, BN, KG, STAGES, SUB, A_KC, B_KC>), dim3(nblk, splits),
                        dim3(256 * KG), 0, stream, A, lda, B, ldb, bias, C, ldc, M, N, K, accumulate,
                        kchunk);
     return hipGetLastError();
@@ -728,10 +736,10 @@ static hipError_t dispatch_layout(const SgemmPlan &p, int M, int N, int K, const
     const bool dma_ok = vec && K % SD_BK == 0;
     if (dma_ok) {
         if (p.cfg == SG_64_KG2)
-            e = launch_dma<64, 64, 2, 4, A_KC, B_KC>(M, N, K, p.splits, p.kchunk, A, lda, B, ldb, b,
+            e = launch_dma<64, 64, 2, 4, 1, A_KC, B_KC>(M, N, K, p.splits, p.kchunk, A, lda, B, ldb, b,
                                                      acc, out, ldo, stream);
         else
-            e = launch_dma<128, 128, 2, 4, A_KC, B_KC>(M, N, K, p.splits, p.kchunk, A, lda, B, ldb, b,
+            e = launch_dma<128, 128, 2, 4, 1, A_KC, B_KC>(M, N, K, p.splits, p.kchunk, A, lda, B, ldb, b,
                                                        acc, out, ldo, stream);
     } else switch (p.cfg) {
     case SG_128_BK16:

@@ -67,6 +67,7 @@ _PROTOS = {
     "pcl_event_elapsed_ms": (_i, [_vp, _vp, C.POINTER(_f)]),
     "pcl_event_destroy": (_i, [_vp]),
     "pcl_set_model_dims": (_i, [_i, _i]),
+    "pcl_set_attn_dims": (_i, [_i, _i, _i]),
     # host-pointer drop-ins
     "matmul": (None, [_vp, _vp, _vp, _i, _i, _i]),
     "matmul_forward": (None, [_vp, _vp, _vp, _vp, _i, _i, _i]),
@@ -79,16 +80,19 @@ _PROTOS = {
     "quantize_A": (_f, [_vp, _vp, _i, _i, _i]),
     "quantize_B_pack": (None, [_vp, _vp, _vp, _vp, _i, _i, _i]),
     "gemm_int8_kernel": (None, [_vp, _i, _vp, _vp, _vp, _vp, _i, _i]),
+    "attention_forward": (None, [_vp, _vp, _vp, _vp, _vp, _i, _i]),
     # device-pointer drop-ins
     "gpu_init": (None, []),
     "gemm_nn": (None, [_vp, _vp, _vp, _vp, _i, _i, _i]),
     "gemm_nt": (None, [_vp, _vp, _vp, _i, _i, _i, _i]),
     "gemm_tn": (None, [_vp, _vp, _vp, _i, _i, _i]),
     "bias_bwd": (None, [_vp, _vp, _i, _i]),
+    "attn_fwd": (None, [_vp, _vp, _vp, _vp, _vp]),
     # native
     "pcl_sgemm": (_i, [_i, _i, _i, _i, _i, _vp, _i, _vp, _i, _vp, _i, _vp, _i, _vp]),
     "pcl_sgemv": (_i, [_i, _i, _i, _i, _vp, _i, _vp, _i, _vp, _i, _vp, _i, _vp]),
     "pcl_bias_bwd": (_i, [_vp, _vp, _i, _i, _i, _vp]),
+    "pcl_attn_fwd": (_i, [_vp, _vp, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i, _vp]),
     "pcl_s8_kpad": (_i, [_i]),
     "pcl_s8_packed_bytes": (_sz, [_i, _i]),
     "pcl_pack_b_s8": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp]),

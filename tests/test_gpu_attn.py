@@ -1,0 +1,153 @@
+"""Causal attention parity on the GPU: pcl_attn_fwd (f32 MFMA, one fused launch)
+against the CPU oracle (train.c:339-370 restated, pinned by the reference
+built from source in tests/test_oracle.py).
+
+Tolerance: max|X-R|/max|R| <= 1e-4 for att and for the stored probabilities,
+the north-star fp32 bar. At the full 350M-class shape (B=4, T=1024, 16 heads of
+64) sampled query rows are checked against f64 numpy, and every probability row
+against the sizes-independent facts: each row sums to one and is zero above
+the diagonal.
+"""
+import numpy as np
+import pytest
+
+import binding as ob
+import pcl
+from gpu_util import FP32_TOL, announce, rel, require_device
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _device():
+    require_device()
+
+
+def _qkv(B, T, ld, seed, std=1.0):
+    return tuple(ob.normal((B * T, ld), seed + i, 0.0, std) for i in range(3))
+
+
+def attn(q, k, v, B, T, H, dh, ld=None, probs=True, cols=(0, 0, 0)):
+    """pcl_attn_fwd on device copies; q/k/v may share one buffer (cols = column
+    offsets of Q, K, V inside it). Returns (att, probs or None)."""
+    ld = q.shape[1] if ld is None else ld
+    bufs = {}
+    ptrs = []
+    for a, c in zip((q, k, v), cols):
+        key = id(a)
+        if key not in bufs:
+            bufs[key] = pcl.dev(a)
+        ptrs.append(bufs[key].ptr + 4 * c)
+    datt = pcl.dev(np.full((B * T, H * dh), np.nan, np.float32))
+    dp = pcl.dev(np.full((B * H, T, T), np.nan, np.float32)) if probs else None
+    pcl.check(pcl.lib.pcl_attn_fwd(ptrs[0], ptrs[1], ptrs[2], ld, datt.ptr, H * dh,
+                                   dp.ptr if dp else None, B, T, H, dh, None))
+    pcl.sync()
+    att = datt.download((B * T, H * dh), np.float32)
+    return att, (dp.download((B * H, T, T), np.float32) if dp else None)
+
+
+SHAPES = [(1, 1, 1, 32), (2, 33, 2, 32), (1, 128, 1, 64), (2, 200, 2, 64), (1, 129, 3, 128),
+          (3, 256, 2, 128), (1, 300, 4, 32)]
+
+
+@pytest.mark.parametrize("B,T,H,dh", SHAPES)
+def test_attn_fwd_vs_oracle(B, T, H, dh):
+    announce("attn_fwd", B, T, H, dh)
+    q, k, v = _qkv(B, T, H * dh, 300 + T + dh)
+    att, pr = attn(q, k, v, B, T, H, dh)
+    att_r, pr_r = ob.attention_forward(q, k, v, B, T, H, dh)
+    assert rel(att, att_r) <= FP32_TOL
+    assert rel(pr, pr_r) <= FP32_TOL
+    assert np.all(np.triu(pr, 1) == 0.0)
+
+
+def test_attn_fwd_without_probs_is_identical():
+    B, T, H, dh = 2, 160, 2, 64
+    announce("attn_fwd probs=NULL", B, T, H, dh)
+    q, k, v = _qkv(B, T, H * dh, 410)
+    a1, _ = attn(q, k, v, B, T, H, dh)
+    a2, _ = attn(q, k, v, B, T, H, dh, probs=False)
+    np.testing.assert_array_equal(a1, a2)
+
+
+def test_attn_fwd_fused_qkv_buffer():
+    # Q, K, V as column slices of one (B*T) x 3D buffer (the fused QKV GEMM output)
+    B, T, H, dh = 2, 96, 4, 32
+    D = H * dh
+    announce("attn_fwd fused qkv", B, T, H, dh)
+    qkv = ob.normal((B * T, 3 * D), 420)
+    att, pr = attn(qkv, qkv, qkv, B, T, H, dh, ld=3 * D, cols=(0, D, 2 * D))
+    q, k, v = (np.ascontiguousarray(qkv[:, i * D:(i + 1) * D]) for i in range(3))
+    att_r, pr_r = ob.attention_forward(q, k, v, B, T, H, dh)
+    assert rel(att, att_r) <= FP32_TOL
+    assert rel(pr, pr_r) <= FP32_TOL
+
+
+def test_attn_fwd_large_scores():
+    # scores of magnitude ~100 (no overflow: the row max is subtracted first)
+    B, T, H, dh = 1, 64, 1, 64
+    announce("attn_fwd large scores")
+    q, k, v = _qkv(B, T, H * dh, 430, std=3.5)
+    att, pr = attn(q, k, v, B, T, H, dh)
+    att_r, pr_r = ob.attention_forward(q, k, v, B, T, H, dh)
+    assert np.isfinite(att).all()
+    assert rel(att, att_r) <= FP32_TOL
+    assert rel(pr, pr_r) <= FP32_TOL
+
+
+@pytest.mark.parametrize("B,T,H,dh", [(4, 1024, 16, 64), (4, 1024, 12, 128), (1, 256, 16, 32)])
+def test_attn_fwd_full_size_properties(B, T, H, dh):
+    # 350M-class (16 heads of 64, B=4, T=1024), the reference GPU trainer's heads
+    # (12 of 128) and the grown model (16 of 32, T=256)
+    announce("attn_fwd full", B, T, H, dh)
+    q, k, v = _qkv(B, T, H * dh, 440 + dh)
+    att, pr = attn(q, k, v, B, T, H, dh)
+    np.testing.assert_allclose(pr.sum(axis=2, dtype=np.float64), 1.0, rtol=0, atol=2e-5)
+    assert np.all(np.triu(pr, 1) == 0.0)
+    rng = np.random.default_rng(7)
+    scale = 1.0 / np.sqrt(np.float32(dh))
+    worst = 0.0
+    for _ in range(24):
+        b, h, i = int(rng.integers(B)), int(rng.integers(H)), int(rng.integers(T))
+        rows = slice(b * T, b * T + i + 1)
+        cols = slice(h * dh, (h + 1) * dh)
+        s = (k[rows, cols].astype(np.float64) @ q[b * T + i, cols].astype(np.float64)) * np.float64(scale)
+        p = np.exp(s - s.max())
+        p /= p.sum()
+        o = p @ v[rows, cols].astype(np.float64)
+        worst = max(worst, rel(att[b * T + i, cols], o), rel(pr[b * H + h, i, : i + 1], p))
+    assert worst <= FP32_TOL
+
+
+def test_attention_dropins():
+    # train.c attention_forward (host pointers) and gpu_kernels.h attn_fwd
+    # (device pointers), dims from pcl_set_model_dims / pcl_set_attn_dims
+    B, T, H, dh = 2, 64, 4, 32
+    D = H * dh
+    announce("attention drop-ins", B, T, H, dh)
+    pcl.check(pcl.lib.pcl_set_model_dims(D, 96))
+    pcl.check(pcl.lib.pcl_set_attn_dims(B, T, H))
+    q, k, v = _qkv(B, T, D, 450)
+    att = np.zeros((B * T, D), np.float32)
+    pr = np.zeros((B * H, T, T), np.float32)
+    pcl.lib.attention_forward(pcl.ptr(q), pcl.ptr(k), pcl.ptr(v), pcl.ptr(att), pcl.ptr(pr), B, T)
+    pcl.check_void()
+    att_r, pr_r = ob.attention_forward(q, k, v, B, T, H, dh)
+    assert rel(att, att_r) <= FP32_TOL and rel(pr, pr_r) <= FP32_TOL
+    dq, dk, dv = pcl.dev(q), pcl.dev(k), pcl.dev(v)
+    datt, dp = pcl.empty((B * T, D), np.float32), pcl.empty((B * H, T, T), np.float32)
+    pcl.lib.attn_fwd(dq.ptr, dk.ptr, dv.ptr, datt.ptr, dp.ptr)
+    pcl.check_void()
+    pcl.sync()
+    np.testing.assert_array_equal(datt.download((B * T, D), np.float32), att)
+    np.testing.assert_array_equal(dp.download((B * H, T, T), np.float32), pr)
+
+
+def test_attn_fwd_argument_errors():
+    q = pcl.empty((64, 64), np.float32)
+    for args in [(q.ptr, q.ptr, q.ptr, 64, q.ptr, 64, None, 1, 64, 1, 48, None),   # head size
+                 (q.ptr, q.ptr, q.ptr, 30, q.ptr, 64, None, 1, 64, 1, 32, None),   # ld < H*dh
+                 (q.ptr + 4, q.ptr, q.ptr, 64, q.ptr, 64, None, 1, 16, 1, 32, None)]:  # alignment
+        assert pcl.lib.pcl_attn_fwd(*args) == pcl.PCL_ERR_INVALID_ARG
+        pcl.lib.pcl_clear_error()

@@ -357,3 +357,94 @@ def test_oracle_vs_ref_train_and_model():
     md.pcl_ref_proj_token(p(y_r), p(x), p(Wp), None, 130, 77)
     O().orc_matvec(p(y_o), p(x), p(Wp), None, 1, 130, 77)
     assert ob.normwise_rel_err(y_o, y_r) < REF_TOL
+
+
+# ------------------------------------------------------------ attention ----
+def _qkv(B, T, D, seed, std=1.0):
+    return (ob.normal((B * T, D), seed, 0.0, std), ob.normal((B * T, D), seed + 1, 0.0, std),
+            ob.normal((B * T, D), seed + 2, 0.0, std))
+
+
+@pytest.mark.parametrize("lib", ["libref_train.so", "libref_train_h64.so"])
+def test_attention_oracle_vs_ref_train(lib):
+    # train.c:339-407 compiled from source at d_head 16 (D=64, 4 heads, T<=16)
+    # and d_head 64 (D=128, 2 heads, T<=64); forward and accumulating backward
+    tr = _ref_or_skip(lib)
+    D, H, Tmax = tr.pcl_ref_train_d_model(), tr.pcl_ref_train_n_heads(), tr.pcl_ref_train_t_size()
+    dh = D // H
+    B, T = 3, Tmax - 3
+    q, k, v = _qkv(B, T, D, 91)
+    att_r = np.zeros((B * T, D), np.float32)
+    pr_r = np.zeros((B * H, T, T), np.float32)
+    tr.pcl_ref_attention_forward(p(q), p(k), p(v), p(att_r), p(pr_r), B, T)
+    att_o, pr_o = ob.attention_forward(q, k, v, B, T, H, dh)
+    assert ob.normwise_rel_err(att_o, att_r) < REF_TOL
+    assert ob.normwise_rel_err(pr_o, pr_r) < REF_TOL
+    d_att = ob.normal((B * T, D), 95)
+    grads_r = [np.ones((B * T, D), np.float32) for _ in range(3)]
+    tr.pcl_ref_attention_backward(p(grads_r[0]), p(grads_r[1]), p(grads_r[2]), p(d_att), p(q), p(k),
+                                  p(v), p(pr_r), B, T)
+    grads_o = ob.attention_backward(d_att, q, k, v, pr_o, B, T, H, dh,
+                                    *[np.ones((B * T, D), np.float32) for _ in range(3)])
+    for a, b in zip(grads_o, grads_r):
+        assert ob.normwise_rel_err(a, b) < REF_TOL
+
+
+def test_attention_oracle_closed_forms():
+    B, T, H, dh = 2, 9, 2, 32
+    D = H * dh
+    q, k, v = _qkv(B, T, D, 101)
+    # T = 1: the single probability is 1 and att = v
+    att, pr = ob.attention_forward(q[:1], k[:1], v[:1], 1, 1, H, dh)
+    np.testing.assert_array_equal(att, v[:1])
+    assert np.all(pr == 1.0)
+    # equal keys: uniform probabilities 1/(i+1), att_i = running mean of v
+    kc = np.repeat(k[:1], B * T, axis=0)
+    att, pr = ob.attention_forward(q, kc, v, B, T, H, dh)
+    for b in range(B):
+        for i in range(T):
+            want = v[b * T: b * T + i + 1].astype(np.float64).mean(axis=0)
+            np.testing.assert_allclose(att[b * T + i], want, rtol=0, atol=1e-5)
+            np.testing.assert_allclose(pr[b * H, i, : i + 1], 1.0 / (i + 1), rtol=1e-6)
+    # rows of p sum to one, zero above the diagonal
+    att, pr = ob.attention_forward(q, k, v, B, T, H, dh)
+    np.testing.assert_allclose(pr.sum(axis=2), 1.0, rtol=0, atol=1e-6)
+    assert np.all(np.triu(pr, 1) == 0.0)
+
+
+@pytest.mark.parametrize("dh", [32, 64, 128])
+def test_attention_oracle_vs_f64(dh):
+    B, T, H = 2, 40, 2
+    q, k, v = _qkv(B, T, H * dh, 111)
+    a32, p32 = ob.attention_forward(q, k, v, B, T, H, dh)
+    a64, p64 = ob.attention_forward(q, k, v, B, T, H, dh, f64=True)
+    assert ob.normwise_rel_err(a32, a64) < 1e-5
+    assert ob.normwise_rel_err(p32, p64) < 1e-5
+
+
+def test_attention_backward_vs_central_differences():
+    # L = sum(G * att) with the f64 forward; dL/dx by central differences at
+    # sampled entries of q, k, v against the accumulating backward
+    B, T, H, dh = 1, 7, 2, 32
+    D = H * dh
+    q, k, v = _qkv(B, T, D, 121, std=0.5)
+    G = ob.normal((B * T, D), 125)
+    _, pr = ob.attention_forward(q, k, v, B, T, H, dh)
+    dq, dk, dv = ob.attention_backward(G, q, k, v, pr, B, T, H, dh)
+    rng = np.random.default_rng(5)
+
+    def loss(qq, kk, vv):
+        a, _ = ob.attention_forward(qq, kk, vv, B, T, H, dh, f64=True)
+        return float(np.sum(G.astype(np.float64) * a))
+
+    eps = 1e-2
+    for which, grad in ((0, dq), (1, dk), (2, dv)):
+        for _ in range(6):
+            r, c = int(rng.integers(B * T)), int(rng.integers(D))
+            xs = [q.copy(), k.copy(), v.copy()]
+            xs[which][r, c] += eps
+            lp = loss(*xs)
+            xs[which][r, c] -= 2 * eps
+            lm = loss(*xs)
+            num = (lp - lm) / (2 * eps)
+            assert abs(num - grad[r, c]) < 2e-3 * max(1.0, abs(num)), (which, r, c, num, grad[r, c])
