@@ -44,7 +44,10 @@ def load_bench():
     lib.pcl_bench_sgemm.argtypes = [i, i, i, i, i, i, i, i, C.POINTER(d)]
     lib.pcl_bench_gemv.argtypes = [C.POINTER(i), i, i, C.POINTER(i), C.POINTER(i), i, i, i, i, C.POINTER(d),
                                    C.POINTER(d)]
-    for f in (lib.pcl_bench_igemm, lib.pcl_bench_sgemm, lib.pcl_bench_gemv):
+    lib.pcl_bench_attn.argtypes = [i, i, i, i, i, i, i, C.POINTER(d)]
+    lib.pcl_bench_attn_bwd.argtypes = [i, i, i, i, i, i, C.POINTER(d)]
+    for f in (lib.pcl_bench_igemm, lib.pcl_bench_sgemm, lib.pcl_bench_gemv, lib.pcl_bench_attn,
+              lib.pcl_bench_attn_bwd):
         f.restype = i
     return pcl, lib
 
@@ -88,6 +91,38 @@ def gemv(pcl, lib, kind, M, shapes, copies, warmup, steps, graph=False):
     gbs = by.value / (per * 1e-3) / 1e9
     return {"M": M, "ms_per_sweep": round(per, 5), "bytes_per_sweep": int(by.value), "GBps": round(gbs, 1),
             "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "weight_copies": copies, "graph": bool(graph)}
+
+
+def attn(pcl, lib, B, T, H, dh, with_probs, warmup, steps):
+    """Causal attention forward. Algorithmic FLOPs: QK^T and PV over the causal
+    triangle including the diagonal, 4*B*H*dh*T(T+1)/2; the kernel issues 1.5x
+    that on the matrix cores (the scores are computed in both passes)."""
+    ms = C.c_double(0)
+    _check(pcl, lib.pcl_bench_attn(B, T, H, dh, int(with_probs), warmup, steps, C.byref(ms)),
+           f"attn B{B} T{T} H{H} dh{dh}")
+    per = ms.value / steps
+    flops = 4.0 * B * H * dh * T * (T + 1) / 2
+    tf = flops / (per * 1e-3) / 1e12
+    probs_bytes = 4.0 * B * H * T * T if with_probs else 0.0
+    return {"B": B, "T": T, "H": H, "dh": dh, "probs": bool(with_probs), "ms": round(per, 5),
+            "TFLOPS": round(tf, 2), "frac_peak": round(tf / PEAK_F32_TFLOPS, 4),
+            "mfma_TFLOPS_issued": round(1.5 * tf, 2),
+            "probs_GBps": round(probs_bytes / (per * 1e-3) / 1e9, 1)}
+
+
+def attn_bwd(pcl, lib, B, T, H, dh, warmup, steps):
+    """Causal attention backward from stored probabilities. Algorithmic FLOPs:
+    dV, dP, dQ, dK over the causal triangle, 8*B*H*dh*T(T+1)/2 (dP is issued
+    twice: 1.25x); HBM: P read three times, dS written once and read once."""
+    ms = C.c_double(0)
+    _check(pcl, lib.pcl_bench_attn_bwd(B, T, H, dh, warmup, steps, C.byref(ms)), f"attn_bwd B{B} T{T} H{H} dh{dh}")
+    per = ms.value / steps
+    flops = 8.0 * B * H * dh * T * (T + 1) / 2
+    tf = flops / (per * 1e-3) / 1e12
+    tt_bytes = 5 * 4.0 * B * H * T * (T + 1) / 2
+    return {"B": B, "T": T, "H": H, "dh": dh, "ms": round(per, 5), "TFLOPS": round(tf, 2),
+            "frac_peak": round(tf / PEAK_F32_TFLOPS, 4), "mfma_TFLOPS_issued": round(1.25 * tf, 2),
+            "causal_TT_GBps": round(tt_bytes / (per * 1e-3) / 1e9, 1)}
 
 
 def read_traffic():
@@ -148,6 +183,11 @@ CASES = {
     "int8_ffn_up": lambda pcl, lib, w, s: igemm(pcl, lib, 4096, 4096, 1024, 2, w, s),
     "fp32_1024": lambda pcl, lib, w, s: sgemm(pcl, lib, 0, 0, 1024, 1024, 1024, 0, w, s),
     "fp32_ffn_up": lambda pcl, lib, w, s: sgemm(pcl, lib, 0, 0, 4096, 4096, 1024, 0, w, s),
+    "attn_350m": lambda pcl, lib, w, s: attn(pcl, lib, 4, 1024, 16, 64, True, w, s),
+    "attn_350m_noprobs": lambda pcl, lib, w, s: attn(pcl, lib, 4, 1024, 16, 64, False, w, s),
+    "attn_trainer_dh128": lambda pcl, lib, w, s: attn(pcl, lib, 4, 1024, 12, 128, True, w, s),
+    "attn_bwd_350m": lambda pcl, lib, w, s: attn_bwd(pcl, lib, 4, 1024, 16, 64, w, s),
+    "attn_bwd_trainer_dh128": lambda pcl, lib, w, s: attn_bwd(pcl, lib, 4, 1024, 12, 128, w, s),
     "gemv_head_fp32_m1": lambda pcl, lib, w, s: gemv(pcl, lib, 1, 1, [(1024, 50257)], 3, w, s),
     "gemv_head_int8_m1": lambda pcl, lib, w, s: gemv(pcl, lib, 2, 1, [(1024, 50257)], 6, w, s),
     "gemv_head_fp32_m8": lambda pcl, lib, w, s: gemv(pcl, lib, 1, 8, [(1024, 50257)], 3, w, s),
@@ -256,7 +296,7 @@ def main():
         "data": "synthetic (xorshift32 u8 activations, s8 weights, scales U[1e-3,1e-2])",
         "config": {"workload": "gemm_bench INT8 GEMM M=N=K=2048, u8 x s8 -> int32, per-row x per-column dequant "
                                "to fp32 (BASELINE.json configs[1])",
-                   "M": M, "N": N, "K": K, "kernel": "igemm_mfma_kernel (v_mfma_i32_32x32x32_i8)",
+                   "M": M, "N": N, "K": K, "kernel": "igemm_wp_kernel (producer/consumer waves, v_mfma_i32_32x32x32_i8)",
                    "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": tops, "peak": PEAK_I8_TOPS, "unit": "TOP/s",
                      "frac": round(tops / PEAK_I8_TOPS, 4), "traffic": read_traffic(),
@@ -308,6 +348,19 @@ def main():
         ex["grown_decode_gemv"] = dec
         ex["head_350m_gemv_fp32"] = {f"M{Mt}": gemv(pcl, lib, 1, Mt, [(1024, 50257)], 3, 2, 20) for Mt in (1, 8)}
         ex["head_350m_gemv_int8"] = {f"M{Mt}": gemv(pcl, lib, 2, Mt, [(1024, 50257)], 6, 2, 20) for Mt in (1, 8)}
+        # causal attention forward: 350M-class (16 heads of 64, B=4, T=1024),
+        # the reference GPU trainer's heads (12 of 128), the grown model (16 of 32, T=256)
+        ex["attn_fwd"] = {
+            "350m_probs": attn(pcl, lib, 4, 1024, 16, 64, True, w, s),
+            "350m_no_probs": attn(pcl, lib, 4, 1024, 16, 64, False, w, s),
+            "trainer_dh128_probs": attn(pcl, lib, 4, 1024, 12, 128, True, w, s),
+            "grown_t256_probs": attn(pcl, lib, 1, 256, 16, 32, True, w, 50),
+        }
+        ex["attn_bwd"] = {
+            "350m": attn_bwd(pcl, lib, 4, 1024, 16, 64, w, s),
+            "trainer_dh128": attn_bwd(pcl, lib, 4, 1024, 12, 128, w, s),
+            "grown_t256": attn_bwd(pcl, lib, 1, 256, 16, 32, w, 50),
+        }
         out["extra"] = ex
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(M, N, K)

@@ -150,6 +150,11 @@ void matvec(float *out, const float *x, const float *W, const float *b, int K, i
 void attention_forward(const float *q, const float *k, const float *v, float *att, float *probs,
                        int B, int T);
 
+/* train.c:374-407: given d_att and the forward's probs, dq, dk, dv ACCUMULATE
+ * the attention gradients (same layouts and dims as attention_forward). */
+void attention_backward(float *dq, float *dk, float *dv, const float *d_att, const float *q,
+                        const float *k, const float *v, const float *probs, int B, int T);
+
 /* gemm_bench.c:225-236: per-tensor symmetric quantisation to u8 (+128 offset),
  * K padded to Kpad with 128. Returns the scale amax*fl(1/127). */
 float quantize_A(const float *A, uint8_t *Au, int M, int K, int Kpad);
@@ -181,6 +186,10 @@ void bias_bwd(float *db, const float *dY, int M, int N);
  * N_HEADS heads (pcl_set_attn_dims / pcl_set_model_dims); probs [B*H][T][T]
  * normalised, zero above the diagonal (gpu_kernels.cu:264-281, 403-432). */
 void attn_fwd(const float *Q, const float *K, const float *V, float *att, float *probs);
+/* gpu_kernels.h:65-68: dQ, dK, dV SET (gpu_kernels.cu:437-486, beta = 0) from
+ * dAtt and the forward's probs; scratch holds B*H*T*T floats (dS). */
+void attn_bwd(float *dQ, float *dK, float *dV, float *scratch, const float *dAtt, const float *Q,
+              const float *K, const float *V, const float *probs);
 
 /* ============================== 3. native entry points =================== */
 
@@ -211,6 +220,17 @@ int pcl_bias_bwd(float *db, const float *dY, int M, int N, int ld, void *stream)
  * Q/K/V may be column slices of one fused (B*T) x 3D QKV buffer (ld = 3D). */
 int pcl_attn_fwd(const float *Q, const float *K, const float *V, int ld, float *att, int ld_att,
                  float *probs, int B, int T, int H, int dh, void *stream);
+
+/* Its backward from the stored probs (train.c:374-407, gpu_kernels.cu:437-486):
+ *   dP_ij = dAtt_i.v_j, D_i = sum_j p_ij dP_ij, dS_ij = p_ij (dP_ij - D_i)/sqrtf(dh),
+ *   dQ_i = sum_j dS_ij k_j, dK_j = sum_i dS_ij q_i, dV_j = sum_i p_ij dAtt_i.
+ * dQ, dK, dV ((B*T) x ld_grad) are set, or added to with accumulate != 0
+ * (train.c's convention). scratch: NULL (library workspace) or B*H*T*T floats,
+ * left holding dS for j <= i. Two launches on the stream; layouts and limits as
+ * pcl_attn_fwd, dAtt (B*T) x ld_att 16-byte aligned. */
+int pcl_attn_bwd(float *dQ, float *dK, float *dV, int ld_grad, float *scratch, const float *dAtt,
+                 int ld_att, const float *Q, const float *K, const float *V, int ld,
+                 const float *probs, int B, int T, int H, int dh, int accumulate, void *stream);
 
 /* ---- INT8: u8 activations x s8 weights -> int32 (gemm_bench.c:212-285) ----
  * Weights live in the GPU-native packed layout: N rows of Kp = pcl_s8_kpad(K)

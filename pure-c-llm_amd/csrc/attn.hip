@@ -97,9 +97,13 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const float *__restric
     __shared__ __attribute__((aligned(16))) float lds[2 * (TL::KFL + TL::VFL)];
     const int tid = threadIdx.x, lane = tid & 63, r32 = lane & 31, lg = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    // heaviest query blocks first (causal work grows with the query index)
-    const int nqb = (T + AT_QB - 1) / AT_QB;
-    const int qblk = nqb - 1 - (int)(blockIdx.x / BH), bh = (int)(blockIdx.x % BH);
+    // Causal work grows with the query block. The first half of the grid takes
+    // the heavy blocks (descending), the second half the light ones
+    // (ascending): the two workgroups a CU receives in the two dispatch rounds
+    // then sum to about the same work (nqb - 1 + 1 blocks' worth).
+    const int nqb = (T + AT_QB - 1) / AT_QB, half = (nqb + 1) / 2;
+    const int L = (int)(blockIdx.x / BH), bh = (int)(blockIdx.x % BH);
+    const int qblk = L < half ? nqb - 1 - L : L - half;
     const int b = bh / H, h = bh % H;
     const long row0 = (long)b * T;  // first token row of this sequence
     const int hc = h * DH;          // first column of this head
@@ -167,6 +171,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const float *__restric
         for (int v = 0; v < 16; v++) oacc[nb][v] = 0.f;
     const bool store_p = P != nullptr && qi < T;
     float *prow = store_p ? P + ((long)bh * T + qi) * T : nullptr;
+    const bool vec_p = (T & 3) == 0 && (reinterpret_cast<uintptr_t>(P) & 15) == 0;
     at_load<DH>(kr, K + hc, ld, row0, 0, T, tid);
     at_load<DH>(vr, V + hc, ld, row0, 0, T, tid);
     at_store<DH, TL::KS>(Kb(0), kr, tid);
@@ -184,7 +189,21 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const float *__restric
             for (int v = 0; v < 16; v++) {
                 const int j = kb * AT_KB + at_key(v, lg);
                 p[v] = (j <= qi && j < T) ? __expf(s[v] * scale - m) * inv : 0.f;
-                if (store_p && j < T) prow[j] = p[v];
+            }
+            // elements 4g .. 4g+3 are keys 8g + 4lg + 0..3: one 16-byte store each
+            if (store_p) {
+#pragma unroll
+                for (int g4 = 0; g4 < 4; g4++) {
+                    const int j0 = kb * AT_KB + 8 * g4 + 4 * lg;
+                    if (vec_p && j0 + 3 < T) {
+                        *reinterpret_cast<v4f *>(prow + j0) =
+                            v4f{p[4 * g4], p[4 * g4 + 1], p[4 * g4 + 2], p[4 * g4 + 3]};
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; e++)
+                            if (j0 + e < T) prow[j0 + e] = p[4 * g4 + e];
+                    }
+                }
             }
             const float *vcol = Vb(kb) + r32;
 #pragma unroll
@@ -218,6 +237,264 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const float *__restric
             for (int c = c0 + lane; c < T; c += 64) zr[c] = 0.f;
         }
     }
+}
+
+// ---------------------------------------------------------------- backward
+// train.c:374-407 attention_backward / gpu_kernels.cu:437-486 attn_bwd, from
+// the forward's stored probabilities P:
+//   dP_ij = dO_i . v_j,  D_i = sum_j P_ij dP_ij,  dS_ij = P_ij (dP_ij - D_i) scale
+//   dQ_i = sum_j dS_ij k_j,  dK_j = sum_i dS_ij q_i,  dV_j = sum_i P_ij dO_i
+// Kernel A (per 128 queries of one head, like the forward): dP^T = V_blk .
+// dO^T in the score layout (lane = query, 16 keys), pass 1 sums D_i, pass 2
+// forms dS (stored to the [B*H][T][T] scratch for kernel B, 16-byte pieces)
+// and accumulates dQ^T = K^T dS^T with dS^T as the register B operand.
+// Kernel B (per 128 keys): dV^T = dO^T P and dK^T = Q^T dS over the query
+// blocks at or after the keys (causal), with dO and Q blocks in LDS (A
+// operand, one float per lane) and P, dS rows read straight from HBM as the B
+// operand (32 consecutive keys per lane half: one 128-byte row piece).
+
+template <int DH>
+__global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(
+    const float *__restrict__ dO, long ldo, const float *__restrict__ K,
+    const float *__restrict__ V, long ld, const float *__restrict__ P, float *__restrict__ dS,
+    float *__restrict__ dQ, long ldg, int T, int H, int BH, float scale, int accumulate) {
+    using TL = AttnTile<DH>;
+    __shared__ __attribute__((aligned(16))) float lds[2 * (TL::KFL + TL::VFL)];
+    const int tid = threadIdx.x, lane = tid & 63, r32 = lane & 31, lg = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nqb = (T + AT_QB - 1) / AT_QB, half = (nqb + 1) / 2;
+    const int L = (int)(blockIdx.x / BH), bh = (int)(blockIdx.x % BH);
+    const int qblk = L < half ? nqb - 1 - L : L - half;
+    const int b = bh / H, h = bh % H;
+    const long row0 = (long)b * T;
+    const int hc = h * DH;
+    const int q0 = qblk * AT_QB, q0w = q0 + wave * 32;
+    const int qi = q0w + r32;
+    const int kb_last = min(T - 1, q0 + AT_QB - 1) / AT_KB;
+    const int kbw = q0w < T ? min(T - 1, q0w + 31) / AT_KB : -1;
+    const bool vec_p = (T & 3) == 0 && (reinterpret_cast<uintptr_t>(P) & 15) == 0 &&
+                       (reinterpret_cast<uintptr_t>(dS) & 15) == 0;
+
+    v4f df[DH / 8];  // dO of this lane's query, score k order
+    {
+        const float *drow = dO + (row0 + min(qi, T - 1)) * ldo + hc + 4 * lg;
+#pragma unroll
+        for (int q = 0; q < DH / 8; q++) df[q] = *reinterpret_cast<const v4f *>(drow + 8 * q);
+    }
+    // V blocks take the score operand's slot (stride KS), K blocks the
+    // value operand's (stride VS)
+    auto Vs = [&](int u) { return lds + (u & 1) * (TL::KFL + TL::VFL); };
+    auto Ks = [&](int u) { return lds + (u & 1) * (TL::KFL + TL::VFL) + TL::KFL; };
+    v4f vr[TL::PT], kr[TL::PT];
+    const long prow = ((long)bh * T + min(qi, T - 1)) * T;
+    // P_ij for this lane's 16 keys of block kb (zero past T)
+    auto load_p = [&](const float *X, int kb, float (&x)[16]) {
+#pragma unroll
+        for (int g4 = 0; g4 < 4; g4++) {
+            const int j0 = kb * AT_KB + 8 * g4 + 4 * lg;
+            if (vec_p && j0 + 3 < T) {
+                const v4f t = *reinterpret_cast<const v4f *>(X + prow + j0);
+#pragma unroll
+                for (int e = 0; e < 4; e++) x[4 * g4 + e] = t[e];
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; e++) x[4 * g4 + e] = j0 + e < T ? X[prow + j0 + e] : 0.f;
+            }
+        }
+    };
+
+    // ---- pass 1: D_i = sum_j P_ij dP_ij (this lane's half of the keys)
+    float Dsum = 0.f;
+    at_load<DH>(vr, V + hc, ld, row0, 0, T, tid);
+    at_store<DH, TL::KS>(Vs(0), vr, tid);
+    __syncthreads();
+    for (int kb = 0; kb <= kb_last; kb++) {
+        if (kb < kb_last) at_load<DH>(vr, V + hc, ld, row0, (kb + 1) * AT_KB, T, tid);
+        if (kb <= kbw) {
+            float pv[16];
+            load_p(P, kb, pv);
+            const v16f dp = at_scores<DH>(Vs(kb), df, r32, lg);
+#pragma unroll
+            for (int v = 0; v < 16; v++) Dsum += pv[v] * dp[v];
+        }
+        if (kb < kb_last) at_store<DH, TL::KS>(Vs(kb + 1), vr, tid);
+        __syncthreads();
+    }
+    Dsum += __shfl_xor(Dsum, 32);
+
+    // ---- pass 2: dS (stored) and dQ^T += K^T dS^T
+    v16f qacc[DH / 32];
+#pragma unroll
+    for (int nb = 0; nb < DH / 32; nb++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) qacc[nb][v] = 0.f;
+    const bool live = qi < T;
+    at_load<DH>(vr, V + hc, ld, row0, 0, T, tid);
+    at_load<DH>(kr, K + hc, ld, row0, 0, T, tid);
+    at_store<DH, TL::KS>(Vs(0), vr, tid);
+    at_store<DH, TL::VS>(Ks(0), kr, tid);
+    __syncthreads();
+    for (int kb = 0; kb <= kb_last; kb++) {
+        if (kb < kb_last) {
+            at_load<DH>(vr, V + hc, ld, row0, (kb + 1) * AT_KB, T, tid);
+            at_load<DH>(kr, K + hc, ld, row0, (kb + 1) * AT_KB, T, tid);
+        }
+        if (kb <= kbw) {
+            float pv[16], ds[16];
+            load_p(P, kb, pv);
+            const v16f dp = at_scores<DH>(Vs(kb), df, r32, lg);
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const int j = kb * AT_KB + at_key(v, lg);
+                ds[v] = (j <= qi && j < T) ? pv[v] * (dp[v] - Dsum) * scale : 0.f;
+            }
+            if (live) {
+#pragma unroll
+                for (int g4 = 0; g4 < 4; g4++) {
+                    const int j0 = kb * AT_KB + 8 * g4 + 4 * lg;
+                    if (vec_p && j0 + 3 < T) {
+                        *reinterpret_cast<v4f *>(dS + prow + j0) =
+                            v4f{ds[4 * g4], ds[4 * g4 + 1], ds[4 * g4 + 2], ds[4 * g4 + 3]};
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; e++)
+                            if (j0 + e < T) dS[prow + j0 + e] = ds[4 * g4 + e];
+                    }
+                }
+            }
+            const float *kcol = Ks(kb) + r32;
+#pragma unroll
+            for (int s4 = 0; s4 < 16; s4++) {
+                const float *krow = kcol + at_key(s4, lg) * TL::VS;
+#pragma unroll
+                for (int nb = 0; nb < DH / 32; nb++)
+                    qacc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(krow[nb * 32], ds[s4], qacc[nb], 0, 0, 0);
+            }
+        }
+        if (kb < kb_last) {
+            at_store<DH, TL::KS>(Vs(kb + 1), vr, tid);
+            at_store<DH, TL::VS>(Ks(kb + 1), kr, tid);
+        }
+        __syncthreads();
+    }
+    if (live) {
+        float *grow = dQ + (row0 + qi) * ldg + hc;
+#pragma unroll
+        for (int nb = 0; nb < DH / 32; nb++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                float *o = grow + nb * 32 + at_key(v, lg);
+                *o = accumulate ? *o + qacc[nb][v] : qacc[nb][v];
+            }
+    }
+}
+
+template <int DH>
+__global__ __launch_bounds__(256, 2) void attn_bwd_dkv_kernel(
+    const float *__restrict__ dO, long ldo, const float *__restrict__ Q, long ld,
+    const float *__restrict__ P, const float *__restrict__ dS, float *__restrict__ dK,
+    float *__restrict__ dV, long ldg, int T, int H, int BH, int accumulate) {
+    using TL = AttnTile<DH>;
+    __shared__ __attribute__((aligned(16))) float lds[2 * 2 * TL::VFL];
+    const int tid = threadIdx.x, lane = tid & 63, r32 = lane & 31, lg = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // key block k needs the query blocks from k on: work falls with k, so the
+    // first half of the grid takes the light-to-heavy mirror of the forward's
+    const int nkb = (T + AT_QB - 1) / AT_QB, half = (nkb + 1) / 2;
+    const int L = (int)(blockIdx.x / BH), bh = (int)(blockIdx.x % BH);
+    const int kblk = L < half ? L : nkb - 1 - (L - half);
+    const int b = bh / H, h = bh % H;
+    const long row0 = (long)b * T;
+    const int hc = h * DH;
+    const int k0 = kblk * AT_QB, k0w = k0 + wave * 32;
+    const int kj = k0w + r32;  // this lane's key (its output column)
+    const int qb_first = k0 / AT_KB, qb_last = (T - 1) / AT_KB;
+    const int qbw = k0w / AT_KB;  // this wave's first query block
+
+    auto Os = [&](int u) { return lds + (u & 1) * 2 * TL::VFL; };
+    auto Qs = [&](int u) { return lds + (u & 1) * 2 * TL::VFL + TL::VFL; };
+    v4f orr[TL::PT], qr[TL::PT];
+    v16f vacc[DH / 32], kacc[DH / 32];
+#pragma unroll
+    for (int nb = 0; nb < DH / 32; nb++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) vacc[nb][v] = 0.f, kacc[nb][v] = 0.f;
+    const float *Pbh = P + (long)bh * T * T, *Sbh = dS + (long)bh * T * T;
+    const int kcol = min(kj, T - 1);
+
+    at_load<DH>(orr, dO + hc, ldo, row0, qb_first * AT_KB, T, tid);
+    at_load<DH>(qr, Q + hc, ld, row0, qb_first * AT_KB, T, tid);
+    at_store<DH, TL::VS>(Os(0), orr, tid);
+    at_store<DH, TL::VS>(Qs(0), qr, tid);
+    __syncthreads();
+    for (int qb = qb_first; qb <= qb_last; qb++) {
+        const int u = qb - qb_first;
+        if (qb < qb_last) {
+            at_load<DH>(orr, dO + hc, ldo, row0, (qb + 1) * AT_KB, T, tid);
+            at_load<DH>(qr, Q + hc, ld, row0, (qb + 1) * AT_KB, T, tid);
+        }
+        if (k0w < T && qb >= qbw) {
+            // P and dS of queries qb*32 + key-layout row s4, key kj (zero past T)
+            float pv[16], sv[16];
+#pragma unroll
+            for (int s4 = 0; s4 < 16; s4++) {
+                const int i = qb * AT_KB + at_key(s4, lg);
+                const long o = (long)min(i, T - 1) * T + kcol;
+                const bool ok = i < T && kj < T;
+                pv[s4] = ok ? Pbh[o] : 0.f;
+                sv[s4] = ok ? Sbh[o] : 0.f;
+            }
+            const float *ocol = Os(u) + r32, *qcol = Qs(u) + r32;
+#pragma unroll
+            for (int s4 = 0; s4 < 16; s4++) {
+                const float *orow = ocol + at_key(s4, lg) * TL::VS;
+                const float *qrow = qcol + at_key(s4, lg) * TL::VS;
+#pragma unroll
+                for (int nb = 0; nb < DH / 32; nb++) {
+                    vacc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(orow[nb * 32], pv[s4], vacc[nb], 0, 0, 0);
+                    kacc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(qrow[nb * 32], sv[s4], kacc[nb], 0, 0, 0);
+                }
+            }
+        }
+        if (qb < qb_last) {
+            at_store<DH, TL::VS>(Os(u + 1), orr, tid);
+            at_store<DH, TL::VS>(Qs(u + 1), qr, tid);
+        }
+        __syncthreads();
+    }
+    if (kj < T) {
+        float *vrow = dV + (row0 + kj) * ldg + hc, *krow = dK + (row0 + kj) * ldg + hc;
+#pragma unroll
+        for (int nb = 0; nb < DH / 32; nb++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const int d = nb * 32 + at_key(v, lg);
+                vrow[d] = accumulate ? vrow[d] + vacc[nb][v] : vacc[nb][v];
+                krow[d] = accumulate ? krow[d] + kacc[nb][v] : kacc[nb][v];
+            }
+    }
+}
+
+hipError_t launch_attn_bwd(const float *dO, long ldo, const float *Q, const float *K,
+                           const float *V, long ld, const float *P, float *dS, float *dQ,
+                           float *dK, float *dV, long ldg, int B, int T, int H, int dh,
+                           float scale, int accumulate, hipStream_t stream) {
+    const int BH = B * H, nb = (T + AT_QB - 1) / AT_QB;
+    if (BH == 0 || T == 0) return hipSuccess;
+    const dim3 grid((unsigned)((long)nb * BH)), block(256);
+#define PCL_ATTN_BWD(D)                                                                            \
+    hipLaunchKernelGGL(attn_bwd_dq_kernel<D>, grid, block, 0, stream, dO, ldo, K, V, ld, P, dS, dQ,  \
+                       ldg, T, H, BH, scale, accumulate);                                          \
+    hipLaunchKernelGGL(attn_bwd_dkv_kernel<D>, grid, block, 0, stream, dO, ldo, Q, ld, P, dS, dK, dV, \
+                       ldg, T, H, BH, accumulate)
+    switch (dh) {
+        case 32: PCL_ATTN_BWD(32); break;
+        case 64: PCL_ATTN_BWD(64); break;
+        case 128: PCL_ATTN_BWD(128); break;
+        default: return hipErrorInvalidValue;
+    }
+#undef PCL_ATTN_BWD
+    return hipGetLastError();
 }
 
 hipError_t launch_attn_fwd(const float *Q, const float *K, const float *V, long ld, float *O,

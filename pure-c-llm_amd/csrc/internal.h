@@ -64,6 +64,14 @@ hipError_t launch_attn_fwd(const float *Q, const float *K, const float *V, long 
                            long ldo, float *P, int B, int T, int H, int dh, float scale,
                            hipStream_t stream);
 
+// Backward from the stored probabilities P: dQ, dK, dV ((B*T) x ldg) set or,
+// with accumulate, added to; dS ([B*H][T][T]) is written as scratch (entries
+// j <= i of each causal row). dO is (B*T) x ldo.
+hipError_t launch_attn_bwd(const float *dO, long ldo, const float *Q, const float *K,
+                           const float *V, long ld, const float *P, float *dS, float *dQ,
+                           float *dK, float *dV, long ldg, int B, int T, int H, int dh,
+                           float scale, int accumulate, hipStream_t stream);
+
 // ---- GEMV (gemv.hip) ----
 GemvPlan plan_sgemv(int w_trans, int M, int N, int K);
 // Column sums of a K x N matrix (bias_bwd): plan for launch_sgemv with x_ones.

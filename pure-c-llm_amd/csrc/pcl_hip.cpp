@@ -487,6 +487,36 @@ int pcl_attn_fwd(const float *Q, const float *K, const float *V, int ld, float *
     return PCL_OK;
 }
 
+int pcl_attn_bwd(float *dQ, float *dK, float *dV, int ld_grad, float *scratch, const float *dAtt,
+                 int ld_att, const float *Q, const float *K, const float *V, int ld,
+                 const float *probs, int B, int T, int H, int dh, int accumulate, void *stream) {
+    CHECK_ARG(B >= 0 && T >= 0 && H >= 0, "pcl_attn_bwd: negative dimension (B=%d T=%d H=%d)", B,
+              T, H);
+    CHECK_ARG(dh == 32 || dh == 64 || dh == 128, "pcl_attn_bwd: head size %d is not 32, 64 or 128",
+              dh);
+    if (B == 0 || T == 0 || H == 0) return PCL_OK;
+    CHECK_ARG(dQ && dK && dV && dAtt && Q && K && V && probs, "pcl_attn_bwd: NULL operand");
+    CHECK_ARG(ld >= H * dh && ld_att >= H * dh && ld_grad >= H * dh,
+              "pcl_attn_bwd: a leading dimension is below H*dh=%d", H * dh);
+    CHECK_ARG(ld % 4 == 0 && ld_att % 4 == 0, "pcl_attn_bwd: ld=%d, ld_att=%d not multiples of 4",
+              ld, ld_att);
+    CHECK_ARG(aligned16(Q) && aligned16(K) && aligned16(V) && aligned16(dAtt),
+              "pcl_attn_bwd: Q, K, V and dAtt must be 16-byte aligned");
+    CHECK_ARG((long)B * T <= INT32_MAX && (long)B * H * T <= INT32_MAX,
+              "pcl_attn_bwd: B*T or B*H*T beyond 2^31");
+    PCL_OK_OR_RETURN(do_init());
+    hipStream_t s = pick(stream);
+    float *dS = scratch;
+    if (!dS) {
+        StreamScratch *sc;
+        PCL_OK_OR_RETURN(get_scratch(s, sizeof(float) * (size_t)B * H * T * T, 0, &sc));
+        dS = static_cast<float *>(sc->ws.buf);
+    }
+    HIP_OK(pcl::launch_attn_bwd(dAtt, ld_att, Q, K, V, ld, probs, dS, dQ, dK, dV, ld_grad, B, T, H,
+                                dh, 1.0f / sqrtf((float)dh), accumulate, s));
+    return PCL_OK;
+}
+
 // ----------------------------------------------------------- INT8 native ----
 int pcl_s8_kpad(int K) { return kpad256(K < 0 ? 0 : K); }
 size_t pcl_s8_packed_bytes(int K, int N) {
@@ -669,6 +699,16 @@ void attn_fwd(const float *Q, const float *K, const float *V, float *att, float 
     finish_void(st);
 }
 
+void attn_bwd(float *dQ, float *dK, float *dV, float *scratch, const float *dAtt, const float *Q,
+              const float *K, const float *V, const float *probs) {
+    int st = need_attn_dims("attn_bwd");
+    if (st == PCL_OK)
+        st = pcl_attn_bwd(dQ, dK, dV, g_d_model, scratch, dAtt, g_d_model, Q, K, V, g_d_model,
+                          probs, g_attn_batch, g_attn_seq, g_attn_heads, g_d_model / g_attn_heads,
+                          0, nullptr);
+    finish_void(st);
+}
+
 // --------------------------------------------------- host-pointer drop-ins ----
 // Slot numbers name the staging buffer each operand uses.
 enum { S_A = 0, S_B, S_C, S_BIAS, S_D, S_E, S_F, S_G };
@@ -758,6 +798,42 @@ static int host_attention_forward(const float *q, const float *k, const float *v
 void attention_forward(const float *q, const float *k, const float *v, float *att, float *probs,
                        int B, int T) {
     finish_void(host_attention_forward(q, k, v, att, probs, B, T));
+}
+
+static int host_attention_backward(float *dq, float *dk, float *dv, const float *d_att,
+                                   const float *q, const float *k, const float *v,
+                                   const float *probs, int B, int T) {
+    PCL_OK_OR_RETURN(need_attn_dims("attention_backward"));
+    CHECK_ARG(B >= 0 && T >= 0, "attention_backward: negative dimension (B=%d T=%d)", B, T);
+    if (B == 0 || T == 0) return PCL_OK;
+    CHECK_ARG(dq && dk && dv && d_att && q && k && v && probs, "attention_backward: NULL operand");
+    const int D = g_d_model, H = g_attn_heads;
+    CHECK_ARG(D % H == 0, "attention_backward: d_model %d not divisible by %d heads", D, H);
+    PCL_OK_OR_RETURN(do_init());
+    const size_t act = sizeof(float) * (size_t)B * T * D, pb = sizeof(float) * (size_t)B * H * T * T;
+    void *ddq, *ddk, *ddv, *ddo, *dqin, *dkin, *dvin, *dp;
+    PCL_OK_OR_RETURN(upload(S_A, q, act, &dqin));
+    PCL_OK_OR_RETURN(upload(S_B, k, act, &dkin));
+    PCL_OK_OR_RETURN(upload(S_D, v, act, &dvin));
+    PCL_OK_OR_RETURN(upload(S_E, probs, pb, &dp));
+    PCL_OK_OR_RETURN(upload(S_C, d_att, act, &ddo));
+    PCL_OK_OR_RETURN(upload(S_F, dq, act, &ddq));
+    PCL_OK_OR_RETURN(upload(S_G, dk, act, &ddk));
+    PCL_OK_OR_RETURN(upload(S_BIAS, dv, act, &ddv));
+    // train.c:374-407 accumulates into dq, dk, dv; dS goes to the library scratch
+    PCL_OK_OR_RETURN(pcl_attn_bwd((float *)ddq, (float *)ddk, (float *)ddv, D, nullptr,
+                                  (const float *)ddo, D, (const float *)dqin, (const float *)dkin,
+                                  (const float *)dvin, D, (const float *)dp, B, T, H, D / H, 1,
+                                  t_stream));
+    PCL_OK_OR_RETURN(download(dq, ddq, act));
+    PCL_OK_OR_RETURN(download(dk, ddk, act));
+    PCL_OK_OR_RETURN(download(dv, ddv, act));
+    return sync_current();
+}
+
+void attention_backward(float *dq, float *dk, float *dv, const float *d_att, const float *q,
+                        const float *k, const float *v, const float *probs, int B, int T) {
+    finish_void(host_attention_backward(dq, dk, dv, d_att, q, k, v, probs, B, T));
 }
 
 static int need_dims(const char *who) {

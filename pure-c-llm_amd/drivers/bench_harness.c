@@ -184,6 +184,83 @@ done:
     return rc;
 }
 
+/* ------------------------------------------------------------ attention ---- */
+/* One step = one pcl_attn_fwd over B sequences of T tokens, H heads of dh
+ * (Q, K, V ~ N-ish(0,1) as U[-1.7,1.7]); probs stored when with_probs. */
+typedef struct {
+    int B, T, H, dh, with_probs;
+    void *Q, *K, *V, *O, *P;
+} attn_ctx;
+
+static int attn_step(void *c_, int i) {
+    attn_ctx *c = c_;
+    (void)i;
+    const int D = c->H * c->dh;
+    return pcl_attn_fwd(c->Q, c->K, c->V, D, c->O, D, c->with_probs ? c->P : NULL, c->B, c->T, c->H,
+                        c->dh, NULL);
+}
+
+int pcl_bench_attn(int B, int T, int H, int dh, int with_probs, int warmup, int steps,
+                   double *ms_total) {
+    int rc = PCL_OK;
+    attn_ctx c = {B, T, H, dh, with_probs, NULL, NULL, NULL, NULL, NULL};
+    const size_t act = (size_t)B * T * H * dh;
+    c.Q = dev_f32(act, 31, -1.7f, 1.7f);
+    c.K = dev_f32(act, 32, -1.7f, 1.7f);
+    c.V = dev_f32(act, 33, -1.7f, 1.7f);
+    c.O = pcl_malloc(act * sizeof(float));
+    if (with_probs) c.P = pcl_malloc((size_t)B * H * T * T * sizeof(float));
+    if (!c.Q || !c.K || !c.V || !c.O || (with_probs && !c.P)) {
+        rc = PCL_ERR_OOM;
+        goto done;
+    }
+    TRY(time_steps(attn_step, &c, warmup, steps, ms_total));
+done:
+    pcl_free(c.Q), pcl_free(c.K), pcl_free(c.V), pcl_free(c.O), pcl_free(c.P);
+    return rc;
+}
+
+/* One step = one pcl_attn_bwd (both kernels) from stored probabilities,
+ * gradients set; dS goes to a caller scratch of B*H*T*T floats. */
+typedef struct {
+    int B, T, H, dh;
+    void *dO, *Q, *K, *V, *P, *S, *dQ, *dK, *dV;
+} attn_bwd_ctx;
+
+static int attn_bwd_step(void *c_, int i) {
+    attn_bwd_ctx *c = c_;
+    (void)i;
+    const int D = c->H * c->dh;
+    return pcl_attn_bwd(c->dQ, c->dK, c->dV, D, c->S, c->dO, D, c->Q, c->K, c->V, D, c->P, c->B,
+                        c->T, c->H, c->dh, 0, NULL);
+}
+
+int pcl_bench_attn_bwd(int B, int T, int H, int dh, int warmup, int steps, double *ms_total) {
+    int rc = PCL_OK;
+    attn_bwd_ctx c = {B, T, H, dh, NULL, NULL, NULL, NULL, NULL, NULL, NULL, NULL, NULL};
+    const size_t act = (size_t)B * T * H * dh, pb = (size_t)B * H * T * T;
+    c.dO = dev_f32(act, 34, -1.7f, 1.7f);
+    c.Q = dev_f32(act, 31, -1.7f, 1.7f);
+    c.K = dev_f32(act, 32, -1.7f, 1.7f);
+    c.V = dev_f32(act, 33, -1.7f, 1.7f);
+    c.P = pcl_malloc(pb * sizeof(float));
+    c.S = pcl_malloc(pb * sizeof(float));
+    c.dQ = pcl_malloc(act * sizeof(float));
+    c.dK = pcl_malloc(act * sizeof(float));
+    c.dV = pcl_malloc(act * sizeof(float));
+    if (!c.dO || !c.Q || !c.K || !c.V || !c.P || !c.S || !c.dQ || !c.dK || !c.dV) {
+        rc = PCL_ERR_OOM;
+        goto done;
+    }
+    /* real probabilities of these inputs */
+    TRY(pcl_attn_fwd(c.Q, c.K, c.V, H * dh, c.dQ, H * dh, c.P, B, T, H, dh, NULL));
+    TRY(time_steps(attn_bwd_step, &c, warmup, steps, ms_total));
+done:
+    pcl_free(c.dO), pcl_free(c.Q), pcl_free(c.K), pcl_free(c.V), pcl_free(c.P), pcl_free(c.S);
+    pcl_free(c.dQ), pcl_free(c.dK), pcl_free(c.dV);
+    return rc;
+}
+
 /* ----------------------------------------------------------------- GEMV ---- */
 /* A decode sweep: per step, one GEMV per weight in `shapes` (K_i x N_i), as
  * the layers of a model are visited, with `copies` rotating copies of the

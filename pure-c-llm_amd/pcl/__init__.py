@@ -81,6 +81,7 @@ _PROTOS = {
     "quantize_B_pack": (None, [_vp, _vp, _vp, _vp, _i, _i, _i]),
     "gemm_int8_kernel": (None, [_vp, _i, _vp, _vp, _vp, _vp, _i, _i]),
     "attention_forward": (None, [_vp, _vp, _vp, _vp, _vp, _i, _i]),
+    "attention_backward": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i]),
     # device-pointer drop-ins
     "gpu_init": (None, []),
     "gemm_nn": (None, [_vp, _vp, _vp, _vp, _i, _i, _i]),
@@ -88,11 +89,13 @@ _PROTOS = {
     "gemm_tn": (None, [_vp, _vp, _vp, _i, _i, _i]),
     "bias_bwd": (None, [_vp, _vp, _i, _i]),
     "attn_fwd": (None, [_vp, _vp, _vp, _vp, _vp]),
+    "attn_bwd": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     # native
     "pcl_sgemm": (_i, [_i, _i, _i, _i, _i, _vp, _i, _vp, _i, _vp, _i, _vp, _i, _vp]),
     "pcl_sgemv": (_i, [_i, _i, _i, _i, _vp, _i, _vp, _i, _vp, _i, _vp, _i, _vp]),
     "pcl_bias_bwd": (_i, [_vp, _vp, _i, _i, _i, _vp]),
     "pcl_attn_fwd": (_i, [_vp, _vp, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i, _vp]),
+    "pcl_attn_bwd": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _vp, _i, _vp, _i, _i, _i, _i, _i, _vp]),
     "pcl_s8_kpad": (_i, [_i]),
     "pcl_s8_packed_bytes": (_sz, [_i, _i]),
     "pcl_pack_b_s8": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp]),

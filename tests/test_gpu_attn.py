@@ -151,3 +151,103 @@ def test_attn_fwd_argument_errors():
                  (q.ptr + 4, q.ptr, q.ptr, 64, q.ptr, 64, None, 1, 16, 1, 32, None)]:  # alignment
         assert pcl.lib.pcl_attn_fwd(*args) == pcl.PCL_ERR_INVALID_ARG
         pcl.lib.pcl_clear_error()
+
+
+# ------------------------------------------------------------- backward ----
+def attn_bwd(d_att, q, k, v, probs, B, T, H, dh, grads0=None, accumulate=False, scratch=False):
+    """pcl_attn_bwd on device copies; returns (dq, dk, dv[, dS])."""
+    D = H * dh
+    bufs = [pcl.dev(x) for x in (d_att, q, k, v, probs)]
+    g = grads0 if grads0 is not None else [np.full((B * T, D), np.nan, np.float32)] * 3
+    dg = [pcl.dev(x) for x in g]
+    ds = pcl.dev(np.zeros((B * H, T, T), np.float32)) if scratch else None
+    pcl.check(pcl.lib.pcl_attn_bwd(dg[0].ptr, dg[1].ptr, dg[2].ptr, D, ds.ptr if ds else None,
+                                   bufs[0].ptr, D, bufs[1].ptr, bufs[2].ptr, bufs[3].ptr, D, bufs[4].ptr,
+                                   B, T, H, dh, int(accumulate), None))
+    pcl.sync()
+    out = [x.download((B * T, D), np.float32) for x in dg]
+    if scratch:
+        out.append(ds.download((B * H, T, T), np.float32))
+    return out
+
+
+@pytest.mark.parametrize("B,T,H,dh", [(1, 1, 1, 32), (2, 33, 2, 32), (1, 128, 1, 64), (2, 200, 2, 64),
+                                      (1, 129, 3, 128), (2, 256, 2, 128), (1, 300, 4, 32)])
+def test_attn_bwd_vs_oracle(B, T, H, dh):
+    announce("attn_bwd", B, T, H, dh)
+    D = H * dh
+    q, k, v = _qkv(B, T, D, 500 + T + dh)
+    d_att = ob.normal((B * T, D), 510 + T)
+    _, pr = attn(q, k, v, B, T, H, dh)
+    g0 = [ob.normal((B * T, D), 520 + i, 0.0, 0.1) for i in range(3)]
+    got = attn_bwd(d_att, q, k, v, pr, B, T, H, dh, grads0=g0, accumulate=True)
+    want = ob.attention_backward(d_att, q, k, v, pr, B, T, H, dh, *g0)
+    for name, a, r in zip("qkv", got, want):
+        assert rel(a, r) <= FP32_TOL, name
+    # set mode equals accumulating onto zeros
+    got0 = attn_bwd(d_att, q, k, v, pr, B, T, H, dh)
+    want0 = ob.attention_backward(d_att, q, k, v, pr, B, T, H, dh)
+    for name, a, r in zip("qkv", got0, want0):
+        assert rel(a, r) <= FP32_TOL, name
+
+
+@pytest.mark.parametrize("B,T,H,dh", [(4, 1024, 16, 64), (4, 1024, 12, 128)])
+def test_attn_bwd_full_size_identities(B, T, H, dh):
+    # With rows of P summing to one: sum_j dS_ij = 0 (so sum_j dK_j = 0 per
+    # head) and sum_j dV_j = sum_i dAtt_i; sampled dQ rows against f64 numpy
+    announce("attn_bwd full", B, T, H, dh)
+    D = H * dh
+    q, k, v = _qkv(B, T, D, 540 + dh)
+    d_att = ob.normal((B * T, D), 545)
+    _, pr = attn(q, k, v, B, T, H, dh)
+    dq, dk, dv, ds = attn_bwd(d_att, q, k, v, pr, B, T, H, dh, scratch=True)
+    scale = np.float64(1.0 / np.sqrt(np.float32(dh)))
+    rs = np.tril(ds.astype(np.float64)).sum(axis=2)
+    assert np.max(np.abs(rs)) <= 1e-4 * max(1.0, np.max(np.abs(ds)))
+    for b in range(B):
+        rows = slice(b * T, (b + 1) * T)
+        sv = dv[rows].astype(np.float64).sum(axis=0)
+        so = d_att[rows].astype(np.float64).sum(axis=0)
+        assert np.max(np.abs(sv - so)) <= 1e-4 * np.max(np.abs(so)) * 4
+        sk = dk[rows].astype(np.float64).sum(axis=0)
+        assert np.max(np.abs(sk)) <= 1e-4 * max(1.0, np.max(np.abs(dk[rows])))
+    rng = np.random.default_rng(11)
+    worst = 0.0
+    for _ in range(16):
+        b, h, i = int(rng.integers(B)), int(rng.integers(H)), int(rng.integers(T))
+        cols = slice(h * dh, (h + 1) * dh)
+        keys = slice(b * T, b * T + i + 1)
+        p = pr[b * H + h, i, : i + 1].astype(np.float64)
+        dp = v[keys, cols].astype(np.float64) @ d_att[b * T + i, cols].astype(np.float64)
+        dsr = p * (dp - np.dot(p, dp)) * scale
+        worst = max(worst, rel(dq[b * T + i, cols], dsr @ k[keys, cols].astype(np.float64)),
+                    rel(ds[b * H + h, i, : i + 1], dsr))
+    assert worst <= FP32_TOL
+
+
+def test_attention_backward_dropins():
+    B, T, H, dh = 2, 64, 4, 32
+    D = H * dh
+    announce("attention backward drop-ins", B, T, H, dh)
+    pcl.check(pcl.lib.pcl_set_model_dims(D, 96))
+    pcl.check(pcl.lib.pcl_set_attn_dims(B, T, H))
+    q, k, v = _qkv(B, T, D, 560)
+    d_att = ob.normal((B * T, D), 565)
+    _, pr = ob.attention_forward(q, k, v, B, T, H, dh)
+    g = [np.ones((B * T, D), np.float32) for _ in range(3)]
+    pcl.lib.attention_backward(*[pcl.ptr(x) for x in g], pcl.ptr(d_att), pcl.ptr(q), pcl.ptr(k),
+                               pcl.ptr(v), pcl.ptr(pr), B, T)
+    pcl.check_void()
+    want = ob.attention_backward(d_att, q, k, v, pr, B, T, H, dh,
+                                 *[np.ones((B * T, D), np.float32) for _ in range(3)])
+    for a, r in zip(g, want):
+        assert rel(a, r) <= FP32_TOL
+    bufs = [pcl.dev(x) for x in (d_att, q, k, v, pr)]
+    dg = [pcl.dev(np.full((B * T, D), 7.0, np.float32)) for _ in range(3)]
+    scr = pcl.empty((B * H, T, T), np.float32)
+    pcl.lib.attn_bwd(dg[0].ptr, dg[1].ptr, dg[2].ptr, scr.ptr, *[x.ptr for x in bufs])
+    pcl.check_void()
+    pcl.sync()
+    want0 = ob.attention_backward(d_att, q, k, v, pr, B, T, H, dh)  # gpu_kernels.cu: beta = 0
+    for x, r in zip(dg, want0):
+        assert rel(x.download((B * T, D), np.float32), r) <= FP32_TOL
