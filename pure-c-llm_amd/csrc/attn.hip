@@ -68,23 +68,60 @@ __device__ __forceinline__ void at_store(float *lds, const v4f (&r)[AttnTile<DH>
 // S^T block (keys x queries) of this wave: A = K rows from LDS (16-byte piece
 // 8q + 4lg of row r32, element e at MFMA step 4q + e), B = the wave's Q in the
 // same k order (registers).
+// key offset (within the block) of accumulator element v for lane half lg
+__device__ __forceinline__ constexpr int at_key(int v, int lg) { return (v >> 2) * 8 + lg * 4 + (v & 3); }
+
+// All of a block's fragment reads are issued before its MFMAs (in groups of
+// up to 8 pieces), so the waits between them count down instead of draining
+// the LDS queue before every MFMA.
 template <int DH>
 __device__ __forceinline__ v16f at_scores(const float *Ks, const v4f (&qf)[DH / 8], int r32, int lg) {
+    constexpr int G = DH >= 128 ? 2 : (DH / 8 < 8 ? DH / 8 : 8);  // pieces per read group
     v16f s;
 #pragma unroll
     for (int v = 0; v < 16; v++) s[v] = 0.f;
     const float *krow = Ks + r32 * AttnTile<DH>::KS + 4 * lg;
 #pragma unroll
-    for (int q = 0; q < DH / 8; q++) {
-        const v4f kf = *reinterpret_cast<const v4f *>(krow + 8 * q);
+    for (int q0 = 0; q0 < DH / 8; q0 += G) {
+        v4f kf[G];
 #pragma unroll
-        for (int e = 0; e < 4; e++) s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[e], qf[q][e], s, 0, 0, 0);
+        for (int q = 0; q < G; q++) kf[q] = *reinterpret_cast<const v4f *>(krow + 8 * (q0 + q));
+        __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs
+#pragma unroll
+        for (int q = 0; q < G; q++)
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[q][e], qf[q0 + q][e], s, 0, 0, 0);
     }
     return s;
 }
 
-// key offset (within the block) of accumulator element v for lane half lg
-__device__ __forceinline__ constexpr int at_key(int v, int lg) { return (v >> 2) * 8 + lg * 4 + (v & 3); }
+// acc[nb] += X^T . W^T over one 32-key block: A = X rows (keys in the score
+// layout's order, one float per lane from LDS, row stride VS), B = w[s4]
+// (this lane's 16 key weights). Reads go out 8 key steps at a time (2 for
+// 128-wide heads, whose accumulators leave fewer registers).
+template <int DH>
+__device__ __forceinline__ void at_accum(v16f (&acc)[DH / 32], const float *Xs, const float (&w)[16],
+                                         int r32, int lg) {
+    constexpr int S8 = DH >= 128 ? 2 : 8;  // key steps per read group
+    const float *xcol = Xs + r32;
+#pragma unroll
+    for (int h8 = 0; h8 < 16; h8 += S8) {
+        float xa[S8][DH / 32];
+#pragma unroll
+        for (int s4 = 0; s4 < S8; s4++)
+#pragma unroll
+            for (int nb = 0; nb < DH / 32; nb++)
+                xa[s4][nb] = xcol[at_key(h8 + s4, lg) * AttnTile<DH>::VS + nb * 32];
+        __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs
+#pragma unroll
+        for (int s4 = 0; s4 < S8; s4++)
+#pragma unroll
+            for (int nb = 0; nb < DH / 32; nb++)
+                acc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[s4][nb], w[h8 + s4], acc[nb], 0, 0, 0);
+    }
+}
+
 
 template <int DH>
 __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const float *__restrict__ Q,
@@ -205,14 +242,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const float *__restric
                     }
                 }
             }
-            const float *vcol = Vb(kb) + r32;
-#pragma unroll
-            for (int s4 = 0; s4 < 16; s4++) {
-                const float *vrow = vcol + at_key(s4, lg) * TL::VS;
-#pragma unroll
-                for (int nb = 0; nb < DH / 32; nb++)
-                    oacc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(vrow[nb * 32], p[s4], oacc[nb], 0, 0, 0);
-            }
+            at_accum<DH>(oacc, Vb(kb), p, r32, lg);
         }
         if (kb < kb_last) {
             at_store<DH, TL::KS>(Kb(kb + 1), kr, tid);
@@ -304,15 +334,20 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(
     };
 
     // ---- pass 1: D_i = sum_j P_ij dP_ij (this lane's half of the keys)
-    float Dsum = 0.f;
+    // P rows are fetched one key block ahead of their use (HBM latency is
+    // about one block of MFMA work)
+    float Dsum = 0.f, pn[16];
     at_load<DH>(vr, V + hc, ld, row0, 0, T, tid);
+    if (kbw >= 0) load_p(P, 0, pn);
     at_store<DH, TL::KS>(Vs(0), vr, tid);
     __syncthreads();
     for (int kb = 0; kb <= kb_last; kb++) {
         if (kb < kb_last) at_load<DH>(vr, V + hc, ld, row0, (kb + 1) * AT_KB, T, tid);
         if (kb <= kbw) {
             float pv[16];
-            load_p(P, kb, pv);
+#pragma unroll
+            for (int v = 0; v < 16; v++) pv[v] = pn[v];
+            if (kb < kbw) load_p(P, kb + 1, pn);
             const v16f dp = at_scores<DH>(Vs(kb), df, r32, lg);
 #pragma unroll
             for (int v = 0; v < 16; v++) Dsum += pv[v] * dp[v];
@@ -331,6 +366,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(
     const bool live = qi < T;
     at_load<DH>(vr, V + hc, ld, row0, 0, T, tid);
     at_load<DH>(kr, K + hc, ld, row0, 0, T, tid);
+    if (kbw >= 0) load_p(P, 0, pn);
     at_store<DH, TL::KS>(Vs(0), vr, tid);
     at_store<DH, TL::VS>(Ks(0), kr, tid);
     __syncthreads();
@@ -341,7 +377,9 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(
         }
         if (kb <= kbw) {
             float pv[16], ds[16];
-            load_p(P, kb, pv);
+#pragma unroll
+            for (int v = 0; v < 16; v++) pv[v] = pn[v];
+            if (kb < kbw) load_p(P, kb + 1, pn);
             const v16f dp = at_scores<DH>(Vs(kb), df, r32, lg);
 #pragma unroll
             for (int v = 0; v < 16; v++) {
@@ -362,14 +400,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(
                     }
                 }
             }
-            const float *kcol = Ks(kb) + r32;
-#pragma unroll
-            for (int s4 = 0; s4 < 16; s4++) {
-                const float *krow = kcol + at_key(s4, lg) * TL::VS;
-#pragma unroll
-                for (int nb = 0; nb < DH / 32; nb++)
-                    qacc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(krow[nb * 32], ds[s4], qacc[nb], 0, 0, 0);
-            }
+            at_accum<DH>(qacc, Ks(kb), ds, r32, lg);
         }
         if (kb < kb_last) {
             at_store<DH, TL::KS>(Vs(kb + 1), vr, tid);
@@ -422,8 +453,22 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkv_kernel(
     const float *Pbh = P + (long)bh * T * T, *Sbh = dS + (long)bh * T * T;
     const int kcol = min(kj, T - 1);
 
+    // P and dS of queries qb*32 + key-layout row s4, key kj (zero past T),
+    // fetched one query block ahead of their use
+    float pn[16], sn[16];
+    auto load_ps = [&](int qb) {
+#pragma unroll
+        for (int s4 = 0; s4 < 16; s4++) {
+            const int i = qb * AT_KB + at_key(s4, lg);
+            const long o = (long)min(i, T - 1) * T + kcol;
+            const bool ok = i < T && kj < T;
+            pn[s4] = ok ? Pbh[o] : 0.f;
+            sn[s4] = ok ? Sbh[o] : 0.f;
+        }
+    };
     at_load<DH>(orr, dO + hc, ldo, row0, qb_first * AT_KB, T, tid);
     at_load<DH>(qr, Q + hc, ld, row0, qb_first * AT_KB, T, tid);
+    if (k0w < T) load_ps(max(qb_first, qbw));
     at_store<DH, TL::VS>(Os(0), orr, tid);
     at_store<DH, TL::VS>(Qs(0), qr, tid);
     __syncthreads();
@@ -434,27 +479,12 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkv_kernel(
             at_load<DH>(qr, Q + hc, ld, row0, (qb + 1) * AT_KB, T, tid);
         }
         if (k0w < T && qb >= qbw) {
-            // P and dS of queries qb*32 + key-layout row s4, key kj (zero past T)
             float pv[16], sv[16];
 #pragma unroll
-            for (int s4 = 0; s4 < 16; s4++) {
-                const int i = qb * AT_KB + at_key(s4, lg);
-                const long o = (long)min(i, T - 1) * T + kcol;
-                const bool ok = i < T && kj < T;
-                pv[s4] = ok ? Pbh[o] : 0.f;
-                sv[s4] = ok ? Sbh[o] : 0.f;
-            }
-            const float *ocol = Os(u) + r32, *qcol = Qs(u) + r32;
-#pragma unroll
-            for (int s4 = 0; s4 < 16; s4++) {
-                const float *orow = ocol + at_key(s4, lg) * TL::VS;
-                const float *qrow = qcol + at_key(s4, lg) * TL::VS;
-#pragma unroll
-                for (int nb = 0; nb < DH / 32; nb++) {
-                    vacc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(orow[nb * 32], pv[s4], vacc[nb], 0, 0, 0);
-                    kacc[nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(qrow[nb * 32], sv[s4], kacc[nb], 0, 0, 0);
-                }
-            }
+            for (int s4 = 0; s4 < 16; s4++) pv[s4] = pn[s4], sv[s4] = sn[s4];
+            if (qb < qb_last) load_ps(qb + 1);
+            at_accum<DH>(vacc, Os(u), pv, r32, lg);
+            at_accum<DH>(kacc, Qs(u), sv, r32, lg);
         }
         if (qb < qb_last) {
             at_store<DH, TL::VS>(Os(u + 1), orr, tid);
