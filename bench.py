@@ -46,8 +46,9 @@ def load_bench():
                                    C.POINTER(d)]
     lib.pcl_bench_attn.argtypes = [i, i, i, i, i, i, i, C.POINTER(d)]
     lib.pcl_bench_attn_bwd.argtypes = [i, i, i, i, i, i, C.POINTER(d)]
+    lib.pcl_bench_sgemm_ex.argtypes = [i, i, i, i, i, i, i, i, i, C.POINTER(d)]
     for f in (lib.pcl_bench_igemm, lib.pcl_bench_sgemm, lib.pcl_bench_gemv, lib.pcl_bench_attn,
-              lib.pcl_bench_attn_bwd):
+              lib.pcl_bench_attn_bwd, lib.pcl_bench_sgemm_ex):
         f.restype = i
     return pcl, lib
 
@@ -125,6 +126,22 @@ def attn_bwd(pcl, lib, B, T, H, dh, warmup, steps):
             "causal_TT_GBps": round(tt_bytes / (per * 1e-3) / 1e9, 1)}
 
 
+def sgemm_epi(pcl, lib, opA, opB, M, N, K, epi, warmup, steps):
+    """Product + epilogue, fused (one kernel) against the reference's two-pass
+    sequence (GEMM, then the elementwise kernel)."""
+    out = {"M": M, "N": N, "K": K, "layout": "NT"[opA] + "NT"[opB],
+           "epilogue": {1: "gelu", 2: "residual", 3: "gelu_bwd"}[epi]}
+    for fused in (1, 0):
+        ms = C.c_double(0)
+        _check(pcl, lib.pcl_bench_sgemm_ex(opA, opB, M, N, K, epi, fused, warmup, steps, C.byref(ms)),
+               f"sgemm_ex {M}x{N}x{K} epi {epi}")
+        per = ms.value / steps
+        out["fused_ms" if fused else "two_pass_ms"] = round(per, 5)
+        out["fused_TFLOPS" if fused else "two_pass_TFLOPS"] = round(2.0 * M * N * K / (per * 1e-3) / 1e12, 2)
+    out["speedup"] = round(out["two_pass_ms"] / out["fused_ms"], 3)
+    return out
+
+
 def read_traffic():
     """HBM bytes per launch of the primary kernel, measured by rocprofv3 --pmc
     (FETCH_SIZE + WRITE_SIZE, calibrated on a copy of known size) and recorded
@@ -183,6 +200,7 @@ CASES = {
     "int8_ffn_up": lambda pcl, lib, w, s: igemm(pcl, lib, 4096, 4096, 1024, 2, w, s),
     "fp32_1024": lambda pcl, lib, w, s: sgemm(pcl, lib, 0, 0, 1024, 1024, 1024, 0, w, s),
     "fp32_ffn_up": lambda pcl, lib, w, s: sgemm(pcl, lib, 0, 0, 4096, 4096, 1024, 0, w, s),
+    "epi_350m_ffn_up_gelu": lambda pcl, lib, w, s: sgemm_epi(pcl, lib, 0, 0, 4096, 4096, 1024, 1, w, s),
     "attn_350m": lambda pcl, lib, w, s: attn(pcl, lib, 4, 1024, 16, 64, True, w, s),
     "attn_350m_noprobs": lambda pcl, lib, w, s: attn(pcl, lib, 4, 1024, 16, 64, False, w, s),
     "attn_trainer_dh128": lambda pcl, lib, w, s: attn(pcl, lib, 4, 1024, 12, 128, True, w, s),
@@ -348,6 +366,13 @@ def main():
         ex["grown_decode_gemv"] = dec
         ex["head_350m_gemv_fp32"] = {f"M{Mt}": gemv(pcl, lib, 1, Mt, [(1024, 50257)], 3, 2, 20) for Mt in (1, 8)}
         ex["head_350m_gemv_int8"] = {f"M{Mt}": gemv(pcl, lib, 2, Mt, [(1024, 50257)], 6, 2, 20) for Mt in (1, 8)}
+        # GEMM epilogues fused against the reference's two-pass sequence (350M class)
+        ex["fp32_350m_epilogues"] = {
+            "ffn_up_gelu": sgemm_epi(pcl, lib, 0, 0, 4096, 4096, 1024, 1, w, s),
+            "attn_out_residual": sgemm_epi(pcl, lib, 0, 0, 4096, 1024, 1024, 2, w, s),
+            "ffn_down_residual": sgemm_epi(pcl, lib, 0, 0, 4096, 1024, 4096, 2, w, s),
+            "bwd_dX_ffn_down_gelu_bwd": sgemm_epi(pcl, lib, 0, 1, 4096, 4096, 1024, 3, w, s),
+        }
         # causal attention forward: 350M-class (16 heads of 64, B=4, T=1024),
         # the reference GPU trainer's heads (12 of 128), the grown model (16 of 32, T=256)
         ex["attn_fwd"] = {

@@ -182,6 +182,11 @@ void gemm_nt(const float *A, const float *B, float *C, int M, int K, int N, int 
 void gemm_tn(const float *A, const float *B, float *C, int M, int K, int N);
 /* gpu_kernels.h:51: db(N) += colsum(dY(M,N)). */
 void bias_bwd(float *db, const float *dY, int M, int N);
+/* gpu_kernels.h:56-58 (gpu_kernels.cu:228-251): Y = tanh-GELU(X); dX = dY * GELU'(X)
+ * (SET); C = A + B -- n elements each. */
+void gelu_fwd(float *Y, const float *X, long n);
+void gelu_bwd(float *dX, const float *dY, const float *X, long n);
+void vec_add(float *C, const float *A, const float *B, long n);
 /* gpu_kernels.h:63-64: causal attention of B_SIZE x T_SIZE tokens, DIM wide,
  * N_HEADS heads (pcl_set_attn_dims / pcl_set_model_dims); probs [B*H][T][T]
  * normalised, zero above the diagonal (gpu_kernels.cu:264-281, 403-432). */
@@ -201,6 +206,30 @@ void attn_bwd(float *dQ, float *dK, float *dV, float *scratch, const float *dAtt
  * Replaces tensor.c:34-53, train.c:181-252/412-447, gpu_kernels.cu:112-138. */
 int pcl_sgemm(int opA, int opB, int M, int N, int K, const float *A, int lda, const float *B,
               int ldb, const float *bias, int accumulate, float *C, int ldc, void *stream);
+
+/* FP32 GEMM with a fused epilogue on v = op(A)·op(B) + bias (the elementwise pass
+ * that follows the product in train.c:522-527/550-552 and gpu_kernels.cu:228-251):
+ *   PCL_EPI_GELU      C = 0.5 v (1 + tanh(sqrt(2/pi) (v + 0.044715 v^3))) (train.c:314-322);
+ *                     aux_out (if not NULL) also receives v, the pre-activation the
+ *                     backward needs (train.c keeps it as A_h)
+ *   PCL_EPI_RESID     C = aux_in + v         (the residual adds, train.c:522, 527)
+ *   PCL_EPI_GELU_BWD  C = v * GELU'(aux_in)  (dX of FF2 times gelu_backward, train.c:324-333)
+ * aux arrays are M x N with leading dimension ld_aux; C is set (no accumulate).
+ * Fused into the GEMM kernel for NN (GELU, RESID) and NT (GELU_BWD) products on
+ * aligned operands with K % 32 == 0 and a full grid; otherwise the same result
+ * comes from the GEMM plus one elementwise pass. PCL_EPI_NONE is pcl_sgemm. */
+#define PCL_EPI_NONE 0
+#define PCL_EPI_GELU 1
+#define PCL_EPI_RESID 2
+#define PCL_EPI_GELU_BWD 3
+int pcl_sgemm_ex(int opA, int opB, int M, int N, int K, const float *A, int lda, const float *B,
+                 int ldb, const float *bias, int epilogue, const float *aux_in, float *aux_out,
+                 int ld_aux, float *C, int ldc, void *stream);
+
+/* Elementwise passes of the reference GPU API with an explicit stream. */
+int pcl_gelu_fwd(float *Y, const float *X, long n, void *stream);
+int pcl_gelu_bwd(float *dX, const float *dY, const float *X, long n, void *stream);
+int pcl_vec_add(float *C, const float *A, const float *B, long n, void *stream);
 
 /* FP32 GEMV (M <= 8 rows): Y(M,N) = (accumulate ? Y : 0) + X(M,K)·op(W) + bias.
  * opW == PCL_OP_N: W is K x N (generate.c:95-107, transformer.c:174-195);

@@ -51,6 +51,8 @@ _ORACLE_PROTOS = {
     "orc_gemm_u8s8_raw_i32": (_l, [_vp, _i, _vp, _i, _vp, _i, _i, _i, _i]),
     "orc_gemm_int8_kernel": (None, [_vp, _i, _vp, _vp, _vp, _vp, _i, _i]),
     "orc_dequant": (None, [_vp, _i, _vp, _vp, _vp, _i, _i, _i]),
+    "orc_gelu_forward": (None, [_vp, _vp, _l]),
+    "orc_gelu_backward": (None, [_vp, _vp, _vp, _l]),
     "orc_attention_forward": (None, [_vp, _vp, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i]),
     "orc_attention_backward": (None, [_vp, _vp, _vp, _vp, _i, _vp, _vp, _vp, _i, _vp, _i, _i, _i, _i]),
     "orc_attention_forward_f64": (None, [_vp, _vp, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i]),
@@ -87,6 +89,8 @@ _REF_PROTOS = {
         "pcl_ref_train_t_size": (_i, []),
         "pcl_ref_attention_forward": (None, [_vp, _vp, _vp, _vp, _vp, _i, _i]),
         "pcl_ref_attention_backward": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i]),
+        "pcl_ref_gelu_forward": (None, [_vp, _vp, _i]),
+        "pcl_ref_gelu_backward": (None, [_vp, _vp, _vp, _i]),
     },
     "libref_train_h64.so": {
         "pcl_ref_train_d_model": (_i, []),
@@ -219,6 +223,21 @@ def dequant(V, sa, sb):
     out = np.empty((M, N), np.float32)
     oracle().orc_dequant(p(np.ascontiguousarray(V)), N, p(sa), p(sb), p(out), N, M, N)
     return out
+
+
+def gelu(x):
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty_like(x)
+    oracle().orc_gelu_forward(p(out), p(x), x.size)
+    return out
+
+
+def gelu_backward(dout, x):
+    x = np.ascontiguousarray(x, np.float32)
+    dout = np.ascontiguousarray(dout, np.float32)
+    din = np.empty_like(x)
+    oracle().orc_gelu_backward(p(din), p(dout), p(x), x.size)
+    return din
 
 
 def attention_forward(q, k, v, B, T, H, dh, f64=False):

@@ -19,6 +19,10 @@
  *                                 sum Au*Bq - 128*colsum = sum (Au-128)*Bq checked
  *                                 against the reference gemm_int8_kernel output
  *   orc_dequant ................. bit-exact against gemm_bench.c's float output
+ *   orc_gelu_forward / _backward  train.c built from source (oracle/_ref); the
+ *                                 exact erf GELU within the tanh approximation's
+ *                                 error; the derivative against central
+ *                                 differences of the forward
  *   orc_attention_forward / _backward
  *                                 train.c built from source (oracle/_ref) at two
  *                                 head sizes (16 and 64); closed forms (T = 1 gives
@@ -288,6 +292,30 @@ void orc_matvec(float *out, const float *x, const float *W, const float *b, int 
             const float *wr = W + (size_t)k * N;
             for (int n = 0; n < N; n++) o[n] += a * wr[n];
         }
+    }
+}
+
+/* ------------------------------------------------------------- GELU ------ */
+static const float ORC_GELU_K = 0.7978845608028654f; /* sqrt(2/pi), train.c:315 */
+
+void orc_gelu_forward(float *out, const float *in, long n) {
+    /* train.c:316-322 */
+    for (long i = 0; i < n; i++) {
+        const float x = in[i];
+        const float t = tanhf(ORC_GELU_K * (x + 0.044715f * x * x * x));
+        out[i] = 0.5f * x * (1.0f + t);
+    }
+}
+
+void orc_gelu_backward(float *din, const float *dout, const float *in, long n) {
+    /* train.c:324-333 */
+    for (long i = 0; i < n; i++) {
+        const float x = in[i];
+        const float u = ORC_GELU_K * (x + 0.044715f * x * x * x);
+        const float t = tanhf(u);
+        const float dudx = ORC_GELU_K * (1.0f + 3.0f * 0.044715f * x * x);
+        const float dgelu = 0.5f * (1.0f + t) + 0.5f * x * (1.0f - t * t) * dudx;
+        din[i] = dout[i] * dgelu;
     }
 }
 

@@ -100,6 +100,11 @@ void orc_quantize_B_cols(const float *B, int8_t *Bq, float *bscale, int K, int N
 /* Unpack the VNNI panel layout back to Bq (K x N row-major; rows >= K unused). */
 void orc_unpack_vnni(const int8_t *Bp, int8_t *Bq, int K, int N, int Kpad);
 
+/* train.c:314-333 tanh-GELU: out = 0.5 x (1 + tanhf(K (x + 0.044715 x^3))),
+ * K = 0.7978845608028654f; backward din = dout * dgelu(x) (SET). */
+void orc_gelu_forward(float *out, const float *in, long n);
+void orc_gelu_backward(float *din, const float *dout, const float *in, long n);
+
 /* Causal multi-head attention, train.c:339-370 attention_forward generalised
  * to B sequences of T tokens, H heads of dh: q/k/v rows of ld floats (row
  * b*T + t, head h at columns [h*dh, (h+1)*dh)), att rows of ld_att.

@@ -32,3 +32,7 @@ void pcl_ref_attention_backward(float *dq, float *dk, float *dv, const float *d_
                                 const float *k, const float *v, const float *probs, int B, int T) {
     attention_backward(dq, dk, dv, d_att, q, k, v, probs, B, T);
 }
+void pcl_ref_gelu_forward(float *out, const float *in, int n) { gelu_forward(out, in, n); }
+void pcl_ref_gelu_backward(float *din, const float *dout, const float *in, int n) {
+    gelu_backward(din, dout, in, n);
+}

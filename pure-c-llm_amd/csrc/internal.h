@@ -36,13 +36,23 @@ struct SgemmPlan {
     size_t part_bytes;  // workspace bytes (0 when splits == 1)
 };
 SgemmPlan plan_sgemm(int M, int N, int K);
-// C(M,N) = (accumulate ? C : 0) + op(A)(M,K) . op(B)(K,N) + bias
+// Epilogues on v = op(A).op(B) + bias (accumulate must be 0 with any but NONE):
+//   EPI_GELU: aux_out[m,n] <- v (when aux_out != NULL), C <- gelu(v)
+//   EPI_RESID: C <- aux_in[m,n] + v;  EPI_GELU_BWD: C <- v * gelu'(aux_in[m,n])
+// aux arrays are M x N with leading dimension ld_aux.
+enum SgemmEpi { EPI_NONE = 0, EPI_GELU = 1, EPI_RESID = 2, EPI_GELU_BWD = 3 };
+// C(M,N) = (accumulate ? C : 0) + op(A)(M,K) . op(B)(K,N) + bias, then the epilogue
 // a_kcontig: element (m,k) of A at A[m*lda + k] (else A[k*lda + m]);
 // b_kcontig: element (k,n) of B at B[n*ldb + k] (else B[k*ldb + n]).
 hipError_t launch_sgemm(const SgemmPlan &p, bool a_kcontig, bool b_kcontig, int M, int N, int K,
                         const float *A, long lda, const float *B, long ldb, const float *bias,
                         int accumulate, float *C, long ldc, const Workspace &ws,
-                        hipStream_t stream);
+                        hipStream_t stream, int epi = EPI_NONE, const float *aux_in = nullptr,
+                        float *aux_out = nullptr, long ld_aux = 0);
+// op 0: out = gelu(a); 1: out = a * gelu'(b) (a = upstream gradient, b =
+// pre-activation); 2: out = a + b -- n elements (gpu_kernels.cu:228-251)
+hipError_t launch_elementwise(int op, long n, float *out, const float *a, const float *b,
+                              hipStream_t stream);
 
 // ---- INT8 GEMM (igemm.hip) ----
 // out_mode 0: C is int32 v; 1: C = float(v+off)*sb[n]; 2: C = float(v+off)*(sa[m]*sb[n])

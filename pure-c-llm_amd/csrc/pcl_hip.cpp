@@ -448,6 +448,59 @@ int pcl_sgemm(int opA, int opB, int M, int N, int K, const float *A, int lda, co
     return PCL_OK;
 }
 
+int pcl_sgemm_ex(int opA, int opB, int M, int N, int K, const float *A, int lda, const float *B,
+                 int ldb, const float *bias, int epilogue, const float *aux_in, float *aux_out,
+                 int ld_aux, float *C, int ldc, void *stream) {
+    CHECK_ARG(epilogue >= PCL_EPI_NONE && epilogue <= PCL_EPI_GELU_BWD,
+              "pcl_sgemm_ex: unknown epilogue %d", epilogue);
+    if (epilogue == PCL_EPI_NONE)
+        return pcl_sgemm(opA, opB, M, N, K, A, lda, B, ldb, bias, 0, C, ldc, stream);
+    CHECK_ARG(M >= 0 && N >= 0 && K >= 0, "pcl_sgemm_ex: negative dimension (M=%d N=%d K=%d)", M, N,
+              K);
+    CHECK_ARG((opA == PCL_OP_N || opA == PCL_OP_T) && (opB == PCL_OP_N || opB == PCL_OP_T),
+              "pcl_sgemm_ex: bad op (%d, %d)", opA, opB);
+    if (M == 0 || N == 0) return PCL_OK;
+    CHECK_ARG(C != nullptr, "pcl_sgemm_ex: C is NULL");
+    CHECK_ARG(ldc >= N, "pcl_sgemm_ex: ldc=%d < N=%d", ldc, N);
+    if (K > 0) {
+        CHECK_ARG(A && B, "pcl_sgemm_ex: NULL operand");
+        CHECK_ARG(lda >= (opA == PCL_OP_N ? K : M), "pcl_sgemm_ex: lda=%d too small", lda);
+        CHECK_ARG(ldb >= (opB == PCL_OP_N ? N : K), "pcl_sgemm_ex: ldb=%d too small", ldb);
+    }
+    CHECK_ARG(epilogue == PCL_EPI_GELU || aux_in != nullptr,
+              "pcl_sgemm_ex: the epilogue needs aux_in");
+    CHECK_ARG((aux_in == nullptr && aux_out == nullptr) || ld_aux >= N,
+              "pcl_sgemm_ex: ld_aux=%d < N=%d", ld_aux, N);
+    PCL_OK_OR_RETURN(do_init());
+    hipStream_t s = pick(stream);
+    pcl::SgemmPlan p = pcl::plan_sgemm(M, N, K);
+    StreamScratch *sc;
+    PCL_OK_OR_RETURN(get_scratch(s, p.part_bytes, 0, &sc));
+    HIP_OK(pcl::launch_sgemm(p, opA == PCL_OP_N, opB == PCL_OP_T, M, N, K, A, lda, B, ldb, bias, 0,
+                             C, ldc, sc->ws, s, epilogue, aux_in, epilogue == PCL_EPI_GELU ? aux_out : nullptr,
+                             ld_aux));
+    return PCL_OK;
+}
+
+static int elementwise(const char *who, int op, float *out, const float *a, const float *b,
+                       long n, void *stream) {
+    CHECK_ARG(n >= 0, "%s: negative length %ld", who, n);
+    if (n == 0) return PCL_OK;
+    CHECK_ARG(out && a && (op == 0 || b), "%s: NULL operand", who);
+    PCL_OK_OR_RETURN(do_init());
+    HIP_OK(pcl::launch_elementwise(op, n, out, a, b, pick(stream)));
+    return PCL_OK;
+}
+int pcl_gelu_fwd(float *Y, const float *X, long n, void *stream) {
+    return elementwise("pcl_gelu_fwd", 0, Y, X, nullptr, n, stream);
+}
+int pcl_gelu_bwd(float *dX, const float *dY, const float *X, long n, void *stream) {
+    return elementwise("pcl_gelu_bwd", 1, dX, dY, X, n, stream);
+}
+int pcl_vec_add(float *C, const float *A, const float *B, long n, void *stream) {
+    return elementwise("pcl_vec_add", 2, C, A, B, n, stream);
+}
+
 int pcl_bias_bwd(float *db, const float *dY, int M, int N, int ld, void *stream) {
     CHECK_ARG(M >= 0 && N >= 0, "pcl_bias_bwd: negative dimension");
     if (N == 0) return PCL_OK;
@@ -682,6 +735,13 @@ void gemm_tn(const float *A, const float *B, float *C, int M, int K, int N) {
 }
 void bias_bwd(float *db, const float *dY, int M, int N) {
     finish_void(pcl_bias_bwd(db, dY, M, N, N, nullptr));
+}
+void gelu_fwd(float *Y, const float *X, long n) { finish_void(pcl_gelu_fwd(Y, X, n, nullptr)); }
+void gelu_bwd(float *dX, const float *dY, const float *X, long n) {
+    finish_void(pcl_gelu_bwd(dX, dY, X, n, nullptr));
+}
+void vec_add(float *C, const float *A, const float *B, long n) {
+    finish_void(pcl_vec_add(C, A, B, n, nullptr));
 }
 
 static int need_attn_dims(const char *who) {

@@ -293,6 +293,75 @@ __global__ __launch_bounds__(256 * KG) void sgemm_mfma_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Epilogues (train.c:314-333 and gpu_kernels.cu:228-243 tanh-GELU, the
+// residual adds of train.c:522/527): applied to v = acc + bias.
+constexpr float GELU_C = 0.7978845608028654f;  // sqrt(2/pi)
+__device__ __forceinline__ float gelu_f(float x) {
+    return 0.5f * x * (1.0f + tanhf(GELU_C * (x + 0.044715f * x * x * x)));
+}
+__device__ __forceinline__ float gelu_grad(float x) {
+    const float t = tanhf(GELU_C * (x + 0.044715f * x * x * x));
+    const float dudx = GELU_C * (1.0f + 3.0f * 0.044715f * x * x);
+    return 0.5f * (1.0f + t) + 0.5f * x * (1.0f - t * t) * dudx;
+}
+// EPI_GELU: aux_out (if set) <- v, C <- gelu(v); EPI_RESID: C <- aux_in + v;
+// EPI_GELU_BWD: C <- v * gelu'(aux_in)
+template <int EPI>
+__device__ __forceinline__ float apply_epi(float v, const float *aux_in, float *aux_out, long ai) {
+    if constexpr (EPI == EPI_GELU) {
+        if (aux_out) aux_out[ai] = v;
+        return gelu_f(v);
+    } else if constexpr (EPI == EPI_RESID) {
+        return aux_in[ai] + v;
+    } else if constexpr (EPI == EPI_GELU_BWD) {
+        return v * gelu_grad(aux_in[ai]);
+    }
+    return v;
+}
+
+// The same epilogue as a separate pass over an M x N product already in C
+// (operands the fused kernels do not take: unaligned, split K, other layouts).
+// Grid (ceil(N / 256), M).
+__global__ void sgemm_epilogue_kernel(int epi, int M, int N, float *__restrict__ C, long ldc,
+                                      const float *__restrict__ aux_in,
+                                      float *__restrict__ aux_out, long ld_aux) {
+    const int n = blockIdx.x * 256 + threadIdx.x;
+    const long m = blockIdx.y;
+    if (n >= N) return;
+    float *c = C + m * ldc + n;
+    const long ai = m * ld_aux + n;
+    if (epi == EPI_GELU) *c = apply_epi<EPI_GELU>(*c, aux_in, aux_out, ai);
+    else if (epi == EPI_RESID) *c = apply_epi<EPI_RESID>(*c, aux_in, aux_out, ai);
+    else if (epi == EPI_GELU_BWD) *c = apply_epi<EPI_GELU_BWD>(*c, aux_in, aux_out, ai);
+}
+
+// Flat elementwise kernels of the reference GPU API (gpu_kernels.cu:228-251).
+__global__ void gelu_fwd_kernel(float *__restrict__ Y, const float *__restrict__ X, long n) {
+    const long i = blockIdx.x * (long)blockDim.x + threadIdx.x;
+    if (i < n) Y[i] = gelu_f(X[i]);
+}
+__global__ void gelu_bwd_kernel(float *__restrict__ dX, const float *__restrict__ dY,
+                                const float *__restrict__ X, long n) {
+    const long i = blockIdx.x * (long)blockDim.x + threadIdx.x;
+    if (i < n) dX[i] = dY[i] * gelu_grad(X[i]);
+}
+__global__ void vec_add_kernel(float *__restrict__ C, const float *__restrict__ A,
+                               const float *__restrict__ B, long n) {
+    const long i = blockIdx.x * (long)blockDim.x + threadIdx.x;
+    if (i < n) C[i] = A[i] + B[i];
+}
+
+hipError_t launch_elementwise(int op, long n, float *out, const float *a, const float *b,
+                              hipStream_t stream) {
+    if (n <= 0) return hipSuccess;
+    const dim3 grid((unsigned)((n + 255) / 256)), block(256);
+    if (op == 0) hipLaunchKernelGGL(gelu_fwd_kernel, grid, block, 0, stream, out, a, n);
+    else if (op == 1) hipLaunchKernelGGL(gelu_bwd_kernel, grid, block, 0, stream, out, a, b, n);
+    else hipLaunchKernelGGL(vec_add_kernel, grid, block, 0, stream, out, a, b, n);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
 // LDS-DMA pipeline. Operand tiles of SD_BK = 32 floats of K go from global
 // memory straight into a STAGES-deep LDS ring with global_load_lds_dwordx4
 // (no VGPR staging, no ds_write), issued by every wave; the wave's waits are
@@ -369,11 +438,12 @@ struct DmaTile {
     }
 };
 
-template <int BM, int BN, int KG, int STAGES, int SUB, bool A_KC, bool B_KC>
+template <int BM, int BN, int KG, int STAGES, int SUB, bool A_KC, bool B_KC, int EPI = EPI_NONE>
 __global__ __launch_bounds__(256 * KG) void sgemm_dma_kernel(
     const float *__restrict__ A, long lda, const float *__restrict__ B, long ldb,
     const float *__restrict__ bias, float *__restrict__ C, long ldc, int M, int N, int K,
-    int accumulate, int kchunk) {
+    int accumulate, int kchunk, const float *__restrict__ aux_in, float *__restrict__ aux_out,
+    long ld_aux) {
     constexpr int NW = 4 * KG;
     constexpr int SUBB = (BM + BN) * SD_BK * 4;  // one K tile of both operands
     using TA = DmaTile<BM, A_KC, NW, SUB, SUBB>;
@@ -610,12 +680,17 @@ __global__ __launch_bounds__(256 * KG) void sgemm_dma_kernel(
 #pragma unroll
         for (int i = 0; i < TM; i++) {
             const int rb = m0 + wm * WTM + i * 32 + g * 4;
+            // old C (accumulate) or the epilogue's input operand, loaded as a
+            // batch before the stores
+            constexpr bool AUX = EPI == EPI_RESID || EPI == EPI_GELU_BWD;
             float old[16];
-            if (accumulate) {
+            if (AUX || accumulate) {
+                const float *src = AUX ? aux_in : Cm;
+                const long lds_ = AUX ? ld_aux : ldcm;
                 static_for<0, 16>([&](auto V) {
                     constexpr int v = V.value;
                     if (KG == 1 || v / VH == kg)
-                        old[v] = Cm[(long)min(rb + (v >> 2) * 8 + (v & 3), M - 1) * ldcm + col];
+                        old[v] = src[(long)min(rb + (v >> 2) * 8 + (v & 3), M - 1) * lds_ + col];
                 });
             }
             static_for<0, 16>([&](auto V) {
@@ -624,7 +699,16 @@ __global__ __launch_bounds__(256 * KG) void sgemm_dma_kernel(
                     const int row = rb + (v >> 2) * 8 + (v & 3);
                     if (row < M) {
                         float out = acc[i][j][v] + bv;
-                        if (accumulate) out = old[v] + out;
+                        if constexpr (EPI == EPI_GELU) {
+                            if (aux_out) aux_out[(long)row * ld_aux + col] = out;
+                            out = gelu_f(out);
+                        } else if constexpr (EPI == EPI_RESID) {
+                            out = old[v] + out;
+                        } else if constexpr (EPI == EPI_GELU_BWD) {
+                            out = out * gelu_grad(old[v]);
+                        } else if (accumulate) {
+                            out = old[v] + out;
+                        }
                         Cm[(long)row * ldcm + col] = out;
                     }
                 }
@@ -633,32 +717,40 @@ __global__ __launch_bounds__(256 * KG) void sgemm_dma_kernel(
     }
 }
 
-template <int BM, int BN, int KG, int STAGES, int SUB, bool A_KC, bool B_KC>
+template <int BM, int BN, int KG, int STAGES, int SUB, bool A_KC, bool B_KC, int EPI = EPI_NONE>
 static hipError_t launch_dma(int M, int N, int K, int splits, int kchunk, const float *A, long lda,
                              const float *B, long ldb, const float *bias, int accumulate, float *C,
-                             long ldc, hipStream_t stream) {
+                             long ldc, hipStream_t stream, const float *aux_in = nullptr,
+                             float *aux_out = nullptr, long ld_aux = 0) {
     const int nblk = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
     if (nblk == 0) return hipSuccess;
-    hipLaunchKernelGGL((sgemm_dma_kernel<BM, BN, KG, STAGES, SUB, A_KC, B_KC>), dim3(nblk, splits),
+    hipLaunchKernelGGL((sgemm_dma_kernel<BM, BN, KG, STAGES, SUB, A_KC, B_KC, EPI>), dim3(nblk, splits),
                        dim3(256 * KG), 0, stream, A, lda, B, ldb, bias, C, ldc, M, N, K, accumulate,
-                       kchunk);
+                       kchunk, aux_in, aux_out, ld_aux);
     return hipGetLastError();
 }
 
 // Split-K epilogue: C = (accumulate ? C : 0) + (P_0 + P_1 + ... + bias), the
 // partial products added in split order (deterministic).
+// Grid (ceil(N / 256), M); applies the epilogue (accumulate only with EPI_NONE).
 __global__ void sgemm_splitk_reduce_kernel(const float *__restrict__ P, int splits, int M, int N,
                                            const float *__restrict__ bias, float *__restrict__ C,
-                                           long ldc, int accumulate) {
-    const long i = blockIdx.x * (long)blockDim.x + threadIdx.x;
-    const long MN = (long)M * N;
-    if (i >= MN) return;
-    const int m = (int)(i / N), n = (int)(i % N);
+                                           long ldc, int accumulate, int epi,
+                                           const float *__restrict__ aux_in,
+                                           float *__restrict__ aux_out, long ld_aux) {
+    const int n = blockIdx.x * 256 + threadIdx.x;
+    const long m = blockIdx.y;
+    if (n >= N) return;
+    const long MN = (long)M * N, i = m * N + n;
     float s = P[i];
     for (int z = 1; z < splits; z++) s += P[z * MN + i];
     float out = s + (bias ? bias[n] : 0.f);
-    float *c = C + (long)m * ldc + n;
-    if (accumulate) out = *c + out;
+    float *c = C + m * ldc + n;
+    const long ai = m * ld_aux + n;
+    if (epi == EPI_GELU) out = apply_epi<EPI_GELU>(out, aux_in, aux_out, ai);
+    else if (epi == EPI_RESID) out = apply_epi<EPI_RESID>(out, aux_in, aux_out, ai);
+    else if (epi == EPI_GELU_BWD) out = apply_epi<EPI_GELU_BWD>(out, aux_in, aux_out, ai);
+    else if (accumulate) out = *c + out;
     *c = out;
 }
 
@@ -714,11 +806,32 @@ SgemmPlan plan_sgemm(int M, int N, int K) {
     return p;
 }
 
+// Fused epilogues exist for the layouts the trainer uses them in: NN
+// (forward FF1 + GELU, O / FF2 + residual) and NT (dX of FF2 times GELU').
+template <bool A_KC, bool B_KC>
+constexpr bool epi_fused(int epi) {
+    return (A_KC && !B_KC && (epi == EPI_GELU || epi == EPI_RESID)) ||
+           (A_KC && B_KC && epi == EPI_GELU_BWD);
+}
+
+template <bool A_KC, bool B_KC, int EPI>
+static hipError_t launch_dma_epi(const SgemmPlan &p, int M, int N, int K, const float *A, long lda,
+                                 const float *B, long ldb, const float *bias, float *C, long ldc,
+                                 const float *aux_in, float *aux_out, long ld_aux,
+                                 hipStream_t stream) {
+    if (p.cfg == SG_64_KG2)
+        return launch_dma<64, 64, 2, 4, 1, A_KC, B_KC, EPI>(M, N, K, 1, K, A, lda, B, ldb, bias, 0, C,
+                                                            ldc, stream, aux_in, aux_out, ld_aux);
+    return launch_dma<128, 128, 2, 4, 1, A_KC, B_KC, EPI>(M, N, K, 1, K, A, lda, B, ldb, bias, 0, C,
+                                                          ldc, stream, aux_in, aux_out, ld_aux);
+}
+
 template <bool A_KC, bool B_KC>
 static hipError_t dispatch_layout(const SgemmPlan &p, int M, int N, int K, const float *A,
                                   long lda, const float *B, long ldb, const float *bias,
                                   int accumulate, float *C, long ldc, const Workspace &ws,
-                                  hipStream_t stream) {
+                                  hipStream_t stream, int epi, const float *aux_in,
+                                  float *aux_out, long ld_aux) {
     // 16-byte vector loads need the contiguous extent and leading dimension to
     // be multiples of 4 floats and 16-byte aligned bases (split-K chunks are
     // multiples of 64, so every chunk keeps that alignment).
@@ -734,6 +847,29 @@ static hipError_t dispatch_layout(const SgemmPlan &p, int M, int N, int K, const
     // Aligned operands with K a multiple of 32 (per split as well: split
     // chunks are multiples of 64) take the LDS-DMA pipeline.
     const bool dma_ok = vec && K % SD_BK == 0;
+    // With a K split the reduce pass applies the epilogue (below); otherwise the
+    // GEMM kernel does (fused layouts) or one elementwise pass after the product.
+    if (epi != EPI_NONE && !split) {
+        if (dma_ok && epi_fused<A_KC, B_KC>(epi)) {
+            if constexpr (A_KC && !B_KC) {
+                if (epi == EPI_GELU)
+                    return launch_dma_epi<A_KC, B_KC, EPI_GELU>(p, M, N, K, A, lda, B, ldb, bias, C, ldc,
+                                                                aux_in, aux_out, ld_aux, stream);
+                return launch_dma_epi<A_KC, B_KC, EPI_RESID>(p, M, N, K, A, lda, B, ldb, bias, C, ldc,
+                                                             aux_in, aux_out, ld_aux, stream);
+            } else if constexpr (A_KC && B_KC) {
+                return launch_dma_epi<A_KC, B_KC, EPI_GELU_BWD>(p, M, N, K, A, lda, B, ldb, bias, C,
+                                                                ldc, aux_in, aux_out, ld_aux, stream);
+            }
+        }
+        e = dispatch_layout<A_KC, B_KC>(p, M, N, K, A, lda, B, ldb, bias, 0, C, ldc, ws, stream,
+                                        EPI_NONE, nullptr, nullptr, 0);
+        if (e != hipSuccess) return e;
+        if ((long)M * N == 0) return hipSuccess;
+        hipLaunchKernelGGL(sgemm_epilogue_kernel, dim3((unsigned)((N + 255) / 256), (unsigned)M),
+                           dim3(256), 0, stream, epi, M, N, C, ldc, aux_in, aux_out, ld_aux);
+        return hipGetLastError();
+    }
     if (dma_ok) {
         if (p.cfg == SG_64_KG2)
             e = launch_dma<64, 64, 2, 4, 1, A_KC, B_KC>(M, N, K, p.splits, p.kchunk, A, lda, B, ldb, b,
@@ -760,28 +896,28 @@ static hipError_t dispatch_layout(const SgemmPlan &p, int M, int N, int K, const
         break;
     }
     if (e != hipSuccess || !split) return e;
-    const long MN = (long)M * N;
-    hipLaunchKernelGGL(sgemm_splitk_reduce_kernel, dim3((unsigned)((MN + 255) / 256)), dim3(256), 0,
-                       stream, static_cast<const float *>(ws.buf), p.splits, M, N, bias, C, ldc,
-                       accumulate);
+    hipLaunchKernelGGL(sgemm_splitk_reduce_kernel, dim3((unsigned)((N + 255) / 256), (unsigned)M),
+                       dim3(256), 0, stream, static_cast<const float *>(ws.buf), p.splits, M, N, bias,
+                       C, ldc, accumulate, epi, aux_in, aux_out, ld_aux);
     return hipGetLastError();
 }
 
 hipError_t launch_sgemm(const SgemmPlan &p, bool a_kcontig, bool b_kcontig, int M, int N, int K,
                         const float *A, long lda, const float *B, long ldb, const float *bias,
                         int accumulate, float *C, long ldc, const Workspace &ws,
-                        hipStream_t stream) {
+                        hipStream_t stream, int epi, const float *aux_in, float *aux_out,
+                        long ld_aux) {
     if (a_kcontig && !b_kcontig)
         return dispatch_layout<true, false>(p, M, N, K, A, lda, B, ldb, bias, accumulate, C, ldc, ws,
-                                            stream);
+                                            stream, epi, aux_in, aux_out, ld_aux);
     if (a_kcontig && b_kcontig)
         return dispatch_layout<true, true>(p, M, N, K, A, lda, B, ldb, bias, accumulate, C, ldc, ws,
-                                           stream);
+                                           stream, epi, aux_in, aux_out, ld_aux);
     if (!a_kcontig && !b_kcontig)
         return dispatch_layout<false, false>(p, M, N, K, A, lda, B, ldb, bias, accumulate, C, ldc,
-                                             ws, stream);
+                                             ws, stream, epi, aux_in, aux_out, ld_aux);
     return dispatch_layout<false, true>(p, M, N, K, A, lda, B, ldb, bias, accumulate, C, ldc, ws,
-                                        stream);
+                                        stream, epi, aux_in, aux_out, ld_aux);
 }
 
 }  // namespace pcl

@@ -184,6 +184,53 @@ done:
     return rc;
 }
 
+/* --------------------------------------------------- GEMM + epilogue ---- */
+/* One step = the product with its elementwise epilogue, either fused
+ * (pcl_sgemm_ex, one kernel) or as the reference sequences it: pcl_sgemm then
+ * gelu_fwd / vec_add / gelu_bwd (two kernels, the product round-tripping HBM). */
+typedef struct {
+    int opA, opB, M, N, K, epi, fused;
+    void *A, *B, *bias, *C, *aux, *tmp;
+} sgemm_ex_ctx;
+
+static int sgemm_ex_step(void *c_, int i) {
+    sgemm_ex_ctx *c = c_;
+    (void)i;
+    const int lda = c->opA == PCL_OP_N ? c->K : c->M, ldb = c->opB == PCL_OP_N ? c->N : c->K;
+    const long mn = (long)c->M * c->N;
+    if (c->fused)
+        return pcl_sgemm_ex(c->opA, c->opB, c->M, c->N, c->K, c->A, lda, c->B, ldb, c->bias, c->epi,
+                            c->epi == PCL_EPI_GELU ? NULL : c->aux,
+                            c->epi == PCL_EPI_GELU ? c->aux : NULL, c->N, c->C, c->N, NULL);
+    void *prod = c->epi == PCL_EPI_GELU ? c->aux : c->tmp;
+    int rc = pcl_sgemm(c->opA, c->opB, c->M, c->N, c->K, c->A, lda, c->B, ldb, c->bias, 0, prod, c->N,
+                       NULL);
+    if (rc != PCL_OK) return rc;
+    if (c->epi == PCL_EPI_GELU) return pcl_gelu_fwd(c->C, prod, mn, NULL);
+    if (c->epi == PCL_EPI_RESID) return pcl_vec_add(c->C, c->aux, prod, mn, NULL);
+    return pcl_gelu_bwd(c->C, prod, c->aux, mn, NULL);
+}
+
+int pcl_bench_sgemm_ex(int opA, int opB, int M, int N, int K, int epi, int fused, int warmup,
+                       int steps, double *ms_total) {
+    int rc = PCL_OK;
+    sgemm_ex_ctx c = {opA, opB, M, N, K, epi, fused, NULL, NULL, NULL, NULL, NULL, NULL};
+    c.A = dev_f32((size_t)M * K, 21, -1.f, 1.f);
+    c.B = dev_f32((size_t)K * N, 22, -0.05f, 0.05f);
+    c.bias = dev_f32((size_t)N, 24, -0.1f, 0.1f);
+    c.C = pcl_malloc((size_t)M * N * sizeof(float));
+    c.aux = dev_f32((size_t)M * N, 25, -1.f, 1.f);
+    c.tmp = pcl_malloc((size_t)M * N * sizeof(float));
+    if (!c.A || !c.B || !c.bias || !c.C || !c.aux || !c.tmp) {
+        rc = PCL_ERR_OOM;
+        goto done;
+    }
+    TRY(time_steps(sgemm_ex_step, &c, warmup, steps, ms_total));
+done:
+    pcl_free(c.A), pcl_free(c.B), pcl_free(c.bias), pcl_free(c.C), pcl_free(c.aux), pcl_free(c.tmp);
+    return rc;
+}
+
 /* ------------------------------------------------------------ attention ---- */
 /* One step = one pcl_attn_fwd over B sequences of T tokens, H heads of dh
  * (Q, K, V ~ N-ish(0,1) as U[-1.7,1.7]); probs stored when with_probs. */

@@ -27,6 +27,7 @@ PCL_ERR_OOM = 4
 PCL_ERR_UNSET_DIMS = 5
 PCL_ERR_RANGE = 6
 OP_N, OP_T = 0, 1
+EPI_NONE, EPI_GELU, EPI_RESID, EPI_GELU_BWD = 0, 1, 2, 3
 
 if not os.path.exists(LIB_PATH):
     raise ImportError(f"{LIB_PATH} is not built (run __graft_entry__.build() or make -C pure-c-llm_amd)")
@@ -89,11 +90,18 @@ _PROTOS = {
     "gemm_tn": (None, [_vp, _vp, _vp, _i, _i, _i]),
     "bias_bwd": (None, [_vp, _vp, _i, _i]),
     "attn_fwd": (None, [_vp, _vp, _vp, _vp, _vp]),
+    "gelu_fwd": (None, [_vp, _vp, C.c_long]),
+    "gelu_bwd": (None, [_vp, _vp, _vp, C.c_long]),
+    "vec_add": (None, [_vp, _vp, _vp, C.c_long]),
     "attn_bwd": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     # native
     "pcl_sgemm": (_i, [_i, _i, _i, _i, _i, _vp, _i, _vp, _i, _vp, _i, _vp, _i, _vp]),
     "pcl_sgemv": (_i, [_i, _i, _i, _i, _vp, _i, _vp, _i, _vp, _i, _vp, _i, _vp]),
     "pcl_bias_bwd": (_i, [_vp, _vp, _i, _i, _i, _vp]),
+    "pcl_sgemm_ex": (_i, [_i, _i, _i, _i, _i, _vp, _i, _vp, _i, _vp, _i, _vp, _vp, _i, _vp, _i, _vp]),
+    "pcl_gelu_fwd": (_i, [_vp, _vp, C.c_long, _vp]),
+    "pcl_gelu_bwd": (_i, [_vp, _vp, _vp, C.c_long, _vp]),
+    "pcl_vec_add": (_i, [_vp, _vp, _vp, C.c_long, _vp]),
     "pcl_attn_fwd": (_i, [_vp, _vp, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i, _vp]),
     "pcl_attn_bwd": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _vp, _i, _vp, _i, _i, _i, _i, _i, _vp]),
     "pcl_s8_kpad": (_i, [_i]),

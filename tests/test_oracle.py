@@ -448,3 +448,35 @@ def test_attention_backward_vs_central_differences():
             lm = loss(*xs)
             num = (lp - lm) / (2 * eps)
             assert abs(num - grad[r, c]) < 2e-3 * max(1.0, abs(num)), (which, r, c, num, grad[r, c])
+
+
+# ----------------------------------------------------------------- GELU ----
+def test_gelu_oracle_vs_ref_train():
+    tr = _ref_or_skip("libref_train.so")
+    x = ob.normal((5000,), 131, 0.0, 2.0)
+    g = ob.normal((5000,), 132)
+    y_r, d_r = np.empty_like(x), np.empty_like(x)
+    tr.pcl_ref_gelu_forward(p(y_r), p(x), x.size)
+    tr.pcl_ref_gelu_backward(p(d_r), p(g), p(x), x.size)
+    # -ffast-math reassociates the cubic and vectorises tanhf: in the tails
+    # (x << 0, where 1 - t^2 cancels) single values differ by a few 1e-6
+    # absolute; the normwise bar is the REF_TOL used for every other function
+    assert ob.normwise_rel_err(ob.gelu(x), y_r) < REF_TOL
+    assert ob.normwise_rel_err(ob.gelu_backward(g, x), d_r) < REF_TOL
+
+
+def test_gelu_oracle_math():
+    # the tanh form approximates x*Phi(x) (exact GELU) to ~1e-3; its derivative
+    # matches central differences of the forward (in double)
+    from math import erf, sqrt
+    x = np.linspace(-6, 6, 1201).astype(np.float32)
+    exact = np.array([0.5 * v * (1 + erf(v / sqrt(2))) for v in x.astype(np.float64)])
+    assert np.max(np.abs(ob.gelu(x) - exact)) < 2e-3
+    assert ob.gelu(np.zeros(3, np.float32)).tolist() == [0.0, 0.0, 0.0]
+    k = 0.7978845608028654
+
+    def g64(v):
+        return 0.5 * v * (1 + np.tanh(k * (v + 0.044715 * v ** 3)))
+    h = 1e-4
+    num = (g64(x.astype(np.float64) + h) - g64(x.astype(np.float64) - h)) / (2 * h)
+    np.testing.assert_allclose(ob.gelu_backward(np.ones_like(x), x), num, rtol=0, atol=2e-5)
