@@ -142,6 +142,62 @@ def sgemm_epi(pcl, lib, opA, opB, M, N, K, epi, warmup, steps):
     return out
 
 
+def decode_e2e(pcl, dims=(256, 512, 16, 2048, 16, 2048), n_new=255, ref_tokens=24):
+    """Greedy decoding of a synthetic CKP1 checkpoint of the grown model
+    (block 256, d 512, 16 heads, d_ff 2048, 16 layers, vocab 2048): one prompt
+    token then n_new tokens fed back on the GPU, eagerly and as one graph
+    replay per token; beside it the reference generate.c forward (built from
+    source in oracle/_ref, OpenMP on all host cores) on the same checkpoint."""
+    import tempfile
+
+    import numpy as np
+
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import binding as ob
+
+    blk, d, h, df, nl, v = dims
+    tmp = tempfile.mkdtemp(prefix="pcl_ckp1_")
+    path = os.path.join(tmp, "grown.ckp1")
+    ob.write_ckp1(path, blk, d, h, df, nl, v, seed=77, wstd=0.05)
+    out = {"model": f"block {blk}, d_model {d}, heads {h}, d_ff {df}, layers {nl}, vocab {v}",
+           "weights_MB": round(4.0 * (v * d + blk * d + nl * (4 * d * d + 2 * d * df)) / 1e6, 1)}
+    m = pcl.lib.pcl_model_load(path.encode())
+    if not m:
+        raise RuntimeError(f"pcl_model_load: {pcl.last_error()}")
+    try:
+        prompt = np.array([1], np.int32)
+        toks = np.empty(n_new, np.int32)
+        for graph in (0, 1):
+            _check(pcl, pcl.lib.pcl_model_generate(m, pcl.ptr(prompt), 1, n_new, pcl.ptr(toks), graph), "generate")
+            t0 = time.perf_counter()
+            _check(pcl, pcl.lib.pcl_model_generate(m, pcl.ptr(prompt), 1, n_new, pcl.ptr(toks), graph), "generate")
+            dt = time.perf_counter() - t0
+            tag = "graph" if graph else "eager"
+            out[f"{tag}_tokens_per_s"] = round(n_new / dt, 1)
+            out[f"{tag}_ms_per_token"] = round(1e3 * dt / n_new, 4)
+    finally:
+        pcl.lib.pcl_model_free(m)
+    gen = ob.ref("libref_generate.so")
+    if gen is not None:
+        gen.pcl_ref_gen_load(path.encode())
+        logits = np.empty(v, np.float32)
+        tok = 1
+        t0 = time.perf_counter()
+        for pos in range(ref_tokens):
+            gen.pcl_ref_gen_forward(tok, pos, ob.p(logits))
+            tok = int(np.argmax(logits))
+        dt = time.perf_counter() - t0
+        out["cpu_reference_tokens_per_s"] = round(ref_tokens / dt, 1)
+        out["cpu_reference_sample"] = (f"generate.c forward, positions 0..{ref_tokens - 1}, "
+                                       f"OpenMP threads {os.environ.get('OMP_NUM_THREADS', 'default')}")
+    try:
+        os.remove(path)
+        os.rmdir(tmp)
+    except OSError:
+        pass
+    return out
+
+
 def read_traffic():
     """HBM bytes per launch of the primary kernel, measured by rocprofv3 --pmc
     (FETCH_SIZE + WRITE_SIZE, calibrated on a copy of known size) and recorded
@@ -201,6 +257,7 @@ CASES = {
     "fp32_1024": lambda pcl, lib, w, s: sgemm(pcl, lib, 0, 0, 1024, 1024, 1024, 0, w, s),
     "fp32_ffn_up": lambda pcl, lib, w, s: sgemm(pcl, lib, 0, 0, 4096, 4096, 1024, 0, w, s),
     "epi_350m_ffn_up_gelu": lambda pcl, lib, w, s: sgemm_epi(pcl, lib, 0, 0, 4096, 4096, 1024, 1, w, s),
+    "decode_e2e": lambda pcl, lib, w, s: decode_e2e(pcl),
     "attn_350m": lambda pcl, lib, w, s: attn(pcl, lib, 4, 1024, 16, 64, True, w, s),
     "attn_350m_noprobs": lambda pcl, lib, w, s: attn(pcl, lib, 4, 1024, 16, 64, False, w, s),
     "attn_trainer_dh128": lambda pcl, lib, w, s: attn(pcl, lib, 4, 1024, 12, 128, True, w, s),
@@ -364,6 +421,7 @@ def main():
                 dec[f"fp32_M{Mt}{tag}"] = gemv(pcl, lib, fp32_kinds, Mt, fp32_step, 3, 2, 10, graph=g)
                 dec[f"int8_M{Mt}{tag}"] = gemv(pcl, lib, 2, Mt, grown_i8, 11, 2, 10, graph=g)
         ex["grown_decode_gemv"] = dec
+        ex["decode_e2e_grown"] = decode_e2e(pcl)
         ex["head_350m_gemv_fp32"] = {f"M{Mt}": gemv(pcl, lib, 1, Mt, [(1024, 50257)], 3, 2, 20) for Mt in (1, 8)}
         ex["head_350m_gemv_int8"] = {f"M{Mt}": gemv(pcl, lib, 2, Mt, [(1024, 50257)], 6, 2, 20) for Mt in (1, 8)}
         # GEMM epilogues fused against the reference's two-pass sequence (350M class)

@@ -312,6 +312,30 @@ int pcl_quantize_b_cols(const float *B, int K, int N, int8_t *Bpk, float *bscale
 int pcl_quantize_b_vnni(const float *B, int K, int N, int Kpad, int8_t *Bp, float *bscale,
                         int32_t *colsum, void *stream);
 
+/* ============================== 4. a checkpoint on the GPU ================ */
+
+/* A CKP1 checkpoint (train.c:633-670 writes it; generate.c:49-76 reads it:
+ * int[8] {0x434B5031, block, d_model, n_heads, d_ff, n_layers, vocab, step}
+ * then the tensors in registration order) loaded once into device memory with
+ * its KV cache, decoded one token at a time as generate.c:118-183 does. The
+ * head size d_model / n_heads must divide 256. NULL on failure (the reason in
+ * pcl_last_error). */
+typedef struct pcl_model pcl_model;
+pcl_model *pcl_model_load(const char *path);
+/* The checkpoint's int[8] header. */
+int pcl_model_header(const pcl_model *m, int hdr[8]);
+/* generate.c forward(tok, pos): one KV-cached step (the cache rows 0..pos-1 must
+ * hold this sequence's earlier positions); logits (host, vocab floats) may be
+ * NULL. Synchronous. */
+int pcl_model_forward(pcl_model *m, int tok, int pos, float *logits);
+/* Greedy decoding (generate.c:188-191 argmax, temperature 0): feeds prompt[0..
+ * n_prompt) at positions 0.., then produces n_new tokens into out, each fed back
+ * on the GPU (the token and position stay in device memory). use_graph != 0
+ * replays one captured step per token. Needs n_prompt + n_new - 1 <= block. */
+int pcl_model_generate(pcl_model *m, const int *prompt, int n_prompt, int n_new, int *out,
+                       int use_graph);
+void pcl_model_free(pcl_model *m);
+
 #ifdef __cplusplus
 }
 #endif

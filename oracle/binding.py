@@ -56,6 +56,10 @@ _ORACLE_PROTOS = {
     "orc_attention_forward": (None, [_vp, _vp, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i]),
     "orc_attention_backward": (None, [_vp, _vp, _vp, _vp, _i, _vp, _vp, _vp, _i, _vp, _i, _i, _i, _i]),
     "orc_attention_forward_f64": (None, [_vp, _vp, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i]),
+    "orc_model_load": (_vp, [C.c_char_p]),
+    "orc_model_header": (None, [_vp, _vp]),
+    "orc_model_forward": (None, [_vp, _i, _i, _vp]),
+    "orc_model_free": (None, [_vp]),
     "orc_rms_rel": (_d, [_vp, _vp, _l]),
     "orc_max_abs_diff": (_d, [_vp, _vp, _l]),
 }
@@ -98,6 +102,10 @@ _REF_PROTOS = {
         "pcl_ref_train_t_size": (_i, []),
         "pcl_ref_attention_forward": (None, [_vp, _vp, _vp, _vp, _vp, _i, _i]),
         "pcl_ref_attention_backward": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i]),
+    },
+    "libref_generate.so": {
+        "pcl_ref_gen_load": (_i, [C.c_char_p]),
+        "pcl_ref_gen_forward": (None, [_i, _i, _vp]),
     },
     "libref_model.so": {
         "pcl_ref_model_d_model": (_i, []),
@@ -261,6 +269,54 @@ def attention_backward(d_att, q, k, v, probs, B, T, H, dh, dq=None, dk=None, dv=
                                     p(v), ld, p(np.ascontiguousarray(probs, np.float32)), B, T,
                                     H, dh)
     return dq, dk, dv
+
+
+def write_ckp1(path, blk, d, h, df, nl, v, seed, step=0, wstd=0.02):
+    """A CKP1 checkpoint (train.c:633-648 layout) with synthetic parameters:
+    gains 1 + N(0, 0.1), biases N(0, 0.02), matrices N(0, wstd), embeddings N(0, 0.1)."""
+    import struct
+    sizes = []
+    sizes.append(("emb", v * d))
+    sizes.append(("emb", blk * d))
+    for _ in range(nl):
+        sizes += [("g", d), ("b", d), ("w", d * d), ("b", d), ("w", d * d), ("b", d), ("w", d * d), ("b", d),
+                  ("w", d * d), ("b", d), ("g", d), ("b", d), ("w", d * df), ("b", df), ("w", df * d), ("b", d)]
+    sizes += [("g", d), ("b", d)]
+    with open(path, "wb") as f:
+        f.write(struct.pack("<8i", 0x434B5031, blk, d, h, df, nl, v, step))
+        for i, (kind, n) in enumerate(sizes):
+            s = seed * 1000 + i + 1
+            if kind == "g":
+                a = normal((n,), s, 1.0, 0.1)
+            elif kind == "b":
+                a = normal((n,), s, 0.0, 0.02)
+            elif kind == "w":
+                a = normal((n,), s, 0.0, wstd)
+            else:
+                a = normal((n,), s, 0.0, 0.1)
+            f.write(a.astype("<f4").tobytes())
+
+
+class OracleModel:
+    """orc_model_* (generate.c restated) over a CKP1 file."""
+
+    def __init__(self, path):
+        self.m = oracle().orc_model_load(path.encode())
+        if not self.m:
+            raise ValueError(f"{path}: not a CKP1 checkpoint")
+        hdr = np.empty(8, np.int32)
+        oracle().orc_model_header(self.m, p(hdr))
+        self.hdr = hdr.tolist()
+
+    def forward(self, tok, pos):
+        out = np.empty(self.hdr[6], np.float32)
+        oracle().orc_model_forward(self.m, tok, pos, p(out))
+        return out
+
+    def close(self):
+        if self.m:
+            oracle().orc_model_free(self.m)
+            self.m = None
 
 
 def normwise_rel_err(X, R):

@@ -23,6 +23,10 @@
  *                                 exact erf GELU within the tanh approximation's
  *                                 error; the derivative against central
  *                                 differences of the forward
+ *   orc_model_load / _forward .. generate.c (with tokenizer.c) built from source
+ *                                 (oracle/_ref) on written checkpoints: logits
+ *                                 token by token; T = 1 and equal-key closed forms
+ *                                 through the attention above
  *   orc_attention_forward / _backward
  *                                 train.c built from source (oracle/_ref) at two
  *                                 head sizes (16 and 64); closed forms (T = 1 gives
@@ -34,6 +38,7 @@
 #include "pcl_oracle.h"
 
 #include <math.h>
+#include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -317,6 +322,141 @@ void orc_gelu_backward(float *din, const float *dout, const float *in, long n) {
         const float dgelu = 0.5f * (1.0f + t) + 0.5f * x * (1.0f - t * t) * dudx;
         din[i] = dout[i] * dgelu;
     }
+}
+
+/* ------------------------------------------------------ CKP1 decode ------ */
+struct orc_model {
+    int hdr[8];
+    int BLK, D, H, DF, L, V, DH;
+    float *wte, *wpe, *gf, *bf, *buf;
+    float **lw; /* per layer: g1 b1 Wq bq Wk bk Wv bv Wo bo g2 b2 W1 bff1 W2 bff2 */
+    float *kc, *vc;
+    float *x, *ln, *q, *att, *proj, *h, *sc;
+};
+
+orc_model *orc_model_load(const char *path) {
+    /* generate.c:49-76 */
+    FILE *f = fopen(path, "rb");
+    if (!f) return NULL;
+    orc_model *m = (orc_model *)calloc(1, sizeof(orc_model));
+    if (fread(m->hdr, sizeof(int), 8, f) != 8 || m->hdr[0] != 0x434B5031) {
+        fclose(f);
+        free(m);
+        return NULL;
+    }
+    m->BLK = m->hdr[1], m->D = m->hdr[2], m->H = m->hdr[3], m->DF = m->hdr[4];
+    m->L = m->hdr[5], m->V = m->hdr[6], m->DH = m->D / m->H;
+    const long D = m->D, F = m->DF;
+    const long sizes[16] = {D, D, D * D, D, D * D, D, D * D, D, D * D, D, D, D, D * F, F, F * D, D};
+    long per = 0;
+    for (int i = 0; i < 16; i++) per += sizes[i];
+    const long n = (long)m->V * D + (long)m->BLK * D + m->L * per + 2 * D;
+    m->buf = (float *)malloc(sizeof(float) * (size_t)n);
+    if (fread(m->buf, sizeof(float), (size_t)n, f) != (size_t)n) {
+        fclose(f);
+        free(m->buf);
+        free(m);
+        return NULL;
+    }
+    fclose(f);
+    float *p = m->buf;
+    m->wte = p, p += (long)m->V * D;
+    m->wpe = p, p += (long)m->BLK * D;
+    m->lw = (float **)malloc(sizeof(float *) * 16 * (size_t)m->L);
+    for (int l = 0; l < m->L; l++)
+        for (int i = 0; i < 16; i++) m->lw[l * 16 + i] = p, p += sizes[i];
+    m->gf = p, p += D;
+    m->bf = p;
+    m->kc = (float *)calloc((size_t)m->L * m->BLK * D, sizeof(float));
+    m->vc = (float *)calloc((size_t)m->L * m->BLK * D, sizeof(float));
+    m->x = (float *)malloc(sizeof(float) * D);
+    m->ln = (float *)malloc(sizeof(float) * D);
+    m->q = (float *)malloc(sizeof(float) * D);
+    m->att = (float *)malloc(sizeof(float) * D);
+    m->proj = (float *)malloc(sizeof(float) * D);
+    m->h = (float *)malloc(sizeof(float) * F);
+    m->sc = (float *)malloc(sizeof(float) * (size_t)m->BLK);
+    return m;
+}
+
+void orc_model_header(const orc_model *m, int hdr[8]) { memcpy(hdr, m->hdr, sizeof m->hdr); }
+
+static void orc_ln_row(const float *x, const float *g, const float *b, float *y, int n) {
+    /* generate.c:106-114 */
+    float mu = 0, var = 0;
+    for (int i = 0; i < n; i++) mu += x[i];
+    mu /= n;
+    for (int i = 0; i < n; i++) {
+        const float d = x[i] - mu;
+        var += d * d;
+    }
+    var /= n;
+    const float rs = 1.0f / sqrtf(var + 1e-5f);
+    for (int i = 0; i < n; i++) y[i] = (x[i] - mu) * rs * g[i] + b[i];
+}
+
+void orc_model_forward(orc_model *m, int tok, int pos, float *logits) {
+    /* generate.c:170-183 forward and :118-167 block */
+    const int D = m->D, DH = m->DH, F = m->DF;
+    const float *te = m->wte + (size_t)tok * D, *pe = m->wpe + (size_t)pos * D;
+    for (int i = 0; i < D; i++) m->x[i] = te[i] + pe[i];
+    for (int l = 0; l < m->L; l++) {
+        float **w = m->lw + l * 16;
+        float *kc = m->kc + (size_t)l * m->BLK * D, *vc = m->vc + (size_t)l * m->BLK * D;
+        float *krow = kc + (size_t)pos * D, *vrow = vc + (size_t)pos * D;
+        orc_ln_row(m->x, w[0], w[1], m->ln, D);
+        orc_matvec(m->q, m->ln, w[2], w[3], 1, D, D);
+        orc_matvec(krow, m->ln, w[4], w[5], 1, D, D);
+        orc_matvec(vrow, m->ln, w[6], w[7], 1, D, D);
+        const float scale = 1.0f / sqrtf((float)DH);
+        for (int h = 0; h < m->H; h++) {
+            const int off = h * DH;
+            float maxv = -1e30f;
+            for (int j = 0; j <= pos; j++) {
+                const float *kj = kc + (size_t)j * D + off;
+                float dot = 0;
+                for (int d = 0; d < DH; d++) dot += m->q[off + d] * kj[d];
+                dot *= scale;
+                m->sc[j] = dot;
+                if (dot > maxv) maxv = dot;
+            }
+            float sum = 0;
+            for (int j = 0; j <= pos; j++) {
+                const float e = expf(m->sc[j] - maxv);
+                m->sc[j] = e;
+                sum += e;
+            }
+            const float inv = 1.0f / sum;
+            float *oh = m->att + off;
+            for (int d = 0; d < DH; d++) oh[d] = 0;
+            for (int j = 0; j <= pos; j++) {
+                const float pj = m->sc[j] * inv;
+                const float *vj = vc + (size_t)j * D + off;
+                for (int d = 0; d < DH; d++) oh[d] += pj * vj[d];
+            }
+        }
+        orc_matvec(m->proj, m->att, w[8], w[9], 1, D, D);
+        for (int i = 0; i < D; i++) m->x[i] += m->proj[i];
+        orc_ln_row(m->x, w[10], w[11], m->ln, D);
+        orc_matvec(m->h, m->ln, w[12], w[13], 1, D, F);
+        orc_gelu_forward(m->h, m->h, F);
+        orc_matvec(m->proj, m->h, w[14], w[15], 1, F, D);
+        for (int i = 0; i < D; i++) m->x[i] += m->proj[i];
+    }
+    orc_ln_row(m->x, m->gf, m->bf, m->ln, D);
+    for (int v = 0; v < m->V; v++) {
+        const float *wv = m->wte + (size_t)v * D;
+        float dot = 0;
+        for (int d = 0; d < D; d++) dot += m->ln[d] * wv[d];
+        logits[v] = dot;
+    }
+}
+
+void orc_model_free(orc_model *m) {
+    if (!m) return;
+    free(m->buf), free(m->lw), free(m->kc), free(m->vc);
+    free(m->x), free(m->ln), free(m->q), free(m->att), free(m->proj), free(m->h), free(m->sc);
+    free(m);
 }
 
 /* -------------------------------------------------------- attention ------ */

@@ -105,6 +105,17 @@ void orc_unpack_vnni(const int8_t *Bp, int8_t *Bq, int K, int N, int Kpad);
 void orc_gelu_forward(float *out, const float *in, long n);
 void orc_gelu_backward(float *din, const float *dout, const float *in, long n);
 
+/* generate.c:49-183 restated: a CKP1 checkpoint (train.c:633-648 layout) in
+ * host memory with its KV cache, and forward(tok, pos) -> logits (V floats):
+ * embedding, per layer ln -> Wq/Wk/Wv matvecs -> attention over the cache ->
+ * Wo matvec added into x -> ln -> W1 matvec -> tanh-GELU -> W2 added into x,
+ * final ln, tied head. NULL when the file is not a CKP1 checkpoint. */
+typedef struct orc_model orc_model;
+orc_model *orc_model_load(const char *path);
+void orc_model_header(const orc_model *m, int hdr[8]);
+void orc_model_forward(orc_model *m, int tok, int pos, float *logits);
+void orc_model_free(orc_model *m);
+
 /* Causal multi-head attention, train.c:339-370 attention_forward generalised
  * to B sequences of T tokens, H heads of dh: q/k/v rows of ld floats (row
  * b*T + t, head h at columns [h*dh, (h+1)*dh)), att rows of ld_att.

@@ -1,0 +1,175 @@
+// decode.hip -- the non-GEMV kernels of one KV-cached decode step
+// (generate.c:118-183): token + position embedding, LayerNorm of one row,
+// attention of the new token over the cache (appending its k, v), and a
+// greedy argmax that writes the next token and advances the position.
+//
+// The token and position live in device memory (tokpos[0], tokpos[1]), so a
+// whole step -- these kernels and the GEMVs between them -- can be captured
+// once as a graph and replayed token after token with no host round trip.
+#include "internal.h"
+
+#include <math.h>
+
+namespace pcl {
+
+// x = wte[tok] + wpe[pos]   (generate.c:172-175)
+__global__ void dec_embed_kernel(const float *__restrict__ wte, const float *__restrict__ wpe,
+                                 float *__restrict__ x, int D, const int *__restrict__ tokpos) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= D) return;
+    const long tok = tokpos[0], pos = tokpos[1];
+    x[i] = wte[tok * D + i] + wpe[pos * D + i];
+}
+
+// Block-wide sum of one value per thread (256 threads, 4 waves).
+__device__ __forceinline__ float dec_block_sum(float v, float *red) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    const int w = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    __syncthreads();
+    return red[0] + red[1] + red[2] + red[3];
+}
+
+// y = (x - mean) / sqrt(var + 1e-5) * g + b over one row of D (generate.c:106-114:
+// the mean first, then the mean squared deviation); one workgroup.
+__global__ __launch_bounds__(256) void dec_layernorm_kernel(const float *__restrict__ x,
+                                                            const float *__restrict__ g,
+                                                            const float *__restrict__ b,
+                                                            float *__restrict__ y, int D) {
+    __shared__ float red[4];
+    float s = 0.f;
+    for (int i = threadIdx.x; i < D; i += 256) s += x[i];
+    const float mu = dec_block_sum(s, red) / D;
+    float q = 0.f;
+    for (int i = threadIdx.x; i < D; i += 256) {
+        const float d = x[i] - mu;
+        q += d * d;
+    }
+    const float var = dec_block_sum(q, red) / D;
+    const float rs = 1.0f / sqrtf(var + 1e-5f);
+    for (int i = threadIdx.x; i < D; i += 256) y[i] = (x[i] - mu) * rs * g[i] + b[i];
+}
+
+// One head per workgroup (generate.c:130-152): append this position's k, v to
+// the cache, scores s_j = (q . k_j) * scale for j <= pos (the new row read
+// from qkv, older rows from the cache), softmax, att = sum_j p_j v_j. qkv
+// holds [q | k | v] (3*D floats); the cache rows are D floats. dh divides 256.
+__global__ __launch_bounds__(256) void dec_attn_kernel(const float *__restrict__ qkv,
+                                                       float *__restrict__ kc,
+                                                       float *__restrict__ vc,
+                                                       float *__restrict__ att, int D, int dh,
+                                                       const int *__restrict__ tokpos,
+                                                       float scale) {
+    extern __shared__ float dec_lds[];  // [blk] scores, then [256] partial sums
+    __shared__ float red[4];
+    const int h = blockIdx.x, tid = threadIdx.x, off = h * dh;
+    const int pos = tokpos[1];
+    const float *q = qkv + off, *knew = qkv + D + off, *vnew = qkv + 2 * D + off;
+    for (int d = tid; d < dh; d += 256) {
+        kc[(long)pos * D + off + d] = knew[d];
+        vc[(long)pos * D + off + d] = vnew[d];
+    }
+    float *sc = dec_lds;
+    float mloc = -INFINITY;
+    for (int j = tid; j <= pos; j += 256) {
+        const float *kj = j == pos ? knew : kc + (long)j * D + off;
+        float dot = 0.f;
+        for (int d = 0; d < dh; d++) dot += q[d] * kj[d];
+        dot *= scale;
+        sc[j] = dot;
+        mloc = fmaxf(mloc, dot);
+    }
+    // block max
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mloc = fmaxf(mloc, __shfl_xor(mloc, o));
+    if ((tid & 63) == 0) red[tid >> 6] = mloc;
+    __syncthreads();
+    const float m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float sloc = 0.f;
+    for (int j = tid; j <= pos; j += 256) {
+        const float e = expf(sc[j] - m);
+        sc[j] = e;
+        sloc += e;
+    }
+    const float inv = 1.0f / dec_block_sum(sloc, red);  // the block sum also orders sc[] writes
+    // output: thread t owns column d = t % dh of key group t / dh
+    const int G = 256 / dh, d = tid % dh, gq = tid / dh;
+    float acc = 0.f;
+    if (gq < G) {
+        for (int j = gq; j <= pos; j += G) {
+            const float *vj = j == pos ? vnew : vc + (long)j * D + off;
+            acc += sc[j] * inv * vj[d];
+        }
+    }
+    float *part = dec_lds + ((pos + 1 + 3) & ~3);
+    part[tid] = acc;
+    __syncthreads();
+    if (tid < dh) {
+        float o = 0.f;
+        for (int g2 = 0; g2 < G; g2++) o += part[g2 * dh + tid];
+        att[off + tid] = o;
+    }
+}
+
+// Greedy pick (generate.c:188-191: the first index of the maximum), written
+// as the next token; the position advances and out[pos + 1] records it.
+__global__ __launch_bounds__(1024) void dec_argmax_kernel(const float *__restrict__ logits, int V,
+                                                          int *__restrict__ tokpos,
+                                                          int *__restrict__ out, int out_cap) {
+    __shared__ float bv[16];
+    __shared__ int bi[16];
+    const int tid = threadIdx.x;
+    float best = -INFINITY;
+    int idx = V;
+    for (int i = tid; i < V; i += 1024) {
+        const float v = logits[i];
+        if (v > best || (v == best && i < idx)) best = v, idx = i;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(best, o);
+        const int oi = __shfl_xor(idx, o);
+        if (ov > best || (ov == best && oi < idx)) best = ov, idx = oi;
+    }
+    if ((tid & 63) == 0) bv[tid >> 6] = best, bi[tid >> 6] = idx;
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < 16; w++)
+            if (bv[w] > best || (bv[w] == best && bi[w] < idx)) best = bv[w], idx = bi[w];
+        const int pos = tokpos[1];
+        if (idx >= V) idx = 0;  // all NaN: keep a valid token
+        tokpos[0] = idx;
+        if (pos + 1 < out_cap) out[pos + 1] = idx;
+        tokpos[1] = pos + 1;
+    }
+}
+
+hipError_t launch_decode_embed(const float *wte, const float *wpe, float *x, int D,
+                               const int *tokpos, hipStream_t s) {
+    hipLaunchKernelGGL(dec_embed_kernel, dim3((D + 255) / 256), dim3(256), 0, s, wte, wpe, x, D,
+                       tokpos);
+    return hipGetLastError();
+}
+hipError_t launch_decode_layernorm(const float *x, const float *g, const float *b, float *y, int D,
+                                   hipStream_t s) {
+    hipLaunchKernelGGL(dec_layernorm_kernel, dim3(1), dim3(256), 0, s, x, g, b, y, D);
+    return hipGetLastError();
+}
+hipError_t launch_decode_attn(const float *qkv, float *kc, float *vc, float *att, int D, int H,
+                              int blk, const int *tokpos, hipStream_t s) {
+    const int dh = D / H;
+    if (dh <= 0 || 256 % dh != 0) return hipErrorInvalidValue;
+    const size_t lds = sizeof(float) * ((size_t)((blk + 3) & ~3) + 256);
+    hipLaunchKernelGGL(dec_attn_kernel, dim3(H), dim3(256), lds, s, qkv, kc, vc, att, D, dh, tokpos,
+                       1.0f / sqrtf((float)dh));
+    return hipGetLastError();
+}
+hipError_t launch_decode_argmax(const float *logits, int V, int *tokpos, int *out, int out_cap,
+                                hipStream_t s) {
+    hipLaunchKernelGGL(dec_argmax_kernel, dim3(1), dim3(1024), 0, s, logits, V, tokpos, out, out_cap);
+    return hipGetLastError();
+}
+
+}  // namespace pcl

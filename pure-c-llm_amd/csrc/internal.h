@@ -82,6 +82,22 @@ hipError_t launch_attn_bwd(const float *dO, long ldo, const float *Q, const floa
                            float *dK, float *dV, long ldg, int B, int T, int H, int dh,
                            float scale, int accumulate, hipStream_t stream);
 
+// ---- decode step (decode.hip); tokpos = {token, position} in device memory ----
+hipError_t launch_decode_embed(const float *wte, const float *wpe, float *x, int D,
+                               const int *tokpos, hipStream_t s);
+hipError_t launch_decode_layernorm(const float *x, const float *g, const float *b, float *y, int D,
+                                   hipStream_t s);
+// dh = D / H must divide 256; the cache holds blk rows of D floats
+hipError_t launch_decode_attn(const float *qkv, float *kc, float *vc, float *att, int D, int H,
+                              int blk, const int *tokpos, hipStream_t s);
+hipError_t launch_decode_argmax(const float *logits, int V, int *tokpos, int *out, int out_cap,
+                                hipStream_t s);
+
+// Error reporting and device set-up of the C-ABI shim, for other translation
+// units of the library (model.cpp).
+int shim_error(int status, const char *msg);
+int shim_init();
+
 // ---- GEMV (gemv.hip) ----
 GemvPlan plan_sgemv(int w_trans, int M, int N, int K);
 // Column sums of a K x N matrix (bias_bwd): plan for launch_sgemv with x_ones.

@@ -1,0 +1,313 @@
+// model.cpp -- a CKP1 checkpoint on the GPU and its KV-cached greedy decode.
+//
+// The checkpoint (train.c:633-670 writes it, generate.c:49-76 reads it): an
+// int[8] header {magic 'CKP1', block, d_model, n_heads, d_ff, n_layers, vocab,
+// step} followed by every tensor's floats in registration order: wte (V x D),
+// wpe (block x D), per layer g1, b1, Wq, bq, Wk, bk, Wv, bv, Wo, bo, g2, b2,
+// W1 (D x FF), bff1, W2 (FF x D), bff2, then gf, bf. It is read once into one
+// device arena (weights, KV cache, per-token state); Wq, Wk, Wv are joined
+// column-wise into one D x 3D matrix so the three projections are one GEMV.
+//
+// One decode step is generate.c's forward(tok, pos) (:118-183): embedding,
+// per layer LayerNorm -> QKV GEMV -> attention over the cache -> O GEMV added
+// into x -> LayerNorm -> FF1 GEMV -> GELU -> FF2 GEMV added into x, then the
+// final LayerNorm, the tied-head GEMV and a greedy argmax. The token and
+// position live in device memory and the argmax advances them, so a step is
+// captured once as a graph and replayed per generated token.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <vector>
+
+#include "../../include/pcl_hip.h"
+#include "internal.h"
+
+namespace {
+
+constexpr int CKP1_MAGIC = 0x434B5031;
+
+struct Layer {
+    float *g1, *b1, *wqkv, *bqkv, *wo, *bo, *g2, *b2, *w1, *bf1, *w2, *bf2, *kc, *vc;
+};
+
+int fail(int status, const char *msg) { return pcl::shim_error(status, msg); }
+
+}  // namespace
+
+struct pcl_model {
+    int hdr[8];
+    int blk, d, h, df, nl, v;
+    float *arena = nullptr;
+    int *ints = nullptr;  // tokpos[2], then out[blk + 1]
+    int *host_tp = nullptr;  // pinned: {token, position} per position, copied to tokpos
+    float *wte, *wpe, *gf, *bf;
+    std::vector<Layer> lay;
+    float *x, *ln, *qkv, *att, *hh, *hg, *logits;
+    void *stream = nullptr;
+    void *graph = nullptr;
+};
+
+namespace {
+
+#define M_HIP(call)                                                        \
+    do {                                                                   \
+        hipError_t e_ = (call);                                            \
+        if (e_ != hipSuccess) {                                            \
+            char b_[256];                                                  \
+            snprintf(b_, sizeof b_, "%s: %s", #call, hipGetErrorString(e_)); \
+            return fail(PCL_ERR_HIP, b_);                                  \
+        }                                                                  \
+    } while (0)
+#define M_OK(expr)                  \
+    do {                            \
+        int s_ = (expr);            \
+        if (s_ != PCL_OK) return s_; \
+    } while (0)
+
+int step(pcl_model *m) {
+    hipStream_t s = (hipStream_t)m->stream;
+    const int D = m->d, F = m->df, V = m->v;
+    int *tokpos = m->ints, *out = m->ints + 2;
+    M_HIP(pcl::launch_decode_embed(m->wte, m->wpe, m->x, D, tokpos, s));
+    for (const Layer &y : m->lay) {
+        M_HIP(pcl::launch_decode_layernorm(m->x, y.g1, y.b1, m->ln, D, s));
+        M_OK(pcl_sgemv(PCL_OP_N, 1, 3 * D, D, m->ln, D, y.wqkv, 3 * D, y.bqkv, 0, m->qkv, 3 * D, s));
+        M_HIP(pcl::launch_decode_attn(m->qkv, y.kc, y.vc, m->att, D, m->h, m->blk, tokpos, s));
+        M_OK(pcl_sgemv(PCL_OP_N, 1, D, D, m->att, D, y.wo, D, y.bo, 1, m->x, D, s));
+        M_HIP(pcl::launch_decode_layernorm(m->x, y.g2, y.b2, m->ln, D, s));
+        M_OK(pcl_sgemv(PCL_OP_N, 1, F, D, m->ln, D, y.w1, F, y.bf1, 0, m->hh, F, s));
+        M_HIP(pcl::launch_elementwise(0, F, m->hg, m->hh, nullptr, s));
+        M_OK(pcl_sgemv(PCL_OP_N, 1, D, F, m->hg, F, y.w2, D, y.bf2, 1, m->x, D, s));
+    }
+    M_HIP(pcl::launch_decode_layernorm(m->x, m->gf, m->bf, m->ln, D, s));
+    M_OK(pcl_sgemv(PCL_OP_T, 1, V, D, m->ln, D, m->wte, D, nullptr, 0, m->logits, V, s));
+    M_HIP(pcl::launch_decode_argmax(m->logits, V, tokpos, out, m->blk + 1, s));
+    return PCL_OK;
+}
+
+// Each position has its own pinned slot, so a copy still queued on the stream
+// never reads a slot rewritten for a later position (callers synchronise the
+// stream before positions repeat).
+int set_tokpos(pcl_model *m, int tok, int pos) {
+    int *tp = m->host_tp + 2 * pos;
+    tp[0] = tok;
+    tp[1] = pos;
+    M_HIP(hipMemcpyAsync(m->ints, tp, 2 * sizeof(int), hipMemcpyHostToDevice, (hipStream_t)m->stream));
+    return PCL_OK;
+}
+
+int load(pcl_model *m, const char *path) {
+    FILE *f = fopen(path, "rb");
+    if (!f) return fail(PCL_ERR_INVALID_ARG, "pcl_model_load: cannot open the checkpoint");
+    std::vector<float> w;
+    int st = PCL_OK;
+    do {
+        if (fread(m->hdr, sizeof(int), 8, f) != 8 || m->hdr[0] != CKP1_MAGIC) {
+            st = fail(PCL_ERR_INVALID_ARG, "pcl_model_load: not a CKP1 checkpoint");
+            break;
+        }
+        m->blk = m->hdr[1], m->d = m->hdr[2], m->h = m->hdr[3], m->df = m->hdr[4];
+        m->nl = m->hdr[5], m->v = m->hdr[6];
+        const int dh = m->h > 0 ? m->d / m->h : 0;
+        if (m->blk <= 0 || m->d <= 0 || m->h <= 0 || m->df <= 0 || m->nl <= 0 || m->v <= 0 ||
+            m->d % m->h != 0 || 256 % dh != 0 || (long)m->d * m->df > (1L << 30) ||
+            (long)m->v * m->d > (1L << 30) || m->blk > 65536) {
+            st = fail(PCL_ERR_INVALID_ARG,
+                      "pcl_model_load: unsupported dims (head size must divide 256)");
+            break;
+        }
+        const long D = m->d, F = m->df;
+        const long per_layer = 2 * D + 3 * (D * D + D) + (D * D + D) + 2 * D + (D * F + F) + (F * D + D);
+        const long n = (long)m->v * D + (long)m->blk * D + m->nl * per_layer + 2 * D;
+        w.resize((size_t)n);
+        if (fread(w.data(), sizeof(float), (size_t)n, f) != (size_t)n) {
+            st = fail(PCL_ERR_INVALID_ARG, "pcl_model_load: short read in the checkpoint");
+            break;
+        }
+    } while (0);
+    fclose(f);
+    if (st != PCL_OK) return st;
+
+    const long D = m->d, F = m->df, V = m->v, BLK = m->blk;
+    // device layout: weights (QKV joined), KV caches, per-token state
+    const long per_layer_dev = 2 * D + (3 * D * D + 3 * D) + (D * D + D) + 2 * D + (D * F + F) +
+                               (F * D + D) + 2 * BLK * D;
+    const long state = D + D + 3 * D + D + F + F + V;
+    const long total = V * D + BLK * D + m->nl * per_layer_dev + 2 * D + state;
+    std::vector<float> h((size_t)total);
+    const float *src = w.data();
+    float *dst = h.data();
+    long at = 0;
+    auto take = [&](long cnt) {  // copy cnt floats from the file stream, return the device offset
+        const long o = at;
+        memcpy(dst + at, src, sizeof(float) * cnt);
+        src += cnt;
+        at += cnt;
+        return o;
+    };
+    const long o_wte = take(V * D), o_wpe = take(BLK * D);
+    struct LOff { long g1, b1, wqkv, bqkv, wo, bo, g2, b2, w1, bf1, w2, bf2, kc, vc; };
+    std::vector<LOff> lo((size_t)m->nl);
+    for (int l = 0; l < m->nl; l++) {
+        LOff &y = lo[(size_t)l];
+        y.g1 = take(D), y.b1 = take(D);
+        // Wq, bq, Wk, bk, Wv, bv -> [Wq | Wk | Wv] (D x 3D) and [bq | bk | bv]
+        y.wqkv = at;
+        at += 3 * D * D;
+        y.bqkv = at;
+        at += 3 * D;
+        for (int part = 0; part < 3; part++) {
+            for (long k = 0; k < D; k++)
+                memcpy(dst + y.wqkv + k * 3 * D + part * D, src + k * D, sizeof(float) * D);
+            src += D * D;
+            memcpy(dst + y.bqkv + part * D, src, sizeof(float) * D);
+            src += D;
+        }
+        y.wo = take(D * D), y.bo = take(D);
+        y.g2 = take(D), y.b2 = take(D);
+        y.w1 = take(D * F), y.bf1 = take(F);
+        y.w2 = take(F * D), y.bf2 = take(D);
+        y.kc = at;
+        at += BLK * D;
+        y.vc = at;
+        at += BLK * D;
+    }
+    const long o_gf = take(D), o_bf = take(D);
+    const long o_state = at;
+    at += state;
+    if (at != total || src != w.data() + w.size())
+        return fail(PCL_ERR_INVALID_ARG, "pcl_model_load: internal layout mismatch");
+    memset(dst + o_state, 0, sizeof(float) * state);
+    for (int l = 0; l < m->nl; l++)
+        memset(dst + lo[(size_t)l].kc, 0, sizeof(float) * 2 * BLK * D);
+
+    M_HIP(hipMalloc((void **)&m->arena, sizeof(float) * (size_t)total));
+    M_HIP(hipMalloc((void **)&m->ints, sizeof(int) * (size_t)(BLK + 3)));
+    M_HIP(hipMemcpy(m->arena, h.data(), sizeof(float) * (size_t)total, hipMemcpyHostToDevice));
+    M_HIP(hipMemset(m->ints, 0, sizeof(int) * (size_t)(BLK + 3)));
+    M_HIP(hipHostMalloc((void **)&m->host_tp, sizeof(int) * 2 * (size_t)BLK, hipHostMallocDefault));
+    float *a = m->arena;
+    m->wte = a + o_wte, m->wpe = a + o_wpe, m->gf = a + o_gf, m->bf = a + o_bf;
+    m->lay.resize((size_t)m->nl);
+    for (int l = 0; l < m->nl; l++) {
+        const LOff &y = lo[(size_t)l];
+        m->lay[(size_t)l] = Layer{a + y.g1, a + y.b1, a + y.wqkv, a + y.bqkv, a + y.wo,
+                                  a + y.bo, a + y.g2, a + y.b2, a + y.w1, a + y.bf1,
+                                  a + y.w2, a + y.bf2, a + y.kc, a + y.vc};
+    }
+    float *sp = a + o_state;
+    m->x = sp, sp += D;
+    m->ln = sp, sp += D;
+    m->qkv = sp, sp += 3 * D;
+    m->att = sp, sp += D;
+    m->hh = sp, sp += F;
+    m->hg = sp, sp += F;
+    m->logits = sp;
+    m->stream = pcl_stream_create();
+    if (!m->stream) return pcl_last_status();
+    return PCL_OK;
+}
+
+void release(pcl_model *m) {
+    if (m->graph) pcl_graph_destroy(m->graph);
+    if (m->stream) pcl_stream_destroy(m->stream);
+    if (m->arena) (void)hipFree(m->arena);
+    if (m->ints) (void)hipFree(m->ints);
+    if (m->host_tp) (void)hipHostFree(m->host_tp);
+    delete m;
+}
+
+// run one step on the model's stream, as a replay of the captured step when
+// use_graph (capturing it the first time)
+int run_step(pcl_model *m, int use_graph) {
+    if (!use_graph) return step(m);
+    void *prev = pcl_get_stream();
+    int st = PCL_OK;
+    pcl_set_stream(m->stream);
+    if (!m->graph) {
+        st = pcl_graph_begin();
+        if (st == PCL_OK) {
+            const int s1 = step(m);
+            void *g = nullptr;
+            const int s2 = pcl_graph_end(&g);
+            st = s1 != PCL_OK ? s1 : s2;
+            if (st == PCL_OK) m->graph = g;
+            else if (g) pcl_graph_destroy(g);
+        }
+    }
+    if (st == PCL_OK) st = pcl_graph_launch(m->graph);
+    pcl_set_stream(prev);
+    return st;
+}
+
+}  // namespace
+
+extern "C" {
+
+pcl_model *pcl_model_load(const char *path) {
+    if (!path) {
+        fail(PCL_ERR_INVALID_ARG, "pcl_model_load: path is NULL");
+        return nullptr;
+    }
+    if (pcl::shim_init() != PCL_OK) return nullptr;
+    pcl_model *m = new pcl_model();
+    if (load(m, path) != PCL_OK) {
+        const int st = pcl_last_status();
+        char msg[512];
+        snprintf(msg, sizeof msg, "%s", pcl_last_error());
+        release(m);
+        fail(st, msg);
+        return nullptr;
+    }
+    return m;
+}
+
+int pcl_model_header(const pcl_model *m, int hdr[8]) {
+    if (!m || !hdr) return fail(PCL_ERR_INVALID_ARG, "pcl_model_header: NULL argument");
+    memcpy(hdr, m->hdr, sizeof m->hdr);
+    return PCL_OK;
+}
+
+int pcl_model_forward(pcl_model *m, int tok, int pos, float *logits) {
+    if (!m) return fail(PCL_ERR_INVALID_ARG, "pcl_model_forward: model is NULL");
+    if (tok < 0 || tok >= m->v || pos < 0 || pos >= m->blk)
+        return fail(PCL_ERR_INVALID_ARG, "pcl_model_forward: token or position out of range");
+    M_OK(set_tokpos(m, tok, pos));
+    M_OK(step(m));
+    if (logits)
+        M_HIP(hipMemcpyAsync(logits, m->logits, sizeof(float) * (size_t)m->v, hipMemcpyDeviceToHost,
+                             (hipStream_t)m->stream));
+    M_HIP(hipStreamSynchronize((hipStream_t)m->stream));
+    return PCL_OK;
+}
+
+int pcl_model_generate(pcl_model *m, const int *prompt, int n_prompt, int n_new, int *out,
+                       int use_graph) {
+    if (!m || !prompt || (n_new > 0 && !out))
+        return fail(PCL_ERR_INVALID_ARG, "pcl_model_generate: NULL argument");
+    if (n_prompt < 1 || n_new < 0 || (long)n_prompt + n_new - 1 > m->blk)
+        return fail(PCL_ERR_INVALID_ARG,
+                    "pcl_model_generate: need 1 <= n_prompt and n_prompt + n_new - 1 <= block");
+    for (int i = 0; i < n_prompt; i++)
+        if (prompt[i] < 0 || prompt[i] >= m->v)
+            return fail(PCL_ERR_INVALID_ARG, "pcl_model_generate: prompt token out of range");
+    for (int i = 0; i < n_prompt; i++) {
+        M_OK(set_tokpos(m, prompt[i], i));
+        M_OK(step(m));
+    }
+    // the last prompt step left the first new token and position n_prompt in
+    // device memory; each further step feeds the previous pick
+    for (int t = 1; t < n_new; t++) M_OK(run_step(m, use_graph));
+    if (n_new > 0)
+        M_HIP(hipMemcpyAsync(out, m->ints + 2 + n_prompt, sizeof(int) * (size_t)n_new,
+                             hipMemcpyDeviceToHost, (hipStream_t)m->stream));
+    M_HIP(hipStreamSynchronize((hipStream_t)m->stream));
+    return PCL_OK;
+}
+
+void pcl_model_free(pcl_model *m) {
+    if (m) release(m);
+}
+
+}  // extern "C"

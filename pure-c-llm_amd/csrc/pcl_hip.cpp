@@ -219,6 +219,11 @@ int sync_current() {
 
 }  // namespace
 
+namespace pcl {
+int shim_error(int status, const char *msg) { return set_error(status, "%s", msg); }
+int shim_init() { return do_init(); }
+}  // namespace pcl
+
 // =========================================================================
 extern "C" {
 

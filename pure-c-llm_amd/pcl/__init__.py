@@ -116,6 +116,12 @@ _PROTOS = {
     "pcl_quantize_a_rows": (_i, [_vp, _i, _i, _vp, _i, _vp, _vp]),
     "pcl_quantize_b_cols": (_i, [_vp, _i, _i, _vp, _vp, _vp, _vp]),
     "pcl_quantize_b_vnni": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp, _vp]),
+    # a checkpoint on the GPU
+    "pcl_model_load": (_vp, [_cp]),
+    "pcl_model_header": (_i, [_vp, _vp]),
+    "pcl_model_forward": (_i, [_vp, _i, _i, _vp]),
+    "pcl_model_generate": (_i, [_vp, _vp, _i, _i, _vp, _i]),
+    "pcl_model_free": (None, [_vp]),
 }
 
 for _name, (_res, _args) in _PROTOS.items():

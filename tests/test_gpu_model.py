@@ -1,0 +1,114 @@
+"""A CKP1 checkpoint decoded on the GPU (pcl_model_*) against the oracle's
+restatement of generate.c (pinned by generate.c built from source in
+tests/test_oracle.py): logits token by token (fp32, <= 1e-4 normwise), and
+greedy generation -- eager and replayed as one graph per token -- where every
+pick must be an argmax of the oracle's logits for the same prefix (up to the
+fp32 tolerance when two logits are that close).
+"""
+import numpy as np
+import pytest
+
+import binding as ob
+import pcl
+from gpu_util import FP32_TOL, announce, rel, require_device
+
+pytestmark = pytest.mark.gpu
+
+SMALL = (32, 64, 4, 256, 2, 96)            # block, d, heads (dh 16), d_ff, layers, vocab
+MID = (48, 128, 4, 512, 3, 160)            # dh 32
+GROWN = (256, 512, 16, 2048, 16, 2048)     # the grown model (dh 32)
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _device():
+    require_device()
+
+
+def _load(path):
+    m = pcl.lib.pcl_model_load(path.encode())
+    if not m:
+        raise pcl.PclError(pcl.lib.pcl_last_status(), pcl.last_error())
+    return m
+
+
+@pytest.mark.parametrize("dims", [SMALL, MID])
+def test_model_forward_logits(tmp_path, dims):
+    blk, d, h, df, nl, v = dims
+    announce("model forward", dims)
+    path = str(tmp_path / "m.ckp1")
+    ob.write_ckp1(path, blk, d, h, df, nl, v, seed=21)
+    m = _load(path)
+    hdr = np.empty(8, np.int32)
+    pcl.check(pcl.lib.pcl_model_header(m, pcl.ptr(hdr)))
+    assert hdr[:7].tolist() == [0x434B5031, blk, d, h, df, nl, v]
+    om = ob.OracleModel(path)
+    toks = [int(t) % v for t in ob.u8((blk,), 23)]
+    got = np.empty(v, np.float32)
+    try:
+        for pos in range(blk):
+            pcl.check(pcl.lib.pcl_model_forward(m, toks[pos], pos, pcl.ptr(got)))
+            assert rel(got, om.forward(toks[pos], pos)) <= FP32_TOL, pos
+    finally:
+        om.close()
+        pcl.lib.pcl_model_free(m)
+
+
+def _check_greedy(path, prompt, out, v):
+    """Each generated token is an argmax of the oracle's logits for its prefix."""
+    om = ob.OracleModel(path)
+    seq = list(prompt) + list(out)
+    worst = 0.0
+    try:
+        for pos in range(len(seq) - 1):
+            lg = om.forward(seq[pos], pos)
+            if pos >= len(prompt) - 1:
+                pick = seq[pos + 1]
+                margin = float(lg.max() - lg[pick])
+                worst = max(worst, margin / max(1e-30, float(np.abs(lg).max())))
+    finally:
+        om.close()
+    assert worst <= FP32_TOL
+
+
+@pytest.mark.parametrize("dims,n_prompt,n_new", [(SMALL, 5, 27), (MID, 1, 48), (GROWN, 8, 56)])
+@pytest.mark.parametrize("graph", [0, 1])
+def test_model_generate_greedy(tmp_path, dims, n_prompt, n_new, graph):
+    blk, d, h, df, nl, v = dims
+    announce("model generate", dims, n_prompt, n_new, "graph" if graph else "eager")
+    path = str(tmp_path / "m.ckp1")
+    ob.write_ckp1(path, blk, d, h, df, nl, v, seed=31, wstd=0.05)
+    m = _load(path)
+    prompt = np.array([int(t) % v for t in ob.u8((n_prompt,), 33)], np.int32)
+    out = np.full(n_new, -1, np.int32)
+    try:
+        pcl.check(pcl.lib.pcl_model_generate(m, pcl.ptr(prompt), n_prompt, n_new, pcl.ptr(out), graph))
+        assert ((out >= 0) & (out < v)).all()
+        # a second call on the same model (graph reused) gives the same tokens
+        out2 = np.full(n_new, -1, np.int32)
+        pcl.check(pcl.lib.pcl_model_generate(m, pcl.ptr(prompt), n_prompt, n_new, pcl.ptr(out2), graph))
+        np.testing.assert_array_equal(out, out2)
+    finally:
+        pcl.lib.pcl_model_free(m)
+    _check_greedy(path, prompt.tolist(), out.tolist(), v)
+
+
+def test_model_errors(tmp_path):
+    bad = tmp_path / "bad.bin"
+    bad.write_bytes(bytes(64))
+    assert not pcl.lib.pcl_model_load(str(bad).encode())
+    assert pcl.lib.pcl_last_status() == pcl.PCL_ERR_INVALID_ARG
+    path = str(tmp_path / "m.ckp1")
+    ob.write_ckp1(path, 8, 64, 4, 128, 1, 32, seed=41)
+    short = tmp_path / "short.ckp1"
+    short.write_bytes(open(path, "rb").read()[:-16])
+    assert not pcl.lib.pcl_model_load(str(short).encode())
+    m = _load(path)
+    try:
+        assert pcl.lib.pcl_model_forward(m, 32, 0, None) == pcl.PCL_ERR_INVALID_ARG
+        assert pcl.lib.pcl_model_forward(m, 0, 8, None) == pcl.PCL_ERR_INVALID_ARG
+        prompt = np.zeros(4, np.int32)
+        out = np.zeros(8, np.int32)
+        assert pcl.lib.pcl_model_generate(m, pcl.ptr(prompt), 4, 6, pcl.ptr(out), 0) == pcl.PCL_ERR_INVALID_ARG
+    finally:
+        pcl.lib.pcl_model_free(m)
+    pcl.lib.pcl_clear_error()

@@ -480,3 +480,60 @@ def test_gelu_oracle_math():
     h = 1e-4
     num = (g64(x.astype(np.float64) + h) - g64(x.astype(np.float64) - h)) / (2 * h)
     np.testing.assert_allclose(ob.gelu_backward(np.ones_like(x), x), num, rtol=0, atol=2e-5)
+
+
+# -------------------------------------------------------- CKP1 decode ----
+@pytest.mark.parametrize("dims", [(32, 64, 4, 256, 2, 96), (24, 128, 4, 512, 3, 160)])
+def test_decode_oracle_vs_ref_generate(tmp_path, dims):
+    # generate.c (+ tokenizer.c) built from source reads the same checkpoint;
+    # logits of a token sequence fed at positions 0.. must agree
+    gen = _ref_or_skip("libref_generate.so")
+    blk, d, h, df, nl, v = dims
+    path = str(tmp_path / "m.ckp1")
+    ob.write_ckp1(path, blk, d, h, df, nl, v, seed=3)
+    assert gen.pcl_ref_gen_load(path.encode()) == v
+    om = ob.OracleModel(path)
+    assert om.hdr[:7] == [0x434B5031, blk, d, h, df, nl, v]
+    toks = [int(t) % v for t in ob.u8((blk,), 5)]
+    ref = np.empty(v, np.float32)
+    for pos in range(blk):
+        got = om.forward(toks[pos], pos)
+        gen.pcl_ref_gen_forward(toks[pos], pos, p(ref))
+        assert ob.normwise_rel_err(got, ref) < REF_TOL, pos
+    om.close()
+
+
+def test_decode_oracle_first_token_closed_form(tmp_path):
+    # at position 0 the attention output is v itself: with identity-free random
+    # weights the logits must equal a direct numpy evaluation of the block
+    blk, d, h, df, nl, v = 4, 64, 4, 128, 1, 32
+    path = str(tmp_path / "m.ckp1")
+    ob.write_ckp1(path, blk, d, h, df, nl, v, seed=9)
+    raw = np.fromfile(path, dtype="<f4")[8:].astype(np.float64)
+    at = 0
+
+    def take(n, shape=None):
+        nonlocal at
+        a = raw[at: at + n]
+        at += n
+        return a.reshape(shape) if shape else a
+    wte, wpe = take(v * d, (v, d)), take(blk * d, (blk, d))
+    g1, b1 = take(d), take(d)
+    Wq, bq, Wk, bk, Wv, bv = take(d * d, (d, d)), take(d), take(d * d, (d, d)), take(d), take(d * d, (d, d)), take(d)
+    Wo, bo, g2, b2 = take(d * d, (d, d)), take(d), take(d), take(d)
+    W1, bf1, W2, bf2 = take(d * df, (d, df)), take(df), take(df * d, (df, d)), take(d)
+    gf, bfin = take(d), take(d)
+
+    def ln(x, g, b):
+        mu = x.mean()
+        return (x - mu) / np.sqrt(((x - mu) ** 2).mean() + 1e-5) * g + b
+    tok = 7
+    x = wte[tok] + wpe[0]
+    att = ln(x, g1, b1) @ Wv + bv  # softmax over one key is 1
+    x = x + att @ Wo + bo
+    u = ln(x, g2, b2) @ W1 + bf1
+    x = x + (0.5 * u * (1 + np.tanh(0.7978845608028654 * (u + 0.044715 * u ** 3)))) @ W2 + bf2
+    want = wte @ ln(x, gf, bfin)
+    om = ob.OracleModel(path)
+    assert ob.normwise_rel_err(om.forward(tok, 0), want) < 1e-5
+    om.close()
