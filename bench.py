@@ -146,7 +146,8 @@ def decode_e2e(pcl, dims=(256, 512, 16, 2048, 16, 2048), n_new=255, ref_tokens=2
     """Greedy decoding of a synthetic CKP1 checkpoint of the grown model
     (block 256, d 512, 16 heads, d_ff 2048, 16 layers, vocab 2048): one prompt
     token then n_new tokens fed back on the GPU, eagerly and as one graph
-    replay per token; beside it the reference generate.c forward (built from
+    replay per token, with fp32 weights and with INT8 weights
+    (pcl_model_load_ex); beside it the reference generate.c forward (built from
     source in oracle/_ref, OpenMP on all host cores) on the same checkpoint."""
     import tempfile
 
@@ -161,22 +162,25 @@ def decode_e2e(pcl, dims=(256, 512, 16, 2048, 16, 2048), n_new=255, ref_tokens=2
     ob.write_ckp1(path, blk, d, h, df, nl, v, seed=77, wstd=0.05)
     out = {"model": f"block {blk}, d_model {d}, heads {h}, d_ff {df}, layers {nl}, vocab {v}",
            "weights_MB": round(4.0 * (v * d + blk * d + nl * (4 * d * d + 2 * d * df)) / 1e6, 1)}
-    m = pcl.lib.pcl_model_load(path.encode())
-    if not m:
-        raise RuntimeError(f"pcl_model_load: {pcl.last_error()}")
-    try:
-        prompt = np.array([1], np.int32)
-        toks = np.empty(n_new, np.int32)
-        for graph in (0, 1):
-            _check(pcl, pcl.lib.pcl_model_generate(m, pcl.ptr(prompt), 1, n_new, pcl.ptr(toks), graph), "generate")
-            t0 = time.perf_counter()
-            _check(pcl, pcl.lib.pcl_model_generate(m, pcl.ptr(prompt), 1, n_new, pcl.ptr(toks), graph), "generate")
-            dt = time.perf_counter() - t0
-            tag = "graph" if graph else "eager"
-            out[f"{tag}_tokens_per_s"] = round(n_new / dt, 1)
-            out[f"{tag}_ms_per_token"] = round(1e3 * dt / n_new, 4)
-    finally:
-        pcl.lib.pcl_model_free(m)
+    for weights, wtag in ((pcl.W_FP32, ""), (pcl.W_INT8, "int8_")):
+        m = pcl.lib.pcl_model_load_ex(path.encode(), weights)
+        if not m:
+            raise RuntimeError(f"pcl_model_load_ex: {pcl.last_error()}")
+        try:
+            prompt = np.array([1], np.int32)
+            toks = np.empty(n_new, np.int32)
+            for graph in (0, 1):
+                _check(pcl, pcl.lib.pcl_model_generate(m, pcl.ptr(prompt), 1, n_new, pcl.ptr(toks), graph),
+                       "generate")
+                t0 = time.perf_counter()
+                _check(pcl, pcl.lib.pcl_model_generate(m, pcl.ptr(prompt), 1, n_new, pcl.ptr(toks), graph),
+                       "generate")
+                dt = time.perf_counter() - t0
+                tag = wtag + ("graph" if graph else "eager")
+                out[f"{tag}_tokens_per_s"] = round(n_new / dt, 1)
+                out[f"{tag}_ms_per_token"] = round(1e3 * dt / n_new, 4)
+        finally:
+            pcl.lib.pcl_model_free(m)
     gen = ob.ref("libref_generate.so")
     if gen is not None:
         gen.pcl_ref_gen_load(path.encode())

@@ -322,6 +322,15 @@ int pcl_quantize_b_vnni(const float *B, int K, int N, int Kpad, int8_t *Bp, floa
  * pcl_last_error). */
 typedef struct pcl_model pcl_model;
 pcl_model *pcl_model_load(const char *path);
+/* weights: PCL_W_FP32 (as pcl_model_load) or PCL_W_INT8: every projection and
+ * the tied head quantised once at load, per output column (the rule of
+ * gemm_bench.c:238-259), and each product's input quantised per token as it is
+ * made (per-row u8, gemm_bench.c:225-236's rule per row): INT8 GEMVs with
+ * int32 sums and per-row x per-column dequant; embeddings, LayerNorm, biases,
+ * attention and the residual stream stay fp32. */
+#define PCL_W_FP32 0
+#define PCL_W_INT8 1
+pcl_model *pcl_model_load_ex(const char *path, int weights);
 /* The checkpoint's int[8] header. */
 int pcl_model_header(const pcl_model *m, int hdr[8]);
 /* generate.c forward(tok, pos): one KV-cached step (the cache rows 0..pos-1 must

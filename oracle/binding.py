@@ -59,6 +59,7 @@ _ORACLE_PROTOS = {
     "orc_model_load": (_vp, [C.c_char_p]),
     "orc_model_header": (None, [_vp, _vp]),
     "orc_model_forward": (None, [_vp, _i, _i, _vp]),
+    "orc_model_forward_int8": (None, [_vp, _i, _i, _vp]),
     "orc_model_free": (None, [_vp]),
     "orc_rms_rel": (_d, [_vp, _vp, _l]),
     "orc_max_abs_diff": (_d, [_vp, _vp, _l]),
@@ -298,9 +299,11 @@ def write_ckp1(path, blk, d, h, df, nl, v, seed, step=0, wstd=0.02):
 
 
 class OracleModel:
-    """orc_model_* (generate.c restated) over a CKP1 file."""
+    """orc_model_* (generate.c restated) over a CKP1 file; int8 selects the
+    INT8-product step (orc_model_forward_int8)."""
 
-    def __init__(self, path):
+    def __init__(self, path, int8=False):
+        self.int8 = int8
         self.m = oracle().orc_model_load(path.encode())
         if not self.m:
             raise ValueError(f"{path}: not a CKP1 checkpoint")
@@ -310,7 +313,8 @@ class OracleModel:
 
     def forward(self, tok, pos):
         out = np.empty(self.hdr[6], np.float32)
-        oracle().orc_model_forward(self.m, tok, pos, p(out))
+        fn = oracle().orc_model_forward_int8 if self.int8 else oracle().orc_model_forward
+        fn(self.m, tok, pos, p(out))
         return out
 
     def close(self):

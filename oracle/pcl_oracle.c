@@ -23,6 +23,10 @@
  *                                 exact erf GELU within the tanh approximation's
  *                                 error; the derivative against central
  *                                 differences of the forward
+ *   orc_model_forward_int8 ..... no counterpart in the reference: composed of the
+ *                                 pinned quantisers, exact int GEMM and dequant
+ *                                 below; against generate.c built from source
+ *                                 within the quantisation error (< 5% normwise)
  *   orc_model_load / _forward .. generate.c (with tokenizer.c) built from source
  *                                 (oracle/_ref) on written checkpoints: logits
  *                                 token by token; T = 1 and equal-key closed forms
@@ -332,6 +336,12 @@ struct orc_model {
     float **lw; /* per layer: g1 b1 Wq bq Wk bk Wv bv Wo bo g2 b2 W1 bff1 W2 bff2 */
     float *kc, *vc;
     float *x, *ln, *q, *att, *proj, *h, *sc;
+    /* INT8 mode: matrices 2 4 6 8 12 14 of each layer and the tied head
+     * quantised per output column (made on the first INT8 call) */
+    int8_t *q8, **lq, *hq;
+    float *q8s, **ls, *hs;
+    uint8_t *xq;
+    int32_t *acc;
 };
 
 orc_model *orc_model_load(const char *path) {
@@ -395,9 +405,57 @@ static void orc_ln_row(const float *x, const float *g, const float *b, float *y,
     for (int i = 0; i < n; i++) y[i] = (x[i] - mu) * rs * g[i] + b[i];
 }
 
-void orc_model_forward(orc_model *m, int tok, int pos, float *logits) {
+static const int ORC_QMAT[6] = {2, 4, 6, 8, 12, 14};
+
+static void orc_model_quantize(orc_model *m) {
+    const long D = m->D, F = m->DF, V = m->V;
+    const long K[6] = {D, D, D, D, D, F}, N[6] = {D, D, D, D, F, D};
+    long nb = V * D, ns = V;
+    for (int i = 0; i < 6; i++) nb += m->L * K[i] * N[i], ns += m->L * N[i];
+    m->q8 = (int8_t *)malloc((size_t)nb);
+    m->q8s = (float *)malloc(sizeof(float) * (size_t)ns);
+    m->lq = (int8_t **)malloc(sizeof(int8_t *) * 6 * (size_t)m->L);
+    m->ls = (float **)malloc(sizeof(float *) * 6 * (size_t)m->L);
+    int8_t *b = m->q8;
+    float *sc = m->q8s;
+    for (int l = 0; l < m->L; l++)
+        for (int i = 0; i < 6; i++) {
+            m->lq[l * 6 + i] = b, m->ls[l * 6 + i] = sc;
+            orc_quantize_B_cols(m->lw[l * 16 + ORC_QMAT[i]], b, sc, (int)K[i], (int)N[i]);
+            b += K[i] * N[i], sc += N[i];
+        }
+    /* the head's K x N operand is wte transposed: one column per vocabulary row */
+    float *wt = (float *)malloc(sizeof(float) * (size_t)(V * D));
+    for (long v = 0; v < V; v++)
+        for (long d = 0; d < D; d++) wt[d * V + v] = m->wte[v * D + d];
+    m->hq = b, m->hs = sc;
+    orc_quantize_B_cols(wt, m->hq, m->hs, (int)D, (int)V);
+    free(wt);
+    const long kmax = D > F ? D : F, nmax = V > F ? (V > D ? V : D) : (F > D ? F : D);
+    m->xq = (uint8_t *)malloc((size_t)kmax);
+    m->acc = (int32_t *)malloc(sizeof(int32_t) * (size_t)nmax);
+}
+
+/* out = dequant(quant_row(x) . Wq) (+ b): the per-token activation rule, int32
+ * sums, sa * sb[n] applied to the sum, then the bias added to the result. */
+static void orc_qmatvec(orc_model *m, float *out, const float *x, const int8_t *Wq,
+                        const float *ws, const float *b, int K, int N) {
+    float sa;
+    orc_quantize_A_rows(x, m->xq, &sa, 1, K, K);
+    orc_gemm_u8s8_i32(m->xq, K, Wq, N, m->acc, N, 1, N, K);
+    orc_dequant(m->acc, N, &sa, ws, out, N, 1, N);
+    if (b)
+        for (int n = 0; n < N; n++) out[n] = out[n] + b[n];
+}
+
+static void orc_model_step(orc_model *m, int tok, int pos, float *logits, int int8) {
     /* generate.c:170-183 forward and :118-167 block */
     const int D = m->D, DH = m->DH, F = m->DF;
+    if (int8 && !m->q8) orc_model_quantize(m);
+#define ORC_MV(out, x, wi, K, N)                                                      \
+    (int8 ? orc_qmatvec(m, out, x, m->lq[l * 6 + (wi)], m->ls[l * 6 + (wi)],           \
+                        w[ORC_QMAT[wi] + 1], K, N)                                     \
+          : orc_matvec(out, x, w[ORC_QMAT[wi]], w[ORC_QMAT[wi] + 1], 1, K, N))
     const float *te = m->wte + (size_t)tok * D, *pe = m->wpe + (size_t)pos * D;
     for (int i = 0; i < D; i++) m->x[i] = te[i] + pe[i];
     for (int l = 0; l < m->L; l++) {
@@ -405,9 +463,9 @@ void orc_model_forward(orc_model *m, int tok, int pos, float *logits) {
         float *kc = m->kc + (size_t)l * m->BLK * D, *vc = m->vc + (size_t)l * m->BLK * D;
         float *krow = kc + (size_t)pos * D, *vrow = vc + (size_t)pos * D;
         orc_ln_row(m->x, w[0], w[1], m->ln, D);
-        orc_matvec(m->q, m->ln, w[2], w[3], 1, D, D);
-        orc_matvec(krow, m->ln, w[4], w[5], 1, D, D);
-        orc_matvec(vrow, m->ln, w[6], w[7], 1, D, D);
+        ORC_MV(m->q, m->ln, 0, D, D);
+        ORC_MV(krow, m->ln, 1, D, D);
+        ORC_MV(vrow, m->ln, 2, D, D);
         const float scale = 1.0f / sqrtf((float)DH);
         for (int h = 0; h < m->H; h++) {
             const int off = h * DH;
@@ -435,15 +493,20 @@ void orc_model_forward(orc_model *m, int tok, int pos, float *logits) {
                 for (int d = 0; d < DH; d++) oh[d] += pj * vj[d];
             }
         }
-        orc_matvec(m->proj, m->att, w[8], w[9], 1, D, D);
+        ORC_MV(m->proj, m->att, 3, D, D);
         for (int i = 0; i < D; i++) m->x[i] += m->proj[i];
         orc_ln_row(m->x, w[10], w[11], m->ln, D);
-        orc_matvec(m->h, m->ln, w[12], w[13], 1, D, F);
+        ORC_MV(m->h, m->ln, 4, D, F);
         orc_gelu_forward(m->h, m->h, F);
-        orc_matvec(m->proj, m->h, w[14], w[15], 1, F, D);
+        ORC_MV(m->proj, m->h, 5, F, D);
         for (int i = 0; i < D; i++) m->x[i] += m->proj[i];
     }
+#undef ORC_MV
     orc_ln_row(m->x, m->gf, m->bf, m->ln, D);
+    if (int8) {
+        orc_qmatvec(m, logits, m->ln, m->hq, m->hs, NULL, D, m->V);
+        return;
+    }
     for (int v = 0; v < m->V; v++) {
         const float *wv = m->wte + (size_t)v * D;
         float dot = 0;
@@ -452,8 +515,17 @@ void orc_model_forward(orc_model *m, int tok, int pos, float *logits) {
     }
 }
 
+void orc_model_forward(orc_model *m, int tok, int pos, float *logits) {
+    orc_model_step(m, tok, pos, logits, 0);
+}
+
+void orc_model_forward_int8(orc_model *m, int tok, int pos, float *logits) {
+    orc_model_step(m, tok, pos, logits, 1);
+}
+
 void orc_model_free(orc_model *m) {
     if (!m) return;
+    free(m->q8), free(m->q8s), free(m->lq), free(m->ls), free(m->xq), free(m->acc);
     free(m->buf), free(m->lw), free(m->kc), free(m->vc);
     free(m->x), free(m->ln), free(m->q), free(m->att), free(m->proj), free(m->h), free(m->sc);
     free(m);

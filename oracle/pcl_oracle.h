@@ -114,6 +114,12 @@ typedef struct orc_model orc_model;
 orc_model *orc_model_load(const char *path);
 void orc_model_header(const orc_model *m, int hdr[8]);
 void orc_model_forward(orc_model *m, int tok, int pos, float *logits);
+/* The same step with INT8 products (one model object is used in one mode: the
+ * KV cache is shared): every matrix and the tied head quantised per output
+ * column (gemm_bench.c:238-259's rule), each product's input quantised per
+ * token (gemm_bench.c:225-236's rule over one row), exact int32 sums,
+ * dequantised by sa * sb[n], then the bias added. */
+void orc_model_forward_int8(orc_model *m, int tok, int pos, float *logits);
 void orc_model_free(orc_model *m);
 
 /* Causal multi-head attention, train.c:339-370 attention_forward generalised

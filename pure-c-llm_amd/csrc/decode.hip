@@ -53,24 +53,33 @@ __global__ __launch_bounds__(256) void dec_layernorm_kernel(const float *__restr
 }
 
 // One head per workgroup (generate.c:130-152): append this position's k, v to
-// the cache, scores s_j = (q . k_j) * scale for j <= pos (the new row read
-// from qkv, older rows from the cache), softmax, att = sum_j p_j v_j. qkv
-// holds [q | k | v] (3*D floats); the cache rows are D floats. dh divides 256.
+// the cache, scores s_j = (q . k_j) * scale for j <= pos (the new row from
+// LDS, older rows from the cache), softmax, att = sum_j p_j v_j. qkv holds
+// [q | k | v] (3*D floats) and bqkv, when given, is added to it here (the
+// INT8 step's projections carry no bias); the cache rows are D floats. dh
+// divides 256.
 __global__ __launch_bounds__(256) void dec_attn_kernel(const float *__restrict__ qkv,
+                                                       const float *__restrict__ bqkv,
                                                        float *__restrict__ kc,
                                                        float *__restrict__ vc,
                                                        float *__restrict__ att, int D, int dh,
                                                        const int *__restrict__ tokpos,
                                                        float scale) {
     extern __shared__ float dec_lds[];  // [blk] scores, then [256] partial sums
-    __shared__ float red[4];
+    __shared__ float red[4], qs[256], ks[256], vs[256];
     const int h = blockIdx.x, tid = threadIdx.x, off = h * dh;
     const int pos = tokpos[1];
-    const float *q = qkv + off, *knew = qkv + D + off, *vnew = qkv + 2 * D + off;
-    for (int d = tid; d < dh; d += 256) {
-        kc[(long)pos * D + off + d] = knew[d];
-        vc[(long)pos * D + off + d] = vnew[d];
+    if (tid < dh) {
+        const float bq = bqkv ? bqkv[off + tid] : 0.f, bk = bqkv ? bqkv[D + off + tid] : 0.f,
+                    bv = bqkv ? bqkv[2 * D + off + tid] : 0.f;
+        qs[tid] = qkv[off + tid] + bq;
+        ks[tid] = qkv[D + off + tid] + bk;
+        vs[tid] = qkv[2 * D + off + tid] + bv;
+        kc[(long)pos * D + off + tid] = ks[tid];
+        vc[(long)pos * D + off + tid] = vs[tid];
     }
+    __syncthreads();
+    const float *q = qs, *knew = ks, *vnew = vs;
     float *sc = dec_lds;
     float mloc = -INFINITY;
     for (int j = tid; j <= pos; j += 256) {
@@ -157,13 +166,91 @@ hipError_t launch_decode_layernorm(const float *x, const float *g, const float *
     hipLaunchKernelGGL(dec_layernorm_kernel, dim3(1), dim3(256), 0, s, x, g, b, y, D);
     return hipGetLastError();
 }
-hipError_t launch_decode_attn(const float *qkv, float *kc, float *vc, float *att, int D, int H,
-                              int blk, const int *tokpos, hipStream_t s) {
+hipError_t launch_decode_attn(const float *qkv, const float *bqkv, float *kc, float *vc, float *att,
+                              int D, int H, int blk, const int *tokpos, hipStream_t s) {
     const int dh = D / H;
     if (dh <= 0 || 256 % dh != 0) return hipErrorInvalidValue;
     const size_t lds = sizeof(float) * ((size_t)((blk + 3) & ~3) + 256);
-    hipLaunchKernelGGL(dec_attn_kernel, dim3(H), dim3(256), lds, s, qkv, kc, vc, att, D, dh, tokpos,
-                       1.0f / sqrtf((float)dh));
+    hipLaunchKernelGGL(dec_attn_kernel, dim3(H), dim3(256), lds, s, qkv, bqkv, kc, vc, att, D, dh,
+                       tokpos, 1.0f / sqrtf((float)dh));
+    return hipGetLastError();
+}
+
+// ---- INT8 step: quantised activations (the per-row rule of quant.hip) ----
+// Per-row quantisation of the n values in v (LDS) into q (Kpad bytes, 128 past
+// n) with its scale, by one workgroup.
+__device__ void dec_quant_row(const float *v, int n, uint8_t *__restrict__ q, int Kpad,
+                              float *__restrict__ sa, float *red) {
+    float mx = 0.f;
+    for (int i = threadIdx.x; i < n; i += 256) mx = fmaxf(mx, fabsf(v[i]));
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    const float amax = fmaxf(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])), AMAX_INIT);
+    const float scale = amax * RCP127, inv = 1.0f / scale;
+    if (threadIdx.x == 0) *sa = scale;
+    for (int k = threadIdx.x; k < Kpad; k += 256) q[k] = (uint8_t)((k < n ? quant_q(v[k], inv) : 0) + 128);
+}
+
+// x += t + b (the pending residual: t = the previous product without its bias
+// b; skipped when t is NULL), then y = LayerNorm(x) quantised per row
+// (generate.c:106-114 and :155/166's additions, then the INT8 operand).
+__global__ __launch_bounds__(256) void dec_add_ln_quant_kernel(
+    float *__restrict__ x, const float *__restrict__ t, const float *__restrict__ b,
+    const float *__restrict__ g, const float *__restrict__ beta, uint8_t *__restrict__ q,
+    float *__restrict__ sa, int D, int Kpad) {
+    extern __shared__ float dec_lds[];  // [D]
+    __shared__ float red[4];
+    float s = 0.f;
+    for (int i = threadIdx.x; i < D; i += 256) {
+        float v = x[i];
+        if (t) {
+            v = v + (t[i] + b[i]);
+            x[i] = v;
+        }
+        dec_lds[i] = v;
+        s += v;
+    }
+    const float mu = dec_block_sum(s, red) / D;
+    float qq = 0.f;
+    for (int i = threadIdx.x; i < D; i += 256) {
+        const float d = dec_lds[i] - mu;
+        qq += d * d;
+    }
+    const float var = dec_block_sum(qq, red) / D;
+    const float rs = 1.0f / sqrtf(var + 1e-5f);
+    for (int i = threadIdx.x; i < D; i += 256) dec_lds[i] = (dec_lds[i] - mu) * rs * g[i] + beta[i];
+    dec_quant_row(dec_lds, D, q, Kpad, sa, red);
+}
+
+// y = gelu(h + b) quantised per row (generate.c:159-164 after the W1 product).
+__global__ __launch_bounds__(256) void dec_bias_gelu_quant_kernel(const float *__restrict__ h,
+                                                                  const float *__restrict__ b,
+                                                                  uint8_t *__restrict__ q,
+                                                                  float *__restrict__ sa, int F,
+                                                                  int Kpad) {
+    extern __shared__ float dec_lds[];  // [F]
+    __shared__ float red[4];
+    for (int i = threadIdx.x; i < F; i += 256) {
+        const float v = h[i] + b[i];
+        dec_lds[i] = 0.5f * v * (1.0f + tanhf(0.7978845608028654f * (v + 0.044715f * v * v * v)));
+    }
+    dec_quant_row(dec_lds, F, q, Kpad, sa, red);
+}
+
+hipError_t launch_decode_add_ln_quant(float *x, const float *t, const float *b, const float *g,
+                                      const float *beta, uint8_t *q, float *sa, int D, int Kpad,
+                                      hipStream_t s) {
+    hipLaunchKernelGGL(dec_add_ln_quant_kernel, dim3(1), dim3(256), sizeof(float) * (size_t)D, s, x,
+                       t, b, g, beta, q, sa, D, Kpad);
+    return hipGetLastError();
+}
+hipError_t launch_decode_bias_gelu_quant(const float *h, const float *b, uint8_t *q, float *sa,
+                                         int F, int Kpad, hipStream_t s) {
+    hipLaunchKernelGGL(dec_bias_gelu_quant_kernel, dim3(1), dim3(256), sizeof(float) * (size_t)F, s,
+                       h, b, q, sa, F, Kpad);
     return hipGetLastError();
 }
 hipError_t launch_decode_argmax(const float *logits, int V, int *tokpos, int *out, int out_cap,

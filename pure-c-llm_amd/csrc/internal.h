@@ -87,9 +87,17 @@ hipError_t launch_decode_embed(const float *wte, const float *wpe, float *x, int
                                const int *tokpos, hipStream_t s);
 hipError_t launch_decode_layernorm(const float *x, const float *g, const float *b, float *y, int D,
                                    hipStream_t s);
-// dh = D / H must divide 256; the cache holds blk rows of D floats
-hipError_t launch_decode_attn(const float *qkv, float *kc, float *vc, float *att, int D, int H,
-                              int blk, const int *tokpos, hipStream_t s);
+// dh = D / H must divide 256; the cache holds blk rows of D floats; bqkv
+// (3*D, may be NULL) is added to qkv inside the kernel
+hipError_t launch_decode_attn(const float *qkv, const float *bqkv, float *kc, float *vc, float *att,
+                              int D, int H, int blk, const int *tokpos, hipStream_t s);
+// x += t + b (when t), q/sa = per-row quantised LayerNorm(x; g, beta), Kpad bytes
+hipError_t launch_decode_add_ln_quant(float *x, const float *t, const float *b, const float *g,
+                                      const float *beta, uint8_t *q, float *sa, int D, int Kpad,
+                                      hipStream_t s);
+// q/sa = per-row quantised gelu(h + b), Kpad bytes
+hipError_t launch_decode_bias_gelu_quant(const float *h, const float *b, uint8_t *q, float *sa,
+                                         int F, int Kpad, hipStream_t s);
 hipError_t launch_decode_argmax(const float *logits, int V, int *tokpos, int *out, int out_cap,
                                 hipStream_t s);
 
@@ -116,6 +124,14 @@ hipError_t launch_igemv(const GemvPlan &p, int out_mode, int M, int N, int K, co
                         hipStream_t stream);
 
 // ---- quantisers and packers (quant.hip) ----
+// The activation/weight rule (gemm_bench.c:225-259 as built): amax starts at
+// 1e-8f, scale = amax * fl(1/127), q = clamp(roundf(x * (1/scale)), +-127).
+constexpr float AMAX_INIT = 1e-8f;
+constexpr float RCP127 = 1.0f / 127.0f;  // rounded to fp32 at compile time
+__device__ __forceinline__ int quant_q(float x, float inv) {
+    int q = (int)roundf(x * inv);
+    return q > 127 ? 127 : (q < -127 ? -127 : q);
+}
 hipError_t launch_quantize_a_tensor(const float *A, int M, int K, uint8_t *Au, int Kpad,
                                     float *scale_dev, unsigned *amax_bits, hipStream_t stream);
 hipError_t launch_quantize_a_rows(const float *A, int M, int K, uint8_t *Au, int Kpad, float *sa,

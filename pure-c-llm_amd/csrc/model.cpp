@@ -30,6 +30,12 @@ constexpr int CKP1_MAGIC = 0x434B5031;
 struct Layer {
     float *g1, *b1, *wqkv, *bqkv, *wo, *bo, *g2, *b2, *w1, *bf1, *w2, *bf2, *kc, *vc;
 };
+// INT8 projections: packed s8 (rows of Kp bytes per output column) + scales
+struct QLayer {
+    int8_t *wqkv, *wo, *w1, *w2;
+    float *sqkv, *so, *s1, *s2;
+};
+int kpad256(int k) { return (k + 255) / 256 * 256; }
 
 int fail(int status, const char *msg) { return pcl::shim_error(status, msg); }
 
@@ -46,6 +52,15 @@ struct pcl_model {
     float *x, *ln, *qkv, *att, *hh, *hg, *logits;
     void *stream = nullptr;
     void *graph = nullptr;
+    // INT8 weights (PCL_W_INT8): projections and the tied head quantised once
+    int wmode = PCL_W_FP32;
+    int kpd = 0, kpf = 0;
+    int8_t *i8 = nullptr;
+    float *qscale = nullptr;  // weight scales, a D-float product, the activation scale
+    std::vector<QLayer> ql;
+    int8_t *whead = nullptr;
+    float *shead = nullptr, *sa = nullptr, *tmp = nullptr;
+    uint8_t *xq = nullptr;
 };
 
 namespace {
@@ -73,7 +88,7 @@ int step(pcl_model *m) {
     for (const Layer &y : m->lay) {
         M_HIP(pcl::launch_decode_layernorm(m->x, y.g1, y.b1, m->ln, D, s));
         M_OK(pcl_sgemv(PCL_OP_N, 1, 3 * D, D, m->ln, D, y.wqkv, 3 * D, y.bqkv, 0, m->qkv, 3 * D, s));
-        M_HIP(pcl::launch_decode_attn(m->qkv, y.kc, y.vc, m->att, D, m->h, m->blk, tokpos, s));
+        M_HIP(pcl::launch_decode_attn(m->qkv, nullptr, y.kc, y.vc, m->att, D, m->h, m->blk, tokpos, s));
         M_OK(pcl_sgemv(PCL_OP_N, 1, D, D, m->att, D, y.wo, D, y.bo, 1, m->x, D, s));
         M_HIP(pcl::launch_decode_layernorm(m->x, y.g2, y.b2, m->ln, D, s));
         M_OK(pcl_sgemv(PCL_OP_N, 1, F, D, m->ln, D, y.w1, F, y.bf1, 0, m->hh, F, s));
@@ -84,6 +99,91 @@ int step(pcl_model *m) {
     M_OK(pcl_sgemv(PCL_OP_T, 1, V, D, m->ln, D, m->wte, D, nullptr, 0, m->logits, V, s));
     M_HIP(pcl::launch_decode_argmax(m->logits, V, tokpos, out, m->blk + 1, s));
     return PCL_OK;
+}
+
+// The same step with INT8 products: each product's input row is quantised per
+// row (u8 + scale, 0x80 past its length up to Kp) by the kernel that makes it,
+// the GEMV dequantises (sa * sb), and the bias -- plus the residual add -- is
+// applied by the next kernel (the QKV bias inside the attention kernel).
+int step_int8(pcl_model *m) {
+    hipStream_t s = (hipStream_t)m->stream;
+    const int D = m->d, F = m->df, V = m->v, KD = m->kpd, KF = m->kpf;
+    int *tokpos = m->ints, *out = m->ints + 2;
+    M_HIP(pcl::launch_decode_embed(m->wte, m->wpe, m->x, D, tokpos, s));
+    const float *t = nullptr, *tb = nullptr;  // pending product and its bias, added into x
+    for (size_t l = 0; l < m->lay.size(); l++) {
+        const Layer &y = m->lay[l];
+        const QLayer &q = m->ql[l];
+        M_HIP(pcl::launch_decode_add_ln_quant(m->x, t, tb, y.g1, y.b1, m->xq, m->sa, D, KD, s));
+        M_OK(pcl_gemv_u8s8_dq(m->xq, KD, q.wqkv, nullptr, m->sa, q.sqkv, m->qkv, 3 * D, 1, 3 * D, KD, s));
+        M_HIP(pcl::launch_decode_attn(m->qkv, y.bqkv, y.kc, y.vc, m->att, D, m->h, m->blk, tokpos, s));
+        M_HIP(pcl::launch_quantize_a_rows(m->att, 1, D, m->xq, KD, m->sa, s));
+        M_OK(pcl_gemv_u8s8_dq(m->xq, KD, q.wo, nullptr, m->sa, q.so, m->tmp, D, 1, D, KD, s));
+        M_HIP(pcl::launch_decode_add_ln_quant(m->x, m->tmp, y.bo, y.g2, y.b2, m->xq, m->sa, D, KD, s));
+        M_OK(pcl_gemv_u8s8_dq(m->xq, KD, q.w1, nullptr, m->sa, q.s1, m->hh, F, 1, F, KD, s));
+        M_HIP(pcl::launch_decode_bias_gelu_quant(m->hh, y.bf1, m->xq, m->sa, F, KF, s));
+        M_OK(pcl_gemv_u8s8_dq(m->xq, KF, q.w2, nullptr, m->sa, q.s2, m->tmp, D, 1, D, KF, s));
+        t = m->tmp, tb = y.bf2;
+    }
+    M_HIP(pcl::launch_decode_add_ln_quant(m->x, t, tb, m->gf, m->bf, m->xq, m->sa, D, KD, s));
+    M_OK(pcl_gemv_u8s8_dq(m->xq, KD, m->whead, nullptr, m->sa, m->shead, m->logits, V, 1, V, KD, s));
+    M_HIP(pcl::launch_decode_argmax(m->logits, V, tokpos, out, m->blk + 1, s));
+    return PCL_OK;
+}
+
+int run_eager(pcl_model *m) { return m->wmode == PCL_W_INT8 ? step_int8(m) : step(m); }
+
+// Quantise every projection (per output column) and the tied head once.
+int quantize_weights(pcl_model *m) {
+    const long D = m->d, F = m->df, V = m->v;
+    const int KD = kpad256((int)D), KF = kpad256((int)F);
+    m->kpd = KD, m->kpf = KF;
+    const long per = 3 * D * KD + D * KD + F * KD + D * KF;
+    const long bytes = m->nl * per + V * KD;
+    const long scales = m->nl * (3 * D + D + F + D) + V + 1 + D;
+    M_HIP(hipMalloc((void **)&m->i8, (size_t)bytes));
+    M_HIP(hipMalloc((void **)&m->qscale, sizeof(float) * (size_t)scales));
+    M_HIP(hipMalloc((void **)&m->xq, (size_t)(KD > KF ? KD : KF)));
+    hipStream_t s = (hipStream_t)m->stream;
+    int8_t *b = m->i8;
+    float *sc = m->qscale;
+    m->ql.resize(m->lay.size());
+    for (size_t l = 0; l < m->lay.size(); l++) {
+        const Layer &y = m->lay[l];
+        QLayer &q = m->ql[l];
+        q.wqkv = b, b += 3 * D * KD;
+        q.wo = b, b += D * KD;
+        q.w1 = b, b += F * KD;
+        q.w2 = b, b += D * KF;
+        q.sqkv = sc, sc += 3 * D;
+        q.so = sc, sc += D;
+        q.s1 = sc, sc += F;
+        q.s2 = sc, sc += D;
+        M_HIP(pcl::launch_quantize_b_cols(y.wqkv, (int)D, (int)(3 * D), 0, q.wqkv, KD, KD, q.sqkv, nullptr, s));
+        M_HIP(pcl::launch_quantize_b_cols(y.wo, (int)D, (int)D, 0, q.wo, KD, KD, q.so, nullptr, s));
+        M_HIP(pcl::launch_quantize_b_cols(y.w1, (int)D, (int)F, 0, q.w1, KD, KD, q.s1, nullptr, s));
+        M_HIP(pcl::launch_quantize_b_cols(y.w2, (int)F, (int)D, 0, q.w2, KF, KF, q.s2, nullptr, s));
+    }
+    m->whead = b;
+    m->shead = sc, sc += V;
+    m->tmp = sc, sc += D;
+    m->sa = sc;
+    // the head quantises wte per vocabulary row: its transpose (D x V) is the
+    // K x N operand of the per-column rule
+    float *wt = nullptr;
+    M_HIP(hipMalloc((void **)&wt, sizeof(float) * (size_t)(V * D)));
+    std::vector<float> h((size_t)(V * D)), ht((size_t)(V * D));
+    M_HIP(hipMemcpy(h.data(), m->wte, sizeof(float) * (size_t)(V * D), hipMemcpyDeviceToHost));
+    for (long v = 0; v < V; v++)
+        for (long d = 0; d < D; d++) ht[(size_t)(d * V + v)] = h[(size_t)(v * D + d)];
+    int st = PCL_OK;
+    if (hipMemcpy(wt, ht.data(), sizeof(float) * (size_t)(V * D), hipMemcpyHostToDevice) != hipSuccess ||
+        pcl::launch_quantize_b_cols(wt, (int)D, (int)V, 0, m->whead, KD, KD, m->shead, nullptr, s) != hipSuccess ||
+        hipStreamSynchronize(s) != hipSuccess)
+        st = fail(PCL_ERR_HIP, "pcl_model_load: INT8 weight quantisation failed");
+    (void)hipFree(wt);
+    if (st == PCL_OK) m->wmode = PCL_W_INT8;
+    return st;
 }
 
 // Each position has its own pinned slot, so a copy still queued on the stream
@@ -213,6 +313,9 @@ void release(pcl_model *m) {
     if (m->graph) pcl_graph_destroy(m->graph);
     if (m->stream) pcl_stream_destroy(m->stream);
     if (m->arena) (void)hipFree(m->arena);
+    if (m->i8) (void)hipFree(m->i8);
+    if (m->qscale) (void)hipFree(m->qscale);
+    if (m->xq) (void)hipFree(m->xq);
     if (m->ints) (void)hipFree(m->ints);
     if (m->host_tp) (void)hipHostFree(m->host_tp);
     delete m;
@@ -221,14 +324,14 @@ void release(pcl_model *m) {
 // run one step on the model's stream, as a replay of the captured step when
 // use_graph (capturing it the first time)
 int run_step(pcl_model *m, int use_graph) {
-    if (!use_graph) return step(m);
+    if (!use_graph) return run_eager(m);
     void *prev = pcl_get_stream();
     int st = PCL_OK;
     pcl_set_stream(m->stream);
     if (!m->graph) {
         st = pcl_graph_begin();
         if (st == PCL_OK) {
-            const int s1 = step(m);
+            const int s1 = run_eager(m);
             void *g = nullptr;
             const int s2 = pcl_graph_end(&g);
             st = s1 != PCL_OK ? s1 : s2;
@@ -245,14 +348,18 @@ int run_step(pcl_model *m, int use_graph) {
 
 extern "C" {
 
-pcl_model *pcl_model_load(const char *path) {
+pcl_model *pcl_model_load_ex(const char *path, int weights) {
     if (!path) {
         fail(PCL_ERR_INVALID_ARG, "pcl_model_load: path is NULL");
         return nullptr;
     }
+    if (weights != PCL_W_FP32 && weights != PCL_W_INT8) {
+        fail(PCL_ERR_INVALID_ARG, "pcl_model_load: weights must be PCL_W_FP32 or PCL_W_INT8");
+        return nullptr;
+    }
     if (pcl::shim_init() != PCL_OK) return nullptr;
     pcl_model *m = new pcl_model();
-    if (load(m, path) != PCL_OK) {
+    if (load(m, path) != PCL_OK || (weights == PCL_W_INT8 && quantize_weights(m) != PCL_OK)) {
         const int st = pcl_last_status();
         char msg[512];
         snprintf(msg, sizeof msg, "%s", pcl_last_error());
@@ -262,6 +369,8 @@ pcl_model *pcl_model_load(const char *path) {
     }
     return m;
 }
+
+pcl_model *pcl_model_load(const char *path) { return pcl_model_load_ex(path, PCL_W_FP32); }
 
 int pcl_model_header(const pcl_model *m, int hdr[8]) {
     if (!m || !hdr) return fail(PCL_ERR_INVALID_ARG, "pcl_model_header: NULL argument");
@@ -274,7 +383,7 @@ int pcl_model_forward(pcl_model *m, int tok, int pos, float *logits) {
     if (tok < 0 || tok >= m->v || pos < 0 || pos >= m->blk)
         return fail(PCL_ERR_INVALID_ARG, "pcl_model_forward: token or position out of range");
     M_OK(set_tokpos(m, tok, pos));
-    M_OK(step(m));
+    M_OK(run_eager(m));
     if (logits)
         M_HIP(hipMemcpyAsync(logits, m->logits, sizeof(float) * (size_t)m->v, hipMemcpyDeviceToHost,
                              (hipStream_t)m->stream));
@@ -294,7 +403,7 @@ int pcl_model_generate(pcl_model *m, const int *prompt, int n_prompt, int n_new,
             return fail(PCL_ERR_INVALID_ARG, "pcl_model_generate: prompt token out of range");
     for (int i = 0; i < n_prompt; i++) {
         M_OK(set_tokpos(m, prompt[i], i));
-        M_OK(step(m));
+        M_OK(run_eager(m));
     }
     // the last prompt step left the first new token and position n_prompt in
     // device memory; each further step feeds the previous pick

@@ -19,14 +19,6 @@
 
 namespace pcl {
 
-constexpr float AMAX_INIT = 1e-8f;
-constexpr float RCP127 = 1.0f / 127.0f;  // rounded to fp32 at compile time
-
-__device__ __forceinline__ int quant_q(float x, float inv) {
-    int q = (int)roundf(x * inv);
-    return q > 127 ? 127 : (q < -127 ? -127 : q);
-}
-
 __device__ __forceinline__ float wave_max(float v) {
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
     return v;

@@ -28,6 +28,7 @@ PCL_ERR_UNSET_DIMS = 5
 PCL_ERR_RANGE = 6
 OP_N, OP_T = 0, 1
 EPI_NONE, EPI_GELU, EPI_RESID, EPI_GELU_BWD = 0, 1, 2, 3
+W_FP32, W_INT8 = 0, 1
 
 if not os.path.exists(LIB_PATH):
     raise ImportError(f"{LIB_PATH} is not built (run __graft_entry__.build() or make -C pure-c-llm_amd)")
@@ -118,6 +119,7 @@ _PROTOS = {
     "pcl_quantize_b_vnni": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp, _vp]),
     # a checkpoint on the GPU
     "pcl_model_load": (_vp, [_cp]),
+    "pcl_model_load_ex": (_vp, [_cp, _i]),
     "pcl_model_header": (_i, [_vp, _vp]),
     "pcl_model_forward": (_i, [_vp, _i, _i, _vp]),
     "pcl_model_generate": (_i, [_vp, _vp, _i, _i, _vp, _i]),
