@@ -47,8 +47,9 @@ def load_bench():
     lib.pcl_bench_attn.argtypes = [i, i, i, i, i, i, i, C.POINTER(d)]
     lib.pcl_bench_attn_bwd.argtypes = [i, i, i, i, i, i, C.POINTER(d)]
     lib.pcl_bench_sgemm_ex.argtypes = [i, i, i, i, i, i, i, i, i, C.POINTER(d)]
+    lib.pcl_bench_head_ce.argtypes = [i, i, i, C.c_long, i, i, i, C.POINTER(d)]
     for f in (lib.pcl_bench_igemm, lib.pcl_bench_sgemm, lib.pcl_bench_gemv, lib.pcl_bench_attn,
-              lib.pcl_bench_attn_bwd, lib.pcl_bench_sgemm_ex):
+              lib.pcl_bench_attn_bwd, lib.pcl_bench_sgemm_ex, lib.pcl_bench_head_ce):
         f.restype = i
     return pcl, lib
 
@@ -139,6 +140,27 @@ def sgemm_epi(pcl, lib, opA, opB, M, N, K, epi, warmup, steps):
         out["fused_ms" if fused else "two_pass_ms"] = round(per, 5)
         out["fused_TFLOPS" if fused else "two_pass_TFLOPS"] = round(2.0 * M * N * K / (per * 1e-3) / 1e12, 2)
     out["speedup"] = round(out["two_pass_ms"] / out["fused_ms"], 3)
+    return out
+
+
+def head_ce(pcl, lib, M, D, V, chunk_bytes, warmup, steps):
+    """The tied head fused with cross-entropy (pcl_head_ce: logits, softmax
+    cross-entropy in place, d_lnf, dwte) against its cross-entropy pass alone.
+    FLOPs: three M x D x V products, 6*M*D*V; the cross-entropy pass moves
+    3 * 4 * M * V bytes (two reads of the logits, one write)."""
+    out = {"M": M, "D": D, "V": V, "chunk_MB": round(chunk_bytes / 2 ** 20) if chunk_bytes > 0 else "1024 (default)"}
+    ms = C.c_double(0)
+    _check(pcl, lib.pcl_bench_head_ce(M, D, V, chunk_bytes, 0, warmup, steps, C.byref(ms)), f"head_ce {M}x{D}x{V}")
+    per = ms.value / steps
+    out["ms"] = round(per, 4)
+    out["TFLOPS"] = round(6.0 * M * D * V / (per * 1e-3) / 1e12, 2)
+    out["frac_peak"] = round(out["TFLOPS"] / PEAK_F32_TFLOPS, 4)
+    ms = C.c_double(0)
+    _check(pcl, lib.pcl_bench_head_ce(M, D, V, 0, 1, warmup, steps, C.byref(ms)), f"cross_entropy {M}x{V}")
+    per = ms.value / steps
+    out["ce_ms"] = round(per, 4)
+    out["ce_GBps"] = round(12.0 * M * V / (per * 1e-3) / 1e9, 1)
+    out["ce_share"] = round(out["ce_ms"] / out["ms"], 4)
     return out
 
 
@@ -262,6 +284,7 @@ CASES = {
     "fp32_ffn_up": lambda pcl, lib, w, s: sgemm(pcl, lib, 0, 0, 4096, 4096, 1024, 0, w, s),
     "epi_350m_ffn_up_gelu": lambda pcl, lib, w, s: sgemm_epi(pcl, lib, 0, 0, 4096, 4096, 1024, 1, w, s),
     "decode_e2e": lambda pcl, lib, w, s: decode_e2e(pcl),
+    "head_ce_350m": lambda pcl, lib, w, s: head_ce(pcl, lib, 4096, 1024, 50257, 0, w, s),
     "attn_350m": lambda pcl, lib, w, s: attn(pcl, lib, 4, 1024, 16, 64, True, w, s),
     "attn_350m_noprobs": lambda pcl, lib, w, s: attn(pcl, lib, 4, 1024, 16, 64, False, w, s),
     "attn_trainer_dh128": lambda pcl, lib, w, s: attn(pcl, lib, 4, 1024, 12, 128, True, w, s),
@@ -434,6 +457,13 @@ def main():
             "attn_out_residual": sgemm_epi(pcl, lib, 0, 0, 4096, 1024, 1024, 2, w, s),
             "ffn_down_residual": sgemm_epi(pcl, lib, 0, 0, 4096, 1024, 4096, 2, w, s),
             "bwd_dX_ffn_down_gelu_bwd": sgemm_epi(pcl, lib, 0, 1, 4096, 4096, 1024, 3, w, s),
+        }
+        # tied head + cross-entropy, forward and backward (350M: 4096 tokens,
+        # d 1024, vocabulary 50257): one 824 MB chunk, and 128 MB chunks
+        ex["head_ce"] = {
+            "350m": head_ce(pcl, lib, 4096, 1024, 50257, 0, 1, max(2, s // 20)),
+            "350m_chunk_128MB": head_ce(pcl, lib, 4096, 1024, 50257, 128 << 20, 1, max(2, s // 20)),
+            "grown_t256": head_ce(pcl, lib, 256, 512, 2048, 0, 3, 50),
         }
         # causal attention forward: 350M-class (16 heads of 64, B=4, T=1024),
         # the reference GPU trainer's heads (12 of 128), the grown model (16 of 32, T=256)

@@ -155,6 +155,11 @@ void attention_forward(const float *q, const float *k, const float *v, float *at
 void attention_backward(float *dq, float *dk, float *dv, const float *d_att, const float *q,
                         const float *k, const float *v, const float *probs, int B, int T);
 
+/* train.c:449-465: softmax cross-entropy over M rows of VOCAB_SIZE logits
+ * (pcl_set_model_dims); fills d_logits = (softmax - onehot)/M, returns the mean
+ * of -log(p[target] + 1e-30). */
+float cross_entropy(const float *logits, const int *targets, float *d_logits, int M);
+
 /* gemm_bench.c:225-236: per-tensor symmetric quantisation to u8 (+128 offset),
  * K padded to Kpad with 128. Returns the scale amax*fl(1/127). */
 float quantize_A(const float *A, uint8_t *Au, int M, int K, int Kpad);
@@ -195,6 +200,11 @@ void attn_fwd(const float *Q, const float *K, const float *V, float *att, float 
  * dAtt and the forward's probs; scratch holds B*H*T*T floats (dS). */
 void attn_bwd(float *dQ, float *dK, float *dV, float *scratch, const float *dAtt, const float *Q,
               const float *K, const float *V, const float *probs);
+/* gpu_kernels.h:78-81 (gpu_kernels.cu:518-547): M_ROWS = B_SIZE*T_SIZE rows
+ * (pcl_set_attn_dims) of VOCAB_SIZE logits (pcl_set_model_dims); the mean loss
+ * is ADDED into *loss_dev (zero it first); dlogits = (softmax - onehot)/M_ROWS
+ * and may be the logits buffer itself. */
+void ce_fwd_bwd(const float *logits, const int *targets, float *dlogits, float *loss_dev);
 
 /* ============================== 3. native entry points =================== */
 
@@ -239,6 +249,28 @@ int pcl_sgemv(int opW, int M, int N, int K, const float *X, int ldx, const float
 
 /* db(N) += colsum(dY) (gpu_kernels.cu:102-108), fixed m order per column. */
 int pcl_bias_bwd(float *db, const float *dY, int M, int N, int ld, void *stream);
+
+/* Softmax cross-entropy (train.c:449-465, gpu_kernels.cu:518-547) over M rows
+ * of V logits (leading dimension ld): dlogits (ldd) = (p - onehot)/M with
+ * p = expf(l - max)·(1/sum expf(l - max)); *loss += mean of -log(p[t] + 1e-30)
+ * (row terms in double, summed in a fixed order). dlogits may be logits itself
+ * (same ld) and must not otherwise overlap it. A target outside [0, V) makes
+ * the loss NaN. Two passes over the logits, one write. */
+int pcl_cross_entropy(const float *logits, int ld, const int *targets, float *dlogits, int ldd,
+                      int M, int V, float *loss, void *stream);
+
+/* The tied head and its cross-entropy, forward and backward in one call
+ * (train.c:412-465 as the trainer runs them, :531 then :718 then :542;
+ * train_kaggle.cu:165-174 + :409 on the GPU): over rows of at most chunk_bytes
+ * of logits at a time (<= 0: 1 GiB; the 350M shape 4096 x 50257 fits whole),
+ *   logits = lnf(M,D)·wte(V,D)^T, the cross-entropy above in place,
+ *   d_lnf(M,D)  = dlogits·wte          (SET; skipped when NULL),
+ *   dwte(V,D)  += dlogits^T·lnf        (ACCUMULATE; skipped when NULL),
+ *   *loss      += mean loss.
+ * The full M x V logits never exist at once beyond one chunk, which lives in the
+ * library's per-stream workspace. All pointers are device memory, rows dense. */
+int pcl_head_ce(const float *lnf, const float *wte, const int *targets, int M, int D, int V,
+                float *loss, float *d_lnf, float *dwte, long chunk_bytes, void *stream);
 
 /* Causal multi-head attention forward on the f32 MFMA (train.c:339-370,
  * gpu_kernels.cu:264-281/403-432), one fused launch: Q, K, V are (B*T) x ld

@@ -56,6 +56,8 @@ _ORACLE_PROTOS = {
     "orc_attention_forward": (None, [_vp, _vp, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i]),
     "orc_attention_backward": (None, [_vp, _vp, _vp, _vp, _i, _vp, _vp, _vp, _i, _vp, _i, _i, _i, _i]),
     "orc_attention_forward_f64": (None, [_vp, _vp, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i]),
+    "orc_cross_entropy": (_f, [_vp, _i, _vp, _vp, _i, _i, _i]),
+    "orc_head_ce": (_f, [_vp, _vp, _vp, _i, _i, _i, _vp, _vp]),
     "orc_model_load": (_vp, [C.c_char_p]),
     "orc_model_header": (None, [_vp, _vp]),
     "orc_model_forward": (None, [_vp, _i, _i, _vp]),
@@ -91,6 +93,7 @@ _REF_PROTOS = {
         "pcl_ref_tied_head_forward": (None, [_vp, _vp, _vp, _i]),
         "pcl_ref_tied_head_backward": (None, [_vp, _vp, _vp, _vp, _vp, _i]),
         "pcl_ref_train_n_heads": (_i, []),
+        "pcl_ref_cross_entropy": (_f, [_vp, _vp, _vp, _i]),
         "pcl_ref_train_t_size": (_i, []),
         "pcl_ref_attention_forward": (None, [_vp, _vp, _vp, _vp, _vp, _i, _i]),
         "pcl_ref_attention_backward": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i]),
@@ -232,6 +235,30 @@ def dequant(V, sa, sb):
     out = np.empty((M, N), np.float32)
     oracle().orc_dequant(p(np.ascontiguousarray(V)), N, p(sa), p(sb), p(out), N, M, N)
     return out
+
+
+def cross_entropy(logits, targets):
+    """orc_cross_entropy (train.c:449-465): (mean loss, dlogits)."""
+    lg = np.ascontiguousarray(logits, np.float32)
+    t = np.ascontiguousarray(targets, np.int32)
+    M, V = lg.shape
+    dl = np.empty_like(lg)
+    loss = oracle().orc_cross_entropy(p(lg), V, p(t), p(dl), V, M, V)
+    return float(loss), dl
+
+
+def head_ce(lnf, wte, targets, dwte=None):
+    """orc_head_ce: (mean loss, d_lnf, dwte after accumulation into a copy of
+    dwte, zeros when None)."""
+    x = np.ascontiguousarray(lnf, np.float32)
+    w = np.ascontiguousarray(wte, np.float32)
+    t = np.ascontiguousarray(targets, np.int32)
+    M, D = x.shape
+    V = w.shape[0]
+    dx = np.empty((M, D), np.float32)
+    dw = np.zeros((V, D), np.float32) if dwte is None else np.array(dwte, np.float32, copy=True)
+    loss = oracle().orc_head_ce(p(x), p(w), p(t), M, D, V, p(dx), p(dw))
+    return float(loss), dx, dw
 
 
 def gelu(x):

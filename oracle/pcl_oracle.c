@@ -23,6 +23,14 @@
  *                                 exact erf GELU within the tanh approximation's
  *                                 error; the derivative against central
  *                                 differences of the forward
+ *   orc_cross_entropy ........... train.c built from source (oracle/_ref): loss and
+ *                                 d_logits; closed forms (uniform logits give
+ *                                 log V and (1/V - onehot)/M; rows of d_logits sum
+ *                                 to zero; a constant added to a row changes
+ *                                 nothing); the loss against an f64 log-sum-exp
+ *   orc_head_ce ................. the pinned tied head and cross-entropy in the
+ *                                 trainer's order; d_lnf and dwte against central
+ *                                 differences of the f64 loss
  *   orc_model_forward_int8 ..... no counterpart in the reference: composed of the
  *                                 pinned quantisers, exact int GEMM and dequant
  *                                 below; against generate.c built from source
@@ -529,6 +537,47 @@ void orc_model_free(orc_model *m) {
     free(m->buf), free(m->lw), free(m->kc), free(m->vc);
     free(m->x), free(m->ln), free(m->q), free(m->att), free(m->proj), free(m->h), free(m->sc);
     free(m);
+}
+
+/* ---------------------------------------------------- cross-entropy ------ */
+float orc_cross_entropy(const float *logits, int ld, const int *targets, float *dlogits, int ldd,
+                        int M, int V) {
+    /* train.c:449-465 with explicit V and leading dimensions: per row the
+     * max, e = expf(l - max) summed in v order, p = e * (1/sum), the loss term
+     * -log((double)p[t] + 1e-30), dl = (p - onehot) / (float)M; the mean as
+     * (float)(double sum / M). dlogits may be logits itself (same ld). */
+    double loss = 0.0;
+    for (int m = 0; m < M; m++) {
+        const float *lo = logits + (size_t)m * ld;
+        float *dl = dlogits + (size_t)m * ldd;
+        const int t = targets[m];
+        float maxl = lo[0];
+        for (int v = 1; v < V; v++)
+            if (lo[v] > maxl) maxl = lo[v];
+        float sum = 0.0f;
+        for (int v = 0; v < V; v++) {
+            const float e = expf(lo[v] - maxl);
+            dl[v] = e;
+            sum += e;
+        }
+        const float inv = 1.0f / sum;
+        for (int v = 0; v < V; v++) dl[v] *= inv;
+        loss += -log((double)dl[t] + 1e-30);
+        for (int v = 0; v < V; v++) dl[v] = (dl[v] - (v == t ? 1.0f : 0.0f)) / (float)M;
+    }
+    return (float)(loss / M);
+}
+
+float orc_head_ce(const float *lnf, const float *wte, const int *targets, int M, int D, int V,
+                  float *d_lnf, float *dwte) {
+    /* train.c:531 (tied_head_forward), :718 (cross_entropy), :542
+     * (tied_head_backward: d_lnf set, dwte accumulated) in sequence */
+    float *lg = (float *)malloc(sizeof(float) * (size_t)M * V);
+    orc_tied_head_forward(lg, lnf, wte, M, D, V);
+    const float loss = orc_cross_entropy(lg, V, targets, lg, V, M, V);
+    orc_tied_head_backward(d_lnf, dwte, lg, lnf, wte, M, D, V);
+    free(lg);
+    return loss;
 }
 
 /* -------------------------------------------------------- attention ------ */

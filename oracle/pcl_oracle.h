@@ -105,6 +105,15 @@ void orc_unpack_vnni(const int8_t *Bp, int8_t *Bq, int K, int N, int Kpad);
 void orc_gelu_forward(float *out, const float *in, long n);
 void orc_gelu_backward(float *din, const float *dout, const float *in, long n);
 
+/* train.c:449-465: mean loss over M rows of V logits; dlogits = (p - onehot)/M
+ * (may alias logits with ldd == ld). */
+float orc_cross_entropy(const float *logits, int ld, const int *targets, float *dlogits, int ldd,
+                        int M, int V);
+/* train.c:531 + :718 + :542: logits = lnf.wte^T, cross-entropy, d_lnf SET and
+ * dwte ACCUMULATED (either may be NULL); returns the mean loss. */
+float orc_head_ce(const float *lnf, const float *wte, const int *targets, int M, int D, int V,
+                  float *d_lnf, float *dwte);
+
 /* generate.c:49-183 restated: a CKP1 checkpoint (train.c:633-648 layout) in
  * host memory with its KV cache, and forward(tok, pos) -> logits (V floats):
  * embedding, per layer ln -> Wq/Wk/Wv matvecs -> attention over the cache ->

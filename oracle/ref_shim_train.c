@@ -2,7 +2,7 @@
  * ref_shim_train.c -- build-time harness around the reference's own train.c
  * (pure-c-llm), compiled where it lies with small -D dims from the Makefile.
  * TEST INFRASTRUCTURE ONLY: exports its static GEMM and attention functions
- * (train.c:181-252, 339-407, 412-447) under pcl_ref_* names to pin the oracle.
+ * (train.c:181-252, 339-407, 412-465) under pcl_ref_* names to pin the oracle.
  */
 #include REF_TRAIN_C
 
@@ -35,4 +35,7 @@ void pcl_ref_attention_backward(float *dq, float *dk, float *dv, const float *d_
 void pcl_ref_gelu_forward(float *out, const float *in, int n) { gelu_forward(out, in, n); }
 void pcl_ref_gelu_backward(float *din, const float *dout, const float *in, int n) {
     gelu_backward(din, dout, in, n);
+}
+float pcl_ref_cross_entropy(const float *logits, const int *targets, float *d_logits, int M) {
+    return cross_entropy(logits, targets, d_logits, M);
 }

@@ -101,6 +101,16 @@ hipError_t launch_decode_bias_gelu_quant(const float *h, const float *b, uint8_t
 hipError_t launch_decode_argmax(const float *logits, int V, int *tokpos, int *out, int out_cap,
                                 hipStream_t s);
 
+// ---- softmax cross-entropy (ce.hip) ----
+// Rows [0, M) of logits (ld) -> dl (ldd, may alias logits): (p - onehot) / rows,
+// columns [V, pad) of dl set to 0 (pad >= V); row_loss[m] = -log(p[t] + 1e-30)
+// (NaN for a target outside [0, V)).
+hipError_t launch_cross_entropy(const float *logits, long ld, const int *targets, float *dl,
+                                long ldd, int M, int V, int pad, int rows, double *row_loss,
+                                hipStream_t s);
+// *loss += (float)(sum of row_loss[0..M) / rows)
+hipError_t launch_ce_loss(const double *row_loss, int M, int rows, float *loss, hipStream_t s);
+
 // Error reporting and device set-up of the C-ABI shim, for other translation
 // units of the library (model.cpp).
 int shim_error(int status, const char *msg);

@@ -1038,4 +1038,119 @@ void gemm_int8_kernel(const uint8_t *Au, int Kpad, const int8_t *Bp, const int32
     finish_void(host_gemm_int8_kernel(Au, Kpad, Bp, corr, dq, C, M, N));
 }
 
+// ------------------------------------------------------ cross-entropy ----
+static bool ranges_overlap(const void *a, size_t na, const void *b, size_t nb) {
+    const uintptr_t x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
+    return x < y + nb && y < x + na;
+}
+
+int pcl_cross_entropy(const float *logits, int ld, const int *targets, float *dlogits, int ldd,
+                      int M, int V, float *loss, void *stream) {
+    CHECK_ARG(M >= 0 && V > 0, "pcl_cross_entropy: bad dims (M=%d V=%d)", M, V);
+    if (M == 0) return PCL_OK;
+    CHECK_ARG(logits && targets && dlogits && loss, "pcl_cross_entropy: NULL operand");
+    CHECK_ARG(ld >= V && ldd >= V, "pcl_cross_entropy: ld=%d, ldd=%d below V=%d", ld, ldd, V);
+    const size_t nl = sizeof(float) * ((size_t)(M - 1) * ld + V);
+    const size_t nd = sizeof(float) * ((size_t)(M - 1) * ldd + V);
+    CHECK_ARG(!ranges_overlap(logits, nl, dlogits, nd) || (logits == dlogits && ld == ldd),
+              "pcl_cross_entropy: dlogits overlaps logits other than in place");
+    PCL_OK_OR_RETURN(do_init());
+    hipStream_t s = pick(stream);
+    StreamScratch *sc;
+    PCL_OK_OR_RETURN(get_scratch(s, 0, sizeof(double) * (size_t)M, &sc));
+    double *rl = static_cast<double *>(sc->aux);
+    HIP_OK(pcl::launch_cross_entropy(logits, ld, targets, dlogits, ldd, M, V, V, M, rl, s));
+    HIP_OK(pcl::launch_ce_loss(rl, M, M, loss, s));
+    return PCL_OK;
+}
+
+int pcl_head_ce(const float *lnf, const float *wte, const int *targets, int M, int D, int V,
+                float *loss, float *d_lnf, float *dwte, long chunk_bytes, void *stream) {
+    CHECK_ARG(M >= 0 && D > 0 && V > 0, "pcl_head_ce: bad dims (M=%d D=%d V=%d)", M, D, V);
+    if (M == 0) return PCL_OK;
+    CHECK_ARG(lnf && wte && targets && loss, "pcl_head_ce: NULL operand");
+    PCL_OK_OR_RETURN(do_init());
+    hipStream_t s = pick(stream);
+    // logits rows padded to 64 floats: 256-byte aligned rows, and a product
+    // over the first V - V % 64 vocabulary entries has K (or M) a multiple of 64
+    const long ldp = (V + 63) / 64 * 64, row_bytes = ldp * (long)sizeof(float);
+    const long cap = chunk_bytes > 0 ? chunk_bytes : (1L << 30);
+    long mc = cap / row_bytes;
+    if (mc < 1) mc = 1;
+    if (mc > M) mc = M;
+    if (mc > 128) mc = mc / 128 * 128;
+    const size_t loss_off = ((size_t)mc * row_bytes + 255) / 256 * 256;
+    StreamScratch *sc;
+    PCL_OK_OR_RETURN(get_scratch(s, 0, loss_off + sizeof(double) * (size_t)M, &sc));
+    float *lg = static_cast<float *>(sc->aux);
+    double *rl = reinterpret_cast<double *>(static_cast<char *>(sc->aux) + loss_off);
+    const int Vm = V / 64 * 64, Vr = V - Vm, L = (int)ldp;
+    for (int m0 = 0; m0 < M; m0 += (int)mc) {
+        const int mm = (int)(M - m0 < mc ? M - m0 : mc);
+        const float *x = lnf + (size_t)m0 * D;
+        // train.c:412-423 on the chunk, then :449-465 in place
+        PCL_OK_OR_RETURN(pcl_sgemm(PCL_OP_N, PCL_OP_T, mm, V, D, x, D, wte, D, nullptr, 0, lg, L, s));
+        HIP_OK(pcl::launch_cross_entropy(lg, ldp, targets + m0, lg, ldp, mm, V, L, M, rl + m0, s));
+        if (d_lnf) {  // train.c:426-435 (set): K = V in two parts
+            float *dx = d_lnf + (size_t)m0 * D;
+            PCL_OK_OR_RETURN(pcl_sgemm(PCL_OP_N, PCL_OP_N, mm, D, Vm, lg, L, wte, D, nullptr, 0, dx, D, s));
+            if (Vr)
+                PCL_OK_OR_RETURN(pcl_sgemm(PCL_OP_N, PCL_OP_N, mm, D, Vr, lg + Vm, L, wte + (size_t)Vm * D,
+                                           D, nullptr, 1, dx, D, s));
+        }
+        if (dwte) {  // train.c:436-446 (accumulate): vocabulary rows in two parts
+            if (Vm)
+                PCL_OK_OR_RETURN(pcl_sgemm(PCL_OP_T, PCL_OP_N, Vm, D, mm, lg, L, x, D, nullptr, 1, dwte, D, s));
+            if (Vr)
+                PCL_OK_OR_RETURN(pcl_sgemm(PCL_OP_T, PCL_OP_N, Vr, D, mm, lg + Vm, L, x, D, nullptr, 1,
+                                           dwte + (size_t)Vm * D, D, s));
+        }
+    }
+    HIP_OK(pcl::launch_ce_loss(rl, M, M, loss, s));
+    return PCL_OK;
+}
+
+// gpu_kernels.h:78-81: M_ROWS = B_SIZE * T_SIZE rows of VOCAB_SIZE logits
+void ce_fwd_bwd(const float *logits, const int *targets, float *dlogits, float *loss_dev) {
+    int st = PCL_OK;
+    if (g_vocab <= 0 || g_attn_batch <= 0 || g_attn_seq <= 0)
+        st = set_error(PCL_ERR_UNSET_DIMS,
+                       "ce_fwd_bwd: call pcl_set_model_dims and pcl_set_attn_dims first");
+    if (st == PCL_OK)
+        st = pcl_cross_entropy(logits, g_vocab, targets, dlogits, g_vocab, g_attn_batch * g_attn_seq,
+                               g_vocab, loss_dev, nullptr);
+    finish_void(st);
+}
+
+// train.c:449-465 on host buffers: returns the mean loss, fills d_logits
+static int host_cross_entropy(const float *logits, const int *targets, float *d_logits, int M,
+                              float *out) {
+    if (g_vocab <= 0)
+        return set_error(PCL_ERR_UNSET_DIMS, "cross_entropy: call pcl_set_model_dims first");
+    CHECK_ARG(M >= 0, "cross_entropy: negative M=%d", M);
+    *out = 0.f;
+    if (M == 0) return PCL_OK;
+    CHECK_ARG(logits && targets && d_logits, "cross_entropy: NULL operand");
+    PCL_OK_OR_RETURN(do_init());
+    const int V = g_vocab;
+    const size_t lb = sizeof(float) * (size_t)M * V;
+    void *dl, *dt, *dd, *dloss;
+    PCL_OK_OR_RETURN(upload(S_A, logits, lb, &dl));
+    PCL_OK_OR_RETURN(upload(S_B, targets, sizeof(int) * (size_t)M, &dt));
+    PCL_OK_OR_RETURN(stage_buf(S_C, lb, &dd));
+    PCL_OK_OR_RETURN(stage_buf(S_D, sizeof(float), &dloss));
+    HIP_OK(hipMemsetAsync(dloss, 0, sizeof(float), t_stream));
+    PCL_OK_OR_RETURN(pcl_cross_entropy((const float *)dl, V, (const int *)dt, (float *)dd, V, M, V,
+                                       (float *)dloss, t_stream));
+    PCL_OK_OR_RETURN(download(d_logits, dd, lb));
+    PCL_OK_OR_RETURN(download(out, dloss, sizeof(float)));
+    return sync_current();
+}
+
+float cross_entropy(const float *logits, const int *targets, float *d_logits, int M) {
+    float loss = 0.f;
+    finish_void(host_cross_entropy(logits, targets, d_logits, M, &loss));
+    return loss;
+}
+
 }  // extern "C"

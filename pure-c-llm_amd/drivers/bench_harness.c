@@ -440,3 +440,59 @@ done:
     pcl_free(c.X), pcl_free(c.Xu8), pcl_free(c.Y), pcl_free(c.sa), pcl_free(c.sb);
     return rc;
 }
+
+/* Tied head + cross-entropy (350M: M=4096 tokens, D=1024, V=50257).
+ * mode 0: one pcl_head_ce (logits, CE in place, d_lnf set, dwte accumulated)
+ *         over chunks of at most chunk_bytes of logits;
+ * mode 1: pcl_cross_entropy alone, M x V logits -> a separate dlogits. */
+typedef struct {
+    int M, D, V, mode;
+    long chunk;
+    void *x, *w, *t, *loss, *dx, *dw, *lg, *dl;
+} head_ctx;
+
+static int head_step(void *c_, int i) {
+    head_ctx *c = c_;
+    (void)i;
+    if (c->mode == 0)
+        return pcl_head_ce(c->x, c->w, c->t, c->M, c->D, c->V, c->loss, c->dx, c->dw, c->chunk, NULL);
+    return pcl_cross_entropy(c->lg, c->V, c->t, c->dl, c->V, c->M, c->V, c->loss, NULL);
+}
+
+int pcl_bench_head_ce(int M, int D, int V, long chunk_bytes, int mode, int warmup, int steps,
+                      double *ms_total) {
+    int rc = PCL_OK;
+    head_ctx c = {M, D, V, mode, chunk_bytes, NULL, NULL, NULL, NULL, NULL, NULL, NULL, NULL};
+    int *ht = malloc(sizeof(int) * (size_t)M);
+    c.t = pcl_malloc(sizeof(int) * (size_t)M);
+    c.loss = dev_f32(1, 40, 0.f, 0.f);
+    if (!ht || !c.t || !c.loss) {
+        rc = PCL_ERR_OOM;
+        goto done;
+    }
+    for (int m = 0; m < M; m++) ht[m] = (int)((long)m * 7919 % V);
+    TRY(pcl_memcpy_h2d(c.t, ht, sizeof(int) * (size_t)M));
+    if (mode == 0) {
+        c.x = dev_f32((size_t)M * D, 41, -1.f, 1.f);
+        c.w = dev_f32((size_t)V * D, 42, -0.05f, 0.05f);
+        c.dx = pcl_malloc(sizeof(float) * (size_t)M * D);
+        c.dw = dev_f32((size_t)V * D, 43, 0.f, 0.f);
+        if (!c.x || !c.w || !c.dx || !c.dw) {
+            rc = PCL_ERR_OOM;
+            goto done;
+        }
+    } else {
+        c.lg = dev_f32((size_t)M * V, 44, -4.f, 4.f);
+        c.dl = pcl_malloc(sizeof(float) * (size_t)M * V);
+        if (!c.lg || !c.dl) {
+            rc = PCL_ERR_OOM;
+            goto done;
+        }
+    }
+    TRY(time_steps(head_step, &c, warmup, steps, ms_total));
+done:
+    free(ht);
+    pcl_free(c.t), pcl_free(c.loss), pcl_free(c.x), pcl_free(c.w), pcl_free(c.dx), pcl_free(c.dw);
+    pcl_free(c.lg), pcl_free(c.dl);
+    return rc;
+}

@@ -83,6 +83,7 @@ _PROTOS = {
     "quantize_B_pack": (None, [_vp, _vp, _vp, _vp, _i, _i, _i]),
     "gemm_int8_kernel": (None, [_vp, _i, _vp, _vp, _vp, _vp, _i, _i]),
     "attention_forward": (None, [_vp, _vp, _vp, _vp, _vp, _i, _i]),
+    "cross_entropy": (C.c_float, [_vp, _vp, _vp, _i]),
     "attention_backward": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i]),
     # device-pointer drop-ins
     "gpu_init": (None, []),
@@ -91,6 +92,7 @@ _PROTOS = {
     "gemm_tn": (None, [_vp, _vp, _vp, _i, _i, _i]),
     "bias_bwd": (None, [_vp, _vp, _i, _i]),
     "attn_fwd": (None, [_vp, _vp, _vp, _vp, _vp]),
+    "ce_fwd_bwd": (None, [_vp, _vp, _vp, _vp]),
     "gelu_fwd": (None, [_vp, _vp, C.c_long]),
     "gelu_bwd": (None, [_vp, _vp, _vp, C.c_long]),
     "vec_add": (None, [_vp, _vp, _vp, C.c_long]),
@@ -105,6 +107,8 @@ _PROTOS = {
     "pcl_vec_add": (_i, [_vp, _vp, _vp, C.c_long, _vp]),
     "pcl_attn_fwd": (_i, [_vp, _vp, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i, _vp]),
     "pcl_attn_bwd": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _vp, _i, _vp, _i, _i, _i, _i, _i, _vp]),
+    "pcl_cross_entropy": (_i, [_vp, _i, _vp, _vp, _i, _i, _i, _vp, _vp]),
+    "pcl_head_ce": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp, _vp, _vp, C.c_long, _vp]),
     "pcl_s8_kpad": (_i, [_i]),
     "pcl_s8_packed_bytes": (_sz, [_i, _i]),
     "pcl_pack_b_s8": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp]),

@@ -561,3 +561,88 @@ def test_decode_oracle_int8_near_ref_generate(tmp_path, dims):
     om.close()
     assert 1e-3 < max(errs) < 5e-2, errs
 
+
+
+# -------------------------------------------------- cross-entropy ----
+def _ce_inputs(M, V, seed, scale=3.0):
+    lg = ob.normal((M, V), seed, 0.0, scale)
+    t = (ob.u8((M,), seed + 1).astype(np.int64) * 7919 % V).astype(np.int32)
+    return lg, t
+
+
+def test_cross_entropy_vs_ref_train():
+    tr = _ref_or_skip("libref_train.so")
+    V = tr.pcl_ref_train_vocab()
+    for M, seed in ((1, 900), (37, 901), (128, 902)):
+        lg, t = _ce_inputs(M, V, seed)
+        t[0] = V - 1
+        dl_ref = np.empty_like(lg)
+        loss_ref = tr.pcl_ref_cross_entropy(p(lg), p(t), p(dl_ref), M)
+        loss, dl = ob.cross_entropy(lg, t)
+        assert loss == pytest.approx(loss_ref, rel=1e-6)
+        assert ob.normwise_rel_err(dl, dl_ref) < REF_TOL
+
+
+def test_cross_entropy_closed_forms():
+    M, V = 5, 1000
+    t = np.array([0, 999, 3, 500, 3], np.int32)
+    # uniform logits: loss log V, dl = (1/V - onehot)/M
+    loss, dl = ob.cross_entropy(np.full((M, V), 2.5, np.float32), t)
+    assert loss == pytest.approx(np.log(V), rel=1e-6)
+    want = np.full((M, V), 1.0 / V, np.float64)
+    want[np.arange(M), t] -= 1.0
+    np.testing.assert_allclose(dl, want / M, rtol=0, atol=1e-8)
+    # random rows: loss against an f64 log-sum-exp, rows of dl sum to zero, a
+    # constant added to a row changes nothing
+    lg, t = _ce_inputs(64, 4096, 910, 4.0)
+    loss, dl = ob.cross_entropy(lg, t)
+    x = lg.astype(np.float64)
+    lse = np.log(np.exp(x - x.max(1, keepdims=True)).sum(1)) + x.max(1)
+    assert loss == pytest.approx(np.mean(lse - x[np.arange(64), t]), rel=1e-5)
+    assert np.abs(dl.astype(np.float64).sum(1)).max() < 1e-6  # vs entries of 1/M = 1.6e-2
+    p64 = np.exp(x - lse[:, None])
+    p64[np.arange(64), t] -= 1.0
+    assert ob.normwise_rel_err(dl, p64 / 64) < 1e-5
+    loss2, dl2 = ob.cross_entropy(lg + np.float32(8.0), t)
+    assert loss2 == pytest.approx(loss, rel=1e-5)
+    assert ob.normwise_rel_err(dl2, dl) < 1e-5
+
+
+def test_head_ce_central_differences():
+    # d_lnf and dwte are the gradients of the mean loss: compare with central
+    # differences of an f64 restatement on a tiny problem
+    M, D, V = 3, 8, 11
+    x = ob.normal((M, D), 920, 0.0, 1.0)
+    w = ob.normal((V, D), 921, 0.0, 0.5)
+    t = np.array([2, 10, 0], np.int32)
+
+    def f64_loss(xx, ww):
+        lg = xx @ ww.T
+        mx = lg.max(1, keepdims=True)
+        lse = np.log(np.exp(lg - mx).sum(1)) + mx[:, 0]
+        return np.mean(lse - lg[np.arange(M), t])
+    loss, dx, dw = ob.head_ce(x, w, t)
+    x64, w64 = x.astype(np.float64), w.astype(np.float64)
+    assert loss == pytest.approx(f64_loss(x64, w64), rel=1e-6)
+    h = 1e-5
+    num_dx = np.zeros((M, D))
+    for i in range(M):
+        for j in range(D):
+            a, b = x64.copy(), x64.copy()
+            a[i, j] += h
+            b[i, j] -= h
+            num_dx[i, j] = (f64_loss(a, w64) - f64_loss(b, w64)) / (2 * h)
+    num_dw = np.zeros((V, D))
+    for i in range(V):
+        for j in range(D):
+            a, b = w64.copy(), w64.copy()
+            a[i, j] += h
+            b[i, j] -= h
+            num_dw[i, j] = (f64_loss(x64, a) - f64_loss(x64, b)) / (2 * h)
+    # the tied weight's gradient through the head only (the embedding path is
+    # outside this function)
+    np.testing.assert_allclose(dx, num_dx, rtol=0, atol=2e-6)
+    np.testing.assert_allclose(dw, num_dw, rtol=0, atol=2e-6)
+    # dwte accumulates
+    _, _, dw2 = ob.head_ce(x, w, t, dwte=dw)
+    np.testing.assert_allclose(dw2, 2 * dw, rtol=1e-6, atol=1e-9)
