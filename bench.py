@@ -164,7 +164,7 @@ def head_ce(pcl, lib, M, D, V, chunk_bytes, warmup, steps):
     return out
 
 
-def decode_e2e(pcl, dims=(256, 512, 16, 2048, 16, 2048), n_new=255, ref_tokens=24):
+def decode_e2e(pcl, dims=(256, 512, 16, 2048, 16, 2048), n_new=255, ref_tokens=24, modes=(0, 1)):
     """Greedy decoding of a synthetic CKP1 checkpoint of the grown model
     (block 256, d 512, 16 heads, d_ff 2048, 16 layers, vocab 2048): one prompt
     token then n_new tokens fed back on the GPU, eagerly and as one graph
@@ -191,7 +191,7 @@ def decode_e2e(pcl, dims=(256, 512, 16, 2048, 16, 2048), n_new=255, ref_tokens=2
         try:
             prompt = np.array([1], np.int32)
             toks = np.empty(n_new, np.int32)
-            for graph in (0, 1):
+            for graph in modes:
                 _check(pcl, pcl.lib.pcl_model_generate(m, pcl.ptr(prompt), 1, n_new, pcl.ptr(toks), graph),
                        "generate")
                 t0 = time.perf_counter()
@@ -203,7 +203,7 @@ def decode_e2e(pcl, dims=(256, 512, 16, 2048, 16, 2048), n_new=255, ref_tokens=2
                 out[f"{tag}_ms_per_token"] = round(1e3 * dt / n_new, 4)
         finally:
             pcl.lib.pcl_model_free(m)
-    gen = ob.ref("libref_generate.so")
+    gen = ob.ref("libref_generate.so") if ref_tokens > 0 else None
     if gen is not None:
         gen.pcl_ref_gen_load(path.encode())
         logits = np.empty(v, np.float32)
@@ -284,6 +284,8 @@ CASES = {
     "fp32_ffn_up": lambda pcl, lib, w, s: sgemm(pcl, lib, 0, 0, 4096, 4096, 1024, 0, w, s),
     "epi_350m_ffn_up_gelu": lambda pcl, lib, w, s: sgemm_epi(pcl, lib, 0, 0, 4096, 4096, 1024, 1, w, s),
     "decode_e2e": lambda pcl, lib, w, s: decode_e2e(pcl),
+    # eager steps only (kernel traces: rocprofv3 does not follow graph launches here)
+    "decode_e2e_eager": lambda pcl, lib, w, s: decode_e2e(pcl, ref_tokens=0, modes=(0,)),
     "head_ce_350m": lambda pcl, lib, w, s: head_ce(pcl, lib, 4096, 1024, 50257, 0, w, s),
     "attn_350m": lambda pcl, lib, w, s: attn(pcl, lib, 4, 1024, 16, 64, True, w, s),
     "attn_350m_noprobs": lambda pcl, lib, w, s: attn(pcl, lib, 4, 1024, 16, 64, False, w, s),
