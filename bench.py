@@ -287,6 +287,7 @@ CASES = {
     # eager steps only (kernel traces: rocprofv3 does not follow graph launches here)
     "decode_e2e_eager": lambda pcl, lib, w, s: decode_e2e(pcl, ref_tokens=0, modes=(0,)),
     "head_ce_350m": lambda pcl, lib, w, s: head_ce(pcl, lib, 4096, 1024, 50257, 0, w, s),
+    "head_ce_350m_chunk128": lambda pcl, lib, w, s: head_ce(pcl, lib, 4096, 1024, 50257, 128 << 20, w, s),
     "attn_350m": lambda pcl, lib, w, s: attn(pcl, lib, 4, 1024, 16, 64, True, w, s),
     "attn_350m_noprobs": lambda pcl, lib, w, s: attn(pcl, lib, 4, 1024, 16, 64, False, w, s),
     "attn_trainer_dh128": lambda pcl, lib, w, s: attn(pcl, lib, 4, 1024, 12, 128, True, w, s),

@@ -350,8 +350,8 @@ int pcl_quantize_b_vnni(const float *B, int K, int N, int Kpad, int8_t *Bp, floa
  * int[8] {0x434B5031, block, d_model, n_heads, d_ff, n_layers, vocab, step}
  * then the tensors in registration order) loaded once into device memory with
  * its KV cache, decoded one token at a time as generate.c:118-183 does. The
- * head size d_model / n_heads must divide 256. NULL on failure (the reason in
- * pcl_last_error). */
+ * head size d_model / n_heads must divide 256; block and d_model at most 32768
+ * (d_ff too with INT8 weights). NULL on failure (the reason in pcl_last_error). */
 typedef struct pcl_model pcl_model;
 pcl_model *pcl_model_load(const char *path);
 /* weights: PCL_W_FP32 (as pcl_model_load) or PCL_W_INT8: every projection and

@@ -136,6 +136,8 @@ int run_eager(pcl_model *m) { return m->wmode == PCL_W_INT8 ? step_int8(m) : ste
 // Quantise every projection (per output column) and the tied head once.
 int quantize_weights(pcl_model *m) {
     const long D = m->d, F = m->df, V = m->v;
+    if (F > 32768)  // bias + GELU + quantisation keeps a d_ff row in LDS
+        return fail(PCL_ERR_INVALID_ARG, "pcl_model_load: INT8 weights need d_ff <= 32768");
     const int KD = kpad256((int)D), KF = kpad256((int)F);
     m->kpd = KD, m->kpf = KF;
     const long per = 3 * D * KD + D * KD + F * KD + D * KF;
@@ -212,9 +214,12 @@ int load(pcl_model *m, const char *path) {
         const int dh = m->h > 0 ? m->d / m->h : 0;
         if (m->blk <= 0 || m->d <= 0 || m->h <= 0 || m->df <= 0 || m->nl <= 0 || m->v <= 0 ||
             m->d % m->h != 0 || 256 % dh != 0 || (long)m->d * m->df > (1L << 30) ||
-            (long)m->v * m->d > (1L << 30) || m->blk > 65536) {
+            (long)m->v * m->d > (1L << 30) || m->blk > 32768 || m->d > 32768) {
+            // the cache attention keeps a block of scores, and the INT8 LayerNorm
+            // a row, in LDS (160 KB per workgroup)
             st = fail(PCL_ERR_INVALID_ARG,
-                      "pcl_model_load: unsupported dims (head size must divide 256)");
+                      "pcl_model_load: unsupported dims (head size must divide 256; block and "
+                      "d_model at most 32768)");
             break;
         }
         const long D = m->d, F = m->df;

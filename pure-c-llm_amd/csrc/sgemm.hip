@@ -791,8 +791,10 @@ SgemmPlan plan_sgemm(int M, int N, int K) {
     } else if (t128 >= 256) {
         p.cfg = SG_128_KG2;
     } else if (t64 < 256 && K >= 128) {
-        // too few tiles for 256 CUs: split K (chunks of whole 64-deep tiles)
+        // too few tiles for 256 CUs: split K (chunks of whole 64-deep tiles);
+        // grids of 129-255 tiles with a long K take 2+ workgroups per CU
         int splits = (int)(256 / (t64 > 0 ? t64 : 1));
+        if (splits < 2 && K >= 2048) splits = (int)((512 + t64 - 1) / t64);
         if (splits > K / 64) splits = K / 64;
         if (splits > 16) splits = 16;
         if (splits > 1) {

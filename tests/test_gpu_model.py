@@ -119,6 +119,10 @@ def test_model_errors(tmp_path):
     short = tmp_path / "short.ckp1"
     short.write_bytes(open(path, "rb").read()[:-16])
     assert not pcl.lib.pcl_model_load(str(short).encode())
+    big = tmp_path / "big.ckp1"  # a block beyond what the cache attention holds in LDS
+    big.write_bytes(np.array([0x434B5031, 40000, 64, 4, 128, 1, 32, 0], "<i4").tobytes())
+    assert not pcl.lib.pcl_model_load(str(big).encode())
+    assert pcl.lib.pcl_last_status() == pcl.PCL_ERR_INVALID_ARG
     m = _load(path)
     try:
         assert pcl.lib.pcl_model_forward(m, 32, 0, None) == pcl.PCL_ERR_INVALID_ARG

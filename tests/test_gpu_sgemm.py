@@ -79,9 +79,11 @@ def test_sgemm_bias_accumulate_and_k0():
 
 
 @pytest.mark.parametrize("opA,opB", [(N_, N_), (N_, T_), (T_, N_)])
-@pytest.mark.parametrize("M,N,K", [(256, 512, 2048), (256, 512, 512), (100, 200, 1000), (64, 96, 4100)])
+@pytest.mark.parametrize("M,N,K", [(256, 512, 2048), (256, 512, 512), (100, 200, 1000), (64, 96, 4100),
+                                   (640, 1024, 4096), (1000, 600, 2100)])
 def test_sgemm_split_k_bias_accumulate(opA, opB, M, N, K):
-    # grids of fewer than 256 64x64 tiles split K over workgroups; the partial
+    # grids of fewer than 256 64x64 tiles split K over workgroups (grids of
+    # 129-255 tiles with K >= 2048 into 2+ workgroups per CU); the partial
     # products are added in split order, then bias, then the old C
     A, B = _operands(opA, opB, M, N, K, 3000 + M + K)
     bias = ob.normal((N,), 3001)
