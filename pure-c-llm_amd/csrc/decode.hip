@@ -57,16 +57,21 @@ __global__ __launch_bounds__(256) void dec_layernorm_kernel(const float *__restr
 // LDS, older rows from the cache), softmax, att = sum_j p_j v_j. qkv holds
 // [q | k | v] (3*D floats) and bqkv, when given, is added to it here (the
 // INT8 step's projections carry no bias); the cache rows are D floats. dh
-// divides 256.
+// divides 256. DHT > 0: the head size at compile time, cache rows read as
+// 16-byte vectors (D % 4 == 0, 16-byte aligned cache); DHT == 0: any head
+// size, scalar reads. Each thread sums its own terms in key order, as before;
+// the loads of 8 keys are issued together.
+template <int DHT>
 __global__ __launch_bounds__(256) void dec_attn_kernel(const float *__restrict__ qkv,
                                                        const float *__restrict__ bqkv,
                                                        float *__restrict__ kc,
                                                        float *__restrict__ vc,
-                                                       float *__restrict__ att, int D, int dh,
+                                                       float *__restrict__ att, int D, int dh_rt,
                                                        const int *__restrict__ tokpos,
                                                        float scale) {
     extern __shared__ float dec_lds[];  // [blk] scores, then [256] partial sums
     __shared__ float red[4], qs[256], ks[256], vs[256];
+    const int dh = DHT > 0 ? DHT : dh_rt;
     const int h = blockIdx.x, tid = threadIdx.x, off = h * dh;
     const int pos = tokpos[1];
     if (tid < dh) {
@@ -83,9 +88,26 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(const float *__restrict__
     float *sc = dec_lds;
     float mloc = -INFINITY;
     for (int j = tid; j <= pos; j += 256) {
-        const float *kj = j == pos ? knew : kc + (long)j * D + off;
         float dot = 0.f;
-        for (int d = 0; d < dh; d++) dot += q[d] * kj[d];
+        if (j == pos) {
+            for (int d = 0; d < dh; d++) dot += q[d] * knew[d];
+        } else if constexpr (DHT > 0) {
+            typedef float v4f_t __attribute__((ext_vector_type(4)));
+            const v4f_t *kj = reinterpret_cast<const v4f_t *>(kc + (long)j * D + off);
+            v4f_t kv[DHT / 4];
+#pragma unroll
+            for (int c = 0; c < DHT / 4; c++) kv[c] = kj[c];
+#pragma unroll
+            for (int c = 0; c < DHT / 4; c++) {
+                dot += q[4 * c] * kv[c][0];
+                dot += q[4 * c + 1] * kv[c][1];
+                dot += q[4 * c + 2] * kv[c][2];
+                dot += q[4 * c + 3] * kv[c][3];
+            }
+        } else {
+            const float *kj = kc + (long)j * D + off;
+            for (int d = 0; d < dh; d++) dot += q[d] * kj[d];
+        }
         dot *= scale;
         sc[j] = dot;
         mloc = fmaxf(mloc, dot);
@@ -107,10 +129,16 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(const float *__restrict__
     const int G = 256 / dh, d = tid % dh, gq = tid / dh;
     float acc = 0.f;
     if (gq < G) {
-        for (int j = gq; j <= pos; j += G) {
-            const float *vj = j == pos ? vnew : vc + (long)j * D + off;
-            acc += sc[j] * inv * vj[d];
+        const float *vcol = vc + off + d;
+        int j = gq;
+        for (; j + 7 * G < pos; j += 8 * G) {  // 8 cache rows, none of them row pos
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) v[u] = vcol[(long)(j + u * G) * D];
+#pragma unroll
+            for (int u = 0; u < 8; u++) acc += sc[j + u * G] * inv * v[u];
         }
+        for (; j <= pos; j += G) acc += sc[j] * inv * (j == pos ? vnew[d] : vcol[(long)j * D]);
     }
     float *part = dec_lds + ((pos + 1 + 3) & ~3);
     part[tid] = acc;
@@ -171,8 +199,20 @@ hipError_t launch_decode_attn(const float *qkv, const float *bqkv, float *kc, fl
     const int dh = D / H;
     if (dh <= 0 || 256 % dh != 0) return hipErrorInvalidValue;
     const size_t lds = sizeof(float) * ((size_t)((blk + 3) & ~3) + 256);
-    hipLaunchKernelGGL(dec_attn_kernel, dim3(H), dim3(256), lds, s, qkv, bqkv, kc, vc, att, D, dh,
-                       tokpos, 1.0f / sqrtf((float)dh));
+    const float scale = 1.0f / sqrtf((float)dh);
+    const bool vec = D % 4 == 0 && ((reinterpret_cast<uintptr_t>(kc) | reinterpret_cast<uintptr_t>(vc)) & 15) == 0;
+    if (vec && dh == 32)
+        hipLaunchKernelGGL(dec_attn_kernel<32>, dim3(H), dim3(256), lds, s, qkv, bqkv, kc, vc, att, D,
+                           dh, tokpos, scale);
+    else if (vec && dh == 64)
+        hipLaunchKernelGGL(dec_attn_kernel<64>, dim3(H), dim3(256), lds, s, qkv, bqkv, kc, vc, att, D,
+                           dh, tokpos, scale);
+    else if (vec && dh == 128)
+        hipLaunchKernelGGL(dec_attn_kernel<128>, dim3(H), dim3(256), lds, s, qkv, bqkv, kc, vc, att, D,
+                           dh, tokpos, scale);
+    else
+        hipLaunchKernelGGL(dec_attn_kernel<0>, dim3(H), dim3(256), lds, s, qkv, bqkv, kc, vc, att, D,
+                           dh, tokpos, scale);
     return hipGetLastError();
 }
 

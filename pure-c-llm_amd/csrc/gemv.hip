@@ -113,6 +113,51 @@ __device__ __forceinline__ void stage_rows(T *xs, int ld, int kchunk, int kvalid
     }
 }
 
+// Input transforms of the decode step applied to a staged activation row
+// (M = 1): XF_LN = LayerNorm over the whole row X[0..K) (generate.c:106-114:
+// mean, mean square deviation, (x - mu) * (1/sqrtf(var + 1e-5)) * g + b), of
+// which this block holds elements [kb, kb + klen); XF_GELU = tanh-GELU
+// (train.c:314-322) elementwise. Every block of a launch computes the same
+// statistics in the same order, so all see identical values.
+constexpr int XF_NONE = 0, XF_LN = 1, XF_GELU = 2;
+
+__device__ __forceinline__ float gv_block_sum(float v, float *red) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return ((red[0] + red[1]) + red[2]) + red[3];
+}
+
+template <int XF>
+__device__ __forceinline__ void gv_xform(float *xs, int klen, int kb, int K,
+                                         const float *__restrict__ X,
+                                         const float *__restrict__ g,
+                                         const float *__restrict__ b) {
+    if constexpr (XF == XF_LN) {
+        __shared__ float red[GV_THREADS / 64];
+        float s = 0.f;
+        for (int k = threadIdx.x; k < K; k += GV_THREADS) s += X[k];
+        const float mu = gv_block_sum(s, red) / K;
+        float q = 0.f;
+        for (int k = threadIdx.x; k < K; k += GV_THREADS) {
+            const float d = X[k] - mu;
+            q += d * d;
+        }
+        const float var = gv_block_sum(q, red) / K;
+        const float rs = 1.0f / sqrtf(var + 1e-5f);
+        for (int k = threadIdx.x; k < klen; k += GV_THREADS)
+            xs[k] = (xs[k] - mu) * rs * g[kb + k] + b[kb + k];
+    } else if constexpr (XF == XF_GELU) {
+        for (int k = threadIdx.x; k < klen; k += GV_THREADS) {
+            const float v = xs[k];
+            xs[k] = 0.5f * v * (1.0f + tanhf(0.7978845608028654f * (v + 0.044715f * v * v * v)));
+        }
+    }
+    __syncthreads();
+}
+
 // Second pass of a split-K GEMV: Y[m,n] = sum over splits in order (+ bias,
 // + Y when accumulating). part is [splits][M][nround].
 __global__ void sgemv_reduce_kernel(const float *__restrict__ part, int splits, int M, int N,
@@ -133,11 +178,12 @@ __global__ void sgemv_reduce_kernel(const float *__restrict__ part, int splits, 
 // rg = tid/(CW/4)) owns columns 4*c4..4*c4+3 and a contiguous run of
 // kchunk/RG rows (RG = row groups per block). Narrow strips (CW = 16) give
 // enough blocks without splitting K when N is small.
-template <int MR, bool VEC, bool XONES, int CW>
+template <int MR, bool VEC, bool XONES, int CW, int XF = XF_NONE>
 __global__ __launch_bounds__(GV_THREADS) void sgemv_n_kernel(
     const float *__restrict__ X, long ldx, const float *__restrict__ W, long ldw,
     const float *__restrict__ bias, float *__restrict__ Y, long ldy, int M, int N, int K,
-    int kchunk, int splits, float *__restrict__ part, int accumulate) {
+    int kchunk, int splits, float *__restrict__ part, int accumulate,
+    const float *__restrict__ xg = nullptr, const float *__restrict__ xb = nullptr) {
     constexpr int CQ = CW / 4;             // threads across a strip row
     constexpr int RG = GV_THREADS / CQ;    // row groups
     __shared__ float red[RG][MR][CW];
@@ -180,6 +226,7 @@ __global__ __launch_bounds__(GV_THREADS) void sgemv_n_kernel(
     if (!XONES) {
         stage_rows<MR, false>(xs, kchunk, kchunk, min(kchunk, K - kb), M, X + kb, ldx);
         __syncthreads();
+        if constexpr (XF != XF_NONE) gv_xform<XF>(xs, min(kchunk, K - kb), kb, K, X, xg, xb);
     }
 
     float acc[MR][4];
@@ -233,11 +280,12 @@ __global__ __launch_bounds__(GV_THREADS) void sgemv_n_kernel(
 // ------------------------------------------------------------- sgemv_t ----
 // Block = SGT_ROWS rows of W (N x K) x kchunk columns. Thread (j = tid%16,
 // rs = tid/16) reads 16-byte vectors k = 4j + 64i of rows rs + 16r.
-template <int MR, bool VEC>
+template <int MR, bool VEC, int XF = XF_NONE>
 __global__ __launch_bounds__(GV_THREADS) void sgemv_t_kernel(
     const float *__restrict__ X, long ldx, const float *__restrict__ W, long ldw,
     const float *__restrict__ bias, float *__restrict__ Y, long ldy, int M, int N, int K,
-    int kchunk, int splits, float *__restrict__ part, int accumulate) {
+    int kchunk, int splits, float *__restrict__ part, int accumulate,
+    const float *__restrict__ xg = nullptr, const float *__restrict__ xb = nullptr) {
     __shared__ float res[MR][SGT_ROWS];
     extern __shared__ __attribute__((aligned(16))) unsigned char gv_dyn[];
     float *xs = reinterpret_cast<float *>(gv_dyn);  // MR x kchunk, sized at launch
@@ -278,6 +326,7 @@ __global__ __launch_bounds__(GV_THREADS) void sgemv_t_kernel(
 
     stage_rows<MR, false>(xs, kchunk, kchunk, klen, M, X + kb, ldx);
     __syncthreads();
+    if constexpr (XF != XF_NONE) gv_xform<XF>(xs, klen, kb, K, X, xg, xb);
 
     float acc[SGT_RPL][MR];
 #pragma unroll
@@ -615,6 +664,63 @@ hipError_t launch_sgemv(const GemvPlan &p, int w_trans, int M, int N, int K, con
         launch_sgemv_mr<8>(p, w_trans, vec, false, M, N, K, X, ldx, W, ldw, bias, accumulate, Y,
                            ldy, ws, stream);
     }
+    return hipGetLastError();
+}
+
+// One row (M = 1) with an input transform; same plans and kernels as
+// launch_sgemv.
+template <int XF>
+static void launch_sgemv_xf_t(const GemvPlan &p, int w_trans, bool vec, int N, int K,
+                              const float *X, const float *W, long ldw, const float *g,
+                              const float *b, const float *bias, int accumulate, float *Y,
+                              const Workspace &ws, hipStream_t s) {
+    dim3 grid(p.strips, p.splits), block(GV_THREADS);
+    float *part = (float *)ws.buf;
+    const size_t xsb = (size_t)p.kchunk * sizeof(float);
+    const long ldx = K, ldy = N;
+    if (w_trans) {
+        if (vec)
+            hipLaunchKernelGGL((sgemv_t_kernel<1, true, XF>), grid, block, xsb, s, X, ldx, W, ldw, bias, Y,
+                               ldy, 1, N, K, p.kchunk, p.splits, part, accumulate, g, b);
+        else
+            hipLaunchKernelGGL((sgemv_t_kernel<1, false, XF>), grid, block, xsb, s, X, ldx, W, ldw, bias, Y,
+                               ldy, 1, N, K, p.kchunk, p.splits, part, accumulate, g, b);
+    } else if (p.cw == 16) {
+        if (vec)
+            hipLaunchKernelGGL((sgemv_n_kernel<1, true, false, 16, XF>), grid, block, xsb, s, X, ldx, W, ldw,
+                               bias, Y, ldy, 1, N, K, p.kchunk, p.splits, part, accumulate, g, b);
+        else
+            hipLaunchKernelGGL((sgemv_n_kernel<1, false, false, 16, XF>), grid, block, xsb, s, X, ldx, W,
+                               ldw, bias, Y, ldy, 1, N, K, p.kchunk, p.splits, part, accumulate, g, b);
+    } else {
+        if (vec)
+            hipLaunchKernelGGL((sgemv_n_kernel<1, true, false, 64, XF>), grid, block, xsb, s, X, ldx, W, ldw,
+                               bias, Y, ldy, 1, N, K, p.kchunk, p.splits, part, accumulate, g, b);
+        else
+            hipLaunchKernelGGL((sgemv_n_kernel<1, false, false, 64, XF>), grid, block, xsb, s, X, ldx, W,
+                               ldw, bias, Y, ldy, 1, N, K, p.kchunk, p.splits, part, accumulate, g, b);
+    }
+    if (p.splits > 1) {
+        const int nround = p.strips * (w_trans ? SGT_ROWS : p.cw);
+        hipLaunchKernelGGL(sgemv_reduce_kernel, dim3(reduce_grid(1, N)), dim3(256), 0, s, part,
+                           p.splits, 1, N, nround, bias, Y, ldy, accumulate);
+    }
+}
+
+hipError_t launch_sgemv_xf(const GemvPlan &p, int w_trans, int xf, int N, int K, const float *X,
+                           const float *W, long ldw, const float *g, const float *b,
+                           const float *bias, int accumulate, float *Y, const Workspace &ws,
+                           hipStream_t stream) {
+    if (N <= 0 || K <= 0) return hipErrorInvalidValue;
+    if (xf == XF_LN && (!g || !b)) return hipErrorInvalidValue;
+    if (p.splits > 1 && (ws.buf == nullptr || ws.bytes_cap < p.part_bytes)) return hipErrorInvalidValue;
+    const bool vec = aligned16(W) && ldw % 4 == 0 && (w_trans ? K % 4 == 0 : N % 4 == 0);
+    if (xf == XF_LN)
+        launch_sgemv_xf_t<XF_LN>(p, w_trans, vec, N, K, X, W, ldw, g, b, bias, accumulate, Y, ws, stream);
+    else if (xf == XF_GELU)
+        launch_sgemv_xf_t<XF_GELU>(p, w_trans, vec, N, K, X, W, ldw, g, b, bias, accumulate, Y, ws, stream);
+    else
+        launch_sgemv_xf_t<XF_NONE>(p, w_trans, vec, N, K, X, W, ldw, g, b, bias, accumulate, Y, ws, stream);
     return hipGetLastError();
 }
 

@@ -115,6 +115,10 @@ hipError_t launch_ce_loss(const double *row_loss, int M, int rows, float *loss, 
 // units of the library (model.cpp).
 int shim_error(int status, const char *msg);
 int shim_init();
+// launch_sgemv_xf on the stream's workspace (status as the C-ABI calls)
+int sgemv_xf(int w_trans, int xf, int N, int K, const float *X, const float *W, int ldw,
+             const float *g, const float *b, const float *bias, int accumulate, float *Y,
+             void *stream);
 
 // ---- GEMV (gemv.hip) ----
 GemvPlan plan_sgemv(int w_trans, int M, int N, int K);
@@ -127,6 +131,14 @@ hipError_t launch_sgemv(const GemvPlan &p, int w_trans, int M, int N, int K, con
                         long ldx, bool x_ones, const float *W, long ldw, const float *bias,
                         int accumulate, float *Y, long ldy, const Workspace &ws,
                         hipStream_t stream);
+// One activation row (M = 1, X of K floats, Y of N floats) through a transform
+// applied as the row is staged: xf 0 none, 1 LayerNorm over the row (g, b of
+// K floats; generate.c:106-114), 2 tanh-GELU; then the GEMV of launch_sgemv
+// (plan from plan_sgemv(w_trans, 1, N, K)).
+hipError_t launch_sgemv_xf(const GemvPlan &p, int w_trans, int xf, int N, int K, const float *X,
+                           const float *W, long ldw, const float *g, const float *b,
+                           const float *bias, int accumulate, float *Y, const Workspace &ws,
+                           hipStream_t stream);
 // INT8 GEMV over the packed layout (ldb = Kp); out_mode as in launch_igemm.
 hipError_t launch_igemv(const GemvPlan &p, int out_mode, int M, int N, int K, const uint8_t *X,
                         long ldx, const int8_t *Bpk, long ldb, const int32_t *col_off,

@@ -85,18 +85,16 @@ int step(pcl_model *m) {
     const int D = m->d, F = m->df, V = m->v;
     int *tokpos = m->ints, *out = m->ints + 2;
     M_HIP(pcl::launch_decode_embed(m->wte, m->wpe, m->x, D, tokpos, s));
+    // LayerNorm and GELU are applied by the GEMV that consumes them, as it
+    // stages its activation row (XF 1 / 2), so a layer is five launches
     for (const Layer &y : m->lay) {
-        M_HIP(pcl::launch_decode_layernorm(m->x, y.g1, y.b1, m->ln, D, s));
-        M_OK(pcl_sgemv(PCL_OP_N, 1, 3 * D, D, m->ln, D, y.wqkv, 3 * D, y.bqkv, 0, m->qkv, 3 * D, s));
+        M_OK(pcl::sgemv_xf(0, 1, 3 * D, D, m->x, y.wqkv, 3 * D, y.g1, y.b1, y.bqkv, 0, m->qkv, s));
         M_HIP(pcl::launch_decode_attn(m->qkv, nullptr, y.kc, y.vc, m->att, D, m->h, m->blk, tokpos, s));
         M_OK(pcl_sgemv(PCL_OP_N, 1, D, D, m->att, D, y.wo, D, y.bo, 1, m->x, D, s));
-        M_HIP(pcl::launch_decode_layernorm(m->x, y.g2, y.b2, m->ln, D, s));
-        M_OK(pcl_sgemv(PCL_OP_N, 1, F, D, m->ln, D, y.w1, F, y.bf1, 0, m->hh, F, s));
-        M_HIP(pcl::launch_elementwise(0, F, m->hg, m->hh, nullptr, s));
-        M_OK(pcl_sgemv(PCL_OP_N, 1, D, F, m->hg, F, y.w2, D, y.bf2, 1, m->x, D, s));
+        M_OK(pcl::sgemv_xf(0, 1, F, D, m->x, y.w1, F, y.g2, y.b2, y.bf1, 0, m->hh, s));
+        M_OK(pcl::sgemv_xf(0, 2, D, F, m->hh, y.w2, D, nullptr, nullptr, y.bf2, 1, m->x, s));
     }
-    M_HIP(pcl::launch_decode_layernorm(m->x, m->gf, m->bf, m->ln, D, s));
-    M_OK(pcl_sgemv(PCL_OP_T, 1, V, D, m->ln, D, m->wte, D, nullptr, 0, m->logits, V, s));
+    M_OK(pcl::sgemv_xf(1, 1, V, D, m->x, m->wte, D, m->gf, m->bf, nullptr, 0, m->logits, s));
     M_HIP(pcl::launch_decode_argmax(m->logits, V, tokpos, out, m->blk + 1, s));
     return PCL_OK;
 }
