@@ -724,6 +724,157 @@ hipError_t launch_sgemv_xf(const GemvPlan &p, int w_trans, int xf, int N, int K,
     return hipGetLastError();
 }
 
+// ---------------------------------------------------- decode INT8 row ----
+// One fp32 activation row through an input transform, quantised per row in
+// LDS (the rule of quant.hip: amax from 1e-8, scale = amax * fl(1/127),
+// q = clamp(roundf(x / scale)), padding past K is 0 after recentring), times
+// the packed s8 weights (N rows of Kp bytes), dequantised by scale * sb[n]:
+//   QX_NONE: the row as is; QX_LN: LayerNorm (g, b; the reduction order of
+//   the decode LayerNorm kernels); QX_BIAS_GELU: tanh-GELU(x + b).
+//   EPI 0: Y[n] = v * dq;  EPI 1: Y[n] = Y[n] + (v * dq + bias[n]).
+// Every block computes the same row, scale and bytes. No K split.
+constexpr int QX_NONE = 0, QX_LN = 1, QX_BIAS_GELU = 2;
+
+__device__ __forceinline__ float gv_sum4(float v, float *red) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return red[0] + red[1] + red[2] + red[3];
+}
+
+template <int QX, int EPI>
+__global__ __launch_bounds__(GV_THREADS) void igemv_q_kernel(
+    const float *__restrict__ X, const float *__restrict__ g, const float *__restrict__ b, int K,
+    const int8_t *__restrict__ B, long ldb, const float *__restrict__ sb,
+    const float *__restrict__ bias, float *__restrict__ Y, int N) {
+    static_assert(GV_THREADS == 256, "the reductions assume four waves");
+    extern __shared__ __attribute__((aligned(16))) unsigned char gv_dyn[];
+    const int Kp = (int)ldb;
+    float *xf = reinterpret_cast<float *>(gv_dyn);          // [Kp]
+    int8_t *xs = reinterpret_cast<int8_t *>(xf + Kp);        // [Kp]
+    __shared__ float red[4], mred[4];
+    __shared__ int32_t res[SGT_ROWS];
+
+    const int tid = threadIdx.x;
+    const int j = tid & 15, rs = tid >> 4;
+    const int n0 = blockIdx.x * SGT_ROWS;
+    const int klen = min(Kp, (K + 15) & ~15);
+    const int8_t *brow[SGT_RPL];
+#pragma unroll
+    for (int r = 0; r < SGT_RPL; r++) brow[r] = B + (long)min(n0 + rs + 16 * r, N - 1) * ldb;
+    constexpr int UK = 4;
+    auto load_batch = [&](v4i (&w)[UK][SGT_RPL], int k0) {
+#pragma unroll
+        for (int u = 0; u < UK; u++)
+#pragma unroll
+            for (int r = 0; r < SGT_RPL; r++)
+                w[u][r] = *reinterpret_cast<const v4i *>(brow[r] + min(k0 + 256 * u, klen - 16));
+    };
+    v4i wn[UK][SGT_RPL];
+    load_batch(wn, 16 * j);  // in flight while the row is made
+
+    if constexpr (QX == QX_LN) {
+        float s0 = 0.f;
+        for (int i = tid; i < K; i += 256) s0 += X[i];
+        const float mu = gv_sum4(s0, red) / K;
+        float q = 0.f;
+        for (int i = tid; i < K; i += 256) {
+            const float d = X[i] - mu;
+            q += d * d;
+        }
+        const float var = gv_sum4(q, red) / K;
+        const float rsd = 1.0f / sqrtf(var + 1e-5f);
+        for (int i = tid; i < K; i += 256) xf[i] = (X[i] - mu) * rsd * g[i] + b[i];
+    } else if constexpr (QX == QX_BIAS_GELU) {
+        for (int i = tid; i < K; i += 256) {
+            const float v = X[i] + b[i];
+            xf[i] = 0.5f * v * (1.0f + tanhf(0.7978845608028654f * (v + 0.044715f * v * v * v)));
+        }
+    } else {
+        for (int i = tid; i < K; i += 256) xf[i] = X[i];
+    }
+    float mx = 0.f;
+    for (int i = tid; i < K; i += 256) mx = fmaxf(mx, fabsf(xf[i]));
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    if ((tid & 63) == 0) mred[tid >> 6] = mx;
+    __syncthreads();
+    const float amax = fmaxf(fmaxf(fmaxf(mred[0], mred[1]), fmaxf(mred[2], mred[3])), AMAX_INIT);
+    const float scale = amax * RCP127, inv = 1.0f / scale;
+    for (int k = tid; k < Kp; k += 256) xs[k] = (int8_t)(k < K ? quant_q(xf[k], inv) : 0);
+    __syncthreads();
+
+    int32_t acc[SGT_RPL] = {};
+    for (int k0 = 16 * j; k0 < klen; k0 += 256 * UK) {
+        v4i w[UK][SGT_RPL];
+#pragma unroll
+        for (int u = 0; u < UK; u++)
+#pragma unroll
+            for (int r = 0; r < SGT_RPL; r++) w[u][r] = wn[u][r];
+        if (k0 + 256 * UK < klen) load_batch(wn, k0 + 256 * UK);
+#pragma unroll
+        for (int u = 0; u < UK; u++) {
+            const int k = k0 + 256 * u;
+            if (k < klen) {
+                const v4i xv = *reinterpret_cast<const v4i *>(&xs[k]);
+#pragma unroll
+                for (int r = 0; r < SGT_RPL; r++) {
+                    int a = acc[r];
+                    a = __builtin_amdgcn_sdot4(xv[0], w[u][r][0], a, false);
+                    a = __builtin_amdgcn_sdot4(xv[1], w[u][r][1], a, false);
+                    a = __builtin_amdgcn_sdot4(xv[2], w[u][r][2], a, false);
+                    a = __builtin_amdgcn_sdot4(xv[3], w[u][r][3], a, false);
+                    acc[r] = a;
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < SGT_RPL; r++) {
+        int v = acc[r];
+        v += __shfl_xor(v, 8, 16);
+        v += __shfl_xor(v, 4, 16);
+        v += __shfl_xor(v, 2, 16);
+        v += __shfl_xor(v, 1, 16);
+        if (j == 0) res[rs + 16 * r] = v;
+    }
+    __syncthreads();
+    if (tid < SGT_ROWS) {
+        const int n = n0 + tid;
+        if (n < N) {
+            const float dq = scale * sb[n];
+            const float y = (float)res[tid] * dq;
+            if (EPI == 1) Y[n] = Y[n] + (y + bias[n]);
+            else Y[n] = y;
+        }
+    }
+}
+
+hipError_t launch_igemv_q(int qx, int epi, const float *X, const float *g, const float *b, int K,
+                          const int8_t *B, int Kp, const float *sb, const float *bias, float *Y,
+                          int N, hipStream_t s) {
+    if (N <= 0 || K <= 0 || K > Kp || Kp % 256 != 0 || Kp > IGEMV_Q_MAX_K) return hipErrorInvalidValue;
+    if ((reinterpret_cast<uintptr_t>(B) & 15) != 0) return hipErrorInvalidValue;
+    if ((qx == QX_LN && (!g || !b)) || (qx == QX_BIAS_GELU && !b) || (epi == 1 && !bias))
+        return hipErrorInvalidValue;
+    const dim3 grid((unsigned)cdiv(N, SGT_ROWS)), block(GV_THREADS);
+    const size_t lds = (size_t)Kp * (sizeof(float) + 1);
+#define IGQ(QXV, EPIV)                                                                        \
+    hipLaunchKernelGGL((igemv_q_kernel<QXV, EPIV>), grid, block, lds, s, X, g, b, K, B, (long)Kp, \
+                       sb, bias, Y, N)
+    if (qx == QX_LN) {
+        if (epi) IGQ(QX_LN, 1); else IGQ(QX_LN, 0);
+    } else if (qx == QX_BIAS_GELU) {
+        if (epi) IGQ(QX_BIAS_GELU, 1); else IGQ(QX_BIAS_GELU, 0);
+    } else {
+        if (epi) IGQ(QX_NONE, 1); else IGQ(QX_NONE, 0);
+    }
+#undef IGQ
+    return hipGetLastError();
+}
+
 template <int MR>
 static void launch_igemv_mr(const GemvPlan &p, int out_mode, int M, int N, int K,
                             const uint8_t *X, long ldx, const int8_t *B, long ldb,

@@ -139,6 +139,14 @@ hipError_t launch_sgemv_xf(const GemvPlan &p, int w_trans, int xf, int N, int K,
                            const float *W, long ldw, const float *g, const float *b,
                            const float *bias, int accumulate, float *Y, const Workspace &ws,
                            hipStream_t stream);
+// Decode INT8 GEMV of one fp32 row: qx 0 none, 1 LayerNorm (g, b), 2
+// GELU(x + b); the row quantised per row in-kernel; packed weights N x Kp
+// (Kp % 256 == 0, K <= Kp <= IGEMV_Q_MAX_K); epi 0: Y = v * scale * sb[n],
+// epi 1: Y += v * scale * sb[n] + bias[n].
+constexpr int IGEMV_Q_MAX_K = 8192;
+hipError_t launch_igemv_q(int qx, int epi, const float *X, const float *g, const float *b, int K,
+                          const int8_t *B, int Kp, const float *sb, const float *bias, float *Y,
+                          int N, hipStream_t s);
 // INT8 GEMV over the packed layout (ldb = Kp); out_mode as in launch_igemm.
 hipError_t launch_igemv(const GemvPlan &p, int out_mode, int M, int N, int K, const uint8_t *X,
                         long ldx, const int8_t *Bpk, long ldb, const int32_t *col_off,

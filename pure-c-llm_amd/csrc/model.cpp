@@ -129,7 +129,33 @@ int step_int8(pcl_model *m) {
     return PCL_OK;
 }
 
-int run_eager(pcl_model *m) { return m->wmode == PCL_W_INT8 ? step_int8(m) : step(m); }
+// The INT8 step with the transform and the quantisation of each product's
+// input done by the GEMV itself (launch_igemv_q), and the Wo / W2 products
+// added with their biases straight into x: five launches per layer.
+int step_int8_fused(pcl_model *m) {
+    hipStream_t s = (hipStream_t)m->stream;
+    const int D = m->d, F = m->df, V = m->v, KD = m->kpd, KF = m->kpf;
+    int *tokpos = m->ints, *out = m->ints + 2;
+    M_HIP(pcl::launch_decode_embed(m->wte, m->wpe, m->x, D, tokpos, s));
+    for (size_t l = 0; l < m->lay.size(); l++) {
+        const Layer &y = m->lay[l];
+        const QLayer &q = m->ql[l];
+        M_HIP(pcl::launch_igemv_q(1, 0, m->x, y.g1, y.b1, D, q.wqkv, KD, q.sqkv, nullptr, m->qkv, 3 * D, s));
+        M_HIP(pcl::launch_decode_attn(m->qkv, y.bqkv, y.kc, y.vc, m->att, D, m->h, m->blk, tokpos, s));
+        M_HIP(pcl::launch_igemv_q(0, 1, m->att, nullptr, nullptr, D, q.wo, KD, q.so, y.bo, m->x, D, s));
+        M_HIP(pcl::launch_igemv_q(1, 0, m->x, y.g2, y.b2, D, q.w1, KD, q.s1, nullptr, m->hh, F, s));
+        M_HIP(pcl::launch_igemv_q(2, 1, m->hh, nullptr, y.bf1, F, q.w2, KF, q.s2, y.bf2, m->x, D, s));
+    }
+    M_HIP(pcl::launch_igemv_q(1, 0, m->x, m->gf, m->bf, D, m->whead, KD, m->shead, nullptr, m->logits, V, s));
+    M_HIP(pcl::launch_decode_argmax(m->logits, V, tokpos, out, m->blk + 1, s));
+    return PCL_OK;
+}
+
+int run_eager(pcl_model *m) {
+    if (m->wmode != PCL_W_INT8) return step(m);
+    return m->kpd <= pcl::IGEMV_Q_MAX_K && m->kpf <= pcl::IGEMV_Q_MAX_K ? step_int8_fused(m)
+                                                                          : step_int8(m);
+}
 
 // Quantise every projection (per output column) and the tied head once.
 int quantize_weights(pcl_model *m) {
