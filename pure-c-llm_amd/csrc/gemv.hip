@@ -744,35 +744,39 @@ __device__ __forceinline__ float gv_sum4(float v, float *red) {
     return red[0] + red[1] + red[2] + red[3];
 }
 
-template <int QX, int EPI>
+// Thread layout: LPR lanes per weight row (16-byte pieces k = 16*lane +
+// 16*LPR*u), 256/LPR row groups of RPL = 2 rows: RPB = 512/LPR rows per block,
+// so shallow products spread over more blocks; UK 16-byte loads per row per
+// batch, chosen so a batch spans the whole row when it is short.
+template <int QX, int EPI, int LPR, int UK>
 __global__ __launch_bounds__(GV_THREADS) void igemv_q_kernel(
     const float *__restrict__ X, const float *__restrict__ g, const float *__restrict__ b, int K,
     const int8_t *__restrict__ B, long ldb, const float *__restrict__ sb,
     const float *__restrict__ bias, float *__restrict__ Y, int N) {
     static_assert(GV_THREADS == 256, "the reductions assume four waves");
+    constexpr int RPL = 2, RG = GV_THREADS / LPR, RPB = RG * RPL;
     extern __shared__ __attribute__((aligned(16))) unsigned char gv_dyn[];
     const int Kp = (int)ldb;
     float *xf = reinterpret_cast<float *>(gv_dyn);          // [Kp]
     int8_t *xs = reinterpret_cast<int8_t *>(xf + Kp);        // [Kp]
     __shared__ float red[4], mred[4];
-    __shared__ int32_t res[SGT_ROWS];
+    __shared__ int32_t res[RPB];
 
     const int tid = threadIdx.x;
-    const int j = tid & 15, rs = tid >> 4;
-    const int n0 = blockIdx.x * SGT_ROWS;
+    const int j = tid % LPR, rs = tid / LPR;
+    const int n0 = blockIdx.x * RPB;
     const int klen = min(Kp, (K + 15) & ~15);
-    const int8_t *brow[SGT_RPL];
+    const int8_t *brow[RPL];
 #pragma unroll
-    for (int r = 0; r < SGT_RPL; r++) brow[r] = B + (long)min(n0 + rs + 16 * r, N - 1) * ldb;
-    constexpr int UK = 4;
-    auto load_batch = [&](v4i (&w)[UK][SGT_RPL], int k0) {
+    for (int r = 0; r < RPL; r++) brow[r] = B + (long)min(n0 + rs + RG * r, N - 1) * ldb;
+    auto load_batch = [&](v4i (&w)[UK][RPL], int k0) {
 #pragma unroll
         for (int u = 0; u < UK; u++)
 #pragma unroll
-            for (int r = 0; r < SGT_RPL; r++)
-                w[u][r] = *reinterpret_cast<const v4i *>(brow[r] + min(k0 + 256 * u, klen - 16));
+            for (int r = 0; r < RPL; r++)
+                w[u][r] = *reinterpret_cast<const v4i *>(brow[r] + min(k0 + 16 * LPR * u, klen - 16));
     };
-    v4i wn[UK][SGT_RPL];
+    v4i wn[UK][RPL];
     load_batch(wn, 16 * j);  // in flight while the row is made
 
     if constexpr (QX == QX_LN) {
@@ -806,21 +810,21 @@ __global__ __launch_bounds__(GV_THREADS) void igemv_q_kernel(
     for (int k = tid; k < Kp; k += 256) xs[k] = (int8_t)(k < K ? quant_q(xf[k], inv) : 0);
     __syncthreads();
 
-    int32_t acc[SGT_RPL] = {};
-    for (int k0 = 16 * j; k0 < klen; k0 += 256 * UK) {
-        v4i w[UK][SGT_RPL];
+    int32_t acc[RPL] = {};
+    for (int k0 = 16 * j; k0 < klen; k0 += 16 * LPR * UK) {
+        v4i w[UK][RPL];
 #pragma unroll
         for (int u = 0; u < UK; u++)
 #pragma unroll
-            for (int r = 0; r < SGT_RPL; r++) w[u][r] = wn[u][r];
-        if (k0 + 256 * UK < klen) load_batch(wn, k0 + 256 * UK);
+            for (int r = 0; r < RPL; r++) w[u][r] = wn[u][r];
+        if (k0 + 16 * LPR * UK < klen) load_batch(wn, k0 + 16 * LPR * UK);
 #pragma unroll
         for (int u = 0; u < UK; u++) {
-            const int k = k0 + 256 * u;
+            const int k = k0 + 16 * LPR * u;
             if (k < klen) {
                 const v4i xv = *reinterpret_cast<const v4i *>(&xs[k]);
 #pragma unroll
-                for (int r = 0; r < SGT_RPL; r++) {
+                for (int r = 0; r < RPL; r++) {
                     int a = acc[r];
                     a = __builtin_amdgcn_sdot4(xv[0], w[u][r][0], a, false);
                     a = __builtin_amdgcn_sdot4(xv[1], w[u][r][1], a, false);
@@ -832,16 +836,14 @@ __global__ __launch_bounds__(GV_THREADS) void igemv_q_kernel(
         }
     }
 #pragma unroll
-    for (int r = 0; r < SGT_RPL; r++) {
+    for (int r = 0; r < RPL; r++) {
         int v = acc[r];
-        v += __shfl_xor(v, 8, 16);
-        v += __shfl_xor(v, 4, 16);
-        v += __shfl_xor(v, 2, 16);
-        v += __shfl_xor(v, 1, 16);
-        if (j == 0) res[rs + 16 * r] = v;
+#pragma unroll
+        for (int o = LPR / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, LPR);
+        if (j == 0) res[rs + RG * r] = v;
     }
     __syncthreads();
-    if (tid < SGT_ROWS) {
+    if (tid < RPB) {
         const int n = n0 + tid;
         if (n < N) {
             const float dq = scale * sb[n];
@@ -852,6 +854,23 @@ __global__ __launch_bounds__(GV_THREADS) void igemv_q_kernel(
     }
 }
 
+template <int QX, int EPI>
+static void launch_igemv_q_shape(const float *X, const float *g, const float *b, int K,
+                                 const int8_t *B, int Kp, const float *sb, const float *bias,
+                                 float *Y, int N, hipStream_t s) {
+    const size_t lds = (size_t)Kp * (sizeof(float) + 1);
+    const dim3 block(GV_THREADS);
+#define IGQ(LPRV, UKV)                                                                       \
+    hipLaunchKernelGGL((igemv_q_kernel<QX, EPI, LPRV, UKV>), dim3((unsigned)cdiv(N, 512 / LPRV)), \
+                       block, lds, s, X, g, b, K, B, (long)Kp, sb, bias, Y, N)
+    if (Kp <= 256) IGQ(16, 1);
+    else if (Kp <= 512) IGQ(32, 1);
+    else if (Kp <= 1024) IGQ(64, 1);
+    else if (Kp <= 2048) IGQ(64, 2);
+    else IGQ(64, 4);
+#undef IGQ
+}
+
 hipError_t launch_igemv_q(int qx, int epi, const float *X, const float *g, const float *b, int K,
                           const int8_t *B, int Kp, const float *sb, const float *bias, float *Y,
                           int N, hipStream_t s) {
@@ -859,19 +878,16 @@ hipError_t launch_igemv_q(int qx, int epi, const float *X, const float *g, const
     if ((reinterpret_cast<uintptr_t>(B) & 15) != 0) return hipErrorInvalidValue;
     if ((qx == QX_LN && (!g || !b)) || (qx == QX_BIAS_GELU && !b) || (epi == 1 && !bias))
         return hipErrorInvalidValue;
-    const dim3 grid((unsigned)cdiv(N, SGT_ROWS)), block(GV_THREADS);
-    const size_t lds = (size_t)Kp * (sizeof(float) + 1);
-#define IGQ(QXV, EPIV)                                                                        \
-    hipLaunchKernelGGL((igemv_q_kernel<QXV, EPIV>), grid, block, lds, s, X, g, b, K, B, (long)Kp, \
-                       sb, bias, Y, N)
     if (qx == QX_LN) {
-        if (epi) IGQ(QX_LN, 1); else IGQ(QX_LN, 0);
+        if (epi) launch_igemv_q_shape<QX_LN, 1>(X, g, b, K, B, Kp, sb, bias, Y, N, s);
+        else launch_igemv_q_shape<QX_LN, 0>(X, g, b, K, B, Kp, sb, bias, Y, N, s);
     } else if (qx == QX_BIAS_GELU) {
-        if (epi) IGQ(QX_BIAS_GELU, 1); else IGQ(QX_BIAS_GELU, 0);
+        if (epi) launch_igemv_q_shape<QX_BIAS_GELU, 1>(X, g, b, K, B, Kp, sb, bias, Y, N, s);
+        else launch_igemv_q_shape<QX_BIAS_GELU, 0>(X, g, b, K, B, Kp, sb, bias, Y, N, s);
     } else {
-        if (epi) IGQ(QX_NONE, 1); else IGQ(QX_NONE, 0);
+        if (epi) launch_igemv_q_shape<QX_NONE, 1>(X, g, b, K, B, Kp, sb, bias, Y, N, s);
+        else launch_igemv_q_shape<QX_NONE, 0>(X, g, b, K, B, Kp, sb, bias, Y, N, s);
     }
-#undef IGQ
     return hipGetLastError();
 }
 
