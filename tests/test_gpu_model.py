@@ -14,7 +14,8 @@ suffices). From that position on the logits differ by about one quantisation
 error: a 1-ulp change to one LayerNorm gain of the oracle's own input moves the
 512-wide models by 1-3e-2 normwise after the first such flip, while the INT8
 step itself is 3-5e-2 from the fp32 step. The small models meet INT8_TOL at
-every position; the 16-layer model must start within INT8_TOL and stay within
+every position; the 16-layer model and the one with 8448-wide rows (which also
+takes the unfused INT8 step) must start within INT8_TOL and stay within
 INT8_BAND.
 """
 import numpy as np
@@ -135,9 +136,12 @@ def test_model_errors(tmp_path):
     pcl.lib.pcl_clear_error()
 
 
-@pytest.mark.parametrize("dims,npos", [(SMALL, 32), (MID, 48), (GROWN, 40)])
+WIDE_FF = (16, 64, 4, 8448, 2, 96)        # d_ff rows past 8192 bytes: the unfused INT8 step
+
+
+@pytest.mark.parametrize("dims,npos", [(SMALL, 32), (MID, 48), (GROWN, 40), (WIDE_FF, 16)])
 def test_model_int8_forward_logits(tmp_path, dims, npos):
-    deep = dims == GROWN
+    flip_prone = dims in (GROWN, WIDE_FF)  # 16 layers, or 8448-wide rows: many quantised values
     blk, d, h, df, nl, v = dims
     announce("model int8 forward", dims)
     path = str(tmp_path / "m.ckp1")
@@ -156,7 +160,7 @@ def test_model_int8_forward_logits(tmp_path, dims, npos):
         pcl.lib.pcl_model_free(m)
     print("int8 decode logits, normwise per position:", " ".join(f"{e:.1e}" for e in errs), flush=True)
     assert errs[0] <= INT8_TOL
-    assert max(errs) <= (INT8_BAND if deep else INT8_TOL)
+    assert max(errs) <= (INT8_BAND if flip_prone else INT8_TOL)
 
 
 @pytest.mark.parametrize("dims,n_prompt,n_new", [(SMALL, 5, 27), (GROWN, 8, 56)])
