@@ -1,7 +1,9 @@
 // decode.hip -- the non-GEMV kernels of one KV-cached decode step
-// (generate.c:118-183): token + position embedding, LayerNorm of one row,
-// attention of the new token over the cache (appending its k, v), and a
-// greedy argmax that writes the next token and advances the position.
+// (generate.c:118-183): token + position embedding, attention of the new
+// token over the cache (appending its k, v), the INT8 step's LayerNorm /
+// GELU + quantisation kernels for rows too long for the fused GEMV, and a
+// greedy argmax that writes the next token and advances the position. (The
+// fp32 step's LayerNorm and GELU run inside the GEMVs, gemv.hip.)
 //
 // The token and position live in device memory (tokpos[0], tokpos[1]), so a
 // whole step -- these kernels and the GEMVs between them -- can be captured
@@ -32,25 +34,6 @@ __device__ __forceinline__ float dec_block_sum(float v, float *red) {
     return red[0] + red[1] + red[2] + red[3];
 }
 
-// y = (x - mean) / sqrt(var + 1e-5) * g + b over one row of D (generate.c:106-114:
-// the mean first, then the mean squared deviation); one workgroup.
-__global__ __launch_bounds__(256) void dec_layernorm_kernel(const float *__restrict__ x,
-                                                            const float *__restrict__ g,
-                                                            const float *__restrict__ b,
-                                                            float *__restrict__ y, int D) {
-    __shared__ float red[4];
-    float s = 0.f;
-    for (int i = threadIdx.x; i < D; i += 256) s += x[i];
-    const float mu = dec_block_sum(s, red) / D;
-    float q = 0.f;
-    for (int i = threadIdx.x; i < D; i += 256) {
-        const float d = x[i] - mu;
-        q += d * d;
-    }
-    const float var = dec_block_sum(q, red) / D;
-    const float rs = 1.0f / sqrtf(var + 1e-5f);
-    for (int i = threadIdx.x; i < D; i += 256) y[i] = (x[i] - mu) * rs * g[i] + b[i];
-}
 
 // One head per workgroup (generate.c:130-152): append this position's k, v to
 // the cache, scores s_j = (q . k_j) * scale for j <= pos (the new row from
@@ -187,11 +170,6 @@ hipError_t launch_decode_embed(const float *wte, const float *wpe, float *x, int
                                const int *tokpos, hipStream_t s) {
     hipLaunchKernelGGL(dec_embed_kernel, dim3((D + 255) / 256), dim3(256), 0, s, wte, wpe, x, D,
                        tokpos);
-    return hipGetLastError();
-}
-hipError_t launch_decode_layernorm(const float *x, const float *g, const float *b, float *y, int D,
-                                   hipStream_t s) {
-    hipLaunchKernelGGL(dec_layernorm_kernel, dim3(1), dim3(256), 0, s, x, g, b, y, D);
     return hipGetLastError();
 }
 hipError_t launch_decode_attn(const float *qkv, const float *bqkv, float *kc, float *vc, float *att,

@@ -85,8 +85,6 @@ hipError_t launch_attn_bwd(const float *dO, long ldo, const float *Q, const floa
 // ---- decode step (decode.hip); tokpos = {token, position} in device memory ----
 hipError_t launch_decode_embed(const float *wte, const float *wpe, float *x, int D,
                                const int *tokpos, hipStream_t s);
-hipError_t launch_decode_layernorm(const float *x, const float *g, const float *b, float *y, int D,
-                                   hipStream_t s);
 // dh = D / H must divide 256; the cache holds blk rows of D floats; bqkv
 // (3*D, may be NULL) is added to qkv inside the kernel
 hipError_t launch_decode_attn(const float *qkv, const float *bqkv, float *kc, float *vc, float *att,

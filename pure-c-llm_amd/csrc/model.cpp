@@ -49,7 +49,7 @@ struct pcl_model {
     int *host_tp = nullptr;  // pinned: {token, position} per position, copied to tokpos
     float *wte, *wpe, *gf, *bf;
     std::vector<Layer> lay;
-    float *x, *ln, *qkv, *att, *hh, *hg, *logits;
+    float *x, *qkv, *att, *hh, *logits;
     void *stream = nullptr;
     void *graph = nullptr;
     // INT8 weights (PCL_W_INT8): projections and the tied head quantised once
@@ -262,7 +262,7 @@ int load(pcl_model *m, const char *path) {
     // device layout: weights (QKV joined), KV caches, per-token state
     const long per_layer_dev = 2 * D + (3 * D * D + 3 * D) + (D * D + D) + 2 * D + (D * F + F) +
                                (F * D + D) + 2 * BLK * D;
-    const long state = D + D + 3 * D + D + F + F + V;
+    const long state = D + 3 * D + D + F + V;  // x, qkv, att, hh, logits
     const long total = V * D + BLK * D + m->nl * per_layer_dev + 2 * D + state;
     std::vector<float> h((size_t)total);
     const float *src = w.data();
@@ -327,11 +327,9 @@ int load(pcl_model *m, const char *path) {
     }
     float *sp = a + o_state;
     m->x = sp, sp += D;
-    m->ln = sp, sp += D;
     m->qkv = sp, sp += 3 * D;
     m->att = sp, sp += D;
     m->hh = sp, sp += F;
-    m->hg = sp, sp += F;
     m->logits = sp;
     m->stream = pcl_stream_create();
     if (!m->stream) return pcl_last_status();
