@@ -71,6 +71,30 @@ def test_model_forward_logits(tmp_path, dims):
         pcl.lib.pcl_model_free(m)
 
 
+# the cache attention's 64- and 128-wide head variants, both weight modes
+@pytest.mark.parametrize("dims", [(24, 256, 4, 512, 2, 80), (24, 256, 2, 512, 2, 80)])
+@pytest.mark.parametrize("int8", [False, True])
+def test_model_forward_wide_heads(tmp_path, dims, int8):
+    blk, d, h, df, nl, v = dims
+    announce("model forward wide heads", dims, "int8" if int8 else "fp32")
+    path = str(tmp_path / "m.ckp1")
+    ob.write_ckp1(path, blk, d, h, df, nl, v, seed=81)
+    m = _load(path, pcl.W_INT8 if int8 else pcl.W_FP32)
+    om = ob.OracleModel(path, int8=int8)
+    toks = [int(t) % v for t in ob.u8((blk,), 83)]
+    got = np.empty(v, np.float32)
+    errs = []
+    try:
+        for pos in range(blk):
+            pcl.check(pcl.lib.pcl_model_forward(m, toks[pos], pos, pcl.ptr(got)))
+            errs.append(rel(got, om.forward(toks[pos], pos)))
+    finally:
+        om.close()
+        pcl.lib.pcl_model_free(m)
+    print("normwise per position:", " ".join(f"{e:.1e}" for e in errs), flush=True)
+    assert max(errs) <= (INT8_TOL if int8 else FP32_TOL)
+
+
 def _check_greedy(path, prompt, out, v, int8=False, tol=FP32_TOL):
     """Each generated token is an argmax of the oracle's logits for its prefix."""
     om = ob.OracleModel(path, int8=int8)
