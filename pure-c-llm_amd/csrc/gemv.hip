@@ -178,12 +178,11 @@ __global__ void sgemv_reduce_kernel(const float *__restrict__ part, int splits, 
 // rg = tid/(CW/4)) owns columns 4*c4..4*c4+3 and a contiguous run of
 // kchunk/RG rows (RG = row groups per block). Narrow strips (CW = 16) give
 // enough blocks without splitting K when N is small.
-template <int MR, bool VEC, bool XONES, int CW, int XF = XF_NONE>
+template <int MR, bool VEC, bool XONES, int CW>
 __global__ __launch_bounds__(GV_THREADS) void sgemv_n_kernel(
     const float *__restrict__ X, long ldx, const float *__restrict__ W, long ldw,
     const float *__restrict__ bias, float *__restrict__ Y, long ldy, int M, int N, int K,
-    int kchunk, int splits, float *__restrict__ part, int accumulate,
-    const float *__restrict__ xg = nullptr, const float *__restrict__ xb = nullptr) {
+    int kchunk, int splits, float *__restrict__ part, int accumulate) {
     constexpr int CQ = CW / 4;             // threads across a strip row
     constexpr int RG = GV_THREADS / CQ;    // row groups
     __shared__ float red[RG][MR][CW];
@@ -226,7 +225,6 @@ __global__ __launch_bounds__(GV_THREADS) void sgemv_n_kernel(
     if (!XONES) {
         stage_rows<MR, false>(xs, kchunk, kchunk, min(kchunk, K - kb), M, X + kb, ldx);
         __syncthreads();
-        if constexpr (XF != XF_NONE) gv_xform<XF>(xs, min(kchunk, K - kb), kb, K, X, xg, xb);
     }
 
     float acc[MR][4];
@@ -669,60 +667,42 @@ hipError_t launch_sgemv(const GemvPlan &p, int w_trans, int M, int N, int K, con
     return hipGetLastError();
 }
 
-// One row (M = 1) with an input transform; same plans and kernels as
-// launch_sgemv.
+// One row (M = 1) with an input transform, over N x K weights (sgemv_t's
+// plans and kernel).
 template <int XF>
-static void launch_sgemv_xf_t(const GemvPlan &p, int w_trans, bool vec, int N, int K,
-                              const float *X, const float *W, long ldw, const float *g,
-                              const float *b, const float *bias, int accumulate, float *Y,
-                              const Workspace &ws, hipStream_t s) {
+static void launch_sgemv_xf_t(const GemvPlan &p, bool vec, int N, int K, const float *X,
+                              const float *W, long ldw, const float *g, const float *b,
+                              const float *bias, int accumulate, float *Y, const Workspace &ws,
+                              hipStream_t s) {
     dim3 grid(p.strips, p.splits), block(GV_THREADS);
     float *part = (float *)ws.buf;
     const size_t xsb = (size_t)p.kchunk * sizeof(float);
     const long ldx = K, ldy = N;
-    if (w_trans) {
-        if (vec)
-            hipLaunchKernelGGL((sgemv_t_kernel<1, true, XF>), grid, block, xsb, s, X, ldx, W, ldw, bias, Y,
-                               ldy, 1, N, K, p.kchunk, p.splits, part, accumulate, g, b);
-        else
-            hipLaunchKernelGGL((sgemv_t_kernel<1, false, XF>), grid, block, xsb, s, X, ldx, W, ldw, bias, Y,
-                               ldy, 1, N, K, p.kchunk, p.splits, part, accumulate, g, b);
-    } else if (p.cw == 16) {
-        if (vec)
-            hipLaunchKernelGGL((sgemv_n_kernel<1, true, false, 16, XF>), grid, block, xsb, s, X, ldx, W, ldw,
-                               bias, Y, ldy, 1, N, K, p.kchunk, p.splits, part, accumulate, g, b);
-        else
-            hipLaunchKernelGGL((sgemv_n_kernel<1, false, false, 16, XF>), grid, block, xsb, s, X, ldx, W,
-                               ldw, bias, Y, ldy, 1, N, K, p.kchunk, p.splits, part, accumulate, g, b);
-    } else {
-        if (vec)
-            hipLaunchKernelGGL((sgemv_n_kernel<1, true, false, 64, XF>), grid, block, xsb, s, X, ldx, W, ldw,
-                               bias, Y, ldy, 1, N, K, p.kchunk, p.splits, part, accumulate, g, b);
-        else
-            hipLaunchKernelGGL((sgemv_n_kernel<1, false, false, 64, XF>), grid, block, xsb, s, X, ldx, W,
-                               ldw, bias, Y, ldy, 1, N, K, p.kchunk, p.splits, part, accumulate, g, b);
-    }
-    if (p.splits > 1) {
-        const int nround = p.strips * (w_trans ? SGT_ROWS : p.cw);
+    if (vec)
+        hipLaunchKernelGGL((sgemv_t_kernel<1, true, XF>), grid, block, xsb, s, X, ldx, W, ldw, bias, Y,
+                           ldy, 1, N, K, p.kchunk, p.splits, part, accumulate, g, b);
+    else
+        hipLaunchKernelGGL((sgemv_t_kernel<1, false, XF>), grid, block, xsb, s, X, ldx, W, ldw, bias, Y,
+                           ldy, 1, N, K, p.kchunk, p.splits, part, accumulate, g, b);
+    if (p.splits > 1)
         hipLaunchKernelGGL(sgemv_reduce_kernel, dim3(reduce_grid(1, N)), dim3(256), 0, s, part,
-                           p.splits, 1, N, nround, bias, Y, ldy, accumulate);
-    }
+                           p.splits, 1, N, p.strips * SGT_ROWS, bias, Y, ldy, accumulate);
 }
 
-hipError_t launch_sgemv_xf(const GemvPlan &p, int w_trans, int xf, int N, int K, const float *X,
+hipError_t launch_sgemv_xf(const GemvPlan &p, int xf, int N, int K, const float *X,
                            const float *W, long ldw, const float *g, const float *b,
                            const float *bias, int accumulate, float *Y, const Workspace &ws,
                            hipStream_t stream) {
     if (N <= 0 || K <= 0) return hipErrorInvalidValue;
     if (xf == XF_LN && (!g || !b)) return hipErrorInvalidValue;
     if (p.splits > 1 && (ws.buf == nullptr || ws.bytes_cap < p.part_bytes)) return hipErrorInvalidValue;
-    const bool vec = aligned16(W) && ldw % 4 == 0 && (w_trans ? K % 4 == 0 : N % 4 == 0);
+    const bool vec = aligned16(W) && ldw % 4 == 0 && K % 4 == 0;
     if (xf == XF_LN)
-        launch_sgemv_xf_t<XF_LN>(p, w_trans, vec, N, K, X, W, ldw, g, b, bias, accumulate, Y, ws, stream);
+        launch_sgemv_xf_t<XF_LN>(p, vec, N, K, X, W, ldw, g, b, bias, accumulate, Y, ws, stream);
     else if (xf == XF_GELU)
-        launch_sgemv_xf_t<XF_GELU>(p, w_trans, vec, N, K, X, W, ldw, g, b, bias, accumulate, Y, ws, stream);
+        launch_sgemv_xf_t<XF_GELU>(p, vec, N, K, X, W, ldw, g, b, bias, accumulate, Y, ws, stream);
     else
-        launch_sgemv_xf_t<XF_NONE>(p, w_trans, vec, N, K, X, W, ldw, g, b, bias, accumulate, Y, ws, stream);
+        launch_sgemv_xf_t<XF_NONE>(p, vec, N, K, X, W, ldw, g, b, bias, accumulate, Y, ws, stream);
     return hipGetLastError();
 }
 
@@ -889,6 +869,132 @@ hipError_t launch_igemv_q(int qx, int epi, const float *X, const float *g, const
     } else {
         if (epi) launch_igemv_q_shape<QX_NONE, 1>(X, g, b, K, B, Kp, sb, bias, Y, N, s);
         else launch_igemv_q_shape<QX_NONE, 0>(X, g, b, K, B, Kp, sb, bias, Y, N, s);
+    }
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------ decode fp32 row ----
+// The fp32 twin of igemv_q_kernel: one activation row through the same input
+// transform (staged in LDS), times fp32 weights stored N x K (a row per output,
+// 16-byte loads along K), + bias; EPI 0: Y[n] = s + bias[n]; EPI 1: Y[n] =
+// Y[n] + (s + bias[n]). LPR lanes per weight row, RPL = 2 rows per lane group.
+template <int QX, int EPI, int LPR, int UK>
+__global__ __launch_bounds__(GV_THREADS) void sgemv_q_kernel(
+    const float *__restrict__ X, const float *__restrict__ g, const float *__restrict__ b, int K,
+    const float *__restrict__ W, long ldw, const float *__restrict__ bias, float *__restrict__ Y,
+    int N) {
+    static_assert(GV_THREADS == 256, "the reductions assume four waves");
+    constexpr int RPL = 2, RG = GV_THREADS / LPR, RPB = RG * RPL;
+    extern __shared__ __attribute__((aligned(16))) unsigned char gv_dyn[];
+    float *xf = reinterpret_cast<float *>(gv_dyn);  // [K]
+    __shared__ float red[4], res[RPB];
+
+    const int tid = threadIdx.x;
+    const int j = tid % LPR, rs = tid / LPR;
+    const int n0 = blockIdx.x * RPB;
+    const float *wrow[RPL];
+#pragma unroll
+    for (int r = 0; r < RPL; r++) wrow[r] = W + (long)min(n0 + rs + RG * r, N - 1) * ldw;
+    auto load_batch = [&](v4f (&w)[UK][RPL], int k0) {
+#pragma unroll
+        for (int u = 0; u < UK; u++)
+#pragma unroll
+            for (int r = 0; r < RPL; r++)
+                w[u][r] = *reinterpret_cast<const v4f *>(wrow[r] + min(k0 + 4 * LPR * u, K - 4));
+    };
+    v4f wn[UK][RPL];
+    load_batch(wn, 4 * j);  // in flight while the row is made
+
+    if constexpr (QX == QX_LN) {
+        float s0 = 0.f;
+        for (int i = tid; i < K; i += 256) s0 += X[i];
+        const float mu = gv_sum4(s0, red) / K;
+        float q = 0.f;
+        for (int i = tid; i < K; i += 256) {
+            const float d = X[i] - mu;
+            q += d * d;
+        }
+        const float var = gv_sum4(q, red) / K;
+        const float rsd = 1.0f / sqrtf(var + 1e-5f);
+        for (int i = tid; i < K; i += 256) xf[i] = (X[i] - mu) * rsd * g[i] + b[i];
+    } else if constexpr (QX == QX_BIAS_GELU) {
+        for (int i = tid; i < K; i += 256) {
+            const float v = X[i] + b[i];
+            xf[i] = 0.5f * v * (1.0f + tanhf(0.7978845608028654f * (v + 0.044715f * v * v * v)));
+        }
+    } else {
+        for (int i = tid; i < K; i += 256) xf[i] = X[i];
+    }
+    __syncthreads();
+
+    float acc[RPL] = {};
+    for (int k0 = 4 * j; k0 < K; k0 += 4 * LPR * UK) {
+        v4f w[UK][RPL];
+#pragma unroll
+        for (int u = 0; u < UK; u++)
+#pragma unroll
+            for (int r = 0; r < RPL; r++) w[u][r] = wn[u][r];
+        if (k0 + 4 * LPR * UK < K) load_batch(wn, k0 + 4 * LPR * UK);
+#pragma unroll
+        for (int u = 0; u < UK; u++) {
+            const int k = k0 + 4 * LPR * u;
+            if (k < K) {
+                const v4f xv = *reinterpret_cast<const v4f *>(&xf[k]);
+#pragma unroll
+                for (int r = 0; r < RPL; r++)
+                    acc[r] += xv[0] * w[u][r][0] + xv[1] * w[u][r][1] + xv[2] * w[u][r][2] +
+                              xv[3] * w[u][r][3];
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < RPL; r++) {
+        float v = acc[r];
+#pragma unroll
+        for (int o = LPR / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, LPR);
+        if (j == 0) res[rs + RG * r] = v;
+    }
+    __syncthreads();
+    if (tid < RPB) {
+        const int n = n0 + tid;
+        if (n < N) {
+            const float y = res[tid] + (bias ? bias[n] : 0.f);
+            if (EPI == 1) Y[n] = Y[n] + y;
+            else Y[n] = y;
+        }
+    }
+}
+
+template <int QX, int EPI>
+static void launch_sgemv_q_shape(const float *X, const float *g, const float *b, int K,
+                                 const float *W, const float *bias, float *Y, int N, hipStream_t s) {
+    const size_t lds = (size_t)K * sizeof(float);
+    const dim3 block(GV_THREADS);
+#define SGQ(LPRV, UKV)                                                                       \
+    hipLaunchKernelGGL((sgemv_q_kernel<QX, EPI, LPRV, UKV>), dim3((unsigned)cdiv(N, 512 / LPRV)), \
+                       block, lds, s, X, g, b, K, W, (long)K, bias, Y, N)
+    if (K <= 64) SGQ(16, 1);
+    else if (K <= 128) SGQ(32, 1);
+    else if (K <= 256) SGQ(64, 1);
+    else if (K <= 512) SGQ(64, 2);
+    else SGQ(64, 4);
+#undef SGQ
+}
+
+hipError_t launch_sgemv_q(int qx, int epi, const float *X, const float *g, const float *b, int K,
+                          const float *W, const float *bias, float *Y, int N, hipStream_t s) {
+    if (N <= 0 || K <= 0 || K % 4 != 0 || K > SGEMV_Q_MAX_K) return hipErrorInvalidValue;
+    if ((reinterpret_cast<uintptr_t>(W) & 15) != 0) return hipErrorInvalidValue;
+    if ((qx == QX_LN && (!g || !b)) || (qx == QX_BIAS_GELU && !b)) return hipErrorInvalidValue;
+    if (qx == QX_LN) {
+        if (epi) launch_sgemv_q_shape<QX_LN, 1>(X, g, b, K, W, bias, Y, N, s);
+        else launch_sgemv_q_shape<QX_LN, 0>(X, g, b, K, W, bias, Y, N, s);
+    } else if (qx == QX_BIAS_GELU) {
+        if (epi) launch_sgemv_q_shape<QX_BIAS_GELU, 1>(X, g, b, K, W, bias, Y, N, s);
+        else launch_sgemv_q_shape<QX_BIAS_GELU, 0>(X, g, b, K, W, bias, Y, N, s);
+    } else {
+        if (epi) launch_sgemv_q_shape<QX_NONE, 1>(X, g, b, K, W, bias, Y, N, s);
+        else launch_sgemv_q_shape<QX_NONE, 0>(X, g, b, K, W, bias, Y, N, s);
     }
     return hipGetLastError();
 }

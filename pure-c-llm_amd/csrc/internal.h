@@ -114,7 +114,7 @@ hipError_t launch_ce_loss(const double *row_loss, int M, int rows, float *loss, 
 int shim_error(int status, const char *msg);
 int shim_init();
 // launch_sgemv_xf on the stream's workspace (status as the C-ABI calls)
-int sgemv_xf(int w_trans, int xf, int N, int K, const float *X, const float *W, int ldw,
+int sgemv_xf(int xf, int N, int K, const float *X, const float *W, int ldw,
              const float *g, const float *b, const float *bias, int accumulate, float *Y,
              void *stream);
 
@@ -131,9 +131,9 @@ hipError_t launch_sgemv(const GemvPlan &p, int w_trans, int M, int N, int K, con
                         hipStream_t stream);
 // One activation row (M = 1, X of K floats, Y of N floats) through a transform
 // applied as the row is staged: xf 0 none, 1 LayerNorm over the row (g, b of
-// K floats; generate.c:106-114), 2 tanh-GELU; then the GEMV of launch_sgemv
-// (plan from plan_sgemv(w_trans, 1, N, K)).
-hipError_t launch_sgemv_xf(const GemvPlan &p, int w_trans, int xf, int N, int K, const float *X,
+// K floats; generate.c:106-114), 2 tanh-GELU; then the N x K-weight GEMV of
+// launch_sgemv (plan from plan_sgemv(1, 1, N, K)).
+hipError_t launch_sgemv_xf(const GemvPlan &p, int xf, int N, int K, const float *X,
                            const float *W, long ldw, const float *g, const float *b,
                            const float *bias, int accumulate, float *Y, const Workspace &ws,
                            hipStream_t stream);
@@ -145,6 +145,12 @@ constexpr int IGEMV_Q_MAX_K = 8192;
 hipError_t launch_igemv_q(int qx, int epi, const float *X, const float *g, const float *b, int K,
                           const int8_t *B, int Kp, const float *sb, const float *bias, float *Y,
                           int N, hipStream_t s);
+// Its fp32 twin over weights stored N x K (rows of K floats, K % 4 == 0,
+// 16-byte aligned, K <= SGEMV_Q_MAX_K): same transforms; epi 0: Y = s + bias,
+// epi 1: Y += s + bias (bias may be NULL).
+constexpr int SGEMV_Q_MAX_K = 16384;
+hipError_t launch_sgemv_q(int qx, int epi, const float *X, const float *g, const float *b, int K,
+                          const float *W, const float *bias, float *Y, int N, hipStream_t s);
 // INT8 GEMV over the packed layout (ldb = Kp); out_mode as in launch_igemm.
 hipError_t launch_igemv(const GemvPlan &p, int out_mode, int M, int N, int K, const uint8_t *X,
                         long ldx, const int8_t *Bpk, long ldb, const int32_t *col_off,

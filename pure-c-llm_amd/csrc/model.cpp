@@ -80,21 +80,36 @@ namespace {
         if (s_ != PCL_OK) return s_; \
     } while (0)
 
+// The fp32 step over the N x K projections. Each product is one sgemv_q
+// launch that makes its input row (LayerNorm, or bias + GELU) and, for Wo and
+// W2, adds product + bias into x: five launches per layer. Dims the kernel
+// does not take (K % 4 != 0 or beyond its LDS row) use the transposed-weight
+// GEMV with the same transforms instead.
 int step(pcl_model *m) {
     hipStream_t s = (hipStream_t)m->stream;
     const int D = m->d, F = m->df, V = m->v;
     int *tokpos = m->ints, *out = m->ints + 2;
     M_HIP(pcl::launch_decode_embed(m->wte, m->wpe, m->x, D, tokpos, s));
-    // LayerNorm and GELU are applied by the GEMV that consumes them, as it
-    // stages its activation row (XF 1 / 2), so a layer is five launches
+    const bool fused = D % 4 == 0 && F % 4 == 0 && D <= pcl::SGEMV_Q_MAX_K && F <= pcl::SGEMV_Q_MAX_K;
     for (const Layer &y : m->lay) {
-        M_OK(pcl::sgemv_xf(0, 1, 3 * D, D, m->x, y.wqkv, 3 * D, y.g1, y.b1, y.bqkv, 0, m->qkv, s));
-        M_HIP(pcl::launch_decode_attn(m->qkv, nullptr, y.kc, y.vc, m->att, D, m->h, m->blk, tokpos, s));
-        M_OK(pcl_sgemv(PCL_OP_N, 1, D, D, m->att, D, y.wo, D, y.bo, 1, m->x, D, s));
-        M_OK(pcl::sgemv_xf(0, 1, F, D, m->x, y.w1, F, y.g2, y.b2, y.bf1, 0, m->hh, s));
-        M_OK(pcl::sgemv_xf(0, 2, D, F, m->hh, y.w2, D, nullptr, nullptr, y.bf2, 1, m->x, s));
+        if (fused) {
+            M_HIP(pcl::launch_sgemv_q(1, 0, m->x, y.g1, y.b1, D, y.wqkv, y.bqkv, m->qkv, 3 * D, s));
+            M_HIP(pcl::launch_decode_attn(m->qkv, nullptr, y.kc, y.vc, m->att, D, m->h, m->blk, tokpos, s));
+            M_HIP(pcl::launch_sgemv_q(0, 1, m->att, nullptr, nullptr, D, y.wo, y.bo, m->x, D, s));
+            M_HIP(pcl::launch_sgemv_q(1, 0, m->x, y.g2, y.b2, D, y.w1, nullptr, m->hh, F, s));
+            M_HIP(pcl::launch_sgemv_q(2, 1, m->hh, nullptr, y.bf1, F, y.w2, y.bf2, m->x, D, s));
+        } else {
+            M_OK(pcl::sgemv_xf(1, 3 * D, D, m->x, y.wqkv, D, y.g1, y.b1, y.bqkv, 0, m->qkv, s));
+            M_HIP(pcl::launch_decode_attn(m->qkv, nullptr, y.kc, y.vc, m->att, D, m->h, m->blk, tokpos, s));
+            M_OK(pcl::sgemv_xf(0, D, D, m->att, y.wo, D, nullptr, nullptr, y.bo, 1, m->x, s));
+            M_OK(pcl::sgemv_xf(1, F, D, m->x, y.w1, D, y.g2, y.b2, y.bf1, 0, m->hh, s));
+            M_OK(pcl::sgemv_xf(2, D, F, m->hh, y.w2, F, nullptr, nullptr, y.bf2, 1, m->x, s));
+        }
     }
-    M_OK(pcl::sgemv_xf(1, 1, V, D, m->x, m->wte, D, m->gf, m->bf, nullptr, 0, m->logits, s));
+    if (fused)
+        M_HIP(pcl::launch_sgemv_q(1, 0, m->x, m->gf, m->bf, D, m->wte, nullptr, m->logits, V, s));
+    else
+        M_OK(pcl::sgemv_xf(1, V, D, m->x, m->wte, D, m->gf, m->bf, nullptr, 0, m->logits, s));
     M_HIP(pcl::launch_decode_argmax(m->logits, V, tokpos, out, m->blk + 1, s));
     return PCL_OK;
 }
@@ -223,7 +238,10 @@ int set_tokpos(pcl_model *m, int tok, int pos) {
     return PCL_OK;
 }
 
-int load(pcl_model *m, const char *path) {
+// nk: store the projections N x K (a row of K floats per output), the layout
+// the fp32 decode GEMVs read; otherwise K x N as in the file (the INT8
+// quantiser's input).
+int load(pcl_model *m, const char *path, bool nk) {
     FILE *f = fopen(path, "rb");
     if (!f) return fail(PCL_ERR_INVALID_ARG, "pcl_model_load: cannot open the checkpoint");
     std::vector<float> w;
@@ -287,16 +305,30 @@ int load(pcl_model *m, const char *path) {
         y.bqkv = at;
         at += 3 * D;
         for (int part = 0; part < 3; part++) {
-            for (long k = 0; k < D; k++)
-                memcpy(dst + y.wqkv + k * 3 * D + part * D, src + k * D, sizeof(float) * D);
+            if (nk) {  // rows part*D + c of the joined matrix's transpose
+                for (long k = 0; k < D; k++)
+                    for (long c = 0; c < D; c++) dst[y.wqkv + (part * D + c) * D + k] = src[k * D + c];
+            } else {
+                for (long k = 0; k < D; k++)
+                    memcpy(dst + y.wqkv + k * 3 * D + part * D, src + k * D, sizeof(float) * D);
+            }
             src += D * D;
             memcpy(dst + y.bqkv + part * D, src, sizeof(float) * D);
             src += D;
         }
-        y.wo = take(D * D), y.bo = take(D);
+        auto take_w = [&](long K, long N) {  // a K x N matrix, transposed when nk
+            if (!nk) return take(K * N);
+            const long o = at;
+            for (long k = 0; k < K; k++)
+                for (long n = 0; n < N; n++) dst[o + n * K + k] = src[k * N + n];
+            src += K * N;
+            at += K * N;
+            return o;
+        };
+        y.wo = take_w(D, D), y.bo = take(D);
         y.g2 = take(D), y.b2 = take(D);
-        y.w1 = take(D * F), y.bf1 = take(F);
-        y.w2 = take(F * D), y.bf2 = take(D);
+        y.w1 = take_w(D, F), y.bf1 = take(F);
+        y.w2 = take_w(F, D), y.bf2 = take(D);
         y.kc = at;
         at += BLK * D;
         y.vc = at;
@@ -386,7 +418,8 @@ pcl_model *pcl_model_load_ex(const char *path, int weights) {
     }
     if (pcl::shim_init() != PCL_OK) return nullptr;
     pcl_model *m = new pcl_model();
-    if (load(m, path) != PCL_OK || (weights == PCL_W_INT8 && quantize_weights(m) != PCL_OK)) {
+    if (load(m, path, weights == PCL_W_FP32) != PCL_OK ||
+        (weights == PCL_W_INT8 && quantize_weights(m) != PCL_OK)) {
         const int st = pcl_last_status();
         char msg[512];
         snprintf(msg, sizeof msg, "%s", pcl_last_error());

@@ -222,15 +222,15 @@ int sync_current() {
 namespace pcl {
 int shim_error(int status, const char *msg) { return set_error(status, "%s", msg); }
 int shim_init() { return do_init(); }
-int sgemv_xf(int w_trans, int xf, int N, int K, const float *X, const float *W, int ldw,
+int sgemv_xf(int xf, int N, int K, const float *X, const float *W, int ldw,
              const float *g, const float *b, const float *bias, int accumulate, float *Y,
              void *stream) {
     PCL_OK_OR_RETURN(do_init());
     hipStream_t s = pick(stream);
-    const GemvPlan p = plan_sgemv(w_trans, 1, N, K);
+    const GemvPlan p = plan_sgemv(1, 1, N, K);
     StreamScratch *sc;
     PCL_OK_OR_RETURN(get_scratch(s, p.part_bytes, 0, &sc));
-    HIP_OK(launch_sgemv_xf(p, w_trans, xf, N, K, X, W, ldw, g, b, bias, accumulate, Y, sc->ws, s));
+    HIP_OK(launch_sgemv_xf(p, xf, N, K, X, W, ldw, g, b, bias, accumulate, Y, sc->ws, s));
     return PCL_OK;
 }
 }  // namespace pcl

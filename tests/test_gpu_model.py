@@ -49,7 +49,10 @@ def _load(path, weights=None):
     return m
 
 
-@pytest.mark.parametrize("dims", [SMALL, MID])
+ODD_FF = (16, 64, 4, 130, 2, 40)          # d_ff % 4 != 0: the fp32 step's transposed-GEMV path
+
+
+@pytest.mark.parametrize("dims", [SMALL, MID, ODD_FF])
 def test_model_forward_logits(tmp_path, dims):
     blk, d, h, df, nl, v = dims
     announce("model forward", dims)
