@@ -93,6 +93,32 @@ def test_igemv_i32_exact(M):
         np.testing.assert_array_equal(igemm_i32(Au, Bq, gemv=True), ob.gemm_u8s8_i32(Au, Bq))
 
 
+@pytest.mark.parametrize("M", [4, 5, 8])
+def test_igemv_wide_exact(M):
+    # several activation rows against a wide N: the 350M head, a K that is a
+    # multiple of 16 but not of 32, and a short K
+    for N, K in ((50257, 1024), (9000, 1040), (8192, 256)):
+        Au = ob.u8((M, K), 130 + M)
+        Bq = ob.s8((K, N), 131 + N)
+        announce("igemv wide i32", M, N, K)
+        np.testing.assert_array_equal(igemm_i32(Au, Bq, gemv=True), ob.gemm_u8s8_i32(Au, Bq))
+
+
+def test_igemv_wide_dequant_bit_exact():
+    M, N, K = 8, 9000, 1024
+    Au = ob.u8((M, K), 140)
+    Bq = ob.s8((K, N), 141)
+    sa = ob.uniform((M,), 142, 1e-3, 1e-2)
+    sb = ob.uniform((N,), 143, 1e-3, 1e-2)
+    off = ob.s8((N,), 144).astype(np.int32) * 1000
+    V = exact(Au, Bq).astype(np.int32)
+    announce("igemv wide dq", M, N, K)
+    np.testing.assert_array_equal(_dq_run(Au, Bq, sa, sb), ob.dequant(V, sa, sb))
+    np.testing.assert_array_equal(_dq_run(Au, Bq, None, sb), ob.dequant(V, None, sb))
+    np.testing.assert_array_equal(_dq_run(Au, Bq, None, sb, off),
+                                  ob.dequant((V + off).astype(np.int32), None, sb))
+
+
 @pytest.mark.parametrize("M,K,ldx", [(3, 130, 144), (8, 2050, 2064), (5, 61, 64)])
 def test_igemv_padded_rows(M, K, ldx):
     # 16-byte aligned activation rows whose K is not a multiple of 16: the
