@@ -164,6 +164,25 @@ def head_ce(pcl, lib, M, D, V, chunk_bytes, warmup, steps):
     return out
 
 
+def _write_ckp1(path, blk, d, h, df, nl, v, seed, wstd=0.02):
+    """A CKP1 checkpoint (train.c:633-648: int[8] header, then the tensors in
+    registration order) of synthetic weights: gains 1 + N(0, 0.1), biases
+    N(0, 0.02), matrices N(0, wstd), embeddings N(0, 0.1)."""
+    import numpy as np
+
+    rng = np.random.default_rng(seed)
+    kinds = [("e", v * d), ("e", blk * d)]
+    for _ in range(nl):
+        kinds += [("g", d), ("b", d)] + [("w", d * d), ("b", d)] * 4 + \
+                 [("g", d), ("b", d), ("w", d * df), ("b", df), ("w", df * d), ("b", d)]
+    kinds += [("g", d), ("b", d)]
+    with open(path, "wb") as f:
+        f.write(np.array([0x434B5031, blk, d, h, df, nl, v, 0], "<i4").tobytes())
+        for kind, n in kinds:
+            mean, std = {"g": (1.0, 0.1), "b": (0.0, 0.02), "w": (0.0, wstd), "e": (0.0, 0.1)}[kind]
+            f.write(rng.normal(mean, std, n).astype("<f4").tobytes())
+
+
 def decode_e2e(pcl, dims=(256, 512, 16, 2048, 16, 2048), n_new=255, ref_tokens=24, modes=(0, 1)):
     """Greedy decoding of a synthetic CKP1 checkpoint of the grown model
     (block 256, d 512, 16 heads, d_ff 2048, 16 layers, vocab 2048): one prompt
@@ -175,13 +194,10 @@ def decode_e2e(pcl, dims=(256, 512, 16, 2048, 16, 2048), n_new=255, ref_tokens=2
 
     import numpy as np
 
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import binding as ob
-
     blk, d, h, df, nl, v = dims
     tmp = tempfile.mkdtemp(prefix="pcl_ckp1_")
     path = os.path.join(tmp, "grown.ckp1")
-    ob.write_ckp1(path, blk, d, h, df, nl, v, seed=77, wstd=0.05)
+    _write_ckp1(path, blk, d, h, df, nl, v, seed=77, wstd=0.05)
     out = {"model": f"block {blk}, d_model {d}, heads {h}, d_ff {df}, layers {nl}, vocab {v}",
            "weights_MB": round(4.0 * (v * d + blk * d + nl * (4 * d * d + 2 * d * df)) / 1e6, 1)}
     for weights, wtag in ((pcl.W_FP32, ""), (pcl.W_INT8, "int8_")):
@@ -203,7 +219,11 @@ def decode_e2e(pcl, dims=(256, 512, 16, 2048, 16, 2048), n_new=255, ref_tokens=2
                 out[f"{tag}_ms_per_token"] = round(1e3 * dt / n_new, 4)
         finally:
             pcl.lib.pcl_model_free(m)
-    gen = ob.ref("libref_generate.so") if ref_tokens > 0 else None
+    gen = None
+    if ref_tokens > 0:  # the CPU reference leg
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import binding as ob
+        gen = ob.ref("libref_generate.so")
     if gen is not None:
         gen.pcl_ref_gen_load(path.encode())
         logits = np.empty(v, np.float32)
@@ -310,6 +330,44 @@ def cpu_model():
     except OSError:
         pass
     return "unknown"
+
+
+def cpu_next_rows():
+    """The oracle's restatements of the reference functions behind the "next"
+    rows, timed on the host beside their GPU numbers (kind "port": train.c is
+    built here only at small compile-time dims): the tied head + cross-entropy
+    forward and backward (train.c:412-465, OpenMP over rows / vocabulary as in
+    train.c) on 4 token rows of the 350M shape, and causal attention forward
+    and backward (train.c:339-407, one thread) on one sequence-head of it."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import numpy as np
+
+    import binding as ob
+
+    out = {"kind": "port", "omp_threads": os.environ.get("OMP_NUM_THREADS", "default")}
+    M, D, V = 4, 1024, 50257
+    x = ob.normal((M, D), 501, 0.0, 1.0)
+    w = ob.normal((V, D), 502, 0.0, 0.05)
+    t = (np.arange(M) * 7919 % V).astype(np.int32)
+    t0 = time.perf_counter()
+    ob.head_ce(x, w, t)
+    dt = time.perf_counter() - t0
+    out["head_ce_350m"] = {"sample": f"{M} of the 4096 token rows (D 1024, V 50257), forward + backward",
+                           "ms_per_row": round(1e3 * dt / M, 2),
+                           "ms_4096_rows_scaled": round(1e3 * dt / M * 4096, 1)}
+    T, dh = 1024, 64
+    q, k, v = (ob.normal((T, dh), 510 + i, 0.0, 1.0) for i in range(3))
+    t0 = time.perf_counter()
+    att, probs = ob.attention_forward(q, k, v, 1, T, 1, dh)
+    t1 = time.perf_counter()
+    ob.attention_backward(ob.normal((T, dh), 513, 0.0, 1.0), q, k, v, probs, 1, T, 1, dh)
+    t2 = time.perf_counter()
+    out["attn_350m"] = {"sample": "1 of the 64 sequence-heads (T 1024, d_head 64)",
+                        "fwd_ms_per_head": round(1e3 * (t1 - t0), 2),
+                        "bwd_ms_per_head": round(1e3 * (t2 - t1), 2),
+                        "fwd_ms_64_heads_scaled": round(1e3 * (t1 - t0) * 64, 1),
+                        "bwd_ms_64_heads_scaled": round(1e3 * (t2 - t1) * 64, 1)}
+    return out
 
 
 def cpu_ladder():
@@ -486,6 +544,7 @@ def main():
         out["cpu_baseline"] = cpu_baseline(M, N, K)
         if not args.primary_only:
             out.setdefault("extra", {})["cpu_reference_fp32"] = cpu_ladder()
+            out["extra"]["cpu_port_next_rows"] = cpu_next_rows()
     print(json.dumps(out), flush=True)
 
 
