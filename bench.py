@@ -7,9 +7,12 @@ quoted on (gemm_bench INT8, M=N=K=2048, u8 x s8 ->
 int32, per-row x per-column dequant to fp32). One step = one pass of the hot
 path over the batch = one pcl_gemm_u8s8_dq call with inputs resident in HBM.
 The other configurations (FP32 1024^3, 350M-class GEMMs in both dtypes and
-backward layouts, grown-model prefill, decode GEMV sweeps) are reported under
-"extra". Timing loops run in C (libpcl_bench.so) between HIP events recorded
-on the stream the kernels are launched on.
+backward layouts, grown-model prefill, decode GEMV sweeps) and the rows built
+around the path (causal attention, fused epilogues, the CKP1 decode engine, the
+tied head with cross-entropy) are reported under "extra", with CPU timings of
+the reference (built from source) or of the oracle's restatement beside them.
+Timing loops run in C (libpcl_bench.so) between HIP events recorded on the
+stream the kernels are launched on.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--primary-only] [--case NAME]
 """
