@@ -3,7 +3,8 @@
 //   p[v] = expf(l[v] - max) * (1 / sum_v expf(l[v] - max)),
 //   loss_m = -log((double)p[t] + 1e-30),  dl[v] = (p[v] - [v == t]) / M.
 //
-// One workgroup per row, two passes over the row in HBM: the first keeps a
+// One workgroup per row, two passes over the row in HBM (16-byte accesses over
+// the row's aligned middle): the first keeps a
 // running (max, sum) per thread (the sum rescaled whenever the max grows), the
 // second writes dl. dl may alias the logits (each element is read before the
 // same thread overwrites it). Row losses go to a double array; a second kernel
@@ -46,22 +47,47 @@ __global__ __launch_bounds__(CE_NT) void ce_rows_kernel(const float *logits, lon
                                                         const int *__restrict__ targets, float *dl,
                                                         long ldd, int V, int pad, float rows,
                                                         double *__restrict__ row_loss) {
+    typedef float v4f_t __attribute__((ext_vector_type(4)));
     __shared__ float sm_m[CE_NT / 64], sm_s[CE_NT / 64];
     const int tid = threadIdx.x, row = blockIdx.x;
     const float *x = logits + (long)row * ld;
+    float *o = dl + (long)row * ldd;
+    // Rows are read (and written) as 16-byte vectors between a scalar head (up
+    // to the first 16-byte boundary) and a scalar tail, when the dlogits row
+    // has the same alignment as the logits row; otherwise element by element.
+    const bool vec = ((reinterpret_cast<uintptr_t>(x) ^ reinterpret_cast<uintptr_t>(o)) & 15) == 0;
+    const int head = vec ? min(V, (int)((16 - (reinterpret_cast<uintptr_t>(x) & 15)) & 15) / 4) : V;
+    const int nv = vec ? (V - head) / 4 : 0;
+    const int tail0 = head + 4 * nv;
+    const v4f_t *x4 = reinterpret_cast<const v4f_t *>(x + head);
     float m = -INFINITY, s = 0.f;
-    int v = tid;
-    for (; v + 3 * CE_NT < V; v += 4 * CE_NT) {
-        const float x0 = x[v], x1 = x[v + CE_NT], x2 = x[v + 2 * CE_NT], x3 = x[v + 3 * CE_NT];
-        ce_push(m, s, x0);
-        ce_push(m, s, x1);
-        ce_push(m, s, x2);
-        ce_push(m, s, x3);
+    if (vec) {
+        if (tid < head) ce_push(m, s, x[tid]);
+        int c = tid;
+        for (; c + CE_NT < nv; c += 2 * CE_NT) {
+            const v4f_t a = x4[c], b = x4[c + CE_NT];
+            ce_push(m, s, a[0]), ce_push(m, s, a[1]), ce_push(m, s, a[2]), ce_push(m, s, a[3]);
+            ce_push(m, s, b[0]), ce_push(m, s, b[1]), ce_push(m, s, b[2]), ce_push(m, s, b[3]);
+        }
+        for (; c < nv; c += CE_NT) {
+            const v4f_t a = x4[c];
+            ce_push(m, s, a[0]), ce_push(m, s, a[1]), ce_push(m, s, a[2]), ce_push(m, s, a[3]);
+        }
+        for (int v = tail0 + tid; v < V; v += CE_NT) ce_push(m, s, x[v]);
+    } else {
+        int v = tid;
+        for (; v + 3 * CE_NT < V; v += 4 * CE_NT) {
+            const float x0 = x[v], x1 = x[v + CE_NT], x2 = x[v + 2 * CE_NT], x3 = x[v + 3 * CE_NT];
+            ce_push(m, s, x0);
+            ce_push(m, s, x1);
+            ce_push(m, s, x2);
+            ce_push(m, s, x3);
+        }
+        for (; v < V; v += CE_NT) ce_push(m, s, x[v]);
     }
-    for (; v < V; v += CE_NT) ce_push(m, s, x[v]);
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float m2 = __shfl_xor(m, o), s2 = __shfl_xor(s, o);
+    for (int sh = 32; sh > 0; sh >>= 1) {
+        const float m2 = __shfl_xor(m, sh), s2 = __shfl_xor(s, sh);
         ce_merge(m, s, m2, s2);
     }
     if ((tid & 63) == 0) sm_m[tid >> 6] = m, sm_s[tid >> 6] = s;
@@ -72,8 +98,25 @@ __global__ __launch_bounds__(CE_NT) void ce_rows_kernel(const float *logits, lon
     const float inv = 1.0f / s;
     const int t = targets[row];
     if (tid == 0 && (t < 0 || t >= V)) row_loss[row] = __longlong_as_double(0x7ff8000000000000LL);
-    float *o = dl + (long)row * ldd;
-    v = tid;
+    // p = expf(x - m) * inv; dl = (p - [v == t]) / rows; the target's loss term
+    auto one = [&](int v, float xv) {
+        const float p = expf(xv - m) * inv;
+        if (v == t) row_loss[row] = -log((double)p + 1e-30);
+        return (p - (v == t ? 1.0f : 0.0f)) / rows;
+    };
+    if (vec) {
+        if (tid < head) o[tid] = one(tid, x[tid]);
+        v4f_t *o4 = reinterpret_cast<v4f_t *>(o + head);
+        for (int c = tid; c < nv; c += CE_NT) {
+            const v4f_t a = x4[c];
+            const int v0 = head + 4 * c;
+            o4[c] = v4f_t{one(v0, a[0]), one(v0 + 1, a[1]), one(v0 + 2, a[2]), one(v0 + 3, a[3])};
+        }
+        for (int v = tail0 + tid; v < V; v += CE_NT) o[v] = one(v, x[v]);
+        for (int v = V + tid; v < pad; v += CE_NT) o[v] = 0.f;
+        return;
+    }
+    int v = tid;
     for (; v + 3 * CE_NT < V; v += 4 * CE_NT) {
         float p[4];
 #pragma unroll
