@@ -50,9 +50,10 @@ def _ce64(lg, t):
 def _check_ce(loss, dl, lg, t):
     want_loss, want_dl = ob.cross_entropy(lg, t)
     loss64, dl64 = _ce64(lg, t)
-    assert loss == pytest.approx(loss64, rel=LOSS_RTOL)
+    assert loss == pytest.approx(loss64, rel=LOSS_RTOL, abs=1e-7)
     assert rel(dl, dl64) <= FP32_TOL
-    assert loss == pytest.approx(want_loss, rel=LOSS_RTOL + abs(want_loss / loss64 - 1))
+    own = abs(want_loss / loss64 - 1) if loss64 else 0.0  # the oracle's own distance
+    assert loss == pytest.approx(want_loss, rel=LOSS_RTOL + own, abs=1e-7)
     assert rel(dl, want_dl) <= FP32_TOL + rel(want_dl, dl64)
 
 
@@ -77,6 +78,31 @@ def test_cross_entropy_vs_oracle(M, V, ld, inplace):
     lg, t = _inputs(M, V, 1000 + M + V)
     loss, dl = _ce(lg, t, ld, inplace)
     _check_ce(loss, dl, lg, t)
+
+
+@pytest.mark.parametrize("M,V", [(7, 1), (5, 3), (9, 5)])
+def test_cross_entropy_tiny_vocab(M, V):
+    # rows shorter than one 16-byte alignment head (V = 1: p = 1, loss 0, dl 0)
+    lg, t = _inputs(M, V, 1050 + V)
+    loss, dl = _ce(lg, t)
+    _check_ce(loss, dl, lg, t)
+    if V == 1:
+        assert loss == 0.0 and not dl.any()
+
+
+def test_cross_entropy_mixed_alignment():
+    # logits rows of 1001 floats, dlogits rows of 1000: the two rows' 16-byte
+    # phases differ, so the element-by-element path runs
+    M, V = 40, 997
+    lg, t = _inputs(M, V, 1060)
+    host = np.zeros((M, 1001), np.float32)
+    host[:, :V] = lg
+    dlg, dt = pcl.dev(host), pcl.dev(t)
+    dd = pcl.dev(np.full((M, 1000), np.nan, np.float32))
+    dloss = pcl.dev(np.zeros(1, np.float32))
+    pcl.check(pcl.lib.pcl_cross_entropy(dlg.ptr, 1001, dt.ptr, dd.ptr, 1000, M, V, dloss.ptr, None))
+    pcl.sync()
+    _check_ce(float(dloss.download((1,), np.float32)[0]), dd.download((M, 1000), np.float32)[:, :V], lg, t)
 
 
 def test_cross_entropy_extreme_rows():
