@@ -115,7 +115,10 @@ def _check_greedy(path, prompt, out, v, int8=False, tol=FP32_TOL):
     assert worst <= tol
 
 
-@pytest.mark.parametrize("dims,n_prompt,n_new", [(SMALL, 5, 27), (MID, 1, 48), (GROWN, 8, 56)])
+# (SMALL, 6, 27) fills the cache exactly (6 + 27 - 1 = block 32); (SMALL, 4, 0)
+# runs the prompt only
+@pytest.mark.parametrize("dims,n_prompt,n_new", [(SMALL, 5, 27), (SMALL, 6, 27), (SMALL, 4, 0),
+                                                 (MID, 1, 48), (GROWN, 8, 56)])
 @pytest.mark.parametrize("graph", [0, 1])
 def test_model_generate_greedy(tmp_path, dims, n_prompt, n_new, graph):
     blk, d, h, df, nl, v = dims
