@@ -424,8 +424,8 @@ def main():
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print("bench.py measures one MI355X: this build has no multi-GPU path (each GPU box here has one GPU; "
-              "see DESIGN.md for how the GEMMs would shard). Run with --gpus 1.", file=sys.stderr)
+        print("bench.py measures one MI355X: this build has no multi-GPU path (it runs the per-GPU shard "
+              "of the path on one GPU). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     pcl, lib = load_bench()
