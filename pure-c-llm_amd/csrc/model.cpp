@@ -18,6 +18,7 @@
 
 #include <cstdio>
 #include <cstring>
+#include <new>
 #include <vector>
 
 #include "../../include/pcl_hip.h"
@@ -266,8 +267,31 @@ int load(pcl_model *m, const char *path, bool nk) {
         }
         const long D = m->d, F = m->df;
         const long per_layer = 2 * D + 3 * (D * D + D) + (D * D + D) + 2 * D + (D * F + F) + (F * D + D);
+        // the header's float count must match what the file holds, checked
+        // before anything is sized from it (a corrupt n_layers would
+        // otherwise ask for an arbitrary allocation)
+        long file_floats = -1;
+        const long here = ftell(f);
+        if (here >= 0 && fseek(f, 0, SEEK_END) == 0) {
+            const long end = ftell(f);
+            if (end >= here) file_floats = (end - here) / (long)sizeof(float);
+            if (fseek(f, here, SEEK_SET) != 0) file_floats = -1;
+        }
+        if (m->nl > (1 << 20) || file_floats < 0) {
+            st = fail(PCL_ERR_INVALID_ARG, "pcl_model_load: unreadable checkpoint size");
+            break;
+        }
         const long n = (long)m->v * D + (long)m->blk * D + m->nl * per_layer + 2 * D;
-        w.resize((size_t)n);
+        if (n > file_floats) {
+            st = fail(PCL_ERR_INVALID_ARG, "pcl_model_load: short read in the checkpoint");
+            break;
+        }
+        try {
+            w.resize((size_t)n);
+        } catch (const std::bad_alloc &) {
+            st = fail(PCL_ERR_OOM, "pcl_model_load: out of host memory");
+            break;
+        }
         if (fread(w.data(), sizeof(float), (size_t)n, f) != (size_t)n) {
             st = fail(PCL_ERR_INVALID_ARG, "pcl_model_load: short read in the checkpoint");
             break;
@@ -417,9 +441,19 @@ pcl_model *pcl_model_load_ex(const char *path, int weights) {
         return nullptr;
     }
     if (pcl::shim_init() != PCL_OK) return nullptr;
-    pcl_model *m = new pcl_model();
-    if (load(m, path, weights == PCL_W_FP32) != PCL_OK ||
-        (weights == PCL_W_INT8 && quantize_weights(m) != PCL_OK)) {
+    pcl_model *m = new (std::nothrow) pcl_model();
+    if (!m) {
+        fail(PCL_ERR_OOM, "pcl_model_load: out of host memory");
+        return nullptr;
+    }
+    int lst;
+    try {  // host staging vectors: no exception crosses the C ABI
+        lst = load(m, path, weights == PCL_W_FP32);
+        if (lst == PCL_OK && weights == PCL_W_INT8) lst = quantize_weights(m);
+    } catch (const std::bad_alloc &) {
+        lst = fail(PCL_ERR_OOM, "pcl_model_load: out of host memory");
+    }
+    if (lst != PCL_OK) {
         const int st = pcl_last_status();
         char msg[512];
         snprintf(msg, sizeof msg, "%s", pcl_last_error());
@@ -455,9 +489,11 @@ int pcl_model_generate(pcl_model *m, const int *prompt, int n_prompt, int n_new,
                        int use_graph) {
     if (!m || !prompt || (n_new > 0 && !out))
         return fail(PCL_ERR_INVALID_ARG, "pcl_model_generate: NULL argument");
-    if (n_prompt < 1 || n_new < 0 || (long)n_prompt + n_new - 1 > m->blk)
+    // Positions fed: 0 .. n_prompt-1 for the prompt, then n_prompt .. n_prompt+n_new-2;
+    // each must be below block (cache rows, wpe rows, pinned token slots).
+    if (n_prompt < 1 || n_new < 0 || n_prompt > m->blk || (long)n_prompt + n_new - 1 > m->blk)
         return fail(PCL_ERR_INVALID_ARG,
-                    "pcl_model_generate: need 1 <= n_prompt and n_prompt + n_new - 1 <= block");
+                    "pcl_model_generate: need 1 <= n_prompt <= block and n_prompt + n_new - 1 <= block");
     for (int i = 0; i < n_prompt; i++)
         if (prompt[i] < 0 || prompt[i] >= m->v)
             return fail(PCL_ERR_INVALID_ARG, "pcl_model_generate: prompt token out of range");

@@ -23,6 +23,13 @@
 
 namespace {
 
+// Byte ranges [a, a+na) and [b, b+nb) share memory.
+bool ranges_overlap(const void *a, size_t na, const void *b, size_t nb) {
+    const uintptr_t x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
+    return x < y + nb && y < x + na;
+}
+
+
 // ----------------------------------------------------------- error state ----
 thread_local int t_status = PCL_OK;
 thread_local char t_msg[512] = "";
@@ -487,6 +494,17 @@ int pcl_sgemm_ex(int opA, int opB, int M, int N, int K, const float *A, int lda,
               "pcl_sgemm_ex: the epilogue needs aux_in");
     CHECK_ARG((aux_in == nullptr && aux_out == nullptr) || ld_aux >= N,
               "pcl_sgemm_ex: ld_aux=%d < N=%d", ld_aux, N);
+    // The epilogue operands may not share memory with C: depending on the
+    // kernel chosen for the shape, C is written before the epilogue reads
+    // aux_in (e.g. an in-place residual would add v twice).
+    {
+        const size_t nc = sizeof(float) * ((size_t)(M - 1) * ldc + N);
+        const size_t na = sizeof(float) * ((size_t)(M - 1) * (size_t)(ld_aux > 0 ? ld_aux : N) + N);
+        CHECK_ARG(!aux_in || !ranges_overlap(aux_in, na, C, nc),
+                  "pcl_sgemm_ex: aux_in overlaps C (write the product to another buffer)");
+        CHECK_ARG(!aux_out || epilogue != PCL_EPI_GELU || !ranges_overlap(aux_out, na, C, nc),
+                  "pcl_sgemm_ex: aux_out overlaps C");
+    }
     PCL_OK_OR_RETURN(do_init());
     hipStream_t s = pick(stream);
     pcl::SgemmPlan p = pcl::plan_sgemm(M, N, K);
@@ -764,6 +782,10 @@ static int need_attn_dims(const char *who) {
     if (g_d_model <= 0 || g_attn_heads <= 0 || g_attn_batch <= 0)
         return set_error(PCL_ERR_UNSET_DIMS,
                          "%s: call pcl_set_model_dims and pcl_set_attn_dims first", who);
+    // the head size is d_model / n_heads; a remainder would leave columns unread
+    if (g_d_model % g_attn_heads != 0)
+        return set_error(PCL_ERR_INVALID_ARG, "%s: d_model %d is not a multiple of n_heads %d", who,
+                         g_d_model, g_attn_heads);
     return PCL_OK;
 }
 
@@ -1050,11 +1072,6 @@ void gemm_int8_kernel(const uint8_t *Au, int Kpad, const int8_t *Bp, const int32
 }
 
 // ------------------------------------------------------ cross-entropy ----
-static bool ranges_overlap(const void *a, size_t na, const void *b, size_t nb) {
-    const uintptr_t x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
-    return x < y + nb && y < x + na;
-}
-
 int pcl_cross_entropy(const float *logits, int ld, const int *targets, float *dlogits, int ldd,
                       int M, int V, float *loss, void *stream) {
     CHECK_ARG(M >= 0 && V > 0, "pcl_cross_entropy: bad dims (M=%d V=%d)", M, V);

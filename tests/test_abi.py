@@ -82,6 +82,43 @@ def test_argument_errors_before_device_work():
     assert L.pcl_s8_packed_bytes(100, 3) == 3 * 256
 
 
+def test_sgemm_ex_rejects_epilogue_operands_aliasing_c():
+    """An epilogue operand sharing memory with C is refused before any device
+    work: with the unfused path C is written before aux_in is read, so an
+    in-place residual would add the product twice. (The pointers are never
+    dereferenced: the check precedes every device call.)"""
+    L = pcl.lib
+    base, M, N, K = 1 << 20, 64, 64, 64
+    A, B, C = base, base + (1 << 16), base + (1 << 17)
+    EPI_RESID, EPI_GELU = 2, 1
+    # aux_in == C, and aux_in starting inside C's last row
+    for aux in (C, C + 4 * ((M - 1) * N + 8)):
+        L.pcl_clear_error()
+        assert L.pcl_sgemm_ex(0, 0, M, N, K, A, K, B, N, None, EPI_RESID, aux, None, N, C, N, None) == \
+            pcl.PCL_ERR_INVALID_ARG
+        assert b"overlaps C" in L.pcl_last_error()
+    # the GELU pre-activation output may not overlap C either
+    L.pcl_clear_error()
+    assert L.pcl_sgemm_ex(0, 0, M, N, K, A, K, B, N, None, EPI_GELU, None, C + 256, N, C, N, None) == \
+        pcl.PCL_ERR_INVALID_ARG
+    L.pcl_clear_error()
+
+
+def test_attention_dims_must_split_into_heads():
+    """d_model must be a multiple of n_heads for the device attention drop-ins
+    (otherwise the last d_model % n_heads columns would be silently ignored)."""
+    L = pcl.lib
+    try:
+        assert L.pcl_set_model_dims(1028, 10) == pcl.PCL_OK
+        assert L.pcl_set_attn_dims(1, 4, 16) == pcl.PCL_OK
+        L.pcl_clear_error()
+        L.attn_fwd(None, None, None, None, None)
+        assert L.pcl_last_status() == pcl.PCL_ERR_INVALID_ARG
+        assert b"multiple of n_heads" in L.pcl_last_error()
+    finally:
+        L.pcl_clear_error()
+
+
 def test_no_device_fails_loudly():
     if pcl.lib.pcl_init() == pcl.PCL_OK:
         pytest.skip("a GPU is present on this host")

@@ -161,6 +161,13 @@ def test_model_errors(tmp_path):
         prompt = np.zeros(4, np.int32)
         out = np.zeros(8, np.int32)
         assert pcl.lib.pcl_model_generate(m, pcl.ptr(prompt), 4, 6, pcl.ptr(out), 0) == pcl.PCL_ERR_INVALID_ARG
+        # a prompt one longer than the block, with nothing generated: its last
+        # position would be the block itself (rejected before any launch)
+        long_prompt = np.zeros(9, np.int32)
+        assert pcl.lib.pcl_model_generate(m, pcl.ptr(long_prompt), 9, 0, pcl.ptr(out), 0) == \
+            pcl.PCL_ERR_INVALID_ARG
+        # the longest prompt that fits, prompt-only: accepted
+        assert pcl.lib.pcl_model_generate(m, pcl.ptr(long_prompt), 8, 0, pcl.ptr(out), 0) == pcl.PCL_OK
     finally:
         pcl.lib.pcl_model_free(m)
     pcl.lib.pcl_clear_error()
