@@ -247,6 +247,17 @@ int pcl_vec_add(float *C, const float *A, const float *B, long n, void *stream);
 int pcl_sgemv(int opW, int M, int N, int K, const float *X, int ldx, const float *W, int ldw,
               const float *bias, int accumulate, float *Y, int ldy, void *stream);
 
+/* pcl_sgemv without any allocation. No counterpart in the reference: it is for
+ * callers that cannot allocate (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). Same arguments, kernels and results
+ * as pcl_sgemv; the split-K partial sums go to a static 4 MiB device array held
+ * by each GPU until the process ends, instead of a per-stream workspace.
+ * Shapes needing more scratch than that fail with PCL_ERR_RANGE before any
+ * launch. Every call on one GPU shares that array: calls that overlap on one
+ * GPU (e.g. on two streams) race and must be ordered by the caller. */
+int pcl_sgemv_noalloc(int opW, int M, int N, int K, const float *X, int ldx, const float *W,
+                      int ldw, const float *bias, int accumulate, float *Y, int ldy, void *stream);
+
 /* db(N) += colsum(dY) (gpu_kernels.cu:102-108), fixed m order per column. */
 int pcl_bias_bwd(float *db, const float *dY, int M, int N, int ld, void *stream);
 

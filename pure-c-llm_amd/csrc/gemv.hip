@@ -1060,4 +1060,17 @@ hipError_t launch_igemv(const GemvPlan &p, int out_mode, int M, int N, int K, co
     return hipGetLastError();
 }
 
+// ---------------------------------------------- allocation-free scratch ----
+// The split-K partial sums of pcl_sgemv_noalloc live in this file-scope device
+// array: one copy per GPU, held until the process ends, shared by every such
+// call on that GPU (calls that overlap on one GPU race on it). In host code
+// the name `scratch` is only a host-side stand-in for the symbol; its device
+// address comes from hipGetSymbolAddress (gemv_noalloc_scratch), once per
+// device, and only that address is ever handed to a kernel.
+static __device__ __align__(256) unsigned char scratch[GEMV_NOALLOC_SCRATCH_BYTES];
+
+hipError_t gemv_noalloc_scratch(void **dev_ptr) {
+    return hipGetSymbolAddress(dev_ptr, HIP_SYMBOL(scratch));
+}
+
 }  // namespace pcl

@@ -120,6 +120,10 @@ int sgemv_xf(int xf, int N, int K, const float *X, const float *W, int ldw,
 
 // ---- GEMV (gemv.hip) ----
 GemvPlan plan_sgemv(int w_trans, int M, int N, int K);
+// Size of the static split-K scratch of the allocation-free GEMV entry point,
+// and its device address on the current device (hipGetSymbolAddress).
+constexpr size_t GEMV_NOALLOC_SCRATCH_BYTES = (size_t)4 << 20;
+hipError_t gemv_noalloc_scratch(void **dev_ptr);
 // Column sums of a K x N matrix (bias_bwd): plan for launch_sgemv with x_ones.
 GemvPlan plan_bias_bwd(int N, int K);
 GemvPlan plan_igemv(int M, int N, int K);

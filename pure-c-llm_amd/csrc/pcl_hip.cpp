@@ -83,6 +83,8 @@ bool g_inited = false;
 int g_init_status = PCL_OK;
 char g_init_msg[256] = "";
 
+void resolve_noalloc_at_init(int dev);
+
 int do_init() {
     std::lock_guard<std::mutex> lk(g_mu);
     if (g_inited) {
@@ -113,6 +115,7 @@ int do_init() {
                  "libpcl_hip is built for gfx950 only; device 0 is %s", prop.gcnArchName);
         return set_error(g_init_status, "%s", g_init_msg);
     }
+    resolve_noalloc_at_init(dev);
     return PCL_OK;
 }
 
@@ -163,6 +166,36 @@ int get_scratch(hipStream_t s, size_t part_bytes, size_t aux_bytes, StreamScratc
     }
     *out = &sc;
     return PCL_OK;
+}
+
+// Device address of the static GEMV scratch (gemv.hip), per device, resolved
+// once with that device current: by the library's init for its device, else
+// by the first pcl_sgemv_noalloc call on another device.
+constexpr int NOALLOC_MAX_DEVICES = 64;
+void *g_noalloc_ptr[NOALLOC_MAX_DEVICES] = {};
+std::mutex g_noalloc_mu;
+
+int noalloc_scratch(int dev, void **out) {
+    if (dev < 0 || dev >= NOALLOC_MAX_DEVICES)
+        return set_error(PCL_ERR_RANGE, "device %d beyond the static scratch table", dev);
+    std::lock_guard<std::mutex> lk(g_noalloc_mu);
+    if (!g_noalloc_ptr[dev]) {
+        void *p = nullptr;
+        const hipError_t e = pcl::gemv_noalloc_scratch(&p);
+        if (e != hipSuccess || !p)
+            return set_error(PCL_ERR_HIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+        g_noalloc_ptr[dev] = p;
+    }
+    *out = g_noalloc_ptr[dev];
+    return PCL_OK;
+}
+
+void resolve_noalloc_at_init(int dev) {
+    if (dev < 0 || dev >= NOALLOC_MAX_DEVICES) return;
+    std::lock_guard<std::mutex> lk(g_noalloc_mu);
+    void *p = nullptr;
+    if (pcl::gemv_noalloc_scratch(&p) == hipSuccess && p) g_noalloc_ptr[dev] = p;
+    else (void)hipGetLastError();  // not fatal here: the entry point retries and reports it
 }
 
 hipStream_t pick(void *stream) { return stream ? (hipStream_t)stream : t_stream; }
@@ -443,6 +476,43 @@ int pcl_sgemv(int opW, int M, int N, int K, const float *X, int ldx, const float
     PCL_OK_OR_RETURN(get_scratch(s, p.part_bytes, 0, &sc));
     HIP_OK(pcl::launch_sgemv(p, opW == PCL_OP_T, M, N, K, X, ldx, false, W, ldw, bias, accumulate,
                              Y, ldy, sc->ws, s));
+    return PCL_OK;
+}
+
+// pcl_sgemv with its split-K partial sums in the static device scratch of
+// gemv.hip instead of the per-stream workspace: no allocation of any kind.
+// Same kernels, plan and summation order as pcl_sgemv, so the results are
+// identical.
+int pcl_sgemv_noalloc(int opW, int M, int N, int K, const float *X, int ldx, const float *W,
+                      int ldw, const float *bias, int accumulate, float *Y, int ldy, void *stream) {
+    CHECK_ARG(M >= 0 && N >= 0 && K >= 0, "pcl_sgemv_noalloc: negative dimension (M=%d N=%d K=%d)",
+              M, N, K);
+    CHECK_ARG(M <= 8, "pcl_sgemv_noalloc: M=%d exceeds the decode limit of 8 rows", M);
+    CHECK_ARG(opW == PCL_OP_N || opW == PCL_OP_T, "pcl_sgemv_noalloc: bad opW %d", opW);
+    if (M == 0 || N == 0) return PCL_OK;
+    CHECK_ARG(Y != nullptr, "pcl_sgemv_noalloc: Y is NULL");
+    CHECK_ARG(ldy >= N, "pcl_sgemv_noalloc: ldy=%d < N=%d", ldy, N);
+    if (K > 0) {
+        CHECK_ARG(X && W, "pcl_sgemv_noalloc: NULL operand");
+        CHECK_ARG(ldx >= K, "pcl_sgemv_noalloc: ldx=%d < K=%d", ldx, K);
+        CHECK_ARG(ldw >= (opW == PCL_OP_N ? N : K), "pcl_sgemv_noalloc: ldw=%d too small", ldw);
+    }
+    PCL_OK_OR_RETURN(do_init());
+    const pcl::GemvPlan p = pcl::plan_sgemv(opW == PCL_OP_T, M, N, K);
+    if (p.part_bytes > pcl::GEMV_NOALLOC_SCRATCH_BYTES)
+        return set_error(PCL_ERR_RANGE,
+                         "pcl_sgemv_noalloc: M=%d N=%d K=%d needs %zu bytes of split-K scratch, "
+                         "beyond the static %zu",
+                         M, N, K, p.part_bytes, pcl::GEMV_NOALLOC_SCRATCH_BYTES);
+    int dev = 0;
+    HIP_OK(hipGetDevice(&dev));
+    void *scr = nullptr;
+    PCL_OK_OR_RETURN(noalloc_scratch(dev, &scr));
+    pcl::Workspace ws;
+    ws.buf = scr;
+    ws.bytes_cap = pcl::GEMV_NOALLOC_SCRATCH_BYTES;
+    HIP_OK(pcl::launch_sgemv(p, opW == PCL_OP_T, M, N, K, X, ldx, false, W, ldw, bias, accumulate,
+                             Y, ldy, ws, pick(stream)));
     return PCL_OK;
 }
 

@@ -100,6 +100,7 @@ _PROTOS = {
     # native
     "pcl_sgemm": (_i, [_i, _i, _i, _i, _i, _vp, _i, _vp, _i, _vp, _i, _vp, _i, _vp]),
     "pcl_sgemv": (_i, [_i, _i, _i, _i, _vp, _i, _vp, _i, _vp, _i, _vp, _i, _vp]),
+    "pcl_sgemv_noalloc": (_i, [_i, _i, _i, _i, _vp, _i, _vp, _i, _vp, _i, _vp, _i, _vp]),
     "pcl_bias_bwd": (_i, [_vp, _vp, _i, _i, _i, _vp]),
     "pcl_sgemm_ex": (_i, [_i, _i, _i, _i, _i, _vp, _i, _vp, _i, _vp, _i, _vp, _vp, _i, _vp, _i, _vp]),
     "pcl_gelu_fwd": (_i, [_vp, _vp, C.c_long, _vp]),
