@@ -47,11 +47,14 @@ def load_bench():
     lib.pcl_bench_sgemm.argtypes = [i, i, i, i, i, i, i, i, C.POINTER(d)]
     lib.pcl_bench_gemv.argtypes = [C.POINTER(i), i, i, C.POINTER(i), C.POINTER(i), i, i, i, i, C.POINTER(d),
                                    C.POINTER(d)]
+    lib.pcl_bench_gemv_group.argtypes = [C.POINTER(i), i, i, C.POINTER(i), C.POINTER(i), i, i, i, C.POINTER(d),
+                                         C.POINTER(d)]
     lib.pcl_bench_attn.argtypes = [i, i, i, i, i, i, i, C.POINTER(d)]
     lib.pcl_bench_attn_bwd.argtypes = [i, i, i, i, i, i, C.POINTER(d)]
     lib.pcl_bench_sgemm_ex.argtypes = [i, i, i, i, i, i, i, i, i, C.POINTER(d)]
     lib.pcl_bench_head_ce.argtypes = [i, i, i, C.c_long, i, i, i, C.POINTER(d)]
-    for f in (lib.pcl_bench_igemm, lib.pcl_bench_sgemm, lib.pcl_bench_gemv, lib.pcl_bench_attn,
+    for f in (lib.pcl_bench_igemm, lib.pcl_bench_sgemm, lib.pcl_bench_gemv, lib.pcl_bench_gemv_group,
+              lib.pcl_bench_attn,
               lib.pcl_bench_attn_bwd, lib.pcl_bench_sgemm_ex, lib.pcl_bench_head_ce):
         f.restype = i
     return pcl, lib
@@ -96,6 +99,22 @@ def gemv(pcl, lib, kind, M, shapes, copies, warmup, steps, graph=False):
     gbs = by.value / (per * 1e-3) / 1e9
     return {"M": M, "ms_per_sweep": round(per, 5), "bytes_per_sweep": int(by.value), "GBps": round(gbs, 1),
             "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "weight_copies": copies, "graph": bool(graph)}
+
+
+def gemv_group(pcl, lib, kind, M, shapes, copies, warmup, steps):
+    """The same sweep as gemv(), every product independent, as one grouped
+    launch per step (pcl_gemv_group_run)."""
+    kinds = kind if isinstance(kind, (list, tuple)) else [kind] * len(shapes)
+    Kd = (C.c_int * len(shapes))(*kinds)
+    Ks = (C.c_int * len(shapes))(*[k for k, _ in shapes])
+    Ns = (C.c_int * len(shapes))(*[n for _, n in shapes])
+    ms, by = C.c_double(0), C.c_double(0)
+    _check(pcl, lib.pcl_bench_gemv_group(Kd, M, len(shapes), Ks, Ns, copies, warmup, steps, C.byref(ms),
+                                         C.byref(by)), f"gemv group kinds {sorted(set(kinds))}")
+    per = ms.value / steps
+    gbs = by.value / (per * 1e-3) / 1e9
+    return {"M": M, "ms_per_sweep": round(per, 5), "bytes_per_sweep": int(by.value), "GBps": round(gbs, 1),
+            "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "weight_copies": copies, "launches_per_sweep": 1}
 
 
 def attn(pcl, lib, B, T, H, dh, with_probs, warmup, steps):
@@ -322,6 +341,14 @@ CASES = {
     "gemv_head_int8_m8": lambda pcl, lib, w, s: gemv(pcl, lib, 2, 8, [(1024, 50257)], 6, w, s),
     "decode_fp32_m1": lambda pcl, lib, w, s: gemv(pcl, lib, [0] * 64 + [1], 1, DECODE_LAYER * 16 + [(512, 2048)],
                                                    3, w, s),
+    "decode_group_fp32_m1": lambda pcl, lib, w, s: gemv_group(pcl, lib, [0] * 64 + [1], 1,
+                                                               DECODE_LAYER * 16 + [(512, 2048)], 3, w, s),
+    "decode_group_fp32_m8": lambda pcl, lib, w, s: gemv_group(pcl, lib, [0] * 64 + [1], 8,
+                                                               DECODE_LAYER * 16 + [(512, 2048)], 3, w, s),
+    "decode_group_int8_m1": lambda pcl, lib, w, s: gemv_group(pcl, lib, 2, 1, DECODE_LAYER * 16 + [(512, 2048)],
+                                                               11, w, s),
+    "decode_group_int8_m8": lambda pcl, lib, w, s: gemv_group(pcl, lib, 2, 8, DECODE_LAYER * 16 + [(512, 2048)],
+                                                               11, w, s),
 }
 
 

@@ -338,6 +338,53 @@ int pcl_gemv_u8s8_dq(const uint8_t *X, int ldx, const int8_t *Bpk, const int32_t
                      const float *sa, const float *sb, float *Y, int ldy, int M, int N, int K,
                      void *stream);
 
+/* ---- grouped decode GEMV: many independent products in one launch ----
+ * Not a reference function: the reference runs its decode products one call
+ * at a time (generate.c:95-107 matvec, three of them on one input for the
+ * separate Wq, Wk, Wv; transformer.c:174-195 proj_token). A group streams
+ * the weights of many independent products together (the projections of one
+ * input, one layer for several sequences, a whole sweep), so short products
+ * do not each pay for a launch. Each product is the single call's product:
+ *   PCL_GEMV_F32_N  Y(M,N) = (accumulate ? Y : 0) + X(M,K)·W + bias, W K x N
+ *                   (pcl_sgemv with PCL_OP_N);
+ *   PCL_GEMV_F32_T  the same with W N x K (pcl_sgemv with PCL_OP_T);
+ *   PCL_GEMV_U8S8   X u8 (+128 offset), W packed s8 (pcl_pack_b_s8; ldw = its
+ *                   row length pcl_s8_kpad(K)): int32 Y when sb is NULL
+ *                   (pcl_gemv_u8s8_i32), else Y = float(v + col_off[n]) *
+ *                   (sa ? sa[m]*sb[n] : sb[n]) (pcl_gemv_u8s8_dq).
+ * FP32 within the 1e-4 bar, INT8 bit-exact, as the single calls. Products must
+ * be independent: no product's Y may share memory with another's X, W or Y. */
+#define PCL_GEMV_F32_N 0
+#define PCL_GEMV_F32_T 1
+#define PCL_GEMV_U8S8 2
+typedef struct pcl_gemv_desc {
+    int kind, M, N, K;
+    const void *X;
+    int ldx;
+    const void *W;
+    int ldw;
+    const float *bias; /* fp32 kinds; may be NULL */
+    int accumulate;    /* fp32 kinds */
+    const int32_t *col_off; /* PCL_GEMV_U8S8; may be NULL */
+    const float *sa, *sb;   /* PCL_GEMV_U8S8 */
+    void *Y;
+    int ldy;
+} pcl_gemv_desc;
+typedef struct pcl_gemv_group pcl_gemv_group;
+/* Validates the n products, plans one launch (each block owns a strip of one
+ * product over its whole K, largest first) and copies the plan to the device:
+ * the group's only allocation. Beyond the single calls it needs 1 <= M <= 8,
+ * K >= 1, 16-byte aligned W with ldw % 4 == 0 and N % 4 == 0 (F32_N) or
+ * K % 4 == 0 (F32_T), packed rows of ldw >= pcl_s8_kpad(K) (U8S8), and staged
+ * activations of at most 64 KB: M' * 4 * K floats for fp32, M' * K bytes for
+ * U8S8, with M' the group's largest M rounded up to 1, 2, 4 or 8 (PCL_ERR_RANGE
+ * otherwise). The descriptors' pointers are kept: the buffers must outlive the
+ * group. */
+int pcl_gemv_group_create(const pcl_gemv_desc *descs, int n, pcl_gemv_group **group);
+/* One launch computing every product of the group (asynchronous on stream). */
+int pcl_gemv_group_run(const pcl_gemv_group *group, void *stream);
+void pcl_gemv_group_free(pcl_gemv_group *group);
+
 /* ---- quantisers (gemm_bench.c:225-259 rules: scale = amax * fl(1/127), the
  * reference's -ffast-math build of amax/127.0f (README.md:104), with amax
  * starting at 1e-8; q = clamp(lroundf(x * (1/scale)), -127, 127)) ---- */

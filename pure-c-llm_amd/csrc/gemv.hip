@@ -1060,6 +1060,301 @@ hipError_t launch_igemv(const GemvPlan &p, int out_mode, int M, int N, int K, co
     return hipGetLastError();
 }
 
+// ------------------------------------------------------- grouped GEMV ----
+// Many independent decode products in one launch (pcl_gemv_group_*). The
+// launch's blocks are a host-built list of (product, strip) work items,
+// largest first, so the weights of every product stream at once instead of
+// one short launch per product. A block owns a strip of outputs over the
+// whole K (no split, no second pass), stages its product's activation rows in
+// LDS while its first weight batch is in flight, and reads every weight byte
+// once with non-temporal 16-byte loads.
+//   GG_F32_N: W K x N (N-contiguous; generate.c:95-107 matvec), 64-column
+//             strips; lane (c4 = lane%16, rr = lane/16) of wave w owns 4
+//             columns and the contiguous run of rows of group 4w + rr; the 16
+//             group sums of a column are added across lanes, then waves, in a
+//             fixed order.
+//   GG_F32_T: W N x K (K-contiguous rows; the tied head, model.c:64-77),
+//             32-row strips: 16 lanes per row, 16-byte pieces k = 4j + 64i.
+//   GG_U8S8:  packed N x Kp s8 rows (the INT8 GEMM's layout), 32-row strips,
+//             exact int32 dot products of the re-centred activations, then
+//             the dequant epilogue of the INT8 GEMM (gemm_bench.c:272-275).
+
+template <int MR>
+__device__ __forceinline__ void gg_f32_n(const GgDesc &d, int strip, float *xs, float (*red)[MR][64]) {
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int c4 = lane & 15, rr = lane >> 4;
+    const int M = d.M, N = d.N, K = d.K, ld = d.xld;
+    const int run = ld >> 4;  // rows per group, a multiple of 8
+    const int n0 = strip * 64, col = n0 + 4 * c4;
+    const int colc = min(col, N - 4);  // N % 4 == 0: clamped lanes feed columns >= N only
+    const float *__restrict__ W = static_cast<const float *>(d.W);
+    const long ldw = d.ldw;
+    const int r0 = (wv * 4 + rr) * run;
+    constexpr int UR = 8;  // rows per load batch
+    // rows past K load row K-1 and are zeroed, so they add exactly nothing
+    auto load_batch = [&](v4f (&w)[UR], int i) {
+#pragma unroll
+        for (int u = 0; u < UR; u++) {
+            const int k = r0 + i + u;
+            v4f v = __builtin_nontemporal_load(reinterpret_cast<const v4f *>(W + (long)min(k, K - 1) * ldw + colc));
+            w[u] = k < K ? v : v4f{0.f, 0.f, 0.f, 0.f};
+        }
+    };
+    v4f wn[UR];
+    load_batch(wn, 0);
+    stage_rows<MR, false>(xs, ld, ld, K, M, static_cast<const float *>(d.X), d.ldx);
+    __syncthreads();
+
+    float acc[MR][4];
+#pragma unroll
+    for (int m = 0; m < MR; m++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[m][j] = 0.f;
+    for (int i = 0; i < run; i += UR) {
+        v4f w[UR];
+#pragma unroll
+        for (int u = 0; u < UR; u++) w[u] = wn[u];
+        if (i + UR < run) load_batch(wn, i + UR);
+#pragma unroll
+        for (int m = 0; m < MR; m++) {
+            const v4f xa = *reinterpret_cast<const v4f *>(&xs[m * ld + r0 + i]);
+            const v4f xb = *reinterpret_cast<const v4f *>(&xs[m * ld + r0 + i + 4]);
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) acc[m][j] += xa[u] * w[u][j];
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) acc[m][j] += xb[u] * w[4 + u][j];
+        }
+    }
+    // groups 4w .. 4w+3 of a column sit in lanes l, l^16, l^32, l^48
+#pragma unroll
+    for (int m = 0; m < MR; m++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            float v = acc[m][j];
+            v += __shfl_xor(v, 16);
+            v += __shfl_xor(v, 32);
+            acc[m][j] = v;
+        }
+    if (rr == 0) {
+#pragma unroll
+        for (int m = 0; m < MR; m++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) red[wv][m][4 * c4 + j] = acc[m][j];
+    }
+    __syncthreads();
+    float *__restrict__ Y = static_cast<float *>(d.Y);
+    for (int o = tid; o < M * 64; o += GV_THREADS) {
+        const int m = o >> 6, c = o & 63, n = n0 + c;
+        if (n < N) {
+            const float sum = ((red[0][m][c] + red[1][m][c]) + red[2][m][c]) + red[3][m][c];
+            const float y = sum + (d.bias ? d.bias[n] : 0.f);
+            float *dst = Y + (long)m * d.ldy + n;
+            *dst = d.accumulate ? *dst + y : y;
+        }
+    }
+}
+
+template <int MR>
+__device__ __forceinline__ void gg_f32_t(const GgDesc &d, int strip, float *xs) {
+    const int tid = threadIdx.x, j = tid & 15, rs = tid >> 4;
+    constexpr int RPL = 2, UK = 4;
+    const int M = d.M, N = d.N, K = d.K, ld = d.xld;
+    const int n0 = strip * 32;
+    const float *__restrict__ W = static_cast<const float *>(d.W);
+    const float *wrow[RPL];
+#pragma unroll
+    for (int r = 0; r < RPL; r++) wrow[r] = W + (long)min(n0 + rs + 16 * r, N - 1) * d.ldw;
+    // K % 4 == 0; k past K is clamped for the load and skipped in the sums
+    auto load_batch = [&](v4f (&w)[UK][RPL], int k0) {
+#pragma unroll
+        for (int u = 0; u < UK; u++)
+#pragma unroll
+            for (int r = 0; r < RPL; r++)
+                w[u][r] = __builtin_nontemporal_load(reinterpret_cast<const v4f *>(wrow[r] + min(k0 + 64 * u, K - 4)));
+    };
+    v4f wn[UK][RPL];
+    load_batch(wn, 4 * j);
+    stage_rows<MR, false>(xs, ld, ld, K, M, static_cast<const float *>(d.X), d.ldx);
+    __syncthreads();
+
+    float acc[RPL][MR];
+#pragma unroll
+    for (int r = 0; r < RPL; r++)
+#pragma unroll
+        for (int m = 0; m < MR; m++) acc[r][m] = 0.f;
+    for (int k0 = 4 * j; k0 < K; k0 += 64 * UK) {
+        v4f w[UK][RPL];
+#pragma unroll
+        for (int u = 0; u < UK; u++)
+#pragma unroll
+            for (int r = 0; r < RPL; r++) w[u][r] = wn[u][r];
+        if (k0 + 64 * UK < K) load_batch(wn, k0 + 64 * UK);
+#pragma unroll
+        for (int u = 0; u < UK; u++) {
+            const int k = k0 + 64 * u;
+            if (k < K) {
+#pragma unroll
+                for (int m = 0; m < MR; m++) {
+                    const v4f xv = *reinterpret_cast<const v4f *>(&xs[m * ld + k]);
+#pragma unroll
+                    for (int r = 0; r < RPL; r++)
+                        acc[r][m] += xv[0] * w[u][r][0] + xv[1] * w[u][r][1] + xv[2] * w[u][r][2] +
+                                     xv[3] * w[u][r][3];
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < RPL; r++)
+#pragma unroll
+        for (int m = 0; m < MR; m++) {
+            float v = acc[r][m];
+            v += __shfl_xor(v, 8, 16);
+            v += __shfl_xor(v, 4, 16);
+            v += __shfl_xor(v, 2, 16);
+            v += __shfl_xor(v, 1, 16);
+            acc[r][m] = v;
+        }
+    if (j == 0) {
+        float *__restrict__ Y = static_cast<float *>(d.Y);
+#pragma unroll
+        for (int r = 0; r < RPL; r++) {
+            const int n = n0 + rs + 16 * r;
+#pragma unroll
+            for (int m = 0; m < MR; m++) {
+                if (m < M && n < N) {
+                    const float y = acc[r][m] + (d.bias ? d.bias[n] : 0.f);
+                    float *dst = Y + (long)m * d.ldy + n;
+                    *dst = d.accumulate ? *dst + y : y;
+                }
+            }
+        }
+    }
+}
+
+template <int MR>
+__device__ __forceinline__ void gg_u8s8(const GgDesc &d, int strip, int8_t *xs) {
+    const int tid = threadIdx.x, j = tid & 15, rs = tid >> 4;
+    constexpr int RPL = 2, UK = MR >= 4 ? 2 : 4;
+    const int M = d.M, N = d.N, ld = d.xld;
+    const int klen = (d.K + 15) & ~15;  // packed rows and staged rows are zero past K
+    const int n0 = strip * 32;
+    const int8_t *__restrict__ B = static_cast<const int8_t *>(d.W);
+    const int8_t *brow[RPL];
+#pragma unroll
+    for (int r = 0; r < RPL; r++) brow[r] = B + (long)min(n0 + rs + 16 * r, N - 1) * d.ldw;
+    auto load_batch = [&](v4i (&w)[UK][RPL], int k0) {
+#pragma unroll
+        for (int u = 0; u < UK; u++)
+#pragma unroll
+            for (int r = 0; r < RPL; r++)
+                w[u][r] = __builtin_nontemporal_load(reinterpret_cast<const v4i *>(brow[r] + min(k0 + 256 * u, klen - 16)));
+    };
+    v4i wn[UK][RPL];
+    load_batch(wn, 16 * j);
+    stage_rows<MR, true>(reinterpret_cast<uint8_t *>(xs), ld, ld, d.K, M, static_cast<const uint8_t *>(d.X),
+                         d.ldx);
+    __syncthreads();
+
+    int32_t acc[RPL][MR];
+#pragma unroll
+    for (int r = 0; r < RPL; r++)
+#pragma unroll
+        for (int m = 0; m < MR; m++) acc[r][m] = 0;
+    for (int k0 = 16 * j; k0 < klen; k0 += 256 * UK) {
+        v4i w[UK][RPL];
+#pragma unroll
+        for (int u = 0; u < UK; u++)
+#pragma unroll
+            for (int r = 0; r < RPL; r++) w[u][r] = wn[u][r];
+        if (k0 + 256 * UK < klen) load_batch(wn, k0 + 256 * UK);
+#pragma unroll
+        for (int u = 0; u < UK; u++) {
+            const int k = k0 + 256 * u;
+            if (k < klen) {
+#pragma unroll
+                for (int m = 0; m < MR; m++) {
+                    const v4i xv = *reinterpret_cast<const v4i *>(&xs[m * ld + k]);
+#pragma unroll
+                    for (int r = 0; r < RPL; r++) {
+                        int a = acc[r][m];
+                        a = __builtin_amdgcn_sdot4(xv[0], w[u][r][0], a, false);
+                        a = __builtin_amdgcn_sdot4(xv[1], w[u][r][1], a, false);
+                        a = __builtin_amdgcn_sdot4(xv[2], w[u][r][2], a, false);
+                        a = __builtin_amdgcn_sdot4(xv[3], w[u][r][3], a, false);
+                        acc[r][m] = a;
+                    }
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < RPL; r++)
+#pragma unroll
+        for (int m = 0; m < MR; m++) {
+            int v = acc[r][m];
+            v += __shfl_xor(v, 8, 16);
+            v += __shfl_xor(v, 4, 16);
+            v += __shfl_xor(v, 2, 16);
+            v += __shfl_xor(v, 1, 16);
+            acc[r][m] = v;
+        }
+    if (j == 0) {
+#pragma unroll
+        for (int r = 0; r < RPL; r++) {
+            const int n = n0 + rs + 16 * r;
+#pragma unroll
+            for (int m = 0; m < MR; m++) {
+                if (m < M && n < N) {
+                    if (d.out_mode == 0)
+                        igemv_write<0>(d.Y, d.ldy, m, n, acc[r][m], d.col_off, d.sa, d.sb);
+                    else if (d.out_mode == 1)
+                        igemv_write<1>(d.Y, d.ldy, m, n, acc[r][m], d.col_off, d.sa, d.sb);
+                    else
+                        igemv_write<2>(d.Y, d.ldy, m, n, acc[r][m], d.col_off, d.sa, d.sb);
+                }
+            }
+        }
+    }
+}
+
+template <int MR>
+__global__ __launch_bounds__(GV_THREADS) void gemv_group_kernel(const GgDesc *__restrict__ descs,
+                                                                const int2 *__restrict__ items) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char gv_dyn[];
+    __shared__ float red[4][MR][64];
+    const int2 it = items[blockIdx.x];
+    const GgDesc d = descs[it.x];
+    if (d.kind == GG_F32_N) gg_f32_n<MR>(d, it.y, reinterpret_cast<float *>(gv_dyn), red);
+    else if (d.kind == GG_F32_T) gg_f32_t<MR>(d, it.y, reinterpret_cast<float *>(gv_dyn));
+    else gg_u8s8<MR>(d, it.y, reinterpret_cast<int8_t *>(gv_dyn));
+}
+
+int gg_strip_rows(int kind) { return kind == GG_F32_N ? 64 : 32; }
+
+int gg_stage_ld(int kind, int K) {
+    if (kind == GG_F32_N) return 16 * ((cdiv(K, 16) + 7) / 8 * 8);
+    if (kind == GG_F32_T) return (K + 63) / 64 * 64;
+    return (K + 255) / 256 * 256;
+}
+
+hipError_t launch_gemv_group(const GgDesc *descs, const int2 *items, int n_items, int mr,
+                             size_t lds_bytes, hipStream_t s) {
+    if (n_items <= 0) return hipSuccess;
+    const dim3 grid(n_items), block(GV_THREADS);
+    switch (mr) {
+        case 1: hipLaunchKernelGGL(gemv_group_kernel<1>, grid, block, lds_bytes, s, descs, items); break;
+        case 2: hipLaunchKernelGGL(gemv_group_kernel<2>, grid, block, lds_bytes, s, descs, items); break;
+        case 4: hipLaunchKernelGGL(gemv_group_kernel<4>, grid, block, lds_bytes, s, descs, items); break;
+        default: hipLaunchKernelGGL(gemv_group_kernel<8>, grid, block, lds_bytes, s, descs, items); break;
+    }
+    return hipGetLastError();
+}
+
 // ---------------------------------------------- allocation-free scratch ----
 // The split-K partial sums of pcl_sgemv_noalloc live in this file-scope device
 // array: one copy per GPU, held until the process ends, shared by every such

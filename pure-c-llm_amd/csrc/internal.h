@@ -120,6 +120,30 @@ int sgemv_xf(int xf, int N, int K, const float *X, const float *W, int ldw,
 
 // ---- GEMV (gemv.hip) ----
 GemvPlan plan_sgemv(int w_trans, int M, int N, int K);
+// Grouped GEMV: one launch over independent products. Device descriptor of
+// one product (validated by the shim); out_mode of GG_U8S8: 0 int32, 1
+// float(v)*sb[n], 2 float(v)*(sa[m]*sb[n]); xld: staged activation row stride
+// (elements) = gg_stage_ld(kind, K). Work items are int2 {product, strip} with
+// strips of gg_strip_rows(kind) outputs; lds_bytes = max over products of
+// mr * xld * element size; mr in {1, 2, 4, 8} >= every product's M.
+enum { GG_F32_N = 0, GG_F32_T = 1, GG_U8S8 = 2 };
+struct GgDesc {
+    int kind, M, N, K;
+    const void *X;
+    long ldx;
+    const void *W;
+    long ldw;
+    const float *bias;
+    const int32_t *col_off;
+    const float *sa, *sb;
+    void *Y;
+    long ldy;
+    int accumulate, out_mode, xld, pad_;
+};
+int gg_strip_rows(int kind);
+int gg_stage_ld(int kind, int K);
+hipError_t launch_gemv_group(const GgDesc *descs, const int2 *items, int n_items, int mr,
+                             size_t lds_bytes, hipStream_t s);
 // Size of the static split-K scratch of the allocation-free GEMV entry point,
 // and its device address on the current device (hipGetSymbolAddress).
 constexpr size_t GEMV_NOALLOC_SCRATCH_BYTES = (size_t)4 << 20;

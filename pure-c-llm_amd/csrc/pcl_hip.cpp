@@ -14,6 +14,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <algorithm>
 #include <mutex>
 #include <unordered_map>
 #include <vector>
@@ -275,6 +276,13 @@ int sgemv_xf(int xf, int N, int K, const float *X, const float *W, int ldw,
 }
 }  // namespace pcl
 
+struct pcl_gemv_group {
+    pcl::GgDesc *d_descs = nullptr;
+    int2 *d_items = nullptr;
+    int n_items = 0, mr = 1;
+    size_t lds = 0;
+};
+
 // =========================================================================
 extern "C" {
 
@@ -477,6 +485,114 @@ int pcl_sgemv(int opW, int M, int N, int K, const float *X, int ldx, const float
     HIP_OK(pcl::launch_sgemv(p, opW == PCL_OP_T, M, N, K, X, ldx, false, W, ldw, bias, accumulate,
                              Y, ldy, sc->ws, s));
     return PCL_OK;
+}
+
+// ------------------------------------------------------ grouped GEMV ----
+int pcl_gemv_group_create(const pcl_gemv_desc *descs, int n, pcl_gemv_group **group) {
+    CHECK_ARG(group != nullptr, "pcl_gemv_group_create: group is NULL");
+    *group = nullptr;
+    CHECK_ARG(descs != nullptr && n > 0, "pcl_gemv_group_create: need n >= 1 products (n=%d)", n);
+    std::vector<pcl::GgDesc> dd((size_t)n);
+    struct Item {
+        long bytes;
+        int prod, strip;
+    };
+    std::vector<Item> items;
+    int mr = 1;
+    size_t stage_max = 0;
+    for (int i = 0; i < n; i++) {
+        const pcl_gemv_desc &q = descs[i];
+        CHECK_ARG(q.kind == PCL_GEMV_F32_N || q.kind == PCL_GEMV_F32_T || q.kind == PCL_GEMV_U8S8,
+                  "pcl_gemv_group_create: product %d: unknown kind %d", i, q.kind);
+        CHECK_ARG(q.M >= 1 && q.M <= 8 && q.N >= 1 && q.K >= 1,
+                  "pcl_gemv_group_create: product %d: need 1 <= M <= 8, N >= 1, K >= 1 (M=%d N=%d K=%d)",
+                  i, q.M, q.N, q.K);
+        CHECK_ARG(q.X && q.W && q.Y, "pcl_gemv_group_create: product %d: NULL operand", i);
+        CHECK_ARG(q.ldy >= q.N, "pcl_gemv_group_create: product %d: ldy=%d < N=%d", i, q.ldy, q.N);
+        CHECK_ARG(q.ldx >= q.K, "pcl_gemv_group_create: product %d: ldx=%d < K=%d", i, q.ldx, q.K);
+        size_t elt = 4;
+        if (q.kind == PCL_GEMV_F32_N) {
+            CHECK_ARG(q.N % 4 == 0 && q.ldw >= q.N && q.ldw % 4 == 0 && aligned16(q.W),
+                      "pcl_gemv_group_create: product %d: F32_N needs N %% 4 == 0, ldw >= N, ldw %% 4 "
+                      "== 0 and a 16-byte aligned W (N=%d ldw=%d)",
+                      i, q.N, q.ldw);
+        } else if (q.kind == PCL_GEMV_F32_T) {
+            CHECK_ARG(q.K % 4 == 0 && q.ldw >= q.K && q.ldw % 4 == 0 && aligned16(q.W),
+                      "pcl_gemv_group_create: product %d: F32_T needs K %% 4 == 0, ldw >= K, ldw %% 4 "
+                      "== 0 and a 16-byte aligned W (K=%d ldw=%d)",
+                      i, q.K, q.ldw);
+        } else {
+            CHECK_ARG(q.ldw >= kpad256(q.K) && q.ldw % 16 == 0 && aligned16(q.W),
+                      "pcl_gemv_group_create: product %d: U8S8 needs packed rows of ldw >= %d "
+                      "(a multiple of 16) and a 16-byte aligned W (ldw=%d)",
+                      i, kpad256(q.K), q.ldw);
+            CHECK_ARG(q.sb || !q.sa, "pcl_gemv_group_create: product %d: sa without sb", i);
+            elt = 1;
+        }
+        pcl::GgDesc &g = dd[(size_t)i];
+        g.kind = q.kind == PCL_GEMV_F32_N ? pcl::GG_F32_N : (q.kind == PCL_GEMV_F32_T ? pcl::GG_F32_T : pcl::GG_U8S8);
+        g.M = q.M, g.N = q.N, g.K = q.K;
+        g.X = q.X, g.ldx = q.ldx, g.W = q.W, g.ldw = q.ldw;
+        g.bias = q.kind == PCL_GEMV_U8S8 ? nullptr : q.bias;
+        g.col_off = q.kind == PCL_GEMV_U8S8 ? q.col_off : nullptr;
+        g.sa = q.sa, g.sb = q.sb;
+        g.Y = q.Y, g.ldy = q.ldy;
+        g.accumulate = q.kind == PCL_GEMV_U8S8 ? 0 : (q.accumulate ? 1 : 0);
+        g.out_mode = q.kind != PCL_GEMV_U8S8 ? 0 : (!q.sb ? 0 : (q.sa ? 2 : 1));
+        g.xld = pcl::gg_stage_ld(g.kind, q.K);
+        g.pad_ = 0;
+        const int m1 = q.M <= 1 ? 1 : (q.M <= 2 ? 2 : (q.M <= 4 ? 4 : 8));
+        if (m1 > mr) mr = m1;
+        if ((size_t)g.xld * elt > stage_max) stage_max = (size_t)g.xld * elt;
+        const int rows = pcl::gg_strip_rows(g.kind);
+        const int strips = (q.N + rows - 1) / rows;
+        const long bytes = (long)rows * (q.kind == PCL_GEMV_U8S8 ? g.ldw : 4L * q.K);
+        for (int t = 0; t < strips; t++) items.push_back({bytes, i, t});
+        CHECK_ARG(items.size() < (size_t)(1 << 30), "pcl_gemv_group_create: too many work items");
+    }
+    const size_t lds = (size_t)mr * stage_max;
+    if (lds > 65536)
+        return set_error(PCL_ERR_RANGE,
+                         "pcl_gemv_group_create: staged activations need %zu bytes of LDS (at most 65536): "
+                         "reduce K or M, or split the group",
+                         lds);
+    // largest blocks first, so the tail of the launch is short ones
+    std::stable_sort(items.begin(), items.end(), [](const Item &a, const Item &b) { return a.bytes > b.bytes; });
+    std::vector<int2> it(items.size());
+    for (size_t t = 0; t < items.size(); t++) it[t] = make_int2(items[t].prod, items[t].strip);
+    PCL_OK_OR_RETURN(do_init());
+    pcl_gemv_group *g = new (std::nothrow) pcl_gemv_group();
+    if (!g) return set_error(PCL_ERR_OOM, "pcl_gemv_group_create: out of host memory");
+    g->n_items = (int)it.size();
+    g->mr = mr;
+    g->lds = lds;
+    if (hipMalloc((void **)&g->d_descs, sizeof(pcl::GgDesc) * dd.size()) != hipSuccess ||
+        hipMalloc((void **)&g->d_items, sizeof(int2) * it.size()) != hipSuccess) {
+        pcl_gemv_group_free(g);
+        return set_error(PCL_ERR_OOM, "pcl_gemv_group_create: device allocation failed");
+    }
+    if (hipMemcpy(g->d_descs, dd.data(), sizeof(pcl::GgDesc) * dd.size(), hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(g->d_items, it.data(), sizeof(int2) * it.size(), hipMemcpyHostToDevice) != hipSuccess) {
+        pcl_gemv_group_free(g);
+        return set_error(PCL_ERR_HIP, "pcl_gemv_group_create: copying the plan to the device failed");
+    }
+    *group = g;
+    return PCL_OK;
+}
+
+int pcl_gemv_group_run(const pcl_gemv_group *group, void *stream) {
+    CHECK_ARG(group != nullptr, "pcl_gemv_group_run: group is NULL");
+    PCL_OK_OR_RETURN(do_init());
+    HIP_OK(pcl::launch_gemv_group(group->d_descs, group->d_items, group->n_items, group->mr, group->lds,
+                                  pick(stream)));
+    return PCL_OK;
+}
+
+void pcl_gemv_group_free(pcl_gemv_group *group) {
+    if (!group) return;
+    if (group->d_descs) (void)hipFree(group->d_descs);
+    if (group->d_items) (void)hipFree(group->d_items);
+    delete group;
 }
 
 // pcl_sgemv with its split-K partial sums in the static device scratch of

@@ -441,6 +441,102 @@ done:
     return rc;
 }
 
+/* The same sweep as one grouped launch per step (pcl_gemv_group_*): every
+ * product of the step is independent (own output rows), one group per weight
+ * copy, rotated as above. kinds: 0 = FP32 W K x N, 1 = FP32 W N x K, 2 = INT8
+ * packed (dequantised per row x per column). */
+typedef struct {
+    void **groups;
+    int n;
+} group_ctx;
+
+static int group_step(void *c_, int i) {
+    group_ctx *c = c_;
+    return pcl_gemv_group_run(c->groups[i % c->n], NULL);
+}
+
+int pcl_bench_gemv_group(const int *kinds, int M, int nshapes, const int *Ks, const int *Ns,
+                         int copies, int warmup, int steps, double *ms_total,
+                         double *bytes_per_step) {
+    int rc = PCL_OK;
+    copies = copies < 1 ? 1 : copies;
+    int kmax = 0, nmax = 0;
+    long ytot = 0;
+    double bytes = 0;
+    for (int s = 0; s < nshapes; s++) {
+        if (Ks[s] > kmax) kmax = Ks[s];
+        if (Ns[s] > nmax) nmax = Ns[s];
+        ytot += (long)M * Ns[s];
+        const int i8 = kinds[s] == 2;
+        double wb = i8 ? (double)Ns[s] * pcl_s8_kpad(Ks[s]) : 4.0 * Ks[s] * Ns[s];
+        double xb = i8 ? (double)M * Ks[s] : 4.0 * M * Ks[s];
+        bytes += wb + xb + 4.0 * M * Ns[s] + (i8 ? 4.0 * (Ns[s] + M) : 0.0);
+    }
+    *bytes_per_step = bytes;
+    void **W = calloc((size_t)copies * nshapes, sizeof(void *));
+    pcl_gemv_desc *d = calloc((size_t)nshapes, sizeof(pcl_gemv_desc));
+    group_ctx g = {calloc((size_t)copies, sizeof(void *)), copies};
+    void *X = dev_f32((size_t)M * kmax, 31, -1.f, 1.f);
+    void *Xu8 = dev_bytes((size_t)M * kmax, 32);
+    float *Y = pcl_malloc((size_t)ytot * 4);
+    void *sa = dev_f32(M, 33, 1e-3f, 1e-2f);
+    void *sb = dev_f32(nmax, 34, 1e-3f, 1e-2f);
+    if (!W || !d || !g.groups || !X || !Xu8 || !Y || !sa || !sb) {
+        rc = PCL_ERR_OOM;
+        goto done;
+    }
+    for (int cp = 0; cp < copies; cp++) {
+        long yoff = 0;
+        for (int s = 0; s < nshapes; s++) {
+            void **slot = &W[cp * nshapes + s];
+            const int i8 = kinds[s] == 2;
+            if (i8) {
+                void *Bq = dev_bytes((size_t)Ks[s] * Ns[s], 40 + s);
+                *slot = pcl_malloc(pcl_s8_packed_bytes(Ks[s], Ns[s]));
+                if (!Bq || !*slot) {
+                    pcl_free(Bq);
+                    rc = PCL_ERR_OOM;
+                    goto done;
+                }
+                rc = pcl_pack_b_s8(Bq, Ns[s], Ks[s], Ns[s], *slot, NULL, NULL);
+                pcl_stream_synchronize();
+                pcl_free(Bq);
+                if (rc != PCL_OK) goto done;
+            } else {
+                *slot = dev_f32((size_t)Ks[s] * Ns[s], 40 + s, -0.02f, 0.02f);
+                if (!*slot) {
+                    rc = PCL_ERR_OOM;
+                    goto done;
+                }
+            }
+            pcl_gemv_desc *q = &d[s];
+            memset(q, 0, sizeof *q);
+            q->kind = i8 ? PCL_GEMV_U8S8 : (kinds[s] == 1 ? PCL_GEMV_F32_T : PCL_GEMV_F32_N);
+            q->M = M, q->N = Ns[s], q->K = Ks[s];
+            q->X = i8 ? Xu8 : X;
+            q->ldx = Ks[s];
+            q->W = *slot;
+            q->ldw = i8 ? pcl_s8_kpad(Ks[s]) : (kinds[s] == 1 ? Ks[s] : Ns[s]);
+            if (i8) q->sa = sa, q->sb = sb;
+            q->Y = Y + yoff;
+            q->ldy = Ns[s];
+            yoff += (long)M * Ns[s];
+        }
+        TRY(pcl_gemv_group_create(d, nshapes, (pcl_gemv_group **)&g.groups[cp]));
+    }
+    TRY(time_steps(group_step, &g, warmup, steps, ms_total));
+done:
+    if (g.groups)
+        for (int cp = 0; cp < copies; cp++) pcl_gemv_group_free(g.groups[cp]);
+    free(g.groups);
+    if (W)
+        for (int j = 0; j < copies * nshapes; j++) pcl_free(W[j]);
+    free(W);
+    free(d);
+    pcl_free(X), pcl_free(Xu8), pcl_free(Y), pcl_free(sa), pcl_free(sb);
+    return rc;
+}
+
 /* Tied head + cross-entropy (350M: M=4096 tokens, D=1024, V=50257).
  * mode 0: one pcl_head_ce (logits, CE in place, d_lnf set, dwte accumulated)
  *         over chunks of at most chunk_bytes of logits;

@@ -131,6 +131,21 @@ _PROTOS = {
     "pcl_model_free": (None, [_vp]),
 }
 
+
+class GemvDesc(C.Structure):
+    """struct pcl_gemv_desc (include/pcl_hip.h): one product of a GEMV group."""
+    _fields_ = [("kind", _i), ("M", _i), ("N", _i), ("K", _i),
+                ("X", _vp), ("ldx", _i), ("W", _vp), ("ldw", _i),
+                ("bias", _vp), ("accumulate", _i),
+                ("col_off", _vp), ("sa", _vp), ("sb", _vp),
+                ("Y", _vp), ("ldy", _i)]
+
+
+GEMV_F32_N, GEMV_F32_T, GEMV_U8S8 = 0, 1, 2
+_PROTOS["pcl_gemv_group_create"] = (_i, [C.POINTER(GemvDesc), _i, C.POINTER(_vp)])
+_PROTOS["pcl_gemv_group_run"] = (_i, [_vp, _vp])
+_PROTOS["pcl_gemv_group_free"] = (None, [_vp])
+
 for _name, (_res, _args) in _PROTOS.items():
     _fn = getattr(lib, _name)
     _fn.restype = _res
@@ -234,3 +249,28 @@ def device_info() -> dict:
 
 def sync() -> None:
     check(lib.pcl_stream_synchronize())
+
+
+class GemvGroup:
+    """A pcl_gemv_group over a list of GemvDesc (freed on close()/GC). The
+    caller keeps the buffers the descriptors point to alive."""
+
+    def __init__(self, descs):
+        arr = (GemvDesc * len(descs))(*descs)
+        h = _vp()
+        check(lib.pcl_gemv_group_create(arr, len(descs), C.byref(h)))
+        self.handle = h.value
+
+    def run(self, stream=None) -> None:
+        check(lib.pcl_gemv_group_run(self.handle, stream))
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            lib.pcl_gemv_group_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
