@@ -44,6 +44,7 @@ def load_bench():
     lib = C.CDLL(path)
     d, i = C.c_double, C.c_int
     lib.pcl_bench_igemm.argtypes = [i, i, i, i, i, i, i, C.POINTER(d)]
+    lib.pcl_bench_igemm_ex.argtypes = [i, i, i, i, i, i, i, C.POINTER(d), C.POINTER(d)]
     lib.pcl_bench_sgemm.argtypes = [i, i, i, i, i, i, i, i, C.POINTER(d)]
     lib.pcl_bench_gemv.argtypes = [C.POINTER(i), i, i, C.POINTER(i), C.POINTER(i), i, i, i, i, C.POINTER(d),
                                    C.POINTER(d)]
@@ -53,7 +54,7 @@ def load_bench():
     lib.pcl_bench_attn_bwd.argtypes = [i, i, i, i, i, i, C.POINTER(d)]
     lib.pcl_bench_sgemm_ex.argtypes = [i, i, i, i, i, i, i, i, i, C.POINTER(d)]
     lib.pcl_bench_head_ce.argtypes = [i, i, i, C.c_long, i, i, i, C.POINTER(d)]
-    for f in (lib.pcl_bench_igemm, lib.pcl_bench_sgemm, lib.pcl_bench_gemv, lib.pcl_bench_gemv_group,
+    for f in (lib.pcl_bench_igemm, lib.pcl_bench_igemm_ex, lib.pcl_bench_sgemm, lib.pcl_bench_gemv, lib.pcl_bench_gemv_group,
               lib.pcl_bench_attn,
               lib.pcl_bench_attn_bwd, lib.pcl_bench_sgemm_ex, lib.pcl_bench_head_ce):
         f.restype = i
@@ -276,49 +277,108 @@ def read_traffic():
     return float(m.group(1)) if m else None
 
 
-def cpu_baseline(M=2048, N=2048, K=2048):
-    """The reference's own INT8 rung (gemm_bench.c:278 gemm_int8_kernel,
-    AVX-512 VNNI, single-threaded as in the reference) built from source into
-    oracle/_ref, on the full primary problem; falls back to the oracle's exact
-    integer GEMM on a bounded row sample when that build is unusable here."""
+def host_cores():
+    """Threads this process may use on the host: the affinity mask, capped by
+    OMP_NUM_THREADS where the GPU boxes set it (the box's share of the host)."""
+    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    return min(cores, share) if share > 0 else cores
+
+
+def _vnni_operands(ob, np, M, N, K, seed):
+    """u8 activations, s8 weights in gemm_bench's VNNI panel layout
+    (gemm_bench.c:254), corr = 128*colsum and dq, as gemm_bench prepares them
+    offline (untimed, gemm_bench.c:368, 379-381)."""
+    Au = ob.u8((M, K), seed)
+    Bq = ob.s8((K, N), seed + 1)
+    Bp = np.empty((N // 16) * (K // 4) * 64, np.int8)
+    for j in range(4):
+        Bp.reshape(N // 16, K // 4, 16, 4)[:, :, :, j] = Bq[j::4, :].reshape(K // 4, N // 16, 16).transpose(1, 0, 2)
+    corr = (128 * Bq.astype(np.int64).sum(0)).astype(np.int32)
+    dq = ob.uniform((N,), seed + 3, 1e-3, 1e-2)
+    return Au, Bp, corr, dq
+
+
+def cpu_reference(M=2048, N=2048, K=2048):
+    """The reference's CPU path timed on this host (oracle/_ref builds of
+    gemm_bench.c and tensor.c from source; kind "reference"), best of runs as
+    gemm_bench.c:329-337:
+      * the VNNI INT8 rung (gemm_int8_kernel, gemm_bench.c:260-285) on the
+        primary 2048^3 problem, single-threaded as in gemm_bench and driven over
+        M bands by 4, 8 and all host threads (1 and 4 threads on a 512-row
+        sample, scaled per operation);
+      * the same rung on the 350M-class K = 1024 / 4096 shapes (a 256-row sample
+        of the 4096 rows, all threads);
+      * FP32 v3-MT (gemm_packed_mt, :167-192) and v1 i-k-j as tensor.c's
+        OpenMP matmul (tensor.c:34-53) on the 1024^3 gemm_bench config, at 1,
+        4, 8 and all threads;
+      * the reference's own 1-core roofs (:287-325).
+    Returns (cpu_baseline, detail); cpu_baseline is None when the reference
+    build is unusable on this host."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import numpy as np
 
     import binding as ob
 
-    Au = ob.u8((M, K), 11)
     gb = ob.ref("libref_gemm_bench.so")
-    if gb is not None and gb.pcl_ref_cpu_ok():
-        Bq = ob.s8((K, N), 12)
-        Bp = np.empty((N // 16) * (K // 4) * 64, np.int8)
-        for j in range(4):  # VNNI panel layout of gemm_bench.c:254
-            Bp.reshape(N // 16, K // 4, 16, 4)[:, :, :, j] = Bq[j::4, :].reshape(K // 4, N // 16, 16).transpose(1, 0, 2)
-        corr = (128 * Bq.astype(np.int64).sum(0)).astype(np.int32)
-        dq = ob.uniform((N,), 14, 1e-3, 1e-2)
-        Cm = np.empty((M, N), np.float32)
-        best = 1e30
-        for _ in range(3):
+    if gb is None or not gb.pcl_ref_cpu_ok():
+        return None, {"unavailable": "reference build missing or the host lacks AVX-512 VNNI (gemm_bench.c:25)"}
+    cores = host_cores()
+    thr = sorted({1, 4, 8, cores})
+    detail = {"cpu": cpu_model(), "cores": cores}
+
+    def best(f, reps):
+        t = 1e30
+        for _ in range(reps):
             t0 = time.perf_counter()
-            gb.pcl_ref_gemm_int8_kernel(ob.p(Au), K, ob.p(Bp), ob.p(corr), ob.p(dq), ob.p(Cm), M, N)
-            best = min(best, time.perf_counter() - t0)
-        return {"value": round(2.0 * M * N * K / best / 1e12, 4), "unit": "TOP/s", "cores": 1,
-                "kind": "reference",
-                "sample": f"full {M}x{N}x{K} u8 x s8 problem through the reference gemm_int8_kernel "
-                          "(AVX-512 VNNI, gemm_bench.c:278-285, single-threaded as in gemm_bench), best of 3"}
-    rows = 128
-    Bq = ob.s8((K, N), 12)
-    threads = os.cpu_count() or 1
-    t0 = time.perf_counter()
-    ob.gemm_u8s8_i32(Au[:rows], Bq)
-    dt = time.perf_counter() - t0
-    return {"value": round(2.0 * rows * N * K / dt / 1e12, 6), "unit": "TOP/s", "cores": threads, "kind": "port",
-            "sample": f"{rows} of {M} rows of the {M}x{N}x{K} problem through the oracle's exact int64 GEMM "
-                      "(the reference VNNI build is unavailable on this host)"}
+            f()
+            t = min(t, time.perf_counter() - t0)
+        return t
+
+    Au, Bp, corr, dq = _vnni_operands(ob, np, M, N, K, 11)
+    Cm = np.empty((M, N), np.float32)
+    i8 = {}
+    for t in thr:
+        rows = M if t >= 8 else 512
+        dt = best(lambda: gb.pcl_ref_gemm_int8_mt(t, ob.p(Au), K, ob.p(Bp), ob.p(corr), ob.p(dq), ob.p(Cm), rows, N),
+                  3 if t >= 8 else 2)
+        i8[f"{t}t"] = round(2.0 * rows * N * K / dt / 1e12, 4)
+    detail["int8_vnni_2048_TOPS"] = i8
+    shapes = {"qkv": (1024, 3072), "attn_out": (1024, 1024), "ffn_up": (1024, 4096), "ffn_down": (4096, 1024)}
+    i8s = {}
+    for name, (k, n) in shapes.items():
+        A2, B2, c2, d2 = _vnni_operands(ob, np, 256, n, k, 21)
+        C2 = np.empty((256, n), np.float32)
+        dt = best(lambda: gb.pcl_ref_gemm_int8_mt(cores, ob.p(A2), k, ob.p(B2), ob.p(c2), ob.p(d2), ob.p(C2), 256, n), 3)
+        i8s[name] = round(2.0 * 256 * n * k / dt / 1e12, 4)
+    detail[f"int8_vnni_350m_TOPS_{cores}t"] = i8s
+    A, B = ob.frand((1024, 1024), 1234), ob.frand((1024, 1024), 1235)
+    Cf = np.empty((1024, 1024), np.float32)
+    v3, v1 = {}, {}
+    mm = ob.ref("libref_model.so")
+    for t in thr:
+        gb.pcl_ref_set_threads(t)
+        v3[f"{t}t"] = round(2.0 * 1024 ** 3 / best(lambda: gb.pcl_ref_gemm_packed_mt(ob.p(A), ob.p(B), ob.p(Cf), 1024,
+                                                                                       1024, 1024), 6) / 1e9, 1)
+        if mm is not None:
+            v1[f"{t}t"] = round(2.0 * 1024 ** 3 / best(lambda: mm.matmul(ob.p(A), ob.p(B), ob.p(Cf), 1024, 1024, 1024),
+                                                       3) / 1e9, 1)
+    gb.pcl_ref_set_threads(1)
+    detail["fp32_v3mt_1024_GFLOPS"] = v3
+    detail["fp32_v1_ikj_tensor_matmul_1024_GFLOPS"] = v1
+    detail["roofs_1core"] = {"fp32_GFLOPS": round(gb.pcl_ref_peak_gflops(), 1),
+                             "int8_GOPS": round(gb.pcl_ref_peak_int8_gops(), 1)}
+    base = {"value": i8[f"{cores}t"], "unit": "TOP/s", "cores": cores, "kind": "reference",
+            "sample": f"full {M}x{N}x{K} u8 x s8 problem through the reference gemm_int8_kernel (AVX-512 VNNI, "
+                      f"gemm_bench.c:260-285) over M bands on {cores} host threads, best of 3"}
+    return base, detail
 
 
 # Single configurations for profiling runs (bench.py --case NAME): the same
 # timing loops as the full run, one configuration per process.
 DECODE_LAYER = [(512, 1536), (512, 512), (512, 2048), (2048, 512)]
+INT8_350M = {"qkv": (4096, 3072, 1024), "attn_out": (4096, 1024, 1024), "ffn_up": (4096, 4096, 1024),
+             "ffn_down": (4096, 1024, 4096), "head": (4096, 50257, 1024)}
 CASES = {
     "int8_2048": lambda pcl, lib, w, s: igemm(pcl, lib, 2048, 2048, 2048, 2, w, s),
     "int8_ffn_up": lambda pcl, lib, w, s: igemm(pcl, lib, 4096, 4096, 1024, 2, w, s),
@@ -400,40 +460,27 @@ def cpu_next_rows():
     return out
 
 
-def cpu_ladder():
-    """The reference's FP32 gemm_bench rung v3-MT (gemm_packed_mt,
-    gemm_bench.c:167-192, OpenMP over M tiles) built from source into
-    oracle/_ref, on the gemm_bench FP32 config (1024^3, A and B uniform in
-    [-1, 1]) at the reference's own thread counts and at every core this
-    process may use; best of 6 as in gemm_bench.c:329-337. None when the
-    reference build is unusable on this host."""
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import binding as ob
+# bytes of the INT8 350M-class products (M x K u8 +
+# K x N s8 + 4 M N fp32 out + scales), for the attainable roof min(peak, I x HBM)
+def _i8_attainable(M, N, K):
+    ops = 2.0 * M * N * K
+    byts = M * K + K * N + 4.0 * M * N + 4.0 * (M + N)
+    return min(PEAK_I8_TOPS, ops / byts * PEAK_HBM_GBS / 1e3)
 
-    gb = ob.ref("libref_gemm_bench.so")
-    if gb is None or not gb.pcl_ref_cpu_ok():
-        return None
-    M = N = K = 1024
-    A, B = ob.frand((M, K), 1234), ob.frand((K, N), 1235)
-    import numpy as np
 
-    Cm = np.empty((M, N), np.float32)
-    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
-    # the share of the host this process is given (OMP_NUM_THREADS on the GPU boxes)
-    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
-    if share > 0:
-        cores = min(cores, share)
-    out = {"cpu": cpu_model(), "cores_used_max": cores, "fp32_v3mt_1024": {}}
-    for t in sorted({1, 4, 8, cores}):
-        gb.pcl_ref_set_threads(t)
-        best = 1e30
-        for _ in range(6):
-            t0 = time.perf_counter()
-            gb.pcl_ref_gemm_packed_mt(ob.p(A), ob.p(B), ob.p(Cm), M, K, N)
-            best = min(best, time.perf_counter() - t0)
-        out["fp32_v3mt_1024"][f"{t}t"] = round(2.0 * M * N * K / best / 1e9, 1)
-    gb.pcl_ref_set_threads(1)
-    out["unit"] = "GFLOP/s"
+def measured_roofs(pcl):
+    """The part's own roofs (pcl_measure_peak_mfma / pcl_measure_bandwidth,
+    gemm_bench.c:195-210 and 287-325 on the GPU)."""
+    d = C.c_double
+    out = {}
+    for key, data in (("mfma_i8_random_TOPS", 0), ("mfma_i8_zero_TOPS", 1), ("mfma_f32_random_TFLOPS", 2)):
+        r = d(0)
+        pcl.check(pcl.lib.pcl_measure_peak_mfma(data, C.byref(r)))
+        out[key] = round(r.value, 1)
+    tri, cp = d(0), d(0)
+    pcl.check(pcl.lib.pcl_measure_bandwidth(512 << 20, C.byref(tri), C.byref(cp)))
+    out["hbm_triad_GBps"] = round(tri.value, 1)
+    out["hbm_copy_GBps"] = round(cp.value, 1)
     return out
 
 
@@ -469,11 +516,16 @@ def main():
         print(json.dumps({"case": args.case, "steps": args.steps, "warmup": args.warmup, **res}), flush=True)
         return
     M = N = K = 2048
+    ops = 2.0 * M * N * K
     pcl.sync()
     t0 = time.perf_counter()
-    prim = igemm(pcl, lib, M, N, K, 2, args.warmup, args.steps)
+    ms, us_each = C.c_double(0), C.c_double(0)
+    _check(pcl, lib.pcl_bench_igemm_ex(M, N, K, 2, 1, args.warmup, args.steps, C.byref(ms), C.byref(us_each)),
+           "igemm 2048^3")
     wall = time.perf_counter() - t0
-    tops = prim["TOPS"]
+    per = ms.value / args.steps
+    tops = round(ops / (per * 1e-3) / 1e12, 1)
+    roofs = measured_roofs(pcl)
     out = {
         "metric": METRIC,
         "value": tops,
@@ -481,7 +533,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": prim["ms"],
+        "ms_per_step": round(per, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -493,8 +545,12 @@ def main():
                    "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": tops, "peak": PEAK_I8_TOPS, "unit": "TOP/s",
                      "frac": round(tops / PEAK_I8_TOPS, 4), "traffic": read_traffic(),
-                     "algorithmic_ops_per_launch": 2 * M * N * K,
+                     "kernel_us": round(us_each.value, 3),
+                     "achieved_per_kernel": round(ops / (us_each.value * 1e-6) / 1e12, 1),
+                     "frac_of_measured_i8_mfma": round(tops / roofs["mfma_i8_random_TOPS"], 4),
+                     "algorithmic_ops_per_launch": int(ops),
                      "algorithmic_bytes_per_launch": M * K + K * N + 4 * M * N + 4 * (M + N)},
+        "measured_roofs": roofs,
         "device": info,
         "timed_wall_s": round(wall, 3),
     }
@@ -504,78 +560,121 @@ def main():
         for _ in range(3):
             pcl.check(pcl.lib.pcl_memcpy_d2d(dst.ptr, src.ptr, nb))
         out["calib_copy_bytes"] = nb
+    ex = {}
     if not args.primary_only:
-        w, s = 5, 20
-        ex = {}
-        ex["fp32_gemm_1024"] = sgemm(pcl, lib, 0, 0, 1024, 1024, 1024, 0, w, 50)
-        ex["int8_350m"] = {name: igemm(pcl, lib, m, n, k, 2, w, s) for name, (m, n, k) in {
-            "qkv": (4096, 3072, 1024), "attn_out": (4096, 1024, 1024), "ffn_up": (4096, 4096, 1024),
-            "ffn_down": (4096, 1024, 4096), "head": (4096, 50257, 1024)}.items()}
-        ex["fp32_350m"] = {name: sgemm(pcl, lib, a, b, m, n, k, acc, w, s) for name, (a, b, m, n, k, acc) in {
-            "qkv": (0, 0, 4096, 3072, 1024, 0), "attn_out": (0, 0, 4096, 1024, 1024, 0),
-            "ffn_up": (0, 0, 4096, 4096, 1024, 0), "ffn_down": (0, 0, 4096, 1024, 4096, 0),
-            "head_nt": (0, 1, 4096, 50257, 1024, 0),
-            "bwd_dX_ffn_up_nt": (0, 1, 4096, 1024, 4096, 1), "bwd_dW_ffn_up_tn": (1, 0, 1024, 4096, 4096, 1)}.items()}
-        ex["grown_prefill_t256"] = {
-            "fp32": {name: sgemm(pcl, lib, a, b, m, n, k, 0, w, 50) for name, (a, b, m, n, k) in {
-                "qkv": (0, 0, 256, 1536, 512), "attn_out": (0, 0, 256, 512, 512), "ffn_up": (0, 0, 256, 2048, 512),
-                "ffn_down": (0, 0, 256, 512, 2048), "head_nt": (0, 1, 256, 2048, 512)}.items()},
-            "int8": {name: igemm(pcl, lib, m, n, k, 2, w, 50) for name, (m, n, k) in {
-                "qkv": (256, 1536, 512), "attn_out": (256, 512, 512), "ffn_up": (256, 2048, 512),
-                "ffn_down": (256, 512, 2048), "head": (256, 2048, 512)}.items()},
-        }
-        layer = [(512, 1536), (512, 512), (512, 2048), (2048, 512)]
-        grown_i8 = layer * 16 + [(512, 2048)]
-        dec = {}
-        # One token step: 16 layers (K x N weights) + the tied head (N x K).
-        # FP32 205 MB per step, 3 rotating weight copies (> the 256 MB
-        # Infinity Cache); INT8 51 MB per step, 11 copies. Each step is run as
-        # one call per product and as a captured graph (one launch per step).
-        fp32_step = layer * 16 + [(512, 2048)]
-        fp32_kinds = [0] * (len(layer) * 16) + [1]
-        for Mt in (1, 4, 8):
-            for g in (False, True):
-                tag = "_graph" if g else ""
-                dec[f"fp32_M{Mt}{tag}"] = gemv(pcl, lib, fp32_kinds, Mt, fp32_step, 3, 2, 10, graph=g)
-                dec[f"int8_M{Mt}{tag}"] = gemv(pcl, lib, 2, Mt, grown_i8, 11, 2, 10, graph=g)
-        ex["grown_decode_gemv"] = dec
-        ex["decode_e2e_grown"] = decode_e2e(pcl)
-        ex["head_350m_gemv_fp32"] = {f"M{Mt}": gemv(pcl, lib, 1, Mt, [(1024, 50257)], 3, 2, 20) for Mt in (1, 8)}
-        ex["head_350m_gemv_int8"] = {f"M{Mt}": gemv(pcl, lib, 2, Mt, [(1024, 50257)], 6, 2, 20) for Mt in (1, 8)}
-        # GEMM epilogues fused against the reference's two-pass sequence (350M class)
-        ex["fp32_350m_epilogues"] = {
-            "ffn_up_gelu": sgemm_epi(pcl, lib, 0, 0, 4096, 4096, 1024, 1, w, s),
-            "attn_out_residual": sgemm_epi(pcl, lib, 0, 0, 4096, 1024, 1024, 2, w, s),
-            "ffn_down_residual": sgemm_epi(pcl, lib, 0, 0, 4096, 1024, 4096, 2, w, s),
-            "bwd_dX_ffn_down_gelu_bwd": sgemm_epi(pcl, lib, 0, 1, 4096, 4096, 1024, 3, w, s),
-        }
-        # tied head + cross-entropy, forward and backward (350M: 4096 tokens,
-        # d 1024, vocabulary 50257): one 824 MB chunk, and 128 MB chunks
-        ex["head_ce"] = {
-            "350m": head_ce(pcl, lib, 4096, 1024, 50257, 0, 1, max(2, s // 20)),
-            "350m_chunk_128MB": head_ce(pcl, lib, 4096, 1024, 50257, 128 << 20, 1, max(2, s // 20)),
-            "grown_t256": head_ce(pcl, lib, 256, 512, 2048, 0, 3, 50),
-        }
-        # causal attention forward: 350M-class (16 heads of 64, B=4, T=1024),
-        # the reference GPU trainer's heads (12 of 128), the grown model (16 of 32, T=256)
-        ex["attn_fwd"] = {
-            "350m_probs": attn(pcl, lib, 4, 1024, 16, 64, True, w, s),
-            "350m_no_probs": attn(pcl, lib, 4, 1024, 16, 64, False, w, s),
-            "trainer_dh128_probs": attn(pcl, lib, 4, 1024, 12, 128, True, w, s),
-            "grown_t256_probs": attn(pcl, lib, 1, 256, 16, 32, True, w, 50),
-        }
-        ex["attn_bwd"] = {
-            "350m": attn_bwd(pcl, lib, 4, 1024, 16, 64, w, s),
-            "trainer_dh128": attn_bwd(pcl, lib, 4, 1024, 12, 128, w, s),
-            "grown_t256": attn_bwd(pcl, lib, 1, 256, 16, 32, w, 50),
-        }
-        out["extra"] = ex
+        ex = run_rows(pcl, lib)
+        out["rows"] = compact_rows(ex, roofs)
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(M, N, K)
+        base, cpu = cpu_reference(M, N, K)
+        if base is not None:
+            out["cpu_baseline"] = base
         if not args.primary_only:
-            out.setdefault("extra", {})["cpu_reference_fp32"] = cpu_ladder()
-            out["extra"]["cpu_port_next_rows"] = cpu_next_rows()
+            ex["cpu_reference"] = cpu
+            ex["cpu_port_next_rows"] = cpu_next_rows()
+            out["cpu"] = {k: v for k, v in cpu.items() if k != "roofs_1core"}
+    if ex:
+        # the full tables: one JSON line on stderr (stdout carries the one result line)
+        print("bench_detail " + json.dumps(ex), file=sys.stderr, flush=True)
     print(json.dumps(out), flush=True)
+
+
+def run_rows(pcl, lib):
+    """Every configuration beside the headline, at the bench's own step counts."""
+    w, s = 5, 20
+    ex = {}
+    ex["fp32_gemm_1024"] = sgemm(pcl, lib, 0, 0, 1024, 1024, 1024, 0, w, 50)
+    ex["int8_350m"] = {name: igemm(pcl, lib, m, n, k, 2, w, s) for name, (m, n, k) in INT8_350M.items()}
+    ex["fp32_350m"] = {name: sgemm(pcl, lib, a, b, m, n, k, acc, w, s) for name, (a, b, m, n, k, acc) in {
+        "qkv": (0, 0, 4096, 3072, 1024, 0), "attn_out": (0, 0, 4096, 1024, 1024, 0),
+        "ffn_up": (0, 0, 4096, 4096, 1024, 0), "ffn_down": (0, 0, 4096, 1024, 4096, 0),
+        "head_nt": (0, 1, 4096, 50257, 1024, 0),
+        "bwd_dX_ffn_up_nt": (0, 1, 4096, 1024, 4096, 1), "bwd_dW_ffn_up_tn": (1, 0, 1024, 4096, 4096, 1)}.items()}
+    ex["grown_prefill_t256"] = {
+        "fp32": {name: sgemm(pcl, lib, a, b, m, n, k, 0, w, 50) for name, (a, b, m, n, k) in {
+            "qkv": (0, 0, 256, 1536, 512), "attn_out": (0, 0, 256, 512, 512), "ffn_up": (0, 0, 256, 2048, 512),
+            "ffn_down": (0, 0, 256, 512, 2048), "head_nt": (0, 1, 256, 2048, 512)}.items()},
+        "int8": {name: igemm(pcl, lib, m, n, k, 2, w, 50) for name, (m, n, k) in {
+            "qkv": (256, 1536, 512), "attn_out": (256, 512, 512), "ffn_up": (256, 2048, 512),
+            "ffn_down": (256, 512, 2048), "head": (256, 2048, 512)}.items()},
+    }
+    # One decode sweep of the grown model: 16 layers (K x N weights) + the tied
+    # head (N x K). FP32 205 MB per sweep, 3 rotating weight copies (> the
+    # 256 MB Infinity Cache); INT8 51 MB, 11 copies. Per product: one call per
+    # product (the dependent decode chain's launch pattern), eager and as one
+    # captured graph; grouped: the 65 independent products in one launch.
+    fp32_step = DECODE_LAYER * 16 + [(512, 2048)]
+    fp32_kinds = [0] * (len(DECODE_LAYER) * 16) + [1]
+    dec = {}
+    for Mt in (1, 4, 8):
+        dec[f"fp32_M{Mt}"] = gemv(pcl, lib, fp32_kinds, Mt, fp32_step, 3, 2, 10)
+        dec[f"fp32_M{Mt}_graph"] = gemv(pcl, lib, fp32_kinds, Mt, fp32_step, 3, 2, 10, graph=True)
+        dec[f"fp32_M{Mt}_grouped"] = gemv_group(pcl, lib, fp32_kinds, Mt, fp32_step, 3, 3, 30)
+        dec[f"int8_M{Mt}"] = gemv(pcl, lib, 2, Mt, fp32_step, 11, 2, 10)
+        dec[f"int8_M{Mt}_graph"] = gemv(pcl, lib, 2, Mt, fp32_step, 11, 2, 10, graph=True)
+        dec[f"int8_M{Mt}_grouped"] = gemv_group(pcl, lib, 2, Mt, fp32_step, 11, 3, 30)
+    ex["grown_decode_gemv"] = dec
+    ex["decode_e2e_grown"] = decode_e2e(pcl)
+    ex["head_350m_gemv_fp32"] = {f"M{Mt}": gemv(pcl, lib, 1, Mt, [(1024, 50257)], 3, 2, 20) for Mt in (1, 8)}
+    ex["head_350m_gemv_int8"] = {f"M{Mt}": gemv(pcl, lib, 2, Mt, [(1024, 50257)], 6, 2, 20) for Mt in (1, 8)}
+    ex["fp32_350m_epilogues"] = {
+        "ffn_up_gelu": sgemm_epi(pcl, lib, 0, 0, 4096, 4096, 1024, 1, w, s),
+        "attn_out_residual": sgemm_epi(pcl, lib, 0, 0, 4096, 1024, 1024, 2, w, s),
+        "ffn_down_residual": sgemm_epi(pcl, lib, 0, 0, 4096, 1024, 4096, 2, w, s),
+        "bwd_dX_ffn_down_gelu_bwd": sgemm_epi(pcl, lib, 0, 1, 4096, 4096, 1024, 3, w, s),
+    }
+    ex["head_ce"] = {
+        "350m": head_ce(pcl, lib, 4096, 1024, 50257, 0, 1, max(2, s // 20)),
+        "350m_chunk_128MB": head_ce(pcl, lib, 4096, 1024, 50257, 128 << 20, 1, max(2, s // 20)),
+        "grown_t256": head_ce(pcl, lib, 256, 512, 2048, 0, 3, 50),
+    }
+    ex["attn_fwd"] = {
+        "350m_probs": attn(pcl, lib, 4, 1024, 16, 64, True, w, s),
+        "350m_no_probs": attn(pcl, lib, 4, 1024, 16, 64, False, w, s),
+        "trainer_dh128_probs": attn(pcl, lib, 4, 1024, 12, 128, True, w, s),
+        "grown_t256_probs": attn(pcl, lib, 1, 256, 16, 32, True, w, 50),
+    }
+    ex["attn_bwd"] = {
+        "350m": attn_bwd(pcl, lib, 4, 1024, 16, 64, w, s),
+        "trainer_dh128": attn_bwd(pcl, lib, 4, 1024, 12, 128, w, s),
+        "grown_t256": attn_bwd(pcl, lib, 1, 256, 16, 32, w, 50),
+    }
+    return ex
+
+
+def compact_rows(ex, roofs):
+    """The north-star rows and the next rows in a few hundred bytes each:
+    [rate, fraction of the datasheet peak, fraction of the attainable roof]."""
+    r = {}
+    r["int8_350m_TOPS"] = {"cols": ["TOPS", "frac_peak", "frac_attainable", "frac_measured_mfma"]}
+    for name, (m, n, k) in INT8_350M.items():
+        t = ex["int8_350m"][name]["TOPS"]
+        r["int8_350m_TOPS"][name] = [t, round(t / PEAK_I8_TOPS, 3), round(t / _i8_attainable(m, n, k), 3),
+                                     round(t / roofs["mfma_i8_random_TOPS"], 3)]
+    r["fp32_350m_TFLOPS"] = {"cols": ["TFLOPS", "frac_peak", "frac_measured_mfma"]}
+    for name, v in ex["fp32_350m"].items():
+        r["fp32_350m_TFLOPS"][name] = [v["TFLOPS"], v["frac_peak"], round(v["TFLOPS"] / roofs["mfma_f32_random_TFLOPS"], 3)]
+    v = ex["fp32_gemm_1024"]
+    r["fp32_1024_TFLOPS"] = [v["TFLOPS"], v["frac_peak"]]
+    r["grown_prefill_us"] = {dt: {k: round(1e3 * q["ms"], 2) for k, q in ex["grown_prefill_t256"][dt].items()}
+                             for dt in ("fp32", "int8")}
+    d = ex["grown_decode_gemv"]
+    r["grown_decode_sweep_GBps"] = {"cols": ["per_product", "per_product_graph", "grouped", "grouped_frac_hbm"]}
+    for key in ("fp32_M1", "fp32_M4", "fp32_M8", "int8_M1", "int8_M4", "int8_M8"):
+        g = d[key + "_grouped"]
+        r["grown_decode_sweep_GBps"][key] = [d[key]["GBps"], d[key + "_graph"]["GBps"], g["GBps"], g["frac_hbm"]]
+    r["head_350m_gemv_GBps"] = {f"{dt}_{m}": [ex[f"head_350m_gemv_{dt}"][m]["GBps"], ex[f"head_350m_gemv_{dt}"][m]["frac_hbm"]]
+                                for dt in ("fp32", "int8") for m in ("M1", "M8")}
+    r["attn_350m_TFLOPS"] = {"fwd_probs": ex["attn_fwd"]["350m_probs"]["TFLOPS"],
+                             "fwd_no_probs": ex["attn_fwd"]["350m_no_probs"]["TFLOPS"],
+                             "bwd": ex["attn_bwd"]["350m"]["TFLOPS"]}
+    r["head_ce_350m"] = {"TFLOPS": ex["head_ce"]["350m"]["TFLOPS"], "ms": ex["head_ce"]["350m"]["ms"]}
+    e = ex["decode_e2e_grown"]
+    r["decode_e2e_grown_tok_s"] = {"fp32": e.get("eager_tokens_per_s"), "fp32_graph": e.get("graph_tokens_per_s"),
+                                   "int8": e.get("int8_eager_tokens_per_s"),
+                                   "int8_graph": e.get("int8_graph_tokens_per_s"),
+                                   "cpu_reference": e.get("cpu_reference_tokens_per_s")}
+    r["epilogue_speedup"] = {k: v["speedup"] for k, v in ex["fp32_350m_epilogues"].items()}
+    return r
 
 
 if __name__ == "__main__":

@@ -338,6 +338,19 @@ int pcl_gemv_u8s8_dq(const uint8_t *X, int ldx, const int8_t *Bpk, const int32_t
                      const float *sa, const float *sb, float *Y, int ldy, int M, int N, int K,
                      void *stream);
 
+/* ---- measured roofs: gemm_bench's measure_peak_int8_gops (gemm_bench.c:287-301),
+ * measure_peak_gflops (:309-325) and measure_bandwidth_gbs (:195-210) on the GPU.
+ * Sustained matrix-core rate with the operands held in registers (eight waves
+ * per CU, four independent accumulators each): data 0 = i8 MFMA on uniformly
+ * random bytes (the gemm_bench INT8 data; the clock drops with the operands'
+ * switching), 1 = i8 on zeros, 2 = f32 MFMA on uniform random floats. *rate in
+ * TOP/s (i8) or TFLOP/s (f32); best of 5 launches. */
+int pcl_measure_peak_mfma(int data, double *rate);
+/* HBM: STREAM triad a = b + s*c (3 arrays of traffic) and a copy (2) over
+ * arrays of bytes_per_array (at least 64 MiB; use > 256 MB to leave the
+ * Infinity Cache), 16-byte accesses; best of 5, GB/s. Allocates the arrays. */
+int pcl_measure_bandwidth(long bytes_per_array, double *triad_gbs, double *copy_gbs);
+
 /* ---- grouped decode GEMV: many independent products in one launch ----
  * Not a reference function: the reference runs its decode products one call
  * at a time (generate.c:95-107 matvec, three of them on one input for the

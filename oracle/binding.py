@@ -80,6 +80,10 @@ _REF_PROTOS = {
         "pcl_ref_quantize_A": (_f, [_vp, _vp, _i, _i, _i]),
         "pcl_ref_quantize_B_pack": (None, [_vp, _vp, _vp, _vp, _i, _i, _i]),
         "pcl_ref_gemm_int8_kernel": (None, [_vp, _i, _vp, _vp, _vp, _vp, _i, _i]),
+        "pcl_ref_gemm_int8_mt": (None, [_i, _vp, _i, _vp, _vp, _vp, _vp, _i, _i]),
+        "pcl_ref_peak_gflops": (_d, []),
+        "pcl_ref_peak_int8_gops": (_d, []),
+        "pcl_ref_bandwidth_gbs": (_d, []),
         "pcl_ref_rms_rel": (_d, [_vp, _vp, _l]),
         "pcl_ref_max_abs_diff": (_d, [_vp, _vp, _l]),
         "pcl_ref_srand": (None, [C.c_uint]),

@@ -40,3 +40,23 @@ double pcl_ref_max_abs_diff(const float *X, const float *Y, long n) { return max
 /* gemm_bench.c:50-52: glibc rand() after the caller's srand() */
 void pcl_ref_srand(unsigned s) { srand(s); }
 void pcl_ref_fill_rand(float *p, long n) { fill_rand(p, n); }
+
+/* The reference INT8 rung (gemm_int8_kernel, single-threaded in gemm_bench)
+ * driven over row bands of Au and C, one band per OpenMP thread: the
+ * multi-threaded CPU baseline over M tiles. Bands are multiples of the
+ * kernel's 8-row microkernel (M % 8 == 0, as the reference requires). */
+void pcl_ref_gemm_int8_mt(int threads, const uint8_t *Au, int Kpad, const int8_t *Bp,
+                          const int32_t *corr, const float *dq, float *C, int M, int N) {
+#pragma omp parallel num_threads(threads)
+    {
+        const int t = omp_get_thread_num(), nt = omp_get_num_threads();
+        const long blocks = M / 8;
+        const int b0 = (int)(blocks * t / nt) * 8, b1 = (int)(blocks * (t + 1) / nt) * 8;
+        if (b1 > b0)
+            gemm_int8_kernel(Au + (size_t)b0 * Kpad, Kpad, Bp, corr, dq, C + (size_t)b0 * N, b1 - b0, N);
+    }
+}
+/* gemm_bench.c:195-210, 287-325: the reference's own 1-core roofs and triad */
+double pcl_ref_peak_gflops(void) { return measure_peak_gflops(); }
+double pcl_ref_peak_int8_gops(void) { return measure_peak_int8_gops(); }
+double pcl_ref_bandwidth_gbs(void) { return measure_bandwidth_gbs(); }

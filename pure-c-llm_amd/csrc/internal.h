@@ -118,6 +118,13 @@ int sgemv_xf(int xf, int N, int K, const float *X, const float *W, int ldw,
              const float *g, const float *b, const float *bias, int accumulate, float *Y,
              void *stream);
 
+// ---- measured roofs (roofs.hip) ----
+// kind 0: i8 MFMA, random bytes; 1: i8 MFMA, zeros; 2: f32 MFMA, random;
+// rate in TOP/s or TFLOP/s over `cus` workgroups of eight waves.
+hipError_t measure_peak_mfma(int kind, int cus, double *rate, hipStream_t s);
+// STREAM triad and copy over arrays of bytes_per_array (GB/s).
+hipError_t measure_bandwidth(long bytes_per_array, double *triad_gbs, double *copy_gbs, hipStream_t s);
+
 // ---- GEMV (gemv.hip) ----
 GemvPlan plan_sgemv(int w_trans, int M, int N, int K);
 // Grouped GEMV: one launch over independent products. Device descriptor of

@@ -487,6 +487,27 @@ int pcl_sgemv(int opW, int M, int N, int K, const float *X, int ldx, const float
     return PCL_OK;
 }
 
+// ------------------------------------------------------ measured roofs ----
+int pcl_measure_peak_mfma(int data, double *rate) {
+    CHECK_ARG(rate != nullptr, "pcl_measure_peak_mfma: rate is NULL");
+    CHECK_ARG(data >= 0 && data <= 2, "pcl_measure_peak_mfma: data must be 0, 1 or 2 (got %d)", data);
+    PCL_OK_OR_RETURN(do_init());
+    int dev = 0, cus = 0;
+    HIP_OK(hipGetDevice(&dev));
+    HIP_OK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    HIP_OK(pcl::measure_peak_mfma(data, cus, rate, pick(nullptr)));
+    return PCL_OK;
+}
+
+int pcl_measure_bandwidth(long bytes_per_array, double *triad_gbs, double *copy_gbs) {
+    CHECK_ARG(triad_gbs && copy_gbs, "pcl_measure_bandwidth: NULL result pointer");
+    CHECK_ARG(bytes_per_array >= (64L << 20), "pcl_measure_bandwidth: arrays of at least 64 MiB (got %ld)",
+              bytes_per_array);
+    PCL_OK_OR_RETURN(do_init());
+    HIP_OK(pcl::measure_bandwidth(bytes_per_array, triad_gbs, copy_gbs, pick(nullptr)));
+    return PCL_OK;
+}
+
 // ------------------------------------------------------ grouped GEMV ----
 int pcl_gemv_group_create(const pcl_gemv_desc *descs, int n, pcl_gemv_group **group) {
     CHECK_ARG(group != nullptr, "pcl_gemv_group_create: group is NULL");

@@ -1,0 +1,206 @@
+// roofs.hip -- the MI355X's own roofs, measured: the GPU counterparts of
+// gemm_bench.c's measure_peak_int8_gops (:287-301), measure_peak_gflops
+// (:309-325) and measure_bandwidth_gbs (STREAM triad, :195-210). The
+// reference times its rungs against roofs it measures on the machine it runs
+// on; these do the same for the matrix cores and HBM, so a kernel's fraction
+// can be read against what the part sustains as well as its datasheet peak.
+//
+// Matrix cores: every CU runs eight waves (two per SIMD), each holding four
+// independent 32x32 accumulators and its operands in registers, so nothing
+// but the MFMA pipe is exercised. The MI355X lowers its shader clock with the
+// switching activity of the operands, so the rate is measured for the data a
+// GEMM sees: uniformly random bytes (the gemm_bench INT8 workload) or zeros
+// for i8, uniform random floats for f32.
+//
+// HBM: the triad a[i] = b[i] + s*c[i] over three arrays far larger than the
+// 256 MB Infinity Cache, and a plain copy, with 16-byte accesses,
+// grid-stride; best of several passes (as gemm_bench's best of 5).
+#include "internal.h"
+
+namespace pcl {
+
+typedef int rf_v4i __attribute__((ext_vector_type(4)));
+typedef int rf_v16i __attribute__((ext_vector_type(16)));
+typedef float rf_v4f __attribute__((ext_vector_type(4)));
+typedef float rf_v16f __attribute__((ext_vector_type(16)));
+
+constexpr int RF_WAVES = 8;     // per CU: two per SIMD
+constexpr int RF_ITERS = 2048;  // four MFMAs each
+
+__device__ __forceinline__ unsigned rf_next(unsigned &s) {
+    s ^= s << 13;
+    s ^= s >> 17;
+    s ^= s << 5;
+    return s;
+}
+
+template <bool RANDOM>
+__global__ __launch_bounds__(64 * RF_WAVES) void roof_i8_kernel(int *out, unsigned seed) {
+    unsigned s = seed ^ (threadIdx.x * 2654435761u) ^ (blockIdx.x * 40503u) ^ 1u;
+    rf_v4i a[2], b[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            a[i][e] = RANDOM ? (int)rf_next(s) : 0;
+            b[i][e] = RANDOM ? (int)rf_next(s) : 0;
+        }
+    rf_v16i acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) acc[i][j][v] = 0;
+    for (int it = 0; it < RF_ITERS; it++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], acc[i][j], 0, 0, 0);
+    int t = 0;
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) t += acc[i][j][v];
+    out[blockIdx.x * blockDim.x + threadIdx.x] = t;
+}
+
+__global__ __launch_bounds__(64 * RF_WAVES) void roof_f32_kernel(float *out, unsigned seed) {
+    unsigned s = seed ^ (threadIdx.x * 2654435761u) ^ (blockIdx.x * 40503u) ^ 1u;
+    float a[2], b[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        a[i] = (float)(rf_next(s) >> 8) * (1.0f / 16777216.0f) - 0.5f;
+        b[i] = (float)(rf_next(s) >> 8) * (1.0f / 16777216.0f) - 0.5f;
+    }
+    rf_v16f acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) acc[i][j][v] = 0.f;
+    for (int it = 0; it < RF_ITERS; it++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) t += acc[i][j][v];
+    out[blockIdx.x * blockDim.x + threadIdx.x] = t;
+}
+
+// a[i] = b[i] + s * c[i] (triad) or a[i] = b[i] (copy), n4 16-byte elements
+template <bool TRIAD>
+__global__ __launch_bounds__(256) void roof_stream_kernel(rf_v4f *__restrict__ a, const rf_v4f *__restrict__ b,
+                                                          const rf_v4f *__restrict__ c, float sc, long n4) {
+    for (long i = blockIdx.x * 256L + threadIdx.x; i < n4; i += (long)gridDim.x * 256) {
+        const rf_v4f x = b[i];
+        a[i] = TRIAD ? x + sc * c[i] : x;
+    }
+}
+
+__global__ void roof_fill_kernel(rf_v4f *p, long n4, float v) {
+    for (long i = blockIdx.x * 256L + threadIdx.x; i < n4; i += (long)gridDim.x * 256)
+        p[i] = rf_v4f{v, v, v, v};
+}
+
+// Best time of `reps` launches of f (each bracketed by events), in ms.
+template <typename F>
+static hipError_t best_ms(F f, int reps, hipStream_t s, float *best) {
+    hipEvent_t e0, e1;
+    hipError_t err = hipEventCreate(&e0);
+    if (err != hipSuccess) return err;
+    err = hipEventCreate(&e1);
+    if (err != hipSuccess) {
+        (void)hipEventDestroy(e0);
+        return err;
+    }
+    *best = 1e30f;
+    for (int r = 0; r < reps && err == hipSuccess; r++) {
+        err = hipEventRecord(e0, s);
+        if (err == hipSuccess) f();
+        if (err == hipSuccess) err = hipGetLastError();
+        if (err == hipSuccess) err = hipEventRecord(e1, s);
+        if (err == hipSuccess) err = hipEventSynchronize(e1);
+        float ms = 0.f;
+        if (err == hipSuccess) err = hipEventElapsedTime(&ms, e0, e1);
+        if (err == hipSuccess && ms < *best) *best = ms;
+    }
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    return err;
+}
+
+hipError_t measure_peak_mfma(int kind, int cus, double *rate, hipStream_t s) {
+    void *out = nullptr;
+    hipError_t err = hipMalloc(&out, (size_t)cus * 64 * RF_WAVES * 4);
+    if (err != hipSuccess) return err;
+    const dim3 grid(cus), block(64 * RF_WAVES);
+    unsigned seed = 12345u;
+    auto launch = [&]() {
+        seed += 7919u;
+        if (kind == 0) hipLaunchKernelGGL(roof_i8_kernel<true>, grid, block, 0, s, (int *)out, seed);
+        else if (kind == 1) hipLaunchKernelGGL(roof_i8_kernel<false>, grid, block, 0, s, (int *)out, seed);
+        else hipLaunchKernelGGL(roof_f32_kernel, grid, block, 0, s, (float *)out, seed);
+    };
+    launch();  // warm-up (clock ramp, code load)
+    float ms = 0.f;
+    err = best_ms(launch, 5, s, &ms);
+    if (err == hipSuccess) {
+        const double per_mfma = kind == 2 ? 32.0 * 32 * 2 * 2 : 32.0 * 32 * 32 * 2;
+        const double ops = (double)cus * RF_WAVES * RF_ITERS * 4 * per_mfma;
+        *rate = ops / (ms * 1e-3) / 1e12;
+    }
+    (void)hipFree(out);
+    return err;
+}
+
+hipError_t measure_bandwidth(long bytes_per_array, double *triad_gbs, double *copy_gbs, hipStream_t s) {
+    const long n4 = bytes_per_array / 16;
+    void *a = nullptr, *b = nullptr, *c = nullptr;
+    hipError_t err = hipMalloc(&a, n4 * 16);
+    if (err == hipSuccess) err = hipMalloc(&b, n4 * 16);
+    if (err == hipSuccess) err = hipMalloc(&c, n4 * 16);
+    const dim3 grid(8192), block(256);
+    if (err == hipSuccess) {
+        hipLaunchKernelGGL(roof_fill_kernel, grid, block, 0, s, (rf_v4f *)a, n4, 0.f);
+        hipLaunchKernelGGL(roof_fill_kernel, grid, block, 0, s, (rf_v4f *)b, n4, 1.f);
+        hipLaunchKernelGGL(roof_fill_kernel, grid, block, 0, s, (rf_v4f *)c, n4, 2.f);
+        err = hipGetLastError();
+    }
+    float ms = 0.f;
+    if (err == hipSuccess) {
+        auto triad = [&]() {
+            hipLaunchKernelGGL(roof_stream_kernel<true>, grid, block, 0, s, (rf_v4f *)a, (const rf_v4f *)b,
+                               (const rf_v4f *)c, 3.0f, n4);
+        };
+        triad();
+        err = best_ms(triad, 5, s, &ms);
+        if (err == hipSuccess) *triad_gbs = 3.0 * 16.0 * n4 / (ms * 1e-3) / 1e9;
+    }
+    if (err == hipSuccess) {
+        auto copy = [&]() {
+            hipLaunchKernelGGL(roof_stream_kernel<false>, grid, block, 0, s, (rf_v4f *)a, (const rf_v4f *)b,
+                               (const rf_v4f *)c, 0.f, n4);
+        };
+        copy();
+        err = best_ms(copy, 5, s, &ms);
+        if (err == hipSuccess) *copy_gbs = 2.0 * 16.0 * n4 / (ms * 1e-3) / 1e9;
+    }
+    if (a) (void)hipFree(a);
+    if (b) (void)hipFree(b);
+    if (c) (void)hipFree(c);
+    return err;
+}
+
+}  // namespace pcl

@@ -106,6 +106,40 @@ done:
     return rc;
 }
 
+/* Each of `steps` steps between its own pair of events (recorded on the
+ * stream right before and after the step's launch): the average duration of
+ * one launch as a kernel trace sees it, without the gaps between launches. */
+static int time_each(step_fn fn, void *ctx, int warmup, int steps, double *us_avg) {
+    int rc = PCL_OK;
+    void **ev = calloc((size_t)2 * steps, sizeof(void *));
+    double tot = 0;
+    if (!ev) return PCL_ERR_OOM;
+    for (int i = 0; i < warmup; i++) TRY(fn(ctx, i));
+    for (int i = 0; i < 2 * steps; i++)
+        if (!(ev[i] = pcl_event_create())) {
+            rc = PCL_ERR_HIP;
+            goto done;
+        }
+    TRY(pcl_stream_synchronize());
+    for (int i = 0; i < steps; i++) {
+        TRY(pcl_event_record(ev[2 * i]));
+        TRY(fn(ctx, warmup + i));
+        TRY(pcl_event_record(ev[2 * i + 1]));
+    }
+    TRY(pcl_stream_synchronize());
+    for (int i = 0; i < steps; i++) {
+        float ms = 0.f;
+        TRY(pcl_event_elapsed_ms(ev[2 * i], ev[2 * i + 1], &ms));
+        tot += ms;
+    }
+    *us_avg = 1e3 * tot / steps;
+done:
+    for (int i = 0; i < 2 * steps; i++)
+        if (ev[i]) pcl_event_destroy(ev[i]);
+    free(ev);
+    return rc;
+}
+
 /* ------------------------------------------------------------ INT8 GEMM ---- */
 typedef struct {
     int M, N, K, out_mode, copies;
@@ -121,9 +155,11 @@ static int igemm_step(void *c_, int i) {
                             c->N, c->M, c->N, c->K, NULL);
 }
 
-/* out_mode: 0 int32 out, 1 per-column dequant, 2 per-row x per-column dequant */
-int pcl_bench_igemm(int M, int N, int K, int out_mode, int copies, int warmup, int steps,
-                    double *ms_total) {
+/* out_mode: 0 int32 out, 1 per-column dequant, 2 per-row x per-column dequant.
+ * ms_total: `steps` back-to-back launches; us_each (may be NULL): then the
+ * average of `steps` launches each timed on its own (time_each). */
+int pcl_bench_igemm_ex(int M, int N, int K, int out_mode, int copies, int warmup, int steps,
+                       double *ms_total, double *us_each) {
     int rc = PCL_OK;
     igemm_ctx c;
     memset(&c, 0, sizeof c);
@@ -147,10 +183,16 @@ int pcl_bench_igemm(int M, int N, int K, int out_mode, int copies, int warmup, i
         TRY(pcl_pack_b_s8(c.Bq, N, K, N, c.Bpk[j], NULL, NULL));
     }
     TRY(time_steps(igemm_step, &c, warmup, steps, ms_total));
+    if (us_each) TRY(time_each(igemm_step, &c, 0, steps, us_each));
 done:
     pcl_free(c.A), pcl_free(c.Bq), pcl_free(c.sa), pcl_free(c.sb), pcl_free(c.C);
     for (int j = 0; j < 8; j++) pcl_free(c.Bpk[j]);
     return rc;
+}
+
+int pcl_bench_igemm(int M, int N, int K, int out_mode, int copies, int warmup, int steps,
+                    double *ms_total) {
+    return pcl_bench_igemm_ex(M, N, K, out_mode, copies, warmup, steps, ms_total, NULL);
 }
 
 /* ------------------------------------------------------------ FP32 GEMM ---- */

@@ -104,6 +104,32 @@ def test_sgemm_ex_rejects_epilogue_operands_aliasing_c():
     L.pcl_clear_error()
 
 
+def test_roofs_and_groups_check_arguments_first():
+    import ctypes as C
+    L = pcl.lib
+    r = C.c_double(0)
+    assert L.pcl_measure_peak_mfma(3, C.byref(r)) == pcl.PCL_ERR_INVALID_ARG
+    assert L.pcl_measure_peak_mfma(0, None) == pcl.PCL_ERR_INVALID_ARG
+    assert L.pcl_measure_bandwidth(1 << 20, C.byref(r), C.byref(r)) == pcl.PCL_ERR_INVALID_ARG
+    h = C.c_void_p()
+    assert L.pcl_gemv_group_create(None, 0, C.byref(h)) == pcl.PCL_ERR_INVALID_ARG
+    fake = 1 << 20
+    bad = [pcl.GemvDesc(kind=7, M=1, N=4, K=4, X=fake, ldx=4, W=fake, ldw=4, Y=fake, ldy=4),
+           pcl.GemvDesc(kind=pcl.GEMV_F32_N, M=9, N=4, K=4, X=fake, ldx=4, W=fake, ldw=4, Y=fake, ldy=4),
+           pcl.GemvDesc(kind=pcl.GEMV_F32_N, M=1, N=6, K=4, X=fake, ldx=4, W=fake, ldw=6, Y=fake, ldy=6),
+           pcl.GemvDesc(kind=pcl.GEMV_F32_T, M=1, N=4, K=6, X=fake, ldx=6, W=fake, ldw=6, Y=fake, ldy=4),
+           pcl.GemvDesc(kind=pcl.GEMV_U8S8, M=1, N=4, K=300, X=fake, ldx=300, W=fake, ldw=304, Y=fake, ldy=4),
+           pcl.GemvDesc(kind=pcl.GEMV_F32_N, M=1, N=4, K=0, X=fake, ldx=4, W=fake, ldw=4, Y=fake, ldy=4)]
+    for d in bad:
+        arr = (pcl.GemvDesc * 1)(d)
+        assert L.pcl_gemv_group_create(arr, 1, C.byref(h)) == pcl.PCL_ERR_INVALID_ARG
+        assert not h.value
+    # 8 rows of 4096 fp32 activations would need 128 KB of LDS: refused
+    big = pcl.GemvDesc(kind=pcl.GEMV_F32_T, M=8, N=64, K=4096, X=fake, ldx=4096, W=fake, ldw=4096, Y=fake, ldy=64)
+    assert L.pcl_gemv_group_create((pcl.GemvDesc * 1)(big), 1, C.byref(h)) == pcl.PCL_ERR_RANGE
+    L.pcl_clear_error()
+
+
 def test_attention_dims_must_split_into_heads():
     """d_model must be a multiple of n_heads for the device attention drop-ins
     (otherwise the last d_model % n_heads columns would be silently ignored)."""
