@@ -409,6 +409,9 @@ CASES = {
                                                                11, w, s),
     "decode_group_int8_m8": lambda pcl, lib, w, s: gemv_group(pcl, lib, 2, 8, DECODE_LAYER * 16 + [(512, 2048)],
                                                                11, w, s),
+    "gemv_group_head_int8_m1": lambda pcl, lib, w, s: gemv_group(pcl, lib, 2, 1, [(1024, 50257)], 6, w, s),
+    "gemv_group_head_int8_m8": lambda pcl, lib, w, s: gemv_group(pcl, lib, 2, 8, [(1024, 50257)], 6, w, s),
+    "gemv_group_head_fp32_m1": lambda pcl, lib, w, s: gemv_group(pcl, lib, 1, 1, [(1024, 50257)], 3, w, s),
 }
 
 
@@ -477,10 +480,10 @@ def measured_roofs(pcl):
         r = d(0)
         pcl.check(pcl.lib.pcl_measure_peak_mfma(data, C.byref(r)))
         out[key] = round(r.value, 1)
-    tri, cp = d(0), d(0)
-    pcl.check(pcl.lib.pcl_measure_bandwidth(512 << 20, C.byref(tri), C.byref(cp)))
-    out["hbm_triad_GBps"] = round(tri.value, 1)
-    out["hbm_copy_GBps"] = round(cp.value, 1)
+    g = (d * 4)()
+    pcl.check(pcl.lib.pcl_measure_bandwidth(512 << 20, g))
+    for n, key in enumerate(("hbm_triad_GBps", "hbm_copy_GBps", "hbm_read_GBps", "hbm_write_GBps")):
+        out[key] = round(g[n], 1)
     return out
 
 

@@ -346,10 +346,11 @@ int pcl_gemv_u8s8_dq(const uint8_t *X, int ldx, const int8_t *Bpk, const int32_t
  * switching), 1 = i8 on zeros, 2 = f32 MFMA on uniform random floats. *rate in
  * TOP/s (i8) or TFLOP/s (f32); best of 5 launches. */
 int pcl_measure_peak_mfma(int data, double *rate);
-/* HBM: STREAM triad a = b + s*c (3 arrays of traffic) and a copy (2) over
- * arrays of bytes_per_array (at least 64 MiB; use > 256 MB to leave the
- * Infinity Cache), 16-byte accesses; best of 5, GB/s. Allocates the arrays. */
-int pcl_measure_bandwidth(long bytes_per_array, double *triad_gbs, double *copy_gbs);
+/* HBM over arrays of bytes_per_array (at least 64 MiB; use > 256 MB to leave
+ * the Infinity Cache), 16-byte non-temporal accesses, best of 5, in GB/s:
+ * gbs[0] STREAM triad a = b + s*c (3 arrays of traffic), gbs[1] copy (2),
+ * gbs[2] read only (1), gbs[3] write only (1). Allocates the arrays. */
+int pcl_measure_bandwidth(long bytes_per_array, double gbs[4]);
 
 /* ---- grouped decode GEMV: many independent products in one launch ----
  * Not a reference function: the reference runs its decode products one call

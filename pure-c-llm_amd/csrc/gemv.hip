@@ -1236,87 +1236,84 @@ __device__ __forceinline__ void gg_f32_t(const GgDesc &d, int strip, float *xs) 
     }
 }
 
-template <int MR>
-__device__ __forceinline__ void gg_u8s8(const GgDesc &d, int strip, int8_t *xs) {
-    const int tid = threadIdx.x, j = tid & 15, rs = tid >> 4;
-    constexpr int RPL = 2, UK = MR >= 4 ? 2 : 4;
-    const int M = d.M, N = d.N, ld = d.xld;
-    const int klen = (d.K + 15) & ~15;  // packed rows and staged rows are zero past K
-    const int n0 = strip * 32;
-    const int8_t *__restrict__ B = static_cast<const int8_t *>(d.W);
-    const int8_t *brow[RPL];
-#pragma unroll
-    for (int r = 0; r < RPL; r++) brow[r] = B + (long)min(n0 + rs + 16 * r, N - 1) * d.ldw;
-    auto load_batch = [&](v4i (&w)[UK][RPL], int k0) {
-#pragma unroll
-        for (int u = 0; u < UK; u++)
-#pragma unroll
-            for (int r = 0; r < RPL; r++)
-                w[u][r] = __builtin_nontemporal_load(reinterpret_cast<const v4i *>(brow[r] + min(k0 + 256 * u, klen - 16)));
-    };
-    v4i wn[UK][RPL];
-    load_batch(wn, 16 * j);
-    stage_rows<MR, true>(reinterpret_cast<uint8_t *>(xs), ld, ld, d.K, M, static_cast<const uint8_t *>(d.X),
-                         d.ldx);
-    __syncthreads();
+// GG_U8S8 through the matrix cores. A block owns 64 weight rows (16 per
+// wave, one tile of v_mfma_i32_16x16x64_i8) over the whole K, walked in
+// 256-byte K slices. A slice of a wave's 16 rows is read with four fully
+// coalesced loads (4 rows x 256 contiguous bytes each), the next slice's
+// loads issued before the current one is used, then turned into the
+// A-operand layout through a 4 KB LDS region private to the wave: chunk q of
+// row r is written at chunk q ^ r and read back by lane (i, g) as logical
+// chunk 4c + g of row i (16 rows at one logical chunk: 16 distinct bank
+// groups, both ways). A wave's LDS operations execute in order, so the
+// region needs no barrier between a slice's reads and the next slice's
+// writes. The activation rows are staged once per block in LDS, re-centred
+// (x ^ 0x80 = x - 128 as s8) and zero past K; lane (m, g) of the B operand
+// reads the same bytes of row m % MR, so every integer product pairs the
+// same k whatever order the hardware sums in. D[i][m] lands in lane
+// 16*(i/4) + m, register i % 4. Rows past N load row N-1 and columns m >= M
+// come from a repeated row; neither is stored.
+constexpr int GGQ_RB = 64;      // rows per block
+constexpr int GGQ_SL = 256;     // bytes of K per slice
+constexpr int GGQ_WREG = 16 * GGQ_SL;  // LDS bytes per wave
 
-    int32_t acc[RPL][MR];
+__host__ __device__ inline int ggq_x_bytes(int mr, int K) { return (mr * ((K + 255) / 256 * 256 + 16) + 15) / 16 * 16; }
+int ggq_lds_bytes(int mr, int K) { return ggq_x_bytes(mr, K) + 4 * GGQ_WREG; }
+
+template <int MR>
+__device__ __forceinline__ void gg_u8s8(const GgDesc &d, int strip, int8_t *lds) {
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int ri = lane & 15, g = lane >> 4;
+    const int M = d.M, N = d.N;
+    const int Kp = (d.K + 255) & ~255;  // packed rows are zero from K to Kp (ldw >= Kp)
+    const int nsl = Kp / GGQ_SL;
+    const int xld = Kp + 16;
+    const int n0 = strip * GGQ_RB;
+    int8_t *xs = lds;
+    int8_t *wreg = lds + ggq_x_bytes(MR, d.K) + wv * GGQ_WREG;
+    const int8_t *__restrict__ B = static_cast<const int8_t *>(d.W);
+    // load u of a slice: row 4u + lane/16 of the wave's tile, bytes 16*(lane%16)
+    const int8_t *src[4];
+    int8_t *wdst[4];
 #pragma unroll
-    for (int r = 0; r < RPL; r++)
+    for (int u = 0; u < 4; u++) {
+        const int r = 4 * u + g;
+        src[u] = B + (long)min(n0 + 16 * wv + r, N - 1) * d.ldw + 16 * ri;
+        wdst[u] = wreg + r * GGQ_SL + ((ri ^ r) << 4);
+    }
+    auto load = [&](v4i (&w)[4], int t) {
 #pragma unroll
-        for (int m = 0; m < MR; m++) acc[r][m] = 0;
-    for (int k0 = 16 * j; k0 < klen; k0 += 256 * UK) {
-        v4i w[UK][RPL];
+        for (int u = 0; u < 4; u++) w[u] = __builtin_nontemporal_load(reinterpret_cast<const v4i *>(src[u] + t * GGQ_SL));
+    };
+    // the first slice is in flight while the activations are staged
+    v4i wn[4];
+    load(wn, 0);
+    stage_rows<MR, true>(reinterpret_cast<uint8_t *>(xs), xld, Kp, d.K, M, static_cast<const uint8_t *>(d.X), d.ldx);
+    __syncthreads();
+    const int8_t *xr = xs + (ri % MR) * xld + 16 * g;
+    v4i acc = {0, 0, 0, 0};
+    for (int t = 0; t < nsl; t++) {
+        v4i w[4];
 #pragma unroll
-        for (int u = 0; u < UK; u++)
+        for (int u = 0; u < 4; u++) w[u] = wn[u];
+        if (t + 1 < nsl) load(wn, t + 1);
 #pragma unroll
-            for (int r = 0; r < RPL; r++) w[u][r] = wn[u][r];
-        if (k0 + 256 * UK < klen) load_batch(wn, k0 + 256 * UK);
+        for (int u = 0; u < 4; u++) *reinterpret_cast<v4i *>(wdst[u]) = w[u];
 #pragma unroll
-        for (int u = 0; u < UK; u++) {
-            const int k = k0 + 256 * u;
-            if (k < klen) {
-#pragma unroll
-                for (int m = 0; m < MR; m++) {
-                    const v4i xv = *reinterpret_cast<const v4i *>(&xs[m * ld + k]);
-#pragma unroll
-                    for (int r = 0; r < RPL; r++) {
-                        int a = acc[r][m];
-                        a = __builtin_amdgcn_sdot4(xv[0], w[u][r][0], a, false);
-                        a = __builtin_amdgcn_sdot4(xv[1], w[u][r][1], a, false);
-                        a = __builtin_amdgcn_sdot4(xv[2], w[u][r][2], a, false);
-                        a = __builtin_amdgcn_sdot4(xv[3], w[u][r][3], a, false);
-                        acc[r][m] = a;
-                    }
-                }
-            }
+        for (int c = 0; c < 4; c++) {
+            const v4i a = *reinterpret_cast<const v4i *>(wreg + ri * GGQ_SL + (((4 * c + g) ^ ri) << 4));
+            const v4i b = *reinterpret_cast<const v4i *>(xr + t * GGQ_SL + 64 * c);
+            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc, 0, 0, 0);
         }
     }
+    const int m = lane & 15;
+    if (m < M) {
 #pragma unroll
-    for (int r = 0; r < RPL; r++)
-#pragma unroll
-        for (int m = 0; m < MR; m++) {
-            int v = acc[r][m];
-            v += __shfl_xor(v, 8, 16);
-            v += __shfl_xor(v, 4, 16);
-            v += __shfl_xor(v, 2, 16);
-            v += __shfl_xor(v, 1, 16);
-            acc[r][m] = v;
-        }
-    if (j == 0) {
-#pragma unroll
-        for (int r = 0; r < RPL; r++) {
-            const int n = n0 + rs + 16 * r;
-#pragma unroll
-            for (int m = 0; m < MR; m++) {
-                if (m < M && n < N) {
-                    if (d.out_mode == 0)
-                        igemv_write<0>(d.Y, d.ldy, m, n, acc[r][m], d.col_off, d.sa, d.sb);
-                    else if (d.out_mode == 1)
-                        igemv_write<1>(d.Y, d.ldy, m, n, acc[r][m], d.col_off, d.sa, d.sb);
-                    else
-                        igemv_write<2>(d.Y, d.ldy, m, n, acc[r][m], d.col_off, d.sa, d.sb);
-                }
+        for (int r = 0; r < 4; r++) {
+            const int n = n0 + 16 * wv + 4 * g + r;
+            if (n < N) {
+                if (d.out_mode == 0) igemv_write<0>(d.Y, d.ldy, m, n, acc[r], d.col_off, d.sa, d.sb);
+                else if (d.out_mode == 1) igemv_write<1>(d.Y, d.ldy, m, n, acc[r], d.col_off, d.sa, d.sb);
+                else igemv_write<2>(d.Y, d.ldy, m, n, acc[r], d.col_off, d.sa, d.sb);
             }
         }
     }
@@ -1334,12 +1331,53 @@ __global__ __launch_bounds__(GV_THREADS) void gemv_group_kernel(const GgDesc *__
     else gg_u8s8<MR>(d, it.y, reinterpret_cast<int8_t *>(gv_dyn));
 }
 
-int gg_strip_rows(int kind) { return kind == GG_F32_N ? 64 : 32; }
+// One product, descriptor by value (no device table): block b = strip b.
+template <int MR>
+__global__ __launch_bounds__(GV_THREADS) void gemv_one_u8s8_kernel(GgDesc d) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char gv_dyn[];
+    gg_u8s8<MR>(d, blockIdx.x, reinterpret_cast<int8_t *>(gv_dyn));
+}
+
+bool igemv_mfma_fits(int M, int N, int K, long ldb) {
+    const int mr = M <= 1 ? 1 : (M <= 2 ? 2 : (M <= 4 ? 4 : 8));
+    return M >= 1 && M <= 8 && K >= 1 && (long)N * ldb < (1L << 31) && ldb >= ((K + 255) & ~255) &&
+           ggq_lds_bytes(mr, K) <= 65536;
+}
+
+hipError_t launch_igemv_mfma(int out_mode, int M, int N, int K, const uint8_t *X, long ldx,
+                             const int8_t *Bpk, long ldb, const int32_t *col_off, const float *sa,
+                             const float *sb, void *Y, long ldy, hipStream_t s) {
+    if (M <= 0 || N <= 0) return hipSuccess;
+    if (!igemv_mfma_fits(M, N, K, ldb)) return hipErrorInvalidValue;
+    GgDesc d = {};
+    d.kind = GG_U8S8, d.M = M, d.N = N, d.K = K;
+    d.X = X, d.ldx = ldx, d.W = Bpk, d.ldw = ldb;
+    d.col_off = col_off, d.sa = sa, d.sb = sb, d.Y = Y, d.ldy = ldy;
+    d.out_mode = out_mode;
+    d.xld = gg_stage_ld(GG_U8S8, K);
+    const dim3 grid(cdiv(N, GGQ_RB)), block(GV_THREADS);
+    const int mr = M <= 1 ? 1 : (M <= 2 ? 2 : (M <= 4 ? 4 : 8));
+    const size_t lds = (size_t)ggq_lds_bytes(mr, K);
+    switch (mr) {
+        case 1: hipLaunchKernelGGL(gemv_one_u8s8_kernel<1>, grid, block, lds, s, d); break;
+        case 2: hipLaunchKernelGGL(gemv_one_u8s8_kernel<2>, grid, block, lds, s, d); break;
+        case 4: hipLaunchKernelGGL(gemv_one_u8s8_kernel<4>, grid, block, lds, s, d); break;
+        default: hipLaunchKernelGGL(gemv_one_u8s8_kernel<8>, grid, block, lds, s, d); break;
+    }
+    return hipGetLastError();
+}
+
+int gg_strip_rows(int kind) { return kind == GG_F32_T ? 32 : (kind == GG_F32_N ? 64 : GGQ_RB); }
 
 int gg_stage_ld(int kind, int K) {
     if (kind == GG_F32_N) return 16 * ((cdiv(K, 16) + 7) / 8 * 8);
     if (kind == GG_F32_T) return (K + 63) / 64 * 64;
-    return (K + 255) / 256 * 256;
+    return (K + 255) / 256 * 256 + 16;
+}
+
+size_t gg_lds_bytes(int kind, int K, int mr) {
+    if (kind == GG_U8S8) return (size_t)ggq_lds_bytes(mr, K);
+    return (size_t)mr * gg_stage_ld(kind, K) * 4;
 }
 
 hipError_t launch_gemv_group(const GgDesc *descs, const int2 *items, int n_items, int mr,

@@ -122,8 +122,9 @@ int sgemv_xf(int xf, int N, int K, const float *X, const float *W, int ldw,
 // kind 0: i8 MFMA, random bytes; 1: i8 MFMA, zeros; 2: f32 MFMA, random;
 // rate in TOP/s or TFLOP/s over `cus` workgroups of eight waves.
 hipError_t measure_peak_mfma(int kind, int cus, double *rate, hipStream_t s);
-// STREAM triad and copy over arrays of bytes_per_array (GB/s).
-hipError_t measure_bandwidth(long bytes_per_array, double *triad_gbs, double *copy_gbs, hipStream_t s);
+// GB/s over arrays of bytes_per_array: gbs[0] STREAM triad, [1] copy, [2]
+// read only, [3] write only.
+hipError_t measure_bandwidth(long bytes_per_array, double gbs[4], hipStream_t s);
 
 // ---- GEMV (gemv.hip) ----
 GemvPlan plan_sgemv(int w_trans, int M, int N, int K);
@@ -132,7 +133,7 @@ GemvPlan plan_sgemv(int w_trans, int M, int N, int K);
 // float(v)*sb[n], 2 float(v)*(sa[m]*sb[n]); xld: staged activation row stride
 // (elements) = gg_stage_ld(kind, K). Work items are int2 {product, strip} with
 // strips of gg_strip_rows(kind) outputs; lds_bytes = max over products of
-// mr * xld * element size; mr in {1, 2, 4, 8} >= every product's M.
+// gg_lds_bytes(kind, K, mr); mr in {1, 2, 4, 8} >= every product's M.
 enum { GG_F32_N = 0, GG_F32_T = 1, GG_U8S8 = 2 };
 struct GgDesc {
     int kind, M, N, K;
@@ -149,8 +150,18 @@ struct GgDesc {
 };
 int gg_strip_rows(int kind);
 int gg_stage_ld(int kind, int K);
+// dynamic LDS a product needs in a group whose largest M rounds to mr
+size_t gg_lds_bytes(int kind, int K, int mr);
 hipError_t launch_gemv_group(const GgDesc *descs, const int2 *items, int n_items, int mr,
                              size_t lds_bytes, hipStream_t s);
+// One INT8 GEMV (M <= 8 rows) on the matrix-core path of the grouped kernel:
+// whole-K blocks of 64 weight rows, no split, no workspace. Applicable when
+// igemv_mfma_fits (32-bit row offsets, packed rows ldb >= roundup(K, 256),
+// staged operands within 64 KB of LDS).
+bool igemv_mfma_fits(int M, int N, int K, long ldb);
+hipError_t launch_igemv_mfma(int out_mode, int M, int N, int K, const uint8_t *X, long ldx,
+                             const int8_t *Bpk, long ldb, const int32_t *col_off, const float *sa,
+                             const float *sb, void *Y, long ldy, hipStream_t s);
 // Size of the static split-K scratch of the allocation-free GEMV entry point,
 // and its device address on the current device (hipGetSymbolAddress).
 constexpr size_t GEMV_NOALLOC_SCRATCH_BYTES = (size_t)4 << 20;

@@ -499,12 +499,12 @@ int pcl_measure_peak_mfma(int data, double *rate) {
     return PCL_OK;
 }
 
-int pcl_measure_bandwidth(long bytes_per_array, double *triad_gbs, double *copy_gbs) {
-    CHECK_ARG(triad_gbs && copy_gbs, "pcl_measure_bandwidth: NULL result pointer");
+int pcl_measure_bandwidth(long bytes_per_array, double gbs[4]) {
+    CHECK_ARG(gbs != nullptr, "pcl_measure_bandwidth: NULL result pointer");
     CHECK_ARG(bytes_per_array >= (64L << 20), "pcl_measure_bandwidth: arrays of at least 64 MiB (got %ld)",
               bytes_per_array);
     PCL_OK_OR_RETURN(do_init());
-    HIP_OK(pcl::measure_bandwidth(bytes_per_array, triad_gbs, copy_gbs, pick(nullptr)));
+    HIP_OK(pcl::measure_bandwidth(bytes_per_array, gbs, pick(nullptr)));
     return PCL_OK;
 }
 
@@ -520,7 +520,6 @@ int pcl_gemv_group_create(const pcl_gemv_desc *descs, int n, pcl_gemv_group **gr
     };
     std::vector<Item> items;
     int mr = 1;
-    size_t stage_max = 0;
     for (int i = 0; i < n; i++) {
         const pcl_gemv_desc &q = descs[i];
         CHECK_ARG(q.kind == PCL_GEMV_F32_N || q.kind == PCL_GEMV_F32_T || q.kind == PCL_GEMV_U8S8,
@@ -531,7 +530,6 @@ int pcl_gemv_group_create(const pcl_gemv_desc *descs, int n, pcl_gemv_group **gr
         CHECK_ARG(q.X && q.W && q.Y, "pcl_gemv_group_create: product %d: NULL operand", i);
         CHECK_ARG(q.ldy >= q.N, "pcl_gemv_group_create: product %d: ldy=%d < N=%d", i, q.ldy, q.N);
         CHECK_ARG(q.ldx >= q.K, "pcl_gemv_group_create: product %d: ldx=%d < K=%d", i, q.ldx, q.K);
-        size_t elt = 4;
         if (q.kind == PCL_GEMV_F32_N) {
             CHECK_ARG(q.N % 4 == 0 && q.ldw >= q.N && q.ldw % 4 == 0 && aligned16(q.W),
                       "pcl_gemv_group_create: product %d: F32_N needs N %% 4 == 0, ldw >= N, ldw %% 4 "
@@ -548,7 +546,6 @@ int pcl_gemv_group_create(const pcl_gemv_desc *descs, int n, pcl_gemv_group **gr
                       "(a multiple of 16) and a 16-byte aligned W (ldw=%d)",
                       i, kpad256(q.K), q.ldw);
             CHECK_ARG(q.sb || !q.sa, "pcl_gemv_group_create: product %d: sa without sb", i);
-            elt = 1;
         }
         pcl::GgDesc &g = dd[(size_t)i];
         g.kind = q.kind == PCL_GEMV_F32_N ? pcl::GG_F32_N : (q.kind == PCL_GEMV_F32_T ? pcl::GG_F32_T : pcl::GG_U8S8);
@@ -564,19 +561,24 @@ int pcl_gemv_group_create(const pcl_gemv_desc *descs, int n, pcl_gemv_group **gr
         g.pad_ = 0;
         const int m1 = q.M <= 1 ? 1 : (q.M <= 2 ? 2 : (q.M <= 4 ? 4 : 8));
         if (m1 > mr) mr = m1;
-        if ((size_t)g.xld * elt > stage_max) stage_max = (size_t)g.xld * elt;
+        CHECK_ARG((long)q.N * q.ldw < (1L << 31),
+                  "pcl_gemv_group_create: product %d: N * ldw must stay below 2^31 bytes", i);
         const int rows = pcl::gg_strip_rows(g.kind);
         const int strips = (q.N + rows - 1) / rows;
         const long bytes = (long)rows * (q.kind == PCL_GEMV_U8S8 ? g.ldw : 4L * q.K);
         for (int t = 0; t < strips; t++) items.push_back({bytes, i, t});
         CHECK_ARG(items.size() < (size_t)(1 << 30), "pcl_gemv_group_create: too many work items");
     }
-    const size_t lds = (size_t)mr * stage_max;
-    if (lds > 65536)
+    size_t lds = 0;
+    for (int i = 0; i < n; i++) {
+        const size_t b = pcl::gg_lds_bytes(dd[(size_t)i].kind, dd[(size_t)i].K, mr);
+        if (b > lds) lds = b;
+    }
+    if (lds > 65536 + 49152)
         return set_error(PCL_ERR_RANGE,
-                         "pcl_gemv_group_create: staged activations need %zu bytes of LDS (at most 65536): "
-                         "reduce K or M, or split the group",
-                         lds);
+                         "pcl_gemv_group_create: staged operands need %zu bytes of LDS per block (at most "
+                         "%d): reduce K or M, or split the group",
+                         lds, 65536 + 49152);
     // largest blocks first, so the tail of the launch is short ones
     std::stable_sort(items.begin(), items.end(), [](const Item &a, const Item &b) { return a.bytes > b.bytes; });
     std::vector<int2> it(items.size());
@@ -863,6 +865,14 @@ static int igemm_common(int out_mode, const uint8_t *A, int lda, const int8_t *B
     PCL_OK_OR_RETURN(do_init());
     const long ldb = kpad256(K);
     hipStream_t s = pick(stream);
+    // Decode rows: with 4-8 rows the matrix-core GEMV (one MFMA per 64 bytes
+    // of 16 weight rows, coalesced loads) beats the dot-product kernel, whose
+    // per-row work grows with M; with 1-2 rows the dot-product kernel streams
+    // slightly faster.
+    if (M >= 4 && M <= 8 && K > 0 && pcl::igemv_mfma_fits(M, N, K, ldb)) {
+        HIP_OK(pcl::launch_igemv_mfma(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa, sb, C, ldc, s));
+        return PCL_OK;
+    }
     if (M <= 8) {
         pcl::GemvPlan p = pcl::plan_igemv(M, N, K);
         StreamScratch *sc;

@@ -12,9 +12,10 @@
 // GEMM sees: uniformly random bytes (the gemm_bench INT8 workload) or zeros
 // for i8, uniform random floats for f32.
 //
-// HBM: the triad a[i] = b[i] + s*c[i] over three arrays far larger than the
-// 256 MB Infinity Cache, and a plain copy, with 16-byte accesses,
-// grid-stride; best of several passes (as gemm_bench's best of 5).
+// HBM: the triad a[i] = b[i] + s*c[i] over arrays far larger than the 256 MB
+// Infinity Cache, a copy, a read-only and a write-only pass, with 16-byte
+// non-temporal accesses, grid-stride; best of several passes (as gemm_bench's
+// best of 5). The read-only rate is the roof of the weight-streaming GEMVs.
 #include "internal.h"
 
 namespace pcl {
@@ -99,14 +100,41 @@ __global__ __launch_bounds__(64 * RF_WAVES) void roof_f32_kernel(float *out, uns
     out[blockIdx.x * blockDim.x + threadIdx.x] = t;
 }
 
-// a[i] = b[i] + s * c[i] (triad) or a[i] = b[i] (copy), n4 16-byte elements
-template <bool TRIAD>
+// Streaming kernels over n4 16-byte elements, grid-stride with RF_U
+// independent elements per thread per iteration (all loads issued before any
+// use) and non-temporal accesses, so each CU keeps enough reads in flight.
+// mode 0: a = b + s*c (triad); 1: a = b (copy); 2: read b (one value per
+// thread written); 3: write a.
+constexpr int RF_U = 4;
+template <int MODE>
 __global__ __launch_bounds__(256) void roof_stream_kernel(rf_v4f *__restrict__ a, const rf_v4f *__restrict__ b,
-                                                          const rf_v4f *__restrict__ c, float sc, long n4) {
-    for (long i = blockIdx.x * 256L + threadIdx.x; i < n4; i += (long)gridDim.x * 256) {
-        const rf_v4f x = b[i];
-        a[i] = TRIAD ? x + sc * c[i] : x;
+                                                          const rf_v4f *__restrict__ c, float sc, long n4,
+                                                          float *__restrict__ sink) {
+    const long stride = (long)gridDim.x * 256;
+    rf_v4f acc = {0.f, 0.f, 0.f, 0.f};
+    long i = blockIdx.x * 256L + threadIdx.x;
+    for (; i + (RF_U - 1) * stride < n4; i += RF_U * stride) {
+        rf_v4f x[RF_U], y[RF_U];
+#pragma unroll
+        for (int u = 0; u < RF_U; u++) {
+            if (MODE != 3) x[u] = __builtin_nontemporal_load(b + i + u * stride);
+            if (MODE == 0) y[u] = __builtin_nontemporal_load(c + i + u * stride);
+        }
+#pragma unroll
+        for (int u = 0; u < RF_U; u++) {
+            if (MODE == 0) __builtin_nontemporal_store(x[u] + sc * y[u], a + i + u * stride);
+            else if (MODE == 1) __builtin_nontemporal_store(x[u], a + i + u * stride);
+            else if (MODE == 2) acc += x[u];
+            else __builtin_nontemporal_store(rf_v4f{sc, sc, sc, sc}, a + i + u * stride);
+        }
     }
+    for (; i < n4; i += stride) {
+        if (MODE == 0) a[i] = b[i] + sc * c[i];
+        else if (MODE == 1) a[i] = b[i];
+        else if (MODE == 2) acc += b[i];
+        else a[i] = rf_v4f{sc, sc, sc, sc};
+    }
+    if (MODE == 2) sink[blockIdx.x * 256 + threadIdx.x] = acc[0] + acc[1] + acc[2] + acc[3];
 }
 
 __global__ void roof_fill_kernel(rf_v4f *p, long n4, float v) {
@@ -165,41 +193,42 @@ hipError_t measure_peak_mfma(int kind, int cus, double *rate, hipStream_t s) {
     return err;
 }
 
-hipError_t measure_bandwidth(long bytes_per_array, double *triad_gbs, double *copy_gbs, hipStream_t s) {
+hipError_t measure_bandwidth(long bytes_per_array, double gbs[4], hipStream_t s) {
     const long n4 = bytes_per_array / 16;
-    void *a = nullptr, *b = nullptr, *c = nullptr;
+    const int GRID = 4096;
+    void *a = nullptr, *b = nullptr, *c = nullptr, *sink = nullptr;
     hipError_t err = hipMalloc(&a, n4 * 16);
     if (err == hipSuccess) err = hipMalloc(&b, n4 * 16);
     if (err == hipSuccess) err = hipMalloc(&c, n4 * 16);
-    const dim3 grid(8192), block(256);
+    if (err == hipSuccess) err = hipMalloc(&sink, (size_t)GRID * 256 * 4);
+    const dim3 grid(GRID), block(256);
     if (err == hipSuccess) {
         hipLaunchKernelGGL(roof_fill_kernel, grid, block, 0, s, (rf_v4f *)a, n4, 0.f);
         hipLaunchKernelGGL(roof_fill_kernel, grid, block, 0, s, (rf_v4f *)b, n4, 1.f);
         hipLaunchKernelGGL(roof_fill_kernel, grid, block, 0, s, (rf_v4f *)c, n4, 2.f);
         err = hipGetLastError();
     }
-    float ms = 0.f;
-    if (err == hipSuccess) {
-        auto triad = [&]() {
-            hipLaunchKernelGGL(roof_stream_kernel<true>, grid, block, 0, s, (rf_v4f *)a, (const rf_v4f *)b,
-                               (const rf_v4f *)c, 3.0f, n4);
+    // bytes moved per pass: triad 3 arrays, copy 2, read 1, write 1
+    const double arrays[4] = {3.0, 2.0, 1.0, 1.0};
+    for (int mode = 0; mode < 4 && err == hipSuccess; mode++) {
+        auto pass = [&]() {
+            rf_v4f *A = (rf_v4f *)a;
+            const rf_v4f *B = (const rf_v4f *)b, *Cc = (const rf_v4f *)c;
+            float *Sk = (float *)sink;
+            if (mode == 0) hipLaunchKernelGGL(roof_stream_kernel<0>, grid, block, 0, s, A, B, Cc, 3.0f, n4, Sk);
+            else if (mode == 1) hipLaunchKernelGGL(roof_stream_kernel<1>, grid, block, 0, s, A, B, Cc, 0.f, n4, Sk);
+            else if (mode == 2) hipLaunchKernelGGL(roof_stream_kernel<2>, grid, block, 0, s, A, B, Cc, 0.f, n4, Sk);
+            else hipLaunchKernelGGL(roof_stream_kernel<3>, grid, block, 0, s, A, B, Cc, 5.0f, n4, Sk);
         };
-        triad();
-        err = best_ms(triad, 5, s, &ms);
-        if (err == hipSuccess) *triad_gbs = 3.0 * 16.0 * n4 / (ms * 1e-3) / 1e9;
-    }
-    if (err == hipSuccess) {
-        auto copy = [&]() {
-            hipLaunchKernelGGL(roof_stream_kernel<false>, grid, block, 0, s, (rf_v4f *)a, (const rf_v4f *)b,
-                               (const rf_v4f *)c, 0.f, n4);
-        };
-        copy();
-        err = best_ms(copy, 5, s, &ms);
-        if (err == hipSuccess) *copy_gbs = 2.0 * 16.0 * n4 / (ms * 1e-3) / 1e9;
+        pass();
+        float ms = 0.f;
+        err = best_ms(pass, 5, s, &ms);
+        if (err == hipSuccess) gbs[mode] = arrays[mode] * 16.0 * n4 / (ms * 1e-3) / 1e9;
     }
     if (a) (void)hipFree(a);
     if (b) (void)hipFree(b);
     if (c) (void)hipFree(c);
+    if (sink) (void)hipFree(sink);
     return err;
 }
 

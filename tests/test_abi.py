@@ -110,7 +110,7 @@ def test_roofs_and_groups_check_arguments_first():
     r = C.c_double(0)
     assert L.pcl_measure_peak_mfma(3, C.byref(r)) == pcl.PCL_ERR_INVALID_ARG
     assert L.pcl_measure_peak_mfma(0, None) == pcl.PCL_ERR_INVALID_ARG
-    assert L.pcl_measure_bandwidth(1 << 20, C.byref(r), C.byref(r)) == pcl.PCL_ERR_INVALID_ARG
+    assert L.pcl_measure_bandwidth(1 << 20, (C.c_double * 4)()) == pcl.PCL_ERR_INVALID_ARG
     h = C.c_void_p()
     assert L.pcl_gemv_group_create(None, 0, C.byref(h)) == pcl.PCL_ERR_INVALID_ARG
     fake = 1 << 20
