@@ -170,6 +170,27 @@ def test_igemm_dequant_bit_exact(M, N, K):
     np.testing.assert_array_equal(C[rows], ob.dequant((V + off).astype(np.int32), None, sb))
 
 
+# BASELINE config 3, INT8: the grown model's prefill GEMMs at T = 256
+# (d_model 512, d_ff 2048): QKV, attention output, FFN up, FFN down, with
+# per-token u8 activations and per-channel s8 weights, dequantised by
+# sa[m] * sb[n] (transformer.c:123-158; gemm_bench.c:272-275). Every output
+# is compared, int32 and dequantised, against the exact integer oracle.
+GROWN_PREFILL = [("qkv", 256, 1536, 512), ("attn_out", 256, 512, 512), ("ffn_up", 256, 2048, 512),
+                 ("ffn_down", 256, 512, 2048)]
+
+
+@pytest.mark.parametrize("name,M,N,K", GROWN_PREFILL)
+def test_igemm_grown_prefill_bit_exact(name, M, N, K):
+    Au = ob.u8((M, K), 90 + K)
+    Bq = ob.s8((K, N), 91 + N)
+    sa = ob.uniform((M,), 92, 1e-3, 1e-2)
+    sb = ob.uniform((N,), 93, 1e-3, 1e-2)
+    V = ob.gemm_u8s8_i32(Au, Bq)
+    announce("igemm grown prefill", name, M, N, K)
+    np.testing.assert_array_equal(igemm_i32(Au, Bq), V)
+    np.testing.assert_array_equal(_dq_run(Au, Bq, sa, sb), ob.dequant(V, sa, sb))
+
+
 @pytest.mark.parametrize("M", [3, 40])
 def test_int8_k0(M):
     # K == 0 reads no activation (NULL A): v = 0, so C = float(col_off) * dq
@@ -193,8 +214,8 @@ def test_int8_k0(M):
     np.testing.assert_array_equal(dI.download((M, N), np.int32), np.zeros((M, N), np.int32))
 
 
-@pytest.mark.parametrize("M,N,K", [(2048, 2048, 2048), (4096, 3072, 1024), (4096, 1024, 4096),
-                                   (4096, 50257, 1024)])
+@pytest.mark.parametrize("M,N,K", [(2048, 2048, 2048), (4096, 3072, 1024), (4096, 1024, 1024),
+                                   (4096, 4096, 1024), (4096, 1024, 4096), (4096, 50257, 1024)])
 def test_igemm_full_size_checksums(M, N, K):
     # size-independent exact properties at the configs' full sizes
     Au = ob.u8((M, K), 60 + K)

@@ -145,6 +145,8 @@ def test_sgemm_deterministic():
 # trainer's backward layouts dX = dY.W^T (NT) and dW = X^T.dY (TN).
 FULL = [
     ("qkv", N_, N_, 4096, 3072, 1024),
+    ("attn_out", N_, N_, 4096, 1024, 1024),
+    ("ff1", N_, N_, 4096, 4096, 1024),
     ("ff2", N_, N_, 4096, 1024, 4096),
     ("head", N_, T_, 4096, 50257, 1024),
     ("dX_ff1", N_, T_, 4096, 1024, 4096),
