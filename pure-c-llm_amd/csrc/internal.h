@@ -49,6 +49,9 @@ hipError_t launch_sgemm(const SgemmPlan &p, bool a_kcontig, bool b_kcontig, int 
                         int accumulate, float *C, long ldc, const Workspace &ws,
                         hipStream_t stream, int epi = EPI_NONE, const float *aux_in = nullptr,
                         float *aux_out = nullptr, long ld_aux = 0);
+// dst (rows x cols, ldd % 4 == 0, 16-byte aligned) <- src (lds, any alignment)
+hipError_t launch_copy_rows(float *dst, long ldd, const float *src, long lds, int rows, int cols,
+                            hipStream_t stream);
 // op 0: out = gelu(a); 1: out = a * gelu'(b) (a = upstream gradient, b =
 // pre-activation); 2: out = a + b -- n elements (gpu_kernels.cu:228-251)
 hipError_t launch_elementwise(int op, long n, float *out, const float *a, const float *b,

@@ -655,6 +655,66 @@ int pcl_sgemv_noalloc(int opW, int M, int N, int K, const float *X, int ldx, con
     return PCL_OK;
 }
 
+// A large product whose operands miss the LDS-DMA kernel's requirements
+// (16-byte aligned rows, contiguous extents a multiple of 4 floats, K a
+// multiple of 32), e.g. the trainer's head backward over 50257-float logits
+// rows (train_kaggle.cu:173-174 through gemm_nn / gemm_tn): each misaligned
+// operand is copied into rows of a multiple of 64 floats (one pass into the
+// stream's workspace, launch_copy_rows), the 64-aligned core (M1 x N1 x K1) runs
+// on the LDS-DMA kernel, and the ragged edges -- the K tail of the core,
+// added on; the rows past M1 and the columns past N1 at full K -- run on the
+// generic kernel with the original operands. Returns 1 when the shape has no
+// aligned core (the caller takes the generic kernel instead).
+static int sgemm_realigned(int opA, int opB, int M, int N, int K, const float *A, int lda,
+                           const float *B, int ldb, const float *bias, int accumulate, float *C,
+                           int ldc, hipStream_t s) {
+    const bool a_kc = opA == PCL_OP_N, b_kc = opB == PCL_OP_T;  // K-contiguous operands
+    const int K1 = K & ~63, M1 = a_kc ? M : (M & ~63), N1 = b_kc ? N : (N & ~63);
+    if (K1 == 0 || M1 == 0 || N1 == 0) return 1;
+    const long rows_a = a_kc ? M : K, cols_a = a_kc ? K : M;
+    const long rows_b = b_kc ? N : K, cols_b = b_kc ? K : N;
+    const bool copy_a = !aligned16(A) || lda % 4 != 0, copy_b = !aligned16(B) || ldb % 4 != 0;
+    const long lda2 = copy_a ? (cols_a + 63) / 64 * 64 : lda, ldb2 = copy_b ? (cols_b + 63) / 64 * 64 : ldb;
+    const size_t abytes = copy_a ? (size_t)rows_a * lda2 * 4 : 0, bbytes = copy_b ? (size_t)rows_b * ldb2 * 4 : 0;
+    const pcl::SgemmPlan pc = pcl::plan_sgemm(M1, N1, K1);
+    const pcl::SgemmPlan pk = pcl::plan_sgemm(M1, N1, K - K1);
+    const pcl::SgemmPlan pm = pcl::plan_sgemm(M - M1, N, K);
+    const pcl::SgemmPlan pn = pcl::plan_sgemm(M1, N - N1, K);
+    size_t part = pc.part_bytes;
+    if (K > K1 && pk.part_bytes > part) part = pk.part_bytes;
+    if (M > M1 && pm.part_bytes > part) part = pm.part_bytes;
+    if (N > N1 && pn.part_bytes > part) part = pn.part_bytes;
+    StreamScratch *sc;
+    PCL_OK_OR_RETURN(get_scratch(s, part, abytes + bbytes + 256, &sc));
+    float *Ac = const_cast<float *>(A), *Bc = const_cast<float *>(B);
+    if (copy_a) {
+        Ac = static_cast<float *>(sc->aux);
+        HIP_OK(pcl::launch_copy_rows(Ac, lda2, A, lda, (int)rows_a, (int)cols_a, s));
+    }
+    if (copy_b) {
+        Bc = reinterpret_cast<float *>(static_cast<char *>(sc->aux) + (abytes + 255) / 256 * 256);
+        HIP_OK(pcl::launch_copy_rows(Bc, ldb2, B, ldb, (int)rows_b, (int)cols_b, s));
+    }
+    // the aligned core, then its K tail added on
+    HIP_OK(pcl::launch_sgemm(pc, a_kc, b_kc, M1, N1, K1, Ac, lda2, Bc, ldb2, bias, accumulate, C, ldc, sc->ws, s));
+    if (K > K1) {
+        const float *Ak = a_kc ? A + K1 : A + (size_t)K1 * lda;
+        const float *Bk = b_kc ? B + K1 : B + (size_t)K1 * ldb;
+        HIP_OK(pcl::launch_sgemm(pk, a_kc, b_kc, M1, N1, K - K1, Ak, lda, Bk, ldb, nullptr, 1, C, ldc, sc->ws, s));
+    }
+    if (M > M1) {  // rows M1.. of C, every column, full K
+        const float *Am = a_kc ? A + (size_t)M1 * lda : A + M1;
+        HIP_OK(pcl::launch_sgemm(pm, a_kc, b_kc, M - M1, N, K, Am, lda, B, ldb, bias, accumulate,
+                                 C + (size_t)M1 * ldc, ldc, sc->ws, s));
+    }
+    if (N > N1) {  // columns N1.. of rows 0 .. M1-1, full K
+        const float *Bn = b_kc ? B + (size_t)N1 * ldb : B + N1;
+        HIP_OK(pcl::launch_sgemm(pn, a_kc, b_kc, M1, N - N1, K, A, lda, Bn, ldb, bias ? bias + N1 : nullptr,
+                                 accumulate, C + N1, ldc, sc->ws, s));
+    }
+    return PCL_OK;
+}
+
 int pcl_sgemm(int opA, int opB, int M, int N, int K, const float *A, int lda, const float *B,
               int ldb, const float *bias, int accumulate, float *C, int ldc, void *stream) {
     CHECK_ARG(M >= 0 && N >= 0 && K >= 0, "pcl_sgemm: negative dimension (M=%d N=%d K=%d)", M, N, K);
@@ -672,6 +732,16 @@ int pcl_sgemm(int opA, int opB, int M, int N, int K, const float *A, int lda, co
     if (M <= 8 && opA == PCL_OP_N)
         return pcl_sgemv(opB, M, N, K, A, lda, B, ldb, bias, accumulate, C, ldc, stream);
     hipStream_t s = pick(stream);
+    if (K > 0 && (double)M * N * K >= (double)(1L << 30)) {
+        const bool a_kc = opA == PCL_OP_N, b_kc = opB == PCL_OP_T;
+        const bool dma_ok = aligned16(A) && aligned16(B) && lda % 4 == 0 && ldb % 4 == 0 &&
+                            (a_kc ? K % 4 == 0 : M % 4 == 0) && (b_kc ? K % 4 == 0 : N % 4 == 0) &&
+                            K % 32 == 0;
+        if (!dma_ok) {
+            const int st = sgemm_realigned(opA, opB, M, N, K, A, lda, B, ldb, bias, accumulate, C, ldc, s);
+            if (st != 1) return st;
+        }
+    }
     pcl::SgemmPlan p = pcl::plan_sgemm(M, N, K);
     StreamScratch *sc;
     PCL_OK_OR_RETURN(get_scratch(s, p.part_bytes, 0, &sc));

@@ -361,6 +361,41 @@ hipError_t launch_elementwise(int op, long n, float *out, const float *a, const 
     return hipGetLastError();
 }
 
+// Copy rows x cols floats from src (leading dimension lds, any 4-byte
+// alignment) into dst (ldd a multiple of 4, 16-byte aligned): each thread
+// gathers 4 consecutive floats with 4-byte loads (consecutive lanes read
+// consecutive 16 bytes, so the reads stay coalesced) and writes them as one
+// 16-byte store; a row's last partial vector is written element by element.
+__global__ __launch_bounds__(256) void copy_rows_kernel(float *__restrict__ dst, long ldd,
+                                                        const float *__restrict__ src, long lds,
+                                                        int rows, int cols) {
+    typedef float v4f_t __attribute__((ext_vector_type(4)));
+    const int nv = (cols + 3) / 4;
+    for (int r = blockIdx.y; r < rows; r += gridDim.y) {
+        const float *sr = src + (long)r * lds;
+        float *dr = dst + (long)r * ldd;
+        for (int v = blockIdx.x * 256 + threadIdx.x; v < nv; v += gridDim.x * 256) {
+            const int c = 4 * v;
+            if (c + 4 <= cols) {
+                const v4f_t x = {__builtin_nontemporal_load(sr + c), __builtin_nontemporal_load(sr + c + 1),
+                                 __builtin_nontemporal_load(sr + c + 2), __builtin_nontemporal_load(sr + c + 3)};
+                *reinterpret_cast<v4f_t *>(dr + c) = x;
+            } else {
+                for (int e = c; e < cols; e++) dr[e] = sr[e];
+            }
+        }
+    }
+}
+
+hipError_t launch_copy_rows(float *dst, long ldd, const float *src, long lds, int rows, int cols,
+                            hipStream_t stream) {
+    if (rows <= 0 || cols <= 0) return hipSuccess;
+    const int nv = (cols + 3) / 4;
+    const dim3 grid((unsigned)((nv + 1023) / 1024), (unsigned)(rows < 4096 ? rows : 4096)), block(256);
+    hipLaunchKernelGGL(copy_rows_kernel, grid, block, 0, stream, dst, ldd, src, lds, rows, cols);
+    return hipGetLastError();
+}
+
 // ---------------------------------------------------------------------------
 // LDS-DMA pipeline. Operand tiles of SD_BK = 32 floats of K go from global
 // memory straight into a STAGES-deep LDS ring with global_load_lds_dwordx4

@@ -107,6 +107,37 @@ def test_lm_head_prefill_and_tied_head_shapes():
         assert rel(lo, ref) <= FP32_TOL
 
 
+def test_device_api_head_backward_vocab_50257():
+    # The GPU trainer's head backward (train_kaggle.cu:173-174) over a
+    # 50257-float logits row: gemm_nn d_lnf = dlogits . wte and gemm_tn
+    # dwte += dlogits^T . lnf. The misaligned rows take the realigned path
+    # (64-float rows, the aligned core on the LDS-DMA kernel, the 17-wide
+    # vocabulary edge on the generic kernel); f64 rows and vocabulary entries
+    # on both sides of the edge are compared.
+    M, V, D = 1024, 50257, 1024
+    dl = ob.normal((M, V), 80, 0.0, 1e-3)
+    wte = ob.normal((V, D), 81, 0.0, 0.02)
+    lnf = ob.normal((M, D), 82)
+    W0 = ob.normal((V, D), 83, 0.0, 1e-3)
+    ddl, dwte, dlnf = pcl.dev(dl), pcl.dev(wte), pcl.dev(lnf)
+    dout = pcl.empty((M, D), np.float32)
+    dW = pcl.dev(W0)
+    L.gpu_init()
+    announce("gemm_nn head backward", M, V, D)
+    L.gemm_nn(ddl.ptr, dwte.ptr, None, dout.ptr, M, V, D)
+    pcl.check_void()
+    announce("gemm_tn head backward", M, V, D)
+    L.gemm_tn(ddl.ptr, dlnf.ptr, dW.ptr, M, V, D)
+    pcl.check_void()
+    pcl.sync()
+    rows = np.unique(np.r_[0, M - 1, np.random.default_rng(5).choice(M, 30, replace=False)])
+    R = dl[rows].astype(np.float64) @ wte.astype(np.float64)
+    assert rel(dout.download((M, D), np.float32)[rows], R) <= FP32_TOL
+    vs = np.unique(np.r_[0, 1, 63, 64, 50239, 50240, 50241, 50256, np.random.default_rng(6).choice(V, 30, replace=False)])
+    R = W0[vs].astype(np.float64) + dl[:, vs].T.astype(np.float64) @ lnf.astype(np.float64)
+    assert rel(dW.download((V, D), np.float32)[vs], R) <= FP32_TOL
+
+
 def test_device_api_dropins():
     M, K, N = 300, 200, 260
     A = ob.normal((M, K), 70)
