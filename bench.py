@@ -475,7 +475,7 @@ def cpu_next_rows():
     return out
 
 
-# bytes of the INT8 350M-class products (M x K u8 +
+# Compulsory bytes of the INT8 350M-class products (M x K u8 +
 # K x N s8 + 4 M N fp32 out + scales), for the attainable roof min(peak, I x HBM)
 def _i8_attainable(M, N, K):
     ops = 2.0 * M * N * K

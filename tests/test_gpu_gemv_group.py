@@ -5,7 +5,7 @@ FP32 products (W K x N as generate.c:95-107 matvec, W N x K as the tied head
 model.c:64-77) against the reference-order oracle (orc_matvec / orc_lm_head)
 and the f64 truth, <= 1e-4; INT8 products (u8 x packed s8) bit-exact against
 the exact integer oracle, int32 and dequantised (gemm_bench.c:272-275 order).
-The groups cover the grown-model decode sweep (BASELINE config 4: 16 layers of
+The groups cover the grown-model decode sweep (BASELINE.json configs[3]: 16 layers of
 QKV 512x1536, O 512x512, FF1 512x2048, FF2 2048x512 and the 2048-vocab head)
 at M = 1, 4, 8, mixed kinds in one launch, ragged N and K, and repeated runs.
 """

@@ -170,7 +170,7 @@ def test_igemm_dequant_bit_exact(M, N, K):
     np.testing.assert_array_equal(C[rows], ob.dequant((V + off).astype(np.int32), None, sb))
 
 
-# BASELINE config 3, INT8: the grown model's prefill GEMMs at T = 256
+# BASELINE.json configs[2], INT8: the grown model's prefill GEMMs at T = 256
 # (d_model 512, d_ff 2048): QKV, attention output, FFN up, FFN down, with
 # per-token u8 activations and per-channel s8 weights, dequantised by
 # sa[m] * sb[n] (transformer.c:123-158; gemm_bench.c:272-275). Every output
