@@ -448,6 +448,26 @@ int pcl_model_forward(pcl_model *m, int tok, int pos, float *logits);
 int pcl_model_generate(pcl_model *m, const int *prompt, int n_prompt, int n_new, int *out,
                        int use_graph);
 void pcl_model_free(pcl_model *m);
+/* Verification tap of a PCL_W_INT8 model; no counterpart in the reference, for
+ * callers that check each INT8 product on its own. With on != 0, every later
+ * pcl_model_forward records per INT8 product what that product used: its
+ * input row before the transform (K floats: the residual stream before a
+ * LayerNorm, the attention row, or the d_ff row before bias + GELU), the
+ * quantised row it read (u8 = q + 128, Kp = K rounded up to 256 bytes), the
+ * row's scale, and its dequantised output v * sa * sb[n] before bias and
+ * residual (N floats). pcl_model_generate records nothing; on = 0 releases the
+ * slots. pcl_model_capture_read copies one product of the last forward to the
+ * host: layer 0..n_layers-1 with product PCL_CAP_QKV (K d_model, N 3 d_model),
+ * PCL_CAP_O (d_model, d_model), PCL_CAP_FF1 (d_model, d_ff), PCL_CAP_FF2
+ * (d_ff, d_model); layer n_layers with product 0 is the head (d_model, vocab).
+ * Any of xin, xq, sa, y may be NULL. */
+#define PCL_CAP_QKV 0
+#define PCL_CAP_O 1
+#define PCL_CAP_FF1 2
+#define PCL_CAP_FF2 3
+int pcl_model_capture(pcl_model *m, int on);
+int pcl_model_capture_read(const pcl_model *m, int layer, int product, float *xin, uint8_t *xq,
+                           float *sa, float *y);
 
 #ifdef __cplusplus
 }

@@ -63,6 +63,9 @@ _ORACLE_PROTOS = {
     "orc_model_forward": (None, [_vp, _i, _i, _vp]),
     "orc_model_forward_int8": (None, [_vp, _i, _i, _vp]),
     "orc_model_free": (None, [_vp]),
+    "orc_layernorm_row": (None, [_vp, _vp, _vp, _vp, _i]),
+    "orc_decode_attention": (None, [_vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp]),
+    "orc_model_int8_weights": (_i, [_vp, _i, _i, _vp, _vp]),
     "orc_rms_rel": (_d, [_vp, _vp, _l]),
     "orc_max_abs_diff": (_d, [_vp, _vp, _l]),
 }
@@ -280,6 +283,59 @@ def gelu_backward(dout, x):
     return din
 
 
+def layernorm_row(x, g, b):
+    """orc_layernorm_row (generate.c:109-117) of one row."""
+    x, g, b = (np.ascontiguousarray(a, np.float32) for a in (x, g, b))
+    y = np.empty_like(x)
+    oracle().orc_layernorm_row(p(x), p(g), p(b), p(y), x.size)
+    return y
+
+
+def quantize_row(x, Kp):
+    """orc_quantize_A_rows over one row: (u8 bytes padded with 128 to Kp, scale)."""
+    x = np.ascontiguousarray(x, np.float32)
+    q = np.empty(Kp, np.uint8)
+    sa = np.empty(1, np.float32)
+    oracle().orc_quantize_A_rows(p(x), p(q), p(sa), 1, x.size, Kp)
+    return q, sa
+
+
+def decode_attention(q, kc, vc, H, dh):
+    """orc_decode_attention (generate.c:130-152): one query row against cache
+    rows 0..len(kc)-1."""
+    q, kc, vc = (np.ascontiguousarray(a, np.float32) for a in (q, kc, vc))
+    n, ld = kc.shape
+    att = np.empty(ld, np.float32)
+    sc = np.empty(n, np.float32)
+    oracle().orc_decode_attention(p(q), p(kc), p(vc), ld, n - 1, H, dh, p(att), p(sc))
+    return att
+
+
+def read_ckp1(path):
+    """The tensors of a CKP1 file (train.c:633-648 order) as float32 arrays:
+    {"hdr", "wte", "wpe", "layers": [{g1 b1 Wq bq Wk bk Wv bv Wo bo g2 b2 W1
+    bff1 W2 bff2}], "gf", "bf"}; matrices K x N as stored."""
+    raw = np.fromfile(path, dtype="<f4")
+    hdr = raw[:8].view("<i4").tolist()
+    blk, d, _, df, nl, v = hdr[1:7]
+    at = [8]
+
+    def take(*shape):
+        n = int(np.prod(shape))
+        a = raw[at[0]:at[0] + n].reshape(shape).astype(np.float32)
+        at[0] += n
+        return a
+    out = {"hdr": hdr, "wte": take(v, d), "wpe": take(blk, d), "layers": []}
+    shapes = [("g1", (d,)), ("b1", (d,)), ("Wq", (d, d)), ("bq", (d,)), ("Wk", (d, d)), ("bk", (d,)),
+              ("Wv", (d, d)), ("bv", (d,)), ("Wo", (d, d)), ("bo", (d,)), ("g2", (d,)), ("b2", (d,)),
+              ("W1", (d, df)), ("bff1", (df,)), ("W2", (df, d)), ("bff2", (d,))]
+    for _ in range(nl):
+        out["layers"].append({k: take(*sh) for k, sh in shapes})
+    out["gf"], out["bf"] = take(d), take(d)
+    assert at[0] == raw.size, "CKP1 size does not match its header"
+    return out
+
+
 def attention_forward(q, k, v, B, T, H, dh, f64=False):
     """(att, probs) of the causal attention restatement; q/k/v (B*T) x ld."""
     q, k, v = (np.ascontiguousarray(x, np.float32) for x in (q, k, v))
@@ -347,6 +403,17 @@ class OracleModel:
         fn = oracle().orc_model_forward_int8 if self.int8 else oracle().orc_model_forward
         fn(self.m, tok, pos, p(out))
         return out
+
+    def int8_weights(self, layer, which):
+        """The INT8 step's quantised operand (K x N int8) and per-column
+        scales: which 0..5 = Wq Wk Wv Wo W1 W2; layer n_layers = the head."""
+        d, df, v, nl = self.hdr[2], self.hdr[4], self.hdr[6], self.hdr[5]
+        K, N = (d, v) if layer == nl else ((df, d) if which == 5 else (d, df if which == 4 else d))
+        Bq = np.empty((K, N), np.int8)
+        sb = np.empty(N, np.float32)
+        got = oracle().orc_model_int8_weights(self.m, layer, which, p(Bq), p(sb))
+        assert got == K * N, (layer, which)
+        return Bq, sb
 
     def close(self):
         if self.m:

@@ -399,8 +399,8 @@ orc_model *orc_model_load(const char *path) {
 
 void orc_model_header(const orc_model *m, int hdr[8]) { memcpy(hdr, m->hdr, sizeof m->hdr); }
 
-static void orc_ln_row(const float *x, const float *g, const float *b, float *y, int n) {
-    /* generate.c:106-114 */
+void orc_layernorm_row(const float *x, const float *g, const float *b, float *y, int n) {
+    /* generate.c:109-117 */
     float mu = 0, var = 0;
     for (int i = 0; i < n; i++) mu += x[i];
     mu /= n;
@@ -456,6 +456,62 @@ static void orc_qmatvec(orc_model *m, float *out, const float *x, const int8_t *
         for (int n = 0; n < N; n++) out[n] = out[n] + b[n];
 }
 
+void orc_decode_attention(const float *q, const float *kc, const float *vc, int ld, int pos,
+                          int H, int DH, float *att, float *sc) {
+    /* generate.c:130-152: per head, scores of q against cache rows 0..pos
+     * (row stride ld), scaled by 1/sqrt(DH), max-subtracted softmax, and the
+     * weighted sum of the value rows; sc holds pos + 1 floats of scratch */
+    const float scale = 1.0f / sqrtf((float)DH);
+    for (int h = 0; h < H; h++) {
+        const int off = h * DH;
+        float maxv = -1e30f;
+        for (int j = 0; j <= pos; j++) {
+            const float *kj = kc + (size_t)j * ld + off;
+            float dot = 0;
+            for (int d = 0; d < DH; d++) dot += q[off + d] * kj[d];
+            dot *= scale;
+            sc[j] = dot;
+            if (dot > maxv) maxv = dot;
+        }
+        float sum = 0;
+        for (int j = 0; j <= pos; j++) {
+            const float e = expf(sc[j] - maxv);
+            sc[j] = e;
+            sum += e;
+        }
+        const float inv = 1.0f / sum;
+        float *oh = att + off;
+        for (int d = 0; d < DH; d++) oh[d] = 0;
+        for (int j = 0; j <= pos; j++) {
+            const float pj = sc[j] * inv;
+            const float *vj = vc + (size_t)j * ld + off;
+            for (int d = 0; d < DH; d++) oh[d] += pj * vj[d];
+        }
+    }
+}
+
+int orc_model_int8_weights(orc_model *m, int layer, int which, int8_t *Bq, float *sb) {
+    /* the INT8 step's quantised operand (K x N, row-major) and its per-column
+     * scales: which 0..5 = Wq Wk Wv Wo W1 W2 of a layer, or the head (layer ==
+     * n_layers, which 0). Returns K * N, or 0 for no such matrix. */
+    if (layer < 0 || layer > m->L || which < 0 || which > 5 || (layer == m->L && which != 0)) return 0;
+    if (!m->q8) orc_model_quantize(m);
+    const long D = m->D, F = m->DF;
+    long K = D, N = D;
+    const int8_t *src;
+    const float *ss;
+    if (layer == m->L) {
+        N = m->V, src = m->hq, ss = m->hs;
+    } else {
+        if (which == 4) N = F;
+        if (which == 5) K = F;
+        src = m->lq[layer * 6 + which], ss = m->ls[layer * 6 + which];
+    }
+    if (Bq) memcpy(Bq, src, (size_t)(K * N));
+    if (sb) memcpy(sb, ss, sizeof(float) * (size_t)N);
+    return (int)(K * N);
+}
+
 static void orc_model_step(orc_model *m, int tok, int pos, float *logits, int int8) {
     /* generate.c:170-183 forward and :118-167 block */
     const int D = m->D, DH = m->DH, F = m->DF;
@@ -470,47 +526,21 @@ static void orc_model_step(orc_model *m, int tok, int pos, float *logits, int in
         float **w = m->lw + l * 16;
         float *kc = m->kc + (size_t)l * m->BLK * D, *vc = m->vc + (size_t)l * m->BLK * D;
         float *krow = kc + (size_t)pos * D, *vrow = vc + (size_t)pos * D;
-        orc_ln_row(m->x, w[0], w[1], m->ln, D);
+        orc_layernorm_row(m->x, w[0], w[1], m->ln, D);
         ORC_MV(m->q, m->ln, 0, D, D);
         ORC_MV(krow, m->ln, 1, D, D);
         ORC_MV(vrow, m->ln, 2, D, D);
-        const float scale = 1.0f / sqrtf((float)DH);
-        for (int h = 0; h < m->H; h++) {
-            const int off = h * DH;
-            float maxv = -1e30f;
-            for (int j = 0; j <= pos; j++) {
-                const float *kj = kc + (size_t)j * D + off;
-                float dot = 0;
-                for (int d = 0; d < DH; d++) dot += m->q[off + d] * kj[d];
-                dot *= scale;
-                m->sc[j] = dot;
-                if (dot > maxv) maxv = dot;
-            }
-            float sum = 0;
-            for (int j = 0; j <= pos; j++) {
-                const float e = expf(m->sc[j] - maxv);
-                m->sc[j] = e;
-                sum += e;
-            }
-            const float inv = 1.0f / sum;
-            float *oh = m->att + off;
-            for (int d = 0; d < DH; d++) oh[d] = 0;
-            for (int j = 0; j <= pos; j++) {
-                const float pj = m->sc[j] * inv;
-                const float *vj = vc + (size_t)j * D + off;
-                for (int d = 0; d < DH; d++) oh[d] += pj * vj[d];
-            }
-        }
+        orc_decode_attention(m->q, kc, vc, D, pos, m->H, DH, m->att, m->sc);
         ORC_MV(m->proj, m->att, 3, D, D);
         for (int i = 0; i < D; i++) m->x[i] += m->proj[i];
-        orc_ln_row(m->x, w[10], w[11], m->ln, D);
+        orc_layernorm_row(m->x, w[10], w[11], m->ln, D);
         ORC_MV(m->h, m->ln, 4, D, F);
         orc_gelu_forward(m->h, m->h, F);
         ORC_MV(m->proj, m->h, 5, F, D);
         for (int i = 0; i < D; i++) m->x[i] += m->proj[i];
     }
 #undef ORC_MV
-    orc_ln_row(m->x, m->gf, m->bf, m->ln, D);
+    orc_layernorm_row(m->x, m->gf, m->bf, m->ln, D);
     if (int8) {
         orc_qmatvec(m, logits, m->ln, m->hq, m->hs, NULL, D, m->V);
         return;

@@ -130,6 +130,16 @@ void orc_model_forward(orc_model *m, int tok, int pos, float *logits);
  * dequantised by sa * sb[n], then the bias added. */
 void orc_model_forward_int8(orc_model *m, int tok, int pos, float *logits);
 void orc_model_free(orc_model *m);
+/* The pieces of that step, for checking a decoder op by op: the LayerNorm row
+ * (generate.c:109-117), the cached attention of one query (generate.c:130-152;
+ * cache rows of ld floats, sc = pos + 1 floats of scratch), and the INT8
+ * step's quantised operands (which 0..5 = Wq Wk Wv Wo W1 W2 of a layer, K x N
+ * bytes row-major plus N scales; layer n_layers, which 0 = the head; returns
+ * K * N, 0 when there is no such matrix). */
+void orc_layernorm_row(const float *x, const float *g, const float *b, float *y, int n);
+void orc_decode_attention(const float *q, const float *kc, const float *vc, int ld, int pos,
+                          int H, int DH, float *att, float *sc);
+int orc_model_int8_weights(orc_model *m, int layer, int which, int8_t *Bq, float *sb);
 
 /* Causal multi-head attention, train.c:339-370 attention_forward generalised
  * to B sequences of T tokens, H heads of dh: q/k/v rows of ld floats (row

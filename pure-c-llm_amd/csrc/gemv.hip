@@ -734,7 +734,7 @@ template <int QX, int EPI, int LPR, int UK>
 __global__ __launch_bounds__(GV_THREADS) void igemv_q_kernel(
     const float *__restrict__ X, const float *__restrict__ g, const float *__restrict__ b, int K,
     const int8_t *__restrict__ B, long ldb, const float *__restrict__ sb,
-    const float *__restrict__ bias, float *__restrict__ Y, int N) {
+    const float *__restrict__ bias, float *__restrict__ Y, int N, GemvTap tap) {
     static_assert(GV_THREADS == 256, "the reductions assume four waves");
     constexpr int RPL = 2, RG = GV_THREADS / LPR, RPB = RG * RPL;
     extern __shared__ __attribute__((aligned(16))) unsigned char gv_dyn[];
@@ -791,6 +791,10 @@ __global__ __launch_bounds__(GV_THREADS) void igemv_q_kernel(
     const float scale = amax * RCP127, inv = 1.0f / scale;
     for (int k = tid; k < Kp; k += 256) xs[k] = (int8_t)(k < K ? quant_q(xf[k], inv) : 0);
     __syncthreads();
+    if (tap.xq && blockIdx.x == 0) {  // every block makes the same row; block 0 records it
+        for (int k = tid; k < Kp; k += 256) tap.xq[k] = (uint8_t)(xs[k] + 128);
+        if (tid == 0) tap.sa[0] = scale;
+    }
 
     int32_t acc[RPL] = {};
     for (int k0 = 16 * j; k0 < klen; k0 += 16 * LPR * UK) {
@@ -830,6 +834,7 @@ __global__ __launch_bounds__(GV_THREADS) void igemv_q_kernel(
         if (n < N) {
             const float dq = scale * sb[n];
             const float y = (float)res[tid] * dq;
+            if (tap.y) tap.y[n] = y;
             if (EPI == 1) Y[n] = Y[n] + (y + bias[n]);
             else Y[n] = y;
         }
@@ -839,12 +844,12 @@ __global__ __launch_bounds__(GV_THREADS) void igemv_q_kernel(
 template <int QX, int EPI>
 static void launch_igemv_q_shape(const float *X, const float *g, const float *b, int K,
                                  const int8_t *B, int Kp, const float *sb, const float *bias,
-                                 float *Y, int N, hipStream_t s) {
+                                 float *Y, int N, hipStream_t s, const GemvTap &tap) {
     const size_t lds = (size_t)Kp * (sizeof(float) + 1);
     const dim3 block(GV_THREADS);
 #define IGQ(LPRV, UKV)                                                                       \
     hipLaunchKernelGGL((igemv_q_kernel<QX, EPI, LPRV, UKV>), dim3((unsigned)cdiv(N, 512 / LPRV)), \
-                       block, lds, s, X, g, b, K, B, (long)Kp, sb, bias, Y, N)
+                       block, lds, s, X, g, b, K, B, (long)Kp, sb, bias, Y, N, tap)
     if (Kp <= 256) IGQ(16, 1);
     else if (Kp <= 512) IGQ(32, 1);
     else if (Kp <= 1024) IGQ(64, 1);
@@ -855,20 +860,21 @@ static void launch_igemv_q_shape(const float *X, const float *g, const float *b,
 
 hipError_t launch_igemv_q(int qx, int epi, const float *X, const float *g, const float *b, int K,
                           const int8_t *B, int Kp, const float *sb, const float *bias, float *Y,
-                          int N, hipStream_t s) {
+                          int N, hipStream_t s, const GemvTap &tap) {
     if (N <= 0 || K <= 0 || K > Kp || Kp % 256 != 0 || Kp > IGEMV_Q_MAX_K) return hipErrorInvalidValue;
+    if ((tap.xq != nullptr) != (tap.sa != nullptr)) return hipErrorInvalidValue;
     if ((reinterpret_cast<uintptr_t>(B) & 15) != 0) return hipErrorInvalidValue;
     if ((qx == QX_LN && (!g || !b)) || (qx == QX_BIAS_GELU && !b) || (epi == 1 && !bias))
         return hipErrorInvalidValue;
     if (qx == QX_LN) {
-        if (epi) launch_igemv_q_shape<QX_LN, 1>(X, g, b, K, B, Kp, sb, bias, Y, N, s);
-        else launch_igemv_q_shape<QX_LN, 0>(X, g, b, K, B, Kp, sb, bias, Y, N, s);
+        if (epi) launch_igemv_q_shape<QX_LN, 1>(X, g, b, K, B, Kp, sb, bias, Y, N, s, tap);
+        else launch_igemv_q_shape<QX_LN, 0>(X, g, b, K, B, Kp, sb, bias, Y, N, s, tap);
     } else if (qx == QX_BIAS_GELU) {
-        if (epi) launch_igemv_q_shape<QX_BIAS_GELU, 1>(X, g, b, K, B, Kp, sb, bias, Y, N, s);
-        else launch_igemv_q_shape<QX_BIAS_GELU, 0>(X, g, b, K, B, Kp, sb, bias, Y, N, s);
+        if (epi) launch_igemv_q_shape<QX_BIAS_GELU, 1>(X, g, b, K, B, Kp, sb, bias, Y, N, s, tap);
+        else launch_igemv_q_shape<QX_BIAS_GELU, 0>(X, g, b, K, B, Kp, sb, bias, Y, N, s, tap);
     } else {
-        if (epi) launch_igemv_q_shape<QX_NONE, 1>(X, g, b, K, B, Kp, sb, bias, Y, N, s);
-        else launch_igemv_q_shape<QX_NONE, 0>(X, g, b, K, B, Kp, sb, bias, Y, N, s);
+        if (epi) launch_igemv_q_shape<QX_NONE, 1>(X, g, b, K, B, Kp, sb, bias, Y, N, s, tap);
+        else launch_igemv_q_shape<QX_NONE, 0>(X, g, b, K, B, Kp, sb, bias, Y, N, s, tap);
     }
     return hipGetLastError();
 }

@@ -191,9 +191,18 @@ hipError_t launch_sgemv_xf(const GemvPlan &p, int xf, int N, int K, const float 
 // (Kp % 256 == 0, K <= Kp <= IGEMV_Q_MAX_K); epi 0: Y = v * scale * sb[n],
 // epi 1: Y += v * scale * sb[n] + bias[n].
 constexpr int IGEMV_Q_MAX_K = 8192;
+// A verification tap (all members null in normal use): where the kernel also
+// records the quantised row it used (as u8 = q + 128, Kp bytes), that row's
+// scale, and the dequantised product v * scale * sb[n] before bias and
+// residual (N floats).
+struct GemvTap {
+    uint8_t *xq = nullptr;
+    float *sa = nullptr;
+    float *y = nullptr;
+};
 hipError_t launch_igemv_q(int qx, int epi, const float *X, const float *g, const float *b, int K,
                           const int8_t *B, int Kp, const float *sb, const float *bias, float *Y,
-                          int N, hipStream_t s);
+                          int N, hipStream_t s, const GemvTap &tap = GemvTap{});
 // Its fp32 twin over weights stored N x K (rows of K floats, K % 4 == 0,
 // 16-byte aligned, K <= SGEMV_Q_MAX_K): same transforms; epi 0: Y = s + bias,
 // epi 1: Y += s + bias (bias may be NULL).

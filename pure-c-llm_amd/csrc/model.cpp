@@ -18,6 +18,7 @@
 
 #include <cstdio>
 #include <cstring>
+#include <algorithm>
 #include <new>
 #include <vector>
 
@@ -62,6 +63,11 @@ struct pcl_model {
     int8_t *whead = nullptr;
     float *shead = nullptr, *sa = nullptr, *tmp = nullptr;
     uint8_t *xq = nullptr;
+    // verification tap (pcl_model_capture): one slot per INT8 product,
+    // written by the eager steps of pcl_model_forward while tap_on
+    unsigned char *tap = nullptr;
+    bool tap_on = false;
+    long tap_km = 0, tap_nm = 0, tap_kpm = 0;
 };
 
 namespace {
@@ -80,6 +86,51 @@ namespace {
         int s_ = (expr);            \
         if (s_ != PCL_OK) return s_; \
     } while (0)
+
+// A tap slot: the product's input row before its transform (K floats), its
+// dequantised output before bias and residual (N floats), the row's scale,
+// and the quantised row (Kp bytes). Products 0-3 of layer l are QKV, O, FF1,
+// FF2; layer n_layers holds the head.
+struct TapSlot {
+    float *xin, *y, *sa;
+    uint8_t *xq;
+};
+long tap_slot_bytes(const pcl_model *m) {
+    return 4 * (m->tap_km + m->tap_nm + 4) + (m->tap_kpm + 15) / 16 * 16;
+}
+TapSlot tap_slot(const pcl_model *m, int l, int p) {
+    unsigned char *b = m->tap + (size_t)(l * 4 + p) * (size_t)tap_slot_bytes(m);
+    float *f = reinterpret_cast<float *>(b);
+    return TapSlot{f, f + m->tap_km, f + m->tap_km + m->tap_nm,
+                   reinterpret_cast<uint8_t *>(f + m->tap_km + m->tap_nm + 4)};
+}
+// Fused products: record the input row, and aim the kernel's own tap at the
+// slot (it writes the quantised row, its scale and the product).
+int tap_fused(pcl_model *m, int l, int p, const float *x, int K, pcl::GemvTap *t) {
+    if (!m->tap_on) return PCL_OK;
+    const TapSlot sl = tap_slot(m, l, p);
+    M_HIP(hipMemcpyAsync(sl.xin, x, sizeof(float) * (size_t)K, hipMemcpyDeviceToDevice,
+                         (hipStream_t)m->stream));
+    *t = pcl::GemvTap{sl.xq, sl.sa, sl.y};
+    return PCL_OK;
+}
+// Unfused products: the input row, the quantised row and scale the GEMV reads
+// (m->xq, m->sa), then its output.
+int tap_row(pcl_model *m, int l, int p, const float *x, int K, int Kp) {
+    if (!m->tap_on) return PCL_OK;
+    const TapSlot sl = tap_slot(m, l, p);
+    hipStream_t s = (hipStream_t)m->stream;
+    M_HIP(hipMemcpyAsync(sl.xin, x, sizeof(float) * (size_t)K, hipMemcpyDeviceToDevice, s));
+    M_HIP(hipMemcpyAsync(sl.xq, m->xq, (size_t)Kp, hipMemcpyDeviceToDevice, s));
+    M_HIP(hipMemcpyAsync(sl.sa, m->sa, sizeof(float), hipMemcpyDeviceToDevice, s));
+    return PCL_OK;
+}
+int tap_out(pcl_model *m, int l, int p, const float *y, int N) {
+    if (!m->tap_on) return PCL_OK;
+    M_HIP(hipMemcpyAsync(tap_slot(m, l, p).y, y, sizeof(float) * (size_t)N, hipMemcpyDeviceToDevice,
+                         (hipStream_t)m->stream));
+    return PCL_OK;
+}
 
 // The fp32 step over the N x K projections. Each product is one sgemv_q
 // launch that makes its input row (LayerNorm, or bias + GELU) and, for Wo and
@@ -125,22 +176,33 @@ int step_int8(pcl_model *m) {
     int *tokpos = m->ints, *out = m->ints + 2;
     M_HIP(pcl::launch_decode_embed(m->wte, m->wpe, m->x, D, tokpos, s));
     const float *t = nullptr, *tb = nullptr;  // pending product and its bias, added into x
-    for (size_t l = 0; l < m->lay.size(); l++) {
-        const Layer &y = m->lay[l];
-        const QLayer &q = m->ql[l];
+    const int L = (int)m->lay.size();
+    for (int l = 0; l < L; l++) {
+        const Layer &y = m->lay[(size_t)l];
+        const QLayer &q = m->ql[(size_t)l];
         M_HIP(pcl::launch_decode_add_ln_quant(m->x, t, tb, y.g1, y.b1, m->xq, m->sa, D, KD, s));
+        M_OK(tap_row(m, l, 0, m->x, D, KD));
         M_OK(pcl_gemv_u8s8_dq(m->xq, KD, q.wqkv, nullptr, m->sa, q.sqkv, m->qkv, 3 * D, 1, 3 * D, KD, s));
+        M_OK(tap_out(m, l, 0, m->qkv, 3 * D));
         M_HIP(pcl::launch_decode_attn(m->qkv, y.bqkv, y.kc, y.vc, m->att, D, m->h, m->blk, tokpos, s));
         M_HIP(pcl::launch_quantize_a_rows(m->att, 1, D, m->xq, KD, m->sa, s));
+        M_OK(tap_row(m, l, 1, m->att, D, KD));
         M_OK(pcl_gemv_u8s8_dq(m->xq, KD, q.wo, nullptr, m->sa, q.so, m->tmp, D, 1, D, KD, s));
+        M_OK(tap_out(m, l, 1, m->tmp, D));
         M_HIP(pcl::launch_decode_add_ln_quant(m->x, m->tmp, y.bo, y.g2, y.b2, m->xq, m->sa, D, KD, s));
+        M_OK(tap_row(m, l, 2, m->x, D, KD));
         M_OK(pcl_gemv_u8s8_dq(m->xq, KD, q.w1, nullptr, m->sa, q.s1, m->hh, F, 1, F, KD, s));
+        M_OK(tap_out(m, l, 2, m->hh, F));
         M_HIP(pcl::launch_decode_bias_gelu_quant(m->hh, y.bf1, m->xq, m->sa, F, KF, s));
+        M_OK(tap_row(m, l, 3, m->hh, F, KF));
         M_OK(pcl_gemv_u8s8_dq(m->xq, KF, q.w2, nullptr, m->sa, q.s2, m->tmp, D, 1, D, KF, s));
+        M_OK(tap_out(m, l, 3, m->tmp, D));
         t = m->tmp, tb = y.bf2;
     }
     M_HIP(pcl::launch_decode_add_ln_quant(m->x, t, tb, m->gf, m->bf, m->xq, m->sa, D, KD, s));
+    M_OK(tap_row(m, L, 0, m->x, D, KD));
     M_OK(pcl_gemv_u8s8_dq(m->xq, KD, m->whead, nullptr, m->sa, m->shead, m->logits, V, 1, V, KD, s));
+    M_OK(tap_out(m, L, 0, m->logits, V));
     M_HIP(pcl::launch_decode_argmax(m->logits, V, tokpos, out, m->blk + 1, s));
     return PCL_OK;
 }
@@ -153,16 +215,23 @@ int step_int8_fused(pcl_model *m) {
     const int D = m->d, F = m->df, V = m->v, KD = m->kpd, KF = m->kpf;
     int *tokpos = m->ints, *out = m->ints + 2;
     M_HIP(pcl::launch_decode_embed(m->wte, m->wpe, m->x, D, tokpos, s));
-    for (size_t l = 0; l < m->lay.size(); l++) {
-        const Layer &y = m->lay[l];
-        const QLayer &q = m->ql[l];
-        M_HIP(pcl::launch_igemv_q(1, 0, m->x, y.g1, y.b1, D, q.wqkv, KD, q.sqkv, nullptr, m->qkv, 3 * D, s));
+    const int L = (int)m->lay.size();
+    pcl::GemvTap tp[4], th;  // stay null unless the tap is on
+    for (int l = 0; l < L; l++) {
+        const Layer &y = m->lay[(size_t)l];
+        const QLayer &q = m->ql[(size_t)l];
+        M_OK(tap_fused(m, l, 0, m->x, D, &tp[0]));
+        M_HIP(pcl::launch_igemv_q(1, 0, m->x, y.g1, y.b1, D, q.wqkv, KD, q.sqkv, nullptr, m->qkv, 3 * D, s, tp[0]));
         M_HIP(pcl::launch_decode_attn(m->qkv, y.bqkv, y.kc, y.vc, m->att, D, m->h, m->blk, tokpos, s));
-        M_HIP(pcl::launch_igemv_q(0, 1, m->att, nullptr, nullptr, D, q.wo, KD, q.so, y.bo, m->x, D, s));
-        M_HIP(pcl::launch_igemv_q(1, 0, m->x, y.g2, y.b2, D, q.w1, KD, q.s1, nullptr, m->hh, F, s));
-        M_HIP(pcl::launch_igemv_q(2, 1, m->hh, nullptr, y.bf1, F, q.w2, KF, q.s2, y.bf2, m->x, D, s));
+        M_OK(tap_fused(m, l, 1, m->att, D, &tp[1]));
+        M_HIP(pcl::launch_igemv_q(0, 1, m->att, nullptr, nullptr, D, q.wo, KD, q.so, y.bo, m->x, D, s, tp[1]));
+        M_OK(tap_fused(m, l, 2, m->x, D, &tp[2]));
+        M_HIP(pcl::launch_igemv_q(1, 0, m->x, y.g2, y.b2, D, q.w1, KD, q.s1, nullptr, m->hh, F, s, tp[2]));
+        M_OK(tap_fused(m, l, 3, m->hh, F, &tp[3]));
+        M_HIP(pcl::launch_igemv_q(2, 1, m->hh, nullptr, y.bf1, F, q.w2, KF, q.s2, y.bf2, m->x, D, s, tp[3]));
     }
-    M_HIP(pcl::launch_igemv_q(1, 0, m->x, m->gf, m->bf, D, m->whead, KD, m->shead, nullptr, m->logits, V, s));
+    M_OK(tap_fused(m, L, 0, m->x, D, &th));
+    M_HIP(pcl::launch_igemv_q(1, 0, m->x, m->gf, m->bf, D, m->whead, KD, m->shead, nullptr, m->logits, V, s, th));
     M_HIP(pcl::launch_decode_argmax(m->logits, V, tokpos, out, m->blk + 1, s));
     return PCL_OK;
 }
@@ -399,6 +468,7 @@ void release(pcl_model *m) {
     if (m->i8) (void)hipFree(m->i8);
     if (m->qscale) (void)hipFree(m->qscale);
     if (m->xq) (void)hipFree(m->xq);
+    if (m->tap) (void)hipFree(m->tap);
     if (m->ints) (void)hipFree(m->ints);
     if (m->host_tp) (void)hipHostFree(m->host_tp);
     delete m;
@@ -477,7 +547,10 @@ int pcl_model_forward(pcl_model *m, int tok, int pos, float *logits) {
     if (tok < 0 || tok >= m->v || pos < 0 || pos >= m->blk)
         return fail(PCL_ERR_INVALID_ARG, "pcl_model_forward: token or position out of range");
     M_OK(set_tokpos(m, tok, pos));
-    M_OK(run_eager(m));
+    m->tap_on = m->tap != nullptr;
+    const int st = run_eager(m);
+    m->tap_on = false;
+    M_OK(st);
     if (logits)
         M_HIP(hipMemcpyAsync(logits, m->logits, sizeof(float) * (size_t)m->v, hipMemcpyDeviceToHost,
                              (hipStream_t)m->stream));
@@ -513,6 +586,51 @@ int pcl_model_generate(pcl_model *m, const int *prompt, int n_prompt, int n_new,
 
 void pcl_model_free(pcl_model *m) {
     if (m) release(m);
+}
+
+int pcl_model_capture(pcl_model *m, int on) {
+    if (!m) return fail(PCL_ERR_INVALID_ARG, "pcl_model_capture: model is NULL");
+    if (m->wmode != PCL_W_INT8)
+        return fail(PCL_ERR_INVALID_ARG, "pcl_model_capture: the model has no INT8 products");
+    if (!on) {
+        if (m->tap) {
+            M_HIP(hipStreamSynchronize((hipStream_t)m->stream));
+            M_HIP(hipFree(m->tap));
+        }
+        m->tap = nullptr;
+        return PCL_OK;
+    }
+    if (m->tap) return PCL_OK;
+    const long D = m->d, F = m->df, V = m->v;
+    m->tap_km = D > F ? D : F;
+    m->tap_nm = std::max(std::max(3 * D, F), V);
+    m->tap_kpm = m->kpd > m->kpf ? m->kpd : m->kpf;
+    const size_t bytes = (size_t)(4 * m->nl + 1) * (size_t)tap_slot_bytes(m);
+    M_HIP(hipMalloc((void **)&m->tap, bytes));
+    M_HIP(hipMemset(m->tap, 0, bytes));
+    return PCL_OK;
+}
+
+int pcl_model_capture_read(const pcl_model *m, int layer, int product, float *xin, uint8_t *xq,
+                           float *sa, float *y) {
+    if (!m || !m->tap)
+        return fail(PCL_ERR_INVALID_ARG, "pcl_model_capture_read: no capture on this model");
+    if (layer < 0 || layer > m->nl || product < 0 || product > 3 || (layer == m->nl && product != 0))
+        return fail(PCL_ERR_INVALID_ARG, "pcl_model_capture_read: no such product");
+    const long D = m->d, F = m->df;
+    long K = D, N = D;
+    if (layer == m->nl) N = m->v;
+    else if (product == 0) N = 3 * D;
+    else if (product == 2) N = F;
+    else if (product == 3) K = F;
+    const long Kp = K == D ? m->kpd : m->kpf;
+    const TapSlot sl = tap_slot(m, layer, product);
+    M_HIP(hipStreamSynchronize((hipStream_t)m->stream));
+    if (xin) M_HIP(hipMemcpy(xin, sl.xin, sizeof(float) * (size_t)K, hipMemcpyDeviceToHost));
+    if (xq) M_HIP(hipMemcpy(xq, sl.xq, (size_t)Kp, hipMemcpyDeviceToHost));
+    if (sa) M_HIP(hipMemcpy(sa, sl.sa, sizeof(float), hipMemcpyDeviceToHost));
+    if (y) M_HIP(hipMemcpy(y, sl.y, sizeof(float) * (size_t)N, hipMemcpyDeviceToHost));
+    return PCL_OK;
 }
 
 }  // extern "C"

@@ -29,6 +29,7 @@ PCL_ERR_RANGE = 6
 OP_N, OP_T = 0, 1
 EPI_NONE, EPI_GELU, EPI_RESID, EPI_GELU_BWD = 0, 1, 2, 3
 W_FP32, W_INT8 = 0, 1
+CAP_QKV, CAP_O, CAP_FF1, CAP_FF2 = 0, 1, 2, 3
 
 if not os.path.exists(LIB_PATH):
     raise ImportError(f"{LIB_PATH} is not built (run __graft_entry__.build() or make -C pure-c-llm_amd)")
@@ -129,6 +130,8 @@ _PROTOS = {
     "pcl_model_forward": (_i, [_vp, _i, _i, _vp]),
     "pcl_model_generate": (_i, [_vp, _vp, _i, _i, _vp, _i]),
     "pcl_model_free": (None, [_vp]),
+    "pcl_model_capture": (_i, [_vp, _i]),
+    "pcl_model_capture_read": (_i, [_vp, _i, _i, _vp, _vp, _vp, _vp]),
 }
 
 

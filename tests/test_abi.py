@@ -130,6 +130,13 @@ def test_roofs_and_groups_check_arguments_first():
     L.pcl_clear_error()
 
 
+def test_model_capture_checks_arguments_first():
+    L = pcl.lib
+    assert L.pcl_model_capture(None, 1) == pcl.PCL_ERR_INVALID_ARG
+    assert L.pcl_model_capture_read(None, 0, pcl.CAP_QKV, None, None, None, None) == pcl.PCL_ERR_INVALID_ARG
+    L.pcl_clear_error()
+
+
 def test_attention_dims_must_split_into_heads():
     """d_model must be a multiple of n_heads for the device attention drop-ins
     (otherwise the last d_model % n_heads columns would be silently ignored)."""

@@ -5,18 +5,26 @@ greedy generation -- eager and replayed as one graph per token -- where every
 pick must be an argmax of the oracle's logits for the same prefix (up to the
 fp32 tolerance when two logits are that close).
 
-The INT8 mode (pcl_model_load_ex(..., PCL_W_INT8)) is compared with the
-oracle's INT8 step (orc_model_forward_int8: the same quantisation rules, exact
-integer sums). The two agree to fp32 rounding (INT8_TOL) until some activation
-lies within fp32 rounding of a rounding boundary of its quantiser and the two
-round it differently (a LayerNorm or softmax sum taken in another order
-suffices). From that position on the logits differ by about one quantisation
-error: a 1-ulp change to one LayerNorm gain of the oracle's own input moves the
-512-wide models by 1-3e-2 normwise after the first such flip, while the INT8
-step itself is 3-5e-2 from the fp32 step. The small models meet INT8_TOL at
-every position; the 16-layer model and the one with 8448-wide rows (which also
-takes the unfused INT8 step) must start within INT8_TOL and stay within
-INT8_BAND.
+The INT8 mode (pcl_model_load_ex(..., PCL_W_INT8)) is pinned product by
+product: with the model's verification tap on, every INT8 product of every
+position (QKV, O, FF1, FF2 of each layer, the head) is checked against the
+oracle's op applied to the GPU's own inputs (tests/int8_steps.py): the
+product bit for bit (exact integer GEMV of the GPU's quantised row, the
+oracle's quantised weights, the GPU's scale), the quantised row byte for byte
+up to one-step differences at rounding boundaries, and the attention, residual
+and GELU inputs between products to fp32 rounding -- the fused step and the
+unfused one (8448-wide rows), the grown model included.
+
+Free-running against the oracle's INT8 step (orc_model_forward_int8), the two
+agree to fp32 rounding (INT8_TOL) until some activation lies within fp32
+rounding of a rounding boundary of its quantiser and the two round it
+differently. From that position on the logits differ by about one
+quantisation error: a 1-ulp change to one LayerNorm gain of the oracle's own
+input moves the 512-wide models by 1-3e-2 normwise after the first such flip,
+while the INT8 step itself is 3-5e-2 from the fp32 step. The small models meet
+INT8_TOL at every position; the 16-layer model and the one with 8448-wide rows
+must start within INT8_TOL and stay within INT8_BAND end to end (each step
+being pinned exactly by the product-by-product test).
 """
 import numpy as np
 import pytest
@@ -24,6 +32,7 @@ import pytest
 import binding as ob
 import pcl
 from gpu_util import FP32_TOL, announce, rel, require_device
+from int8_steps import Int8StepChecker, kpad256
 
 pytestmark = pytest.mark.gpu
 
@@ -200,6 +209,71 @@ def test_model_int8_forward_logits(tmp_path, dims, npos):
     assert max(errs) <= (INT8_BAND if flip_prone else INT8_TOL)
 
 
+def _tap_source(m, dims):
+    """The model's verification tap as the checker's source: (xin, xq, sa, y)
+    of product prod of layer l in the last pcl_model_forward."""
+    _, d, _, df, nl, v = dims
+
+    def read(l, prod):
+        K = df if (l < nl and prod == pcl.CAP_FF2) else d
+        N = v if l == nl else (3 * d, d, df, d)[prod]
+        xin, xq = np.empty(K, np.float32), np.empty(kpad256(K), np.uint8)
+        sa, y = np.empty(1, np.float32), np.empty(N, np.float32)
+        pcl.check(pcl.lib.pcl_model_capture_read(m, l, prod, pcl.ptr(xin), pcl.ptr(xq), pcl.ptr(sa),
+                                                 pcl.ptr(y)))
+        return xin, xq, sa, y
+    return read
+
+
+@pytest.mark.parametrize("dims,npos", [(SMALL, 32), (MID, 24), (GROWN, 40), (WIDE_FF, 16)])
+def test_model_int8_products_pinned(tmp_path, dims, npos):
+    # same checkpoints and tokens as test_model_int8_forward_logits
+    blk, d, h, df, nl, v = dims
+    announce("model int8 products pinned", dims, npos)
+    path = str(tmp_path / "m.ckp1")
+    ob.write_ckp1(path, blk, d, h, df, nl, v, seed=51, wstd=0.05)
+    m = _load(path, pcl.W_INT8)
+    chk = Int8StepChecker(path)
+    toks = [int(t) % v for t in ob.u8((npos,), 53)]
+    got = np.empty(v, np.float32)
+    tapped = []
+    try:
+        pcl.check(pcl.lib.pcl_model_capture(m, 1))
+        src = _tap_source(m, dims)
+        for pos in range(npos):
+            pcl.check(pcl.lib.pcl_model_forward(m, toks[pos], pos, pcl.ptr(got)))
+            np.testing.assert_array_equal(got, chk.step(toks[pos], pos, source=src), err_msg=str(pos))
+            tapped.append(got.copy())
+        # the tap changes nothing: the same positions again with it off
+        pcl.check(pcl.lib.pcl_model_capture(m, 0))
+        for pos in range(npos):
+            pcl.check(pcl.lib.pcl_model_forward(m, toks[pos], pos, pcl.ptr(got)))
+            np.testing.assert_array_equal(got, tapped[pos])
+    finally:
+        chk.close()
+        pcl.lib.pcl_model_free(m)
+    print(f"quantised values {chk.values}, boundary flips {chk.flips}, attention rows <= {chk.att_err:.1e}",
+          flush=True)
+    assert chk.flips <= 1e-3 * chk.values
+
+
+def _check_greedy_eager(m, prompt, out):
+    """Each generated token is an argmax of the model's own eager logits for
+    its prefix (those logits being pinned product by product)."""
+    seq = list(prompt) + list(out)
+    lg = np.empty(pcl_vocab(m), np.float32)
+    for pos in range(len(seq) - 1):
+        pcl.check(pcl.lib.pcl_model_forward(m, seq[pos], pos, pcl.ptr(lg)))
+        if pos >= len(prompt) - 1:
+            assert lg[seq[pos + 1]] == lg.max(), pos
+
+
+def pcl_vocab(m):
+    hdr = np.empty(8, np.int32)
+    pcl.check(pcl.lib.pcl_model_header(m, pcl.ptr(hdr)))
+    return int(hdr[6])
+
+
 @pytest.mark.parametrize("dims,n_prompt,n_new", [(SMALL, 5, 27), (GROWN, 8, 56)])
 @pytest.mark.parametrize("graph", [0, 1])
 def test_model_int8_generate_greedy(tmp_path, dims, n_prompt, n_new, graph):
@@ -215,6 +289,7 @@ def test_model_int8_generate_greedy(tmp_path, dims, n_prompt, n_new, graph):
         out2 = np.full(n_new, -1, np.int32)
         pcl.check(pcl.lib.pcl_model_generate(m, pcl.ptr(prompt), n_prompt, n_new, pcl.ptr(out2), graph))
         np.testing.assert_array_equal(out, out2)
+        _check_greedy_eager(m, prompt.tolist(), out.tolist())
     finally:
         pcl.lib.pcl_model_free(m)
     _check_greedy(path, prompt.tolist(), out.tolist(), v, int8=True,

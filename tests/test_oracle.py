@@ -562,6 +562,91 @@ def test_decode_oracle_int8_near_ref_generate(tmp_path, dims):
     assert 1e-3 < max(errs) < 5e-2, errs
 
 
+# the small model, the grown model (16 layers, d 512, d_ff 2048, vocab 2048),
+# 8448-wide d_ff rows
+INT8_WALK_DIMS = [((32, 64, 4, 256, 2, 96), 12), ((256, 512, 16, 2048, 16, 2048), 3),
+                  ((16, 64, 4, 8448, 2, 96), 4)]
+
+
+@pytest.mark.parametrize("dims,npos", INT8_WALK_DIMS)
+def test_int8_step_walk_is_the_oracle_step(tmp_path, dims, npos):
+    # the op-by-op walk that checks the GPU's INT8 step, run on its own values,
+    # gives orc_model_forward_int8's logits bit for bit at every position: the
+    # same QKV column join, bias placement, residual order, cached attention,
+    # GELU input and head
+    from int8_steps import Int8StepChecker
+    blk, d, h, df, nl, v = dims
+    path = str(tmp_path / "m.ckp1")
+    ob.write_ckp1(path, blk, d, h, df, nl, v, seed=51, wstd=0.05)
+    chk = Int8StepChecker(path)
+    om = ob.OracleModel(path, int8=True)
+    toks = [int(t) % v for t in ob.u8((npos,), 53)]
+    try:
+        for pos in range(npos):
+            np.testing.assert_array_equal(chk.step(toks[pos], pos), om.forward(toks[pos], pos))
+    finally:
+        chk.close()
+        om.close()
+
+
+def test_int8_step_walk_catches_planted_mistakes(tmp_path):
+    # the walk's own record, fed back as the source, passes with no byte
+    # difference; each planted mistake in it (a bias dropped from a residual,
+    # an attention value off by 1e-4 relative, a quantised byte off by one away
+    # from any rounding boundary, a scale off by 1e-4, a product off by one
+    # ulp, a d_ff row not the FF1 output) fails
+    from int8_steps import Int8StepChecker
+    blk, d, h, df, nl, v = 8, 64, 4, 256, 2, 96
+    path = str(tmp_path / "m.ckp1")
+    ob.write_ckp1(path, blk, d, h, df, nl, v, seed=57, wstd=0.05)
+    src = Int8StepChecker(path)
+    src.step(5, 0)
+    rec = src.record
+    src.close()
+
+    def run(plant=None):
+        r = {k: [np.array(a, copy=True) for a in vals] for k, vals in rec.items()}
+        if plant:
+            plant(r)
+        chk = Int8StepChecker(path)
+        try:
+            chk.step(5, 0, source=lambda l, pr: tuple(r[(l, pr)]))
+            return chk.flips
+        finally:
+            chk.close()
+
+    assert run() == 0
+    lw = ob.read_ckp1(path)["layers"]
+
+    def drop_bias(r):
+        r[(1, 0)][0] -= lw[0]["bff2"]
+
+    def att_off(r):
+        a = r[(1, 1)][0]
+        a[np.argmax(np.abs(a))] *= np.float32(1 + 1e-4)
+
+    def byte_off(r):
+        xf = r[(0, 1)][0]
+        q, sa = ob.quantize_row(xf, 256)
+        t = np.abs(xf / sa[0])
+        k = int(np.flatnonzero(np.abs(t - np.round(t)) < 0.25)[0])  # far from a boundary
+        r[(0, 1)][1][k] = np.uint8(int(r[(0, 1)][1][k]) + (1 if r[(0, 1)][1][k] < 255 else -1))
+
+    def scale_off(r):
+        r[(1, 2)][2] *= np.float32(1 + 1e-4)
+
+    def ulp_off(r):
+        y = r[(0, 3)][3]
+        y[7] = np.nextafter(y[7], np.float32(np.inf))
+
+    def ff_row(r):
+        r[(1, 3)][0][0] += np.float32(1e-3)
+
+    for plant in (drop_bias, att_off, byte_off, scale_off, ulp_off, ff_row):
+        with pytest.raises(AssertionError):
+            run(plant)
+
+
 
 # -------------------------------------------------- cross-entropy ----
 def _ce_inputs(M, V, seed, scale=3.0):
