@@ -293,6 +293,15 @@ int pcl_head_ce(const float *lnf, const float *wte, const int *targets, int M, i
 int pcl_attn_fwd(const float *Q, const float *K, const float *V, int ld, float *att, int ld_att,
                  float *probs, int B, int T, int H, int dh, void *stream);
 
+/* The forward without probabilities, in one pass (a running row maximum;
+ * pcl_attn_fwd takes the same path when probs is NULL): no counterpart in the
+ * reference's interface, whose forward always stores probabilities. att as
+ * pcl_attn_fwd (within fp32 rounding of it); lse NULL or (B*H) x T floats,
+ * lse[(b*H + h)*T + i] = log sum_{j<=i} exp(q_i.k_j / sqrtf(dh)), so that
+ * p_ij = exp(q_i.k_j / sqrtf(dh) - lse_i). Limits as pcl_attn_fwd. */
+int pcl_attn_fwd_lse(const float *Q, const float *K, const float *V, int ld, float *att, int ld_att,
+                     float *lse, int B, int T, int H, int dh, void *stream);
+
 /* Its backward from the stored probs (train.c:374-407, gpu_kernels.cu:437-486):
  *   dP_ij = dAtt_i.v_j, D_i = sum_j p_ij dP_ij, dS_ij = p_ij (dP_ij - D_i)/sqrtf(dh),
  *   dQ_i = sum_j dS_ij k_j, dK_j = sum_i dS_ij q_i, dV_j = sum_i p_ij dAtt_i.

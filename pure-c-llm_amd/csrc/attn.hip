@@ -144,7 +144,10 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const float *__restric
     const int b = bh / H, h = bh % H;
     const long row0 = (long)b * T;  // first token row of this sequence
     const int hc = h * DH;          // first column of this head
-    const int q0 = qblk * AT_QB, q0w = q0 + wave * 32;
+    // the light half takes its 32-query slices in reverse wave order, so the
+    // waves sharing a SIMD (one from each half) sum to the same work
+    const int wslot = L < half ? wave : 3 - wave;
+    const int q0 = qblk * AT_QB, q0w = q0 + wslot * 32;
     const int qi = q0w + r32;              // this lane's query
     const int qlast = min(T - 1, q0 + AT_QB - 1);
     const int kb_last = qlast / AT_KB;     // last key block of the workgroup
@@ -266,6 +269,108 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const float *__restric
             float *zr = P + ((long)bh * T + q0w + rr) * T;
             for (int c = c0 + lane; c < T; c += 64) zr[c] = 0.f;
         }
+    }
+}
+
+// One pass with a running maximum, for callers that need no probabilities:
+// per key block the two lanes of a query agree on the new maximum (one
+// exchange), rescale their row sum and O^T accumulators by exp(m_old - m_new)
+// and add exp(s - m_new) . v. Scores are computed once (2/3 of the two-pass
+// matrix work); att = O / l, and the row's log-sum-exp m + log(l) is stored
+// when lse is given (p_ij = exp(scale q_i.k_j - lse_i)).
+template <int DH>
+__global__ __launch_bounds__(256, 2) void attn_fwd_online_kernel(const float *__restrict__ Q,
+                                                                 const float *__restrict__ K,
+                                                                 const float *__restrict__ V, long ld,
+                                                                 float *__restrict__ O, long ldo,
+                                                                 float *__restrict__ lse, int T, int H,
+                                                                 int BH, float scale) {
+    using TL = AttnTile<DH>;
+    __shared__ __attribute__((aligned(16))) float lds[2 * (TL::KFL + TL::VFL)];
+    const int tid = threadIdx.x, lane = tid & 63, r32 = lane & 31, lg = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nqb = (T + AT_QB - 1) / AT_QB, half = (nqb + 1) / 2;
+    const int L = (int)(blockIdx.x / BH), bh = (int)(blockIdx.x % BH);
+    const int qblk = L < half ? nqb - 1 - L : L - half;
+    // the light half takes its 32-query slices in reverse wave order, so the
+    // waves sharing a SIMD (one from each half) sum to the same work
+    const int wslot = L < half ? wave : 3 - wave;
+    const int b = bh / H, h = bh % H;
+    const long row0 = (long)b * T;
+    const int hc = h * DH;
+    const int q0 = qblk * AT_QB, q0w = q0 + wslot * 32;
+    const int qi = q0w + r32;
+    const int qlast = min(T - 1, q0 + AT_QB - 1);
+    const int kb_last = qlast / AT_KB;
+    const int kbw = q0w < T ? min(T - 1, q0w + 31) / AT_KB : -1;
+
+    v4f qf[DH / 8];
+    {
+        const float *qrow = Q + (row0 + min(qi, T - 1)) * ld + hc + 4 * lg;
+#pragma unroll
+        for (int q = 0; q < DH / 8; q++) qf[q] = *reinterpret_cast<const v4f *>(qrow + 8 * q);
+    }
+    auto Kb = [&](int u) { return lds + (u & 1) * (TL::KFL + TL::VFL); };
+    auto Vb = [&](int u) { return lds + (u & 1) * (TL::KFL + TL::VFL) + TL::KFL; };
+    v4f kr[TL::PT], vr[TL::PT];
+
+    v16f oacc[DH / 32];
+#pragma unroll
+    for (int nb = 0; nb < DH / 32; nb++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) oacc[nb][v] = 0.f;
+    float m = -INFINITY, l = 0.f;
+    at_load<DH>(kr, K + hc, ld, row0, 0, T, tid);
+    at_load<DH>(vr, V + hc, ld, row0, 0, T, tid);
+    at_store<DH, TL::KS>(Kb(0), kr, tid);
+    at_store<DH, TL::VS>(Vb(0), vr, tid);
+    __syncthreads();
+    for (int kb = 0; kb <= kb_last; kb++) {
+        if (kb < kb_last) {
+            at_load<DH>(kr, K + hc, ld, row0, (kb + 1) * AT_KB, T, tid);
+            at_load<DH>(vr, V + hc, ld, row0, (kb + 1) * AT_KB, T, tid);
+        }
+        if (kb <= kbw) {
+            const v16f s = at_scores<DH>(Kb(kb), qf, r32, lg);
+            float x[16], bm = -INFINITY;
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const int j = kb * AT_KB + at_key(v, lg);
+                x[v] = (j <= qi && j < T) ? s[v] * scale : -INFINITY;
+                bm = fmaxf(bm, x[v]);
+            }
+            // key 0 is visible to every query, so the first block makes mn finite
+            const float mn = fmaxf(m, fmaxf(bm, __shfl_xor(bm, 32)));
+            const float alpha = __expf(m - mn);  // 0 on the first block (m = -inf)
+            float p[16], ps = 0.f;
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                p[v] = __expf(x[v] - mn);
+                ps += p[v];
+            }
+            l = l * alpha + ps;
+            m = mn;
+#pragma unroll
+            for (int nb = 0; nb < DH / 32; nb++)
+#pragma unroll
+                for (int v = 0; v < 16; v++) oacc[nb][v] *= alpha;
+            at_accum<DH>(oacc, Vb(kb), p, r32, lg);
+        }
+        if (kb < kb_last) {
+            at_store<DH, TL::KS>(Kb(kb + 1), kr, tid);
+            at_store<DH, TL::VS>(Vb(kb + 1), vr, tid);
+        }
+        __syncthreads();
+    }
+    l += __shfl_xor(l, 32);  // the two key halves share m
+    if (qi < T) {
+        const float inv = 1.f / l;
+        float *orow = O + (row0 + qi) * ldo + hc;
+#pragma unroll
+        for (int nb = 0; nb < DH / 32; nb++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) orow[nb * 32 + at_key(v, lg)] = oacc[nb][v] * inv;
+        if (lse && lg == 0) lse[(long)bh * T + qi] = m + logf(l);
     }
 }
 
@@ -529,10 +634,27 @@ hipError_t launch_attn_bwd(const float *dO, long ldo, const float *Q, const floa
 
 hipError_t launch_attn_fwd(const float *Q, const float *K, const float *V, long ld, float *O,
                            long ldo, float *P, int B, int T, int H, int dh, float scale,
-                           hipStream_t stream) {
+                           hipStream_t stream, float *lse) {
     const int BH = B * H, nqb = (T + AT_QB - 1) / AT_QB;
     if (BH == 0 || T == 0) return hipSuccess;
     const dim3 grid((unsigned)((long)nqb * BH)), block(256);
+    if (P == nullptr) {  // no probabilities: one pass
+        switch (dh) {
+            case 32:
+                hipLaunchKernelGGL(attn_fwd_online_kernel<32>, grid, block, 0, stream, Q, K, V, ld, O, ldo, lse, T, H, BH, scale);
+                break;
+            case 64:
+                hipLaunchKernelGGL(attn_fwd_online_kernel<64>, grid, block, 0, stream, Q, K, V, ld, O, ldo, lse, T, H, BH, scale);
+                break;
+            case 128:
+                hipLaunchKernelGGL(attn_fwd_online_kernel<128>, grid, block, 0, stream, Q, K, V, ld, O, ldo, lse, T, H, BH, scale);
+                break;
+            default:
+                return hipErrorInvalidValue;
+        }
+        return hipGetLastError();
+    }
+    if (lse) return hipErrorInvalidValue;
     switch (dh) {
         case 32:
             hipLaunchKernelGGL(attn_fwd_kernel<32>, grid, block, 0, stream, Q, K, V, ld, O, ldo, P, T, H, BH, scale);

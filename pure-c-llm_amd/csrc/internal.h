@@ -73,9 +73,11 @@ hipError_t launch_pad_a_u8(const uint8_t *A, long lda, int M, int K, uint8_t *ds
 // Q, K, V: (B*T) x ld row-major, head h at columns [h*dh, (h+1)*dh); O: (B*T) x
 // ldo; P: NULL or [B*H][T][T] probabilities (zero above the diagonal).
 // dh in {32, 64, 128}; ld, ldo multiples of 4 and 16-byte aligned bases.
+// Without P the one-pass kernel runs, and lse (NULL or (B*H) x T floats)
+// receives each row's log-sum-exp of the scaled scores.
 hipError_t launch_attn_fwd(const float *Q, const float *K, const float *V, long ld, float *O,
                            long ldo, float *P, int B, int T, int H, int dh, float scale,
-                           hipStream_t stream);
+                           hipStream_t stream, float *lse = nullptr);
 
 // Backward from the stored probabilities P: dQ, dK, dV ((B*T) x ldg) set or,
 // with accumulate, added to; dS ([B*H][T][T]) is written as scratch (entries

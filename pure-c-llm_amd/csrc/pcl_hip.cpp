@@ -853,6 +853,33 @@ int pcl_attn_fwd(const float *Q, const float *K, const float *V, int ld, float *
     return PCL_OK;
 }
 
+int pcl_attn_fwd_lse(const float *Q, const float *K, const float *V, int ld, float *att, int ld_att,
+                     float *lse, int B, int T, int H, int dh, void *stream) {
+    CHECK_ARG(B >= 0 && T >= 0 && H >= 0, "pcl_attn_fwd_lse: negative dimension (B=%d T=%d H=%d)",
+              B, T, H);
+    CHECK_ARG(dh == 32 || dh == 64 || dh == 128,
+              "pcl_attn_fwd_lse: head size %d is not 32, 64 or 128", dh);
+    if (B == 0 || T == 0 || H == 0) return PCL_OK;
+    CHECK_ARG(Q && K && V && att, "pcl_attn_fwd_lse: NULL operand");
+    CHECK_ARG(ld >= H * dh && ld_att >= H * dh, "pcl_attn_fwd_lse: ld=%d / ld_att=%d < H*dh=%d", ld,
+              ld_att, H * dh);
+    CHECK_ARG(ld % 4 == 0 && ld_att % 4 == 0,
+              "pcl_attn_fwd_lse: ld=%d, ld_att=%d not multiples of 4", ld, ld_att);
+    CHECK_ARG(aligned16(Q) && aligned16(K) && aligned16(V) && aligned16(att),
+              "pcl_attn_fwd_lse: Q, K, V and att must be 16-byte aligned");
+    CHECK_ARG((long)B * T <= INT32_MAX && (long)B * H * T <= INT32_MAX,
+              "pcl_attn_fwd_lse: B*T or B*H*T beyond 2^31");
+    if (lse) {
+        const long n = (long)B * H * T;
+        CHECK_ARG(!ranges_overlap(lse, 4 * n, att, 4 * ((long)(B * T - 1) * ld_att + H * dh)),
+                  "pcl_attn_fwd_lse: lse overlaps att");
+    }
+    PCL_OK_OR_RETURN(do_init());
+    HIP_OK(pcl::launch_attn_fwd(Q, K, V, ld, att, ld_att, nullptr, B, T, H, dh,
+                                1.0f / sqrtf((float)dh), pick(stream), lse));
+    return PCL_OK;
+}
+
 int pcl_attn_bwd(float *dQ, float *dK, float *dV, int ld_grad, float *scratch, const float *dAtt,
                  int ld_att, const float *Q, const float *K, const float *V, int ld,
                  const float *probs, int B, int T, int H, int dh, int accumulate, void *stream) {

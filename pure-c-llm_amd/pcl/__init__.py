@@ -108,6 +108,7 @@ _PROTOS = {
     "pcl_gelu_bwd": (_i, [_vp, _vp, _vp, C.c_long, _vp]),
     "pcl_vec_add": (_i, [_vp, _vp, _vp, C.c_long, _vp]),
     "pcl_attn_fwd": (_i, [_vp, _vp, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i, _vp]),
+    "pcl_attn_fwd_lse": (_i, [_vp, _vp, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i, _vp]),
     "pcl_attn_bwd": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _vp, _i, _vp, _i, _i, _i, _i, _i, _vp]),
     "pcl_cross_entropy": (_i, [_vp, _i, _vp, _vp, _i, _i, _i, _vp, _vp]),
     "pcl_head_ce": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp, _vp, _vp, C.c_long, _vp]),

@@ -62,13 +62,51 @@ def test_attn_fwd_vs_oracle(B, T, H, dh):
     assert np.all(np.triu(pr, 1) == 0.0)
 
 
-def test_attn_fwd_without_probs_is_identical():
+def attn_lse(q, k, v, B, T, H, dh):
+    """pcl_attn_fwd_lse: (att, lse (B*H) x T)."""
+    dq, dk, dv = pcl.dev(q), pcl.dev(k), pcl.dev(v)
+    datt = pcl.dev(np.full((B * T, H * dh), np.nan, np.float32))
+    dl = pcl.dev(np.full((B * H, T), np.nan, np.float32))
+    pcl.check(pcl.lib.pcl_attn_fwd_lse(dq.ptr, dk.ptr, dv.ptr, q.shape[1], datt.ptr, H * dh, dl.ptr,
+                                       B, T, H, dh, None))
+    pcl.sync()
+    return datt.download((B * T, H * dh), np.float32), dl.download((B * H, T), np.float32)
+
+
+def probs_from_lse(q, k, lse, B, T, H, dh):
+    """p_ij = exp(s_ij - lse_i) for j <= i, s = q.k / sqrtf(dh) in f64."""
+    scale = np.float64(1.0 / np.sqrt(np.float32(dh)))
+    P = np.zeros((B * H, T, T))
+    for b in range(B):
+        for h in range(H):
+            c = slice(h * dh, (h + 1) * dh)
+            S = q[b * T:(b + 1) * T, c].astype(np.float64) @ k[b * T:(b + 1) * T, c].astype(np.float64).T
+            P[b * H + h] = np.tril(np.exp(S * scale - lse[b * H + h][:, None]))
+    return P
+
+
+@pytest.mark.parametrize("B,T,H,dh", SHAPES)
+def test_attn_fwd_one_pass_and_lse_vs_oracle(B, T, H, dh):
+    # the one-pass kernel (no probabilities): att against the oracle, and the
+    # row log-sum-exp reproduces the oracle's probabilities exp(s - lse)
+    announce("attn_fwd one pass", B, T, H, dh)
+    q, k, v = _qkv(B, T, H * dh, 300 + T + dh)
+    att, lse = attn_lse(q, k, v, B, T, H, dh)
+    att_r, pr_r = ob.attention_forward(q, k, v, B, T, H, dh)
+    assert rel(att, att_r) <= FP32_TOL
+    assert rel(probs_from_lse(q, k, lse, B, T, H, dh), pr_r) <= FP32_TOL
+    # pcl_attn_fwd without probabilities is the same kernel
+    a2, _ = attn(q, k, v, B, T, H, dh, probs=False)
+    np.testing.assert_array_equal(att, a2)
+
+
+def test_attn_fwd_without_probs_agrees():
     B, T, H, dh = 2, 160, 2, 64
     announce("attn_fwd probs=NULL", B, T, H, dh)
     q, k, v = _qkv(B, T, H * dh, 410)
     a1, _ = attn(q, k, v, B, T, H, dh)
     a2, _ = attn(q, k, v, B, T, H, dh, probs=False)
-    np.testing.assert_array_equal(a1, a2)
+    assert rel(a2, a1) <= FP32_TOL
 
 
 def test_attn_fwd_fused_qkv_buffer():
@@ -94,6 +132,11 @@ def test_attn_fwd_large_scores():
     assert np.isfinite(att).all()
     assert rel(att, att_r) <= FP32_TOL
     assert rel(pr, pr_r) <= FP32_TOL
+    # the one-pass kernel rescales as the running maximum grows
+    att1, lse = attn_lse(q, k, v, B, T, H, dh)
+    assert np.isfinite(att1).all() and np.isfinite(lse).all()
+    assert rel(att1, att_r) <= FP32_TOL
+    assert rel(probs_from_lse(q, k, lse, B, T, H, dh), pr_r) <= FP32_TOL
 
 
 @pytest.mark.parametrize("B,T,H,dh", [(4, 1024, 16, 64), (4, 1024, 12, 128), (1, 256, 16, 32)])
@@ -117,6 +160,19 @@ def test_attn_fwd_full_size_properties(B, T, H, dh):
         p /= p.sum()
         o = p @ v[rows, cols].astype(np.float64)
         worst = max(worst, rel(att[b * T + i, cols], o), rel(pr[b * H + h, i, : i + 1], p))
+    assert worst <= FP32_TOL
+    # the one-pass kernel at the same size: sampled rows and their log-sum-exp
+    att1, lse = attn_lse(q, k, v, B, T, H, dh)
+    worst = 0.0
+    for _ in range(24):
+        b, h, i = int(rng.integers(B)), int(rng.integers(H)), int(rng.integers(T))
+        rows = slice(b * T, b * T + i + 1)
+        cols = slice(h * dh, (h + 1) * dh)
+        s = (k[rows, cols].astype(np.float64) @ q[b * T + i, cols].astype(np.float64)) * np.float64(scale)
+        ls = s.max() + np.log(np.exp(s - s.max()).sum())
+        o = np.exp(s - ls) @ v[rows, cols].astype(np.float64)
+        worst = max(worst, rel(att1[b * T + i, cols], o))
+        assert abs(lse[b * H + h, i] - ls) <= 1e-5 * max(1.0, abs(ls))
     assert worst <= FP32_TOL
 
 
@@ -150,7 +206,13 @@ def test_attn_fwd_argument_errors():
                  (q.ptr, q.ptr, q.ptr, 30, q.ptr, 64, None, 1, 64, 1, 32, None),   # ld < H*dh
                  (q.ptr + 4, q.ptr, q.ptr, 64, q.ptr, 64, None, 1, 16, 1, 32, None)]:  # alignment
         assert pcl.lib.pcl_attn_fwd(*args) == pcl.PCL_ERR_INVALID_ARG
+        assert pcl.lib.pcl_attn_fwd_lse(*args) == pcl.PCL_ERR_INVALID_ARG
         pcl.lib.pcl_clear_error()
+    # lse may not overlap att
+    a = pcl.empty((64, 64), np.float32)
+    assert pcl.lib.pcl_attn_fwd_lse(q.ptr, q.ptr, q.ptr, 64, a.ptr, 64, a.ptr + 4 * 64, 1, 64, 2, 32,
+                                    None) == pcl.PCL_ERR_INVALID_ARG
+    pcl.lib.pcl_clear_error()
 
 
 # ------------------------------------------------------------- backward ----
