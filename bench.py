@@ -52,11 +52,12 @@ def load_bench():
                                          C.POINTER(d)]
     lib.pcl_bench_attn.argtypes = [i, i, i, i, i, i, i, C.POINTER(d)]
     lib.pcl_bench_attn_bwd.argtypes = [i, i, i, i, i, i, C.POINTER(d)]
+    lib.pcl_bench_attn_bwd_ex.argtypes = [i, i, i, i, i, i, i, C.POINTER(d)]
     lib.pcl_bench_sgemm_ex.argtypes = [i, i, i, i, i, i, i, i, i, C.POINTER(d)]
     lib.pcl_bench_head_ce.argtypes = [i, i, i, C.c_long, i, i, i, C.POINTER(d)]
     for f in (lib.pcl_bench_igemm, lib.pcl_bench_igemm_ex, lib.pcl_bench_sgemm, lib.pcl_bench_gemv, lib.pcl_bench_gemv_group,
               lib.pcl_bench_attn,
-              lib.pcl_bench_attn_bwd, lib.pcl_bench_sgemm_ex, lib.pcl_bench_head_ce):
+              lib.pcl_bench_attn_bwd, lib.pcl_bench_attn_bwd_ex, lib.pcl_bench_sgemm_ex, lib.pcl_bench_head_ce):
         f.restype = i
     return pcl, lib
 
@@ -136,18 +137,22 @@ def attn(pcl, lib, B, T, H, dh, with_probs, warmup, steps):
             "probs_GBps": round(probs_bytes / (per * 1e-3) / 1e9, 1)}
 
 
-def attn_bwd(pcl, lib, B, T, H, dh, warmup, steps):
+def attn_bwd(pcl, lib, B, T, H, dh, warmup, steps, with_att=False):
     """Causal attention backward from stored probabilities. Algorithmic FLOPs:
-    dV, dP, dQ, dK over the causal triangle, 8*B*H*dh*T(T+1)/2 (dP is issued
-    twice: 1.25x); HBM: P read three times, dS written once and read once."""
+    dV, dP, dQ, dK over the causal triangle, 8*B*H*dh*T(T+1)/2. From P alone
+    dP is issued twice (1.25x) and P read three times; handed the forward's
+    output (pcl_attn_bwd_ex) dP is issued once (1.0x) and P read twice; dS is
+    written once and read once."""
     ms = C.c_double(0)
-    _check(pcl, lib.pcl_bench_attn_bwd(B, T, H, dh, warmup, steps, C.byref(ms)), f"attn_bwd B{B} T{T} H{H} dh{dh}")
+    _check(pcl, lib.pcl_bench_attn_bwd_ex(B, T, H, dh, int(with_att), warmup, steps, C.byref(ms)),
+           f"attn_bwd B{B} T{T} H{H} dh{dh}")
     per = ms.value / steps
     flops = 8.0 * B * H * dh * T * (T + 1) / 2
     tf = flops / (per * 1e-3) / 1e12
-    tt_bytes = 5 * 4.0 * B * H * T * (T + 1) / 2
-    return {"B": B, "T": T, "H": H, "dh": dh, "ms": round(per, 5), "TFLOPS": round(tf, 2),
-            "frac_peak": round(tf / PEAK_F32_TFLOPS, 4), "mfma_TFLOPS_issued": round(1.25 * tf, 2),
+    tt_bytes = (4 if with_att else 5) * 4.0 * B * H * T * (T + 1) / 2
+    return {"B": B, "T": T, "H": H, "dh": dh, "with_att": bool(with_att), "ms": round(per, 5),
+            "TFLOPS": round(tf, 2), "frac_peak": round(tf / PEAK_F32_TFLOPS, 4),
+            "mfma_TFLOPS_issued": round((1.0 if with_att else 1.25) * tf, 2),
             "causal_TT_GBps": round(tt_bytes / (per * 1e-3) / 1e9, 1)}
 
 
@@ -407,6 +412,7 @@ CASES = {
     "attn_350m_noprobs": lambda pcl, lib, w, s: attn(pcl, lib, 4, 1024, 16, 64, False, w, s),
     "attn_trainer_dh128": lambda pcl, lib, w, s: attn(pcl, lib, 4, 1024, 12, 128, True, w, s),
     "attn_bwd_350m": lambda pcl, lib, w, s: attn_bwd(pcl, lib, 4, 1024, 16, 64, w, s),
+    "attn_bwd_350m_with_att": lambda pcl, lib, w, s: attn_bwd(pcl, lib, 4, 1024, 16, 64, w, s, True),
     "attn_bwd_trainer_dh128": lambda pcl, lib, w, s: attn_bwd(pcl, lib, 4, 1024, 12, 128, w, s),
     "gemv_head_fp32_m1": lambda pcl, lib, w, s: gemv(pcl, lib, 1, 1, [(1024, 50257)], 3, w, s),
     "gemv_head_int8_m1": lambda pcl, lib, w, s: gemv(pcl, lib, 2, 1, [(1024, 50257)], 6, w, s),
@@ -651,6 +657,7 @@ def run_rows(pcl, lib):
     }
     ex["attn_bwd"] = {
         "350m": attn_bwd(pcl, lib, 4, 1024, 16, 64, w, s),
+        "350m_with_att": attn_bwd(pcl, lib, 4, 1024, 16, 64, w, s, True),
         "trainer_dh128": attn_bwd(pcl, lib, 4, 1024, 12, 128, w, s),
         "grown_t256": attn_bwd(pcl, lib, 1, 256, 16, 32, w, 50),
     }
@@ -682,7 +689,8 @@ def compact_rows(ex, roofs):
                                 for dt in ("fp32", "int8") for m in ("M1", "M8")}
     r["attn_350m_TFLOPS"] = {"fwd_probs": ex["attn_fwd"]["350m_probs"]["TFLOPS"],
                              "fwd_one_pass": ex["attn_fwd"]["350m_no_probs"]["TFLOPS"],
-                             "bwd": ex["attn_bwd"]["350m"]["TFLOPS"]}
+                             "bwd": ex["attn_bwd"]["350m"]["TFLOPS"],
+                             "bwd_with_att": ex["attn_bwd"]["350m_with_att"]["TFLOPS"]}
     r["head_ce_350m"] = {"TFLOPS": ex["head_ce"]["350m"]["TFLOPS"], "ms": ex["head_ce"]["350m"]["ms"]}
     e = ex["decode_e2e_grown"]
     r["decode_e2e_grown_tok_s"] = {"fp32": e.get("eager_tokens_per_s"), "fp32_graph": e.get("graph_tokens_per_s"),

@@ -313,6 +313,17 @@ int pcl_attn_bwd(float *dQ, float *dK, float *dV, int ld_grad, float *scratch, c
                  int ld_att, const float *Q, const float *K, const float *V, int ld,
                  const float *probs, int B, int T, int H, int dh, int accumulate, void *stream);
 
+/* pcl_attn_bwd given also the forward's output att ((B*T) x ld_o, ld_o a
+ * multiple of 4, 16-byte aligned): D_i = dAtt_i . att_i replaces the pass over
+ * P and dP that forms D_i = sum_j p_ij dP_ij (the same sum, since att_i =
+ * sum_j p_ij v_j), so the query-block kernel reads P once and issues dP once.
+ * Results within fp32 rounding of pcl_attn_bwd. No counterpart in the
+ * reference's interface, whose backward is not handed the forward's output. */
+int pcl_attn_bwd_ex(float *dQ, float *dK, float *dV, int ld_grad, float *scratch,
+                    const float *dAtt, int ld_att, const float *Q, const float *K, const float *V,
+                    int ld, const float *probs, const float *att, int ld_o, int B, int T, int H,
+                    int dh, int accumulate, void *stream);
+
 /* ---- INT8: u8 activations x s8 weights -> int32 (gemm_bench.c:212-285) ----
  * Weights live in the GPU-native packed layout: N rows of Kp = pcl_s8_kpad(K)
  * bytes (K-contiguous per output column, zero-padded), i.e. B^T. */

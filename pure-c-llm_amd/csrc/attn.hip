@@ -392,7 +392,8 @@ template <int DH>
 __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(
     const float *__restrict__ dO, long ldo, const float *__restrict__ K,
     const float *__restrict__ V, long ld, const float *__restrict__ P, float *__restrict__ dS,
-    float *__restrict__ dQ, long ldg, int T, int H, int BH, float scale, int accumulate) {
+    float *__restrict__ dQ, long ldg, int T, int H, int BH, float scale, int accumulate,
+    const float *__restrict__ Ofw, long ldfw) {
     using TL = AttnTile<DH>;
     __shared__ __attribute__((aligned(16))) float lds[2 * (TL::KFL + TL::VFL)];
     const int tid = threadIdx.x, lane = tid & 63, r32 = lane & 31, lg = lane >> 5;
@@ -438,27 +439,39 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(
         }
     };
 
-    // ---- pass 1: D_i = sum_j P_ij dP_ij (this lane's half of the keys)
-    // P rows are fetched one key block ahead of their use (HBM latency is
-    // about one block of MFMA work)
+    // ---- pass 1: D_i = sum_j P_ij dP_ij (this lane's half of the keys), or,
+    // given the forward's output, D_i = dO_i . att_i (the same sum, since
+    // att_i = sum_j P_ij v_j) from the lane's half of the row
     float Dsum = 0.f, pn[16];
-    at_load<DH>(vr, V + hc, ld, row0, 0, T, tid);
-    if (kbw >= 0) load_p(P, 0, pn);
-    at_store<DH, TL::KS>(Vs(0), vr, tid);
-    __syncthreads();
-    for (int kb = 0; kb <= kb_last; kb++) {
-        if (kb < kb_last) at_load<DH>(vr, V + hc, ld, row0, (kb + 1) * AT_KB, T, tid);
-        if (kb <= kbw) {
-            float pv[16];
+    if (Ofw) {
+        const float *orow = Ofw + (row0 + min(qi, T - 1)) * ldfw + hc + 4 * lg;
 #pragma unroll
-            for (int v = 0; v < 16; v++) pv[v] = pn[v];
-            if (kb < kbw) load_p(P, kb + 1, pn);
-            const v16f dp = at_scores<DH>(Vs(kb), df, r32, lg);
+        for (int q = 0; q < DH / 8; q++) {
+            const v4f o = *reinterpret_cast<const v4f *>(orow + 8 * q);
 #pragma unroll
-            for (int v = 0; v < 16; v++) Dsum += pv[v] * dp[v];
+            for (int e = 0; e < 4; e++) Dsum += df[q][e] * o[e];
         }
-        if (kb < kb_last) at_store<DH, TL::KS>(Vs(kb + 1), vr, tid);
+    } else {
+        // P rows are fetched one key block ahead of their use (HBM latency is
+        // about one block of MFMA work)
+        at_load<DH>(vr, V + hc, ld, row0, 0, T, tid);
+        if (kbw >= 0) load_p(P, 0, pn);
+        at_store<DH, TL::KS>(Vs(0), vr, tid);
         __syncthreads();
+        for (int kb = 0; kb <= kb_last; kb++) {
+            if (kb < kb_last) at_load<DH>(vr, V + hc, ld, row0, (kb + 1) * AT_KB, T, tid);
+            if (kb <= kbw) {
+                float pv[16];
+#pragma unroll
+                for (int v = 0; v < 16; v++) pv[v] = pn[v];
+                if (kb < kbw) load_p(P, kb + 1, pn);
+                const v16f dp = at_scores<DH>(Vs(kb), df, r32, lg);
+#pragma unroll
+                for (int v = 0; v < 16; v++) Dsum += pv[v] * dp[v];
+            }
+            if (kb < kb_last) at_store<DH, TL::KS>(Vs(kb + 1), vr, tid);
+            __syncthreads();
+        }
     }
     Dsum += __shfl_xor(Dsum, 32);
 
@@ -613,13 +626,14 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkv_kernel(
 hipError_t launch_attn_bwd(const float *dO, long ldo, const float *Q, const float *K,
                            const float *V, long ld, const float *P, float *dS, float *dQ,
                            float *dK, float *dV, long ldg, int B, int T, int H, int dh,
-                           float scale, int accumulate, hipStream_t stream) {
+                           float scale, int accumulate, hipStream_t stream, const float *Ofw,
+                           long ldfw) {
     const int BH = B * H, nb = (T + AT_QB - 1) / AT_QB;
     if (BH == 0 || T == 0) return hipSuccess;
     const dim3 grid((unsigned)((long)nb * BH)), block(256);
 #define PCL_ATTN_BWD(D)                                                                            \
     hipLaunchKernelGGL(attn_bwd_dq_kernel<D>, grid, block, 0, stream, dO, ldo, K, V, ld, P, dS, dQ,  \
-                       ldg, T, H, BH, scale, accumulate);                                          \
+                       ldg, T, H, BH, scale, accumulate, Ofw, ldfw);                               \
     hipLaunchKernelGGL(attn_bwd_dkv_kernel<D>, grid, block, 0, stream, dO, ldo, Q, ld, P, dS, dK, dV, \
                        ldg, T, H, BH, accumulate)
     switch (dh) {

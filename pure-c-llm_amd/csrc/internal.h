@@ -81,11 +81,14 @@ hipError_t launch_attn_fwd(const float *Q, const float *K, const float *V, long 
 
 // Backward from the stored probabilities P: dQ, dK, dV ((B*T) x ldg) set or,
 // with accumulate, added to; dS ([B*H][T][T]) is written as scratch (entries
-// j <= i of each causal row). dO is (B*T) x ldo.
+// j <= i of each causal row). dO is (B*T) x ldo. Ofw (NULL, or the forward's
+// output, (B*T) x ldfw) gives D_i = dO_i . att_i directly instead of the
+// query-block kernel's first pass over P and dP.
 hipError_t launch_attn_bwd(const float *dO, long ldo, const float *Q, const float *K,
                            const float *V, long ld, const float *P, float *dS, float *dQ,
                            float *dK, float *dV, long ldg, int B, int T, int H, int dh,
-                           float scale, int accumulate, hipStream_t stream);
+                           float scale, int accumulate, hipStream_t stream,
+                           const float *Ofw = nullptr, long ldfw = 0);
 
 // ---- decode step (decode.hip); tokpos = {token, position} in device memory ----
 hipError_t launch_decode_embed(const float *wte, const float *wpe, float *x, int D,

@@ -880,23 +880,26 @@ int pcl_attn_fwd_lse(const float *Q, const float *K, const float *V, int ld, flo
     return PCL_OK;
 }
 
-int pcl_attn_bwd(float *dQ, float *dK, float *dV, int ld_grad, float *scratch, const float *dAtt,
-                 int ld_att, const float *Q, const float *K, const float *V, int ld,
-                 const float *probs, int B, int T, int H, int dh, int accumulate, void *stream) {
-    CHECK_ARG(B >= 0 && T >= 0 && H >= 0, "pcl_attn_bwd: negative dimension (B=%d T=%d H=%d)", B,
-              T, H);
-    CHECK_ARG(dh == 32 || dh == 64 || dh == 128, "pcl_attn_bwd: head size %d is not 32, 64 or 128",
-              dh);
+namespace {
+int attn_bwd_common(const char *fn, float *dQ, float *dK, float *dV, int ld_grad, float *scratch,
+                    const float *dAtt, int ld_att, const float *Q, const float *K, const float *V,
+                    int ld, const float *probs, const float *att, int ld_o, int B, int T, int H,
+                    int dh, int accumulate, void *stream) {
+    CHECK_ARG(B >= 0 && T >= 0 && H >= 0, "%s: negative dimension (B=%d T=%d H=%d)", fn, B, T, H);
+    CHECK_ARG(dh == 32 || dh == 64 || dh == 128, "%s: head size %d is not 32, 64 or 128", fn, dh);
     if (B == 0 || T == 0 || H == 0) return PCL_OK;
-    CHECK_ARG(dQ && dK && dV && dAtt && Q && K && V && probs, "pcl_attn_bwd: NULL operand");
+    CHECK_ARG(dQ && dK && dV && dAtt && Q && K && V && probs, "%s: NULL operand", fn);
     CHECK_ARG(ld >= H * dh && ld_att >= H * dh && ld_grad >= H * dh,
-              "pcl_attn_bwd: a leading dimension is below H*dh=%d", H * dh);
-    CHECK_ARG(ld % 4 == 0 && ld_att % 4 == 0, "pcl_attn_bwd: ld=%d, ld_att=%d not multiples of 4",
-              ld, ld_att);
+              "%s: a leading dimension is below H*dh=%d", fn, H * dh);
+    CHECK_ARG(ld % 4 == 0 && ld_att % 4 == 0, "%s: ld=%d, ld_att=%d not multiples of 4", fn, ld,
+              ld_att);
     CHECK_ARG(aligned16(Q) && aligned16(K) && aligned16(V) && aligned16(dAtt),
-              "pcl_attn_bwd: Q, K, V and dAtt must be 16-byte aligned");
+              "%s: Q, K, V and dAtt must be 16-byte aligned", fn);
+    if (att)
+        CHECK_ARG(ld_o >= H * dh && ld_o % 4 == 0 && aligned16(att),
+                  "%s: att needs ld_o >= H*dh, a multiple of 4, and 16-byte alignment", fn);
     CHECK_ARG((long)B * T <= INT32_MAX && (long)B * H * T <= INT32_MAX,
-              "pcl_attn_bwd: B*T or B*H*T beyond 2^31");
+              "%s: B*T or B*H*T beyond 2^31", fn);
     PCL_OK_OR_RETURN(do_init());
     hipStream_t s = pick(stream);
     float *dS = scratch;
@@ -906,8 +909,25 @@ int pcl_attn_bwd(float *dQ, float *dK, float *dV, int ld_grad, float *scratch, c
         dS = static_cast<float *>(sc->ws.buf);
     }
     HIP_OK(pcl::launch_attn_bwd(dAtt, ld_att, Q, K, V, ld, probs, dS, dQ, dK, dV, ld_grad, B, T, H,
-                                dh, 1.0f / sqrtf((float)dh), accumulate, s));
+                                dh, 1.0f / sqrtf((float)dh), accumulate, s, att, ld_o));
     return PCL_OK;
+}
+}  // namespace
+
+int pcl_attn_bwd(float *dQ, float *dK, float *dV, int ld_grad, float *scratch, const float *dAtt,
+                 int ld_att, const float *Q, const float *K, const float *V, int ld,
+                 const float *probs, int B, int T, int H, int dh, int accumulate, void *stream) {
+    return attn_bwd_common("pcl_attn_bwd", dQ, dK, dV, ld_grad, scratch, dAtt, ld_att, Q, K, V, ld,
+                           probs, nullptr, 0, B, T, H, dh, accumulate, stream);
+}
+
+int pcl_attn_bwd_ex(float *dQ, float *dK, float *dV, int ld_grad, float *scratch,
+                    const float *dAtt, int ld_att, const float *Q, const float *K, const float *V,
+                    int ld, const float *probs, const float *att, int ld_o, int B, int T, int H,
+                    int dh, int accumulate, void *stream) {
+    if (!att) return set_error(PCL_ERR_INVALID_ARG, "pcl_attn_bwd_ex: att is NULL");
+    return attn_bwd_common("pcl_attn_bwd_ex", dQ, dK, dV, ld_grad, scratch, dAtt, ld_att, Q, K, V,
+                           ld, probs, att, ld_o, B, T, H, dh, accumulate, stream);
 }
 
 // ----------------------------------------------------------- INT8 native ----

@@ -312,21 +312,26 @@ done:
 /* One step = one pcl_attn_bwd (both kernels) from stored probabilities,
  * gradients set; dS goes to a caller scratch of B*H*T*T floats. */
 typedef struct {
-    int B, T, H, dh;
-    void *dO, *Q, *K, *V, *P, *S, *dQ, *dK, *dV;
+    int B, T, H, dh, with_att;
+    void *dO, *Q, *K, *V, *P, *S, *dQ, *dK, *dV, *O;
 } attn_bwd_ctx;
 
 static int attn_bwd_step(void *c_, int i) {
     attn_bwd_ctx *c = c_;
     (void)i;
     const int D = c->H * c->dh;
+    if (c->with_att)
+        return pcl_attn_bwd_ex(c->dQ, c->dK, c->dV, D, c->S, c->dO, D, c->Q, c->K, c->V, D, c->P, c->O,
+                               D, c->B, c->T, c->H, c->dh, 0, NULL);
     return pcl_attn_bwd(c->dQ, c->dK, c->dV, D, c->S, c->dO, D, c->Q, c->K, c->V, D, c->P, c->B,
                         c->T, c->H, c->dh, 0, NULL);
 }
 
-int pcl_bench_attn_bwd(int B, int T, int H, int dh, int warmup, int steps, double *ms_total) {
+/* with_att: pcl_attn_bwd_ex, handed the forward's output */
+int pcl_bench_attn_bwd_ex(int B, int T, int H, int dh, int with_att, int warmup, int steps,
+                          double *ms_total) {
     int rc = PCL_OK;
-    attn_bwd_ctx c = {B, T, H, dh, NULL, NULL, NULL, NULL, NULL, NULL, NULL, NULL, NULL};
+    attn_bwd_ctx c = {B, T, H, dh, with_att, NULL, NULL, NULL, NULL, NULL, NULL, NULL, NULL, NULL, NULL};
     const size_t act = (size_t)B * T * H * dh, pb = (size_t)B * H * T * T;
     c.dO = dev_f32(act, 34, -1.7f, 1.7f);
     c.Q = dev_f32(act, 31, -1.7f, 1.7f);
@@ -337,17 +342,22 @@ int pcl_bench_attn_bwd(int B, int T, int H, int dh, int warmup, int steps, doubl
     c.dQ = pcl_malloc(act * sizeof(float));
     c.dK = pcl_malloc(act * sizeof(float));
     c.dV = pcl_malloc(act * sizeof(float));
-    if (!c.dO || !c.Q || !c.K || !c.V || !c.P || !c.S || !c.dQ || !c.dK || !c.dV) {
+    c.O = pcl_malloc(act * sizeof(float));
+    if (!c.dO || !c.Q || !c.K || !c.V || !c.P || !c.S || !c.dQ || !c.dK || !c.dV || !c.O) {
         rc = PCL_ERR_OOM;
         goto done;
     }
-    /* real probabilities of these inputs */
-    TRY(pcl_attn_fwd(c.Q, c.K, c.V, H * dh, c.dQ, H * dh, c.P, B, T, H, dh, NULL));
+    /* real probabilities and output of these inputs */
+    TRY(pcl_attn_fwd(c.Q, c.K, c.V, H * dh, c.O, H * dh, c.P, B, T, H, dh, NULL));
     TRY(time_steps(attn_bwd_step, &c, warmup, steps, ms_total));
 done:
     pcl_free(c.dO), pcl_free(c.Q), pcl_free(c.K), pcl_free(c.V), pcl_free(c.P), pcl_free(c.S);
-    pcl_free(c.dQ), pcl_free(c.dK), pcl_free(c.dV);
+    pcl_free(c.dQ), pcl_free(c.dK), pcl_free(c.dV), pcl_free(c.O);
     return rc;
+}
+
+int pcl_bench_attn_bwd(int B, int T, int H, int dh, int warmup, int steps, double *ms_total) {
+    return pcl_bench_attn_bwd_ex(B, T, H, dh, 0, warmup, steps, ms_total);
 }
 
 /* ----------------------------------------------------------------- GEMV ---- */

@@ -110,6 +110,8 @@ _PROTOS = {
     "pcl_attn_fwd": (_i, [_vp, _vp, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i, _vp]),
     "pcl_attn_fwd_lse": (_i, [_vp, _vp, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i, _vp]),
     "pcl_attn_bwd": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _vp, _i, _vp, _i, _i, _i, _i, _i, _vp]),
+    "pcl_attn_bwd_ex": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _vp, _i, _vp, _vp, _i, _i, _i, _i, _i,
+                             _i, _vp]),
     "pcl_cross_entropy": (_i, [_vp, _i, _vp, _vp, _i, _i, _i, _vp, _vp]),
     "pcl_head_ce": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp, _vp, _vp, C.c_long, _vp]),
     "pcl_s8_kpad": (_i, [_i]),

@@ -216,16 +216,23 @@ def test_attn_fwd_argument_errors():
 
 
 # ------------------------------------------------------------- backward ----
-def attn_bwd(d_att, q, k, v, probs, B, T, H, dh, grads0=None, accumulate=False, scratch=False):
-    """pcl_attn_bwd on device copies; returns (dq, dk, dv[, dS])."""
+def attn_bwd(d_att, q, k, v, probs, B, T, H, dh, grads0=None, accumulate=False, scratch=False, att=None):
+    """pcl_attn_bwd (pcl_attn_bwd_ex when the forward's output att is given)
+    on device copies; returns (dq, dk, dv[, dS])."""
     D = H * dh
     bufs = [pcl.dev(x) for x in (d_att, q, k, v, probs)]
     g = grads0 if grads0 is not None else [np.full((B * T, D), np.nan, np.float32)] * 3
     dg = [pcl.dev(x) for x in g]
     ds = pcl.dev(np.zeros((B * H, T, T), np.float32)) if scratch else None
-    pcl.check(pcl.lib.pcl_attn_bwd(dg[0].ptr, dg[1].ptr, dg[2].ptr, D, ds.ptr if ds else None,
-                                   bufs[0].ptr, D, bufs[1].ptr, bufs[2].ptr, bufs[3].ptr, D, bufs[4].ptr,
-                                   B, T, H, dh, int(accumulate), None))
+    if att is None:
+        pcl.check(pcl.lib.pcl_attn_bwd(dg[0].ptr, dg[1].ptr, dg[2].ptr, D, ds.ptr if ds else None,
+                                       bufs[0].ptr, D, bufs[1].ptr, bufs[2].ptr, bufs[3].ptr, D, bufs[4].ptr,
+                                       B, T, H, dh, int(accumulate), None))
+    else:
+        da = pcl.dev(att)
+        pcl.check(pcl.lib.pcl_attn_bwd_ex(dg[0].ptr, dg[1].ptr, dg[2].ptr, D, ds.ptr if ds else None,
+                                          bufs[0].ptr, D, bufs[1].ptr, bufs[2].ptr, bufs[3].ptr, D,
+                                          bufs[4].ptr, da.ptr, att.shape[1], B, T, H, dh, int(accumulate), None))
     pcl.sync()
     out = [x.download((B * T, D), np.float32) for x in dg]
     if scratch:
@@ -250,6 +257,11 @@ def test_attn_bwd_vs_oracle(B, T, H, dh):
     got0 = attn_bwd(d_att, q, k, v, pr, B, T, H, dh)
     want0 = ob.attention_backward(d_att, q, k, v, pr, B, T, H, dh)
     for name, a, r in zip("qkv", got0, want0):
+        assert rel(a, r) <= FP32_TOL, name
+    # given the forward's output, D_i = dAtt_i . att_i: the same gradients
+    att, _ = attn(q, k, v, B, T, H, dh)
+    got_ex = attn_bwd(d_att, q, k, v, pr, B, T, H, dh, grads0=g0, accumulate=True, att=att)
+    for name, a, r in zip("qkv", got_ex, want):
         assert rel(a, r) <= FP32_TOL, name
 
 
@@ -285,6 +297,19 @@ def test_attn_bwd_full_size_identities(B, T, H, dh):
         worst = max(worst, rel(dq[b * T + i, cols], dsr @ k[keys, cols].astype(np.float64)),
                     rel(ds[b * H + h, i, : i + 1], dsr))
     assert worst <= FP32_TOL
+    # with the forward's output: the same dS and gradients within the fp32 bar
+    att, _ = attn(q, k, v, B, T, H, dh, probs=False)
+    dq2, dk2, dv2, ds2 = attn_bwd(d_att, q, k, v, pr, B, T, H, dh, scratch=True, att=att)
+    for a, r in ((dq2, dq), (dk2, dk), (dv2, dv), (np.tril(ds2), np.tril(ds))):
+        assert rel(a, r) <= FP32_TOL
+
+
+def test_attn_bwd_ex_argument_errors():
+    q = pcl.empty((64, 64), np.float32)
+    base = [q.ptr, q.ptr, q.ptr, 64, None, q.ptr, 64, q.ptr, q.ptr, q.ptr, 64, q.ptr]
+    for att, ld_o in ((None, 64), (q.ptr, 30), (q.ptr, 62), (q.ptr + 4, 64)):
+        assert pcl.lib.pcl_attn_bwd_ex(*base, att, ld_o, 1, 64, 2, 32, 0, None) == pcl.PCL_ERR_INVALID_ARG
+        pcl.lib.pcl_clear_error()
 
 
 def test_attention_backward_dropins():
