@@ -857,9 +857,9 @@ static hipError_t launch_dma_epi(const SgemmPlan &p, int M, int N, int K, const 
                                  const float *aux_in, float *aux_out, long ld_aux,
                                  hipStream_t stream) {
     if (p.cfg == SG_64_KG2)
-        return launch_dma<64, 64, 2, 4, 1, A_KC, B_KC, EPI>(M, N, K, 1, K, A, lda, B, ldb, bias, 0, C,
+        return launch_dma<64, 64, 2, 2, 1, A_KC, B_KC, EPI>(M, N, K, 1, K, A, lda, B, ldb, bias, 0, C,
                                                             ldc, stream, aux_in, aux_out, ld_aux);
-    return launch_dma<128, 128, 2, 4, 1, A_KC, B_KC, EPI>(M, N, K, 1, K, A, lda, B, ldb, bias, 0, C,
+    return launch_dma<128, 128, 2, 2, 1, A_KC, B_KC, EPI>(M, N, K, 1, K, A, lda, B, ldb, bias, 0, C,
                                                           ldc, stream, aux_in, aux_out, ld_aux);
 }
 
@@ -909,10 +909,10 @@ static hipError_t dispatch_layout(const SgemmPlan &p, int M, int N, int K, const
     }
     if (dma_ok) {
         if (p.cfg == SG_64_KG2)
-            e = launch_dma<64, 64, 2, 4, 1, A_KC, B_KC>(M, N, K, p.splits, p.kchunk, A, lda, B, ldb, b,
+            e = launch_dma<64, 64, 2, 2, 1, A_KC, B_KC>(M, N, K, p.splits, p.kchunk, A, lda, B, ldb, b,
                                                      acc, out, ldo, stream);
         else
-            e = launch_dma<128, 128, 2, 4, 1, A_KC, B_KC>(M, N, K, p.splits, p.kchunk, A, lda, B, ldb, b,
+            e = launch_dma<128, 128, 2, 2, 1, A_KC, B_KC>(M, N, K, p.splits, p.kchunk, A, lda, B, ldb, b,
                                                        acc, out, ldo, stream);
     } else switch (p.cfg) {
     case SG_128_BK16:
