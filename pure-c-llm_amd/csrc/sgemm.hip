@@ -779,14 +779,16 @@ static hipError_t launch_dma(int M, int N, int K, int splits, int kchunk, const 
 // so the sum over k is unchanged), and holds outputs (4q + v, r16) of a block.
 // LDS layouts, unpadded and swizzled (conflict-free reads both ways):
 //  * K-contiguous operand: rows of 64 bytes (four 16-byte pieces); logical
-//    piece p of row r sits at p ^ ((r >> 2) & 3). A lane reads one piece
-//    (its four k) per block.
+//    piece p of row r sits at p ^ ((r >> 1) & 3) (SQ_LDS_BANK_CONFLICT reads
+//    zero for this map; (r >> 2) & 3, r & 3 and no swizzle all conflict). A
+//    lane reads one piece (its four k) per block.
 //  * MN-contiguous operand: 16 k-rows of ROWS floats; logical 16-byte chunk
 //    c of k-row k sits at c ^ (((k >> 2) & 3) << 2). A lane reads four floats
 //    (k = 4q .. 4q + 3) per block.
 // Every step issues one tile's DMA (clamped to the last tile past the end,
 // into a stage no one reads again), so the wait for tile kt+1 is always
-// vmcnt((STAGES - 2) * LOADS).
+// vmcnt((STAGES - 2) * LOADS); the DMA instructions are spread over the
+// step's MFMAs (issued together they stall the wave: +3-6% spread).
 constexpr int S16_BK = 16;
 
 template <int ROWS, bool KC, int NW>
@@ -804,7 +806,7 @@ struct Dma16 {
             const int inst = q * NW + wave;
             if (KC) {
                 const int r = inst * 16 + lane / 4;
-                const int gp = (lane % 4) ^ ((r >> 2) & 3);
+                const int gp = (lane % 4) ^ ((r >> 1) & 3);
                 voff[q] = (long)min(rows0 + r, nrows - 1) * ld + gp * 4;
             } else {
                 const int e = inst * 64 + lane, k = e / CHR, c = e % CHR;
@@ -874,7 +876,7 @@ __global__ __launch_bounds__(256, 2) void sgemm16_kernel(
     const unsigned lds0 = (unsigned)(uintptr_t)(const __attribute__((address_space(3))) void *)lds;
     unsigned a_addr[A_KC ? 1 : TM], b_addr[B_KC ? 1 : TN];
     if constexpr (A_KC) {
-        a_addr[0] = (wm * WTM + r16) * 64 + ((q ^ ((r16 >> 2) & 3)) << 4);
+        a_addr[0] = (wm * WTM + r16) * 64 + ((q ^ ((r16 >> 1) & 3)) << 4);
     } else {
 #pragma unroll
         for (int i = 0; i < TM; i++) {
@@ -883,7 +885,7 @@ __global__ __launch_bounds__(256, 2) void sgemm16_kernel(
         }
     }
     if constexpr (B_KC) {
-        b_addr[0] = TA::BYTES + (wn * WTN + r16) * 64 + ((q ^ ((r16 >> 2) & 3)) << 4);
+        b_addr[0] = TA::BYTES + (wn * WTN + r16) * 64 + ((q ^ ((r16 >> 1) & 3)) << 4);
     } else {
 #pragma unroll
         for (int j = 0; j < TN; j++) {
@@ -976,19 +978,28 @@ __global__ __launch_bounds__(256, 2) void sgemm16_kernel(
         // Step kt: this wave's reads of tile kt have landed and its DMA of
         // tile kt+1 too; after the barrier every wave's have, and the stage
         // of tile kt (read into registers by all) takes tile kt+STAGES; tile
-        // kt+1's fragments are read while tile kt's MFMAs run. The phases are
-        // fenced so the compiler keeps the reads ahead of the MFMAs and the
-        // MFMAs ahead of the next wait.
+        // kt+1's fragments are read while tile kt's MFMAs run. Schedule of
+        // the step: the fragment reads first, then the MFMAs with one DMA
+        // instruction after every NMF / LOADS of them; fenced on both sides so
+        // the MFMAs stay ahead of the next wait.
+        constexpr int NMF = 4 * TM * TN, NRD = (A_KC ? TM : 4 * TM) + (B_KC ? TN : 4 * TN);
+        constexpr int PER = NMF / LOADS, REST = NMF - PER * LOADS;
         auto step = [&](auto SL, int kt) {
             constexpr int sl = decltype(SL)::value;
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             fence_slot(SL);
             __builtin_amdgcn_s_waitcnt(sd_waitcnt_vm((STAGES - 2) * LOADS));
             __builtin_amdgcn_s_barrier();
-            dma(kt + STAGES);
-            read_tile(IC<sl ^ 1>{}, lds0 + ((kt + 1) % STAGES) * STAGE);
             __builtin_amdgcn_sched_barrier(0);
+            read_tile(IC<sl ^ 1>{}, lds0 + ((kt + 1) % STAGES) * STAGE);
             mfma_tile(SL);
+            dma(kt + STAGES);
+            __builtin_amdgcn_sched_group_barrier(0x100, NRD, 0);  // LDS reads
+            static_for<0, LOADS>([&](auto) {
+                __builtin_amdgcn_sched_group_barrier(0x008, PER, 0);  // MFMAs
+                __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);    // one DMA
+            });
+            if constexpr (REST > 0) __builtin_amdgcn_sched_group_barrier(0x008, REST, 0);
             __builtin_amdgcn_sched_barrier(0);
         };
         for (int kt = 0; kt < nk; kt += 2) {

@@ -1,0 +1,201 @@
+// gemm_yardstick.cpp -- a measurement yardstick, not part of the product: the
+// vendor GEMM library (hipBLASLt) timed beside libpcl_hip on the same buffers
+// and shapes, in one process, so a fraction of the datasheet peak can be read
+// against what a tuned library reaches on the same part at the same sizes.
+// libpcl_hip never links this library; the Makefile builds this program only
+// on request (make yardstick).
+//
+// Shapes: the gemm_bench INT8 square (2048^3) and the 350M-class projections
+// (BASELINE.json configs[1] and [4]). INT8: u8 (or s8) activations x s8
+// weights stored N x K (K-contiguous per output column, the packed layout of
+// libpcl_hip) -> int32, and libpcl_hip's dequantised fp32 form beside it.
+// FP32: C = A . B^T with B stored N x K (the same operand layout), fp32
+// inputs uniform in [-1, 1], checked against a double-precision sum on four
+// rows. Each rate is the best of 3 runs of 20 back-to-back calls.
+#include <hip/hip_runtime.h>
+#include <hipblaslt/hipblaslt.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <vector>
+
+#include "../../include/pcl_hip.h"
+
+#define CK(x)                                                                                  \
+    do {                                                                                       \
+        hipError_t e_ = (x);                                                                   \
+        if (e_ != hipSuccess) {                                                                \
+            fprintf(stderr, "%s:%d %s\n", __FILE__, __LINE__, hipGetErrorString(e_));          \
+            exit(1);                                                                           \
+        }                                                                                      \
+    } while (0)
+
+__global__ void yard_fill(unsigned *p, size_t n, unsigned seed, int f32) {
+    for (size_t i = blockIdx.x * 256ull + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
+        unsigned s = (unsigned)i * 2654435761u ^ seed;
+        s ^= s << 13, s ^= s >> 17, s ^= s << 5, s ^= s << 13, s ^= s >> 17, s ^= s << 5;
+        p[i] = f32 ? __float_as_uint((s >> 8) * (1.0f / 16777216.0f) * 2.f - 1.f) : s;
+    }
+}
+
+template <typename F>
+static double best_ms(F f) {
+    hipEvent_t e0, e1;
+    CK(hipEventCreate(&e0));
+    CK(hipEventCreate(&e1));
+    f();
+    CK(hipDeviceSynchronize());
+    double best = 1e30;
+    for (int r = 0; r < 3; r++) {
+        CK(hipEventRecord(e0, 0));
+        for (int i = 0; i < 20; i++) f();
+        CK(hipEventRecord(e1, 0));
+        CK(hipEventSynchronize(e1));
+        float ms;
+        CK(hipEventElapsedTime(&ms, e0, e1));
+        best = ms / 20 < best ? ms / 20 : best;
+    }
+    CK(hipEventDestroy(e0));
+    CK(hipEventDestroy(e1));
+    return best;
+}
+
+// The library's best algorithm (of its top 16 heuristics) for row-major
+// C (M x N) = A (M x K, row-major) . Bt^T (Bt N x K, row-major), computed as
+// the column-major C^T = Bt . A^T. Returns its time, or -1.
+static double vendor(hipblasLtHandle_t h, bool i8, const void *A, const void *Bt, void *C, int M, int N,
+                     int K, void *ws, size_t wsb) {
+    const hipDataType ab = i8 ? HIP_R_8I : HIP_R_32F, ct = i8 ? HIP_R_32I : HIP_R_32F;
+    const hipblasComputeType_t comp = i8 ? HIPBLAS_COMPUTE_32I : HIPBLAS_COMPUTE_32F;
+    hipblasLtMatmulDesc_t d;
+    if (hipblasLtMatmulDescCreate(&d, comp, i8 ? HIP_R_32I : HIP_R_32F) != HIPBLAS_STATUS_SUCCESS) return -1;
+    hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
+    hipblasLtMatmulDescSetAttribute(d, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof ta);
+    hipblasLtMatmulDescSetAttribute(d, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof tb);
+    hipblasLtMatrixLayout_t la, lb, lc;
+    hipblasLtMatrixLayoutCreate(&la, ab, K, N, K);
+    hipblasLtMatrixLayoutCreate(&lb, ab, K, M, K);
+    hipblasLtMatrixLayoutCreate(&lc, ct, N, M, N);
+    hipblasLtMatmulPreference_t pref;
+    hipblasLtMatmulPreferenceCreate(&pref);
+    uint64_t wsz = wsb;
+    hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsz, sizeof wsz);
+    hipblasLtMatmulHeuristicResult_t res[16];
+    int n = 0;
+    hipblasLtMatmulAlgoGetHeuristic(h, d, la, lb, lc, lc, pref, 16, res, &n);
+    float af = 1.f, bf = 0.f;
+    int32_t ai = 1, bi = 0;
+    const void *alpha = i8 ? (const void *)&ai : (const void *)&af;
+    const void *beta = i8 ? (const void *)&bi : (const void *)&bf;
+    double best = -1;
+    for (int a = 0; a < n; a++) {
+        auto run = [&]() { hipblasLtMatmul(h, d, alpha, Bt, la, A, lb, beta, C, lc, C, lc, &res[a].algo, ws, wsb, 0); };
+        if (hipblasLtMatmul(h, d, alpha, Bt, la, A, lb, beta, C, lc, C, lc, &res[a].algo, ws, wsb, 0) !=
+            HIPBLAS_STATUS_SUCCESS)
+            continue;
+        const double t = best_ms(run);
+        if (best < 0 || t < best) best = t;
+    }
+    hipblasLtMatmulPreferenceDestroy(pref);
+    hipblasLtMatrixLayoutDestroy(la);
+    hipblasLtMatrixLayoutDestroy(lb);
+    hipblasLtMatrixLayoutDestroy(lc);
+    hipblasLtMatmulDescDestroy(d);
+    return best;
+}
+
+// max |C - R| / max |R| over four rows, R in double
+static double f32_rel(const float *dA, const float *dBt, const float *dC, int N, int K) {
+    std::vector<float> a((size_t)4 * K), b((size_t)N * K), c((size_t)4 * N);
+    CK(hipMemcpy(a.data(), dA, a.size() * 4, hipMemcpyDeviceToHost));
+    CK(hipMemcpy(b.data(), dBt, b.size() * 4, hipMemcpyDeviceToHost));
+    CK(hipMemcpy(c.data(), dC, c.size() * 4, hipMemcpyDeviceToHost));
+    double e = 0, r = 0;
+    for (int m = 0; m < 4; m++)
+        for (int n = 0; n < N; n++) {
+            double s = 0;
+            for (int k = 0; k < K; k++) s += (double)a[(size_t)m * K + k] * b[(size_t)n * K + k];
+            e = fmax(e, fabs(s - c[(size_t)m * N + n]));
+            r = fmax(r, fabs(s));
+        }
+    return e / r;
+}
+
+int main() {
+    if (pcl_init() != PCL_OK) {
+        fprintf(stderr, "libpcl_hip: %s\n", pcl_last_error());
+        return 1;
+    }
+    hipblasLtHandle_t h;
+    if (hipblasLtCreate(&h) != HIPBLAS_STATUS_SUCCESS) {
+        fprintf(stderr, "hipblasLtCreate failed\n");
+        return 1;
+    }
+    const size_t wsb = 256u << 20;
+    void *ws;
+    CK(hipMalloc(&ws, wsb));
+    struct Shape { const char *name; int M, N, K; };
+    const Shape i8s[] = {{"2048^3", 2048, 2048, 2048}, {"qkv", 4096, 3072, 1024}, {"attn_out", 4096, 1024, 1024},
+                         {"ffn_up", 4096, 4096, 1024}, {"ffn_down", 4096, 1024, 4096}, {"head", 4096, 50257, 1024}};
+    printf("INT8 GEMM, TOP/s (best of 3 x 20 calls)\n");
+    printf("%-9s %5s %6s %5s | %9s %12s | %9s\n", "shape", "M", "N", "K", "pcl_i32", "pcl_dequant", "vendor_i32");
+    for (const Shape &s : i8s) {
+        void *A, *Bt, *C, *Cv, *sa, *sb;
+        CK(hipMalloc(&A, (size_t)s.M * s.K));
+        CK(hipMalloc(&Bt, (size_t)s.N * s.K));
+        CK(hipMalloc(&C, (size_t)s.M * s.N * 4));
+        CK(hipMalloc(&Cv, (size_t)s.M * s.N * 4));
+        CK(hipMalloc(&sa, (size_t)s.M * 4));
+        CK(hipMalloc(&sb, (size_t)s.N * 4));
+        hipLaunchKernelGGL(yard_fill, dim3(4096), dim3(256), 0, 0, (unsigned *)A, (size_t)s.M * s.K / 4, 17u, 0);
+        hipLaunchKernelGGL(yard_fill, dim3(4096), dim3(256), 0, 0, (unsigned *)Bt, (size_t)s.N * s.K / 4, 91u, 0);
+        CK(hipMemset(sa, 0, (size_t)s.M * 4));
+        CK(hipMemset(sb, 0, (size_t)s.N * 4));
+        CK(hipDeviceSynchronize());
+        const double ops = 2.0 * s.M * s.N * s.K;
+        // K is a multiple of 256 here, so Bt (N x K) is already the packed layout
+        const double t_i32 = best_ms([&]() {
+            pcl_gemm_u8s8_i32((const uint8_t *)A, s.K, (const int8_t *)Bt, (int32_t *)C, s.N, s.M, s.N, s.K, nullptr);
+        });
+        const double t_dq = best_ms([&]() {
+            pcl_gemm_u8s8_dq((const uint8_t *)A, s.K, (const int8_t *)Bt, nullptr, (const float *)sa,
+                             (const float *)sb, (float *)C, s.N, s.M, s.N, s.K, nullptr);
+        });
+        const double t_v = vendor(h, true, A, Bt, Cv, s.M, s.N, s.K, ws, wsb);
+        printf("%-9s %5d %6d %5d | %9.1f %12.1f | %9.1f\n", s.name, s.M, s.N, s.K, ops / t_i32 / 1e9,
+               ops / t_dq / 1e9, t_v > 0 ? ops / t_v / 1e9 : 0.0);
+        fflush(stdout);
+        CK(hipFree(A)); CK(hipFree(Bt)); CK(hipFree(C)); CK(hipFree(Cv)); CK(hipFree(sa)); CK(hipFree(sb));
+    }
+    const Shape f32s[] = {{"1024^3", 1024, 1024, 1024}, {"qkv", 4096, 3072, 1024}, {"attn_out", 4096, 1024, 1024},
+                          {"ffn_up", 4096, 4096, 1024}, {"ffn_down", 4096, 1024, 4096}, {"head", 4096, 50257, 1024}};
+    printf("\nFP32 GEMM C = A . B^T (B stored N x K), TFLOP/s; accuracy max|C-R|/max|R| on 4 rows\n");
+    printf("%-9s %5s %6s %5s | %9s %9s | %9s %9s\n", "shape", "M", "N", "K", "pcl", "pcl_err", "vendor", "vendor_err");
+    for (const Shape &s : f32s) {
+        float *A, *Bt, *C, *Cv;
+        CK(hipMalloc(&A, (size_t)s.M * s.K * 4));
+        CK(hipMalloc(&Bt, (size_t)s.N * s.K * 4));
+        CK(hipMalloc(&C, (size_t)s.M * s.N * 4));
+        CK(hipMalloc(&Cv, (size_t)s.M * s.N * 4));
+        hipLaunchKernelGGL(yard_fill, dim3(4096), dim3(256), 0, 0, (unsigned *)A, (size_t)s.M * s.K, 23u, 1);
+        hipLaunchKernelGGL(yard_fill, dim3(4096), dim3(256), 0, 0, (unsigned *)Bt, (size_t)s.N * s.K, 29u, 1);
+        CK(hipDeviceSynchronize());
+        const double fl = 2.0 * s.M * s.N * s.K;
+        const double t_p = best_ms([&]() {
+            pcl_sgemm(PCL_OP_N, PCL_OP_T, s.M, s.N, s.K, A, s.K, Bt, s.K, nullptr, 0, C, s.N, nullptr);
+        });
+        CK(hipDeviceSynchronize());
+        const double e_p = f32_rel(A, Bt, C, s.N, s.K);
+        const double t_v = vendor(h, false, A, Bt, Cv, s.M, s.N, s.K, ws, wsb);
+        CK(hipDeviceSynchronize());
+        const double e_v = t_v > 0 ? f32_rel(A, Bt, Cv, s.N, s.K) : 0.0;
+        printf("%-9s %5d %6d %5d | %9.1f %9.1e | %9.1f %9.1e\n", s.name, s.M, s.N, s.K, fl / t_p / 1e9, e_p,
+               t_v > 0 ? fl / t_v / 1e9 : 0.0, e_v);
+        fflush(stdout);
+        CK(hipFree(A)); CK(hipFree(Bt)); CK(hipFree(C)); CK(hipFree(Cv));
+    }
+    CK(hipFree(ws));
+    hipblasLtDestroy(h);
+    return 0;
+}
