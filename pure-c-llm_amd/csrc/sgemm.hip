@@ -767,33 +767,40 @@ static hipError_t launch_dma(int M, int N, int K, int splits, int kchunk, const 
 }
 
 // ---------------------------------------------------------------------------
-// The same pipeline on v_mfma_f32_16x16x4f32, which sustains a higher f32 rate
-// on this part than the 32x32x2 form (145 against ~135 TFLOP/s for a loop of
-// nothing but MFMAs), with 16-deep K tiles so a workgroup's ring is small
-// enough for two workgroups per CU (their barriers are independent, so one
-// SIMD always has a second wave to issue from).
+// The same products on v_mfma_f32_16x16x4f32, which sustains a higher f32
+// rate on this part than the 32x32x2 form (145 against ~135 TFLOP/s for a
+// loop of nothing but MFMAs), with a ring small enough for two workgroups
+// per CU (their barriers are independent, so a SIMD always has a second wave
+// to issue from).
 //
 // Tile: BM x BN per workgroup of 4 waves in a 2x2 grid; a wave owns
-// (BM/2) x (BN/2) as TM x TN blocks of 16x16. Lane (r16, q) = (lane % 16,
-// lane / 16) feeds k = 4q + s at MFMA step s of a tile (the same for A and B,
-// so the sum over k is unchanged), and holds outputs (4q + v, r16) of a block.
-// LDS layouts, unpadded and swizzled (conflict-free reads both ways):
-//  * K-contiguous operand: rows of 64 bytes (four 16-byte pieces); logical
-//    piece p of row r sits at p ^ ((r >> 1) & 3) (SQ_LDS_BANK_CONFLICT reads
-//    zero for this map; (r >> 2) & 3, r & 3 and no swizzle all conflict). A
-//    lane reads one piece (its four k) per block.
-//  * MN-contiguous operand: 16 k-rows of ROWS floats; logical 16-byte chunk
+// (BM/2) x (BN/2) as TM x TN blocks of 16x16. A ring stage holds 32 k, used
+// as two sub-steps of 16: lane (r16, q) = (lane % 16, lane / 16) feeds
+// k = 16u + 4q + s at MFMA step s of sub-step u (the same for A and B, so the
+// sum over k is unchanged) and holds outputs (4q + v, r16) of a block.
+// LDS layouts, unpadded and swizzled (SQ_LDS_BANK_CONFLICT reads zero):
+//  * K-contiguous operand: rows of 128 bytes (eight 16-byte pieces); logical
+//    piece p of row r sits at p ^ ((r >> 1) & 7). A lane reads one piece
+//    (its four k) per block per sub-step. (The maps (r >> 1) & 3 and
+//    ((r >> 1) & 3) | ((r & 1) << 2) conflict.)
+//  * MN-contiguous operand: 32 k-rows of ROWS floats; logical 16-byte chunk
 //    c of k-row k sits at c ^ (((k >> 2) & 3) << 2). A lane reads four floats
-//    (k = 4q .. 4q + 3) per block.
-// Every step issues one tile's DMA (clamped to the last tile past the end,
-// into a stage no one reads again), so the wait for tile kt+1 is always
-// vmcnt((STAGES - 2) * LOADS); the DMA instructions are spread over the
-// step's MFMAs (issued together they stall the wave: +3-6% spread).
-constexpr int S16_BK = 16;
+//    (k = 16u + 4q .. + 3) per block per sub-step.
+// Per stage: sub-step 0 reads sub-step 1's fragments while its MFMAs run;
+// sub-step 1 waits for this wave's DMA of the next stage, crosses the one
+// barrier of the stage (after it every wave has read this stage and every
+// DMA of the next has landed), reads the next stage's first fragments,
+// refills this stage (tile kt + STAGES) and runs its MFMAs with the DMA
+// instructions spread among them (issued together they stall the wave).
+// Every stage issues one tile's DMA (clamped to the last tile past the end,
+// into a stage no one reads again), so the wait is always
+// vmcnt((STAGES - 2) * LOADS). 32-deep stages against 16-deep ones with a
+// barrier each: +6-8% in a same-run comparison.
+constexpr int S16_BK = 32;
 
 template <int ROWS, bool KC, int NW>
 struct Dma16 {
-    static constexpr int BYTES = ROWS * S16_BK * 4;  // one K tile
+    static constexpr int BYTES = ROWS * S16_BK * 4;  // one ring stage of this operand
     static constexpr int INST = BYTES / 1024;
     static constexpr int PER_WAVE = INST / NW;
     static_assert(INST % NW == 0, "DMA instructions must split over the waves");
@@ -805,8 +812,8 @@ struct Dma16 {
         for (int q = 0; q < PER_WAVE; q++) {
             const int inst = q * NW + wave;
             if (KC) {
-                const int r = inst * 16 + lane / 4;
-                const int gp = (lane % 4) ^ ((r >> 1) & 3);
+                const int r = inst * 8 + lane / 8;
+                const int gp = (lane % 8) ^ ((r >> 1) & 7);
                 voff[q] = (long)min(rows0 + r, nrows - 1) * ld + gp * 4;
             } else {
                 const int e = inst * 64 + lane, k = e / CHR, c = e % CHR;
@@ -872,11 +879,14 @@ __global__ __launch_bounds__(256, 2) void sgemm16_kernel(
         TA::dma(A, lda, tk * S16_BK, voa, lda_o, st);
         TB::dma(B, ldb, tk * S16_BK, vob, ldb_o, st + TA::BYTES);
     };
-    // fragment addresses within a stage (block offsets as immediates)
+    // fragment addresses within a stage (block offsets as immediates; the
+    // K-contiguous swizzle depends only on r16 since row bases are multiples
+    // of 16)
     const unsigned lds0 = (unsigned)(uintptr_t)(const __attribute__((address_space(3))) void *)lds;
-    unsigned a_addr[A_KC ? 1 : TM], b_addr[B_KC ? 1 : TN];
+    unsigned a_addr[A_KC ? 2 : TM], b_addr[B_KC ? 2 : TN];
     if constexpr (A_KC) {
-        a_addr[0] = (wm * WTM + r16) * 64 + ((q ^ ((r16 >> 1) & 3)) << 4);
+#pragma unroll
+        for (int u = 0; u < 2; u++) a_addr[u] = (wm * WTM + r16) * 128 + (((4 * u + q) ^ ((r16 >> 1) & 7)) << 4);
     } else {
 #pragma unroll
         for (int i = 0; i < TM; i++) {
@@ -885,7 +895,9 @@ __global__ __launch_bounds__(256, 2) void sgemm16_kernel(
         }
     }
     if constexpr (B_KC) {
-        b_addr[0] = TA::BYTES + (wn * WTN + r16) * 64 + ((q ^ ((r16 >> 1) & 3)) << 4);
+#pragma unroll
+        for (int u = 0; u < 2; u++)
+            b_addr[u] = TA::BYTES + (wn * WTN + r16) * 128 + (((4 * u + q) ^ ((r16 >> 1) & 7)) << 4);
     } else {
 #pragma unroll
         for (int j = 0; j < TN; j++) {
@@ -895,28 +907,29 @@ __global__ __launch_bounds__(256, 2) void sgemm16_kernel(
     }
     v4f fak[2][A_KC ? TM : 1], fbk[2][B_KC ? TN : 1];
     float fam[2][A_KC ? 1 : TM][4], fbm[2][B_KC ? 1 : TN][4];
-    auto read_tile = [&](auto SL, unsigned st) {
-        constexpr int sl = decltype(SL)::value;
+    // sub-step u of the stage at st into slot sl
+    auto read_sub = [&](auto SL, auto U, unsigned st) {
+        constexpr int sl = decltype(SL)::value, u = decltype(U)::value;
         static_for<0, TM>([&](auto I) {
             constexpr int i = decltype(I)::value;
             if constexpr (A_KC) {
-                sd_read128<i * 16 * 64>(fak[sl][i], st + a_addr[0]);
+                sd_read128<i * 16 * 128>(fak[sl][i], st + a_addr[u]);
             } else {
-                sd_read32<0 * BM * 4>(fam[sl][i][0], st + a_addr[i]);
-                sd_read32<1 * BM * 4>(fam[sl][i][1], st + a_addr[i]);
-                sd_read32<2 * BM * 4>(fam[sl][i][2], st + a_addr[i]);
-                sd_read32<3 * BM * 4>(fam[sl][i][3], st + a_addr[i]);
+                sd_read32<(16 * u + 0) * BM * 4>(fam[sl][i][0], st + a_addr[i]);
+                sd_read32<(16 * u + 1) * BM * 4>(fam[sl][i][1], st + a_addr[i]);
+                sd_read32<(16 * u + 2) * BM * 4>(fam[sl][i][2], st + a_addr[i]);
+                sd_read32<(16 * u + 3) * BM * 4>(fam[sl][i][3], st + a_addr[i]);
             }
         });
         static_for<0, TN>([&](auto J) {
             constexpr int j = decltype(J)::value;
             if constexpr (B_KC) {
-                sd_read128<j * 16 * 64>(fbk[sl][j], st + b_addr[0]);
+                sd_read128<j * 16 * 128>(fbk[sl][j], st + b_addr[u]);
             } else {
-                sd_read32<0 * BN * 4>(fbm[sl][j][0], st + b_addr[j]);
-                sd_read32<1 * BN * 4>(fbm[sl][j][1], st + b_addr[j]);
-                sd_read32<2 * BN * 4>(fbm[sl][j][2], st + b_addr[j]);
-                sd_read32<3 * BN * 4>(fbm[sl][j][3], st + b_addr[j]);
+                sd_read32<(16 * u + 0) * BN * 4>(fbm[sl][j][0], st + b_addr[j]);
+                sd_read32<(16 * u + 1) * BN * 4>(fbm[sl][j][1], st + b_addr[j]);
+                sd_read32<(16 * u + 2) * BN * 4>(fbm[sl][j][2], st + b_addr[j]);
+                sd_read32<(16 * u + 3) * BN * 4>(fbm[sl][j][3], st + b_addr[j]);
             }
         });
     };
@@ -946,7 +959,7 @@ __global__ __launch_bounds__(256, 2) void sgemm16_kernel(
     for (int i = 0; i < TM; i++)
 #pragma unroll
         for (int j = 0; j < TN; j++) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
-    auto mfma_tile = [&](auto SL) {
+    auto mfma_sub = [&](auto SL) {
         constexpr int sl = decltype(SL)::value;
         static_for<0, 4>([&](auto S) {
             constexpr int s4 = decltype(S)::value;
@@ -969,30 +982,33 @@ __global__ __launch_bounds__(256, 2) void sgemm16_kernel(
     long ldcm = ldc;
     asm volatile("" : "+s"(Cm), "+s"(ldcm));
 
+    constexpr int NMF = 4 * TM * TN, NRD = (A_KC ? TM : 4 * TM) + (B_KC ? TN : 4 * TN);
+    constexpr int PER = NMF / LOADS > 0 ? NMF / LOADS : 1;
+    constexpr int REST = NMF - PER * LOADS > 0 ? NMF - PER * LOADS : 0;
     if (nk > 0) {
 #pragma unroll
         for (int t = 0; t < STAGES; t++) dma(t);
         __builtin_amdgcn_s_waitcnt(sd_waitcnt_vm((STAGES - 1) * LOADS));
         __builtin_amdgcn_s_barrier();
-        read_tile(IC<0>{}, lds0);
-        // Step kt: this wave's reads of tile kt have landed and its DMA of
-        // tile kt+1 too; after the barrier every wave's have, and the stage
-        // of tile kt (read into registers by all) takes tile kt+STAGES; tile
-        // kt+1's fragments are read while tile kt's MFMAs run. Schedule of
-        // the step: the fragment reads first, then the MFMAs with one DMA
-        // instruction after every NMF / LOADS of them; fenced on both sides so
-        // the MFMAs stay ahead of the next wait.
-        constexpr int NMF = 4 * TM * TN, NRD = (A_KC ? TM : 4 * TM) + (B_KC ? TN : 4 * TN);
-        constexpr int PER = NMF / LOADS, REST = NMF - PER * LOADS;
-        auto step = [&](auto SL, int kt) {
-            constexpr int sl = decltype(SL)::value;
+        read_sub(IC<0>{}, IC<0>{}, lds0);
+        for (int kt = 0; kt < nk; kt++) {
+            const unsigned st = lds0 + (kt % STAGES) * STAGE;
+            // sub-step 0
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            fence_slot(SL);
+            fence_slot(IC<0>{});
+            __builtin_amdgcn_sched_barrier(0);
+            read_sub(IC<1>{}, IC<1>{}, st);
+            __builtin_amdgcn_sched_barrier(0);
+            mfma_sub(IC<0>{});
+            __builtin_amdgcn_sched_barrier(0);
+            // sub-step 1: the stage boundary
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            fence_slot(IC<1>{});
             __builtin_amdgcn_s_waitcnt(sd_waitcnt_vm((STAGES - 2) * LOADS));
             __builtin_amdgcn_s_barrier();
             __builtin_amdgcn_sched_barrier(0);
-            read_tile(IC<sl ^ 1>{}, lds0 + ((kt + 1) % STAGES) * STAGE);
-            mfma_tile(SL);
+            read_sub(IC<0>{}, IC<0>{}, lds0 + ((kt + 1) % STAGES) * STAGE);
+            mfma_sub(IC<1>{});
             dma(kt + STAGES);
             __builtin_amdgcn_sched_group_barrier(0x100, NRD, 0);  // LDS reads
             static_for<0, LOADS>([&](auto) {
@@ -1001,52 +1017,75 @@ __global__ __launch_bounds__(256, 2) void sgemm16_kernel(
             });
             if constexpr (REST > 0) __builtin_amdgcn_sched_group_barrier(0x008, REST, 0);
             __builtin_amdgcn_sched_barrier(0);
-        };
-        for (int kt = 0; kt < nk; kt += 2) {
-            step(IC<0>{}, kt);
-            if (kt + 1 < nk) step(IC<1>{}, kt + 1);
         }
         // no DMA or fragment read in flight past the loop
         __builtin_amdgcn_s_waitcnt(sd_waitcnt_vm(0));
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     }
 
+    // Epilogue. A tile wholly inside C takes the form without bounds checks.
+    // One address per output row (row * ldc once per row, the TN columns at
+    // immediate offsets); C is stored through a global pointer (the asm above
+    // hides its provenance, which would otherwise give flat stores).
+    typedef __attribute__((address_space(1))) float gfloat;
+    gfloat *Cg = (gfloat *)Cm;
+    constexpr bool AUX = EPI == EPI_RESID || EPI == EPI_GELU_BWD;
+    const int row0 = m0 + wm * WTM + 4 * q, col0 = n0 + wn * WTN + r16;
+    auto store = [&](auto CHECK) {
+        constexpr bool chk = decltype(CHECK)::value != 0;
+        float bv[TN];
+        int cj[TN];  // column of block j (clamped into C when checking)
 #pragma unroll
-    for (int j = 0; j < TN; j++) {
-        const int col = n0 + wn * WTN + j * 16 + r16;
-        if (col >= N) continue;
-        const float bv = bias ? bias[col] : 0.f;
+        for (int j = 0; j < TN; j++) {
+            cj[j] = chk ? min(col0 + j * 16, N - 1) : col0 + j * 16;
+            bv[j] = bias ? bias[cj[j]] : 0.f;
+        }
 #pragma unroll
         for (int i = 0; i < TM; i++) {
-            const int rb = m0 + wm * WTM + i * 16 + 4 * q;
-            constexpr bool AUX = EPI == EPI_RESID || EPI == EPI_GELU_BWD;
-            float old[4];
+            float old[4][TN];
             if (AUX || accumulate) {
-                const float *src = AUX ? aux_in : Cm;
-                const long lds_ = AUX ? ld_aux : ldcm;
 #pragma unroll
-                for (int v = 0; v < 4; v++) old[v] = src[(long)min(rb + v, M - 1) * lds_ + col];
+                for (int v = 0; v < 4; v++) {
+                    const int row = chk ? min(row0 + i * 16 + v, M - 1) : row0 + i * 16 + v;
+                    if constexpr (AUX) {
+                        const float *src = aux_in + (long)row * ld_aux;
+#pragma unroll
+                        for (int j = 0; j < TN; j++) old[v][j] = src[cj[j]];
+                    } else {
+                        const gfloat *src = Cg + (long)row * ldcm;
+#pragma unroll
+                        for (int j = 0; j < TN; j++) old[v][j] = src[cj[j]];
+                    }
+                }
             }
 #pragma unroll
             for (int v = 0; v < 4; v++) {
-                const int row = rb + v;
-                if (row < M) {
-                    float out = acc[i][j][v] + bv;
+                const int row = row0 + i * 16 + v;
+                if (chk && row >= M) continue;
+                gfloat *dst = Cg + (long)row * ldcm;
+#pragma unroll
+                for (int j = 0; j < TN; j++) {
+                    if (chk && col0 + j * 16 >= N) continue;
+                    float out = acc[i][j][v] + bv[j];
                     if constexpr (EPI == EPI_GELU) {
-                        if (aux_out) aux_out[(long)row * ld_aux + col] = out;
+                        if (aux_out) aux_out[(long)row * ld_aux + cj[j]] = out;
                         out = gelu_f(out);
                     } else if constexpr (EPI == EPI_RESID) {
-                        out = old[v] + out;
+                        out = old[v][j] + out;
                     } else if constexpr (EPI == EPI_GELU_BWD) {
-                        out = out * gelu_grad(old[v]);
+                        out = out * gelu_grad(old[v][j]);
                     } else if (accumulate) {
-                        out = old[v] + out;
+                        out = old[v][j] + out;
                     }
-                    Cm[(long)row * ldcm + col] = out;
+                    dst[cj[j]] = out;
                 }
             }
         }
-    }
+    };
+    if (m0 + BM <= M && n0 + BN <= N)
+        store(IC<0>{});
+    else
+        store(IC<1>{});
 }
 
 template <int BM, int BN, int STAGES, bool A_KC, bool B_KC, int EPI = EPI_NONE>
@@ -1168,10 +1207,10 @@ static hipError_t launch_dma_epi(const SgemmPlan &p, int M, int N, int K, const 
                                  hipStream_t stream) {
     const int s16 = s16_tile(M, N);
     if (s16 == 1)
-        return launch_s16<128, 128, 4, A_KC, B_KC, EPI>(M, N, K, 1, K, A, lda, B, ldb, bias, 0, C, ldc,
+        return launch_s16<128, 128, 2, A_KC, B_KC, EPI>(M, N, K, 1, K, A, lda, B, ldb, bias, 0, C, ldc,
                                                          stream, aux_in, aux_out, ld_aux);
     if (s16 == 2)
-        return launch_s16<128, 64, 4, A_KC, B_KC, EPI>(M, N, K, 1, K, A, lda, B, ldb, bias, 0, C, ldc,
+        return launch_s16<128, 64, 3, A_KC, B_KC, EPI>(M, N, K, 1, K, A, lda, B, ldb, bias, 0, C, ldc,
                                                         stream, aux_in, aux_out, ld_aux);
     if (p.cfg == SG_64_KG2)
         return launch_dma<64, 64, 2, 2, 1, A_KC, B_KC, EPI>(M, N, K, 1, K, A, lda, B, ldb, bias, 0, C,
@@ -1226,9 +1265,9 @@ static hipError_t dispatch_layout(const SgemmPlan &p, int M, int N, int K, const
     }
     const int s16 = split ? 0 : s16_tile(M, N);
     if (dma_ok && s16 == 1) {
-        e = launch_s16<128, 128, 4, A_KC, B_KC>(M, N, K, 1, K, A, lda, B, ldb, b, acc, out, ldo, stream);
+        e = launch_s16<128, 128, 2, A_KC, B_KC>(M, N, K, 1, K, A, lda, B, ldb, b, acc, out, ldo, stream);
     } else if (dma_ok && s16 == 2) {
-        e = launch_s16<128, 64, 4, A_KC, B_KC>(M, N, K, 1, K, A, lda, B, ldb, b, acc, out, ldo, stream);
+        e = launch_s16<128, 64, 3, A_KC, B_KC>(M, N, K, 1, K, A, lda, B, ldb, b, acc, out, ldo, stream);
     } else if (dma_ok) {
         if (p.cfg == SG_64_KG2)
             e = launch_dma<64, 64, 2, 2, 1, A_KC, B_KC>(M, N, K, p.splits, p.kchunk, A, lda, B, ldb, b,
