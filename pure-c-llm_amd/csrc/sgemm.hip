@@ -774,33 +774,38 @@ static hipError_t launch_dma(int M, int N, int K, int splits, int kchunk, const 
 // to issue from).
 //
 // Tile: BM x BN per workgroup of 4 waves in a 2x2 grid; a wave owns
-// (BM/2) x (BN/2) as TM x TN blocks of 16x16. A ring stage holds 32 k, used
-// as two sub-steps of 16: lane (r16, q) = (lane % 16, lane / 16) feeds
-// k = 16u + 4q + s at MFMA step s of sub-step u (the same for A and B, so the
-// sum over k is unchanged) and holds outputs (4q + v, r16) of a block.
-// LDS layouts, unpadded and swizzled (SQ_LDS_BANK_CONFLICT reads zero):
-//  * K-contiguous operand: rows of 128 bytes (eight 16-byte pieces); logical
-//    piece p of row r sits at p ^ ((r >> 1) & 7). A lane reads one piece
-//    (its four k) per block per sub-step. (The maps (r >> 1) & 3 and
-//    ((r >> 1) & 3) | ((r & 1) << 2) conflict.)
-//  * MN-contiguous operand: 32 k-rows of ROWS floats; logical 16-byte chunk
+// (BM/2) x (BN/2) as TM x TN blocks of 16x16. A ring stage holds BK = 16 SUB
+// k (SUB = 1 or 2), used as SUB sub-steps of 16: lane (r16, q) = (lane % 16,
+// lane / 16) feeds k = 16u + 4q + s at MFMA step s of sub-step u (the same
+// for A and B, so the sum over k is unchanged) and holds outputs (4q + v,
+// r16) of a block. LDS layouts, unpadded and swizzled (SQ_LDS_BANK_CONFLICT
+// reads zero):
+//  * K-contiguous operand: rows of 4 BK bytes (4 SUB pieces of 16 bytes);
+//    logical piece p of row r sits at p ^ ((r >> 1) & (4 SUB - 1)). A lane
+//    reads one piece (its four k) per block per sub-step. (For 64-byte rows
+//    the map (r >> 2) & 3 conflicts; for 128-byte rows (r >> 1) & 3 and
+//    ((r >> 1) & 3) | ((r & 1) << 2) do.)
+//  * MN-contiguous operand: BK k-rows of ROWS floats; logical 16-byte chunk
 //    c of k-row k sits at c ^ (((k >> 2) & 3) << 2). A lane reads four floats
 //    (k = 16u + 4q .. + 3) per block per sub-step.
-// Per stage: sub-step 0 reads sub-step 1's fragments while its MFMAs run;
-// sub-step 1 waits for this wave's DMA of the next stage, crosses the one
-// barrier of the stage (after it every wave has read this stage and every
-// DMA of the next has landed), reads the next stage's first fragments,
-// refills this stage (tile kt + STAGES) and runs its MFMAs with the DMA
-// instructions spread among them (issued together they stall the wave).
-// Every stage issues one tile's DMA (clamped to the last tile past the end,
-// into a stage no one reads again), so the wait is always
-// vmcnt((STAGES - 2) * LOADS). 32-deep stages against 16-deep ones with a
-// barrier each: +6-8% in a same-run comparison.
-constexpr int S16_BK = 32;
-
-template <int ROWS, bool KC, int NW>
+// Per sub-step: wait for this wave's reads of the sub-step's fragments; on
+// the last sub-step of a stage also wait for this wave's DMA of the next
+// stage and cross the stage's one barrier (after it every wave has read this
+// stage and every DMA of the next has landed); read the next sub-step's
+// fragments (the next stage's first after the barrier) while this
+// sub-step's MFMAs run; on the last sub-step refill this stage (tile kt +
+// STAGES) with the DMA instructions spread among the MFMAs (issued together
+// they stall the wave). Every stage issues one tile's DMA (clamped to the
+// last tile past the end, into a stage no one reads again), so the wait is
+// always vmcnt((STAGES - 2) * LOADS). What decides between the shapes is
+// how far ahead the DMA runs, (STAGES - 1) * BK k: 128x128 tiles take a
+// 4-stage ring of 16-deep stages (48 k ahead in 64 KB; 32-deep stages fit
+// only two, 32 k ahead, 3-5% slower), 128x64 tiles a 3-stage ring of
+// 32-deep stages (64 k ahead in 72 KB).
+template <int ROWS, bool KC, int NW, int BK>
 struct Dma16 {
-    static constexpr int BYTES = ROWS * S16_BK * 4;  // one ring stage of this operand
+    static constexpr int PC = BK / 4;                // 16-byte pieces per K-contiguous row
+    static constexpr int BYTES = ROWS * BK * 4;      // one ring stage of this operand
     static constexpr int INST = BYTES / 1024;
     static constexpr int PER_WAVE = INST / NW;
     static_assert(INST % NW == 0, "DMA instructions must split over the waves");
@@ -812,8 +817,8 @@ struct Dma16 {
         for (int q = 0; q < PER_WAVE; q++) {
             const int inst = q * NW + wave;
             if (KC) {
-                const int r = inst * 8 + lane / 8;
-                const int gp = (lane % 8) ^ ((r >> 1) & 7);
+                const int r = inst * (64 / PC) + lane / PC;
+                const int gp = (lane % PC) ^ ((r >> 1) & (PC - 1));
                 voff[q] = (long)min(rows0 + r, nrows - 1) * ld + gp * 4;
             } else {
                 const int e = inst * 64 + lane, k = e / CHR, c = e % CHR;
@@ -834,15 +839,17 @@ struct Dma16 {
     }
 };
 
-template <int BM, int BN, int STAGES, bool A_KC, bool B_KC, int EPI = EPI_NONE>
+template <int BM, int BN, int STAGES, int SUB, bool A_KC, bool B_KC, int EPI = EPI_NONE>
 __global__ __launch_bounds__(256, 2) void sgemm16_kernel(
     const float *__restrict__ A, long lda, const float *__restrict__ B, long ldb,
     const float *__restrict__ bias, float *__restrict__ C, long ldc, int M, int N, int K,
     int accumulate, int kchunk, const float *__restrict__ aux_in, float *__restrict__ aux_out,
     long ld_aux) {
     constexpr int NW = 4;
-    using TA = Dma16<BM, A_KC, NW>;
-    using TB = Dma16<BN, B_KC, NW>;
+    constexpr int BK = 16 * SUB, PC = 4 * SUB;
+    static_assert(SUB == 1 || SUB == 2, "16- or 32-deep stages");
+    using TA = Dma16<BM, A_KC, NW, BK>;
+    using TB = Dma16<BN, B_KC, NW, BK>;
     constexpr int STAGE = TA::BYTES + TB::BYTES;
     constexpr int WTM = BM / 2, WTN = BN / 2, TM = WTM / 16, TN = WTN / 16;
     constexpr int LOADS = TA::PER_WAVE + TB::PER_WAVE;
@@ -867,7 +874,7 @@ __global__ __launch_bounds__(256, 2) void sgemm16_kernel(
         B += B_KC ? kbeg : (long)kbeg * ldb;
         C += (long)blockIdx.y * M * ldc;
     }
-    const int nk = K / S16_BK;
+    const int nk = K / BK;
 
     long voa[TA::PER_WAVE], vob[TB::PER_WAVE];
     int lda_o[TA::PER_WAVE], ldb_o[TB::PER_WAVE];
@@ -876,17 +883,18 @@ __global__ __launch_bounds__(256, 2) void sgemm16_kernel(
     auto dma = [&](int t) {
         int8_t *st = lds + (t % STAGES) * STAGE;
         const int tk = min(t, nk - 1);
-        TA::dma(A, lda, tk * S16_BK, voa, lda_o, st);
-        TB::dma(B, ldb, tk * S16_BK, vob, ldb_o, st + TA::BYTES);
+        TA::dma(A, lda, tk * BK, voa, lda_o, st);
+        TB::dma(B, ldb, tk * BK, vob, ldb_o, st + TA::BYTES);
     };
     // fragment addresses within a stage (block offsets as immediates; the
     // K-contiguous swizzle depends only on r16 since row bases are multiples
     // of 16)
     const unsigned lds0 = (unsigned)(uintptr_t)(const __attribute__((address_space(3))) void *)lds;
-    unsigned a_addr[A_KC ? 2 : TM], b_addr[B_KC ? 2 : TN];
+    unsigned a_addr[A_KC ? SUB : TM], b_addr[B_KC ? SUB : TN];
     if constexpr (A_KC) {
 #pragma unroll
-        for (int u = 0; u < 2; u++) a_addr[u] = (wm * WTM + r16) * 128 + (((4 * u + q) ^ ((r16 >> 1) & 7)) << 4);
+        for (int u = 0; u < SUB; u++)
+            a_addr[u] = (wm * WTM + r16) * (4 * BK) + (((4 * u + q) ^ ((r16 >> 1) & (PC - 1))) << 4);
     } else {
 #pragma unroll
         for (int i = 0; i < TM; i++) {
@@ -896,8 +904,8 @@ __global__ __launch_bounds__(256, 2) void sgemm16_kernel(
     }
     if constexpr (B_KC) {
 #pragma unroll
-        for (int u = 0; u < 2; u++)
-            b_addr[u] = TA::BYTES + (wn * WTN + r16) * 128 + (((4 * u + q) ^ ((r16 >> 1) & 7)) << 4);
+        for (int u = 0; u < SUB; u++)
+            b_addr[u] = TA::BYTES + (wn * WTN + r16) * (4 * BK) + (((4 * u + q) ^ ((r16 >> 1) & (PC - 1))) << 4);
     } else {
 #pragma unroll
         for (int j = 0; j < TN; j++) {
@@ -913,7 +921,7 @@ __global__ __launch_bounds__(256, 2) void sgemm16_kernel(
         static_for<0, TM>([&](auto I) {
             constexpr int i = decltype(I)::value;
             if constexpr (A_KC) {
-                sd_read128<i * 16 * 128>(fak[sl][i], st + a_addr[u]);
+                sd_read128<i * 16 * 4 * BK>(fak[sl][i], st + a_addr[u]);
             } else {
                 sd_read32<(16 * u + 0) * BM * 4>(fam[sl][i][0], st + a_addr[i]);
                 sd_read32<(16 * u + 1) * BM * 4>(fam[sl][i][1], st + a_addr[i]);
@@ -924,7 +932,7 @@ __global__ __launch_bounds__(256, 2) void sgemm16_kernel(
         static_for<0, TN>([&](auto J) {
             constexpr int j = decltype(J)::value;
             if constexpr (B_KC) {
-                sd_read128<j * 16 * 128>(fbk[sl][j], st + b_addr[u]);
+                sd_read128<j * 16 * 4 * BK>(fbk[sl][j], st + b_addr[u]);
             } else {
                 sd_read32<(16 * u + 0) * BN * 4>(fbm[sl][j][0], st + b_addr[j]);
                 sd_read32<(16 * u + 1) * BN * 4>(fbm[sl][j][1], st + b_addr[j]);
@@ -991,32 +999,46 @@ __global__ __launch_bounds__(256, 2) void sgemm16_kernel(
         __builtin_amdgcn_s_waitcnt(sd_waitcnt_vm((STAGES - 1) * LOADS));
         __builtin_amdgcn_s_barrier();
         read_sub(IC<0>{}, IC<0>{}, lds0);
-        for (int kt = 0; kt < nk; kt++) {
-            const unsigned st = lds0 + (kt % STAGES) * STAGE;
-            // sub-step 0
+        // sub-step U of stage kt, its fragments in slot SL
+        auto sub = [&](auto SL, auto U, int kt) {
+            constexpr int sl = decltype(SL)::value, u = decltype(U)::value;
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            fence_slot(IC<0>{});
-            __builtin_amdgcn_sched_barrier(0);
-            read_sub(IC<1>{}, IC<1>{}, st);
-            __builtin_amdgcn_sched_barrier(0);
-            mfma_sub(IC<0>{});
-            __builtin_amdgcn_sched_barrier(0);
-            // sub-step 1: the stage boundary
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            fence_slot(IC<1>{});
-            __builtin_amdgcn_s_waitcnt(sd_waitcnt_vm((STAGES - 2) * LOADS));
-            __builtin_amdgcn_s_barrier();
-            __builtin_amdgcn_sched_barrier(0);
-            read_sub(IC<0>{}, IC<0>{}, lds0 + ((kt + 1) % STAGES) * STAGE);
-            mfma_sub(IC<1>{});
-            dma(kt + STAGES);
-            __builtin_amdgcn_sched_group_barrier(0x100, NRD, 0);  // LDS reads
-            static_for<0, LOADS>([&](auto) {
-                __builtin_amdgcn_sched_group_barrier(0x008, PER, 0);  // MFMAs
-                __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);    // one DMA
-            });
-            if constexpr (REST > 0) __builtin_amdgcn_sched_group_barrier(0x008, REST, 0);
-            __builtin_amdgcn_sched_barrier(0);
+            fence_slot(SL);
+            if constexpr (u + 1 < SUB) {
+                __builtin_amdgcn_sched_barrier(0);
+                read_sub(IC<sl ^ 1>{}, IC<u + 1>{}, lds0 + (kt % STAGES) * STAGE);
+                __builtin_amdgcn_sched_barrier(0);
+                mfma_sub(SL);
+                __builtin_amdgcn_sched_barrier(0);
+            } else {
+                __builtin_amdgcn_s_waitcnt(sd_waitcnt_vm((STAGES - 2) * LOADS));
+                __builtin_amdgcn_s_barrier();
+                __builtin_amdgcn_sched_barrier(0);
+                read_sub(IC<sl ^ 1>{}, IC<0>{}, lds0 + ((kt + 1) % STAGES) * STAGE);
+                mfma_sub(SL);
+                dma(kt + STAGES);
+                __builtin_amdgcn_sched_group_barrier(0x100, NRD, 0);  // LDS reads
+                static_for<0, LOADS>([&](auto) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, PER, 0);  // MFMAs
+                    __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);    // one DMA
+                });
+                if constexpr (REST > 0) __builtin_amdgcn_sched_group_barrier(0x008, REST, 0);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        };
+        if constexpr (SUB == 2) {
+            for (int kt = 0; kt < nk; kt++) {
+                sub(IC<0>{}, IC<0>{}, kt);
+                sub(IC<1>{}, IC<1>{}, kt);
+            }
+        } else {
+            // one sub-step per stage: the slot alternates with the stage
+            int kt = 0;
+            for (; kt + 1 < nk; kt += 2) {
+                sub(IC<0>{}, IC<0>{}, kt);
+                sub(IC<1>{}, IC<0>{}, kt + 1);
+            }
+            if (kt < nk) sub(IC<0>{}, IC<0>{}, kt);
         }
         // no DMA or fragment read in flight past the loop
         __builtin_amdgcn_s_waitcnt(sd_waitcnt_vm(0));
@@ -1088,14 +1110,14 @@ __global__ __launch_bounds__(256, 2) void sgemm16_kernel(
         store(IC<1>{});
 }
 
-template <int BM, int BN, int STAGES, bool A_KC, bool B_KC, int EPI = EPI_NONE>
+template <int BM, int BN, int STAGES, int SUB, bool A_KC, bool B_KC, int EPI = EPI_NONE>
 static hipError_t launch_s16(int M, int N, int K, int splits, int kchunk, const float *A, long lda,
                              const float *B, long ldb, const float *bias, int accumulate, float *C,
                              long ldc, hipStream_t stream, const float *aux_in = nullptr,
                              float *aux_out = nullptr, long ld_aux = 0) {
     const int nblk = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
     if (nblk == 0) return hipSuccess;
-    hipLaunchKernelGGL((sgemm16_kernel<BM, BN, STAGES, A_KC, B_KC, EPI>), dim3(nblk, splits), dim3(256), 0,
+    hipLaunchKernelGGL((sgemm16_kernel<BM, BN, STAGES, SUB, A_KC, B_KC, EPI>), dim3(nblk, splits), dim3(256), 0,
                        stream, A, lda, B, ldb, bias, C, ldc, M, N, K, accumulate, kchunk, aux_in, aux_out,
                        ld_aux);
     return hipGetLastError();
@@ -1207,10 +1229,10 @@ static hipError_t launch_dma_epi(const SgemmPlan &p, int M, int N, int K, const 
                                  hipStream_t stream) {
     const int s16 = s16_tile(M, N);
     if (s16 == 1)
-        return launch_s16<128, 128, 2, A_KC, B_KC, EPI>(M, N, K, 1, K, A, lda, B, ldb, bias, 0, C, ldc,
+        return launch_s16<128, 128, 4, 1, A_KC, B_KC, EPI>(M, N, K, 1, K, A, lda, B, ldb, bias, 0, C, ldc,
                                                          stream, aux_in, aux_out, ld_aux);
     if (s16 == 2)
-        return launch_s16<128, 64, 3, A_KC, B_KC, EPI>(M, N, K, 1, K, A, lda, B, ldb, bias, 0, C, ldc,
+        return launch_s16<128, 64, 3, 2, A_KC, B_KC, EPI>(M, N, K, 1, K, A, lda, B, ldb, bias, 0, C, ldc,
                                                         stream, aux_in, aux_out, ld_aux);
     if (p.cfg == SG_64_KG2)
         return launch_dma<64, 64, 2, 2, 1, A_KC, B_KC, EPI>(M, N, K, 1, K, A, lda, B, ldb, bias, 0, C,
@@ -1265,9 +1287,9 @@ static hipError_t dispatch_layout(const SgemmPlan &p, int M, int N, int K, const
     }
     const int s16 = split ? 0 : s16_tile(M, N);
     if (dma_ok && s16 == 1) {
-        e = launch_s16<128, 128, 2, A_KC, B_KC>(M, N, K, 1, K, A, lda, B, ldb, b, acc, out, ldo, stream);
+        e = launch_s16<128, 128, 4, 1, A_KC, B_KC>(M, N, K, 1, K, A, lda, B, ldb, b, acc, out, ldo, stream);
     } else if (dma_ok && s16 == 2) {
-        e = launch_s16<128, 64, 3, A_KC, B_KC>(M, N, K, 1, K, A, lda, B, ldb, b, acc, out, ldo, stream);
+        e = launch_s16<128, 64, 3, 2, A_KC, B_KC>(M, N, K, 1, K, A, lda, B, ldb, b, acc, out, ldo, stream);
     } else if (dma_ok) {
         if (p.cfg == SG_64_KG2)
             e = launch_dma<64, 64, 2, 2, 1, A_KC, B_KC>(M, N, K, p.splits, p.kchunk, A, lda, B, ldb, b,
