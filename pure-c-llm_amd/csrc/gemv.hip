@@ -58,6 +58,7 @@ __device__ __forceinline__ void stage_rows(T *xs, int ld, int kchunk, int kvalid
         if constexpr (RECENTRE) return (T)(x ^ (T)0x80);
         else return x;
     };
+    const auto Xg = gbl(X0);
     const bool vec = ((reinterpret_cast<uintptr_t>(X0) | (uintptr_t)(ldx * sizeof(T))) & 15) == 0;
     if (vec) {
         constexpr int JU = MR >= 16 ? 1 : 16 / MR;  // vector loads per row per round
@@ -71,9 +72,9 @@ __device__ __forceinline__ void stage_rows(T *xs, int ld, int kchunk, int kvalid
                     const int kk = (tid + (c0 + ju) * GV_THREADS) * V;
                     vec_t x = (T)0;
                     if (m < M && kk < kchunk) {
-                        const T *src = X0 + (long)m * ldx + kk;
+                        const auto src = Xg + (long)m * ldx + kk;
                         if (kk + V <= kvalid) {
-                            x = *reinterpret_cast<const vec_t *>(src);
+                            x = *gvec<vec_t>(src);
                             if constexpr (RECENTRE) x ^= (T)0x80;
                         } else {
 #pragma unroll
@@ -100,7 +101,7 @@ __device__ __forceinline__ void stage_rows(T *xs, int ld, int kchunk, int kvalid
 #pragma unroll
                 for (int ju = 0; ju < JU; ju++) {
                     const int kk = tid + (j0 + ju) * GV_THREADS;
-                    v[m][ju] = (m < M && kk < kvalid) ? fix(X0[(long)m * ldx + kk]) : (T)0;
+                    v[m][ju] = (m < M && kk < kvalid) ? fix(Xg[(long)m * ldx + kk]) : (T)0;
                 }
 #pragma unroll
             for (int m = 0; m < MR; m++)
@@ -399,7 +400,7 @@ __global__ __launch_bounds__(GV_THREADS) void sgemv_t_kernel(
 // (k = 16j + 256i) of rows rs + 16r; activations are staged re-centred
 // (x ^ 0x80 = x - 128) so v_dot4_i32_i8 accumulates sum (x-128)*w exactly.
 __device__ __forceinline__ int32_t epi_int(int32_t v, const int32_t *col_off, int n) {
-    return col_off ? (int32_t)((unsigned)v + (unsigned)col_off[n]) : v;
+    return col_off ? (int32_t)((unsigned)v + (unsigned)gbl(col_off)[n]) : v;
 }
 
 template <int OUT>
@@ -408,10 +409,10 @@ __device__ __forceinline__ void igemv_write(void *Yv, long ldy, int m, int n, in
                                             const float *sb) {
     v = epi_int(v, col_off, n);
     if (OUT == 0) {
-        reinterpret_cast<int32_t *>(Yv)[(long)m * ldy + n] = v;
+        gbl(reinterpret_cast<int32_t *>(Yv))[(long)m * ldy + n] = v;
     } else {
-        const float dq = (OUT == 2) ? sa[m] * sb[n] : sb[n];
-        reinterpret_cast<float *>(Yv)[(long)m * ldy + n] = (float)v * dq;
+        const float dq = (OUT == 2) ? gbl(sa)[m] * gbl(sb)[n] : gbl(sb)[n];
+        gbl(reinterpret_cast<float *>(Yv))[(long)m * ldy + n] = (float)v * dq;
     }
 }
 
@@ -1093,7 +1094,7 @@ __device__ __forceinline__ void gg_f32_n(const GgDesc &d, int strip, float *xs, 
     const int run = ld >> 4;  // rows per group, a multiple of 8
     const int n0 = strip * 64, col = n0 + 4 * c4;
     const int colc = min(col, N - 4);  // N % 4 == 0: clamped lanes feed columns >= N only
-    const float *__restrict__ W = static_cast<const float *>(d.W);
+    const auto W = gbl(static_cast<const float *>(d.W));
     const long ldw = d.ldw;
     const int r0 = (wv * 4 + rr) * run;
     constexpr int UR = 8;  // rows per load batch
@@ -1102,7 +1103,7 @@ __device__ __forceinline__ void gg_f32_n(const GgDesc &d, int strip, float *xs, 
 #pragma unroll
         for (int u = 0; u < UR; u++) {
             const int k = r0 + i + u;
-            v4f v = __builtin_nontemporal_load(reinterpret_cast<const v4f *>(W + (long)min(k, K - 1) * ldw + colc));
+            v4f v = __builtin_nontemporal_load(gvec<v4f>(W + (long)min(k, K - 1) * ldw + colc));
             w[u] = k < K ? v : v4f{0.f, 0.f, 0.f, 0.f};
         }
     };
@@ -1152,13 +1153,13 @@ __device__ __forceinline__ void gg_f32_n(const GgDesc &d, int strip, float *xs, 
             for (int j = 0; j < 4; j++) red[wv][m][4 * c4 + j] = acc[m][j];
     }
     __syncthreads();
-    float *__restrict__ Y = static_cast<float *>(d.Y);
+    const auto Y = gbl(static_cast<float *>(d.Y));
     for (int o = tid; o < M * 64; o += GV_THREADS) {
         const int m = o >> 6, c = o & 63, n = n0 + c;
         if (n < N) {
             const float sum = ((red[0][m][c] + red[1][m][c]) + red[2][m][c]) + red[3][m][c];
-            const float y = sum + (d.bias ? d.bias[n] : 0.f);
-            float *dst = Y + (long)m * d.ldy + n;
+            const float y = sum + (d.bias ? gbl(d.bias)[n] : 0.f);
+            const auto dst = Y + (long)m * d.ldy + n;
             *dst = d.accumulate ? *dst + y : y;
         }
     }
@@ -1170,8 +1171,8 @@ __device__ __forceinline__ void gg_f32_t(const GgDesc &d, int strip, float *xs) 
     constexpr int RPL = 2, UK = 4;
     const int M = d.M, N = d.N, K = d.K, ld = d.xld;
     const int n0 = strip * 32;
-    const float *__restrict__ W = static_cast<const float *>(d.W);
-    const float *wrow[RPL];
+    const auto W = gbl(static_cast<const float *>(d.W));
+    const __attribute__((address_space(1))) float *wrow[RPL];
 #pragma unroll
     for (int r = 0; r < RPL; r++) wrow[r] = W + (long)min(n0 + rs + 16 * r, N - 1) * d.ldw;
     // K % 4 == 0; k past K is clamped for the load and skipped in the sums
@@ -1180,7 +1181,7 @@ __device__ __forceinline__ void gg_f32_t(const GgDesc &d, int strip, float *xs) 
         for (int u = 0; u < UK; u++)
 #pragma unroll
             for (int r = 0; r < RPL; r++)
-                w[u][r] = __builtin_nontemporal_load(reinterpret_cast<const v4f *>(wrow[r] + min(k0 + 64 * u, K - 4)));
+                w[u][r] = __builtin_nontemporal_load(gvec<v4f>(wrow[r] + min(k0 + 64 * u, K - 4)));
     };
     v4f wn[UK][RPL];
     load_batch(wn, 4 * j);
@@ -1226,15 +1227,15 @@ __device__ __forceinline__ void gg_f32_t(const GgDesc &d, int strip, float *xs) 
             acc[r][m] = v;
         }
     if (j == 0) {
-        float *__restrict__ Y = static_cast<float *>(d.Y);
+        const auto Y = gbl(static_cast<float *>(d.Y));
 #pragma unroll
         for (int r = 0; r < RPL; r++) {
             const int n = n0 + rs + 16 * r;
 #pragma unroll
             for (int m = 0; m < MR; m++) {
                 if (m < M && n < N) {
-                    const float y = acc[r][m] + (d.bias ? d.bias[n] : 0.f);
-                    float *dst = Y + (long)m * d.ldy + n;
+                    const float y = acc[r][m] + (d.bias ? gbl(d.bias)[n] : 0.f);
+                    const auto dst = Y + (long)m * d.ldy + n;
                     *dst = d.accumulate ? *dst + y : y;
                 }
             }
@@ -1276,9 +1277,9 @@ __device__ __forceinline__ void gg_u8s8(const GgDesc &d, int strip, int8_t *lds)
     const int n0 = strip * GGQ_RB;
     int8_t *xs = lds;
     int8_t *wreg = lds + ggq_x_bytes(MR, d.K) + wv * GGQ_WREG;
-    const int8_t *__restrict__ B = static_cast<const int8_t *>(d.W);
+    const auto B = gbl(static_cast<const int8_t *>(d.W));
     // load u of a slice: row 4u + lane/16 of the wave's tile, bytes 16*(lane%16)
-    const int8_t *src[4];
+    const __attribute__((address_space(1))) int8_t *src[4];
     int8_t *wdst[4];
 #pragma unroll
     for (int u = 0; u < 4; u++) {
@@ -1288,7 +1289,7 @@ __device__ __forceinline__ void gg_u8s8(const GgDesc &d, int strip, int8_t *lds)
     }
     auto load = [&](v4i (&w)[4], int t) {
 #pragma unroll
-        for (int u = 0; u < 4; u++) w[u] = __builtin_nontemporal_load(reinterpret_cast<const v4i *>(src[u] + t * GGQ_SL));
+        for (int u = 0; u < 4; u++) w[u] = __builtin_nontemporal_load(gvec<v4i>(src[u] + t * GGQ_SL));
     };
     // the first slice is in flight while the activations are staged
     v4i wn[4];

@@ -106,7 +106,7 @@ struct StepPlan {
 // of 128-byte K tiles; OCC workgroups are meant to share a CU (the LDS ring
 // is sized for it and the register budget is capped accordingly).
 // Requires M*lda and N*ldb below 2^32 (32-bit per-lane DMA offsets).
-template <int BM, int BN, int WM, int WN, int STAGES, int OCC, int OUT>
+template <int BM, int BN, int WM, int WN, int STAGES, int OCC, int OUT, int NTS>
 __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(
     (OCC * WM * WN + 3) / 4))) void igemm_mfma_kernel(const uint8_t *__restrict__ A, long lda,
                                                      const int8_t *__restrict__ B, long ldb,
@@ -114,7 +114,7 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(
                                                      const float *__restrict__ sa,
                                                      const float *__restrict__ sb,
                                                      void *__restrict__ Cv, long ldc, int M, int N,
-                                                     int K, int nt_store) {
+                                                     int K) {
     constexpr int NW = WM * WN;
     constexpr int WTM = BM / WM, WTN = BN / WN;
     constexpr int TM = WTM / 32, TN = WTN / 32;
@@ -324,13 +324,13 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(
                     // output dirty in L2 for the end-of-kernel release to
                     // flush. Large outputs stream better through L2.
                     if (OUT == 0) {
-                        if (nt_store) __builtin_nontemporal_store(acc[i][j][v], (gint32_t *)C_out + o);
-                        else reinterpret_cast<int32_t *>(C_out)[o] = acc[i][j][v];
+                        if constexpr (NTS) __builtin_nontemporal_store(acc[i][j][v], (gint32_t *)C_out + o);
+                        else ((gint32_t *)C_out)[o] = acc[i][j][v];
                     } else {
                         const int32_t vv = (int32_t)((unsigned)acc[i][j][v] + offv[j]);
                         const float dq = (OUT == 2) ? rs[v] * sbv[j] : sbv[j];
-                        if (nt_store) __builtin_nontemporal_store((float)vv * dq, (gfloat_t *)C_out + o);
-                        else reinterpret_cast<float *>(C_out)[o] = (float)vv * dq;
+                        if constexpr (NTS) __builtin_nontemporal_store((float)vv * dq, (gfloat_t *)C_out + o);
+                        else ((gfloat_t *)C_out)[o] = (float)vv * dq;
                     }
                 }
             }
@@ -356,7 +356,7 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(
 // Before B(g) the producers have waited for K tile g+1 (leaving g+2 .. in
 // flight) and every consumer has issued and retired its reads of K tile g;
 // after it the producers refill tile g's stage with tile g + STAGES.
-template <int BM, int BN, int WM, int WN, int STAGES, int NWP, int OUT>
+template <int BM, int BN, int WM, int WN, int STAGES, int NWP, int OUT, int NTS>
 __global__ __launch_bounds__(64 * (WM * WN + NWP)) __attribute__((amdgpu_waves_per_eu(
     (WM * WN + NWP + 3) / 4))) void igemm_wp_kernel(const uint8_t *__restrict__ A, long lda,
                                                       const int8_t *__restrict__ B, long ldb,
@@ -364,7 +364,7 @@ __global__ __launch_bounds__(64 * (WM * WN + NWP)) __attribute__((amdgpu_waves_p
                                                       const float *__restrict__ sa,
                                                       const float *__restrict__ sb,
                                                       void *__restrict__ Cv, long ldc, int M, int N,
-                                                      int K, int nt_store) {
+                                                      int K) {
     constexpr int NWC = WM * WN, BK = IG_BK;
     constexpr int WTM = BM / WM, WTN = BN / WN, TM = WTM / 32, TN = WTN / 32;
     constexpr int NM = TM * TN, NR = TM + TN;
@@ -607,13 +607,13 @@ __global__ __launch_bounds__(64 * (WM * WN + NWP)) __attribute__((amdgpu_waves_p
                         if (row < Mv && col < Nv) {
                             const long o = (long)row * ld_out + col;
                             if (OUT == 0) {
-                                if (nt_store) __builtin_nontemporal_store(acc[a][b][v], (gint32_t *)C_out + o);
-                                else reinterpret_cast<int32_t *>(C_out)[o] = acc[a][b][v];
+                                if constexpr (NTS) __builtin_nontemporal_store(acc[a][b][v], (gint32_t *)C_out + o);
+                                else ((gint32_t *)C_out)[o] = acc[a][b][v];
                             } else {
                                 const int32_t vv = (int32_t)((unsigned)acc[a][b][v] + offv[b]);
                                 const float dq = (OUT == 2) ? rs4[e] * sbv[b] : sbv[b];
-                                if (nt_store) __builtin_nontemporal_store((float)vv * dq, (gfloat_t *)C_out + o);
-                                else reinterpret_cast<float *>(C_out)[o] = (float)vv * dq;
+                                if constexpr (NTS) __builtin_nontemporal_store((float)vv * dq, (gfloat_t *)C_out + o);
+                                else ((gfloat_t *)C_out)[o] = (float)vv * dq;
                             }
                         }
                     }
@@ -643,21 +643,29 @@ static hipError_t launch_wp_band(int out_mode, int M, int N, int K, const uint8_
     if (ntiles == 0 || K / IG_BK == 0) return hipSuccess;
     const int grid = (int)(ntiles < device_cus() ? ntiles : device_cus());
     const dim3 block(64 * (WM * WN + NWP));
-    const int nt = (long)M * N * 4 <= (256L << 20);
-    switch (out_mode) {
-        case 0:
-            hipLaunchKernelGGL((igemm_wp_kernel<BM, BN, WM, WN, STAGES, NWP, 0>), dim3(grid), block, 0,
-                               stream, A, lda, B, ldb, col_off, sa, sb, C, ldc, M, N, K, nt);
-            break;
-        case 1:
-            hipLaunchKernelGGL((igemm_wp_kernel<BM, BN, WM, WN, STAGES, NWP, 1>), dim3(grid), block, 0,
-                               stream, A, lda, B, ldb, col_off, sa, sb, C, ldc, M, N, K, nt);
-            break;
-        default:
-            hipLaunchKernelGGL((igemm_wp_kernel<BM, BN, WM, WN, STAGES, NWP, 2>), dim3(grid), block, 0,
-                               stream, A, lda, B, ldb, col_off, sa, sb, C, ldc, M, N, K, nt);
-            break;
-    }
+    // outputs up to 256 MiB: streaming (non-temporal) stores, chosen at compile
+    // time (a run-time choice between two otherwise equal stores is merged by
+    // the compiler into one without the hint)
+    const bool nt = (long)M * N * 4 <= (256L << 20);
+    auto go = [&](auto NT) {
+        constexpr int nts = decltype(NT)::value;
+        switch (out_mode) {
+            case 0:
+                hipLaunchKernelGGL((igemm_wp_kernel<BM, BN, WM, WN, STAGES, NWP, 0, nts>), dim3(grid), block, 0,
+                                   stream, A, lda, B, ldb, col_off, sa, sb, C, ldc, M, N, K);
+                break;
+            case 1:
+                hipLaunchKernelGGL((igemm_wp_kernel<BM, BN, WM, WN, STAGES, NWP, 1, nts>), dim3(grid), block, 0,
+                                   stream, A, lda, B, ldb, col_off, sa, sb, C, ldc, M, N, K);
+                break;
+            default:
+                hipLaunchKernelGGL((igemm_wp_kernel<BM, BN, WM, WN, STAGES, NWP, 2, nts>), dim3(grid), block, 0,
+                                   stream, A, lda, B, ldb, col_off, sa, sb, C, ldc, M, N, K);
+                break;
+        }
+    };
+    if (nt) go(IC<1>{});
+    else go(IC<0>{});
     return hipGetLastError();
 }
 
@@ -693,21 +701,26 @@ static hipError_t launch_icfg(int out_mode, int M, int N, int K, const uint8_t *
     const int nblk = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
     if (nblk == 0) return hipSuccess;
     dim3 grid(nblk), block(64 * WM * WN);
-    const int nt = (long)M * N * 4 <= (256L << 20);  // outputs up to 256 MiB: streaming stores
-    switch (out_mode) {
-        case 0:
-            hipLaunchKernelGGL((igemm_mfma_kernel<BM, BN, WM, WN, STAGES, OCC, 0>), grid, block, 0,
-                               stream, A, lda, B, ldb, col_off, sa, sb, C, ldc, M, N, K, nt);
-            break;
-        case 1:
-            hipLaunchKernelGGL((igemm_mfma_kernel<BM, BN, WM, WN, STAGES, OCC, 1>), grid, block, 0,
-                               stream, A, lda, B, ldb, col_off, sa, sb, C, ldc, M, N, K, nt);
-            break;
-        default:
-            hipLaunchKernelGGL((igemm_mfma_kernel<BM, BN, WM, WN, STAGES, OCC, 2>), grid, block, 0,
-                               stream, A, lda, B, ldb, col_off, sa, sb, C, ldc, M, N, K, nt);
-            break;
-    }
+    const bool nt = (long)M * N * 4 <= (256L << 20);  // as in launch_wp_band
+    auto go = [&](auto NT) {
+        constexpr int nts = decltype(NT)::value;
+        switch (out_mode) {
+            case 0:
+                hipLaunchKernelGGL((igemm_mfma_kernel<BM, BN, WM, WN, STAGES, OCC, 0, nts>), grid, block, 0,
+                                   stream, A, lda, B, ldb, col_off, sa, sb, C, ldc, M, N, K);
+                break;
+            case 1:
+                hipLaunchKernelGGL((igemm_mfma_kernel<BM, BN, WM, WN, STAGES, OCC, 1, nts>), grid, block, 0,
+                                   stream, A, lda, B, ldb, col_off, sa, sb, C, ldc, M, N, K);
+                break;
+            default:
+                hipLaunchKernelGGL((igemm_mfma_kernel<BM, BN, WM, WN, STAGES, OCC, 2, nts>), grid, block, 0,
+                                   stream, A, lda, B, ldb, col_off, sa, sb, C, ldc, M, N, K);
+                break;
+        }
+    };
+    if (nt) go(IC<1>{});
+    else go(IC<0>{});
     return hipGetLastError();
 }
 

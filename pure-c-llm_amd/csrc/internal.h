@@ -262,6 +262,23 @@ __device__ __forceinline__ void static_for(F &&f) {
     }
 }
 
+// A global-memory view of a device pointer. Accesses through a pointer the
+// compiler cannot trace to a kernel argument (a field of a descriptor read
+// from memory, a value passed through inline asm) are otherwise flat
+// instructions, which count in lgkmcnt as well as vmcnt: every later wait for
+// an LDS access then also waits for them, which serialises a weight prefetch
+// with the LDS work it is meant to overlap. Only for pointers into device
+// memory (never LDS).
+template <typename T>
+__device__ __forceinline__ __attribute__((address_space(1))) T *gbl(T *p) {
+    return (__attribute__((address_space(1))) T *)p;
+}
+// The same view re-typed to V (a vector of T's elements, for 16-byte accesses).
+template <typename V, typename T>
+__device__ __forceinline__ const __attribute__((address_space(1))) V *gvec(const __attribute__((address_space(1))) T *p) {
+    return (const __attribute__((address_space(1))) V *)p;
+}
+
 // Workgroups are dispatched round-robin over the 8 XCDs of an MI355X
 // (workgroup i runs on XCD i % 8). Renumber them so that each XCD receives a
 // contiguous range of logical tiles; with the grouped tile order below those

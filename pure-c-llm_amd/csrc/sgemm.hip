@@ -721,7 +721,7 @@ __global__ __launch_bounds__(256 * KG) void sgemm_dma_kernel(
             constexpr bool AUX = EPI == EPI_RESID || EPI == EPI_GELU_BWD;
             float old[16];
             if (AUX || accumulate) {
-                const float *src = AUX ? aux_in : Cm;
+                const auto src = gbl(AUX ? aux_in : Cm);
                 const long lds_ = AUX ? ld_aux : ldcm;
                 static_for<0, 16>([&](auto V) {
                     constexpr int v = V.value;
@@ -745,7 +745,7 @@ __global__ __launch_bounds__(256 * KG) void sgemm_dma_kernel(
                         } else if (accumulate) {
                             out = old[v] + out;
                         }
-                        Cm[(long)row * ldcm + col] = out;
+                        gbl(Cm)[(long)row * ldcm + col] = out;
                     }
                 }
             });
