@@ -11,6 +11,8 @@ backward layouts, grown-model prefill, decode GEMV sweeps) and the rows built
 around the path (causal attention, fused epilogues, the CKP1 decode engine, the
 tied head with cross-entropy) are reported under "extra", with CPU timings of
 the reference (built from source) or of the oracle's restatement beside them.
+"vendor_library" holds the vendor GEMM library timed on the same GEMM shapes by
+a separate measurement program (drivers/gemm_yardstick.cpp), for context.
 Timing loops run in C (libpcl_bench.so) between HIP events recorded on the
 stream the kernels are launched on.
 
@@ -21,6 +23,7 @@ import ctypes as C
 import json
 import os
 import re
+import subprocess
 import sys
 import time
 
@@ -586,6 +589,9 @@ def main():
     if not args.primary_only:
         ex = run_rows(pcl, lib)
         out["rows"] = compact_rows(ex, roofs)
+        ys = vendor_yardstick()
+        if ys is not None:
+            out["vendor_library"] = ys
     if not args.no_cpu_baseline:
         base, cpu = cpu_reference(M, N, K)
         if base is not None:
@@ -598,6 +604,25 @@ def main():
         # the full tables: one JSON line on stderr (stdout carries the one result line)
         print("bench_detail " + json.dumps(ex), file=sys.stderr, flush=True)
     print(json.dumps(out), flush=True)
+
+
+def vendor_yardstick():
+    """The vendor GEMM library (hipBLASLt) timed beside libpcl_hip on the
+    gemm_bench and 350M-class shapes, by a separate measurement program
+    (drivers/gemm_yardstick.cpp, run after this process's own timed work):
+    context for the fractions of the datasheet peak. libpcl_hip never links
+    the vendor library. None when the program is not built."""
+    exe = os.path.join(PKG, "build", "gemm_yardstick")
+    if not os.path.exists(exe):
+        return None
+    try:
+        r = subprocess.run([exe], capture_output=True, text=True, timeout=240)
+    except (OSError, subprocess.TimeoutExpired):
+        return None
+    for line in r.stdout.splitlines():
+        if line.startswith("yardstick_json "):
+            return json.loads(line[len("yardstick_json "):])
+    return None
 
 
 def run_rows(pcl, lib):

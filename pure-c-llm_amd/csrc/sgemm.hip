@@ -839,28 +839,29 @@ struct Dma16 {
     }
 };
 
-template <int BM, int BN, int STAGES, int SUB, bool A_KC, bool B_KC, int EPI = EPI_NONE>
-__global__ __launch_bounds__(256, 2) void sgemm16_kernel(
+template <int BM, int BN, int STAGES, int SUB, bool A_KC, bool B_KC, int EPI = EPI_NONE, int WM = 2,
+          int WN = 2, int OCC = 2>
+__global__ __launch_bounds__(64 * WM * WN, OCC) void sgemm16_kernel(
     const float *__restrict__ A, long lda, const float *__restrict__ B, long ldb,
     const float *__restrict__ bias, float *__restrict__ C, long ldc, int M, int N, int K,
     int accumulate, int kchunk, const float *__restrict__ aux_in, float *__restrict__ aux_out,
     long ld_aux) {
-    constexpr int NW = 4;
+    constexpr int NW = WM * WN;
     constexpr int BK = 16 * SUB, PC = 4 * SUB;
     static_assert(SUB == 1 || SUB == 2, "16- or 32-deep stages");
     using TA = Dma16<BM, A_KC, NW, BK>;
     using TB = Dma16<BN, B_KC, NW, BK>;
     constexpr int STAGE = TA::BYTES + TB::BYTES;
-    constexpr int WTM = BM / 2, WTN = BN / 2, TM = WTM / 16, TN = WTN / 16;
+    constexpr int WTM = BM / WM, WTN = BN / WN, TM = WTM / 16, TN = WTN / 16;
     constexpr int LOADS = TA::PER_WAVE + TB::PER_WAVE;
     static_assert(STAGES >= 2 && (STAGES - 1) * LOADS <= 63, "vmcnt range");
-    static_assert(STAGE <= 65536 && STAGES * STAGE <= 80 * 1024, "two workgroups per CU");
+    static_assert(STAGE <= 65536 && STAGES * STAGE <= 160 * 1024 / OCC, "OCC workgroups per CU");
     static_assert(WTM % 16 == 0 && WTN % 16 == 0, "tile");
     __shared__ __attribute__((aligned(1024))) int8_t lds[STAGES * STAGE];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / WN, wn = wave % WN;
     const int r16 = lane & 15, q = lane >> 4;
 
     const int nbm = (M + BM - 1) / BM, nbn = (N + BN - 1) / BN;
@@ -1110,14 +1111,16 @@ __global__ __launch_bounds__(256, 2) void sgemm16_kernel(
         store(IC<1>{});
 }
 
-template <int BM, int BN, int STAGES, int SUB, bool A_KC, bool B_KC, int EPI = EPI_NONE>
+template <int BM, int BN, int STAGES, int SUB, bool A_KC, bool B_KC, int EPI = EPI_NONE, int WM = 2, int WN = 2,
+          int OCC = 2>
 static hipError_t launch_s16(int M, int N, int K, int splits, int kchunk, const float *A, long lda,
                              const float *B, long ldb, const float *bias, int accumulate, float *C,
                              long ldc, hipStream_t stream, const float *aux_in = nullptr,
                              float *aux_out = nullptr, long ld_aux = 0) {
     const int nblk = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
     if (nblk == 0) return hipSuccess;
-    hipLaunchKernelGGL((sgemm16_kernel<BM, BN, STAGES, SUB, A_KC, B_KC, EPI>), dim3(nblk, splits), dim3(256), 0,
+    hipLaunchKernelGGL((sgemm16_kernel<BM, BN, STAGES, SUB, A_KC, B_KC, EPI, WM, WN, OCC>), dim3(nblk, splits),
+                       dim3(64 * WM * WN), 0,
                        stream, A, lda, B, ldb, bias, C, ldc, M, N, K, accumulate, kchunk, aux_in, aux_out,
                        ld_aux);
     return hipGetLastError();

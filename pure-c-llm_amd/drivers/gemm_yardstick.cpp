@@ -2,8 +2,9 @@
 // vendor GEMM library (hipBLASLt) timed beside libpcl_hip on the same buffers
 // and shapes, in one process, so a fraction of the datasheet peak can be read
 // against what a tuned library reaches on the same part at the same sizes.
-// libpcl_hip never links this library; the Makefile builds this program only
-// on request (make yardstick).
+// libpcl_hip never links this library; this program is measurement only (built
+// with the drivers; bench.py runs it after its own timed work and reports its
+// final `yardstick_json` line beside the rows it measured).
 //
 // Shapes: the gemm_bench INT8 square (2048^3) and the 350M-class projections
 // (BASELINE.json configs[1] and [4]). INT8: u8 (or s8) activations x s8
@@ -18,6 +19,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
+#include <string>
 #include <vector>
 
 #include "../../include/pcl_hip.h"
@@ -133,6 +135,9 @@ int main() {
         return 1;
     }
     const size_t wsb = 256u << 20;
+    // the same figures as one JSON line at the end (read by bench.py)
+    std::string js = "{\"int8_TOPS\": {\"cols\": [\"pcl_i32\", \"pcl_dequant\", \"vendor_i32\"]";
+    char buf[256];
     void *ws;
     CK(hipMalloc(&ws, wsb));
     struct Shape { const char *name; int M, N, K; };
@@ -165,11 +170,15 @@ int main() {
         const double t_v = vendor(h, true, A, Bt, Cv, s.M, s.N, s.K, ws, wsb);
         printf("%-9s %5d %6d %5d | %9.1f %12.1f | %9.1f\n", s.name, s.M, s.N, s.K, ops / t_i32 / 1e9,
                ops / t_dq / 1e9, t_v > 0 ? ops / t_v / 1e9 : 0.0);
+        snprintf(buf, sizeof buf, ", \"%s\": [%.1f, %.1f, %.1f]", s.name, ops / t_i32 / 1e9, ops / t_dq / 1e9,
+                 t_v > 0 ? ops / t_v / 1e9 : 0.0);
+        js += buf;
         fflush(stdout);
         CK(hipFree(A)); CK(hipFree(Bt)); CK(hipFree(C)); CK(hipFree(Cv)); CK(hipFree(sa)); CK(hipFree(sb));
     }
     const Shape f32s[] = {{"1024^3", 1024, 1024, 1024}, {"qkv", 4096, 3072, 1024}, {"attn_out", 4096, 1024, 1024},
                           {"ffn_up", 4096, 4096, 1024}, {"ffn_down", 4096, 1024, 4096}, {"head", 4096, 50257, 1024}};
+    js += "}, \"fp32_NT_TFLOPS\": {\"cols\": [\"pcl\", \"vendor\", \"pcl_err\", \"vendor_err\"]";
     printf("\nFP32 GEMM C = A . B^T (B stored N x K), TFLOP/s; accuracy max|C-R|/max|R| on 4 rows\n");
     printf("%-9s %5s %6s %5s | %9s %9s | %9s %9s\n", "shape", "M", "N", "K", "pcl", "pcl_err", "vendor", "vendor_err");
     for (const Shape &s : f32s) {
@@ -192,9 +201,14 @@ int main() {
         const double e_v = t_v > 0 ? f32_rel(A, Bt, Cv, s.N, s.K) : 0.0;
         printf("%-9s %5d %6d %5d | %9.1f %9.1e | %9.1f %9.1e\n", s.name, s.M, s.N, s.K, fl / t_p / 1e9, e_p,
                t_v > 0 ? fl / t_v / 1e9 : 0.0, e_v);
+        snprintf(buf, sizeof buf, ", \"%s\": [%.1f, %.1f, %.1e, %.1e]", s.name, fl / t_p / 1e9,
+                 t_v > 0 ? fl / t_v / 1e9 : 0.0, e_p, e_v);
+        js += buf;
         fflush(stdout);
         CK(hipFree(A)); CK(hipFree(Bt)); CK(hipFree(C)); CK(hipFree(Cv));
     }
+    js += "}}";
+    printf("\nyardstick_json %s\n", js.c_str());
     CK(hipFree(ws));
     hipblasLtDestroy(h);
     return 0;
