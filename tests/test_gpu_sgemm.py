@@ -118,6 +118,32 @@ def test_sgemm_lds_dma_edges(opA, opB, M, N, K):
     np.testing.assert_array_equal(C[:, N:], C0[:, N:])  # padding columns untouched
 
 
+@pytest.mark.parametrize("opA,opB", [(N_, N_), (N_, T_), (T_, N_), (T_, T_)])
+@pytest.mark.parametrize("M,N,K", [(2900, 2980, 96), (4000, 1000, 64)])
+def test_sgemm_16x16_grid_edges(opA, opB, M, N, K):
+    # grids of >= 512 tiles take the 16x16x4 kernel: 128x128 tiles on 16-deep
+    # stages (2900 x 2980) and 128x64 tiles on 32-deep stages (4000 x 1000),
+    # with ragged last tile rows and columns (the bounds-checked epilogue
+    # beside the unchecked one of interior tiles), padded leading dimensions,
+    # bias and accumulate, all four layouts, against the f64 product
+    A = ob.frand((M, K + 8) if opA == N_ else (K, M + 12), 4100 + M)
+    B = ob.frand((K, N + 4) if opB == N_ else (N, K + 8), 4101 + N)
+    bias = ob.normal((N,), 4102)
+    C0 = ob.normal((M, N + 4), 4103)
+    dA, dB, db, dC = pcl.dev(A), pcl.dev(B), pcl.dev(bias), pcl.dev(C0)
+    announce("sgemm 16x16 edges", opA, opB, M, N, K)
+    pcl.check(pcl.lib.pcl_sgemm(opA, opB, M, N, K, dA.ptr, A.shape[1], dB.ptr, B.shape[1], db.ptr, 1, dC.ptr,
+                                N + 4, None))
+    pcl.sync()
+    C = dC.download((M, N + 4), np.float32)
+    Av = A[:, :K] if opA == N_ else A[:, :M]
+    Bv = B[:, :N] if opB == N_ else B[:, :K]
+    R = ob.gemm_f64(np.ascontiguousarray(Av), np.ascontiguousarray(Bv), transA=opA == T_, transB=opB == T_,
+                    bias=bias, C0=np.ascontiguousarray(C0[:, :N]))
+    assert rel(C[:, :N], R) <= FP32_TOL
+    np.testing.assert_array_equal(C[:, N:], C0[:, N:])  # padding columns untouched
+
+
 def test_sgemm_strided_leading_dims():
     # sub-matrix views: lda/ldb/ldc larger than the logical width
     M, N, K = 96, 80, 72
