@@ -3,8 +3,8 @@ one rounding) followed by the oracle's elementwise step (train.c:314-333 GELU,
 the residual add of train.c:522/527), and the reference GPU API's elementwise
 drop-ins gelu_fwd / gelu_bwd / vec_add (gpu_kernels.cu:228-251).
 
-Fused cases (NN and NT products on grids that take the LDS-DMA kernel without
-a K split) and fallback cases (TN, unaligned K, split-K grids) must give the
+Fused cases (NN and NT products on grids that take the LDS-DMA kernel or the
+16x16x4 kernel without a K split, ragged last tiles included) and fallback cases (TN, unaligned K, split-K grids) must give the
 same values; tolerance max|X-R|/max|R| <= 1e-4.
 """
 import numpy as np
@@ -40,7 +40,10 @@ def run_ex(opA, opB, A, B, M, N, K, bias, epi, aux_in=None, want_aux_out=False):
 CASES = [(1024, 1024, 256, N_, N_, "fused 64x64"), (2048, 2048, 128, N_, N_, "fused 128x128"),
          (1024, 1024, 256, N_, T_, "fused NT"), (300, 500, 200, N_, N_, "split K"),
          (1024, 1024, 250, N_, N_, "K % 32 != 0"), (1024, 1024, 256, T_, N_, "TN"),
-         (1000, 1030, 256, N_, N_, "ragged edges")]
+         (1000, 1030, 256, N_, N_, "ragged edges"),
+         (2900, 2980, 96, N_, N_, "16x16 kernel, 128x128, ragged"),
+         (2900, 2980, 96, N_, T_, "16x16 kernel, 128x128 NT, ragged"),
+         (4000, 1000, 64, N_, N_, "16x16 kernel, 128x64, ragged")]
 
 
 @pytest.mark.parametrize("M,N,K,opA,opB,path", CASES)
