@@ -306,19 +306,24 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(
     // column l%32 of each 32x32 block. The row scale of rl is fetched from
     // lane rl by a cross-lane permute (no memory access); stores carry no
     // waits, so they stream out back to back.
+    // A tile wholly inside C stores without bounds checks; one address per
+    // output row serves the TN columns of the row (immediate offsets).
+    auto store_tile = [&](auto CHECK) {
+        constexpr bool chk = decltype(CHECK)::value != 0;
 #pragma unroll
-    for (int i = 0; i < TM; i++) {
-        float rs[16];
+        for (int i = 0; i < TM; i++) {
+            float rs[16];
 #pragma unroll
-        for (int v = 0; v < 16; v++) rs[v] = (OUT == 2) ? __shfl(sav[i], (v >> 2) * 8 + g * 4 + (v & 3)) : 0.f;
-#pragma unroll
-        for (int j = 0; j < TN; j++) {
-            const int col = wcol0 + j * 32 + r32;
+            for (int v = 0; v < 16; v++) rs[v] = (OUT == 2) ? __shfl(sav[i], (v >> 2) * 8 + g * 4 + (v & 3)) : 0.f;
 #pragma unroll
             for (int v = 0; v < 16; v++) {
                 const int row = wrow0 + i * 32 + (v >> 2) * 8 + g * 4 + (v & 3);
-                if (row < M && col < N) {
-                    const long o = (long)row * ld_out + col;
+                if (chk && row >= M) continue;
+                const long ro = (long)row * ld_out + wcol0 + r32;
+#pragma unroll
+                for (int j = 0; j < TN; j++) {
+                    if (chk && wcol0 + j * 32 + r32 >= N) continue;
+                    const long o = ro + j * 32;
                     // Outputs up to 256 MiB are written with streaming (non-temporal)
                     // stores: write-back through L2 would leave the whole
                     // output dirty in L2 for the end-of-kernel release to
@@ -335,7 +340,11 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(
                 }
             }
         }
-    }
+    };
+    if (m0 + BM <= M && n0 + BN <= N)
+        store_tile(IC<0>{});
+    else
+        store_tile(IC<1>{});
 }
 
 // ---------------------------------------------------------------------------
@@ -589,23 +598,28 @@ __global__ __launch_bounds__(64 * (WM * WN + NWP)) __attribute__((amdgpu_waves_p
             sbv[b] = (OUT != 0) ? sc[cl] : 0.f;
             offv[b] = (OUT != 0 && col_off) ? reinterpret_cast<const unsigned *>(sc)[BN + cl] : 0u;
         }
+        // a tile wholly inside C stores without bounds checks, one address per
+        // output row for its TN columns
+        auto store_tile = [&](auto CHECK) {
+            constexpr bool chk = decltype(CHECK)::value != 0;
 #pragma unroll
-        for (int a = 0; a < TM; a++) {
+            for (int a = 0; a < TM; a++) {
 #pragma unroll
-            for (int vq = 0; vq < 4; vq++) {
-                typedef float v4f_t __attribute__((ext_vector_type(4)));
-                const v4f_t rs4 = (OUT == 2) ? *reinterpret_cast<const v4f_t *>(
-                                                   sc + 2 * BN + wm * WTM + a * 32 + vq * 8 + lg * 4)
-                                             : v4f_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int b = 0; b < TN; b++) {
-                    const int col = wcol0 + b * 32 + r32;
+                for (int vq = 0; vq < 4; vq++) {
+                    typedef float v4f_t __attribute__((ext_vector_type(4)));
+                    const v4f_t rs4 = (OUT == 2) ? *reinterpret_cast<const v4f_t *>(
+                                                       sc + 2 * BN + wm * WTM + a * 32 + vq * 8 + lg * 4)
+                                                 : v4f_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                     for (int e = 0; e < 4; e++) {
                         const int v = vq * 4 + e;
                         const int row = wrow0 + a * 32 + vq * 8 + lg * 4 + e;
-                        if (row < Mv && col < Nv) {
-                            const long o = (long)row * ld_out + col;
+                        if (chk && row >= Mv) continue;
+                        const long ro = (long)row * ld_out + wcol0 + r32;
+#pragma unroll
+                        for (int b = 0; b < TN; b++) {
+                            if (chk && wcol0 + b * 32 + r32 >= Nv) continue;
+                            const long o = ro + b * 32;
                             if (OUT == 0) {
                                 if constexpr (NTS) __builtin_nontemporal_store(acc[a][b][v], (gint32_t *)C_out + o);
                                 else ((gint32_t *)C_out)[o] = acc[a][b][v];
@@ -619,7 +633,11 @@ __global__ __launch_bounds__(64 * (WM * WN + NWP)) __attribute__((amdgpu_waves_p
                     }
                 }
             }
-        }
+        };
+        if (m0 + BM <= Mv && n0 + BN <= Nv)
+            store_tile(IC<0>{});
+        else
+            store_tile(IC<1>{});
     }
 }
 
