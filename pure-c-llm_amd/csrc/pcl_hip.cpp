@@ -122,8 +122,13 @@ int do_init() {
 
 // ----------------------------------------------------------- workspaces ----
 // One scratch set per stream: work on one stream is ordered on the GPU, so
-// calls that share a stream may share its scratch.
+// calls that share a stream may share its scratch. A call holds the stream's
+// call lock from taking the scratch until its last launch is enqueued
+// (ScratchLease), so a call from another host thread on the same stream (the
+// null stream is every thread's default) cannot grow, and so free, a buffer
+// the first call has taken but not yet handed to a kernel.
 struct StreamScratch {
+    std::recursive_mutex call_mu;  // recursive: a call may nest another on the stream
     pcl::Workspace ws;
     void *aux = nullptr;  // padded INT8 activations
     size_t aux_cap = 0;
@@ -134,6 +139,12 @@ struct StreamScratch {
     std::vector<void *> retired;
 };
 std::unordered_map<hipStream_t, StreamScratch> g_scratch;
+
+struct ScratchLease {
+    StreamScratch *p = nullptr;
+    std::unique_lock<std::recursive_mutex> lk;
+    StreamScratch *operator->() const { return p; }
+};
 
 int grow(void **p, size_t *cap, size_t need, hipStream_t s, StreamScratch &sc) {
     if (need <= *cap) return PCL_OK;
@@ -156,16 +167,22 @@ int grow(void **p, size_t *cap, size_t need, hipStream_t s, StreamScratch &sc) {
     return PCL_OK;
 }
 
-int get_scratch(hipStream_t s, size_t part_bytes, size_t aux_bytes, StreamScratch **out) {
+int get_scratch(hipStream_t s, size_t part_bytes, size_t aux_bytes, ScratchLease *out) {
+    StreamScratch *entry;
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        entry = &g_scratch[s];  // map nodes keep their address
+    }
+    if (!out->lk.owns_lock()) out->lk = std::unique_lock<std::recursive_mutex>(entry->call_mu);
     std::lock_guard<std::mutex> lk(g_mu);
-    StreamScratch &sc = g_scratch[s];
+    StreamScratch &sc = *entry;
     PCL_OK_OR_RETURN(grow(&sc.ws.buf, &sc.ws.bytes_cap, part_bytes, s, sc));
     PCL_OK_OR_RETURN(grow(&sc.aux, &sc.aux_cap, aux_bytes, s, sc));
     if (!sc.amax) {
         if (hipMalloc((void **)&sc.amax, 256) != hipSuccess)
             return set_error(PCL_ERR_OOM, "amax scratch allocation failed");
     }
-    *out = &sc;
+    out->p = &sc;
     return PCL_OK;
 }
 
@@ -269,7 +286,7 @@ int sgemv_xf(int xf, int N, int K, const float *X, const float *W, int ldw,
     PCL_OK_OR_RETURN(do_init());
     hipStream_t s = pick(stream);
     const GemvPlan p = plan_sgemv(1, 1, N, K);
-    StreamScratch *sc;
+    ScratchLease sc;
     PCL_OK_OR_RETURN(get_scratch(s, p.part_bytes, 0, &sc));
     HIP_OK(launch_sgemv_xf(p, xf, N, K, X, W, ldw, g, b, bias, accumulate, Y, sc->ws, s));
     return PCL_OK;
@@ -480,7 +497,7 @@ int pcl_sgemv(int opW, int M, int N, int K, const float *X, int ldx, const float
     PCL_OK_OR_RETURN(do_init());
     hipStream_t s = pick(stream);
     pcl::GemvPlan p = pcl::plan_sgemv(opW == PCL_OP_T, M, N, K);
-    StreamScratch *sc;
+    ScratchLease sc;
     PCL_OK_OR_RETURN(get_scratch(s, p.part_bytes, 0, &sc));
     HIP_OK(pcl::launch_sgemv(p, opW == PCL_OP_T, M, N, K, X, ldx, false, W, ldw, bias, accumulate,
                              Y, ldy, sc->ws, s));
@@ -684,7 +701,7 @@ static int sgemm_realigned(int opA, int opB, int M, int N, int K, const float *A
     if (K > K1 && pk.part_bytes > part) part = pk.part_bytes;
     if (M > M1 && pm.part_bytes > part) part = pm.part_bytes;
     if (N > N1 && pn.part_bytes > part) part = pn.part_bytes;
-    StreamScratch *sc;
+    ScratchLease sc;
     PCL_OK_OR_RETURN(get_scratch(s, part, abytes + bbytes + 256, &sc));
     float *Ac = const_cast<float *>(A), *Bc = const_cast<float *>(B);
     if (copy_a) {
@@ -743,7 +760,7 @@ int pcl_sgemm(int opA, int opB, int M, int N, int K, const float *A, int lda, co
         }
     }
     pcl::SgemmPlan p = pcl::plan_sgemm(M, N, K);
-    StreamScratch *sc;
+    ScratchLease sc;
     PCL_OK_OR_RETURN(get_scratch(s, p.part_bytes, 0, &sc));
     HIP_OK(pcl::launch_sgemm(p, opA == PCL_OP_N, opB == PCL_OP_T, M, N, K, A, lda, B, ldb, bias,
                              accumulate, C, ldc, sc->ws, s));
@@ -787,7 +804,7 @@ int pcl_sgemm_ex(int opA, int opB, int M, int N, int K, const float *A, int lda,
     PCL_OK_OR_RETURN(do_init());
     hipStream_t s = pick(stream);
     pcl::SgemmPlan p = pcl::plan_sgemm(M, N, K);
-    StreamScratch *sc;
+    ScratchLease sc;
     PCL_OK_OR_RETURN(get_scratch(s, p.part_bytes, 0, &sc));
     HIP_OK(pcl::launch_sgemm(p, opA == PCL_OP_N, opB == PCL_OP_T, M, N, K, A, lda, B, ldb, bias, 0,
                              C, ldc, sc->ws, s, epilogue, aux_in, epilogue == PCL_EPI_GELU ? aux_out : nullptr,
@@ -825,7 +842,7 @@ int pcl_bias_bwd(float *db, const float *dY, int M, int N, int ld, void *stream)
     PCL_OK_OR_RETURN(do_init());
     hipStream_t s = pick(stream);
     pcl::GemvPlan p = pcl::plan_bias_bwd(N, M);
-    StreamScratch *sc;
+    ScratchLease sc;
     PCL_OK_OR_RETURN(get_scratch(s, p.part_bytes, 0, &sc));
     HIP_OK(pcl::launch_sgemv(p, 0, 1, N, M, nullptr, 0, true, dY, ld, nullptr, 1, db, N, sc->ws, s));
     return PCL_OK;
@@ -904,7 +921,7 @@ int attn_bwd_common(const char *fn, float *dQ, float *dK, float *dV, int ld_grad
     hipStream_t s = pick(stream);
     float *dS = scratch;
     if (!dS) {
-        StreamScratch *sc;
+        ScratchLease sc;
         PCL_OK_OR_RETURN(get_scratch(s, sizeof(float) * (size_t)B * H * T * T, 0, &sc));
         dS = static_cast<float *>(sc->ws.buf);
     }
@@ -992,7 +1009,7 @@ static int igemm_common(int out_mode, const uint8_t *A, int lda, const int8_t *B
     }
     if (M <= 8) {
         pcl::GemvPlan p = pcl::plan_igemv(M, N, K);
-        StreamScratch *sc;
+        ScratchLease sc;
         PCL_OK_OR_RETURN(get_scratch(s, p.part_bytes, 0, &sc));
         HIP_OK(pcl::launch_igemv(p, out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa, sb, C, ldc,
                                  sc->ws, s));
@@ -1006,7 +1023,7 @@ static int igemm_common(int out_mode, const uint8_t *A, int lda, const int8_t *B
     // activations: copy A into a Kp-wide buffer padded with 0x80 (zero after
     // re-centring; the packed weights are zero past K as well).
     const int Kp = (int)ldb;
-    StreamScratch *sc;
+    ScratchLease sc;
     PCL_OK_OR_RETURN(get_scratch(s, 0, (size_t)M * Kp, &sc));
     uint8_t *Ap = (uint8_t *)sc->aux;
     HIP_OK(pcl::launch_pad_a_u8(A, lda, M, K, Ap, Kp, s));
@@ -1049,7 +1066,7 @@ int pcl_quantize_a_tensor(const float *A, int M, int K, uint8_t *Au, int Kpad, f
     CHECK_ARG(Au && scale_dev && (M * (long)K == 0 || A), "pcl_quantize_a_tensor: NULL operand");
     PCL_OK_OR_RETURN(do_init());
     hipStream_t s = pick(stream);
-    StreamScratch *sc;
+    ScratchLease sc;
     PCL_OK_OR_RETURN(get_scratch(s, 0, 0, &sc));
     HIP_OK(pcl::launch_quantize_a_tensor(A, M, K, Au, Kpad, scale_dev, sc->amax, s));
     return PCL_OK;
@@ -1418,7 +1435,7 @@ int pcl_cross_entropy(const float *logits, int ld, const int *targets, float *dl
               "pcl_cross_entropy: dlogits overlaps logits other than in place");
     PCL_OK_OR_RETURN(do_init());
     hipStream_t s = pick(stream);
-    StreamScratch *sc;
+    ScratchLease sc;
     PCL_OK_OR_RETURN(get_scratch(s, 0, sizeof(double) * (size_t)M, &sc));
     double *rl = static_cast<double *>(sc->aux);
     HIP_OK(pcl::launch_cross_entropy(logits, ld, targets, dlogits, ldd, M, V, V, M, rl, s));
@@ -1442,7 +1459,7 @@ int pcl_head_ce(const float *lnf, const float *wte, const int *targets, int M, i
     if (mc > M) mc = M;
     if (mc > 128) mc = mc / 128 * 128;
     const size_t loss_off = ((size_t)mc * row_bytes + 255) / 256 * 256;
-    StreamScratch *sc;
+    ScratchLease sc;
     PCL_OK_OR_RETURN(get_scratch(s, 0, loss_off + sizeof(double) * (size_t)M, &sc));
     float *lg = static_cast<float *>(sc->aux);
     double *rl = reinterpret_cast<double *>(static_cast<char *>(sc->aux) + loss_off);

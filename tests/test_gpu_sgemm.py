@@ -158,6 +158,40 @@ def test_sgemm_strided_leading_dims():
     assert np.all(C[:, N:] == 5.0)  # untouched padding columns
 
 
+def test_sgemm_host_threads_share_the_null_stream():
+    # two host threads call on their default (null) stream at once, with split-K
+    # grids of different sizes, so each call's workspace may have to grow while
+    # the other thread's call holds the stream's scratch
+    import threading
+    shapes = [(300, 500, 2000), (200, 260, 4096), (330, 520, 2048), (100, 700, 3000)]
+    cases = []
+    for i, (M, N, K) in enumerate(shapes):
+        A, B = ob.frand((M, K), 6000 + i), ob.frand((K, N), 6100 + i)
+        cases.append((A, B, ob.gemm_f64(A, B)))
+    errors = []
+
+    def worker(order):
+        try:
+            for _ in range(5):
+                for i in order:
+                    A, B, R = cases[i]
+                    (M, K), N = A.shape, B.shape[1]
+                    err = rel(sgemm(N_, N_, A, B, M, N, K), R)
+                    if err > FP32_TOL:
+                        errors.append((i, err))
+        except Exception as e:  # surfaced by the assert below
+            errors.append(repr(e))
+
+    announce("sgemm two host threads")
+    threads = [threading.Thread(target=worker, args=(o,)) for o in ([0, 1, 2, 3], [3, 2, 1, 0])]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=120)
+    assert not any(t.is_alive() for t in threads)
+    assert errors == []
+
+
 def test_sgemm_deterministic():
     M, N, K = 512, 512, 777
     A, B = _operands(N_, T_, M, N, K, 95)
