@@ -773,8 +773,9 @@ static hipError_t launch_dma(int M, int N, int K, int splits, int kchunk, const 
 // per CU (their barriers are independent, so a SIMD always has a second wave
 // to issue from).
 //
-// Tile: BM x BN per workgroup of 4 waves in a 2x2 grid; a wave owns
-// (BM/2) x (BN/2) as TM x TN blocks of 16x16. A ring stage holds BK = 16 SUB
+// Tile: BM x BN per workgroup of WM x WN waves (2 x 2 in every launch here;
+// OCC workgroups per CU size the LDS budget); a wave owns (BM/WM) x (BN/WN)
+// as TM x TN blocks of 16x16. A ring stage holds BK = 16 SUB
 // k (SUB = 1 or 2), used as SUB sub-steps of 16: lane (r16, q) = (lane % 16,
 // lane / 16) feeds k = 16u + 4q + s at MFMA step s of sub-step u (the same
 // for A and B, so the sum over k is unchanged) and holds outputs (4q + v,
