@@ -48,7 +48,7 @@ static int cdiv(long a, long b) { return (int)((a + b - 1) / b); }
 // 16-byte vectors (the chunk that straddles kvalid is assembled element by
 // element); otherwise single elements. RECENTRE: u8 activations are stored
 // as x ^ 0x80 (= x - 128 as s8), padding stays 0.
-template <int MR, bool RECENTRE, typename T>
+template <int MR, bool RECENTRE, typename T, int JUMAX = 16>
 __device__ __forceinline__ void stage_rows(T *xs, int ld, int kchunk, int kvalid, int M,
                                            const T *X0, long ldx) {
     typedef T vec_t __attribute__((ext_vector_type(16 / sizeof(T))));
@@ -61,7 +61,7 @@ __device__ __forceinline__ void stage_rows(T *xs, int ld, int kchunk, int kvalid
     const auto Xg = gbl(X0);
     const bool vec = ((reinterpret_cast<uintptr_t>(X0) | (uintptr_t)(ldx * sizeof(T))) & 15) == 0;
     if (vec) {
-        constexpr int JU = MR >= 16 ? 1 : 16 / MR;  // vector loads per row per round
+        constexpr int JU0 = MR >= 16 ? 1 : 16 / MR, JU = JU0 < JUMAX ? JU0 : JUMAX;  // vector loads per row per round
         const int nch = kchunk / V;                  // kchunk is a multiple of 64 elements
         for (int c0 = 0; c0 * GV_THREADS < nch; c0 += JU) {
             vec_t v[MR][JU];
@@ -93,7 +93,7 @@ __device__ __forceinline__ void stage_rows(T *xs, int ld, int kchunk, int kvalid
                 }
         }
     } else {
-        constexpr int JU = MR >= 16 ? 1 : 16 / MR;  // element loads per row per round
+        constexpr int JU0 = MR >= 16 ? 1 : 16 / MR, JU = JU0 < JUMAX ? JU0 : JUMAX;  // element loads per row per round
         for (int j0 = 0; j0 * GV_THREADS < kchunk; j0 += JU) {
             T v[MR][JU];
 #pragma unroll
@@ -1294,7 +1294,10 @@ __device__ __forceinline__ void gg_u8s8(const GgDesc &d, int strip, int8_t *lds)
     // the first slice is in flight while the activations are staged
     v4i wn[4];
     load(wn, 0);
-    stage_rows<MR, true>(reinterpret_cast<uint8_t *>(xs), xld, Kp, d.K, M, static_cast<const uint8_t *>(d.X), d.ldx);
+    // one 16-byte load per row per thread and round: rows up to 4 KB stage in one
+    // round, and the staging holds MR vector registers instead of 16
+    stage_rows<MR, true, uint8_t, 1>(reinterpret_cast<uint8_t *>(xs), xld, Kp, d.K, M,
+                                     static_cast<const uint8_t *>(d.X), d.ldx);
     __syncthreads();
     const int8_t *xr = xs + (ri % MR) * xld + 16 * g;
     v4i acc = {0, 0, 0, 0};
@@ -1336,6 +1339,18 @@ __global__ __launch_bounds__(GV_THREADS) void gemv_group_kernel(const GgDesc *__
     if (d.kind == GG_F32_N) gg_f32_n<MR>(d, it.y, reinterpret_cast<float *>(gv_dyn), red);
     else if (d.kind == GG_F32_T) gg_f32_t<MR>(d, it.y, reinterpret_cast<float *>(gv_dyn));
     else gg_u8s8<MR>(d, it.y, reinterpret_cast<int8_t *>(gv_dyn));
+}
+
+// A group whose products are all INT8: the same work items through the
+// matrix-core path alone, so the kernel holds only that path's registers
+// (58-86 against 124 for the kernel that also carries the fp32 paths) and a
+// SIMD takes five or more of its waves instead of four.
+template <int MR>
+__global__ __launch_bounds__(GV_THREADS) void gemv_group_u8s8_kernel(const GgDesc *__restrict__ descs,
+                                                                     const int2 *__restrict__ items) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char gv_dyn[];
+    const int2 it = items[blockIdx.x];
+    gg_u8s8<MR>(descs[it.x], it.y, reinterpret_cast<int8_t *>(gv_dyn));
 }
 
 // One product, descriptor by value (no device table): block b = strip b.
@@ -1388,9 +1403,18 @@ size_t gg_lds_bytes(int kind, int K, int mr) {
 }
 
 hipError_t launch_gemv_group(const GgDesc *descs, const int2 *items, int n_items, int mr,
-                             size_t lds_bytes, hipStream_t s) {
+                             size_t lds_bytes, bool all_u8s8, hipStream_t s) {
     if (n_items <= 0) return hipSuccess;
     const dim3 grid(n_items), block(GV_THREADS);
+    if (all_u8s8) {
+        switch (mr) {
+            case 1: hipLaunchKernelGGL(gemv_group_u8s8_kernel<1>, grid, block, lds_bytes, s, descs, items); break;
+            case 2: hipLaunchKernelGGL(gemv_group_u8s8_kernel<2>, grid, block, lds_bytes, s, descs, items); break;
+            case 4: hipLaunchKernelGGL(gemv_group_u8s8_kernel<4>, grid, block, lds_bytes, s, descs, items); break;
+            default: hipLaunchKernelGGL(gemv_group_u8s8_kernel<8>, grid, block, lds_bytes, s, descs, items); break;
+        }
+        return hipGetLastError();
+    }
     switch (mr) {
         case 1: hipLaunchKernelGGL(gemv_group_kernel<1>, grid, block, lds_bytes, s, descs, items); break;
         case 2: hipLaunchKernelGGL(gemv_group_kernel<2>, grid, block, lds_bytes, s, descs, items); break;

@@ -160,8 +160,9 @@ int gg_strip_rows(int kind);
 int gg_stage_ld(int kind, int K);
 // dynamic LDS a product needs in a group whose largest M rounds to mr
 size_t gg_lds_bytes(int kind, int K, int mr);
+// all_u8s8: every product is GG_U8S8 (a kernel with only that path)
 hipError_t launch_gemv_group(const GgDesc *descs, const int2 *items, int n_items, int mr,
-                             size_t lds_bytes, hipStream_t s);
+                             size_t lds_bytes, bool all_u8s8, hipStream_t s);
 // One INT8 GEMV (M <= 8 rows) on the matrix-core path of the grouped kernel:
 // whole-K blocks of 64 weight rows, no split, no workspace. Applicable when
 // igemv_mfma_fits (32-bit row offsets, packed rows ldb >= roundup(K, 256),

@@ -297,6 +297,7 @@ struct pcl_gemv_group {
     pcl::GgDesc *d_descs = nullptr;
     int2 *d_items = nullptr;
     int n_items = 0, mr = 1;
+    bool all_u8s8 = false;
     size_t lds = 0;
 };
 
@@ -606,6 +607,7 @@ int pcl_gemv_group_create(const pcl_gemv_desc *descs, int n, pcl_gemv_group **gr
     g->n_items = (int)it.size();
     g->mr = mr;
     g->lds = lds;
+    g->all_u8s8 = std::all_of(dd.begin(), dd.end(), [](const pcl::GgDesc &q) { return q.kind == pcl::GG_U8S8; });
     if (hipMalloc((void **)&g->d_descs, sizeof(pcl::GgDesc) * dd.size()) != hipSuccess ||
         hipMalloc((void **)&g->d_items, sizeof(int2) * it.size()) != hipSuccess) {
         pcl_gemv_group_free(g);
@@ -624,7 +626,7 @@ int pcl_gemv_group_run(const pcl_gemv_group *group, void *stream) {
     CHECK_ARG(group != nullptr, "pcl_gemv_group_run: group is NULL");
     PCL_OK_OR_RETURN(do_init());
     HIP_OK(pcl::launch_gemv_group(group->d_descs, group->d_items, group->n_items, group->mr, group->lds,
-                                  pick(stream)));
+                                  group->all_u8s8, pick(stream)));
     return PCL_OK;
 }
 
