@@ -43,12 +43,14 @@ static int cdiv(long a, long b) { return (int)((a + b - 1) / b); }
 // Stage MR activation rows of one split (elements [0, kchunk) of row m start
 // at X0 + m*ldx; elements at or past kvalid, and rows m >= M, stage as zero)
 // into LDS rows of stride ld. Each thread issues up to 16 independent loads
-// before it writes any of them, so the staging costs one memory latency
-// rather than one per element. With 16-byte aligned rows the loads are
+// (at most JUMAX per row) before it writes any of them, so the staging costs
+// one memory latency rather than one per element; JUMAX caps the registers
+// the batch holds (16 16-byte loads take 64 of them, which set the
+// occupancy of the GEMVs with one or two rows). With 16-byte aligned rows the loads are
 // 16-byte vectors (the chunk that straddles kvalid is assembled element by
 // element); otherwise single elements. RECENTRE: u8 activations are stored
 // as x ^ 0x80 (= x - 128 as s8), padding stays 0.
-template <int MR, bool RECENTRE, typename T, int JUMAX = 16>
+template <int MR, bool RECENTRE, typename T, int JUMAX = 4>
 __device__ __forceinline__ void stage_rows(T *xs, int ld, int kchunk, int kvalid, int M,
                                            const T *X0, long ldx) {
     typedef T vec_t __attribute__((ext_vector_type(16 / sizeof(T))));
@@ -1109,7 +1111,7 @@ __device__ __forceinline__ void gg_f32_n(const GgDesc &d, int strip, float *xs, 
     };
     v4f wn[UR];
     load_batch(wn, 0);
-    stage_rows<MR, false>(xs, ld, ld, K, M, static_cast<const float *>(d.X), d.ldx);
+    stage_rows<MR, false, float, 16>(xs, ld, ld, K, M, static_cast<const float *>(d.X), d.ldx);
     __syncthreads();
 
     float acc[MR][4];
@@ -1185,7 +1187,7 @@ __device__ __forceinline__ void gg_f32_t(const GgDesc &d, int strip, float *xs) 
     };
     v4f wn[UK][RPL];
     load_batch(wn, 4 * j);
-    stage_rows<MR, false>(xs, ld, ld, K, M, static_cast<const float *>(d.X), d.ldx);
+    stage_rows<MR, false, float, 16>(xs, ld, ld, K, M, static_cast<const float *>(d.X), d.ldx);
     __syncthreads();
 
     float acc[RPL][MR];
