@@ -63,8 +63,41 @@ __device__ __forceinline__ void stage_rows(T *xs, int ld, int kchunk, int kvalid
     const auto Xg = gbl(X0);
     const bool vec = ((reinterpret_cast<uintptr_t>(X0) | (uintptr_t)(ldx * sizeof(T))) & 15) == 0;
     if (vec) {
-        constexpr int JU0 = MR >= 16 ? 1 : 16 / MR, JU = JU0 < JUMAX ? JU0 : JUMAX;  // vector loads per row per round
         const int nch = kchunk / V;                  // kchunk is a multiple of 64 elements
+        if (MR > 1 && nch < GV_THREADS) {
+            // Rows shorter than one chunk per thread: thread t takes chunk t % nch
+            // of rows t / nch, t / nch + rp, ... (rp rows side by side), so every
+            // wave shares the loads instead of the first nch threads holding
+            // MR each while the others wait at the block's barrier.
+            const int rp = GV_THREADS / nch, m0 = tid / nch, kk = (tid - m0 * nch) * V;
+            if (m0 < rp) {
+                vec_t v[MR];
+#pragma unroll
+                for (int s = 0; s < MR; s++) {
+                    const int m = m0 + s * rp;
+                    vec_t x = (T)0;
+                    if (m < M) {
+                        const auto src = Xg + (long)m * ldx + kk;
+                        if (kk + V <= kvalid) {
+                            x = *gvec<vec_t>(src);
+                            if constexpr (RECENTRE) x ^= (T)0x80;
+                        } else {
+#pragma unroll
+                            for (int e = 0; e < V; e++)
+                                if (kk + e < kvalid) x[e] = fix(src[e]);
+                        }
+                    }
+                    v[s] = x;
+                }
+#pragma unroll
+                for (int s = 0; s < MR; s++) {
+                    const int m = m0 + s * rp;
+                    if (m < MR) *reinterpret_cast<vec_t *>(xs + m * ld + kk) = v[s];
+                }
+            }
+            return;
+        }
+        constexpr int JU0 = MR >= 16 ? 1 : 16 / MR, JU = JU0 < JUMAX ? JU0 : JUMAX;  // vector loads per row per round
         for (int c0 = 0; c0 * GV_THREADS < nch; c0 += JU) {
             vec_t v[MR][JU];
 #pragma unroll
@@ -415,6 +448,34 @@ __device__ __forceinline__ void igemv_write(void *Yv, long ldy, int m, int n, in
     } else {
         const float dq = (OUT == 2) ? gbl(sa)[m] * gbl(sb)[n] : gbl(sb)[n];
         gbl(reinterpret_cast<float *>(Yv))[(long)m * ldy + n] = (float)v * dq;
+    }
+}
+
+// Outputs n .. n+3 of row m (n + 3 < N) in one 16-byte store, each value as
+// igemv_write gives it. The store is only 4-byte aligned when ldy is not a
+// multiple of 4 (a vocabulary-wide logits row); global accesses on this target
+// may be unaligned, and the compiler still emits one dwordx4 store.
+template <int OUT>
+__device__ __forceinline__ void igemv_write4(void *Yv, long ldy, int m, int n, v4i v,
+                                             const int32_t *col_off, const float *sa,
+                                             const float *sb) {
+    typedef int32_t v4i_u __attribute__((ext_vector_type(4), aligned(4)));
+    typedef float v4f_u __attribute__((ext_vector_type(4), aligned(4)));
+    v4i_u r;
+#pragma unroll
+    for (int e = 0; e < 4; e++) r[e] = epi_int(v[e], col_off, n + e);
+    if (OUT == 0) {
+        *reinterpret_cast<__attribute__((address_space(1))) v4i_u *>(
+            gbl(reinterpret_cast<int32_t *>(Yv)) + (long)m * ldy + n) = r;
+    } else {
+        v4f_u f;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const float dq = (OUT == 2) ? gbl(sa)[m] * gbl(sb)[n + e] : gbl(sb)[n + e];
+            f[e] = (float)r[e] * dq;
+        }
+        *reinterpret_cast<__attribute__((address_space(1))) v4f_u *>(
+            gbl(reinterpret_cast<float *>(Yv)) + (long)m * ldy + n) = f;
     }
 }
 
@@ -1317,15 +1378,22 @@ __device__ __forceinline__ void gg_u8s8(const GgDesc &d, int strip, int8_t *lds)
             acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc, 0, 0, 0);
         }
     }
-    const int m = lane & 15;
+    // a lane's four results are outputs nb .. nb+3 of row m: one 16-byte store
+    const int m = lane & 15, nb = n0 + 16 * wv + 4 * g;
     if (m < M) {
+        if (nb + 4 <= N) {
+            if (d.out_mode == 0) igemv_write4<0>(d.Y, d.ldy, m, nb, acc, d.col_off, d.sa, d.sb);
+            else if (d.out_mode == 1) igemv_write4<1>(d.Y, d.ldy, m, nb, acc, d.col_off, d.sa, d.sb);
+            else igemv_write4<2>(d.Y, d.ldy, m, nb, acc, d.col_off, d.sa, d.sb);
+        } else {
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int n = n0 + 16 * wv + 4 * g + r;
-            if (n < N) {
-                if (d.out_mode == 0) igemv_write<0>(d.Y, d.ldy, m, n, acc[r], d.col_off, d.sa, d.sb);
-                else if (d.out_mode == 1) igemv_write<1>(d.Y, d.ldy, m, n, acc[r], d.col_off, d.sa, d.sb);
-                else igemv_write<2>(d.Y, d.ldy, m, n, acc[r], d.col_off, d.sa, d.sb);
+            for (int r = 0; r < 4; r++) {
+                const int n = nb + r;
+                if (n < N) {
+                    if (d.out_mode == 0) igemv_write<0>(d.Y, d.ldy, m, n, acc[r], d.col_off, d.sa, d.sb);
+                    else if (d.out_mode == 1) igemv_write<1>(d.Y, d.ldy, m, n, acc[r], d.col_off, d.sa, d.sb);
+                    else igemv_write<2>(d.Y, d.ldy, m, n, acc[r], d.col_off, d.sa, d.sb);
+                }
             }
         }
     }
