@@ -1207,14 +1207,18 @@ SgemmPlan plan_sgemm(int M, int N, int K) {
 
 // Grids of at least two workgroups per CU take the 16x16x4 kernel (its
 // workgroups pair up on a CU): 1 = 128x128 tiles, 2 = 128x64 tiles (grids that
-// have only one 128x128 tile per CU), 0 = the 32x32x2 kernel (smaller grids,
-// where its two K groups keep two waves on every SIMD). Measured on the
-// 350M-class shapes in one run: 128x128 +8-11% where it applies, 128x64 +1-11%.
+// have only one 128x128 tile per CU), 3 = 64x64 tiles (two per CU only at that
+// size, e.g. 2048 x 1024), 0 = the 32x32x2 kernel (smaller grids, where its two
+// K groups keep two waves on every SIMD). Measured on the 350M-class shapes in
+// one run: 128x128 +8-11% where it applies, 128x64 +1-11%; 64x64 on
+// 2048 x 1024 x 1024: +11% (with one 64x64 tile per CU, 1024^3, it is not ahead).
 static int s16_tile(int M, int N) {
     const long t128 = (long)((M + 127) / 128) * ((N + 127) / 128);
     const long t64 = (long)((M + 127) / 128) * ((N + 63) / 64);
+    const long t6464 = (long)((M + 63) / 64) * ((N + 63) / 64);
     if (t128 >= 512) return 1;
     if (t64 >= 512) return 2;
+    if (t6464 >= 512) return 3;
     return 0;
 }
 
@@ -1238,6 +1242,9 @@ static hipError_t launch_dma_epi(const SgemmPlan &p, int M, int N, int K, const 
     if (s16 == 2)
         return launch_s16<128, 64, 3, 2, A_KC, B_KC, EPI>(M, N, K, 1, K, A, lda, B, ldb, bias, 0, C, ldc,
                                                         stream, aux_in, aux_out, ld_aux);
+    if (s16 == 3)
+        return launch_s16<64, 64, 4, 1, A_KC, B_KC, EPI>(M, N, K, 1, K, A, lda, B, ldb, bias, 0, C, ldc,
+                                                       stream, aux_in, aux_out, ld_aux);
     if (p.cfg == SG_64_KG2)
         return launch_dma<64, 64, 2, 2, 1, A_KC, B_KC, EPI>(M, N, K, 1, K, A, lda, B, ldb, bias, 0, C,
                                                             ldc, stream, aux_in, aux_out, ld_aux);
@@ -1294,6 +1301,8 @@ static hipError_t dispatch_layout(const SgemmPlan &p, int M, int N, int K, const
         e = launch_s16<128, 128, 4, 1, A_KC, B_KC>(M, N, K, 1, K, A, lda, B, ldb, b, acc, out, ldo, stream);
     } else if (dma_ok && s16 == 2) {
         e = launch_s16<128, 64, 3, 2, A_KC, B_KC>(M, N, K, 1, K, A, lda, B, ldb, b, acc, out, ldo, stream);
+    } else if (dma_ok && s16 == 3) {
+        e = launch_s16<64, 64, 4, 1, A_KC, B_KC>(M, N, K, 1, K, A, lda, B, ldb, b, acc, out, ldo, stream);
     } else if (dma_ok) {
         if (p.cfg == SG_64_KG2)
             e = launch_dma<64, 64, 2, 2, 1, A_KC, B_KC>(M, N, K, p.splits, p.kchunk, A, lda, B, ldb, b,
