@@ -421,6 +421,11 @@ CASES = {
     "gemv_head_int8_m1": lambda pcl, lib, w, s: gemv(pcl, lib, 2, 1, [(1024, 50257)], 6, w, s),
     "gemv_head_fp32_m8": lambda pcl, lib, w, s: gemv(pcl, lib, 1, 8, [(1024, 50257)], 3, w, s),
     "gemv_head_int8_m8": lambda pcl, lib, w, s: gemv(pcl, lib, 2, 8, [(1024, 50257)], 6, w, s),
+    "gemv_head_int8_m2": lambda pcl, lib, w, s: gemv(pcl, lib, 2, 2, [(1024, 50257)], 6, w, s),
+    "gemv_head_int8_m3": lambda pcl, lib, w, s: gemv(pcl, lib, 2, 3, [(1024, 50257)], 6, w, s),
+    "gemv_head_int8_m4": lambda pcl, lib, w, s: gemv(pcl, lib, 2, 4, [(1024, 50257)], 6, w, s),
+    "decode_int8_m1": lambda pcl, lib, w, s: gemv(pcl, lib, 2, 1, DECODE_LAYER * 16 + [(512, 2048)], 11, w, s),
+    "decode_int8_m4": lambda pcl, lib, w, s: gemv(pcl, lib, 2, 4, DECODE_LAYER * 16 + [(512, 2048)], 11, w, s),
     "decode_fp32_m1": lambda pcl, lib, w, s: gemv(pcl, lib, [0] * 64 + [1], 1, DECODE_LAYER * 16 + [(512, 2048)],
                                                    3, w, s),
     "decode_group_fp32_m1": lambda pcl, lib, w, s: gemv_group(pcl, lib, [0] * 64 + [1], 1,

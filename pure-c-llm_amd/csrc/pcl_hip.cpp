@@ -1001,11 +1001,11 @@ static int igemm_common(int out_mode, const uint8_t *A, int lda, const int8_t *B
     PCL_OK_OR_RETURN(do_init());
     const long ldb = kpad256(K);
     hipStream_t s = pick(stream);
-    // Decode rows: with 4-8 rows the matrix-core GEMV (one MFMA per 64 bytes
+    // Decode rows: with 3-8 rows the matrix-core GEMV (one MFMA per 64 bytes
     // of 16 weight rows, coalesced loads) beats the dot-product kernel, whose
-    // per-row work grows with M; with 1-2 rows the dot-product kernel streams
-    // slightly faster.
-    if (M >= 4 && M <= 8 && K > 0 && pcl::igemv_mfma_fits(M, N, K, ldb)) {
+    // per-row work grows with M (3 rows run its 4-row form: +10% on the 350M
+    // head); with 1-2 rows the dot-product kernel streams 2-4% faster.
+    if (M >= 3 && M <= 8 && K > 0 && pcl::igemv_mfma_fits(M, N, K, ldb)) {
         HIP_OK(pcl::launch_igemv_mfma(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa, sb, C, ldc, s));
         return PCL_OK;
     }

@@ -93,7 +93,7 @@ def test_igemv_i32_exact(M):
         np.testing.assert_array_equal(igemm_i32(Au, Bq, gemv=True), ob.gemm_u8s8_i32(Au, Bq))
 
 
-@pytest.mark.parametrize("M", [4, 5, 8])
+@pytest.mark.parametrize("M", [3, 4, 5, 8])
 def test_igemv_wide_exact(M):
     # several activation rows against a wide N: the 350M head, a K that is a
     # multiple of 16 but not of 32, and a short K
@@ -104,8 +104,11 @@ def test_igemv_wide_exact(M):
         np.testing.assert_array_equal(igemm_i32(Au, Bq, gemv=True), ob.gemm_u8s8_i32(Au, Bq))
 
 
-def test_igemv_wide_dequant_bit_exact():
-    M, N, K = 8, 9000, 1024
+@pytest.mark.parametrize("M,N", [(8, 9000), (8, 9001), (3, 9001)])
+def test_igemv_wide_dequant_bit_exact(M, N):
+    # the matrix-core GEMV stores a lane's four adjacent outputs with one 16-byte
+    # store; an odd N leaves every output row but the first misaligned
+    K = 1024
     Au = ob.u8((M, K), 140)
     Bq = ob.s8((K, N), 141)
     sa = ob.uniform((M,), 142, 1e-3, 1e-2)
