@@ -826,17 +826,22 @@ __global__ __launch_bounds__(GV_THREADS) void igemv_q_kernel(
     load_batch(wn, 16 * j);  // in flight while the row is made
 
     if constexpr (QX == QX_LN) {
+        // the row is read once into LDS; each thread revisits only its own elements
         float s0 = 0.f;
-        for (int i = tid; i < K; i += 256) s0 += X[i];
+        for (int i = tid; i < K; i += 256) {
+            const float v = X[i];
+            xf[i] = v;
+            s0 += v;
+        }
         const float mu = gv_sum4(s0, red) / K;
         float q = 0.f;
         for (int i = tid; i < K; i += 256) {
-            const float d = X[i] - mu;
+            const float d = xf[i] - mu;
             q += d * d;
         }
         const float var = gv_sum4(q, red) / K;
         const float rsd = 1.0f / sqrtf(var + 1e-5f);
-        for (int i = tid; i < K; i += 256) xf[i] = (X[i] - mu) * rsd * g[i] + b[i];
+        for (int i = tid; i < K; i += 256) xf[i] = (xf[i] - mu) * rsd * g[i] + b[i];
     } else if constexpr (QX == QX_BIAS_GELU) {
         for (int i = tid; i < K; i += 256) {
             const float v = X[i] + b[i];
@@ -976,17 +981,22 @@ __global__ __launch_bounds__(GV_THREADS) void sgemv_q_kernel(
     load_batch(wn, 4 * j);  // in flight while the row is made
 
     if constexpr (QX == QX_LN) {
+        // the row is read once into LDS; each thread revisits only its own elements
         float s0 = 0.f;
-        for (int i = tid; i < K; i += 256) s0 += X[i];
+        for (int i = tid; i < K; i += 256) {
+            const float v = X[i];
+            xf[i] = v;
+            s0 += v;
+        }
         const float mu = gv_sum4(s0, red) / K;
         float q = 0.f;
         for (int i = tid; i < K; i += 256) {
-            const float d = X[i] - mu;
+            const float d = xf[i] - mu;
             q += d * d;
         }
         const float var = gv_sum4(q, red) / K;
         const float rsd = 1.0f / sqrtf(var + 1e-5f);
-        for (int i = tid; i < K; i += 256) xf[i] = (X[i] - mu) * rsd * g[i] + b[i];
+        for (int i = tid; i < K; i += 256) xf[i] = (xf[i] - mu) * rsd * g[i] + b[i];
     } else if constexpr (QX == QX_BIAS_GELU) {
         for (int i = tid; i < K; i += 256) {
             const float v = X[i] + b[i];
