@@ -361,10 +361,11 @@ int pcl_gemv_u8s8_dq(const uint8_t *X, int ldx, const int8_t *Bpk, const int32_t
 /* ---- measured roofs: gemm_bench's measure_peak_int8_gops (gemm_bench.c:287-301),
  * measure_peak_gflops (:309-325) and measure_bandwidth_gbs (:195-210) on the GPU.
  * Sustained matrix-core rate with the operands held in registers (eight waves
- * per CU, four independent accumulators each): data 0 = i8 MFMA on uniformly
- * random bytes (the gemm_bench INT8 data; the clock drops with the operands'
- * switching), 1 = i8 on zeros, 2 = f32 MFMA on uniform random floats. *rate in
- * TOP/s (i8) or TFLOP/s (f32); best of 5 launches. */
+ * per CU; four independent 32x32x32 accumulators each for i8, eight 16x16x4
+ * for f32): data 0 = i8 MFMA on uniformly random bytes (the gemm_bench INT8
+ * data; the clock drops with the operands' switching), 1 = i8 on zeros, 2 = f32
+ * MFMA on uniform random floats. *rate in TOP/s (i8) or TFLOP/s (f32); best of 5
+ * launches after 30 warm-up launches. */
 int pcl_measure_peak_mfma(int data, double *rate);
 /* HBM over arrays of bytes_per_array (at least 64 MiB; use > 256 MB to leave
  * the Infinity Cache), 16-byte non-temporal accesses, best of 5, in GB/s:

@@ -5,12 +5,14 @@
 // on; these do the same for the matrix cores and HBM, so a kernel's fraction
 // can be read against what the part sustains as well as its datasheet peak.
 //
-// Matrix cores: every CU runs eight waves (two per SIMD), each holding four
-// independent 32x32 accumulators and its operands in registers, so nothing
-// but the MFMA pipe is exercised. The MI355X lowers its shader clock with the
+// Matrix cores: every CU runs eight waves (two per SIMD), each holding
+// independent accumulators (four 32x32 for i8, eight 16x16 for f32: the
+// instructions the GEMMs use) and its operands in registers, so nothing but
+// the MFMA pipe is exercised. The MI355X lowers its shader clock with the
 // switching activity of the operands, so the rate is measured for the data a
 // GEMM sees: uniformly random bytes (the gemm_bench INT8 workload) or zeros
-// for i8, uniform random floats for f32.
+// for i8, uniform random floats for f32. Thirty warm-up launches (10-20 ms of
+// load) bring the clock up first: a short run from idle reads 5-15% low.
 //
 // HBM: the triad a[i] = b[i] + s*c[i] over arrays far larger than the 256 MB
 // Infinity Cache, a copy, a read-only and a write-only pass, with 16-byte
@@ -23,10 +25,10 @@ namespace pcl {
 typedef int rf_v4i __attribute__((ext_vector_type(4)));
 typedef int rf_v16i __attribute__((ext_vector_type(16)));
 typedef float rf_v4f __attribute__((ext_vector_type(4)));
-typedef float rf_v16f __attribute__((ext_vector_type(16)));
 
 constexpr int RF_WAVES = 8;     // per CU: two per SIMD
-constexpr int RF_ITERS = 2048;  // four MFMAs each
+constexpr int RF_ITERS = 4096;  // four i8 or eight f32 MFMAs each
+constexpr int RF_F32_CHAINS = 8;
 
 __device__ __forceinline__ unsigned rf_next(unsigned &s) {
     s ^= s << 13;
@@ -71,32 +73,26 @@ __global__ __launch_bounds__(64 * RF_WAVES) void roof_i8_kernel(int *out, unsign
 
 __global__ __launch_bounds__(64 * RF_WAVES) void roof_f32_kernel(float *out, unsigned seed) {
     unsigned s = seed ^ (threadIdx.x * 2654435761u) ^ (blockIdx.x * 40503u) ^ 1u;
-    float a[2], b[2];
+    float a[4], b[4];
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
+    for (int i = 0; i < 4; i++) {
         a[i] = (float)(rf_next(s) >> 8) * (1.0f / 16777216.0f) - 0.5f;
         b[i] = (float)(rf_next(s) >> 8) * (1.0f / 16777216.0f) - 0.5f;
     }
-    rf_v16f acc[2][2];
+    rf_v4f acc[RF_F32_CHAINS];
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < RF_F32_CHAINS; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++)
-#pragma unroll
-            for (int v = 0; v < 16; v++) acc[i][j][v] = 0.f;
+        for (int v = 0; v < 4; v++) acc[i][v] = 0.f;
     for (int it = 0; it < RF_ITERS; it++)
 #pragma unroll
-        for (int j = 0; j < 2; j++)
-#pragma unroll
-            for (int i = 0; i < 2; i++)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
+        for (int i = 0; i < RF_F32_CHAINS; i++)
+            acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i & 3], b[(i >> 2) & 3], acc[i], 0, 0, 0);
     float t = 0.f;
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < RF_F32_CHAINS; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++)
-#pragma unroll
-            for (int v = 0; v < 16; v++) t += acc[i][j][v];
+        for (int v = 0; v < 4; v++) t += acc[i][v];
     out[blockIdx.x * blockDim.x + threadIdx.x] = t;
 }
 
@@ -181,12 +177,13 @@ hipError_t measure_peak_mfma(int kind, int cus, double *rate, hipStream_t s) {
         else if (kind == 1) hipLaunchKernelGGL(roof_i8_kernel<false>, grid, block, 0, s, (int *)out, seed);
         else hipLaunchKernelGGL(roof_f32_kernel, grid, block, 0, s, (float *)out, seed);
     };
-    launch();  // warm-up (clock ramp, code load)
+    for (int w = 0; w < 30; w++) launch();  // warm-up: 10-20 ms of load brings the clock up
     float ms = 0.f;
     err = best_ms(launch, 5, s, &ms);
     if (err == hipSuccess) {
-        const double per_mfma = kind == 2 ? 32.0 * 32 * 2 * 2 : 32.0 * 32 * 32 * 2;
-        const double ops = (double)cus * RF_WAVES * RF_ITERS * 4 * per_mfma;
+        // ops per wave per iteration: four 32x32x32 i8 or eight 16x16x4 f32 MFMAs
+        const double per_iter = kind == 2 ? RF_F32_CHAINS * 16.0 * 16 * 4 * 2 : 4 * 32.0 * 32 * 32 * 2;
+        const double ops = (double)cus * RF_WAVES * RF_ITERS * per_iter;
         *rate = ops / (ms * 1e-3) / 1e12;
     }
     (void)hipFree(out);
