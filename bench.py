@@ -572,7 +572,8 @@ def main():
         "config": {"workload": "gemm_bench INT8 GEMM M=N=K=2048, u8 x s8 -> int32, per-row x per-column dequant "
                                "to fp32 (BASELINE.json configs[1])",
                    "M": M, "N": N, "K": K, "kernel": "igemm_wp_kernel (producer/consumer waves, v_mfma_i32_32x32x32_i8)",
-                   "parallelism": "single GPU"},
+                   "parallelism": "single GPU",
+                   "warmup_min_ms": 20},
         "roofline": {"bound": "mfma", "achieved": tops, "peak": PEAK_I8_TOPS, "unit": "TOP/s",
                      "frac": round(tops / PEAK_I8_TOPS, 4), "traffic": read_traffic(),
                      "trace_kernel_us": read_trace_us(),

@@ -12,10 +12,12 @@
  *
  * Built into libpcl_bench.so (see ../Makefile); only bench.py loads it.
  */
+#define _POSIX_C_SOURCE 199309L /* clock_gettime */
 #include <stdint.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <time.h>
 
 #include "pcl_hip.h"
 
@@ -82,12 +84,37 @@ static void *dev_bytes(size_t n, uint32_t seed) {
 typedef int (*step_fn)(void *ctx, int i);
 
 /* warmup + timed loop shared by every benchmark */
+/* Untimed warm-up: the `warmup` steps asked for, then more until the part has
+ * been busy for at least WARM_MIN_MS. An MI355X brought out of idle (or out of
+ * the host-side set-up between two measurements) raises its clock over ~10-20 ms
+ * of load; steps timed before that read 5-15% slow. *next = the index of the
+ * first timed step (weight copies keep rotating through the warm-up). */
+#define WARM_MIN_MS 20.0
+static double now_ms(void) {
+    struct timespec t;
+    clock_gettime(CLOCK_MONOTONIC, &t);
+    return (double)t.tv_sec * 1e3 + (double)t.tv_nsec * 1e-6;
+}
+
+static int warm_up(step_fn fn, void *ctx, int warmup, int *next) {
+    int rc = PCL_OK, i = 0;
+    const double t0 = now_ms();
+    for (; i < warmup; i++) TRY(fn(ctx, i));
+    TRY(pcl_stream_synchronize());
+    while (now_ms() - t0 < WARM_MIN_MS) {
+        for (int j = 0; j < 8; j++, i++) TRY(fn(ctx, i));
+        TRY(pcl_stream_synchronize());
+    }
+done:
+    *next = i;
+    return rc;
+}
+
 static int time_steps(step_fn fn, void *ctx, int warmup, int steps, double *ms_total) {
-    int rc = PCL_OK;
+    int rc = PCL_OK, first = 0;
     void *e0 = NULL, *e1 = NULL;
     float ms = 0.f;
-    for (int i = 0; i < warmup; i++) TRY(fn(ctx, i));
-    TRY(pcl_stream_synchronize());
+    TRY(warm_up(fn, ctx, warmup, &first));
     e0 = pcl_event_create();
     e1 = pcl_event_create();
     if (!e0 || !e1) {
@@ -95,7 +122,7 @@ static int time_steps(step_fn fn, void *ctx, int warmup, int steps, double *ms_t
         goto done;
     }
     TRY(pcl_event_record(e0));
-    for (int i = 0; i < steps; i++) TRY(fn(ctx, warmup + i));
+    for (int i = 0; i < steps; i++) TRY(fn(ctx, first + i));
     TRY(pcl_event_record(e1));
     TRY(pcl_event_elapsed_ms(e0, e1, &ms));
     TRY(pcl_stream_synchronize());
@@ -110,11 +137,11 @@ done:
  * stream right before and after the step's launch): the average duration of
  * one launch as a kernel trace sees it, without the gaps between launches. */
 static int time_each(step_fn fn, void *ctx, int warmup, int steps, double *us_avg) {
-    int rc = PCL_OK;
+    int rc = PCL_OK, first = 0;
     void **ev = calloc((size_t)2 * steps, sizeof(void *));
     double tot = 0;
     if (!ev) return PCL_ERR_OOM;
-    for (int i = 0; i < warmup; i++) TRY(fn(ctx, i));
+    TRY(warm_up(fn, ctx, warmup, &first));
     for (int i = 0; i < 2 * steps; i++)
         if (!(ev[i] = pcl_event_create())) {
             rc = PCL_ERR_HIP;
@@ -123,7 +150,7 @@ static int time_each(step_fn fn, void *ctx, int warmup, int steps, double *us_av
     TRY(pcl_stream_synchronize());
     for (int i = 0; i < steps; i++) {
         TRY(pcl_event_record(ev[2 * i]));
-        TRY(fn(ctx, warmup + i));
+        TRY(fn(ctx, first + i));
         TRY(pcl_event_record(ev[2 * i + 1]));
     }
     TRY(pcl_stream_synchronize());
