@@ -12,7 +12,8 @@
 // libpcl_hip) -> int32, and libpcl_hip's dequantised fp32 form beside it.
 // FP32: C = A . B^T with B stored N x K (the same operand layout), fp32
 // inputs uniform in [-1, 1], checked against a double-precision sum on four
-// rows. Each rate is the best of 3 runs of 20 back-to-back calls.
+// rows. Each rate is the best of 3 runs of 20 back-to-back calls, after 20 ms of untimed calls.
+#include <chrono>
 #include <hip/hip_runtime.h>
 #include <hipblaslt/hipblaslt.h>
 
@@ -41,13 +42,19 @@ __global__ void yard_fill(unsigned *p, size_t n, unsigned seed, int f32) {
     }
 }
 
+// Each measurement first keeps the part busy for 20 ms (untimed): the clock
+// rises over ~10-20 ms of load, and a rate timed before that reads 5-15% low,
+// whichever library happens to run first.
 template <typename F>
 static double best_ms(F f) {
     hipEvent_t e0, e1;
     CK(hipEventCreate(&e0));
     CK(hipEventCreate(&e1));
-    f();
-    CK(hipDeviceSynchronize());
+    const auto t0 = std::chrono::steady_clock::now();
+    do {
+        for (int i = 0; i < 4; i++) f();
+        CK(hipDeviceSynchronize());
+    } while (std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count() < 20.0);
     double best = 1e30;
     for (int r = 0; r < 3; r++) {
         CK(hipEventRecord(e0, 0));
