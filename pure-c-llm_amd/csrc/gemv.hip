@@ -959,10 +959,13 @@ __global__ __launch_bounds__(GV_THREADS) void sgemv_q_kernel(
     const float *__restrict__ W, long ldw, const float *__restrict__ bias, float *__restrict__ Y,
     int N) {
     static_assert(GV_THREADS == 256, "the reductions assume four waves");
-    constexpr int RPL = 2, RG = GV_THREADS / LPR, RPB = RG * RPL;
+    // LPR 128 / 256: a row spans two / four waves (the products with few rows
+    // spread over more workgroups); the wave sums are added through LDS in wave order
+    static_assert(LPR == 16 || LPR == 32 || LPR == 64 || LPR == 128 || LPR == 256, "lanes per row");
+    constexpr int RPL = 2, RG = GV_THREADS / LPR, RPB = RG * RPL, LW = LPR < 64 ? LPR : 64;
     extern __shared__ __attribute__((aligned(16))) unsigned char gv_dyn[];
     float *xf = reinterpret_cast<float *>(gv_dyn);  // [K]
-    __shared__ float red[4], res[RPB];
+    __shared__ float red[4], res[RPB], wsum[LPR > 64 ? 4 : 1][RPL];
 
     const int tid = threadIdx.x;
     const int j = tid % LPR, rs = tid / LPR;
@@ -1031,8 +1034,23 @@ __global__ __launch_bounds__(GV_THREADS) void sgemv_q_kernel(
     for (int r = 0; r < RPL; r++) {
         float v = acc[r];
 #pragma unroll
-        for (int o = LPR / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, LPR);
-        if (j == 0) res[rs + RG * r] = v;
+        for (int o = LW / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, LW);
+        if constexpr (LPR > 64) {
+            if ((tid & 63) == 0) wsum[tid >> 6][r] = v;
+        } else {
+            if (j == 0) res[rs + RG * r] = v;
+        }
+    }
+    if constexpr (LPR > 64) {
+        // row rs + RG*r of the block: waves rs*(LPR/64) .. +LPR/64-1, added in order
+        __syncthreads();
+        if (tid < RPB) {
+            const int g0 = tid % RG, r = tid / RG;
+            float v = 0.f;
+#pragma unroll
+            for (int w = 0; w < LPR / 64; w++) v += wsum[g0 * (LPR / 64) + w][r];
+            res[tid] = v;
+        }
     }
     __syncthreads();
     if (tid < RPB) {
@@ -1053,7 +1071,16 @@ static void launch_sgemv_q_shape(const float *X, const float *g, const float *b,
 #define SGQ(LPRV, UKV)                                                                       \
     hipLaunchKernelGGL((sgemv_q_kernel<QX, EPI, LPRV, UKV>), dim3((unsigned)cdiv(N, 512 / LPRV)), \
                        block, lds, s, X, g, b, K, W, (long)K, bias, Y, N)
-    if (K <= 64) SGQ(16, 1);
+    // Products with few rows (N <= 1024: at most 128 workgroups of 8 rows)
+    // spread each row over two or four waves instead: 2-4 rows per workgroup,
+    // 256-512 workgroups.
+    if (N <= 1024 && K >= 1024) {
+        if (K <= 1024) SGQ(256, 1);
+        else if (K <= 2048) SGQ(256, 2);
+        else SGQ(256, 4);
+    } else if (N <= 1024 && K >= 512) {
+        SGQ(128, 1);
+    } else if (K <= 64) SGQ(16, 1);
     else if (K <= 128) SGQ(32, 1);
     else if (K <= 256) SGQ(64, 1);
     else if (K <= 512) SGQ(64, 2);
