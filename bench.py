@@ -418,12 +418,12 @@ CASES = {
     "attn_bwd_350m_with_att": lambda pcl, lib, w, s: attn_bwd(pcl, lib, 4, 1024, 16, 64, w, s, True),
     "attn_bwd_trainer_dh128": lambda pcl, lib, w, s: attn_bwd(pcl, lib, 4, 1024, 12, 128, w, s),
     "gemv_head_fp32_m1": lambda pcl, lib, w, s: gemv(pcl, lib, 1, 1, [(1024, 50257)], 3, w, s),
-    "gemv_head_int8_m1": lambda pcl, lib, w, s: gemv(pcl, lib, 2, 1, [(1024, 50257)], 6, w, s),
+    "gemv_head_int8_m1": lambda pcl, lib, w, s: gemv(pcl, lib, 2, 1, [(1024, 50257)], 11, w, s),
     "gemv_head_fp32_m8": lambda pcl, lib, w, s: gemv(pcl, lib, 1, 8, [(1024, 50257)], 3, w, s),
-    "gemv_head_int8_m8": lambda pcl, lib, w, s: gemv(pcl, lib, 2, 8, [(1024, 50257)], 6, w, s),
-    "gemv_head_int8_m2": lambda pcl, lib, w, s: gemv(pcl, lib, 2, 2, [(1024, 50257)], 6, w, s),
-    "gemv_head_int8_m3": lambda pcl, lib, w, s: gemv(pcl, lib, 2, 3, [(1024, 50257)], 6, w, s),
-    "gemv_head_int8_m4": lambda pcl, lib, w, s: gemv(pcl, lib, 2, 4, [(1024, 50257)], 6, w, s),
+    "gemv_head_int8_m8": lambda pcl, lib, w, s: gemv(pcl, lib, 2, 8, [(1024, 50257)], 11, w, s),
+    "gemv_head_int8_m2": lambda pcl, lib, w, s: gemv(pcl, lib, 2, 2, [(1024, 50257)], 11, w, s),
+    "gemv_head_int8_m3": lambda pcl, lib, w, s: gemv(pcl, lib, 2, 3, [(1024, 50257)], 11, w, s),
+    "gemv_head_int8_m4": lambda pcl, lib, w, s: gemv(pcl, lib, 2, 4, [(1024, 50257)], 11, w, s),
     "decode_int8_m1": lambda pcl, lib, w, s: gemv(pcl, lib, 2, 1, DECODE_LAYER * 16 + [(512, 2048)], 11, w, s),
     "decode_int8_m4": lambda pcl, lib, w, s: gemv(pcl, lib, 2, 4, DECODE_LAYER * 16 + [(512, 2048)], 11, w, s),
     "decode_fp32_m1": lambda pcl, lib, w, s: gemv(pcl, lib, [0] * 64 + [1], 1, DECODE_LAYER * 16 + [(512, 2048)],
@@ -436,8 +436,8 @@ CASES = {
                                                                11, w, s),
     "decode_group_int8_m8": lambda pcl, lib, w, s: gemv_group(pcl, lib, 2, 8, DECODE_LAYER * 16 + [(512, 2048)],
                                                                11, w, s),
-    "gemv_group_head_int8_m1": lambda pcl, lib, w, s: gemv_group(pcl, lib, 2, 1, [(1024, 50257)], 6, w, s),
-    "gemv_group_head_int8_m8": lambda pcl, lib, w, s: gemv_group(pcl, lib, 2, 8, [(1024, 50257)], 6, w, s),
+    "gemv_group_head_int8_m1": lambda pcl, lib, w, s: gemv_group(pcl, lib, 2, 1, [(1024, 50257)], 11, w, s),
+    "gemv_group_head_int8_m8": lambda pcl, lib, w, s: gemv_group(pcl, lib, 2, 8, [(1024, 50257)], 11, w, s),
     "gemv_group_head_fp32_m1": lambda pcl, lib, w, s: gemv_group(pcl, lib, 1, 1, [(1024, 50257)], 3, w, s),
 }
 
@@ -668,7 +668,7 @@ def run_rows(pcl, lib):
     ex["grown_decode_gemv"] = dec
     ex["decode_e2e_grown"] = decode_e2e(pcl)
     ex["head_350m_gemv_fp32"] = {f"M{Mt}": gemv(pcl, lib, 1, Mt, [(1024, 50257)], 3, 2, 20) for Mt in (1, 8)}
-    ex["head_350m_gemv_int8"] = {f"M{Mt}": gemv(pcl, lib, 2, Mt, [(1024, 50257)], 6, 2, 20) for Mt in (1, 8)}
+    ex["head_350m_gemv_int8"] = {f"M{Mt}": gemv(pcl, lib, 2, Mt, [(1024, 50257)], 11, 2, 20) for Mt in (1, 8)}
     ex["fp32_350m_epilogues"] = {
         "ffn_up_gelu": sgemm_epi(pcl, lib, 0, 0, 4096, 4096, 1024, 1, w, s),
         "attn_out_residual": sgemm_epi(pcl, lib, 0, 0, 4096, 1024, 1024, 2, w, s),
