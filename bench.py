@@ -405,6 +405,11 @@ CASES = {
     "int8_head": lambda pcl, lib, w, s: igemm(pcl, lib, 4096, 50257, 1024, 2, w, s),
     "fp32_1024": lambda pcl, lib, w, s: sgemm(pcl, lib, 0, 0, 1024, 1024, 1024, 0, w, s),
     "fp32_ffn_up": lambda pcl, lib, w, s: sgemm(pcl, lib, 0, 0, 4096, 4096, 1024, 0, w, s),
+    "fp32_attn_out": lambda pcl, lib, w, s: sgemm(pcl, lib, 0, 0, 4096, 1024, 1024, 0, w, s),
+    "fp32_ffn_down": lambda pcl, lib, w, s: sgemm(pcl, lib, 0, 0, 4096, 1024, 4096, 0, w, s),
+    "fp32_bwd_dx_nt": lambda pcl, lib, w, s: sgemm(pcl, lib, 0, 1, 4096, 1024, 4096, 1, w, s),
+    "fp32_bwd_dw_tn": lambda pcl, lib, w, s: sgemm(pcl, lib, 1, 0, 1024, 4096, 4096, 1, w, s),
+    "epi_350m_ffn_down_resid": lambda pcl, lib, w, s: sgemm_epi(pcl, lib, 0, 0, 4096, 1024, 4096, 2, w, s),
     "epi_350m_ffn_up_gelu": lambda pcl, lib, w, s: sgemm_epi(pcl, lib, 0, 0, 4096, 4096, 1024, 1, w, s),
     "decode_e2e": lambda pcl, lib, w, s: decode_e2e(pcl),
     # eager steps only (kernel traces: rocprofv3 does not follow graph launches here)

@@ -1206,12 +1206,15 @@ SgemmPlan plan_sgemm(int M, int N, int K) {
 }
 
 // Grids of at least two workgroups per CU take the 16x16x4 kernel (its
-// workgroups pair up on a CU): 1 = 128x128 tiles, 2 = 128x64 tiles (grids that
-// have only one 128x128 tile per CU), 3 = 64x64 tiles (two per CU only at that
-// size, e.g. 2048 x 1024), 0 = the 32x32x2 kernel (smaller grids, where its two
-// K groups keep two waves on every SIMD). Measured on the 350M-class shapes in
-// one run: 128x128 +8-11% where it applies, 128x64 +1-11%; 64x64 on
-// 2048 x 1024 x 1024: +11% (with one 64x64 tile per CU, 1024^3, it is not ahead).
+// workgroups pair up on a CU): 1 = 128x128 tiles, 2 = grids that have only one
+// 128x128 tile per CU: one 128x128 workgroup of 8 waves (32x64 each; 16-deep
+// stages, 32-deep for NT) per CU, or for TT two 128x64 workgroups of 4 waves,
+// 3 = 64x64 tiles (two per CU only at that size, e.g. 2048 x 1024), 0 = the
+// 32x32x2 kernel (smaller grids, where its two K groups keep two waves on
+// every SIMD). Measured on the 350M-class shapes: 128x128 +8-11% where it
+// applies; the 8-wave 128x128 workgroup +3-7% over two 128x64 ones (the
+// attention projection, FF2 and dW); 64x64 on 2048 x 1024 x 1024: +11% (with
+// one 64x64 tile per CU, 1024^3, it is not ahead).
 static int s16_tile(int M, int N) {
     const long t128 = (long)((M + 127) / 128) * ((N + 127) / 128);
     const long t64 = (long)((M + 127) / 128) * ((N + 63) / 64);
@@ -1220,6 +1223,26 @@ static int s16_tile(int M, int N) {
     if (t64 >= 512) return 2;
     if (t6464 >= 512) return 3;
     return 0;
+}
+
+// Route 2 of s16_tile: one 8-wave 128x128 workgroup per CU (NT on 32-deep
+// stages), two 4-wave 128x64 workgroups for TT.
+template <bool A_KC, bool B_KC, int EPI = EPI_NONE>
+static hipError_t launch_s16_one_per_cu(int M, int N, int K, const float *A, long lda, const float *B,
+                                        long ldb, const float *bias, int accumulate, float *C, long ldc,
+                                        hipStream_t stream, const float *aux_in = nullptr,
+                                        float *aux_out = nullptr, long ld_aux = 0) {
+    if constexpr (!A_KC && B_KC)
+        return launch_s16<128, 64, 3, 2, A_KC, B_KC, EPI>(M, N, K, 1, K, A, lda, B, ldb, bias, accumulate, C,
+                                                        ldc, stream, aux_in, aux_out, ld_aux);
+    else if constexpr (A_KC && B_KC)
+        return launch_s16<128, 128, 4, 2, A_KC, B_KC, EPI, 4, 2, 1>(M, N, K, 1, K, A, lda, B, ldb, bias,
+                                                                  accumulate, C, ldc, stream, aux_in, aux_out,
+                                                                  ld_aux);
+    else
+        return launch_s16<128, 128, 4, 1, A_KC, B_KC, EPI, 4, 2, 1>(M, N, K, 1, K, A, lda, B, ldb, bias,
+                                                                  accumulate, C, ldc, stream, aux_in, aux_out,
+                                                                  ld_aux);
 }
 
 // Fused epilogues exist for the layouts the trainer uses them in: NN
@@ -1240,8 +1263,8 @@ static hipError_t launch_dma_epi(const SgemmPlan &p, int M, int N, int K, const 
         return launch_s16<128, 128, 4, 1, A_KC, B_KC, EPI>(M, N, K, 1, K, A, lda, B, ldb, bias, 0, C, ldc,
                                                          stream, aux_in, aux_out, ld_aux);
     if (s16 == 2)
-        return launch_s16<128, 64, 3, 2, A_KC, B_KC, EPI>(M, N, K, 1, K, A, lda, B, ldb, bias, 0, C, ldc,
-                                                        stream, aux_in, aux_out, ld_aux);
+        return launch_s16_one_per_cu<A_KC, B_KC, EPI>(M, N, K, A, lda, B, ldb, bias, 0, C, ldc, stream, aux_in,
+                                                      aux_out, ld_aux);
     if (s16 == 3)
         return launch_s16<64, 64, 4, 1, A_KC, B_KC, EPI>(M, N, K, 1, K, A, lda, B, ldb, bias, 0, C, ldc,
                                                        stream, aux_in, aux_out, ld_aux);
@@ -1300,7 +1323,7 @@ static hipError_t dispatch_layout(const SgemmPlan &p, int M, int N, int K, const
     if (dma_ok && s16 == 1) {
         e = launch_s16<128, 128, 4, 1, A_KC, B_KC>(M, N, K, 1, K, A, lda, B, ldb, b, acc, out, ldo, stream);
     } else if (dma_ok && s16 == 2) {
-        e = launch_s16<128, 64, 3, 2, A_KC, B_KC>(M, N, K, 1, K, A, lda, B, ldb, b, acc, out, ldo, stream);
+        e = launch_s16_one_per_cu<A_KC, B_KC>(M, N, K, A, lda, B, ldb, b, acc, out, ldo, stream);
     } else if (dma_ok && s16 == 3) {
         e = launch_s16<64, 64, 4, 1, A_KC, B_KC>(M, N, K, 1, K, A, lda, B, ldb, b, acc, out, ldo, stream);
     } else if (dma_ok) {
