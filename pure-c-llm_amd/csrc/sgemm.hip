@@ -1225,6 +1225,33 @@ static int s16_tile(int M, int N) {
     return 0;
 }
 
+// Route 1 of s16_tile: two 4-wave 128x128 workgroups per CU; for NN, one
+// 8-wave 128x256 workgroup per CU (a quarter less LDS fill per CU) where its
+// tiles fill whole rounds of 256 CUs (at least two, at most 1/16 of the last
+// round idle): +2.6-3.2% on 4096 x 4096 x 1024 and three other NN grids of
+// 512-768 such tiles; on 4096 x 3072 (384 tiles, half a round idle) it was
+// 21% slower, and on NT and TN grids slower or level.
+static bool s16_wide_nn(int M, int N) {
+    const long t = (long)((M + 127) / 128) * ((N + 255) / 256);
+    const long slots = (t + 255) / 256 * 256;
+    return t >= 512 && (slots - t) * 16 <= 256;
+}
+
+template <bool A_KC, bool B_KC, int EPI = EPI_NONE>
+static hipError_t launch_s16_two_per_cu(int M, int N, int K, const float *A, long lda, const float *B,
+                                        long ldb, const float *bias, int accumulate, float *C, long ldc,
+                                        hipStream_t stream, const float *aux_in = nullptr,
+                                        float *aux_out = nullptr, long ld_aux = 0) {
+    if constexpr (A_KC && !B_KC) {
+        if (s16_wide_nn(M, N))
+            return launch_s16<128, 256, 4, 1, A_KC, B_KC, EPI, 2, 4, 1>(M, N, K, 1, K, A, lda, B, ldb, bias,
+                                                                      accumulate, C, ldc, stream, aux_in, aux_out,
+                                                                      ld_aux);
+    }
+    return launch_s16<128, 128, 4, 1, A_KC, B_KC, EPI>(M, N, K, 1, K, A, lda, B, ldb, bias, accumulate, C, ldc,
+                                                     stream, aux_in, aux_out, ld_aux);
+}
+
 // Route 2 of s16_tile: one 8-wave 128x128 workgroup per CU (NT on 32-deep
 // stages), two 4-wave 128x64 workgroups for TT.
 template <bool A_KC, bool B_KC, int EPI = EPI_NONE>
@@ -1260,8 +1287,8 @@ static hipError_t launch_dma_epi(const SgemmPlan &p, int M, int N, int K, const 
                                  hipStream_t stream) {
     const int s16 = s16_tile(M, N);
     if (s16 == 1)
-        return launch_s16<128, 128, 4, 1, A_KC, B_KC, EPI>(M, N, K, 1, K, A, lda, B, ldb, bias, 0, C, ldc,
-                                                         stream, aux_in, aux_out, ld_aux);
+        return launch_s16_two_per_cu<A_KC, B_KC, EPI>(M, N, K, A, lda, B, ldb, bias, 0, C, ldc, stream, aux_in,
+                                                      aux_out, ld_aux);
     if (s16 == 2)
         return launch_s16_one_per_cu<A_KC, B_KC, EPI>(M, N, K, A, lda, B, ldb, bias, 0, C, ldc, stream, aux_in,
                                                       aux_out, ld_aux);
@@ -1321,7 +1348,7 @@ static hipError_t dispatch_layout(const SgemmPlan &p, int M, int N, int K, const
     }
     const int s16 = split ? 0 : s16_tile(M, N);
     if (dma_ok && s16 == 1) {
-        e = launch_s16<128, 128, 4, 1, A_KC, B_KC>(M, N, K, 1, K, A, lda, B, ldb, b, acc, out, ldo, stream);
+        e = launch_s16_two_per_cu<A_KC, B_KC>(M, N, K, A, lda, B, ldb, b, acc, out, ldo, stream);
     } else if (dma_ok && s16 == 2) {
         e = launch_s16_one_per_cu<A_KC, B_KC>(M, N, K, A, lda, B, ldb, b, acc, out, ldo, stream);
     } else if (dma_ok && s16 == 3) {
