@@ -405,6 +405,8 @@ CASES = {
     "int8_head": lambda pcl, lib, w, s: igemm(pcl, lib, 4096, 50257, 1024, 2, w, s),
     "fp32_1024": lambda pcl, lib, w, s: sgemm(pcl, lib, 0, 0, 1024, 1024, 1024, 0, w, s),
     "fp32_ffn_up": lambda pcl, lib, w, s: sgemm(pcl, lib, 0, 0, 4096, 4096, 1024, 0, w, s),
+    "fp32_qkv": lambda pcl, lib, w, s: sgemm(pcl, lib, 0, 0, 4096, 3072, 1024, 0, w, s),
+    "fp32_qkv_nt": lambda pcl, lib, w, s: sgemm(pcl, lib, 0, 1, 4096, 3072, 1024, 0, w, s),
     "fp32_attn_out": lambda pcl, lib, w, s: sgemm(pcl, lib, 0, 0, 4096, 1024, 1024, 0, w, s),
     "fp32_ffn_down": lambda pcl, lib, w, s: sgemm(pcl, lib, 0, 0, 4096, 1024, 4096, 0, w, s),
     "fp32_bwd_dx_nt": lambda pcl, lib, w, s: sgemm(pcl, lib, 0, 1, 4096, 1024, 4096, 1, w, s),

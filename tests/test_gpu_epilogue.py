@@ -44,6 +44,8 @@ CASES = [(1024, 1024, 256, N_, N_, "fused 64x64"), (2048, 2048, 128, N_, N_, "fu
          (2900, 2980, 96, N_, N_, "16x16 kernel, 128x128, ragged"),
          (2900, 2980, 96, N_, T_, "16x16 kernel, 128x128 NT, ragged"),
          (4000, 4000, 96, N_, N_, "16x16 kernel, 8-wave 128x256, ragged"),
+         (4000, 3000, 64, N_, N_, "16x16 kernel, 128x192, ragged"),
+         (4000, 3000, 64, N_, T_, "16x16 kernel, 8-wave 256x192 NT, ragged"),
          (4000, 1000, 64, N_, N_, "16x16 kernel, 8-wave 128x128, ragged"),
          (4000, 1000, 64, N_, T_, "16x16 kernel, 8-wave 128x128 NT, ragged"),
          (2000, 1100, 160, N_, N_, "16x16 kernel, 64x64, ragged"),
