@@ -400,6 +400,7 @@ INT8_350M = {"qkv": (4096, 3072, 1024), "attn_out": (4096, 1024, 1024), "ffn_up"
              "ffn_down": (4096, 1024, 4096), "head": (4096, 50257, 1024)}
 CASES = {
     "int8_2048": lambda pcl, lib, w, s: igemm(pcl, lib, 2048, 2048, 2048, 2, w, s),
+    "int8_qkv": lambda pcl, lib, w, s: igemm(pcl, lib, 4096, 3072, 1024, 2, w, s),
     "int8_ffn_up": lambda pcl, lib, w, s: igemm(pcl, lib, 4096, 4096, 1024, 2, w, s),
     "int8_ffn_down": lambda pcl, lib, w, s: igemm(pcl, lib, 4096, 1024, 4096, 2, w, s),
     "int8_head": lambda pcl, lib, w, s: igemm(pcl, lib, 4096, 50257, 1024, 2, w, s),

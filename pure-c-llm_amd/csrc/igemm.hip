@@ -777,7 +777,9 @@ hipError_t launch_igemm(int out_mode, int M, int N, int K, const uint8_t *A, lon
     //  * outputs beyond 256 MiB (the 50257-vocab head): producer/consumer
     //    256x128 tiles, the stores of one tile draining under the next;
     //  * 256x256 tiles with 8 waves when they still cover most of the 256 CUs
-    //    (K = 1024 projections: fewer operand bytes per output);
+    //    (K = 1024 projections: fewer operand bytes per output); 256x192 when
+    //    those fill the CUs clearly better (4096 x 3072: 256 tiles, one round,
+    //    against 192 of 256x256; +2.5-2.8% on that shape, bit-identical);
     //  * producer/consumer 128x128 tiles when those fill the chip;
     //  * 64x64 otherwise, and for K = 0 (the epilogue alone).
     const long t256 = (long)((M + 255) / 256) * ((N + 255) / 256);
@@ -786,9 +788,17 @@ hipError_t launch_igemm(int out_mode, int M, int N, int K, const uint8_t *A, lon
     if (K > 0 && t256 >= 192 && huge)
         return launch_wp<256, 128, 4, 2, 3>(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa, sb, C,
                                             ldc, stream);
-    if (K > 0 && t256 >= 192)
+    if (K > 0 && t256 >= 192) {
+        const long t192 = (long)((M + 255) / 256) * ((N + 191) / 192);
+        const double area = (double)M * N;
+        const double f256 = area / ((double)((t256 + 255) / 256 * 256) * 256 * 256);
+        const double f192 = area / ((double)((t192 + 255) / 256 * 256) * 256 * 192);
+        if (f192 > f256 + 0.05)
+            return launch_split<256, 192, 4, 2, 2, 1>(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa,
+                                                      sb, C, ldc, stream);
         return launch_split<256, 256, 4, 2, 2, 1>(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa,
                                                   sb, C, ldc, stream);
+    }
     if (K > 0 && t128 >= 256)
         return launch_wp<128, 128, 4, 2, 3>(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa, sb, C,
                                             ldc, stream);

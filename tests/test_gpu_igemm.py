@@ -152,7 +152,7 @@ def _dq_run(Au, Bq, sa, sb, col_off=None):
     return dC.download((M, N), np.float32)
 
 
-@pytest.mark.parametrize("M,N,K", [(2048, 2048, 2048), (4, 1536, 512), (200, 300, 96)])
+@pytest.mark.parametrize("M,N,K", [(2048, 2048, 2048), (4096, 3072, 1024), (4, 1536, 512), (200, 300, 96)])
 def test_igemm_dequant_bit_exact(M, N, K):
     # gemm_bench INT8 config: per-row x per-column scales ~ U[1e-3, 1e-2]
     Au = ob.u8((M, K), 40)
@@ -276,10 +276,10 @@ def test_igemm_dequant_output_beyond_256mib():
     np.testing.assert_array_equal(C[rows], ob.dequant(V, None, sb))
 
 
-@pytest.mark.parametrize("M,N,K", [(2100, 2070, 1040), (4100, 3100, 528), (2056, 2048, 2064)])
+@pytest.mark.parametrize("M,N,K", [(2100, 2070, 1040), (4100, 3100, 528), (4000, 3000, 528), (2056, 2048, 2064)])
 def test_igemm_ragged_large_tiles(M, N, K):
-    # ragged M, N and K (K % 128 != 0) on the 128x128 (two K groups) and
-    # 256x256 tile paths; float64 products of these integers are exact
+    # ragged M, N and K (K % 128 != 0) on the 128x128 (two K groups),
+    # 256x256 and 256x192 (4000 x 3000) tile paths; float64 products of these integers are exact
     # (every partial sum stays far below 2**53)
     Au = ob.u8((M, K), 80 + M)
     Bq = ob.s8((K, N), 81 + N)
