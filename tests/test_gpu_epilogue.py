@@ -41,8 +41,10 @@ CASES = [(1024, 1024, 256, N_, N_, "fused 64x64"), (2048, 2048, 128, N_, N_, "fu
          (1024, 1024, 256, N_, T_, "fused NT"), (300, 500, 200, N_, N_, "split K"),
          (1024, 1024, 250, N_, N_, "K % 32 != 0"), (1024, 1024, 256, T_, N_, "TN"),
          (1000, 1030, 256, N_, N_, "ragged edges"),
-         (2900, 2980, 96, N_, N_, "16x16 kernel, 128x128, ragged"),
-         (2900, 2980, 96, N_, T_, "16x16 kernel, 128x128 NT, ragged"),
+         (4100, 4100, 64, N_, N_, "16x16 kernel, 128x128, ragged"),
+         (4100, 4100, 64, N_, T_, "16x16 kernel, 128x128 NT, ragged"),
+         (2900, 2980, 96, N_, N_, "16x16 kernel, 128x192, ragged"),
+         (2900, 2980, 96, N_, T_, "16x16 kernel, 8-wave 256x192 NT, ragged"),
          (4000, 4000, 96, N_, N_, "16x16 kernel, 8-wave 128x256, ragged"),
          (4000, 3000, 64, N_, N_, "16x16 kernel, 128x192, ragged"),
          (4000, 3000, 64, N_, T_, "16x16 kernel, 8-wave 256x192 NT, ragged"),

@@ -119,13 +119,14 @@ def test_sgemm_lds_dma_edges(opA, opB, M, N, K):
 
 
 @pytest.mark.parametrize("opA,opB", [(N_, N_), (N_, T_), (T_, N_), (T_, T_)])
-@pytest.mark.parametrize("M,N,K", [(2900, 2980, 96), (4000, 4000, 64), (4000, 3000, 96), (4000, 1000, 64),
-                                   (4100, 1000, 352), (2000, 1100, 160)])
+@pytest.mark.parametrize("M,N,K", [(4100, 4100, 64), (2900, 2980, 96), (4000, 4000, 64), (4000, 3000, 96),
+                                   (4000, 1000, 64), (4100, 1000, 352), (2000, 1100, 160)])
 def test_sgemm_16x16_grid_edges(opA, opB, M, N, K):
     # grids of >= 512 tiles take the 16x16x4 kernel: 128x128 tiles on 16-deep
-    # stages (2900 x 2980); NN grids that fill whole rounds of 128x256 tiles
-    # (4000 x 4000) one 8-wave 128x256 workgroup per CU; grids that fill the
-    # chip better with 192-wide tiles (4000 x 3000) two 4-wave 128x192
+    # stages (4100 x 4100, and 4000 x 4000 in the layouts other than NN); NN
+    # grids that fill whole rounds of 128x256 tiles (4000 x 4000) one 8-wave
+    # 128x256 workgroup per CU; grids that fill the
+    # chip better with 192-wide tiles (4000 x 3000, 2900 x 2980) two 4-wave 128x192
     # workgroups per CU, for NT one 8-wave 256x192 on 32-deep stages; grids of one 128x128
     # tile per CU (4000 x 1000, 4100 x 1000) an 8-wave 128x128 workgroup on
     # 16-deep stages (NN, TN) or 32-deep ones (NT), and for TT 128x64 tiles on
