@@ -195,15 +195,29 @@ __device__ __forceinline__ void gv_xform(float *xs, int klen, int kb, int K,
 }
 
 // Second pass of a split-K GEMV: Y[m,n] = sum over splits in order (+ bias,
-// + Y when accumulating). part is [splits][M][nround].
+// + Y when accumulating). part is [splits][M][nround]. Partials are loaded
+// eight at a time before they are added (in split order), so a thread waits
+// for one memory round trip per eight splits rather than per split: these
+// grids are a few workgroups (a bias gradient of 1024 columns: four), so the
+// loads' latency, not bandwidth, sets the time.
 __global__ void sgemv_reduce_kernel(const float *__restrict__ part, int splits, int M, int N,
                                     int nround, const float *__restrict__ bias,
                                     float *__restrict__ Y, long ldy, int accumulate) {
     const long i = blockIdx.x * (long)blockDim.x + threadIdx.x;
     if (i >= (long)M * N) return;
     const int m = (int)(i / N), n = (int)(i % N);
+    const long stride = (long)M * nround;
+    const float *p = part + (long)m * nround + n;
     float s = 0.f;
-    for (int q = 0; q < splits; q++) s += part[((long)q * M + m) * nround + n];
+    int q = 0;
+    for (; q + 8 <= splits; q += 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = p[(q + u) * stride];
+#pragma unroll
+        for (int u = 0; u < 8; u++) s += v[u];
+    }
+    for (; q < splits; q++) s += p[q * stride];
     float y = s + (bias ? bias[n] : 0.f);
     float *dst = Y + (long)m * ldy + n;
     *dst = accumulate ? *dst + y : y;
