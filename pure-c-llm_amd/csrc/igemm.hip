@@ -64,6 +64,7 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(1))) int32_t gint32_t;
 typedef __attribute__((address_space(1))) float gfloat_t;
+typedef __attribute__((address_space(1))) unsigned gu32_t;
 
 constexpr int IG_BK = 128;  // bytes of K per tile
 constexpr int IG_KC = 4;    // 32-byte MFMA k-chunks (steps) per tile
@@ -82,6 +83,11 @@ template <int OFF>
 __device__ __forceinline__ void lds_read16(v4i &r, unsigned addr) {
     static_assert(OFF >= 0 && OFF < 65536, "ds_read offset field");
     asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
+}
+template <int OFF>
+__device__ __forceinline__ void lds_write16(unsigned addr, const v4i &v) {
+    static_assert(OFF >= 0 && OFF < 65536, "ds_write offset field");
+    asm volatile("ds_write_b128 %0, %1 offset:%2" ::"v"(addr), "v"(v), "i"(OFF));
 }
 template <int N>
 __device__ __forceinline__ void lds_wait() {
@@ -641,6 +647,301 @@ __global__ __launch_bounds__(64 * (WM * WN + NWP)) __attribute__((amdgpu_waves_p
     }
 }
 
+// ---------------------------------------------------------------------------
+// Producer/consumer kernel for grids of about one 128x128 output tile per CU
+// (2048^3, the K = 4096 down projection, the attention output projection):
+// one tile per workgroup, eight consumer waves on v_mfma_i32_16x16x64_i8,
+// NWP producer waves, a STAGES-deep ring of 128-byte K tiles.
+//
+// What bounds it. A 128x128 tile consumes 32 KB of operands per 128-byte K
+// tile. The L2 -> LDS stream of these grids moves ~22 TB/s into LDS (about
+// 88 GB/s per CU; measured with the DMA alone), so the loop is bound by the
+// operand feed, and the feed runs at the shader clock, which the matrix cores
+// pull down to 1.4-1.8 GHz on random operands. Two choices follow:
+//  * every consumer wave reads a whole K tile's fragments into registers one
+//    tile ahead, so a stage can be refilled as soon as the MFMAs of its tile
+//    begin: with a 3- or 4-deep ring two or three K tiles are in flight;
+//  * the 16x16x64 instruction: a loop of it alone holds ~2.05 GHz on random
+//    bytes against ~1.7 GHz for the 32x32x32 form at the same work per clock.
+// KGR = 1: 4x2 consumer waves of 32x64, each over the whole K tile (12
+// fragment reads per K tile). KGR = 2: two K groups of 2x2 waves of 64x64,
+// group g multiplies the 64 k-bytes g of every K tile (8 reads: a third fewer
+// LDS bytes) and the groups' partial tiles are added once at the end through
+// the freed ring. Integer sums are exact in any order: both forms are
+// bit-identical to the integer definition.
+//
+// Barrier protocol (every wave runs the same sequence): P0 once K tile 0 has
+// landed; then B(kt) for each K tile, after the first MFMA of tile kt in the
+// consumers. Before B(kt) every consumer has retired its reads of K tile kt
+// (issued during tile kt-1) and the producers have waited for K tile kt+1;
+// after it the producers refill tile kt's stage with tile kt + STAGES and the
+// consumers read tile kt+1. With KGR = 2 one more barrier orders the exchange.
+template <int STAGES, int NWP, int KGR, int OUT, int NTS>
+__global__ __launch_bounds__(64 * (8 + NWP)) __attribute__((amdgpu_waves_per_eu(
+    (8 + NWP + 3) / 4))) void igemm_kg_kernel(const uint8_t *__restrict__ A, long lda,
+                                             const int8_t *__restrict__ B, long ldb,
+                                             const int32_t *__restrict__ col_off,
+                                             const float *__restrict__ sa,
+                                             const float *__restrict__ sb,
+                                             void *__restrict__ Cv, long ldc, int M, int N,
+                                             int K) {
+    constexpr int BM = 128, BN = 128, BK = IG_BK, CH = BK / 16, RPI = 1024 / BK;
+    constexpr int SIZE_A = BM * BK, STAGE = (BM + BN) * BK;
+    constexpr int PIA = BM / (RPI * NWP), PIB = BN / (RPI * NWP), PL = PIA + PIB;
+    constexpr int LDS_BYTES = STAGES * STAGE;
+    constexpr int XW = 8192;  // exchange bytes per consumer wave (half of a 64x64 int32 tile)
+    static_assert(NWP == 2 || NWP == 4, "producer waves");
+    static_assert(KGR == 1 || KGR == 2, "K groups");
+    static_assert(STAGES >= 3 && LDS_BYTES <= 160 * 1024, "ring");
+    static_assert(LDS_BYTES >= 8 * XW, "the exchange reuses the ring");
+    static_assert((STAGES - 1) * PL <= 63, "vmcnt range");
+    __shared__ __attribute__((aligned(1024))) int8_t lds[LDS_BYTES];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nbm = (M + BM - 1) / BM, nbn = (N + BN - 1) / BN;
+    int bm, bn;
+    tile_coords(xcd_remap(blockIdx.x, nbm * nbn), nbm, nbn, 8, bm, bn);
+    const int m0 = bm * BM, n0 = bn * BN;
+    const int nk = K / BK;
+
+    if (wave >= 8) {
+        // ------------------------------------------------------ producers
+        const int pw = wave - 8;
+        const int8_t *A8 = reinterpret_cast<const int8_t *>(A);
+        unsigned voff[PL];
+        int ldso[PL];
+#pragma unroll
+        for (int d = 0; d < PL; d++) {
+            const bool isA = d < PIA;
+            const int rb = ((isA ? d : d - PIA) * NWP + pw) * RPI;
+            const int r = rb + lane / CH;
+            const int c = (lane % CH) ^ ((r >> 1) & (CH - 1));
+            const int grow = min((isA ? m0 : n0) + r, (isA ? M : N) - 1);
+            voff[d] = (unsigned)grow * (unsigned)(isA ? lda : ldb) + (unsigned)(c * 16);
+            ldso[d] = (isA ? 0 : SIZE_A) + rb * BK;
+        }
+        auto dma = [&](int t) {
+            int8_t *stage = lds + (t % STAGES) * STAGE;
+            const long koff = (long)t * BK;
+#pragma unroll
+            for (int d = 0; d < PL; d++)
+                __builtin_amdgcn_global_load_lds((const void *)((d < PIA ? A8 : B) + koff + voff[d]),
+                                                 (lds_void_t *)(stage + ldso[d]), 16, 0, 0);
+        };
+        // Prologue: tiles 0 and 1, P0 once tile 0 has landed, then the rest of
+        // the ring (issued all at once, tile 0 would queue behind the whole ring
+        // in L2 and the first MFMA would wait for it).
+        dma(0);
+        if (nk > 1) {
+            dma(1);
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm(PL));
+        } else {
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+        }
+        __builtin_amdgcn_s_barrier();  // P0
+#pragma unroll
+        for (int t = 2; t < STAGES; t++)
+            if (t < nk) dma(t);
+        for (int kt = 0; kt < nk; kt++) {
+            // K tile kt+1 has landed; tiles kt+2 .. kt+STAGES-1 may still fly
+            if (kt + STAGES - 1 < nk) __builtin_amdgcn_s_waitcnt(waitcnt_vm((STAGES - 2) * PL));
+            else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+            __builtin_amdgcn_s_barrier();  // B(kt)
+            if (kt + STAGES < nk) dma(kt + STAGES);
+        }
+        if constexpr (KGR == 2) __builtin_amdgcn_s_barrier();  // exchange
+        return;
+    }
+
+    // ---------------------------------------------------------- consumers
+    constexpr int WM = KGR == 2 ? 2 : 4;
+    constexpr int WTM = BM / WM, WTN = 64;     // wave tile
+    constexpr int NBM = WTM / 16, NBN = WTN / 16;  // 16x16 blocks
+    constexpr int KS = 2 / KGR;                // 64-byte k-steps per wave per K tile
+    constexpr int NFA = KS * NBM, NFB = KS * NBN, NF = NFA + NFB;
+    constexpr int NM = KS * NBM * NBN;         // MFMAs per K tile
+    const int kg = KGR == 2 ? wave >> 2 : 0;
+    const int wm = KGR == 2 ? (wave >> 1) & 1 : wave >> 1, wn = wave & 1;
+
+    // Epilogue operands first (clamped, no branches): their loads complete
+    // under the K loop. Lane l holds column l%16 of each 16-wide block and
+    // rows 4(l/16) + r of each stored 16-row block (the rows kg*32 .. kg*32+31
+    // of the wave tile).
+    void *C_out = Cv;
+    long ld_out = ldc;
+    int Mv = M, Nv = N;
+    asm volatile("" : "+s"(C_out), "+s"(ld_out), "+s"(Mv), "+s"(Nv));
+    const int wrow0 = m0 + wm * WTM, wcol0 = n0 + wn * WTN;
+    const int lcol = lane & 15;
+    float sbv[NBN];
+    unsigned offv[NBN];
+#pragma unroll
+    for (int j = 0; j < NBN; j++) {
+        const int colc = min(wcol0 + j * 16 + lcol, Nv - 1);
+        sbv[j] = (OUT != 0) ? sb[colc] : 0.f;
+        offv[j] = (OUT != 0 && col_off) ? (unsigned)col_off[colc] : 0u;
+    }
+    float sav[8];
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+        const int r = kg * 32 + (q >> 2) * 16 + 4 * (lane >> 4) + (q & 3);
+        sav[q] = (OUT == 2) ? sa[min(wrow0 + r, Mv - 1)] : 0.f;
+    }
+
+    const unsigned lds0 = lds_addr(lds);
+    // Fragment offsets in a stage: lane (r16, g4) reads row r16 of a 16-row
+    // block at 16-byte chunk 4(kg*KS + s) + g4 of the 128-byte K tile. Rows are
+    // stored with chunk c at c ^ ((row >> 1) & 7); blocks start at multiples of
+    // 16 rows, so the swizzle depends on the lane only.
+    const int lrow = lane & 15, lgrp = lane >> 4;
+    const int swz = (lrow >> 1) & (CH - 1);
+    unsigned offa[KS], offb[KS];
+#pragma unroll
+    for (int s = 0; s < KS; s++) {
+        const int chunk = 4 * (kg * KS + s) + lgrp;
+        offa[s] = (wm * WTM + lrow) * BK + ((chunk ^ swz) << 4);
+        offb[s] = SIZE_A + (wn * WTN + lrow) * BK + ((chunk ^ swz) << 4);
+    }
+
+    v4i acc[NBM][NBN];
+#pragma unroll
+    for (int i = 0; i < NBM; i++)
+#pragma unroll
+        for (int j = 0; j < NBN; j++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) acc[i][j][v] = 0;
+
+    // Two register slots of a K tile's fragments: fa[slot][s*NBM + i], fb[slot][s*NBN + j].
+    v4i fa[2][NFA], fb[2][NFB];
+    auto read_frag = [&](unsigned base, auto S, auto F) {
+        constexpr int sl = decltype(S)::value, f = decltype(F)::value;
+        if constexpr (f < NFA) lds_read16<(f % NBM) * 16 * BK>(fa[sl][f], base + offa[f / NBM]);
+        else lds_read16<((f - NFA) % NBN) * 16 * BK>(fb[sl][f - NFA], base + offb[(f - NFA) / NBN]);
+    };
+    auto land = [&](auto S) {  // the slot's reads have retired: fence, re-centre A
+        constexpr int sl = decltype(S)::value;
+        lds_wait<0>();
+        static_for<0, NFA>([&](auto F) { reg_fence(fa[sl][F.value]); });
+        static_for<0, NFB>([&](auto F) { reg_fence(fb[sl][F.value]); });
+        static_for<0, NFA>([&](auto F) { fa[sl][F.value] ^= (int)0x80808080u; });
+    };
+
+    __builtin_amdgcn_s_barrier();  // P0
+    static_for<0, NF>([&](auto F) { read_frag(lds0, IC<0>{}, F); });
+    land(IC<0>{});
+
+    // One K tile from slot S: MFMA 0, the barrier, then the next tile's NF
+    // reads spread over the gaps of the first half of the tile's MFMAs; the
+    // next slot lands before the last MFMA.
+    auto tile = [&](int kt, auto S) {
+        constexpr int sl = decltype(S)::value, ns = 1 - sl;
+        const unsigned nbase = lds0 + ((kt + 1) % STAGES) * STAGE;
+        constexpr int RPG = (NF + NM / 2 - 1) / (NM / 2);  // reads per gap
+        static_for<0, NM>([&](auto Q) {
+            constexpr int q = Q.value;
+            constexpr int s = q / (NBM * NBN), j = (q / NBM) % NBN, i = q % NBM;
+            acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[sl][s * NBM + i], fb[sl][s * NBN + j],
+                                                              acc[i][j], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (q == 0) __builtin_amdgcn_s_barrier();  // B(kt)
+            if constexpr (q < NM / 2)
+                static_for<q * RPG, (q + 1) * RPG < NF ? (q + 1) * RPG : NF>(
+                    [&](auto F) { read_frag(nbase, IC<ns>{}, F); });
+            if constexpr (q == NM - 2) land(IC<ns>{});
+            __builtin_amdgcn_sched_barrier(0);
+        });
+    };
+    // Tiles in pairs (the slot index is a compile-time constant). The last
+    // tile's reads ahead are issued too, without a branch: they read the
+    // stage after it, inside the ring and no longer written by any DMA (the
+    // producers waited for every tile before its barrier), and are unused.
+    for (int kt = 0; kt < nk; kt += 2) {
+        tile(kt, IC<0>{});
+        if (kt + 1 < nk) tile(kt + 1, IC<1>{});
+    }
+    lds_wait<0>();
+
+    // Stores. A 16x16 block puts 4 rows x 16 columns in a register (64-byte
+    // row pieces per store); blocks j and j+1 are regrouped with two lane
+    // swaps so each store writes 2 rows x 32 columns (whole 128-byte lines):
+    // with X = block j, Y = block j+1 and row groups g = lane/16,
+    // permlane16_swap gives X = [X0 Y0 X2 Y2], Y = [X1 Y1 X3 Y3], then
+    // permlane32_swap X = [X0 Y0 X1 Y1] (rows r, 4+r), Y = [X2 Y2 X3 Y3]
+    // (rows 8+r, 12+r). Row blocks RB0 .. RB0+NRB-1 of the wave tile.
+    auto store_rows = [&](auto RB0, auto NRB, auto CHECK) {
+        constexpr int rb0 = decltype(RB0)::value, nrb = decltype(NRB)::value;
+        constexpr bool chk = decltype(CHECK)::value != 0;
+        const int hrow = 4 * (lane >> 5), hcol = lane & 31;
+        static_for<0, nrb>([&](auto I) {
+            constexpr int i = rb0 + I.value;
+            static_for<0, 4>([&](auto V) {
+                constexpr int v = V.value;
+                const float rs = sav[I.value * 4 + v];
+                static_for<0, NBN / 2>([&](auto JP) {
+                    constexpr int j0 = 2 * JP.value;
+                    unsigned x, y;
+                    if constexpr (OUT == 0) {
+                        x = (unsigned)acc[i][j0][v];
+                        y = (unsigned)acc[i][j0 + 1][v];
+                    } else {
+                        const float dx = (OUT == 2) ? rs * sbv[j0] : sbv[j0];
+                        const float dy = (OUT == 2) ? rs * sbv[j0 + 1] : sbv[j0 + 1];
+                        x = __float_as_uint((float)(int32_t)((unsigned)acc[i][j0][v] + offv[j0]) * dx);
+                        y = __float_as_uint((float)(int32_t)((unsigned)acc[i][j0 + 1][v] + offv[j0 + 1]) * dy);
+                    }
+                    const auto p16 = __builtin_amdgcn_permlane16_swap(x, y, false, false);
+                    const auto p32 = __builtin_amdgcn_permlane32_swap(p16[0], p16[1], false, false);
+                    const int col = wcol0 + j0 * 16 + hcol;
+#pragma unroll
+                    for (int h = 0; h < 2; h++) {
+                        const int row = wrow0 + i * 16 + 8 * h + hrow + v;
+                        if (chk && (row >= Mv || col >= Nv)) continue;
+                        const long o = (long)row * ld_out + col;
+                        const unsigned val = h == 0 ? p32[0] : p32[1];
+                        if constexpr (NTS) __builtin_nontemporal_store(val, (gu32_t *)C_out + o);
+                        else ((gu32_t *)C_out)[o] = val;
+                    }
+                });
+            });
+        });
+    };
+    const bool inside = m0 + BM <= Mv && n0 + BN <= Nv;
+    if constexpr (KGR == 1) {
+        if (inside) store_rows(IC<0>{}, IC<NBM>{}, IC<0>{});
+        else store_rows(IC<0>{}, IC<NBM>{}, IC<1>{});
+    } else {
+        // Partial-tile exchange: group kg stores the 32 rows of its wave tile
+        // it does not own lane-linearly into its 8 KB of the freed ring; after
+        // the barrier it adds its partner's copy of its own half (the partner
+        // is wave ^ 4), then stores that half.
+        constexpr int HB = NBM / 2;
+        auto exchange_and_store = [&](auto KG) {
+            constexpr int own = decltype(KG)::value, oth = 1 - own;
+            const unsigned waddr = lds0 + wave * XW + lane * 16, paddr = lds0 + (wave ^ 4) * XW + lane * 16;
+            static_for<0, HB * NBN>([&](auto P) {
+                constexpr int i = oth * HB + P.value / NBN, j = P.value % NBN;
+                lds_write16<P.value * 1024>(waddr, acc[i][j]);
+            });
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            __builtin_amdgcn_s_barrier();  // exchange
+            v4i t[HB * NBN];
+            static_for<0, HB * NBN>([&](auto P) { lds_read16<P.value * 1024>(t[P.value], paddr); });
+            lds_wait<0>();
+            static_for<0, HB * NBN>([&](auto P) {
+                constexpr int i = own * HB + P.value / NBN, j = P.value % NBN;
+                reg_fence(t[P.value]);
+#pragma unroll
+                for (int e = 0; e < 4; e++) acc[i][j][e] = (int)((unsigned)acc[i][j][e] + (unsigned)t[P.value][e]);
+            });
+            if (inside) store_rows(IC<own * HB>{}, IC<HB>{}, IC<0>{});
+            else store_rows(IC<own * HB>{}, IC<HB>{}, IC<1>{});
+        };
+        if (kg == 0) exchange_and_store(IC<0>{});
+        else exchange_and_store(IC<1>{});
+    }
+}
+
 static int device_cus() {
     static const int cus = [] {
         int dev = 0, n = 0;
@@ -706,6 +1007,61 @@ static hipError_t launch_wp(int out_mode, int M, int N, int K, const uint8_t *A,
                 out_mode, mm, nn, K, A + m * lda, lda, B + n * ldb, ldb,
                 col_off ? col_off + n : nullptr, sa ? sa + m : nullptr, sb ? sb + n : nullptr,
                 (char *)C + (m * ldc + n) * 4, ldc, stream);
+            if (e != hipSuccess) return e;
+        }
+    }
+    return hipSuccess;
+}
+
+template <int STAGES, int NWP, int KGR>
+static hipError_t launch_kg_band(int out_mode, int M, int N, int K, const uint8_t *A, long lda,
+                                 const int8_t *B, long ldb, const int32_t *col_off,
+                                 const float *sa, const float *sb, void *C, long ldc,
+                                 hipStream_t stream) {
+    const int nblk = ((M + 127) / 128) * ((N + 127) / 128);
+    if (nblk == 0 || K / IG_BK == 0) return hipSuccess;
+    const dim3 grid(nblk), block(64 * (8 + NWP));
+    const bool nt = (long)M * N * 4 <= (256L << 20);  // as in launch_wp_band
+    auto go = [&](auto NT) {
+        constexpr int nts = decltype(NT)::value;
+        switch (out_mode) {
+            case 0:
+                hipLaunchKernelGGL((igemm_kg_kernel<STAGES, NWP, KGR, 0, nts>), grid, block, 0, stream, A, lda, B,
+                                   ldb, col_off, sa, sb, C, ldc, M, N, K);
+                break;
+            case 1:
+                hipLaunchKernelGGL((igemm_kg_kernel<STAGES, NWP, KGR, 1, nts>), grid, block, 0, stream, A, lda, B,
+                                   ldb, col_off, sa, sb, C, ldc, M, N, K);
+                break;
+            default:
+                hipLaunchKernelGGL((igemm_kg_kernel<STAGES, NWP, KGR, 2, nts>), grid, block, 0, stream, A, lda, B,
+                                   ldb, col_off, sa, sb, C, ldc, M, N, K);
+                break;
+        }
+    };
+    if (nt) go(IC<1>{});
+    else go(IC<0>{});
+    return hipGetLastError();
+}
+
+// 32-bit per-lane DMA offsets: row bands of A and column bands of B whose
+// byte spans stay below 2^31 (as launch_split).
+template <int STAGES, int NWP, int KGR>
+static hipError_t launch_kg(int out_mode, int M, int N, int K, const uint8_t *A, long lda,
+                            const int8_t *B, long ldb, const int32_t *col_off, const float *sa,
+                            const float *sb, void *C, long ldc, hipStream_t stream) {
+    const long LIM = 1L << 31;
+    long mband = lda > 0 ? LIM / lda : M, nband = ldb > 0 ? LIM / ldb : N;
+    mband = mband >= M ? M : (mband / 128) * 128;
+    nband = nband >= N ? N : (nband / 128) * 128;
+    if (mband <= 0 || nband <= 0) return hipErrorInvalidValue;
+    for (long m = 0; m < M; m += mband) {
+        for (long n = 0; n < N; n += nband) {
+            const int mm = (int)(M - m < mband ? M - m : mband);
+            const int nn = (int)(N - n < nband ? N - n : nband);
+            hipError_t e = launch_kg_band<STAGES, NWP, KGR>(
+                out_mode, mm, nn, K, A + m * lda, lda, B + n * ldb, ldb, col_off ? col_off + n : nullptr,
+                sa ? sa + m : nullptr, sb ? sb + n : nullptr, (char *)C + (m * ldc + n) * 4, ldc, stream);
             if (e != hipSuccess) return e;
         }
     }
@@ -780,7 +1136,12 @@ hipError_t launch_igemm(int out_mode, int M, int N, int K, const uint8_t *A, lon
     //    (K = 1024 projections: fewer operand bytes per output); 256x192 when
     //    those fill the CUs clearly better (4096 x 3072: 256 tiles, one round,
     //    against 192 of 256x256; +2.5-2.8% on that shape, bit-identical);
-    //  * producer/consumer 128x128 tiles when those fill the chip;
+    //  * one round of 128x128 tiles (2048^3, the K = 4096 down projection,
+    //    the attention output projection): igemm_kg_kernel, one tile per
+    //    workgroup (same-box alternation against the persistent kernel:
+    //    2048^3 12.18 against 12.60 us, FF2 19.02 against 20.75 us);
+    //  * producer/consumer 128x128 tiles when those fill the chip over
+    //    several rounds;
     //  * 64x64 otherwise, and for K = 0 (the epilogue alone).
     const long t256 = (long)((M + 255) / 256) * ((N + 255) / 256);
     const long t128 = (long)((M + 127) / 128) * ((N + 127) / 128);
@@ -798,6 +1159,14 @@ hipError_t launch_igemm(int out_mode, int M, int N, int K, const uint8_t *A, lon
                                                       sb, C, ldc, stream);
         return launch_split<256, 256, 4, 2, 2, 1>(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa,
                                                   sb, C, ldc, stream);
+    }
+    // one round of 128x128 tiles (about one per CU): the K-grouped 16x16x64
+    // kernel, two K groups once K is long (K >= 4096: a third fewer LDS
+    // fragment bytes per K tile, one exchange at the end), one otherwise
+    if (K > 0 && t128 >= 256 && t128 <= device_cus()) {
+        if (K >= 4096)
+            return launch_kg<4, 4, 2>(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa, sb, C, ldc, stream);
+        return launch_kg<4, 2, 1>(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa, sb, C, ldc, stream);
     }
     if (K > 0 && t128 >= 256)
         return launch_wp<128, 128, 4, 2, 3>(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa, sb, C,

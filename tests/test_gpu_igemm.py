@@ -289,6 +289,48 @@ def test_igemm_ragged_large_tiles(M, N, K):
     np.testing.assert_array_equal(C, ref.astype(np.int64))
 
 
+def _exact_f64(Au, Bq):
+    # float64 products of these integers are exact (every partial sum stays
+    # far below 2**53), so BLAS gives the whole int32 result
+    return ((Au.astype(np.float64) - 128) @ Bq.astype(np.float64)).astype(np.int64)
+
+
+def test_igemm_headline_full_compare():
+    # BASELINE.json configs[1] (gemm_bench INT8, M = N = K = 2048): every
+    # output compared, int32 and dequantised (per-row x per-column scales ~
+    # U[1e-3, 1e-2], gemm_bench.c:272-275), not only sampled rows
+    M = N = K = 2048
+    Au = ob.u8((M, K), 100)
+    Bq = ob.s8((K, N), 101)
+    sa = ob.uniform((M,), 102, 1e-3, 1e-2)
+    sb = ob.uniform((N,), 103, 1e-3, 1e-2)
+    announce("igemm headline full", M, N, K)
+    V = _exact_f64(Au, Bq)
+    np.testing.assert_array_equal(igemm_i32(Au, Bq), V)
+    np.testing.assert_array_equal(_dq_run(Au, Bq, sa, sb), ob.dequant(V.astype(np.int32), sa, sb))
+
+
+# One round of 128x128 tiles (256 tiles on 256 CUs) runs the K-grouped
+# 16x16x64 kernel: one K group below K = 4096, two from there on. Exact and
+# ragged extents in M, N and K (K padded to 256 by the host entry point),
+# every output compared, int32 and dequantised with per-row and per-column
+# scales and column offsets.
+@pytest.mark.parametrize("M,N,K", [(4096, 1024, 1024), (2000, 2040, 2064), (4096, 1024, 4096),
+                                   (4000, 1000, 4100), (2040, 1985, 8192)])
+def test_igemm_one_round_tiles_full_compare(M, N, K):
+    Au = ob.u8((M, K), 110 + K % 97)
+    Bq = ob.s8((K, N), 111 + N % 89)
+    sa = ob.uniform((M,), 112, 1e-3, 1e-2)
+    sb = ob.uniform((N,), 113, 1e-3, 1e-2)
+    off = ob.s8((N,), 114).astype(np.int32) * 1000
+    announce("igemm one round", M, N, K)
+    V = _exact_f64(Au, Bq)
+    np.testing.assert_array_equal(igemm_i32(Au, Bq), V)
+    V32 = V.astype(np.int32)
+    np.testing.assert_array_equal(_dq_run(Au, Bq, sa, sb, off), ob.dequant((V32 + off).astype(np.int32), sa, sb))
+    np.testing.assert_array_equal(_dq_run(Au, Bq, None, sb), ob.dequant(V32, None, sb))
+
+
 def test_quantizers_byte_exact():
     M, K, N = 96, 250, 80
     A = ob.normal((M, K), 70)
