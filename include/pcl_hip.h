@@ -75,12 +75,26 @@ int pcl_stream_synchronize(void);
  *     graphs captured on it first.
  *   pcl_graph_begin/end: capture this thread's native device-pointer calls on
  *     its stream (which must come from pcl_stream_create) into *graph; the
- *     calls are recorded, not run. Host-pointer drop-ins cannot be captured.
+ *     calls are recorded, not run. Host-pointer drop-ins cannot be captured:
+ *     while the thread's stream captures (through pcl_graph_begin or the
+ *     caller's own hipStreamBeginCapture) they fail with
+ *     PCL_ERR_INVALID_ARG before touching the stream.
  *   pcl_graph_launch: replay on this thread's stream. Every replay uses the
  *     pointers and sizes recorded at capture time; scratch used by a graph
  *     stays allocated until its stream is destroyed. */
 void *pcl_stream_create(void);
 int pcl_stream_destroy(void *stream);
+/* Scratch memory. Calls keep per-stream device buffers that grow to the
+ * largest request and are reused: split-K partial sums, the padded INT8
+ * activations, pcl_head_ce's logits chunk, and the realigned copies of
+ * misaligned FP32 operands that pcl_sgemm makes for products of >= 2^30
+ * multiply-adds (for the trainer's head backward over 4096 x 50257 logits
+ * about 0.8 GB). pcl_release_scratch waits for the stream (hip_stream, NULL =
+ * null stream) and frees these buffers; the next call allocates again. It
+ * fails with PCL_ERR_INVALID_ARG on a stream a graph was captured on (the
+ * graph may use them; pcl_stream_destroy frees them). Calls on the stream
+ * from other threads must not overlap it. No counterpart in the reference. */
+int pcl_release_scratch(void *hip_stream);
 int pcl_graph_begin(void);
 int pcl_graph_end(void **graph);
 int pcl_graph_launch(void *graph);
@@ -411,10 +425,11 @@ typedef struct pcl_gemv_group pcl_gemv_group;
  * the group's only allocation. Beyond the single calls it needs 1 <= M <= 8,
  * K >= 1, 16-byte aligned W with ldw % 4 == 0 and N % 4 == 0 (F32_N) or
  * K % 4 == 0 (F32_T), packed rows of ldw >= pcl_s8_kpad(K) (U8S8), and staged
- * activations of at most 64 KB: M' * 4 * K floats for fp32, M' * K bytes for
- * U8S8, with M' the group's largest M rounded up to 1, 2, 4 or 8 (PCL_ERR_RANGE
- * otherwise). The descriptors' pointers are kept: the buffers must outlive the
- * group. */
+ * operands within 112 KB of LDS per block: M' * K' * 4 bytes for fp32 (K'
+ * = K rounded up to 64 for F32_T, to 128 for F32_N), M' * (pcl_s8_kpad(K) +
+ * 16) + 16384 bytes for U8S8, with M' the group's largest M rounded up to 1,
+ * 2, 4 or 8 (PCL_ERR_RANGE otherwise, at creation). The descriptors' pointers
+ * are kept: the buffers must outlive the group. */
 int pcl_gemv_group_create(const pcl_gemv_desc *descs, int n, pcl_gemv_group **group);
 /* One launch computing every product of the group (asynchronous on stream). */
 int pcl_gemv_group_run(const pcl_gemv_group *group, void *stream);

@@ -130,8 +130,13 @@ int do_init() {
 struct StreamScratch {
     std::recursive_mutex call_mu;  // recursive: a call may nest another on the stream
     pcl::Workspace ws;
-    void *aux = nullptr;  // padded INT8 activations
+    void *aux = nullptr;  // padded INT8 activations; head_ce's logits chunk and row losses
     size_t aux_cap = 0;
+    // Realigned copies of misaligned FP32 GEMM operands (sgemm_realigned).
+    // Kept apart from aux: pcl_head_ce holds its logits chunk in aux while it
+    // calls pcl_sgemm, which may realign on the same stream.
+    void *realign = nullptr;
+    size_t realign_cap = 0;
     unsigned *amax = nullptr;  // per-tensor amax bits
     // Set once a graph has been captured on the stream: buffers a graph may
     // reference are never freed before the stream is destroyed.
@@ -167,7 +172,8 @@ int grow(void **p, size_t *cap, size_t need, hipStream_t s, StreamScratch &sc) {
     return PCL_OK;
 }
 
-int get_scratch(hipStream_t s, size_t part_bytes, size_t aux_bytes, ScratchLease *out) {
+int get_scratch(hipStream_t s, size_t part_bytes, size_t aux_bytes, ScratchLease *out,
+                size_t realign_bytes = 0) {
     StreamScratch *entry;
     {
         std::lock_guard<std::mutex> lk(g_mu);
@@ -178,6 +184,7 @@ int get_scratch(hipStream_t s, size_t part_bytes, size_t aux_bytes, ScratchLease
     StreamScratch &sc = *entry;
     PCL_OK_OR_RETURN(grow(&sc.ws.buf, &sc.ws.bytes_cap, part_bytes, s, sc));
     PCL_OK_OR_RETURN(grow(&sc.aux, &sc.aux_cap, aux_bytes, s, sc));
+    PCL_OK_OR_RETURN(grow(&sc.realign, &sc.realign_cap, realign_bytes, s, sc));
     if (!sc.amax) {
         if (hipMalloc((void **)&sc.amax, 256) != hipSuccess)
             return set_error(PCL_ERR_OOM, "amax scratch allocation failed");
@@ -227,14 +234,42 @@ int kpad256(int K) { return ((K + 255) / 256) * 256; }
 
 // ------------------------------------------------------- host staging ----
 // Device copies of host operands for the host-pointer drop-ins; one growing
-// buffer per slot per thread, kept for the life of the process.
+// buffer per slot per thread, freed when the thread exits (its last calls
+// ended with a synchronisation, so no kernel still reads them).
 struct HostStage {
     void *p[8] = {nullptr};
     size_t cap[8] = {0};
+    ~HostStage() {
+        for (void *q : p)
+            if (q) (void)hipFree(q);
+    }
 };
 thread_local HostStage t_stage;
 
+// This thread's stream is being captured: by pcl_graph_begin, or by the
+// caller's own hipStreamBeginCapture on the stream it handed to pcl_set_stream.
+thread_local bool t_capturing = false;
+
+// Host-pointer drop-ins copy operands through the staging slots and wait for
+// the stream: neither can be recorded into a graph (the copies would read the
+// host buffers at replay time, the wait would end the capture). They refuse
+// while the stream captures; every one of them stages through here first.
+int refuse_capture() {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (!t_capturing && t_stream != nullptr && hipStreamIsCapturing(t_stream, &cs) != hipSuccess) {
+        (void)hipGetLastError();
+        cs = hipStreamCaptureStatusNone;
+    }
+    if (t_capturing || cs != hipStreamCaptureStatusNone)
+        return set_error(PCL_ERR_INVALID_ARG,
+                         "host-pointer drop-ins cannot run while this thread's stream is being captured "
+                         "(they copy host operands and wait for the stream); call them outside "
+                         "pcl_graph_begin/pcl_graph_end, or capture the device-pointer entry points");
+    return PCL_OK;
+}
+
 int stage_buf(int slot, size_t bytes, void **out) {
+    PCL_OK_OR_RETURN(refuse_capture());
     if (bytes == 0) bytes = 16;
     if (bytes > t_stage.cap[slot]) {
         if (t_stage.p[slot]) {
@@ -256,6 +291,7 @@ int stage_buf(int slot, size_t bytes, void **out) {
 // Upload `bytes` from host `src` into staging slot `slot` (src may be NULL:
 // then *dev is NULL too, for optional operands such as bias).
 int upload(int slot, const void *src, size_t bytes, void **dev) {
+    PCL_OK_OR_RETURN(refuse_capture());
     if (!src) {
         *dev = nullptr;
         return PCL_OK;
@@ -345,12 +381,45 @@ int pcl_stream_destroy(void *stream) {
             for (void *q : sc.retired) HIP_OK(hipFree(q));
             if (sc.ws.buf) HIP_OK(hipFree(sc.ws.buf));
             if (sc.aux) HIP_OK(hipFree(sc.aux));
+            if (sc.realign) HIP_OK(hipFree(sc.realign));
             if (sc.amax) HIP_OK(hipFree(sc.amax));
             g_scratch.erase(it);
         }
     }
     if (t_stream == st) t_stream = nullptr;
     HIP_OK(hipStreamDestroy(st));
+    return PCL_OK;
+}
+
+int pcl_release_scratch(void *stream) {
+    PCL_OK_OR_RETURN(do_init());
+    hipStream_t st = (hipStream_t)stream;
+    StreamScratch *entry = nullptr;
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        auto it = g_scratch.find(st);
+        if (it == g_scratch.end()) return PCL_OK;
+        entry = &it->second;  // map nodes keep their address
+    }
+    // a call in flight on the stream holds its call lock until its last launch
+    std::lock_guard<std::recursive_mutex> call(entry->call_mu);
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (entry->pinned)
+        return set_error(PCL_ERR_INVALID_ARG,
+                         "pcl_release_scratch: a graph was captured on this stream and may use its "
+                         "scratch; it is freed by pcl_stream_destroy");
+    HIP_OK(hipStreamSynchronize(st));
+    void **bufs[3] = {&entry->ws.buf, &entry->aux, &entry->realign};
+    size_t *caps[3] = {&entry->ws.bytes_cap, &entry->aux_cap, &entry->realign_cap};
+    for (int i = 0; i < 3; i++) {
+        if (*bufs[i]) HIP_OK(hipFree(*bufs[i]));
+        *bufs[i] = nullptr;
+        *caps[i] = 0;
+    }
+    for (void *q : entry->retired) HIP_OK(hipFree(q));
+    entry->retired.clear();
+    if (entry->amax) HIP_OK(hipFree(entry->amax));
+    entry->amax = nullptr;
     return PCL_OK;
 }
 
@@ -363,6 +432,7 @@ int pcl_graph_begin(void) {
         g_scratch[t_stream].pinned = true;
     }
     HIP_OK(hipStreamBeginCapture(t_stream, hipStreamCaptureModeRelaxed));
+    t_capturing = true;
     return PCL_OK;
 }
 
@@ -371,6 +441,7 @@ int pcl_graph_end(void **graph) {
     PCL_OK_OR_RETURN(do_init());
     CHECK_ARG(t_stream != nullptr, "pcl_graph_end: this thread's stream is the null stream");
     hipGraph_t g = nullptr;
+    t_capturing = false;
     HIP_OK(hipStreamEndCapture(t_stream, &g));
     hipGraphExec_t ge = nullptr;
     hipError_t e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
@@ -704,14 +775,14 @@ static int sgemm_realigned(int opA, int opB, int M, int N, int K, const float *A
     if (M > M1 && pm.part_bytes > part) part = pm.part_bytes;
     if (N > N1 && pn.part_bytes > part) part = pn.part_bytes;
     ScratchLease sc;
-    PCL_OK_OR_RETURN(get_scratch(s, part, abytes + bbytes + 256, &sc));
+    PCL_OK_OR_RETURN(get_scratch(s, part, 0, &sc, abytes + bbytes + 256));
     float *Ac = const_cast<float *>(A), *Bc = const_cast<float *>(B);
     if (copy_a) {
-        Ac = static_cast<float *>(sc->aux);
+        Ac = static_cast<float *>(sc->realign);
         HIP_OK(pcl::launch_copy_rows(Ac, lda2, A, lda, (int)rows_a, (int)cols_a, s));
     }
     if (copy_b) {
-        Bc = reinterpret_cast<float *>(static_cast<char *>(sc->aux) + (abytes + 255) / 256 * 256);
+        Bc = reinterpret_cast<float *>(static_cast<char *>(sc->realign) + (abytes + 255) / 256 * 256);
         HIP_OK(pcl::launch_copy_rows(Bc, ldb2, B, ldb, (int)rows_b, (int)cols_b, s));
     }
     // the aligned core, then its K tail added on
@@ -1519,8 +1590,8 @@ static int host_cross_entropy(const float *logits, const int *targets, float *d_
     PCL_OK_OR_RETURN(upload(S_A, logits, lb, &dl));
     PCL_OK_OR_RETURN(upload(S_B, targets, sizeof(int) * (size_t)M, &dt));
     PCL_OK_OR_RETURN(stage_buf(S_C, lb, &dd));
-    PCL_OK_OR_RETURN(stage_buf(S_D, sizeof(float), &dloss));
-    HIP_OK(hipMemsetAsync(dloss, 0, sizeof(float), t_stream));
+    static const float zero = 0.f;  // the loss is added into this slot
+    PCL_OK_OR_RETURN(upload(S_D, &zero, sizeof(float), &dloss));
     PCL_OK_OR_RETURN(pcl_cross_entropy((const float *)dl, V, (const int *)dt, (float *)dd, V, M, V,
                                        (float *)dloss, t_stream));
     PCL_OK_OR_RETURN(download(d_logits, dd, lb));

@@ -54,6 +54,7 @@ _PROTOS = {
     "pcl_stream_synchronize": (_i, []),
     "pcl_stream_create": (_vp, []),
     "pcl_stream_destroy": (_i, [_vp]),
+    "pcl_release_scratch": (_i, [_vp]),
     "pcl_graph_begin": (_i, []),
     "pcl_graph_end": (_i, [C.POINTER(_vp)]),
     "pcl_graph_launch": (_i, [_vp]),

@@ -252,3 +252,21 @@ def test_head_ce_350m_full_size():
     assert rel(dx_c, dx) <= FP32_TOL
     assert rel(dw_c, dw) <= FP32_TOL
     assert np.log(V) * 0.5 < loss < np.log(V) * 2
+
+
+def test_head_ce_realigned_operands():
+    # D % 4 != 0 (rows not 16-byte aligned) and chunk products of >= 2^30
+    # multiply-adds: the logits, d_lnf and dwte products copy their misaligned
+    # operands into the stream's realign buffer while the logits chunk and the
+    # row losses stay in the head's own scratch; two chunks of 256 rows
+    M, D, V = 512, 1022, 8192
+    announce("head_ce realigned", M, D, V)
+    x = ob.normal((M, D), 1700, 0.0, 1.0)
+    w = ob.normal((V, D), 1701, 0.0, 0.05)
+    t = (ob.u8((M,), 1702).astype(np.int64) * 7919 % V).astype(np.int32)
+    dw0 = ob.normal((V, D), 1703, 0.0, 1e-3)
+    loss, dx, dw = _head(x, w, t, dw0, 256 * V * 4)
+    loss64, dx64, dw64 = _head64(x, w, t, dw0)
+    assert loss == pytest.approx(loss64, rel=LOSS_RTOL)
+    assert rel(dx, dx64) <= FP32_TOL
+    assert rel(dw - dw0, dw64 - dw0) <= FP32_TOL

@@ -9,6 +9,8 @@ The groups cover the grown-model decode sweep (16 laye
 QKV 512x1536, O 512x512, FF1 512x2048, FF2 2048x512 and the 2048-vocab head)
 at M = 1, 4, 8, mixed kinds in one launch, ragged N and K, and repeated runs.
 """
+import ctypes as C
+
 import numpy as np
 import pytest
 
@@ -181,3 +183,30 @@ def test_group_head_350m_int8():
     run_group(prods)
     for q in prods:
         q.check()
+
+
+def test_group_staging_beyond_64kb():
+    # staged activations above 64 KB of LDS (the limit is 112 KB per block):
+    # fp32 N x K weights with 8 rows of K = 3072 stage 96 KB; INT8 8 rows of
+    # K = 8192 stage 8 * (8192 + 16) bytes plus the 16 KB operand regions
+    prods = [Product(pcl.GEMV_F32_T, 8, 3072, 1000, 6000, bias=True),
+             Product(pcl.GEMV_F32_T, 7, 3000, 333, 6010, accumulate=True)]
+    announce("gemv group 96 KB staging")
+    run_group(prods)
+    for q in prods:
+        q.check()
+    prods = [Product(pcl.GEMV_U8S8, 8, 8192, 700, 6020, mode=2, col_off=True)]
+    announce("gemv group int8 82 KB staging")
+    run_group(prods)
+    for q in prods:
+        q.check()
+
+
+def test_group_staging_limit_is_reported():
+    # beyond 112 KB per block: PCL_ERR_RANGE at creation, before any launch
+    q = Product(pcl.GEMV_F32_T, 8, 4096, 16, 6030)
+    grp = C.c_void_p()
+    arr = (pcl.GemvDesc * 1)(q.desc)
+    st = pcl.lib.pcl_gemv_group_create(arr, 1, C.byref(grp))
+    assert st == pcl.PCL_ERR_RANGE, st
+    assert b"LDS" in pcl.lib.pcl_last_error()

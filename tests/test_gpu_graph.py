@@ -135,3 +135,70 @@ def test_graph_replays_match_eager(stream, warm):
 def test_graph_needs_a_created_stream():
     pcl.check(pcl.lib.pcl_set_stream(None))
     assert pcl.lib.pcl_graph_begin() == pcl.PCL_ERR_INVALID_ARG
+
+
+def test_host_dropins_refuse_under_capture(stream):
+    # host-pointer drop-ins copy host operands and wait for the stream: while
+    # the thread's stream captures they fail before touching it, the capture
+    # stays valid, and they run again once it has ended
+    announce("graph host drop-in refusal")
+    M, K, N = 64, 32, 48
+    A = ob.uniform((M, K), 20, -1, 1).astype(np.float32)
+    B = ob.uniform((K, N), 21, -1, 1).astype(np.float32)
+    Cout = np.full((M, N), np.nan, np.float32)
+    dA, dB, dC = pcl.dev(A), pcl.dev(B), pcl.empty((M, N), np.float32)
+    pcl.check(pcl.lib.pcl_graph_begin())
+    try:
+        pcl.lib.matmul(pcl.ptr(A), pcl.ptr(B), pcl.ptr(Cout), M, K, N)
+        assert pcl.lib.pcl_last_status() == pcl.PCL_ERR_INVALID_ARG
+        assert b"captured" in pcl.lib.pcl_last_error()
+        assert np.isnan(Cout).all()
+        pcl.check(pcl.lib.pcl_set_model_dims(N, N))
+        lg = ob.normal((4, N), 22)
+        t = np.arange(4, dtype=np.int32)
+        dl = np.full_like(lg, np.nan)
+        pcl.lib.cross_entropy(pcl.ptr(lg), pcl.ptr(t), pcl.ptr(dl), 4)
+        assert pcl.lib.pcl_last_status() == pcl.PCL_ERR_INVALID_ARG
+        # a native call is still recorded into the same capture
+        pcl.check(pcl.lib.pcl_sgemm(OP_N, OP_N, M, N, K, dA.ptr, K, dB.ptr, N, None, 0, dC.ptr, N, None))
+    finally:
+        g = C.c_void_p()
+        pcl.check(pcl.lib.pcl_graph_end(C.byref(g)))
+    try:
+        pcl.check(pcl.lib.pcl_graph_launch(g))
+        pcl.sync()
+        pcl.lib.matmul(pcl.ptr(A), pcl.ptr(B), pcl.ptr(Cout), M, K, N)
+        pcl.check_void()
+        np.testing.assert_array_equal(dC.download((M, N), np.float32), Cout)
+        assert np.abs(Cout - A.astype(np.float64) @ B).max() <= 1e-4 * np.abs(Cout).max()
+    finally:
+        pcl.check(pcl.lib.pcl_graph_destroy(g))
+
+
+def test_release_scratch(stream):
+    # split-K GEMV workspace released and grown again: same bits; a stream a
+    # graph was captured on keeps its scratch (the graph may use it)
+    announce("release scratch")
+    x = pcl.dev(ob.uniform((8, 8192), 30, -1, 1).astype(np.float32))
+    W = pcl.dev(ob.uniform((8192, 2048), 31, -0.01, 0.01).astype(np.float32))
+    y = pcl.empty((8, 2048), np.float32)
+
+    def run():
+        pcl.check(pcl.lib.pcl_sgemv(OP_N, 8, 2048, 8192, x.ptr, 8192, W.ptr, 2048, None, 0, y.ptr, 2048, None))
+        pcl.sync()
+        return y.download((8, 2048), np.float32)
+
+    first = run()
+    pcl.check(pcl.lib.pcl_release_scratch(stream))
+    np.testing.assert_array_equal(run(), first)
+    pcl.check(pcl.lib.pcl_graph_begin())
+    pcl.check(pcl.lib.pcl_sgemv(OP_N, 8, 2048, 8192, x.ptr, 8192, W.ptr, 2048, None, 0, y.ptr, 2048, None))
+    g = C.c_void_p()
+    pcl.check(pcl.lib.pcl_graph_end(C.byref(g)))
+    try:
+        assert pcl.lib.pcl_release_scratch(stream) == pcl.PCL_ERR_INVALID_ARG
+        pcl.check(pcl.lib.pcl_graph_launch(g))
+        pcl.sync()
+        np.testing.assert_array_equal(y.download((8, 2048), np.float32), first)
+    finally:
+        pcl.check(pcl.lib.pcl_graph_destroy(g))
