@@ -543,9 +543,17 @@ __global__ __launch_bounds__(GV_THREADS) void igemv_kernel(
             for (int r = 0; r < SGT_RPL; r++)
                 w[u][r] = __builtin_nontemporal_load(reinterpret_cast<const v4i *>(brow[r] + min(k0 + 256 * u, klen - 16)));
     };
-    // the first weight batch is in flight while the activations are staged
+    // the first weight batch is in flight while the activations are staged,
+    // and so are the epilogue operands of this thread's output (o = tid, one
+    // per thread: M * SGT_ROWS <= 256), so the block's life holds one memory
+    // latency rather than two
     v4i wn[UK][SGT_RPL];
     load_batch(wn, 16 * j);
+    const int om = tid / SGT_ROWS, on = min(n0 + tid % SGT_ROWS, N - 1);
+    const bool owns = splits == 1 && tid < M * SGT_ROWS;
+    const float dq_pre = (OUT == 0 || !owns) ? 0.f
+                         : (OUT == 2 ? gbl(sa)[om] * gbl(sb)[on] : gbl(sb)[on]);
+    const unsigned off_pre = (owns && col_off) ? (unsigned)gbl(col_off)[on] : 0u;
 
     stage_rows<MR, true>(reinterpret_cast<uint8_t *>(xs), kchunk, kchunk, min(kchunk, K - kb), M,
                          X + kb, ldx);
@@ -606,10 +614,15 @@ __global__ __launch_bounds__(GV_THREADS) void igemv_kernel(
     __syncthreads();
 
     const int nround = gridDim.x * SGT_ROWS;
-    for (int o = tid; o < M * SGT_ROWS; o += GV_THREADS) {
-        const int m = o / SGT_ROWS, c = o % SGT_ROWS, n = n0 + c;
+    if (tid < M * SGT_ROWS) {
+        const int m = tid / SGT_ROWS, c = tid % SGT_ROWS, n = n0 + c;
         if (splits == 1) {
-            if (n < N) igemv_write<OUT>(Yv, ldy, m, n, res[m][c], col_off, sa, sb);
+            // igemv_write with the operands loaded at the start
+            if (n < N) {
+                const int32_t v = (int32_t)((unsigned)res[m][c] + off_pre);
+                if (OUT == 0) gbl(reinterpret_cast<int32_t *>(Yv))[(long)m * ldy + n] = v;
+                else gbl(reinterpret_cast<float *>(Yv))[(long)m * ldy + n] = (float)v * dq_pre;
+            }
         } else {
             part[((long)sp * M + m) * nround + n] = res[m][c];
         }
@@ -1405,7 +1418,9 @@ __device__ __forceinline__ void gg_u8s8(const GgDesc &d, int strip, int8_t *lds)
 #pragma unroll
         for (int u = 0; u < 4; u++) w[u] = __builtin_nontemporal_load(gvec<v4i>(src[u] + t * GGQ_SL));
     };
-    // the first slice is in flight while the activations are staged
+    // the first slice is in flight while the activations are staged (the
+    // epilogue's scales load at the end: loading them here as well takes 12
+    // more registers, one wave less per SIMD, and was slower)
     v4i wn[4];
     load(wn, 0);
     // one 16-byte load per row per thread and round: rows up to 4 KB stage in one
@@ -1450,16 +1465,16 @@ __device__ __forceinline__ void gg_u8s8(const GgDesc &d, int strip, int8_t *lds)
     }
 }
 
+// Work item b is flat[b]: its product's descriptor with the strip index in
+// `strip`, so a block reaches its operands' addresses with one lookup.
 template <int MR>
-__global__ __launch_bounds__(GV_THREADS) void gemv_group_kernel(const GgDesc *__restrict__ descs,
-                                                                const int2 *__restrict__ items) {
+__global__ __launch_bounds__(GV_THREADS) void gemv_group_kernel(const GgDesc *__restrict__ flat) {
     extern __shared__ __attribute__((aligned(16))) unsigned char gv_dyn[];
     __shared__ float red[4][MR][64];
-    const int2 it = items[blockIdx.x];
-    const GgDesc d = descs[it.x];
-    if (d.kind == GG_F32_N) gg_f32_n<MR>(d, it.y, reinterpret_cast<float *>(gv_dyn), red);
-    else if (d.kind == GG_F32_T) gg_f32_t<MR>(d, it.y, reinterpret_cast<float *>(gv_dyn));
-    else gg_u8s8<MR>(d, it.y, reinterpret_cast<int8_t *>(gv_dyn));
+    const GgDesc d = flat[blockIdx.x];
+    if (d.kind == GG_F32_N) gg_f32_n<MR>(d, d.strip, reinterpret_cast<float *>(gv_dyn), red);
+    else if (d.kind == GG_F32_T) gg_f32_t<MR>(d, d.strip, reinterpret_cast<float *>(gv_dyn));
+    else gg_u8s8<MR>(d, d.strip, reinterpret_cast<int8_t *>(gv_dyn));
 }
 
 // A group whose products are all INT8: the same work items through the
@@ -1467,11 +1482,140 @@ __global__ __launch_bounds__(GV_THREADS) void gemv_group_kernel(const GgDesc *__
 // (58-86 against 124 for the kernel that also carries the fp32 paths) and a
 // SIMD takes five or more of its waves instead of four.
 template <int MR>
-__global__ __launch_bounds__(GV_THREADS) void gemv_group_u8s8_kernel(const GgDesc *__restrict__ descs,
-                                                                     const int2 *__restrict__ items) {
+__global__ __launch_bounds__(GV_THREADS) void gemv_group_u8s8_kernel(const GgDesc *__restrict__ flat) {
     extern __shared__ __attribute__((aligned(16))) unsigned char gv_dyn[];
-    const int2 it = items[blockIdx.x];
-    gg_u8s8<MR>(descs[it.x], it.y, reinterpret_cast<int8_t *>(gv_dyn));
+    const GgDesc d = flat[blockIdx.x];
+    gg_u8s8<MR>(d, d.strip, reinterpret_cast<int8_t *>(gv_dyn));
+}
+
+// GG_U8S8 with one or two activation rows through dot products: the same
+// 64-row strips, 16 lanes per weight row and four rows per 16-lane group;
+// lane j reads bytes 16j + 256u of each row (fully coalesced: a 16-lane group
+// covers 256 contiguous bytes of a row), 512 bytes of K per batch, the next
+// batch in flight while the current one is multiplied, the first one (and
+// the epilogue's scales) before the activations are staged. Products with
+// v_dot4_i32_i8 of the re-centred activations (x ^ 0x80 = x - 128, zero from
+// K to Kp as the packed weights are) are exact in any order; the 16 lanes of
+// a row are then summed by shuffles. With one or two rows the matrix-core
+// path spends more LDS traffic (a transposing round trip of every weight
+// byte) than the products need. (Strips sized to ~32 KB per product -- 16
+// rows at K = 2048 -- were slower on the grown decode sweep: the extra work
+// items no longer fit the chip in one round.)
+constexpr int GGD_RPL = 4;  // rows per 16-lane group
+constexpr int GGD_UK = 2;   // 256-byte K steps per batch
+static_assert(16 * GGD_RPL == GGQ_RB, "the dot path uses the matrix-core path's strips");
+
+template <int MR>
+__device__ __forceinline__ void gg_u8s8_dot(const GgDesc &d, int strip, int8_t *xs) {
+    const int tid = threadIdx.x, j = tid & 15, rs = tid >> 4;
+    const int M = d.M, N = d.N;
+    const int Kp = (d.K + 255) & ~255;  // packed rows are zero from K to Kp (ldw >= Kp)
+    const int xld = Kp + 16;
+    const int n0 = strip * GGQ_RB;
+    const auto B = gbl(static_cast<const int8_t *>(d.W));
+    const __attribute__((address_space(1))) int8_t *wrow[GGD_RPL];
+#pragma unroll
+    for (int r = 0; r < GGD_RPL; r++) wrow[r] = B + (long)min(n0 + rs + 16 * r, N - 1) * d.ldw + 16 * j;
+    // steps k = 256u past Kp are clamped to the last step for the load and
+    // skipped in the products
+    auto load_batch = [&](v4i (&w)[GGD_UK][GGD_RPL], int k0) {
+#pragma unroll
+        for (int u = 0; u < GGD_UK; u++)
+#pragma unroll
+            for (int r = 0; r < GGD_RPL; r++)
+                w[u][r] = __builtin_nontemporal_load(gvec<v4i>(wrow[r] + min(k0 + 256 * u, Kp - 256)));
+    };
+    v4i wn[GGD_UK][GGD_RPL];
+    load_batch(wn, 0);
+    // the epilogue's operands load with the first batch (a block's life is
+    // then one memory latency, not two): column scale and offset of the
+    // group's four rows, row scales
+    float sbv[GGD_RPL], sav[MR];
+    unsigned offv[GGD_RPL];
+#pragma unroll
+    for (int r = 0; r < GGD_RPL; r++) {
+        const int n = min(n0 + rs + 16 * r, N - 1);
+        sbv[r] = d.out_mode != 0 ? gbl(d.sb)[n] : 0.f;
+        offv[r] = d.col_off ? (unsigned)gbl(d.col_off)[n] : 0u;
+    }
+#pragma unroll
+    for (int m = 0; m < MR; m++) sav[m] = d.out_mode == 2 ? gbl(d.sa)[min(m, M - 1)] : 1.f;
+    stage_rows<MR, true, uint8_t, 1>(reinterpret_cast<uint8_t *>(xs), xld, Kp, d.K, M,
+                                     static_cast<const uint8_t *>(d.X), d.ldx);
+    __syncthreads();
+    int32_t acc[GGD_RPL][MR];
+#pragma unroll
+    for (int r = 0; r < GGD_RPL; r++)
+#pragma unroll
+        for (int m = 0; m < MR; m++) acc[r][m] = 0;
+    for (int k0 = 0; k0 < Kp; k0 += 256 * GGD_UK) {
+        v4i w[GGD_UK][GGD_RPL];
+#pragma unroll
+        for (int u = 0; u < GGD_UK; u++)
+#pragma unroll
+            for (int r = 0; r < GGD_RPL; r++) w[u][r] = wn[u][r];
+        if (k0 + 256 * GGD_UK < Kp) load_batch(wn, k0 + 256 * GGD_UK);
+#pragma unroll
+        for (int u = 0; u < GGD_UK; u++) {
+            const int k = k0 + 256 * u;
+            if (k < Kp) {
+                v4i xv[MR];
+#pragma unroll
+                for (int m = 0; m < MR; m++) xv[m] = *reinterpret_cast<const v4i *>(xs + m * xld + k + 16 * j);
+#pragma unroll
+                for (int r = 0; r < GGD_RPL; r++)
+#pragma unroll
+                    for (int m = 0; m < MR; m++) {
+                        int a = acc[r][m];
+                        a = __builtin_amdgcn_sdot4(xv[m][0], w[u][r][0], a, false);
+                        a = __builtin_amdgcn_sdot4(xv[m][1], w[u][r][1], a, false);
+                        a = __builtin_amdgcn_sdot4(xv[m][2], w[u][r][2], a, false);
+                        a = __builtin_amdgcn_sdot4(xv[m][3], w[u][r][3], a, false);
+                        acc[r][m] = a;
+                    }
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < GGD_RPL; r++)
+#pragma unroll
+        for (int m = 0; m < MR; m++) {
+            int v = acc[r][m];
+            v += __shfl_xor(v, 8, 16);
+            v += __shfl_xor(v, 4, 16);
+            v += __shfl_xor(v, 2, 16);
+            v += __shfl_xor(v, 1, 16);
+            acc[r][m] = v;
+        }
+    // lane j of a group writes row m = j of its four outputs (rows past M and
+    // outputs past N are not stored), as igemv_write: v + col_off, then
+    // float(v) * dq with dq = sb[n] or sa[m] * sb[n]
+#pragma unroll
+    for (int m = 0; m < MR; m++) {
+        if (j == m && m < M) {
+#pragma unroll
+            for (int r = 0; r < GGD_RPL; r++) {
+                const int n = n0 + rs + 16 * r;
+                if (n < N) {
+                    const int32_t v = (int32_t)((unsigned)acc[r][m] + offv[r]);
+                    const long o = (long)m * d.ldy + n;
+                    if (d.out_mode == 0) {
+                        gbl(reinterpret_cast<int32_t *>(d.Y))[o] = v;
+                    } else {
+                        const float dq = d.out_mode == 2 ? sav[m] * sbv[r] : sbv[r];
+                        gbl(reinterpret_cast<float *>(d.Y))[o] = (float)v * dq;
+                    }
+                }
+            }
+        }
+    }
+}
+
+template <int MR>
+__global__ __launch_bounds__(GV_THREADS) void gemv_group_dot_kernel(const GgDesc *__restrict__ flat) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char gv_dyn[];
+    const GgDesc d = flat[blockIdx.x];
+    gg_u8s8_dot<MR>(d, d.strip, reinterpret_cast<int8_t *>(gv_dyn));
 }
 
 // One product, descriptor by value (no device table): block b = strip b.
@@ -1523,24 +1667,27 @@ size_t gg_lds_bytes(int kind, int K, int mr) {
     return (size_t)mr * gg_stage_ld(kind, K) * 4;
 }
 
-hipError_t launch_gemv_group(const GgDesc *descs, const int2 *items, int n_items, int mr,
+hipError_t launch_gemv_group(const GgDesc *flat, int n_items, int mr,
                              size_t lds_bytes, bool all_u8s8, hipStream_t s) {
     if (n_items <= 0) return hipSuccess;
     const dim3 grid(n_items), block(GV_THREADS);
     if (all_u8s8) {
+        // one or two rows: dot products (the staging is the same as the
+        // matrix-core path's, without its 16 KB of per-wave regions)
+        const size_t dot_lds = lds_bytes > 4 * (size_t)GGQ_WREG ? lds_bytes - 4 * (size_t)GGQ_WREG : lds_bytes;
         switch (mr) {
-            case 1: hipLaunchKernelGGL(gemv_group_u8s8_kernel<1>, grid, block, lds_bytes, s, descs, items); break;
-            case 2: hipLaunchKernelGGL(gemv_group_u8s8_kernel<2>, grid, block, lds_bytes, s, descs, items); break;
-            case 4: hipLaunchKernelGGL(gemv_group_u8s8_kernel<4>, grid, block, lds_bytes, s, descs, items); break;
-            default: hipLaunchKernelGGL(gemv_group_u8s8_kernel<8>, grid, block, lds_bytes, s, descs, items); break;
+            case 1: hipLaunchKernelGGL(gemv_group_dot_kernel<1>, grid, block, dot_lds, s, flat); break;
+            case 2: hipLaunchKernelGGL(gemv_group_dot_kernel<2>, grid, block, dot_lds, s, flat); break;
+            case 4: hipLaunchKernelGGL(gemv_group_u8s8_kernel<4>, grid, block, lds_bytes, s, flat); break;
+            default: hipLaunchKernelGGL(gemv_group_u8s8_kernel<8>, grid, block, lds_bytes, s, flat); break;
         }
         return hipGetLastError();
     }
     switch (mr) {
-        case 1: hipLaunchKernelGGL(gemv_group_kernel<1>, grid, block, lds_bytes, s, descs, items); break;
-        case 2: hipLaunchKernelGGL(gemv_group_kernel<2>, grid, block, lds_bytes, s, descs, items); break;
-        case 4: hipLaunchKernelGGL(gemv_group_kernel<4>, grid, block, lds_bytes, s, descs, items); break;
-        default: hipLaunchKernelGGL(gemv_group_kernel<8>, grid, block, lds_bytes, s, descs, items); break;
+        case 1: hipLaunchKernelGGL(gemv_group_kernel<1>, grid, block, lds_bytes, s, flat); break;
+        case 2: hipLaunchKernelGGL(gemv_group_kernel<2>, grid, block, lds_bytes, s, flat); break;
+        case 4: hipLaunchKernelGGL(gemv_group_kernel<4>, grid, block, lds_bytes, s, flat); break;
+        default: hipLaunchKernelGGL(gemv_group_kernel<8>, grid, block, lds_bytes, s, flat); break;
     }
     return hipGetLastError();
 }

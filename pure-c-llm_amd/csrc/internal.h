@@ -137,11 +137,12 @@ hipError_t measure_bandwidth(long bytes_per_array, double gbs[4], hipStream_t s)
 // ---- GEMV (gemv.hip) ----
 GemvPlan plan_sgemv(int w_trans, int M, int N, int K);
 // Grouped GEMV: one launch over independent products. Device descriptor of
-// one product (validated by the shim); out_mode of GG_U8S8: 0 int32, 1
-// float(v)*sb[n], 2 float(v)*(sa[m]*sb[n]); xld: staged activation row stride
-// (elements) = gg_stage_ld(kind, K). Work items are int2 {product, strip} with
-// strips of gg_strip_rows(kind) outputs; lds_bytes = max over products of
-// gg_lds_bytes(kind, K, mr); mr in {1, 2, 4, 8} >= every product's M.
+// one product's work item (validated by the shim); out_mode of GG_U8S8: 0
+// int32, 1 float(v)*sb[n], 2 float(v)*(sa[m]*sb[n]); xld: staged activation
+// row stride (elements) = gg_stage_ld(kind, K); strip: the item's strip of
+// gg_strip_rows(kind) outputs. The launch takes one descriptor per work item;
+// lds_bytes = max over products of gg_lds_bytes(kind, K, mr); mr in {1, 2, 4,
+// 8} >= every product's M.
 enum { GG_F32_N = 0, GG_F32_T = 1, GG_U8S8 = 2 };
 struct GgDesc {
     int kind, M, N, K;
@@ -154,14 +155,15 @@ struct GgDesc {
     const float *sa, *sb;
     void *Y;
     long ldy;
-    int accumulate, out_mode, xld, pad_;
+    int accumulate, out_mode, xld;
+    int strip;  // the work item's strip (one descriptor per work item)
 };
 int gg_strip_rows(int kind);
 int gg_stage_ld(int kind, int K);
 // dynamic LDS a product needs in a group whose largest M rounds to mr
 size_t gg_lds_bytes(int kind, int K, int mr);
 // all_u8s8: every product is GG_U8S8 (a kernel with only that path)
-hipError_t launch_gemv_group(const GgDesc *descs, const int2 *items, int n_items, int mr,
+hipError_t launch_gemv_group(const GgDesc *flat, int n_items, int mr,
                              size_t lds_bytes, bool all_u8s8, hipStream_t s);
 // One INT8 GEMV (M <= 8 rows) on the matrix-core path of the grouped kernel:
 // whole-K blocks of 64 weight rows, no split, no workspace. Applicable when

@@ -330,8 +330,7 @@ int sgemv_xf(int xf, int N, int K, const float *X, const float *W, int ldw,
 }  // namespace pcl
 
 struct pcl_gemv_group {
-    pcl::GgDesc *d_descs = nullptr;
-    int2 *d_items = nullptr;
+    pcl::GgDesc *d_flat = nullptr;  // one descriptor per work item (strip in .strip)
     int n_items = 0, mr = 1;
     bool all_u8s8 = false;
     size_t lds = 0;
@@ -647,14 +646,19 @@ int pcl_gemv_group_create(const pcl_gemv_desc *descs, int n, pcl_gemv_group **gr
         g.accumulate = q.kind == PCL_GEMV_U8S8 ? 0 : (q.accumulate ? 1 : 0);
         g.out_mode = q.kind != PCL_GEMV_U8S8 ? 0 : (!q.sb ? 0 : (q.sa ? 2 : 1));
         g.xld = pcl::gg_stage_ld(g.kind, q.K);
-        g.pad_ = 0;
+        g.strip = 0;
         const int m1 = q.M <= 1 ? 1 : (q.M <= 2 ? 2 : (q.M <= 4 ? 4 : 8));
         if (m1 > mr) mr = m1;
         CHECK_ARG((long)q.N * q.ldw < (1L << 31),
                   "pcl_gemv_group_create: product %d: N * ldw must stay below 2^31 bytes", i);
+    }
+    const bool all_u8s8 =
+        std::all_of(dd.begin(), dd.end(), [](const pcl::GgDesc &q) { return q.kind == pcl::GG_U8S8; });
+    for (int i = 0; i < n; i++) {
+        const pcl::GgDesc &g = dd[(size_t)i];
         const int rows = pcl::gg_strip_rows(g.kind);
-        const int strips = (q.N + rows - 1) / rows;
-        const long bytes = (long)rows * (q.kind == PCL_GEMV_U8S8 ? g.ldw : 4L * q.K);
+        const int strips = (g.N + rows - 1) / rows;
+        const long bytes = (long)rows * (g.kind == pcl::GG_U8S8 ? g.ldw : 4L * g.K);
         for (int t = 0; t < strips; t++) items.push_back({bytes, i, t});
         CHECK_ARG(items.size() < (size_t)(1 << 30), "pcl_gemv_group_create: too many work items");
     }
@@ -670,22 +674,23 @@ int pcl_gemv_group_create(const pcl_gemv_desc *descs, int n, pcl_gemv_group **gr
                          lds, 65536 + 49152);
     // largest blocks first, so the tail of the launch is short ones
     std::stable_sort(items.begin(), items.end(), [](const Item &a, const Item &b) { return a.bytes > b.bytes; });
-    std::vector<int2> it(items.size());
-    for (size_t t = 0; t < items.size(); t++) it[t] = make_int2(items[t].prod, items[t].strip);
+    std::vector<pcl::GgDesc> flat(items.size());
+    for (size_t t = 0; t < items.size(); t++) {
+        flat[t] = dd[(size_t)items[t].prod];
+        flat[t].strip = items[t].strip;
+    }
     PCL_OK_OR_RETURN(do_init());
     pcl_gemv_group *g = new (std::nothrow) pcl_gemv_group();
     if (!g) return set_error(PCL_ERR_OOM, "pcl_gemv_group_create: out of host memory");
-    g->n_items = (int)it.size();
+    g->n_items = (int)flat.size();
     g->mr = mr;
     g->lds = lds;
-    g->all_u8s8 = std::all_of(dd.begin(), dd.end(), [](const pcl::GgDesc &q) { return q.kind == pcl::GG_U8S8; });
-    if (hipMalloc((void **)&g->d_descs, sizeof(pcl::GgDesc) * dd.size()) != hipSuccess ||
-        hipMalloc((void **)&g->d_items, sizeof(int2) * it.size()) != hipSuccess) {
+    g->all_u8s8 = all_u8s8;
+    if (hipMalloc((void **)&g->d_flat, sizeof(pcl::GgDesc) * flat.size()) != hipSuccess) {
         pcl_gemv_group_free(g);
         return set_error(PCL_ERR_OOM, "pcl_gemv_group_create: device allocation failed");
     }
-    if (hipMemcpy(g->d_descs, dd.data(), sizeof(pcl::GgDesc) * dd.size(), hipMemcpyHostToDevice) != hipSuccess ||
-        hipMemcpy(g->d_items, it.data(), sizeof(int2) * it.size(), hipMemcpyHostToDevice) != hipSuccess) {
+    if (hipMemcpy(g->d_flat, flat.data(), sizeof(pcl::GgDesc) * flat.size(), hipMemcpyHostToDevice) != hipSuccess) {
         pcl_gemv_group_free(g);
         return set_error(PCL_ERR_HIP, "pcl_gemv_group_create: copying the plan to the device failed");
     }
@@ -696,15 +701,14 @@ int pcl_gemv_group_create(const pcl_gemv_desc *descs, int n, pcl_gemv_group **gr
 int pcl_gemv_group_run(const pcl_gemv_group *group, void *stream) {
     CHECK_ARG(group != nullptr, "pcl_gemv_group_run: group is NULL");
     PCL_OK_OR_RETURN(do_init());
-    HIP_OK(pcl::launch_gemv_group(group->d_descs, group->d_items, group->n_items, group->mr, group->lds,
+    HIP_OK(pcl::launch_gemv_group(group->d_flat, group->n_items, group->mr, group->lds,
                                   group->all_u8s8, pick(stream)));
     return PCL_OK;
 }
 
 void pcl_gemv_group_free(pcl_gemv_group *group) {
     if (!group) return;
-    if (group->d_descs) (void)hipFree(group->d_descs);
-    if (group->d_items) (void)hipFree(group->d_items);
+    if (group->d_flat) (void)hipFree(group->d_flat);
     delete group;
 }
 

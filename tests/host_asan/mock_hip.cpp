@@ -181,7 +181,7 @@ GemvPlan plan_sgemv(int, int M, int N, int K) {
 int gg_strip_rows(int kind) { return kind == GG_U8S8 ? 64 : 32; }
 int gg_stage_ld(int, int K) { return (K + 255) / 256 * 256 + 16; }
 size_t gg_lds_bytes(int, int K, int mr) { return (size_t)mr * ((K + 63) / 64 * 64) * 4; }
-hipError_t launch_gemv_group(const GgDesc *, const int2 *, int, int, size_t, bool, hipStream_t) { return hipSuccess; }
+hipError_t launch_gemv_group(const GgDesc *, int, int, size_t, bool, hipStream_t) { return hipSuccess; }
 bool igemv_mfma_fits(int M, int, int, long) { return M >= 3; }
 hipError_t launch_igemv_mfma(int, int M, int N, int, const uint8_t *, long, const int8_t *, long, const int32_t *,
                              const float *, const float *, void *Y, long ldy, hipStream_t) {

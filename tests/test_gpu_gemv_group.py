@@ -210,3 +210,19 @@ def test_group_staging_limit_is_reported():
     st = pcl.lib.pcl_gemv_group_create(arr, 1, C.byref(grp))
     assert st == pcl.PCL_ERR_RANGE, st
     assert b"LDS" in pcl.lib.pcl_last_error()
+
+
+@pytest.mark.parametrize("M", [1, 2])
+def test_group_int8_dot_path_ragged(M):
+    # an all-INT8 group of one or two rows runs the dot-product path: ragged
+    # N (not a multiple of the 64-row strip), K not a multiple of 16 or of
+    # 256, long K, every output form, column offsets
+    prods = [Product(pcl.GEMV_U8S8, M, 100, 33, 7000, mode=1),
+             Product(pcl.GEMV_U8S8, M, 1040, 300, 7010, mode=2, col_off=True),
+             Product(pcl.GEMV_U8S8, M, 2048, 512, 7020, mode=0),
+             Product(pcl.GEMV_U8S8, M, 7, 70, 7030, mode=0, col_off=True),
+             Product(pcl.GEMV_U8S8, M, 8192, 129, 7040, mode=2)]
+    announce("gemv group int8 dot path", M)
+    run_group(prods, repeat=2)
+    for q in prods:
+        q.check()

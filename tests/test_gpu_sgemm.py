@@ -233,3 +233,59 @@ def test_sgemm_350m_sampled(name, opA, opB, M, N, K):
     R = sampled_rows_f64(Arows, B, rows, transB=opB == T_)
     assert rel(C[rows], R) <= FP32_TOL
     assert np.isfinite(C).all()
+
+
+def test_sgemm_grown_prefill_ff1_with_bias():
+    # the grown model's FFN up projection at prefill,
+    # T = 256 tokens of d_model 512 into d_ff 2048 (transformer.c:150,
+    # train.c:524 through matmul_forward, train.c:181-211): activations ~ N(0,1),
+    # weights ~ N(0, 0.02), bias added; every output against the f64 truth and
+    # the reference-order restatement (i-k-j, tensor.c:34-53) plus the bias
+    M, K, N = 256, 512, 2048
+    A = ob.normal((M, K), 610, 0.0, 1.0)
+    W = ob.normal((K, N), 611, 0.0, 0.02)
+    b = ob.normal((N,), 612, 0.0, 0.02)
+    announce("sgemm grown FF1 + bias", M, N, K)
+    C = sgemm(N_, N_, A, W, M, N, K, bias=b)
+    assert rel(C, ob.gemm_f64(A, W, bias=b)) <= FP32_TOL
+    assert rel(C, ob.matmul_ikj(A, W) + b) <= FP32_TOL
+
+
+# The trainer's backward products on the 350M-class shapes (train.c:551-569:
+# matmul_backward for the QKV, attention-output and FFN-down weights; d_model
+# 1024, d_ff 4096, 4 x 1024 tokens), with upstream gradients ~ N(0, 1e-3)
+# accumulated onto existing gradients as
+# train.c's += does: dX = dY . W^T (NT), dW = X^T . dY (TN).
+BWD = [  # name, layout, M, N, K, operand shapes (A, B)
+    ("dX_qkv", N_, T_, 4096, 1024, 3072),
+    ("dW_qkv", T_, N_, 1024, 3072, 4096),
+    ("dX_attn_out", N_, T_, 4096, 1024, 1024),
+    ("dW_attn_out", T_, N_, 1024, 1024, 4096),
+    ("dX_ff2", N_, T_, 4096, 4096, 1024),
+    ("dW_ff2", T_, N_, 4096, 1024, 4096),
+]
+
+
+@pytest.mark.parametrize("name,opA,opB,M,N,K", BWD)
+def test_sgemm_350m_backward_sampled(name, opA, opB, M, N, K):
+    if opA == N_:  # dX: A = dY (M x K gradients), B = W stored N x K
+        A = ob.normal((M, K), 700, 0.0, 1e-3)
+        B = ob.normal((N, K), 701, 0.0, 0.02)
+    else:  # dW: A = X (K tokens x M), B = dY (K x N gradients)
+        A = ob.normal((K, M), 702, 0.0, 1.0)
+        B = ob.normal((K, N), 703, 0.0, 1e-3)
+    C0 = ob.normal((M, N), 704, 0.0, 1e-3)
+    announce("sgemm 350M backward", name, M, N, K)
+    C = sgemm(opA, opB, A, B, M, N, K, C0=C0)
+    rows = np.random.default_rng(5).choice(M, 48, replace=False)
+    Arows = A if opA == N_ else np.ascontiguousarray(A.T)
+    R = sampled_rows_f64(Arows, B, rows, transB=opB == T_) + C0[rows]
+    assert rel(C[rows], R) <= FP32_TOL
+    # the whole product through its row and column sums (f64): 1^T C and C 1
+    Af, Bf = A.astype(np.float64), B.astype(np.float64)
+    Aop = Af if opA == N_ else Af.T
+    Bop = Bf.T if opB == T_ else Bf
+    colsum = Aop.sum(0) @ Bop + C0.astype(np.float64).sum(0)
+    rowsum = Aop @ Bop.sum(1) + C0.astype(np.float64).sum(1)
+    assert rel(C.astype(np.float64).sum(0), colsum) <= FP32_TOL
+    assert rel(C.astype(np.float64).sum(1), rowsum) <= FP32_TOL
