@@ -318,20 +318,44 @@ def _vnni_operands(ob, np, M, N, K, seed):
     return Au, Bp, corr, dq
 
 
+def host_share(threads):
+    """What the host lends this process: the cgroup CPU quota (cpu.max), the
+    load average, and the share of `threads` hardware threads the timed CPU
+    runs actually obtained (process CPU time over wall time x threads). A box
+    whose host is busy with other tenants shows a low share; it is why the
+    same CPU rung reads differently from box to box."""
+    out = {"threads": threads}
+    try:
+        q, per = open("/sys/fs/cgroup/cpu.max").read().split()
+        out["cgroup_cpu_max"] = "unlimited" if q == "max" else round(int(q) / int(per), 2)
+    except (OSError, ValueError):
+        out["cgroup_cpu_max"] = "unreadable"
+    try:
+        out["loadavg_1m"] = round(os.getloadavg()[0], 2)
+    except OSError:
+        pass
+    out["online_cpus"] = os.cpu_count()
+    return out
+
+
 def cpu_reference(M=2048, N=2048, K=2048):
     """The reference's CPU path timed on this host (oracle/_ref builds of
-    gemm_bench.c and tensor.c from source; kind "reference"), best of runs as
-    gemm_bench.c:329-337:
+    gemm_bench.c and tensor.c from source; kind "reference"), best of 6 runs
+    as gemm_bench.c:329-337 (packing and quantisation untimed, :368, 379-381):
       * the VNNI INT8 rung (gemm_int8_kernel, gemm_bench.c:260-285) on the
         primary 2048^3 problem, single-threaded as in gemm_bench and driven over
         M bands by 4, 8 and all host threads (1 and 4 threads on a 512-row
         sample, scaled per operation);
-      * the same rung on the 350M-class K = 1024 / 4096 shapes (a 256-row sample
-        of the 4096 rows, all threads);
-      * FP32 v3-MT (gemm_packed_mt, :167-192) and v1 i-k-j as tensor.c's
-        OpenMP matmul (tensor.c:34-53) on the 1024^3 gemm_bench config, at 1,
-        4, 8 and all threads;
-      * the reference's own 1-core roofs (:287-325).
+      * the same rung on the 350M-class shapes, full 4096 rows at all threads,
+        and on the tied head 4096 x 50257 x 1024 (a 512-row sample; N padded to
+        50272, the 16-column VNNI panel of gemm_bench.c:254);
+      * FP32 v3-MT (gemm_packed_mt, :167-192) on both gemm_bench configs
+        (1024^3 and M 1024, K 1024, N 4096, gemm_bench.c:413-414) at 1, 4, 8
+        and all threads, and on the 350M-class forward shapes (full 4096 rows)
+        at all threads;
+      * v1 i-k-j as tensor.c's OpenMP matmul (tensor.c:34-53) on 1024^3;
+      * the reference's own 1-core roofs (:287-325);
+      * the host share the runs obtained (host_share).
     Returns (cpu_baseline, detail); cpu_baseline is None when the reference
     build is unusable on this host."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -345,13 +369,19 @@ def cpu_reference(M=2048, N=2048, K=2048):
     cores = host_cores()
     thr = sorted({1, 4, 8, cores})
     detail = {"cpu": cpu_model(), "cores": cores}
+    share = host_share(cores)
+    cpu_s, wall_s = [0.0], [0.0]
 
-    def best(f, reps):
+    def best(f, reps=6, threads=1):
         t = 1e30
         for _ in range(reps):
-            t0 = time.perf_counter()
+            c0, t0 = time.process_time(), time.perf_counter()
             f()
-            t = min(t, time.perf_counter() - t0)
+            dt = time.perf_counter() - t0
+            if threads == cores:
+                cpu_s[0] += time.process_time() - c0
+                wall_s[0] += dt * cores
+            t = min(t, dt)
         return t
 
     Au, Bp, corr, dq = _vnni_operands(ob, np, M, N, K, 11)
@@ -360,36 +390,54 @@ def cpu_reference(M=2048, N=2048, K=2048):
     for t in thr:
         rows = M if t >= 8 else 512
         dt = best(lambda: gb.pcl_ref_gemm_int8_mt(t, ob.p(Au), K, ob.p(Bp), ob.p(corr), ob.p(dq), ob.p(Cm), rows, N),
-                  3 if t >= 8 else 2)
+                  threads=t)
         i8[f"{t}t"] = round(2.0 * rows * N * K / dt / 1e12, 4)
     detail["int8_vnni_2048_TOPS"] = i8
-    shapes = {"qkv": (1024, 3072), "attn_out": (1024, 1024), "ffn_up": (1024, 4096), "ffn_down": (4096, 1024)}
+    shapes = {"qkv": (4096, 1024, 3072), "attn_out": (4096, 1024, 1024), "ffn_up": (4096, 1024, 4096),
+              "ffn_down": (4096, 4096, 1024), "head": (512, 1024, 50272)}
     i8s = {}
-    for name, (k, n) in shapes.items():
-        A2, B2, c2, d2 = _vnni_operands(ob, np, 256, n, k, 21)
-        C2 = np.empty((256, n), np.float32)
-        dt = best(lambda: gb.pcl_ref_gemm_int8_mt(cores, ob.p(A2), k, ob.p(B2), ob.p(c2), ob.p(d2), ob.p(C2), 256, n), 3)
-        i8s[name] = round(2.0 * 256 * n * k / dt / 1e12, 4)
+    for name, (m, k, n) in shapes.items():
+        A2, B2, c2, d2 = _vnni_operands(ob, np, m, n, k, 21)
+        C2 = np.empty((m, n), np.float32)
+        dt = best(lambda: gb.pcl_ref_gemm_int8_mt(cores, ob.p(A2), k, ob.p(B2), ob.p(c2), ob.p(d2), ob.p(C2), m, n),
+                  threads=cores)
+        i8s[name] = round(2.0 * m * n * k / dt / 1e12, 4)
+        del A2, B2, C2
     detail[f"int8_vnni_350m_TOPS_{cores}t"] = i8s
-    A, B = ob.frand((1024, 1024), 1234), ob.frand((1024, 1024), 1235)
-    Cf = np.empty((1024, 1024), np.float32)
-    v3, v1 = {}, {}
     mm = ob.ref("libref_model.so")
-    for t in thr:
-        gb.pcl_ref_set_threads(t)
-        v3[f"{t}t"] = round(2.0 * 1024 ** 3 / best(lambda: gb.pcl_ref_gemm_packed_mt(ob.p(A), ob.p(B), ob.p(Cf), 1024,
-                                                                                       1024, 1024), 6) / 1e9, 1)
-        if mm is not None:
-            v1[f"{t}t"] = round(2.0 * 1024 ** 3 / best(lambda: mm.matmul(ob.p(A), ob.p(B), ob.p(Cf), 1024, 1024, 1024),
-                                                       3) / 1e9, 1)
-    gb.pcl_ref_set_threads(1)
-    detail["fp32_v3mt_1024_GFLOPS"] = v3
+    v1 = {}
+    for (m, k, n) in ((1024, 1024, 1024), (1024, 1024, 4096)):
+        A, B = ob.frand((m, k), 1234), ob.frand((k, n), 1235)
+        Cf = np.empty((m, n), np.float32)
+        v3 = {}
+        for t in thr:
+            gb.pcl_ref_set_threads(t)
+            v3[f"{t}t"] = round(2.0 * m * n * k / best(lambda: gb.pcl_ref_gemm_packed_mt(ob.p(A), ob.p(B), ob.p(Cf),
+                                                                                         m, k, n), threads=t) / 1e9, 1)
+            if mm is not None and n == 1024:
+                v1[f"{t}t"] = round(2.0 * m * n * k / best(lambda: mm.matmul(ob.p(A), ob.p(B), ob.p(Cf), m, k, n),
+                                                           3, threads=t) / 1e9, 1)
+        detail[f"fp32_v3mt_{m}x{k}x{n}_GFLOPS"] = v3
     detail["fp32_v1_ikj_tensor_matmul_1024_GFLOPS"] = v1
+    gb.pcl_ref_set_threads(cores)
+    f3 = {}
+    for name, (m, k, n) in shapes.items():
+        if name == "head":
+            continue
+        A, B = ob.frand((m, k), 1236), ob.frand((k, n), 1237)
+        Cf = np.empty((m, n), np.float32)
+        f3[name] = round(2.0 * m * n * k / best(lambda: gb.pcl_ref_gemm_packed_mt(ob.p(A), ob.p(B), ob.p(Cf), m, k, n),
+                                                threads=cores) / 1e9, 1)
+    detail[f"fp32_v3mt_350m_GFLOPS_{cores}t"] = f3
+    gb.pcl_ref_set_threads(1)
     detail["roofs_1core"] = {"fp32_GFLOPS": round(gb.pcl_ref_peak_gflops(), 1),
                              "int8_GOPS": round(gb.pcl_ref_peak_int8_gops(), 1)}
+    share["obtained"] = round(cpu_s[0] / wall_s[0], 3) if wall_s[0] > 0 else None
+    detail["host_share"] = share
     base = {"value": i8[f"{cores}t"], "unit": "TOP/s", "cores": cores, "kind": "reference",
             "sample": f"full {M}x{N}x{K} u8 x s8 problem through the reference gemm_int8_kernel (AVX-512 VNNI, "
-                      f"gemm_bench.c:260-285) over M bands on {cores} host threads, best of 3"}
+                      f"gemm_bench.c:260-285) over M bands on {cores} host threads, best of 6; the runs at "
+                      f"{cores} threads obtained {share['obtained']} of them (process CPU time / wall x threads)"}
     return base, detail
 
 
@@ -519,6 +567,13 @@ def measured_roofs(pcl):
     pcl.check(pcl.lib.pcl_measure_bandwidth(512 << 20, g))
     for n, key in enumerate(("hbm_triad_GBps", "hbm_copy_GBps", "hbm_read_GBps", "hbm_write_GBps")):
         out[key] = round(g[n], 1)
+    # the INT8 kernels' operand feed (L2 -> LDS) on the one-tile-per-CU grids,
+    # and the floor it sets on their K loop at the feed's own clock
+    for key, (m, n, k) in (("2048", (2048, 2048, 2048)), ("ffn_down", (4096, 1024, 4096))):
+        r = d(0)
+        pcl.check(pcl.lib.pcl_measure_lds_feed(m, n, k, C.byref(r)))
+        out[f"int8_tile_feed_{key}_GBps"] = round(r.value, 1)
+        out[f"int8_tile_feed_{key}_loop_floor_us"] = round((m // 128) * (n // 128) * 256.0 * k / (r.value * 1e3), 2)
     return out
 
 
@@ -579,7 +634,9 @@ def main():
         "data": "synthetic (xorshift32 u8 activations, s8 weights, scales U[1e-3,1e-2])",
         "config": {"workload": "gemm_bench INT8 GEMM M=N=K=2048, u8 x s8 -> int32, per-row x per-column dequant "
                                "to fp32 (BASELINE.json configs[1])",
-                   "M": M, "N": N, "K": K, "kernel": "igemm_wp_kernel (producer/consumer waves, v_mfma_i32_32x32x32_i8)",
+                   "M": M, "N": N, "K": K,
+                   "kernel": "igemm_kg_kernel<4,2,1> (one 128x128 tile per workgroup, 2 producer waves filling "
+                             "a 4-deep LDS ring by DMA, 8 consumer waves on v_mfma_i32_16x16x64_i8)",
                    "parallelism": "single GPU",
                    "warmup_min_ms": 20},
         "roofline": {"bound": "mfma", "achieved": tops, "peak": PEAK_I8_TOPS, "unit": "TOP/s",
@@ -642,7 +699,13 @@ def vendor_yardstick():
 def run_rows(pcl, lib):
     """Every configuration beside the headline, at the bench's own step counts."""
     w, s = 5, 20
-    ex = {}
+
+    class Rows(dict):  # a progress line on stderr as each row finishes
+        def __setitem__(self, k, v):
+            super().__setitem__(k, v)
+            print(f"bench: {k} done", file=sys.stderr, flush=True)
+
+    ex = Rows()
     ex["fp32_gemm_1024"] = sgemm(pcl, lib, 0, 0, 1024, 1024, 1024, 0, w, 50)
     ex["int8_350m"] = {name: igemm(pcl, lib, m, n, k, 2, w, s) for name, (m, n, k) in INT8_350M.items()}
     ex["fp32_350m"] = {name: sgemm(pcl, lib, a, b, m, n, k, acc, w, s) for name, (a, b, m, n, k, acc) in {
@@ -700,7 +763,7 @@ def run_rows(pcl, lib):
         "trainer_dh128": attn_bwd(pcl, lib, 4, 1024, 12, 128, w, s),
         "grown_t256": attn_bwd(pcl, lib, 1, 256, 16, 32, w, 50),
     }
-    return ex
+    return dict(ex)
 
 
 def compact_rows(ex, roofs):

@@ -386,6 +386,15 @@ int pcl_measure_peak_mfma(int data, double *rate);
  * gbs[0] STREAM triad a = b + s*c (3 arrays of traffic), gbs[1] copy (2),
  * gbs[2] read only (1), gbs[3] write only (1). Allocates the arrays. */
 int pcl_measure_bandwidth(long bytes_per_array, double gbs[4]);
+/* The operand feed of the INT8 GEMM's 128x128 tiles: one workgroup per output
+ * tile of an M x N x K product streams the tile's A and B panels (rows of K
+ * bytes) into LDS the way the kernels' producer waves do, in their tile order,
+ * with no products; *gbs = GB/s into LDS, best of 5 batches of 50
+ * back-to-back launches after one warm-up batch. M, N, K positive multiples of 128 (PCL_ERR_INVALID_ARG
+ * otherwise). The K loop of a grid of one such tile per CU cannot run faster
+ * than this feed. No counterpart in the reference (its roofs are gemm_bench's
+ * CPU ones). Allocates its operands. */
+int pcl_measure_lds_feed(int M, int N, int K, double *gbs);
 
 /* ---- grouped decode GEMV: many independent products in one launch ----
  * Not a reference function: the reference runs its decode products one call

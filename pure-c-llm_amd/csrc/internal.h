@@ -133,6 +133,9 @@ hipError_t measure_peak_mfma(int kind, int cus, double *rate, hipStream_t s);
 // GB/s over arrays of bytes_per_array: gbs[0] STREAM triad, [1] copy, [2]
 // read only, [3] write only.
 hipError_t measure_bandwidth(long bytes_per_array, double gbs[4], hipStream_t s);
+// GB/s into LDS of the operand stream of a 128x128-tile INT8 GEMM (M, N, K
+// multiples of 128; M*K and N*K below 2^31), no products.
+hipError_t measure_lds_feed(int M, int N, int K, double *gbs, hipStream_t s);
 
 // ---- GEMV (gemv.hip) ----
 GemvPlan plan_sgemv(int w_trans, int M, int N, int K);

@@ -233,4 +233,81 @@ hipError_t measure_bandwidth(long bytes_per_array, double gbs[4], hipStream_t s)
     return err;
 }
 
+// ---- the operand feed of a 128x128-tile INT8 GEMM: L2 -> LDS ----
+// One workgroup per 128x128 output tile of an M x N x K product (A M x K
+// bytes, B N x K bytes, rows K bytes apart), in the INT8 kernels' tile order
+// (xcd_remap + grouped tiles): four waves stream the tile's A and B panels
+// over K into a 3-deep LDS ring with global_load_lds_dwordx4, exactly as the
+// kernels' producer waves issue them (eight rows of 128 bytes per instruction,
+// chunks swizzled), two K tiles in flight, with no products. Its rate is the
+// ceiling of those kernels' K loop when the operands must come through L2.
+constexpr int RF_FEED_NWP = 4;
+__global__ __launch_bounds__(64 * RF_FEED_NWP) void roof_feed_kernel(const int8_t *__restrict__ A,
+                                                                     const int8_t *__restrict__ B, int M,
+                                                                     int N, int K, int *__restrict__ sink) {
+    constexpr int BM = 128, BN = 128, BK = 128, CH = 8, RPI = 8, SIZE_A = BM * BK, STAGE = (BM + BN) * BK;
+    constexpr int PIA = BM / (RPI * RF_FEED_NWP), PIB = BN / (RPI * RF_FEED_NWP), PL = PIA + PIB;
+    constexpr int STAGES = 3;
+    __shared__ __attribute__((aligned(1024))) int8_t lds[STAGES * STAGE];
+    const int tid = threadIdx.x, lane = tid & 63, pw = tid >> 6;
+    const int nbm = M / BM, nbn = N / BN;
+    int bm, bn;
+    tile_coords(xcd_remap(blockIdx.x, nbm * nbn), nbm, nbn, 8, bm, bn);
+    unsigned voff[PL];
+    int ldso[PL];
+#pragma unroll
+    for (int d = 0; d < PL; d++) {
+        const bool isA = d < PIA;
+        const int rb = ((isA ? d : d - PIA) * RF_FEED_NWP + pw) * RPI;
+        const int r = rb + lane / CH;
+        const int c = (lane % CH) ^ ((r >> 1) & (CH - 1));
+        voff[d] = (unsigned)((isA ? bm * BM : bn * BN) + r) * (unsigned)K + (unsigned)(c * 16);
+        ldso[d] = (isA ? 0 : SIZE_A) + rb * BK;
+    }
+    const int nk = K / BK;
+    for (int t = 0; t < nk; t++) {
+        int8_t *stage = lds + (t % STAGES) * STAGE;
+#pragma unroll
+        for (int d = 0; d < PL; d++)
+            __builtin_amdgcn_global_load_lds((const void *)((d < PIA ? A : B) + (long)t * BK + voff[d]),
+                                             (__attribute__((address_space(3))) void *)(stage + ldso[d]), 16, 0,
+                                             0);
+        // two K tiles in flight: "vmcnt <= PL", expcnt and lgkmcnt unchecked
+        __builtin_amdgcn_s_waitcnt((PL & 15) | (((PL >> 4) & 3) << 14) | (7 << 4) | (15 << 8));
+    }
+    __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));  // vmcnt(0)
+    if (tid == 0) sink[blockIdx.x] = lds[lane];
+}
+
+hipError_t measure_lds_feed(int M, int N, int K, double *gbs, hipStream_t s) {
+    if (M % 128 || N % 128 || K % 128 || M <= 0 || N <= 0 || K <= 0 || (long)M * K >= (1L << 31) ||
+        (long)N * K >= (1L << 31))
+        return hipErrorInvalidValue;
+    void *a = nullptr, *b = nullptr, *sink = nullptr;
+    const int tiles = (M / 128) * (N / 128);
+    hipError_t err = hipMalloc(&a, (size_t)M * K);
+    if (err == hipSuccess) err = hipMalloc(&b, (size_t)N * K);
+    if (err == hipSuccess) err = hipMalloc(&sink, (size_t)tiles * 4);
+    if (err == hipSuccess) err = hipMemsetAsync(a, 1, (size_t)M * K, s);
+    if (err == hipSuccess) err = hipMemsetAsync(b, 2, (size_t)N * K, s);
+    if (err == hipSuccess) {
+        // batches of back-to-back launches: a launch alone between two events
+        // would add the event overhead (a few us) to a kernel of a few us
+        constexpr int BATCH = 50;
+        auto pass = [&]() {
+            for (int i = 0; i < BATCH; i++)
+                hipLaunchKernelGGL(roof_feed_kernel, dim3(tiles), dim3(64 * RF_FEED_NWP), 0, s, (const int8_t *)a,
+                                   (const int8_t *)b, M, N, K, (int *)sink);
+        };
+        pass();
+        float ms = 0.f;
+        err = best_ms(pass, 5, s, &ms);
+        if (err == hipSuccess) *gbs = (double)tiles * 256.0 * K * BATCH / (ms * 1e-3) / 1e9;
+    }
+    if (a) (void)hipFree(a);
+    if (b) (void)hipFree(b);
+    if (sink) (void)hipFree(sink);
+    return err;
+}
+
 }  // namespace pcl
