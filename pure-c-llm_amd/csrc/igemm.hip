@@ -371,6 +371,18 @@ __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(
 // Before B(g) the producers have waited for K tile g+1 (leaving g+2 .. in
 // flight) and every consumer has issued and retired its reads of K tile g;
 // after it the producers refill tile g's stage with tile g + STAGES.
+//
+// Row classes (P > 1 or col_shift): an output whose rows do not all start on
+// a 128-byte line (a pitch like the 50257-float vocabulary head, or a base
+// off a line) would have every 32-float store chunk straddle two lines, and
+// lines written in two parts by different waves or workgroups halve the HBM
+// write rate. Rows r and r + P start at the same offset within a line when
+// P * ldc is a multiple of 32 floats, so a tile takes BM rows of one class
+// (rows cls, cls + P, cls + 2P, ...) and a column window shifted left by the
+// class's offset: its every 32-float chunk is then one whole line. Row
+// class cls = bm % P, class-local rows bm / P * BM ...; column tile bn covers
+// [bn*BN - csh, bn*BN - csh + BN) with csh = (C's element offset within a
+// line + cls * ldc) mod 32. P = 1 without col_shift is the plain tiling.
 template <int BM, int BN, int WM, int WN, int STAGES, int NWP, int OUT, int NTS>
 __global__ __launch_bounds__(64 * (WM * WN + NWP)) __attribute__((amdgpu_waves_per_eu(
     (WM * WN + NWP + 3) / 4))) void igemm_wp_kernel(const uint8_t *__restrict__ A, long lda,
@@ -379,7 +391,7 @@ __global__ __launch_bounds__(64 * (WM * WN + NWP)) __attribute__((amdgpu_waves_p
                                                       const float *__restrict__ sa,
                                                       const float *__restrict__ sb,
                                                       void *__restrict__ Cv, long ldc, int M, int N,
-                                                      int K) {
+                                                      int K, int P, int col_shift, int gm) {
     constexpr int NWC = WM * WN, BK = IG_BK;
     constexpr int WTM = BM / WM, WTN = BN / WN, TM = WTM / 32, TN = WTN / 32;
     constexpr int NM = TM * TN, NR = TM + TN;
@@ -394,24 +406,30 @@ __global__ __launch_bounds__(64 * (WM * WN + NWP)) __attribute__((amdgpu_waves_p
     static_assert(TM >= 1 && TN >= 1 && STAGES >= 2, "tile configuration");
     static_assert(LDS_BYTES <= 160 * 1024, "LDS budget of a CU");
     static_assert(BN == 128 && BM <= 256, "epilogue operands: two 64-lane DMA per producer wave");
-    static_assert((STAGES - 1) * PL + NS <= 63, "vmcnt range");
+    static_assert((STAGES - 1) * (PL + NS) <= 63, "vmcnt range");
     __shared__ __attribute__((aligned(1024))) int8_t lds[LDS_BYTES];
     float *scl = reinterpret_cast<float *>(lds + STAGES * STAGE);  // [3 tiles][sb | col_off | sa]
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int nbm = (M + BM - 1) / BM, nbn = (N + BN - 1) / BN, ntiles = nbm * nbn;
+    const int Mc = (M + P - 1) / P;  // rows of the largest class
+    const int nbm = P * ((Mc + BM - 1) / BM), nbn = (N + (col_shift ? 31 : 0) + BN - 1) / BN;
+    const int ntiles = nbm * nbn;
+    const int cb0 = col_shift ? (int)((reinterpret_cast<unsigned long>(Cv) >> 2) & 31) : 0;
     const int nb = gridDim.x;
     const int slot = xcd_remap(blockIdx.x, nb);
     const int my_tiles = slot < ntiles ? (ntiles - 1 - slot) / nb + 1 : 0;
     const int nk = K / BK;
     const int G = my_tiles * nk;  // K tiles this workgroup streams
     if (G == 0) return;           // uniform: no barrier is left unmatched
-    auto tile_origin = [&](int i, int &m0, int &n0) {
+    // tile i of this workgroup: row class, class-local first row, first column
+    // (negative for the window that holds a class's first partial line)
+    auto tile_origin = [&](int i, int &cls, int &r0, int &n0) {
         int bm, bn;
-        tile_coords(i * nb + slot, nbm, nbn, 8, bm, bn);
-        m0 = bm * BM;
-        n0 = bn * BN;
+        tile_coords(i * nb + slot, nbm, nbn, gm, bm, bn);
+        cls = bm % P;
+        r0 = bm / P * BM;
+        n0 = bn * BN - (col_shift ? (int)((cb0 + (long)cls * ldc) & 31) : 0);
     };
 
     if (wave >= NWC) {
@@ -428,15 +446,17 @@ __global__ __launch_bounds__(64 * (WM * WN + NWP)) __attribute__((amdgpu_waves_p
         // rows past BM) loads sb again into the spare slot, so every producer
         // issues the same count.
         auto begin_tile = [&](int i) {
-            int m0, n0;
-            tile_origin(i, m0, n0);
+            int cls, r0, n0;
+            tile_origin(i, cls, r0, n0);
 #pragma unroll
             for (int d = 0; d < PL; d++) {
                 const bool isA = d < PIA;
                 const int rb = ((isA ? d : d - PIA) * NWP + pw) * RPI;
                 const int r = rb + lane / CH;
                 const int c = (lane % CH) ^ ((r >> 1) & (CH - 1));
-                const int grow = min((isA ? m0 : n0) + r, (isA ? M : N) - 1);
+                // rows past the output re-read the last row; columns outside
+                // [0, N) the nearest one (their results are never stored)
+                const int grow = isA ? min(cls + P * (r0 + r), M - 1) : max(min(n0 + r, N - 1), 0);
                 voff[d] = (unsigned)grow * (unsigned)(isA ? lda : ldb) + (unsigned)(c * 16);
                 ldso[d] = (isA ? 0 : SIZE_A) + rb * BK;
             }
@@ -445,18 +465,18 @@ __global__ __launch_bounds__(64 * (WM * WN + NWP)) __attribute__((amdgpu_waves_p
 #pragma unroll
                 for (int h = 0; h < NS; h++) {
                     const int piece = pw * NS + h;
-                    const float *src = sb + min(n0 + (piece & 1) * 64 + lane, N - 1);
+                    const float *src = sb + max(min(n0 + (piece & 1) * 64 + lane, N - 1), 0);
                     float *to = dst + 2 * BN + BM + (piece & 1) * 64;  // spare slot
                     if (piece < 2) {
                         to = dst + piece * 64;
                     } else if (piece < 4) {
                         if (col_off) {
                             src = reinterpret_cast<const float *>(col_off) +
-                                  min(n0 + (piece - 2) * 64 + lane, N - 1);
+                                  max(min(n0 + (piece - 2) * 64 + lane, N - 1), 0);
                             to = dst + BN + (piece - 2) * 64;
                         }
                     } else if (OUT == 2 && (piece - 4) * 64 < BM) {
-                        src = sa + min(m0 + (piece - 4) * 64 + lane, M - 1);
+                        src = sa + min(cls + P * (r0 + (piece - 4) * 64 + lane), M - 1);
                         to = dst + 2 * BN + (piece - 4) * 64;
                     }
                     __builtin_amdgcn_global_load_lds((const void *)src, (lds_void_t *)to, 4, 0, 0);
@@ -481,22 +501,30 @@ __global__ __launch_bounds__(64 * (WM * WN + NWP)) __attribute__((amdgpu_waves_p
             return first && NS > 0;
         };
         // hist bit j: the j-th most recently issued K-tile DMA also carried
-        // epilogue operands (NS more vmcnt entries than PL); a wait that would
-        // have to count those waits for everything instead.
+        // epilogue operands (NS more vmcnt entries than PL, issued before its
+        // PL loads). Waits count them exactly: "the NY youngest K tiles may
+        // still fly" is vmcnt <= NY * PL + NS * (those of them that carried
+        // operands), so a tile boundary does not drain the DMA queue.
         unsigned hist = 0;
+        auto wait_younger = [&](auto NYC) {
+            constexpr int ny = decltype(NYC)::value;
+            const int c = __builtin_popcount(hist & ((1u << ny) - 1));
+            static_for<0, ny + 1>([&](auto Cc) {
+                constexpr int cc = decltype(Cc)::value;
+                if (c == cc) __builtin_amdgcn_s_waitcnt(waitcnt_vm(ny * PL + cc * NS));
+            });
+        };
         // prologue: K tiles 0 .. STAGES-1; P0 once K tile 0 has landed
 #pragma unroll
         for (int t = 0; t < STAGES; t++)
             if (t < G) hist = (hist << 1) | (dma_next() ? 1u : 0u);
-        if (G >= STAGES && (hist & ((1u << (STAGES - 1)) - 1)) == 0)
-            __builtin_amdgcn_s_waitcnt(waitcnt_vm((STAGES - 1) * PL));
+        if (G >= STAGES) wait_younger(IC<STAGES - 1>{});
         else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
         __builtin_amdgcn_s_barrier();
         // before B(g) K tiles g+1 .. g+STAGES-1 have been issued, oldest first
         for (int g = 0; g < G; g++) {
             // K tile g+1 has landed; the STAGES-2 younger ones may still fly
-            if (g + STAGES - 1 < G && (hist & ((1u << (STAGES - 2)) - 1)) == 0)
-                __builtin_amdgcn_s_waitcnt(waitcnt_vm((STAGES - 2) * PL));
+            if (g + STAGES - 1 < G) wait_younger(IC<STAGES - 2>{});
             else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
             __builtin_amdgcn_s_barrier();  // B(g)
             if (g + STAGES < G) hist = (hist << 1) | (dma_next() ? 1u : 0u);  // into stage g % STAGES
@@ -592,9 +620,9 @@ __global__ __launch_bounds__(64 * (WM * WN + NWP)) __attribute__((amdgpu_waves_p
 
         // Epilogue (layout as in igemm_mfma_kernel); operands from LDS. The
         // stores carry no wait: they drain while the next tile is multiplied.
-        int m0, n0;
-        tile_origin(i, m0, n0);
-        const int wrow0 = m0 + wm * WTM, wcol0 = n0 + wn * WTN;
+        int cls, r0, n0;
+        tile_origin(i, cls, r0, n0);
+        const int wrow0 = r0 + wm * WTM, wcol0 = n0 + wn * WTN;  // class-local row
         const float *sc = scl + (i % 3) * SCL;
         float sbv[TN];
         unsigned offv[TN];
@@ -619,12 +647,13 @@ __global__ __launch_bounds__(64 * (WM * WN + NWP)) __attribute__((amdgpu_waves_p
 #pragma unroll
                     for (int e = 0; e < 4; e++) {
                         const int v = vq * 4 + e;
-                        const int row = wrow0 + a * 32 + vq * 8 + lg * 4 + e;
+                        const int row = cls + P * (wrow0 + a * 32 + vq * 8 + lg * 4 + e);
                         if (chk && row >= Mv) continue;
                         const long ro = (long)row * ld_out + wcol0 + r32;
 #pragma unroll
                         for (int b = 0; b < TN; b++) {
-                            if (chk && wcol0 + b * 32 + r32 >= Nv) continue;
+                            const int col = wcol0 + b * 32 + r32;
+                            if (chk && (col < 0 || col >= Nv)) continue;
                             const long o = ro + b * 32;
                             if (OUT == 0) {
                                 if constexpr (NTS) __builtin_nontemporal_store(acc[a][b][v], (gint32_t *)C_out + o);
@@ -640,7 +669,7 @@ __global__ __launch_bounds__(64 * (WM * WN + NWP)) __attribute__((amdgpu_waves_p
                 }
             }
         };
-        if (m0 + BM <= Mv && n0 + BN <= Nv)
+        if (cls + P * (r0 + BM - 1) < Mv && n0 >= 0 && n0 + BN <= Nv)
             store_tile(IC<0>{});
         else
             store_tile(IC<1>{});
@@ -942,6 +971,301 @@ __global__ __launch_bounds__(64 * (8 + NWP)) __attribute__((amdgpu_waves_per_eu(
     }
 }
 
+// ---------------------------------------------------------------------------
+// Persistent form of igemm_kg_kernel for grids of many 128x128 tiles (the
+// 50257-vocab head): the consumers of igemm_kg_kernel (one K group, eight
+// waves of 32x64 on v_mfma_i32_16x16x64_i8, a whole K tile's fragments read
+// one tile ahead) and the producers of igemm_wp_kernel (the K-tile stream runs
+// across output tiles through the ring; the epilogue operands of a tile are
+// DMA'd into LDS, three tiles deep, so the consumers never wait on vmcnt and
+// the stores of one tile drain under the next). Row classes as in
+// igemm_wp_kernel (P, col_shift). K is a multiple of 256 (an even number of
+// K tiles per output tile: the two fragment slots alternate within a tile and
+// the reads ahead of a tile's last K tile are the next tile's first).
+template <int STAGES, int NWP, int OUT, int NTS>
+__global__ __launch_bounds__(64 * (8 + NWP)) __attribute__((amdgpu_waves_per_eu(
+    (8 + NWP + 3) / 4))) void igemm_kgp_kernel(const uint8_t *__restrict__ A, long lda,
+                                              const int8_t *__restrict__ B, long ldb,
+                                              const int32_t *__restrict__ col_off,
+                                              const float *__restrict__ sa,
+                                              const float *__restrict__ sb,
+                                              void *__restrict__ Cv, long ldc, int M, int N, int K,
+                                              int P, int col_shift, int gm) {
+    constexpr int BM = 128, BN = 128, BK = IG_BK, CH = BK / 16, RPI = 1024 / BK;
+    constexpr int SIZE_A = BM * BK, STAGE = (BM + BN) * BK;
+    constexpr int PIA = BM / (RPI * NWP), PIB = BN / (RPI * NWP), PL = PIA + PIB;
+    constexpr int SCL = 2 * BN + BM + 128;      // floats per tile: sb, col_off, sa, spare
+    constexpr int NS = OUT != 0 ? 8 / NWP : 0;  // epilogue-operand DMA instructions per producer
+    constexpr int LDS_BYTES = STAGES * STAGE + 3 * SCL * 4;
+    static_assert(NWP == 2 || NWP == 4, "producer waves");
+    static_assert(STAGES >= 3 && LDS_BYTES <= 160 * 1024, "ring");
+    static_assert((STAGES - 1) * (PL + NS) <= 63, "vmcnt range");
+    __shared__ __attribute__((aligned(1024))) int8_t lds[LDS_BYTES];
+    float *scl = reinterpret_cast<float *>(lds + STAGES * STAGE);  // [3 tiles][sb | col_off | sa]
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int Mc = (M + P - 1) / P;
+    const int nbm = P * ((Mc + BM - 1) / BM), nbn = (N + (col_shift ? 31 : 0) + BN - 1) / BN;
+    const int ntiles = nbm * nbn;
+    const int cb0 = col_shift ? (int)((reinterpret_cast<unsigned long>(Cv) >> 2) & 31) : 0;
+    const int nb = gridDim.x;
+    const int slot = xcd_remap(blockIdx.x, nb);
+    const int my_tiles = slot < ntiles ? (ntiles - 1 - slot) / nb + 1 : 0;
+    const int nk = K / BK;
+    const int G = my_tiles * nk;  // K tiles this workgroup streams
+    if (G == 0) return;           // uniform: no barrier is left unmatched
+    auto tile_origin = [&](int i, int &cls, int &r0, int &n0) {
+        int bm, bn;
+        tile_coords(i * nb + slot, nbm, nbn, gm, bm, bn);
+        cls = bm % P;
+        r0 = bm / P * BM;
+        n0 = bn * BN - (col_shift ? (int)((cb0 + (long)cls * ldc) & 31) : 0);
+    };
+
+    if (wave >= 8) {
+        // ------------------------------------------------------ producers
+        const int pw = wave - 8;
+        const int8_t *A8 = reinterpret_cast<const int8_t *>(A);
+        unsigned voff[PL];
+        int ldso[PL];
+        // Output tile i starts: its rows' and columns' source offsets, and the
+        // 4-byte DMA of its epilogue operands into LDS buffer i % 3 (pieces as
+        // in igemm_wp_kernel: sb 0-1, col_off 2-3, sa 4-5, absent ones load
+        // sb again into the spare slot).
+        auto begin_tile = [&](int i) {
+            int cls, r0, n0;
+            tile_origin(i, cls, r0, n0);
+#pragma unroll
+            for (int d = 0; d < PL; d++) {
+                const bool isA = d < PIA;
+                const int rb = ((isA ? d : d - PIA) * NWP + pw) * RPI;
+                const int r = rb + lane / CH;
+                const int c = (lane % CH) ^ ((r >> 1) & (CH - 1));
+                const int grow = isA ? min(cls + P * (r0 + r), M - 1) : max(min(n0 + r, N - 1), 0);
+                voff[d] = (unsigned)grow * (unsigned)(isA ? lda : ldb) + (unsigned)(c * 16);
+                ldso[d] = (isA ? 0 : SIZE_A) + rb * BK;
+            }
+            if (OUT != 0) {
+                float *dst = scl + (i % 3) * SCL;
+#pragma unroll
+                for (int h = 0; h < NS; h++) {
+                    const int piece = pw * NS + h;
+                    const float *src = sb + max(min(n0 + (piece & 1) * 64 + lane, N - 1), 0);
+                    float *to = dst + 2 * BN + BM + (piece & 1) * 64;  // spare slot
+                    if (piece < 2) {
+                        to = dst + piece * 64;
+                    } else if (piece < 4) {
+                        if (col_off) {
+                            src = reinterpret_cast<const float *>(col_off) +
+                                  max(min(n0 + (piece - 2) * 64 + lane, N - 1), 0);
+                            to = dst + BN + (piece - 2) * 64;
+                        }
+                    } else if (OUT == 2 && piece < 6) {
+                        src = sa + min(cls + P * (r0 + (piece - 4) * 64 + lane), M - 1);
+                        to = dst + 2 * BN + (piece - 4) * 64;
+                    }
+                    __builtin_amdgcn_global_load_lds((const void *)src, (lds_void_t *)to, 4, 0, 0);
+                }
+            }
+        };
+        int di = 0, dk = 0;  // output tile and K tile of the next DMA
+        auto dma_next = [&]() -> bool {
+            const bool first = dk == 0;
+            if (first) begin_tile(di);
+            const long koff = (long)dk * BK;
+            int8_t *stage = lds + ((di * nk + dk) % STAGES) * STAGE;
+#pragma unroll
+            for (int d = 0; d < PL; d++)
+                __builtin_amdgcn_global_load_lds((const void *)((d < PIA ? A8 : B) + koff + voff[d]),
+                                                 (lds_void_t *)(stage + ldso[d]), 16, 0, 0);
+            if (++dk == nk) {
+                dk = 0;
+                di++;
+            }
+            return first && NS > 0;
+        };
+        // hist bit j: the j-th most recently issued K-tile DMA carried
+        // epilogue operands (NS more vmcnt entries, issued before its PL).
+        unsigned hist = 0;
+        auto wait_younger = [&](auto NYC) {  // the NY youngest K tiles may still fly
+            constexpr int ny = decltype(NYC)::value;
+            const int c = __builtin_popcount(hist & ((1u << ny) - 1));
+            static_for<0, ny + 1>([&](auto Cc) {
+                constexpr int cc = decltype(Cc)::value;
+                if (c == cc) __builtin_amdgcn_s_waitcnt(waitcnt_vm(ny * PL + cc * NS));
+            });
+        };
+        // Prologue as in igemm_kg_kernel: K tiles 0 and 1, P0 once tile 0 has
+        // landed, then the rest of the ring.
+        hist = (hist << 1) | (dma_next() ? 1u : 0u);
+        if (G > 1) {
+            hist = (hist << 1) | (dma_next() ? 1u : 0u);
+            wait_younger(IC<1>{});
+        } else {
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+        }
+        __builtin_amdgcn_s_barrier();  // P0
+#pragma unroll
+        for (int t = 2; t < STAGES; t++)
+            if (t < G) hist = (hist << 1) | (dma_next() ? 1u : 0u);
+        for (int g = 0; g < G; g++) {
+            // K tile g+1 has landed; tiles g+2 .. g+STAGES-1 may still fly
+            if (g + STAGES - 1 < G) wait_younger(IC<STAGES - 2>{});
+            else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+            __builtin_amdgcn_s_barrier();  // B(g)
+            if (g + STAGES < G) hist = (hist << 1) | (dma_next() ? 1u : 0u);
+        }
+        return;
+    }
+
+    // ---------------------------------------------------------- consumers
+    constexpr int WTM = 32, WTN = 64;           // wave tile (4 x 2 waves)
+    constexpr int NBM = WTM / 16, NBN = WTN / 16;  // 16x16 blocks
+    constexpr int KS = 2;                       // 64-byte k-steps per K tile
+    constexpr int NFA = KS * NBM, NFB = KS * NBN, NF = NFA + NFB;
+    constexpr int NM = KS * NBM * NBN;          // MFMAs per K tile
+    const int wm = wave >> 1, wn = wave & 1;
+    void *C_out = Cv;
+    long ld_out = ldc;
+    int Mv = M, Nv = N, Pv = P;
+    asm volatile("" : "+s"(C_out), "+s"(ld_out), "+s"(Mv), "+s"(Nv), "+s"(Pv));
+    const int lcol = lane & 15;
+    const unsigned lds0 = lds_addr(lds);
+    const int lrow = lane & 15, lgrp = lane >> 4;
+    const int swz = (lrow >> 1) & (CH - 1);
+    unsigned offa[KS], offb[KS];
+#pragma unroll
+    for (int s = 0; s < KS; s++) {
+        const int chunk = 4 * s + lgrp;
+        offa[s] = (wm * WTM + lrow) * BK + ((chunk ^ swz) << 4);
+        offb[s] = SIZE_A + (wn * WTN + lrow) * BK + ((chunk ^ swz) << 4);
+    }
+
+    v4i acc[NBM][NBN];
+#pragma unroll
+    for (int i = 0; i < NBM; i++)
+#pragma unroll
+        for (int j = 0; j < NBN; j++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) acc[i][j][v] = 0;
+
+    v4i fa[2][NFA], fb[2][NFB];
+    auto read_frag = [&](unsigned base, auto S, auto F) {
+        constexpr int sl = decltype(S)::value, f = decltype(F)::value;
+        if constexpr (f < NFA) lds_read16<(f % NBM) * 16 * BK>(fa[sl][f], base + offa[f / NBM]);
+        else lds_read16<((f - NFA) % NBN) * 16 * BK>(fb[sl][f - NFA], base + offb[(f - NFA) / NBN]);
+    };
+    auto land = [&](auto S) {
+        constexpr int sl = decltype(S)::value;
+        lds_wait<0>();
+        static_for<0, NFA>([&](auto F) { reg_fence(fa[sl][F.value]); });
+        static_for<0, NFB>([&](auto F) { reg_fence(fb[sl][F.value]); });
+        static_for<0, NFA>([&](auto F) { fa[sl][F.value] ^= (int)0x80808080u; });
+    };
+
+    __builtin_amdgcn_s_barrier();  // P0
+    static_for<0, NF>([&](auto F) { read_frag(lds0, IC<0>{}, F); });
+    land(IC<0>{});
+
+    // K tile g (global index in this workgroup's stream) from slot S: MFMA 0,
+    // the barrier, the next K tile's reads over the first half of the MFMAs,
+    // the next slot landed before the last MFMA. The reads ahead of the last
+    // K tile of the stream read a stage inside the ring that no DMA writes
+    // any more, and are unused.
+    auto ktile = [&](int g, auto S) {
+        constexpr int sl = decltype(S)::value, ns = 1 - sl;
+        const unsigned nbase = lds0 + ((g + 1) % STAGES) * STAGE;
+        constexpr int RPG = (NF + NM / 2 - 1) / (NM / 2);
+        static_for<0, NM>([&](auto Q) {
+            constexpr int q = Q.value;
+            constexpr int s = q / (NBM * NBN), j = (q / NBM) % NBN, i = q % NBM;
+            acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[sl][s * NBM + i], fb[sl][s * NBN + j],
+                                                              acc[i][j], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (q == 0) __builtin_amdgcn_s_barrier();  // B(g)
+            if constexpr (q < NM / 2)
+                static_for<q * RPG, (q + 1) * RPG < NF ? (q + 1) * RPG : NF>(
+                    [&](auto F) { read_frag(nbase, IC<ns>{}, F); });
+            if constexpr (q == NM - 2) land(IC<ns>{});
+            __builtin_amdgcn_sched_barrier(0);
+        });
+    };
+
+    int g = 0;
+    for (int t = 0; t < my_tiles; t++) {
+        for (int kt = 0; kt < nk; kt += 2, g += 2) {
+            ktile(g, IC<0>{});
+            ktile(g + 1, IC<1>{});
+        }
+        // Epilogue of tile t (operands from LDS buffer t % 3; stores as in
+        // igemm_kg_kernel, 2 rows x 32 columns per store after two lane
+        // swaps). The stores carry no wait: they drain under tile t + 1.
+        int cls, r0, n0;
+        tile_origin(t, cls, r0, n0);
+        const float *sc = scl + (t % 3) * SCL;
+        const int wrow0 = r0 + wm * WTM, wcol0 = n0 + wn * WTN;  // class-local row
+        float sbv[NBN], sav[8];
+        unsigned offv[NBN];
+#pragma unroll
+        for (int j = 0; j < NBN; j++) {
+            const int cl = wn * WTN + j * 16 + lcol;
+            sbv[j] = (OUT != 0) ? sc[cl] : 0.f;
+            offv[j] = (OUT != 0 && col_off) ? reinterpret_cast<const unsigned *>(sc)[BN + cl] : 0u;
+        }
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+            const int r = (q >> 2) * 16 + 4 * (lane >> 4) + (q & 3);
+            sav[q] = (OUT == 2) ? sc[2 * BN + wm * WTM + r] : 0.f;
+        }
+        auto store_rows = [&](auto CHECK) {
+            constexpr bool chk = decltype(CHECK)::value != 0;
+            const int hrow = 4 * (lane >> 5), hcol = lane & 31;
+            static_for<0, NBM>([&](auto I) {
+                constexpr int i = I.value;
+                static_for<0, 4>([&](auto V) {
+                    constexpr int v = V.value;
+                    const float rs = sav[i * 4 + v];
+                    static_for<0, NBN / 2>([&](auto JP) {
+                        constexpr int j0 = 2 * JP.value;
+                        unsigned x, y;
+                        if constexpr (OUT == 0) {
+                            x = (unsigned)acc[i][j0][v];
+                            y = (unsigned)acc[i][j0 + 1][v];
+                        } else {
+                            const float dx = (OUT == 2) ? rs * sbv[j0] : sbv[j0];
+                            const float dy = (OUT == 2) ? rs * sbv[j0 + 1] : sbv[j0 + 1];
+                            x = __float_as_uint((float)(int32_t)((unsigned)acc[i][j0][v] + offv[j0]) * dx);
+                            y = __float_as_uint((float)(int32_t)((unsigned)acc[i][j0 + 1][v] + offv[j0 + 1]) * dy);
+                        }
+                        const auto p16 = __builtin_amdgcn_permlane16_swap(x, y, false, false);
+                        const auto p32 = __builtin_amdgcn_permlane32_swap(p16[0], p16[1], false, false);
+                        const int col = wcol0 + j0 * 16 + hcol;
+#pragma unroll
+                        for (int h = 0; h < 2; h++) {
+                            const int row = cls + Pv * (wrow0 + i * 16 + 8 * h + hrow + v);
+                            if (chk && (row >= Mv || col < 0 || col >= Nv)) continue;
+                            const long o = (long)row * ld_out + col;
+                            const unsigned val = h == 0 ? p32[0] : p32[1];
+                            if constexpr (NTS) __builtin_nontemporal_store(val, (gu32_t *)C_out + o);
+                            else ((gu32_t *)C_out)[o] = val;
+                        }
+                    });
+                });
+            });
+        };
+        if (cls + Pv * (r0 + BM - 1) < Mv && n0 >= 0 && n0 + BN <= Nv) store_rows(IC<0>{});
+        else store_rows(IC<1>{});
+#pragma unroll
+        for (int i = 0; i < NBM; i++)
+#pragma unroll
+            for (int j = 0; j < NBN; j++)
+#pragma unroll
+                for (int v = 0; v < 4; v++) acc[i][j][v] = 0;
+    }
+    lds_wait<0>();
+}
+
 static int device_cus() {
     static const int cus = [] {
         int dev = 0, n = 0;
@@ -953,38 +1277,59 @@ static int device_cus() {
     return cus;
 }
 
+// Row classes of a 4-byte output (igemm_wp_kernel): rows r and r + P start at
+// the same offset within a 128-byte line; shift: some row starts off a line.
+struct RowClasses {
+    int P, shift;
+};
+static RowClasses row_classes(const void *C, long ldc) {
+    const int lm = (int)(ldc & 31), cb = (int)((reinterpret_cast<uintptr_t>(C) >> 2) & 31);
+    return RowClasses{lm ? 32 / (lm & -lm) : 1, (lm || cb) ? 1 : 0};
+}
+// Whether the row-class tiling suits an output: its rows are off lines and
+// the classes fill BM-row tiles with at most 1/8 of the tile rows idle.
+static bool classes_fill(int M, long ldc, const void *C, int BM) {
+    const RowClasses rc = row_classes(C, ldc);
+    if (!rc.shift || M <= 0) return false;
+    const long Mc = (M + rc.P - 1) / rc.P;
+    return (long)rc.P * ((Mc + BM - 1) / BM * BM) * 8 <= (long)M * 9;
+}
+
 template <int BM, int BN, int WM, int WN, int STAGES, int NWP>
 static hipError_t launch_wp_band(int out_mode, int M, int N, int K, const uint8_t *A, long lda,
                                  const int8_t *B, long ldb, const int32_t *col_off,
-                                 const float *sa, const float *sb, void *C, long ldc,
+                                 const float *sa, const float *sb, void *C, long ldc, bool classes,
                                  hipStream_t stream) {
-    const long ntiles = (long)((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-    if (ntiles == 0 || K / IG_BK == 0) return hipSuccess;
+    const RowClasses rc = classes ? row_classes(C, ldc) : RowClasses{1, 0};
+    const int gm = rc.P > 1 ? 16 : 8;  // 16 classes x 2 column tiles per XCD and round
+    const long Mc = (M + rc.P - 1) / rc.P;
+    const long ntiles = rc.P * ((Mc + BM - 1) / BM) * ((N + (rc.shift ? 31 : 0) + BN - 1) / BN);
+    if (M == 0 || N == 0 || K / IG_BK == 0) return hipSuccess;
     const int grid = (int)(ntiles < device_cus() ? ntiles : device_cus());
     const dim3 block(64 * (WM * WN + NWP));
-    // outputs up to 256 MiB: streaming (non-temporal) stores, chosen at compile
-    // time (a run-time choice between two otherwise equal stores is merged by
-    // the compiler into one without the hint)
-    const bool nt = (long)M * N * 4 <= (256L << 20);
+    // streaming (non-temporal) stores at every size: on the 823 MB output of
+    // the 50257-vocab head they take 386-392 us against 425-436 us for plain
+    // stores (two boxes, same build). The hint is a compile-time choice (a
+    // run-time choice between two otherwise equal stores is merged by the
+    // compiler into one without it).
     auto go = [&](auto NT) {
         constexpr int nts = decltype(NT)::value;
         switch (out_mode) {
             case 0:
                 hipLaunchKernelGGL((igemm_wp_kernel<BM, BN, WM, WN, STAGES, NWP, 0, nts>), dim3(grid), block, 0,
-                                   stream, A, lda, B, ldb, col_off, sa, sb, C, ldc, M, N, K);
+                                   stream, A, lda, B, ldb, col_off, sa, sb, C, ldc, M, N, K, rc.P, rc.shift, gm);
                 break;
             case 1:
                 hipLaunchKernelGGL((igemm_wp_kernel<BM, BN, WM, WN, STAGES, NWP, 1, nts>), dim3(grid), block, 0,
-                                   stream, A, lda, B, ldb, col_off, sa, sb, C, ldc, M, N, K);
+                                   stream, A, lda, B, ldb, col_off, sa, sb, C, ldc, M, N, K, rc.P, rc.shift, gm);
                 break;
             default:
                 hipLaunchKernelGGL((igemm_wp_kernel<BM, BN, WM, WN, STAGES, NWP, 2, nts>), dim3(grid), block, 0,
-                                   stream, A, lda, B, ldb, col_off, sa, sb, C, ldc, M, N, K);
+                                   stream, A, lda, B, ldb, col_off, sa, sb, C, ldc, M, N, K, rc.P, rc.shift, gm);
                 break;
         }
     };
-    if (nt) go(IC<1>{});
-    else go(IC<0>{});
+    go(IC<1>{});
     return hipGetLastError();
 }
 
@@ -993,7 +1338,7 @@ static hipError_t launch_wp_band(int out_mode, int M, int N, int K, const uint8_
 template <int BM, int BN, int WM, int WN, int STAGES, int NWP = 4>
 static hipError_t launch_wp(int out_mode, int M, int N, int K, const uint8_t *A, long lda,
                             const int8_t *B, long ldb, const int32_t *col_off, const float *sa,
-                            const float *sb, void *C, long ldc, hipStream_t stream) {
+                            const float *sb, void *C, long ldc, bool classes, hipStream_t stream) {
     const long LIM = 1L << 31;
     long mband = lda > 0 ? LIM / lda : M, nband = ldb > 0 ? LIM / ldb : N;
     mband = mband >= M ? M : (mband / BM) * BM;
@@ -1006,7 +1351,61 @@ static hipError_t launch_wp(int out_mode, int M, int N, int K, const uint8_t *A,
             hipError_t e = launch_wp_band<BM, BN, WM, WN, STAGES, NWP>(
                 out_mode, mm, nn, K, A + m * lda, lda, B + n * ldb, ldb,
                 col_off ? col_off + n : nullptr, sa ? sa + m : nullptr, sb ? sb + n : nullptr,
-                (char *)C + (m * ldc + n) * 4, ldc, stream);
+                (char *)C + (m * ldc + n) * 4, ldc, classes, stream);
+            if (e != hipSuccess) return e;
+        }
+    }
+    return hipSuccess;
+}
+
+// The persistent 16x16x64 kernel over 128x128 tiles (row classes optional).
+template <int STAGES, int NWP>
+static hipError_t launch_kgp_band(int out_mode, int M, int N, int K, const uint8_t *A, long lda,
+                                  const int8_t *B, long ldb, const int32_t *col_off, const float *sa,
+                                  const float *sb, void *C, long ldc, bool classes, hipStream_t stream) {
+    if (M == 0 || N == 0 || K / IG_BK == 0) return hipSuccess;
+    if (K % (2 * IG_BK) != 0) return hipErrorInvalidValue;  // an even number of K tiles
+    const RowClasses rc = classes ? row_classes(C, ldc) : RowClasses{1, 0};
+    const int gm = rc.P > 1 ? 16 : 8;
+    const long Mc = (M + rc.P - 1) / rc.P;
+    const long ntiles = rc.P * ((Mc + 127) / 128) * ((N + (rc.shift ? 31 : 0) + 127) / 128);
+    const int grid = (int)(ntiles < device_cus() ? ntiles : device_cus());
+    const dim3 block(64 * (8 + NWP));
+    switch (out_mode) {
+        case 0:
+            hipLaunchKernelGGL((igemm_kgp_kernel<STAGES, NWP, 0, 1>), dim3(grid), block, 0, stream, A, lda, B, ldb,
+                               col_off, sa, sb, C, ldc, M, N, K, rc.P, rc.shift, gm);
+            break;
+        case 1:
+            hipLaunchKernelGGL((igemm_kgp_kernel<STAGES, NWP, 1, 1>), dim3(grid), block, 0, stream, A, lda, B, ldb,
+                               col_off, sa, sb, C, ldc, M, N, K, rc.P, rc.shift, gm);
+            break;
+        default:
+            hipLaunchKernelGGL((igemm_kgp_kernel<STAGES, NWP, 2, 1>), dim3(grid), block, 0, stream, A, lda, B, ldb,
+                               col_off, sa, sb, C, ldc, M, N, K, rc.P, rc.shift, gm);
+            break;
+    }
+    return hipGetLastError();
+}
+
+// 32-bit per-lane DMA offsets: row bands of A and column bands of B whose
+// byte spans stay below 2^31.
+template <int STAGES, int NWP>
+static hipError_t launch_kgp(int out_mode, int M, int N, int K, const uint8_t *A, long lda,
+                             const int8_t *B, long ldb, const int32_t *col_off, const float *sa,
+                             const float *sb, void *C, long ldc, bool classes, hipStream_t stream) {
+    const long LIM = 1L << 31;
+    long mband = lda > 0 ? LIM / lda : M, nband = ldb > 0 ? LIM / ldb : N;
+    mband = mband >= M ? M : (mband / 128) * 128;
+    nband = nband >= N ? N : (nband / 128) * 128;
+    if (mband <= 0 || nband <= 0) return hipErrorInvalidValue;
+    for (long m = 0; m < M; m += mband) {
+        for (long n = 0; n < N; n += nband) {
+            const int mm = (int)(M - m < mband ? M - m : mband);
+            const int nn = (int)(N - n < nband ? N - n : nband);
+            hipError_t e = launch_kgp_band<STAGES, NWP>(
+                out_mode, mm, nn, K, A + m * lda, lda, B + n * ldb, ldb, col_off ? col_off + n : nullptr,
+                sa ? sa + m : nullptr, sb ? sb + n : nullptr, (char *)C + (m * ldc + n) * 4, ldc, classes, stream);
             if (e != hipSuccess) return e;
         }
     }
@@ -1021,7 +1420,7 @@ static hipError_t launch_kg_band(int out_mode, int M, int N, int K, const uint8_
     const int nblk = ((M + 127) / 128) * ((N + 127) / 128);
     if (nblk == 0 || K / IG_BK == 0) return hipSuccess;
     const dim3 grid(nblk), block(64 * (8 + NWP));
-    const bool nt = (long)M * N * 4 <= (256L << 20);  // as in launch_wp_band
+    const bool nt = (long)M * N * 4 <= (256L << 20);  // outputs up to 256 MiB: streaming stores
     auto go = [&](auto NT) {
         constexpr int nts = decltype(NT)::value;
         switch (out_mode) {
@@ -1075,7 +1474,7 @@ static hipError_t launch_icfg(int out_mode, int M, int N, int K, const uint8_t *
     const int nblk = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
     if (nblk == 0) return hipSuccess;
     dim3 grid(nblk), block(64 * WM * WN);
-    const bool nt = (long)M * N * 4 <= (256L << 20);  // as in launch_wp_band
+    const bool nt = (long)M * N * 4 <= (256L << 20);  // outputs up to 256 MiB: streaming stores
     auto go = [&](auto NT) {
         constexpr int nts = decltype(NT)::value;
         switch (out_mode) {
@@ -1130,8 +1529,10 @@ hipError_t launch_igemm(int out_mode, int M, int N, int K, const uint8_t *A, lon
                         const float *sb, void *C, long ldc, hipStream_t stream) {
     if (K % 256 != 0 || lda % 16 != 0 || ldb < K) return hipErrorInvalidValue;
     // Tile choice (measured on the 350M-class and gemm_bench shapes):
-    //  * outputs beyond 256 MiB (the 50257-vocab head): producer/consumer
-    //    256x128 tiles, the stores of one tile draining under the next;
+    //  * outputs beyond 256 MiB (the 50257-vocab head): persistent
+    //    producer/consumer kernels, the stores of one tile draining under the
+    //    next; 128x128 row-class tiles when rows start off 128-byte lines,
+    //    256x128 tiles otherwise;
     //  * 256x256 tiles with 8 waves when they still cover most of the 256 CUs
     //    (K = 1024 projections: fewer operand bytes per output); 256x192 when
     //    those fill the CUs clearly better (4096 x 3072: 256 tiles, one round,
@@ -1141,14 +1542,22 @@ hipError_t launch_igemm(int out_mode, int M, int N, int K, const uint8_t *A, lon
     //    workgroup (same-box alternation against the persistent kernel:
     //    2048^3 12.18 against 12.60 us, FF2 19.02 against 20.75 us);
     //  * producer/consumer 128x128 tiles when those fill the chip over
-    //    several rounds;
+    //    several rounds (row classes when rows start off 128-byte lines);
     //  * 64x64 otherwise, and for K = 0 (the epilogue alone).
     const long t256 = (long)((M + 255) / 256) * ((N + 255) / 256);
     const long t128 = (long)((M + 127) / 128) * ((N + 127) / 128);
     const bool huge = (long)M * N * 4 > (256L << 20);
-    if (K > 0 && t256 >= 192 && huge)
+    if (K > 0 && t256 >= 192 && huge) {
+        // rows off 128-byte lines (the 50257-float head): row-class 128x128
+        // tiles, whose stores are whole lines, on the persistent 16x16x64
+        // kernel (head 4096 x 50257 x 1024, same box: 308-313 us against
+        // 392-397 us for plain 256x128 tiles on igemm_wp_kernel and 311 us
+        // for row classes there; bit-identical)
+        if (classes_fill(M, ldc, C, 128))
+            return launch_kgp<4, 2>(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa, sb, C, ldc, true, stream);
         return launch_wp<256, 128, 4, 2, 3>(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa, sb, C,
-                                            ldc, stream);
+                                            ldc, false, stream);
+    }
     if (K > 0 && t256 >= 192) {
         const long t192 = (long)((M + 255) / 256) * ((N + 191) / 192);
         const double area = (double)M * N;
@@ -1170,7 +1579,7 @@ hipError_t launch_igemm(int out_mode, int M, int N, int K, const uint8_t *A, lon
     }
     if (K > 0 && t128 >= 256)
         return launch_wp<128, 128, 4, 2, 3>(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa, sb, C,
-                                            ldc, stream);
+                                            ldc, classes_fill(M, ldc, C, 128), stream);
     return launch_split<64, 64, 2, 2, 4, 1>(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa, sb, C,
                                             ldc, stream);
 }

@@ -256,11 +256,13 @@ def test_igemm_persistent_multi_tile(M, N, K):
     np.testing.assert_array_equal(C[rows], ob.dequant((V + off).astype(np.int32), sa[rows], sb))
 
 
-def test_igemm_dequant_output_beyond_256mib():
-    # outputs past 256 MiB take the producer/consumer 256x128 kernel; every
-    # dequant operand (per-row, per-column scales and column offsets) is
-    # staged through LDS there
-    M, N, K = 4096, 16400, 256
+@pytest.mark.parametrize("N", [16400, 16384])
+def test_igemm_dequant_output_beyond_256mib(N):
+    # outputs past 256 MiB take the persistent producer/consumer kernels:
+    # 128x128 row-class tiles at a pitch off 128-byte lines (16400 floats: two
+    # classes), 256x128 tiles at a line-multiple pitch; every dequant operand
+    # (per-row, per-column scales and column offsets) is staged through LDS
+    M, K = 4096, 256
     Au = ob.u8((M, K), 70)
     Bq = ob.s8((K, N), 71)
     sa = ob.uniform((M,), 72, 1e-3, 1e-2)
@@ -329,6 +331,81 @@ def test_igemm_one_round_tiles_full_compare(M, N, K):
     V32 = V.astype(np.int32)
     np.testing.assert_array_equal(_dq_run(Au, Bq, sa, sb, off), ob.dequant((V32 + off).astype(np.int32), sa, sb))
     np.testing.assert_array_equal(_dq_run(Au, Bq, None, sb), ob.dequant(V32, None, sb))
+
+
+def _run_pitched(Au, Bq, ldc, shift, sa=None, sb=None, col_off=None):
+    """C (M x N) written at pitch ldc, starting `shift` elements into its
+    buffer; int32 when sb is None, else dequantised. Returns the M x N view."""
+    M, K = Au.shape
+    N = Bq.shape[1]
+    dBp, _ = pack(Bq)
+    dA = pcl.dev(Au)
+    total = (M - 1) * ldc + N + shift
+    dC = pcl.DeviceBuffer(4 * total)
+    pcl.check(pcl.lib.pcl_memset(dC.ptr, 0xFF, 4 * total))
+    cptr = dC.ptr + 4 * shift
+    if sb is None:
+        pcl.check(pcl.lib.pcl_gemm_u8s8_i32(dA.ptr, K, dBp.ptr, cptr, ldc, M, N, K, None))
+        dt = np.int32
+    else:
+        dsa = pcl.dev(sa) if sa is not None else None
+        dsb = pcl.dev(sb)
+        doff = pcl.dev(col_off) if col_off is not None else None
+        pcl.check(pcl.lib.pcl_gemm_u8s8_dq(dA.ptr, K, dBp.ptr, doff.ptr if doff else None,
+                                           dsa.ptr if dsa else None, dsb.ptr, cptr, ldc, M, N, K, None))
+        dt = np.float32
+    pcl.sync()
+    flat = dC.download((total,), dt)
+    out = np.lib.stride_tricks.as_strided(flat[shift:], (M, N), (4 * ldc, 4)).copy()
+    # nothing written between the rows
+    gaps = np.lib.stride_tricks.as_strided(flat[shift + N:], (M - 1, ldc - N), (4 * ldc, 4)) if ldc > N else None
+    if gaps is not None:
+        assert (gaps.view(np.uint32) == 0xFFFFFFFF).all()
+    return out
+
+
+# Outputs whose rows start off 128-byte lines (odd pitch: 32 row classes;
+# pitch = 2 mod 4: 16; a line-multiple pitch from a base 4 bytes into a
+# line: one shifted class) take row-class tiles on the producer/consumer
+# kernel: every output compared, int32 and dequantised, and the padding
+# between rows left untouched.
+@pytest.mark.parametrize("M,N,K,ldc,shift", [(4096, 1281, 512, 1281, 0), (4096, 1282, 768, 1282, 0),
+                                             (4096, 1280, 512, 1280, 1), (4000, 1300, 520, 1301, 3),
+                                             (4096, 2200, 256, 2203, 0)])
+def test_igemm_row_class_tiles_full_compare(M, N, K, ldc, shift):
+    Au = ob.u8((M, K), 120 + N % 91)
+    Bq = ob.s8((K, N), 121 + K % 83)
+    sa = ob.uniform((M,), 122, 1e-3, 1e-2)
+    sb = ob.uniform((N,), 123, 1e-3, 1e-2)
+    off = ob.s8((N,), 124).astype(np.int32) * 1000
+    announce("igemm row classes", M, N, K, ldc, shift)
+    V = _exact_f64(Au, Bq)
+    np.testing.assert_array_equal(_run_pitched(Au, Bq, ldc, shift), V)
+    V32 = V.astype(np.int32)
+    np.testing.assert_array_equal(_run_pitched(Au, Bq, ldc, shift, sa, sb, off),
+                                  ob.dequant((V32 + off).astype(np.int32), sa, sb))
+    np.testing.assert_array_equal(_run_pitched(Au, Bq, ldc, shift, None, sb),
+                                  ob.dequant(V32, None, sb))
+
+
+def test_igemm_row_class_tiles_beyond_256mib():
+    # the head's route (outputs past 256 MiB) with an odd pitch: 32 row
+    # classes of 128 rows; every output compared in row blocks
+    M, N, K = 4096, 16401, 256
+    Au = ob.u8((M, K), 130)
+    Bq = ob.s8((K, N), 131)
+    sa = ob.uniform((M,), 132, 1e-3, 1e-2)
+    sb = ob.uniform((N,), 133, 1e-3, 1e-2)
+    off = ob.s8((N,), 134).astype(np.int32) * 1000
+    announce("igemm row classes > 256 MiB", M, N, K)
+    C = _run_pitched(Au, Bq, N, 0)
+    for r in range(0, M, 512):
+        np.testing.assert_array_equal(C[r:r + 512], _exact_f64(Au[r:r + 512], Bq))
+    del C
+    C = _run_pitched(Au, Bq, N, 0, sa, sb, off)
+    for r in range(0, M, 512):
+        V = _exact_f64(Au[r:r + 512], Bq).astype(np.int32)
+        np.testing.assert_array_equal(C[r:r + 512], ob.dequant((V + off).astype(np.int32), sa[r:r + 512], sb))
 
 
 def test_quantizers_byte_exact():
