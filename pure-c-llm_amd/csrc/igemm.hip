@@ -982,26 +982,46 @@ __global__ __launch_bounds__(64 * (8 + NWP)) __attribute__((amdgpu_waves_per_eu(
 // igemm_wp_kernel (P, col_shift). K is a multiple of 256 (an even number of
 // K tiles per output tile: the two fragment slots alternate within a tile and
 // the reads ahead of a tile's last K tile are the next tile's first).
-template <int STAGES, int NWP, int OUT, int NTS>
-__global__ __launch_bounds__(64 * (8 + NWP)) __attribute__((amdgpu_waves_per_eu(
-    (8 + NWP + 3) / 4))) void igemm_kgp_kernel(const uint8_t *__restrict__ A, long lda,
+//
+// DYN: tiles handed out from a counter per XCD instead of fixed slots, so a
+// workgroup that starts late (its CU busy) takes fewer tiles and no tile
+// waits for it. The workgroups of XCD x (blockIdx % 8 == x) share the
+// logical tiles i * grid + s0 + j (its slots s0 .. s0 + cnt - 1, every round
+// i) in that order: elements j and cnt + j are workgroup j's first two
+// tiles (as with fixed slots), element 2 cnt + v goes to the fetch that
+// returns v from tile_ctr[x]. One more wave (the scheduler, no DMA, no MFMA)
+// fetches tile t + 2 when tile t starts (one atomic add with return, lane
+// 0), until a fetch has come back past the list, and at tile t's last K tile
+// -- a tile later, the atomic's latency covered; atomics are its only memory
+// operations, so neither the DMA stream nor the output stores wait behind
+// one -- writes the tile's logical index (or -1) into an LDS ring of four
+// before that K tile's barrier. The producers read it two barriers later, at
+// least STAGES K tiles before its first DMA (nk >= STAGES + 1), the consumers
+// at the end of tile t + 1; every wave sees the same sequence of tiles and
+// runs the same barriers. When its fetches are done every workgroup adds one
+// to tile_ctr[8 + x]; the last of the XCD's workgroups resets both counters
+// for the next launch (stream order). Counters start at zero.
+template <int STAGES, int NWP, int OUT, int NTS, int DYN>
+__global__ __launch_bounds__(64 * (8 + NWP + DYN)) __attribute__((amdgpu_waves_per_eu(
+    (8 + NWP + DYN + 3) / 4))) void igemm_kgp_kernel(const uint8_t *__restrict__ A, long lda,
                                               const int8_t *__restrict__ B, long ldb,
                                               const int32_t *__restrict__ col_off,
                                               const float *__restrict__ sa,
                                               const float *__restrict__ sb,
                                               void *__restrict__ Cv, long ldc, int M, int N, int K,
-                                              int P, int col_shift, int gm) {
+                                              int P, int col_shift, int gm, int *__restrict__ tile_ctr) {
     constexpr int BM = 128, BN = 128, BK = IG_BK, CH = BK / 16, RPI = 1024 / BK;
     constexpr int SIZE_A = BM * BK, STAGE = (BM + BN) * BK;
     constexpr int PIA = BM / (RPI * NWP), PIB = BN / (RPI * NWP), PL = PIA + PIB;
     constexpr int SCL = 2 * BN + BM + 128;      // floats per tile: sb, col_off, sa, spare
     constexpr int NS = OUT != 0 ? 8 / NWP : 0;  // epilogue-operand DMA instructions per producer
-    constexpr int LDS_BYTES = STAGES * STAGE + 3 * SCL * 4;
+    constexpr int LDS_BYTES = STAGES * STAGE + 3 * SCL * 4 + 16;
     static_assert(NWP == 2 || NWP == 4, "producer waves");
     static_assert(STAGES >= 3 && LDS_BYTES <= 160 * 1024, "ring");
     static_assert((STAGES - 1) * (PL + NS) <= 63, "vmcnt range");
     __shared__ __attribute__((aligned(1024))) int8_t lds[LDS_BYTES];
     float *scl = reinterpret_cast<float *>(lds + STAGES * STAGE);  // [3 tiles][sb | col_off | sa]
+    int *ring = reinterpret_cast<int *>(lds + STAGES * STAGE + 3 * SCL * 4);  // DYN: later tiles
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1013,15 +1033,78 @@ __global__ __launch_bounds__(64 * (8 + NWP)) __attribute__((amdgpu_waves_per_eu(
     const int slot = xcd_remap(blockIdx.x, nb);
     const int my_tiles = slot < ntiles ? (ntiles - 1 - slot) / nb + 1 : 0;
     const int nk = K / BK;
-    const int G = my_tiles * nk;  // K tiles this workgroup streams
-    if (G == 0) return;           // uniform: no barrier is left unmatched
-    auto tile_origin = [&](int i, int &cls, int &r0, int &n0) {
+    // K tiles this workgroup streams: all of them known here, or (DYN) the
+    // first AH + 1 tiles', growing as later ones are handed out
+    constexpr int AH = 1;  // DYN: tiles by slot beyond the first
+    int G = DYN ? min(my_tiles, AH + 1) * nk : my_tiles * nk;
+    if (G == 0) return;  // uniform: no barrier is left unmatched
+    // DYN: this XCD's slots s0 .. s0 + cnt - 1 and how many of its logical
+    // tiles exist (valid_x): element k of its list is tile
+    // (k / cnt) * nb + s0 + k % cnt, increasing in k
+    const int xcd = blockIdx.x % 8, xq = nb / 8, xr = nb % 8;
+    const int s0 = xcd * xq + min(xcd, xr), cnt = xq + (xcd < xr ? 1 : 0);
+    const int valid_x = (ntiles / nb) * cnt + min(max(ntiles % nb - s0, 0), cnt);
+    auto tile_origin = [&](int logical, int &cls, int &r0, int &n0) {
         int bm, bn;
-        tile_coords(i * nb + slot, nbm, nbn, gm, bm, bn);
+        tile_coords(logical, nbm, nbn, gm, bm, bn);
         cls = bm % P;
         r0 = bm / P * BM;
         n0 = bn * BN - (col_shift ? (int)((cb0 + (long)cls * ldc) & 31) : 0);
     };
+    // logical tile of local tile i (fixed slots; DYN: the first AH + 1 by
+    // slot, later ones from the ring)
+    auto logical_of = [&](int i) {
+        return DYN && i > AH ? __builtin_amdgcn_readfirstlane(ring[i & 3]) : i * nb + slot;
+    };
+
+    if (DYN && wave == 8 + NWP) {
+        // ------------------------------------------------------ scheduler
+        static_assert(AH == 1, "one fetch in flight, made and used within a tile");
+        int Gs = G;
+        bool more = my_tiles >= AH + 1;  // tile t + 1 exists and no fetch came back empty
+        __builtin_amdgcn_s_barrier();    // P0
+        for (int t = 0; t * nk < Gs; t++) {
+            // Tile t starts: fetch tile t + 2. The atomic runs on lane 0
+            // alone (exec narrowed inside the asm) and every tile, adding 0
+            // once fetching is over: its result register is then defined on
+            // every path and read only after the wait below (the compiler,
+            // unaware of the atomic, would otherwise copy it at a merge
+            // before it lands; its own atomic would wait for it at once).
+            int fetched;
+            unsigned long long exec_save;
+            const int inc = more ? 1 : 0, voff0 = 0;
+            asm volatile(
+                "s_mov_b64 %1, exec\n\t"
+                "s_mov_b64 exec, 1\n\t"
+                "global_atomic_add %0, %2, %3, %4 sc0\n\t"
+                "s_mov_b64 exec, %1"
+                : "=&v"(fetched), "=&s"(exec_save)
+                : "v"(voff0), "v"(inc), "s"(tile_ctr + xcd)
+                : "memory");
+            for (int kk = 0; kk < nk; kk++) {
+                if (kk == nk - 1 && inc) {
+                    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+                    asm volatile("" : "+v"(fetched));
+                    const int v = __builtin_amdgcn_readfirstlane(fetched);
+                    const int k = (AH + 1) * cnt + v;
+                    const int nxt = k < valid_x ? (k / cnt) * nb + s0 + k % cnt : -1;
+                    if (lane == 0) ring[(t + AH + 1) & 3] = nxt;
+                    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                    if (nxt >= 0) Gs += nk;
+                    else more = false;
+                }
+                __builtin_amdgcn_s_barrier();  // B(t nk + kk)
+            }
+        }
+        // every fetch of this workgroup has returned: count it done; the
+        // XCD's last workgroup resets its counters
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+        if (lane == 0 && atomicAdd(tile_ctr + IGEMM_TILE_CTRS / 2 + xcd, 1) == cnt - 1) {
+            atomicExch(tile_ctr + xcd, 0);
+            atomicExch(tile_ctr + IGEMM_TILE_CTRS / 2 + xcd, 0);
+        }
+        return;
+    }
 
     if (wave >= 8) {
         // ------------------------------------------------------ producers
@@ -1035,7 +1118,7 @@ __global__ __launch_bounds__(64 * (8 + NWP)) __attribute__((amdgpu_waves_per_eu(
         // sb again into the spare slot).
         auto begin_tile = [&](int i) {
             int cls, r0, n0;
-            tile_origin(i, cls, r0, n0);
+            tile_origin(logical_of(i), cls, r0, n0);
 #pragma unroll
             for (int d = 0; d < PL; d++) {
                 const bool isA = d < PIA;
@@ -1110,6 +1193,11 @@ __global__ __launch_bounds__(64 * (8 + NWP)) __attribute__((amdgpu_waves_per_eu(
         for (int t = 2; t < STAGES; t++)
             if (t < G) hist = (hist << 1) | (dma_next() ? 1u : 0u);
         for (int g = 0; g < G; g++) {
+            // DYN: tile t > AH was published before B((t - 1) nk - 1); read
+            // it here, STAGES or more K tiles before its first DMA
+            if (DYN && g >= AH * nk + 1 && g % nk == 1 &&
+                __builtin_amdgcn_readfirstlane(ring[(g / nk + 1) & 3]) >= 0)
+                G += nk;
             // K tile g+1 has landed; tiles g+2 .. g+STAGES-1 may still fly
             if (g + STAGES - 1 < G) wait_younger(IC<STAGES - 2>{});
             else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
@@ -1193,16 +1281,20 @@ __global__ __launch_bounds__(64 * (8 + NWP)) __attribute__((amdgpu_waves_per_eu(
     };
 
     int g = 0;
-    for (int t = 0; t < my_tiles; t++) {
+    for (int t = 0; DYN || t < my_tiles; t++) {
         for (int kt = 0; kt < nk; kt += 2, g += 2) {
             ktile(g, IC<0>{});
             ktile(g + 1, IC<1>{});
         }
+        // DYN: tile t + 1 (the first AH + 1 by slot; later ones published
+        // before B(t nk - 1), read after this tile's last barrier)
+        const int next = !DYN ? 0 : t + 1 <= AH ? (my_tiles >= t + 2 ? 1 : -1)
+                                                : __builtin_amdgcn_readfirstlane(ring[(t + 1) & 3]);
         // Epilogue of tile t (operands from LDS buffer t % 3; stores as in
         // igemm_kg_kernel, 2 rows x 32 columns per store after two lane
         // swaps). The stores carry no wait: they drain under tile t + 1.
         int cls, r0, n0;
-        tile_origin(t, cls, r0, n0);
+        tile_origin(logical_of(t), cls, r0, n0);
         const float *sc = scl + (t % 3) * SCL;
         const int wrow0 = r0 + wm * WTM, wcol0 = n0 + wn * WTN;  // class-local row
         float sbv[NBN], sav[8];
@@ -1262,6 +1354,7 @@ __global__ __launch_bounds__(64 * (8 + NWP)) __attribute__((amdgpu_waves_per_eu(
             for (int j = 0; j < NBN; j++)
 #pragma unroll
                 for (int v = 0; v < 4; v++) acc[i][j][v] = 0;
+        if (DYN && next < 0) break;
     }
     lds_wait<0>();
 }
@@ -1359,10 +1452,14 @@ static hipError_t launch_wp(int out_mode, int M, int N, int K, const uint8_t *A,
 }
 
 // The persistent 16x16x64 kernel over 128x128 tiles (row classes optional).
+// tile_ctr (IGEMM_TILE_CTRS zeroed ints, or NULL): tiles handed out per XCD
+// from these counters when a tile has more than STAGES K tiles, else fixed
+// slots.
 template <int STAGES, int NWP>
 static hipError_t launch_kgp_band(int out_mode, int M, int N, int K, const uint8_t *A, long lda,
                                   const int8_t *B, long ldb, const int32_t *col_off, const float *sa,
-                                  const float *sb, void *C, long ldc, bool classes, hipStream_t stream) {
+                                  const float *sb, void *C, long ldc, bool classes, int *tile_ctr,
+                                  hipStream_t stream) {
     if (M == 0 || N == 0 || K / IG_BK == 0) return hipSuccess;
     if (K % (2 * IG_BK) != 0) return hipErrorInvalidValue;  // an even number of K tiles
     const RowClasses rc = classes ? row_classes(C, ldc) : RowClasses{1, 0};
@@ -1370,21 +1467,22 @@ static hipError_t launch_kgp_band(int out_mode, int M, int N, int K, const uint8
     const long Mc = (M + rc.P - 1) / rc.P;
     const long ntiles = rc.P * ((Mc + 127) / 128) * ((N + (rc.shift ? 31 : 0) + 127) / 128);
     const int grid = (int)(ntiles < device_cus() ? ntiles : device_cus());
-    const dim3 block(64 * (8 + NWP));
-    switch (out_mode) {
-        case 0:
-            hipLaunchKernelGGL((igemm_kgp_kernel<STAGES, NWP, 0, 1>), dim3(grid), block, 0, stream, A, lda, B, ldb,
-                               col_off, sa, sb, C, ldc, M, N, K, rc.P, rc.shift, gm);
-            break;
-        case 1:
-            hipLaunchKernelGGL((igemm_kgp_kernel<STAGES, NWP, 1, 1>), dim3(grid), block, 0, stream, A, lda, B, ldb,
-                               col_off, sa, sb, C, ldc, M, N, K, rc.P, rc.shift, gm);
-            break;
-        default:
-            hipLaunchKernelGGL((igemm_kgp_kernel<STAGES, NWP, 2, 1>), dim3(grid), block, 0, stream, A, lda, B, ldb,
-                               col_off, sa, sb, C, ldc, M, N, K, rc.P, rc.shift, gm);
-            break;
-    }
+    const bool dyn = tile_ctr != nullptr && K / IG_BK >= STAGES + 1;
+    const dim3 block(64 * (8 + NWP + (dyn ? 1 : 0)));
+    auto go = [&](auto OUTC, auto DYNC) {
+        constexpr int o = decltype(OUTC)::value, dy = decltype(DYNC)::value;
+        hipLaunchKernelGGL((igemm_kgp_kernel<STAGES, NWP, o, 1, dy>), dim3(grid), block, 0, stream, A, lda, B,
+                           ldb, col_off, sa, sb, C, ldc, M, N, K, rc.P, rc.shift, gm, dy ? tile_ctr : nullptr);
+    };
+    auto go_out = [&](auto DYNC) {
+        switch (out_mode) {
+            case 0: go(IC<0>{}, DYNC); break;
+            case 1: go(IC<1>{}, DYNC); break;
+            default: go(IC<2>{}, DYNC); break;
+        }
+    };
+    if (dyn) go_out(IC<1>{});
+    else go_out(IC<0>{});
     return hipGetLastError();
 }
 
@@ -1393,7 +1491,8 @@ static hipError_t launch_kgp_band(int out_mode, int M, int N, int K, const uint8
 template <int STAGES, int NWP>
 static hipError_t launch_kgp(int out_mode, int M, int N, int K, const uint8_t *A, long lda,
                              const int8_t *B, long ldb, const int32_t *col_off, const float *sa,
-                             const float *sb, void *C, long ldc, bool classes, hipStream_t stream) {
+                             const float *sb, void *C, long ldc, bool classes, int *tile_ctr,
+                             hipStream_t stream) {
     const long LIM = 1L << 31;
     long mband = lda > 0 ? LIM / lda : M, nband = ldb > 0 ? LIM / ldb : N;
     mband = mband >= M ? M : (mband / 128) * 128;
@@ -1405,7 +1504,8 @@ static hipError_t launch_kgp(int out_mode, int M, int N, int K, const uint8_t *A
             const int nn = (int)(N - n < nband ? N - n : nband);
             hipError_t e = launch_kgp_band<STAGES, NWP>(
                 out_mode, mm, nn, K, A + m * lda, lda, B + n * ldb, ldb, col_off ? col_off + n : nullptr,
-                sa ? sa + m : nullptr, sb ? sb + n : nullptr, (char *)C + (m * ldc + n) * 4, ldc, classes, stream);
+                sa ? sa + m : nullptr, sb ? sb + n : nullptr, (char *)C + (m * ldc + n) * 4, ldc, classes,
+                tile_ctr, stream);
             if (e != hipSuccess) return e;
         }
     }
@@ -1524,9 +1624,18 @@ static hipError_t launch_split(int out_mode, int M, int N, int K, const uint8_t 
     return hipSuccess;
 }
 
+__global__ void igemm_tiles_zero_kernel(int *ctr) {
+    if (threadIdx.x < IGEMM_TILE_CTRS) ctr[threadIdx.x] = 0;
+}
+
+hipError_t launch_igemm_tiles_init(int *ctr, hipStream_t s) {
+    hipLaunchKernelGGL(igemm_tiles_zero_kernel, dim3(1), dim3(64), 0, s, ctr);
+    return hipGetLastError();
+}
+
 hipError_t launch_igemm(int out_mode, int M, int N, int K, const uint8_t *A, long lda,
                         const int8_t *Bpk, long ldb, const int32_t *col_off, const float *sa,
-                        const float *sb, void *C, long ldc, hipStream_t stream) {
+                        const float *sb, void *C, long ldc, int *tile_ctr, hipStream_t stream) {
     if (K % 256 != 0 || lda % 16 != 0 || ldb < K) return hipErrorInvalidValue;
     // Tile choice (measured on the 350M-class and gemm_bench shapes):
     //  * outputs beyond 256 MiB (the 50257-vocab head): persistent
@@ -1554,7 +1663,8 @@ hipError_t launch_igemm(int out_mode, int M, int N, int K, const uint8_t *A, lon
         // 392-397 us for plain 256x128 tiles on igemm_wp_kernel and 311 us
         // for row classes there; bit-identical)
         if (classes_fill(M, ldc, C, 128))
-            return launch_kgp<4, 2>(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa, sb, C, ldc, true, stream);
+            return launch_kgp<4, 2>(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa, sb, C, ldc, true, tile_ctr,
+                                    stream);
         return launch_wp<256, 128, 4, 2, 3>(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa, sb, C,
                                             ldc, false, stream);
     }

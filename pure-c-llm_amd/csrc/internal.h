@@ -62,9 +62,14 @@ hipError_t launch_elementwise(int op, long n, float *out, const float *a, const 
 // Requires K % 256 == 0, lda % 16 == 0, A and Bpk 16-byte aligned, and packed
 // weight rows of ldb >= K bytes (the packers use roundup(K_true, 256), zero
 // past the true K; A columns past the true K must be 0x80).
+// tile_ctr: IGEMM_TILE_CTRS ints, zero between launches (launch_igemm_tiles_init
+// once; the kernels that use them leave them zero), private to the stream; or
+// NULL (persistent kernels then give each workgroup fixed tiles).
+constexpr int IGEMM_TILE_CTRS = 16;  // a fetch counter and a done counter per XCD
 hipError_t launch_igemm(int out_mode, int M, int N, int K, const uint8_t *A, long lda,
                         const int8_t *Bpk, long ldb, const int32_t *col_off, const float *sa,
-                        const float *sb, void *C, long ldc, hipStream_t stream);
+                        const float *sb, void *C, long ldc, int *tile_ctr, hipStream_t stream);
+hipError_t launch_igemm_tiles_init(int *ctr, hipStream_t s);
 // Copy A (M x K, lda) into dst (M x Kd, Kd >= K), padding with 0x80.
 hipError_t launch_pad_a_u8(const uint8_t *A, long lda, int M, int K, uint8_t *dst, int Kd,
                            hipStream_t stream);

@@ -138,6 +138,7 @@ struct StreamScratch {
     void *realign = nullptr;
     size_t realign_cap = 0;
     unsigned *amax = nullptr;  // per-tensor amax bits
+    int *tiles = nullptr;      // the INT8 GEMM's per-XCD tile counters (zero between calls)
     // Set once a graph has been captured on the stream: buffers a graph may
     // reference are never freed before the stream is destroyed.
     bool pinned = false;
@@ -188,6 +189,13 @@ int get_scratch(hipStream_t s, size_t part_bytes, size_t aux_bytes, ScratchLease
     if (!sc.amax) {
         if (hipMalloc((void **)&sc.amax, 256) != hipSuccess)
             return set_error(PCL_ERR_OOM, "amax scratch allocation failed");
+    }
+    if (!sc.tiles) {
+        if (hipMalloc((void **)&sc.tiles, 256) != hipSuccess)
+            return set_error(PCL_ERR_OOM, "tile counter allocation failed");
+        // zeroed by a kernel on the stream (also inside a capture, where a
+        // replay re-zeroes counters that are zero anyway)
+        HIP_OK(pcl::launch_igemm_tiles_init(sc.tiles, s));
     }
     out->p = &sc;
     return PCL_OK;
@@ -382,6 +390,7 @@ int pcl_stream_destroy(void *stream) {
             if (sc.aux) HIP_OK(hipFree(sc.aux));
             if (sc.realign) HIP_OK(hipFree(sc.realign));
             if (sc.amax) HIP_OK(hipFree(sc.amax));
+            if (sc.tiles) HIP_OK(hipFree(sc.tiles));
             g_scratch.erase(it);
         }
     }
@@ -419,6 +428,8 @@ int pcl_release_scratch(void *stream) {
     entry->retired.clear();
     if (entry->amax) HIP_OK(hipFree(entry->amax));
     entry->amax = nullptr;
+    if (entry->tiles) HIP_OK(hipFree(entry->tiles));
+    entry->tiles = nullptr;
     return PCL_OK;
 }
 
@@ -1104,7 +1115,9 @@ static int igemm_common(int out_mode, const uint8_t *A, int lda, const int8_t *B
         return PCL_OK;
     }
     if (K % 256 == 0 && lda % 16 == 0 && aligned16(A)) {
-        HIP_OK(pcl::launch_igemm(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa, sb, C, ldc, s));
+        ScratchLease sc;  // the stream's tile counters
+        PCL_OK_OR_RETURN(get_scratch(s, 0, 0, &sc));
+        HIP_OK(pcl::launch_igemm(out_mode, M, N, K, A, lda, Bpk, ldb, col_off, sa, sb, C, ldc, sc->tiles, s));
         return PCL_OK;
     }
     // K not a multiple of 256 (the K tile granularity), or unaligned
@@ -1115,7 +1128,7 @@ static int igemm_common(int out_mode, const uint8_t *A, int lda, const int8_t *B
     PCL_OK_OR_RETURN(get_scratch(s, 0, (size_t)M * Kp, &sc));
     uint8_t *Ap = (uint8_t *)sc->aux;
     HIP_OK(pcl::launch_pad_a_u8(A, lda, M, K, Ap, Kp, s));
-    HIP_OK(pcl::launch_igemm(out_mode, M, N, Kp, Ap, Kp, Bpk, ldb, col_off, sa, sb, C, ldc, s));
+    HIP_OK(pcl::launch_igemm(out_mode, M, N, Kp, Ap, Kp, Bpk, ldb, col_off, sa, sb, C, ldc, sc->tiles, s));
     return PCL_OK;
 }
 

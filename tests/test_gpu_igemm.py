@@ -388,10 +388,14 @@ def test_igemm_row_class_tiles_full_compare(M, N, K, ldc, shift):
                                   ob.dequant(V32, None, sb))
 
 
-def test_igemm_row_class_tiles_beyond_256mib():
+@pytest.mark.parametrize("K", [256, 768])
+def test_igemm_row_class_tiles_beyond_256mib(K):
     # the head's route (outputs past 256 MiB) with an odd pitch: 32 row
-    # classes of 128 rows; every output compared in row blocks
-    M, N, K = 4096, 16401, 256
+    # classes of 128 rows on the persistent kernel, tiles in fixed slots
+    # (K = 256: two K tiles per tile) or handed out from the stream's per-XCD
+    # counters (K = 768), three calls in a row (the counters must be back at
+    # zero after each); every output compared in row blocks
+    M, N = 4096, 16401
     Au = ob.u8((M, K), 130)
     Bq = ob.s8((K, N), 131)
     sa = ob.uniform((M,), 132, 1e-3, 1e-2)
@@ -406,6 +410,11 @@ def test_igemm_row_class_tiles_beyond_256mib():
     for r in range(0, M, 512):
         V = _exact_f64(Au[r:r + 512], Bq).astype(np.int32)
         np.testing.assert_array_equal(C[r:r + 512], ob.dequant((V + off).astype(np.int32), sa[r:r + 512], sb))
+    del C
+    C = _run_pitched(Au, Bq, N, 0, None, sb)
+    for r in range(0, M, 1024):
+        V = _exact_f64(Au[r:r + 1024], Bq).astype(np.int32)
+        np.testing.assert_array_equal(C[r:r + 1024], ob.dequant(V, None, sb))
 
 
 def test_quantizers_byte_exact():
