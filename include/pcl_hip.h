@@ -86,7 +86,10 @@ void *pcl_stream_create(void);
 int pcl_stream_destroy(void *stream);
 /* Scratch memory. Calls keep per-stream device buffers that grow to the
  * largest request and are reused: split-K partial sums, the padded INT8
- * activations, pcl_head_ce's logits chunk, and the realigned copies of
+ * activations, the INT8 GEMM's tile counters (64 bytes: the persistent kernel
+ * of outputs past 256 MiB hands its tiles out from them, so calls on one
+ * stream must not overlap -- stream order guarantees it), pcl_head_ce's
+ * logits chunk, and the realigned copies of
  * misaligned FP32 operands that pcl_sgemm makes for products of >= 2^30
  * multiply-adds (for the trainer's head backward over 4096 x 50257 logits
  * about 0.8 GB). pcl_release_scratch waits for the stream (hip_stream, NULL =
