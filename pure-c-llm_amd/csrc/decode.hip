@@ -42,8 +42,12 @@ __device__ __forceinline__ float dec_block_sum(float v, float *red) {
 // INT8 step's projections carry no bias); the cache rows are D floats. dh
 // divides 256. DHT > 0: the head size at compile time, cache rows read as
 // 16-byte vectors (D % 4 == 0, 16-byte aligned cache); DHT == 0: any head
-// size, scalar reads. Each thread sums its own terms in key order, as before;
-// the loads of 8 keys are issued together.
+// size, scalar reads. p . v: with DHT > 0 thread t owns 4 columns (t mod
+// DHT/4) of every (256 / (DHT/4))-th key, and issues the 16-byte loads of 8
+// of its keys together, so at the grown model's head size (32) and a block of
+// 256 every V row the sum needs is in flight at once (one memory latency, not
+// four); each thread sums its keys in order, then the key groups are added in
+// order. DHT == 0: thread (column, key group), 8 keys per load batch.
 template <int DHT>
 __global__ __launch_bounds__(256) void dec_attn_kernel(const float *__restrict__ qkv,
                                                        const float *__restrict__ bqkv,
@@ -52,8 +56,9 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(const float *__restrict__
                                                        float *__restrict__ att, int D, int dh_rt,
                                                        const int *__restrict__ tokpos,
                                                        float scale) {
-    extern __shared__ float dec_lds[];  // [blk] scores, then [256] partial sums
-    __shared__ float red[4], qs[256], ks[256], vs[256];
+    extern __shared__ __attribute__((aligned(16))) float dec_lds[];  // [blk] scores, then partial sums
+    __shared__ float red[4], qs[256], ks[256];
+    __shared__ __attribute__((aligned(16))) float vs[256];
     const int dh = DHT > 0 ? DHT : dh_rt;
     const int h = blockIdx.x, tid = threadIdx.x, off = h * dh;
     const int pos = tokpos[1];
@@ -108,28 +113,63 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(const float *__restrict__
         sloc += e;
     }
     const float inv = 1.0f / dec_block_sum(sloc, red);  // the block sum also orders sc[] writes
-    // output: thread t owns column d = t % dh of key group t / dh
-    const int G = 256 / dh, d = tid % dh, gq = tid / dh;
-    float acc = 0.f;
-    if (gq < G) {
-        const float *vcol = vc + off + d;
-        int j = gq;
-        for (; j + 7 * G < pos; j += 8 * G) {  // 8 cache rows, none of them row pos
-            float v[8];
-#pragma unroll
-            for (int u = 0; u < 8; u++) v[u] = vcol[(long)(j + u * G) * D];
-#pragma unroll
-            for (int u = 0; u < 8; u++) acc += sc[j + u * G] * inv * v[u];
-        }
-        for (; j <= pos; j += G) acc += sc[j] * inv * (j == pos ? vnew[d] : vcol[(long)j * D]);
-    }
     float *part = dec_lds + ((pos + 1 + 3) & ~3);
-    part[tid] = acc;
-    __syncthreads();
-    if (tid < dh) {
-        float o = 0.f;
-        for (int g2 = 0; g2 < G; g2++) o += part[g2 * dh + tid];
-        att[off + tid] = o;
+    if constexpr (DHT > 0) {
+        typedef float v4f_t __attribute__((ext_vector_type(4)));
+        constexpr int L = DHT / 4, KG = 256 / L;  // lanes per V row, key groups
+        const int d4 = tid % L, kg = tid / L;
+        const float *vrow = vc + off + 4 * d4;
+        v4f_t acc = {0.f, 0.f, 0.f, 0.f};
+        for (int j0 = kg; j0 <= pos; j0 += 8 * KG) {
+            v4f_t v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {  // rows past pos read row 0 and add nothing
+                const int j = j0 + u * KG;
+                v[u] = *reinterpret_cast<const v4f_t *>(vrow + (long)(j < pos ? j : 0) * D);
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int j = j0 + u * KG;
+                if (j <= pos) {
+                    const float p = sc[j] * inv;
+                    const v4f_t vv = j == pos ? *reinterpret_cast<const v4f_t *>(vnew + 4 * d4) : v[u];
+                    acc[0] += p * vv[0];
+                    acc[1] += p * vv[1];
+                    acc[2] += p * vv[2];
+                    acc[3] += p * vv[3];
+                }
+            }
+        }
+        *reinterpret_cast<v4f_t *>(part + 4 * tid) = acc;  // part[kg][4 d4 + c]
+        __syncthreads();
+        if (tid < DHT) {
+            float o = 0.f;
+            for (int g2 = 0; g2 < KG; g2++) o += part[g2 * DHT + tid];
+            att[off + tid] = o;
+        }
+    } else {
+        // output: thread t owns column d = t % dh of key group t / dh
+        const int G = 256 / dh, d = tid % dh, gq = tid / dh;
+        float acc = 0.f;
+        if (gq < G) {
+            const float *vcol = vc + off + d;
+            int j = gq;
+            for (; j + 7 * G < pos; j += 8 * G) {  // 8 cache rows, none of them row pos
+                float v[8];
+#pragma unroll
+                for (int u = 0; u < 8; u++) v[u] = vcol[(long)(j + u * G) * D];
+#pragma unroll
+                for (int u = 0; u < 8; u++) acc += sc[j + u * G] * inv * v[u];
+            }
+            for (; j <= pos; j += G) acc += sc[j] * inv * (j == pos ? vnew[d] : vcol[(long)j * D]);
+        }
+        part[tid] = acc;
+        __syncthreads();
+        if (tid < dh) {
+            float o = 0.f;
+            for (int g2 = 0; g2 < G; g2++) o += part[g2 * dh + tid];
+            att[off + tid] = o;
+        }
     }
 }
 
@@ -176,7 +216,7 @@ hipError_t launch_decode_attn(const float *qkv, const float *bqkv, float *kc, fl
                               int D, int H, int blk, const int *tokpos, hipStream_t s) {
     const int dh = D / H;
     if (dh <= 0 || 256 % dh != 0) return hipErrorInvalidValue;
-    const size_t lds = sizeof(float) * ((size_t)((blk + 3) & ~3) + 256);
+    const size_t lds = sizeof(float) * ((size_t)((blk + 3) & ~3) + 1024);  // scores, then 256 x 4 partials
     const float scale = 1.0f / sqrtf((float)dh);
     const bool vec = D % 4 == 0 && ((reinterpret_cast<uintptr_t>(kc) | reinterpret_cast<uintptr_t>(vc)) & 15) == 0;
     if (vec && dh == 32)
