@@ -817,6 +817,119 @@ __device__ __forceinline__ float gv_sum4(float v, float *red) {
     return red[0] + red[1] + red[2] + red[3];
 }
 
+// The input transform of the decode rows. A thread owns elements tid + 256 e;
+// the transform's per-element vectors of its first QPF elements are loaded
+// into registers up front (qx_prefetch), the rest when they are used.
+constexpr int QPF = 8;
+
+template <int QX>
+__device__ __forceinline__ void qx_prefetch(const float *__restrict__ g, const float *__restrict__ b, int K,
+                                            float (&gpf)[QPF], float (&bpf)[QPF]) {
+#pragma unroll
+    for (int e = 0; e < QPF; e++) {
+        const int i = (int)threadIdx.x + 256 * e;
+        gpf[e] = QX == QX_LN && i < K ? g[i] : 0.f;
+        bpf[e] = QX != QX_NONE && i < K ? b[i] : 0.f;
+    }
+}
+
+__device__ __forceinline__ float qx_gelu(float v) {
+    return 0.5f * v * (1.0f + tanhf(0.7978845608028654f * (v + 0.044715f * v * v * v)));
+}
+
+// xf[0..K) = transform(X): QX_LN LayerNorm (mean, then the mean square of the
+// deviations, each a sum over the thread's elements in order and then over the
+// four waves; (x - mu) * rsd * g + b), QX_BIAS_GELU tanh-GELU(x + b), QX_NONE
+// x. The row is read once into LDS; each thread revisits only its own
+// elements. Ends with the block's barrier.
+template <int QX>
+__device__ __forceinline__ void qx_row(const float *__restrict__ X, const float *__restrict__ g,
+                                       const float *__restrict__ b, int K, const float (&gpf)[QPF],
+                                       const float (&bpf)[QPF], float *xf, float *red) {
+    const int tid = threadIdx.x;
+    if constexpr (QX == QX_LN) {
+        float s0 = 0.f;
+        for (int i = tid; i < K; i += 256) {
+            const float v = X[i];
+            xf[i] = v;
+            s0 += v;
+        }
+        const float mu = gv_sum4(s0, red) / K;
+        float q = 0.f;
+        for (int i = tid; i < K; i += 256) {
+            const float d = xf[i] - mu;
+            q += d * d;
+        }
+        const float var = gv_sum4(q, red) / K;
+        const float rsd = 1.0f / sqrtf(var + 1e-5f);
+#pragma unroll
+        for (int e = 0; e < QPF; e++) {
+            const int i = tid + 256 * e;
+            if (i < K) xf[i] = (xf[i] - mu) * rsd * gpf[e] + bpf[e];
+        }
+        for (int i = tid + 256 * QPF; i < K; i += 256) xf[i] = (xf[i] - mu) * rsd * g[i] + b[i];
+    } else if constexpr (QX == QX_BIAS_GELU) {
+#pragma unroll
+        for (int e = 0; e < QPF; e++) {
+            const int i = tid + 256 * e;
+            if (i < K) xf[i] = qx_gelu(X[i] + bpf[e]);
+        }
+        for (int i = tid + 256 * QPF; i < K; i += 256) xf[i] = qx_gelu(X[i] + b[i]);
+    } else {
+        for (int i = tid; i < K; i += 256) xf[i] = X[i];
+    }
+    __syncthreads();
+}
+
+// Sum over the block of one value per thread, in the order of gv_sum4, into
+// a red[4] used once per launch (no barrier before the writes).
+__device__ __forceinline__ float gv_sum4_once(float v, float *red) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return red[0] + red[1] + red[2] + red[3];
+}
+
+// qx_row for rows of at most 256 * QPF elements, kept in registers: v[e] =
+// transform(X)[tid + 256 e] (0 past K). The same operations in the same
+// order as qx_row, so the same values; no LDS round trips, one barrier per
+// LayerNorm sum. red: 8 floats, each half used once.
+template <int QX>
+__device__ __forceinline__ void qx_regs(const float *__restrict__ X, int K, const float (&gpf)[QPF],
+                                        const float (&bpf)[QPF], float (&v)[QPF], float *red) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int e = 0; e < QPF; e++) {
+        const int i = tid + 256 * e;
+        v[e] = i < K ? X[i] : 0.f;
+    }
+    if constexpr (QX == QX_LN) {
+        float s0 = 0.f;
+#pragma unroll
+        for (int e = 0; e < QPF; e++)
+            if (tid + 256 * e < K) s0 += v[e];
+        const float mu = gv_sum4_once(s0, red) / K;
+        float q = 0.f;
+#pragma unroll
+        for (int e = 0; e < QPF; e++) {
+            if (tid + 256 * e < K) {
+                const float d = v[e] - mu;
+                q += d * d;
+            }
+        }
+        const float var = gv_sum4_once(q, red + 4) / K;
+        const float rsd = 1.0f / sqrtf(var + 1e-5f);
+#pragma unroll
+        for (int e = 0; e < QPF; e++)
+            if (tid + 256 * e < K) v[e] = (v[e] - mu) * rsd * gpf[e] + bpf[e];
+    } else if constexpr (QX == QX_BIAS_GELU) {
+#pragma unroll
+        for (int e = 0; e < QPF; e++)
+            if (tid + 256 * e < K) v[e] = qx_gelu(v[e] + bpf[e]);
+    }
+}
+
 // Thread layout: LPR lanes per weight row (16-byte pieces k = 16*lane +
 // 16*LPR*u), 256/LPR row groups of RPL = 2 rows: RPB = 512/LPR rows per block,
 // so shallow products spread over more blocks; UK 16-byte loads per row per
@@ -832,7 +945,7 @@ __global__ __launch_bounds__(GV_THREADS) void igemv_q_kernel(
     const int Kp = (int)ldb;
     float *xf = reinterpret_cast<float *>(gv_dyn);          // [Kp]
     int8_t *xs = reinterpret_cast<int8_t *>(xf + Kp);        // [Kp]
-    __shared__ float red[4], mred[4];
+    __shared__ float red[4], mred[4], red8[8];
     __shared__ int32_t res[RPB];
 
     const int tid = threadIdx.x;
@@ -851,41 +964,46 @@ __global__ __launch_bounds__(GV_THREADS) void igemv_q_kernel(
     };
     v4i wn[UK][RPL];
     load_batch(wn, 16 * j);  // in flight while the row is made
-
-    if constexpr (QX == QX_LN) {
-        // the row is read once into LDS; each thread revisits only its own elements
-        float s0 = 0.f;
-        for (int i = tid; i < K; i += 256) {
-            const float v = X[i];
-            xf[i] = v;
-            s0 += v;
-        }
-        const float mu = gv_sum4(s0, red) / K;
-        float q = 0.f;
-        for (int i = tid; i < K; i += 256) {
-            const float d = xf[i] - mu;
-            q += d * d;
-        }
-        const float var = gv_sum4(q, red) / K;
-        const float rsd = 1.0f / sqrtf(var + 1e-5f);
-        for (int i = tid; i < K; i += 256) xf[i] = (xf[i] - mu) * rsd * g[i] + b[i];
-    } else if constexpr (QX == QX_BIAS_GELU) {
-        for (int i = tid; i < K; i += 256) {
-            const float v = X[i] + b[i];
-            xf[i] = 0.5f * v * (1.0f + tanhf(0.7978845608028654f * (v + 0.044715f * v * v * v)));
-        }
-    } else {
-        for (int i = tid; i < K; i += 256) xf[i] = X[i];
+    // what does not depend on the row loads with the weights, so the block's
+    // chain holds one dependent global read (the row) instead of three: the
+    // transform's vectors for a thread's first QPF elements, the epilogue's
+    // scale, bias and residual of output n0 + tid
+    float gpf[QPF], bpf[QPF];
+    qx_prefetch<QX>(g, b, K, gpf, bpf);
+    float esb = 0.f, ebias = 0.f, ey = 0.f;
+    if (tid < RPB && n0 + tid < N) {
+        esb = sb[n0 + tid];
+        if (EPI == 1) ebias = bias[n0 + tid], ey = Y[n0 + tid];
     }
+    // rows of at most 256 * QPF bytes (Kp <= 256 * QPF) stay in registers
+    // from the load to the quantised bytes; longer rows go through LDS
+    const bool regs = Kp <= 256 * QPF;
+    float v[QPF];
     float mx = 0.f;
-    for (int i = tid; i < K; i += 256) mx = fmaxf(mx, fabsf(xf[i]));
+    if (regs) {
+        qx_regs<QX>(X, K, gpf, bpf, v, red8);
+#pragma unroll
+        for (int e = 0; e < QPF; e++)
+            if (tid + 256 * e < K) mx = fmaxf(mx, fabsf(v[e]));
+    } else {
+        qx_row<QX>(X, g, b, K, gpf, bpf, xf, red);
+        for (int i = tid; i < K; i += 256) mx = fmaxf(mx, fabsf(xf[i]));
+    }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
     if ((tid & 63) == 0) mred[tid >> 6] = mx;
     __syncthreads();
     const float amax = fmaxf(fmaxf(fmaxf(mred[0], mred[1]), fmaxf(mred[2], mred[3])), AMAX_INIT);
     const float scale = amax * RCP127, inv = 1.0f / scale;
-    for (int k = tid; k < Kp; k += 256) xs[k] = (int8_t)(k < K ? quant_q(xf[k], inv) : 0);
+    if (regs) {
+#pragma unroll
+        for (int e = 0; e < QPF; e++) {
+            const int k = tid + 256 * e;
+            if (k < Kp) xs[k] = (int8_t)(k < K ? quant_q(v[e], inv) : 0);
+        }
+    } else {
+        for (int k = tid; k < Kp; k += 256) xs[k] = (int8_t)(k < K ? quant_q(xf[k], inv) : 0);
+    }
     __syncthreads();
     if (tap.xq && blockIdx.x == 0) {  // every block makes the same row; block 0 records it
         for (int k = tid; k < Kp; k += 256) tap.xq[k] = (uint8_t)(xs[k] + 128);
@@ -928,10 +1046,10 @@ __global__ __launch_bounds__(GV_THREADS) void igemv_q_kernel(
     if (tid < RPB) {
         const int n = n0 + tid;
         if (n < N) {
-            const float dq = scale * sb[n];
+            const float dq = scale * esb;
             const float y = (float)res[tid] * dq;
             if (tap.y) tap.y[n] = y;
-            if (EPI == 1) Y[n] = Y[n] + (y + bias[n]);
+            if (EPI == 1) Y[n] = ey + (y + ebias);
             else Y[n] = y;
         }
     }
@@ -992,7 +1110,7 @@ __global__ __launch_bounds__(GV_THREADS) void sgemv_q_kernel(
     constexpr int RPL = 2, RG = GV_THREADS / LPR, RPB = RG * RPL, LW = LPR < 64 ? LPR : 64;
     extern __shared__ __attribute__((aligned(16))) unsigned char gv_dyn[];
     float *xf = reinterpret_cast<float *>(gv_dyn);  // [K]
-    __shared__ float red[4], res[RPB], wsum[LPR > 64 ? 4 : 1][RPL];
+    __shared__ float red[4], red8[8], res[RPB], wsum[LPR > 64 ? 4 : 1][RPL];
 
     const int tid = threadIdx.x;
     const int j = tid % LPR, rs = tid / LPR;
@@ -1009,33 +1127,25 @@ __global__ __launch_bounds__(GV_THREADS) void sgemv_q_kernel(
     };
     v4f wn[UK][RPL];
     load_batch(wn, 4 * j);  // in flight while the row is made
-
-    if constexpr (QX == QX_LN) {
-        // the row is read once into LDS; each thread revisits only its own elements
-        float s0 = 0.f;
-        for (int i = tid; i < K; i += 256) {
-            const float v = X[i];
-            xf[i] = v;
-            s0 += v;
-        }
-        const float mu = gv_sum4(s0, red) / K;
-        float q = 0.f;
-        for (int i = tid; i < K; i += 256) {
-            const float d = xf[i] - mu;
-            q += d * d;
-        }
-        const float var = gv_sum4(q, red) / K;
-        const float rsd = 1.0f / sqrtf(var + 1e-5f);
-        for (int i = tid; i < K; i += 256) xf[i] = (xf[i] - mu) * rsd * g[i] + b[i];
-    } else if constexpr (QX == QX_BIAS_GELU) {
-        for (int i = tid; i < K; i += 256) {
-            const float v = X[i] + b[i];
-            xf[i] = 0.5f * v * (1.0f + tanhf(0.7978845608028654f * (v + 0.044715f * v * v * v)));
-        }
-    } else {
-        for (int i = tid; i < K; i += 256) xf[i] = X[i];
+    // loaded with the weights: the transform's vectors, the epilogue's bias
+    // and residual (one dependent global read in the block's chain, the row)
+    float gpf[QPF], bpf[QPF];
+    qx_prefetch<QX>(g, b, K, gpf, bpf);
+    float ebias = 0.f, ey = 0.f;
+    if (tid < RPB && n0 + tid < N) {
+        if (bias) ebias = bias[n0 + tid];
+        if (EPI == 1) ey = Y[n0 + tid];
     }
-    __syncthreads();
+    if (K <= 256 * QPF) {
+        float v[QPF];
+        qx_regs<QX>(X, K, gpf, bpf, v, red8);
+#pragma unroll
+        for (int e = 0; e < QPF; e++)
+            if (tid + 256 * e < K) xf[tid + 256 * e] = v[e];
+        __syncthreads();
+    } else {
+        qx_row<QX>(X, g, b, K, gpf, bpf, xf, red);
+    }
 
     float acc[RPL] = {};
     for (int k0 = 4 * j; k0 < K; k0 += 4 * LPR * UK) {
@@ -1083,8 +1193,8 @@ __global__ __launch_bounds__(GV_THREADS) void sgemv_q_kernel(
     if (tid < RPB) {
         const int n = n0 + tid;
         if (n < N) {
-            const float y = res[tid] + (bias ? bias[n] : 0.f);
-            if (EPI == 1) Y[n] = Y[n] + y;
+            const float y = res[tid] + ebias;
+            if (EPI == 1) Y[n] = ey + y;
             else Y[n] = y;
         }
     }

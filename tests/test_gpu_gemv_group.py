@@ -213,6 +213,27 @@ def test_group_staging_limit_is_reported():
 
 
 @pytest.mark.parametrize("M", [1, 2])
+def test_group_int8_dot_geometry(M):
+    # an all-INT8 group of one or two rows over rows of 1 to 32 packed
+    # segments of 256 bytes in one launch (short, ragged N; every output
+    # form; column offsets), then a group with a row of 9000 bytes
+    shapes = ((7, 129), (300, 63), (700, 33), (1000, 95), (1040, 17), (2048, 31), (2100, 9),
+              (4096, 23), (4200, 5), (8192, 7))
+    prods = [Product(pcl.GEMV_U8S8, M, K, N, 7100 + 10 * i, mode=i % 3, col_off=i % 2 == 1)
+             for i, (K, N) in enumerate(shapes)]
+    announce("gemv group int8 dot geometry", M)
+    run_group(prods, repeat=2)
+    for q in prods:
+        q.check()
+    prods = [Product(pcl.GEMV_U8S8, M, 9000, 70, 7300, mode=2, col_off=True),
+             Product(pcl.GEMV_U8S8, M, 512, 100, 7310, mode=1)]
+    announce("gemv group int8 past the dot path", M)
+    run_group(prods, repeat=2)
+    for q in prods:
+        q.check()
+
+
+@pytest.mark.parametrize("M", [1, 2])
 def test_group_int8_dot_path_ragged(M):
     # an all-INT8 group of one or two rows runs the dot-product path: ragged
     # N (not a multiple of the 64-row strip), K not a multiple of 16 or of

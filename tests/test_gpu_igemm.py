@@ -122,6 +122,29 @@ def test_igemv_wide_dequant_bit_exact(M, N):
                                   ob.dequant((V + off).astype(np.int32), None, sb))
 
 
+# (K, N) for one or two activation rows: rows of 1 to 33 packed segments of
+# 256 bytes (K from 7 to 9000, whole and partial segments) against short,
+# ragged N, every output form, column offsets
+DOT_SHAPES = ((7, 129), (300, 63), (700, 33), (1000, 95), (1040, 17), (2048, 31), (2100, 9),
+              (4096, 23), (4200, 5), (8192, 7), (9000, 70))
+
+
+@pytest.mark.parametrize("M", [1, 2])
+def test_igemv_dot_geometry(M):
+    for K, N in DOT_SHAPES:
+        Au = ob.u8((M, K), 150 + K)
+        Bq = ob.s8((K, N), 151 + N)
+        sa = ob.uniform((M,), 152, 1e-3, 1e-2)
+        sb = ob.uniform((N,), 153, 1e-3, 1e-2)
+        off = ob.s8((N,), 154).astype(np.int32) * 1000
+        V = exact(Au, Bq).astype(np.int32)
+        announce("igemv dot geometry", M, N, K)
+        np.testing.assert_array_equal(igemm_i32(Au, Bq, gemv=True), V)
+        np.testing.assert_array_equal(_dq_run(Au, Bq, sa, sb, off),
+                                      ob.dequant((V + off).astype(np.int32), sa, sb))
+        np.testing.assert_array_equal(_dq_run(Au, Bq, None, sb), ob.dequant(V, None, sb))
+
+
 @pytest.mark.parametrize("M,K,ldx", [(3, 130, 144), (8, 2050, 2064), (5, 61, 64)])
 def test_igemv_padded_rows(M, K, ldx):
     # 16-byte aligned activation rows whose K is not a multiple of 16: the
