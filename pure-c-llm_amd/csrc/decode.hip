@@ -44,10 +44,12 @@ __device__ __forceinline__ float dec_block_sum(float v, float *red) {
 // 16-byte vectors (D % 4 == 0, 16-byte aligned cache); DHT == 0: any head
 // size, scalar reads. p . v: with DHT > 0 thread t owns 4 columns (t mod
 // DHT/4) of every (256 / (DHT/4))-th key, and issues the 16-byte loads of 8
-// of its keys together, so at the grown model's head size (32) and a block of
-// 256 every V row the sum needs is in flight at once (one memory latency, not
-// four); each thread sums its keys in order, then the key groups are added in
-// order. DHT == 0: thread (column, key group), 8 keys per load batch.
+// of its keys together, the first 8 before the scores (they depend on the
+// position only), so at the grown model's head size (32) and a block of 256
+// every V row the sum needs arrives under the scores and the softmax; each
+// thread sums its keys in order, the key groups of a wave are added by
+// shuffles and the four waves in order. DHT == 0: thread (column, key group),
+// 8 keys per load batch.
 template <int DHT>
 __global__ __launch_bounds__(256) void dec_attn_kernel(const float *__restrict__ qkv,
                                                        const float *__restrict__ bqkv,
@@ -62,6 +64,19 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(const float *__restrict__
     const int dh = DHT > 0 ? DHT : dh_rt;
     const int h = blockIdx.x, tid = threadIdx.x, off = h * dh;
     const int pos = tokpos[1];
+    typedef float v4f_t __attribute__((ext_vector_type(4)));
+    // DHT > 0: the first batch of this thread's V rows (they depend on pos
+    // only) is loaded before q / k / v are staged and the scores made
+    constexpr int PVL = DHT > 0 ? DHT / 4 : 1, PVG = 256 / PVL;  // lanes per V row, key groups
+    v4f_t vpre[8];
+    if constexpr (DHT > 0) {
+        const float *vrow = vc + off + 4 * (tid % PVL);
+#pragma unroll
+        for (int u = 0; u < 8; u++) {  // rows past pos (and row pos) read row 0 and add nothing
+            const int j = tid / PVL + u * PVG;
+            vpre[u] = *reinterpret_cast<const v4f_t *>(vrow + (long)(j < pos ? j : 0) * D);
+        }
+    }
     if (tid < dh) {
         const float bq = bqkv ? bqkv[off + tid] : 0.f, bk = bqkv ? bqkv[D + off + tid] : 0.f,
                     bv = bqkv ? bqkv[2 * D + off + tid] : 0.f;
@@ -115,8 +130,7 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(const float *__restrict__
     const float inv = 1.0f / dec_block_sum(sloc, red);  // the block sum also orders sc[] writes
     float *part = dec_lds + ((pos + 1 + 3) & ~3);
     if constexpr (DHT > 0) {
-        typedef float v4f_t __attribute__((ext_vector_type(4)));
-        constexpr int L = DHT / 4, KG = 256 / L;  // lanes per V row, key groups
+        constexpr int L = PVL, KG = PVG;
         const int d4 = tid % L, kg = tid / L;
         const float *vrow = vc + off + 4 * d4;
         v4f_t acc = {0.f, 0.f, 0.f, 0.f};
@@ -125,7 +139,7 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(const float *__restrict__
 #pragma unroll
             for (int u = 0; u < 8; u++) {  // rows past pos read row 0 and add nothing
                 const int j = j0 + u * KG;
-                v[u] = *reinterpret_cast<const v4f_t *>(vrow + (long)(j < pos ? j : 0) * D);
+                v[u] = j0 == kg ? vpre[u] : *reinterpret_cast<const v4f_t *>(vrow + (long)(j < pos ? j : 0) * D);
             }
 #pragma unroll
             for (int u = 0; u < 8; u++) {
@@ -140,13 +154,15 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(const float *__restrict__
                 }
             }
         }
-        *reinterpret_cast<v4f_t *>(part + 4 * tid) = acc;  // part[kg][4 d4 + c]
+        // the 64 / L key groups of a wave added by shuffles (lane bits above
+        // the column's), then the four waves' sums in wave order
+#pragma unroll
+        for (int o = L; o < 64; o <<= 1)
+#pragma unroll
+            for (int c = 0; c < 4; c++) acc[c] += __shfl_xor(acc[c], o);
+        if ((tid & 63) < L) *reinterpret_cast<v4f_t *>(part + (tid >> 6) * DHT + 4 * d4) = acc;
         __syncthreads();
-        if (tid < DHT) {
-            float o = 0.f;
-            for (int g2 = 0; g2 < KG; g2++) o += part[g2 * DHT + tid];
-            att[off + tid] = o;
-        }
+        if (tid < DHT) att[off + tid] = ((part[tid] + part[DHT + tid]) + part[2 * DHT + tid]) + part[3 * DHT + tid];
     } else {
         // output: thread t owns column d = t % dh of key group t / dh
         const int G = 256 / dh, d = tid % dh, gq = tid / dh;

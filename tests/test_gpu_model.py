@@ -83,8 +83,11 @@ def test_model_forward_logits(tmp_path, dims):
         pcl.lib.pcl_model_free(m)
 
 
-# the cache attention's 64- and 128-wide head variants, both weight modes
-@pytest.mark.parametrize("dims", [(24, 256, 4, 512, 2, 80), (24, 256, 2, 512, 2, 80)])
+# the cache attention's 64- and 128-wide head variants, both weight modes; a
+# block past 256 positions (the scores and the V rows of a key group take a
+# second round from position 256 on) at head sizes 32 and 64
+@pytest.mark.parametrize("dims", [(24, 256, 4, 512, 2, 80), (24, 256, 2, 512, 2, 80),
+                                  (300, 128, 4, 256, 1, 64), (300, 128, 2, 256, 1, 64)])
 @pytest.mark.parametrize("int8", [False, True])
 def test_model_forward_wide_heads(tmp_path, dims, int8):
     blk, d, h, df, nl, v = dims
@@ -104,7 +107,11 @@ def test_model_forward_wide_heads(tmp_path, dims, int8):
         om.close()
         pcl.lib.pcl_model_free(m)
     print("normwise per position:", " ".join(f"{e:.1e}" for e in errs), flush=True)
-    assert max(errs) <= (INT8_TOL if int8 else FP32_TOL)
+    if int8 and blk > 256:  # 300 positions of INT8 steps: flip-prone, as the 16-layer model
+        assert errs[0] <= INT8_TOL
+        assert max(errs) <= INT8_BAND
+    else:
+        assert max(errs) <= (INT8_TOL if int8 else FP32_TOL)
 
 
 def _check_greedy(path, prompt, out, v, int8=False, tol=FP32_TOL):
