@@ -65,10 +65,25 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(const float *__restrict__
     const int h = blockIdx.x, tid = threadIdx.x, off = h * dh;
     const int pos = tokpos[1];
     typedef float v4f_t __attribute__((ext_vector_type(4)));
-    // DHT > 0: the first batch of this thread's V rows (they depend on pos
-    // only) is loaded before q / k / v are staged and the scores made
+    // The new token's q, k, v (+ bias) load first: the staging barrier waits
+    // for them, and a load issued later does not hold up that wait. Then, for
+    // DHT > 0, the cache rows this thread reads first, which depend on pos
+    // only: the first batch of its V rows and key row tid (if tid < pos).
+    // (the pointers are materialised first, so the row loads do not wait for
+    // the scalar load of pos)
+    const float *qkv_p = qkv, *bqkv_p = bqkv;
+    asm volatile("" : "+s"(qkv_p), "+s"(bqkv_p));
+    float nq = 0.f, nk = 0.f, nv = 0.f, bq = 0.f, bk = 0.f, bv = 0.f;
+    if (tid < dh) {  // global (not flat) loads: a flat load would also count in the wait for pos
+        const auto qg = gbl(qkv_p);
+        nq = qg[off + tid], nk = qg[D + off + tid], nv = qg[2 * D + off + tid];
+        if (bqkv_p) {
+            const auto bg = gbl(bqkv_p);
+            bq = bg[off + tid], bk = bg[D + off + tid], bv = bg[2 * D + off + tid];
+        }
+    }
     constexpr int PVL = DHT > 0 ? DHT / 4 : 1, PVG = 256 / PVL;  // lanes per V row, key groups
-    v4f_t vpre[8];
+    v4f_t vpre[8], kpre[DHT > 0 ? DHT / 4 : 1];
     if constexpr (DHT > 0) {
         const float *vrow = vc + off + 4 * (tid % PVL);
 #pragma unroll
@@ -76,15 +91,17 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(const float *__restrict__
             const int j = tid / PVL + u * PVG;
             vpre[u] = *reinterpret_cast<const v4f_t *>(vrow + (long)(j < pos ? j : 0) * D);
         }
+        const v4f_t *kj = reinterpret_cast<const v4f_t *>(kc + (long)(tid < pos ? tid : 0) * D + off);
+#pragma unroll
+        for (int c = 0; c < DHT / 4; c++) kpre[c] = kj[c];
     }
     if (tid < dh) {
-        const float bq = bqkv ? bqkv[off + tid] : 0.f, bk = bqkv ? bqkv[D + off + tid] : 0.f,
-                    bv = bqkv ? bqkv[2 * D + off + tid] : 0.f;
-        qs[tid] = qkv[off + tid] + bq;
-        ks[tid] = qkv[D + off + tid] + bk;
-        vs[tid] = qkv[2 * D + off + tid] + bv;
-        kc[(long)pos * D + off + tid] = ks[tid];
-        vc[(long)pos * D + off + tid] = vs[tid];
+        nq += bq, nk += bk, nv += bv;
+        qs[tid] = nq;
+        ks[tid] = nk;
+        vs[tid] = nv;
+        kc[(long)pos * D + off + tid] = nk;
+        vc[(long)pos * D + off + tid] = nv;
     }
     __syncthreads();
     const float *q = qs, *knew = ks, *vnew = vs;
@@ -95,11 +112,10 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(const float *__restrict__
         if (j == pos) {
             for (int d = 0; d < dh; d++) dot += q[d] * knew[d];
         } else if constexpr (DHT > 0) {
-            typedef float v4f_t __attribute__((ext_vector_type(4)));
             const v4f_t *kj = reinterpret_cast<const v4f_t *>(kc + (long)j * D + off);
             v4f_t kv[DHT / 4];
 #pragma unroll
-            for (int c = 0; c < DHT / 4; c++) kv[c] = kj[c];
+            for (int c = 0; c < DHT / 4; c++) kv[c] = j == tid ? kpre[c] : kj[c];
 #pragma unroll
             for (int c = 0; c < DHT / 4; c++) {
                 dot += q[4 * c] * kv[c][0];
