@@ -802,8 +802,8 @@ hipError_t launch_sgemv_xf(const GemvPlan &p, int xf, int N, int K, const float 
 // LDS (the rule of quant.hip: amax from 1e-8, scale = amax * fl(1/127),
 // q = clamp(roundf(x / scale)), padding past K is 0 after recentring), times
 // the packed s8 weights (N rows of Kp bytes), dequantised by scale * sb[n]:
-//   QX_NONE: the row as is; QX_LN: LayerNorm (g, b; the reduction order of
-//   the decode LayerNorm kernels); QX_BIAS_GELU: tanh-GELU(x + b).
+//   QX_NONE: the row as is; QX_LN: LayerNorm (g, b; two passes, mean then
+//   the mean square of the deviations); QX_BIAS_GELU: tanh-GELU(x + b).
 //   EPI 0: Y[n] = v * dq;  EPI 1: Y[n] = Y[n] + (v * dq + bias[n]).
 // Every block computes the same row, scale and bytes. No K split.
 constexpr int QX_NONE = 0, QX_LN = 1, QX_BIAS_GELU = 2;
@@ -881,20 +881,68 @@ __device__ __forceinline__ void qx_row(const float *__restrict__ X, const float 
     __syncthreads();
 }
 
-// Sum over the block of one value per thread, in the order of gv_sum4, into
-// a red[4] used once per launch (no barrier before the writes).
+// Lane reductions on the DPP network (VALU operands from other lanes: no LDS
+// crossbar round trip per step as a shuffle takes). An inclusive scan of
+// row_shr 1, 2, 4, 8 leaves each 16-lane row's total in its last lane;
+// row_bcast15 adds row 0's total into row 1 and row 2's into row 3, and
+// row_bcast31 adds lane 31 into rows 2 and 3. The total (or, for values >= 0,
+// the maximum) of each aligned group of W = 16, 32 or 64 lanes lands in the
+// group's last lane; the other lanes hold partial results. Sources outside a
+// row read 0.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, ROWS, 0xF, true);
+}
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROWS, 0xF, true));
+}
+template <int W>
+__device__ __forceinline__ int dpp_sum_last(int v) {
+    v += dpp_i<0x111, 0xF>(v);
+    v += dpp_i<0x112, 0xF>(v);
+    v += dpp_i<0x114, 0xF>(v);
+    v += dpp_i<0x118, 0xF>(v);
+    if constexpr (W >= 32) v += dpp_i<0x142, 0xA>(v);
+    if constexpr (W >= 64) v += dpp_i<0x143, 0xC>(v);
+    return v;
+}
+template <int W>
+__device__ __forceinline__ float dpp_sum_last(float v) {
+    v += dpp_f<0x111, 0xF>(v);
+    v += dpp_f<0x112, 0xF>(v);
+    v += dpp_f<0x114, 0xF>(v);
+    v += dpp_f<0x118, 0xF>(v);
+    if constexpr (W >= 32) v += dpp_f<0x142, 0xA>(v);
+    if constexpr (W >= 64) v += dpp_f<0x143, 0xC>(v);
+    return v;
+}
+__device__ __forceinline__ float dpp_max_last64(float v) {  // v >= 0
+    v = fmaxf(v, dpp_f<0x111, 0xF>(v));
+    v = fmaxf(v, dpp_f<0x112, 0xF>(v));
+    v = fmaxf(v, dpp_f<0x114, 0xF>(v));
+    v = fmaxf(v, dpp_f<0x118, 0xF>(v));
+    v = fmaxf(v, dpp_f<0x142, 0xA>(v));
+    v = fmaxf(v, dpp_f<0x143, 0xC>(v));
+    return v;
+}
+
+// Sum over the block of one value per thread: each wave's total (DPP, in its
+// last lane), then the four waves in order, into a red[4] used once per
+// launch (no barrier before the writes).
 __device__ __forceinline__ float gv_sum4_once(float v, float *red) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    v = dpp_sum_last<64>(v);
+    if ((threadIdx.x & 63) == 63) red[threadIdx.x >> 6] = v;
     __syncthreads();
     return red[0] + red[1] + red[2] + red[3];
 }
 
 // qx_row for rows of at most 256 * QPF elements, kept in registers: v[e] =
-// transform(X)[tid + 256 e] (0 past K). The same operations in the same
-// order as qx_row, so the same values; no LDS round trips, one barrier per
-// LayerNorm sum. red: 8 floats, each half used once.
+// transform(X)[tid + 256 e] (0 past K). The same per-thread partial sums as
+// qx_row; a wave's partials are added on the DPP network (another
+// association than qx_row's shuffles, so LayerNorm statistics may differ in
+// the last bit); no LDS round trips, one barrier per LayerNorm sum. red: 8
+// floats, each half used once.
 template <int QX>
 __device__ __forceinline__ void qx_regs(const float *__restrict__ X, int K, const float (&gpf)[QPF],
                                         const float (&bpf)[QPF], float (&v)[QPF], float *red) {
@@ -989,9 +1037,8 @@ __global__ __launch_bounds__(GV_THREADS) void igemv_q_kernel(
         qx_row<QX>(X, g, b, K, gpf, bpf, xf, red);
         for (int i = tid; i < K; i += 256) mx = fmaxf(mx, fabsf(xf[i]));
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-    if ((tid & 63) == 0) mred[tid >> 6] = mx;
+    mx = dpp_max_last64(mx);
+    if ((tid & 63) == 63) mred[tid >> 6] = mx;
     __syncthreads();
     const float amax = fmaxf(fmaxf(fmaxf(mred[0], mred[1]), fmaxf(mred[2], mred[3])), AMAX_INIT);
     const float scale = amax * RCP127, inv = 1.0f / scale;
@@ -1036,11 +1083,9 @@ __global__ __launch_bounds__(GV_THREADS) void igemv_q_kernel(
         }
     }
 #pragma unroll
-    for (int r = 0; r < RPL; r++) {
-        int v = acc[r];
-#pragma unroll
-        for (int o = LPR / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, LPR);
-        if (j == 0) res[rs + RG * r] = v;
+    for (int r = 0; r < RPL; r++) {  // the row's LPR lanes, exact in any order
+        const int v = dpp_sum_last<LPR>(acc[r]);
+        if (j == LPR - 1) res[rs + RG * r] = v;
     }
     __syncthreads();
     if (tid < RPB) {
@@ -1169,13 +1214,11 @@ __global__ __launch_bounds__(GV_THREADS) void sgemv_q_kernel(
     }
 #pragma unroll
     for (int r = 0; r < RPL; r++) {
-        float v = acc[r];
-#pragma unroll
-        for (int o = LW / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, LW);
+        const float v = dpp_sum_last<LW>(acc[r]);
         if constexpr (LPR > 64) {
-            if ((tid & 63) == 0) wsum[tid >> 6][r] = v;
+            if ((tid & 63) == 63) wsum[tid >> 6][r] = v;
         } else {
-            if (j == 0) res[rs + RG * r] = v;
+            if (j == LW - 1) res[rs + RG * r] = v;
         }
     }
     if constexpr (LPR > 64) {
