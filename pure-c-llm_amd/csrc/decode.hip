@@ -23,6 +23,35 @@ __global__ void dec_embed_kernel(const float *__restrict__ wte, const float *__r
     x[i] = wte[tok * D + i] + wpe[pos * D + i];
 }
 
+// A wave's maximum (any values) or sum in its last lane, on the DPP network:
+// row_shr 1, 2, 4, 8 within rows of 16 lanes, then row_bcast 15 and 31 across
+// rows. For the maximum a lane with no source keeps its own value; for the
+// sum it adds 0.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float dec_dpp_keep(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, ROWS, 0xF, false));
+}
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float dec_dpp_zero(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROWS, 0xF, true));
+}
+__device__ __forceinline__ float dec_wave_max_last(float v) {
+    v = fmaxf(v, dec_dpp_keep<0x111, 0xF>(v));
+    v = fmaxf(v, dec_dpp_keep<0x112, 0xF>(v));
+    v = fmaxf(v, dec_dpp_keep<0x114, 0xF>(v));
+    v = fmaxf(v, dec_dpp_keep<0x118, 0xF>(v));
+    v = fmaxf(v, dec_dpp_keep<0x142, 0xA>(v));
+    return fmaxf(v, dec_dpp_keep<0x143, 0xC>(v));
+}
+__device__ __forceinline__ float dec_wave_sum_last(float v) {
+    v += dec_dpp_zero<0x111, 0xF>(v);
+    v += dec_dpp_zero<0x112, 0xF>(v);
+    v += dec_dpp_zero<0x114, 0xF>(v);
+    v += dec_dpp_zero<0x118, 0xF>(v);
+    v += dec_dpp_zero<0x142, 0xA>(v);
+    return v + dec_dpp_zero<0x143, 0xC>(v);
+}
+
 // Block-wide sum of one value per thread (256 threads, 4 waves).
 __device__ __forceinline__ float dec_block_sum(float v, float *red) {
 #pragma unroll
@@ -59,7 +88,7 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(const float *__restrict__
                                                        const int *__restrict__ tokpos,
                                                        float scale) {
     extern __shared__ __attribute__((aligned(16))) float dec_lds[];  // [blk] scores, then partial sums
-    __shared__ float red[4], qs[256], ks[256];
+    __shared__ float red[4], red2[4], qs[256], ks[256];
     __shared__ __attribute__((aligned(16))) float vs[256];
     const int dh = DHT > 0 ? DHT : dh_rt;
     const int h = blockIdx.x, tid = threadIdx.x, off = h * dh;
@@ -131,10 +160,9 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(const float *__restrict__
         sc[j] = dot;
         mloc = fmaxf(mloc, dot);
     }
-    // block max
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mloc = fmaxf(mloc, __shfl_xor(mloc, o));
-    if ((tid & 63) == 0) red[tid >> 6] = mloc;
+    // block max: each wave's in its last lane (DPP), then the four waves
+    mloc = dec_wave_max_last(mloc);
+    if ((tid & 63) == 63) red[tid >> 6] = mloc;
     __syncthreads();
     const float m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     float sloc = 0.f;
@@ -143,7 +171,11 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(const float *__restrict__
         sc[j] = e;
         sloc += e;
     }
-    const float inv = 1.0f / dec_block_sum(sloc, red);  // the block sum also orders sc[] writes
+    // block sum the same way (its barrier also orders the sc[] writes)
+    sloc = dec_wave_sum_last(sloc);
+    if ((tid & 63) == 63) red2[tid >> 6] = sloc;
+    __syncthreads();
+    const float inv = 1.0f / (((red2[0] + red2[1]) + red2[2]) + red2[3]);
     float *part = dec_lds + ((pos + 1 + 3) & ~3);
     if constexpr (DHT > 0) {
         constexpr int L = PVL, KG = PVG;
@@ -205,36 +237,64 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(const float *__restrict__
     }
 }
 
+// One step of a (value, index) maximum across lanes on the DPP network: the
+// larger value wins, equal values the smaller index (so the order of the
+// steps does not matter); a lane with no source, or outside ROWS, keeps its
+// own pair. NaN never wins.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ void dec_amax_step(float &best, int &idx) {
+    const float ov = __int_as_float(
+        __builtin_amdgcn_update_dpp(__float_as_int(best), __float_as_int(best), CTRL, ROWS, 0xF, false));
+    const int oi = __builtin_amdgcn_update_dpp(idx, idx, CTRL, ROWS, 0xF, false);
+    if (ov > best || (ov == best && oi < idx)) best = ov, idx = oi;
+}
+// the pair of a row of 16 lanes (rows of 16, then W = 64 lanes) in its last lane
+template <int W>
+__device__ __forceinline__ void dec_amax_last(float &best, int &idx) {
+    dec_amax_step<0x111, 0xF>(best, idx);  // row_shr:1, 2, 4, 8
+    dec_amax_step<0x112, 0xF>(best, idx);
+    dec_amax_step<0x114, 0xF>(best, idx);
+    dec_amax_step<0x118, 0xF>(best, idx);
+    if constexpr (W >= 32) dec_amax_step<0x142, 0xA>(best, idx);  // row_bcast:15
+    if constexpr (W >= 64) dec_amax_step<0x143, 0xC>(best, idx);  // row_bcast:31
+}
+
 // Greedy pick (generate.c:188-191: the first index of the maximum), written
-// as the next token; the position advances and out[pos + 1] records it.
+// as the next token; the position advances and out[pos + 1] records it. 1024
+// threads read the logits in batches of four loads each (one memory latency
+// per 4096 logits), each wave's pair lands in its last lane, and wave 0 picks
+// among the 16 waves' pairs.
 __global__ __launch_bounds__(1024) void dec_argmax_kernel(const float *__restrict__ logits, int V,
                                                           int *__restrict__ tokpos,
                                                           int *__restrict__ out, int out_cap) {
     __shared__ float bv[16];
     __shared__ int bi[16];
     const int tid = threadIdx.x;
+    const int pos = tokpos[1];
     float best = -INFINITY;
     int idx = V;
-    for (int i = tid; i < V; i += 1024) {
-        const float v = logits[i];
-        if (v > best || (v == best && i < idx)) best = v, idx = i;
-    }
+    for (int i0 = tid; i0 < V; i0 += 4096) {
+        float v[4];
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(best, o);
-        const int oi = __shfl_xor(idx, o);
-        if (ov > best || (ov == best && oi < idx)) best = ov, idx = oi;
+        for (int u = 0; u < 4; u++) v[u] = i0 + 1024 * u < V ? logits[i0 + 1024 * u] : -INFINITY;
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int i = i0 + 1024 * u;
+            if (i < V && (v[u] > best || (v[u] == best && i < idx))) best = v[u], idx = i;
+        }
     }
-    if ((tid & 63) == 0) bv[tid >> 6] = best, bi[tid >> 6] = idx;
+    dec_amax_last<64>(best, idx);
+    if ((tid & 63) == 63) bv[tid >> 6] = best, bi[tid >> 6] = idx;
     __syncthreads();
-    if (tid == 0) {
-        for (int w = 1; w < 16; w++)
-            if (bv[w] > best || (bv[w] == best && bi[w] < idx)) best = bv[w], idx = bi[w];
-        const int pos = tokpos[1];
-        if (idx >= V) idx = 0;  // all NaN: keep a valid token
-        tokpos[0] = idx;
-        if (pos + 1 < out_cap) out[pos + 1] = idx;
-        tokpos[1] = pos + 1;
+    if (tid < 16) {
+        best = bv[tid], idx = bi[tid];
+        dec_amax_last<16>(best, idx);
+        if (tid == 15) {
+            if (idx >= V) idx = 0;  // all NaN: keep a valid token
+            tokpos[0] = idx;
+            if (pos + 1 < out_cap) out[pos + 1] = idx;
+            tokpos[1] = pos + 1;
+        }
     }
 }
 

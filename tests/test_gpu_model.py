@@ -310,3 +310,35 @@ def test_model_load_ex_errors(tmp_path):
     assert pcl.lib.pcl_last_status() == pcl.PCL_ERR_INVALID_ARG
     assert not pcl.lib.pcl_model_load_ex(None, pcl.W_INT8)
     pcl.lib.pcl_clear_error()
+
+
+@pytest.mark.parametrize("int8", [False, True])
+@pytest.mark.parametrize("graph", [0, 1])
+def test_model_greedy_ties_pick_first_index(tmp_path, int8, graph):
+    # generate.c:188-191 keeps the first index of the maximum. Every row of
+    # the tied embedding is c_v * w with c_v = 1 + v % 5, so the logits are
+    # c_v * s and come in exact ties: the pick must be 4 (s > 0) or 0 (s <= 0),
+    # the first index among the tied maxima, at every step
+    blk, d, h, df, nl, v = SMALL
+    announce("model greedy ties", "int8" if int8 else "fp32", "graph" if graph else "eager")
+    path = str(tmp_path / "tie.ckp1")
+    ob.write_ckp1(path, blk, d, h, df, nl, v, seed=91)
+    raw = np.fromfile(path, dtype="<f4")
+    w = raw[8:8 + d].copy()
+    c = (1 + np.arange(v) % 5).astype(np.float32)
+    raw[8:8 + v * d] = (c[:, None] * w[None, :]).astype(np.float32).ravel()
+    raw.tofile(path)
+    m = _load(path, pcl.W_INT8 if int8 else pcl.W_FP32)
+    prompt = np.array([3, 7], np.int32)
+    out = np.full(20, -1, np.int32)
+    try:
+        pcl.check(pcl.lib.pcl_model_generate(m, pcl.ptr(prompt), 2, 20, pcl.ptr(out), graph))
+        seq = prompt.tolist() + out.tolist()
+        lg = np.empty(v, np.float32)
+        for pos in range(len(seq) - 1):
+            pcl.check(pcl.lib.pcl_model_forward(m, seq[pos], pos, pcl.ptr(lg)))
+            if pos >= len(prompt) - 1:
+                assert seq[pos + 1] == int(np.argmax(lg)), pos
+                assert seq[pos + 1] in (0, 4), (pos, seq[pos + 1])
+    finally:
+        pcl.lib.pcl_model_free(m)
