@@ -40,6 +40,53 @@ constexpr int SGT_ROWS = 16 * SGT_RPL;   // rows of W per block
 
 static int cdiv(long a, long b) { return (int)((a + b - 1) / b); }
 
+// Lane reductions on the DPP network (VALU operands from other lanes: no LDS
+// crossbar round trip per step as a shuffle takes). An inclusive scan of
+// row_shr 1, 2, 4, 8 leaves each 16-lane row's total in its last lane;
+// row_bcast15 adds row 0's total into row 1 and row 2's into row 3, and
+// row_bcast31 adds lane 31 into rows 2 and 3. The total (or, for values >= 0,
+// the maximum) of each aligned group of W = 16, 32 or 64 lanes lands in the
+// group's last lane; the other lanes hold partial results. Sources outside a
+// row read 0.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, ROWS, 0xF, true);
+}
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROWS, 0xF, true));
+}
+template <int W>
+__device__ __forceinline__ int dpp_sum_last(int v) {
+    v += dpp_i<0x111, 0xF>(v);
+    v += dpp_i<0x112, 0xF>(v);
+    v += dpp_i<0x114, 0xF>(v);
+    v += dpp_i<0x118, 0xF>(v);
+    if constexpr (W >= 32) v += dpp_i<0x142, 0xA>(v);
+    if constexpr (W >= 64) v += dpp_i<0x143, 0xC>(v);
+    return v;
+}
+template <int W>
+__device__ __forceinline__ float dpp_sum_last(float v) {
+    v += dpp_f<0x111, 0xF>(v);
+    v += dpp_f<0x112, 0xF>(v);
+    v += dpp_f<0x114, 0xF>(v);
+    v += dpp_f<0x118, 0xF>(v);
+    if constexpr (W >= 32) v += dpp_f<0x142, 0xA>(v);
+    if constexpr (W >= 64) v += dpp_f<0x143, 0xC>(v);
+    return v;
+}
+__device__ __forceinline__ float dpp_max_last64(float v) {  // v >= 0
+    v = fmaxf(v, dpp_f<0x111, 0xF>(v));
+    v = fmaxf(v, dpp_f<0x112, 0xF>(v));
+    v = fmaxf(v, dpp_f<0x114, 0xF>(v));
+    v = fmaxf(v, dpp_f<0x118, 0xF>(v));
+    v = fmaxf(v, dpp_f<0x142, 0xA>(v));
+    v = fmaxf(v, dpp_f<0x143, 0xC>(v));
+    return v;
+}
+
+
 // Stage MR activation rows of one split (elements [0, kchunk) of row m start
 // at X0 + m*ldx; elements at or past kvalid, and rows m >= M, stage as zero)
 // into LDS rows of stride ld. Each thread issues up to 16 independent loads
@@ -408,19 +455,12 @@ __global__ __launch_bounds__(GV_THREADS) void sgemv_t_kernel(
         }
     }
 
-    // reduce over the 16 lanes of each row group (xor butterfly stays inside)
+    // reduce over the 16 lanes of each row group (DPP, into the group's last lane)
 #pragma unroll
     for (int r = 0; r < SGT_RPL; r++)
 #pragma unroll
-        for (int m = 0; m < MR; m++) {
-            float v = acc[r][m];
-            v += __shfl_xor(v, 8, 16);
-            v += __shfl_xor(v, 4, 16);
-            v += __shfl_xor(v, 2, 16);
-            v += __shfl_xor(v, 1, 16);
-            acc[r][m] = v;
-        }
-    if (j == 0) {
+        for (int m = 0; m < MR; m++) acc[r][m] = dpp_sum_last<16>(acc[r][m]);
+    if (j == 15) {
 #pragma unroll
         for (int r = 0; r < SGT_RPL; r++)
 #pragma unroll
@@ -597,15 +637,8 @@ __global__ __launch_bounds__(GV_THREADS) void igemv_kernel(
 #pragma unroll
     for (int r = 0; r < SGT_RPL; r++)
 #pragma unroll
-        for (int m = 0; m < MR; m++) {
-            int v = acc[r][m];
-            v += __shfl_xor(v, 8, 16);
-            v += __shfl_xor(v, 4, 16);
-            v += __shfl_xor(v, 2, 16);
-            v += __shfl_xor(v, 1, 16);
-            acc[r][m] = v;
-        }
-    if (j == 0) {
+        for (int m = 0; m < MR; m++) acc[r][m] = dpp_sum_last<16>(acc[r][m]);  // exact in any order
+    if (j == 15) {
 #pragma unroll
         for (int r = 0; r < SGT_RPL; r++)
 #pragma unroll
@@ -879,52 +912,6 @@ __device__ __forceinline__ void qx_row(const float *__restrict__ X, const float 
         for (int i = tid; i < K; i += 256) xf[i] = X[i];
     }
     __syncthreads();
-}
-
-// Lane reductions on the DPP network (VALU operands from other lanes: no LDS
-// crossbar round trip per step as a shuffle takes). An inclusive scan of
-// row_shr 1, 2, 4, 8 leaves each 16-lane row's total in its last lane;
-// row_bcast15 adds row 0's total into row 1 and row 2's into row 3, and
-// row_bcast31 adds lane 31 into rows 2 and 3. The total (or, for values >= 0,
-// the maximum) of each aligned group of W = 16, 32 or 64 lanes lands in the
-// group's last lane; the other lanes hold partial results. Sources outside a
-// row read 0.
-template <int CTRL, int ROWS>
-__device__ __forceinline__ int dpp_i(int v) {
-    return __builtin_amdgcn_update_dpp(0, v, CTRL, ROWS, 0xF, true);
-}
-template <int CTRL, int ROWS>
-__device__ __forceinline__ float dpp_f(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROWS, 0xF, true));
-}
-template <int W>
-__device__ __forceinline__ int dpp_sum_last(int v) {
-    v += dpp_i<0x111, 0xF>(v);
-    v += dpp_i<0x112, 0xF>(v);
-    v += dpp_i<0x114, 0xF>(v);
-    v += dpp_i<0x118, 0xF>(v);
-    if constexpr (W >= 32) v += dpp_i<0x142, 0xA>(v);
-    if constexpr (W >= 64) v += dpp_i<0x143, 0xC>(v);
-    return v;
-}
-template <int W>
-__device__ __forceinline__ float dpp_sum_last(float v) {
-    v += dpp_f<0x111, 0xF>(v);
-    v += dpp_f<0x112, 0xF>(v);
-    v += dpp_f<0x114, 0xF>(v);
-    v += dpp_f<0x118, 0xF>(v);
-    if constexpr (W >= 32) v += dpp_f<0x142, 0xA>(v);
-    if constexpr (W >= 64) v += dpp_f<0x143, 0xC>(v);
-    return v;
-}
-__device__ __forceinline__ float dpp_max_last64(float v) {  // v >= 0
-    v = fmaxf(v, dpp_f<0x111, 0xF>(v));
-    v = fmaxf(v, dpp_f<0x112, 0xF>(v));
-    v = fmaxf(v, dpp_f<0x114, 0xF>(v));
-    v = fmaxf(v, dpp_f<0x118, 0xF>(v));
-    v = fmaxf(v, dpp_f<0x142, 0xA>(v));
-    v = fmaxf(v, dpp_f<0x143, 0xC>(v));
-    return v;
 }
 
 // Sum over the block of one value per thread: each wave's total (DPP, in its
@@ -1498,15 +1485,8 @@ __device__ __forceinline__ void gg_f32_t(const GgDesc &d, int strip, float *xs) 
 #pragma unroll
     for (int r = 0; r < RPL; r++)
 #pragma unroll
-        for (int m = 0; m < MR; m++) {
-            float v = acc[r][m];
-            v += __shfl_xor(v, 8, 16);
-            v += __shfl_xor(v, 4, 16);
-            v += __shfl_xor(v, 2, 16);
-            v += __shfl_xor(v, 1, 16);
-            acc[r][m] = v;
-        }
-    if (j == 0) {
+        for (int m = 0; m < MR; m++) acc[r][m] = dpp_sum_last<16>(acc[r][m]);  // the row's 16 lanes, into lane 15
+    if (j == 15) {
         const auto Y = gbl(static_cast<float *>(d.Y));
 #pragma unroll
         for (int r = 0; r < RPL; r++) {
@@ -1732,20 +1712,13 @@ __device__ __forceinline__ void gg_u8s8_dot(const GgDesc &d, int strip, int8_t *
 #pragma unroll
     for (int r = 0; r < GGD_RPL; r++)
 #pragma unroll
-        for (int m = 0; m < MR; m++) {
-            int v = acc[r][m];
-            v += __shfl_xor(v, 8, 16);
-            v += __shfl_xor(v, 4, 16);
-            v += __shfl_xor(v, 2, 16);
-            v += __shfl_xor(v, 1, 16);
-            acc[r][m] = v;
-        }
-    // lane j of a group writes row m = j of its four outputs (rows past M and
+        for (int m = 0; m < MR; m++) acc[r][m] = dpp_sum_last<16>(acc[r][m]);  // into lane 15, exact
+    // lane 15 of a group writes its four outputs of each row m (rows past M and
     // outputs past N are not stored), as igemv_write: v + col_off, then
     // float(v) * dq with dq = sb[n] or sa[m] * sb[n]
 #pragma unroll
     for (int m = 0; m < MR; m++) {
-        if (j == m && m < M) {
+        if (j == 15 && m < M) {
 #pragma unroll
             for (int r = 0; r < GGD_RPL; r++) {
                 const int n = n0 + rs + 16 * r;
