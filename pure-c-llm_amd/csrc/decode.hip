@@ -35,6 +35,17 @@ template <int CTRL, int ROWS>
 __device__ __forceinline__ float dec_dpp_zero(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROWS, 0xF, true));
 }
+// v + the value of lane ^ 16 (v_permlane16_swap exchanges the odd rows of one
+// copy with the even rows of the other) and v + lane ^ 32 (permlane32_swap):
+// the sums of a shuffle butterfly, as VALU operations.
+__device__ __forceinline__ float dec_swap16_sum(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float dec_swap32_sum(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 __device__ __forceinline__ float dec_wave_max_last(float v) {
     v = fmaxf(v, dec_dpp_keep<0x111, 0xF>(v));
     v = fmaxf(v, dec_dpp_keep<0x112, 0xF>(v));
@@ -205,9 +216,13 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(const float *__restrict__
         // the 64 / L key groups of a wave added by shuffles (lane bits above
         // the column's), then the four waves' sums in wave order
 #pragma unroll
-        for (int o = L; o < 64; o <<= 1)
-#pragma unroll
-            for (int c = 0; c < 4; c++) acc[c] += __shfl_xor(acc[c], o);
+        for (int c = 0; c < 4; c++) {
+            float a = acc[c];
+            if constexpr (L == 8) a += dec_dpp_zero<0x128, 0xF>(a);  // row_ror:8 = lane ^ 8
+            if constexpr (L <= 16) a = dec_swap16_sum(a);
+            if constexpr (L <= 32) a = dec_swap32_sum(a);
+            acc[c] = a;
+        }
         if ((tid & 63) < L) *reinterpret_cast<v4f_t *>(part + (tid >> 6) * DHT + 4 * d4) = acc;
         __syncthreads();
         if (tid < DHT) att[off + tid] = ((part[tid] + part[DHT + tid]) + part[2 * DHT + tid]) + part[3 * DHT + tid];

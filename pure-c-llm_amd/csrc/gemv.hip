@@ -1403,15 +1403,16 @@ __device__ __forceinline__ void gg_f32_n(const GgDesc &d, int strip, float *xs, 
                 for (int j = 0; j < 4; j++) acc[m][j] += xb[u] * w[4 + u][j];
         }
     }
-    // groups 4w .. 4w+3 of a column sit in lanes l, l^16, l^32, l^48
+    // groups 4w .. 4w+3 of a column sit in lanes l, l^16, l^32, l^48: the
+    // butterfly's sums (l + l^16, then + the other pair) by permlane swaps
 #pragma unroll
     for (int m = 0; m < MR; m++)
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            float v = acc[m][j];
-            v += __shfl_xor(v, 16);
-            v += __shfl_xor(v, 32);
-            acc[m][j] = v;
+            const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(acc[m][j]), __float_as_uint(acc[m][j]), false, false);
+            const float v = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
+            const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+            acc[m][j] = __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
         }
     if (rr == 0) {
 #pragma unroll
