@@ -65,6 +65,13 @@ __device__ __forceinline__ void at_store(float *lds, const v4f (&r)[AttnTile<DH>
     }
 }
 
+// max(v, the value of lane ^ 32) through v_permlane32_swap (a VALU exchange
+// of the wave's halves, no LDS crossbar round trip)
+__device__ __forceinline__ float at_max_halves(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 // S^T block (keys x queries) of this wave: A = K rows from LDS (16-byte piece
 // 8q + 4lg of row r32, element e at MFMA step 4q + e), B = the wave's Q in the
 // same k order (registers).
@@ -340,7 +347,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_online_kernel(const float *__
                 bm = fmaxf(bm, x[v]);
             }
             // key 0 is visible to every query, so the first block makes mn finite
-            const float mn = fmaxf(m, fmaxf(bm, __shfl_xor(bm, 32)));
+            const float mn = fmaxf(m, at_max_halves(bm));
             const float alpha = __expf(m - mn);  // 0 on the first block (m = -inf)
             float p[16], ps = 0.f;
 #pragma unroll
