@@ -315,9 +315,14 @@ __global__ __launch_bounds__(GV_THREADS) void sgemv_n_kernel(
             }
         }
     };
-    // the first weight batch is in flight while the activations are staged
+    // the first weight batch is in flight while the activations are staged,
+    // and so are the bias and old output of this thread's first output
     v4f wn[UR];
     load_batch(wn, 0);
+    const int pn = n0 + tid % CW;
+    const bool pown = splits == 1 && tid < M * CW && pn < N;
+    const float pbias = pown && bias ? bias[pn] : 0.f;
+    const float pold = pown && accumulate ? Y[(long)(tid / CW) * ldy + pn] : 0.f;
 
     if (!XONES) {
         stage_rows<MR, false>(xs, kchunk, kchunk, min(kchunk, K - kb), M, X + kb, ldx);
@@ -362,9 +367,9 @@ __global__ __launch_bounds__(GV_THREADS) void sgemv_n_kernel(
         for (int r = 0; r < RG; r++) s += red[r][m][c];
         if (splits == 1) {
             if (n < N) {
-                float y = s + (bias ? bias[n] : 0.f);
+                float y = s + (o == tid ? pbias : (bias ? bias[n] : 0.f));
                 float *dst = Y + (long)m * ldy + n;
-                *dst = accumulate ? *dst + y : y;
+                *dst = accumulate ? (o == tid ? pold : *dst) + y : y;
             }
         } else {
             part[((long)sp * M + m) * nround + n] = s;
@@ -417,9 +422,15 @@ __global__ __launch_bounds__(GV_THREADS) void sgemv_t_kernel(
                 }
             }
     };
-    // the first weight batch is in flight while the activations are staged
+    // the first weight batch is in flight while the activations are staged,
+    // and so are the bias and old output of this thread's output (one per
+    // thread: M * SGT_ROWS <= 256)
     v4f wn[UK][SGT_RPL];
     load_batch(wn, 4 * j);
+    const int pn = n0 + tid % SGT_ROWS;
+    const bool pown = splits == 1 && tid < M * SGT_ROWS && pn < N;
+    const float pbias = pown && bias ? bias[pn] : 0.f;
+    const float pold = pown && accumulate ? Y[(long)(tid / SGT_ROWS) * ldy + pn] : 0.f;
 
     stage_rows<MR, false>(xs, kchunk, kchunk, klen, M, X + kb, ldx);
     __syncthreads();
@@ -474,9 +485,9 @@ __global__ __launch_bounds__(GV_THREADS) void sgemv_t_kernel(
         const float s = res[m][c];
         if (splits == 1) {
             if (n < N) {
-                float y = s + (bias ? bias[n] : 0.f);
+                const float y = s + pbias;
                 float *dst = Y + (long)m * ldy + n;
-                *dst = accumulate ? *dst + y : y;
+                *dst = accumulate ? pold + y : y;
             }
         } else {
             part[((long)sp * M + m) * nround + n] = s;
