@@ -574,6 +574,9 @@ def measured_roofs(pcl):
         pcl.check(pcl.lib.pcl_measure_lds_feed(m, n, k, C.byref(r)))
         out[f"int8_tile_feed_{key}_GBps"] = round(r.value, 1)
         out[f"int8_tile_feed_{key}_loop_floor_us"] = round((m // 128) * (n // 128) * 256.0 * k / (r.value * 1e3), 2)
+        # the same stream read into registers: is the ceiling the DMA or L2 -> CU?
+        pcl.check(pcl.lib.pcl_measure_tile_read(m, n, k, C.byref(r)))
+        out[f"int8_tile_read_vgpr_{key}_GBps"] = round(r.value, 1)
     return out
 
 

@@ -398,6 +398,13 @@ int pcl_measure_bandwidth(long bytes_per_array, double gbs[4]);
  * than this feed. No counterpart in the reference (its roofs are gemm_bench's
  * CPU ones). Allocates its operands. */
 int pcl_measure_lds_feed(int M, int N, int K, double *gbs);
+/* The same operand stream (addresses, tile order, one workgroup per tile) read
+ * into registers instead of LDS: eight waves per tile, each with the loads of
+ * two K tiles in flight. *gbs = GB/s read, measured as pcl_measure_lds_feed;
+ * the same arguments and errors. When the two agree, the feed's ceiling is the
+ * path from L2 to the CU rather than the LDS DMA. No counterpart in the
+ * reference. Allocates its operands. */
+int pcl_measure_tile_read(int M, int N, int K, double *gbs);
 
 /* ---- grouped decode GEMV: many independent products in one launch ----
  * Not a reference function: the reference runs its decode products one call

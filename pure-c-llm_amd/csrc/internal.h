@@ -140,7 +140,8 @@ hipError_t measure_peak_mfma(int kind, int cus, double *rate, hipStream_t s);
 hipError_t measure_bandwidth(long bytes_per_array, double gbs[4], hipStream_t s);
 // GB/s into LDS of the operand stream of a 128x128-tile INT8 GEMM (M, N, K
 // multiples of 128; M*K and N*K below 2^31), no products.
-hipError_t measure_lds_feed(int M, int N, int K, double *gbs, hipStream_t s);
+// vgpr: the same stream read into registers (8 waves, 2 K tiles in flight)
+hipError_t measure_lds_feed(int M, int N, int K, double *gbs, hipStream_t s, bool vgpr = false);
 
 // ---- GEMV (gemv.hip) ----
 GemvPlan plan_sgemv(int w_trans, int M, int N, int K);

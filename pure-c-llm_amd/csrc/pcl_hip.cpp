@@ -618,6 +618,17 @@ int pcl_measure_lds_feed(int M, int N, int K, double *gbs) {
     return PCL_OK;
 }
 
+int pcl_measure_tile_read(int M, int N, int K, double *gbs) {
+    CHECK_ARG(gbs != nullptr, "pcl_measure_tile_read: NULL result pointer");
+    CHECK_ARG(M > 0 && N > 0 && K > 0 && M % 128 == 0 && N % 128 == 0 && K % 128 == 0,
+              "pcl_measure_tile_read: M, N, K must be positive multiples of 128 (%d, %d, %d)", M, N, K);
+    CHECK_ARG((long)M * K < (1L << 31) && (long)N * K < (1L << 31),
+              "pcl_measure_tile_read: operands of 2^31 bytes or more");
+    PCL_OK_OR_RETURN(do_init());
+    HIP_OK(pcl::measure_lds_feed(M, N, K, gbs, pick(nullptr), true));
+    return PCL_OK;
+}
+
 // ------------------------------------------------------ grouped GEMV ----
 int pcl_gemv_group_create(const pcl_gemv_desc *descs, int n, pcl_gemv_group **group) {
     CHECK_ARG(group != nullptr, "pcl_gemv_group_create: group is NULL");

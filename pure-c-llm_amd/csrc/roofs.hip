@@ -279,7 +279,49 @@ __global__ __launch_bounds__(64 * RF_FEED_NWP) void roof_feed_kernel(const int8_
     if (tid == 0) sink[blockIdx.x] = lds[lane];
 }
 
-hipError_t measure_lds_feed(int M, int N, int K, double *gbs, hipStream_t s) {
+// The same operand stream (addresses and tile order as roof_feed_kernel)
+// read into registers instead of LDS: eight waves, each with the loads of two
+// K tiles in flight, folded by xor. Equal rates say the ceiling is the path
+// from L2 to the CU, not the LDS DMA.
+constexpr int RF_VG_NWP = 8;
+__global__ __launch_bounds__(64 * RF_VG_NWP) void roof_feed_vgpr_kernel(const int8_t *__restrict__ A,
+                                                                        const int8_t *__restrict__ B, int M,
+                                                                        int N, int K, int *__restrict__ sink) {
+    typedef int rf_v4i __attribute__((ext_vector_type(4)));
+    constexpr int BM = 128, BN = 128, BK = 128, CH = 8, RPI = 8;
+    constexpr int PIA = BM / (RPI * RF_VG_NWP), PIB = BN / (RPI * RF_VG_NWP), PL = PIA + PIB;
+    const int tid = threadIdx.x, lane = tid & 63, pw = tid >> 6;
+    const int nbm = M / BM, nbn = N / BN;
+    int bm, bn;
+    tile_coords(xcd_remap(blockIdx.x, nbm * nbn), nbm, nbn, 8, bm, bn);
+    unsigned voff[PL];
+#pragma unroll
+    for (int d = 0; d < PL; d++) {
+        const bool isA = d < PIA;
+        const int rb = ((isA ? d : d - PIA) * RF_VG_NWP + pw) * RPI;
+        const int r = rb + lane / CH;
+        const int c = (lane % CH) ^ ((r >> 1) & (CH - 1));
+        voff[d] = (unsigned)((isA ? bm * BM : bn * BN) + r) * (unsigned)K + (unsigned)(c * 16);
+    }
+    auto load = [&](rf_v4i (&v)[PL], int t) {
+#pragma unroll
+        for (int d = 0; d < PL; d++)
+            v[d] = *reinterpret_cast<const rf_v4i *>((d < PIA ? A : B) + (long)t * BK + voff[d]);
+    };
+    const int nk = K / BK;
+    rf_v4i cur[PL], nxt[PL], acc = {0, 0, 0, 0};
+    load(cur, 0);
+    for (int t = 0; t < nk; t++) {
+        if (t + 1 < nk) load(nxt, t + 1);
+#pragma unroll
+        for (int d = 0; d < PL; d++) acc ^= cur[d];
+#pragma unroll
+        for (int d = 0; d < PL; d++) cur[d] = nxt[d];
+    }
+    if ((acc[0] ^ acc[1] ^ acc[2] ^ acc[3]) == 0x5a5a5a5a) sink[blockIdx.x] = 1;
+}
+
+hipError_t measure_lds_feed(int M, int N, int K, double *gbs, hipStream_t s, bool vgpr) {
     if (M % 128 || N % 128 || K % 128 || M <= 0 || N <= 0 || K <= 0 || (long)M * K >= (1L << 31) ||
         (long)N * K >= (1L << 31))
         return hipErrorInvalidValue;
@@ -295,9 +337,14 @@ hipError_t measure_lds_feed(int M, int N, int K, double *gbs, hipStream_t s) {
         // would add the event overhead (a few us) to a kernel of a few us
         constexpr int BATCH = 50;
         auto pass = [&]() {
-            for (int i = 0; i < BATCH; i++)
-                hipLaunchKernelGGL(roof_feed_kernel, dim3(tiles), dim3(64 * RF_FEED_NWP), 0, s, (const int8_t *)a,
-                                   (const int8_t *)b, M, N, K, (int *)sink);
+            for (int i = 0; i < BATCH; i++) {
+                if (vgpr)
+                    hipLaunchKernelGGL(roof_feed_vgpr_kernel, dim3(tiles), dim3(64 * RF_VG_NWP), 0, s,
+                                       (const int8_t *)a, (const int8_t *)b, M, N, K, (int *)sink);
+                else
+                    hipLaunchKernelGGL(roof_feed_kernel, dim3(tiles), dim3(64 * RF_FEED_NWP), 0, s,
+                                       (const int8_t *)a, (const int8_t *)b, M, N, K, (int *)sink);
+            }
         };
         pass();
         float ms = 0.f;

@@ -152,6 +152,7 @@ GEMV_F32_N, GEMV_F32_T, GEMV_U8S8 = 0, 1, 2
 _PROTOS["pcl_measure_peak_mfma"] = (_i, [_i, C.POINTER(C.c_double)])
 _PROTOS["pcl_measure_bandwidth"] = (_i, [C.c_long, C.POINTER(C.c_double)])
 _PROTOS["pcl_measure_lds_feed"] = (_i, [_i, _i, _i, C.POINTER(C.c_double)])
+_PROTOS["pcl_measure_tile_read"] = (_i, [_i, _i, _i, C.POINTER(C.c_double)])
 _PROTOS["pcl_gemv_group_create"] = (_i, [C.POINTER(GemvDesc), _i, C.POINTER(_vp)])
 _PROTOS["pcl_gemv_group_run"] = (_i, [_vp, _vp])
 _PROTOS["pcl_gemv_group_free"] = (None, [_vp])

@@ -175,7 +175,7 @@ hipError_t launch_ce_loss(const double *, int, int, float *loss, hipStream_t) {
 }
 hipError_t measure_peak_mfma(int, int, double *rate, hipStream_t) { *rate = 1; return hipSuccess; }
 hipError_t measure_bandwidth(long, double gbs[4], hipStream_t) { gbs[0] = gbs[1] = gbs[2] = gbs[3] = 1; return hipSuccess; }
-hipError_t measure_lds_feed(int, int, int, double *gbs, hipStream_t) { *gbs = 1; return hipSuccess; }
+hipError_t measure_lds_feed(int, int, int, double *gbs, hipStream_t, bool) { *gbs = 1; return hipSuccess; }
 GemvPlan plan_sgemv(int, int M, int N, int K) {
     GemvPlan p{(int)cdiv(N, 64), 1, K, 0, 64};
     if (K > 1024) {

@@ -51,4 +51,7 @@ def test_int8_tile_feed_roof():
     for m, n, k in ((2048, 2048, 2048), (4096, 1024, 4096)):
         pcl.check(pcl.lib.pcl_measure_lds_feed(m, n, k, C.byref(r)))
         assert 1000.0 < r.value <= 256 * 64 * 2.4
+        pcl.check(pcl.lib.pcl_measure_tile_read(m, n, k, C.byref(r)))  # the same stream into registers
+        assert 1000.0 < r.value <= 256 * 64 * 2.4
     assert pcl.lib.pcl_measure_lds_feed(2000, 2048, 2048, C.byref(r)) == pcl.PCL_ERR_INVALID_ARG
+    assert pcl.lib.pcl_measure_tile_read(2048, 2048, 2000, C.byref(r)) == pcl.PCL_ERR_INVALID_ARG
