@@ -35,7 +35,9 @@ struct SgemmPlan {
     int kchunk;         // K per split (a multiple of 64 when split)
     size_t part_bytes;  // workspace bytes (0 when splits == 1)
 };
-SgemmPlan plan_sgemm(int M, int N, int K);
+// a_kcontig: op(A) is K-contiguous (row-major A, no transpose), which the
+// 32x64 small-grid configuration needs
+SgemmPlan plan_sgemm(int M, int N, int K, bool a_kcontig = false);
 // Epilogues on v = op(A).op(B) + bias (accumulate must be 0 with any but NONE):
 //   EPI_GELU: aux_out[m,n] <- v (when aux_out != NULL), C <- gelu(v)
 //   EPI_RESID: C <- aux_in[m,n] + v;  EPI_GELU_BWD: C <- v * gelu'(aux_in[m,n])

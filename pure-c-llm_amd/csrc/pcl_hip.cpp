@@ -869,7 +869,7 @@ int pcl_sgemm(int opA, int opB, int M, int N, int K, const float *A, int lda, co
             if (st != 1) return st;
         }
     }
-    pcl::SgemmPlan p = pcl::plan_sgemm(M, N, K);
+    pcl::SgemmPlan p = pcl::plan_sgemm(M, N, K, opA == PCL_OP_N);
     ScratchLease sc;
     PCL_OK_OR_RETURN(get_scratch(s, p.part_bytes, 0, &sc));
     HIP_OK(pcl::launch_sgemm(p, opA == PCL_OP_N, opB == PCL_OP_T, M, N, K, A, lda, B, ldb, bias,
@@ -913,7 +913,7 @@ int pcl_sgemm_ex(int opA, int opB, int M, int N, int K, const float *A, int lda,
     }
     PCL_OK_OR_RETURN(do_init());
     hipStream_t s = pick(stream);
-    pcl::SgemmPlan p = pcl::plan_sgemm(M, N, K);
+    pcl::SgemmPlan p = pcl::plan_sgemm(M, N, K, opA == PCL_OP_N);
     ScratchLease sc;
     PCL_OK_OR_RETURN(get_scratch(s, p.part_bytes, 0, &sc));
     HIP_OK(pcl::launch_sgemm(p, opA == PCL_OP_N, opB == PCL_OP_T, M, N, K, A, lda, B, ldb, bias, 0,

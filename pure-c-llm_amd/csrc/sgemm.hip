@@ -1175,12 +1175,22 @@ enum SgemmCfg {
     SG_128_BK32 = 1,     // 128x128, BK 32, 4 waves: 2 workgroups per CU
     SG_128_KG2 = 2,      // 128x128, BK 32, 8 waves in two K groups, 2 tiles in flight
     SG_64_KG2 = 3,       // 64x64, BK 64, 8 waves in two K groups, 2 tiles in flight
+    SG_32x64 = 4,        // 32x64 on the 16x16x4 kernel, no split (A K-contiguous, K <= 512)
 };
 
-SgemmPlan plan_sgemm(int M, int N, int K) {
+SgemmPlan plan_sgemm(int M, int N, int K, bool a_kcontig) {
     SgemmPlan p{SG_64_KG2, 1, K > 0 ? K : 1, 0};
     const long t128 = (long)((M + 127) / 128) * ((N + 127) / 128);
     const long t64 = (long)((M + 63) / 64) * ((N + 63) / 64);
+    // Grids too small for 256 CUs with a short K (the grown model's prefill
+    // products, M = 256): 32x64 tiles in one launch -- twice the workgroups of
+    // 64x64 and no split-K sum pass (256 x 1536 x 512: 12.0 -> 8.6 us, the NT
+    // head 11.0 -> 7.5, 256 x 512 x 512: 9.9 -> 8.5; with K = 2048 the split
+    // stays ahead, 13.1 against 26.9 us).
+    if (a_kcontig && t64 < 256 && K >= 32 && K <= 512) {
+        p.cfg = SG_32x64;
+        return p;
+    }
     if (t128 >= 512) {
         // whole rounds of 2 per CU take the deeper tile, otherwise 4 per CU
         // keep more of the grid resident at once
@@ -1326,6 +1336,11 @@ static hipError_t launch_dma_epi(const SgemmPlan &p, int M, int N, int K, const 
     if (s16 == 3)
         return launch_s16<64, 64, 4, 1, A_KC, B_KC, EPI>(M, N, K, 1, K, A, lda, B, ldb, bias, 0, C, ldc,
                                                        stream, aux_in, aux_out, ld_aux);
+    if constexpr (A_KC) {
+        if (p.cfg == SG_32x64)
+            return launch_s16<32, 64, 3, 2, A_KC, B_KC, EPI, 2, 2, 4>(M, N, K, 1, K, A, lda, B, ldb, bias, 0, C,
+                                                                    ldc, stream, aux_in, aux_out, ld_aux);
+    }
     if (p.cfg == SG_64_KG2)
         return launch_dma<64, 64, 2, 2, 1, A_KC, B_KC, EPI>(M, N, K, 1, K, A, lda, B, ldb, bias, 0, C,
                                                             ldc, stream, aux_in, aux_out, ld_aux);
@@ -1384,6 +1399,12 @@ static hipError_t dispatch_layout(const SgemmPlan &p, int M, int N, int K, const
         e = launch_s16_one_per_cu<A_KC, B_KC>(M, N, K, A, lda, B, ldb, b, acc, out, ldo, stream);
     } else if (dma_ok && s16 == 3) {
         e = launch_s16<64, 64, 4, 1, A_KC, B_KC>(M, N, K, 1, K, A, lda, B, ldb, b, acc, out, ldo, stream);
+    } else if (A_KC && dma_ok && p.cfg == SG_32x64) {
+        // 16x16 blocks of 16 x 32 per wave (2 x 2 waves), 32-deep stages, a
+        // 3-stage ring sized for four workgroups per CU
+        if constexpr (A_KC)
+            e = launch_s16<32, 64, 3, 2, A_KC, B_KC, EPI_NONE, 2, 2, 4>(M, N, K, 1, K, A, lda, B, ldb, b, acc,
+                                                                      out, ldo, stream);
     } else if (dma_ok) {
         if (p.cfg == SG_64_KG2)
             e = launch_dma<64, 64, 2, 2, 1, A_KC, B_KC>(M, N, K, p.splits, p.kchunk, A, lda, B, ldb, b,

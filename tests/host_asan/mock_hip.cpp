@@ -105,7 +105,7 @@ void out2(void *C, long ld, int rows, int cols, size_t esz) {
     if (rows > 0 && cols > 0) touch(C, ((size_t)(rows - 1) * ld + cols) * esz);
 }
 }  // namespace
-SgemmPlan plan_sgemm(int M, int N, int K) {
+SgemmPlan plan_sgemm(int M, int N, int K, bool) {
     SgemmPlan p{0, 1, K, 0};
     if ((long)M * N < 65536 && K >= 1024) {  // small grids split K
         p.splits = 4;

@@ -38,7 +38,10 @@ def run_ex(opA, opB, A, B, M, N, K, bias, epi, aux_in=None, want_aux_out=False):
 
 # (M, N, K, opA, opB, path): "fused" grids take the LDS-DMA kernel unsplit
 CASES = [(1024, 1024, 256, N_, N_, "fused 64x64"), (2048, 2048, 128, N_, N_, "fused 128x128"),
-         (1024, 1024, 256, N_, T_, "fused NT"), (300, 500, 200, N_, N_, "split K"),
+         (1024, 1024, 256, N_, T_, "fused NT"), (300, 500, 200, N_, N_, "small grid, K % 32 != 0"),
+         (300, 500, 1024, N_, N_, "split K"), (300, 500, 1024, T_, N_, "split K TN"),
+         (250, 700, 480, N_, N_, "16x16 kernel, 32x64, ragged"),
+         (250, 700, 480, N_, T_, "16x16 kernel, 32x64 NT, ragged"),
          (1024, 1024, 250, N_, N_, "K % 32 != 0"), (1024, 1024, 256, T_, N_, "TN"),
          (1000, 1030, 256, N_, N_, "ragged edges"),
          (4100, 4100, 64, N_, N_, "16x16 kernel, 128x128, ragged"),

@@ -28,7 +28,10 @@ def _operands(opA, opB, M, N, K, seed):
 
 
 SHAPES = [(17, 33, 65), (64, 64, 64), (128, 128, 128), (1000, 1001, 999), (256, 1536, 512),
-          (9, 5, 1), (33, 260, 300), (130, 70, 4)]
+          (9, 5, 1), (33, 260, 300), (130, 70, 4),
+          # small grids with a short K: 32x64 tiles in one launch for row-major A
+          # (ragged M and N, K a multiple of 32 up to 512, and one past it)
+          (250, 700, 480), (256, 512, 512), (100, 2000, 32), (256, 512, 544)]
 
 
 @pytest.mark.parametrize("opA,opB", [(N_, N_), (N_, T_), (T_, N_), (T_, T_)])
