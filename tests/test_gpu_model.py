@@ -312,14 +312,17 @@ def test_model_load_ex_errors(tmp_path):
     pcl.lib.pcl_clear_error()
 
 
+@pytest.mark.parametrize("vocab", [96, 5000])
 @pytest.mark.parametrize("int8", [False, True])
 @pytest.mark.parametrize("graph", [0, 1])
-def test_model_greedy_ties_pick_first_index(tmp_path, int8, graph):
+def test_model_greedy_ties_pick_first_index(tmp_path, int8, graph, vocab):
     # generate.c:188-191 keeps the first index of the maximum. Every row of
     # the tied embedding is c_v * w with c_v = 1 + v % 5, so the logits are
     # c_v * s and come in exact ties: the pick must be 4 (s > 0) or 0 (s <= 0),
-    # the first index among the tied maxima, at every step
-    blk, d, h, df, nl, v = SMALL
+    # the first index among the tied maxima, at every step (a 5000-word
+    # vocabulary puts tied maxima in the argmax's second batch of 4096 too)
+    blk, d, h, df, nl, _ = SMALL
+    v = vocab
     announce("model greedy ties", "int8" if int8 else "fp32", "graph" if graph else "eager")
     path = str(tmp_path / "tie.ckp1")
     ob.write_ckp1(path, blk, d, h, df, nl, v, seed=91)
