@@ -59,9 +59,10 @@ def _load(path, weights=None):
 
 
 ODD_FF = (16, 64, 4, 130, 2, 40)          # d_ff % 4 != 0: the fp32 step's transposed-GEMV path
+FF3K = (16, 64, 4, 3072, 2, 96)           # d_ff rows past 2048: the fused GEMVs' LDS transform path
 
 
-@pytest.mark.parametrize("dims", [SMALL, MID, ODD_FF])
+@pytest.mark.parametrize("dims", [SMALL, MID, ODD_FF, FF3K])
 def test_model_forward_logits(tmp_path, dims):
     blk, d, h, df, nl, v = dims
     announce("model forward", dims)
@@ -192,7 +193,7 @@ def test_model_errors(tmp_path):
 WIDE_FF = (16, 64, 4, 8448, 2, 96)        # d_ff rows past 8192 bytes: the unfused INT8 step
 
 
-@pytest.mark.parametrize("dims,npos", [(SMALL, 32), (MID, 48), (GROWN, 40), (WIDE_FF, 16)])
+@pytest.mark.parametrize("dims,npos", [(SMALL, 32), (MID, 48), (GROWN, 40), (WIDE_FF, 16), (FF3K, 16)])
 def test_model_int8_forward_logits(tmp_path, dims, npos):
     flip_prone = dims in (GROWN, WIDE_FF)  # 16 layers, or 8448-wide rows: many quantised values
     blk, d, h, df, nl, v = dims
@@ -232,7 +233,7 @@ def _tap_source(m, dims):
     return read
 
 
-@pytest.mark.parametrize("dims,npos", [(SMALL, 32), (MID, 24), (GROWN, 40), (WIDE_FF, 16)])
+@pytest.mark.parametrize("dims,npos", [(SMALL, 32), (MID, 24), (GROWN, 40), (WIDE_FF, 16), (FF3K, 16)])
 def test_model_int8_products_pinned(tmp_path, dims, npos):
     # same checkpoints and tokens as test_model_int8_forward_logits
     blk, d, h, df, nl, v = dims
