@@ -130,6 +130,62 @@ __device__ __forceinline__ void at_accum(v16f (&acc)[DH / 32], const float *Xs, 
 }
 
 
+// The online-softmax step of one key block in the log2 domain: the wave's Q
+// fragments carry scale * log2(e), so s is already the exponent base 2 and
+// p = 2^(s - m). Only a block holding keys past a query of the wave or past T
+// (the diagonal block, the tail) is masked. The running maximum m moves only
+// when a row's block maximum exceeds it by more than AT_LAZY (then the row's
+// O^T and l are rescaled by 2^(m_old - m_new)); otherwise p = 2^(s - m) stays
+// below 2^AT_LAZY. O / l and m + log2(l) do not depend on which m was used.
+// The caller guarantees a visible key in every block it passes (so m is
+// finite after the first).
+constexpr float AT_LAZY = 8.f;
+constexpr float AT_LOG2E = 1.44269504088896341f, AT_LN2 = 0.693147180559945309f;
+
+// x = the block's scores with keys j > qi or j >= T set to -inf (only when
+// the wave-uniform masked is set; keys k0 + at_key(v, lg)); returns max x.
+__device__ __forceinline__ float at_mask(const v16f &s, bool masked, int k0, int qi, int T, int lg,
+                                         float (&x)[16]) {
+    if (masked) {
+        const int lim = min(qi, T - 1) - k0;
+#pragma unroll
+        for (int v = 0; v < 16; v++) x[v] = at_key(v, lg) <= lim ? s[v] : -INFINITY;
+    } else {
+#pragma unroll
+        for (int v = 0; v < 16; v++) x[v] = s[v];
+    }
+    float bm = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < 16; v++) bm = fmaxf(bm, x[v]);
+    return bm;
+}
+
+template <int DH>
+__device__ __forceinline__ void at_online(const v16f &s, bool masked, int k0, int qi, int T, int lg, float &m,
+                                          float &l, v16f (&oacc)[DH / 32], float (&p)[16]) {
+    float x[16];
+    const float bm = at_mask(s, masked, k0, qi, T, lg, x);
+    const float mn = fmaxf(m, at_max_halves(bm));  // lanes i and i ^ 32 agree
+    const bool grow = mn > m + AT_LAZY;
+    if (__any(grow)) {
+        const float mu = grow ? mn : m;
+        const float alpha = __builtin_amdgcn_exp2f(m - mu);  // 1 where m stays, 0 on the first block
+        l *= alpha;
+#pragma unroll
+        for (int nb = 0; nb < DH / 32; nb++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) oacc[nb][v] *= alpha;
+        m = mu;
+    }
+    float ps = 0.f;
+#pragma unroll
+    for (int v = 0; v < 16; v++) {
+        p[v] = __builtin_amdgcn_exp2f(x[v] - m);
+        ps += p[v];
+    }
+    l += ps;
+}
+
 template <int DH>
 __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const float *__restrict__ Q,
                                                           const float *__restrict__ K,
@@ -160,11 +216,14 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const float *__restric
     const int kb_last = qlast / AT_KB;     // last key block of the workgroup
     const int kbw = q0w < T ? min(T - 1, q0w + 31) / AT_KB : -1;  // last key block of this wave
 
+    // Q carries scale * log2(e): scores come out in log2 units and
+    // p = 2^(s - m) / l = 2^(s - (m + log2 l))
     v4f qf[DH / 8];
+    const float qsc = scale * AT_LOG2E;
     {
         const float *qrow = Q + (row0 + min(qi, T - 1)) * ld + hc + 4 * lg;
 #pragma unroll
-        for (int q = 0; q < DH / 8; q++) qf[q] = *reinterpret_cast<const v4f *>(qrow + 8 * q);
+        for (int q = 0; q < DH / 8; q++) qf[q] = *reinterpret_cast<const v4f *>(qrow + 8 * q) * qsc;
     }
     // buffer u of the double-buffered K and V blocks
     auto Kb = [&](int u) { return lds + (u & 1) * (TL::KFL + TL::VFL); };
@@ -180,19 +239,14 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const float *__restric
         if (kb < kb_last) at_load<DH>(kr, K + hc, ld, row0, (kb + 1) * AT_KB, T, tid);
         if (kb <= kbw) {
             const v16f s = at_scores<DH>(Kb(kb), qf, r32, lg);
-            float x[16], bm = -INFINITY;
-#pragma unroll
-            for (int v = 0; v < 16; v++) {
-                const int j = kb * AT_KB + at_key(v, lg);
-                x[v] = (j <= qi && j < T) ? s[v] * scale : -INFINITY;
-                bm = fmaxf(bm, x[v]);
-            }
-            const float mn = fmaxf(m, bm);
-            if (mn != -INFINITY) {
+            float x[16];
+            const float mn = fmaxf(m, at_mask(s, kb * AT_KB >= q0w || (kb + 1) * AT_KB > T, kb * AT_KB, qi, T,
+                                              lg, x));
+            if (mn != -INFINITY) {  // this lane half may not have seen a key yet
                 float acc = 0.f;
 #pragma unroll
-                for (int v = 0; v < 16; v++) acc += __expf(x[v] - mn);
-                l = l * __expf(m - mn) + acc;
+                for (int v = 0; v < 16; v++) acc += __builtin_amdgcn_exp2f(x[v] - mn);
+                l = l * __builtin_amdgcn_exp2f(m - mn) + acc;
                 m = mn;
             }
         }
@@ -203,12 +257,10 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const float *__restric
     {
         const float mo = __shfl_xor(m, 32), lo = __shfl_xor(l, 32);
         const float mx = fmaxf(m, mo);
-        const float lt = (m == -INFINITY ? 0.f : l * __expf(m - mx)) +
-                         (mo == -INFINITY ? 0.f : lo * __expf(mo - mx));
-        m = mx;
-        l = lt;
+        const float lt = (m == -INFINITY ? 0.f : l * __builtin_amdgcn_exp2f(m - mx)) +
+                         (mo == -INFINITY ? 0.f : lo * __builtin_amdgcn_exp2f(mo - mx));
+        m = mx + __log2f(lt);  // p = 2^(s - m) from here on
     }
-    const float inv = 1.f / l;
 
     // ---- pass 2: normalised probabilities, stored if asked, and O^T += V^T P^T
     v16f oacc[DH / 32];
@@ -232,11 +284,9 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const float *__restric
         if (kb <= kbw) {
             const v16f s = at_scores<DH>(Kb(kb), qf, r32, lg);
             float p[16];
+            at_mask(s, kb * AT_KB >= q0w || (kb + 1) * AT_KB > T, kb * AT_KB, qi, T, lg, p);
 #pragma unroll
-            for (int v = 0; v < 16; v++) {
-                const int j = kb * AT_KB + at_key(v, lg);
-                p[v] = (j <= qi && j < T) ? __expf(s[v] * scale - m) * inv : 0.f;
-            }
+            for (int v = 0; v < 16; v++) p[v] = __builtin_amdgcn_exp2f(p[v] - m);  // 2^-inf = 0
             // elements 4g .. 4g+3 are keys 8g + 4lg + 0..3: one 16-byte store each
             if (store_p) {
 #pragma unroll
@@ -280,11 +330,12 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const float *__restric
 }
 
 // One pass with a running maximum, for callers that need no probabilities:
-// per key block the two lanes of a query agree on the new maximum (one
-// exchange), rescale their row sum and O^T accumulators by exp(m_old - m_new)
-// and add exp(s - m_new) . v. Scores are computed once (2/3 of the two-pass
-// matrix work); att = O / l, and the row's log-sum-exp m + log(l) is stored
-// when lse is given (p_ij = exp(scale q_i.k_j - lse_i)).
+// per key block the two lanes of a query agree on the block maximum (one
+// exchange) and add 2^(s - m) . v (at_online: base 2, scale folded into Q,
+// masking and rescaling only where a block needs them). Scores are computed
+// once (2/3 of the two-pass matrix work); att = O / l, and the row's natural
+// log-sum-exp ln2 (m + log2 l) is stored when lse is given
+// (p_ij = exp(scale q_i.k_j - lse_i)).
 template <int DH>
 __global__ __launch_bounds__(256, 2) void attn_fwd_online_kernel(const float *__restrict__ Q,
                                                                  const float *__restrict__ K,
@@ -312,10 +363,11 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_online_kernel(const float *__
     const int kbw = q0w < T ? min(T - 1, q0w + 31) / AT_KB : -1;
 
     v4f qf[DH / 8];
+    const float qsc = scale * AT_LOG2E;  // scores in log2 units
     {
         const float *qrow = Q + (row0 + min(qi, T - 1)) * ld + hc + 4 * lg;
 #pragma unroll
-        for (int q = 0; q < DH / 8; q++) qf[q] = *reinterpret_cast<const v4f *>(qrow + 8 * q);
+        for (int q = 0; q < DH / 8; q++) qf[q] = *reinterpret_cast<const v4f *>(qrow + 8 * q) * qsc;
     }
     auto Kb = [&](int u) { return lds + (u & 1) * (TL::KFL + TL::VFL); };
     auto Vb = [&](int u) { return lds + (u & 1) * (TL::KFL + TL::VFL) + TL::KFL; };
@@ -339,28 +391,8 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_online_kernel(const float *__
         }
         if (kb <= kbw) {
             const v16f s = at_scores<DH>(Kb(kb), qf, r32, lg);
-            float x[16], bm = -INFINITY;
-#pragma unroll
-            for (int v = 0; v < 16; v++) {
-                const int j = kb * AT_KB + at_key(v, lg);
-                x[v] = (j <= qi && j < T) ? s[v] * scale : -INFINITY;
-                bm = fmaxf(bm, x[v]);
-            }
-            // key 0 is visible to every query, so the first block makes mn finite
-            const float mn = fmaxf(m, at_max_halves(bm));
-            const float alpha = __expf(m - mn);  // 0 on the first block (m = -inf)
-            float p[16], ps = 0.f;
-#pragma unroll
-            for (int v = 0; v < 16; v++) {
-                p[v] = __expf(x[v] - mn);
-                ps += p[v];
-            }
-            l = l * alpha + ps;
-            m = mn;
-#pragma unroll
-            for (int nb = 0; nb < DH / 32; nb++)
-#pragma unroll
-                for (int v = 0; v < 16; v++) oacc[nb][v] *= alpha;
+            float p[16];
+            at_online<DH>(s, kb * AT_KB >= q0w || (kb + 1) * AT_KB > T, kb * AT_KB, qi, T, lg, m, l, oacc, p);
             at_accum<DH>(oacc, Vb(kb), p, r32, lg);
         }
         if (kb < kb_last) {
@@ -377,7 +409,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_online_kernel(const float *__
         for (int nb = 0; nb < DH / 32; nb++)
 #pragma unroll
             for (int v = 0; v < 16; v++) orow[nb * 32 + at_key(v, lg)] = oacc[nb][v] * inv;
-        if (lse && lg == 0) lse[(long)bh * T + qi] = m + logf(l);
+        if (lse && lg == 0) lse[(long)bh * T + qi] = (m + __log2f(l)) * AT_LN2;
     }
 }
 
