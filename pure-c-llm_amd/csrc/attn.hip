@@ -336,7 +336,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const float *__restric
 // once (2/3 of the two-pass matrix work); att = O / l, and the row's natural
 // log-sum-exp ln2 (m + log2 l) is stored when lse is given
 // (p_ij = exp(scale q_i.k_j - lse_i)).
-template <int DH>
+template <int DH, int SB>
 __global__ __launch_bounds__(256, 2) void attn_fwd_online_kernel(const float *__restrict__ Q,
                                                                  const float *__restrict__ K,
                                                                  const float *__restrict__ V, long ld,
@@ -344,7 +344,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_online_kernel(const float *__
                                                                  float *__restrict__ lse, int T, int H,
                                                                  int BH, float scale) {
     using TL = AttnTile<DH>;
-    __shared__ __attribute__((aligned(16))) float lds[2 * (TL::KFL + TL::VFL)];
+    __shared__ __attribute__((aligned(16))) float lds[2 * SB * (TL::KFL + TL::VFL)];
     const int tid = threadIdx.x, lane = tid & 63, r32 = lane & 31, lg = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int nqb = (T + AT_QB - 1) / AT_QB, half = (nqb + 1) / 2;
@@ -369,9 +369,11 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_online_kernel(const float *__
 #pragma unroll
         for (int q = 0; q < DH / 8; q++) qf[q] = *reinterpret_cast<const v4f *>(qrow + 8 * q) * qsc;
     }
-    auto Kb = [&](int u) { return lds + (u & 1) * (TL::KFL + TL::VFL); };
-    auto Vb = [&](int u) { return lds + (u & 1) * (TL::KFL + TL::VFL) + TL::KFL; };
-    v4f kr[TL::PT], vr[TL::PT];
+    // SB key blocks per stage of a double-buffered ring, one barrier per stage
+    auto Kb = [&](int u, int sb) { return lds + ((u & 1) * SB + sb) * (TL::KFL + TL::VFL); };
+    auto Vb = [&](int u, int sb) { return lds + ((u & 1) * SB + sb) * (TL::KFL + TL::VFL) + TL::KFL; };
+    v4f kr[SB][TL::PT], vr[SB][TL::PT];
+    const int nst = kb_last / SB + 1;
 
     v16f oacc[DH / 32];
 #pragma unroll
@@ -379,25 +381,41 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_online_kernel(const float *__
 #pragma unroll
         for (int v = 0; v < 16; v++) oacc[nb][v] = 0.f;
     float m = -INFINITY, l = 0.f;
-    at_load<DH>(kr, K + hc, ld, row0, 0, T, tid);
-    at_load<DH>(vr, V + hc, ld, row0, 0, T, tid);
-    at_store<DH, TL::KS>(Kb(0), kr, tid);
-    at_store<DH, TL::VS>(Vb(0), vr, tid);
+#pragma unroll
+    for (int sb = 0; sb < SB; sb++) {
+        at_load<DH>(kr[sb], K + hc, ld, row0, sb * AT_KB, T, tid);
+        at_load<DH>(vr[sb], V + hc, ld, row0, sb * AT_KB, T, tid);
+    }
+#pragma unroll
+    for (int sb = 0; sb < SB; sb++) {
+        at_store<DH, TL::KS>(Kb(0, sb), kr[sb], tid);
+        at_store<DH, TL::VS>(Vb(0, sb), vr[sb], tid);
+    }
     __syncthreads();
-    for (int kb = 0; kb <= kb_last; kb++) {
-        if (kb < kb_last) {
-            at_load<DH>(kr, K + hc, ld, row0, (kb + 1) * AT_KB, T, tid);
-            at_load<DH>(vr, V + hc, ld, row0, (kb + 1) * AT_KB, T, tid);
+    for (int st = 0; st < nst; st++) {
+        if (st + 1 < nst) {
+#pragma unroll
+            for (int sb = 0; sb < SB; sb++) {
+                at_load<DH>(kr[sb], K + hc, ld, row0, ((st + 1) * SB + sb) * AT_KB, T, tid);
+                at_load<DH>(vr[sb], V + hc, ld, row0, ((st + 1) * SB + sb) * AT_KB, T, tid);
+            }
         }
-        if (kb <= kbw) {
-            const v16f s = at_scores<DH>(Kb(kb), qf, r32, lg);
-            float p[16];
-            at_online<DH>(s, kb * AT_KB >= q0w || (kb + 1) * AT_KB > T, kb * AT_KB, qi, T, lg, m, l, oacc, p);
-            at_accum<DH>(oacc, Vb(kb), p, r32, lg);
+#pragma unroll
+        for (int sb = 0; sb < SB; sb++) {
+            const int kb = st * SB + sb;
+            if (kb <= kbw) {
+                const v16f s = at_scores<DH>(Kb(st, sb), qf, r32, lg);
+                float p[16];
+                at_online<DH>(s, kb * AT_KB >= q0w || (kb + 1) * AT_KB > T, kb * AT_KB, qi, T, lg, m, l, oacc, p);
+                at_accum<DH>(oacc, Vb(st, sb), p, r32, lg);
+            }
         }
-        if (kb < kb_last) {
-            at_store<DH, TL::KS>(Kb(kb + 1), kr, tid);
-            at_store<DH, TL::VS>(Vb(kb + 1), vr, tid);
+        if (st + 1 < nst) {
+#pragma unroll
+            for (int sb = 0; sb < SB; sb++) {
+                at_store<DH, TL::KS>(Kb(st + 1, sb), kr[sb], tid);
+                at_store<DH, TL::VS>(Vb(st + 1, sb), vr[sb], tid);
+            }
         }
         __syncthreads();
     }
@@ -539,9 +557,11 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(
             if (kb < kbw) load_p(P, kb + 1, pn);
             const v16f dp = at_scores<DH>(Vs(kb), df, r32, lg);
 #pragma unroll
-            for (int v = 0; v < 16; v++) {
-                const int j = kb * AT_KB + at_key(v, lg);
-                ds[v] = (j <= qi && j < T) ? pv[v] * (dp[v] - Dsum) * scale : 0.f;
+            for (int v = 0; v < 16; v++) ds[v] = pv[v] * (dp[v] - Dsum) * scale;
+            if (kb * AT_KB >= q0w || (kb + 1) * AT_KB > T) {  // diagonal or tail block (wave-uniform)
+                const int lim = min(qi, T - 1) - kb * AT_KB;
+#pragma unroll
+                for (int v = 0; v < 16; v++) ds[v] = at_key(v, lg) <= lim ? ds[v] : 0.f;
             }
             if (live) {
 #pragma unroll
@@ -694,13 +714,13 @@ hipError_t launch_attn_fwd(const float *Q, const float *K, const float *V, long 
     if (P == nullptr) {  // no probabilities: one pass
         switch (dh) {
             case 32:
-                hipLaunchKernelGGL(attn_fwd_online_kernel<32>, grid, block, 0, stream, Q, K, V, ld, O, ldo, lse, T, H, BH, scale);
+                hipLaunchKernelGGL((attn_fwd_online_kernel<32, 2>), grid, block, 0, stream, Q, K, V, ld, O, ldo, lse, T, H, BH, scale);
                 break;
             case 64:
-                hipLaunchKernelGGL(attn_fwd_online_kernel<64>, grid, block, 0, stream, Q, K, V, ld, O, ldo, lse, T, H, BH, scale);
+                hipLaunchKernelGGL((attn_fwd_online_kernel<64, 2>), grid, block, 0, stream, Q, K, V, ld, O, ldo, lse, T, H, BH, scale);
                 break;
             case 128:
-                hipLaunchKernelGGL(attn_fwd_online_kernel<128>, grid, block, 0, stream, Q, K, V, ld, O, ldo, lse, T, H, BH, scale);
+                hipLaunchKernelGGL((attn_fwd_online_kernel<128, 1>), grid, block, 0, stream, Q, K, V, ld, O, ldo, lse, T, H, BH, scale);
                 break;
             default:
                 return hipErrorInvalidValue;
