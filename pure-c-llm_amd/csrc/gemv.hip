@@ -1566,11 +1566,13 @@ __device__ __forceinline__ void gg_u8s8(const GgDesc &d, int strip, int8_t *lds)
     // the first slice is in flight while the activations are staged (the
     // epilogue's scales load at the end: loading them here as well takes 12
     // more registers, one wave less per SIMD, and was slower)
-    // two slices in flight per wave (8 KB): slice t + 2 loads into the
-    // registers slice t has just handed to LDS
+    // eight rows: two slices in flight per wave (8 KB), slice t + 2 loading
+    // into the registers slice t has just handed to LDS; fewer rows: one (the
+    // second slice's registers cost a wave per SIMD there, 1-4% slower)
+    constexpr bool TWO = MR >= 8;
     v4i wa[4], wb[4];
     load(wa, 0);
-    if (nsl > 1) load(wb, 1);
+    if (TWO && nsl > 1) load(wb, 1);
     // one 16-byte load per row per thread and round: rows up to 4 KB stage in one
     // round, and the staging holds MR vector registers instead of 16
     stage_rows<MR, true, uint8_t, 1>(reinterpret_cast<uint8_t *>(xs), xld, Kp, d.K, M,
@@ -1589,9 +1591,25 @@ __device__ __forceinline__ void gg_u8s8(const GgDesc &d, int strip, int8_t *lds)
             acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc, 0, 0, 0);
         }
     };
-    for (int t = 0; t < nsl; t += 2) {
-        step(wa, t);
-        if (t + 1 < nsl) step(wb, t + 1);
+    if constexpr (TWO) {
+        for (int t = 0; t < nsl; t += 2) {
+            step(wa, t);
+            if (t + 1 < nsl) step(wb, t + 1);
+        }
+    } else {
+        for (int t = 0; t < nsl; t++) {
+#pragma unroll
+            for (int u = 0; u < 4; u++) wb[u] = wa[u];
+            if (t + 1 < nsl) load(wa, t + 1);
+#pragma unroll
+            for (int u = 0; u < 4; u++) *reinterpret_cast<v4i *>(wdst[u]) = wb[u];
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const v4i a = *reinterpret_cast<const v4i *>(wreg + ri * GGQ_SL + (((4 * c + g) ^ ri) << 4));
+                const v4i b = *reinterpret_cast<const v4i *>(xr + t * GGQ_SL + 64 * c);
+                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc, 0, 0, 0);
+            }
+        }
     }
     // a lane's four results are outputs nb .. nb+3 of row m: one 16-byte store
     const int m = lane & 15, nb = n0 + 16 * wv + 4 * g;
