@@ -490,6 +490,8 @@ CASES = {
                                                                DECODE_LAYER * 16 + [(512, 2048)], 3, w, s),
     "decode_group_int8_m1": lambda pcl, lib, w, s: gemv_group(pcl, lib, 2, 1, DECODE_LAYER * 16 + [(512, 2048)],
                                                                11, w, s),
+    "decode_group_int8_m4": lambda pcl, lib, w, s: gemv_group(pcl, lib, 2, 4, DECODE_LAYER * 16 + [(512, 2048)],
+                                                               11, w, s),
     "decode_group_int8_m8": lambda pcl, lib, w, s: gemv_group(pcl, lib, 2, 8, DECODE_LAYER * 16 + [(512, 2048)],
                                                                11, w, s),
     "gemv_group_head_int8_m1": lambda pcl, lib, w, s: gemv_group(pcl, lib, 2, 1, [(1024, 50257)], 11, w, s),

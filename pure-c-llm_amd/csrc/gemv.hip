@@ -1538,7 +1538,7 @@ constexpr int GGQ_WREG = 16 * GGQ_SL;  // LDS bytes per wave
 __host__ __device__ inline int ggq_x_bytes(int mr, int K) { return (mr * ((K + 255) / 256 * 256 + 16) + 15) / 16 * 16; }
 int ggq_lds_bytes(int mr, int K) { return ggq_x_bytes(mr, K) + 4 * GGQ_WREG; }
 
-template <int MR>
+template <int MR, bool TWO = (MR >= 8)>
 __device__ __forceinline__ void gg_u8s8(const GgDesc &d, int strip, int8_t *lds) {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int ri = lane & 15, g = lane >> 4;
@@ -1566,10 +1566,8 @@ __device__ __forceinline__ void gg_u8s8(const GgDesc &d, int strip, int8_t *lds)
     // the first slice is in flight while the activations are staged (the
     // epilogue's scales load at the end: loading them here as well takes 12
     // more registers, one wave less per SIMD, and was slower)
-    // eight rows: two slices in flight per wave (8 KB), slice t + 2 loading
-    // into the registers slice t has just handed to LDS; fewer rows: one (the
-    // second slice's registers cost a wave per SIMD there, 1-4% slower)
-    constexpr bool TWO = MR >= 8;
+    // TWO: two slices in flight per wave (8 KB), slice t + 2 loading into
+    // the registers slice t has just handed to LDS; else one
     v4i wa[4], wb[4];
     load(wa, 0);
     if (TWO && nsl > 1) load(wb, 1);
@@ -1641,7 +1639,7 @@ __global__ __launch_bounds__(GV_THREADS) void gemv_group_kernel(const GgDesc *__
     const GgDesc d = flat[blockIdx.x];
     if (d.kind == GG_F32_N) gg_f32_n<MR>(d, d.strip, reinterpret_cast<float *>(gv_dyn), red);
     else if (d.kind == GG_F32_T) gg_f32_t<MR>(d, d.strip, reinterpret_cast<float *>(gv_dyn));
-    else gg_u8s8<MR>(d, d.strip, reinterpret_cast<int8_t *>(gv_dyn));
+    else gg_u8s8<MR, (MR >= 4)>(d, d.strip, reinterpret_cast<int8_t *>(gv_dyn));
 }
 
 // A group whose products are all INT8: the same work items through the
@@ -1652,7 +1650,7 @@ template <int MR>
 __global__ __launch_bounds__(GV_THREADS) void gemv_group_u8s8_kernel(const GgDesc *__restrict__ flat) {
     extern __shared__ __attribute__((aligned(16))) unsigned char gv_dyn[];
     const GgDesc d = flat[blockIdx.x];
-    gg_u8s8<MR>(d, d.strip, reinterpret_cast<int8_t *>(gv_dyn));
+    gg_u8s8<MR, (MR >= 4)>(d, d.strip, reinterpret_cast<int8_t *>(gv_dyn));
 }
 
 // GG_U8S8 with one or two activation rows through dot products: the same
