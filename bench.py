@@ -486,6 +486,8 @@ CASES = {
                                                    3, w, s),
     "decode_group_fp32_m1": lambda pcl, lib, w, s: gemv_group(pcl, lib, [0] * 64 + [1], 1,
                                                                DECODE_LAYER * 16 + [(512, 2048)], 3, w, s),
+    "decode_group_fp32_m4": lambda pcl, lib, w, s: gemv_group(pcl, lib, [0] * 64 + [1], 4,
+                                                               DECODE_LAYER * 16 + [(512, 2048)], 3, w, s),
     "decode_group_fp32_m8": lambda pcl, lib, w, s: gemv_group(pcl, lib, [0] * 64 + [1], 8,
                                                                DECODE_LAYER * 16 + [(512, 2048)], 3, w, s),
     "decode_group_int8_m1": lambda pcl, lib, w, s: gemv_group(pcl, lib, 2, 1, DECODE_LAYER * 16 + [(512, 2048)],
