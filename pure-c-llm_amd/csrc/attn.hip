@@ -630,17 +630,40 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkv_kernel(
     const float *Pbh = P + (long)bh * T * T, *Sbh = dS + (long)bh * T * T;
     const int kcol = min(kj, T - 1);
 
-    // P and dS of queries qb*32 + key-layout row s4, key kj (zero past T),
-    // fetched one query block ahead of their use
+    // P and dS of queries qb*32 + key-layout row s4, key kj, fetched one
+    // query block ahead of their use. Heads of 32 and 64: rows past T read
+    // row T-1 and keys past T key T-1, finite values that meet zero dO / Q
+    // rows in LDS or land in output columns that are not stored, so nothing
+    // is zeroed, and a block inside T addresses row qb*32 + at_key(s4, lg) as
+    // a uniform row base plus the lane's 32-bit offset. 128-wide heads keep
+    // the per-element clamp and zero (the other form's addresses spill there).
     float pn[16], sn[16];
+    const unsigned lane_off = (unsigned)(4 * lg * T + kcol);
     auto load_ps = [&](int qb) {
+        if constexpr (DH > 64) {
 #pragma unroll
-        for (int s4 = 0; s4 < 16; s4++) {
-            const int i = qb * AT_KB + at_key(s4, lg);
-            const long o = (long)min(i, T - 1) * T + kcol;
-            const bool ok = i < T && kj < T;
-            pn[s4] = ok ? Pbh[o] : 0.f;
-            sn[s4] = ok ? Sbh[o] : 0.f;
+            for (int s4 = 0; s4 < 16; s4++) {
+                const int i = qb * AT_KB + at_key(s4, lg);
+                const long o = (long)min(i, T - 1) * T + kcol;
+                const bool ok = i < T && kj < T;
+                pn[s4] = ok ? Pbh[o] : 0.f;
+                sn[s4] = ok ? Sbh[o] : 0.f;
+            }
+        } else if ((qb + 1) * AT_KB <= T) {
+            const float *pr = Pbh + (long)qb * AT_KB * T, *sr = Sbh + (long)qb * AT_KB * T;
+#pragma unroll
+            for (int s4 = 0; s4 < 16; s4++) {
+                const long ro = (long)(8 * (s4 >> 2) + (s4 & 3)) * T;
+                pn[s4] = (pr + ro)[lane_off];
+                sn[s4] = (sr + ro)[lane_off];
+            }
+        } else {
+#pragma unroll
+            for (int s4 = 0; s4 < 16; s4++) {
+                const long o = (long)min(qb * AT_KB + at_key(s4, lg), T - 1) * T + kcol;
+                pn[s4] = Pbh[o];
+                sn[s4] = Sbh[o];
+            }
         }
     };
     at_load<DH>(orr, dO + hc, ldo, row0, qb_first * AT_KB, T, tid);
@@ -660,6 +683,11 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkv_kernel(
 #pragma unroll
             for (int s4 = 0; s4 < 16; s4++) pv[s4] = pn[s4], sv[s4] = sn[s4];
             if (qb < qb_last) load_ps(qb + 1);
+            if (qb == qbw) {  // the diagonal block: queries before the key take nothing
+#pragma unroll
+                for (int s4 = 0; s4 < 16; s4++)
+                    if (qb * AT_KB + at_key(s4, lg) < kj) pv[s4] = 0.f, sv[s4] = 0.f;
+            }
             at_accum<DH>(vacc, Os(u), pv, r32, lg);
             at_accum<DH>(kacc, Qs(u), sv, r32, lg);
         }
