@@ -482,6 +482,18 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(
     const long prow = ((long)bh * T + min(qi, T - 1)) * T;
     // P_ij for this lane's 16 keys of block kb (zero past T)
     auto load_p = [&](const float *X, int kb, float (&x)[16]) {
+        // a whole block inside T (wave-uniform; 128-wide heads keep the
+        // per-piece form, whose registers they can hold without a spill)
+        if (DH <= 64 && vec_p && (kb + 1) * AT_KB <= T) {
+            const float *xr = X + prow + kb * AT_KB + 4 * lg;
+#pragma unroll
+            for (int g4 = 0; g4 < 4; g4++) {
+                const v4f t = *reinterpret_cast<const v4f *>(xr + 8 * g4);
+#pragma unroll
+                for (int e = 0; e < 4; e++) x[4 * g4 + e] = t[e];
+            }
+            return;
+        }
 #pragma unroll
         for (int g4 = 0; g4 < 4; g4++) {
             const int j0 = kb * AT_KB + 8 * g4 + 4 * lg;
@@ -556,14 +568,27 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(
             for (int v = 0; v < 16; v++) pv[v] = pn[v];
             if (kb < kbw) load_p(P, kb + 1, pn);
             const v16f dp = at_scores<DH>(Vs(kb), df, r32, lg);
+            if constexpr (DH > 64) {  // the mask on every block (no spill at 256 registers)
 #pragma unroll
-            for (int v = 0; v < 16; v++) ds[v] = pv[v] * (dp[v] - Dsum) * scale;
-            if (kb * AT_KB >= q0w || (kb + 1) * AT_KB > T) {  // diagonal or tail block (wave-uniform)
-                const int lim = min(qi, T - 1) - kb * AT_KB;
+                for (int v = 0; v < 16; v++) {
+                    const int j = kb * AT_KB + at_key(v, lg);
+                    ds[v] = (j <= qi && j < T) ? pv[v] * (dp[v] - Dsum) * scale : 0.f;
+                }
+            } else {
 #pragma unroll
-                for (int v = 0; v < 16; v++) ds[v] = at_key(v, lg) <= lim ? ds[v] : 0.f;
+                for (int v = 0; v < 16; v++) ds[v] = pv[v] * (dp[v] - Dsum) * scale;
+                if (kb * AT_KB >= q0w || (kb + 1) * AT_KB > T) {  // diagonal or tail block (wave-uniform)
+                    const int lim = min(qi, T - 1) - kb * AT_KB;
+#pragma unroll
+                    for (int v = 0; v < 16; v++) ds[v] = at_key(v, lg) <= lim ? ds[v] : 0.f;
+                }
             }
-            if (live) {
+            if (DH <= 64 && live && vec_p && (kb + 1) * AT_KB <= T) {
+                float *sr = dS + prow + kb * AT_KB + 4 * lg;
+#pragma unroll
+                for (int g4 = 0; g4 < 4; g4++)
+                    *reinterpret_cast<v4f *>(sr + 8 * g4) = v4f{ds[4 * g4], ds[4 * g4 + 1], ds[4 * g4 + 2], ds[4 * g4 + 3]};
+            } else if (live) {
 #pragma unroll
                 for (int g4 = 0; g4 < 4; g4++) {
                     const int j0 = kb * AT_KB + 8 * g4 + 4 * lg;
