@@ -288,7 +288,12 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const float *__restric
 #pragma unroll
             for (int v = 0; v < 16; v++) p[v] = __builtin_amdgcn_exp2f(p[v] - m);  // 2^-inf = 0
             // elements 4g .. 4g+3 are keys 8g + 4lg + 0..3: one 16-byte store each
-            if (store_p) {
+            if (store_p && vec_p && (kb + 1) * AT_KB <= T) {  // a whole block inside T
+                float *pr = prow + kb * AT_KB + 4 * lg;
+#pragma unroll
+                for (int g4 = 0; g4 < 4; g4++)
+                    *reinterpret_cast<v4f *>(pr + 8 * g4) = v4f{p[4 * g4], p[4 * g4 + 1], p[4 * g4 + 2], p[4 * g4 + 3]};
+            } else if (store_p) {
 #pragma unroll
                 for (int g4 = 0; g4 < 4; g4++) {
                     const int j0 = kb * AT_KB + 8 * g4 + 4 * lg;
