@@ -494,6 +494,11 @@ CASES = {
                                                                11, w, s),
     "decode_group_int8_m4": lambda pcl, lib, w, s: gemv_group(pcl, lib, 2, 4, DECODE_LAYER * 16 + [(512, 2048)],
                                                                11, w, s),
+    # one weight copy (52 / 206 MB): the sweep reads the Infinity Cache, not HBM
+    "decode_group_int8_m1_1copy": lambda pcl, lib, w, s: gemv_group(pcl, lib, 2, 1,
+                                                                     DECODE_LAYER * 16 + [(512, 2048)], 1, w, s),
+    "decode_group_fp32_m1_1copy": lambda pcl, lib, w, s: gemv_group(pcl, lib, [0] * 64 + [1], 1,
+                                                                     DECODE_LAYER * 16 + [(512, 2048)], 1, w, s),
     "decode_group_int8_m8": lambda pcl, lib, w, s: gemv_group(pcl, lib, 2, 8, DECODE_LAYER * 16 + [(512, 2048)],
                                                                11, w, s),
     "gemv_group_head_int8_m1": lambda pcl, lib, w, s: gemv_group(pcl, lib, 2, 1, [(1024, 50257)], 11, w, s),
