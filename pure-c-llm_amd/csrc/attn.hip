@@ -12,7 +12,8 @@
 // v_mfma_f32_32x32x2f32, so a lane holds 16 scores of ONE query (its column)
 // and a row reduction is 16 lane-local values plus one exchange with lane^32.
 // Pass 1 accumulates the row maximum and exp-sum; pass 2 recomputes S^T, forms
-// the normalised p (the reference's order: p = exp(s - max) / sum, then
+// the normalised p (the reference's p = exp(s - max) / sum, computed in base 2
+// as 2^(s' - (max' + log2 sum)) with Q pre-scaled by scale * log2 e, then
 // att = sum_j p_j v_j), stores p when asked, and accumulates
 // O^T = V^T . P^T where P^T is exactly the register layout S^T left behind
 // (B operand), V^T comes from LDS one float per lane (A operand).
