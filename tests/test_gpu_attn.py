@@ -47,8 +47,10 @@ def attn(q, k, v, B, T, H, dh, ld=None, probs=True, cols=(0, 0, 0)):
     return att, (dp.download((B * H, T, T), np.float32) if dp else None)
 
 
+# T = 96 and 160 end on a stage of two 32-key blocks whose second block lies past T;
+# 130 has rows that are not a multiple of four floats (no 16-byte probability stores)
 SHAPES = [(1, 1, 1, 32), (2, 33, 2, 32), (1, 128, 1, 64), (2, 200, 2, 64), (1, 129, 3, 128),
-          (3, 256, 2, 128), (1, 300, 4, 32)]
+          (3, 256, 2, 128), (1, 300, 4, 32), (1, 96, 2, 64), (2, 160, 1, 32), (1, 130, 2, 64)]
 
 
 @pytest.mark.parametrize("B,T,H,dh", SHAPES)
@@ -240,8 +242,11 @@ def attn_bwd(d_att, q, k, v, probs, B, T, H, dh, grads0=None, accumulate=False, 
     return out
 
 
+# 96 / 160: a last block inside T and its stage partner past it; 130: rows not a multiple of
+# four floats (no 16-byte P and dS access) with heads of 64
 @pytest.mark.parametrize("B,T,H,dh", [(1, 1, 1, 32), (2, 33, 2, 32), (1, 128, 1, 64), (2, 200, 2, 64),
-                                      (1, 129, 3, 128), (2, 256, 2, 128), (1, 300, 4, 32)])
+                                      (1, 129, 3, 128), (2, 256, 2, 128), (1, 300, 4, 32), (1, 96, 2, 64),
+                                      (2, 160, 1, 32), (1, 130, 2, 64)])
 def test_attn_bwd_vs_oracle(B, T, H, dh):
     announce("attn_bwd", B, T, H, dh)
     D = H * dh
