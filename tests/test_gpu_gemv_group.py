@@ -233,6 +233,21 @@ def test_group_int8_dot_geometry(M):
         q.check()
 
 
+@pytest.mark.parametrize("M", [3, 4, 8])
+def test_group_int8_matrix_core_slice_counts(M):
+    # an all-INT8 group of three to eight rows runs the matrix-core path with
+    # two 256-byte weight slices in flight per wave: rows of 1, 2, 3, 4, 5, 8
+    # and 9 slices (the pair loop's odd tails included), ragged N, every
+    # output form, column offsets; run twice
+    shapes = ((100, 70), (512, 64), (700, 130), (1024, 33), (1040, 200), (2048, 65), (2100, 9))
+    prods = [Product(pcl.GEMV_U8S8, M, K, N, 7400 + 10 * i, mode=i % 3, col_off=i % 2 == 0)
+             for i, (K, N) in enumerate(shapes)]
+    announce("gemv group int8 matrix-core slice counts", M)
+    run_group(prods, repeat=2)
+    for q in prods:
+        q.check()
+
+
 @pytest.mark.parametrize("M", [1, 2])
 def test_group_int8_dot_path_ragged(M):
     # an all-INT8 group of one or two rows runs the dot-product path: ragged
