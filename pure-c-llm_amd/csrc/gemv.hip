@@ -935,6 +935,17 @@ __device__ __forceinline__ float gv_sum4_once(float v, float *red) {
     return red[0] + red[1] + red[2] + red[3];
 }
 
+// Two block sums in one barrier: a and b on the DPP network (two independent
+// chains), lane 63 of wave w leaves them in red[w] and red[4 + w].
+__device__ __forceinline__ void gv_sum4x2_once(float &a, float &b, float *red) {
+    a = dpp_sum_last<64>(a);
+    b = dpp_sum_last<64>(b);
+    if ((threadIdx.x & 63) == 63) red[threadIdx.x >> 6] = a, red[4 + (threadIdx.x >> 6)] = b;
+    __syncthreads();
+    a = red[0] + red[1] + red[2] + red[3];
+    b = red[4] + red[5] + red[6] + red[7];
+}
+
 // qx_row for rows of at most 256 * QPF elements, kept in registers: v[e] =
 // transform(X)[tid + 256 e] (0 past K). The same per-thread partial sums as
 // qx_row; a wave's partials are added on the DPP network (another
@@ -951,20 +962,23 @@ __device__ __forceinline__ void qx_regs(const float *__restrict__ X, int K, cons
         v[e] = i < K ? X[i] : 0.f;
     }
     if constexpr (QX == QX_LN) {
-        float s0 = 0.f;
-#pragma unroll
-        for (int e = 0; e < QPF; e++)
-            if (tid + 256 * e < K) s0 += v[e];
-        const float mu = gv_sum4_once(s0, red) / K;
-        float q = 0.f;
+        // mean and variance from one reduction, shifted by the row's first
+        // element (so the difference of the two sums does not cancel when the
+        // mean is large against the spread): with d = x - x0,
+        // mu = x0 + sum(d) / K, var = sum(d^2) / K - (sum(d) / K)^2
+        const float x0 = X[0];
+        float s0 = 0.f, s1 = 0.f;
 #pragma unroll
         for (int e = 0; e < QPF; e++) {
             if (tid + 256 * e < K) {
-                const float d = v[e] - mu;
-                q += d * d;
+                const float d = v[e] - x0;
+                s0 += d;
+                s1 += d * d;
             }
         }
-        const float var = gv_sum4_once(q, red + 4) / K;
+        gv_sum4x2_once(s0, s1, red);
+        const float dm = s0 / K, mu = x0 + dm;
+        const float var = fmaxf(s1 / K - dm * dm, 0.f);
         const float rsd = 1.0f / sqrtf(var + 1e-5f);
 #pragma unroll
         for (int e = 0; e < QPF; e++)
